@@ -1,0 +1,86 @@
+"""ctypes binding of libhclsm_amd.so (the C ABI declared in include/hclsm_amd.h).
+
+torch is imported first on purpose: torch's ROCm wheel ships its own
+``libamdhip64.so`` (SONAME ``libamdhip64.so.7``), and loading it before our library
+makes the dynamic linker resolve our library's HIP dependency to that same
+runtime, so device pointers and ``hipStream_t`` handles from torch are valid here.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import torch  # noqa: F401  (must precede the CDLL load, see module docstring)
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libhclsm_amd.so"
+
+F32, BF16, F16 = 0, 1, 2
+SCAN_RAW, SCAN_MODEL = 0, 1
+
+_c_void_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_f32 = ctypes.c_float
+
+# name -> argtypes, in header order
+_SIGNATURES: dict[str, list] = {
+    "hclsm_abi_version": [],
+    "hclsm_strerror": [_int],
+    "hclsm_ssm_scan_fwd": [_c_void_p] * 8 + [_i64] * 4 + [_int, _int, _c_void_p],
+}
+_RESTYPES = {"hclsm_strerror": ctypes.c_char_p}
+
+_lib = None
+
+
+class HipKernelError(RuntimeError):
+    """An hclsm_amd entry point returned a non-zero code."""
+
+
+def lib() -> ctypes.CDLL:
+    """Load (once) and return the library; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build the HIP kernels first "
+                "(python -m hclsm_amd.build, or __graft_entry__.build())")
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, argtypes in _SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = argtypes
+            fn.restype = _RESTYPES.get(name, _int)
+        _lib = handle
+    return _lib
+
+
+def exported_symbols() -> list[str]:
+    return list(_SIGNATURES)
+
+
+def strerror(code: int) -> str:
+    return lib().hclsm_strerror(int(code)).decode()
+
+
+def check(code: int, what: str) -> None:
+    if code != 0:
+        raise HipKernelError(f"{what} failed: {strerror(code)} (code {code})")
+
+
+def ptr(t: "torch.Tensor | None") -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.float32:
+        return F32
+    if dt == torch.bfloat16:
+        return BF16
+    if dt == torch.float16:
+        return F16
+    raise TypeError(f"hclsm_amd kernels take float32/bfloat16/float16 tensors, got {dt}")
+
+
+def stream_of(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream

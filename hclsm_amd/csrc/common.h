@@ -1,0 +1,60 @@
+// Shared device helpers for the gfx950 kernels of libhclsm_amd.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/hclsm_amd.h"
+
+#define HCLSM_LOG2E 1.4426950408889634f
+
+namespace hclsm {
+
+// ---- element types ---------------------------------------------------------
+// Tensors of bf16 are handled as raw uint16_t bit patterns; conversions are
+// explicit so the generated code is exactly the shift / round we want.
+struct bf16 { uint16_t bits; };
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  // round to nearest even; NaN stays NaN (quiet bit set)
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+template <int DT> struct Elem;
+template <> struct Elem<HCLSM_F32> {
+  using T = float;
+  static __device__ __forceinline__ float ld(const T* p) { return *p; }
+  static __device__ __forceinline__ void st(T* p, float v) { *p = v; }
+};
+template <> struct Elem<HCLSM_BF16> {
+  using T = uint16_t;
+  static __device__ __forceinline__ float ld(const T* p) { return bf16_bits_to_f32(*p); }
+  static __device__ __forceinline__ void st(T* p, float v) { *p = f32_to_bf16_bits(v); }
+};
+template <> struct Elem<HCLSM_F16> {
+  using T = _Float16;
+  static __device__ __forceinline__ float ld(const T* p) { return (float)(*p); }
+  static __device__ __forceinline__ void st(T* p, float v) { *p = (_Float16)v; }
+};
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+}  // namespace hclsm
+
+// Launch helper: returns a hipError_t as int (0 on success).
+#define HCLSM_LAUNCH_CHECK()                         \
+  do {                                               \
+    hipError_t _e = hipGetLastError();               \
+    if (_e != hipSuccess) return (int)_e;            \
+  } while (0)
+
+namespace hclsm {
+// Zero-fill with a kernel (not hipMemsetAsync, so callers may capture it in a graph).
+int zero_fill_f32(float* p, int64_t n, hipStream_t st);
+int zero_fill_bytes(void* p, int64_t nbytes, hipStream_t st);
+}  // namespace hclsm

@@ -1,0 +1,42 @@
+"""Drop-in counterpart of the reference's ``hclsm/kernels/__init__.py`` (:9-61).
+
+Every public name runs on libhclsm_amd.so (gfx950 HIP).  ``TRITON_AVAILABLE`` is kept
+for callers that test it and is always False: there is no Triton path here.
+``HIP_AVAILABLE`` says whether the library is loadable and a ROCm GPU is visible.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from hclsm_amd.kernels.ssm_scan_kernel import (
+    ssm_scan_fn,
+    sequential_ssm_scan,
+    parallel_ssm_scan_pytorch,
+    fused_ssm_scan_triton,
+    fused_ssm_scan_hip,
+)
+
+TRITON_AVAILABLE = False
+
+
+def _hip_available() -> bool:
+    try:
+        from hclsm_amd import _lib
+        _lib.lib()
+    except Exception:
+        return False
+    return torch.cuda.is_available()
+
+
+HIP_AVAILABLE = _hip_available()
+
+__all__ = [
+    "ssm_scan_fn",
+    "sequential_ssm_scan",
+    "parallel_ssm_scan_pytorch",
+    "fused_ssm_scan_triton",
+    "fused_ssm_scan_hip",
+    "TRITON_AVAILABLE",
+    "HIP_AVAILABLE",
+]

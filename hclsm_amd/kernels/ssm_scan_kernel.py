@@ -1,0 +1,149 @@
+"""Selective SSM scan on MI355X -- drop-in for ``hclsm/kernels/ssm_scan_kernel.py``.
+
+Same public names, positional signatures, defaults and return types as the
+reference module:
+
+    ssm_scan_fn(x, dt, A_log, B, C, backend="auto") -> y          (ssm_scan_kernel.py:394-421)
+    sequential_ssm_scan(x, dt, A_log, B, C) -> y                  (:42-86)
+    parallel_ssm_scan_pytorch(x, dt, A_log, B, C) -> y            (:168-218)
+    fused_ssm_scan_triton(x, dt, A_log, B, C) -> y                (:379-387)
+
+Every name runs the hand-written gfx950 kernel of libhclsm_amd.so; the reference's
+backends differ only in semantics, which map to the kernel's clamp mode:
+
+    backend / function                      mode    reference path it reproduces
+    "auto", "triton", "hip", "parallel"     raw     Triton kernel / Blelloch scan (no clamps)
+    "sequential", any unknown string        model   sequential_ssm_scan (clamps at :63,68,77)
+
+(The reference's "auto" on a GPU tensor picks Triton, i.e. raw semantics; unknown
+backend strings fall through to the sequential path, i.e. model semantics.)
+
+Keyword-only extensions, all defaulting to reference behaviour: ``D`` (skip term
+y += D*x), ``clamp_mode`` ("raw"/"model", overrides the backend's mode) and
+``return_h_final`` (also return the final state (batch, d_inner, d_state) fp32, as the
+Triton kernel stores at :289-290).
+
+Inputs must be on a ROCm GPU; there is no CPU implementation.  Output dtype is
+x.dtype (:86, :319).  Autograd: gradients for x, dt, A_log, B, C (and D) come from
+the HIP reverse-scan kernel (replacing ``_TritonSSMScan.backward``, :321-377).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from hclsm_amd import _lib
+from hclsm_amd.kernels._common import common_float_dtype, require_gpu
+
+_RAW_BACKENDS = ("auto", "triton", "hip", "parallel")
+
+
+def _mode_code(clamp_mode: str) -> int:
+    if clamp_mode == "raw":
+        return _lib.SCAN_RAW
+    if clamp_mode == "model":
+        return _lib.SCAN_MODEL
+    raise ValueError(f"clamp_mode must be 'raw' or 'model', got {clamp_mode!r}")
+
+
+def _check_shapes(x, dt, A_log, B, C, D):
+    if x.dim() != 3:
+        raise ValueError(f"x must be (batch, T, d_inner), got shape {tuple(x.shape)}")
+    batch, T, d_inner = x.shape
+    if dt.shape != x.shape:
+        raise ValueError(f"dt shape {tuple(dt.shape)} != x shape {tuple(x.shape)}")
+    if B.dim() != 3 or B.shape[:2] != (batch, T):
+        raise ValueError(f"B must be (batch, T, d_state), got {tuple(B.shape)}")
+    d_state = B.shape[2]
+    if C.shape != B.shape:
+        raise ValueError(f"C shape {tuple(C.shape)} != B shape {tuple(B.shape)}")
+    if A_log.shape != (d_inner, d_state):
+        raise ValueError(f"A_log must be (d_inner, d_state)=({d_inner}, {d_state}), got {tuple(A_log.shape)}")
+    if D is not None and D.shape != (d_inner,):
+        raise ValueError(f"D must be (d_inner,)=({d_inner},), got {tuple(D.shape)}")
+    return batch, T, d_inner, d_state
+
+
+def _scan_forward(x, dt, A_log, B, C, D, mode: int, want_h: bool):
+    """Launch hclsm_ssm_scan_fwd; returns (y in x.dtype, h_final or None, io dtype)."""
+    batch, T, d_inner, d_state = _check_shapes(x, dt, A_log, B, C, D)
+    io = common_float_dtype(x, dt, B, C)
+    xc = x.to(io).contiguous()
+    dtc = dt.to(io).contiguous()
+    Bc = B.to(io).contiguous()
+    Cc = C.to(io).contiguous()
+    Ac = A_log.to(torch.float32).contiguous()
+    Dc = None if D is None else D.to(torch.float32).contiguous()
+    y = torch.empty((batch, T, d_inner), dtype=io, device=x.device)
+    h = torch.empty((batch, d_inner, d_state), dtype=torch.float32, device=x.device) if want_h else None
+    code = _lib.lib().hclsm_ssm_scan_fwd(
+        _lib.ptr(xc), _lib.ptr(dtc), _lib.ptr(Ac), _lib.ptr(Bc), _lib.ptr(Cc), _lib.ptr(Dc),
+        _lib.ptr(y), _lib.ptr(h), batch, T, d_inner, d_state,
+        _lib.dtype_code(io), mode, _lib.stream_of(x))
+    _lib.check(code, "hclsm_ssm_scan_fwd")
+    if y.dtype != x.dtype:
+        y = y.to(x.dtype)
+    return y, h
+
+
+class _HipSSMScan(torch.autograd.Function):
+    """Autograd wrapper: HIP forward scan, HIP reverse-scan backward."""
+
+    @staticmethod
+    def forward(ctx, x, dt, A_log, B, C, D, mode, want_h):
+        y, h = _scan_forward(x, dt, A_log, B, C, D, mode, want_h)
+        ctx.save_for_backward(x, dt, A_log, B, C, D)
+        ctx.mode = mode
+        if h is not None:
+            ctx.mark_non_differentiable(h)
+            return y, h
+        return y
+
+    @staticmethod
+    def backward(ctx, gy, *unused):
+        from hclsm_amd.kernels.ssm_scan_bwd import scan_backward
+        x, dt, A_log, B, C, D = ctx.saved_tensors
+        grads = scan_backward(x, dt, A_log, B, C, D, gy, ctx.mode)
+        return (grads["x"], grads["dt"], grads["A_log"], grads["B"], grads["C"],
+                grads.get("D"), None, None)
+
+
+def fused_ssm_scan_hip(x, dt, A_log, B, C, *, D=None, clamp_mode="raw", return_h_final=False):
+    """The HIP scan with explicit semantics (see module docstring)."""
+    require_gpu("ssm_scan", x, dt, A_log, B, C, D)
+    mode = _mode_code(clamp_mode)
+    out = _HipSSMScan.apply(x, dt, A_log, B, C, D, mode, bool(return_h_final))
+    return out
+
+
+def fused_ssm_scan_triton(x, dt, A_log, B, C, *, D=None, return_h_final=False):
+    """Name kept from ssm_scan_kernel.py:379-387; raw semantics on the HIP kernel."""
+    return fused_ssm_scan_hip(x, dt, A_log, B, C, D=D, clamp_mode="raw", return_h_final=return_h_final)
+
+
+def sequential_ssm_scan(x, dt, A_log, B, C, *, D=None, return_h_final=False):
+    """Clamped (model) semantics of ssm_scan_kernel.py:42-86, on the HIP kernel."""
+    return fused_ssm_scan_hip(x, dt, A_log, B, C, D=D, clamp_mode="model", return_h_final=return_h_final)
+
+
+def parallel_ssm_scan_pytorch(x, dt, A_log, B, C, *, D=None, return_h_final=False):
+    """Unclamped (raw) semantics of ssm_scan_kernel.py:168-218, on the HIP kernel."""
+    return fused_ssm_scan_hip(x, dt, A_log, B, C, D=D, clamp_mode="raw", return_h_final=return_h_final)
+
+
+def ssm_scan_fn(x, dt, A_log, B, C, backend: str = "auto", *, D=None, clamp_mode=None,
+                return_h_final=False):
+    """Dispatcher with the reference's signature (ssm_scan_kernel.py:394-421).
+
+    Args:
+        x:  (batch, T, d_inner); dt: (batch, T, d_inner); A_log: (d_inner, d_state);
+        B, C: (batch, T, d_state).
+        backend: "auto" | "triton" | "hip" | "parallel" (raw) or "sequential" (model);
+            any other string behaves like "sequential", as in the reference.
+    Returns:
+        y (batch, T, d_inner) in x.dtype [, h_final (batch, d_inner, d_state) fp32].
+    """
+    if clamp_mode is None:
+        clamp_mode = "raw" if backend in _RAW_BACKENDS else "model"
+    return fused_ssm_scan_hip(x, dt, A_log, B, C, D=D, clamp_mode=clamp_mode,
+                              return_h_final=return_h_final)

@@ -1,0 +1,51 @@
+"""Seeded synthetic inputs for the benchmark configurations of the hot path.
+
+Each generator draws on the CPU from ``torch.Generator().manual_seed(1000 + cfg)``
+in a fixed order, rounds to the I/O dtype, and returns CPU tensors; callers copy
+the same tensors to the GPU, and checkers upcast the rounded values.
+
+  cfg 0: scan fp32  (128, 16, 256), d_state 16, raw mode, skip D
+  cfg 1: scan bf16  (1024, 64, 384), d_state 16, raw mode, skip D  (bandwidth test)
+  cfg 2: fused slot attention, B=32, M=196, K=32, D=384, 3 iterations, MLP 768
+  cfg 3: sparse event attention, 1024 tracks, T=64, 6 heads x 64, p=0.15, t=0 forced
+  cfg 4: scan chain (1024, 1024, 768) bf16 x4 + event attention 12 x 64, p=0.05
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn.functional as F
+
+SCAN_SHAPES = {
+    0: dict(batch=128, T=16, d_inner=256, d_state=16, dtype=torch.float32),
+    1: dict(batch=1024, T=64, d_inner=384, d_state=16, dtype=torch.bfloat16),
+    4: dict(batch=1024, T=1024, d_inner=768, d_state=16, dtype=torch.bfloat16),
+}
+
+
+def scan_inputs(batch, T, d_inner, d_state, dtype=torch.float32, seed=1000):
+    """x ~ N(0,1); dt = softplus(-2 + 0.5 N(0,1)); A_log ~ U(0, ln 16) so A in [-16,-1];
+    B, C ~ N(0,1)/sqrt(d_state); D ~ N(0,1).  Returns dict of CPU tensors."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(batch, T, d_inner, generator=g)
+    dt = F.softplus(-2.0 + 0.5 * torch.randn(batch, T, d_inner, generator=g))
+    A_log = torch.rand(d_inner, d_state, generator=g) * math.log(16.0)
+    B = torch.randn(batch, T, d_state, generator=g) / math.sqrt(d_state)
+    C = torch.randn(batch, T, d_state, generator=g) / math.sqrt(d_state)
+    D = torch.randn(d_inner, generator=g)
+    return dict(x=x.to(dtype), dt=dt.to(dtype), A_log=A_log, B=B.to(dtype), C=C.to(dtype), D=D)
+
+
+def scan_config(cfg: int):
+    s = SCAN_SHAPES[cfg]
+    return scan_inputs(s["batch"], s["T"], s["d_inner"], s["d_state"], s["dtype"], seed=1000 + cfg)
+
+
+def scan_algorithmic_bytes(batch, T, d_inner, d_state, io_bytes, with_D=True):
+    """HBM bytes one scan must move: read x, dt, B, C, A_log (+D); write y."""
+    b = 3 * batch * T * d_inner * io_bytes + 2 * batch * T * d_state * io_bytes + d_inner * d_state * 4
+    if with_D:
+        b += d_inner * 4
+    return b

@@ -1,0 +1,168 @@
+"""GPU parity of the HIP selective scan against the numpy oracle.
+
+Tolerances (normwise relative, max|got-ref|/max|ref|):
+  fp32 I/O: 1e-5;  bf16 / fp16 I/O with fp32 state: 2e-2 (oracle fed the rounded inputs).
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.ssm_scan import normwise_rel_err, ssm_scan_ref
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 1e-5
+LOWP_TOL = 2e-2
+
+
+def _inputs(N, T, Dn, S, dtype=torch.float32, seed=0, A_hi=math.log(16.0), dt_kind="softplus"):
+    from hclsm_amd.workloads import scan_inputs
+    d = scan_inputs(N, T, Dn, S, dtype=dtype, seed=seed)
+    if dt_kind == "ref_test":   # tests/test_kernels.py:125 distribution
+        g = torch.Generator().manual_seed(seed + 7)
+        d["dt"] = (torch.rand(N, T, Dn, generator=g).abs() + 0.01).to(dtype)
+        d["A_log"] = torch.randn(Dn, S, generator=g)
+    else:
+        d["A_log"] = d["A_log"] * (A_hi / math.log(16.0))
+    return d
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+def _run(d, mode, with_D, dev="cuda", want_h=False):
+    from hclsm_amd.kernels import fused_ssm_scan_hip
+    args = [d[k].to(dev) for k in ("x", "dt", "A_log", "B", "C")]
+    return fused_ssm_scan_hip(*args, D=d["D"].to(dev) if with_D else None, clamp_mode=mode,
+                              return_h_final=want_h)
+
+
+@pytest.mark.parametrize("mode", ["raw", "model"])
+@pytest.mark.parametrize("with_D", [False, True])
+def test_config0_fp32(mode, with_D):
+    from hclsm_amd.workloads import scan_config
+    d = scan_config(0)
+    y = _run(d, mode, with_D)
+    torch.cuda.synchronize()
+    ref = ssm_scan_ref(_np(d["x"]), _np(d["dt"]), _np(d["A_log"]), _np(d["B"]), _np(d["C"]),
+                       D=_np(d["D"]) if with_D else None, clamp_mode=mode)
+    assert y.dtype == torch.float32
+    err = normwise_rel_err(_np(y), ref)
+    assert err <= FP32_TOL, f"cfg0 {mode} D={with_D}: normwise err {err:.3e}"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_lowp_io(dtype):
+    d = _inputs(64, 40, 192, 16, dtype=dtype, seed=3)
+    y = _run(d, "raw", True)
+    ref = ssm_scan_ref(_np(d["x"]), _np(d["dt"]), _np(d["A_log"]), _np(d["B"]), _np(d["C"]),
+                       D=_np(d["D"]), clamp_mode="raw")
+    assert y.dtype == dtype
+    err = normwise_rel_err(_np(y), ref)
+    assert err <= LOWP_TOL, f"{dtype}: normwise err {err:.3e}"
+
+
+@pytest.mark.parametrize("N,T,Dn,S", [
+    (1, 1, 1, 1),        # smallest
+    (3, 7, 5, 3),        # ragged everything, T < chunk
+    (2, 9, 70, 5),       # T = chunk + 1, D not a multiple of 64
+    (2, 17, 130, 17),    # S just over a power of two
+    (2, 16, 64, 32),
+    (1, 24, 128, 33),
+    (1, 8, 64, 64),      # maximum d_state
+    (4, 33, 384, 8),
+])
+@pytest.mark.parametrize("mode", ["raw", "model"])
+def test_shapes_fp32(N, T, Dn, S, mode):
+    d = _inputs(N, T, Dn, S, seed=N * 1000 + T * 10 + S, dt_kind="ref_test")
+    y, h = _run(d, mode, True, want_h=True)
+    ref, href = ssm_scan_ref(_np(d["x"]), _np(d["dt"]), _np(d["A_log"]), _np(d["B"]), _np(d["C"]),
+                             D=_np(d["D"]), clamp_mode=mode, return_h_final=True)
+    assert normwise_rel_err(_np(y), ref) <= FP32_TOL
+    assert normwise_rel_err(_np(h), href) <= FP32_TOL
+
+
+def test_reference_test_distribution_modes_differ():
+    """On the reference test's own inputs (tests/test_kernels.py:120-128) raw and model
+    semantics disagree, as the reference's parallel-vs-sequential test would show."""
+    d = _inputs(2, 16, 32, 8, seed=11, dt_kind="ref_test")
+    y_raw = _run(d, "raw", False)
+    y_mod = _run(d, "model", False)
+    ref_raw = ssm_scan_ref(_np(d["x"]), _np(d["dt"]), _np(d["A_log"]), _np(d["B"]), _np(d["C"]), clamp_mode="raw")
+    ref_mod = ssm_scan_ref(_np(d["x"]), _np(d["dt"]), _np(d["A_log"]), _np(d["B"]), _np(d["C"]), clamp_mode="model")
+    assert normwise_rel_err(_np(y_raw), ref_raw) <= FP32_TOL
+    assert normwise_rel_err(_np(y_mod), ref_mod) <= FP32_TOL
+    assert normwise_rel_err(ref_raw, ref_mod) > 1e-2
+
+
+def test_config1_bf16_subset_and_properties():
+    """Full config-1 launch (1024, 64, 384) bf16; oracle on a subset of sequences,
+    plus size-independent properties on the whole output."""
+    from hclsm_amd.workloads import scan_config
+    d = scan_config(1)
+    y = _run(d, "raw", True)
+    torch.cuda.synchronize()
+    assert y.shape == (1024, 64, 384) and y.dtype == torch.bfloat16
+    assert torch.isfinite(y).all()
+    sel = list(range(0, 48)) + list(range(1000, 1024))
+    sub = {k: (v[sel] if k in ("x", "dt", "B", "C") else v) for k, v in d.items()}
+    ref = ssm_scan_ref(_np(sub["x"]), _np(sub["dt"]), _np(sub["A_log"]), _np(sub["B"]), _np(sub["C"]),
+                       D=_np(sub["D"]), clamp_mode="raw")
+    err = normwise_rel_err(_np(y[sel]), ref)
+    assert err <= LOWP_TOL, f"cfg1 normwise err {err:.3e}"
+    # linearity in x (dt fixed): y(2x) - D*2x == 2 (y(x) - D*x) up to bf16 rounding
+    d2 = dict(d)
+    d2["x"] = (d["x"].float() * 2).to(torch.bfloat16)   # exact in bf16
+    y2 = _run(d2, "raw", False)
+    y1 = _run(d, "raw", False)
+    err_lin = normwise_rel_err(_np(y2), 2 * _np(y1))
+    assert err_lin <= 1e-2, f"linearity err {err_lin:.3e}"
+
+
+def test_causality_and_zero_B():
+    d = _inputs(4, 20, 96, 16, seed=5)
+    y = _run(d, "raw", False)
+    d2 = {k: v.clone() for k, v in d.items()}
+    d2["x"][:, 12:] = torch.randn_like(d2["x"][:, 12:])
+    d2["dt"][:, 12:] = 0.3
+    y2 = _run(d2, "raw", False)
+    assert torch.equal(y[:, :12], y2[:, :12])  # outputs before t=12 ignore later inputs
+    d3 = {k: v.clone() for k, v in d.items()}
+    d3["B"].zero_()
+    y3 = _run(d3, "raw", True)
+    assert torch.allclose(y3, d3["x"].cuda() * d3["D"].cuda(), rtol=1e-6, atol=1e-6)
+
+
+def test_empty_and_errors():
+    from hclsm_amd.kernels import ssm_scan_fn
+    x = torch.zeros(0, 5, 8, device="cuda")
+    y = ssm_scan_fn(x, x, torch.zeros(8, 4, device="cuda"), torch.zeros(0, 5, 4, device="cuda"),
+                    torch.zeros(0, 5, 4, device="cuda"))
+    assert y.shape == (0, 5, 8)
+    xc = torch.zeros(2, 3, 8)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ssm_scan_fn(xc, xc, torch.zeros(8, 4), torch.zeros(2, 3, 4), torch.zeros(2, 3, 4))
+    from hclsm_amd._lib import HipKernelError
+    xg = torch.zeros(1, 2, 8, device="cuda")
+    with pytest.raises(HipKernelError, match="not supported"):
+        ssm_scan_fn(xg, xg, torch.zeros(8, 65, device="cuda"), torch.zeros(1, 2, 65, device="cuda"),
+                    torch.zeros(1, 2, 65, device="cuda"))
+
+
+def test_backend_semantics():
+    """Backend strings map to the reference's semantics (ssm_scan_kernel.py:412-421)."""
+    from hclsm_amd.kernels import ssm_scan_fn
+    d = _inputs(2, 16, 32, 8, seed=21, dt_kind="ref_test")
+    args = [d[k].cuda() for k in ("x", "dt", "A_log", "B", "C")]
+    raw = ssm_scan_ref(*[_np(d[k]) for k in ("x", "dt", "A_log", "B", "C")], clamp_mode="raw")
+    mod = ssm_scan_ref(*[_np(d[k]) for k in ("x", "dt", "A_log", "B", "C")], clamp_mode="model")
+    for be in ("auto", "triton", "hip", "parallel"):
+        assert normwise_rel_err(_np(ssm_scan_fn(*args, backend=be)), raw) <= FP32_TOL
+    for be in ("sequential", "no-such-backend"):
+        assert normwise_rel_err(_np(ssm_scan_fn(*args, backend=be)), mod) <= FP32_TOL
