@@ -1,0 +1,183 @@
+#!/usr/bin/env python3
+"""Benchmark of the hclsm_amd hot path on one MI355X.
+
+Workload (one "step"): one selective-SSM scan of config 1 -- 1024 sequences
+(B=32 x 32 slots), T=64, d_inner=384, d_state=16, bf16 x/dt/B/C/y, fp32 A_log/D,
+fp32 state, raw semantics plus skip term -- launched through the C ABI
+(hclsm_ssm_scan_fwd) on torch's current stream.
+
+Honest-HBM measurement: the config-1 working set (155 MB) fits in the 256 MB
+Infinity Cache, so the timed loop rotates over NSETS distinct input/output sets
+(>600 MB total); every launch reads inputs last touched three launches earlier.
+
+Prints ONE JSON line.  `value` is the scan's algorithmic bytes / average step time
+(GB/s); `roofline` prices the same kernel against MI355X's 8 TB/s HBM peak with the
+per-launch duration measured by HIP events; `cpu_baseline` times the numpy oracle
+(float32, the reference's sequential_ssm_scan semantics in raw mode) on a bounded
+sample of the same workload on the host cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "SSM scan GB/s (% of HBM peak) + slot-attn/event-attn tokens/s, small preset, 1 GPU"
+HBM_PEAK_GBS = 8000.0
+NSETS = 4
+
+
+def _parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="after the timed loop, run a 1 GiB device-to-device copy 5 times (a kernel of "
+                        "known traffic for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE counters)")
+    return p.parse_args()
+
+
+def _traffic_from_profile():
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if present."""
+    path = os.path.join(ROOT, "profiles", "ssm_scan_cfg1_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def _cpu_baseline(d, nseq=1024, reps=5):
+    import numpy as np
+    from oracle.ssm_scan import ssm_scan_ref
+    from hclsm_amd.workloads import scan_algorithmic_bytes
+    sel = slice(0, nseq)
+    args = [d[k][sel].float().numpy() if k in ("x", "dt", "B", "C") else d[k].numpy()
+            for k in ("x", "dt", "A_log", "B", "C")]
+    Dn = d["D"].numpy()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        ssm_scan_ref(*args, D=Dn, clamp_mode="raw", dtype=np.float32)
+        times.append(time.perf_counter() - t0)
+    med = sorted(times)[len(times) // 2]
+    T, d_inner = d["x"].shape[1:]
+    S = d["B"].shape[2]
+    nbytes = scan_algorithmic_bytes(nseq, T, d_inner, S, 2)
+    return {"value": round(nbytes / med / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{nseq} of {d['x'].shape[0]} config-1 sequences, numpy float32 sequential scan "
+                      f"(oracle/ssm_scan.py), median of {reps}: {med:.3f} s"}
+
+
+def main():
+    args = _parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
+              "the scan shards over sequences with no exchange -- run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from hclsm_amd import _lib
+    from hclsm_amd.workloads import scan_algorithmic_bytes, scan_config
+
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm GPU visible", file=sys.stderr)
+        sys.exit(1)
+    L = _lib.lib()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+
+    d = scan_config(1)
+    N, T, Dn = d["x"].shape
+    S = d["B"].shape[2]
+    nbytes = scan_algorithmic_bytes(N, T, Dn, S, 2)
+    sets = []
+    for r in range(NSETS):
+        g = {k: v.to(dev) for k, v in d.items()}
+        if r:
+            g["x"] = torch.roll(g["x"], shifts=r, dims=0).contiguous()
+        g["y"] = torch.empty_like(g["x"])
+        sets.append(g)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+
+    def launch(g):
+        code = L.hclsm_ssm_scan_fwd(g["x"].data_ptr(), g["dt"].data_ptr(), g["A_log"].data_ptr(),
+                                    g["B"].data_ptr(), g["C"].data_ptr(), g["D"].data_ptr(),
+                                    g["y"].data_ptr(), None, N, T, Dn, S,
+                                    _lib.BF16, _lib.SCAN_RAW, stream)
+        if code:
+            raise RuntimeError(_lib.strerror(code))
+
+    for i in range(args.warmup):
+        launch(sets[i % NSETS])
+    torch.cuda.synchronize()
+
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i, (a, b) in enumerate(evs):
+        a.record()
+        launch(sets[i % NSETS])
+        b.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    durs = sorted(a.elapsed_time(b) * 1e-3 for a, b in evs)   # seconds per launch
+    avg = sum(durs) / len(durs)
+    med = durs[len(durs) // 2]
+
+    # correctness spot check of the last output against the oracle (8 sequences)
+    from oracle.ssm_scan import normwise_rel_err, ssm_scan_ref
+    last = sets[(args.steps - 1) % NSETS]
+    sel = slice(0, 8)
+    ref = ssm_scan_ref(*[last[k][sel].float().cpu().numpy() if k in ("x", "dt", "B", "C") else last[k].cpu().numpy()
+                         for k in ("x", "dt", "A_log", "B", "C")], D=last["D"].cpu().numpy(), clamp_mode="raw")
+    err = normwise_rel_err(last["y"][sel].float().cpu().numpy(), ref)
+    if not err <= 2e-2:
+        raise SystemExit(f"bench.py: parity check failed (normwise {err:.3e})")
+
+    if args.copy_calibration:
+        src = torch.empty(1 << 28, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
+    achieved = nbytes / avg / 1e9
+    out = {
+        "metric": METRIC,
+        "value": round(nbytes * args.steps / wall / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "ssm_scan config 1: 1024 seq x T=64 x d_inner=384, d_state=16, "
+                               "bf16 I/O, fp32 state, raw mode + skip D",
+                   "io_dtype": "bf16", "input_sets_rotated": NSETS,
+                   "algorithmic_bytes_per_step": nbytes, "parity_normwise_err": err},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic_from_profile(),
+                     "kernel": "ssm_scan_fwd_sgpr_kernel<bf16,16,raw,2,4>",
+                     "avg_launch_us": round(avg * 1e6, 3), "median_launch_us": round(med * 1e6, 3)},
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = _cpu_baseline(d)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

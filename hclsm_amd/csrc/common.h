@@ -17,12 +17,17 @@ struct bf16 { uint16_t bits; };
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Round-to-nearest-even conversions; gfx950 does these with v_cvt_pk_bf16_f32.
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  // round to nearest even; NaN stays NaN (quiet bit set)
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
+}
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  bf16x2_t r;
+  r.x = (__bf16)lo;
+  r.y = (__bf16)hi;
+  return __builtin_bit_cast(uint32_t, r);
 }
 
 template <int DT> struct Elem;

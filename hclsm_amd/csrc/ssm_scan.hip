@@ -48,10 +48,11 @@ ssm_scan_fwd_kernel(const typename Elem<DT>::T* __restrict__ x,
 #pragma unroll
   for (int s = 0; s < SP; ++s) {
     float a = 0.f;
-    if (s < S) {
-      float e = expf(A_log[(size_t)dd * S + s]);
+    {
+      // unconditional load of a valid element, then select: no divergent branch
+      float e = expf(A_log[(size_t)dd * S + (s < S ? s : S - 1)]);
       if (MODE == HCLSM_SCAN_MODEL) e = fminf(fmaxf(e, 1e-6f), 1.0f);
-      a = -e * HCLSM_LOG2E;
+      a = (s < S) ? -e * HCLSM_LOG2E : 0.f;
     }
     a2[s] = a;
   }
@@ -79,16 +80,14 @@ ssm_scan_fwd_kernel(const typename Elem<DT>::T* __restrict__ x,
 #pragma unroll
     for (int k = 0; k < STAGE_MAX; ++k) {
       const int i = threadIdx.x + k * blockDim.x;
-      float bv = 0.f, cv = 0.f;
-      if (i < TC * SP) {
-        const int tt = i / SP, s = i % SP, t = t0 + tt;
-        if (t < T && s < S) {
-          bv = E::ld(bp + (size_t)t * S + s);
-          cv = E::ld(cp + (size_t)t * S + s);
-        }
-      }
-      stB[k] = bv;
-      stC[k] = cv;
+      const int ii = i < TC * SP ? i : 0;
+      const int tt = ii / SP, s = ii % SP, t = t0 + tt;
+      const bool ok = (i < TC * SP) && (t < T) && (s < S);
+      const int tc = t < T ? t : T - 1, sc = s < S ? s : S - 1;
+      const float bv = E::ld(bp + (size_t)tc * S + sc);
+      const float cv = E::ld(cp + (size_t)tc * S + sc);
+      stB[k] = ok ? bv : 0.f;
+      stC[k] = ok ? cv : 0.f;
     }
   };
   auto stage_store = [&](int buf) {
@@ -105,9 +104,9 @@ ssm_scan_fwd_kernel(const typename Elem<DT>::T* __restrict__ x,
   auto xd_load = [&](int t0, float* xo, float* dO) {
 #pragma unroll
     for (int j = 0; j < TC; ++j) {
-      const int t = t0 + j;
-      xo[j] = (t < T) ? E::ld(xp + (size_t)t * Dn) : 0.f;
-      dO[j] = (t < T) ? E::ld(dp + (size_t)t * Dn) : 0.f;
+      const int t = t0 + j < T ? t0 + j : T - 1;  // clamped: always a valid address
+      xo[j] = E::ld(xp + (size_t)t * Dn);
+      dO[j] = E::ld(dp + (size_t)t * Dn);
     }
   };
 
@@ -183,6 +182,215 @@ ssm_scan_fwd_kernel(const typename Elem<DT>::T* __restrict__ x,
   }
 }
 
+// ---------------------------------------------------------------------------
+// Fast path: d_state == SP, B/C rows small enough to live in SGPRs.
+//
+// B_t and C_t are the same for every lane of the workgroup, so they are fetched
+// with scalar loads (s_load_dwordx*) one step ahead and unpacked by the scalar
+// ALU; the VALU then reads them as SGPR operands.  No LDS and no barriers.  Each
+// lane owns DPL adjacent channels (DPL=2 gives 32-bit bf16 pair loads/stores and
+// shares the scalar unpack between two channels).  x/dt for the next TC steps are
+// loaded (clamped addresses, unconditional) before the current TC steps compute.
+template <int DT, int SP, int MODE, int DPL, int TC>
+__global__ void __launch_bounds__(64)
+ssm_scan_fwd_sgpr_kernel(const typename Elem<DT>::T* __restrict__ x,
+                         const typename Elem<DT>::T* __restrict__ dt,
+                         const float* __restrict__ A_log,
+                         const typename Elem<DT>::T* __restrict__ Bm,
+                         const typename Elem<DT>::T* __restrict__ Cm,
+                         const float* __restrict__ Dskip,
+                         typename Elem<DT>::T* __restrict__ y,
+                         float* __restrict__ h_final,
+                         int T, int Dn) {
+  using E = Elem<DT>;
+  using TT = typename E::T;
+  constexpr int NW = SP * (int)sizeof(TT) / 4;  // 32-bit words per B/C row
+  static_assert(NW >= 1, "row must be at least one word");
+
+  const int n = blockIdx.x;
+  const int lane_d = (blockIdx.y * 64 + threadIdx.x) * DPL;  // first channel of this lane
+  const bool act = lane_d < Dn;
+  const int d0 = act ? lane_d : 0;
+
+  float a2[DPL][SP];
+#pragma unroll
+  for (int k = 0; k < DPL; ++k)
+#pragma unroll
+    for (int s = 0; s < SP; ++s) {
+      float e = expf(A_log[(size_t)(d0 + k) * SP + s]);
+      if (MODE == HCLSM_SCAN_MODEL) e = fminf(fmaxf(e, 1e-6f), 1.0f);
+      a2[k][s] = -e * HCLSM_LOG2E;
+    }
+  const bool has_d = Dskip != nullptr;
+  float dsk[DPL];
+#pragma unroll
+  for (int k = 0; k < DPL; ++k) dsk[k] = has_d ? Dskip[d0 + k] : 0.f;
+
+  float h[DPL][SP];
+#pragma unroll
+  for (int k = 0; k < DPL; ++k)
+#pragma unroll
+    for (int s = 0; s < SP; ++s) h[k][s] = 0.f;
+
+  const size_t row0 = (size_t)n * T;
+  const TT* xp = x + row0 * Dn + d0;
+  const TT* dp = dt + row0 * Dn + d0;
+  TT* yp = y + row0 * Dn + d0;
+  const uint32_t* bw0 = reinterpret_cast<const uint32_t*>(Bm + row0 * SP);
+  const uint32_t* cw0 = reinterpret_cast<const uint32_t*>(Cm + row0 * SP);
+
+  auto ld_pair = [&](const TT* p, float* o) {
+    if constexpr (DPL == 2 && DT == HCLSM_BF16) {
+      const uint32_t w = *reinterpret_cast<const uint32_t*>(p);
+      o[0] = __uint_as_float(w << 16);
+      o[1] = __uint_as_float(w & 0xffff0000u);
+    } else if constexpr (DPL == 2 && DT == HCLSM_F32) {
+      const float2 v = *reinterpret_cast<const float2*>(p);
+      o[0] = v.x;
+      o[1] = v.y;
+    } else {
+#pragma unroll
+      for (int k = 0; k < DPL; ++k) o[k] = E::ld(p + k);
+    }
+  };
+  auto st_pair = [&](TT* p, const float* v) {
+    if constexpr (DPL == 2 && DT == HCLSM_BF16) {
+      const uint32_t w = pack_bf16x2(v[0], v[1]);
+      *reinterpret_cast<uint32_t*>(p) = w;
+    } else if constexpr (DPL == 2 && DT == HCLSM_F32) {
+      *reinterpret_cast<float2*>(p) = make_float2(v[0], v[1]);
+    } else {
+#pragma unroll
+      for (int k = 0; k < DPL; ++k) E::st(p + k, v[k]);
+    }
+  };
+  auto unpack = [&](const uint32_t (&w)[NW], float (&v)[SP]) {
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+      if constexpr (DT == HCLSM_BF16) {
+        v[2 * i] = __uint_as_float(w[i] << 16);
+        v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+      } else {
+        v[i] = __uint_as_float(w[i]);
+      }
+    }
+  };
+
+  float xv[TC][DPL], dv[TC][DPL];
+  auto xd_load = [&](int t0, float (*xo)[DPL], float (*dO)[DPL]) {
+#pragma unroll
+    for (int j = 0; j < TC; ++j) {
+      const int t = t0 + j < T ? t0 + j : T - 1;  // clamped: always a valid address
+      ld_pair(xp + (size_t)t * Dn, xo[j]);
+      ld_pair(dp + (size_t)t * Dn, dO[j]);
+    }
+  };
+
+  uint32_t bw[NW], cw[NW];
+#pragma unroll
+  for (int i = 0; i < NW; ++i) { bw[i] = bw0[i]; cw[i] = cw0[i]; }
+
+  auto step = [&](int t, const float* xs, const float* ds) {
+    // fetch next step's rows first (uniform address -> scalar loads)
+    const int tn = t + 1 < T ? t + 1 : T - 1;
+    uint32_t bwn[NW], cwn[NW];
+#pragma unroll
+    for (int i = 0; i < NW; ++i) { bwn[i] = bw0[(size_t)tn * NW + i]; cwn[i] = cw0[(size_t)tn * NW + i]; }
+    float bv[SP], cv[SP];
+    unpack(bw, bv);
+    unpack(cw, cv);
+    float yo[DPL];
+#pragma unroll
+    for (int k = 0; k < DPL; ++k) {
+      float dtv = ds[k];
+      if (MODE == HCLSM_SCAN_MODEL) dtv = fminf(fmaxf(dtv, 1e-3f), 1.0f);
+      // MODEL mode: |dt*A| <= 1 < 20, so the [-20, 0] clamp of ssm_scan_kernel.py:77 never binds.
+      const float u = dtv * xs[k];
+      float y0 = 0.f, y1 = 0.f;
+#pragma unroll
+      for (int s = 0; s < SP; ++s) {
+        const float g = fast_exp2(dtv * a2[k][s]);
+        h[k][s] = fmaf(g, h[k][s], u * bv[s]);
+        if (s & 1) y1 = fmaf(h[k][s], cv[s], y1); else y0 = fmaf(h[k][s], cv[s], y0);
+      }
+      float yv = y0 + y1;
+      if (has_d) yv = fmaf(dsk[k], xs[k], yv);
+      yo[k] = yv;
+    }
+    if (act) st_pair(yp + (size_t)t * Dn, yo);
+#pragma unroll
+    for (int i = 0; i < NW; ++i) { bw[i] = bwn[i]; cw[i] = cwn[i]; }
+  };
+
+  xd_load(0, xv, dv);
+  const int tfull = T - T % TC;
+  for (int t0 = 0; t0 < tfull; t0 += TC) {
+    float xn[TC][DPL], dn[TC][DPL];
+    xd_load(t0 + TC, xn, dn);
+#pragma unroll
+    for (int j = 0; j < TC; ++j) step(t0 + j, xv[j], dv[j]);
+#pragma unroll
+    for (int j = 0; j < TC; ++j)
+#pragma unroll
+      for (int k = 0; k < DPL; ++k) { xv[j][k] = xn[j][k]; dv[j][k] = dn[j][k]; }
+  }
+  // tail (T % TC steps): xv/dv already hold them
+#pragma unroll
+  for (int j = 0; j < TC - 1; ++j)
+    if (tfull + j < T) step(tfull + j, xv[j], dv[j]);
+
+  if (h_final != nullptr && act) {
+#pragma unroll
+    for (int k = 0; k < DPL; ++k) {
+      float* hp = h_final + ((size_t)n * Dn + d0 + k) * SP;
+#pragma unroll
+      for (int s = 0; s < SP; ++s) hp[s] = h[k][s];
+    }
+  }
+}
+
+template <int DT, int SP, int MODE, int DPL, int TC>
+static int launch_scan_sgpr(const void* x, const void* dt, const float* A_log, const void* B,
+                            const void* C, const float* Dskip, void* y, float* h_final,
+                            int64_t batch, int64_t T, int64_t Dn, hipStream_t st) {
+  using TT = typename Elem<DT>::T;
+  const int64_t lanes = (Dn + DPL - 1) / DPL;
+  dim3 grid((unsigned)batch, (unsigned)((lanes + 63) / 64));
+  hipLaunchKernelGGL((ssm_scan_fwd_sgpr_kernel<DT, SP, MODE, DPL, TC>), grid, dim3(64), 0, st,
+                     (const TT*)x, (const TT*)dt, A_log, (const TT*)B, (const TT*)C, Dskip,
+                     (TT*)y, h_final, (int)T, (int)Dn);
+  HCLSM_LAUNCH_CHECK();
+  return 0;
+}
+
+static inline bool aligned(const void* p, uintptr_t a) { return (((uintptr_t)p) & (a - 1)) == 0; }
+
+// Returns 1 if no fast kernel applies (caller falls back to the generic kernel).
+template <int DT, int MODE>
+static int try_scan_sgpr(const void* x, const void* dt, const float* A_log, const void* B,
+                         const void* C, const float* Dskip, void* y, float* h_final,
+                         int64_t batch, int64_t T, int64_t Dn, int64_t S, hipStream_t st) {
+  constexpr int ES = (int)sizeof(typename Elem<DT>::T);
+  if (!aligned(B, 4) || !aligned(C, 4)) return 1;
+  const bool pair = (Dn % 2 == 0) && aligned(x, 2 * ES) && aligned(dt, 2 * ES) && aligned(y, 2 * ES);
+#define HCLSM_SCAN_SGPR(SPV)                                                                      \
+  if (S == SPV) {                                                                                  \
+    if (pair) return launch_scan_sgpr<DT, SPV, MODE, 2, 4>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, st); \
+    return launch_scan_sgpr<DT, SPV, MODE, 1, 8>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, st); \
+  }
+  if constexpr (DT == HCLSM_BF16) {
+    HCLSM_SCAN_SGPR(4)
+    HCLSM_SCAN_SGPR(8)
+    HCLSM_SCAN_SGPR(16)
+  } else if constexpr (DT == HCLSM_F32) {
+    HCLSM_SCAN_SGPR(4)
+    HCLSM_SCAN_SGPR(8)
+    HCLSM_SCAN_SGPR(16)
+  }
+#undef HCLSM_SCAN_SGPR
+  return 1;
+}
+
 template <int DT, int SP, int MODE>
 static int launch_scan(const void* x, const void* dt, const float* A_log, const void* B,
                        const void* C, const float* Dskip, void* y, float* h_final,
@@ -201,6 +409,14 @@ template <int DT, int SP>
 static int dispatch_mode(int mode, const void* x, const void* dt, const float* A_log, const void* B,
                          const void* C, const float* Dskip, void* y, float* h_final,
                          int64_t batch, int64_t T, int64_t Dn, int64_t S, hipStream_t st) {
+  if constexpr (DT == HCLSM_BF16 || DT == HCLSM_F32) {
+    if (SP == S) {
+      const int r = (mode == HCLSM_SCAN_RAW)
+          ? try_scan_sgpr<DT, HCLSM_SCAN_RAW>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, S, st)
+          : try_scan_sgpr<DT, HCLSM_SCAN_MODEL>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, S, st);
+      if (r != 1) return r;
+    }
+  }
   if (mode == HCLSM_SCAN_RAW)
     return launch_scan<DT, SP, HCLSM_SCAN_RAW>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, S, st);
   return launch_scan<DT, SP, HCLSM_SCAN_MODEL>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, S, st);

@@ -1,0 +1,68 @@
+"""The C-ABI library loads without a GPU and exports every entry point of include/hclsm_amd.h.
+
+No compute calls here (there is no GPU in the CPU test environment); argument
+validation that happens before any launch is exercised with NULL device pointers.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "hclsm_amd.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(hclsm_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from hclsm_amd import _lib
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libhclsm_amd.so not built (run python -m hclsm_amd.build)")
+    return _lib.lib()
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    assert "hclsm_ssm_scan_fwd" in names and "hclsm_abi_version" in names
+
+
+def test_every_declared_symbol_is_exported(lib):
+    from hclsm_amd import _lib
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (hclsm_[a-z0-9_]+)$", out, flags=re.M))
+    missing = [n for n in _declared() if n not in exported]
+    assert not missing, f"declared in the header but not exported: {missing}"
+    for n in _declared():
+        assert hasattr(lib, n)
+    # the Python binding declares argtypes for exactly the header's entry points
+    assert sorted(_lib.exported_symbols()) == _declared()
+
+
+def test_version_and_strerror(lib):
+    from hclsm_amd import _lib
+    assert lib.hclsm_abi_version() == 1
+    for code in (0, -1, -2, -3, -4, -5):
+        assert _lib.strerror(code)
+    assert "unknown" in _lib.strerror(-999)
+
+
+def test_argument_errors_before_launch(lib):
+    f = lib.hclsm_ssm_scan_fwd
+    # negative size, bad dtype, bad mode, oversized d_state, NULL pointer: all rejected on the host
+    assert f(None, None, None, None, None, None, None, None, -1, 4, 4, 4, 0, 0, None) == -2
+    assert f(None, None, None, None, None, None, None, None, 1, 4, 4, 4, 7, 0, None) == -3
+    assert f(None, None, None, None, None, None, None, None, 1, 4, 4, 4, 0, 9, None) == -5
+    assert f(None, None, None, None, None, None, None, None, 1, 4, 4, 65, 0, 0, None) == -4
+    assert f(None, None, None, None, None, None, None, None, 1, 4, 4, 4, 0, 0, None) == -1
+    # empty problem: nothing to launch, success
+    assert f(None, None, None, None, None, None, None, None, 0, 4, 4, 4, 0, 0, None) == 0
