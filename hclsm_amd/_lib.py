@@ -15,8 +15,10 @@ import torch  # noqa: F401  (must precede the CDLL load, see module docstring)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libhclsm_amd.so"
 
-F32, BF16, F16 = 0, 1, 2
+F32, BF16, F16, U8 = 0, 1, 2, 3
 SCAN_RAW, SCAN_MODEL = 0, 1
+EVENT_GT_HALF, EVENT_NONZERO = 0, 1
+ATTN_TRACK_CAUSAL, ATTN_SLOTS = 0, 1
 
 _c_void_p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -28,6 +30,12 @@ _SIGNATURES: dict[str, list] = {
     "hclsm_abi_version": [],
     "hclsm_strerror": [_int],
     "hclsm_ssm_scan_fwd": [_c_void_p] * 8 + [_i64] * 4 + [_int, _int, _c_void_p],
+    "hclsm_event_index": [_c_void_p, _int, _i64, _i64, _int] + [_c_void_p] * 6 + [_c_void_p],
+    "hclsm_event_gather": [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64] + [_c_void_p] * 3 + [_c_void_p],
+    "hclsm_event_gather_packed": [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64] + [_c_void_p] * 3 + [_c_void_p],
+    "hclsm_event_scatter": [_c_void_p] * 3 + [_i64] * 4 + [_c_void_p, _c_void_p],
+    "hclsm_event_scatter_packed": [_c_void_p] * 3 + [_i64] * 3 + [_c_void_p, _c_void_p, _c_void_p],
+    "hclsm_event_attention": [_c_void_p] * 8 + [_i64] * 5 + [_f32, _int, _int, _c_void_p],
 }
 _RESTYPES = {"hclsm_strerror": ctypes.c_char_p}
 

@@ -1,0 +1,272 @@
+// Variable-length event attention for gfx950 (MFMA).
+//
+// A "segment" p is a list of rows of a [P, T, H, dh] tensor given by int32
+// offsets/indices (the event index): rows (p, indices[offsets[p] + i]), i < L_p.
+//   TRACK_CAUSAL: query i attends keys j <= i of its segment (BASELINE config 3/4).
+//   SLOTS:        query i attends every key j of its segment not flagged in
+//                 key_pad[p, j] (the N x N attention of Level-1, level1_event.py:37-52).
+//
+// One wave owns one (segment, head) and walks 16-row query tiles x 16-row key
+// tiles with an online softmax.  Scores are formed transposed, S^T = K Q^T, and the
+// output as O^T = V^T P^T, both with v_mfma_f32_16x16x16_{bf16,f16} (or the
+// 16x16x4 f32 form for fp32 inputs).  With that orientation every lane owns one
+// query row (i = lane % 16) in all three tiles:
+//   S^T tile  : lane holds keys j = 4g + r (g = lane / 16, r = 0..3) of its query,
+//   P^T       : those same values are exactly the B operand of the O^T product,
+//   O^T tile  : lane holds dh/4 contiguous output columns of its query row.
+// The head dimension inside the K.Q^T contraction is permuted so that a lane's
+// K and Q operands are dh/4 contiguous elements of one row, and the output
+// columns are permuted so that the lane's V operand is dh/16 contiguous elements
+// per key and its output is dh/4 contiguous elements: every global access of the
+// kernel is a contiguous per-lane vector, and no LDS or barrier is needed.
+// Softmax statistics (max, sum) are per query: reduced over r in-lane and over
+// the four lanes {i, i+16, i+32, i+48} with two xor shuffles.
+#include "common.h"
+
+namespace hclsm {
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Element-type traits: KPL = k-values per lane per MFMA (K = 4*KPL).
+template <int DT> struct AttnT;
+template <> struct AttnT<HCLSM_BF16> {
+  using T = uint16_t;
+  static constexpr int KPL = 4;
+  using Op = s16x4;
+  static __device__ __forceinline__ float f(T v) { return bf16_bits_to_f32(v); }
+  static __device__ __forceinline__ T from(float v) { return f32_to_bf16_bits(v); }
+  static __device__ __forceinline__ Op pack(const T* e) {
+    Op o;
+    o[0] = (short)e[0]; o[1] = (short)e[1]; o[2] = (short)e[2]; o[3] = (short)e[3];
+    return o;
+  }
+  static __device__ __forceinline__ Op pack_f(const float* x) {
+    T e[4] = {from(x[0]), from(x[1]), from(x[2]), from(x[3])};
+    return pack(e);
+  }
+  static __device__ __forceinline__ f32x4 mfma(Op a, Op b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct AttnT<HCLSM_F16> {
+  using T = _Float16;
+  static constexpr int KPL = 4;
+  using Op = f16x4;
+  static __device__ __forceinline__ float f(T v) { return (float)v; }
+  static __device__ __forceinline__ T from(float v) { return (_Float16)v; }
+  static __device__ __forceinline__ Op pack(const T* e) {
+    Op o;
+    o[0] = e[0]; o[1] = e[1]; o[2] = e[2]; o[3] = e[3];
+    return o;
+  }
+  static __device__ __forceinline__ Op pack_f(const float* x) {
+    Op o;
+    o[0] = (_Float16)x[0]; o[1] = (_Float16)x[1]; o[2] = (_Float16)x[2]; o[3] = (_Float16)x[3];
+    return o;
+  }
+  static __device__ __forceinline__ f32x4 mfma(Op a, Op b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct AttnT<HCLSM_F32> {
+  using T = float;
+  static constexpr int KPL = 1;
+  using Op = float;
+  static __device__ __forceinline__ float f(T v) { return v; }
+  static __device__ __forceinline__ T from(float v) { return v; }
+  static __device__ __forceinline__ Op pack(const T* e) { return e[0]; }
+  static __device__ __forceinline__ Op pack_f(const float* x) { return x[0]; }
+  static __device__ __forceinline__ f32x4 mfma(Op a, Op b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+  }
+};
+
+constexpr int ATTN_WAVES = 4;
+
+// Load n contiguous elements (n a compile-time constant) from p into e[].
+template <typename T, int N>
+__device__ __forceinline__ void load_row(const T* __restrict__ p, T* e) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) e[i] = p[i];
+}
+
+template <int DT, int DH, int MODE>
+__global__ void __launch_bounds__(64 * ATTN_WAVES)
+event_attn_kernel(const typename AttnT<DT>::T* __restrict__ q, const typename AttnT<DT>::T* __restrict__ k,
+                  const typename AttnT<DT>::T* __restrict__ v, typename AttnT<DT>::T* __restrict__ out_packed,
+                  typename AttnT<DT>::T* __restrict__ out_grid, const int32_t* __restrict__ offsets,
+                  const int32_t* __restrict__ indices, const uint8_t* __restrict__ key_pad,
+                  int64_t nseg, int64_t T, int H, int64_t capacity, float scale_log2) {
+  using A = AttnT<DT>;
+  using TT = typename A::T;
+  constexpr int QD = DH / 4;          // contiguous head columns per lane
+  constexpr int NT = DH / 16;         // output tiles of 16 columns
+  constexpr int KPL = A::KPL;
+  constexpr int NCH = QD / KPL;       // MFMAs per 16x16 score tile
+  static_assert(DH % 16 == 0, "head dim must be a multiple of 16");
+
+  const int64_t wave = (int64_t)blockIdx.x * ATTN_WAVES + (threadIdx.x >> 6);
+  if (wave >= nseg * H) return;  // whole wave exits
+  const int64_t p = wave / H;
+  const int h = (int)(wave - p * H);
+  const int lane = threadIdx.x & 63, g = lane >> 4, li = lane & 15;
+  const int32_t base = offsets[p];
+  const int L = offsets[p + 1] - base;
+  if (L <= 0) return;
+  const int64_t rstride = (int64_t)H * DH;
+  auto row_ptr = [&](const TT* t, int i) -> const TT* {
+    const int ic = i < L ? i : L - 1;  // clamp: always a valid row of this segment
+    int64_t tr = indices[base + ic];
+    tr = tr < 0 ? 0 : (tr >= T ? T - 1 : tr);
+    return t + ((int64_t)p * T + tr) * rstride + (int64_t)h * DH;
+  };
+
+  const int nqt = (L + 15) >> 4;
+  for (int qt = 0; qt < nqt; ++qt) {
+    const int i = qt * 16 + li;
+    TT qe[QD];
+    load_row<TT, QD>(row_ptr(q, i) + g * QD, qe);
+    float m = -INFINITY, l = 0.f;
+    float acc[4][NT];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) acc[r][nt] = 0.f;
+
+    const int kt_end = (MODE == 0) ? qt : nqt - 1;   // MODE 0 = track-causal
+    for (int kt = 0; kt <= kt_end; ++kt) {
+      TT ke[QD];
+      load_row<TT, QD>(row_ptr(k, kt * 16 + li) + g * QD, ke);
+      f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) s4 = A::mfma(A::pack(ke + c * KPL), A::pack(qe + c * KPL), s4);
+      // s4[r] = S[query i][key j = kt*16 + 4g + r]
+      float s[4];
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = kt * 16 + 4 * g + r;
+        bool ok = (i < L) && (j < L);
+        if (MODE == 0) ok = ok && (j <= i);
+        else if (key_pad != nullptr) {
+          int64_t tj = indices[base + (j < L ? j : L - 1)];
+          tj = tj < 0 ? 0 : (tj >= T ? T - 1 : tj);
+          ok = ok && (key_pad[p * T + tj] == 0);
+        }
+        s[r] = ok ? s4[r] * scale_log2 : -INFINITY;
+        tmax = fmaxf(tmax, s[r]);
+      }
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      const float m_new = fmaxf(m, tmax);
+      float pr[4], psum = 0.f;
+      float alpha = 1.f;
+      if (m_new != -INFINITY) {
+        alpha = fast_exp2(m - m_new);   // m == -inf -> 0
+#pragma unroll
+        for (int r = 0; r < 4; ++r) { pr[r] = fast_exp2(s[r] - m_new); psum += pr[r]; }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pr[r] = 0.f;
+      }
+      psum += __shfl_xor(psum, 16, 64);
+      psum += __shfl_xor(psum, 32, 64);
+      l = l * alpha + psum;
+      m = m_new;
+      // V operand: keys j = kt*16 + 4g + r, columns NT*li .. NT*li + NT - 1
+      TT ve[4][NT];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) load_row<TT, NT>(row_ptr(v, kt * 16 + 4 * g + r) + NT * li, ve[r]);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        f32x4 o4 = {acc[0][nt] * alpha, acc[1][nt] * alpha, acc[2][nt] * alpha, acc[3][nt] * alpha};
+        if constexpr (KPL == 4) {
+          TT a_e[4] = {ve[0][nt], ve[1][nt], ve[2][nt], ve[3][nt]};
+          o4 = A::mfma(A::pack(a_e), A::pack_f(pr), o4);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o4 = A::mfma(ve[r][nt], pr[r], o4);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r][nt] = o4[r];
+      }
+    }
+    if (i < L) {
+      const float inv = 1.f / l;   // l == 0 (every key padded) -> NaN output, as softmax over all -inf
+      TT o[QD];
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) o[r * NT + nt] = A::from(acc[r][nt] * inv);
+      if (out_packed && (int64_t)base + i < capacity) {
+        TT* dst = out_packed + ((int64_t)base + i) * rstride + (int64_t)h * DH + g * QD;
+#pragma unroll
+        for (int e = 0; e < QD; ++e) dst[e] = o[e];
+      }
+      if (out_grid) {
+        int64_t tr = indices[base + i];
+        tr = tr < 0 ? 0 : (tr >= T ? T - 1 : tr);
+        TT* dst = out_grid + ((int64_t)p * T + tr) * rstride + (int64_t)h * DH + g * QD;
+#pragma unroll
+        for (int e = 0; e < QD; ++e) dst[e] = o[e];
+      }
+    }
+  }
+}
+
+template <int DT, int DH>
+static int launch_attn(int mode, const void* q, const void* k, const void* v, void* outp, void* outg,
+                       const int32_t* offsets, const int32_t* indices, const uint8_t* kp, int64_t nseg,
+                       int64_t T, int H, int64_t cap, float scale, hipStream_t st) {
+  using TT = typename AttnT<DT>::T;
+  const int64_t waves = nseg * H;
+  const unsigned grid = (unsigned)((waves + ATTN_WAVES - 1) / ATTN_WAVES);
+  const float sl2 = scale * HCLSM_LOG2E;
+  if (mode == HCLSM_ATTN_TRACK_CAUSAL)
+    hipLaunchKernelGGL((event_attn_kernel<DT, DH, 0>), dim3(grid), dim3(64 * ATTN_WAVES), 0, st, (const TT*)q,
+                       (const TT*)k, (const TT*)v, (TT*)outp, (TT*)outg, offsets, indices, kp, nseg, T, H, cap, sl2);
+  else
+    hipLaunchKernelGGL((event_attn_kernel<DT, DH, 1>), dim3(grid), dim3(64 * ATTN_WAVES), 0, st, (const TT*)q,
+                       (const TT*)k, (const TT*)v, (TT*)outp, (TT*)outg, offsets, indices, kp, nseg, T, H, cap, sl2);
+  HCLSM_LAUNCH_CHECK();
+  return 0;
+}
+
+template <int DT>
+static int dispatch_dh(int dh, int mode, const void* q, const void* k, const void* v, void* outp, void* outg,
+                       const int32_t* offsets, const int32_t* indices, const uint8_t* kp, int64_t nseg,
+                       int64_t T, int H, int64_t cap, float scale, hipStream_t st) {
+  switch (dh) {
+    case 16: return launch_attn<DT, 16>(mode, q, k, v, outp, outg, offsets, indices, kp, nseg, T, H, cap, scale, st);
+    case 32: return launch_attn<DT, 32>(mode, q, k, v, outp, outg, offsets, indices, kp, nseg, T, H, cap, scale, st);
+    case 64: return launch_attn<DT, 64>(mode, q, k, v, outp, outg, offsets, indices, kp, nseg, T, H, cap, scale, st);
+    case 128: return launch_attn<DT, 128>(mode, q, k, v, outp, outg, offsets, indices, kp, nseg, T, H, cap, scale, st);
+    default: return HCLSM_ERR_UNSUPPORTED;
+  }
+}
+
+}  // namespace hclsm
+
+extern "C" int hclsm_event_attention(const void* q, const void* k, const void* v, void* out_packed, void* out_grid,
+                                     const int32_t* offsets, const int32_t* indices, const uint8_t* key_pad,
+                                     int64_t nseg, int64_t T, int64_t H, int64_t dh, int64_t capacity,
+                                     float scale, int dtype, int mode, void* stream) {
+  using namespace hclsm;
+  if (nseg < 0 || T < 0 || H < 0 || dh < 0 || capacity < 0 || nseg * T > 0x7fffffffLL) return HCLSM_ERR_SHAPE;
+  if (mode != HCLSM_ATTN_TRACK_CAUSAL && mode != HCLSM_ATTN_SLOTS) return HCLSM_ERR_MODE;
+  if (dtype != HCLSM_F32 && dtype != HCLSM_BF16 && dtype != HCLSM_F16) return HCLSM_ERR_DTYPE;
+  if (dh != 16 && dh != 32 && dh != 64 && dh != 128) return HCLSM_ERR_UNSUPPORTED;
+  if (nseg == 0 || H == 0 || T == 0) return 0;
+  if (!q || !k || !v || !offsets || !indices || (!out_packed && !out_grid)) return HCLSM_ERR_NULL;
+  hipStream_t st = (hipStream_t)stream;
+  switch (dtype) {
+    case HCLSM_BF16:
+      return dispatch_dh<HCLSM_BF16>((int)dh, mode, q, k, v, out_packed, out_grid, offsets, indices, key_pad, nseg, T, (int)H, capacity, scale, st);
+    case HCLSM_F16:
+      return dispatch_dh<HCLSM_F16>((int)dh, mode, q, k, v, out_packed, out_grid, offsets, indices, key_pad, nseg, T, (int)H, capacity, scale, st);
+    default:
+      return dispatch_dh<HCLSM_F32>((int)dh, mode, q, k, v, out_packed, out_grid, offsets, indices, key_pad, nseg, T, (int)H, capacity, scale, st);
+  }
+}

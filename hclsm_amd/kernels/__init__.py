@@ -17,6 +17,24 @@ from hclsm_amd.kernels.ssm_scan_kernel import (
     fused_ssm_scan_hip,
 )
 
+from hclsm_amd.kernels.sparse_event_attn import (
+    sparse_event_attn_fn,
+    naive_sparse_event_attention,
+    sparse_event_attention,
+    EventIndex,
+    build_event_index,
+    gather_events_padded,
+    scatter_events_padded,
+    gather_packed,
+    scatter_packed,
+)
+
+from hclsm_amd.kernels.event_attention import (
+    event_attention,
+    track_causal_event_attention,
+    slots_attention,
+)
+
 TRITON_AVAILABLE = False
 
 
@@ -37,6 +55,18 @@ __all__ = [
     "parallel_ssm_scan_pytorch",
     "fused_ssm_scan_triton",
     "fused_ssm_scan_hip",
+    "sparse_event_attn_fn",
+    "naive_sparse_event_attention",
+    "sparse_event_attention",
+    "EventIndex",
+    "build_event_index",
+    "gather_events_padded",
+    "scatter_events_padded",
+    "gather_packed",
+    "scatter_packed",
+    "event_attention",
+    "track_causal_event_attention",
+    "slots_attention",
     "TRITON_AVAILABLE",
     "HIP_AVAILABLE",
 ]

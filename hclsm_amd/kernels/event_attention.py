@@ -1,0 +1,116 @@
+"""Variable-length event attention on MFMA (libhclsm_amd.so: hclsm_event_attention).
+
+Two semantics over the same kernel:
+
+  * ``track_causal``: for each track, causal softmax attention among that track's event
+    timesteps (the sparse Level-1 event attention of the benchmark configurations: per-track
+    segments packed by int32 prefix-sum offsets).
+  * ``slots``: for each (batch, event) problem, attention across its N slot rows with a key
+    padding mask -- the attention core of ``nn.MultiheadAttention`` inside
+    ``EventTransformerBlock`` (reference dynamics/level1_event.py:37-52; projections stay
+    outside, as in MHA's in_proj / out_proj).
+
+Inputs are (P, T, H, dh) tensors on the GPU (bf16, fp16 or fp32; softmax and accumulation
+in fp32); dh in {16, 32, 64, 128}.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from hclsm_amd import _lib
+from hclsm_amd.kernels._common import require_gpu
+from hclsm_amd.kernels.sparse_event_attn import EventIndex, build_event_index
+
+_MODES = {"track_causal": _lib.ATTN_TRACK_CAUSAL, "slots": _lib.ATTN_SLOTS}
+
+
+def _check_qkv(q, k, v):
+    if q.dim() != 4 or k.shape != q.shape or v.shape != q.shape:
+        raise ValueError(f"q, k, v must share a (P, T, H, dh) shape, got {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
+    if not (q.dtype == k.dtype == v.dtype) or q.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise TypeError("q, k, v must share one dtype among bfloat16, float16, float32")
+
+
+def event_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, index: EventIndex,
+                    mode: str = "track_causal", scale: float | None = None,
+                    key_pad: torch.Tensor | None = None, out: str = "packed",
+                    capacity: int | None = None, out_grid: torch.Tensor | None = None) -> torch.Tensor:
+    """Attention over the segments of ``index`` (segment p = rows (p, indices[offsets[p]:offsets[p+1]])).
+
+    out="packed": returns (capacity, H, dh) with row offsets[p] + i = query i of segment p
+        (capacity defaults to index.total(), one host read);
+    out="grid":   returns (P, T, H, dh) holding the outputs at the query rows; other rows are
+        copied from ``out_grid`` if given (written in place) or zero.
+    """
+    require_gpu("event_attention", q, k, v, key_pad)
+    _check_qkv(q, k, v)
+    P, T, H, dh = q.shape
+    if (index.B, index.T) != (P, T):
+        raise ValueError(f"event index is for ({index.B}, {index.T}) but q is ({P}, {T}, ...)")
+    qc, kc, vc = q.contiguous(), k.contiguous(), v.contiguous()
+    kp = None
+    if key_pad is not None:
+        if key_pad.shape != (P, T):
+            raise ValueError(f"key_pad must be ({P}, {T}), got {tuple(key_pad.shape)}")
+        kp = key_pad.to(torch.uint8).contiguous()
+    if scale is None:
+        scale = dh ** -0.5
+    outp = outg = None
+    cap = 0
+    if out == "packed":
+        cap = index.total() if capacity is None else int(capacity)
+        outp = torch.empty((max(cap, 0), H, dh), dtype=q.dtype, device=q.device)
+        result = outp
+    elif out == "grid":
+        outg = out_grid if out_grid is not None else torch.zeros_like(qc)
+        if outg.shape != qc.shape or outg.dtype != qc.dtype or not outg.is_contiguous():
+            raise ValueError("out_grid must be a contiguous tensor shaped and typed like q")
+        result = outg
+    else:
+        raise ValueError(f"out must be 'packed' or 'grid', got {out!r}")
+    rc = _lib.lib().hclsm_event_attention(
+        _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), _lib.ptr(outp), _lib.ptr(outg),
+        _lib.ptr(index.offsets), _lib.ptr(index.indices), _lib.ptr(kp), P, T, H, dh, max(cap, 0), float(scale),
+        _lib.dtype_code(q.dtype), _MODES[mode], _lib.stream_of(qc))
+    _lib.check(rc, "hclsm_event_attention")
+    return result
+
+
+def track_causal_event_attention(q, k, v, event_mask, scale=None, out="packed", rule="gt_half"):
+    """Per-track causal attention among the event timesteps of ``event_mask`` (P, T).
+    Returns (packed output, event index)."""
+    idx = build_event_index(event_mask, rule)
+    return event_attention(q, k, v, idx, "track_causal", scale=scale, out=out), idx
+
+
+_DENSE_CACHE: dict = {}
+
+
+def _dense_index(P: int, N: int, device) -> EventIndex:
+    key = (P, N, str(device))
+    idx = _DENSE_CACHE.get(key)
+    if idx is None:
+        i32 = dict(dtype=torch.int32, device=device)
+        offsets = torch.arange(0, (P + 1) * N, N, **i32)
+        indices = torch.arange(N, **i32).repeat(P)
+        rows = torch.arange(P, **i32).repeat_interleave(N)
+        slot_of = torch.arange(N, **i32).repeat(P, 1)
+        stats = torch.tensor([P * N, N], **i32)
+        idx = EventIndex(P, N, torch.full((P,), N, **i32), offsets, indices, rows, slot_of, stats)
+        if len(_DENSE_CACHE) > 64:
+            _DENSE_CACHE.clear()
+        _DENSE_CACHE[key] = idx
+    return idx
+
+
+def slots_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                    key_padding_mask: torch.Tensor | None = None, scale: float | None = None) -> torch.Tensor:
+    """Attention across the N slot rows of each of P problems: q, k, v (P, N, H, dh);
+    key_padding_mask (P, N) bool, True = ignore that key (nn.MultiheadAttention's convention).
+    Returns (P, N, H, dh).  A query with every key padded returns NaN, like the reference."""
+    require_gpu("slots_attention", q, k, v, key_padding_mask)
+    P, N = q.shape[:2]
+    idx = _dense_index(P, N, q.device)
+    return event_attention(q, k, v, idx, "slots", scale=scale, key_pad=key_padding_mask, out="grid",
+                           out_grid=torch.empty_like(q.contiguous()))

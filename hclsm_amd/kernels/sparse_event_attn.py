@@ -1,0 +1,270 @@
+"""Sparse event attention plumbing on MI355X -- drop-in for ``hclsm/kernels/sparse_event_attn.py``.
+
+Reference names kept (same positional signatures, defaults and return types):
+
+    naive_sparse_event_attention(states, event_mask, attn_fn, max_events=None)   (:35-86)
+    sparse_event_attention(states, event_mask, attn_fn, max_events=None)         (:153-188)
+    sparse_event_attn_fn(states, event_mask, attn_fn, max_events=None, backend="auto")  (:242-263)
+    _vectorized_gather(states, event_mask, max_events)                            (:93-131)
+    _vectorized_scatter(output, updated_events, event_indices, event_pad_mask)    (:134-150)
+
+Event index construction, gathers and scatters run on libhclsm_amd.so (bit-exact byte
+moves driven by int32 counts / offsets / ascending indices).  ``attn_fn`` is the caller's
+callable on the padded (B*K, N, D) batch, exactly as in the reference.
+
+Semantics:
+  * "naive" uses the reference's ``nonzero`` rule (mask != 0, :65); the vectorised path
+    and HierarchyManager use mask > 0.5 (:124, hierarchy_manager.py:61).
+  * ``max_events`` defaults to int(max row sum of the mask) as at :56 / :173; K = max(it, 1).
+  * Events past K in a row are dropped, earliest-first order kept (the reference's naive
+    path keeps idx[:K] in ascending order; its topk path breaks ties arbitrarily).
+  * Padded rows are exact zeros (the reference multiplies by the pad mask, which turns
+    inf/NaN source rows into NaN; here padding never reads the source).
+
+Packed, sync-free API (new): ``build_event_index`` / ``gather_packed`` / ``scatter_packed``
+work on device-side int32 tables and never read a size back to the host.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Callable
+
+import torch
+
+from hclsm_amd import _lib
+from hclsm_amd.kernels._common import require_gpu
+
+
+@dataclass
+class EventIndex:
+    """Device-side event tables of a (B, T) mask (all int32, built without host sync)."""
+    B: int
+    T: int
+    counts: torch.Tensor      # (B,)
+    offsets: torch.Tensor     # (B+1,)   exclusive prefix sum; offsets[B] = total
+    indices: torch.Tensor     # (B*T,)   capacity; first `total` are event timesteps
+    rows: torch.Tensor        # (B*T,)   capacity; row of each packed event
+    slot_of: torch.Tensor     # (B, T)   rank of t among row b's events, -1 otherwise
+    stats: torch.Tensor       # (2,)     {total, max count}
+
+    def total(self) -> int:
+        """Number of events (reads one int32 back to the host)."""
+        return int(self.stats[0].item())
+
+    def kmax(self) -> int:
+        return int(self.stats[1].item())
+
+
+def _mask_code(m: torch.Tensor):
+    if m.dtype == torch.float32:
+        return m, _lib.F32
+    if m.dtype == torch.bfloat16:
+        return m, _lib.BF16
+    if m.dtype == torch.float16:
+        return m, _lib.F16
+    if m.dtype in (torch.bool, torch.uint8):
+        return m.view(torch.uint8) if m.dtype == torch.bool else m, _lib.U8
+    return m.to(torch.float32), _lib.F32
+
+
+def build_event_index(event_mask: torch.Tensor, rule: str = "gt_half") -> EventIndex:
+    """Counts, int32 offsets and ascending indices of a (B, T) event mask, on the GPU."""
+    require_gpu("build_event_index", event_mask)
+    if event_mask.dim() != 2:
+        raise ValueError(f"event_mask must be (B, T), got {tuple(event_mask.shape)}")
+    rule_code = {"gt_half": _lib.EVENT_GT_HALF, "nonzero": _lib.EVENT_NONZERO}[rule]
+    m, code = _mask_code(event_mask.detach().contiguous())
+    B, T = m.shape
+    dev = m.device
+    i32 = dict(dtype=torch.int32, device=dev)
+    idx = EventIndex(B, T, torch.empty(B, **i32), torch.empty(B + 1, **i32), torch.empty(max(B * T, 1), **i32),
+                     torch.empty(max(B * T, 1), **i32), torch.empty((B, T), **i32), torch.empty(2, **i32))
+    rc = _lib.lib().hclsm_event_index(_lib.ptr(m), code, B, T, rule_code, _lib.ptr(idx.counts), _lib.ptr(idx.offsets),
+                                      _lib.ptr(idx.indices), _lib.ptr(idx.rows), _lib.ptr(idx.slot_of),
+                                      _lib.ptr(idx.stats), _lib.stream_of(m))
+    _lib.check(rc, "hclsm_event_index")
+    return idx
+
+
+def _row_bytes(t: torch.Tensor) -> int:
+    n = 1
+    for s in t.shape[2:]:
+        n *= s
+    return n * t.element_size()
+
+
+def _gather_padded_raw(states: torch.Tensor, idx: EventIndex, K: int) -> torch.Tensor:
+    src = states.contiguous()
+    out = torch.empty((src.shape[0], K) + tuple(src.shape[2:]), dtype=src.dtype, device=src.device)
+    rc = _lib.lib().hclsm_event_gather(_lib.ptr(src), _lib.ptr(out), _row_bytes(src), idx.B, idx.T, K,
+                                       _lib.ptr(idx.counts), _lib.ptr(idx.offsets), _lib.ptr(idx.indices),
+                                       _lib.stream_of(src))
+    _lib.check(rc, "hclsm_event_gather")
+    return out
+
+
+def _scatter_padded_raw(base, updates, idx: EventIndex, K: int, like: torch.Tensor) -> torch.Tensor:
+    b = None if base is None else base.contiguous()
+    u = None if updates is None else updates.contiguous()
+    out = torch.empty((idx.B, idx.T) + tuple(like.shape[2:]), dtype=like.dtype, device=like.device)
+    rc = _lib.lib().hclsm_event_scatter(_lib.ptr(b), _lib.ptr(u), _lib.ptr(out), _row_bytes(out), idx.B, idx.T, K,
+                                        _lib.ptr(idx.slot_of), _lib.stream_of(out))
+    _lib.check(rc, "hclsm_event_scatter")
+    return out
+
+
+class _GatherPadded(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, states, idx, K):
+        ctx.idx, ctx.K = idx, K
+        ctx.like = torch.empty((0, 0) + tuple(states.shape[2:]), dtype=states.dtype, device=states.device)
+        return _gather_padded_raw(states, idx, K)
+
+    @staticmethod
+    def backward(ctx, g):
+        # d states[b, t] = g[b, slot_of[b, t]] for event rows with slot < K, else 0
+        return _scatter_padded_raw(None, g, ctx.idx, ctx.K, ctx.like), None, None
+
+
+class _ScatterPadded(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, base, updates, idx, K):
+        ctx.idx, ctx.K = idx, K
+        if updates.dtype != base.dtype:
+            updates = updates.to(base.dtype)
+        return _scatter_padded_raw(base, updates, idx, K, base)
+
+    @staticmethod
+    def backward(ctx, g):
+        g = g.contiguous()
+        g_base = _scatter_padded_raw(g, None, ctx.idx, ctx.K, g)       # zero at replaced rows
+        g_upd = _gather_padded_raw(g, ctx.idx, ctx.K)                  # zero at padded slots
+        return g_base, g_upd, None, None
+
+
+def gather_events_padded(states: torch.Tensor, idx: EventIndex, K: int) -> torch.Tensor:
+    """(B, T, ...) -> (B, K, ...) event rows, ascending, zero rows past each row's count."""
+    require_gpu("gather_events_padded", states)
+    return _GatherPadded.apply(states, idx, int(K))
+
+
+def scatter_events_padded(base: torch.Tensor, updates: torch.Tensor, idx: EventIndex) -> torch.Tensor:
+    """out = base with out[b, t] = updates[b, slot_of[b,t]] for event rows whose slot < K."""
+    require_gpu("scatter_events_padded", base, updates)
+    return _ScatterPadded.apply(base, updates, idx, int(updates.shape[1]))
+
+
+def pad_mask_from_index(idx: EventIndex, K: int, dtype=torch.float32) -> torch.Tensor:
+    ar = torch.arange(K, device=idx.counts.device, dtype=torch.int32)
+    return (ar[None, :] < idx.counts[:, None]).to(dtype)
+
+
+def gather_packed(src: torch.Tensor, idx: EventIndex, capacity: int | None = None) -> torch.Tensor:
+    """(B, T, ...) -> (capacity, ...) packed event rows (first idx.total() valid); no host sync
+    when ``capacity`` is given."""
+    require_gpu("gather_packed", src)
+    s = src.contiguous()
+    cap = idx.B * idx.T if capacity is None else int(capacity)
+    out = torch.empty((cap,) + tuple(s.shape[2:]), dtype=s.dtype, device=s.device)
+    rc = _lib.lib().hclsm_event_gather_packed(_lib.ptr(s), _lib.ptr(out), _row_bytes(s), idx.B, idx.T, cap,
+                                              _lib.ptr(idx.rows), _lib.ptr(idx.indices), _lib.ptr(idx.stats),
+                                              _lib.stream_of(s))
+    _lib.check(rc, "hclsm_event_gather_packed")
+    return out
+
+
+def scatter_packed(base: torch.Tensor | None, packed: torch.Tensor, idx: EventIndex,
+                   out: torch.Tensor | None = None) -> torch.Tensor:
+    """out[b, t] = packed[offsets[b] + slot_of[b, t]] at events, base[b, t] elsewhere
+    (zeros if base is None)."""
+    require_gpu("scatter_packed", base, packed)
+    p = packed.contiguous()
+    b = None if base is None else base.contiguous()
+    if out is None:
+        out = torch.empty((idx.B, idx.T) + tuple(p.shape[1:]), dtype=p.dtype, device=p.device)
+    rb = out.element_size()
+    for s in out.shape[2:]:
+        rb *= s
+    rc = _lib.lib().hclsm_event_scatter_packed(_lib.ptr(b), _lib.ptr(p), _lib.ptr(out), rb, idx.B, idx.T,
+                                               _lib.ptr(idx.offsets), _lib.ptr(idx.slot_of), _lib.stream_of(p))
+    _lib.check(rc, "hclsm_event_scatter_packed")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# reference-named API
+# ---------------------------------------------------------------------------
+
+def _max_events_default(event_mask: torch.Tensor) -> int:
+    # sparse_event_attn.py:56 / :173 -- int() of the largest row sum (one host read)
+    return int(event_mask.float().sum(dim=1).max().item()) if event_mask.numel() else 0
+
+
+def _run(states, event_mask, attn_fn, max_events, rule):
+    require_gpu("sparse_event_attention", states, event_mask)
+    B, T, N, D = states.shape
+    if max_events is None:
+        max_events = _max_events_default(event_mask)
+    K = max(int(max_events), 1)
+    idx = build_event_index(event_mask, rule)
+    ev = gather_events_padded(states, idx, K)                    # (B, K, N, D)
+    upd = attn_fn(ev.reshape(B * K, N, D)).reshape(B, K, N, D)
+    return scatter_events_padded(states, upd, idx)
+
+
+def naive_sparse_event_attention(states: torch.Tensor, event_mask: torch.Tensor, attn_fn: Callable,
+                                 max_events: int | None = None) -> torch.Tensor:
+    """Gather events -> attn_fn -> scatter back (reference :35-86; rule mask != 0)."""
+    return _run(states, event_mask, attn_fn, max_events, "nonzero")
+
+
+def sparse_event_attention(states: torch.Tensor, event_mask: torch.Tensor, attn_fn: Callable,
+                           max_events: int | None = None) -> torch.Tensor:
+    """Vectorised variant (reference :153-188; rule mask > 0.5)."""
+    return _run(states, event_mask, attn_fn, max_events, "gt_half")
+
+
+def sparse_event_attn_fn(states: torch.Tensor, event_mask: torch.Tensor, attn_fn: Callable,
+                         max_events: int | None = None, backend: str = "auto") -> torch.Tensor:
+    """Dispatcher (reference :242-263): "naive" -> nonzero rule, anything else -> > 0.5 rule."""
+    if backend == "naive":
+        return naive_sparse_event_attention(states, event_mask, attn_fn, max_events)
+    return sparse_event_attention(states, event_mask, attn_fn, max_events)
+
+
+def _vectorized_gather(states: torch.Tensor, event_mask: torch.Tensor, max_events: int):
+    """Reference :93-131: returns (event_states (B,K,N,D), pad_mask (B,K) bool, indices (B,K) long).
+    Index entries past a row's count are 0 (the reference leaves them tie-dependent)."""
+    idx = build_event_index(event_mask, "gt_half")
+    K = int(max_events)
+    ev = gather_events_padded(states, idx, K)
+    pad = pad_mask_from_index(idx, K, torch.bool)
+    t_idx = gather_events_padded(torch.arange(idx.T, device=states.device, dtype=torch.int32)
+                                 .expand(idx.B, idx.T).contiguous().unsqueeze(-1), idx, K).squeeze(-1).long()
+    return ev, pad, t_idx
+
+
+def _vectorized_scatter(output: torch.Tensor, updated_events: torch.Tensor, event_indices: torch.Tensor,
+                        event_pad_mask: torch.Tensor) -> torch.Tensor:
+    """Reference :134-150: writes updated_events[b, k] to output[b, event_indices[b, k]] where the
+    pad mask is set (in place on ``output``, which is also returned).  Any index order works:
+    the (B, T) slot table is built from the given indices, then one scatter kernel runs."""
+    require_gpu("_vectorized_scatter", output, updated_events)
+    B, T = output.shape[:2]
+    K = updated_events.shape[1]
+    valid = event_pad_mask.bool()
+    slot_of = torch.full((B, T), -1, dtype=torch.int32, device=output.device)
+    ks = torch.arange(K, dtype=torch.int32, device=output.device).expand(B, K)
+    tgt = torch.where(valid, event_indices.long(), torch.full_like(event_indices.long(), T))
+    slot_pad = torch.cat([slot_of, slot_of[:, :1]], dim=1)            # column T absorbs invalid writes
+    slot_pad.scatter_(1, tgt, torch.where(valid, ks, torch.full_like(ks, -1)))
+    slot_of = slot_pad[:, :T].contiguous()
+    out = output.contiguous()
+    upd = updated_events.to(out.dtype).contiguous()
+    rc = _lib.lib().hclsm_event_scatter(_lib.ptr(out), _lib.ptr(upd), _lib.ptr(out), _row_bytes(out), B, T, K,
+                                        _lib.ptr(slot_of), _lib.stream_of(out))
+    _lib.check(rc, "hclsm_event_scatter")
+    if out.data_ptr() != output.data_ptr():
+        output.copy_(out)
+    return output

@@ -31,6 +31,15 @@ extern "C" {
 #define HCLSM_F32  0
 #define HCLSM_BF16 1
 #define HCLSM_F16  2
+#define HCLSM_U8   3  /* event masks only: bool / uint8 */
+
+/* event rules for masks */
+#define HCLSM_EVENT_GT_HALF 0 /* mask > 0.5: hierarchy_manager.py:61, sparse_event_attn.py:124 */
+#define HCLSM_EVENT_NONZERO 1 /* mask != 0 (NaN is an event): sparse_event_attn.py:65 */
+
+/* event attention modes */
+#define HCLSM_ATTN_TRACK_CAUSAL 0 /* causal over the events of one track (BASELINE configs 3/4) */
+#define HCLSM_ATTN_SLOTS        1 /* all rows of a segment, key padding (level1_event.py:37-52) */
 
 /* SSM scan clamp modes */
 #define HCLSM_SCAN_RAW   0  /* A=-exp(A_log), no clamps: ssm_scan_kernel.py:191, :255 */
@@ -69,6 +78,84 @@ int hclsm_ssm_scan_fwd(const void* x, const void* dt, const float* A_log,
                        void* y, float* h_final,
                        int64_t batch, int64_t T, int64_t d_inner, int64_t d_state,
                        int dtype, int mode, void* stream);
+
+/*
+ * Event index of a [B, T] mask, built on the device with no host synchronisation.
+ *   counts  [B]      int32  events per row
+ *   offsets [B+1]    int32  exclusive prefix sum of counts; offsets[B] = total
+ *   indices [B*T]    int32  capacity; first `total` hold the event timesteps, ascending
+ *                           within each row, rows concatenated
+ *   rows    [B*T]    int32  capacity, nullable; rows[e] = row of packed event e
+ *   slot_of [B, T]   int32  nullable; rank of t among row b's events, or -1
+ *   stats   [2]      int32  {total, max count}
+ * mask_dtype: HCLSM_F32 / BF16 / F16 / U8; rule: HCLSM_EVENT_GT_HALF / NONZERO (U8 masks: any nonzero).
+ * Replaces the index construction of HierarchyManager.gather_events (hierarchy_manager.py:59-67),
+ *   _vectorized_gather (sparse_event_attn.py:104-120) and the nonzero loop of
+ *   naive_sparse_event_attention (sparse_event_attn.py:64-70), and removes their .item() syncs
+ *   (hierarchy_manager.py:63, sparse_event_attn.py:56,173).
+ */
+int hclsm_event_index(const void* mask, int mask_dtype, int64_t B, int64_t T, int rule,
+                      int32_t* counts, int32_t* offsets, int32_t* indices, int32_t* rows,
+                      int32_t* slot_of, int32_t* stats, void* stream);
+
+/*
+ * Padded gather: dst[b, k, :] = src[b, indices[offsets[b]+k], :] for k < counts[b], zero bytes for
+ * counts[b] <= k < K.  src [B, T, row_bytes], dst [B, K, row_bytes]; any element type (byte copy).
+ * Replaces the gathers of HierarchyManager.gather_events (hierarchy_manager.py:69-75),
+ *   _vectorized_gather (sparse_event_attn.py:121-128) and the naive loop (:64-70); never launched
+ *   Triton _sparse_gather_kernel (:197-235).
+ */
+int hclsm_event_gather(const void* src, void* dst, int64_t row_bytes, int64_t B, int64_t T, int64_t K,
+                       const int32_t* counts, const int32_t* offsets, const int32_t* indices,
+                       void* stream);
+
+/*
+ * Packed gather: dst[e, :] = src[rows[e], indices[e], :] for e < min(stats[0], capacity); rows
+ * beyond the device-side total are left untouched.  dst [capacity, row_bytes].
+ * (No reference counterpart: the packed, sync-free layout of the event segments.)
+ */
+int hclsm_event_gather_packed(const void* src, void* dst, int64_t row_bytes, int64_t B, int64_t T,
+                              int64_t capacity, const int32_t* rows, const int32_t* indices,
+                              const int32_t* stats, void* stream);
+
+/*
+ * Padded scatter: out[b, t, :] = updates[b, s, :] where 0 <= s = slot_of[b, t] < K, else base[b, t, :].
+ * base / updates may be NULL (read as zero bytes); out may alias base.
+ * Replaces HierarchyManager.scatter_events (hierarchy_manager.py:79-118), _vectorized_scatter
+ *   (sparse_event_attn.py:134-150) and the naive scatter loop (:78-84).
+ */
+int hclsm_event_scatter(const void* base, const void* updates, void* out, int64_t row_bytes,
+                        int64_t B, int64_t T, int64_t K, const int32_t* slot_of, void* stream);
+
+/*
+ * Packed scatter: out[b, t, :] = packed[offsets[b] + s, :] where s = slot_of[b, t] >= 0, else base.
+ * base / packed may be NULL (zeros); out may alias base.  (Packed counterpart of the above.)
+ */
+int hclsm_event_scatter_packed(const void* base, const void* packed, void* out, int64_t row_bytes,
+                               int64_t B, int64_t T, const int32_t* offsets, const int32_t* slot_of,
+                               void* stream);
+
+/*
+ * Variable-length attention over event segments, on MFMA.
+ *   q, k, v   [nseg, T, H, dh]  element type `dtype` (bf16 / f16 / f32), contiguous
+ *   offsets   [nseg+1], indices [>= offsets[nseg]]  int32 (an event index: segment p is the rows
+ *             (p, indices[offsets[p] + i]), i < offsets[p+1] - offsets[p], in that order)
+ *   key_pad   [nseg, T] uint8, nullable; SLOTS mode ignores keys whose row is flagged nonzero
+ *   out_packed [capacity, H, dh], nullable: row offsets[p] + i = output of query i of segment p
+ *             (rows at or past `capacity` are not written)
+ *   out_grid   [nseg, T, H, dh], nullable: output written at the query's own row; other rows untouched
+ * mode TRACK_CAUSAL: query i attends keys j <= i; mode SLOTS: all unpadded keys of the segment.
+ * softmax in fp32 with `scale` applied to q.k; dh in {16, 32, 64, 128}.  A query whose keys are all
+ * padded produces NaN, as softmax over an all -inf row does in the reference.
+ * Replaces: the attention core of nn.MultiheadAttention in EventTransformerBlock
+ *   (dynamics/level1_event.py:37-52, SLOTS mode) and the per-track causal event attention of the
+ *   benchmark configuration (TRACK_CAUSAL), fed by the event index instead of the padded
+ *   gather of hierarchy_manager.py:42-77.
+ */
+int hclsm_event_attention(const void* q, const void* k, const void* v, void* out_packed, void* out_grid,
+                          const int32_t* offsets, const int32_t* indices, const uint8_t* key_pad,
+                          int64_t nseg, int64_t T, int64_t H, int64_t dh, int64_t capacity,
+                          float scale, int dtype, int mode, void* stream);
 
 #ifdef __cplusplus
 }

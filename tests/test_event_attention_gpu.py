@@ -1,0 +1,115 @@
+"""GPU parity of the MFMA event attention against the numpy oracle (oracle/events.py).
+
+Tolerances, normwise relative (max|got-ref|/max|ref|): fp32 1e-5; bf16/fp16 inputs with fp32
+softmax 2e-2 (oracle fed the rounded inputs)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import events as ev
+from oracle.ssm_scan import normwise_rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def _data(P, T, H, dh, dtype, p, seed, force0=True):
+    g = torch.Generator().manual_seed(seed)
+    q, k, v = (torch.randn(P, T, H, dh, generator=g).to(dtype) for _ in range(3))
+    m = (torch.rand(P, T, generator=g) < p).float()
+    if force0:
+        m[:, 0] = 1
+    return q, k, v, m
+
+
+def _np(t):
+    return t.float().cpu().numpy().astype(np.float64)
+
+
+def _run_causal(q, k, v, m, out="packed"):
+    from hclsm_amd.kernels.event_attention import track_causal_event_attention
+    o, idx = track_causal_event_attention(q.cuda(), k.cuda(), v.cuda(), m.cuda(), out=out)
+    torch.cuda.synchronize()
+    return o, idx
+
+
+def test_config3_bf16():
+    """1024 tracks, T=64, 6 heads x 64, p=0.15 with t=0 forced."""
+    q, k, v, m = _data(1024, 64, 6, 64, torch.bfloat16, 0.15, seed=1003)
+    o, _ = _run_causal(q, k, v, m)
+    i = ev.event_index(m.numpy())
+    ref = ev.track_causal_attention(_np(q), _np(k), _np(v), i)
+    assert o.shape == ref.shape
+    err = normwise_rel_err(_np(o), ref)
+    assert err <= 2e-2, f"config 3 normwise err {err:.3e}"
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.float16, 2e-2), (torch.bfloat16, 2e-2)])
+@pytest.mark.parametrize("dh", [16, 32, 64, 128])
+def test_dtypes_and_head_dims(dtype, tol, dh):
+    q, k, v, m = _data(9, 40, 3, dh, dtype, 0.5, seed=dh)
+    o, _ = _run_causal(q, k, v, m)
+    ref = ev.track_causal_attention(_np(q), _np(k), _np(v), ev.event_index(m.numpy()))
+    err = normwise_rel_err(_np(o), ref)
+    assert err <= tol, f"{dtype} dh={dh}: {err:.3e}"
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
+def test_long_segments_cross_many_key_tiles(dtype, tol):
+    q, k, v, m = _data(5, 300, 2, 64, dtype, 0.9, seed=7)
+    m[3] = 0                          # an empty track
+    m[4] = 0
+    m[4, 299] = 1                     # a single event at the last step
+    o, _ = _run_causal(q, k, v, m)
+    i = ev.event_index(m.numpy())
+    ref = ev.track_causal_attention(_np(q), _np(k), _np(v), i)
+    assert normwise_rel_err(_np(o), ref) <= tol
+    # segment of length one: output equals v at that row
+    last = i["offsets"][4]
+    np.testing.assert_allclose(_np(o[last]), _np(v[4, 299]), rtol=0, atol=0)
+
+
+def test_grid_output_leaves_other_rows():
+    from hclsm_amd.kernels.event_attention import event_attention
+    from hclsm_amd.kernels.sparse_event_attn import build_event_index
+    q, k, v, m = _data(6, 50, 2, 32, torch.float32, 0.3, seed=9)
+    base = torch.randn(6, 50, 2, 32)
+    idx = build_event_index(m.cuda())
+    og = base.cuda().clone()
+    event_attention(q.cuda(), k.cuda(), v.cuda(), idx, out="grid", out_grid=og)
+    i = ev.event_index(m.numpy())
+    ref = ev.scatter_packed(_np(base), ev.track_causal_attention(_np(q), _np(k), _np(v), i), i)
+    assert normwise_rel_err(_np(og), ref) <= 1e-5
+    nonev = (m < 0.5)
+    assert torch.equal(og.cpu()[nonev], base[nonev])
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
+def test_slots_mode_with_key_padding(dtype, tol):
+    from hclsm_amd.kernels.event_attention import slots_attention
+    g = torch.Generator().manual_seed(13)
+    P, N, H, dh = 40, 32, 6, 64               # small preset: 32 slots, 6 heads x 64
+    q, k, v = (torch.randn(P, N, H, dh, generator=g).to(dtype) for _ in range(3))
+    pad = torch.rand(P, N, generator=g) < 0.25
+    pad[:, 0] = False
+    out = slots_attention(q.cuda(), k.cuda(), v.cuda(), pad.cuda())
+    ref = ev.slots_attention(_np(q), _np(k), _np(v), key_pad=pad.numpy())
+    assert normwise_rel_err(_np(out), ref) <= tol
+    allpad = torch.ones(1, N, dtype=torch.bool)
+    o2 = slots_attention(q[:1].cuda(), k[:1].cuda(), v[:1].cuda(), allpad.cuda())
+    assert torch.isnan(o2).all()
+
+
+def test_against_torch_sdpa_on_gpu():
+    """Independent library check: per-track torch SDPA (fp32, math) on the GPU."""
+    import torch.nn.functional as F
+    q, k, v, m = _data(8, 48, 4, 64, torch.float32, 0.4, seed=21)
+    o, idx = _run_causal(q, k, v, m)
+    offs = idx.offsets.cpu().tolist()
+    for b in range(8):
+        ts = torch.nonzero(m[b] > 0.5).flatten()
+        qq, kk, vv = (t[b, ts].permute(1, 0, 2).cuda() for t in (q, k, v))
+        ref = F.scaled_dot_product_attention(qq, kk, vv, is_causal=True).permute(1, 0, 2)
+        assert torch.allclose(o[offs[b]:offs[b + 1]], ref, rtol=1e-4, atol=1e-5)
