@@ -36,6 +36,15 @@ _SIGNATURES: dict[str, list] = {
     "hclsm_event_scatter": [_c_void_p] * 3 + [_i64] * 4 + [_c_void_p, _c_void_p],
     "hclsm_event_scatter_packed": [_c_void_p] * 3 + [_i64] * 3 + [_c_void_p, _c_void_p, _c_void_p],
     "hclsm_event_attention": [_c_void_p] * 8 + [_i64] * 5 + [_f32, _int, _int, _c_void_p],
+    "hclsm_layer_norm": [_c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _f32, _int, _int,
+                         _c_void_p],
+    "hclsm_linear": [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _c_void_p, _i64, _int,
+                     _c_void_p, _i64, _i64, _i64, _i64, _int, _f32, _int, _c_void_p],
+    "hclsm_gru_cell": [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p,
+                       _c_void_p, _c_void_p, _i64, _c_void_p, _i64, _i64, _i64, _i64, _int, _c_void_p],
+    "hclsm_slot_attn_core": [_c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p,
+                             _i64, _i64, _c_void_p, _int, _i64, _i64, _i64, _i64, _f32, _f32, _f32, _f32,
+                             _int, _c_void_p],
 }
 _RESTYPES = {"hclsm_strerror": ctypes.c_char_p}
 

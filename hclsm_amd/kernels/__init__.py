@@ -35,6 +35,21 @@ from hclsm_amd.kernels.event_attention import (
     slots_attention,
 )
 
+from hclsm_amd.kernels.slot_attention_kernel import (
+    slot_attention_fn,
+    naive_slot_attention,
+    compiled_slot_attention,
+    fused_slot_attention_triton,
+)
+from hclsm_amd.kernels.slot_iteration import (
+    SlotMode,
+    SlotWeights,
+    REFERENCE_MODE,
+    CONFIG2_MODE,
+    slot_attention_iteration,
+    slot_attention_forward,
+)
+
 TRITON_AVAILABLE = False
 
 
@@ -50,6 +65,16 @@ def _hip_available() -> bool:
 HIP_AVAILABLE = _hip_available()
 
 __all__ = [
+    "slot_attention_fn",
+    "naive_slot_attention",
+    "compiled_slot_attention",
+    "fused_slot_attention_triton",
+    "SlotMode",
+    "SlotWeights",
+    "REFERENCE_MODE",
+    "CONFIG2_MODE",
+    "slot_attention_iteration",
+    "slot_attention_forward",
     "ssm_scan_fn",
     "sequential_ssm_scan",
     "parallel_ssm_scan_pytorch",

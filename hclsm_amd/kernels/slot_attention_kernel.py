@@ -1,0 +1,101 @@
+"""Slot attention on MI355X -- drop-in for ``hclsm/kernels/slot_attention_kernel.py``.
+
+Reference names kept (same positional signatures, defaults and return types):
+
+    slot_attention_fn(Q, K, V, scale=None, backend="auto") -> (out, attn)     (:324-355)
+    naive_slot_attention(Q, K, V, scale=None) -> (out, attn)                 (:265-291)
+    compiled_slot_attention(Q, K, V, scale=None) -> (out, attn)              (:308-317)
+    fused_slot_attention_triton(Q, K, V, scale=None) -> (out, attn)          (:239-258)
+
+All run ``hclsm_slot_attn_core`` (one MFMA workgroup per frame: logits, softmax over the
+slot axis, attn @ V).  Semantics per name, as in the reference:
+    "auto" / "triton" / "hip" and fused_slot_attention_triton: denominator + 1e-8 (:126)
+    "naive" / "compiled" and their functions:                  plain softmax (:287, :303)
+Softmax over SLOTS (dim=1): every token's column of attn sums to 1.  Q: (B, N, D),
+K, V: (B, M, D); out (B, N, D) in Q.dtype; attn (B, N, M) in Q.dtype.  D must be a multiple of
+16 (32 for 16-bit inputs).  Autograd: the backward is the reference's own bmm formulation
+(:215-236) in torch on the GPU.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from hclsm_amd import _lib
+from hclsm_amd.kernels._common import common_float_dtype, require_gpu
+
+_EPS_BACKENDS = ("auto", "triton", "hip")
+
+
+def _core_raw(Q, K, V, scale, denom_eps, logit_clamp=None, renorm_eps=None, want_attn=True,
+              attn_dtype=None):
+    B, N, D = Q.shape
+    M = K.shape[1]
+    io = common_float_dtype(Q, K, V)
+    q, k, v = (t.to(io).contiguous() for t in (Q, K, V))
+    out = torch.empty((B, N, D), dtype=io, device=Q.device)
+    at = attn_dtype or io
+    attn = torch.empty((B, N, M), dtype=at, device=Q.device) if want_attn else None
+    rc = _lib.lib().hclsm_slot_attn_core(
+        _lib.ptr(q), D, N * D, _lib.ptr(k), D, M * D, _lib.ptr(v), D, M * D, _lib.ptr(out), D, N * D,
+        _lib.ptr(attn), _lib.dtype_code(at), B, N, M, D, float(scale), float(denom_eps),
+        float(logit_clamp) if logit_clamp else 0.0, float(renorm_eps) if renorm_eps is not None else -1.0,
+        _lib.dtype_code(io), _lib.stream_of(q))
+    _lib.check(rc, "hclsm_slot_attn_core")
+    return out, attn
+
+
+class _SlotAttnCore(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, Q, K, V, scale, denom_eps):
+        out, attn = _core_raw(Q, K, V, scale, denom_eps)
+        ctx.save_for_backward(Q, K, V, attn)
+        ctx.scale = scale
+        return out.to(Q.dtype), attn.to(Q.dtype)
+
+    @staticmethod
+    def backward(ctx, grad_out, grad_attn):
+        Q, K, V, attn = ctx.saved_tensors
+        attn = attn.to(grad_out.dtype if grad_out is not None else Q.dtype)
+        d_attn = torch.zeros_like(attn) if grad_out is None else torch.bmm(grad_out, V.transpose(1, 2).contiguous())
+        if grad_attn is not None:
+            d_attn = d_attn + grad_attn
+        sum_da = (attn * d_attn).sum(dim=1, keepdim=True)      # softmax over slots (dim 1)
+        d_logits = attn * (d_attn - sum_da) * ctx.scale
+        d_Q = torch.bmm(d_logits, K)
+        d_K = torch.bmm(d_logits.transpose(1, 2).contiguous(), Q)
+        d_V = torch.bmm(attn.transpose(1, 2).contiguous(), grad_out) if grad_out is not None else torch.zeros_like(V)
+        return d_Q, d_K, d_V, None, None
+
+
+def _check(Q, K, V):
+    require_gpu("slot_attention", Q, K, V)
+    if Q.dim() != 3 or K.dim() != 3 or V.shape != K.shape or Q.shape[0] != K.shape[0] or Q.shape[2] != K.shape[2]:
+        raise ValueError(f"expected Q (B,N,D), K/V (B,M,D); got {tuple(Q.shape)}, {tuple(K.shape)}, {tuple(V.shape)}")
+
+
+def _run(Q, K, V, scale, denom_eps):
+    _check(Q, K, V)
+    if scale is None:
+        scale = Q.shape[-1] ** -0.5
+    return _SlotAttnCore.apply(Q, K, V, float(scale), float(denom_eps))
+
+
+def naive_slot_attention(Q, K, V, scale=None):
+    """Softmax over slots, no epsilon (reference :265-291), on the HIP core."""
+    return _run(Q, K, V, scale, 0.0)
+
+
+def compiled_slot_attention(Q, K, V, scale=None):
+    """Name kept from :308-317 (torch.compile of the naive math); same semantics as naive."""
+    return _run(Q, K, V, scale, 0.0)
+
+
+def fused_slot_attention_triton(Q, K, V, scale=None):
+    """Name kept from :239-258: softmax denominator + 1e-8 as the Triton kernel (:126)."""
+    return _run(Q, K, V, scale, 1e-8)
+
+
+def slot_attention_fn(Q, K, V, scale=None, backend="auto"):
+    """Dispatcher with the reference's signature (:324-355)."""
+    return _run(Q, K, V, scale, 1e-8 if backend in _EPS_BACKENDS else 0.0)

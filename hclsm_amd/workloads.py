@@ -49,3 +49,40 @@ def scan_algorithmic_bytes(batch, T, d_inner, d_state, io_bytes, with_D=True):
     if with_D:
         b += d_inner * 4
     return b
+
+
+def xavier_uniform(shape, generator):
+    fan_out, fan_in = shape
+    bound = math.sqrt(6.0 / (fan_in + fan_out))
+    return (torch.rand(shape, generator=generator) * 2 - 1) * bound
+
+
+def slot_config(B=32, M=196, N=32, d=384, hidden=768, seed=1002, wdtype=torch.bfloat16):
+    """BASELINE config 2: tokens = LayerNorm(randn(B, M, d)) (no affine); mu ~ 0.1 N(0,1);
+    slots0 = mu + 0.5 N(0,1); Xavier-uniform W_q, W_k, W_v (d x d), GRU W_ih, W_hh (3d x d),
+    MLP d -> hidden -> d; biases 0, LayerNorm weight 1 / bias 0; matrices rounded to ``wdtype``.
+    Returns (inputs, slots0, weights) as CPU tensors (weights already rounded, stored fp32)."""
+    g = torch.Generator().manual_seed(seed)
+    tokens = F.layer_norm(torch.randn(B, M, d, generator=g), (d,))
+    mu = 0.1 * torch.randn(d, generator=g)
+    slots0 = mu + 0.5 * torch.randn(B, N, d, generator=g)
+    rnd = lambda t: t.to(wdtype).float()
+    w = dict(w_q=rnd(xavier_uniform((d, d), g)), w_k=rnd(xavier_uniform((d, d), g)),
+             w_v=rnd(xavier_uniform((d, d), g)), w_ih=rnd(xavier_uniform((3 * d, d), g)),
+             w_hh=rnd(xavier_uniform((3 * d, d), g)), w1=rnd(xavier_uniform((hidden, d), g)),
+             w2=rnd(xavier_uniform((d, hidden), g)))
+    z = lambda n: torch.zeros(n)
+    o = lambda n: torch.ones(n)
+    w.update(b_ih=z(3 * d), b_hh=z(3 * d), b1=z(hidden), b2=z(d), ln_pre_w=o(d), ln_pre_b=z(d),
+             ln_mlp_w=o(d), ln_mlp_b=z(d), ln_in_w=o(d), ln_in_b=z(d))
+    return tokens, slots0, w
+
+
+def slot_flops(B=32, M=196, N=32, d=384, hidden=768, n_iter=3):
+    """Algorithmic FLOPs of config 2 (k/v projections once + n_iter iterations)."""
+    kv = 2 * B * M * d * d * 2
+    it = (2 * B * N * d * d            # q
+          + 2 * B * N * M * d * 2       # logits + attn @ v
+          + 2 * B * N * d * 3 * d * 2   # GRU W_ih, W_hh
+          + 2 * B * N * d * hidden * 2)  # MLP
+    return kv + n_iter * it

@@ -157,6 +157,60 @@ int hclsm_event_attention(const void* q, const void* k, const void* v, void* out
                           int64_t nseg, int64_t T, int64_t H, int64_t dh, int64_t capacity,
                           float scale, int dtype, int mode, void* stream);
 
+/*
+ * LayerNorm over the last dimension of a [M, D] row-major tensor (row strides ldx / ldy):
+ *   y = (x - mean) / sqrt(var + eps) * w + b, population variance, fp32 statistics.
+ * w, b: [D] float32, nullable (then 1 / 0).  (in, out) dtype pairs: (F32,F32) (F32,BF16) (BF16,BF16)
+ * (BF16,F32) (F32,F16) (F16,F16).
+ * Replaces: nn.LayerNorm of DynamicSlotAttention (objects/dynamic_slots.py:72-73,111,128,152),
+ *   SimplifiedSSMBlock (dynamics/level0_ssm.py:59,68) and EventTransformerBlock (level1_event.py:36,40).
+ */
+int hclsm_layer_norm(const void* x, int64_t ldx, const float* w, const float* b, void* y, int64_t ldy,
+                     int64_t M, int64_t D, float eps, int in_dtype, int out_dtype, void* stream);
+
+/*
+ * Linear layer on MFMA: Y[M, N] = X[M, K] . W[N, K]^T (+ bias[N]) (ReLU if relu) (+ resid[M, N] fp32)
+ *   (clamped to +-clamp if clamp > 0).  X, W: `dtype` (BF16 / F16 with 16-byte aligned rows and
+ *   K % 32 == 0; F32 with K % 4 == 0); Y: y_dtype (F32 or dtype); y2 (nullable): a second copy of Y
+ *   in `dtype`.  Row strides ldx, ldw, ldr, ldy, ldy2 in elements.
+ * Replaces: the nn.Linear layers of the slot iteration (dynamic_slots.py:51-53,64-68,112,128).
+ */
+int hclsm_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, const float* bias,
+                 const float* resid, int64_t ldr, void* y, int64_t ldy, int y_dtype, void* y2,
+                 int64_t ldy2, int64_t M, int64_t N, int64_t K, int relu, float clamp, int dtype,
+                 void* stream);
+
+/*
+ * torch.nn.GRUCell on MFMA for M rows: x [M, Kx] and h (both as `dtype` hb [M, H] for the products
+ * and as float32 h [M, H] for the blend), w_ih [3H, Kx], w_hh [3H, H] (`dtype`, rows [r; z; n]),
+ * b_ih, b_hh [3H] float32 nullable.  out [M, H] float32 = (1 - z) * n + z * h; out2 (nullable) the
+ * same in `dtype`.  Kx, H multiples of 32 (16-bit types) or 4 (F32).
+ * Replaces: self.gru of DynamicSlotAttention._iteration_step (objects/dynamic_slots.py:55-60,123-126).
+ */
+int hclsm_gru_cell(const void* x, int64_t ldx, const void* hb, int64_t ldhb, const float* h, int64_t ldh,
+                   const void* w_ih, const void* w_hh, const float* b_ih, const float* b_hh, float* out,
+                   int64_t ldo, void* out2, int64_t ldo2, int64_t M, int64_t H, int64_t Kx, int dtype,
+                   void* stream);
+
+/*
+ * Slot-attention core for B frames, one workgroup per frame:
+ *   logits = scale * q k^T (clamped to +-logit_clamp if logit_clamp > 0);
+ *   attn = softmax over the N slots for each of the M tokens, denominator + denom_eps;
+ *   if renorm_eps >= 0: attn = (attn + renorm_eps) / sum over tokens (attn + renorm_eps);
+ *   out = attn v.
+ * q [B][N][D], k, v [B][M][D], out [B][N][D]: `dtype` with row strides ldq/ldk/ldv/ldo and frame
+ * strides *_bstride (elements); attn (nullable) [B, N, M] contiguous, attn_dtype F32 or `dtype`, holds
+ * the softmax (before renormalisation).  D % 16 == 0 (and % 32 for 16-bit types).
+ * Replaces: slot_attention_fn / naive_slot_attention / compiled_slot_attention / the two Triton
+ *   kernels (hclsm/kernels/slot_attention_kernel.py:43-355; denom_eps 1e-8 is the Triton form, :126)
+ *   and the attention part of DynamicSlotAttention._iteration_step (objects/dynamic_slots.py:115-121).
+ */
+int hclsm_slot_attn_core(const void* q, int64_t ldq, int64_t q_bstride, const void* k, int64_t ldk,
+                         int64_t k_bstride, const void* v, int64_t ldv, int64_t v_bstride, void* out,
+                         int64_t ldo, int64_t o_bstride, void* attn, int attn_dtype, int64_t B, int64_t N,
+                         int64_t M, int64_t D, float scale, float denom_eps, float logit_clamp,
+                         float renorm_eps, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,150 @@
+"""GPU parity of the slot-attention kernels (hclsm_slot_attn_core, hclsm_layer_norm, hclsm_linear,
+hclsm_gru_cell) and the full iteration against oracle/slot_attention.py.
+
+Tolerances (normwise relative): fp32 1e-5; bf16 operands with fp32 accumulation 2e-2."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import slot_attention as sa
+from oracle.ssm_scan import normwise_rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+@pytest.mark.parametrize("B,N,M,D", [(2, 16, 64, 128), (1, 8, 32, 64), (4, 32, 196, 256), (3, 32, 196, 384)])
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
+def test_core_matches_oracle(B, N, M, D, dtype, tol):
+    from hclsm_amd.kernels import naive_slot_attention, slot_attention_fn
+    g = torch.Generator().manual_seed(B + N + M)
+    Q, K, V = (torch.randn(s, generator=g).to(dtype) for s in ((B, N, D), (B, M, D), (B, M, D)))
+    out, attn = naive_slot_attention(Q.cuda(), K.cuda(), V.cuda())
+    ref_o, ref_a = sa.slot_attention_core(_np(Q), _np(K), _np(V))
+    assert out.shape == (B, N, D) and attn.shape == (B, N, M) and out.dtype == dtype
+    assert normwise_rel_err(_np(out), ref_o) <= tol
+    assert normwise_rel_err(_np(attn), ref_a) <= tol
+    out2, attn2 = slot_attention_fn(Q.cuda(), K.cuda(), V.cuda())     # Triton semantics: +1e-8
+    ref_o2, _ = sa.slot_attention_core(_np(Q), _np(K), _np(V), denom_eps=1e-8)
+    assert normwise_rel_err(_np(out2), ref_o2) <= tol
+
+
+def test_reference_column_sums_and_dispatch():
+    """tests/test_kernels.py:66-77 and :88-97 on the HIP path."""
+    from hclsm_amd.kernels import naive_slot_attention, slot_attention_fn
+    torch.manual_seed(0)
+    for (B, N, M, D) in [(2, 16, 64, 128), (1, 8, 32, 64), (4, 32, 196, 256)]:
+        Q, K, V = torch.randn(B, N, D, device="cuda"), torch.randn(B, M, D, device="cuda"), torch.randn(B, M, D, device="cuda")
+        _, attn = naive_slot_attention(Q, K, V)
+        cs = attn.sum(dim=1)
+        assert torch.allclose(cs, torch.ones_like(cs), atol=1e-5)
+        a, _ = naive_slot_attention(Q, K, V)
+        b, _ = slot_attention_fn(Q, K, V, backend="naive")
+        assert torch.allclose(a, b, atol=1e-5)
+        _, attn_auto = slot_attention_fn(Q, K, V)
+        assert torch.allclose(attn_auto.sum(1), torch.ones_like(cs), atol=1e-4)
+
+
+def test_core_backward_matches_torch_autograd():
+    from hclsm_amd.kernels import naive_slot_attention
+    g = torch.Generator().manual_seed(7)
+    Q, K, V = (torch.randn(s, generator=g, dtype=torch.float64) for s in ((2, 8, 32), (2, 20, 32), (2, 20, 32)))
+    w = torch.randn(2, 8, 32, generator=g, dtype=torch.float64)
+    qc, kc, vc = (t.float().cuda().requires_grad_() for t in (Q, K, V))
+    out, attn = naive_slot_attention(qc, kc, vc)
+    ((out * w.float().cuda()).sum() + attn.sum() * 0.5).backward()
+    q64, k64, v64 = (t.clone().requires_grad_() for t in (Q, K, V))
+    a64 = torch.softmax(torch.bmm(q64, k64.transpose(1, 2)) * 32 ** -0.5, dim=1)
+    ((torch.bmm(a64, v64) * w).sum() + a64.sum() * 0.5).backward()
+    for got, ref in ((qc.grad, q64.grad), (kc.grad, k64.grad), (vc.grad, v64.grad)):
+        assert normwise_rel_err(_np(got), ref.numpy()) <= 1e-5
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
+def test_building_blocks(dtype, tol):
+    from hclsm_amd.kernels import slot_iteration as si
+    g = torch.Generator().manual_seed(9)
+    M, K, N = 100, 96, 72
+    x = torch.randn(M, K, generator=g)
+    w = torch.randn(N, K, generator=g) / 8
+    b = torch.randn(N, generator=g)
+    r = torch.randn(M, N, generator=g)
+    xd, wd = x.to(dtype), w.to(dtype)
+    st = torch.cuda.current_stream().cuda_stream
+    y = si._linear(xd.cuda(), wd.cuda(), bias=b.cuda(), resid=r.cuda(), relu=True, clamp=1.5,
+                   out_dtype=torch.float32, stream=st)
+    ref = np.clip(np.maximum(_np(xd) @ _np(wd).T + _np(b), 0) + _np(r), -1.5, 1.5)
+    assert normwise_rel_err(_np(y), ref) <= tol
+    lw, lb = torch.rand(K, generator=g) + 0.5, torch.randn(K, generator=g)
+    ln = si._ln(x.cuda(), K, M, K, lw.cuda(), lb.cuda(), dtype, st)
+    assert normwise_rel_err(_np(ln), sa.layer_norm(_np(x), _np(lw), _np(lb))) <= (1e-5 if dtype == torch.float32 else 8e-3)
+    H = 64
+    cell = torch.nn.GRUCell(K, H)
+    xin = torch.randn(M, K, generator=g).to(dtype)
+    h = torch.randn(M, H, generator=g)
+    W = si.SlotWeights(dtype, H, 0, {"w_ih": cell.weight_ih.detach().to(dtype).cuda(), "w_hh": cell.weight_hh.detach().to(dtype).cuda(),
+                                      "b_ih": cell.bias_ih.detach().cuda(), "b_hh": cell.bias_hh.detach().cuda()})
+    hb = h.to(dtype)
+    out = si._gru(xin.cuda(), hb.cuda(), h.cuda(), W, st)
+    # gate products see h rounded to the operand dtype; the blend uses the fp32 h
+    H_ = H
+    gi = _np(xin) @ _np(W.t["w_ih"]).T + _np(cell.bias_ih)
+    gh = _np(hb) @ _np(W.t["w_hh"]).T + _np(cell.bias_hh)
+    rg = sa.sigmoid(gi[:, :H_] + gh[:, :H_])
+    zg = sa.sigmoid(gi[:, H_:2 * H_] + gh[:, H_:2 * H_])
+    ng = np.tanh(gi[:, 2 * H_:] + rg * gh[:, 2 * H_:])
+    ref = (1 - zg) * ng + zg * _np(h)
+    assert normwise_rel_err(_np(out), ref) <= tol
+
+
+def _weights(d, hidden, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    from hclsm_amd.workloads import xavier_uniform
+    w = dict(w_q=xavier_uniform((d, d), g), w_ih=xavier_uniform((3 * d, d), g) * scale,
+             w_hh=xavier_uniform((3 * d, d), g) * scale, w1=xavier_uniform((hidden, d), g),
+             w2=xavier_uniform((d, hidden), g), b_ih=torch.randn(3 * d, generator=g) * 0.1,
+             b_hh=torch.randn(3 * d, generator=g) * 0.1, b1=torch.randn(hidden, generator=g) * 0.1,
+             b2=torch.randn(d, generator=g) * 0.1, ln_pre_w=torch.rand(d, generator=g) + 0.5,
+             ln_pre_b=torch.randn(d, generator=g) * 0.1, ln_mlp_w=torch.rand(d, generator=g) + 0.5,
+             ln_mlp_b=torch.randn(d, generator=g) * 0.1)
+    return w
+
+
+@pytest.mark.parametrize("mode_name,dtype,tol", [("reference", torch.float32, 1e-5), ("config2", torch.bfloat16, 2e-2),
+                                                 ("reference", torch.bfloat16, 2e-2)])
+def test_iteration_matches_oracle(mode_name, dtype, tol):
+    from hclsm_amd.kernels import slot_iteration as si
+    d, hidden, B, N, M = 128, 512 if mode_name == "reference" else 256, 3, 16, 49
+    w = _weights(d, hidden, seed=11)
+    w = {n: t.to(dtype).float() if n in si._WEIGHT_KEYS else t for n, t in w.items()}
+    W = si.SlotWeights.from_dict(w, dtype)
+    g = torch.Generator().manual_seed(12)
+    slots = torch.randn(B, N, d, generator=g)
+    k = torch.randn(B, M, d, generator=g).to(dtype)
+    v = torch.randn(B, M, d, generator=g).to(dtype)
+    mode = si.REFERENCE_MODE if mode_name == "reference" else si.CONFIG2_MODE
+    out = si.slot_attention_iteration(slots.cuda(), k.cuda(), v.cuda(), W, mode)
+    kw = dict(logit_clamp=mode.logit_clamp, renorm_eps=mode.renorm_eps, slot_clamp=mode.slot_clamp)
+    ref = sa.slot_iteration(_np(slots), _np(k), _np(v), {n: _np(t) for n, t in w.items()}, **kw)
+    err = normwise_rel_err(_np(out), ref)
+    assert err <= tol, f"{mode_name} {dtype}: {err:.3e}"
+
+
+def test_config2_forward_bf16():
+    """32 frames x 196 tokens x 384, 32 slots, 3 iterations, MLP 768, bf16 weights."""
+    from hclsm_amd.kernels import slot_iteration as si
+    from hclsm_amd.workloads import slot_config
+    tokens, slots0, w = slot_config()
+    W = si.SlotWeights.from_dict(w, torch.bfloat16)
+    out = si.slot_attention_forward(tokens.cuda(), slots0.cuda(), W, 3, si.CONFIG2_MODE)
+    torch.cuda.synchronize()
+    ref = sa.slot_attention_forward(tokens.numpy(), slots0.numpy(), {n: t.numpy() for n, t in w.items()}, 3,
+                                    logit_clamp=None, renorm_eps=1e-8, slot_clamp=None)
+    err = normwise_rel_err(_np(out), ref)
+    assert err <= 2e-2, f"config 2 normwise err {err:.3e}"
