@@ -77,6 +77,64 @@ def _cpu_baseline(d, nseq=1024, reps=5):
                       f"(oracle/ssm_scan.py), median of {reps}: {med:.3f} s"}
 
 
+def _event_timing(fn, n, warmup):
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for a, b in evs:
+        a.record()
+        fn()
+        b.record()
+    torch.cuda.synchronize()
+    ts = sorted(a.elapsed_time(b) * 1e-3 for a, b in evs)
+    return ts[len(ts) // 2], sum(ts) / len(ts)
+
+
+def _bench_slot(dev, n, warmup):
+    """Config 2: k/v projections + 3 slot-attention iterations (bf16 operands, fp32 accumulation)."""
+    import torch
+    from hclsm_amd.kernels import slot_iteration as si
+    from hclsm_amd.workloads import slot_config, slot_flops
+    tokens, slots0, w = slot_config()
+    W = si.SlotWeights.from_dict(w, torch.bfloat16, dev)
+    tk, s0 = tokens.to(dev), slots0.to(dev)
+    med, avg = _event_timing(lambda: si.slot_attention_forward(tk, s0, W, 3, si.CONFIG2_MODE), n, warmup)
+    fl = slot_flops()
+    ntok = tokens.shape[0] * tokens.shape[1]
+    return {"workload": "config 2: 32 frames x 196 tokens x 384, 32 slots, 3 iterations, MLP 768, bf16 MFMA",
+            "metric": "tokens/s", "value": round(ntok / med, 1), "median_us": round(med * 1e6, 2),
+            "roofline": {"bound": "mfma", "achieved": round(fl / med / 1e12, 3), "peak": 2500.0,
+                         "unit": "TFLOP/s", "frac": round(fl / med / 1e12 / 2500.0, 5), "flops_per_call": fl}}
+
+
+def _bench_events(dev, n, warmup):
+    """Config 3: event index + per-track causal attention, 1024 tracks x T=64, 6 x 64 heads, p=0.15."""
+    import torch
+    from hclsm_amd.kernels.event_attention import event_attention
+    from hclsm_amd.kernels.sparse_event_attn import build_event_index
+    g = torch.Generator().manual_seed(1003)
+    q, k, v = (torch.randn(1024, 64, 6, 64, generator=g).to(torch.bfloat16).to(dev) for _ in range(3))
+    m = (torch.rand(1024, 64, generator=g) < 0.15).float()
+    m[:, 0] = 1
+    m = m.to(dev)
+    total = build_event_index(m).total()
+
+    def step():
+        idx = build_event_index(m)
+        event_attention(q, k, v, idx, capacity=total)
+    med, avg = _event_timing(step, n, warmup)
+    nbytes = total * 6 * 64 * 2 * 4 + m.numel() * 4 + (1025 + 2 * total + 2 * 65536) * 4
+    return {"workload": "config 3: 1024 tracks x T=64, 6 heads x 64, p=0.15 (t=0 forced), bf16, "
+                        "index build + causal event attention, packed output",
+            "events": total, "metric": "event-tokens/s", "value": round(total / med, 1),
+            "grid_tokens_per_s": round(65536 / med, 1), "median_us": round(med * 1e6, 2),
+            "roofline": {"bound": "hbm", "achieved": round(nbytes / med / 1e9, 2), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(nbytes / med / 1e9 / HBM_PEAK_GBS, 5),
+                         "bytes_per_call": nbytes}}
+
+
 def main():
     args = _parse()
     if args.gpus != 1:
@@ -174,6 +232,8 @@ def main():
                      "kernel": "ssm_scan_fwd_sgpr_kernel<bf16,16,raw,2,4>",
                      "avg_launch_us": round(avg * 1e6, 3), "median_launch_us": round(med * 1e6, 3)},
     }
+    out["slot_attn"] = _bench_slot(dev, 30, 5)
+    out["event_attn"] = _bench_events(dev, 50, 5)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = _cpu_baseline(d)
     print(json.dumps(out), flush=True)

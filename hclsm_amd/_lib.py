@@ -38,15 +38,31 @@ _SIGNATURES: dict[str, list] = {
     "hclsm_event_attention": [_c_void_p] * 8 + [_i64] * 5 + [_f32, _int, _int, _c_void_p],
     "hclsm_layer_norm": [_c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _f32, _int, _int,
                          _c_void_p],
-    "hclsm_linear": [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _c_void_p, _i64, _int,
-                     _c_void_p, _i64, _i64, _i64, _i64, _int, _f32, _int, _c_void_p],
+    "hclsm_linear": [_c_void_p, _i64, _int, _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _c_void_p, _i64, _int,
+                     _c_void_p, _i64, _i64, _i64, _i64, _int, _f32, _int, _c_void_p, _c_void_p, _f32, _int,
+                     _c_void_p],
     "hclsm_gru_cell": [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p,
                        _c_void_p, _c_void_p, _i64, _c_void_p, _i64, _i64, _i64, _i64, _int, _c_void_p],
+    "hclsm_slot_attn_core_workspace": [_i64, _i64, _i64, _int],
     "hclsm_slot_attn_core": [_c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p,
                              _i64, _i64, _c_void_p, _int, _i64, _i64, _i64, _i64, _f32, _f32, _f32, _f32,
-                             _int, _c_void_p],
+                             _int, _c_void_p, _i64, _c_void_p],
+    "hclsm_slot_attention_workspace": [_i64, _i64, _i64, _i64, _i64, _i64, _int],
+    "hclsm_slot_attention_iteration": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _c_void_p,
+                                       _i64, _i64, _i64, _i64, _i64, _f32, _f32, _f32, _f32, _int, _c_void_p,
+                                       _i64, _c_void_p],
+    "hclsm_slot_attention_forward": [_c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64,
+                                     _i64, _i64, _f32, _f32, _f32, _f32, _int, _c_void_p, _i64, _c_void_p],
 }
-_RESTYPES = {"hclsm_strerror": ctypes.c_char_p}
+_RESTYPES = {"hclsm_strerror": ctypes.c_char_p, "hclsm_slot_attn_core_workspace": ctypes.c_int64,
+             "hclsm_slot_attention_workspace": ctypes.c_int64}
+
+
+class HclsmSlotWeights(ctypes.Structure):
+    """Mirror of the C struct HclsmSlotWeights (include/hclsm_amd.h)."""
+    _fields_ = [(n, ctypes.c_void_p) for n in (
+        "w_q", "w_kv", "w_ih", "w_hh", "w1", "w2", "b_ih", "b_hh", "b1", "b2",
+        "ln_in_w", "ln_in_b", "ln_pre_w", "ln_pre_b", "ln_mlp_w", "ln_mlp_b")]
 
 _lib = None
 

@@ -1,91 +1,171 @@
-// Slot attention on gfx950: the attention core and the building blocks of the
-// slot-attention iteration (LayerNorm, MFMA linear layers, fused GRU cell).
+// Slot attention on gfx950: the attention core and the slot-attention iteration.
 //
-// slot_core_kernel (one workgroup per frame b, 4 waves):
-//   phase 1  logits[n][m] = scale * q[n] . k[m]          MFMA, tiles of 16 slots x 16 tokens,
-//                                                         fp32 into LDS
-//   phase 2  softmax over the slot axis for every token  (optional logit clamp, optional
-//            +denom_eps in the denominator), optional renormalisation over tokens
-//            (attn + eps) / sum_m (attn + eps); attn written to global if asked
-//   phase 3  updates[n] = sum_m attn[n][m] v[m]           MFMA over 32-token chunks of v,
-//            each chunk staged transposed in LDS so both operands are contiguous
-// linear_kernel: Y = X W^T (+ bias) (ReLU) (+ residual) (clamp), X / W K-contiguous, one
-//   wave per 32x32 output tile, lane group g streaming its quarter of K.
-// gru_kernel: the six gate products of torch.nn.GRUCell for a 32x16 tile of h', with the
-//   gate nonlinearities and the (1-z) n + z h blend in the epilogue.
+// Every dense contraction runs on v_mfma_f32_16x16x32_{bf16,f16} (fp32 inputs: 16x16x4 f32).
+// The contraction dimension is walked in 32-wide blocks (lane group g = lane/16 takes
+// elements 8g..8g+7 of a block, one 16-byte load per operand row).
+//
+// linear_kernel   one workgroup per 32x32 output tile, its 4 waves splitting the K blocks
+//                 (block s goes to wave s % 4); partial tiles are summed through LDS, then
+//                 the epilogue adds bias, ReLU, residual, clamp.  Optional LayerNorm
+//                 prologue: row statistics from the same split (sums shifted by the row's
+//                 first element), then normalised operands are formed on the fly.
+// gru_kernel      the six gate products of torch.nn.GRUCell for a 32x16 tile of h', same
+//                 split-K scheme, gates and (1-z) n + z h in the epilogue.
+// core_logits     grid (frame, 64-token block): each wave forms a 16-token x N-slot logit
+//                 tile, softmax over the slot axis in registers (two xor shuffles cover the
+//                 four lane groups), writes attn and per-slot partial sums over its tokens.
+// core_update     grid (frame, 64-column block of D): attn (A operand, row-major in HBM) times
+//                 v staged transposed through LDS in 32-token chunks; optional
+//                 renormalisation (attn + eps) / sum_m (attn + eps) folded into the epilogue.
 #include "mfma.h"
 
 namespace hclsm {
 
-// ---------------------------------------------------------------------------
-// LayerNorm over the last dim: one wave per row, two-pass mean / variance in fp32.
-template <int DTI, int DTO>
-__global__ void __launch_bounds__(256)
-layer_norm_kernel(const typename MM<DTI>::T* __restrict__ x, int64_t ldx, const float* __restrict__ w,
-                  const float* __restrict__ b, typename MM<DTO>::T* __restrict__ y, int64_t ldy, int64_t M,
-                  int D, float eps) {
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (row >= M) return;
-  const typename MM<DTI>::T* xr = x + row * ldx;
-  float s = 0.f;
-  for (int i = lane; i < D; i += 64) s += MM<DTI>::tof(xr[i]);
+template <typename T> struct Cvt;
+template <> struct Cvt<float> { static __device__ __forceinline__ float f(float v) { return v; } };
+template <> struct Cvt<uint16_t> { static __device__ __forceinline__ float f(uint16_t v) { return bf16_bits_to_f32(v); } };
+template <> struct Cvt<_Float16> { static __device__ __forceinline__ float f(_Float16 v) { return (float)v; } };
+
+// Operand of one 32-wide K block for this lane (8 elements at k0 + 8g), converted to DT.
+template <int DT, typename XT>
+__device__ __forceinline__ typename MM<DT>::Op load_op(const XT* p) {
+  using A = MM<DT>;
+  if constexpr (std::is_same_v<XT, typename A::T>) {
+    return A::load(p);
+  } else {
+    if constexpr (A::KPL == 8) {
+      typename A::T e[8];
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
-  const float mean = s / (float)D;
-  float v = 0.f;
-  for (int i = lane; i < D; i += 64) {
-    const float d = MM<DTI>::tof(xr[i]) - mean;
-    v += d * d;
-  }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  const float rstd = 1.f / sqrtf(v / (float)D + eps);
-  typename MM<DTO>::T* yr = y + row * ldy;
-  for (int i = lane; i < D; i += 64) {
-    float t = (MM<DTI>::tof(xr[i]) - mean) * rstd;
-    if (w) t *= w[i];
-    if (b) t += b[i];
-    yr[i] = MM<DTO>::fromf(t);
+      for (int i = 0; i < 8; ++i) e[i] = A::fromf(Cvt<XT>::f(p[i]));
+      return __builtin_bit_cast(typename A::Op, *reinterpret_cast<uint4*>(e));
+    } else {
+      return Cvt<XT>::f(p[0]);
+    }
   }
 }
 
-// ---------------------------------------------------------------------------
-// Linear layer, NT: Y[M][N] = X[M][K] . W[N][K]^T
-template <int DT, int OT>
-__global__ void __launch_bounds__(256)
-linear_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const typename MM<DT>::T* __restrict__ W,
-              int64_t ldw, const float* __restrict__ bias, const float* __restrict__ resid, int64_t ldr,
-              typename MM<OT>::T* __restrict__ Y, int64_t ldy, typename MM<DT>::T* __restrict__ Y2, int64_t ldy2,
-              int64_t M, int64_t N, int64_t K, int relu, float clamp_v) {
+// LayerNorm-transformed operand: (x - mean) * rstd * w + b, converted to DT.
+template <int DT, typename XT>
+__device__ __forceinline__ typename MM<DT>::Op load_op_ln(const XT* p, int k, float mean, float rstd,
+                                                          const float* __restrict__ w, const float* __restrict__ b) {
   using A = MM<DT>;
   constexpr int KPL = A::KPL;
-  const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int64_t tiles_n = (N + 31) / 32;
-  if (wave >= ((M + 31) / 32) * tiles_n) return;
-  const int64_t tm = wave / tiles_n, tn = wave - tm * tiles_n;
-  const int lane = threadIdx.x & 63, g = lane >> 4, li = lane & 15;
-  const int64_t K4 = K / 4;
+  float x[KPL];
+#pragma unroll
+  for (int i = 0; i < KPL; ++i) {
+    float t = (Cvt<XT>::f(p[i]) - mean) * rstd;
+    if (w) t *= w[k + i];
+    if (b) t += b[k + i];
+    x[i] = t;
+  }
+  if constexpr (KPL == 8) {
+    typename A::T e[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) e[i] = A::fromf(x[i]);
+    return __builtin_bit_cast(typename A::Op, *reinterpret_cast<uint4*>(e));
+  } else {
+    return x[0];
+  }
+}
+
+// Row statistics for the LayerNorm prologue: rows r0 + li and r0 + 16 + li, this wave's K blocks,
+// reduced across lane groups and the 4 waves through LDS.  Uses sums of (x - c) with c = row's x[0].
+template <typename XT, int KPL>
+__device__ __forceinline__ void ln_stats(const XT* const pa[2], int64_t K, int wid, int g, int li, float eps,
+                                         float* lds, float mean[2], float rstd[2]) {
+  const int BLK = 4 * KPL;
+  const int nblk = (int)(K / BLK);
+  float s1[2] = {0.f, 0.f}, s2[2] = {0.f, 0.f};
+  float c[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) c[t] = Cvt<XT>::f(pa[t][-(int64_t)(KPL * g)]);  // x[row][0]
+  for (int s = wid; s < nblk; s += 4) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int i = 0; i < KPL; ++i) {
+        const float d = Cvt<XT>::f(pa[t][(int64_t)s * BLK + i]) - c[t];
+        s1[t] += d;
+        s2[t] += d * d;
+      }
+  }
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    s1[t] += __shfl_xor(s1[t], 16, 64);
+    s1[t] += __shfl_xor(s1[t], 32, 64);
+    s2[t] += __shfl_xor(s2[t], 16, 64);
+    s2[t] += __shfl_xor(s2[t], 32, 64);
+  }
+  // lds layout: [wave][row 0..31][2]
+  if (g == 0) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      lds[(wid * 32 + 16 * t + li) * 2 + 0] = s1[t];
+      lds[(wid * 32 + 16 * t + li) * 2 + 1] = s2[t];
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    float a1 = 0.f, a2 = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      a1 += lds[(w * 32 + 16 * t + li) * 2 + 0];
+      a2 += lds[(w * 32 + 16 * t + li) * 2 + 1];
+    }
+    const float m1 = a1 / (float)K;
+    const float var = fmaxf(a2 / (float)K - m1 * m1, 0.f);
+    mean[t] = c[t] + m1;
+    rstd[t] = 1.f / sqrtf(var + eps);
+  }
+  __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// Optional split of a linear layer's output: columns >= col go, transposed per frame of
+// frame_rows rows, to yt[frame][col - split][row % frame_rows] (row stride ldyt, frame stride
+// bstride) instead of Y.  Used to emit v^T next to k from one [W_k; W_v] projection.
+struct OutSplit {
+  int64_t col, frame_rows, ldyt, bstride;
+  void* yt;
+};
+
+// 64x64 output tile per workgroup, each wave a 32x32 quadrant over the full K (large M x N).
+template <int DT, int OT>
+__global__ void __launch_bounds__(256)
+linear_quad_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const typename MM<DT>::T* __restrict__ W,
+                   int64_t ldw, const float* __restrict__ bias, const float* __restrict__ resid, int64_t ldr,
+                   typename MM<OT>::T* __restrict__ Y, int64_t ldy, typename MM<DT>::T* __restrict__ Y2,
+                   int64_t ldy2, int64_t M, int64_t N, int64_t K, int relu, float clamp_v, OutSplit os) {
+  using A = MM<DT>;
+  constexpr int KPL = A::KPL;
+  constexpr int BLK = 4 * KPL;
+  const int64_t tiles_n = (N + 63) / 64;
+  const int64_t tm = blockIdx.x / tiles_n, tn = blockIdx.x - tm * tiles_n;
+  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, g = lane >> 4, li = lane & 15;
+  const int64_t r0 = tm * 64 + 32 * (wid >> 1), c0 = tn * 64 + 32 * (wid & 1);
   const typename A::T* pa[2];
   const typename A::T* pb[2];
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    int64_t r = tm * 32 + 16 * t + li;
+    int64_t r = r0 + 16 * t + li;
     r = r < M ? r : M - 1;
-    pa[t] = X + r * ldx + g * K4;
-    int64_t c = tn * 32 + 16 * t + li;
+    pa[t] = X + r * ldx + KPL * g;
+    int64_t c = c0 + 16 * t + li;
     c = c < N ? c : N - 1;
-    pb[t] = W + c * ldw + g * K4;
+    pb[t] = W + c * ldw + KPL * g;
   }
   f32x4 acc[2][2];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll 2
-  for (int64_t c = 0; c < K4; c += KPL) {
-    const typename A::Op a0 = A::load(pa[0] + c), a1 = A::load(pa[1] + c);
-    const typename A::Op b0 = A::load(pb[0] + c), b1 = A::load(pb[1] + c);
+  const int nblk = (int)(K / BLK);
+#pragma unroll 4
+  for (int s = 0; s < nblk; ++s) {
+    const int64_t k0 = (int64_t)s * BLK;
+    const typename A::Op a0 = A::load(pa[0] + k0), a1 = A::load(pa[1] + k0);
+    const typename A::Op b0 = A::load(pb[0] + k0), b1 = A::load(pb[1] + k0);
     acc[0][0] = A::mfma(a0, b0, acc[0][0]);
     acc[0][1] = A::mfma(a0, b1, acc[0][1]);
     acc[1][0] = A::mfma(a1, b0, acc[1][0]);
@@ -93,29 +173,111 @@ linear_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const typen
   }
 #pragma unroll
   for (int tj = 0; tj < 2; ++tj) {
-    const int64_t col = tn * 32 + 16 * tj + li;
+    const int64_t col = c0 + 16 * tj + li;
     if (col >= N) continue;
     const float bv = bias ? bias[col] : 0.f;
 #pragma unroll
     for (int ti = 0; ti < 2; ++ti)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int64_t row = tm * 32 + 16 * ti + 4 * g + r;
+        const int64_t row = r0 + 16 * ti + 4 * g + r;
         if (row >= M) continue;
         float val = acc[ti][tj][r] + bv;
+        if (relu) val = fmaxf(val, 0.f);
+        if (resid) val += resid[row * ldr + col];
+        if (clamp_v > 0.f) val = fminf(fmaxf(val, -clamp_v), clamp_v);
+        if (os.yt != nullptr && col >= os.col) {
+          const int64_t fr = row / os.frame_rows, rr = row - fr * os.frame_rows;
+          reinterpret_cast<typename MM<OT>::T*>(os.yt)[fr * os.bstride + (col - os.col) * os.ldyt + rr] =
+              MM<OT>::fromf(val);
+        } else {
+          Y[row * ldy + col] = MM<OT>::fromf(val);
+        }
+        if (Y2) Y2[row * ldy2 + col] = A::fromf(val);
+      }
+  }
+}
+
+template <int DT, int OT, typename XT, bool LN>
+__global__ void __launch_bounds__(256)
+linear_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>::T* __restrict__ W, int64_t ldw,
+              const float* __restrict__ bias, const float* __restrict__ resid, int64_t ldr,
+              typename MM<OT>::T* __restrict__ Y, int64_t ldy, typename MM<DT>::T* __restrict__ Y2, int64_t ldy2,
+              int64_t M, int64_t N, int64_t K, int relu, float clamp_v, const float* __restrict__ lnw,
+              const float* __restrict__ lnb, float ln_eps) {
+  using A = MM<DT>;
+  constexpr int KPL = A::KPL;
+  constexpr int BLK = 4 * KPL;
+  __shared__ float red[4][2][2][4][64];   // [wave][ti][tj][r][lane]: 16 KB
+  const int64_t tiles_n = (N + 31) / 32;
+  const int64_t tm = blockIdx.x / tiles_n, tn = blockIdx.x - tm * tiles_n;
+  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, g = lane >> 4, li = lane & 15;
+  const XT* pa[2];
+  const typename A::T* pb[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    int64_t r = tm * 32 + 16 * t + li;
+    r = r < M ? r : M - 1;
+    pa[t] = X + r * ldx + KPL * g;
+    int64_t c = tn * 32 + 16 * t + li;
+    c = c < N ? c : N - 1;
+    pb[t] = W + c * ldw + KPL * g;
+  }
+  float mean[2] = {0.f, 0.f}, rstd[2] = {1.f, 1.f};
+  if constexpr (LN) ln_stats<XT, KPL>(pa, K, wid, g, li, ln_eps, &red[0][0][0][0][0], mean, rstd);
+  f32x4 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int nblk = (int)(K / BLK);
+#pragma unroll 2
+  for (int s = wid; s < nblk; s += 4) {
+    const int64_t k0 = (int64_t)s * BLK;
+    typename A::Op a0, a1;
+    if constexpr (LN) {
+      a0 = load_op_ln<DT, XT>(pa[0] + k0, (int)k0 + KPL * g, mean[0], rstd[0], lnw, lnb);
+      a1 = load_op_ln<DT, XT>(pa[1] + k0, (int)k0 + KPL * g, mean[1], rstd[1], lnw, lnb);
+    } else {
+      a0 = load_op<DT, XT>(pa[0] + k0);
+      a1 = load_op<DT, XT>(pa[1] + k0);
+    }
+    const typename A::Op b0 = A::load(pb[0] + k0), b1 = A::load(pb[1] + k0);
+    acc[0][0] = A::mfma(a0, b0, acc[0][0]);
+    acc[0][1] = A::mfma(a0, b1, acc[0][1]);
+    acc[1][0] = A::mfma(a1, b0, acc[1][0]);
+    acc[1][1] = A::mfma(a1, b1, acc[1][1]);
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[wid][i][j][r][lane] = acc[i][j][r];
+  __syncthreads();
+  // 1024 outputs, 4 per thread: thread -> (ti, tj) = wave index, lane, all four r
+  {
+    const int ti = wid >> 1, tj = wid & 1;
+    const int64_t col = tn * 32 + 16 * tj + li;
+    if (col < N) {
+      const float bv = bias ? bias[col] : 0.f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t row = tm * 32 + 16 * ti + 4 * g + r;
+        if (row >= M) continue;
+        float val = red[0][ti][tj][r][lane] + red[1][ti][tj][r][lane] + red[2][ti][tj][r][lane] +
+                    red[3][ti][tj][r][lane] + bv;
         if (relu) val = fmaxf(val, 0.f);
         if (resid) val += resid[row * ldr + col];
         if (clamp_v > 0.f) val = fminf(fmaxf(val, -clamp_v), clamp_v);
         Y[row * ldy + col] = MM<OT>::fromf(val);
         if (Y2) Y2[row * ldy2 + col] = A::fromf(val);
       }
+    }
   }
 }
 
 // ---------------------------------------------------------------------------
-// torch.nn.GRUCell: h' = (1 - z) * n + z * h with
-//   r = sig(x Wir^T + bir + h Whr^T + bhr), z = sig(x Wiz^T + biz + h Whz^T + bhz),
-//   n = tanh(x Win^T + bin + r * (h Whn^T + bhn)); weight rows ordered [r; z; n].
 template <int DT>
 __global__ void __launch_bounds__(256)
 gru_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const typename MM<DT>::T* __restrict__ Hb,
@@ -125,240 +287,580 @@ gru_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const typename
            int64_t H, int64_t Kx) {
   using A = MM<DT>;
   constexpr int KPL = A::KPL;
-  const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  constexpr int BLK = 4 * KPL;
+  __shared__ float red[4][2][6][4][64];  // 48 KB
   const int64_t tiles_n = (H + 15) / 16;
-  if (wave >= ((M + 31) / 32) * tiles_n) return;
-  const int64_t tm = wave / tiles_n, tn = wave - tm * tiles_n;
-  const int lane = threadIdx.x & 63, g = lane >> 4, li = lane & 15;
+  const int64_t tm = blockIdx.x / tiles_n, tn = blockIdx.x - tm * tiles_n;
+  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, g = lane >> 4, li = lane & 15;
   int64_t colr = tn * 16 + li;
   colr = colr < H ? colr : H - 1;
-  f32x4 acc[2][6];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 6; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   int64_t rows[2];
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int64_t r = tm * 32 + 16 * t + li;
     rows[t] = r < M ? r : M - 1;
   }
-  {  // input gates: x . W_ih^T
-    const int64_t K4 = Kx / 4;
-    const typename A::T* pa[2] = {X + rows[0] * ldx + g * K4, X + rows[1] * ldx + g * K4};
-    const typename A::T* pw[3] = {Wih + colr * Kx + g * K4, Wih + (H + colr) * Kx + g * K4,
-                                  Wih + (2 * H + colr) * Kx + g * K4};
-    for (int64_t c = 0; c < K4; c += KPL) {
-      const typename A::Op a0 = A::load(pa[0] + c), a1 = A::load(pa[1] + c);
+  f32x4 acc[2][6];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 6; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  {
+    const typename A::T* pa[2] = {X + rows[0] * ldx + KPL * g, X + rows[1] * ldx + KPL * g};
+    const typename A::T* pw[3] = {Wih + colr * Kx + KPL * g, Wih + (H + colr) * Kx + KPL * g,
+                                  Wih + (2 * H + colr) * Kx + KPL * g};
+    const int nblk = (int)(Kx / BLK);
+    for (int s = wid; s < nblk; s += 4) {
+      const int64_t k0 = (int64_t)s * BLK;
+      const typename A::Op a0 = A::load(pa[0] + k0), a1 = A::load(pa[1] + k0);
 #pragma unroll
       for (int q = 0; q < 3; ++q) {
-        const typename A::Op bq = A::load(pw[q] + c);
+        const typename A::Op bq = A::load(pw[q] + k0);
         acc[0][q] = A::mfma(a0, bq, acc[0][q]);
         acc[1][q] = A::mfma(a1, bq, acc[1][q]);
       }
     }
   }
-  {  // hidden gates: h . W_hh^T
-    const int64_t K4 = H / 4;
-    const typename A::T* pa[2] = {Hb + rows[0] * ldhb + g * K4, Hb + rows[1] * ldhb + g * K4};
-    const typename A::T* pw[3] = {Whh + colr * H + g * K4, Whh + (H + colr) * H + g * K4,
-                                  Whh + (2 * H + colr) * H + g * K4};
-    for (int64_t c = 0; c < K4; c += KPL) {
-      const typename A::Op a0 = A::load(pa[0] + c), a1 = A::load(pa[1] + c);
+  {
+    const typename A::T* pa[2] = {Hb + rows[0] * ldhb + KPL * g, Hb + rows[1] * ldhb + KPL * g};
+    const typename A::T* pw[3] = {Whh + colr * H + KPL * g, Whh + (H + colr) * H + KPL * g,
+                                  Whh + (2 * H + colr) * H + KPL * g};
+    const int nblk = (int)(H / BLK);
+    for (int s = wid; s < nblk; s += 4) {
+      const int64_t k0 = (int64_t)s * BLK;
+      const typename A::Op a0 = A::load(pa[0] + k0), a1 = A::load(pa[1] + k0);
 #pragma unroll
       for (int q = 0; q < 3; ++q) {
-        const typename A::Op bq = A::load(pw[q] + c);
+        const typename A::Op bq = A::load(pw[q] + k0);
         acc[0][3 + q] = A::mfma(a0, bq, acc[0][3 + q]);
         acc[1][3 + q] = A::mfma(a1, bq, acc[1][3 + q]);
       }
     }
   }
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int q = 0; q < 6; ++q)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[wid][t][q][r][lane] = acc[t][q][r];
+  __syncthreads();
+  // 512 outputs (32 rows x 16 cols): thread -> (t = wid >> 1, r pair = 2 * (wid & 1) .. +1), lane
   const int64_t col = tn * 16 + li;
   if (col >= H) return;
   const float bir = bih ? bih[col] : 0.f, biz = bih ? bih[H + col] : 0.f, bin = bih ? bih[2 * H + col] : 0.f;
   const float bhr = bhh ? bhh[col] : 0.f, bhz = bhh ? bhh[H + col] : 0.f, bhn = bhh ? bhh[2 * H + col] : 0.f;
+  const int t = wid >> 1;
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+  for (int rr = 0; rr < 2; ++rr) {
+    const int r = 2 * (wid & 1) + rr;
+    const int64_t row = tm * 32 + 16 * t + 4 * g + r;
+    if (row >= M) continue;
+    float gsum[6];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int64_t row = tm * 32 + 16 * t + 4 * g + r;
-      if (row >= M) continue;
-      const float rg = sigmoid_f(acc[t][0][r] + bir + acc[t][3][r] + bhr);
-      const float zg = sigmoid_f(acc[t][1][r] + biz + acc[t][4][r] + bhz);
-      const float ng = tanh_f(acc[t][2][r] + bin + rg * (acc[t][5][r] + bhn));
-      const float hv = Hf[row * ldh + col];
-      const float o = (1.f - zg) * ng + zg * hv;
-      out[row * ldo + col] = o;
-      if (out2) out2[row * ldo2 + col] = A::fromf(o);
-    }
+    for (int q = 0; q < 6; ++q)
+      gsum[q] = red[0][t][q][r][lane] + red[1][t][q][r][lane] + red[2][t][q][r][lane] + red[3][t][q][r][lane];
+    const float rg = sigmoid_f(gsum[0] + bir + gsum[3] + bhr);
+    const float zg = sigmoid_f(gsum[1] + biz + gsum[4] + bhz);
+    const float ng = tanh_f(gsum[2] + bin + rg * (gsum[5] + bhn));
+    const float hv = Hf[row * ldh + col];
+    const float o = (1.f - zg) * ng + zg * hv;
+    out[row * ldo + col] = o;
+    if (out2) out2[row * ldo2 + col] = A::fromf(o);
+  }
 }
 
 // ---------------------------------------------------------------------------
-// Slot-attention core, one workgroup per frame.
+// Slot-attention core.
 struct CoreArgs {
   int64_t ldq, ldk, ldv, ldo, qb, kb, vb, ob;  // row strides and frame strides (elements)
-  int N, M, D, NP, MP;                          // NP, MP: N, M rounded up to 16
+  int N, M, D, NT, MT;                          // NT = ceil(N/16), MT = ceil(M/16)
   float scale, denom_eps, logit_clamp, renorm_eps;
 };
 
-constexpr int CORE_VCHUNK = 32;   // tokens of v staged per phase-3 step
-constexpr int CORE_VPAD = 8;      // LDS row padding (elements) of the transposed v chunk
-constexpr int CORE_MAX_TILES = 16;  // output tiles per wave per phase-3 pass
+constexpr int CORE_MAX_NT = 8;  // up to 128 slots
 
+// P: [B][N][Mp] (Mp = 32 * ceil(M/32)) softmax in DT, zero for m >= M.  part: [B][MT][N] fp32.
+// Grid (frame, 16-token tile); the 4 waves split the D blocks, partial logits meet in LDS and
+// wave 0 finishes the softmax over slots.
 template <int DT, int AT>
 __global__ void __launch_bounds__(256)
-slot_core_kernel(const typename MM<DT>::T* __restrict__ q, const typename MM<DT>::T* __restrict__ k,
-                 const typename MM<DT>::T* __restrict__ v, typename MM<DT>::T* __restrict__ out,
-                 typename MM<AT>::T* __restrict__ attn_out, CoreArgs a) {
+core_logits_kernel(const typename MM<DT>::T* __restrict__ q, const typename MM<DT>::T* __restrict__ k,
+                   typename MM<DT>::T* __restrict__ P, int64_t Mp, float* __restrict__ part,
+                   typename MM<AT>::T* __restrict__ attn_out, CoreArgs a) {
   using A = MM<DT>;
-  using TT = typename A::T;
   constexpr int KPL = A::KPL;
-  extern __shared__ __align__(16) unsigned char smem[];
-  float* S = reinterpret_cast<float*>(smem);                          // [NP][MP] fp32
-  TT* P = reinterpret_cast<TT*>(S + (size_t)a.NP * a.MP);             // [NP][MP] operand copy
-  float* rs = reinterpret_cast<float*>(P + (size_t)a.NP * a.MP);       // [NP]
-  TT* VT = reinterpret_cast<TT*>(rs + a.NP + 4);                       // [D][VCHUNK + VPAD]
-  const int VLD = CORE_VCHUNK + CORE_VPAD;
-
+  constexpr int BLK = 4 * KPL;
+  __shared__ float red[4][CORE_MAX_NT][4][64];   // 32 KB
   const int64_t b = blockIdx.x;
-  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, g = lane >> 4, li = lane & 15;
-  const TT* qb = q + b * a.qb;
-  const TT* kb = k + b * a.kb;
-  const TT* vb = v + b * a.vb;
-
-  // ---- phase 1: logits
-  {
-    const int nt_n = a.NP / 16, nt_m = a.MP / 16;
-    const int D4 = a.D / 4;
-    for (int tile = wid; tile < nt_n * nt_m; tile += 4) {
-      const int tn = tile / nt_m, tmm = tile - tn * nt_m;
-      int rn = tn * 16 + li;
-      rn = rn < a.N ? rn : a.N - 1;
-      int rm = tmm * 16 + li;
-      rm = rm < a.M ? rm : a.M - 1;
-      const TT* pq = qb + (int64_t)rn * a.ldq + g * D4;
-      const TT* pk = kb + (int64_t)rm * a.ldk + g * D4;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      for (int c = 0; c < D4; c += KPL) acc = A::mfma(A::load(pq + c), A::load(pk + c), acc);
+  const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, li = lane & 15;
+  const int mt = blockIdx.y;
+  const int m = mt * 16 + li;                  // this lane's token (column)
+  const bool mvalid = m < a.M;
+  const typename A::T* kp = k + b * a.kb + (int64_t)(mvalid ? m : a.M - 1) * a.ldk + KPL * g;
+  f32x4 acc[CORE_MAX_NT];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) S[(tn * 16 + 4 * g + r) * a.MP + tmm * 16 + li] = acc[r] * a.scale;
+  for (int nt = 0; nt < CORE_MAX_NT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int nblk = a.D / BLK;
+  const typename A::T* qrow[CORE_MAX_NT];
+#pragma unroll
+  for (int nt = 0; nt < CORE_MAX_NT; ++nt) {
+    int n = nt * 16 + li;
+    n = n < a.N ? n : a.N - 1;
+    qrow[nt] = q + b * a.qb + (int64_t)n * a.ldq + KPL * g;
+  }
+#pragma unroll 2
+  for (int s = wid; s < nblk; s += 4) {
+    const typename A::Op kb_ = A::load(kp + (int64_t)s * BLK);
+#pragma unroll
+    for (int nt = 0; nt < CORE_MAX_NT; ++nt) {
+      if (nt < a.NT) {
+        const typename A::Op qa = A::load(qrow[nt] + (int64_t)s * BLK);
+        acc[nt] = A::mfma(qa, kb_, acc[nt]);   // acc[nt][r] = logit[n = 16nt + 4g + r][m]
+      }
     }
   }
+#pragma unroll
+  for (int nt = 0; nt < CORE_MAX_NT; ++nt)
+    if (nt < a.NT)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[wid][nt][r][lane] = acc[nt][r];
   __syncthreads();
-
-  // ---- phase 2: softmax over slots per token (+ optional renorm over tokens)
-  for (int m = tid; m < a.MP; m += 256) {
-    if (m < a.M) {
-      float mx = -INFINITY;
-      for (int n = 0; n < a.N; ++n) {
-        float s = S[n * a.MP + m];
-        if (a.logit_clamp > 0.f) s = fminf(fmaxf(s, -a.logit_clamp), a.logit_clamp);
-        S[n * a.MP + m] = s;
-        mx = fmaxf(mx, s);
-      }
-      float sum = 0.f;
-      for (int n = 0; n < a.N; ++n) {
-        const float e = __expf(S[n * a.MP + m] - mx);
-        S[n * a.MP + m] = e;
-        sum += e;
-      }
-      const float inv = 1.f / (sum + a.denom_eps);
-      for (int n = 0; n < a.N; ++n) {
-        const float p = S[n * a.MP + m] * inv;
-        S[n * a.MP + m] = p;
-        if (attn_out) attn_out[b * (int64_t)a.N * a.M + (int64_t)n * a.M + m] = MM<AT>::fromf(p);
-      }
-      for (int n = a.N; n < a.NP; ++n) S[n * a.MP + m] = 0.f;
-    } else {
-      for (int n = 0; n < a.NP; ++n) S[n * a.MP + m] = 0.f;
+  if (wid != 0) return;
+#pragma unroll
+  for (int nt = 0; nt < CORE_MAX_NT; ++nt)
+    if (nt < a.NT)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        acc[nt][r] = red[0][nt][r][lane] + red[1][nt][r][lane] + red[2][nt][r][lane] + red[3][nt][r][lane];
+  // softmax over slots for column m: values over (nt, r) in-lane and over g across lanes
+  float mx = -INFINITY;
+#pragma unroll
+  for (int nt = 0; nt < CORE_MAX_NT; ++nt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int n = nt * 16 + 4 * g + r;
+      float s = acc[nt][r] * a.scale;
+      if (a.logit_clamp > 0.f) s = fminf(fmaxf(s, -a.logit_clamp), a.logit_clamp);
+      s = (nt < a.NT && n < a.N) ? s : -INFINITY;
+      acc[nt][r] = s;
+      mx = fmaxf(mx, s);
     }
-  }
-  __syncthreads();
-  const bool renorm = a.renorm_eps >= 0.f;
-  if (renorm) {
-    for (int n = wid; n < a.N; n += 4) {
-      float s = 0.f;
-      for (int m = lane; m < a.M; m += 64) s += S[n * a.MP + m] + a.renorm_eps;
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  float sum = 0.f;
 #pragma unroll
-      for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
-      if (lane == 0) rs[n] = 1.f / s;
+  for (int nt = 0; nt < CORE_MAX_NT; ++nt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float e = (nt < a.NT) ? __expf(acc[nt][r] - mx) : 0.f;
+      acc[nt][r] = e;
+      sum += e;
     }
-    __syncthreads();
-  }
-  for (int i = tid; i < a.NP * a.MP; i += 256) {
-    const int n = i / a.MP, m = i - n * a.MP;
-    float p = S[i];
-    if (renorm) p = (n < a.N && m < a.M) ? (p + a.renorm_eps) * rs[n] : 0.f;
-    P[i] = A::fromf(p);
-  }
-  __syncthreads();
-
-  // ---- phase 3: updates = attn . v, 32 tokens at a time, v chunk transposed in LDS
-  const int nt_n = a.NP / 16, nt_d = a.D / 16;
-  const int ntiles = nt_n * nt_d;
-  for (int tbase = 0; tbase < ntiles; tbase += 4 * CORE_MAX_TILES) {
-    f32x4 acc[CORE_MAX_TILES];
+  sum += __shfl_xor(sum, 16, 64);
+  sum += __shfl_xor(sum, 32, 64);
+  const float inv = 1.f / (sum + a.denom_eps);
 #pragma unroll
-    for (int i = 0; i < CORE_MAX_TILES; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int m0 = 0; m0 < a.MP; m0 += CORE_VCHUNK) {
-      // stage v[m0 .. m0+31][0 .. D) transposed: VT[d][ml]; rows past M are zero
-      for (int i = tid; i < CORE_VCHUNK * a.D; i += 256) {
-        const int ml = i / a.D, d = i - ml * a.D;
-        const int m = m0 + ml;
-        VT[d * VLD + ml] = (m < a.M) ? vb[(int64_t)m * a.ldv + d] : A::fromf(0.f);
-      }
-      __syncthreads();
+  for (int nt = 0; nt < CORE_MAX_NT; ++nt) {
+    if (nt >= a.NT) break;
 #pragma unroll
-      for (int i = 0; i < CORE_MAX_TILES; ++i) {
-        const int tile = tbase + wid + 4 * i;
-        if (tile < ntiles) {
-          const int tn = tile / nt_d, td = tile - tn * nt_d;
-          const TT* pp = P + (tn * 16 + li) * a.MP + m0;
-          const TT* pv = VT + (td * 16 + li) * VLD;
-          if constexpr (KPL == 8) {
-            // one MFMA: lane group g covers tokens m0 + 8g .. 8g+7
-            acc[i] = A::mfma(A::load(pp + 8 * g), A::load(pv + 8 * g), acc[i]);
-          } else {
-#pragma unroll
-            for (int s = 0; s < CORE_VCHUNK / 4; ++s)
-              acc[i] = A::mfma(A::load(pp + 4 * s + g), A::load(pv + 4 * s + g), acc[i]);
-          }
-        }
-      }
-      __syncthreads();
-    }
-#pragma unroll
-    for (int i = 0; i < CORE_MAX_TILES; ++i) {
-      const int tile = tbase + wid + 4 * i;
-      if (tile < ntiles) {
-        const int tn = tile / nt_d, td = tile - tn * nt_d;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int n = tn * 16 + 4 * g + r;
-          if (n < a.N) out[b * a.ob + (int64_t)n * a.ldo + td * 16 + li] = A::fromf(acc[i][r]);
-        }
+    for (int r = 0; r < 4; ++r) {
+      const int n = nt * 16 + 4 * g + r;
+      const float p = mvalid ? acc[nt][r] * inv : 0.f;
+      float ps = p;   // partial sum over this tile's 16 tokens, for the renormalisation
+      ps += __shfl_xor(ps, 1, 64);
+      ps += __shfl_xor(ps, 2, 64);
+      ps += __shfl_xor(ps, 4, 64);
+      ps += __shfl_xor(ps, 8, 64);
+      if (n < a.N) {
+        P[(b * a.N + n) * Mp + m] = A::fromf(p);
+        if (attn_out && mvalid) attn_out[(b * a.N + n) * (int64_t)a.M + m] = MM<AT>::fromf(p);
+        if (li == 0 && part && mt < a.MT) part[(b * a.MT + mt) * a.N + n] = ps;
       }
     }
   }
 }
 
-static size_t core_smem(int NP, int MP, int D, int esize) {
-  return (size_t)NP * MP * 4 + (size_t)NP * MP * esize + (size_t)(NP + 4) * 4 +
-         (size_t)D * (CORE_VCHUNK + CORE_VPAD) * esize;
+// attn . v with v given transposed per frame: vt[b][d][Mp] (rows of Mp tokens, m >= M ignored).
+// Grid (frame, 64-column block); wave w owns 16 columns; no LDS.
+template <int DT>
+__global__ void __launch_bounds__(256)
+core_update_t_kernel(const typename MM<DT>::T* __restrict__ P, int64_t Mp, const float* __restrict__ part,
+                     const typename MM<DT>::T* __restrict__ vt, typename MM<DT>::T* __restrict__ out, CoreArgs a) {
+  using A = MM<DT>;
+  using TT = typename A::T;
+  constexpr int KPL = A::KPL;
+  __shared__ float rinv_s[CORE_MAX_NT * 16];
+  const int64_t b = blockIdx.x;
+  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, g = lane >> 4, li = lane & 15;
+  const int d = blockIdx.y * 64 + wid * 16 + li;
+  const int dc = d < a.D ? d : a.D - 1;
+  const bool renorm = a.renorm_eps >= 0.f;
+  if (tid < a.NT * 16) {   // 1 / sum_m (attn + eps) per slot, from the per-tile partial sums
+    float s = 1.f;
+    if (renorm && tid < a.N) {
+      float t = 0.f;
+      for (int j = 0; j < a.MT; ++j) t += part[(b * a.MT + j) * a.N + tid];
+      s = 1.f / (t + (float)a.M * a.renorm_eps);
+    }
+    rinv_s[tid] = s;
+  }
+  __syncthreads();
+  const TT* pv = vt + b * a.vb + (int64_t)dc * Mp;
+  const TT* prow[CORE_MAX_NT];
+#pragma unroll
+  for (int nt = 0; nt < CORE_MAX_NT; ++nt) {
+    int n = nt * 16 + li;
+    n = n < a.N ? n : a.N - 1;
+    prow[nt] = P + (b * a.N + n) * Mp;
+  }
+  f32x4 acc[CORE_MAX_NT];
+#pragma unroll
+  for (int nt = 0; nt < CORE_MAX_NT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float cs = 0.f;
+#pragma unroll 2
+  for (int m0 = 0; m0 < (int)Mp; m0 += 32) {
+    if constexpr (KPL == 8) {
+      typename A::Op bv = A::load(pv + m0 + 8 * g);
+      if (m0 + 32 > a.M) {   // tokens past M: v rows are not initialised, zero them
+        TT e[8];
+        *reinterpret_cast<uint4*>(e) = __builtin_bit_cast(uint4, bv);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          if (m0 + 8 * g + i >= a.M) e[i] = A::fromf(0.f);
+        bv = __builtin_bit_cast(typename A::Op, *reinterpret_cast<uint4*>(e));
+      }
+      if (renorm) {
+        TT e[8];
+        *reinterpret_cast<uint4*>(e) = __builtin_bit_cast(uint4, bv);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) cs += A::tof(e[i]);
+      }
+#pragma unroll
+      for (int nt = 0; nt < CORE_MAX_NT; ++nt)
+        if (nt < a.NT) acc[nt] = A::mfma(A::load(prow[nt] + m0 + 8 * g), bv, acc[nt]);
+    } else {
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const int mm = m0 + 4 * s + g;
+        float bv = mm < a.M ? pv[mm] : 0.f;
+        if (renorm) cs += bv;
+#pragma unroll
+        for (int nt = 0; nt < CORE_MAX_NT; ++nt)
+          if (nt < a.NT) acc[nt] = A::mfma(prow[nt][mm], bv, acc[nt]);
+      }
+    }
+  }
+  cs += __shfl_xor(cs, 16, 64);
+  cs += __shfl_xor(cs, 32, 64);
+  if (d >= a.D) return;
+  const float epsv = renorm ? a.renorm_eps * cs : 0.f;
+#pragma unroll
+  for (int nt = 0; nt < CORE_MAX_NT; ++nt) {
+    if (nt >= a.NT) break;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int n = nt * 16 + 4 * g + r;
+      if (n < a.N) out[b * a.ob + (int64_t)n * a.ldo + d] = A::fromf((acc[nt][r] + epsv) * rinv_s[n]);
+    }
+  }
+}
+
+constexpr int CORE_DB = 64;          // output columns per workgroup
+constexpr int CORE_MAXM = 256;       // tokens staged in LDS at once (longer inputs loop)
+
+template <int DT>
+__global__ void __launch_bounds__(256)
+core_update_kernel(const typename MM<DT>::T* __restrict__ P, int64_t Mp, const float* __restrict__ part,
+                   const typename MM<DT>::T* __restrict__ v, typename MM<DT>::T* __restrict__ out, CoreArgs a) {
+  using A = MM<DT>;
+  using TT = typename A::T;
+  constexpr int KPL = A::KPL;
+  constexpr int VLD = CORE_MAXM + 8;   // row stride of the transposed chunk (elements)
+  __shared__ __align__(16) TT VT[CORE_DB * VLD];
+  __shared__ float colsum[CORE_DB];
+  __shared__ float rinv[CORE_MAX_NT * 16];
+  const int64_t b = blockIdx.x;
+  const int d0 = blockIdx.y * CORE_DB;
+  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, g = lane >> 4, li = lane & 15;
+  const bool renorm = a.renorm_eps >= 0.f;
+  if (tid < a.NT * 16) {
+    float s = 1.f;
+    if (renorm && tid < a.N) {
+      float t = 0.f;
+      for (int j = 0; j < a.MT; ++j) t += part[(b * a.MT + j) * a.N + tid];
+      s = 1.f / (t + (float)a.M * a.renorm_eps);
+    }
+    rinv[tid] = s;
+  }
+  const int dt = wid;   // wave -> 16-column tile of the 64-column block
+  f32x4 acc[CORE_MAX_NT];
+#pragma unroll
+  for (int nt = 0; nt < CORE_MAX_NT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const TT* vb = v + b * a.vb;
+  float cs = 0.f;
+  for (int m0 = 0; m0 < (int)Mp; m0 += CORE_MAXM) {
+    const int mc = ((int)Mp - m0) < CORE_MAXM ? ((int)Mp - m0) : CORE_MAXM;   // multiple of 32
+    __syncthreads();
+    // one pass: thread i loads v[m0 + ml][d0 + dl] for all (ml, dl) of the chunk
+    for (int i = tid; i < mc * CORE_DB; i += 256) {
+      const int ml = i / CORE_DB, dl = i - ml * CORE_DB;
+      const int m = m0 + ml, d = d0 + dl;
+      VT[dl * VLD + ml] = (m < a.M && d < a.D) ? vb[(int64_t)m * a.ldv + d] : A::fromf(0.f);
+    }
+    __syncthreads();
+    if (renorm && tid < CORE_DB)
+      for (int ml = 0; ml < mc; ++ml) cs += A::tof(VT[tid * VLD + ml]);
+    const TT* pv = VT + (dt * 16 + li) * VLD;
+    for (int mm = 0; mm < mc; mm += 32) {
+#pragma unroll
+      for (int nt = 0; nt < CORE_MAX_NT; ++nt) {
+        if (nt < a.NT) {
+          int n = nt * 16 + li;
+          n = n < a.N ? n : a.N - 1;
+          const TT* pp = P + (b * a.N + n) * Mp + m0 + mm;
+          if constexpr (KPL == 8) {
+            acc[nt] = A::mfma(A::load(pp + 8 * g), A::load(pv + mm + 8 * g), acc[nt]);
+          } else {
+#pragma unroll
+            for (int s = 0; s < 8; ++s)
+              acc[nt] = A::mfma(A::load(pp + 4 * s + g), A::load(pv + mm + 4 * s + g), acc[nt]);
+          }
+        }
+      }
+    }
+  }
+  if (tid < CORE_DB) colsum[tid] = cs;
+  __syncthreads();
+  const int d = d0 + dt * 16 + li;
+  if (d >= a.D) return;
+  const float epsv = renorm ? a.renorm_eps * colsum[dt * 16 + li] : 0.f;
+#pragma unroll
+  for (int nt = 0; nt < CORE_MAX_NT; ++nt) {
+    if (nt >= a.NT) break;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int n = nt * 16 + 4 * g + r;
+      if (n < a.N) out[b * a.ob + (int64_t)n * a.ldo + d] = A::fromf((acc[nt][r] + epsv) * rinv[n]);
+    }
+  }
 }
 
 static bool al16(const void* p) { return (((uintptr_t)p) & 15) == 0; }
 
-}  // namespace hclsm
+static size_t core_ws_bytes(int64_t B, int64_t N, int64_t M, int esize) {
+  const int64_t Mp = (M + 31) / 32 * 32, MT = (M + 15) / 16;
+  size_t p = (size_t)B * N * Mp * esize;
+  p = (p + 255) / 256 * 256;
+  return p + (size_t)B * MT * N * 4;
+}
 
-using namespace hclsm;
+static int launch_core(const void* q, int64_t ldq, int64_t qbs, const void* k, int64_t ldk, int64_t kbs,
+                       const void* v, int64_t ldv, int64_t vbs, void* out, int64_t ldo, int64_t obs, void* attn,
+                       int attn_dtype, int64_t B, int64_t N, int64_t M, int64_t D, float scale, float denom_eps,
+                       float logit_clamp, float renorm_eps, int dtype, void* ws, hipStream_t st,
+                       bool v_transposed = false) {
+  CoreArgs a;
+  a.ldq = ldq; a.ldk = ldk; a.ldv = ldv; a.ldo = ldo;
+  a.qb = qbs; a.kb = kbs; a.vb = vbs; a.ob = obs;
+  a.N = (int)N; a.M = (int)M; a.D = (int)D;
+  a.NT = (int)((N + 15) / 16);
+  a.MT = (int)((M + 15) / 16);
+  a.scale = scale; a.denom_eps = denom_eps; a.logit_clamp = logit_clamp; a.renorm_eps = renorm_eps;
+  const int64_t Mp = (M + 31) / 32 * 32;
+  const int esize = dtype == HCLSM_F32 ? 4 : 2;
+  size_t poff = (size_t)B * N * Mp * esize;
+  poff = (poff + 255) / 256 * 256;
+  float* part = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + poff);
+  dim3 g1((unsigned)B, (unsigned)(Mp / 16));
+  dim3 g2((unsigned)B, (unsigned)((D + CORE_DB - 1) / CORE_DB));
+#define HCLSM_CORE(D_, A_)                                                                                   \
+  if (dtype == D_ && (attn == nullptr ? A_ == D_ : attn_dtype == A_)) {                                      \
+    hipLaunchKernelGGL((core_logits_kernel<D_, A_>), g1, dim3(256), 0, st, (const MM<D_>::T*)q,             \
+                       (const MM<D_>::T*)k, (MM<D_>::T*)ws, Mp, part, (MM<A_>::T*)attn, a);                  \
+    HCLSM_LAUNCH_CHECK();                                                                                    \
+    if (v_transposed)                                                                                        \
+      hipLaunchKernelGGL((core_update_t_kernel<D_>), g2, dim3(256), 0, st, (const MM<D_>::T*)ws, Mp, part,   \
+                         (const MM<D_>::T*)v, (MM<D_>::T*)out, a);                                           \
+    else                                                                                                     \
+      hipLaunchKernelGGL((core_update_kernel<D_>), g2, dim3(256), 0, st, (const MM<D_>::T*)ws, Mp, part,     \
+                         (const MM<D_>::T*)v, (MM<D_>::T*)out, a);                                           \
+    HCLSM_LAUNCH_CHECK();                                                                                    \
+    return 0;                                                                                                \
+  }
+  HCLSM_CORE(HCLSM_BF16, HCLSM_BF16)
+  HCLSM_CORE(HCLSM_BF16, HCLSM_F32)
+  HCLSM_CORE(HCLSM_F16, HCLSM_F16)
+  HCLSM_CORE(HCLSM_F16, HCLSM_F32)
+  HCLSM_CORE(HCLSM_F32, HCLSM_F32)
+#undef HCLSM_CORE
+  return HCLSM_ERR_DTYPE;
+}
 
-extern "C" int hclsm_layer_norm(const void* x, int64_t ldx, const float* w, const float* b, void* y, int64_t ldy,
-                                int64_t M, int64_t D, float eps, int in_dtype, int out_dtype, void* stream) {
+static int check_core(const void* q, int64_t ldq, int64_t qbs, const void* k, int64_t ldk, int64_t kbs, int64_t B,
+                      int64_t N, int64_t M, int64_t D, int dtype) {
+  if (B < 0 || N < 0 || M < 0 || D < 0 || B > 65535 || M > (1 << 20)) return HCLSM_ERR_SHAPE;
+  if (N > 16 * CORE_MAX_NT) return HCLSM_ERR_UNSUPPORTED;
+  if (dtype != HCLSM_BF16 && dtype != HCLSM_F16 && dtype != HCLSM_F32) return HCLSM_ERR_DTYPE;
+  const int kpl = dtype == HCLSM_F32 ? 1 : 8;
+  if (D % (4 * kpl) || D % 16) return HCLSM_ERR_UNSUPPORTED;
+  if (kpl == 8 && (!al16(q) || !al16(k) || ldq % 8 || ldk % 8 || qbs % 8 || kbs % 8)) return HCLSM_ERR_UNSUPPORTED;
+  return 0;
+}
+
+template <int DT, int OT, typename XT>
+static void launch_linear_quad(const void* x, int64_t ldx, const void* w, int64_t ldw, const float* bias,
+                               const float* resid, int64_t ldr, void* y, int64_t ldy, void* y2, int64_t ldy2,
+                               int64_t M, int64_t N, int64_t K, int relu, float clamp, hipStream_t st,
+                               OutSplit os = OutSplit{0, 1, 0, 0, nullptr}) {
+  if constexpr (std::is_same_v<XT, typename MM<DT>::T>) {
+    const unsigned grid = (unsigned)(((M + 63) / 64) * ((N + 63) / 64));
+    hipLaunchKernelGGL((linear_quad_kernel<DT, OT>), dim3(grid), dim3(256), 0, st, (const typename MM<DT>::T*)x, ldx,
+                       (const typename MM<DT>::T*)w, ldw, bias, resid, ldr, (typename MM<OT>::T*)y, ldy,
+                       (typename MM<DT>::T*)y2, ldy2, M, N, K, relu, clamp, os);
+  }
+}
+
+template <int DT, int OT, typename XT>
+static void launch_linear_t(bool ln, const void* x, int64_t ldx, const void* w, int64_t ldw, const float* bias,
+                            const float* resid, int64_t ldr, void* y, int64_t ldy, void* y2, int64_t ldy2, int64_t M,
+                            int64_t N, int64_t K, int relu, float clamp, const float* lnw, const float* lnb,
+                            float eps, hipStream_t st) {
+  const int64_t tiles32 = ((M + 31) / 32) * ((N + 31) / 32);
+  if (!ln && std::is_same_v<XT, typename MM<DT>::T> && tiles32 >= 2048) {
+    launch_linear_quad<DT, OT, XT>(x, ldx, w, ldw, bias, resid, ldr, y, ldy, y2, ldy2, M, N, K, relu, clamp, st);
+    return;
+  }
+  const unsigned grid = (unsigned)tiles32;
+  if (ln)
+    hipLaunchKernelGGL((linear_kernel<DT, OT, XT, true>), dim3(grid), dim3(256), 0, st, (const XT*)x, ldx,
+                       (const typename MM<DT>::T*)w, ldw, bias, resid, ldr, (typename MM<OT>::T*)y, ldy,
+                       (typename MM<DT>::T*)y2, ldy2, M, N, K, relu, clamp, lnw, lnb, eps);
+  else
+    hipLaunchKernelGGL((linear_kernel<DT, OT, XT, false>), dim3(grid), dim3(256), 0, st, (const XT*)x, ldx,
+                       (const typename MM<DT>::T*)w, ldw, bias, resid, ldr, (typename MM<OT>::T*)y, ldy,
+                       (typename MM<DT>::T*)y2, ldy2, M, N, K, relu, clamp, lnw, lnb, eps);
+}
+
+static int linear_impl(const void* x, int64_t ldx, int x_dtype, const void* w, int64_t ldw, const float* bias,
+                       const float* resid, int64_t ldr, void* y, int64_t ldy, int y_dtype, void* y2, int64_t ldy2,
+                       int64_t M, int64_t N, int64_t K, int relu, float clamp, int ln, const float* lnw,
+                       const float* lnb, float ln_eps, int dtype, hipStream_t st) {
+  if (M < 0 || N < 0 || K < 0) return HCLSM_ERR_SHAPE;
+  if (M == 0 || N == 0) return 0;
+  if (!x || !w || !y) return HCLSM_ERR_NULL;
+  const int kpl = dtype == HCLSM_F32 ? 1 : 8;
+  if (K % (4 * kpl) != 0 || K == 0) return HCLSM_ERR_UNSUPPORTED;
+  if (kpl == 8 && (!al16(w) || ldw % 8)) return HCLSM_ERR_UNSUPPORTED;
+  if (kpl == 8 && x_dtype == dtype && (!al16(x) || ldx % 8)) return HCLSM_ERR_UNSUPPORTED;
+  const bool LNf = ln != 0;
+#define HCLSM_LIN(D, O, XD, XT)                                                                              \
+  if (dtype == D && y_dtype == O && x_dtype == XD) {                                                         \
+    launch_linear_t<D, O, XT>(LNf, x, ldx, w, ldw, bias, resid, ldr, y, ldy, y2, ldy2, M, N, K, relu, clamp, lnw, \
+                              lnb, ln_eps, st);                                                              \
+    HCLSM_LAUNCH_CHECK();                                                                                    \
+    return 0;                                                                                                \
+  }
+  HCLSM_LIN(HCLSM_BF16, HCLSM_BF16, HCLSM_BF16, uint16_t)
+  HCLSM_LIN(HCLSM_BF16, HCLSM_F32, HCLSM_BF16, uint16_t)
+  HCLSM_LIN(HCLSM_BF16, HCLSM_BF16, HCLSM_F32, float)
+  HCLSM_LIN(HCLSM_BF16, HCLSM_F32, HCLSM_F32, float)
+  HCLSM_LIN(HCLSM_F16, HCLSM_F16, HCLSM_F16, _Float16)
+  HCLSM_LIN(HCLSM_F16, HCLSM_F32, HCLSM_F16, _Float16)
+  HCLSM_LIN(HCLSM_F16, HCLSM_F16, HCLSM_F32, float)
+  HCLSM_LIN(HCLSM_F16, HCLSM_F32, HCLSM_F32, float)
+  HCLSM_LIN(HCLSM_F32, HCLSM_F32, HCLSM_F32, float)
+#undef HCLSM_LIN
+  return HCLSM_ERR_DTYPE;
+}
+
+static int gru_impl(const void* x, int64_t ldx, const void* hb, int64_t ldhb, const float* h, int64_t ldh,
+                    const void* w_ih, const void* w_hh, const float* b_ih, const float* b_hh, float* out, int64_t ldo,
+                    void* out2, int64_t ldo2, int64_t M, int64_t H, int64_t Kx, int dtype, hipStream_t st) {
+  if (M < 0 || H < 0 || Kx < 0) return HCLSM_ERR_SHAPE;
+  if (M == 0 || H == 0) return 0;
+  if (!x || !hb || !h || !w_ih || !w_hh || !out) return HCLSM_ERR_NULL;
+  const int kpl = dtype == HCLSM_F32 ? 1 : 8;
+  if (Kx % (4 * kpl) || H % (4 * kpl)) return HCLSM_ERR_UNSUPPORTED;
+  if (kpl == 8 && (!al16(x) || !al16(hb) || !al16(w_ih) || !al16(w_hh) || ldx % 8 || ldhb % 8))
+    return HCLSM_ERR_UNSUPPORTED;
+  const unsigned grid = (unsigned)(((M + 31) / 32) * ((H + 15) / 16));
+#define HCLSM_GRU(D)                                                                                        \
+  if (dtype == D) {                                                                                         \
+    hipLaunchKernelGGL((gru_kernel<D>), dim3(grid), dim3(256), 0, st, (const MM<D>::T*)x, ldx,               \
+                       (const MM<D>::T*)hb, ldhb, h, ldh, (const MM<D>::T*)w_ih, (const MM<D>::T*)w_hh, b_ih, \
+                       b_hh, out, ldo, (MM<D>::T*)out2, ldo2, M, H, Kx);                                    \
+    HCLSM_LAUNCH_CHECK();                                                                                   \
+    return 0;                                                                                               \
+  }
+  HCLSM_GRU(HCLSM_BF16)
+  HCLSM_GRU(HCLSM_F16)
+  HCLSM_GRU(HCLSM_F32)
+#undef HCLSM_GRU
+  return HCLSM_ERR_DTYPE;
+}
+
+// ---------------------------------------------------------------------------
+// LayerNorm kernel (standalone entry point): one wave per row, values kept in registers.
+template <int DTI, int DTO>
+__global__ void __launch_bounds__(256)
+layer_norm_kernel(const typename MM<DTI>::T* __restrict__ x, int64_t ldx, const float* __restrict__ w,
+                  const float* __restrict__ b, typename MM<DTO>::T* __restrict__ y, int64_t ldy, int64_t M,
+                  int D, float eps) {
+  constexpr int MAXPL = 16;  // elements per lane held in registers (D <= 1024); larger D re-reads
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= M) return;
+  const typename MM<DTI>::T* xr = x + row * ldx;
+  float vals[MAXPL];
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < MAXPL; ++j) {
+    const int i = lane + 64 * j;
+    vals[j] = i < D ? MM<DTI>::tof(xr[i]) : 0.f;
+    s += vals[j];
+  }
+  for (int i = lane + 64 * MAXPL; i < D; i += 64) s += MM<DTI>::tof(xr[i]);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+  const float mean = s / (float)D;
+  float v = 0.f;
+#pragma unroll
+  for (int j = 0; j < MAXPL; ++j) {
+    const int i = lane + 64 * j;
+    const float d = vals[j] - mean;
+    v += i < D ? d * d : 0.f;
+  }
+  for (int i = lane + 64 * MAXPL; i < D; i += 64) {
+    const float d = MM<DTI>::tof(xr[i]) - mean;
+    v += d * d;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  const float rstd = 1.f / sqrtf(v / (float)D + eps);
+  typename MM<DTO>::T* yr = y + row * ldy;
+#pragma unroll
+  for (int j = 0; j < MAXPL; ++j) {
+    const int i = lane + 64 * j;
+    if (i < D) {
+      float t = (vals[j] - mean) * rstd;
+      if (w) t *= w[i];
+      if (b) t += b[i];
+      yr[i] = MM<DTO>::fromf(t);
+    }
+  }
+  for (int i = lane + 64 * MAXPL; i < D; i += 64) {
+    float t = (MM<DTI>::tof(xr[i]) - mean) * rstd;
+    if (w) t *= w[i];
+    if (b) t += b[i];
+    yr[i] = MM<DTO>::fromf(t);
+  }
+}
+
+static int ln_impl(const void* x, int64_t ldx, const float* w, const float* b, void* y, int64_t ldy, int64_t M,
+                   int64_t D, float eps, int in_dtype, int out_dtype, hipStream_t st) {
   if (M < 0 || D < 0 || D > 0x7fffffff) return HCLSM_ERR_SHAPE;
   if (M == 0 || D == 0) return 0;
   if (!x || !y) return HCLSM_ERR_NULL;
-  hipStream_t st = (hipStream_t)stream;
   const unsigned grid = (unsigned)((M + 3) / 4);
 #define HCLSM_LN(I, O)                                                                                     \
   if (in_dtype == I && out_dtype == O) {                                                                   \
@@ -377,106 +879,231 @@ extern "C" int hclsm_layer_norm(const void* x, int64_t ldx, const float* w, cons
   return HCLSM_ERR_DTYPE;
 }
 
-extern "C" int hclsm_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, const float* bias,
+}  // namespace hclsm
+
+using namespace hclsm;
+
+extern "C" int hclsm_layer_norm(const void* x, int64_t ldx, const float* w, const float* b, void* y, int64_t ldy,
+                                int64_t M, int64_t D, float eps, int in_dtype, int out_dtype, void* stream) {
+  return ln_impl(x, ldx, w, b, y, ldy, M, D, eps, in_dtype, out_dtype, (hipStream_t)stream);
+}
+
+extern "C" int hclsm_linear(const void* x, int64_t ldx, int x_dtype, const void* w, int64_t ldw, const float* bias,
                             const float* resid, int64_t ldr, void* y, int64_t ldy, int y_dtype, void* y2,
-                            int64_t ldy2, int64_t M, int64_t N, int64_t K, int relu, float clamp, int dtype,
-                            void* stream) {
-  if (M < 0 || N < 0 || K < 0) return HCLSM_ERR_SHAPE;
-  if (M == 0 || N == 0) return 0;
-  if (!x || !w || !y) return HCLSM_ERR_NULL;
-  const int kpl = dtype == HCLSM_F32 ? 1 : 8;
-  if (K % (4 * kpl) != 0) return HCLSM_ERR_UNSUPPORTED;
-  if (kpl == 8 && (!al16(x) || !al16(w) || ldx % 8 || ldw % 8)) return HCLSM_ERR_UNSUPPORTED;
-  hipStream_t st = (hipStream_t)stream;
-  const int64_t waves = ((M + 31) / 32) * ((N + 31) / 32);
-  const unsigned grid = (unsigned)((waves + 3) / 4);
-#define HCLSM_LIN(D, O)                                                                                    \
-  if (dtype == D && y_dtype == O) {                                                                        \
-    hipLaunchKernelGGL((linear_kernel<D, O>), dim3(grid), dim3(256), 0, st, (const MM<D>::T*)x, ldx,        \
-                       (const MM<D>::T*)w, ldw, bias, resid, ldr, (MM<O>::T*)y, ldy, (MM<D>::T*)y2, ldy2, M,  \
-                       N, K, relu, clamp);                                                                 \
-    HCLSM_LAUNCH_CHECK();                                                                                  \
-    return 0;                                                                                              \
-  }
-  HCLSM_LIN(HCLSM_BF16, HCLSM_BF16)
-  HCLSM_LIN(HCLSM_BF16, HCLSM_F32)
-  HCLSM_LIN(HCLSM_F16, HCLSM_F16)
-  HCLSM_LIN(HCLSM_F16, HCLSM_F32)
-  HCLSM_LIN(HCLSM_F32, HCLSM_F32)
-#undef HCLSM_LIN
-  return HCLSM_ERR_DTYPE;
+                            int64_t ldy2, int64_t M, int64_t N, int64_t K, int relu, float clamp, int ln,
+                            const float* ln_w, const float* ln_b, float ln_eps, int dtype, void* stream) {
+  return linear_impl(x, ldx, x_dtype, w, ldw, bias, resid, ldr, y, ldy, y_dtype, y2, ldy2, M, N, K, relu, clamp, ln,
+                     ln_w, ln_b, ln_eps, dtype, (hipStream_t)stream);
 }
 
 extern "C" int hclsm_gru_cell(const void* x, int64_t ldx, const void* hb, int64_t ldhb, const float* h, int64_t ldh,
                               const void* w_ih, const void* w_hh, const float* b_ih, const float* b_hh, float* out,
                               int64_t ldo, void* out2, int64_t ldo2, int64_t M, int64_t H, int64_t Kx, int dtype,
                               void* stream) {
-  if (M < 0 || H < 0 || Kx < 0) return HCLSM_ERR_SHAPE;
-  if (M == 0 || H == 0) return 0;
-  if (!x || !hb || !h || !w_ih || !w_hh || !out) return HCLSM_ERR_NULL;
-  const int kpl = dtype == HCLSM_F32 ? 1 : 8;
-  if (Kx % (4 * kpl) || H % (4 * kpl)) return HCLSM_ERR_UNSUPPORTED;
-  if (kpl == 8 && (!al16(x) || !al16(hb) || !al16(w_ih) || !al16(w_hh) || ldx % 8 || ldhb % 8))
-    return HCLSM_ERR_UNSUPPORTED;
-  hipStream_t st = (hipStream_t)stream;
-  const int64_t waves = ((M + 31) / 32) * ((H + 15) / 16);
-  const unsigned grid = (unsigned)((waves + 3) / 4);
-#define HCLSM_GRU(D)                                                                                        \
-  if (dtype == D) {                                                                                         \
-    hipLaunchKernelGGL((gru_kernel<D>), dim3(grid), dim3(256), 0, st, (const MM<D>::T*)x, ldx,               \
-                       (const MM<D>::T*)hb, ldhb, h, ldh, (const MM<D>::T*)w_ih, (const MM<D>::T*)w_hh, b_ih, \
-                       b_hh, out, ldo, (MM<D>::T*)out2, ldo2, M, H, Kx);                                    \
-    HCLSM_LAUNCH_CHECK();                                                                                   \
-    return 0;                                                                                               \
-  }
-  HCLSM_GRU(HCLSM_BF16)
-  HCLSM_GRU(HCLSM_F16)
-  HCLSM_GRU(HCLSM_F32)
-#undef HCLSM_GRU
-  return HCLSM_ERR_DTYPE;
+  return gru_impl(x, ldx, hb, ldhb, h, ldh, w_ih, w_hh, b_ih, b_hh, out, ldo, out2, ldo2, M, H, Kx, dtype,
+                  (hipStream_t)stream);
+}
+
+extern "C" int64_t hclsm_slot_attn_core_workspace(int64_t B, int64_t N, int64_t M, int dtype) {
+  if (B < 0 || N < 0 || M < 0) return HCLSM_ERR_SHAPE;
+  return (int64_t)core_ws_bytes(B, N, M, dtype == HCLSM_F32 ? 4 : 2);
 }
 
 extern "C" int hclsm_slot_attn_core(const void* q, int64_t ldq, int64_t q_bstride, const void* k, int64_t ldk,
                                     int64_t k_bstride, const void* v, int64_t ldv, int64_t v_bstride, void* out,
                                     int64_t ldo, int64_t o_bstride, void* attn, int attn_dtype, int64_t B, int64_t N,
                                     int64_t M, int64_t D, float scale, float denom_eps, float logit_clamp,
-                                    float renorm_eps, int dtype, void* stream) {
-  if (B < 0 || N < 0 || M < 0 || D < 0 || B > 0x7fffffff || N > 4096 || M > 0x7fffffff) return HCLSM_ERR_SHAPE;
-  if (B == 0 || N == 0) return 0;
-  if (!q || !k || !v || !out) return HCLSM_ERR_NULL;
-  if (dtype != HCLSM_BF16 && dtype != HCLSM_F16 && dtype != HCLSM_F32) return HCLSM_ERR_DTYPE;
-  if (attn && attn_dtype != HCLSM_F32 && attn_dtype != dtype) return HCLSM_ERR_DTYPE;
-  const int kpl = dtype == HCLSM_F32 ? 1 : 8;
-  if (D % 16 || D % (4 * kpl)) return HCLSM_ERR_UNSUPPORTED;
-  if (kpl == 8 && (!al16(q) || !al16(k) || ldq % 8 || ldk % 8 || q_bstride % 8 || k_bstride % 8))
-    return HCLSM_ERR_UNSUPPORTED;
-  CoreArgs a;
-  a.ldq = ldq; a.ldk = ldk; a.ldv = ldv; a.ldo = ldo;
-  a.qb = q_bstride; a.kb = k_bstride; a.vb = v_bstride; a.ob = o_bstride;
-  a.N = (int)N; a.M = (int)M; a.D = (int)D;
-  a.NP = (int)((N + 15) / 16 * 16);
-  a.MP = (int)((M + 31) / 32 * 32);
-  a.scale = scale; a.denom_eps = denom_eps; a.logit_clamp = logit_clamp; a.renorm_eps = renorm_eps;
-  const int esize = dtype == HCLSM_F32 ? 4 : 2;
-  const size_t smem = core_smem(a.NP, a.MP, a.D, esize);
-  if (smem > 160 * 1024) return HCLSM_ERR_UNSUPPORTED;
+                                    float renorm_eps, int dtype, void* workspace, int64_t workspace_bytes,
+                                    void* stream) {
+  const int c = check_core(q, ldq, q_bstride, k, ldk, k_bstride, B, N, M, D, dtype);
+  if (c) return c;
+  if (B == 0 || N == 0 || D == 0) return 0;
   if (M == 0) return HCLSM_ERR_SHAPE;
+  if (!q || !k || !v || !out || !workspace) return HCLSM_ERR_NULL;
+  if (attn && attn_dtype != HCLSM_F32 && attn_dtype != dtype) return HCLSM_ERR_DTYPE;
+  if (workspace_bytes < (int64_t)core_ws_bytes(B, N, M, dtype == HCLSM_F32 ? 4 : 2)) return HCLSM_ERR_SHAPE;
+  if (!al16(workspace)) return HCLSM_ERR_UNSUPPORTED;
+  return launch_core(q, ldq, q_bstride, k, ldk, k_bstride, v, ldv, v_bstride, out, ldo, o_bstride, attn, attn_dtype, B,
+                     N, M, D, scale, denom_eps, logit_clamp, renorm_eps, dtype, workspace, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------
+// Whole iterations: the sequence of launches above, on one stream, out of one workspace.
+
+static size_t al256(size_t x) { return (x + 255) / 256 * 256; }
+
+struct SlotWs {
+  size_t q, core, upd, h, sb, m1, sfa, kv, vt, xn, xin, total;
+};
+
+static SlotWs slot_ws_layout(int64_t B, int64_t N, int64_t M, int64_t d, int64_t hidden, int esize, bool with_kv,
+                             int64_t d_in = 0) {
+  SlotWs w;
+  size_t o = 0;
+  const size_t rows = (size_t)B * N;
+  w.xn = o; o += al256(rows * d * esize);
+  w.xin = o; o += with_kv ? al256((size_t)B * M * (d_in > 0 ? d_in : d) * esize) : 0;
+  w.q = o; o += al256(rows * d * esize);
+  w.core = o; o += al256(core_ws_bytes(B, N, M, esize));
+  w.upd = o; o += al256(rows * d * esize);
+  w.h = o; o += al256(rows * d * 4);
+  w.sb = o; o += al256(rows * d * esize);
+  w.m1 = o; o += al256(rows * hidden * esize);
+  w.sfa = o; o += al256(rows * d * 4);
+  w.kv = o; o += with_kv ? al256((size_t)B * M * d * esize) : 0;
+  w.vt = o; o += with_kv ? al256((size_t)B * d * ((M + 31) / 32 * 32) * esize) : 0;
+  w.total = o;
+  return w;
+}
+
+extern "C" int64_t hclsm_slot_attention_workspace(int64_t B, int64_t N, int64_t M, int64_t d_in, int64_t d,
+                                                  int64_t hidden, int dtype) {
+  if (B < 0 || N < 0 || M < 0 || d_in < 0 || d < 0 || hidden < 0) return HCLSM_ERR_SHAPE;
+  return (int64_t)slot_ws_layout(B, N, M, d, hidden, dtype == HCLSM_F32 ? 4 : 2, true, d_in).total;
+}
+
+template <int DT>
+__global__ void __launch_bounds__(256)
+convert_f32_kernel(const float* __restrict__ src, typename MM<DT>::T* __restrict__ dst, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = MM<DT>::fromf(src[i]);
+}
+
+static int convert_f32(const float* src, void* dst, int64_t n, int dtype, hipStream_t st) {
+  if (n <= 0) return 0;
+  int64_t g = (n + 255) / 256;
+  g = g > 4096 ? 4096 : g;
+  if (dtype == HCLSM_BF16)
+    hipLaunchKernelGGL(convert_f32_kernel<HCLSM_BF16>, dim3((unsigned)g), dim3(256), 0, st, src, (uint16_t*)dst, n);
+  else if (dtype == HCLSM_F16)
+    hipLaunchKernelGGL(convert_f32_kernel<HCLSM_F16>, dim3((unsigned)g), dim3(256), 0, st, src, (_Float16*)dst, n);
+  else
+    hipLaunchKernelGGL(convert_f32_kernel<HCLSM_F32>, dim3((unsigned)g), dim3(256), 0, st, src, (float*)dst, n);
+  HCLSM_LAUNCH_CHECK();
+  return 0;
+}
+
+// One iteration (dynamic_slots.py:98-131).  slots_in fp32 and sb (the same slots in `dtype`) are
+// read; slots_out (may alias slots_in: it is written by the last launch, after every read) and
+// sb (rewritten with the new slots in `dtype`) are produced.
+static int slot_iteration_impl(const HclsmSlotWeights* W, const float* slots_in, void* sb, const void* k,
+                               int64_t ldk, int64_t k_bstride, const void* v, int64_t ldv, int64_t v_bstride,
+                               bool v_transposed, float* slots_out, int64_t B, int64_t N, int64_t M, int64_t d,
+                               int64_t hidden, float scale, float logit_clamp, float renorm_eps, float slot_clamp,
+                               int dtype, char* ws, const SlotWs& L, hipStream_t st) {
+  const int64_t rows = B * N;
+  void* q = ws + L.q;
+  void* upd = ws + L.upd;
+  float* h = reinterpret_cast<float*>(ws + L.h);
+  void* m1 = ws + L.m1;
+  void* xn = ws + L.xn;
+  // q = LN_pre(slots) W_q^T
+  int rc = ln_impl(slots_in, d, W->ln_pre_w, W->ln_pre_b, xn, d, rows, d, 1e-5f, HCLSM_F32, dtype, st);
+  if (rc) return rc;
+  rc = linear_impl(xn, d, dtype, W->w_q, d, nullptr, nullptr, 0, q, d, dtype, nullptr, 0, rows, d, d, 0, 0.f, 0,
+                   nullptr, nullptr, 0.f, dtype, st);
+  if (rc) return rc;
+  // updates = attention core (logits, softmax over slots, [renorm], attn v)
+  rc = launch_core(q, d, N * d, k, ldk, k_bstride, v, ldv, v_bstride, upd, d, N * d, nullptr, dtype, B, N, M, d,
+                   scale, 0.f, logit_clamp, renorm_eps, dtype, ws + L.core, st, v_transposed);
+  if (rc) return rc;
+  // h = GRUCell(updates, slots)
+  rc = gru_impl(upd, d, sb, d, slots_in, d, W->w_ih, W->w_hh, W->b_ih, W->b_hh, h, d, nullptr, 0, rows, d, d, dtype,
+                st);
+  if (rc) return rc;
+  // m1 = ReLU(LN_mlp(h) W1^T + b1)
+  rc = ln_impl(h, d, W->ln_mlp_w, W->ln_mlp_b, xn, d, rows, d, 1e-5f, HCLSM_F32, dtype, st);
+  if (rc) return rc;
+  rc = linear_impl(xn, d, dtype, W->w1, d, W->b1, nullptr, 0, m1, hidden, dtype, nullptr, 0, rows, hidden, d, 1, 0.f,
+                   0, nullptr, nullptr, 0.f, dtype, st);
+  if (rc) return rc;
+  // slots_out = clamp(h + m1 W2^T + b2); sb = the same in dtype
+  return linear_impl(m1, hidden, dtype, W->w2, hidden, W->b2, h, d, slots_out, d, HCLSM_F32, sb, d, rows, d, hidden, 0,
+                     slot_clamp, 0, nullptr, nullptr, 0.f, dtype, st);
+}
+
+static int check_slot_args(const HclsmSlotWeights* W, int64_t B, int64_t N, int64_t M, int64_t d, int64_t hidden,
+                           int dtype, void* workspace, int64_t workspace_bytes, bool with_kv, SlotWs* L,
+                           int64_t d_in = 0) {
+  if (!W || !workspace) return HCLSM_ERR_NULL;
+  if (!W->w_q || !W->w_ih || !W->w_hh || !W->w1 || !W->w2 || (with_kv && !W->w_kv)) return HCLSM_ERR_NULL;
+  if (B < 0 || N < 0 || M < 1 || d < 1 || hidden < 1) return HCLSM_ERR_SHAPE;
+  if (dtype != HCLSM_BF16 && dtype != HCLSM_F16 && dtype != HCLSM_F32) return HCLSM_ERR_DTYPE;
+  const int kpl = dtype == HCLSM_F32 ? 1 : 8;
+  if (d % 16 || d % (4 * kpl) || hidden % (4 * kpl)) return HCLSM_ERR_UNSUPPORTED;
+  if (N > 16 * CORE_MAX_NT || B > 65535) return HCLSM_ERR_UNSUPPORTED;
+  *L = slot_ws_layout(B, N, M, d, hidden, dtype == HCLSM_F32 ? 4 : 2, with_kv, d_in);
+  if (workspace_bytes < (int64_t)L->total) return HCLSM_ERR_SHAPE;
+  if (!al16(workspace)) return HCLSM_ERR_UNSUPPORTED;
+  return 0;
+}
+
+extern "C" int hclsm_slot_attention_iteration(const HclsmSlotWeights* W, const float* slots_in, const void* k,
+                                              const void* v, int64_t ldkv, int64_t kv_bstride, float* slots_out,
+                                              int64_t B, int64_t N, int64_t M, int64_t d, int64_t hidden, float scale,
+                                              float logit_clamp, float renorm_eps, float slot_clamp, int dtype,
+                                              void* workspace, int64_t workspace_bytes, void* stream) {
+  SlotWs L;
+  int rc = check_slot_args(W, B, N, M, d, hidden, dtype, workspace, workspace_bytes, false, &L);
+  if (rc) return rc;
+  if (!slots_in || !k || !v || !slots_out) return HCLSM_ERR_NULL;
+  rc = check_core(k, ldkv, kv_bstride, k, ldkv, kv_bstride, B, N, M, d, dtype);
+  if (rc) return rc;
+  if (B == 0 || N == 0) return 0;
   hipStream_t st = (hipStream_t)stream;
-#define HCLSM_CORE(D_, A_)                                                                                  \
-  if (dtype == D_ && (attn == nullptr ? A_ == D_ : attn_dtype == A_)) {                                     \
-    if (smem > 64 * 1024)                                                                                   \
-      hipFuncSetAttribute((const void*)slot_core_kernel<D_, A_>, hipFuncAttributeMaxDynamicSharedMemorySize, \
-                          (int)smem);                                                                       \
-    hipLaunchKernelGGL((slot_core_kernel<D_, A_>), dim3((unsigned)B), dim3(256), smem, st, (const MM<D_>::T*)q, \
-                       (const MM<D_>::T*)k, (const MM<D_>::T*)v, (MM<D_>::T*)out, (MM<A_>::T*)attn, a);      \
-    HCLSM_LAUNCH_CHECK();                                                                                   \
-    return 0;                                                                                               \
+  char* ws = reinterpret_cast<char*>(workspace);
+  rc = convert_f32(slots_in, ws + L.sb, B * N * d, dtype, st);
+  if (rc) return rc;
+  return slot_iteration_impl(W, slots_in, ws + L.sb, k, ldkv, kv_bstride, v, ldkv, kv_bstride, false, slots_out, B,
+                             N, M, d, hidden, scale, logit_clamp, renorm_eps, slot_clamp, dtype, ws, L, st);
+}
+
+extern "C" int hclsm_slot_attention_forward(const HclsmSlotWeights* W, const float* inputs, int64_t d_in,
+                                            const float* slots0, float* slots_out, int64_t B, int64_t N, int64_t M,
+                                            int64_t d, int64_t hidden, int64_t n_iter, float scale, float logit_clamp,
+                                            float renorm_eps, float slot_clamp, int dtype, void* workspace,
+                                            int64_t workspace_bytes, void* stream) {
+  SlotWs L;
+  int rc = check_slot_args(W, B, N, M, d, hidden, dtype, workspace, workspace_bytes, true, &L, d_in);
+  if (rc) return rc;
+  if (B * M > 0x7fffffffLL) return HCLSM_ERR_SHAPE;
+  if (!inputs || !slots0 || !slots_out) return HCLSM_ERR_NULL;
+  if (d_in < 1 || n_iter < 0) return HCLSM_ERR_SHAPE;
+  if (d_in % (4 * (dtype == HCLSM_F32 ? 1 : 8))) return HCLSM_ERR_UNSUPPORTED;
+  if (B == 0 || N == 0) return 0;
+  hipStream_t st = (hipStream_t)stream;
+  char* ws = reinterpret_cast<char*>(workspace);
+  const int esize = dtype == HCLSM_F32 ? 4 : 2;
+  void* kv = ws + L.kv;
+  // k | v = LN_in(inputs) [W_k; W_v]^T     (dynamic_slots.py:152-154)
+  void* xin = ws + L.xin;
+  rc = ln_impl(inputs, d_in, W->ln_in_w, W->ln_in_b, xin, d_in, B * M, d_in, 1e-5f, HCLSM_F32, dtype, st);
+  if (rc) return rc;
+  // k rows [B*M][d]; v written transposed per frame: vt[b][d][Mp]
+  const int64_t Mp = (M + 31) / 32 * 32;
+  void* vt = ws + L.vt;
+  {
+    const OutSplit os{d, M, Mp, d * Mp, vt};
+#define HCLSM_KV(D_, XT_)                                                                                    \
+    if (dtype == D_)                                                                                         \
+      launch_linear_quad<D_, D_, XT_>(xin, d_in, W->w_kv, d_in, nullptr, nullptr, 0, kv, d, nullptr, 0, B * M, \
+                                      2 * d, d_in, 0, 0.f, st, os);
+    HCLSM_KV(HCLSM_BF16, uint16_t)
+    HCLSM_KV(HCLSM_F16, _Float16)
+    HCLSM_KV(HCLSM_F32, float)
+#undef HCLSM_KV
+    HCLSM_LAUNCH_CHECK();
   }
-  HCLSM_CORE(HCLSM_BF16, HCLSM_BF16)
-  HCLSM_CORE(HCLSM_BF16, HCLSM_F32)
-  HCLSM_CORE(HCLSM_F16, HCLSM_F16)
-  HCLSM_CORE(HCLSM_F16, HCLSM_F32)
-  HCLSM_CORE(HCLSM_F32, HCLSM_F32)
-#undef HCLSM_CORE
-  return HCLSM_ERR_DTYPE;
+  (void)esize;
+  const void* k = kv;
+  rc = convert_f32(slots0, ws + L.sb, B * N * d, dtype, st);
+  if (rc) return rc;
+  if (n_iter == 0) return (int)hipMemcpyAsync(slots_out, slots0, (size_t)B * N * d * 4, hipMemcpyDeviceToDevice, st);
+  for (int64_t it = 0; it < n_iter; ++it) {
+    rc = slot_iteration_impl(W, it == 0 ? slots0 : slots_out, ws + L.sb, k, d, M * d, vt, Mp, d * Mp, true,
+                             slots_out, B, N, M, d, hidden, scale, logit_clamp, renorm_eps, slot_clamp, dtype, ws, L,
+                             st);
+    if (rc) return rc;
+  }
+  return 0;
 }

@@ -7,8 +7,8 @@ Reference names kept (same positional signatures, defaults and return types):
     compiled_slot_attention(Q, K, V, scale=None) -> (out, attn)              (:308-317)
     fused_slot_attention_triton(Q, K, V, scale=None) -> (out, attn)          (:239-258)
 
-All run ``hclsm_slot_attn_core`` (one MFMA workgroup per frame: logits, softmax over the
-slot axis, attn @ V).  Semantics per name, as in the reference:
+All run ``hclsm_slot_attn_core`` (two MFMA launches: logits + softmax over the slot axis per
+(frame, 64-token block), then attn @ V per (frame, 64-column block)).  Semantics per name:
     "auto" / "triton" / "hip" and fused_slot_attention_triton: denominator + 1e-8 (:126)
     "naive" / "compiled" and their functions:                  plain softmax (:287, :303)
 Softmax over SLOTS (dim=1): every token's column of attn sums to 1.  Q: (B, N, D),
@@ -36,11 +36,14 @@ def _core_raw(Q, K, V, scale, denom_eps, logit_clamp=None, renorm_eps=None, want
     out = torch.empty((B, N, D), dtype=io, device=Q.device)
     at = attn_dtype or io
     attn = torch.empty((B, N, M), dtype=at, device=Q.device) if want_attn else None
-    rc = _lib.lib().hclsm_slot_attn_core(
+    L = _lib.lib()
+    wsb = L.hclsm_slot_attn_core_workspace(B, N, M, _lib.dtype_code(io))
+    ws = torch.empty(max(int(wsb), 16), dtype=torch.uint8, device=Q.device)
+    rc = L.hclsm_slot_attn_core(
         _lib.ptr(q), D, N * D, _lib.ptr(k), D, M * D, _lib.ptr(v), D, M * D, _lib.ptr(out), D, N * D,
         _lib.ptr(attn), _lib.dtype_code(at), B, N, M, D, float(scale), float(denom_eps),
         float(logit_clamp) if logit_clamp else 0.0, float(renorm_eps) if renorm_eps is not None else -1.0,
-        _lib.dtype_code(io), _lib.stream_of(q))
+        _lib.dtype_code(io), _lib.ptr(ws), ws.numel(), _lib.stream_of(q))
     _lib.check(rc, "hclsm_slot_attn_core")
     return out, attn
 

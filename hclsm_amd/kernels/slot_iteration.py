@@ -20,6 +20,7 @@ mean, MLP hidden 768).
 
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
 
 import torch
@@ -82,29 +83,22 @@ def _ln(x, ldx, M, D, w, b, out_dtype, stream, eps=1e-5):
     return y
 
 
-def _linear(x, w, bias=None, resid=None, relu=False, clamp=None, out_dtype=None, shadow=False, stream=None):
+def _linear(x, w, bias=None, resid=None, relu=False, clamp=None, out_dtype=None, shadow=False, stream=None,
+            ln_w=None, ln_b=None, ln=False, dtype=None):
+    """Y = [LN](x) w^T (+bias)(ReLU)(+resid)(clamp) through hclsm_linear (test / building-block helper)."""
     M, K = x.shape
     N = w.shape[0]
-    out_dtype = out_dtype or x.dtype
+    dtype = dtype or w.dtype
+    out_dtype = out_dtype or dtype
     y = torch.empty((M, N), dtype=out_dtype, device=x.device)
-    y2 = torch.empty((M, N), dtype=x.dtype, device=x.device) if shadow else None
-    rc = _lib.lib().hclsm_linear(_lib.ptr(x), K, _lib.ptr(w), K, _lib.ptr(bias), _lib.ptr(resid),
-                                 0 if resid is None else resid.shape[1], _lib.ptr(y), N, _lib.dtype_code(out_dtype),
-                                 _lib.ptr(y2), N, M, N, K, int(relu), float(clamp) if clamp else 0.0,
-                                 _lib.dtype_code(x.dtype), stream)
+    y2 = torch.empty((M, N), dtype=dtype, device=x.device) if shadow else None
+    rc = _lib.lib().hclsm_linear(_lib.ptr(x), K, _lib.dtype_code(x.dtype), _lib.ptr(w), K, _lib.ptr(bias),
+                                 _lib.ptr(resid), 0 if resid is None else resid.shape[1], _lib.ptr(y), N,
+                                 _lib.dtype_code(out_dtype), _lib.ptr(y2), N, M, N, K, int(relu),
+                                 float(clamp) if clamp else 0.0, int(ln), _lib.ptr(ln_w), _lib.ptr(ln_b), 1e-5,
+                                 _lib.dtype_code(dtype), stream)
     _lib.check(rc, "hclsm_linear")
     return (y, y2) if shadow else y
-
-
-def _core(q, k, v, B, N, M, d, ldk, kbs, scale, mode, stream):
-    out = torch.empty((B * N, d), dtype=q.dtype, device=q.device)
-    rc = _lib.lib().hclsm_slot_attn_core(
-        _lib.ptr(q), d, N * d, _lib.ptr(k), ldk, kbs, _lib.ptr(v), ldk, kbs, _lib.ptr(out), d, N * d,
-        None, _lib.F32, B, N, M, d, float(scale), 0.0,
-        float(mode.logit_clamp) if mode.logit_clamp else 0.0,
-        float(mode.renorm_eps) if mode.renorm_eps is not None else -1.0, _lib.dtype_code(q.dtype), stream)
-    _lib.check(rc, "hclsm_slot_attn_core")
-    return out
 
 
 def _gru(upd, hb, hf, W, stream):
@@ -118,54 +112,81 @@ def _gru(upd, hb, hf, W, stream):
     return out
 
 
-def _iteration(slots_f, slots_b, k, v, B, N, M, W, mode, scale, ldk, kbs, stream):
-    d = W.d
-    t = W.t
-    sn = _ln(slots_f, d, B * N, d, t.get("ln_pre_w"), t.get("ln_pre_b"), W.dtype, stream)
-    q = _linear(sn, t["w_q"], stream=stream)
-    upd = _core(q, k, v, B, N, M, d, ldk, kbs, scale, mode, stream)
-    h = _gru(upd, slots_b, slots_f, W, stream)
-    hn = _ln(h, d, B * N, d, t.get("ln_mlp_w"), t.get("ln_mlp_b"), W.dtype, stream)
-    m1 = _linear(hn, t["w1"], bias=t.get("b1"), relu=True, stream=stream)
-    return _linear(m1, t["w2"], bias=t.get("b2"), resid=h, clamp=mode.slot_clamp, out_dtype=torch.float32,
-                   shadow=True, stream=stream)
+def _struct(W: SlotWeights) -> "_lib.HclsmSlotWeights":
+    st = _lib.HclsmSlotWeights()
+    for name, _ in _lib.HclsmSlotWeights._fields_:
+        t = W.t.get(name)
+        setattr(st, name, None if t is None else t.data_ptr())
+    return st
+
+
+_WS_CACHE: dict = {}
+
+
+def _workspace(nbytes: int, device) -> torch.Tensor:
+    """A cached uint8 device buffer of at least nbytes (one per device; grown on demand).  Calls that
+    share it run in stream order on the current stream."""
+    key = str(device)
+    buf = _WS_CACHE.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+        _WS_CACHE[key] = buf
+    return buf
+
+
+def _mode_args(mode: SlotMode):
+    return (float(mode.logit_clamp) if mode.logit_clamp else 0.0,
+            float(mode.renorm_eps) if mode.renorm_eps is not None else -1.0,
+            float(mode.slot_clamp) if mode.slot_clamp else 0.0)
 
 
 def slot_attention_iteration(slots: torch.Tensor, k: torch.Tensor, v: torch.Tensor, W: SlotWeights,
                              mode: SlotMode = REFERENCE_MODE, scale: float | None = None) -> torch.Tensor:
-    """One iteration.  slots (B, N, d) (any float dtype; carried as fp32), k, v (B, M, d) in
-    W.dtype.  Returns the new slots (B, N, d) fp32."""
+    """One iteration.  slots (B, N, d) (any float dtype; carried as fp32), k, v (B, M, d).
+    Returns the new slots (B, N, d) fp32.  One C call: eight launches on the current stream."""
     require_gpu("slot_attention_iteration", slots, k, v)
     B, N, d = slots.shape
     M = k.shape[1]
     if scale is None:
         scale = d ** -0.5
     sf = slots.reshape(B * N, d).to(torch.float32).contiguous()
-    sb = sf.to(W.dtype)
     kc = k.to(W.dtype).contiguous()
     vc = v.to(W.dtype).contiguous()
-    out, _ = _iteration(sf, sb, kc, vc, B, N, M, W, mode, scale, d, M * d, _lib.stream_of(sf))
+    out = torch.empty_like(sf)
+    L = _lib.lib()
+    code = _lib.dtype_code(W.dtype)
+    wsb = L.hclsm_slot_attention_workspace(B, N, M, d, d, W.hidden, code)
+    ws = _workspace(int(wsb), sf.device)
+    lc, re, sc = _mode_args(mode)
+    st = _struct(W)
+    rc = L.hclsm_slot_attention_iteration(ctypes.byref(st), _lib.ptr(sf), _lib.ptr(kc), _lib.ptr(vc), d, M * d,
+                                          _lib.ptr(out), B, N, M, d, W.hidden, float(scale), lc, re, sc, code,
+                                          _lib.ptr(ws), ws.numel(), _lib.stream_of(sf))
+    _lib.check(rc, "hclsm_slot_attention_iteration")
     return out.reshape(B, N, d)
 
 
 def slot_attention_forward(inputs: torch.Tensor, slots0: torch.Tensor, W: SlotWeights, n_iter: int,
                            mode: SlotMode = REFERENCE_MODE, scale: float | None = None) -> torch.Tensor:
     """k, v = LN_in(inputs) W_k^T, W_v^T (one MFMA linear over [W_k; W_v]), then n_iter iterations
-    from slots0.  inputs (B, M, d_in), slots0 (B, N, d).  Returns slots (B, N, d) fp32."""
+    from slots0.  inputs (B, M, d_in), slots0 (B, N, d).  Returns slots (B, N, d) fp32.
+    One C call (3 + 8 * n_iter launches), no host synchronisation."""
     require_gpu("slot_attention_forward", inputs, slots0)
     B, M, d_in = inputs.shape
     N, d = slots0.shape[1], W.d
     if scale is None:
         scale = d ** -0.5
-    st = _lib.stream_of(inputs)
-    t = W.t
-    x = inputs.reshape(B * M, d_in).contiguous()
-    xn = _ln(x, d_in, B * M, d_in, t.get("ln_in_w"), t.get("ln_in_b"), W.dtype, st)
-    kv = _linear(xn, t["w_kv"], stream=st)                      # (B*M, 2d): k | v
-    k = kv
-    v = kv[:, d:]
-    sf = slots0.reshape(B * N, d).to(torch.float32).contiguous()
-    sb = sf.to(W.dtype)
-    for _ in range(n_iter):
-        sf, sb = _iteration(sf, sb, k, v, B, N, M, W, mode, scale, 2 * d, M * 2 * d, st)
-    return sf.reshape(B, N, d)
+    x = inputs.to(torch.float32).contiguous()
+    s0 = slots0.to(torch.float32).contiguous()
+    out = torch.empty_like(s0)
+    L = _lib.lib()
+    code = _lib.dtype_code(W.dtype)
+    wsb = L.hclsm_slot_attention_workspace(B, N, M, d_in, d, W.hidden, code)
+    ws = _workspace(int(wsb), x.device)
+    lc, re, sc = _mode_args(mode)
+    st = _struct(W)
+    rc = L.hclsm_slot_attention_forward(ctypes.byref(st), _lib.ptr(x), d_in, _lib.ptr(s0), _lib.ptr(out), B, N, M, d,
+                                        W.hidden, int(n_iter), float(scale), lc, re, sc, code, _lib.ptr(ws),
+                                        ws.numel(), _lib.stream_of(x))
+    _lib.check(rc, "hclsm_slot_attention_forward")
+    return out

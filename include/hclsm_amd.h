@@ -169,16 +169,19 @@ int hclsm_layer_norm(const void* x, int64_t ldx, const float* w, const float* b,
                      int64_t M, int64_t D, float eps, int in_dtype, int out_dtype, void* stream);
 
 /*
- * Linear layer on MFMA: Y[M, N] = X[M, K] . W[N, K]^T (+ bias[N]) (ReLU if relu) (+ resid[M, N] fp32)
- *   (clamped to +-clamp if clamp > 0).  X, W: `dtype` (BF16 / F16 with 16-byte aligned rows and
- *   K % 32 == 0; F32 with K % 4 == 0); Y: y_dtype (F32 or dtype); y2 (nullable): a second copy of Y
- *   in `dtype`.  Row strides ldx, ldw, ldr, ldy, ldy2 in elements.
- * Replaces: the nn.Linear layers of the slot iteration (dynamic_slots.py:51-53,64-68,112,128).
+ * Linear layer on MFMA: Y[M, N] = A[M, K] . W[N, K]^T (+ bias[N]) (ReLU if relu) (+ resid[M, N] fp32)
+ *   (clamped to +-clamp if clamp > 0), where A = X, or A = LayerNorm(X) rows (ln != 0; ln_w / ln_b
+ *   [K] float32 nullable, eps ln_eps) formed on the fly.  X: x_dtype (F32, or = dtype); W: `dtype`
+ *   (BF16 / F16: 16-byte aligned rows, K % 32 == 0; F32: K % 4 == 0); Y: y_dtype (F32 or dtype);
+ *   y2 (nullable): a second copy of Y in `dtype`.  Row strides in elements.  One workgroup per
+ *   32x32 output tile, K split across its four waves.
+ * Replaces: the nn.Linear layers (with their preceding nn.LayerNorm) of the slot iteration
+ *   (objects/dynamic_slots.py:51-53,64-73,111-112,128,152-154).
  */
-int hclsm_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, const float* bias,
+int hclsm_linear(const void* x, int64_t ldx, int x_dtype, const void* w, int64_t ldw, const float* bias,
                  const float* resid, int64_t ldr, void* y, int64_t ldy, int y_dtype, void* y2,
-                 int64_t ldy2, int64_t M, int64_t N, int64_t K, int relu, float clamp, int dtype,
-                 void* stream);
+                 int64_t ldy2, int64_t M, int64_t N, int64_t K, int relu, float clamp, int ln,
+                 const float* ln_w, const float* ln_b, float ln_eps, int dtype, void* stream);
 
 /*
  * torch.nn.GRUCell on MFMA for M rows: x [M, Kx] and h (both as `dtype` hb [M, H] for the products
@@ -193,23 +196,74 @@ int hclsm_gru_cell(const void* x, int64_t ldx, const void* hb, int64_t ldhb, con
                    void* stream);
 
 /*
- * Slot-attention core for B frames, one workgroup per frame:
+ * Slot-attention core for B frames:
  *   logits = scale * q k^T (clamped to +-logit_clamp if logit_clamp > 0);
  *   attn = softmax over the N slots for each of the M tokens, denominator + denom_eps;
  *   if renorm_eps >= 0: attn = (attn + renorm_eps) / sum over tokens (attn + renorm_eps);
  *   out = attn v.
  * q [B][N][D], k, v [B][M][D], out [B][N][D]: `dtype` with row strides ldq/ldk/ldv/ldo and frame
  * strides *_bstride (elements); attn (nullable) [B, N, M] contiguous, attn_dtype F32 or `dtype`, holds
- * the softmax (before renormalisation).  D % 16 == 0 (and % 32 for 16-bit types).
+ * the softmax (before renormalisation).  N <= 128; D % 16 == 0 (and % 32 for 16-bit types).
+ * workspace: >= hclsm_slot_attn_core_workspace(B, N, M, dtype) bytes, 16-byte aligned.
+ * Two launches: logits + softmax over (frame, 64-token block); attn . v over (frame, 64-column block).
  * Replaces: slot_attention_fn / naive_slot_attention / compiled_slot_attention / the two Triton
  *   kernels (hclsm/kernels/slot_attention_kernel.py:43-355; denom_eps 1e-8 is the Triton form, :126)
  *   and the attention part of DynamicSlotAttention._iteration_step (objects/dynamic_slots.py:115-121).
  */
+int64_t hclsm_slot_attn_core_workspace(int64_t B, int64_t N, int64_t M, int dtype);
 int hclsm_slot_attn_core(const void* q, int64_t ldq, int64_t q_bstride, const void* k, int64_t ldk,
                          int64_t k_bstride, const void* v, int64_t ldv, int64_t v_bstride, void* out,
                          int64_t ldo, int64_t o_bstride, void* attn, int attn_dtype, int64_t B, int64_t N,
                          int64_t M, int64_t D, float scale, float denom_eps, float logit_clamp,
-                         float renorm_eps, int dtype, void* stream);
+                         float renorm_eps, int dtype, void* workspace, int64_t workspace_bytes,
+                         void* stream);
+
+/* Parameters of one DynamicSlotAttention (objects/dynamic_slots.py:47-82).  Matrices in the compute
+ * dtype, row-major as torch stores nn.Linear / nn.GRUCell weights; vectors float32 (nullable = 0 bias,
+ * unit LayerNorm weight). */
+typedef struct HclsmSlotWeights {
+  const void* w_q;     /* [d, d]          project_q.weight */
+  const void* w_kv;    /* [2d, d_in]      [project_k.weight; project_v.weight] (forward only) */
+  const void* w_ih;    /* [3d, d]         gru.weight_ih (rows r, z, n) */
+  const void* w_hh;    /* [3d, d]         gru.weight_hh */
+  const void* w1;      /* [hidden, d]     mlp[0].weight */
+  const void* w2;      /* [d, hidden]     mlp[2].weight */
+  const float* b_ih;   /* [3d] */
+  const float* b_hh;   /* [3d] */
+  const float* b1;     /* [hidden] */
+  const float* b2;     /* [d] */
+  const float* ln_in_w;  const float* ln_in_b;   /* [d_in] norm_input */
+  const float* ln_pre_w; const float* ln_pre_b;  /* [d]    norm_pre_attn */
+  const float* ln_mlp_w; const float* ln_mlp_b;  /* [d]    norm_slots */
+} HclsmSlotWeights;
+
+/* Workspace bytes for hclsm_slot_attention_iteration / _forward (16-byte aligned buffer). */
+int64_t hclsm_slot_attention_workspace(int64_t B, int64_t N, int64_t M, int64_t d_in, int64_t d, int64_t hidden,
+                                       int dtype);
+
+/*
+ * One slot-attention iteration (objects/dynamic_slots.py:98-131) for B frames of N slots:
+ *   q = LN_pre(slots) W_q^T; attention core (logit clamp, renorm as above); GRUCell; slots + MLP(LN(.));
+ *   clamp to +-slot_clamp if slot_clamp > 0.  slots_in / slots_out [B, N, d] float32 (may alias);
+ *   k, v rows of `dtype` with row stride ldkv and frame stride kv_bstride.  Eight launches, no host sync.
+ */
+int hclsm_slot_attention_iteration(const HclsmSlotWeights* W, const float* slots_in, const void* k,
+                                   const void* v, int64_t ldkv, int64_t kv_bstride, float* slots_out,
+                                   int64_t B, int64_t N, int64_t M, int64_t d, int64_t hidden, float scale,
+                                   float logit_clamp, float renorm_eps, float slot_clamp, int dtype,
+                                   void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * DynamicSlotAttention forward up to the iterations (objects/dynamic_slots.py:149-164): k | v =
+ * LN_in(inputs) [W_k; W_v]^T for inputs [B, M, d_in] float32, then n_iter iterations from slots0
+ * [B, N, d] float32 into slots_out.  The slot initialisation draw (:86-96), existence head and slot
+ * birth (:166-199) stay with the caller.
+ */
+int hclsm_slot_attention_forward(const HclsmSlotWeights* W, const float* inputs, int64_t d_in,
+                                 const float* slots0, float* slots_out, int64_t B, int64_t N, int64_t M,
+                                 int64_t d, int64_t hidden, int64_t n_iter, float scale, float logit_clamp,
+                                 float renorm_eps, float slot_clamp, int dtype, void* workspace,
+                                 int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -81,6 +81,15 @@ def test_building_blocks(dtype, tol):
                    out_dtype=torch.float32, stream=st)
     ref = np.clip(np.maximum(_np(xd) @ _np(wd).T + _np(b), 0) + _np(r), -1.5, 1.5)
     assert normwise_rel_err(_np(y), ref) <= tol
+    # LayerNorm prologue from fp32 rows with a large common offset (the shifted statistics matter)
+    lw0, lb0 = torch.rand(K, generator=g) + 0.5, torch.randn(K, generator=g)
+    xo = x * 0.5 + 40.0
+    y_ln = si._linear(xo.cuda(), wd.cuda(), ln=True, ln_w=lw0.cuda(), ln_b=lb0.cuda(), out_dtype=torch.float32,
+                      stream=st)
+    xn = sa.layer_norm(_np(xo), _np(lw0), _np(lb0))
+    if dtype != torch.float32:
+        xn = _np(torch.from_numpy(xn).to(dtype))
+    assert normwise_rel_err(_np(y_ln), xn @ _np(wd).T) <= tol
     lw, lb = torch.rand(K, generator=g) + 0.5, torch.randn(K, generator=g)
     ln = si._ln(x.cuda(), K, M, K, lw.cuda(), lb.cuda(), dtype, st)
     assert normwise_rel_err(_np(ln), sa.layer_norm(_np(x), _np(lw), _np(lb))) <= (1e-5 if dtype == torch.float32 else 8e-3)
