@@ -1,0 +1,389 @@
+// Selective SSM scan, backward (reverse scan) for gfx950.
+//
+// Gradients of L = sum(gy * y) for y_t[d] = sum_s C_t[s] h_t[d,s] (+ D[d] x_t[d]) with
+// h_t = exp(dt A) h_{t-1} + dt B_t x_t:
+//   gh_t   = gy_t C_t + exp(dt_{t+1} A) gh_{t+1}
+//   gx_t   = dt sum_s gh_t B_t + D gy_t              gdt_t = sum_s g_arg A + x sum_s gh_t B_t
+//   gB_t[s] = sum_d gh_t dt x                        gC_t[s] = sum_d gy_t h_t
+//   gA[d,s] = sum_{n,t} g_arg dt   with g_arg = gh_t h_{t-1} exp(dt A)
+// (model mode: each clamp passes gradient only inside its closed interval).
+//
+// Mapping: one lane owns channel d of sequence n and SG <= 8 of its states (G = d_state/SG lanes
+// per channel, adjacent).  Pass 1 recomputes h forward and writes the state at every chunk
+// start (chunks of K = 64/SG steps) to a checkpoint buffer.  Pass 2 walks the chunks backwards:
+// it recomputes the chunk's states into registers, then runs the reverse recurrence step by step.
+// Sums over the state axis (gx, gdt) are xor shuffles inside the G-lane group; sums over the
+// channel axis (gB, gC) are a recursive-halving reduce-scatter across the wave's channels followed
+// by a cross-wave sum through LDS once per chunk.  A second kernel casts gB/gC and reduces the
+// per-sequence partials of gA_log and gD.
+#include "common.h"
+
+namespace hclsm {
+
+constexpr int BWD_MAX_THREADS = 512;  // keeps 256 VGPRs per lane: the chunk states stay in registers
+
+template <int V, int MASK_LO>
+struct RS {
+  // Reduce-scatter V values across the lanes that differ in bits [MASK_LO, 32] of the lane id.
+  // On return v[0 .. V/2^h) holds sums for value indices starting at `off` (h = halving steps).
+  template <int CNT, int M>
+  static __device__ __forceinline__ void step(float* v, int lane, int& off) {
+    if constexpr (M >= MASK_LO) {
+      if constexpr (CNT > 1) {
+        const bool upper = (lane & M) != 0;
+#pragma unroll
+        for (int i = 0; i < CNT / 2; ++i) {
+          const float keep = upper ? v[i + CNT / 2] : v[i];
+          const float send = upper ? v[i] : v[i + CNT / 2];
+          v[i] = keep + __shfl_xor(send, M, 64);
+        }
+        if (upper) off += CNT / 2;
+        step<CNT / 2, M / 2>(v, lane, off);
+      } else {
+        v[0] += __shfl_xor(v[0], M, 64);
+        step<1, M / 2>(v, lane, off);
+      }
+    }
+  }
+  static __device__ __forceinline__ int run(float* v, int lane) {
+    int off = 0;
+    step<V, 32>(v, lane, off);
+    return off;
+  }
+};
+
+template <int N_, int MASK_LO> struct RSCount {  // values left per lane after RS
+  static constexpr int h(int cnt, int m) { return (m < MASK_LO || cnt <= 1) ? cnt : h(cnt / 2, m / 2); }
+  static constexpr int value = h(N_, 32);
+};
+
+struct BwdArgs {
+  int T, Dn, S, nchunk, DW;
+  int64_t ld_ck;  // floats per (n, chunk) checkpoint slab = Dn * SP
+};
+
+template <int DT, int SP, int MODE>
+__global__ void __launch_bounds__(BWD_MAX_THREADS)
+ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename Elem<DT>::T* __restrict__ dt,
+                    const float* __restrict__ A_log, const typename Elem<DT>::T* __restrict__ Bm,
+                    const typename Elem<DT>::T* __restrict__ Cm, const float* __restrict__ Dskip,
+                    const typename Elem<DT>::T* __restrict__ gy, typename Elem<DT>::T* __restrict__ gx,
+                    typename Elem<DT>::T* __restrict__ gdt, float* __restrict__ ckpt, float* __restrict__ gbc,
+                    float* __restrict__ gA_part, float* __restrict__ gD_part, BwdArgs a) {
+  using E = Elem<DT>;
+  using TT = typename E::T;
+  constexpr int SG = SP < 8 ? SP : 8;
+  constexpr int G = SP / SG;
+  constexpr int K = 64 / SG;
+  constexpr int V = 2 * SG;                        // values reduced over channels: gB, gC
+  constexpr int VL = RSCount<V, G>::value;        // values per lane after the reduce-scatter
+  constexpr int WMAX = BWD_MAX_THREADS / 64;
+  __shared__ float red[K][WMAX][2 * SP];           // per-chunk wave partials of gB | gC
+  const int n = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, nw = blockDim.x >> 6;
+  const int dl = tid / G, gi = tid - dl * G;
+  const int d = blockIdx.y * a.DW + dl;
+  const bool act = d < a.Dn && dl < a.DW;
+  const int dd = act ? d : 0;
+  const int s0 = gi * SG;
+  const int T = a.T, Dn = a.Dn, S = a.S;
+
+  float a2[SG], aN[SG];   // A * log2(e) and A (natural) for this lane's states; padded states: 0
+#pragma unroll
+  for (int j = 0; j < SG; ++j) {
+    const int s = s0 + j;
+    const float e = expf(A_log[(size_t)dd * S + (s < S ? s : S - 1)]);
+    const float ec = (MODE == HCLSM_SCAN_MODEL) ? fminf(fmaxf(e, 1e-6f), 1.0f) : e;
+    aN[j] = (s < S) ? -ec : 0.f;
+    a2[j] = aN[j] * HCLSM_LOG2E;
+  }
+  const float dsk = Dskip ? Dskip[dd] : 0.f;
+  const size_t row0 = (size_t)n * T;
+  auto ldB = [&](int t, float* o) {
+#pragma unroll
+    for (int j = 0; j < SG; ++j) {
+      const int s = s0 + j;
+      o[j] = (s < S) ? E::ld(Bm + (row0 + t) * S + s) : 0.f;
+    }
+  };
+  auto ldC = [&](int t, float* o) {
+#pragma unroll
+    for (int j = 0; j < SG; ++j) {
+      const int s = s0 + j;
+      o[j] = (s < S) ? E::ld(Cm + (row0 + t) * S + s) : 0.f;
+    }
+  };
+  auto dtc_of = [&](float v) { return (MODE == HCLSM_SCAN_MODEL) ? fminf(fmaxf(v, 1e-3f), 1.0f) : v; };
+  float* ck = ckpt + (size_t)n * a.nchunk * a.ld_ck + (size_t)dd * SP + s0;
+
+  // ---- pass 1: forward recompute, checkpoint at every chunk start
+  float h[SG];
+#pragma unroll
+  for (int j = 0; j < SG; ++j) h[j] = 0.f;
+  for (int c = 0; c < a.nchunk; ++c) {
+    if (act)
+#pragma unroll
+      for (int j = 0; j < SG; ++j) ck[(size_t)c * a.ld_ck + j] = h[j];
+    const int t0 = c * K, t1 = (t0 + K < T) ? t0 + K : T;
+    for (int t = t0; t < t1; ++t) {
+      const float dtv = dtc_of(E::ld(dt + (row0 + t) * Dn + dd));
+      const float u = dtv * E::ld(x + (row0 + t) * Dn + dd);
+      float bv[SG];
+      ldB(t, bv);
+#pragma unroll
+      for (int j = 0; j < SG; ++j) h[j] = fmaf(fast_exp2(dtv * a2[j]), h[j], u * bv[j]);
+    }
+  }
+
+  // ---- pass 2: reverse
+  float gh[SG], gA[SG];
+#pragma unroll
+  for (int j = 0; j < SG; ++j) { gh[j] = 0.f; gA[j] = 0.f; }
+  float gD = 0.f;
+  for (int c = a.nchunk - 1; c >= 0; --c) {
+    const int t0 = c * K, len = ((t0 + K < T) ? t0 + K : T) - t0;
+    float h0[SG];
+#pragma unroll
+    for (int j = 0; j < SG; ++j) h0[j] = act ? ck[(size_t)c * a.ld_ck + j] : 0.f;
+    float hk[K][SG];
+    {
+      float hc[SG];
+#pragma unroll
+      for (int j = 0; j < SG; ++j) hc[j] = h0[j];
+#pragma unroll
+      for (int i = 0; i < K; ++i) {
+        if (i < len) {
+          const int t = t0 + i;
+          const float dtv = dtc_of(E::ld(dt + (row0 + t) * Dn + dd));
+          const float u = dtv * E::ld(x + (row0 + t) * Dn + dd);
+          float bv[SG];
+          ldB(t, bv);
+#pragma unroll
+          for (int j = 0; j < SG; ++j) hc[j] = fmaf(fast_exp2(dtv * a2[j]), hc[j], u * bv[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < SG; ++j) hk[i][j] = hc[j];
+      }
+    }
+#pragma unroll
+    for (int i = K - 1; i >= 0; --i) {
+      if (i < len) {
+        const int t = t0 + i;
+        const float draw = E::ld(dt + (row0 + t) * Dn + dd);
+        const float dtv = dtc_of(draw);
+        const float xv = E::ld(x + (row0 + t) * Dn + dd);
+        const float gyv = act ? E::ld(gy + (row0 + t) * Dn + dd) : 0.f;
+        const float u = dtv * xv;
+        float bv[SG], cv[SG];
+        ldB(t, bv);
+        ldC(t, cv);
+        float w[V];
+        float q = 0.f, gda = 0.f;
+#pragma unroll
+        for (int j = 0; j < SG; ++j) {
+          const float hp = (i > 0) ? hk[i > 0 ? i - 1 : 0][j] : h0[j];
+          gh[j] = fmaf(gyv, cv[j], gh[j]);
+          w[SG + j] = gyv * hk[i][j];                  // -> gC
+          const float gate = fast_exp2(dtv * a2[j]);
+          const float garg = gh[j] * hp * gate;
+          gda = fmaf(garg, aN[j], gda);
+          gA[j] = fmaf(garg, dtv, gA[j]);
+          q = fmaf(gh[j], bv[j], q);
+          w[j] = gh[j] * u;                            // -> gB
+          gh[j] *= gate;
+        }
+#pragma unroll
+        for (int m = 1; m < G; m <<= 1) {
+          q += __shfl_xor(q, m, 64);
+          gda += __shfl_xor(gda, m, 64);
+        }
+        if (gi == 0 && act) {
+          float gdv = gda + q * xv;
+          if (MODE == HCLSM_SCAN_MODEL && !(draw >= 1e-3f && draw <= 1.0f)) gdv = 0.f;
+          E::st(gx + (row0 + t) * Dn + d, fmaf(q, dtv, dsk * gyv));
+          E::st(gdt + (row0 + t) * Dn + d, gdv);
+          gD = fmaf(gyv, xv, gD);
+        }
+        if (!act) {
+#pragma unroll
+          for (int j = 0; j < V; ++j) w[j] = 0.f;
+        }
+        const int off = RS<V, G>::run(w, lane);
+        // lanes sharing the reduced slot write identical values; only the lowest writes
+        const int rs_lo_bits = lane & (G - 1);   // state-group bits are not reduced
+        (void)rs_lo_bits;
+#pragma unroll
+        for (int e = 0; e < VL; ++e) {
+          const int vi = off + e;                       // 0..V-1 within this lane's group
+          const int which = vi / SG, j = vi - which * SG;
+          // duplicates: lanes that differ only in the bits below the last halving hold copies
+          red[i][wid][which * SP + s0 + j] = w[e];
+        }
+      } else {
+        // keep the LDS slots of missing steps at zero for the chunk sum below
+        for (int e = lane; e < 2 * SP; e += 64) red[i][wid][e] = 0.f;
+      }
+    }
+    __syncthreads();
+    // sum the chunk's wave partials: K steps x 2*SP values
+    for (int e = tid; e < K * 2 * SP; e += blockDim.x) {
+      const int i = e / (2 * SP), v = e - i * 2 * SP;
+      if (i < len) {
+        float sacc = 0.f;
+        for (int w = 0; w < nw; ++w) sacc += red[i][w][v];
+        float* dst = gbc + ((size_t)n * T + t0 + i) * 2 * SP + v;
+        if (gridDim.y > 1) atomicAdd(dst, sacc);
+        else *dst = sacc;
+      }
+    }
+    __syncthreads();
+  }
+  if (act) {
+#pragma unroll
+    for (int j = 0; j < SG; ++j) gA_part[((size_t)n * Dn + d) * SP + s0 + j] = gA[j];
+    if (gi == 0) gD_part[(size_t)n * Dn + d] = gD;
+  }
+}
+
+// gB, gC (dtype) from gbc; gA_log[d, s] = sum_n gA_part * dA/dA_log; gD[d] = sum_n gD_part.
+template <int DT, int SP, int MODE>
+__global__ void __launch_bounds__(256)
+ssm_scan_bwd_finalize(const float* __restrict__ gbc, const float* __restrict__ gA_part,
+                      const float* __restrict__ gD_part, const float* __restrict__ A_log,
+                      typename Elem<DT>::T* __restrict__ gB, typename Elem<DT>::T* __restrict__ gC,
+                      float* __restrict__ gA_log, float* __restrict__ gD, int64_t N, int T, int Dn, int S) {
+  using E = Elem<DT>;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t tid0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t nbc = N * T * S;
+  for (int64_t i = tid0; i < nbc; i += stride) {
+    const int64_t r = i / S, s = i - r * S;
+    E::st(gB + i, gbc[r * 2 * SP + s]);
+    E::st(gC + i, gbc[r * 2 * SP + SP + s]);
+  }
+  for (int64_t i = tid0; i < (int64_t)Dn * S; i += stride) {
+    const int64_t dd = i / S, s = i - dd * S;
+    float acc = 0.f;
+    for (int64_t n = 0; n < N; ++n) acc += gA_part[(n * Dn + dd) * SP + s];
+    const float e = expf(A_log[i]);
+    float dadl = -e;                          // d(-exp(A_log))/dA_log
+    if (MODE == HCLSM_SCAN_MODEL && !(e >= 1e-6f && e <= 1.0f)) dadl = 0.f;
+    gA_log[i] = acc * dadl;
+  }
+  if (gD) {
+    for (int64_t dd = tid0; dd < Dn; dd += stride) {
+      float acc = 0.f;
+      for (int64_t n = 0; n < N; ++n) acc += gD_part[n * Dn + dd];
+      gD[dd] = acc;
+    }
+  }
+}
+
+static int64_t sp_of(int64_t S) { return S <= 4 ? 4 : S <= 8 ? 8 : S <= 16 ? 16 : S <= 32 ? 32 : 64; }
+
+struct BwdWs {
+  size_t ck, gbc, ga, gd, total;
+  int nchunk;
+};
+
+static BwdWs bwd_ws(int64_t N, int64_t T, int64_t Dn, int64_t S) {
+  const int64_t SP = sp_of(S);
+  const int64_t SG = SP < 8 ? SP : 8;
+  const int64_t K = 64 / SG;
+  BwdWs w;
+  w.nchunk = (int)((T + K - 1) / K);
+  auto al = [](size_t v) { return (v + 255) / 256 * 256; };
+  size_t o = 0;
+  w.ck = o; o += al((size_t)N * w.nchunk * Dn * SP * 4);
+  w.gbc = o; o += al((size_t)N * T * 2 * SP * 4);
+  w.ga = o; o += al((size_t)N * Dn * SP * 4);
+  w.gd = o; o += al((size_t)N * Dn * 4);
+  w.total = o;
+  return w;
+}
+
+template <int DT, int SP, int MODE>
+static int launch_bwd(const void* x, const void* dt, const float* A_log, const void* B, const void* C,
+                      const float* Dskip, const void* gy, void* gx, void* gdt, float* gA_log, void* gB, void* gC,
+                      float* gD, char* ws, const BwdWs& L, int64_t N, int64_t T, int64_t Dn, int64_t S,
+                      hipStream_t st) {
+  using TT = typename Elem<DT>::T;
+  constexpr int SG = SP < 8 ? SP : 8;
+  constexpr int G = SP / SG;
+  int DW = (int)Dn;
+  if ((int64_t)DW * G > BWD_MAX_THREADS) DW = BWD_MAX_THREADS / G;
+  const int nblk_d = (int)((Dn + DW - 1) / DW);
+  int threads = DW * G;
+  threads = (threads + 63) / 64 * 64;
+  BwdArgs a;
+  a.T = (int)T; a.Dn = (int)Dn; a.S = (int)S; a.nchunk = L.nchunk; a.DW = DW;
+  a.ld_ck = Dn * SP;
+  float* gbc = reinterpret_cast<float*>(ws + L.gbc);
+  if (nblk_d > 1) {
+    const int rc = zero_fill_f32(gbc, N * T * 2 * SP, st);
+    if (rc) return rc;
+  }
+  hipLaunchKernelGGL((ssm_scan_bwd_kernel<DT, SP, MODE>), dim3((unsigned)N, (unsigned)nblk_d), dim3(threads), 0, st,
+                     (const TT*)x, (const TT*)dt, A_log, (const TT*)B, (const TT*)C, Dskip, (const TT*)gy, (TT*)gx,
+                     (TT*)gdt, reinterpret_cast<float*>(ws + L.ck), gbc, reinterpret_cast<float*>(ws + L.ga),
+                     reinterpret_cast<float*>(ws + L.gd), a);
+  HCLSM_LAUNCH_CHECK();
+  int64_t g = (N * T * S + 255) / 256;
+  g = g < 1 ? 1 : (g > 2048 ? 2048 : g);
+  hipLaunchKernelGGL((ssm_scan_bwd_finalize<DT, SP, MODE>), dim3((unsigned)g), dim3(256), 0, st, gbc,
+                     reinterpret_cast<const float*>(ws + L.ga), reinterpret_cast<const float*>(ws + L.gd), A_log,
+                     (TT*)gB, (TT*)gC, gA_log, gD, N, (int)T, (int)Dn, (int)S);
+  HCLSM_LAUNCH_CHECK();
+  return 0;
+}
+
+}  // namespace hclsm
+
+using namespace hclsm;
+
+extern "C" int64_t hclsm_ssm_scan_bwd_workspace(int64_t batch, int64_t T, int64_t d_inner, int64_t d_state) {
+  if (batch < 0 || T < 0 || d_inner < 0 || d_state < 1 || d_state > 64) return HCLSM_ERR_SHAPE;
+  return (int64_t)bwd_ws(batch, T, d_inner, d_state).total;
+}
+
+extern "C" int hclsm_ssm_scan_bwd(const void* x, const void* dt, const float* A_log, const void* B, const void* C,
+                                  const float* Dskip, const void* gy, void* gx, void* gdt, float* gA_log, void* gB,
+                                  void* gC, float* gD, int64_t batch, int64_t T, int64_t d_inner, int64_t d_state,
+                                  int dtype, int mode, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (batch < 0 || T < 0 || d_inner < 0 || d_state < 1) return HCLSM_ERR_SHAPE;
+  if (batch > 0x7fffffffLL || T > 0x7fffffffLL || d_inner > 0x7fffffffLL) return HCLSM_ERR_SHAPE;
+  if (d_state > 64) return HCLSM_ERR_UNSUPPORTED;
+  if (mode != HCLSM_SCAN_RAW && mode != HCLSM_SCAN_MODEL) return HCLSM_ERR_MODE;
+  if (dtype != HCLSM_F32 && dtype != HCLSM_BF16 && dtype != HCLSM_F16) return HCLSM_ERR_DTYPE;
+  hipStream_t st = (hipStream_t)stream;
+  if (batch == 0 || T == 0 || d_inner == 0) {
+    // no products: every gradient is zero
+    if (gA_log && d_inner > 0) { int rc = zero_fill_f32(gA_log, d_inner * d_state, st); if (rc) return rc; }
+    if (gD && d_inner > 0) { int rc = zero_fill_f32(gD, d_inner, st); if (rc) return rc; }
+    const int64_t es = dtype == HCLSM_F32 ? 4 : 2;
+    if (gB && batch * T > 0) { int rc = zero_fill_bytes(gB, batch * T * d_state * es, st); if (rc) return rc; }
+    if (gC && batch * T > 0) { int rc = zero_fill_bytes(gC, batch * T * d_state * es, st); if (rc) return rc; }
+    return 0;
+  }
+  if (!x || !dt || !A_log || !B || !C || !gy || !gx || !gdt || !gA_log || !gB || !gC || !workspace)
+    return HCLSM_ERR_NULL;
+  const BwdWs L = bwd_ws(batch, T, d_inner, d_state);
+  if (workspace_bytes < (int64_t)L.total) return HCLSM_ERR_SHAPE;
+  char* ws = reinterpret_cast<char*>(workspace);
+#define HCLSM_BWD(DT_, SP_)                                                                                  \
+  if (sp_of(d_state) == SP_) {                                                                               \
+    if (mode == HCLSM_SCAN_RAW)                                                                              \
+      return launch_bwd<DT_, SP_, HCLSM_SCAN_RAW>(x, dt, A_log, B, C, Dskip, gy, gx, gdt, gA_log, gB, gC, gD, ws, L, \
+                                                  batch, T, d_inner, d_state, st);                           \
+    return launch_bwd<DT_, SP_, HCLSM_SCAN_MODEL>(x, dt, A_log, B, C, Dskip, gy, gx, gdt, gA_log, gB, gC, gD, ws, L, \
+                                                  batch, T, d_inner, d_state, st);                           \
+  }
+#define HCLSM_BWD_DT(DT_) \
+  HCLSM_BWD(DT_, 4) HCLSM_BWD(DT_, 8) HCLSM_BWD(DT_, 16) HCLSM_BWD(DT_, 32) HCLSM_BWD(DT_, 64)
+  if (dtype == HCLSM_F32) { HCLSM_BWD_DT(HCLSM_F32) }
+  if (dtype == HCLSM_BF16) { HCLSM_BWD_DT(HCLSM_BF16) }
+  if (dtype == HCLSM_F16) { HCLSM_BWD_DT(HCLSM_F16) }
+#undef HCLSM_BWD_DT
+#undef HCLSM_BWD
+  return HCLSM_ERR_UNSUPPORTED;
+}

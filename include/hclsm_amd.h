@@ -79,6 +79,23 @@ int hclsm_ssm_scan_fwd(const void* x, const void* dt, const float* A_log,
                        int64_t batch, int64_t T, int64_t d_inner, int64_t d_state,
                        int dtype, int mode, void* stream);
 
+/* Workspace bytes for hclsm_ssm_scan_bwd. */
+int64_t hclsm_ssm_scan_bwd_workspace(int64_t batch, int64_t T, int64_t d_inner, int64_t d_state);
+
+/*
+ * Selective SSM scan, backward: gradients of sum(gy * y) for the forward of hclsm_ssm_scan_fwd with the
+ * same arguments and mode.  gy, gx, gdt [batch, T, d_inner] and gB, gC [batch, T, d_state] in `dtype`;
+ * gA_log [d_inner, d_state] float32; gD [d_inner] float32 (nullable; Dskip nullable as in the forward).
+ * MODEL mode passes gradient through each clamp only inside its closed interval.  Chunk checkpoints and
+ * partial sums live in `workspace` (>= hclsm_ssm_scan_bwd_workspace bytes).  Three launches at most.
+ * Replaces: _TritonSSMScan.backward (hclsm/kernels/ssm_scan_kernel.py:321-377) and the autograd of
+ *   sequential_ssm_scan (:42-86) / the inline scan of SimplifiedSSMBlock (dynamics/level0_ssm.py:82-101).
+ */
+int hclsm_ssm_scan_bwd(const void* x, const void* dt, const float* A_log, const void* B, const void* C,
+                       const float* Dskip, const void* gy, void* gx, void* gdt, float* gA_log, void* gB,
+                       void* gC, float* gD, int64_t batch, int64_t T, int64_t d_inner, int64_t d_state,
+                       int dtype, int mode, void* workspace, int64_t workspace_bytes, void* stream);
+
 /*
  * Event index of a [B, T] mask, built on the device with no host synchronisation.
  *   counts  [B]      int32  events per row
