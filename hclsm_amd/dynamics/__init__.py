@@ -1,0 +1,10 @@
+"""Counterparts of the reference's hclsm/dynamics modules on the hot path, routed through
+hclsm_amd.kernels (the reference modules inline their own PyTorch versions instead)."""
+
+from hclsm_amd.dynamics.level0_ssm import Level0SSM, SimplifiedSSMBlock
+from hclsm_amd.dynamics.level1_event import EventTransformerBlock, Level1EventDynamics, SwiGLUFFN
+from hclsm_amd.dynamics.hierarchy_manager import HierarchyManager
+from hclsm_amd.dynamics.event_detector import event_mask_rule
+
+__all__ = ["Level0SSM", "SimplifiedSSMBlock", "EventTransformerBlock", "Level1EventDynamics", "SwiGLUFFN",
+           "HierarchyManager", "event_mask_rule"]

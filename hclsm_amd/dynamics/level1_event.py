@@ -1,0 +1,85 @@
+"""Level-1 event dynamics on MI355X: counterpart of hclsm/dynamics/level1_event.py.
+
+Same module tree and parameter names (``attn`` stays an nn.MultiheadAttention so state dicts
+load unchanged).  The attention core of every EventTransformerBlock -- per event, all N slots
+attend to each other with key padding from the alive mask (:37-52) -- runs on the MFMA
+varlen-attention kernel (``hclsm_amd.kernels.slots_attention``); the in/out projections use the
+same weights through torch GEMMs.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from hclsm_amd.kernels.event_attention import slots_attention
+
+
+class SwiGLUFFN(nn.Module):
+    """w2(silu(w1 x) * w3 x) with hidden = expansion * d_model (reference :17-28)."""
+
+    def __init__(self, d_model: int, expansion: int = 4) -> None:
+        super().__init__()
+        hidden = d_model * expansion
+        self.w1 = nn.Linear(d_model, hidden, bias=False)
+        self.w3 = nn.Linear(d_model, hidden, bias=False)
+        self.w2 = nn.Linear(hidden, d_model, bias=False)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.w2(F.silu(self.w1(x)) * self.w3(x))
+
+
+class EventTransformerBlock(nn.Module):
+    """Pre-LN block: x + MHA(LN x) over the slot axis, then x + SwiGLU(LN x) (reference :31-54)."""
+
+    def __init__(self, d_model: int, n_heads: int) -> None:
+        super().__init__()
+        self.norm1 = nn.LayerNorm(d_model)
+        self.attn = nn.MultiheadAttention(d_model, n_heads, batch_first=True, bias=False)
+        self.norm2 = nn.LayerNorm(d_model)
+        self.ffn = SwiGLUFFN(d_model)
+
+    def forward(self, x: torch.Tensor, key_padding_mask: torch.Tensor | None = None) -> torch.Tensor:
+        normed = self.norm1(x)
+        P, N, d = normed.shape
+        H = self.attn.num_heads
+        dh = d // H
+        qkv = F.linear(normed, self.attn.in_proj_weight, self.attn.in_proj_bias)
+        q, k, v = (t.reshape(P, N, H, dh) for t in qkv.split(d, dim=-1))
+        o = slots_attention(q, k, v, key_padding_mask)
+        attn_out = F.linear(o.reshape(P, N, d), self.attn.out_proj.weight, self.attn.out_proj.bias)
+        x = x + attn_out
+        return x + self.ffn(self.norm2(x))
+
+
+class Level1EventDynamics(nn.Module):
+    """Sparse transformer over object states at event timesteps (reference :57-133)."""
+
+    def __init__(self, config, d_slot: int, use_gradient_checkpointing: bool = False) -> None:
+        super().__init__()
+        self.d_model = config.d_model
+        self.d_slot = d_slot
+        self.use_gradient_checkpointing = use_gradient_checkpointing
+        self.proj_in = nn.Linear(d_slot, config.d_model, bias=False)
+        self.proj_out = nn.Linear(config.d_model, d_slot, bias=False)
+        self.blocks = nn.ModuleList([EventTransformerBlock(config.d_model, config.n_heads)
+                                     for _ in range(config.n_layers)])
+        self.norm = nn.LayerNorm(config.d_model)
+
+    def forward(self, event_states: torch.Tensor, event_pad_mask: torch.Tensor | None = None,
+                obj_mask: torch.Tensor | None = None) -> torch.Tensor:
+        B, K, N, D = event_states.shape
+        x = self.proj_in(event_states.reshape(B * K, N, D))                     # :102-107
+        kpm = None
+        if obj_mask is not None:                                                 # :110-114
+            kpm = (~(obj_mask > 0.5)).unsqueeze(1).expand(B, K, N).reshape(B * K, N)
+        for block in self.blocks:                                                # :116-122
+            if self.use_gradient_checkpointing and self.training:
+                x = torch.utils.checkpoint.checkpoint(block, x, kpm, use_reentrant=False)
+            else:
+                x = block(x, key_padding_mask=kpm)
+        x = self.proj_out(self.norm(x)).reshape(B, K, N, D)                      # :124-128
+        if event_pad_mask is not None:                                           # :130-131
+            x = x * event_pad_mask[:, :, None, None]
+        return x

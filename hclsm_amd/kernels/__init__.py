@@ -36,6 +36,7 @@ from hclsm_amd.kernels.event_attention import (
 )
 
 from hclsm_amd.kernels.slot_attention_kernel import (
+    slot_attention_core,
     slot_attention_fn,
     naive_slot_attention,
     compiled_slot_attention,
@@ -65,6 +66,7 @@ def _hip_available() -> bool:
 HIP_AVAILABLE = _hip_available()
 
 __all__ = [
+    "slot_attention_core",
     "slot_attention_fn",
     "naive_slot_attention",
     "compiled_slot_attention",

@@ -104,13 +104,50 @@ def _dense_index(P: int, N: int, device) -> EventIndex:
     return idx
 
 
+def _slots_attention_raw(q, k, v, key_padding_mask, scale):
+    P, N = q.shape[:2]
+    idx = _dense_index(P, N, q.device)
+    return event_attention(q, k, v, idx, "slots", scale=scale, key_pad=key_padding_mask, out="grid",
+                           out_grid=torch.empty(q.shape, dtype=q.dtype, device=q.device))
+
+
+class _SlotsAttention(torch.autograd.Function):
+    """HIP forward; backward recomputes the (small, N x N) softmax in fp32 with torch on the GPU."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, key_padding_mask, scale):
+        ctx.save_for_backward(q, k, v, key_padding_mask if key_padding_mask is not None else torch.empty(0))
+        ctx.has_kp = key_padding_mask is not None
+        ctx.scale = scale
+        return _slots_attention_raw(q, k, v, key_padding_mask, scale)
+
+    @staticmethod
+    def backward(ctx, go):
+        q, k, v, kp = ctx.saved_tensors
+        qf, kf, vf, gf = (t.float().permute(0, 2, 1, 3).contiguous() for t in (q, k, v, go))   # (P, H, N, dh)
+        s = torch.matmul(qf, kf.transpose(-1, -2).contiguous()) * ctx.scale
+        if ctx.has_kp:
+            s = s.masked_fill(kp.bool()[:, None, None, :], float("-inf"))
+        p = torch.softmax(s, dim=-1)
+        dv = torch.matmul(p.transpose(-1, -2).contiguous(), gf)
+        dp = torch.matmul(gf, vf.transpose(-1, -2).contiguous())
+        ds = p * (dp - (dp * p).sum(dim=-1, keepdim=True))
+        dq = torch.matmul(ds, kf) * ctx.scale
+        dk = torch.matmul(ds.transpose(-1, -2).contiguous(), qf) * ctx.scale
+        back = lambda t, like: t.permute(0, 2, 1, 3).contiguous().to(like.dtype)
+        return back(dq, q), back(dk, k), back(dv, v), None, None
+
+
 def slots_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                     key_padding_mask: torch.Tensor | None = None, scale: float | None = None) -> torch.Tensor:
     """Attention across the N slot rows of each of P problems: q, k, v (P, N, H, dh);
     key_padding_mask (P, N) bool, True = ignore that key (nn.MultiheadAttention's convention).
-    Returns (P, N, H, dh).  A query with every key padded returns NaN, like the reference."""
+    Returns (P, N, H, dh).  A query with every key padded returns NaN, like the reference.
+    Differentiable (forward on the HIP kernel)."""
     require_gpu("slots_attention", q, k, v, key_padding_mask)
-    P, N = q.shape[:2]
-    idx = _dense_index(P, N, q.device)
-    return event_attention(q, k, v, idx, "slots", scale=scale, key_pad=key_padding_mask, out="grid",
-                           out_grid=torch.empty_like(q.contiguous()))
+    if scale is None:
+        scale = q.shape[-1] ** -0.5
+    kp = None if key_padding_mask is None else key_padding_mask.to(torch.bool).contiguous()
+    if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
+        return _SlotsAttention.apply(q, k, v, kp, float(scale))
+    return _slots_attention_raw(q, k, v, kp, float(scale))

@@ -50,10 +50,11 @@ def _core_raw(Q, K, V, scale, denom_eps, logit_clamp=None, renorm_eps=None, want
 
 class _SlotAttnCore(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, Q, K, V, scale, denom_eps):
-        out, attn = _core_raw(Q, K, V, scale, denom_eps)
+    def forward(ctx, Q, K, V, scale, denom_eps, logit_clamp=None):
+        out, attn = _core_raw(Q, K, V, scale, denom_eps, logit_clamp=logit_clamp)
         ctx.save_for_backward(Q, K, V, attn)
         ctx.scale = scale
+        ctx.logit_clamp = logit_clamp
         return out.to(Q.dtype), attn.to(Q.dtype)
 
     @staticmethod
@@ -65,10 +66,22 @@ class _SlotAttnCore(torch.autograd.Function):
             d_attn = d_attn + grad_attn
         sum_da = (attn * d_attn).sum(dim=1, keepdim=True)      # softmax over slots (dim 1)
         d_logits = attn * (d_attn - sum_da) * ctx.scale
+        if ctx.logit_clamp:   # clamp passes gradient only inside [-c, c] (dynamic_slots.py:118)
+            logits = torch.bmm(Q, K.transpose(1, 2).contiguous()) * ctx.scale
+            d_logits = d_logits * (logits.abs() <= ctx.logit_clamp).to(d_logits.dtype)
         d_Q = torch.bmm(d_logits, K)
         d_K = torch.bmm(d_logits.transpose(1, 2).contiguous(), Q)
         d_V = torch.bmm(attn.transpose(1, 2).contiguous(), grad_out) if grad_out is not None else torch.zeros_like(V)
-        return d_Q, d_K, d_V, None, None
+        return d_Q, d_K, d_V, None, None, None
+
+
+def slot_attention_core(Q, K, V, scale=None, denom_eps=0.0, logit_clamp=None):
+    """The core with the in-model options: logits clamped to +-logit_clamp before the softmax over
+    slots (dynamic_slots.py:116-119).  Differentiable."""
+    _check(Q, K, V)
+    if scale is None:
+        scale = Q.shape[-1] ** -0.5
+    return _SlotAttnCore.apply(Q, K, V, float(scale), float(denom_eps), logit_clamp)
 
 
 def _check(Q, K, V):

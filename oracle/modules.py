@@ -1,0 +1,108 @@
+"""Oracle: the in-model modules around the hot-path kernels.  TEST INFRASTRUCTURE ONLY.
+
+Numpy float64 restatements, taking parameters as plain arrays (names as in the reference's
+state dicts):
+  simplified_ssm_block_ref  hclsm/dynamics/level0_ssm.py:58-107 (scan in model mode)
+  level0_ssm_ref            hclsm/dynamics/level0_ssm.py:159-220
+  event_block_ref           hclsm/dynamics/level1_event.py:44-54 (MHA over slots + SwiGLU)
+  level1_ref                hclsm/dynamics/level1_event.py:85-133
+  event_mask_rule_ref       hclsm/dynamics/event_detector.py:160-170
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from oracle.events import slots_attention
+from oracle.slot_attention import layer_norm, sigmoid
+from oracle.ssm_scan import ssm_scan_ref
+
+
+def _lin(x, w, b=None):
+    y = x @ np.asarray(w, np.float64).T
+    return y if b is None else y + b
+
+
+def softplus(x):
+    return np.where(x > 20, x, np.log1p(np.exp(np.minimum(x, 20))))
+
+
+def silu(x):
+    return x * sigmoid(x)
+
+
+def simplified_ssm_block_ref(x, p):
+    """p keys: norm.weight, norm.bias, in_proj.weight, gate_proj.weight, dt_proj.weight, dt_proj.bias,
+    B_proj.weight, C_proj.weight, A_log, out_proj.weight."""
+    x = np.asarray(x, np.float64)
+    h = layer_norm(x, p["norm.weight"], p["norm.bias"])
+    z = _lin(h, p["in_proj.weight"])
+    gate = silu(_lin(h, p["gate_proj.weight"]))
+    dt = np.clip(softplus(_lin(z, p["dt_proj.weight"], p["dt_proj.bias"])), 1e-3, 1.0)
+    Bm = _lin(z, p["B_proj.weight"])
+    Cm = _lin(z, p["C_proj.weight"])
+    y = ssm_scan_ref(z, dt, p["A_log"], Bm, Cm, clamp_mode="model")
+    return x + _lin(y * gate, p["out_proj.weight"])
+
+
+def level0_ssm_ref(obj_states, obj_mask, p, n_blocks):
+    """p: state-dict-like mapping with keys global_blocks.{i}.*, object_blocks.{i}.*, condition_proj.weight."""
+    s = np.asarray(obj_states, np.float64)
+    B, N, T, D = s.shape
+    blk = lambda pre, i: {k[len(f"{pre}.{i}."):]: v for k, v in p.items() if k.startswith(f"{pre}.{i}.")}
+    if obj_mask is not None:
+        m = np.asarray(obj_mask, np.float64)
+        n_alive = np.maximum(m.sum(1, keepdims=True), 1.0)
+        g = (s * m[:, :, None, None]).sum(1) / n_alive[:, :, None]
+    else:
+        g = s.mean(1)
+    for i in range(n_blocks):
+        g = simplified_ssm_block_ref(g, blk("global_blocks", i))
+    cond = _lin(g, p["condition_proj.weight"])
+    x = (s + cond[:, None]).reshape(B * N, T, D)
+    for i in range(n_blocks):
+        x = simplified_ssm_block_ref(x, blk("object_blocks", i))
+    x = np.clip(np.nan_to_num(x.reshape(B, N, T, D), nan=0.0, posinf=100.0, neginf=-100.0), -100, 100)
+    if obj_mask is not None:
+        x = x * np.asarray(obj_mask, np.float64)[:, :, None, None]
+    return x
+
+
+def event_block_ref(x, key_pad, p, n_heads):
+    """p keys: norm1.*, attn.in_proj_weight, attn.out_proj.weight, norm2.*, ffn.w1/w2/w3.weight."""
+    x = np.asarray(x, np.float64)
+    P, N, d = x.shape
+    dh = d // n_heads
+    h = layer_norm(x, p["norm1.weight"], p["norm1.bias"])
+    q, k, v = np.split(_lin(h, p["attn.in_proj_weight"]), 3, axis=-1)
+    o = slots_attention(*(t.reshape(P, N, n_heads, dh) for t in (q, k, v)), key_pad=key_pad)
+    x = x + _lin(o.reshape(P, N, d), p["attn.out_proj.weight"])
+    h2 = layer_norm(x, p["norm2.weight"], p["norm2.bias"])
+    f = _lin(silu(_lin(h2, p["ffn.w1.weight"])) * _lin(h2, p["ffn.w3.weight"]), p["ffn.w2.weight"])
+    return x + f
+
+
+def level1_ref(event_states, event_pad_mask, obj_mask, p, n_layers, n_heads):
+    e = np.asarray(event_states, np.float64)
+    B, K, N, D = e.shape
+    x = _lin(e.reshape(B * K, N, D), p["proj_in.weight"])
+    kp = None
+    if obj_mask is not None:
+        kp = np.broadcast_to(~(np.asarray(obj_mask) > 0.5)[:, None, :], (B, K, N)).reshape(B * K, N)
+    for i in range(n_layers):
+        blk = {k[len(f"blocks.{i}."):]: v for k, v in p.items() if k.startswith(f"blocks.{i}.")}
+        x = event_block_ref(x, kp, blk, n_heads)
+    x = _lin(layer_norm(x, p["norm.weight"], p["norm.bias"]), p["proj_out.weight"]).reshape(B, K, N, D)
+    if event_pad_mask is not None:
+        x = x * np.asarray(event_pad_mask, np.float64)[:, :, None, None]
+    return x
+
+
+def event_mask_rule_ref(probs, threshold_logit):
+    probs = np.asarray(probs, np.float64)
+    thr = sigmoid(np.asarray(threshold_logit, np.float64))
+    hard = (probs > thr).astype(np.float64)
+    mask = hard - probs + probs
+    if mask.shape[1] and hard.sum(1).min() == 0:
+        mask[:, 0] = 1.0
+    return mask
