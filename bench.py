@@ -39,6 +39,7 @@ def _parse():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-extra", action="store_true", help="time only the config-1 scan (configs 2-4 skipped)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="after the timed loop, run a 1 GiB device-to-device copy 5 times (a kernel of "
                         "known traffic for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE counters)")
@@ -92,7 +93,7 @@ def _event_timing(fn, n, warmup):
     return ts[len(ts) // 2], sum(ts) / len(ts)
 
 
-def _bench_slot(dev, n, warmup):
+def _bench_slot(dev, n, warmup, cpu):
     """Config 2: k/v projections + 3 slot-attention iterations (bf16 operands, fp32 accumulation)."""
     import torch
     from hclsm_amd.kernels import slot_iteration as si
@@ -103,13 +104,29 @@ def _bench_slot(dev, n, warmup):
     med, avg = _event_timing(lambda: si.slot_attention_forward(tk, s0, W, 3, si.CONFIG2_MODE), n, warmup)
     fl = slot_flops()
     ntok = tokens.shape[0] * tokens.shape[1]
-    return {"workload": "config 2: 32 frames x 196 tokens x 384, 32 slots, 3 iterations, MLP 768, bf16 MFMA",
-            "metric": "tokens/s", "value": round(ntok / med, 1), "median_us": round(med * 1e6, 2),
-            "roofline": {"bound": "mfma", "achieved": round(fl / med / 1e12, 3), "peak": 2500.0,
-                         "unit": "TFLOP/s", "frac": round(fl / med / 1e12 / 2500.0, 5), "flops_per_call": fl}}
+    res = {"workload": "config 2: 32 frames x 196 tokens x 384, 32 slots, 3 iterations, MLP 768, bf16 MFMA",
+           "metric": "tokens/s", "value": round(ntok / med, 1), "median_us": round(med * 1e6, 2),
+           "roofline": {"bound": "mfma", "achieved": round(fl / med / 1e12, 3), "peak": 2500.0,
+                        "unit": "TFLOP/s", "frac": round(fl / med / 1e12 / 2500.0, 5), "flops_per_call": fl}}
+    if cpu:
+        from threadpoolctl import threadpool_limits
+        from oracle.slot_attention import slot_attention_forward as ref_fwd
+        tn, sn = tokens.numpy(), slots0.numpy()
+        wn = {k: t.numpy() for k, t in w.items()}
+        with threadpool_limits(1):
+            ts = []
+            for _ in range(3):
+                t0 = time.perf_counter()
+                ref_fwd(tn, sn, wn, 3, logit_clamp=None, renorm_eps=1e-8, slot_clamp=None)
+                ts.append(time.perf_counter() - t0)
+        cmed = sorted(ts)[1]
+        res["cpu_baseline"] = {"value": round(ntok / cmed, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
+                               "sample": f"full config 2, numpy float64 oracle (oracle/slot_attention.py), "
+                                         f"1 BLAS thread, median of 3: {cmed:.3f} s"}
+    return res
 
 
-def _bench_events(dev, n, warmup):
+def _bench_events(dev, n, warmup, cpu):
     """Config 3: event index + per-track causal attention, 1024 tracks x T=64, 6 x 64 heads, p=0.15."""
     import torch
     from hclsm_amd.kernels.event_attention import event_attention
@@ -126,13 +143,93 @@ def _bench_events(dev, n, warmup):
         event_attention(q, k, v, idx, capacity=total)
     med, avg = _event_timing(step, n, warmup)
     nbytes = total * 6 * 64 * 2 * 4 + m.numel() * 4 + (1025 + 2 * total + 2 * 65536) * 4
-    return {"workload": "config 3: 1024 tracks x T=64, 6 heads x 64, p=0.15 (t=0 forced), bf16, "
+    res = {"workload": "config 3: 1024 tracks x T=64, 6 heads x 64, p=0.15 (t=0 forced), bf16, "
                         "index build + causal event attention, packed output",
             "events": total, "metric": "event-tokens/s", "value": round(total / med, 1),
             "grid_tokens_per_s": round(65536 / med, 1), "median_us": round(med * 1e6, 2),
             "roofline": {"bound": "hbm", "achieved": round(nbytes / med / 1e9, 2), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(nbytes / med / 1e9 / HBM_PEAK_GBS, 5),
                          "bytes_per_call": nbytes}}
+    if cpu:
+        from threadpoolctl import threadpool_limits
+        from oracle import events as oe
+        mn = m.cpu().numpy()
+        qn, kn, vn = (t.float().cpu().numpy() for t in (q, k, v))
+        with threadpool_limits(1):
+            ts = []
+            for _ in range(3):
+                t0 = time.perf_counter()
+                oe.track_causal_attention(qn, kn, vn, oe.event_index(mn))
+                ts.append(time.perf_counter() - t0)
+        cmed = sorted(ts)[1]
+        res["cpu_baseline"] = {"value": round(total / cmed, 1), "unit": "event-tokens/s", "cores": 1, "kind": "port",
+                               "sample": f"full config 3, numpy oracle index + per-track causal attention "
+                                         f"(oracle/events.py), 1 BLAS thread, median of 3: {cmed:.3f} s"}
+    return res
+
+
+def _bench_chain(dev, n, warmup):
+    """Config 4: four chained scans at (1024, 1024, 768), S=16, bf16 (each fed the previous output),
+    then the event index of a p=0.05 mask (t=0 forced) and causal event attention, 12 heads x 64."""
+    import torch
+    from hclsm_amd import _lib
+    from hclsm_amd.kernels.event_attention import event_attention
+    from hclsm_amd.kernels.sparse_event_attn import build_event_index
+    from hclsm_amd.workloads import scan_algorithmic_bytes
+    from oracle.ssm_scan import normwise_rel_err, ssm_scan_ref
+    L = _lib.lib()
+    N, T, Dn, S = 1024, 1024, 768, 16
+    g = torch.Generator(device=dev).manual_seed(1004)
+    bf = torch.bfloat16
+    x0 = torch.randn(N, T, Dn, generator=g, device=dev).to(bf)
+    dt = torch.nn.functional.softplus(-2 + 0.5 * torch.randn(N, T, Dn, generator=g, device=dev)).to(bf)
+    A_log = torch.rand(Dn, S, generator=g, device=dev) * float(torch.log(torch.tensor(16.0)))
+    Bm = (torch.randn(N, T, S, generator=g, device=dev) / 4).to(bf)
+    Cm = (torch.randn(N, T, S, generator=g, device=dev) / 4).to(bf)
+    Dv = torch.randn(Dn, generator=g, device=dev)
+    ys = [torch.empty_like(x0), torch.empty_like(x0)]
+    stream = torch.cuda.current_stream(dev).cuda_stream
+
+    def scan(xin, yout):
+        code = L.hclsm_ssm_scan_fwd(xin.data_ptr(), dt.data_ptr(), A_log.data_ptr(), Bm.data_ptr(), Cm.data_ptr(),
+                                    Dv.data_ptr(), yout.data_ptr(), None, N, T, Dn, S, _lib.BF16, _lib.SCAN_RAW, stream)
+        if code:
+            raise RuntimeError(_lib.strerror(code))
+
+    def scans():
+        scan(x0, ys[0])
+        scan(ys[0], ys[1])
+        scan(ys[1], ys[0])
+        scan(ys[0], ys[1])
+
+    m = (torch.rand(N, T, generator=g, device=dev) < 0.05).float()
+    m[:, 0] = 1
+    H, dh = 12, 64
+    q, k, v = (torch.randn(N, T, H, dh, generator=g, device=dev).to(bf) for _ in range(3))
+    total = build_event_index(m).total()
+
+    def attn():
+        event_attention(q, k, v, build_event_index(m), capacity=total)
+
+    # parity spot check of the first scan on 2 sequences
+    scan(x0, ys[0])
+    sel = slice(0, 2)
+    ref = ssm_scan_ref(*(t[sel].float().cpu().numpy() for t in (x0, dt)), A_log.cpu().numpy(),
+                       *(t[sel].float().cpu().numpy() for t in (Bm, Cm)), D=Dv.cpu().numpy(), clamp_mode="raw")
+    err = normwise_rel_err(ys[0][sel].float().cpu().numpy(), ref)
+    if not err <= 2e-2:
+        raise SystemExit(f"bench.py: config-4 scan parity failed (normwise {err:.3e})")
+    s_med, _ = _event_timing(scans, n, warmup)
+    a_med, _ = _event_timing(attn, n, warmup)
+    sb = scan_algorithmic_bytes(N, T, Dn, S, 2)
+    ab = total * H * dh * 2 * 4 + m.numel() * 4 + (N + 1 + 2 * total + 2 * N * T) * 4
+    return {"workload": "config 4: 4 chained scans (1024 seq x T=1024 x 768, S=16, bf16, raw + skip), then "
+                        "index + causal event attention (p=0.05, t=0 forced, 12 heads x 64, packed output)",
+            "chain_ms": round((s_med + a_med) * 1e3, 4), "scan_us_each": round(s_med / 4 * 1e6, 1),
+            "scan_gbs": round(4 * sb / s_med / 1e9, 1), "scan_frac": round(4 * sb / s_med / 1e9 / HBM_PEAK_GBS, 4),
+            "scan_bytes_each": sb, "events": total, "attn_us": round(a_med * 1e6, 2),
+            "event_tokens_per_s": round(total / a_med, 1), "attn_gbs": round(ab / a_med / 1e9, 1),
+            "scan_parity_normwise_err": err}
 
 
 def main():
@@ -190,6 +287,7 @@ def main():
     durs = sorted(a.elapsed_time(b) * 1e-3 for a, b in evs)   # seconds per launch
     avg = sum(durs) / len(durs)
     med = durs[len(durs) // 2]
+    p10, p90 = durs[len(durs) // 10], durs[(len(durs) * 9) // 10]
 
     # correctness spot check of the last output against the oracle (8 sequences)
     from oracle.ssm_scan import normwise_rel_err, ssm_scan_ref
@@ -229,13 +327,16 @@ def main():
                    "algorithmic_bytes_per_step": nbytes, "parity_normwise_err": err},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic_from_profile(),
-                     "kernel": "ssm_scan_fwd_sgpr_kernel<bf16,16,raw,2,4>",
-                     "avg_launch_us": round(avg * 1e6, 3), "median_launch_us": round(med * 1e6, 3)},
+                     "kernel": "ssm_scan_fwd_mfma_kernel<raw,TC=8,DPL=2>",
+                     "avg_launch_us": round(avg * 1e6, 3), "median_launch_us": round(med * 1e6, 3),
+                     "p10_launch_us": round(p10 * 1e6, 3), "p90_launch_us": round(p90 * 1e6, 3)},
     }
-    out["slot_attn"] = _bench_slot(dev, 30, 5)
-    out["event_attn"] = _bench_events(dev, 50, 5)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = _cpu_baseline(d)
+    if not args.no_extra:
+        out["slot_attn"] = _bench_slot(dev, 100, 10, not args.no_cpu_baseline)
+        out["event_attn"] = _bench_events(dev, 100, 10, not args.no_cpu_baseline)
+        out["chain"] = _bench_chain(dev, 20, 3)
     print(json.dumps(out), flush=True)
 
 

@@ -29,6 +29,12 @@ HIPCC_FLAGS = [
     "-fno-gpu-rdc", "-Wno-unused-result",
 ]
 
+# Per-source extras.  The scan keeps its MFMA accumulator in the VGPRs it also updates with
+# VALU ops every step; the VGPR form of MFMA avoids an AGPR<->VGPR copy of all 16 states.
+FILE_FLAGS = {
+    "ssm_scan.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
 
 def _hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
@@ -56,7 +62,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
 
     def compile_one(src: Path) -> Path:
         obj = objdir / (src.stem + ".o")
-        cmd = [hipcc, *HIPCC_FLAGS, "-I", str(PKG.parent / "include"), "-c", str(src), "-o", str(obj)]
+        cmd = [hipcc, *HIPCC_FLAGS, *FILE_FLAGS.get(src.name, []), "-I", str(PKG.parent / "include"), "-c", str(src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)
         r = subprocess.run(cmd, capture_output=True, text=True)

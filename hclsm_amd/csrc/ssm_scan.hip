@@ -11,8 +11,10 @@
 // works.
 //
 // Per state update the lane does: mul (dt*A*log2e), v_exp_f32, mul (dt*x*B),
-// fma (gate*h + ...), fma (y += h*C).  No MFMA: there is no shared operand across
-// lanes that would make the contraction over d_state a GEMM.
+// fma (gate*h + ...), fma (y += h*C).  The loop is bound by VALU issue, not HBM.
+// For bf16 I/O with d_state 16 the rank-1 input term dt*x*B and its add into h
+// run on the matrix core instead (ssm_scan_fwd_mfma_kernel below), which leaves
+// mul, exp, mul, fma per state update on the VALU.
 #include "common.h"
 
 namespace hclsm {
@@ -363,6 +365,180 @@ static int launch_scan_sgpr(const void* x, const void* dt, const float* A_log, c
   return 0;
 }
 
+// ---------------------------------------------------------------------------
+// bf16 I/O, d_state == 16: the rank-1 input term on the matrix core.
+//
+// Per step the state update is h[d][s] = g[d][s] * h[d][s] + u[d] * b[s] with
+// g = exp2(dt[d] * a2[d][s]) and u = dt * x.  One v_mfma_f32_32x32x8_bf16 per
+// wave and step computes D = A * B + C over a 32 x 32 tile whose accumulator
+// layout gives lane l the 16 rows i = 8*(r/4) + 4*(l/32) + r%4 (r = 0..15) of
+// column j = l%32.  Rows are read as (state s = r, half c = l/32), columns as
+// j, so lane l holds exactly the 16 states of channel c*32 + j = l, in register
+// order r = s: the y contraction stays an in-lane fp32 FMA chain and the
+// per-lane decay g * h is an elementwise VALU product fed as the accumulator C.
+// The product u * b enters through the k dimension:
+//   B operand (lane l: k = 4*(l/32) .. +3 of column l%32) = (u_hi, u_lo, 0, 0)
+//   of the lane's own channel, where u = u_hi + u_lo exactly: dt and x are
+//   bf16, so u has at most 16 significant bits; u_hi is u truncated to bf16 and
+//   the remainder has at most 8 (in MODEL mode a clamped dt can leave a
+//   remainder below 2^-16 of u, which is dropped);
+//   A operand (lane l: k = 4*(l/32) .. +3 of row l%32) = (b_s, b_s, 0, 0) with
+//   s = s(row), when the row's half c(row) matches the lane's k half, else 0.
+// Both products are exact in fp32, so the state keeps fp32 accuracy; the
+// matrix core replaces one multiply and turns the FMA into a multiply, which
+// lowers the VALU work per state update from ~5.4 to ~4.4 instructions on
+// this VALU-bound loop.  Each lane needs b_s for a lane-dependent s, so the B
+// row is read with a per-lane 2-byte load; the C row is uniform and goes
+// through scalar loads.
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// Word 3 of a gfx9-family buffer resource for raw (stride 0) byte addressing.
+constexpr int kRawBufferWord3 = 0x00020000;
+
+template <int MODE, int TC, int DPL>
+__global__ void __launch_bounds__(64)
+ssm_scan_fwd_mfma_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ dt,
+                         const float* __restrict__ A_log, const uint16_t* __restrict__ Bm,
+                         const uint16_t* __restrict__ Cm, const float* __restrict__ Dskip,
+                         uint16_t* __restrict__ y, float* __restrict__ h_final, int T, int Dn) {
+  constexpr int SP = 16;
+  const int n = blockIdx.x;
+  const int l = threadIdx.x;
+  const int c0 = (blockIdx.y * 64 + l) * DPL;          // this lane's first channel
+  const bool act = c0 < Dn;
+  const int d0 = act ? c0 : Dn - DPL;                  // Dn % DPL == 0 (checked by the dispatcher)
+  const int ii = l & 31;                               // A-operand row of this lane
+  const bool a_on = (((ii >> 2) & 1) == (l >> 5));     // row half == lane's k half
+  const int s_row = (ii & 3) + 4 * (ii >> 3);          // state of that row
+
+  float a2[DPL][SP];
+  float dsk[DPL];
+#pragma unroll
+  for (int k = 0; k < DPL; ++k) {
+#pragma unroll
+    for (int s = 0; s < SP; ++s) {
+      float e = expf(A_log[(size_t)(d0 + k) * SP + s]);
+      if (MODE == HCLSM_SCAN_MODEL) e = fminf(fmaxf(e, 1e-6f), 1.0f);
+      a2[k][s] = -e * HCLSM_LOG2E;
+    }
+    dsk[k] = Dskip != nullptr ? Dskip[d0 + k] : 0.f;
+  }
+
+  f32x16_t h[DPL];
+#pragma unroll
+  for (int k = 0; k < DPL; ++k)
+#pragma unroll
+    for (int s = 0; s < SP; ++s) h[k][s] = 0.f;
+
+  // Per-sequence buffer resources: byte offsets are (lane constant) + (step * row pitch, uniform).
+  const size_t row0 = (size_t)n * T;
+  const int slab = T * Dn * 2;                         // < 2^31 (checked by the dispatcher)
+  const auto rx = __builtin_amdgcn_make_buffer_rsrc((void*)(x + row0 * Dn), 0, slab, kRawBufferWord3);
+  const auto rd = __builtin_amdgcn_make_buffer_rsrc((void*)(dt + row0 * Dn), 0, slab, kRawBufferWord3);
+  const auto ry = __builtin_amdgcn_make_buffer_rsrc((void*)(y + row0 * Dn), 0, slab, kRawBufferWord3);
+  const auto rb = __builtin_amdgcn_make_buffer_rsrc((void*)(Bm + row0 * SP), 0, T * SP * 2, kRawBufferWord3);
+  const int vo = d0 * 2;
+  const int vo_st = act ? vo : 0x7ffffff0;             // past num_records: the store is dropped
+  const int vo_b = s_row * 2;
+  const int pitch = Dn * 2;
+  const uint32_t* cw0 = reinterpret_cast<const uint32_t*>(Cm + row0 * SP);
+
+  uint32_t xv[TC], dv[TC];
+  uint16_t bv[TC];
+  auto load = [&](int t0, uint32_t* xo, uint32_t* dO, uint16_t* bO) {
+#pragma unroll
+    for (int j = 0; j < TC; ++j) {
+      const int t = t0 + j < T ? t0 + j : T - 1;
+      if constexpr (DPL == 2) {
+        xo[j] = __builtin_amdgcn_raw_buffer_load_b32(rx, vo, t * pitch, 0);
+        dO[j] = __builtin_amdgcn_raw_buffer_load_b32(rd, vo, t * pitch, 0);
+      } else {
+        xo[j] = __builtin_amdgcn_raw_buffer_load_b16(rx, vo, t * pitch, 0);
+        dO[j] = __builtin_amdgcn_raw_buffer_load_b16(rd, vo, t * pitch, 0);
+      }
+      bO[j] = __builtin_amdgcn_raw_buffer_load_b16(rb, vo_b, t * (SP * 2), 0);
+    }
+  };
+
+  uint32_t cw[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) cw[i] = cw0[i];
+
+  auto step = [&](int t, uint32_t xw, uint32_t dw, uint16_t bb) {
+    const int tn = t + 1 < T ? t + 1 : T - 1;
+    uint32_t cwn[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) cwn[i] = cw0[(size_t)tn * 8 + i];
+    const short ab = a_on ? (short)bb : (short)0;
+    const s16x4_t aop = {ab, ab, 0, 0};
+    float yo[DPL];
+#pragma unroll
+    for (int k = 0; k < DPL; ++k) {
+      const float xs = __uint_as_float(k == 0 ? xw << 16 : xw & 0xffff0000u);
+      float dtv = __uint_as_float(k == 0 ? dw << 16 : dw & 0xffff0000u);
+      if (MODE == HCLSM_SCAN_MODEL) dtv = fminf(fmaxf(dtv, 1e-3f), 1.0f);
+      const float u = dtv * xs;
+      const uint32_t uhi = __float_as_uint(u) & 0xffff0000u;
+      const float ulo = u - __uint_as_float(uhi);
+      const s16x4_t bop = {(short)(uhi >> 16), (short)(__float_as_uint(ulo) >> 16), 0, 0};
+#pragma unroll
+      for (int s = 0; s < SP; ++s) h[k][s] *= fast_exp2(dtv * a2[k][s]);
+      h[k] = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(aop, bop, h[k], 0, 0, 0);
+      float y0 = 0.f, y1 = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        y0 = fmaf(h[k][2 * i], __uint_as_float(cw[i] << 16), y0);
+        y1 = fmaf(h[k][2 * i + 1], __uint_as_float(cw[i] & 0xffff0000u), y1);
+      }
+      yo[k] = fmaf(dsk[k], xs, y0 + y1);
+    }
+    if constexpr (DPL == 2)
+      __builtin_amdgcn_raw_buffer_store_b32(pack_bf16x2(yo[0], yo[1]), ry, vo_st, t * pitch, 0);
+    else
+      __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(yo[0]), ry, vo_st, t * pitch, 0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) cw[i] = cwn[i];
+  };
+
+  load(0, xv, dv, bv);
+  const int tfull = T - T % TC;
+  for (int t0 = 0; t0 < tfull; t0 += TC) {
+    uint32_t xn[TC], dn[TC];
+    uint16_t bn[TC];
+    load(t0 + TC, xn, dn, bn);
+#pragma unroll
+    for (int j = 0; j < TC; ++j) step(t0 + j, xv[j], dv[j], bv[j]);
+#pragma unroll
+    for (int j = 0; j < TC; ++j) { xv[j] = xn[j]; dv[j] = dn[j]; bv[j] = bn[j]; }
+  }
+#pragma unroll
+  for (int j = 0; j < TC - 1; ++j)
+    if (tfull + j < T) step(tfull + j, xv[j], dv[j], bv[j]);
+
+  if (h_final != nullptr && act) {
+#pragma unroll
+    for (int k = 0; k < DPL; ++k) {
+      float* hp = h_final + ((size_t)n * Dn + d0 + k) * SP;
+#pragma unroll
+      for (int s = 0; s < SP; ++s) hp[s] = h[k][s];
+    }
+  }
+}
+
+template <int MODE, int TC, int DPL>
+static int launch_scan_mfma(const void* x, const void* dt, const float* A_log, const void* B,
+                            const void* C, const float* Dskip, void* y, float* h_final,
+                            int64_t batch, int64_t T, int64_t Dn, hipStream_t st) {
+  const int64_t lanes = Dn / DPL;
+  dim3 grid((unsigned)batch, (unsigned)((lanes + 63) / 64));
+  hipLaunchKernelGGL((ssm_scan_fwd_mfma_kernel<MODE, TC, DPL>), grid, dim3(64), 0, st,
+                     (const uint16_t*)x, (const uint16_t*)dt, A_log, (const uint16_t*)B,
+                     (const uint16_t*)C, Dskip, (uint16_t*)y, h_final, (int)T, (int)Dn);
+  HCLSM_LAUNCH_CHECK();
+  return 0;
+}
+
 static inline bool aligned(const void* p, uintptr_t a) { return (((uintptr_t)p) & (a - 1)) == 0; }
 
 // Returns 1 if no fast kernel applies (caller falls back to the generic kernel).
@@ -379,9 +555,12 @@ static int try_scan_sgpr(const void* x, const void* dt, const float* A_log, cons
     return launch_scan_sgpr<DT, SPV, MODE, 1, 8>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, st); \
   }
   if constexpr (DT == HCLSM_BF16) {
+    if (S == 16 && T * Dn * 2 < 0x7fffffffLL) {
+      if (pair) return launch_scan_mfma<MODE, 8, 2>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, st);
+      return launch_scan_mfma<MODE, 8, 1>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, st);
+    }
     HCLSM_SCAN_SGPR(4)
     HCLSM_SCAN_SGPR(8)
-    HCLSM_SCAN_SGPR(16)
   } else if constexpr (DT == HCLSM_F32) {
     HCLSM_SCAN_SGPR(4)
     HCLSM_SCAN_SGPR(8)

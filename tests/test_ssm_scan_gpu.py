@@ -166,3 +166,50 @@ def test_backend_semantics():
         assert normwise_rel_err(_np(ssm_scan_fn(*args, backend=be)), raw) <= FP32_TOL
     for be in ("sequential", "no-such-backend"):
         assert normwise_rel_err(_np(ssm_scan_fn(*args, backend=be)), mod) <= FP32_TOL
+
+
+@pytest.mark.parametrize("N,T,Dn", [
+    (1, 1, 2),           # one step, one lane pair
+    (3, 7, 5),           # odd channels (one channel per lane), T < chunk
+    (2, 9, 70),          # T = chunk + 1, partial wave
+    (2, 17, 130),        # second channel group holds a single active lane pair
+    (1, 33, 129),        # odd channels, several chunks plus a tail
+    (2, 64, 384),        # config-1 slice
+])
+@pytest.mark.parametrize("mode", ["raw", "model"])
+def test_shapes_bf16_state16(N, T, Dn, mode):
+    """bf16 I/O with d_state 16 runs the matrix-core kernel (rank-1 input term split into two
+    exact bf16 halves).  The fp32 final state must match the oracle at the fp32 bar: the
+    only rounding that the bf16 path adds is the bf16 output."""
+    d = _inputs(N, T, Dn, 16, dtype=torch.bfloat16, seed=N * 100 + T + Dn,
+                dt_kind="ref_test" if mode == "model" else "softplus")
+    y, h = _run(d, mode, True, want_h=True)
+    ref, href = ssm_scan_ref(_np(d["x"]), _np(d["dt"]), _np(d["A_log"]), _np(d["B"]), _np(d["C"]),
+                             D=_np(d["D"]), clamp_mode=mode, return_h_final=True)
+    assert y.dtype == torch.bfloat16
+    assert normwise_rel_err(_np(h), href) <= FP32_TOL, "final state"
+    assert normwise_rel_err(_np(y), ref) <= 5e-3, "bf16 output: one rounding, at most 2^-8 relative"
+
+
+def test_bf16_state16_misaligned_pointer():
+    """x starting at an odd element: the pair-load kernel does not apply and the one-channel
+    form runs; results equal the aligned call bit for bit."""
+    from hclsm_amd import _lib
+    d = _inputs(2, 12, 64, 16, dtype=torch.bfloat16, seed=5)
+    dev = "cuda"
+    x, dt, A, B, C, D = (d[k].to(dev) for k in ("x", "dt", "A_log", "B", "C", "D"))
+    y0 = torch.empty_like(x)
+    y1 = torch.empty_like(x)
+    buf = torch.empty(x.numel() + 1, dtype=torch.bfloat16, device=dev)
+    buf[1:] = x.reshape(-1)
+    L = _lib.lib()
+    st = torch.cuda.current_stream().cuda_stream
+    for xp, yp in ((x.data_ptr(), y0), (buf.data_ptr() + 2, y1)):
+        _lib.check(L.hclsm_ssm_scan_fwd(xp, dt.data_ptr(), A.data_ptr(), B.data_ptr(), C.data_ptr(), D.data_ptr(),
+                                        yp.data_ptr(), None, 2, 12, 64, 16, _lib.BF16, _lib.SCAN_RAW, st),
+                   "hclsm_ssm_scan_fwd")
+    torch.cuda.synchronize()
+    assert torch.equal(y0, y1)
+    ref = ssm_scan_ref(_np(d["x"]), _np(d["dt"]), _np(d["A_log"]), _np(d["B"]), _np(d["C"]), D=_np(d["D"]),
+                       clamp_mode="raw")
+    assert normwise_rel_err(_np(y0), ref) <= 5e-3
