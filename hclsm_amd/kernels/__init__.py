@@ -65,6 +65,8 @@ def _hip_available() -> bool:
 
 HIP_AVAILABLE = _hip_available()
 
+from hclsm_amd.kernels import ops  # noqa: E402  registers the hclsm_hip:: torch.library ops
+
 __all__ = [
     "slot_attention_core",
     "slot_attention_fn",
@@ -96,4 +98,5 @@ __all__ = [
     "slots_attention",
     "TRITON_AVAILABLE",
     "HIP_AVAILABLE",
+    "ops",
 ]

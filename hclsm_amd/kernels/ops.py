@@ -1,0 +1,165 @@
+"""torch.library registration of the hot-path entry points (namespace ``hclsm_hip``).
+
+Each op calls the same C ABI as the eager functions of ``hclsm_amd.kernels`` and carries a fake
+kernel, so the ops propagate shapes under FakeTensorMode / torch.compile tracing and on ``meta``
+tensors.  The eager functions call the C ABI directly rather than through these ops: a custom op
+adds tens of microseconds of Python dispatch per call, which is the size of the kernels.
+
+    hclsm_hip::ssm_scan_fwd(x, dt, A_log, B, C, D?, mode, want_h) -> (y, h_final)
+        y in x.dtype; h_final (batch, d_inner, d_state) fp32, or shape (0,) when want_h is False
+        (ssm_scan_kernel.py:294-319 forward; mode 0 raw, 1 clamped model form)
+    hclsm_hip::ssm_scan_bwd(x, dt, A_log, B, C, D?, gy, mode) -> (gx, gdt, gA_log, gB, gC, gD)
+        gD has shape (0,) when D is None (ssm_scan_kernel.py:321-377)
+    hclsm_hip::slot_attn_core(Q, K, V, scale, denom_eps, logit_clamp, renorm_eps) -> (out, attn)
+        softmax over the slot axis; logit_clamp 0 = none, renorm_eps < 0 = none
+        (slot_attention_kernel.py:43-152, dynamic_slots.py:116-121)
+    hclsm_hip::event_index(mask, rule) -> (counts, offsets, indices, rows, slot_of, stats)
+        int32; rule 0 = mask > 0.5 (hierarchy_manager.py:61), 1 = nonzero (sparse_event_attn.py:64)
+    hclsm_hip::event_gather(states, counts, offsets, indices, K) -> (B, K, ...)
+        zero rows past each count (hierarchy_manager.py:66-75)
+    hclsm_hip::event_scatter(base, updates, slot_of) -> (B, T, ...)
+        (hierarchy_manager.py:103-116)
+    hclsm_hip::event_attention(q, k, v, offsets, indices, key_pad?, scale, mode, capacity) -> (capacity, H, dh)
+        mode 0 track-causal, 1 slots with key padding (level1_event.py:37-52)
+    hclsm_hip::slot_attention_forward(inputs, slots0, weights, n_iter, scale, logit_clamp, renorm_eps,
+                                      slot_clamp, compute_dtype) -> slots fp32
+        weights in the order of SLOT_WEIGHT_ORDER (dynamic_slots.py:98-164)
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from hclsm_amd.kernels.event_attention import event_attention as _event_attention
+from hclsm_amd.kernels.slot_attention_kernel import _core_raw
+from hclsm_amd.kernels.slot_iteration import SlotMode, SlotWeights, slot_attention_forward as _slot_forward
+from hclsm_amd.kernels.sparse_event_attn import EventIndex, _gather_padded_raw, _scatter_padded_raw, build_event_index
+from hclsm_amd.kernels.ssm_scan_bwd import scan_backward
+from hclsm_amd.kernels.ssm_scan_kernel import _scan_forward
+
+Tensor = torch.Tensor
+SLOT_WEIGHT_ORDER = ("w_q", "w_k", "w_v", "w_ih", "w_hh", "w1", "w2", "b_ih", "b_hh", "b1", "b2",
+                     "ln_pre_w", "ln_pre_b", "ln_mlp_w", "ln_mlp_b", "ln_in_w", "ln_in_b")
+_RULES = ("gt_half", "nonzero")
+_ATTN_MODES = ("track_causal", "slots")
+
+
+def _index_of(B, T, counts, offsets, indices, slot_of=None):
+    return EventIndex(B, T, counts, offsets, indices, None, slot_of, None)
+
+
+# --------------------------------------------------------------------------- scan
+
+@torch.library.custom_op("hclsm_hip::ssm_scan_fwd", mutates_args=())
+def ssm_scan_fwd(x: Tensor, dt: Tensor, A_log: Tensor, B: Tensor, C: Tensor, D: Optional[Tensor],
+                 mode: int, want_h: bool) -> tuple[Tensor, Tensor]:
+    y, h = _scan_forward(x, dt, A_log, B, C, D, int(mode), bool(want_h))
+    return y, (h if h is not None else x.new_empty((0,), dtype=torch.float32))
+
+
+@ssm_scan_fwd.register_fake
+def _(x, dt, A_log, B, C, D, mode, want_h):
+    h = x.new_empty((x.shape[0], x.shape[2], B.shape[2]) if want_h else (0,), dtype=torch.float32)
+    return torch.empty_like(x), h
+
+
+@torch.library.custom_op("hclsm_hip::ssm_scan_bwd", mutates_args=())
+def ssm_scan_bwd(x: Tensor, dt: Tensor, A_log: Tensor, B: Tensor, C: Tensor, D: Optional[Tensor], gy: Tensor,
+                 mode: int) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    g = scan_backward(x, dt, A_log, B, C, D, gy, int(mode))
+    gD = g.get("D")
+    return (g["x"], g["dt"], g["A_log"], g["B"], g["C"],
+            gD if gD is not None else x.new_empty((0,), dtype=torch.float32))
+
+
+@ssm_scan_bwd.register_fake
+def _(x, dt, A_log, B, C, D, gy, mode):
+    f32 = torch.float32
+    return (torch.empty_like(x), torch.empty_like(dt), torch.empty_like(A_log, dtype=f32), torch.empty_like(B),
+            torch.empty_like(C), x.new_empty((x.shape[2],) if D is not None else (0,), dtype=f32))
+
+
+# --------------------------------------------------------------------------- slot attention
+
+@torch.library.custom_op("hclsm_hip::slot_attn_core", mutates_args=())
+def slot_attn_core(Q: Tensor, K: Tensor, V: Tensor, scale: float, denom_eps: float, logit_clamp: float,
+                   renorm_eps: float) -> tuple[Tensor, Tensor]:
+    out, attn = _core_raw(Q, K, V, scale, denom_eps, logit_clamp=logit_clamp or None,
+                          renorm_eps=renorm_eps if renorm_eps >= 0 else None)
+    return out.to(Q.dtype), attn.to(Q.dtype)
+
+
+@slot_attn_core.register_fake
+def _(Q, K, V, scale, denom_eps, logit_clamp, renorm_eps):
+    return torch.empty_like(Q), Q.new_empty((Q.shape[0], Q.shape[1], K.shape[1]))
+
+
+@torch.library.custom_op("hclsm_hip::slot_attention_forward", mutates_args=())
+def slot_attention_forward(inputs: Tensor, slots0: Tensor, weights: list[Tensor], n_iter: int, scale: float,
+                           logit_clamp: float, renorm_eps: float, slot_clamp: float,
+                           compute_dtype: torch.dtype) -> Tensor:
+    if len(weights) != len(SLOT_WEIGHT_ORDER):
+        raise ValueError(f"expected {len(SLOT_WEIGHT_ORDER)} weights in the order {SLOT_WEIGHT_ORDER}")
+    W = SlotWeights.from_dict(dict(zip(SLOT_WEIGHT_ORDER, weights)), compute_dtype, inputs.device)
+    mode = SlotMode(logit_clamp=logit_clamp or None, renorm_eps=renorm_eps if renorm_eps >= 0 else None,
+                    slot_clamp=slot_clamp or None)
+    return _slot_forward(inputs, slots0, W, int(n_iter), mode, scale=scale)
+
+
+@slot_attention_forward.register_fake
+def _(inputs, slots0, weights, n_iter, scale, logit_clamp, renorm_eps, slot_clamp, compute_dtype):
+    return torch.empty_like(slots0, dtype=torch.float32)
+
+
+# --------------------------------------------------------------------------- events
+
+@torch.library.custom_op("hclsm_hip::event_index", mutates_args=())
+def event_index(mask: Tensor, rule: int) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    idx = build_event_index(mask, _RULES[rule])
+    return idx.counts, idx.offsets, idx.indices, idx.rows, idx.slot_of, idx.stats
+
+
+@event_index.register_fake
+def _(mask, rule):
+    B, T = mask.shape
+    i32 = dict(dtype=torch.int32, device=mask.device)
+    n = max(B * T, 1)
+    return (torch.empty(B, **i32), torch.empty(B + 1, **i32), torch.empty(n, **i32), torch.empty(n, **i32),
+            torch.empty((B, T), **i32), torch.empty(2, **i32))
+
+
+@torch.library.custom_op("hclsm_hip::event_gather", mutates_args=())
+def event_gather(states: Tensor, counts: Tensor, offsets: Tensor, indices: Tensor, K: int) -> Tensor:
+    return _gather_padded_raw(states, _index_of(states.shape[0], states.shape[1], counts, offsets, indices), int(K))
+
+
+@event_gather.register_fake
+def _(states, counts, offsets, indices, K):
+    return states.new_empty((states.shape[0], K) + tuple(states.shape[2:]))
+
+
+@torch.library.custom_op("hclsm_hip::event_scatter", mutates_args=())
+def event_scatter(base: Tensor, updates: Tensor, slot_of: Tensor) -> Tensor:
+    B, T = slot_of.shape
+    idx = _index_of(B, T, None, None, None, slot_of)
+    return _scatter_padded_raw(base, updates.to(base.dtype), idx, updates.shape[1], base)
+
+
+@event_scatter.register_fake
+def _(base, updates, slot_of):
+    return torch.empty_like(base)
+
+
+@torch.library.custom_op("hclsm_hip::event_attention", mutates_args=())
+def event_attention(q: Tensor, k: Tensor, v: Tensor, offsets: Tensor, indices: Tensor, key_pad: Optional[Tensor],
+                    scale: float, mode: int, capacity: int) -> Tensor:
+    idx = _index_of(q.shape[0], q.shape[1], None, offsets, indices)
+    return _event_attention(q, k, v, idx, _ATTN_MODES[mode], scale=scale, key_pad=key_pad, out="packed",
+                            capacity=int(capacity))
+
+
+@event_attention.register_fake
+def _(q, k, v, offsets, indices, key_pad, scale, mode, capacity):
+    return q.new_empty((capacity, q.shape[2], q.shape[3]))

@@ -124,9 +124,11 @@ _WS_CACHE: dict = {}
 
 
 def _workspace(nbytes: int, device) -> torch.Tensor:
-    """A cached uint8 device buffer of at least nbytes (one per device; grown on demand).  Calls that
-    share it run in stream order on the current stream."""
-    key = str(device)
+    """A cached uint8 device buffer of at least nbytes, one per (device, current stream), grown on
+    demand.  Every call that uses a buffer is enqueued on the stream it is keyed by, so the calls
+    that share it are ordered by that stream; torch's allocator recycles a replaced buffer only
+    after the work queued on that stream."""
+    key = (str(device), torch.cuda.current_stream(device).cuda_stream)
     buf = _WS_CACHE.get(key)
     if buf is None or buf.numel() < nbytes:
         buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)

@@ -1,0 +1,71 @@
+"""torch.library ops (namespace hclsm_hip) on the GPU: each op returns what the eager function
+of hclsm_amd.kernels returns (same kernels, bit for bit) and passes torch.library.opcheck's
+schema and fake-tensor checks."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import hclsm_amd.kernels.ops as hops
+
+pytestmark = pytest.mark.gpu
+OPS = torch.ops.hclsm_hip
+
+
+def test_scan_ops_equal_eager():
+    from hclsm_amd.kernels import ssm_scan_fn
+    from hclsm_amd.kernels.ssm_scan_bwd import scan_backward
+    from hclsm_amd.workloads import scan_inputs
+    d = {k: v.cuda() for k, v in scan_inputs(3, 20, 64, 16, dtype=torch.bfloat16, seed=2).items()}
+    args = (d["x"], d["dt"], d["A_log"], d["B"], d["C"])
+    y, h = OPS.ssm_scan_fwd(*args, d["D"], 0, True)
+    ye, he = ssm_scan_fn(*args, backend="hip", D=d["D"], return_h_final=True)
+    assert torch.equal(y, ye) and torch.equal(h, he)
+    gy = torch.randn_like(y)
+    g = OPS.ssm_scan_bwd(*args, d["D"], gy, 1)
+    ge = scan_backward(*args, d["D"], gy, 1)
+    for t, n in zip(g, ("x", "dt", "A_log", "B", "C", "D")):
+        assert torch.equal(t, ge[n]), n
+    torch.library.opcheck(OPS.ssm_scan_fwd.default, (*args, d["D"], 0, True), test_utils=("test_schema", "test_faketensor"))
+
+
+def test_event_ops_equal_eager():
+    from hclsm_amd.kernels.event_attention import event_attention
+    from hclsm_amd.kernels.sparse_event_attn import build_event_index, gather_events_padded, scatter_events_padded
+    g = torch.Generator().manual_seed(4)
+    m = (torch.rand(6, 21, generator=g) < 0.3).float().cuda()
+    idx = build_event_index(m)
+    t = OPS.event_index(m, 0)
+    n = idx.total()
+    for a, b in zip(t, (idx.counts, idx.offsets, idx.indices[:n], idx.rows[:n], idx.slot_of, idx.stats)):
+        assert torch.equal(a[: b.numel()] if a.dim() == 1 else a, b)   # entries past the total are unused
+    K = max(idx.kmax(), 1)
+    st = torch.randn(6, 21, 3, 8, generator=g).cuda()
+    gp = OPS.event_gather(st, t[0], t[1], t[2], K)
+    assert torch.equal(gp, gather_events_padded(st, idx, K))
+    upd = torch.randn(6, K, 3, 8, generator=g).cuda()
+    assert torch.equal(OPS.event_scatter(st, upd, t[4]), scatter_events_padded(st, upd, idx))
+    q, k, v = (torch.randn(6, 21, 2, 32, generator=g).to(torch.bfloat16).cuda() for _ in range(3))
+    tot = idx.total()
+    o = OPS.event_attention(q, k, v, t[1], t[2], None, 32 ** -0.5, 0, tot)
+    assert torch.equal(o, event_attention(q, k, v, idx, capacity=tot))
+    torch.library.opcheck(OPS.event_gather.default, (st, t[0], t[1], t[2], K), test_utils=("test_schema", "test_faketensor"))
+
+
+def test_slot_ops_equal_eager():
+    from hclsm_amd.kernels import naive_slot_attention
+    from hclsm_amd.kernels import slot_iteration as si
+    from hclsm_amd.workloads import slot_config
+    g = torch.Generator().manual_seed(6)
+    Q, K, V = (torch.randn(s, generator=g).cuda() for s in ((2, 8, 64), (2, 40, 64), (2, 40, 64)))
+    out, attn = OPS.slot_attn_core(Q, K, V, 0.125, 0.0, 0.0, -1.0)
+    oe, ae = naive_slot_attention(Q, K, V, scale=0.125)
+    assert torch.equal(out, oe) and torch.equal(attn, ae)
+    tokens, slots0, w = slot_config(B=2)
+    ws = [w[n].cuda() for n in hops.SLOT_WEIGHT_ORDER]
+    s = OPS.slot_attention_forward(tokens.cuda(), slots0.cuda(), ws, 3, 384 ** -0.5, 0.0, 1e-8, 0.0, torch.bfloat16)
+    W = si.SlotWeights.from_dict(w, torch.bfloat16)
+    assert torch.equal(s, si.slot_attention_forward(tokens.cuda(), slots0.cuda(), W, 3, si.CONFIG2_MODE))
+    torch.library.opcheck(OPS.slot_attn_core.default, (Q, K, V, 0.125, 0.0, 0.0, -1.0),
+                          test_utils=("test_schema", "test_faketensor"))
