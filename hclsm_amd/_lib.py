@@ -118,5 +118,11 @@ def dtype_code(dt: torch.dtype) -> int:
     raise TypeError(f"hclsm_amd kernels take float32/bfloat16/float16 tensors, got {dt}")
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(t: torch.Tensor) -> int:
+    """hipStream_t of torch's current stream on t's device."""
+    if _raw_stream is not None:
+        return _raw_stream(t.get_device())
     return torch.cuda.current_stream(t.device).cuda_stream

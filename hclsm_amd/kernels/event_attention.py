@@ -71,7 +71,7 @@ def event_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, index: Ev
         raise ValueError(f"out must be 'packed' or 'grid', got {out!r}")
     rc = _lib.lib().hclsm_event_attention(
         _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), _lib.ptr(outp), _lib.ptr(outg),
-        _lib.ptr(index.offsets), _lib.ptr(index.indices), _lib.ptr(kp), P, T, H, dh, max(cap, 0), float(scale),
+        index.ptr("offsets"), index.ptr("indices"), _lib.ptr(kp), P, T, H, dh, max(cap, 0), float(scale),
         _lib.dtype_code(q.dtype), _MODES[mode], _lib.stream_of(qc))
     _lib.check(rc, "hclsm_event_attention")
     return result

@@ -32,17 +32,18 @@ from typing import Optional
 
 import torch
 
+from hclsm_amd import _lib
+from hclsm_amd.kernels._common import require_gpu
 from hclsm_amd.kernels.event_attention import event_attention as _event_attention
 from hclsm_amd.kernels.slot_attention_kernel import _core_raw
 from hclsm_amd.kernels.slot_iteration import SlotMode, SlotWeights, slot_attention_forward as _slot_forward
-from hclsm_amd.kernels.sparse_event_attn import EventIndex, _gather_padded_raw, _scatter_padded_raw, build_event_index
+from hclsm_amd.kernels.sparse_event_attn import EventIndex, _gather_padded_raw, _mask_code, _scatter_padded_raw
 from hclsm_amd.kernels.ssm_scan_bwd import scan_backward
 from hclsm_amd.kernels.ssm_scan_kernel import _scan_forward
 
 Tensor = torch.Tensor
 SLOT_WEIGHT_ORDER = ("w_q", "w_k", "w_v", "w_ih", "w_hh", "w1", "w2", "b_ih", "b_hh", "b1", "b2",
                      "ln_pre_w", "ln_pre_b", "ln_mlp_w", "ln_mlp_b", "ln_in_w", "ln_in_b")
-_RULES = ("gt_half", "nonzero")
 _ATTN_MODES = ("track_causal", "slots")
 
 
@@ -117,8 +118,21 @@ def _(inputs, slots0, weights, n_iter, scale, logit_clamp, renorm_eps, slot_clam
 
 @torch.library.custom_op("hclsm_hip::event_index", mutates_args=())
 def event_index(mask: Tensor, rule: int) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
-    idx = build_event_index(mask, _RULES[rule])
-    return idx.counts, idx.offsets, idx.indices, idx.rows, idx.slot_of, idx.stats
+    # separate allocations: a custom op's outputs may not alias each other (the eager
+    # build_event_index carves all six tables out of one buffer)
+    require_gpu("event_index", mask)
+    if mask.dim() != 2:
+        raise ValueError(f"event_mask must be (B, T), got {tuple(mask.shape)}")
+    m, code = _mask_code(mask.detach().contiguous())
+    B, T = m.shape
+    i32 = dict(dtype=torch.int32, device=m.device)
+    cap = max(B * T, 1)
+    t = (torch.empty(B, **i32), torch.empty(B + 1, **i32), torch.empty(cap, **i32), torch.empty(cap, **i32),
+         torch.empty((B, T), **i32), torch.empty(2, **i32))
+    rc = _lib.lib().hclsm_event_index(_lib.ptr(m), code, B, T, (_lib.EVENT_GT_HALF, _lib.EVENT_NONZERO)[rule],
+                                      *(_lib.ptr(x) for x in t), _lib.stream_of(m))
+    _lib.check(rc, "hclsm_event_index")
+    return t
 
 
 @event_index.register_fake

@@ -27,7 +27,6 @@ work on device-side int32 tables and never read a size back to the host.
 
 from __future__ import annotations
 
-from dataclasses import dataclass
 from typing import Callable
 
 import torch
@@ -36,17 +35,64 @@ from hclsm_amd import _lib
 from hclsm_amd.kernels._common import require_gpu
 
 
-@dataclass
 class EventIndex:
-    """Device-side event tables of a (B, T) mask (all int32, built without host sync)."""
-    B: int
-    T: int
-    counts: torch.Tensor      # (B,)
-    offsets: torch.Tensor     # (B+1,)   exclusive prefix sum; offsets[B] = total
-    indices: torch.Tensor     # (B*T,)   capacity; first `total` are event timesteps
-    rows: torch.Tensor        # (B*T,)   capacity; row of each packed event
-    slot_of: torch.Tensor     # (B, T)   rank of t among row b's events, -1 otherwise
-    stats: torch.Tensor       # (2,)     {total, max count}
+    """Device-side event tables of a (B, T) mask (all int32, built without host sync):
+
+        counts  (B,)     events per row
+        offsets (B+1,)   exclusive prefix sum; offsets[B] = total
+        indices (B*T,)   capacity; the first `total` entries are event timesteps, ascending per row
+        rows    (B*T,)   capacity; row of each packed event
+        slot_of (B, T)   rank of t among row b's events, -1 otherwise
+        stats   (2,)     {total, max count}
+
+    Built by build_event_index, the six tables live in one allocation; launches take raw
+    pointers into it (``ptr``) and tensor views are made only when a caller asks for one."""
+
+    _NAMES = ("stats", "counts", "offsets", "indices", "rows", "slot_of")
+
+    def __init__(self, B: int, T: int, counts=None, offsets=None, indices=None, rows=None, slot_of=None,
+                 stats=None):
+        self.B, self.T = B, T
+        self._t = dict(counts=counts, offsets=offsets, indices=indices, rows=rows, slot_of=slot_of, stats=stats)
+        self._buf = None
+        self._off: dict = {}
+
+    @classmethod
+    def allocate(cls, B: int, T: int, device) -> "EventIndex":
+        cap = max(B * T, 1)
+        sizes = dict(stats=2, counts=B, offsets=B + 1, indices=cap, rows=cap, slot_of=B * T)
+        idx = cls(B, T)
+        o = 0
+        for n in cls._NAMES:
+            idx._off[n] = (o, sizes[n])
+            o += sizes[n]
+        idx._buf = torch.empty(o, dtype=torch.int32, device=device)
+        idx._base = idx._buf.data_ptr()
+        return idx
+
+    def ptr(self, name: str):
+        """Device address of a table (None if absent)."""
+        if self._buf is not None:
+            return self._base + 4 * self._off[name][0]
+        t = self._t[name]
+        return None if t is None else t.data_ptr()
+
+    def _get(self, name: str):
+        t = self._t[name]
+        if t is None and self._buf is not None:
+            o, n = self._off[name]
+            t = self._buf[o:o + n]
+            if name == "slot_of":
+                t = t.view(self.B, self.T)
+            self._t[name] = t
+        return t
+
+    counts = property(lambda self: self._get("counts"))
+    offsets = property(lambda self: self._get("offsets"))
+    indices = property(lambda self: self._get("indices"))
+    rows = property(lambda self: self._get("rows"))
+    slot_of = property(lambda self: self._get("slot_of"))
+    stats = property(lambda self: self._get("stats"))
 
     def total(self) -> int:
         """Number of events (reads one int32 back to the host)."""
@@ -76,13 +122,10 @@ def build_event_index(event_mask: torch.Tensor, rule: str = "gt_half") -> EventI
     rule_code = {"gt_half": _lib.EVENT_GT_HALF, "nonzero": _lib.EVENT_NONZERO}[rule]
     m, code = _mask_code(event_mask.detach().contiguous())
     B, T = m.shape
-    dev = m.device
-    i32 = dict(dtype=torch.int32, device=dev)
-    idx = EventIndex(B, T, torch.empty(B, **i32), torch.empty(B + 1, **i32), torch.empty(max(B * T, 1), **i32),
-                     torch.empty(max(B * T, 1), **i32), torch.empty((B, T), **i32), torch.empty(2, **i32))
-    rc = _lib.lib().hclsm_event_index(_lib.ptr(m), code, B, T, rule_code, _lib.ptr(idx.counts), _lib.ptr(idx.offsets),
-                                      _lib.ptr(idx.indices), _lib.ptr(idx.rows), _lib.ptr(idx.slot_of),
-                                      _lib.ptr(idx.stats), _lib.stream_of(m))
+    idx = EventIndex.allocate(B, T, m.device)
+    p = idx.ptr
+    rc = _lib.lib().hclsm_event_index(m.data_ptr(), code, B, T, rule_code, p("counts"), p("offsets"), p("indices"),
+                                      p("rows"), p("slot_of"), p("stats"), _lib.stream_of(m))
     _lib.check(rc, "hclsm_event_index")
     return idx
 
@@ -98,8 +141,7 @@ def _gather_padded_raw(states: torch.Tensor, idx: EventIndex, K: int) -> torch.T
     src = states.contiguous()
     out = torch.empty((src.shape[0], K) + tuple(src.shape[2:]), dtype=src.dtype, device=src.device)
     rc = _lib.lib().hclsm_event_gather(_lib.ptr(src), _lib.ptr(out), _row_bytes(src), idx.B, idx.T, K,
-                                       _lib.ptr(idx.counts), _lib.ptr(idx.offsets), _lib.ptr(idx.indices),
-                                       _lib.stream_of(src))
+                                       idx.ptr("counts"), idx.ptr("offsets"), idx.ptr("indices"), _lib.stream_of(src))
     _lib.check(rc, "hclsm_event_gather")
     return out
 
@@ -109,7 +151,7 @@ def _scatter_padded_raw(base, updates, idx: EventIndex, K: int, like: torch.Tens
     u = None if updates is None else updates.contiguous()
     out = torch.empty((idx.B, idx.T) + tuple(like.shape[2:]), dtype=like.dtype, device=like.device)
     rc = _lib.lib().hclsm_event_scatter(_lib.ptr(b), _lib.ptr(u), _lib.ptr(out), _row_bytes(out), idx.B, idx.T, K,
-                                        _lib.ptr(idx.slot_of), _lib.stream_of(out))
+                                        idx.ptr("slot_of"), _lib.stream_of(out))
     _lib.check(rc, "hclsm_event_scatter")
     return out
 
@@ -168,7 +210,7 @@ def gather_packed(src: torch.Tensor, idx: EventIndex, capacity: int | None = Non
     cap = idx.B * idx.T if capacity is None else int(capacity)
     out = torch.empty((cap,) + tuple(s.shape[2:]), dtype=s.dtype, device=s.device)
     rc = _lib.lib().hclsm_event_gather_packed(_lib.ptr(s), _lib.ptr(out), _row_bytes(s), idx.B, idx.T, cap,
-                                              _lib.ptr(idx.rows), _lib.ptr(idx.indices), _lib.ptr(idx.stats),
+                                              idx.ptr("rows"), idx.ptr("indices"), idx.ptr("stats"),
                                               _lib.stream_of(s))
     _lib.check(rc, "hclsm_event_gather_packed")
     return out
@@ -187,7 +229,7 @@ def scatter_packed(base: torch.Tensor | None, packed: torch.Tensor, idx: EventIn
     for s in out.shape[2:]:
         rb *= s
     rc = _lib.lib().hclsm_event_scatter_packed(_lib.ptr(b), _lib.ptr(p), _lib.ptr(out), rb, idx.B, idx.T,
-                                               _lib.ptr(idx.offsets), _lib.ptr(idx.slot_of), _lib.stream_of(p))
+                                               idx.ptr("offsets"), idx.ptr("slot_of"), _lib.stream_of(p))
     _lib.check(rc, "hclsm_event_scatter_packed")
     return out
 

@@ -213,3 +213,19 @@ def test_bf16_state16_misaligned_pointer():
     ref = ssm_scan_ref(_np(d["x"]), _np(d["dt"]), _np(d["A_log"]), _np(d["B"]), _np(d["C"]), D=_np(d["D"]),
                        clamp_mode="raw")
     assert normwise_rel_err(_np(y0), ref) <= 5e-3
+
+
+def test_launch_on_current_side_stream():
+    """Launches go to torch's current stream: on a side stream the result is ordered by that stream."""
+    from hclsm_amd import _lib
+    from hclsm_amd.kernels import ssm_scan_fn
+    d = _inputs(4, 16, 64, 16, dtype=torch.bfloat16, seed=21)
+    side = torch.cuda.Stream()
+    args = [d[k].cuda() for k in ("x", "dt", "A_log", "B", "C")]
+    torch.cuda.synchronize()
+    with torch.cuda.stream(side):
+        assert _lib.stream_of(args[0]) == side.cuda_stream
+        y = ssm_scan_fn(*args, backend="hip")
+    side.synchronize()
+    ref = ssm_scan_ref(*(_np(d[k]) for k in ("x", "dt", "A_log", "B", "C")), clamp_mode="raw")
+    assert normwise_rel_err(_np(y), ref) <= 5e-3
