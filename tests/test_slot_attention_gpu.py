@@ -157,3 +157,32 @@ def test_config2_forward_bf16():
                                     logit_clamp=None, renorm_eps=1e-8, slot_clamp=None)
     err = normwise_rel_err(_np(out), ref)
     assert err <= 2e-2, f"config 2 normwise err {err:.3e}"
+
+
+@pytest.mark.parametrize("mode_name,dtype,B,N,M,d,d_in,hidden", [
+    ("reference", torch.bfloat16, 3, 7, 50, 128, 96, 512),     # partial slot tile, logit / slot clamps
+    ("config2", torch.bfloat16, 2, 64, 197, 256, 128, 256),    # 64 slots (four row tiles), M not a multiple of 32
+    ("reference", torch.float16, 2, 16, 33, 64, 64, 256),
+    ("config2", torch.float16, 4, 32, 196, 128, 160, 384),
+])
+def test_forward_two_launch_iteration_matches_oracle(mode_name, dtype, B, N, M, d, d_in, hidden):
+    """hclsm_slot_attention_forward with 16-bit operands runs each iteration as two launches
+    (attention block per frame, GRU + MLP block per 16 rows); result against the oracle."""
+    from hclsm_amd.kernels import slot_iteration as si
+    from hclsm_amd.workloads import xavier_uniform
+    g = torch.Generator().manual_seed(B * 100 + N + M)
+    w = _weights(d, hidden, seed=B + N)
+    w["w_k"] = xavier_uniform((d, d_in), g)
+    w["w_v"] = xavier_uniform((d, d_in), g)
+    w["ln_in_w"] = torch.rand(d_in, generator=g) + 0.5
+    w["ln_in_b"] = torch.randn(d_in, generator=g) * 0.1
+    w = {n: t.to(dtype).float() if n in si._WEIGHT_KEYS else t for n, t in w.items()}
+    W = si.SlotWeights.from_dict(w, dtype)
+    tokens = torch.randn(B, M, d_in, generator=g)
+    slots0 = torch.randn(B, N, d, generator=g) * 0.5
+    mode = si.REFERENCE_MODE if mode_name == "reference" else si.CONFIG2_MODE
+    out = si.slot_attention_forward(tokens.cuda(), slots0.cuda(), W, 3, mode)
+    ref = sa.slot_attention_forward(tokens.numpy(), slots0.numpy(), {n: _np(t) for n, t in w.items()}, 3,
+                                    logit_clamp=mode.logit_clamp, renorm_eps=mode.renorm_eps, slot_clamp=mode.slot_clamp)
+    err = normwise_rel_err(_np(out), ref)
+    assert err <= 2e-2, f"{mode_name} {dtype}: {err:.3e}"
