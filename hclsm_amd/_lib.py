@@ -30,6 +30,7 @@ _SIGNATURES: dict[str, list] = {
     "hclsm_abi_version": [],
     "hclsm_strerror": [_int],
     "hclsm_ssm_scan_fwd": [_c_void_p] * 8 + [_i64] * 4 + [_int, _int, _c_void_p],
+    "hclsm_ssm_block_scan_fwd": [_c_void_p] * 9 + [_i64] * 4 + [_int, _c_void_p],
     "hclsm_ssm_scan_bwd_workspace": [_i64, _i64, _i64, _i64],
     "hclsm_ssm_scan_bwd": [_c_void_p] * 13 + [_i64] * 4 + [_int, _int, _c_void_p, _i64, _c_void_p],
     "hclsm_event_index": [_c_void_p, _int, _i64, _i64, _int] + [_c_void_p] * 6 + [_c_void_p],

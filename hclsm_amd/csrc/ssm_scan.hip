@@ -19,6 +19,35 @@
 
 namespace hclsm {
 
+// Internal mode of hclsm_ssm_block_scan_fwd: the MODEL clamps, dt = softplus(dt input) before
+// its clamp, and the output multiplied by silu(gate) -- the SimplifiedSSMBlock epilogues
+// (level0_ssm.py:73, :76, :103) fused into the scan.
+constexpr int SCAN_BLOCK = 2;
+struct ScanEpi {
+  const void* gate;   // [batch][T][d_inner], I/O type; required in SCAN_BLOCK
+  void* y_pre;        // optional: the scan output before gating (kept for the backward)
+};
+
+// softplus(v) = max(v, 0) + log1p(exp(-|v|)), torch's threshold 20 kept.  log1p(e) for e in (0, 1] as
+// log(u) * e / (u - 1) with u = 1 + e (the rounding of u cancels to first order; e / (u - 1) = 1
+// when u rounds to 1).
+__device__ __forceinline__ float softplus_f(float v) {
+  const float e = __expf(-fabsf(v));
+  const float u = 1.f + e;
+  const float d = u - 1.f;
+  const float l = d == 0.f ? e : __logf(u) * (e * __builtin_amdgcn_rcpf(d));
+  return v > 20.f ? v : fmaxf(v, 0.f) + l;
+}
+
+template <int MODE>
+__device__ __forceinline__ float scan_dt(float v) {
+  if constexpr (MODE == SCAN_BLOCK) v = softplus_f(v);
+  if constexpr (MODE != HCLSM_SCAN_RAW) v = fminf(fmaxf(v, 1e-3f), 1.0f);
+  return v;
+}
+
+__device__ __forceinline__ float silu_f(float g) { return g * __builtin_amdgcn_rcpf(1.f + __expf(-g)); }
+
 constexpr int SCAN_TCHUNK = 8;
 constexpr int SCAN_MAX_BLOCK = 256;
 
@@ -32,7 +61,7 @@ ssm_scan_fwd_kernel(const typename Elem<DT>::T* __restrict__ x,
                     const float* __restrict__ Dskip,
                     typename Elem<DT>::T* __restrict__ y,
                     float* __restrict__ h_final,
-                    int T, int Dn, int S) {
+                    int T, int Dn, int S, ScanEpi epi) {
   using E = Elem<DT>;
   using TT = typename E::T;
   constexpr int TC = SCAN_TCHUNK;
@@ -53,7 +82,7 @@ ssm_scan_fwd_kernel(const typename Elem<DT>::T* __restrict__ x,
     {
       // unconditional load of a valid element, then select: no divergent branch
       float e = expf(A_log[(size_t)dd * S + (s < S ? s : S - 1)]);
-      if (MODE == HCLSM_SCAN_MODEL) e = fminf(fmaxf(e, 1e-6f), 1.0f);
+      if (MODE != HCLSM_SCAN_RAW) e = fminf(fmaxf(e, 1e-6f), 1.0f);
       a = (s < S) ? -e * HCLSM_LOG2E : 0.f;
     }
     a2[s] = a;
@@ -112,9 +141,18 @@ ssm_scan_fwd_kernel(const typename Elem<DT>::T* __restrict__ x,
     }
   };
 
+  auto store_y = [&](int t, float yv) {
+    if constexpr (MODE == SCAN_BLOCK) {
+      const size_t o = row0 * Dn + dd + (size_t)t * Dn;
+      if (epi.y_pre) E::st(reinterpret_cast<TT*>(epi.y_pre) + o, yv);
+      yv *= silu_f(E::ld(reinterpret_cast<const TT*>(epi.gate) + o));
+    }
+    E::st(yp + (size_t)t * Dn, yv);
+  };
+
   auto step = [&](int buf, int j, float xval, float dval) -> float {
     float dtv = dval;
-    if (MODE == HCLSM_SCAN_MODEL) dtv = fminf(fmaxf(dtv, 1e-3f), 1.0f);
+    dtv = scan_dt<MODE>(dtv);
     // In MODEL mode |dt*A| <= 1*1 < 20, so the clamp of dt*A to [-20, 0]
     // (ssm_scan_kernel.py:77) can never bind and is not applied.
     const float u = dtv * xval;
@@ -157,7 +195,7 @@ ssm_scan_fwd_kernel(const typename Elem<DT>::T* __restrict__ x,
 #pragma unroll
       for (int j = 0; j < TC; ++j) {
         const float yv = step(buf, j, xv[j], dv[j]);
-        if (act) E::st(yp + (size_t)(t0 + j) * Dn, yv);
+        if (act) store_y(t0 + j, yv);
       }
     } else {
       for (int j = 0; j < T - t0; ++j) {
@@ -165,7 +203,7 @@ ssm_scan_fwd_kernel(const typename Elem<DT>::T* __restrict__ x,
 #pragma unroll
         for (int k = 0; k < TC; ++k) if (k == j) { xj = xv[k]; dj = dv[k]; }
         const float yv = step(buf, j, xj, dj);
-        if (act) E::st(yp + (size_t)(t0 + j) * Dn, yv);
+        if (act) store_y(t0 + j, yv);
       }
     }
     if (more) {
@@ -203,7 +241,7 @@ ssm_scan_fwd_sgpr_kernel(const typename Elem<DT>::T* __restrict__ x,
                          const float* __restrict__ Dskip,
                          typename Elem<DT>::T* __restrict__ y,
                          float* __restrict__ h_final,
-                         int T, int Dn) {
+                         int T, int Dn, ScanEpi epi) {
   using E = Elem<DT>;
   using TT = typename E::T;
   constexpr int NW = SP * (int)sizeof(TT) / 4;  // 32-bit words per B/C row
@@ -220,7 +258,7 @@ ssm_scan_fwd_sgpr_kernel(const typename Elem<DT>::T* __restrict__ x,
 #pragma unroll
     for (int s = 0; s < SP; ++s) {
       float e = expf(A_log[(size_t)(d0 + k) * SP + s]);
-      if (MODE == HCLSM_SCAN_MODEL) e = fminf(fmaxf(e, 1e-6f), 1.0f);
+      if (MODE != HCLSM_SCAN_RAW) e = fminf(fmaxf(e, 1e-6f), 1.0f);
       a2[k][s] = -e * HCLSM_LOG2E;
     }
   const bool has_d = Dskip != nullptr;
@@ -305,7 +343,7 @@ ssm_scan_fwd_sgpr_kernel(const typename Elem<DT>::T* __restrict__ x,
 #pragma unroll
     for (int k = 0; k < DPL; ++k) {
       float dtv = ds[k];
-      if (MODE == HCLSM_SCAN_MODEL) dtv = fminf(fmaxf(dtv, 1e-3f), 1.0f);
+      dtv = scan_dt<MODE>(dtv);
       // MODEL mode: |dt*A| <= 1 < 20, so the [-20, 0] clamp of ssm_scan_kernel.py:77 never binds.
       const float u = dtv * xs[k];
       float y0 = 0.f, y1 = 0.f;
@@ -318,6 +356,14 @@ ssm_scan_fwd_sgpr_kernel(const typename Elem<DT>::T* __restrict__ x,
       float yv = y0 + y1;
       if (has_d) yv = fmaf(dsk[k], xs[k], yv);
       yo[k] = yv;
+    }
+    if constexpr (MODE == SCAN_BLOCK) {
+      const size_t o = row0 * Dn + d0 + (size_t)t * Dn;
+      if (epi.y_pre && act) st_pair(reinterpret_cast<TT*>(epi.y_pre) + o, yo);
+      float gv[DPL];
+      ld_pair(reinterpret_cast<const TT*>(epi.gate) + o, gv);
+#pragma unroll
+      for (int k = 0; k < DPL; ++k) yo[k] *= silu_f(gv[k]);
     }
     if (act) st_pair(yp + (size_t)t * Dn, yo);
 #pragma unroll
@@ -354,13 +400,13 @@ ssm_scan_fwd_sgpr_kernel(const typename Elem<DT>::T* __restrict__ x,
 template <int DT, int SP, int MODE, int DPL, int TC>
 static int launch_scan_sgpr(const void* x, const void* dt, const float* A_log, const void* B,
                             const void* C, const float* Dskip, void* y, float* h_final,
-                            int64_t batch, int64_t T, int64_t Dn, hipStream_t st) {
+                            int64_t batch, int64_t T, int64_t Dn, hipStream_t st, ScanEpi epi) {
   using TT = typename Elem<DT>::T;
   const int64_t lanes = (Dn + DPL - 1) / DPL;
   dim3 grid((unsigned)batch, (unsigned)((lanes + 63) / 64));
   hipLaunchKernelGGL((ssm_scan_fwd_sgpr_kernel<DT, SP, MODE, DPL, TC>), grid, dim3(64), 0, st,
                      (const TT*)x, (const TT*)dt, A_log, (const TT*)B, (const TT*)C, Dskip,
-                     (TT*)y, h_final, (int)T, (int)Dn);
+                     (TT*)y, h_final, (int)T, (int)Dn, epi);
   HCLSM_LAUNCH_CHECK();
   return 0;
 }
@@ -401,7 +447,7 @@ __global__ void __launch_bounds__(64)
 ssm_scan_fwd_mfma_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ dt,
                          const float* __restrict__ A_log, const uint16_t* __restrict__ Bm,
                          const uint16_t* __restrict__ Cm, const float* __restrict__ Dskip,
-                         uint16_t* __restrict__ y, float* __restrict__ h_final, int T, int Dn) {
+                         uint16_t* __restrict__ y, float* __restrict__ h_final, int T, int Dn, ScanEpi epi) {
   constexpr int SP = 16;
   const int n = blockIdx.x;
   const int l = threadIdx.x;
@@ -419,7 +465,7 @@ ssm_scan_fwd_mfma_kernel(const uint16_t* __restrict__ x, const uint16_t* __restr
 #pragma unroll
     for (int s = 0; s < SP; ++s) {
       float e = expf(A_log[(size_t)(d0 + k) * SP + s]);
-      if (MODE == HCLSM_SCAN_MODEL) e = fminf(fmaxf(e, 1e-6f), 1.0f);
+      if (MODE != HCLSM_SCAN_RAW) e = fminf(fmaxf(e, 1e-6f), 1.0f);
       a2[k][s] = -e * HCLSM_LOG2E;
     }
     dsk[k] = Dskip != nullptr ? Dskip[d0 + k] : 0.f;
@@ -438,24 +484,35 @@ ssm_scan_fwd_mfma_kernel(const uint16_t* __restrict__ x, const uint16_t* __restr
   const auto rd = __builtin_amdgcn_make_buffer_rsrc((void*)(dt + row0 * Dn), 0, slab, kRawBufferWord3);
   const auto ry = __builtin_amdgcn_make_buffer_rsrc((void*)(y + row0 * Dn), 0, slab, kRawBufferWord3);
   const auto rb = __builtin_amdgcn_make_buffer_rsrc((void*)(Bm + row0 * SP), 0, T * SP * 2, kRawBufferWord3);
+  // SCAN_BLOCK: gate read like x; the optional pre-gate output through a resource of 0 records when
+  // it is not wanted, so its stores are dropped without a branch
+  const auto rg = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(MODE == SCAN_BLOCK ? reinterpret_cast<const uint16_t*>(epi.gate) + row0 * Dn : x + row0 * Dn), 0, slab,
+      kRawBufferWord3);
+  const auto rp = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(epi.y_pre ? reinterpret_cast<uint16_t*>(epi.y_pre) + row0 * Dn : y + row0 * Dn), 0,
+      epi.y_pre ? slab : 0, kRawBufferWord3);
   const int vo = d0 * 2;
   const int vo_st = act ? vo : 0x7ffffff0;             // past num_records: the store is dropped
   const int vo_b = s_row * 2;
   const int pitch = Dn * 2;
   const uint32_t* cw0 = reinterpret_cast<const uint32_t*>(Cm + row0 * SP);
 
-  uint32_t xv[TC], dv[TC];
+  constexpr int GC = MODE == SCAN_BLOCK ? TC : 1;   // gate words prefetched with x / dt in SCAN_BLOCK
+  uint32_t xv[TC], dv[TC], gv[GC];
   uint16_t bv[TC];
-  auto load = [&](int t0, uint32_t* xo, uint32_t* dO, uint16_t* bO) {
+  auto load = [&](int t0, uint32_t* xo, uint32_t* dO, uint16_t* bO, uint32_t* gO) {
 #pragma unroll
     for (int j = 0; j < TC; ++j) {
       const int t = t0 + j < T ? t0 + j : T - 1;
       if constexpr (DPL == 2) {
         xo[j] = __builtin_amdgcn_raw_buffer_load_b32(rx, vo, t * pitch, 0);
         dO[j] = __builtin_amdgcn_raw_buffer_load_b32(rd, vo, t * pitch, 0);
+        if constexpr (MODE == SCAN_BLOCK) gO[j] = __builtin_amdgcn_raw_buffer_load_b32(rg, vo, t * pitch, 0);
       } else {
         xo[j] = __builtin_amdgcn_raw_buffer_load_b16(rx, vo, t * pitch, 0);
         dO[j] = __builtin_amdgcn_raw_buffer_load_b16(rd, vo, t * pitch, 0);
+        if constexpr (MODE == SCAN_BLOCK) gO[j] = __builtin_amdgcn_raw_buffer_load_b16(rg, vo, t * pitch, 0);
       }
       bO[j] = __builtin_amdgcn_raw_buffer_load_b16(rb, vo_b, t * (SP * 2), 0);
     }
@@ -465,7 +522,7 @@ ssm_scan_fwd_mfma_kernel(const uint16_t* __restrict__ x, const uint16_t* __restr
 #pragma unroll
   for (int i = 0; i < 8; ++i) cw[i] = cw0[i];
 
-  auto step = [&](int t, uint32_t xw, uint32_t dw, uint16_t bb) {
+  auto step = [&](int t, uint32_t xw, uint32_t dw, uint16_t bb, uint32_t gw) {
     const int tn = t + 1 < T ? t + 1 : T - 1;
     uint32_t cwn[8];
 #pragma unroll
@@ -477,7 +534,7 @@ ssm_scan_fwd_mfma_kernel(const uint16_t* __restrict__ x, const uint16_t* __restr
     for (int k = 0; k < DPL; ++k) {
       const float xs = __uint_as_float(k == 0 ? xw << 16 : xw & 0xffff0000u);
       float dtv = __uint_as_float(k == 0 ? dw << 16 : dw & 0xffff0000u);
-      if (MODE == HCLSM_SCAN_MODEL) dtv = fminf(fmaxf(dtv, 1e-3f), 1.0f);
+      dtv = scan_dt<MODE>(dtv);
       const float u = dtv * xs;
       const uint32_t uhi = __float_as_uint(u) & 0xffff0000u;
       const float ulo = u - __uint_as_float(uhi);
@@ -493,6 +550,14 @@ ssm_scan_fwd_mfma_kernel(const uint16_t* __restrict__ x, const uint16_t* __restr
       }
       yo[k] = fmaf(dsk[k], xs, y0 + y1);
     }
+    if constexpr (MODE == SCAN_BLOCK) {
+      if constexpr (DPL == 2)
+        __builtin_amdgcn_raw_buffer_store_b32(pack_bf16x2(yo[0], yo[1]), rp, vo_st, t * pitch, 0);
+      else
+        __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(yo[0]), rp, vo_st, t * pitch, 0);
+#pragma unroll
+      for (int k = 0; k < DPL; ++k) yo[k] *= silu_f(__uint_as_float(k == 0 ? gw << 16 : gw & 0xffff0000u));
+    }
     if constexpr (DPL == 2)
       __builtin_amdgcn_raw_buffer_store_b32(pack_bf16x2(yo[0], yo[1]), ry, vo_st, t * pitch, 0);
     else
@@ -501,20 +566,22 @@ ssm_scan_fwd_mfma_kernel(const uint16_t* __restrict__ x, const uint16_t* __restr
     for (int i = 0; i < 8; ++i) cw[i] = cwn[i];
   };
 
-  load(0, xv, dv, bv);
+  load(0, xv, dv, bv, gv);
   const int tfull = T - T % TC;
   for (int t0 = 0; t0 < tfull; t0 += TC) {
-    uint32_t xn[TC], dn[TC];
+    uint32_t xn[TC], dn[TC], gn[GC];
     uint16_t bn[TC];
-    load(t0 + TC, xn, dn, bn);
+    load(t0 + TC, xn, dn, bn, gn);
 #pragma unroll
-    for (int j = 0; j < TC; ++j) step(t0 + j, xv[j], dv[j], bv[j]);
+    for (int j = 0; j < TC; ++j) step(t0 + j, xv[j], dv[j], bv[j], gv[j < GC ? j : 0]);
 #pragma unroll
     for (int j = 0; j < TC; ++j) { xv[j] = xn[j]; dv[j] = dn[j]; bv[j] = bn[j]; }
+#pragma unroll
+    for (int j = 0; j < GC; ++j) gv[j] = gn[j];
   }
 #pragma unroll
   for (int j = 0; j < TC - 1; ++j)
-    if (tfull + j < T) step(tfull + j, xv[j], dv[j], bv[j]);
+    if (tfull + j < T) step(tfull + j, xv[j], dv[j], bv[j], gv[j < GC ? j : 0]);
 
   if (h_final != nullptr && act) {
 #pragma unroll
@@ -529,12 +596,12 @@ ssm_scan_fwd_mfma_kernel(const uint16_t* __restrict__ x, const uint16_t* __restr
 template <int MODE, int TC, int DPL>
 static int launch_scan_mfma(const void* x, const void* dt, const float* A_log, const void* B,
                             const void* C, const float* Dskip, void* y, float* h_final,
-                            int64_t batch, int64_t T, int64_t Dn, hipStream_t st) {
+                            int64_t batch, int64_t T, int64_t Dn, hipStream_t st, ScanEpi epi) {
   const int64_t lanes = Dn / DPL;
   dim3 grid((unsigned)batch, (unsigned)((lanes + 63) / 64));
   hipLaunchKernelGGL((ssm_scan_fwd_mfma_kernel<MODE, TC, DPL>), grid, dim3(64), 0, st,
                      (const uint16_t*)x, (const uint16_t*)dt, A_log, (const uint16_t*)B,
-                     (const uint16_t*)C, Dskip, (uint16_t*)y, h_final, (int)T, (int)Dn);
+                     (const uint16_t*)C, Dskip, (uint16_t*)y, h_final, (int)T, (int)Dn, epi);
   HCLSM_LAUNCH_CHECK();
   return 0;
 }
@@ -545,19 +612,21 @@ static inline bool aligned(const void* p, uintptr_t a) { return (((uintptr_t)p) 
 template <int DT, int MODE>
 static int try_scan_sgpr(const void* x, const void* dt, const float* A_log, const void* B,
                          const void* C, const float* Dskip, void* y, float* h_final,
-                         int64_t batch, int64_t T, int64_t Dn, int64_t S, hipStream_t st) {
+                         int64_t batch, int64_t T, int64_t Dn, int64_t S, hipStream_t st, ScanEpi epi) {
   constexpr int ES = (int)sizeof(typename Elem<DT>::T);
   if (!aligned(B, 4) || !aligned(C, 4)) return 1;
-  const bool pair = (Dn % 2 == 0) && aligned(x, 2 * ES) && aligned(dt, 2 * ES) && aligned(y, 2 * ES);
+  const bool pair = (Dn % 2 == 0) && aligned(x, 2 * ES) && aligned(dt, 2 * ES) && aligned(y, 2 * ES) &&
+                    (!epi.gate || aligned(epi.gate, 2 * ES)) && (!epi.y_pre || aligned(epi.y_pre, 2 * ES));
 #define HCLSM_SCAN_SGPR(SPV)                                                                      \
   if (S == SPV) {                                                                                  \
-    if (pair) return launch_scan_sgpr<DT, SPV, MODE, 2, 4>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, st); \
-    return launch_scan_sgpr<DT, SPV, MODE, 1, 8>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, st); \
+    if (pair) return launch_scan_sgpr<DT, SPV, MODE, 2, 4>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, st, epi); \
+    return launch_scan_sgpr<DT, SPV, MODE, 1, 8>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, st, epi); \
   }
   if constexpr (DT == HCLSM_BF16) {
     if (S == 16 && T * Dn * 2 < 0x7fffffffLL) {
-      if (pair) return launch_scan_mfma<MODE, 8, 2>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, st);
-      return launch_scan_mfma<MODE, 8, 1>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, st);
+      constexpr int TCM = MODE == SCAN_BLOCK ? 4 : 8;   // the gate prefetch costs registers: shorter chunks
+      if (pair) return launch_scan_mfma<MODE, TCM, 2>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, st, epi);
+      return launch_scan_mfma<MODE, TCM, 1>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, st, epi);
     }
     HCLSM_SCAN_SGPR(4)
     HCLSM_SCAN_SGPR(8)
@@ -573,43 +642,74 @@ static int try_scan_sgpr(const void* x, const void* dt, const float* A_log, cons
 template <int DT, int SP, int MODE>
 static int launch_scan(const void* x, const void* dt, const float* A_log, const void* B,
                        const void* C, const float* Dskip, void* y, float* h_final,
-                       int64_t batch, int64_t T, int64_t Dn, int64_t S, hipStream_t st) {
+                       int64_t batch, int64_t T, int64_t Dn, int64_t S, hipStream_t st, ScanEpi epi) {
   using TT = typename Elem<DT>::T;
   const int block = (Dn % 256 == 0) ? 256 : (Dn % 128 == 0 ? 128 : 64);
   dim3 grid((unsigned)batch, (unsigned)((Dn + block - 1) / block));
   hipLaunchKernelGGL((ssm_scan_fwd_kernel<DT, SP, MODE>), grid, dim3(block), 0, st,
                      (const TT*)x, (const TT*)dt, A_log, (const TT*)B, (const TT*)C, Dskip,
-                     (TT*)y, h_final, (int)T, (int)Dn, (int)S);
+                     (TT*)y, h_final, (int)T, (int)Dn, (int)S, epi);
   HCLSM_LAUNCH_CHECK();
   return 0;
+}
+
+template <int DT, int SP, int MODE>
+static int dispatch_one(const void* x, const void* dt, const float* A_log, const void* B, const void* C,
+                        const float* Dskip, void* y, float* h_final, int64_t batch, int64_t T, int64_t Dn,
+                        int64_t S, hipStream_t st, ScanEpi epi) {
+  if constexpr (DT == HCLSM_BF16 || DT == HCLSM_F32) {
+    if (SP == S) {
+      const int r = try_scan_sgpr<DT, MODE>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, S, st, epi);
+      if (r != 1) return r;
+    }
+  }
+  return launch_scan<DT, SP, MODE>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, S, st, epi);
 }
 
 template <int DT, int SP>
 static int dispatch_mode(int mode, const void* x, const void* dt, const float* A_log, const void* B,
                          const void* C, const float* Dskip, void* y, float* h_final,
-                         int64_t batch, int64_t T, int64_t Dn, int64_t S, hipStream_t st) {
-  if constexpr (DT == HCLSM_BF16 || DT == HCLSM_F32) {
-    if (SP == S) {
-      const int r = (mode == HCLSM_SCAN_RAW)
-          ? try_scan_sgpr<DT, HCLSM_SCAN_RAW>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, S, st)
-          : try_scan_sgpr<DT, HCLSM_SCAN_MODEL>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, S, st);
-      if (r != 1) return r;
-    }
-  }
+                         int64_t batch, int64_t T, int64_t Dn, int64_t S, hipStream_t st, ScanEpi epi) {
   if (mode == HCLSM_SCAN_RAW)
-    return launch_scan<DT, SP, HCLSM_SCAN_RAW>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, S, st);
-  return launch_scan<DT, SP, HCLSM_SCAN_MODEL>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, S, st);
+    return dispatch_one<DT, SP, HCLSM_SCAN_RAW>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, S, st, epi);
+  if (mode == HCLSM_SCAN_MODEL)
+    return dispatch_one<DT, SP, HCLSM_SCAN_MODEL>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, S, st, epi);
+  return dispatch_one<DT, SP, SCAN_BLOCK>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, S, st, epi);
 }
 
 template <int DT>
 static int dispatch_sp(int mode, const void* x, const void* dt, const float* A_log, const void* B,
                        const void* C, const float* Dskip, void* y, float* h_final,
-                       int64_t batch, int64_t T, int64_t Dn, int64_t S, hipStream_t st) {
-  if (S <= 4) return dispatch_mode<DT, 4>(mode, x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, S, st);
-  if (S <= 8) return dispatch_mode<DT, 8>(mode, x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, S, st);
-  if (S <= 16) return dispatch_mode<DT, 16>(mode, x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, S, st);
-  if (S <= 32) return dispatch_mode<DT, 32>(mode, x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, S, st);
-  return dispatch_mode<DT, 64>(mode, x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, S, st);
+                       int64_t batch, int64_t T, int64_t Dn, int64_t S, hipStream_t st, ScanEpi epi) {
+  if (S <= 4) return dispatch_mode<DT, 4>(mode, x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, S, st, epi);
+  if (S <= 8) return dispatch_mode<DT, 8>(mode, x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, S, st, epi);
+  if (S <= 16) return dispatch_mode<DT, 16>(mode, x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, S, st, epi);
+  if (S <= 32) return dispatch_mode<DT, 32>(mode, x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, S, st, epi);
+  return dispatch_mode<DT, 64>(mode, x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, S, st, epi);
+}
+
+static int scan_entry(int mode, const void* x, const void* dt, const float* A_log, const void* B, const void* C,
+                      const float* Dskip, void* y, float* h_final, int64_t batch, int64_t T, int64_t d_inner,
+                      int64_t d_state, int dtype, hipStream_t st, ScanEpi epi) {
+  if (batch < 0 || T < 0 || d_inner < 0 || d_state < 1) return HCLSM_ERR_SHAPE;
+  if (batch > 0x7fffffffLL || T > 0x7fffffffLL || d_inner > 0x7fffffffLL) return HCLSM_ERR_SHAPE;
+  if ((d_inner + 63) / 64 > 65535) return HCLSM_ERR_SHAPE;
+  if (d_state > 64) return HCLSM_ERR_UNSUPPORTED;
+  if (dtype != HCLSM_F32 && dtype != HCLSM_BF16 && dtype != HCLSM_F16) return HCLSM_ERR_DTYPE;
+  if (batch == 0 || T == 0 || d_inner == 0) {
+    // nothing to scan; h_final (if any) is the zero initial state
+    if (h_final && batch > 0 && d_inner > 0) return zero_fill_f32(h_final, batch * d_inner * d_state, st);
+    return 0;
+  }
+  if (!x || !dt || !A_log || !B || !C || !y) return HCLSM_ERR_NULL;
+  switch (dtype) {
+    case HCLSM_F32:
+      return dispatch_sp<HCLSM_F32>(mode, x, dt, A_log, B, C, Dskip, y, h_final, batch, T, d_inner, d_state, st, epi);
+    case HCLSM_BF16:
+      return dispatch_sp<HCLSM_BF16>(mode, x, dt, A_log, B, C, Dskip, y, h_final, batch, T, d_inner, d_state, st, epi);
+    default:
+      return dispatch_sp<HCLSM_F16>(mode, x, dt, A_log, B, C, Dskip, y, h_final, batch, T, d_inner, d_state, st, epi);
+  }
 }
 
 }  // namespace hclsm
@@ -619,28 +719,16 @@ extern "C" int hclsm_ssm_scan_fwd(const void* x, const void* dt, const float* A_
                                   void* y, float* h_final,
                                   int64_t batch, int64_t T, int64_t d_inner, int64_t d_state,
                                   int dtype, int mode, void* stream) {
-  if (batch < 0 || T < 0 || d_inner < 0 || d_state < 1) return HCLSM_ERR_SHAPE;
-  if (batch > 0x7fffffffLL || T > 0x7fffffffLL || d_inner > 0x7fffffffLL) return HCLSM_ERR_SHAPE;
-  if ((d_inner + 63) / 64 > 65535) return HCLSM_ERR_SHAPE;
-  if (d_state > 64) return HCLSM_ERR_UNSUPPORTED;
   if (mode != HCLSM_SCAN_RAW && mode != HCLSM_SCAN_MODEL) return HCLSM_ERR_MODE;
-  if (dtype != HCLSM_F32 && dtype != HCLSM_BF16 && dtype != HCLSM_F16) return HCLSM_ERR_DTYPE;
-  if (batch == 0 || T == 0 || d_inner == 0) {
-    // nothing to scan; h_final (if any) is the zero initial state
-    if (h_final && batch > 0 && d_inner > 0) {
-      return hclsm::zero_fill_f32(h_final, batch * d_inner * d_state, (hipStream_t)stream);
-    }
-    return 0;
-  }
-  if (!x || !dt || !A_log || !B || !C || !y) return HCLSM_ERR_NULL;
-  hipStream_t st = (hipStream_t)stream;
-  using namespace hclsm;
-  switch (dtype) {
-    case HCLSM_F32:
-      return dispatch_sp<HCLSM_F32>(mode, x, dt, A_log, B, C, Dskip, y, h_final, batch, T, d_inner, d_state, st);
-    case HCLSM_BF16:
-      return dispatch_sp<HCLSM_BF16>(mode, x, dt, A_log, B, C, Dskip, y, h_final, batch, T, d_inner, d_state, st);
-    default:
-      return dispatch_sp<HCLSM_F16>(mode, x, dt, A_log, B, C, Dskip, y, h_final, batch, T, d_inner, d_state, st);
-  }
+  return hclsm::scan_entry(mode, x, dt, A_log, B, C, Dskip, y, h_final, batch, T, d_inner, d_state, dtype,
+                           (hipStream_t)stream, hclsm::ScanEpi{nullptr, nullptr});
+}
+
+extern "C" int hclsm_ssm_block_scan_fwd(const void* z, const void* dt_in, const float* A_log, const void* B,
+                                        const void* C, const void* gate, void* y, void* y_pre, float* h_final,
+                                        int64_t batch, int64_t T, int64_t d_inner, int64_t d_state, int dtype,
+                                        void* stream) {
+  if (batch > 0 && T > 0 && d_inner > 0 && !gate) return HCLSM_ERR_NULL;
+  return hclsm::scan_entry(hclsm::SCAN_BLOCK, z, dt_in, A_log, B, C, nullptr, y, h_final, batch, T, d_inner,
+                           d_state, dtype, (hipStream_t)stream, hclsm::ScanEpi{gate, y_pre});
 }

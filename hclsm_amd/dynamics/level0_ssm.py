@@ -1,18 +1,17 @@
 """Level-0 SSM on MI355X: counterpart of hclsm/dynamics/level0_ssm.py.
 
 Same module tree and parameter names as the reference (state dicts load unchanged).  The
-selective scan -- a Python loop over T in the reference (:95-100) -- runs on the gfx950 kernel
-through ``hclsm_amd.kernels.ssm_scan_fn`` with the reference's clamped ("model") semantics;
-projections and elementwise epilogues are torch ops on the GPU.
+selective scan -- a Python loop over T in the reference (:95-100) -- runs on the gfx950 kernel with
+the reference's clamped ("model") semantics, with softplus / clamp of dt and the silu gate fused into
+it (``hclsm_amd.kernels.ssm_block_scan``); the projections are torch GEMMs.
 """
 
 from __future__ import annotations
 
 import torch
 import torch.nn as nn
-import torch.nn.functional as F
 
-from hclsm_amd.kernels.ssm_scan_kernel import ssm_scan_fn
+from hclsm_amd.kernels.ssm_scan_kernel import ssm_block_scan
 
 
 class SimplifiedSSMBlock(nn.Module):
@@ -36,14 +35,13 @@ class SimplifiedSSMBlock(nn.Module):
         residual = x
         x = self.norm(x)
         z = self.in_proj(x)                                                 # :72
-        gate = F.silu(self.gate_proj(x))                                    # :73
-        dt = F.softplus(self.dt_proj(z)).clamp(min=1e-3, max=1.0)           # :76
+        gate_in = self.gate_proj(x)                                         # :73 (silu in the kernel)
+        dt_in = self.dt_proj(z)                                             # :76 (softplus, clamp in the kernel)
         B_param = self.B_proj(z)
         C_param = self.C_proj(z)
-        # clamped scan (:82-101): A = -clamp(exp(A_log), 1e-6, 1), fp32 state, output in x.dtype
-        y = ssm_scan_fn(z, dt, self.A_log, B_param, C_param, backend="sequential", clamp_mode="model")
-        y = y.to(x.dtype) * gate
-        return residual + self.out_proj(y)
+        # clamped scan (:82-101, A = -clamp(exp(A_log), 1e-6, 1), fp32 state) times silu(gate) (:103)
+        y = ssm_block_scan(z, dt_in, self.A_log, B_param, C_param, gate_in)
+        return residual + self.out_proj(y.to(x.dtype))
 
 
 class Level0SSM(nn.Module):

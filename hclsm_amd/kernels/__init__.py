@@ -11,6 +11,7 @@ import torch
 
 from hclsm_amd.kernels.ssm_scan_kernel import (
     ssm_scan_fn,
+    ssm_block_scan,
     sequential_ssm_scan,
     parallel_ssm_scan_pytorch,
     fused_ssm_scan_triton,
@@ -80,6 +81,7 @@ __all__ = [
     "slot_attention_iteration",
     "slot_attention_forward",
     "ssm_scan_fn",
+    "ssm_block_scan",
     "sequential_ssm_scan",
     "parallel_ssm_scan_pytorch",
     "fused_ssm_scan_triton",

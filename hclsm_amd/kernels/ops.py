@@ -8,6 +8,8 @@ adds tens of microseconds of Python dispatch per call, which is the size of the 
     hclsm_hip::ssm_scan_fwd(x, dt, A_log, B, C, D?, mode, want_h) -> (y, h_final)
         y in x.dtype; h_final (batch, d_inner, d_state) fp32, or shape (0,) when want_h is False
         (ssm_scan_kernel.py:294-319 forward; mode 0 raw, 1 clamped model form)
+    hclsm_hip::ssm_block_scan_fwd(z, dt_in, A_log, B, C, gate) -> (y, y_pre)
+        y = silu(gate) * clamped scan with dt = clamp(softplus(dt_in), 1e-3, 1) (level0_ssm.py:72-103)
     hclsm_hip::ssm_scan_bwd(x, dt, A_log, B, C, D?, gy, mode) -> (gx, gdt, gA_log, gB, gC, gD)
         gD has shape (0,) when D is None (ssm_scan_kernel.py:321-377)
     hclsm_hip::slot_attn_core(Q, K, V, scale, denom_eps, logit_clamp, renorm_eps) -> (out, attn)
@@ -39,7 +41,7 @@ from hclsm_amd.kernels.slot_attention_kernel import _core_raw
 from hclsm_amd.kernels.slot_iteration import SlotMode, SlotWeights, slot_attention_forward as _slot_forward
 from hclsm_amd.kernels.sparse_event_attn import EventIndex, _gather_padded_raw, _mask_code, _scatter_padded_raw
 from hclsm_amd.kernels.ssm_scan_bwd import scan_backward
-from hclsm_amd.kernels.ssm_scan_kernel import _scan_forward
+from hclsm_amd.kernels.ssm_scan_kernel import _block_forward, _scan_forward
 
 Tensor = torch.Tensor
 SLOT_WEIGHT_ORDER = ("w_q", "w_k", "w_v", "w_ih", "w_hh", "w1", "w2", "b_ih", "b_hh", "b1", "b2",
@@ -64,6 +66,17 @@ def ssm_scan_fwd(x: Tensor, dt: Tensor, A_log: Tensor, B: Tensor, C: Tensor, D: 
 def _(x, dt, A_log, B, C, D, mode, want_h):
     h = x.new_empty((x.shape[0], x.shape[2], B.shape[2]) if want_h else (0,), dtype=torch.float32)
     return torch.empty_like(x), h
+
+
+@torch.library.custom_op("hclsm_hip::ssm_block_scan_fwd", mutates_args=())
+def ssm_block_scan_fwd(z: Tensor, dt_in: Tensor, A_log: Tensor, B: Tensor, C: Tensor,
+                       gate: Tensor) -> tuple[Tensor, Tensor]:
+    return _block_forward(z, dt_in, A_log, B, C, gate, True)
+
+
+@ssm_block_scan_fwd.register_fake
+def _(z, dt_in, A_log, B, C, gate):
+    return torch.empty_like(z), torch.empty_like(z)
 
 
 @torch.library.custom_op("hclsm_hip::ssm_scan_bwd", mutates_args=())

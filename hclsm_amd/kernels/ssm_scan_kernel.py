@@ -147,3 +147,57 @@ def ssm_scan_fn(x, dt, A_log, B, C, backend: str = "auto", *, D=None, clamp_mode
         clamp_mode = "raw" if backend in _RAW_BACKENDS else "model"
     return fused_ssm_scan_hip(x, dt, A_log, B, C, D=D, clamp_mode=clamp_mode,
                               return_h_final=return_h_final)
+
+
+def _block_forward(z, dt_in, A_log, B, C, gate, want_pre: bool):
+    batch, T, d_inner, d_state = _check_shapes(z, dt_in, A_log, B, C, None)
+    if gate.shape != z.shape:
+        raise ValueError(f"gate shape {tuple(gate.shape)} != z shape {tuple(z.shape)}")
+    io = common_float_dtype(z, dt_in, B, C, gate)
+    zc, dc, Bc, Cc, gc = (t.to(io).contiguous() for t in (z, dt_in, B, C, gate))
+    Ac = A_log.to(torch.float32).contiguous()
+    y = torch.empty((batch, T, d_inner), dtype=io, device=z.device)
+    y_pre = torch.empty_like(y) if want_pre else None
+    code = _lib.lib().hclsm_ssm_block_scan_fwd(
+        _lib.ptr(zc), _lib.ptr(dc), _lib.ptr(Ac), _lib.ptr(Bc), _lib.ptr(Cc), _lib.ptr(gc), _lib.ptr(y),
+        _lib.ptr(y_pre), None, batch, T, d_inner, d_state, _lib.dtype_code(io), _lib.stream_of(zc))
+    _lib.check(code, "hclsm_ssm_block_scan_fwd")
+    return y, y_pre
+
+
+class _HipSSMBlockScan(torch.autograd.Function):
+    """Fused block scan forward on HIP; backward = HIP reverse scan (model mode) plus the chain rule
+    through softplus / clamp (torch's clamp passes gradient inside the closed interval) and silu."""
+
+    @staticmethod
+    def forward(ctx, z, dt_in, A_log, B, C, gate):
+        need = any(ctx.needs_input_grad)
+        y, y_pre = _block_forward(z, dt_in, A_log, B, C, gate, need)
+        if need:
+            ctx.save_for_backward(z, dt_in, A_log, B, C, gate, y_pre)
+        return y
+
+    @staticmethod
+    def backward(ctx, g):
+        from hclsm_amd.kernels.ssm_scan_bwd import scan_backward
+        import torch.nn.functional as F
+        z, dt_in, A_log, B, C, gate, y_pre = ctx.saved_tensors
+        gf, gatef = g.float(), gate.float()
+        sg = torch.sigmoid(gatef)
+        g_y = gf * gatef * sg
+        g_gate = gf * y_pre.float() * sg * (1.0 + gatef * (1.0 - sg))
+        dtf = dt_in.float()
+        sp = F.softplus(dtf)
+        dt = sp.clamp(1e-3, 1.0)
+        grads = scan_backward(z, dt.to(y_pre.dtype), A_log, B, C, None, g_y.to(y_pre.dtype), _lib.SCAN_MODEL)
+        g_dt_in = grads["dt"].float() * torch.sigmoid(dtf) * ((sp >= 1e-3) & (sp <= 1.0)).to(torch.float32)
+        return (grads["x"].to(z.dtype), g_dt_in.to(dt_in.dtype), grads["A_log"], grads["B"].to(B.dtype),
+                grads["C"].to(C.dtype), g_gate.to(gate.dtype))
+
+
+def ssm_block_scan(z, dt_in, A_log, B, C, gate):
+    """silu(gate) * clamped-scan(z, clamp(softplus(dt_in), 1e-3, 1), A_log, B, C): the scan of
+    SimplifiedSSMBlock (level0_ssm.py:72-103) with its elementwise epilogues in the kernel.
+    Output dtype: the common I/O dtype of the inputs.  Differentiable."""
+    require_gpu("ssm_block_scan", z, dt_in, A_log, B, C, gate)
+    return _HipSSMBlockScan.apply(z, dt_in, A_log, B, C, gate)

@@ -79,6 +79,22 @@ int hclsm_ssm_scan_fwd(const void* x, const void* dt, const float* A_log,
                        int64_t batch, int64_t T, int64_t d_inner, int64_t d_state,
                        int dtype, int mode, void* stream);
 
+/*
+ * The scan of SimplifiedSSMBlock with its elementwise epilogues fused
+ * (hclsm/dynamics/level0_ssm.py:72-103):
+ *   dt    = clamp(softplus(dt_in), 1e-3, 1)           (:76, softplus threshold 20 as in torch)
+ *   y_pre = clamped selective scan of z with dt, A_log, B, C   (MODEL mode, :82-101)
+ *   y     = y_pre * silu(gate)                        (:73, :103)
+ * z, dt_in, gate, y, y_pre: [batch][T][d_inner] in `dtype`; B, C: [batch][T][d_state]; A_log fp32.
+ * y_pre (kept for the backward) and h_final are nullable.  No skip term.
+ * Replaces: the softplus / clamp of dt, the inline scan, F.silu(gate) and the gating product of
+ *   SimplifiedSSMBlock.forward.
+ */
+int hclsm_ssm_block_scan_fwd(const void* z, const void* dt_in, const float* A_log, const void* B,
+                             const void* C, const void* gate, void* y, void* y_pre, float* h_final,
+                             int64_t batch, int64_t T, int64_t d_inner, int64_t d_state, int dtype,
+                             void* stream);
+
 /* Workspace bytes for hclsm_ssm_scan_bwd. */
 int64_t hclsm_ssm_scan_bwd_workspace(int64_t batch, int64_t T, int64_t d_inner, int64_t d_state);
 

@@ -2,6 +2,7 @@
 
 Numpy float64 restatements, taking parameters as plain arrays (names as in the reference's
 state dicts):
+  block_scan_ref            hclsm/dynamics/level0_ssm.py:73-103 (softplus/clamp of dt, scan, silu gate)
   simplified_ssm_block_ref  hclsm/dynamics/level0_ssm.py:58-107 (scan in model mode)
   level0_ssm_ref            hclsm/dynamics/level0_ssm.py:159-220
   event_block_ref           hclsm/dynamics/level1_event.py:44-54 (MHA over slots + SwiGLU)
@@ -31,18 +32,21 @@ def silu(x):
     return x * sigmoid(x)
 
 
+def block_scan_ref(z, dt_in, A_log, B, C, gate):
+    """silu(gate) * clamped scan of z with dt = clip(softplus(dt_in), 1e-3, 1) (level0_ssm.py:73-103)."""
+    dt = np.clip(softplus(np.asarray(dt_in, np.float64)), 1e-3, 1.0)
+    return ssm_scan_ref(z, dt, A_log, B, C, clamp_mode="model") * silu(np.asarray(gate, np.float64))
+
+
 def simplified_ssm_block_ref(x, p):
     """p keys: norm.weight, norm.bias, in_proj.weight, gate_proj.weight, dt_proj.weight, dt_proj.bias,
     B_proj.weight, C_proj.weight, A_log, out_proj.weight."""
     x = np.asarray(x, np.float64)
     h = layer_norm(x, p["norm.weight"], p["norm.bias"])
     z = _lin(h, p["in_proj.weight"])
-    gate = silu(_lin(h, p["gate_proj.weight"]))
-    dt = np.clip(softplus(_lin(z, p["dt_proj.weight"], p["dt_proj.bias"])), 1e-3, 1.0)
-    Bm = _lin(z, p["B_proj.weight"])
-    Cm = _lin(z, p["C_proj.weight"])
-    y = ssm_scan_ref(z, dt, p["A_log"], Bm, Cm, clamp_mode="model")
-    return x + _lin(y * gate, p["out_proj.weight"])
+    y = block_scan_ref(z, _lin(z, p["dt_proj.weight"], p["dt_proj.bias"]), p["A_log"], _lin(z, p["B_proj.weight"]),
+                       _lin(z, p["C_proj.weight"]), _lin(h, p["gate_proj.weight"]))
+    return x + _lin(y, p["out_proj.weight"])
 
 
 def level0_ssm_ref(obj_states, obj_mask, p, n_blocks):

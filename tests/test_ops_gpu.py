@@ -69,3 +69,14 @@ def test_slot_ops_equal_eager():
     assert torch.equal(s, si.slot_attention_forward(tokens.cuda(), slots0.cuda(), W, 3, si.CONFIG2_MODE))
     torch.library.opcheck(OPS.slot_attn_core.default, (Q, K, V, 0.125, 0.0, 0.0, -1.0),
                           test_utils=("test_schema", "test_faketensor"))
+
+
+def test_block_scan_op_equals_eager():
+    from hclsm_amd.kernels import ssm_block_scan
+    g = torch.Generator().manual_seed(8)
+    z, dt_in, gate = (torch.randn(2, 16, 64, generator=g).to(torch.bfloat16).cuda() for _ in range(3))
+    A_log = (-torch.rand(64, 16, generator=g) * 0.5).cuda()
+    Bm, Cm = (torch.randn(2, 16, 16, generator=g).to(torch.bfloat16).cuda() for _ in range(2))
+    y, y_pre = OPS.ssm_block_scan_fwd(z, dt_in, A_log, Bm, Cm, gate)
+    assert torch.equal(y, ssm_block_scan(z, dt_in, A_log, Bm, Cm, gate))
+    assert torch.allclose(y.float(), (y_pre.float() * torch.nn.functional.silu(gate.float())), rtol=1e-2, atol=1e-2)

@@ -229,3 +229,57 @@ def test_launch_on_current_side_stream():
     side.synchronize()
     ref = ssm_scan_ref(*(_np(d[k]) for k in ("x", "dt", "A_log", "B", "C")), clamp_mode="raw")
     assert normwise_rel_err(_np(y), ref) <= 5e-3
+
+
+@pytest.mark.parametrize("N,T,Dn,S,dtype,tol", [
+    (3, 20, 64, 16, torch.float32, FP32_TOL),    # fp32 SGPR kernel
+    (2, 9, 70, 8, torch.float32, FP32_TOL),      # fp32 SGPR, one channel per lane
+    (2, 33, 48, 48, torch.float32, FP32_TOL),    # generic kernel (d_state 48, the small preset's)
+    (4, 64, 384, 16, torch.bfloat16, LOWP_TOL),  # bf16 matrix-core kernel, two channels per lane
+    (2, 17, 129, 16, torch.bfloat16, LOWP_TOL),  # bf16 matrix-core kernel, one channel per lane
+    (2, 12, 40, 8, torch.float16, LOWP_TOL),     # fp16 generic kernel
+])
+def test_block_scan_fused_epilogues(N, T, Dn, S, dtype, tol):
+    """hclsm_ssm_block_scan_fwd: softplus / clamp of dt, the clamped scan and silu(gate) in one kernel,
+    against the oracle (oracle.modules.block_scan_ref)."""
+    from oracle.modules import block_scan_ref
+    from hclsm_amd.kernels import ssm_block_scan
+    g = torch.Generator().manual_seed(N * 1000 + T + S)
+    z = torch.randn(N, T, Dn, generator=g).to(dtype)
+    dt_in = (torch.randn(N, T, Dn, generator=g) * 2 - 1).to(dtype)     # softplus spans both clamps
+    dt_in[0, 0, :4] = torch.tensor([30.0, -9.0, 0.5, 25.0]).to(dtype)   # threshold and lower-clamp branches
+    A_log = -torch.rand(Dn, S, generator=g) * 0.5
+    Bm = (torch.randn(N, T, S, generator=g) / 4).to(dtype)
+    Cm = (torch.randn(N, T, S, generator=g) / 4).to(dtype)
+    gate = torch.randn(N, T, Dn, generator=g).to(dtype)
+    y = ssm_block_scan(*(t.cuda() for t in (z, dt_in, A_log, Bm, Cm, gate)))
+    ref = block_scan_ref(*(_np(t) for t in (z, dt_in, A_log, Bm, Cm, gate)))
+    assert y.dtype == dtype
+    assert normwise_rel_err(_np(y), ref) <= tol
+
+
+def test_block_scan_gradients_match_float64_autograd():
+    """Backward of the fused block scan (HIP reverse scan + chain rule through softplus / clamp / silu)
+    against float64 torch autograd of the same math on the CPU."""
+    import torch.nn.functional as F
+    from hclsm_amd.kernels import ssm_block_scan
+    g = torch.Generator().manual_seed(77)
+    N, T, Dn, S = 2, 24, 32, 16
+    z, dt_in, gate = (torch.randn(N, T, Dn, generator=g, dtype=torch.float64) for _ in range(3))
+    dt_in = dt_in * 2 - 1
+    A_log = -torch.rand(Dn, S, generator=g, dtype=torch.float64) * 0.5
+    Bm, Cm = (torch.randn(N, T, S, generator=g, dtype=torch.float64) / 4 for _ in range(2))
+    w = torch.randn(N, T, Dn, generator=g, dtype=torch.float64)
+    ins = [t.float().cuda().requires_grad_() for t in (z, dt_in, A_log, Bm, Cm, gate)]
+    (ssm_block_scan(*ins) * w.float().cuda()).sum().backward()
+    r = [t.clone().requires_grad_() for t in (z, dt_in, A_log, Bm, Cm, gate)]
+    dt = F.softplus(r[1]).clamp(1e-3, 1.0)
+    A = -torch.exp(r[2]).clamp(1e-6, 1.0)
+    h = torch.zeros(N, Dn, S, dtype=torch.float64)
+    ys = []
+    for t in range(T):
+        h = torch.exp((dt[:, t, :, None] * A).clamp(-20.0, 0.0)) * h + (dt[:, t] * r[0][:, t])[:, :, None] * r[3][:, t, None, :]
+        ys.append((h * r[4][:, t, None, :]).sum(-1))
+    ((torch.stack(ys, 1) * F.silu(r[5])) * w).sum().backward()
+    for got, ref, name in zip(ins, r, ("z", "dt_in", "A_log", "B", "C", "gate")):
+        assert normwise_rel_err(_np(got.grad), _np(ref.grad)) <= 1e-5, name
