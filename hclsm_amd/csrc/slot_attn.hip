@@ -131,6 +131,141 @@ struct OutSplit {
 };
 
 // 64x64 output tile per workgroup, each wave a 32x32 quadrant over the full K (large M x N).
+// 64x64 output tile per workgroup, 16-bit operands: the tile's A rows and W rows are staged in LDS in
+// K chunks of 128 (each global byte read once per workgroup), the next chunk's global loads in flight
+// while the current chunk is multiplied; each wave computes a 32x32 quadrant from LDS.  34 KB of LDS,
+// so several workgroups share a CU.
+constexpr int LT_KC = 128;
+constexpr int LT_LD = LT_KC + 8;   // LDS row pitch (elements): spreads the 16 rows of an operand over banks
+
+template <int DT, int OT>
+__global__ void __launch_bounds__(256)
+linear_lds_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const typename MM<DT>::T* __restrict__ W,
+                  int64_t ldw, const float* __restrict__ bias, const float* __restrict__ resid, int64_t ldr,
+                  typename MM<OT>::T* __restrict__ Y, int64_t ldy, typename MM<DT>::T* __restrict__ Y2,
+                  int64_t ldy2, int64_t M, int64_t N, int64_t K, int relu, float clamp_v, OutSplit os) {
+  using A = MM<DT>;
+  using T = typename A::T;
+  static_assert(A::KPL == 8, "16-bit operands");
+  __shared__ __align__(16) T As[64 * LT_LD];
+  __shared__ __align__(16) T Bs[64 * LT_LD];
+  const int64_t tiles_n = (N + 63) / 64;
+  const int64_t tm = blockIdx.x / tiles_n, tn = blockIdx.x - tm * tiles_n;
+  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, g = lane >> 4, li = lane & 15;
+  const int wr = wid >> 1, wc = wid & 1;
+  // staging map: 64 rows x (KC / 8) 16-byte units = 1024 units per operand, 4 per thread
+  const T* pa[4];
+  const T* pb[4];
+  int soff[4], ucol[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int u = tid + 256 * i, r = u >> 4;
+    ucol[i] = (u & 15) * 8;
+    int64_t ra = tm * 64 + r, rb = tn * 64 + r;
+    ra = ra < M ? ra : M - 1;
+    rb = rb < N ? rb : N - 1;
+    pa[i] = X + ra * ldx + ucol[i];
+    pb[i] = W + rb * ldw + ucol[i];
+    soff[i] = r * LT_LD + ucol[i];
+  }
+  uint4 ra_[4], rb_[4];
+  auto fetch = [&](int64_t k0, int kc) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool in = ucol[i] < kc;
+      ra_[i] = in ? *reinterpret_cast<const uint4*>(pa[i] + k0) : make_uint4(0u, 0u, 0u, 0u);
+      rb_[i] = in ? *reinterpret_cast<const uint4*>(pb[i] + k0) : make_uint4(0u, 0u, 0u, 0u);
+    }
+  };
+  f32x4 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  fetch(0, (int)(K < LT_KC ? K : LT_KC));
+  for (int64_t k0 = 0; k0 < K; k0 += LT_KC) {
+    const int kc = (int)(K - k0 < LT_KC ? K - k0 : LT_KC);
+    __syncthreads();   // the previous chunk is consumed
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      *reinterpret_cast<uint4*>(As + soff[i]) = ra_[i];
+      *reinterpret_cast<uint4*>(Bs + soff[i]) = rb_[i];
+    }
+    __syncthreads();
+    if (k0 + LT_KC < K) fetch(k0 + LT_KC, (int)(K - k0 - LT_KC < LT_KC ? K - k0 - LT_KC : LT_KC));
+    for (int s = 0; s < kc / 32; ++s) {
+      const typename A::Op a0 = A::load(As + (wr * 32 + li) * LT_LD + s * 32 + 8 * g);
+      const typename A::Op a1 = A::load(As + (wr * 32 + 16 + li) * LT_LD + s * 32 + 8 * g);
+      const typename A::Op b0 = A::load(Bs + (wc * 32 + li) * LT_LD + s * 32 + 8 * g);
+      const typename A::Op b1 = A::load(Bs + (wc * 32 + 16 + li) * LT_LD + s * 32 + 8 * g);
+      acc[0][0] = A::mfma(a0, b0, acc[0][0]);
+      acc[0][1] = A::mfma(a0, b1, acc[0][1]);
+      acc[1][0] = A::mfma(a1, b0, acc[1][0]);
+      acc[1][1] = A::mfma(a1, b1, acc[1][1]);
+    }
+  }
+  const int64_t r0 = tm * 64 + 32 * wr, c0 = tn * 64 + 32 * wc;
+  if (os.yt != nullptr && Y2 == nullptr && os.col % 64 == 0 && tn * 64 >= os.col) {
+    // a tile of the transposed half: transpose through LDS so that consecutive threads write
+    // consecutive rows (tokens) of yt
+    constexpr int TP = 66;   // pitch of the transposed tile (elements)
+    T* Ts = As;
+    __syncthreads();   // the last chunk is consumed
+#pragma unroll
+    for (int tj = 0; tj < 2; ++tj) {
+      const int64_t col = c0 + 16 * tj + li;
+      const float bv = (bias && col < N) ? bias[col] : 0.f;
+#pragma unroll
+      for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t row = r0 + 16 * ti + 4 * g + r;
+          float val = acc[ti][tj][r] + bv;
+          if (relu) val = fmaxf(val, 0.f);
+          if (resid && row < M && col < N) val += resid[row * ldr + col];
+          if (clamp_v > 0.f) val = fminf(fmaxf(val, -clamp_v), clamp_v);
+          Ts[(32 * wc + 16 * tj + li) * TP + 32 * wr + 16 * ti + 4 * g + r] = MM<OT>::fromf(val);
+        }
+    }
+    __syncthreads();
+    typename MM<OT>::T* yt = reinterpret_cast<typename MM<OT>::T*>(os.yt);
+    for (int i = tid; i < 64 * 64; i += 256) {
+      const int c = i >> 6, rl = i & 63;
+      const int64_t row = tm * 64 + rl, col = tn * 64 + c;
+      if (row < M && col < N) {
+        const int64_t fr = row / os.frame_rows, rr = row - fr * os.frame_rows;
+        yt[fr * os.bstride + (col - os.col) * os.ldyt + rr] = Ts[c * TP + rl];
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int tj = 0; tj < 2; ++tj) {
+    const int64_t col = c0 + 16 * tj + li;
+    if (col >= N) continue;
+    const float bv = bias ? bias[col] : 0.f;
+#pragma unroll
+    for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t row = r0 + 16 * ti + 4 * g + r;
+        if (row >= M) continue;
+        float val = acc[ti][tj][r] + bv;
+        if (relu) val = fmaxf(val, 0.f);
+        if (resid) val += resid[row * ldr + col];
+        if (clamp_v > 0.f) val = fminf(fmaxf(val, -clamp_v), clamp_v);
+        if (os.yt != nullptr && col >= os.col) {
+          const int64_t fr = row / os.frame_rows, rr = row - fr * os.frame_rows;
+          reinterpret_cast<typename MM<OT>::T*>(os.yt)[fr * os.bstride + (col - os.col) * os.ldyt + rr] =
+              MM<OT>::fromf(val);
+        } else {
+          Y[row * ldy + col] = MM<OT>::fromf(val);
+        }
+        if (Y2) Y2[row * ldy2 + col] = A::fromf(val);
+      }
+  }
+}
+
 template <int DT, int OT>
 __global__ void __launch_bounds__(256)
 linear_quad_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const typename MM<DT>::T* __restrict__ W,
@@ -714,9 +849,14 @@ static void launch_linear_quad(const void* x, int64_t ldx, const void* w, int64_
                                OutSplit os = OutSplit{0, 1, 0, 0, nullptr}) {
   if constexpr (std::is_same_v<XT, typename MM<DT>::T>) {
     const unsigned grid = (unsigned)(((M + 63) / 64) * ((N + 63) / 64));
-    hipLaunchKernelGGL((linear_quad_kernel<DT, OT>), dim3(grid), dim3(256), 0, st, (const typename MM<DT>::T*)x, ldx,
-                       (const typename MM<DT>::T*)w, ldw, bias, resid, ldr, (typename MM<OT>::T*)y, ldy,
-                       (typename MM<DT>::T*)y2, ldy2, M, N, K, relu, clamp, os);
+    if constexpr (MM<DT>::KPL == 8)
+      hipLaunchKernelGGL((linear_lds_kernel<DT, OT>), dim3(grid), dim3(256), 0, st, (const typename MM<DT>::T*)x, ldx,
+                         (const typename MM<DT>::T*)w, ldw, bias, resid, ldr, (typename MM<OT>::T*)y, ldy,
+                         (typename MM<DT>::T*)y2, ldy2, M, N, K, relu, clamp, os);
+    else
+      hipLaunchKernelGGL((linear_quad_kernel<DT, OT>), dim3(grid), dim3(256), 0, st, (const typename MM<DT>::T*)x,
+                         ldx, (const typename MM<DT>::T*)w, ldw, bias, resid, ldr, (typename MM<OT>::T*)y, ldy,
+                         (typename MM<DT>::T*)y2, ldy2, M, N, K, relu, clamp, os);
   }
 }
 

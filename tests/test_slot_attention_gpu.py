@@ -186,3 +186,21 @@ def test_forward_two_launch_iteration_matches_oracle(mode_name, dtype, B, N, M, 
                                     logit_clamp=mode.logit_clamp, renorm_eps=mode.renorm_eps, slot_clamp=mode.slot_clamp)
     err = normwise_rel_err(_np(out), ref)
     assert err <= 2e-2, f"{mode_name} {dtype}: {err:.3e}"
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.bfloat16, 2e-2), (torch.float16, 2e-2)])
+def test_large_linear_lds_tiles(dtype, tol):
+    """hclsm_linear at a size that takes the LDS-staged 64x64-tile kernel (>= 2048 32x32 tiles), with
+    bias, ReLU, residual and clamp, ragged M and N, and K not a multiple of the 128-wide chunk."""
+    from hclsm_amd.kernels import slot_iteration as si
+    g = torch.Generator().manual_seed(31)
+    M, N, K = 2085, 1040, 416
+    x = torch.randn(M, K, generator=g).to(dtype)
+    w = (torch.randn(N, K, generator=g) / 16).to(dtype)
+    b = torch.randn(N, generator=g)
+    r = torch.randn(M, N, generator=g)
+    st = torch.cuda.current_stream().cuda_stream
+    y = si._linear(x.cuda(), w.cuda(), bias=b.cuda(), resid=r.cuda(), relu=True, clamp=2.0, out_dtype=torch.float32,
+                   stream=st)
+    ref = np.clip(np.maximum(_np(x) @ _np(w).T + _np(b), 0) + _np(r), -2.0, 2.0)
+    assert normwise_rel_err(_np(y), ref) <= tol
