@@ -1,7 +1,8 @@
 // Event index construction and event gather / scatter for gfx950.
 //
-// Index build (bit-exact, ascending t within each row) in three launches with no
-// host synchronisation:
+// Index build (bit-exact, ascending t within each row) with no host synchronisation.  For
+// B <= 16384 rows: event_count_kernel, then event_fill_prefix_kernel (below), which folds the prefix
+// sum into the fill.  Larger B, three launches:
 //   1. event_count_kernel : one wave per row; 64 timesteps per ballot, popcount.
 //   2. event_scan_kernel  : one workgroup; exclusive prefix sum of the counts over
 //                           tiles of 4096 rows with a running carry; also total
@@ -139,6 +140,81 @@ event_fill_kernel(const void* __restrict__ mask, int mdt, int64_t B, int64_t T, 
   }
 }
 
+// Fill with the prefix sum folded in (B <= PREFIX_MAX_ROWS): each workgroup sums counts[0, b0) of
+// the rows before its own (a few KB from L2), so no separate scan launch is needed; the last
+// workgroup also writes offsets[B] and the stats {total, max count}.
+constexpr int64_t PREFIX_MAX_ROWS = 16384;
+
+__device__ __forceinline__ int32_t block_sum(int32_t v, int32_t* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  int32_t t = 0;
+  for (int w = 0; w < EV_WAVES; ++w) t += red[w];
+  return t;
+}
+
+__global__ void __launch_bounds__(64 * EV_WAVES)
+event_fill_prefix_kernel(const void* __restrict__ mask, int mdt, int64_t B, int64_t T, int rule,
+                         const int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+                         int32_t* __restrict__ indices, int32_t* __restrict__ rows,
+                         int32_t* __restrict__ slot_of, int32_t* __restrict__ stats) {
+  __shared__ int32_t red[EV_WAVES];
+  const int64_t b0 = (int64_t)blockIdx.x * EV_WAVES;
+  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
+  int32_t s = 0;
+  for (int64_t i = tid; i < b0; i += 64 * EV_WAVES) s += counts[i];
+  const int32_t prefix = block_sum(s, red);
+  const int64_t b = b0 + wid;
+  int32_t off = prefix;
+  for (int w = 0; w < wid; ++w) off += (b0 + w < B) ? counts[b0 + w] : 0;
+  if (b < B) {
+    if (lane == 0) offsets[b] = off;
+    int32_t run = 0;
+    for (int64_t t0 = 0; t0 < T; t0 += 64) {
+      const int64_t t = t0 + lane;
+      const bool ev = (t < T) && is_event(mask, mdt, b * T + (t < T ? t : 0), rule);
+      const uint64_t bal = __ballot(ev);
+      const int32_t rank = (int32_t)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                             __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+      if (t < T) {
+        if (slot_of) slot_of[b * T + t] = ev ? run + rank : -1;
+        if (ev) {
+          indices[off + run + rank] = (int32_t)t;
+          if (rows) rows[off + run + rank] = (int32_t)b;
+        }
+      }
+      run += __popcll(bal);
+    }
+  }
+  if (blockIdx.x == gridDim.x - 1) {   // totals: every row count, summed and maxed by this workgroup
+    int32_t t = 0, m = 0;
+    for (int64_t i = tid; i < B; i += 64 * EV_WAVES) {
+      const int32_t c = counts[i];
+      t += c;
+      m = c > m ? c : m;
+    }
+    const int32_t total = block_sum(t, red);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const int32_t v = __shfl_xor(m, o, 64);
+      m = v > m ? v : m;
+    }
+    __syncthreads();
+    if (lane == 0) red[wid] = m;
+    __syncthreads();
+    if (tid == 0) {
+      int32_t mx = 0;
+      for (int w = 0; w < EV_WAVES; ++w) mx = red[w] > mx ? red[w] : mx;
+      offsets[B] = total;
+      stats[0] = total;
+      stats[1] = mx;
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // byte-unit gather / scatter
 // ---------------------------------------------------------------------------
@@ -264,6 +340,13 @@ extern "C" int hclsm_event_index(const void* mask, int mask_dtype, int64_t B, in
     const unsigned g = (unsigned)((B + EV_WAVES - 1) / EV_WAVES);
     hipLaunchKernelGGL(event_count_kernel, dim3(g), dim3(64 * EV_WAVES), 0, st, mask, mask_dtype, B, T, rule, counts);
     HCLSM_LAUNCH_CHECK();
+  }
+  if (B > 0 && B <= PREFIX_MAX_ROWS) {   // two launches: counts, then fill with the prefix folded in
+    const unsigned g = (unsigned)((B + EV_WAVES - 1) / EV_WAVES);
+    hipLaunchKernelGGL(event_fill_prefix_kernel, dim3(g), dim3(64 * EV_WAVES), 0, st, mask, mask_dtype, B, T, rule,
+                       counts, offsets, indices, rows, slot_of, stats);
+    HCLSM_LAUNCH_CHECK();
+    return 0;
   }
   hipLaunchKernelGGL(event_scan_kernel, dim3(1), dim3(SCAN_THREADS), 0, st, counts, B, offsets, stats);
   HCLSM_LAUNCH_CHECK();

@@ -37,7 +37,8 @@ def _check_index(m_cpu, rule="gt_half", dtype=None):
 
 @pytest.mark.parametrize("B,T,p", [(1, 1, 1.0), (3, 7, 0.4), (1024, 64, 0.15), (7, 130, 0.3), (5, 64, 0.0),
                                    (2, 200, 1.0), (9000, 3, 0.5), (1024, 1024, 0.05),
-                                   (8192, 32, 0.3), (4096, 65, 0.2)])
+                                   (8192, 32, 0.3), (4096, 65, 0.2),
+                                   (20000, 3, 0.5)])   # past the two-launch row limit: separate scan
 def test_index_bit_exact(B, T, p):
     _check_index(_mask(B, T, p, seed=B + T, force0=(p == 0.15)))
 
