@@ -56,26 +56,45 @@ def _traffic_from_profile():
         return None
 
 
-def _cpu_baseline(d, nseq=1024, reps=5):
-    import numpy as np
-    from oracle.ssm_scan import ssm_scan_ref
-    from hclsm_amd.workloads import scan_algorithmic_bytes
-    sel = slice(0, nseq)
-    args = [d[k][sel].float().numpy() if k in ("x", "dt", "B", "C") else d[k].numpy()
-            for k in ("x", "dt", "A_log", "B", "C")]
-    Dn = d["D"].numpy()
-    times = []
+def _cpu_threads():
+    """All host cores this process may use (torch intra-op threads), and the CPU model string."""
+    import torch
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    model = "unknown CPU"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return torch.get_num_threads(), model
+
+
+def _cpu_time(fn, reps):
+    fn()                                   # warmup
+    ts = []
     for _ in range(reps):
         t0 = time.perf_counter()
-        ssm_scan_ref(*args, D=Dn, clamp_mode="raw", dtype=np.float32)
-        times.append(time.perf_counter() - t0)
-    med = sorted(times)[len(times) // 2]
-    T, d_inner = d["x"].shape[1:]
-    S = d["B"].shape[2]
-    nbytes = scan_algorithmic_bytes(nseq, T, d_inner, S, 2)
-    return {"value": round(nbytes / med / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"{nseq} of {d['x'].shape[0]} config-1 sequences, numpy float32 sequential scan "
-                      f"(oracle/ssm_scan.py), median of {reps}: {med:.3f} s"}
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2]
+
+
+def _cpu_baseline(d, reps=3):
+    """The reference's sequential scan loop (ssm_scan_kernel.py:42-86, raw mode) as torch CPU ops
+    (oracle/torch_cpu.py) over the full config-1 input, on every host core."""
+    from oracle.torch_cpu import scan_torch
+    from hclsm_amd.workloads import scan_algorithmic_bytes
+    cores, model = _cpu_threads()
+    args = [d[k].float() if k in ("x", "dt", "B", "C") else d[k] for k in ("x", "dt", "A_log", "B", "C")]
+    med = _cpu_time(lambda: scan_torch(*args, D=d["D"], clamp_mode="raw"), reps)
+    n, T, d_inner = d["x"].shape
+    nbytes = scan_algorithmic_bytes(n, T, d_inner, d["B"].shape[2], 2)
+    return {"value": round(nbytes / med / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"full config 1 ({n} sequences), the reference's sequential loop as torch CPU ops "
+                      f"(oracle/torch_cpu.py), {cores} threads on {model}, median of {reps}: {med:.3f} s"}
 
 
 def _event_timing(fn, n, warmup):
@@ -109,20 +128,14 @@ def _bench_slot(dev, n, warmup, cpu):
            "roofline": {"bound": "mfma", "achieved": round(fl / med / 1e12, 3), "peak": 2500.0,
                         "unit": "TFLOP/s", "frac": round(fl / med / 1e12 / 2500.0, 5), "flops_per_call": fl}}
     if cpu:
-        from threadpoolctl import threadpool_limits
-        from oracle.slot_attention import slot_attention_forward as ref_fwd
-        tn, sn = tokens.numpy(), slots0.numpy()
-        wn = {k: t.numpy() for k, t in w.items()}
-        with threadpool_limits(1):
-            ts = []
-            for _ in range(3):
-                t0 = time.perf_counter()
-                ref_fwd(tn, sn, wn, 3, logit_clamp=None, renorm_eps=1e-8, slot_clamp=None)
-                ts.append(time.perf_counter() - t0)
-        cmed = sorted(ts)[1]
-        res["cpu_baseline"] = {"value": round(ntok / cmed, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
-                               "sample": f"full config 2, numpy float64 oracle (oracle/slot_attention.py), "
-                                         f"1 BLAS thread, median of 3: {cmed:.3f} s"}
+        from oracle.torch_cpu import slot_forward_torch
+        cores, model = _cpu_threads()
+        cmed = _cpu_time(lambda: slot_forward_torch(tokens, slots0, w, 3, logit_clamp=None, renorm_eps=1e-8,
+                                                    slot_clamp=None), 5)
+        res["cpu_baseline"] = {"value": round(ntok / cmed, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
+                               "sample": f"full config 2, the iteration's torch ops in fp32 on the CPU "
+                                         f"(oracle/torch_cpu.py), {cores} threads on {model}, median of 5: "
+                                         f"{cmed:.3f} s"}
     return res
 
 
@@ -151,20 +164,15 @@ def _bench_events(dev, n, warmup, cpu):
                          "unit": "GB/s", "frac": round(nbytes / med / 1e9 / HBM_PEAK_GBS, 5),
                          "bytes_per_call": nbytes}}
     if cpu:
-        from threadpoolctl import threadpool_limits
-        from oracle import events as oe
-        mn = m.cpu().numpy()
-        qn, kn, vn = (t.float().cpu().numpy() for t in (q, k, v))
-        with threadpool_limits(1):
-            ts = []
-            for _ in range(3):
-                t0 = time.perf_counter()
-                oe.track_causal_attention(qn, kn, vn, oe.event_index(mn))
-                ts.append(time.perf_counter() - t0)
-        cmed = sorted(ts)[1]
-        res["cpu_baseline"] = {"value": round(total / cmed, 1), "unit": "event-tokens/s", "cores": 1, "kind": "port",
-                               "sample": f"full config 3, numpy oracle index + per-track causal attention "
-                                         f"(oracle/events.py), 1 BLAS thread, median of 3: {cmed:.3f} s"}
+        from oracle.torch_cpu import event_attention_torch
+        cores, model = _cpu_threads()
+        qc, kc, vc, mc = (t.cpu() for t in (q, k, v, m))
+        cmed = _cpu_time(lambda: event_attention_torch(qc, kc, vc, mc), 3)
+        res["cpu_baseline"] = {"value": round(total / cmed, 1), "unit": "event-tokens/s", "cores": cores,
+                               "kind": "port",
+                               "sample": f"full config 3, nonzero gather + per-track causal SDPA as torch CPU ops "
+                                         f"(oracle/torch_cpu.py), {cores} threads on {model}, median of 3: "
+                                         f"{cmed:.3f} s"}
     return res
 
 
@@ -197,6 +205,42 @@ def _bench_block_scan(dev, n, warmup):
             "fused_us": round(fused_med * 1e6, 2), "unfused_us": round(unfused_med * 1e6, 2),
             "speedup": round(unfused_med / fused_med, 3), "fused_gbs": round(nbytes / fused_med / 1e9, 1),
             "fused_vs_unfused_normwise": err}
+
+
+def _bench_scan_bwd(dev, n, warmup):
+    """Reverse scan (gradients of sum(gy * y) for x, dt, A_log, B, C, D) at the config-1 shape, bf16, raw
+    mode, through the C ABI with a preallocated workspace; HBM roofline over the algorithmic bytes
+    (read x, dt, B, C, gy; write gx, gdt, gB, gC; A_log / D and their gradients)."""
+    import torch
+    from hclsm_amd import _lib
+    from hclsm_amd.workloads import scan_config
+    L = _lib.lib()
+    d = {k: v.to(dev) for k, v in scan_config(1).items()}
+    N, T, Dn = d["x"].shape
+    S = d["B"].shape[2]
+    gy = torch.randn_like(d["x"])
+    gx, gdt = torch.empty_like(d["x"]), torch.empty_like(d["dt"])
+    gB, gC = torch.empty_like(d["B"]), torch.empty_like(d["C"])
+    gA = torch.empty_like(d["A_log"])
+    gD = torch.empty_like(d["D"])
+    wsb = int(L.hclsm_ssm_scan_bwd_workspace(N, T, Dn, S))
+    ws = torch.empty(max(wsb, 256), dtype=torch.uint8, device=dev)
+    st = torch.cuda.current_stream(dev).cuda_stream
+
+    def step():
+        rc = L.hclsm_ssm_scan_bwd(d["x"].data_ptr(), d["dt"].data_ptr(), d["A_log"].data_ptr(), d["B"].data_ptr(),
+                                  d["C"].data_ptr(), d["D"].data_ptr(), gy.data_ptr(), gx.data_ptr(), gdt.data_ptr(),
+                                  gA.data_ptr(), gB.data_ptr(), gC.data_ptr(), gD.data_ptr(), N, T, Dn, S,
+                                  _lib.BF16, _lib.SCAN_RAW, ws.data_ptr(), ws.numel(), st)
+        if rc:
+            raise RuntimeError(_lib.strerror(rc))
+    med, _ = _event_timing(step, n, warmup)
+    nbytes = 2 * (N * T * Dn * 5 + N * T * S * 4) + 4 * (Dn * S + Dn) * 2
+    return {"workload": "scan backward, config-1 shape (1024 x 64 x 384, S=16, bf16, raw + D), one C call "
+                        "(checkpoint pass, reverse pass, finalize)",
+            "median_us": round(med * 1e6, 2), "workspace_bytes": wsb,
+            "roofline": {"bound": "hbm", "achieved": round(nbytes / med / 1e9, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(nbytes / med / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_call": nbytes}}
 
 
 def _bench_chain(dev, n, warmup):
@@ -369,6 +413,7 @@ def main():
         out["event_attn"] = _bench_events(dev, 100, 10, not args.no_cpu_baseline)
         out["chain"] = _bench_chain(dev, 20, 3)
         out["block_scan"] = _bench_block_scan(dev, 50, 5)
+        out["scan_bwd"] = _bench_scan_bwd(dev, 50, 5)
     print(json.dumps(out), flush=True)
 
 

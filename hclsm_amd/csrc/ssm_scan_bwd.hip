@@ -20,7 +20,11 @@
 
 namespace hclsm {
 
-constexpr int BWD_MAX_THREADS = 512;  // keeps 256 VGPRs per lane: the chunk states stay in registers
+// States per lane: all of a channel's states up to 16 (the B_t / C_t rows are then uniform across the
+// workgroup and read with scalar loads); d_state 32 / 64 use 2 / 4 lanes per channel.
+constexpr int bwd_sg(int SP) { return SP < 16 ? SP : 16; }
+// Lanes per workgroup: the chunk's recomputed states stay in registers (256 VGPRs at 384 lanes).
+constexpr int bwd_max_threads(int SP) { return bwd_sg(SP) >= 16 ? 384 : 512; }
 
 template <int V, int MASK_LO>
 struct RS {
@@ -63,7 +67,7 @@ struct BwdArgs {
 };
 
 template <int DT, int SP, int MODE>
-__global__ void __launch_bounds__(BWD_MAX_THREADS)
+__global__ void __launch_bounds__(bwd_max_threads(SP))
 ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename Elem<DT>::T* __restrict__ dt,
                     const float* __restrict__ A_log, const typename Elem<DT>::T* __restrict__ Bm,
                     const typename Elem<DT>::T* __restrict__ Cm, const float* __restrict__ Dskip,
@@ -72,12 +76,12 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
                     float* __restrict__ gA_part, float* __restrict__ gD_part, BwdArgs a) {
   using E = Elem<DT>;
   using TT = typename E::T;
-  constexpr int SG = SP < 8 ? SP : 8;
+  constexpr int SG = bwd_sg(SP);
   constexpr int G = SP / SG;
   constexpr int K = 64 / SG;
   constexpr int V = 2 * SG;                        // values reduced over channels: gB, gC
   constexpr int VL = RSCount<V, G>::value;        // values per lane after the reduce-scatter
-  constexpr int WMAX = BWD_MAX_THREADS / 64;
+  constexpr int WMAX = bwd_max_threads(SP) / 64;
   __shared__ float red[K][WMAX][2 * SP];           // per-chunk wave partials of gB | gC
   const int n = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, nw = blockDim.x >> 6;
@@ -99,20 +103,40 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
   }
   const float dsk = Dskip ? Dskip[dd] : 0.f;
   const size_t row0 = (size_t)n * T;
-  auto ldB = [&](int t, float* o) {
+  // 16-bit B / C rows with an even d_state and 4-byte alignment are read as 32-bit words: with one lane
+  // group per channel (G == 1) the address is uniform and the loads become scalar.
+  const bool words = sizeof(TT) == 2 && (S % 2) == 0 && ((reinterpret_cast<uintptr_t>(Bm) |
+                                                         reinterpret_cast<uintptr_t>(Cm)) & 3) == 0;
+  auto ld_row = [&](const TT* base, int t, float* o) {
+    const TT* p = base + (row0 + t) * S + s0;
+    if constexpr (sizeof(TT) == 2 && SG % 2 == 0) {
+      if (words) {
+        const uint32_t* pw = reinterpret_cast<const uint32_t*>(p);
+#pragma unroll
+        for (int w = 0; w < SG / 2; ++w) {
+          // unconditional load of a word inside the row (clamped index), then mask: S is even, so a
+          // word is all in or all out
+          const int wi = s0 + 2 * w < S ? w : (S - s0) / 2 - 1;
+          uint32_t v = pw[wi < 0 ? 0 : wi];
+          v = (s0 + 2 * w < S) ? v : 0u;
+          o[2 * w] = __uint_as_float(v << 16);
+          o[2 * w + 1] = __uint_as_float(v & 0xffff0000u);
+          if constexpr (DT == HCLSM_F16) {
+            o[2 * w] = (float)__builtin_bit_cast(_Float16, (uint16_t)(v & 0xffffu));
+            o[2 * w + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16));
+          }
+        }
+        return;
+      }
+    }
 #pragma unroll
     for (int j = 0; j < SG; ++j) {
       const int s = s0 + j;
-      o[j] = (s < S) ? E::ld(Bm + (row0 + t) * S + s) : 0.f;
+      o[j] = (s < S) ? E::ld(p + j) : 0.f;
     }
   };
-  auto ldC = [&](int t, float* o) {
-#pragma unroll
-    for (int j = 0; j < SG; ++j) {
-      const int s = s0 + j;
-      o[j] = (s < S) ? E::ld(Cm + (row0 + t) * S + s) : 0.f;
-    }
-  };
+  auto ldB = [&](int t, float* o) { ld_row(Bm, t, o); };
+  auto ldC = [&](int t, float* o) { ld_row(Cm, t, o); };
   auto dtc_of = [&](float v) { return (MODE == HCLSM_SCAN_MODEL) ? fminf(fmaxf(v, 1e-3f), 1.0f) : v; };
   float* ck = ckpt + (size_t)n * a.nchunk * a.ld_ck + (size_t)dd * SP + s0;
 
@@ -245,11 +269,33 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
   }
 }
 
-// gB, gC (dtype) from gbc; gA_log[d, s] = sum_n gA_part * dA/dA_log; gD[d] = sum_n gD_part.
+// out[c] = sum_n part[n * ncols + c]: 64 columns per workgroup, 16 row groups, reads coalesced along c.
+__global__ void __launch_bounds__(1024)
+ssm_scan_bwd_reduce(const float* __restrict__ part, int64_t N, int64_t ncols, float* __restrict__ out) {
+  __shared__ float red[16][64];
+  const int c = threadIdx.x & 63, rg = threadIdx.x >> 6;
+  const int64_t col = (int64_t)blockIdx.x * 64 + c;
+  float acc = 0.f;
+  if (col < ncols) {
+#pragma unroll 8
+    for (int64_t n = rg; n < N; n += 16) acc += part[n * ncols + col];
+  }
+  red[rg][c] = acc;
+  __syncthreads();
+  if (rg == 0 && col < ncols) {
+    float t = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) t += red[r][c];
+    out[col] = t;
+  }
+}
+
+// gB, gC (dtype) from gbc; gA_log[d, s] = (sum_n gA_part) * dA/dA_log; gD[d] = sum_n gD_part (both sums
+// already reduced into ga_sum / gd_sum).
 template <int DT, int SP, int MODE>
 __global__ void __launch_bounds__(256)
-ssm_scan_bwd_finalize(const float* __restrict__ gbc, const float* __restrict__ gA_part,
-                      const float* __restrict__ gD_part, const float* __restrict__ A_log,
+ssm_scan_bwd_finalize(const float* __restrict__ gbc, const float* __restrict__ ga_sum,
+                      const float* __restrict__ gd_sum, const float* __restrict__ A_log,
                       typename Elem<DT>::T* __restrict__ gB, typename Elem<DT>::T* __restrict__ gC,
                       float* __restrict__ gA_log, float* __restrict__ gD, int64_t N, int T, int Dn, int S) {
   using E = Elem<DT>;
@@ -263,32 +309,25 @@ ssm_scan_bwd_finalize(const float* __restrict__ gbc, const float* __restrict__ g
   }
   for (int64_t i = tid0; i < (int64_t)Dn * S; i += stride) {
     const int64_t dd = i / S, s = i - dd * S;
-    float acc = 0.f;
-    for (int64_t n = 0; n < N; ++n) acc += gA_part[(n * Dn + dd) * SP + s];
     const float e = expf(A_log[i]);
     float dadl = -e;                          // d(-exp(A_log))/dA_log
     if (MODE == HCLSM_SCAN_MODEL && !(e >= 1e-6f && e <= 1.0f)) dadl = 0.f;
-    gA_log[i] = acc * dadl;
+    gA_log[i] = ga_sum[dd * SP + s] * dadl;
   }
-  if (gD) {
-    for (int64_t dd = tid0; dd < Dn; dd += stride) {
-      float acc = 0.f;
-      for (int64_t n = 0; n < N; ++n) acc += gD_part[n * Dn + dd];
-      gD[dd] = acc;
-    }
-  }
+  if (gD)
+    for (int64_t dd = tid0; dd < Dn; dd += stride) gD[dd] = gd_sum[dd];
 }
 
 static int64_t sp_of(int64_t S) { return S <= 4 ? 4 : S <= 8 ? 8 : S <= 16 ? 16 : S <= 32 ? 32 : 64; }
 
 struct BwdWs {
-  size_t ck, gbc, ga, gd, total;
+  size_t ck, gbc, ga, gd, ga_sum, gd_sum, total;
   int nchunk;
 };
 
 static BwdWs bwd_ws(int64_t N, int64_t T, int64_t Dn, int64_t S) {
   const int64_t SP = sp_of(S);
-  const int64_t SG = SP < 8 ? SP : 8;
+  const int64_t SG = bwd_sg((int)SP);
   const int64_t K = 64 / SG;
   BwdWs w;
   w.nchunk = (int)((T + K - 1) / K);
@@ -298,6 +337,8 @@ static BwdWs bwd_ws(int64_t N, int64_t T, int64_t Dn, int64_t S) {
   w.gbc = o; o += al((size_t)N * T * 2 * SP * 4);
   w.ga = o; o += al((size_t)N * Dn * SP * 4);
   w.gd = o; o += al((size_t)N * Dn * 4);
+  w.ga_sum = o; o += al((size_t)Dn * SP * 4);
+  w.gd_sum = o; o += al((size_t)Dn * 4);
   w.total = o;
   return w;
 }
@@ -308,10 +349,10 @@ static int launch_bwd(const void* x, const void* dt, const float* A_log, const v
                       float* gD, char* ws, const BwdWs& L, int64_t N, int64_t T, int64_t Dn, int64_t S,
                       hipStream_t st) {
   using TT = typename Elem<DT>::T;
-  constexpr int SG = SP < 8 ? SP : 8;
+  constexpr int SG = bwd_sg(SP);
   constexpr int G = SP / SG;
   int DW = (int)Dn;
-  if ((int64_t)DW * G > BWD_MAX_THREADS) DW = BWD_MAX_THREADS / G;
+  if ((int64_t)DW * G > bwd_max_threads(SP)) DW = bwd_max_threads(SP) / G;
   const int nblk_d = (int)((Dn + DW - 1) / DW);
   int threads = DW * G;
   threads = (threads + 63) / 64 * 64;
@@ -328,11 +369,21 @@ static int launch_bwd(const void* x, const void* dt, const float* A_log, const v
                      (TT*)gdt, reinterpret_cast<float*>(ws + L.ck), gbc, reinterpret_cast<float*>(ws + L.ga),
                      reinterpret_cast<float*>(ws + L.gd), a);
   HCLSM_LAUNCH_CHECK();
+  float* ga_sum = reinterpret_cast<float*>(ws + L.ga_sum);
+  float* gd_sum = reinterpret_cast<float*>(ws + L.gd_sum);
+  const int64_t nga = Dn * SP;
+  hipLaunchKernelGGL(ssm_scan_bwd_reduce, dim3((unsigned)((nga + 63) / 64)), dim3(1024), 0, st,
+                     reinterpret_cast<const float*>(ws + L.ga), N, nga, ga_sum);
+  HCLSM_LAUNCH_CHECK();
+  if (gD) {
+    hipLaunchKernelGGL(ssm_scan_bwd_reduce, dim3((unsigned)((Dn + 63) / 64)), dim3(1024), 0, st,
+                       reinterpret_cast<const float*>(ws + L.gd), N, Dn, gd_sum);
+    HCLSM_LAUNCH_CHECK();
+  }
   int64_t g = (N * T * S + 255) / 256;
   g = g < 1 ? 1 : (g > 2048 ? 2048 : g);
-  hipLaunchKernelGGL((ssm_scan_bwd_finalize<DT, SP, MODE>), dim3((unsigned)g), dim3(256), 0, st, gbc,
-                     reinterpret_cast<const float*>(ws + L.ga), reinterpret_cast<const float*>(ws + L.gd), A_log,
-                     (TT*)gB, (TT*)gC, gA_log, gD, N, (int)T, (int)Dn, (int)S);
+  hipLaunchKernelGGL((ssm_scan_bwd_finalize<DT, SP, MODE>), dim3((unsigned)g), dim3(256), 0, st, gbc, ga_sum,
+                     gd_sum, A_log, (TT*)gB, (TT*)gC, gA_log, gD, N, (int)T, (int)Dn, (int)S);
   HCLSM_LAUNCH_CHECK();
   return 0;
 }
