@@ -7,6 +7,7 @@
 #include "../../include/hclsm_amd.h"
 
 #define HCLSM_LOG2E 1.4426950408889634f
+#define HCLSM_LN2 0.6931471805599453f
 
 namespace hclsm {
 

@@ -26,6 +26,42 @@ constexpr int bwd_sg(int SP) { return SP < 16 ? SP : 16; }
 // Lanes per workgroup: the chunk's recomputed states stay in registers (256 VGPRs at 384 lanes).
 constexpr int bwd_max_threads(int SP) { return bwd_sg(SP) >= 16 ? 384 : 512; }
 
+// Value of the partner lane across bit M for the reduce-scatter steps below 16 lanes.  The partner only
+// has to differ in bit M and agree in the bits above it; when every bit below M is reduced later too
+// (MASK_LO == 1) the DPP mirrors are used (lane ^ 15, lane ^ 7 inside a row), else exact xor partners.
+template <int M, int MASK_LO>
+__device__ __forceinline__ float rs_partner(float v) {
+  const int b = __float_as_int(v);
+  if constexpr (M == 8) {
+    return __int_as_float(MASK_LO == 1 ? __builtin_amdgcn_update_dpp(0, b, 0x140, 0xf, 0xf, true)     // row_mirror
+                                       : __builtin_amdgcn_update_dpp(0, b, 0x128, 0xf, 0xf, true));   // row_ror:8
+  } else if constexpr (M == 4) {
+    if constexpr (MASK_LO == 1)
+      return __int_as_float(__builtin_amdgcn_update_dpp(0, b, 0x141, 0xf, 0xf, true));   // row_half_mirror
+    else
+      return __shfl_xor(v, 4, 64);
+  } else if constexpr (M == 2) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, b, 0x4e, 0xf, 0xf, true));      // quad_perm 2,3,0,1
+  } else {
+    static_assert(M == 1, "rs_partner: M in {1, 2, 4, 8}");
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, b, 0xb1, 0xf, 0xf, true));      // quad_perm 1,0,3,2
+  }
+}
+
+// (lo, hi) -> lo summed over the lane pair for the lower lane, hi summed for the upper lane, where the
+// pair differs in bit 5 (M == 32) or bit 4 (M == 16): one gfx950 permlane swap exchanges the halves.
+template <int M>
+__device__ __forceinline__ float rs_swap_sum(float lo, float hi) {
+  if constexpr (M == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(lo), __float_as_uint(hi), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  } else {
+    static_assert(M == 16, "rs_swap_sum: M in {16, 32}");
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(lo), __float_as_uint(hi), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+}
+
 template <int V, int MASK_LO>
 struct RS {
   // Reduce-scatter V values across the lanes that differ in bits [MASK_LO, 32] of the lane id.
@@ -37,14 +73,19 @@ struct RS {
         const bool upper = (lane & M) != 0;
 #pragma unroll
         for (int i = 0; i < CNT / 2; ++i) {
-          const float keep = upper ? v[i + CNT / 2] : v[i];
-          const float send = upper ? v[i] : v[i + CNT / 2];
-          v[i] = keep + __shfl_xor(send, M, 64);
+          if constexpr (M >= 16) {
+            v[i] = rs_swap_sum<M>(v[i], v[i + CNT / 2]);
+          } else {
+            const float keep = upper ? v[i + CNT / 2] : v[i];
+            const float send = upper ? v[i] : v[i + CNT / 2];
+            v[i] = keep + rs_partner<M, MASK_LO>(send);
+          }
         }
         if (upper) off += CNT / 2;
         step<CNT / 2, M / 2>(v, lane, off);
       } else {
-        v[0] += __shfl_xor(v[0], M, 64);
+        if constexpr (M >= 16) v[0] = rs_swap_sum<M>(v[0], v[0]);
+        else v[0] += rs_partner<M, MASK_LO>(v[0]);
         step<1, M / 2>(v, lane, off);
       }
     }
@@ -79,8 +120,7 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
   constexpr int SG = bwd_sg(SP);
   constexpr int G = SP / SG;
   constexpr int K = 64 / SG;
-  constexpr int V = 2 * SG;                        // values reduced over channels: gB, gC
-  constexpr int VL = RSCount<V, G>::value;        // values per lane after the reduce-scatter
+  constexpr int VL = RSCount<SG, G>::value;       // values per lane after reduce-scattering gB (then gC)
   constexpr int WMAX = bwd_max_threads(SP) / 64;
   __shared__ float red[K][WMAX][2 * SP];           // per-chunk wave partials of gB | gC
   const int n = blockIdx.x;
@@ -92,14 +132,13 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
   const int s0 = gi * SG;
   const int T = a.T, Dn = a.Dn, S = a.S;
 
-  float a2[SG], aN[SG];   // A * log2(e) and A (natural) for this lane's states; padded states: 0
+  float a2[SG];   // A * log2(e) for this lane's states (padded states: 0); A = a2 * ln 2 where needed
 #pragma unroll
   for (int j = 0; j < SG; ++j) {
     const int s = s0 + j;
     const float e = expf(A_log[(size_t)dd * S + (s < S ? s : S - 1)]);
     const float ec = (MODE == HCLSM_SCAN_MODEL) ? fminf(fmaxf(e, 1e-6f), 1.0f) : e;
-    aN[j] = (s < S) ? -ec : 0.f;
-    a2[j] = aN[j] * HCLSM_LOG2E;
+    a2[j] = (s < S) ? -ec * HCLSM_LOG2E : 0.f;
   }
   const float dsk = Dskip ? Dskip[dd] : 0.f;
   const size_t row0 = (size_t)n * T;
@@ -201,47 +240,44 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
         float bv[SG], cv[SG];
         ldB(t, bv);
         ldC(t, cv);
-        float w[V];
-        float q = 0.f, gda = 0.f;
+        const float um = act ? u : 0.f;   // gy is zero on inactive lanes, so gh is too; um zeroes their gB terms
+        float w[SG];
+        float q = 0.f, gda2 = 0.f;   // gda2 = sum garg * A * log2(e); times ln 2 below
 #pragma unroll
         for (int j = 0; j < SG; ++j) {
           const float hp = (i > 0) ? hk[i > 0 ? i - 1 : 0][j] : h0[j];
           gh[j] = fmaf(gyv, cv[j], gh[j]);
-          w[SG + j] = gyv * hk[i][j];                  // -> gC
           const float gate = fast_exp2(dtv * a2[j]);
           const float garg = gh[j] * hp * gate;
-          gda = fmaf(garg, aN[j], gda);
+          gda2 = fmaf(garg, a2[j], gda2);
           gA[j] = fmaf(garg, dtv, gA[j]);
           q = fmaf(gh[j], bv[j], q);
-          w[j] = gh[j] * u;                            // -> gB
+          w[j] = gh[j] * um;                           // -> gB
           gh[j] *= gate;
         }
 #pragma unroll
         for (int m = 1; m < G; m <<= 1) {
           q += __shfl_xor(q, m, 64);
-          gda += __shfl_xor(gda, m, 64);
+          gda2 += __shfl_xor(gda2, m, 64);
         }
         if (gi == 0 && act) {
-          float gdv = gda + q * xv;
+          float gdv = fmaf(gda2, HCLSM_LN2, q * xv);
           if (MODE == HCLSM_SCAN_MODEL && !(draw >= 1e-3f && draw <= 1.0f)) gdv = 0.f;
           E::st(gx + (row0 + t) * Dn + d, fmaf(q, dtv, dsk * gyv));
           E::st(gdt + (row0 + t) * Dn + d, gdv);
           gD = fmaf(gyv, xv, gD);
         }
-        if (!act) {
+        // sums over the wave's channels: gB values, then gC values (16 at a time keeps registers low);
+        // lanes that differ only in bits below the last halving hold identical copies
 #pragma unroll
-          for (int j = 0; j < V; ++j) w[j] = 0.f;
-        }
-        const int off = RS<V, G>::run(w, lane);
-        // lanes sharing the reduced slot write identical values; only the lowest writes
-        const int rs_lo_bits = lane & (G - 1);   // state-group bits are not reduced
-        (void)rs_lo_bits;
+        for (int which = 0; which < 2; ++which) {
+          if (which == 1) {
 #pragma unroll
-        for (int e = 0; e < VL; ++e) {
-          const int vi = off + e;                       // 0..V-1 within this lane's group
-          const int which = vi / SG, j = vi - which * SG;
-          // duplicates: lanes that differ only in the bits below the last halving hold copies
-          red[i][wid][which * SP + s0 + j] = w[e];
+            for (int j = 0; j < SG; ++j) w[j] = gyv * hk[i][j];   // -> gC (gyv = 0 on inactive lanes)
+          }
+          const int off = RS<SG, G>::run(w, lane);
+#pragma unroll
+          for (int e = 0; e < VL; ++e) red[i][wid][which * SP + s0 + off + e] = w[e];
         }
       } else {
         // keep the LDS slots of missing steps at zero for the chunk sum below
