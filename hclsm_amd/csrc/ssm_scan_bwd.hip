@@ -107,6 +107,9 @@ struct BwdArgs {
   int64_t ld_ck;  // floats per (n, chunk) checkpoint slab = Dn * SP
 };
 
+// Steps of B / C rows staged in LDS at a time (a multiple of every chunk length K = 64 / SG).
+constexpr int BWD_WT = 64;
+
 template <int DT, int SP, int MODE>
 __global__ void __launch_bounds__(bwd_max_threads(SP))
 ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename Elem<DT>::T* __restrict__ dt,
@@ -116,13 +119,15 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
                     typename Elem<DT>::T* __restrict__ gdt, float* __restrict__ ckpt, float* __restrict__ gbc,
                     float* __restrict__ gA_part, float* __restrict__ gD_part, BwdArgs a) {
   using E = Elem<DT>;
-  using TT = typename E::T;
   constexpr int SG = bwd_sg(SP);
   constexpr int G = SP / SG;
   constexpr int K = 64 / SG;
   constexpr int VL = RSCount<SG, G>::value;       // values per lane after reduce-scattering gB (then gC)
   constexpr int WMAX = bwd_max_threads(SP) / 64;
+  static_assert(BWD_WT % K == 0, "an LDS window holds whole chunks");
   __shared__ float red[K][WMAX][2 * SP];           // per-chunk wave partials of gB | gC
+  __shared__ __align__(16) float sB[BWD_WT][SP];   // B / C rows of the current window, fp32, states >= S zero
+  __shared__ __align__(16) float sC[BWD_WT][SP];
   const int n = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, nw = blockDim.x >> 6;
   const int dl = tid / G, gi = tid - dl * G;
@@ -142,72 +147,98 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
   }
   const float dsk = Dskip ? Dskip[dd] : 0.f;
   const size_t row0 = (size_t)n * T;
-  // 16-bit B / C rows with an even d_state and 4-byte alignment are read as 32-bit words: with one lane
-  // group per channel (G == 1) the address is uniform and the loads become scalar.
-  const bool words = sizeof(TT) == 2 && (S % 2) == 0 && ((reinterpret_cast<uintptr_t>(Bm) |
-                                                         reinterpret_cast<uintptr_t>(Cm)) & 3) == 0;
-  auto ld_row = [&](const TT* base, int t, float* o) {
-    const TT* p = base + (row0 + t) * S + s0;
-    if constexpr (sizeof(TT) == 2 && SG % 2 == 0) {
-      if (words) {
-        const uint32_t* pw = reinterpret_cast<const uint32_t*>(p);
-#pragma unroll
-        for (int w = 0; w < SG / 2; ++w) {
-          // unconditional load of a word inside the row (clamped index), then mask: S is even, so a
-          // word is all in or all out
-          const int wi = s0 + 2 * w < S ? w : (S - s0) / 2 - 1;
-          uint32_t v = pw[wi < 0 ? 0 : wi];
-          v = (s0 + 2 * w < S) ? v : 0u;
-          o[2 * w] = __uint_as_float(v << 16);
-          o[2 * w + 1] = __uint_as_float(v & 0xffff0000u);
-          if constexpr (DT == HCLSM_F16) {
-            o[2 * w] = (float)__builtin_bit_cast(_Float16, (uint16_t)(v & 0xffffu));
-            o[2 * w + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16));
-          }
-        }
-        return;
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < SG; ++j) {
-      const int s = s0 + j;
-      o[j] = (s < S) ? E::ld(p + j) : 0.f;
+  if (S < SP)
+    for (int e = tid; e < BWD_WT * SP; e += blockDim.x)
+      if (e % SP >= S) { (&sB[0][0])[e] = 0.f; (&sC[0][0])[e] = 0.f; }
+  // rows [w0, w0 + wl) of B (and C): one contiguous span of wl * S elements each
+  auto stage = [&](int w0, int wl, bool with_c) {
+    const typename E::T* pb = Bm + (row0 + w0) * S;
+    const typename E::T* pc = Cm + (row0 + w0) * S;
+    for (int e = tid; e < wl * S; e += blockDim.x) {
+      const int r = e / S, s = e - r * S;
+      sB[r][s] = E::ld(pb + e);
+      if (with_c) sC[r][s] = E::ld(pc + e);
     }
   };
-  auto ldB = [&](int t, float* o) { ld_row(Bm, t, o); };
-  auto ldC = [&](int t, float* o) { ld_row(Cm, t, o); };
+  auto row = [&](const float (*src)[SP], int r, float* o) {
+#pragma unroll
+    for (int j = 0; j < SG; ++j) o[j] = src[r][s0 + j];
+  };
   auto dtc_of = [&](float v) { return (MODE == HCLSM_SCAN_MODEL) ? fminf(fmaxf(v, 1e-3f), 1.0f) : v; };
+  // x / dt (and gy) of chunk c into registers; steps past T repeat the last step (never used)
+  auto ld_chunk = [&](int c, float* xo, float* dto) {
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      const int t = (c * K + i < T) ? c * K + i : T - 1;
+      xo[i] = E::ld(x + (row0 + t) * Dn + dd);
+      dto[i] = E::ld(dt + (row0 + t) * Dn + dd);
+    }
+  };
   float* ck = ckpt + (size_t)n * a.nchunk * a.ld_ck + (size_t)dd * SP + s0;
 
-  // ---- pass 1: forward recompute, checkpoint at every chunk start
-  float h[SG];
+  // ---- pass 1: forward recompute, checkpoint at every chunk start; the next chunk's x / dt are in
+  // flight while a chunk is stepped
+  {
+    float h[SG];
 #pragma unroll
-  for (int j = 0; j < SG; ++j) h[j] = 0.f;
-  for (int c = 0; c < a.nchunk; ++c) {
-    if (act)
+    for (int j = 0; j < SG; ++j) h[j] = 0.f;
+    float xc[K], dc[K];
+    ld_chunk(0, xc, dc);
+    int wcur = -1;
+    for (int c = 0; c < a.nchunk; ++c) {
+      const int t0 = c * K, len = (t0 + K < T ? t0 + K : T) - t0;
+      const int w0 = t0 / BWD_WT * BWD_WT;
+      if (w0 != wcur) {
+        __syncthreads();
+        stage(w0, (w0 + BWD_WT < T ? w0 + BWD_WT : T) - w0, false);
+        __syncthreads();
+        wcur = w0;
+      }
+      float xn[K], dn[K];
+      ld_chunk(c + 1, xn, dn);
+      if (act)
 #pragma unroll
-      for (int j = 0; j < SG; ++j) ck[(size_t)c * a.ld_ck + j] = h[j];
-    const int t0 = c * K, t1 = (t0 + K < T) ? t0 + K : T;
-    for (int t = t0; t < t1; ++t) {
-      const float dtv = dtc_of(E::ld(dt + (row0 + t) * Dn + dd));
-      const float u = dtv * E::ld(x + (row0 + t) * Dn + dd);
-      float bv[SG];
-      ldB(t, bv);
+        for (int j = 0; j < SG; ++j) ck[(size_t)c * a.ld_ck + j] = h[j];
 #pragma unroll
-      for (int j = 0; j < SG; ++j) h[j] = fmaf(fast_exp2(dtv * a2[j]), h[j], u * bv[j]);
+      for (int i = 0; i < K; ++i) {
+        if (i < len) {
+          const float dtv = dtc_of(dc[i]);
+          const float u = dtv * xc[i];
+          float bv[SG];
+          row(sB, t0 + i - w0, bv);
+#pragma unroll
+          for (int j = 0; j < SG; ++j) h[j] = fmaf(fast_exp2(dtv * a2[j]), h[j], u * bv[j]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < K; ++i) { xc[i] = xn[i]; dc[i] = dn[i]; }
     }
   }
+  __syncthreads();   // pass 1's reads of the window are done before pass 2 restages it
 
-  // ---- pass 2: reverse
+  // ---- pass 2: reverse, one chunk at a time
   float gh[SG], gA[SG];
 #pragma unroll
   for (int j = 0; j < SG; ++j) { gh[j] = 0.f; gA[j] = 0.f; }
   float gD = 0.f;
+  int wcur = -1;
   for (int c = a.nchunk - 1; c >= 0; --c) {
-    const int t0 = c * K, len = ((t0 + K < T) ? t0 + K : T) - t0;
-    float h0[SG];
+    const int t0 = c * K, len = (t0 + K < T ? t0 + K : T) - t0;
+    const int w0 = t0 / BWD_WT * BWD_WT;
+    float h0[SG], xs[K], ds[K], gs[K];
 #pragma unroll
     for (int j = 0; j < SG; ++j) h0[j] = act ? ck[(size_t)c * a.ld_ck + j] : 0.f;
+    ld_chunk(c, xs, ds);
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      const int t = (t0 + i < T) ? t0 + i : T - 1;
+      gs[i] = act ? E::ld(gy + (row0 + t) * Dn + dd) : 0.f;
+    }
+    if (w0 != wcur) {   // the previous chunk ended on a barrier: no lane still reads the old window
+      stage(w0, (w0 + BWD_WT < T ? w0 + BWD_WT : T) - w0, true);
+      __syncthreads();
+      wcur = w0;
+    }
     float hk[K][SG];
     {
       float hc[SG];
@@ -216,11 +247,10 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
 #pragma unroll
       for (int i = 0; i < K; ++i) {
         if (i < len) {
-          const int t = t0 + i;
-          const float dtv = dtc_of(E::ld(dt + (row0 + t) * Dn + dd));
-          const float u = dtv * E::ld(x + (row0 + t) * Dn + dd);
+          const float dtv = dtc_of(ds[i]);
+          const float u = dtv * xs[i];
           float bv[SG];
-          ldB(t, bv);
+          row(sB, t0 + i - w0, bv);
 #pragma unroll
           for (int j = 0; j < SG; ++j) hc[j] = fmaf(fast_exp2(dtv * a2[j]), hc[j], u * bv[j]);
         }
@@ -228,19 +258,23 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
         for (int j = 0; j < SG; ++j) hk[i][j] = hc[j];
       }
     }
+    // the reverse steps recompute the gates and reread the rows instead of keeping the recompute's
+    // K * SG values live (registers are the occupancy limit): hide both from CSE
+    asm volatile("" ::: "memory");
 #pragma unroll
     for (int i = K - 1; i >= 0; --i) {
       if (i < len) {
         const int t = t0 + i;
-        const float draw = E::ld(dt + (row0 + t) * Dn + dd);
-        const float dtv = dtc_of(draw);
-        const float xv = E::ld(x + (row0 + t) * Dn + dd);
-        const float gyv = act ? E::ld(gy + (row0 + t) * Dn + dd) : 0.f;
+        const float draw = ds[i];
+        float dtv = dtc_of(draw);
+        asm volatile("" : "+v"(dtv));
+        const float xv = xs[i];
+        const float gyv = gs[i];
         const float u = dtv * xv;
-        float bv[SG], cv[SG];
-        ldB(t, bv);
-        ldC(t, cv);
         const float um = act ? u : 0.f;   // gy is zero on inactive lanes, so gh is too; um zeroes their gB terms
+        float bv[SG], cv[SG];
+        row(sB, t - w0, bv);
+        row(sC, t - w0, cv);
         float w[SG];
         float q = 0.f, gda2 = 0.f;   // gda2 = sum garg * A * log2(e); times ln 2 below
 #pragma unroll
