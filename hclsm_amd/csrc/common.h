@@ -50,6 +50,31 @@ template <> struct Elem<HCLSM_F16> {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Word 3 of a gfx9-family buffer resource for raw (stride 0) byte addressing: loads at or past
+// num_records bytes return 0, stores there are dropped.
+constexpr int kRawBufferWord3 = 0x00020000;
+
+// One element through a raw buffer resource: byte offset = vo (per lane) + so (uniform).
+template <int DT>
+__device__ __forceinline__ float buf_ld(__amdgpu_buffer_rsrc_t r, int vo, int so) {
+  if constexpr (DT == HCLSM_F32) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, vo, so, 0));
+  } else {
+    const uint16_t b = __builtin_amdgcn_raw_buffer_load_b16(r, vo, so, 0);
+    if constexpr (DT == HCLSM_BF16) return bf16_bits_to_f32(b);
+    else return (float)__builtin_bit_cast(_Float16, b);
+  }
+}
+template <int DT>
+__device__ __forceinline__ void buf_st(float v, __amdgpu_buffer_rsrc_t r, int vo, int so) {
+  if constexpr (DT == HCLSM_F32)
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, vo, so, 0);
+  else if constexpr (DT == HCLSM_BF16)
+    __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(v), r, vo, so, 0);
+  else
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (_Float16)v), r, vo, so, 0);
+}
+
 }  // namespace hclsm
 
 // Launch helper: returns a hipError_t as int (0 on success).

@@ -439,9 +439,6 @@ static int launch_scan_sgpr(const void* x, const void* dt, const float* A_log, c
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-// Word 3 of a gfx9-family buffer resource for raw (stride 0) byte addressing.
-constexpr int kRawBufferWord3 = 0x00020000;
-
 template <int MODE, int TC, int DPL>
 __global__ void __launch_bounds__(64)
 ssm_scan_fwd_mfma_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ dt,

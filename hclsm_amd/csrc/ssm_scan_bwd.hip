@@ -9,22 +9,33 @@
 // (model mode: each clamp passes gradient only inside its closed interval).
 //
 // Mapping: one lane owns channel d of sequence n and SG <= 8 of its states (G = d_state/SG lanes
-// per channel, adjacent).  Pass 1 recomputes h forward and writes the state at every chunk
-// start (chunks of K = 64/SG steps) to a checkpoint buffer.  Pass 2 walks the chunks backwards:
-// it recomputes the chunk's states into registers, then runs the reverse recurrence step by step.
-// Sums over the state axis (gx, gdt) are xor shuffles inside the G-lane group; sums over the
-// channel axis (gB, gC) are a recursive-halving reduce-scatter across the wave's channels followed
-// by a cross-wave sum through LDS once per chunk.  A second kernel casts gB/gC and reduces the
-// per-sequence partials of gA_log and gD.
+// per channel, adjacent); a workgroup holds up to 384 lanes of one sequence's channels.  Pass 1
+// recomputes h forward and writes the state at every chunk start (chunks of K = 32/SG steps) to a
+// checkpoint buffer.  Pass 2 walks the chunks backwards: it recomputes the chunk's states into
+// registers, then runs the reverse recurrence step by step.  B_t / C_t rows are staged in LDS as fp32,
+// 64 steps at a time.  Sums over the state axis (gx, gdt) are DPP sums inside the G-lane group; sums
+// over the channel axis (gB, gC) are a recursive-halving reduce-scatter across the wave's channels
+// followed by a cross-wave sum through LDS once per chunk, one part per channel block.  Small kernels
+// then reduce the per-sequence partials of gA_log and gD, and add the blocks' gB / gC parts and cast.
 #include "common.h"
 
 namespace hclsm {
 
-// States per lane: all of a channel's states up to 16 (the B_t / C_t rows are then uniform across the
-// workgroup and read with scalar loads); d_state 32 / 64 use 2 / 4 lanes per channel.
+// States per lane: all of a channel's states up to 16 (G = SP / SG adjacent lanes per channel for
+// d_state 32 / 64).  Chunks of K = 64 / SG steps: the chunk's recomputed states (64 floats) stay in
+// registers.
 constexpr int bwd_sg(int SP) { return SP < 16 ? SP : 16; }
-// Lanes per workgroup: the chunk's recomputed states stay in registers (256 VGPRs at 384 lanes).
-constexpr int bwd_max_threads(int SP) { return bwd_sg(SP) >= 16 ? 384 : 512; }
+constexpr int bwd_k(int SP) { return 64 / bwd_sg(SP); }
+// Lanes per workgroup (six waves).
+constexpr int BWD_MAX_THREADS = 384;
+
+// Channels per workgroup and workgroups per sequence: the channels of a sequence split evenly.
+struct BwdGrid { int DW, nblk; };
+static inline BwdGrid bwd_grid(int64_t Dn, int G) {
+  const int64_t nblk = (Dn * G + BWD_MAX_THREADS - 1) / BWD_MAX_THREADS;
+  const int64_t nb = nblk < 1 ? 1 : nblk;
+  return BwdGrid{(int)((Dn + nb - 1) / nb), (int)nb};
+}
 
 // Value of the partner lane across bit M for the reduce-scatter steps below 16 lanes.  The partner only
 // has to differ in bit M and agree in the bits above it; when every bit below M is reduced later too
@@ -60,6 +71,16 @@ __device__ __forceinline__ float rs_swap_sum(float lo, float hi) {
     const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(lo), __float_as_uint(hi), false, false);
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
   }
+}
+
+// Sum over the G adjacent lanes of a channel (G a power of two <= 8), every lane gets the total.
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr (G >= 2) v += rs_partner<1, 1>(v);
+  if constexpr (G >= 4) v += rs_partner<2, 1>(v);
+  if constexpr (G >= 8) v += rs_partner<4, 1>(v);   // lane ^ 7: the other quad of the 8-lane group
+  static_assert(G <= 8, "group_sum: at most 8 lanes");
+  return v;
 }
 
 template <int V, int MASK_LO>
@@ -107,27 +128,27 @@ struct BwdArgs {
   int64_t ld_ck;  // floats per (n, chunk) checkpoint slab = Dn * SP
 };
 
-// Steps of B / C rows staged in LDS at a time (a multiple of every chunk length K = 64 / SG).
+// Steps of B / C rows staged in LDS at a time (a multiple of every chunk length K).
 constexpr int BWD_WT = 64;
 
 template <int DT, int SP, int MODE>
-__global__ void __launch_bounds__(bwd_max_threads(SP))
+__global__ void __launch_bounds__(BWD_MAX_THREADS)
 ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename Elem<DT>::T* __restrict__ dt,
                     const float* __restrict__ A_log, const typename Elem<DT>::T* __restrict__ Bm,
                     const typename Elem<DT>::T* __restrict__ Cm, const float* __restrict__ Dskip,
                     const typename Elem<DT>::T* __restrict__ gy, typename Elem<DT>::T* __restrict__ gx,
                     typename Elem<DT>::T* __restrict__ gdt, float* __restrict__ ckpt, float* __restrict__ gbc,
                     float* __restrict__ gA_part, float* __restrict__ gD_part, BwdArgs a) {
-  using E = Elem<DT>;
+  constexpr int ES = (int)sizeof(typename Elem<DT>::T);
   constexpr int SG = bwd_sg(SP);
   constexpr int G = SP / SG;
-  constexpr int K = 64 / SG;
+  constexpr int K = bwd_k(SP);
   constexpr int VL = RSCount<SG, G>::value;       // values per lane after reduce-scattering gB (then gC)
-  constexpr int WMAX = bwd_max_threads(SP) / 64;
+  constexpr int WMAX = BWD_MAX_THREADS / 64;
   static_assert(BWD_WT % K == 0, "an LDS window holds whole chunks");
   __shared__ float red[K][WMAX][2 * SP];           // per-chunk wave partials of gB | gC
-  __shared__ __align__(16) float sB[BWD_WT][SP];   // B / C rows of the current window, fp32, states >= S zero
-  __shared__ __align__(16) float sC[BWD_WT][SP];
+  __shared__ __align__(16) float sB[BWD_WT][SP];   // B / C rows of the current window, fp32; states >= S
+  __shared__ __align__(16) float sC[BWD_WT][SP];   // and steps >= T are zero
   const int n = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, nw = blockDim.x >> 6;
   const int dl = tid / G, gi = tid - dl * G;
@@ -146,32 +167,51 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
     a2[j] = (s < S) ? -ec * HCLSM_LOG2E : 0.f;
   }
   const float dsk = Dskip ? Dskip[dd] : 0.f;
+
+  // Per-sequence buffer resources, byte offset = lane part + step * pitch.  Steps at or past T read 0
+  // (so a chunk's missing steps have dt = x = gy = 0 and B = C = 0: the state passes through unchanged)
+  // and stores there are dropped; lanes without a channel store past the slab.
   const size_t row0 = (size_t)n * T;
+  const unsigned pitch = (unsigned)Dn * ES;
+  const int slab = (int)(T * pitch);               // < 2^31: checked by the entry point
+  const auto rx = __builtin_amdgcn_make_buffer_rsrc((void*)(x + row0 * Dn), 0, slab, kRawBufferWord3);
+  const auto rdt = __builtin_amdgcn_make_buffer_rsrc((void*)(dt + row0 * Dn), 0, slab, kRawBufferWord3);
+  const auto rgy = __builtin_amdgcn_make_buffer_rsrc((void*)(gy + row0 * Dn), 0, slab, kRawBufferWord3);
+  const auto rgx = __builtin_amdgcn_make_buffer_rsrc((void*)(gx + row0 * Dn), 0, slab, kRawBufferWord3);
+  const auto rgdt = __builtin_amdgcn_make_buffer_rsrc((void*)(gdt + row0 * Dn), 0, slab, kRawBufferWord3);
+  const auto rb = __builtin_amdgcn_make_buffer_rsrc((void*)(Bm + row0 * S), 0, T * S * ES, kRawBufferWord3);
+  const auto rc = __builtin_amdgcn_make_buffer_rsrc((void*)(Cm + row0 * S), 0, T * S * ES, kRawBufferWord3);
+  const int vo = dd * ES;
+  const int vo_st = (act && gi == 0) ? d * ES : 0x7ffffff0;
+
   if (S < SP)
     for (int e = tid; e < BWD_WT * SP; e += blockDim.x)
       if (e % SP >= S) { (&sB[0][0])[e] = 0.f; (&sC[0][0])[e] = 0.f; }
-  // rows [w0, w0 + wl) of B (and C): one contiguous span of wl * S elements each
-  auto stage = [&](int w0, int wl, bool with_c) {
-    const typename E::T* pb = Bm + (row0 + w0) * S;
-    const typename E::T* pc = Cm + (row0 + w0) * S;
-    for (int e = tid; e < wl * S; e += blockDim.x) {
+  // rows [w0, w0 + BWD_WT) of B (and C) as fp32; rows past T read as zero
+  auto stage = [&](int w0, bool with_c) {
+    for (int e = tid; e < BWD_WT * S; e += blockDim.x) {
       const int r = e / S, s = e - r * S;
-      sB[r][s] = E::ld(pb + e);
-      if (with_c) sC[r][s] = E::ld(pc + e);
+      const int off = (w0 * S + e) * ES;
+      sB[r][s] = buf_ld<DT>(rb, off, 0);
+      if (with_c) sC[r][s] = buf_ld<DT>(rc, off, 0);
     }
   };
   auto row = [&](const float (*src)[SP], int r, float* o) {
 #pragma unroll
     for (int j = 0; j < SG; ++j) o[j] = src[r][s0 + j];
   };
-  auto dtc_of = [&](float v) { return (MODE == HCLSM_SCAN_MODEL) ? fminf(fmaxf(v, 1e-3f), 1.0f) : v; };
-  // x / dt (and gy) of chunk c into registers; steps past T repeat the last step (never used)
+  // dt as the recurrence uses it; 0 for a missing step (its raw dt reads 0, which the model clamp
+  // would lift to 1e-3)
+  auto dt_of = [&](float v, bool live) {
+    if constexpr (MODE == HCLSM_SCAN_MODEL) return live ? fminf(fmaxf(v, 1e-3f), 1.0f) : 0.f;
+    else return v;
+  };
   auto ld_chunk = [&](int c, float* xo, float* dto) {
 #pragma unroll
     for (int i = 0; i < K; ++i) {
-      const int t = (c * K + i < T) ? c * K + i : T - 1;
-      xo[i] = E::ld(x + (row0 + t) * Dn + dd);
-      dto[i] = E::ld(dt + (row0 + t) * Dn + dd);
+      const int so = (int)((unsigned)(c * K + i) * pitch);   // past the slab for steps >= T: reads 0
+      xo[i] = buf_ld<DT>(rx, vo, so);
+      dto[i] = buf_ld<DT>(rdt, vo, so);
     }
   };
   float* ck = ckpt + (size_t)n * a.nchunk * a.ld_ck + (size_t)dd * SP + s0;
@@ -190,7 +230,7 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
       const int w0 = t0 / BWD_WT * BWD_WT;
       if (w0 != wcur) {
         __syncthreads();
-        stage(w0, (w0 + BWD_WT < T ? w0 + BWD_WT : T) - w0, false);
+        stage(w0, false);
         __syncthreads();
         wcur = w0;
       }
@@ -201,14 +241,12 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
         for (int j = 0; j < SG; ++j) ck[(size_t)c * a.ld_ck + j] = h[j];
 #pragma unroll
       for (int i = 0; i < K; ++i) {
-        if (i < len) {
-          const float dtv = dtc_of(dc[i]);
-          const float u = dtv * xc[i];
-          float bv[SG];
-          row(sB, t0 + i - w0, bv);
+        const float dtv = dt_of(dc[i], i < len);
+        const float u = dtv * xc[i];
+        float bv[SG];
+        row(sB, t0 + i - w0, bv);
 #pragma unroll
-          for (int j = 0; j < SG; ++j) h[j] = fmaf(fast_exp2(dtv * a2[j]), h[j], u * bv[j]);
-        }
+        for (int j = 0; j < SG; ++j) h[j] = fmaf(fast_exp2(dtv * a2[j]), h[j], u * bv[j]);
       }
 #pragma unroll
       for (int i = 0; i < K; ++i) { xc[i] = xn[i]; dc[i] = dn[i]; }
@@ -231,11 +269,11 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
     ld_chunk(c, xs, ds);
 #pragma unroll
     for (int i = 0; i < K; ++i) {
-      const int t = (t0 + i < T) ? t0 + i : T - 1;
-      gs[i] = act ? E::ld(gy + (row0 + t) * Dn + dd) : 0.f;
+      const float v = buf_ld<DT>(rgy, vo, (int)((unsigned)(t0 + i) * pitch));
+      gs[i] = act ? v : 0.f;
     }
     if (w0 != wcur) {   // the previous chunk ended on a barrier: no lane still reads the old window
-      stage(w0, (w0 + BWD_WT < T ? w0 + BWD_WT : T) - w0, true);
+      stage(w0, true);
       __syncthreads();
       wcur = w0;
     }
@@ -246,16 +284,15 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
       for (int j = 0; j < SG; ++j) hc[j] = h0[j];
 #pragma unroll
       for (int i = 0; i < K; ++i) {
-        if (i < len) {
-          const float dtv = dtc_of(ds[i]);
-          const float u = dtv * xs[i];
-          float bv[SG];
-          row(sB, t0 + i - w0, bv);
+        const float dtv = dt_of(ds[i], i < len);
+        const float u = dtv * xs[i];
+        float bv[SG];
+        row(sB, t0 + i - w0, bv);
 #pragma unroll
-          for (int j = 0; j < SG; ++j) hc[j] = fmaf(fast_exp2(dtv * a2[j]), hc[j], u * bv[j]);
+        for (int j = 0; j < SG; ++j) {
+          hc[j] = fmaf(fast_exp2(dtv * a2[j]), hc[j], u * bv[j]);
+          hk[i][j] = hc[j];
         }
-#pragma unroll
-        for (int j = 0; j < SG; ++j) hk[i][j] = hc[j];
       }
     }
     // the reverse steps recompute the gates and reread the rows instead of keeping the recompute's
@@ -263,59 +300,48 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
     asm volatile("" ::: "memory");
 #pragma unroll
     for (int i = K - 1; i >= 0; --i) {
-      if (i < len) {
-        const int t = t0 + i;
-        const float draw = ds[i];
-        float dtv = dtc_of(draw);
-        asm volatile("" : "+v"(dtv));
-        const float xv = xs[i];
-        const float gyv = gs[i];
-        const float u = dtv * xv;
-        const float um = act ? u : 0.f;   // gy is zero on inactive lanes, so gh is too; um zeroes their gB terms
-        float bv[SG], cv[SG];
-        row(sB, t - w0, bv);
-        row(sC, t - w0, cv);
-        float w[SG];
-        float q = 0.f, gda2 = 0.f;   // gda2 = sum garg * A * log2(e); times ln 2 below
+      const int t = t0 + i;
+      const float draw = ds[i];
+      float dtv = dt_of(draw, i < len);
+      asm volatile("" : "+v"(dtv));
+      const float xv = xs[i];
+      const float gyv = gs[i];
+      const float um = act ? dtv * xv : 0.f;   // gy is zero on inactive lanes, so gh is too; um zeroes their gB terms
+      float bv[SG], cv[SG];
+      row(sB, t - w0, bv);
+      row(sC, t - w0, cv);
+      float w[SG];
+      float q = 0.f, gda2 = 0.f;   // gda2 = sum garg * A * log2(e); times ln 2 below
 #pragma unroll
-        for (int j = 0; j < SG; ++j) {
-          const float hp = (i > 0) ? hk[i > 0 ? i - 1 : 0][j] : h0[j];
-          gh[j] = fmaf(gyv, cv[j], gh[j]);
-          const float gate = fast_exp2(dtv * a2[j]);
-          const float garg = gh[j] * hp * gate;
-          gda2 = fmaf(garg, a2[j], gda2);
-          gA[j] = fmaf(garg, dtv, gA[j]);
-          q = fmaf(gh[j], bv[j], q);
-          w[j] = gh[j] * um;                           // -> gB
-          gh[j] *= gate;
+      for (int j = 0; j < SG; ++j) {
+        const float hp = (i > 0) ? hk[i > 0 ? i - 1 : 0][j] : h0[j];
+        gh[j] = fmaf(gyv, cv[j], gh[j]);
+        q = fmaf(gh[j], bv[j], q);
+        w[j] = gh[j] * um;                           // -> gB
+        gh[j] *= fast_exp2(dtv * a2[j]);             // carried to step t-1
+        const float garg = gh[j] * hp;               // gh_t h_{t-1} exp(dt A)
+        gda2 = fmaf(garg, a2[j], gda2);
+        gA[j] = fmaf(garg, dtv, gA[j]);
+      }
+      q = group_sum<G>(q);
+      gda2 = group_sum<G>(gda2);
+      float gdv = fmaf(gda2, HCLSM_LN2, q * xv);
+      if (MODE == HCLSM_SCAN_MODEL && !(draw >= 1e-3f && draw <= 1.0f)) gdv = 0.f;
+      const int so = (i < len) ? (int)((unsigned)t * pitch) : slab;   // a missing step stores nothing
+      buf_st<DT>(fmaf(q, dtv, dsk * gyv), rgx, vo_st, so);
+      buf_st<DT>(gdv, rgdt, vo_st, so);
+      gD = fmaf(gyv, xv, gD);
+      // sums over the wave's channels: gB values, then gC values (16 at a time keeps registers low);
+      // lanes that differ only in bits below the last halving hold identical copies
+#pragma unroll
+      for (int which = 0; which < 2; ++which) {
+        if (which == 1) {
+#pragma unroll
+          for (int j = 0; j < SG; ++j) w[j] = gyv * hk[i][j];   // -> gC (gyv = 0 on inactive lanes)
         }
+        const int off = RS<SG, G>::run(w, lane);
 #pragma unroll
-        for (int m = 1; m < G; m <<= 1) {
-          q += __shfl_xor(q, m, 64);
-          gda2 += __shfl_xor(gda2, m, 64);
-        }
-        if (gi == 0 && act) {
-          float gdv = fmaf(gda2, HCLSM_LN2, q * xv);
-          if (MODE == HCLSM_SCAN_MODEL && !(draw >= 1e-3f && draw <= 1.0f)) gdv = 0.f;
-          E::st(gx + (row0 + t) * Dn + d, fmaf(q, dtv, dsk * gyv));
-          E::st(gdt + (row0 + t) * Dn + d, gdv);
-          gD = fmaf(gyv, xv, gD);
-        }
-        // sums over the wave's channels: gB values, then gC values (16 at a time keeps registers low);
-        // lanes that differ only in bits below the last halving hold identical copies
-#pragma unroll
-        for (int which = 0; which < 2; ++which) {
-          if (which == 1) {
-#pragma unroll
-            for (int j = 0; j < SG; ++j) w[j] = gyv * hk[i][j];   // -> gC (gyv = 0 on inactive lanes)
-          }
-          const int off = RS<SG, G>::run(w, lane);
-#pragma unroll
-          for (int e = 0; e < VL; ++e) red[i][wid][which * SP + s0 + off + e] = w[e];
-        }
-      } else {
-        // keep the LDS slots of missing steps at zero for the chunk sum below
-        for (int e = lane; e < 2 * SP; e += 64) red[i][wid][e] = 0.f;
+        for (int e = 0; e < VL; ++e) red[i][wid][which * SP + s0 + off + e] = w[e];
       }
     }
     __syncthreads();
@@ -325,9 +351,7 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
       if (i < len) {
         float sacc = 0.f;
         for (int w = 0; w < nw; ++w) sacc += red[i][w][v];
-        float* dst = gbc + ((size_t)n * T + t0 + i) * 2 * SP + v;
-        if (gridDim.y > 1) atomicAdd(dst, sacc);
-        else *dst = sacc;
+        gbc[(((size_t)blockIdx.y * gridDim.x + n) * T + t0 + i) * 2 * SP + v] = sacc;   // this block's part
       }
     }
     __syncthreads();
@@ -360,22 +384,29 @@ ssm_scan_bwd_reduce(const float* __restrict__ part, int64_t N, int64_t ncols, fl
   }
 }
 
-// gB, gC (dtype) from gbc; gA_log[d, s] = (sum_n gA_part) * dA/dA_log; gD[d] = sum_n gD_part (both sums
+// gB, gC (dtype) from the channel blocks' parts in gbc (summed in block order); gA_log[d, s] = (sum_n gA_part) * dA/dA_log; gD[d] = sum_n gD_part (both sums
 // already reduced into ga_sum / gd_sum).
 template <int DT, int SP, int MODE>
 __global__ void __launch_bounds__(256)
 ssm_scan_bwd_finalize(const float* __restrict__ gbc, const float* __restrict__ ga_sum,
                       const float* __restrict__ gd_sum, const float* __restrict__ A_log,
                       typename Elem<DT>::T* __restrict__ gB, typename Elem<DT>::T* __restrict__ gC,
-                      float* __restrict__ gA_log, float* __restrict__ gD, int64_t N, int T, int Dn, int S) {
+                      float* __restrict__ gA_log, float* __restrict__ gD, int64_t N, int T, int Dn, int S,
+                      int nblk) {
   using E = Elem<DT>;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   const int64_t tid0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t nbc = N * T * S;
+  const int64_t part = N * T * 2 * SP;   // floats per channel block's partial
   for (int64_t i = tid0; i < nbc; i += stride) {
     const int64_t r = i / S, s = i - r * S;
-    E::st(gB + i, gbc[r * 2 * SP + s]);
-    E::st(gC + i, gbc[r * 2 * SP + SP + s]);
+    float b = 0.f, c = 0.f;
+    for (int k = 0; k < nblk; ++k) {   // fixed order: deterministic
+      b += gbc[k * part + r * 2 * SP + s];
+      c += gbc[k * part + r * 2 * SP + SP + s];
+    }
+    E::st(gB + i, b);
+    E::st(gC + i, c);
   }
   for (int64_t i = tid0; i < (int64_t)Dn * S; i += stride) {
     const int64_t dd = i / S, s = i - dd * S;
@@ -393,18 +424,20 @@ static int64_t sp_of(int64_t S) { return S <= 4 ? 4 : S <= 8 ? 8 : S <= 16 ? 16 
 struct BwdWs {
   size_t ck, gbc, ga, gd, ga_sum, gd_sum, total;
   int nchunk;
+  BwdGrid grid;
 };
 
 static BwdWs bwd_ws(int64_t N, int64_t T, int64_t Dn, int64_t S) {
   const int64_t SP = sp_of(S);
   const int64_t SG = bwd_sg((int)SP);
-  const int64_t K = 64 / SG;
+  const int64_t K = bwd_k((int)SP);
   BwdWs w;
   w.nchunk = (int)((T + K - 1) / K);
+  w.grid = bwd_grid(Dn, (int)(SP / SG));
   auto al = [](size_t v) { return (v + 255) / 256 * 256; };
   size_t o = 0;
   w.ck = o; o += al((size_t)N * w.nchunk * Dn * SP * 4);
-  w.gbc = o; o += al((size_t)N * T * 2 * SP * 4);
+  w.gbc = o; o += al((size_t)w.grid.nblk * N * T * 2 * SP * 4);
   w.ga = o; o += al((size_t)N * Dn * SP * 4);
   w.gd = o; o += al((size_t)N * Dn * 4);
   w.ga_sum = o; o += al((size_t)Dn * SP * 4);
@@ -421,19 +454,13 @@ static int launch_bwd(const void* x, const void* dt, const float* A_log, const v
   using TT = typename Elem<DT>::T;
   constexpr int SG = bwd_sg(SP);
   constexpr int G = SP / SG;
-  int DW = (int)Dn;
-  if ((int64_t)DW * G > bwd_max_threads(SP)) DW = bwd_max_threads(SP) / G;
-  const int nblk_d = (int)((Dn + DW - 1) / DW);
+  const int DW = L.grid.DW, nblk_d = L.grid.nblk;
   int threads = DW * G;
   threads = (threads + 63) / 64 * 64;
   BwdArgs a;
   a.T = (int)T; a.Dn = (int)Dn; a.S = (int)S; a.nchunk = L.nchunk; a.DW = DW;
   a.ld_ck = Dn * SP;
   float* gbc = reinterpret_cast<float*>(ws + L.gbc);
-  if (nblk_d > 1) {
-    const int rc = zero_fill_f32(gbc, N * T * 2 * SP, st);
-    if (rc) return rc;
-  }
   hipLaunchKernelGGL((ssm_scan_bwd_kernel<DT, SP, MODE>), dim3((unsigned)N, (unsigned)nblk_d), dim3(threads), 0, st,
                      (const TT*)x, (const TT*)dt, A_log, (const TT*)B, (const TT*)C, Dskip, (const TT*)gy, (TT*)gx,
                      (TT*)gdt, reinterpret_cast<float*>(ws + L.ck), gbc, reinterpret_cast<float*>(ws + L.ga),
@@ -453,7 +480,7 @@ static int launch_bwd(const void* x, const void* dt, const float* A_log, const v
   int64_t g = (N * T * S + 255) / 256;
   g = g < 1 ? 1 : (g > 2048 ? 2048 : g);
   hipLaunchKernelGGL((ssm_scan_bwd_finalize<DT, SP, MODE>), dim3((unsigned)g), dim3(256), 0, st, gbc, ga_sum,
-                     gd_sum, A_log, (TT*)gB, (TT*)gC, gA_log, gD, N, (int)T, (int)Dn, (int)S);
+                     gd_sum, A_log, (TT*)gB, (TT*)gC, gA_log, gD, N, (int)T, (int)Dn, (int)S, nblk_d);
   HCLSM_LAUNCH_CHECK();
   return 0;
 }
@@ -474,6 +501,8 @@ extern "C" int hclsm_ssm_scan_bwd(const void* x, const void* dt, const float* A_
   if (batch < 0 || T < 0 || d_inner < 0 || d_state < 1) return HCLSM_ERR_SHAPE;
   if (batch > 0x7fffffffLL || T > 0x7fffffffLL || d_inner > 0x7fffffffLL) return HCLSM_ERR_SHAPE;
   if (d_state > 64) return HCLSM_ERR_UNSUPPORTED;
+  // per-sequence slabs are addressed through 32-bit buffer offsets
+  if (T * d_inner * (dtype == HCLSM_F32 ? 4 : 2) >= (1LL << 31)) return HCLSM_ERR_UNSUPPORTED;
   if (mode != HCLSM_SCAN_RAW && mode != HCLSM_SCAN_MODEL) return HCLSM_ERR_MODE;
   if (dtype != HCLSM_F32 && dtype != HCLSM_BF16 && dtype != HCLSM_F16) return HCLSM_ERR_DTYPE;
   hipStream_t st = (hipStream_t)stream;
