@@ -103,7 +103,9 @@ int64_t hclsm_ssm_scan_bwd_workspace(int64_t batch, int64_t T, int64_t d_inner, 
  * same arguments and mode.  gy, gx, gdt [batch, T, d_inner] and gB, gC [batch, T, d_state] in `dtype`;
  * gA_log [d_inner, d_state] float32; gD [d_inner] float32 (nullable; Dskip nullable as in the forward).
  * MODEL mode passes gradient through each clamp only inside its closed interval.  Chunk checkpoints and
- * partial sums live in `workspace` (>= hclsm_ssm_scan_bwd_workspace bytes).  Three launches at most.
+ * partial sums live in `workspace` (>= hclsm_ssm_scan_bwd_workspace bytes).  Four launches at most.
+ * Deterministic (no float atomics).  One sequence's [T, d_inner] slab must be < 2^31 bytes
+ * (HCLSM_ERR_UNSUPPORTED otherwise).
  * Replaces: _TritonSSMScan.backward (hclsm/kernels/ssm_scan_kernel.py:321-377) and the autograd of
  *   sequential_ssm_scan (:42-86) / the inline scan of SimplifiedSSMBlock (dynamics/level0_ssm.py:82-101).
  */

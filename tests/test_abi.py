@@ -66,3 +66,13 @@ def test_argument_errors_before_launch(lib):
     assert f(None, None, None, None, None, None, None, None, 1, 4, 4, 4, 0, 0, None) == -1
     # empty problem: nothing to launch, success
     assert f(None, None, None, None, None, None, None, None, 0, 4, 4, 4, 0, 0, None) == 0
+
+
+def test_scan_backward_argument_errors_before_launch(lib):
+    f = lib.hclsm_ssm_scan_bwd
+    null13 = [None] * 13
+    # bad mode, oversized d_state, a per-sequence slab past 32-bit buffer offsets, NULL pointers
+    assert f(*null13, 1, 4, 4, 4, 1, 7, None, 0, None) == -5
+    assert f(*null13, 1, 4, 4, 65, 1, 0, None, 0, None) == -4
+    assert f(*null13, 1, 1 << 20, 1 << 10, 16, 1, 0, None, 0, None) == -4   # 2^30 bf16 elements = 2 GiB
+    assert f(*null13, 1, 4, 4, 4, 1, 0, None, 0, None) == -1
