@@ -26,8 +26,8 @@ namespace hclsm {
 // registers.
 constexpr int bwd_sg(int SP) { return SP < 16 ? SP : 16; }
 constexpr int bwd_k(int SP) { return 64 / bwd_sg(SP); }
-// Lanes per workgroup (six waves).
-constexpr int BWD_MAX_THREADS = 384;
+// Lanes per workgroup: two waves, so whole workgroups fill the four SIMDs of a CU evenly.
+constexpr int BWD_MAX_THREADS = 128;
 
 // Channels per workgroup and workgroups per sequence: the channels of a sequence split evenly.
 struct BwdGrid { int DW, nblk; };
