@@ -149,6 +149,7 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
   __shared__ float red[K][WMAX][2 * SP];           // per-chunk wave partials of gB | gC
   __shared__ __align__(16) float sB[BWD_WT][SP];   // B / C rows of the current window, fp32; states >= S
   __shared__ __align__(16) float sC[BWD_WT][SP];   // and steps >= T are zero
+  __shared__ float sH0[SG][BWD_MAX_THREADS];       // the chunk's starting state, read back at its first step
   const int n = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, nw = blockDim.x >> 6;
   const int dl = tid / G, gi = tid - dl * G;
@@ -263,9 +264,9 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
   for (int c = a.nchunk - 1; c >= 0; --c) {
     const int t0 = c * K, len = (t0 + K < T ? t0 + K : T) - t0;
     const int w0 = t0 / BWD_WT * BWD_WT;
-    float h0[SG], xs[K], ds[K], gs[K];
+    float hc[SG], xs[K], ds[K], gs[K];
 #pragma unroll
-    for (int j = 0; j < SG; ++j) h0[j] = act ? ck[(size_t)c * a.ld_ck + j] : 0.f;
+    for (int j = 0; j < SG; ++j) hc[j] = act ? ck[(size_t)c * a.ld_ck + j] : 0.f;
     ld_chunk(c, xs, ds);
 #pragma unroll
     for (int i = 0; i < K; ++i) {
@@ -277,23 +278,27 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
       __syncthreads();
       wcur = w0;
     }
-    float hk[K][SG];
-    {
-      float hc[SG];
+    // recompute the chunk's states h_{t0+i} into hk (registers; the starting state goes to LDS) and
+    // reduce gC_t = sum_d gy_t h_t over the wave's channels on the way (gy = 0 on inactive lanes and
+    // missing steps); lanes that differ only in bits below the last halving hold identical copies
 #pragma unroll
-      for (int j = 0; j < SG; ++j) hc[j] = h0[j];
+    for (int j = 0; j < SG; ++j) sH0[j][tid] = hc[j];
+    float hk[K - 1][SG];
 #pragma unroll
-      for (int i = 0; i < K; ++i) {
-        const float dtv = dt_of(ds[i], i < len);
-        const float u = dtv * xs[i];
-        float bv[SG];
-        row(sB, t0 + i - w0, bv);
+    for (int i = 0; i < K; ++i) {
+      const float dtv = dt_of(ds[i], i < len);
+      const float u = dtv * xs[i];
+      float bv[SG], w[SG];
+      row(sB, t0 + i - w0, bv);
 #pragma unroll
-        for (int j = 0; j < SG; ++j) {
-          hc[j] = fmaf(fast_exp2(dtv * a2[j]), hc[j], u * bv[j]);
-          hk[i][j] = hc[j];
-        }
+      for (int j = 0; j < SG; ++j) {
+        hc[j] = fmaf(fast_exp2(dtv * a2[j]), hc[j], u * bv[j]);
+        if (i < K - 1) hk[i < K - 1 ? i : 0][j] = hc[j];
+        w[j] = gs[i] * hc[j];
       }
+      const int off = RS<SG, G>::run(w, lane);
+#pragma unroll
+      for (int e = 0; e < VL; ++e) red[i][wid][SP + s0 + off + e] = w[e];
     }
     // the reverse steps recompute the gates and reread the rows instead of keeping the recompute's
     // K * SG values live (registers are the occupancy limit): hide both from CSE
@@ -307,19 +312,20 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
       const float xv = xs[i];
       const float gyv = gs[i];
       const float um = act ? dtv * xv : 0.f;   // gy is zero on inactive lanes, so gh is too; um zeroes their gB terms
-      float bv[SG], cv[SG];
+      float bv[SG], cv[SG], hp[SG];
       row(sB, t - w0, bv);
       row(sC, t - w0, cv);
+#pragma unroll
+      for (int j = 0; j < SG; ++j) hp[j] = (i > 0) ? hk[i > 0 ? i - 1 : 0][j] : sH0[j][tid];   // h_{t-1}
       float w[SG];
       float q = 0.f, gda2 = 0.f;   // gda2 = sum garg * A * log2(e); times ln 2 below
 #pragma unroll
       for (int j = 0; j < SG; ++j) {
-        const float hp = (i > 0) ? hk[i > 0 ? i - 1 : 0][j] : h0[j];
         gh[j] = fmaf(gyv, cv[j], gh[j]);
         q = fmaf(gh[j], bv[j], q);
         w[j] = gh[j] * um;                           // -> gB
         gh[j] *= fast_exp2(dtv * a2[j]);             // carried to step t-1
-        const float garg = gh[j] * hp;               // gh_t h_{t-1} exp(dt A)
+        const float garg = gh[j] * hp[j];            // gh_t h_{t-1} exp(dt A)
         gda2 = fmaf(garg, a2[j], gda2);
         gA[j] = fmaf(garg, dtv, gA[j]);
       }
@@ -331,18 +337,10 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
       buf_st<DT>(fmaf(q, dtv, dsk * gyv), rgx, vo_st, so);
       buf_st<DT>(gdv, rgdt, vo_st, so);
       gD = fmaf(gyv, xv, gD);
-      // sums over the wave's channels: gB values, then gC values (16 at a time keeps registers low);
-      // lanes that differ only in bits below the last halving hold identical copies
+      // gB_t = sum over the wave's channels (as for gC above)
+      const int off = RS<SG, G>::run(w, lane);
 #pragma unroll
-      for (int which = 0; which < 2; ++which) {
-        if (which == 1) {
-#pragma unroll
-          for (int j = 0; j < SG; ++j) w[j] = gyv * hk[i][j];   // -> gC (gyv = 0 on inactive lanes)
-        }
-        const int off = RS<SG, G>::run(w, lane);
-#pragma unroll
-        for (int e = 0; e < VL; ++e) red[i][wid][which * SP + s0 + off + e] = w[e];
-      }
+      for (int e = 0; e < VL; ++e) red[i][wid][s0 + off + e] = w[e];
     }
     __syncthreads();
     // sum the chunk's wave partials: K steps x 2*SP values
