@@ -30,6 +30,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "SSM scan GB/s (% of HBM peak) + slot-attn/event-attn tokens/s, small preset, 1 GPU"
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 NSETS = 4
 
 
@@ -243,6 +244,60 @@ def _bench_scan_bwd(dev, n, warmup):
                          "unit": "GB/s", "frac": round(nbytes / med / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_call": nbytes}}
 
 
+def _bench_level1(dev, n, warmup):
+    """Level-1 step of the small preset (config.py:221-242) on packed events: 32 clips x T=64 x 32 slots
+    (d_slot 192), a Bernoulli(0.15) event mask with t=0 forced, 80% live slots, Level-1 d_model 384,
+    3 layers, 6 heads, SwiGLU hidden 1536.  level1_events_packed (device event index, packed gather, one
+    hclsm_level1_forward call over the live events, packed scatter and top-down gating; no host sync),
+    fp32 and under a bf16 autocast, against the reference-shaped padded flow (gather_events with its
+    K_max host read, Level-1 over B x K_max events, HierarchyManager.forward) in fp32."""
+    import torch
+    from types import SimpleNamespace
+    from hclsm_amd.dynamics import HierarchyManager, Level1EventDynamics, level1_events_packed
+    torch.manual_seed(1006)
+    B, T, N, D, DL2 = 32, 64, 32, 192, 512
+    cfg = SimpleNamespace(d_model=384, n_layers=3, n_heads=6)
+    hid = 4 * cfg.d_model
+    hm, l1 = HierarchyManager(D, DL2).to(dev), Level1EventDynamics(cfg, D).to(dev)
+    g = torch.Generator(device=dev).manual_seed(1007)
+    states = torch.randn(B, T, N, D, generator=g, device=dev)
+    mask = (torch.rand(B, T, generator=g, device=dev) < 0.15).float()
+    mask[:, 0] = 1.0
+    obj = (torch.rand(B, N, generator=g, device=dev) < 0.8).float()
+    obj[:, 0] = 1.0
+    l2 = torch.randn(B, 4, DL2, generator=g, device=dev)
+
+    def packed():
+        return level1_events_packed(hm, l1, states, mask, obj, l2)
+
+    def padded():
+        ev, pad, K = hm.gather_events(states, mask)
+        return hm(states, l1(ev, pad, obj), l2, mask, obj)
+    with torch.no_grad():
+        E = int(mask.sum().item())
+        f32_med, _ = _event_timing(packed, n, warmup)
+        ref = padded()
+        err32 = float(((packed() - ref).norm() / ref.norm()).item())
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            bf_med, _ = _event_timing(packed, n, warmup)
+            out_bf = packed()
+        errbf = float(((out_bf.float() - ref).norm() / ref.norm()).item())
+        pad_med, _ = _event_timing(padded, n, warmup)
+    dm, L, H = cfg.d_model, cfg.n_layers, cfg.n_heads
+    flops = E * N * (2 * D * dm + L * (2 * dm * 3 * dm + 2 * dm * dm + 3 * 2 * dm * hid) + 2 * dm * D) \
+        + E * L * 2 * 2 * N * N * dm
+    tf = flops / bf_med / 1e12
+    return {"workload": "Level-1 step, small preset: 32 clips x T=64 x 32 slots (d_slot 192), p=0.15 events (t=0 "
+                        "forced), d_model 384, 3 layers, 6 heads, SwiGLU 1536, Level-2 gating; packed and sync-free "
+                        "vs the padded flow",
+            "events": E, "rows": E * N,
+            "packed_bf16_us": round(bf_med * 1e6, 2), "packed_fp32_us": round(f32_med * 1e6, 2),
+            "padded_fp32_us": round(pad_med * 1e6, 2), "speedup_bf16_vs_padded": round(pad_med / bf_med, 3),
+            "packed_fp32_vs_padded_normwise": err32, "packed_bf16_vs_padded_normwise": errbf,
+            "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4), "flops_per_call": flops}}
+
+
 def _bench_chain(dev, n, warmup):
     """Config 4: four chained scans at (1024, 1024, 768), S=16, bf16 (each fed the previous output),
     then the event index of a p=0.05 mask (t=0 forced) and causal event attention, 12 heads x 64."""
@@ -414,6 +469,7 @@ def main():
         out["chain"] = _bench_chain(dev, 20, 3)
         out["block_scan"] = _bench_block_scan(dev, 50, 5)
         out["scan_bwd"] = _bench_scan_bwd(dev, 50, 5)
+        out["level1"] = _bench_level1(dev, 30, 3)
     print(json.dumps(out), flush=True)
 
 

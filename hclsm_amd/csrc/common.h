@@ -50,6 +50,9 @@ template <> struct Elem<HCLSM_F16> {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// x * sigmoid(x) (torch.nn.functional.silu).
+__device__ __forceinline__ float silu_f(float g) { return g * __builtin_amdgcn_rcpf(1.f + __expf(-g)); }
+
 // Word 3 of a gfx9-family buffer resource for raw (stride 0) byte addressing: loads at or past
 // num_records bytes return 0, stores there are dropped.
 constexpr int kRawBufferWord3 = 0x00020000;

@@ -21,7 +21,7 @@
 // kernel is a contiguous per-lane vector, and no LDS or barrier is needed.
 // Softmax statistics (max, sum) are per query: reduced over r in-lane and over
 // the four lanes {i, i+16, i+32, i+48} with two xor shuffles.
-#include "common.h"
+#include "internal.h"
 
 namespace hclsm {
 
@@ -92,13 +92,23 @@ __device__ __forceinline__ void load_row(const T* __restrict__ p, T* e) {
   for (int i = 0; i < N; ++i) e[i] = p[i];
 }
 
+// MODE 2 (uniform segments, the packed Level-1 layout): segment p < *nseg_dev is rows p*T .. p*T+T-1 of
+// q / k / v (row stride ldi elements) and of out_packed (row stride ldo); key j of segment p is live iff
+// obj_mask is null or obj_mask[seg_rows[p] * T + j] > 0.5.  Unused by modes 0 / 1.
+struct AttnExt {
+  const int32_t* nseg_dev;
+  int64_t ldi, ldo;
+  const float* obj_mask;
+  const int32_t* seg_rows;
+};
+
 template <int DT, int DH, int MODE>
 __global__ void __launch_bounds__(64 * ATTN_WAVES)
 event_attn_kernel(const typename AttnT<DT>::T* __restrict__ q, const typename AttnT<DT>::T* __restrict__ k,
                   const typename AttnT<DT>::T* __restrict__ v, typename AttnT<DT>::T* __restrict__ out_packed,
                   typename AttnT<DT>::T* __restrict__ out_grid, const int32_t* __restrict__ offsets,
                   const int32_t* __restrict__ indices, const uint8_t* __restrict__ key_pad,
-                  int64_t nseg, int64_t T, int H, int64_t capacity, float scale_log2) {
+                  int64_t nseg, int64_t T, int H, int64_t capacity, float scale_log2, AttnExt ex) {
   using A = AttnT<DT>;
   using TT = typename A::T;
   constexpr int QD = DH / 4;          // contiguous head columns per lane
@@ -112,16 +122,27 @@ event_attn_kernel(const typename AttnT<DT>::T* __restrict__ q, const typename At
   const int64_t p = wave / H;
   const int h = (int)(wave - p * H);
   const int lane = threadIdx.x & 63, g = lane >> 4, li = lane & 15;
-  const int32_t base = offsets[p];
-  const int L = offsets[p + 1] - base;
+  int64_t base;
+  int L;
+  if constexpr (MODE == 2) {
+    if (p >= *ex.nseg_dev) return;
+    base = p * T;
+    L = (int)T;
+  } else {
+    base = offsets[p];
+    L = offsets[p + 1] - (int32_t)base;
+  }
   if (L <= 0) return;
   const int64_t rstride = (int64_t)H * DH;
+  const int64_t ldi = MODE == 2 ? ex.ldi : rstride, ldo = MODE == 2 ? ex.ldo : rstride;
   auto row_ptr = [&](const TT* t, int i) -> const TT* {
     const int ic = i < L ? i : L - 1;  // clamp: always a valid row of this segment
+    if constexpr (MODE == 2) return t + (base + ic) * ldi + (int64_t)h * DH;
     int64_t tr = indices[base + ic];
     tr = tr < 0 ? 0 : (tr >= T ? T - 1 : tr);
     return t + ((int64_t)p * T + tr) * rstride + (int64_t)h * DH;
   };
+  const float* om = MODE == 2 && ex.obj_mask ? ex.obj_mask + (int64_t)ex.seg_rows[p] * T : nullptr;
 
   const int nqt = (L + 15) >> 4;
   for (int qt = 0; qt < nqt; ++qt) {
@@ -150,6 +171,7 @@ event_attn_kernel(const typename AttnT<DT>::T* __restrict__ q, const typename At
         const int j = kt * 16 + 4 * g + r;
         bool ok = (i < L) && (j < L);
         if (MODE == 0) ok = ok && (j <= i);
+        else if (MODE == 2) ok = ok && (om == nullptr || om[j < L ? j : L - 1] > 0.5f);
         else if (key_pad != nullptr) {
           int64_t tj = indices[base + (j < L ? j : L - 1)];
           tj = tj < 0 ? 0 : (tj >= T ? T - 1 : tj);
@@ -200,12 +222,12 @@ event_attn_kernel(const typename AttnT<DT>::T* __restrict__ q, const typename At
       for (int r = 0; r < 4; ++r)
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) o[r * NT + nt] = A::from(acc[r][nt] * inv);
-      if (out_packed && (int64_t)base + i < capacity) {
-        TT* dst = out_packed + ((int64_t)base + i) * rstride + (int64_t)h * DH + g * QD;
+      if (out_packed && base + i < capacity) {
+        TT* dst = out_packed + (base + i) * ldo + (int64_t)h * DH + g * QD;
 #pragma unroll
         for (int e = 0; e < QD; ++e) dst[e] = o[e];
       }
-      if (out_grid) {
+      if (MODE != 2 && out_grid) {
         int64_t tr = indices[base + i];
         tr = tr < 0 ? 0 : (tr >= T ? T - 1 : tr);
         TT* dst = out_grid + ((int64_t)p * T + tr) * rstride + (int64_t)h * DH + g * QD;
@@ -226,10 +248,12 @@ static int launch_attn(int mode, const void* q, const void* k, const void* v, vo
   const float sl2 = scale * HCLSM_LOG2E;
   if (mode == HCLSM_ATTN_TRACK_CAUSAL)
     hipLaunchKernelGGL((event_attn_kernel<DT, DH, 0>), dim3(grid), dim3(64 * ATTN_WAVES), 0, st, (const TT*)q,
-                       (const TT*)k, (const TT*)v, (TT*)outp, (TT*)outg, offsets, indices, kp, nseg, T, H, cap, sl2);
+                       (const TT*)k, (const TT*)v, (TT*)outp, (TT*)outg, offsets, indices, kp, nseg, T, H, cap, sl2,
+                       AttnExt{});
   else
     hipLaunchKernelGGL((event_attn_kernel<DT, DH, 1>), dim3(grid), dim3(64 * ATTN_WAVES), 0, st, (const TT*)q,
-                       (const TT*)k, (const TT*)v, (TT*)outp, (TT*)outg, offsets, indices, kp, nseg, T, H, cap, sl2);
+                       (const TT*)k, (const TT*)v, (TT*)outp, (TT*)outg, offsets, indices, kp, nseg, T, H, cap, sl2,
+                       AttnExt{});
   HCLSM_LAUNCH_CHECK();
   return 0;
 }
@@ -245,6 +269,35 @@ static int dispatch_dh(int dh, int mode, const void* q, const void* k, const voi
     case 128: return launch_attn<DT, 128>(mode, q, k, v, outp, outg, offsets, indices, kp, nseg, T, H, cap, scale, st);
     default: return HCLSM_ERR_UNSUPPORTED;
   }
+}
+
+// Packed Level-1 attention (MODE 2), for composite entry points in other files (declared in internal.h):
+// cap segments of N rows, the first *nseg_dev of them live; q / k / v rows with stride ldi, out rows ldo.
+int attn_slots_packed(const void* q, const void* k, const void* v, int64_t ldi, void* out, int64_t ldo,
+                      const int32_t* nseg_dev, int64_t cap, int64_t N, int H, int dh, const float* obj_mask,
+                      const int32_t* seg_rows, float scale, int dtype, hipStream_t st) {
+  if (cap < 0 || N <= 0 || H <= 0 || cap * N > 0x7fffffffLL) return HCLSM_ERR_SHAPE;
+  if (cap == 0) return 0;
+  if (!q || !k || !v || !out || !nseg_dev || (obj_mask && !seg_rows)) return HCLSM_ERR_NULL;
+  const float sl2 = scale * HCLSM_LOG2E;
+  const unsigned grid = (unsigned)((cap * H + ATTN_WAVES - 1) / ATTN_WAVES);
+  const AttnExt ex{nseg_dev, ldi, ldo, obj_mask, seg_rows};
+#define HCLSM_SP(DT_, DH_)                                                                                   \
+  if (dtype == DT_ && dh == DH_) {                                                                           \
+    using TT = typename AttnT<DT_>::T;                                                                       \
+    hipLaunchKernelGGL((event_attn_kernel<DT_, DH_, 2>), dim3(grid), dim3(64 * ATTN_WAVES), 0, st, (const TT*)q, \
+                       (const TT*)k, (const TT*)v, (TT*)out, (TT*)nullptr, nullptr, nullptr, nullptr, cap, N, H,   \
+                       cap * N, sl2, ex);                                                                    \
+    HCLSM_LAUNCH_CHECK();                                                                                    \
+    return 0;                                                                                                \
+  }
+#define HCLSM_SP_DT(DT_) HCLSM_SP(DT_, 16) HCLSM_SP(DT_, 32) HCLSM_SP(DT_, 64) HCLSM_SP(DT_, 128)
+  HCLSM_SP_DT(HCLSM_BF16)
+  HCLSM_SP_DT(HCLSM_F16)
+  HCLSM_SP_DT(HCLSM_F32)
+#undef HCLSM_SP_DT
+#undef HCLSM_SP
+  return (dh == 16 || dh == 32 || dh == 64 || dh == 128) ? HCLSM_ERR_DTYPE : HCLSM_ERR_UNSUPPORTED;
 }
 
 }  // namespace hclsm

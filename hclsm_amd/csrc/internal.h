@@ -1,0 +1,30 @@
+// Launchers shared between the translation units of libhclsm_amd (not part of the C ABI).
+#pragma once
+
+#include "common.h"
+
+namespace hclsm {
+
+// Y[M, N] = A . W^T (+ resid) with A = X or LayerNorm(X) rows (ln != 0), the row count taken as
+// min(M, *m_dev * m_mul) when m_dev is set (read on the device), and, when glu is set, the
+// gated-linear epilogue val = silu(glu[row, col]) * val (glu in `dtype`, row stride ldg).
+// Defined in slot_attn.hip.
+int linear_rows(const void* x, int64_t ldx, int x_dtype, const void* w, int64_t ldw, const float* resid,
+                int64_t ldr, void* y, int64_t ldy, int y_dtype, int64_t M, int64_t N, int64_t K, int ln,
+                const float* ln_w, const float* ln_b, float ln_eps, const void* glu, int64_t ldg,
+                const int32_t* m_dev, int64_t m_mul, int dtype, hipStream_t st);
+
+// LayerNorm of M rows (row count min(M, *m_dev * m_mul) when m_dev is set), as hclsm_layer_norm.
+// Defined in slot_attn.hip.
+int layer_norm_rows(const void* x, int64_t ldx, const float* w, const float* b, void* y, int64_t ldy, int64_t M,
+                    int64_t D, float eps, int in_dtype, int out_dtype, const int32_t* m_dev, int64_t m_mul,
+                    hipStream_t st);
+
+// Attention among the N rows of each of cap uniform segments (the first *nseg_dev live): rows p*N + i
+// of q / k / v (row stride ldi) and out (row stride ldo), H heads of dh columns; key j of segment p is
+// excluded when obj_mask[seg_rows[p] * N + j] <= 0.5 (obj_mask nullable).  Defined in event_attn.hip.
+int attn_slots_packed(const void* q, const void* k, const void* v, int64_t ldi, void* out, int64_t ldo,
+                      const int32_t* nseg_dev, int64_t cap, int64_t N, int H, int dh, const float* obj_mask,
+                      const int32_t* seg_rows, float scale, int dtype, hipStream_t st);
+
+}  // namespace hclsm

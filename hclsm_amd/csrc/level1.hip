@@ -1,0 +1,123 @@
+// Level-1 event dynamics on packed events, for gfx950.
+//
+// Level1EventDynamics.forward (hclsm/dynamics/level1_event.py:57-133) for the live events of a packed
+// layout: event e < *n_events is rows e*N .. e*N+N-1 (its N slots).  Every launch is sized for the
+// capacity and reads the live count on the device, so nothing here waits on the host:
+//
+//   x   = ev . proj_in^T                                  (fp32 residual stream)        :102-107
+//   per layer (EventTransformerBlock, :31-54):
+//     xn  = LN1(x)                                        (operand dtype)
+//     qkv = xn . in_proj^T
+//     o   = softmax(q k^T / sqrt(dh), keys of dead slots excluded) v, per event and head   :49-51
+//     x  += o . out_proj^T                                (residual in the GEMM epilogue)
+//     xn  = LN2(x);  h1 = xn . w1^T
+//     g   = silu(h1) * (xn . w3^T)                        (gated-linear epilogue)          :17-28
+//     x  += g . w2^T
+//   out = LN(x) . proj_out^T                                                                 :124-128
+//
+// GEMMs are the MFMA linear kernels of slot_attn.hip (64x64 LDS-staged tiles for 16-bit operands at
+// these sizes), LayerNorm its one-wave-per-row kernel, the attention the uniform-segment mode of the
+// varlen event-attention kernel (event_attn.hip).  The reference's event_pad_mask multiply (:130-131)
+// has nothing to do here: packed rows are all real events.
+#include "internal.h"
+
+namespace hclsm {
+
+struct L1Ws {
+  size_t x, xn, qkv, o, h1, g, total;
+};
+
+static size_t al256(size_t v) { return (v + 255) / 256 * 256; }
+
+static L1Ws l1_ws(int64_t cap, int64_t N, int64_t dm, int64_t hid, int es) {
+  const size_t R = (size_t)cap * N;
+  L1Ws w;
+  size_t o = 0;
+  w.x = o; o += al256(R * dm * 4);
+  w.xn = o; o += al256(R * dm * es);
+  w.qkv = o; o += al256(R * 3 * dm * es);
+  w.o = o; o += al256(R * dm * es);
+  w.h1 = o; o += al256(R * hid * es);
+  w.g = o; o += al256(R * hid * es);
+  w.total = o;
+  return w;
+}
+
+}  // namespace hclsm
+
+using namespace hclsm;
+
+extern "C" int64_t hclsm_level1_forward_workspace(int64_t capacity, int64_t N, int64_t d_model, int64_t hidden,
+                                                  int dtype) {
+  if (capacity < 0 || N < 0 || d_model < 0 || hidden < 0) return HCLSM_ERR_SHAPE;
+  if (dtype != HCLSM_F32 && dtype != HCLSM_BF16 && dtype != HCLSM_F16) return HCLSM_ERR_DTYPE;
+  return (int64_t)l1_ws(capacity, N, d_model, hidden, dtype == HCLSM_F32 ? 4 : 2).total;
+}
+
+extern "C" int hclsm_level1_forward(const void* ev, int ev_dtype, void* out, int out_dtype, const int32_t* n_events,
+                                    int64_t capacity, int64_t N, const int32_t* ev_rows, const float* obj_mask,
+                                    int64_t d_slot, int64_t d_model, int64_t n_heads, int64_t hidden,
+                                    int64_t n_layers, const void* const* params, float ln_eps, int dtype,
+                                    void* workspace, int64_t workspace_bytes, void* stream) {
+  if (capacity < 0 || N < 0 || d_slot <= 0 || d_model <= 0 || n_heads <= 0 || hidden <= 0 || n_layers < 0)
+    return HCLSM_ERR_SHAPE;
+  if (capacity * N > 0x7fffffffLL || d_model % n_heads) return HCLSM_ERR_SHAPE;
+  if (dtype != HCLSM_F32 && dtype != HCLSM_BF16 && dtype != HCLSM_F16) return HCLSM_ERR_DTYPE;
+  if ((ev_dtype != HCLSM_F32 && ev_dtype != dtype) || (out_dtype != HCLSM_F32 && out_dtype != dtype))
+    return HCLSM_ERR_DTYPE;
+  const int64_t dh = d_model / n_heads;
+  if (dh != 16 && dh != 32 && dh != 64 && dh != 128) return HCLSM_ERR_UNSUPPORTED;
+  const int64_t kmul = dtype == HCLSM_F32 ? 4 : 32;   // GEMM contraction granule of the linear kernels
+  if (d_slot % kmul || d_model % kmul || hidden % kmul) return HCLSM_ERR_UNSUPPORTED;
+  if (capacity == 0 || N == 0) return 0;
+  if (!ev || !out || !n_events || !params || !workspace || (obj_mask && !ev_rows)) return HCLSM_ERR_NULL;
+  const int es = dtype == HCLSM_F32 ? 4 : 2;
+  const L1Ws L = l1_ws(capacity, N, d_model, hidden, es);
+  if (workspace_bytes < (int64_t)L.total) return HCLSM_ERR_SHAPE;
+  for (int64_t i = 0; i < 4 + 9 * n_layers; ++i)
+    if (params[i] == nullptr) return HCLSM_ERR_NULL;
+  hipStream_t st = (hipStream_t)stream;
+  char* ws = reinterpret_cast<char*>(workspace);
+  float* x = reinterpret_cast<float*>(ws + L.x);
+  void* xn = ws + L.xn;
+  char* qkv = ws + L.qkv;
+  void* o = ws + L.o;
+  void* h1 = ws + L.h1;
+  void* g = ws + L.g;
+  const int64_t R = capacity * N, dm = d_model;
+  auto P = [&](int64_t i) { return params[i]; };
+  auto Pf = [&](int64_t i) { return reinterpret_cast<const float*>(params[i]); };
+  int rc;
+#define HCLSM_TRY(call) \
+  do {                  \
+    rc = (call);        \
+    if (rc) return rc;  \
+  } while (0)
+  // GEMM Y[R, n] = X[R, k] . W^T (+ resid) (gated by glu), rows of the live events only
+  auto gemm = [&](const void* X, int xdt, const void* W, int64_t n, int64_t k, const float* resid, void* Y, int ydt,
+                  const void* glu) {
+    return linear_rows(X, k, xdt, W, k, resid, n, Y, n, ydt, R, n, k, 0, nullptr, nullptr, ln_eps, glu, n, n_events,
+                       N, dtype, st);
+  };
+  auto norm = [&](const float* w, const float* b) {
+    return layer_norm_rows(x, dm, w, b, xn, dm, R, dm, ln_eps, HCLSM_F32, dtype, n_events, N, st);
+  };
+  HCLSM_TRY(gemm(ev, ev_dtype, P(0), dm, d_slot, nullptr, x, HCLSM_F32, nullptr));   // x = ev . proj_in^T
+  const float scale = 1.f / sqrtf((float)dh);
+  for (int64_t l = 0; l < n_layers; ++l) {
+    const int64_t b = 4 + 9 * l;   // ln1_w, ln1_b, in_proj, out_proj, ln2_w, ln2_b, w1, w3, w2
+    HCLSM_TRY(norm(Pf(b), Pf(b + 1)));
+    HCLSM_TRY(gemm(xn, dtype, P(b + 2), 3 * dm, dm, nullptr, qkv, dtype, nullptr));
+    HCLSM_TRY(attn_slots_packed(qkv, qkv + dm * es, qkv + 2 * dm * es, 3 * dm, o, dm, n_events, capacity, N,
+                                (int)n_heads, (int)dh, obj_mask, ev_rows, scale, dtype, st));
+    HCLSM_TRY(gemm(o, dtype, P(b + 3), dm, dm, x, x, HCLSM_F32, nullptr));
+    HCLSM_TRY(norm(Pf(b + 4), Pf(b + 5)));
+    HCLSM_TRY(gemm(xn, dtype, P(b + 6), hidden, dm, nullptr, h1, dtype, nullptr));
+    HCLSM_TRY(gemm(xn, dtype, P(b + 7), hidden, dm, nullptr, g, dtype, h1));
+    HCLSM_TRY(gemm(g, dtype, P(b + 8), dm, hidden, x, x, HCLSM_F32, nullptr));
+  }
+  HCLSM_TRY(norm(Pf(1), Pf(2)));
+  HCLSM_TRY(gemm(xn, dtype, P(3), d_slot, dm, nullptr, out, out_dtype, nullptr));   // out = LN(x) . proj_out^T
+#undef HCLSM_TRY
+  return 0;
+}

@@ -18,6 +18,7 @@
 //                 v staged transposed through LDS in 32-token chunks; optional
 //                 renormalisation (attn + eps) / sum_m (attn + eps) folded into the epilogue.
 #include "mfma.h"
+#include "internal.h"
 
 namespace hclsm {
 
@@ -130,6 +131,30 @@ struct OutSplit {
   void* yt;
 };
 
+// Optional extras of a linear layer:
+// - a device-side row count: rows = min(M, *m_dev * m_mul), read at kernel start, so a launch sized
+//   for a capacity does only the rows a preceding kernel produced (workgroups past them exit);
+// - a gated-linear epilogue: val = silu(glu[row, col]) * val (glu in the operand type), applied after
+//   bias / ReLU and before the residual.
+struct LinExt {
+  const int32_t* m_dev;
+  int64_t m_mul;
+  const void* glu;
+  int64_t ldg;
+};
+constexpr LinExt kNoLinExt{nullptr, 1, nullptr, 0};
+
+__device__ __forceinline__ int64_t ext_rows(const LinExt& e, int64_t M) {
+  if (e.m_dev == nullptr) return M;
+  const int64_t md = (int64_t)(*e.m_dev) * e.m_mul;
+  return md < M ? md : M;
+}
+template <int DT>
+__device__ __forceinline__ float ext_glu(const LinExt& e, int64_t row, int64_t col, float val) {
+  if (e.glu == nullptr) return val;
+  return silu_f(Cvt<typename MM<DT>::T>::f(reinterpret_cast<const typename MM<DT>::T*>(e.glu)[row * e.ldg + col])) * val;
+}
+
 // 64x64 output tile per workgroup, each wave a 32x32 quadrant over the full K (large M x N).
 // 64x64 output tile per workgroup, 16-bit operands: the tile's A rows and W rows are staged in LDS in
 // K chunks of 128 (each global byte read once per workgroup), the next chunk's global loads in flight
@@ -143,7 +168,7 @@ __global__ void __launch_bounds__(256)
 linear_lds_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const typename MM<DT>::T* __restrict__ W,
                   int64_t ldw, const float* __restrict__ bias, const float* __restrict__ resid, int64_t ldr,
                   typename MM<OT>::T* __restrict__ Y, int64_t ldy, typename MM<DT>::T* __restrict__ Y2,
-                  int64_t ldy2, int64_t M, int64_t N, int64_t K, int relu, float clamp_v, OutSplit os) {
+                  int64_t ldy2, int64_t M, int64_t N, int64_t K, int relu, float clamp_v, OutSplit os, LinExt ext) {
   using A = MM<DT>;
   using T = typename A::T;
   static_assert(A::KPL == 8, "16-bit operands");
@@ -151,6 +176,8 @@ linear_lds_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const t
   __shared__ __align__(16) T Bs[64 * LT_LD];
   const int64_t tiles_n = (N + 63) / 64;
   const int64_t tm = blockIdx.x / tiles_n, tn = blockIdx.x - tm * tiles_n;
+  M = ext_rows(ext, M);
+  if (tm * 64 >= M) return;   // the whole workgroup, before any barrier
   const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, g = lane >> 4, li = lane & 15;
   const int wr = wid >> 1, wc = wid & 1;
   // staging map: 64 rows x (KC / 8) 16-byte units = 1024 units per operand, 4 per thread
@@ -252,6 +279,7 @@ linear_lds_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const t
         if (row >= M) continue;
         float val = acc[ti][tj][r] + bv;
         if (relu) val = fmaxf(val, 0.f);
+        val = ext_glu<DT>(ext, row, col, val);
         if (resid) val += resid[row * ldr + col];
         if (clamp_v > 0.f) val = fminf(fmaxf(val, -clamp_v), clamp_v);
         if (os.yt != nullptr && col >= os.col) {
@@ -266,17 +294,121 @@ linear_lds_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const t
   }
 }
 
+// fp32 operands: the same 64x64 tile with A and W rows staged in LDS in K chunks of 64 floats (the next
+// chunk in flight), each wave a 32x32 quadrant of v_mfma_f32_16x16x4_f32.  The contraction is permuted
+// so that a lane's operands are float4 reads: in a 16-wide k block, lane group g owns k = 4g .. 4g+3 and
+// MFMA j of the block contracts k = 4g + j across the four groups.
+constexpr int LF_KC = 64;
+constexpr int LF_LD = LF_KC + 4;   // LDS row pitch (floats)
+
+template <int OT>
+__global__ void __launch_bounds__(256)
+linear_lds_f32_kernel(const float* __restrict__ X, int64_t ldx, const float* __restrict__ W, int64_t ldw,
+                      const float* __restrict__ bias, const float* __restrict__ resid, int64_t ldr,
+                      typename MM<OT>::T* __restrict__ Y, int64_t ldy, float* __restrict__ Y2, int64_t ldy2,
+                      int64_t M, int64_t N, int64_t K, int relu, float clamp_v, LinExt ext) {
+  __shared__ __align__(16) float As[64 * LF_LD];
+  __shared__ __align__(16) float Bs[64 * LF_LD];
+  const int64_t tiles_n = (N + 63) / 64;
+  const int64_t tm = blockIdx.x / tiles_n, tn = blockIdx.x - tm * tiles_n;
+  M = ext_rows(ext, M);
+  if (tm * 64 >= M) return;   // the whole workgroup, before any barrier
+  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, g = lane >> 4, li = lane & 15;
+  const int wr = wid >> 1, wc = wid & 1;
+  // staging map: 64 rows x (KC / 4) float4 units = 1024 units per operand, 4 per thread
+  const float* pa[4];
+  const float* pb[4];
+  int soff[4], ucol[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int u = tid + 256 * i, r = u >> 4;
+    ucol[i] = (u & 15) * 4;
+    int64_t ra = tm * 64 + r, rb = tn * 64 + r;
+    ra = ra < M ? ra : M - 1;
+    rb = rb < N ? rb : N - 1;
+    pa[i] = X + ra * ldx + ucol[i];
+    pb[i] = W + rb * ldw + ucol[i];
+    soff[i] = r * LF_LD + ucol[i];
+  }
+  float4 ra_[4], rb_[4];
+  auto fetch = [&](int64_t k0, int kc) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool in = ucol[i] < kc;
+      ra_[i] = in ? *reinterpret_cast<const float4*>(pa[i] + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+      rb_[i] = in ? *reinterpret_cast<const float4*>(pb[i] + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  f32x4 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  fetch(0, (int)(K < LF_KC ? K : LF_KC));
+  for (int64_t k0 = 0; k0 < K; k0 += LF_KC) {
+    const int kc = (int)(K - k0 < LF_KC ? K - k0 : LF_KC);
+    __syncthreads();   // the previous chunk is consumed
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      *reinterpret_cast<float4*>(As + soff[i]) = ra_[i];
+      *reinterpret_cast<float4*>(Bs + soff[i]) = rb_[i];
+    }
+    __syncthreads();
+    if (k0 + LF_KC < K) fetch(k0 + LF_KC, (int)(K - k0 - LF_KC < LF_KC ? K - k0 - LF_KC : LF_KC));
+    for (int kb = 0; kb < (kc + 15) / 16; ++kb) {   // zero-padded past kc
+      float4 a[2], b[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        a[t] = *reinterpret_cast<const float4*>(As + (wr * 32 + 16 * t + li) * LF_LD + kb * 16 + 4 * g);
+        b[t] = *reinterpret_cast<const float4*>(Bs + (wc * 32 + 16 * t + li) * LF_LD + kb * 16 + 4 * g);
+      }
+#pragma unroll
+      for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+        for (int tj = 0; tj < 2; ++tj) {
+          acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[ti].x, b[tj].x, acc[ti][tj], 0, 0, 0);
+          acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[ti].y, b[tj].y, acc[ti][tj], 0, 0, 0);
+          acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[ti].z, b[tj].z, acc[ti][tj], 0, 0, 0);
+          acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[ti].w, b[tj].w, acc[ti][tj], 0, 0, 0);
+        }
+    }
+  }
+  const int64_t r0 = tm * 64 + 32 * wr, c0 = tn * 64 + 32 * wc;
+#pragma unroll
+  for (int tj = 0; tj < 2; ++tj) {
+    const int64_t col = c0 + 16 * tj + li;
+    if (col >= N) continue;
+    const float bv = bias ? bias[col] : 0.f;
+#pragma unroll
+    for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t row = r0 + 16 * ti + 4 * g + r;
+        if (row >= M) continue;
+        float val = acc[ti][tj][r] + bv;
+        if (relu) val = fmaxf(val, 0.f);
+        val = ext_glu<HCLSM_F32>(ext, row, col, val);
+        if (resid) val += resid[row * ldr + col];
+        if (clamp_v > 0.f) val = fminf(fmaxf(val, -clamp_v), clamp_v);
+        Y[row * ldy + col] = MM<OT>::fromf(val);
+        if (Y2) Y2[row * ldy2 + col] = val;
+      }
+  }
+}
+
 template <int DT, int OT>
 __global__ void __launch_bounds__(256)
 linear_quad_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const typename MM<DT>::T* __restrict__ W,
                    int64_t ldw, const float* __restrict__ bias, const float* __restrict__ resid, int64_t ldr,
                    typename MM<OT>::T* __restrict__ Y, int64_t ldy, typename MM<DT>::T* __restrict__ Y2,
-                   int64_t ldy2, int64_t M, int64_t N, int64_t K, int relu, float clamp_v, OutSplit os) {
+                   int64_t ldy2, int64_t M, int64_t N, int64_t K, int relu, float clamp_v, OutSplit os, LinExt ext) {
   using A = MM<DT>;
   constexpr int KPL = A::KPL;
   constexpr int BLK = 4 * KPL;
   const int64_t tiles_n = (N + 63) / 64;
   const int64_t tm = blockIdx.x / tiles_n, tn = blockIdx.x - tm * tiles_n;
+  M = ext_rows(ext, M);
+  if (tm * 64 >= M) return;
   const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, g = lane >> 4, li = lane & 15;
   const int64_t r0 = tm * 64 + 32 * (wid >> 1), c0 = tn * 64 + 32 * (wid & 1);
   const typename A::T* pa[2];
@@ -319,6 +451,7 @@ linear_quad_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const 
         if (row >= M) continue;
         float val = acc[ti][tj][r] + bv;
         if (relu) val = fmaxf(val, 0.f);
+        val = ext_glu<DT>(ext, row, col, val);
         if (resid) val += resid[row * ldr + col];
         if (clamp_v > 0.f) val = fminf(fmaxf(val, -clamp_v), clamp_v);
         if (os.yt != nullptr && col >= os.col) {
@@ -339,13 +472,15 @@ linear_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>::T* _
               const float* __restrict__ bias, const float* __restrict__ resid, int64_t ldr,
               typename MM<OT>::T* __restrict__ Y, int64_t ldy, typename MM<DT>::T* __restrict__ Y2, int64_t ldy2,
               int64_t M, int64_t N, int64_t K, int relu, float clamp_v, const float* __restrict__ lnw,
-              const float* __restrict__ lnb, float ln_eps) {
+              const float* __restrict__ lnb, float ln_eps, LinExt ext) {
   using A = MM<DT>;
   constexpr int KPL = A::KPL;
   constexpr int BLK = 4 * KPL;
   __shared__ float red[4][2][2][4][64];   // [wave][ti][tj][r][lane]: 16 KB
   const int64_t tiles_n = (N + 31) / 32;
   const int64_t tm = blockIdx.x / tiles_n, tn = blockIdx.x - tm * tiles_n;
+  M = ext_rows(ext, M);
+  if (tm * 32 >= M) return;   // the whole workgroup, before any barrier
   const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, g = lane >> 4, li = lane & 15;
   const XT* pa[2];
   const typename A::T* pb[2];
@@ -403,6 +538,7 @@ linear_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>::T* _
         float val = red[0][ti][tj][r][lane] + red[1][ti][tj][r][lane] + red[2][ti][tj][r][lane] +
                     red[3][ti][tj][r][lane] + bv;
         if (relu) val = fmaxf(val, 0.f);
+        val = ext_glu<DT>(ext, row, col, val);
         if (resid) val += resid[row * ldr + col];
         if (clamp_v > 0.f) val = fminf(fmaxf(val, -clamp_v), clamp_v);
         Y[row * ldy + col] = MM<OT>::fromf(val);
@@ -846,17 +982,21 @@ template <int DT, int OT, typename XT>
 static void launch_linear_quad(const void* x, int64_t ldx, const void* w, int64_t ldw, const float* bias,
                                const float* resid, int64_t ldr, void* y, int64_t ldy, void* y2, int64_t ldy2,
                                int64_t M, int64_t N, int64_t K, int relu, float clamp, hipStream_t st,
-                               OutSplit os = OutSplit{0, 1, 0, 0, nullptr}) {
+                               OutSplit os = OutSplit{0, 1, 0, 0, nullptr}, LinExt ext = kNoLinExt) {
   if constexpr (std::is_same_v<XT, typename MM<DT>::T>) {
     const unsigned grid = (unsigned)(((M + 63) / 64) * ((N + 63) / 64));
     if constexpr (MM<DT>::KPL == 8)
       hipLaunchKernelGGL((linear_lds_kernel<DT, OT>), dim3(grid), dim3(256), 0, st, (const typename MM<DT>::T*)x, ldx,
                          (const typename MM<DT>::T*)w, ldw, bias, resid, ldr, (typename MM<OT>::T*)y, ldy,
-                         (typename MM<DT>::T*)y2, ldy2, M, N, K, relu, clamp, os);
+                         (typename MM<DT>::T*)y2, ldy2, M, N, K, relu, clamp, os, ext);
+    else if (os.yt == nullptr && al16(x) && al16(w) && ldx % 4 == 0 && ldw % 4 == 0)
+      hipLaunchKernelGGL((linear_lds_f32_kernel<OT>), dim3(grid), dim3(256), 0, st, (const float*)x, ldx,
+                         (const float*)w, ldw, bias, resid, ldr, (typename MM<OT>::T*)y, ldy, (float*)y2, ldy2, M,
+                         N, K, relu, clamp, ext);
     else
       hipLaunchKernelGGL((linear_quad_kernel<DT, OT>), dim3(grid), dim3(256), 0, st, (const typename MM<DT>::T*)x,
                          ldx, (const typename MM<DT>::T*)w, ldw, bias, resid, ldr, (typename MM<OT>::T*)y, ldy,
-                         (typename MM<DT>::T*)y2, ldy2, M, N, K, relu, clamp, os);
+                         (typename MM<DT>::T*)y2, ldy2, M, N, K, relu, clamp, os, ext);
   }
 }
 
@@ -864,27 +1004,28 @@ template <int DT, int OT, typename XT>
 static void launch_linear_t(bool ln, const void* x, int64_t ldx, const void* w, int64_t ldw, const float* bias,
                             const float* resid, int64_t ldr, void* y, int64_t ldy, void* y2, int64_t ldy2, int64_t M,
                             int64_t N, int64_t K, int relu, float clamp, const float* lnw, const float* lnb,
-                            float eps, hipStream_t st) {
+                            float eps, hipStream_t st, LinExt ext = kNoLinExt) {
   const int64_t tiles32 = ((M + 31) / 32) * ((N + 31) / 32);
   if (!ln && std::is_same_v<XT, typename MM<DT>::T> && tiles32 >= 2048) {
-    launch_linear_quad<DT, OT, XT>(x, ldx, w, ldw, bias, resid, ldr, y, ldy, y2, ldy2, M, N, K, relu, clamp, st);
+    launch_linear_quad<DT, OT, XT>(x, ldx, w, ldw, bias, resid, ldr, y, ldy, y2, ldy2, M, N, K, relu, clamp, st,
+                                   OutSplit{0, 1, 0, 0, nullptr}, ext);
     return;
   }
   const unsigned grid = (unsigned)tiles32;
   if (ln)
     hipLaunchKernelGGL((linear_kernel<DT, OT, XT, true>), dim3(grid), dim3(256), 0, st, (const XT*)x, ldx,
                        (const typename MM<DT>::T*)w, ldw, bias, resid, ldr, (typename MM<OT>::T*)y, ldy,
-                       (typename MM<DT>::T*)y2, ldy2, M, N, K, relu, clamp, lnw, lnb, eps);
+                       (typename MM<DT>::T*)y2, ldy2, M, N, K, relu, clamp, lnw, lnb, eps, ext);
   else
     hipLaunchKernelGGL((linear_kernel<DT, OT, XT, false>), dim3(grid), dim3(256), 0, st, (const XT*)x, ldx,
                        (const typename MM<DT>::T*)w, ldw, bias, resid, ldr, (typename MM<OT>::T*)y, ldy,
-                       (typename MM<DT>::T*)y2, ldy2, M, N, K, relu, clamp, lnw, lnb, eps);
+                       (typename MM<DT>::T*)y2, ldy2, M, N, K, relu, clamp, lnw, lnb, eps, ext);
 }
 
 static int linear_impl(const void* x, int64_t ldx, int x_dtype, const void* w, int64_t ldw, const float* bias,
                        const float* resid, int64_t ldr, void* y, int64_t ldy, int y_dtype, void* y2, int64_t ldy2,
                        int64_t M, int64_t N, int64_t K, int relu, float clamp, int ln, const float* lnw,
-                       const float* lnb, float ln_eps, int dtype, hipStream_t st) {
+                       const float* lnb, float ln_eps, int dtype, hipStream_t st, LinExt ext = kNoLinExt) {
   if (M < 0 || N < 0 || K < 0) return HCLSM_ERR_SHAPE;
   if (M == 0 || N == 0) return 0;
   if (!x || !w || !y) return HCLSM_ERR_NULL;
@@ -896,7 +1037,7 @@ static int linear_impl(const void* x, int64_t ldx, int x_dtype, const void* w, i
 #define HCLSM_LIN(D, O, XD, XT)                                                                              \
   if (dtype == D && y_dtype == O && x_dtype == XD) {                                                         \
     launch_linear_t<D, O, XT>(LNf, x, ldx, w, ldw, bias, resid, ldr, y, ldy, y2, ldy2, M, N, K, relu, clamp, lnw, \
-                              lnb, ln_eps, st);                                                              \
+                              lnb, ln_eps, st, ext);                                                         \
     HCLSM_LAUNCH_CHECK();                                                                                    \
     return 0;                                                                                                \
   }
@@ -911,6 +1052,17 @@ static int linear_impl(const void* x, int64_t ldx, int x_dtype, const void* w, i
   HCLSM_LIN(HCLSM_F32, HCLSM_F32, HCLSM_F32, float)
 #undef HCLSM_LIN
   return HCLSM_ERR_DTYPE;
+}
+
+// Linear layer with a device-side row count and an optional gated-linear epilogue, for composite
+// entry points in other files (declared in internal.h).
+int linear_rows(const void* x, int64_t ldx, int x_dtype, const void* w, int64_t ldw, const float* resid,
+                int64_t ldr, void* y, int64_t ldy, int y_dtype, int64_t M, int64_t N, int64_t K, int ln,
+                const float* ln_w, const float* ln_b, float ln_eps, const void* glu, int64_t ldg,
+                const int32_t* m_dev, int64_t m_mul, int dtype, hipStream_t st) {
+  if (glu && (x_dtype != dtype && x_dtype != HCLSM_F32)) return HCLSM_ERR_DTYPE;
+  return linear_impl(x, ldx, x_dtype, w, ldw, nullptr, resid, ldr, y, ldy, y_dtype, nullptr, 0, M, N, K, 0, 0.f, ln,
+                     ln_w, ln_b, ln_eps, dtype, st, LinExt{m_dev, m_mul, glu, ldg});
 }
 
 static int gru_impl(const void* x, int64_t ldx, const void* hb, int64_t ldhb, const float* h, int64_t ldh,
@@ -945,10 +1097,11 @@ template <int DTI, int DTO>
 __global__ void __launch_bounds__(256)
 layer_norm_kernel(const typename MM<DTI>::T* __restrict__ x, int64_t ldx, const float* __restrict__ w,
                   const float* __restrict__ b, typename MM<DTO>::T* __restrict__ y, int64_t ldy, int64_t M,
-                  int D, float eps) {
+                  int D, float eps, LinExt ext) {
   constexpr int MAXPL = 16;  // elements per lane held in registers (D <= 1024); larger D re-reads
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
+  M = ext_rows(ext, M);
   if (row >= M) return;
   const typename MM<DTI>::T* xr = x + row * ldx;
   float vals[MAXPL];
@@ -997,7 +1150,7 @@ layer_norm_kernel(const typename MM<DTI>::T* __restrict__ x, int64_t ldx, const 
 }
 
 static int ln_impl(const void* x, int64_t ldx, const float* w, const float* b, void* y, int64_t ldy, int64_t M,
-                   int64_t D, float eps, int in_dtype, int out_dtype, hipStream_t st) {
+                   int64_t D, float eps, int in_dtype, int out_dtype, hipStream_t st, LinExt ext = kNoLinExt) {
   if (M < 0 || D < 0 || D > 0x7fffffff) return HCLSM_ERR_SHAPE;
   if (M == 0 || D == 0) return 0;
   if (!x || !y) return HCLSM_ERR_NULL;
@@ -1005,7 +1158,7 @@ static int ln_impl(const void* x, int64_t ldx, const float* w, const float* b, v
 #define HCLSM_LN(I, O)                                                                                     \
   if (in_dtype == I && out_dtype == O) {                                                                   \
     hipLaunchKernelGGL((layer_norm_kernel<I, O>), dim3(grid), dim3(256), 0, st, (const MM<I>::T*)x, ldx, w, b, \
-                       (MM<O>::T*)y, ldy, M, (int)D, eps);                                                 \
+                       (MM<O>::T*)y, ldy, M, (int)D, eps, ext);                                            \
     HCLSM_LAUNCH_CHECK();                                                                                  \
     return 0;                                                                                              \
   }
@@ -1017,6 +1170,12 @@ static int ln_impl(const void* x, int64_t ldx, const float* w, const float* b, v
   HCLSM_LN(HCLSM_F16, HCLSM_F16)
 #undef HCLSM_LN
   return HCLSM_ERR_DTYPE;
+}
+
+int layer_norm_rows(const void* x, int64_t ldx, const float* w, const float* b, void* y, int64_t ldy, int64_t M,
+                    int64_t D, float eps, int in_dtype, int out_dtype, const int32_t* m_dev, int64_t m_mul,
+                    hipStream_t st) {
+  return ln_impl(x, ldx, w, b, y, ldy, M, D, eps, in_dtype, out_dtype, st, LinExt{m_dev, m_mul, nullptr, 0});
 }
 
 }  // namespace hclsm

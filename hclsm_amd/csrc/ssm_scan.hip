@@ -46,7 +46,6 @@ __device__ __forceinline__ float scan_dt(float v) {
   return v;
 }
 
-__device__ __forceinline__ float silu_f(float g) { return g * __builtin_amdgcn_rcpf(1.f + __expf(-g)); }
 
 constexpr int SCAN_TCHUNK = 8;
 constexpr int SCAN_MAX_BLOCK = 256;

@@ -3,7 +3,8 @@
 gather_events / scatter_events run on the device-built int32 event index and the byte-exact
 gather / scatter kernels (rule mask > 0.5, ascending event order, exact zero padding); the
 top-down gating of forward() is unchanged torch math.  gather_events still returns K_max as a
-Python int, as the reference does (:63), which costs one host read of the index statistics.
+Python int, as the reference does (:63), which costs one host read of the index statistics;
+the packed counterparts (gather_events_packed, forward_packed, level1_events_packed) need none.
 """
 
 from __future__ import annotations
@@ -11,8 +12,9 @@ from __future__ import annotations
 import torch
 import torch.nn as nn
 
-from hclsm_amd.kernels.sparse_event_attn import (build_event_index, gather_events_padded,
-                                                 pad_mask_from_index, scatter_events_padded)
+from hclsm_amd.kernels.sparse_event_attn import (EventIndex, build_event_index, gather_events_packed,
+                                                 gather_events_padded, pad_mask_from_index,
+                                                 scatter_events_packed, scatter_events_padded)
 
 
 class HierarchyManager(nn.Module):
@@ -38,6 +40,9 @@ class HierarchyManager(nn.Module):
 
     def forward(self, level0_states, level1_states, level2_context, event_mask, obj_mask=None):
         combined = self.scatter_events(level0_states, level1_states, event_mask)      # :143
+        return self._top_down(combined, level2_context, obj_mask)
+
+    def _top_down(self, combined, level2_context, obj_mask):
         if level2_context is not None:                                                # :146-156
             l2_proj = self.l2_to_l1(level2_context.mean(dim=1))
             l2b = l2_proj[:, None, None, :].expand_as(combined)
@@ -46,3 +51,30 @@ class HierarchyManager(nn.Module):
         if obj_mask is not None:                                                      # :159-160
             combined = combined * obj_mask[:, None, :, None]
         return combined
+
+    # ---- packed, sync-free counterparts (no K_max host read)
+
+    def gather_events_packed(self, states: torch.Tensor, event_mask: torch.Tensor):
+        """(B, T, N, D) -> (packed event states (B*T, N, D), index): event e < index.total() in row e,
+        zero rows after.  Differentiable; no host sync."""
+        idx = build_event_index(event_mask, "gt_half")
+        return gather_events_packed(states, idx), idx
+
+    def forward_packed(self, level0_states, level1_packed, index: EventIndex, level2_context=None,
+                       obj_mask=None):
+        """forward() with Level-1 outputs in the packed layout of gather_events_packed."""
+        combined = scatter_events_packed(level0_states, level1_packed, index)
+        return self._top_down(combined, level2_context, obj_mask)
+
+
+def level1_events_packed(hierarchy: HierarchyManager, level1, level0_states: torch.Tensor,
+                         event_mask: torch.Tensor, obj_mask: torch.Tensor | None = None,
+                         level2_context: torch.Tensor | None = None) -> torch.Tensor:
+    """The Level-1 step of the reference model (model.py:298-310: gather_events, level1_event,
+    hierarchy_manager) on packed events, without host synchronisation: event index on the device,
+    packed gather, Level-1 over the live events only, packed scatter plus the top-down gating.
+    Returns the combined (B, T, N, D) states.  (Level-2 consumes the padded gather and is not on
+    this path.)"""
+    ev, idx = hierarchy.gather_events_packed(level0_states, event_mask)
+    out = level1.forward_packed(ev, idx, obj_mask)
+    return hierarchy.forward_packed(level0_states, out, idx, level2_context, obj_mask)

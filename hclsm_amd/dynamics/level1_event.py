@@ -14,6 +14,8 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from hclsm_amd.kernels.event_attention import slots_attention
+from hclsm_amd.kernels.level1_packed import Level1Weights, level1_forward_packed
+from hclsm_amd.kernels.sparse_event_attn import EventIndex
 
 
 class SwiGLUFFN(nn.Module):
@@ -83,3 +85,38 @@ class Level1EventDynamics(nn.Module):
         if event_pad_mask is not None:                                           # :130-131
             x = x * event_pad_mask[:, :, None, None]
         return x
+
+    def _needs_grad(self, x: torch.Tensor) -> bool:
+        if not torch.is_grad_enabled():
+            return False
+        return x.requires_grad or any(p.requires_grad for p in self.parameters())
+
+    def forward_packed(self, event_states: torch.Tensor, index: EventIndex,
+                       obj_mask: torch.Tensor | None = None) -> torch.Tensor:
+        """The same computation on packed events: event_states (capacity, N, d_slot) as gathered by
+        gather_packed / gather_events_packed with ``index`` (event e < index.total() in row e);
+        returns (capacity, N, d_slot), rows past the live count unspecified.  No host sync.
+
+        Without autograd this is one C call (hclsm_level1_forward, compute in fp32, or bf16 under a
+        bf16 autocast).  With autograd it is this module's ops over all capacity rows, so the rows past
+        the live count must be finite (gather_events_packed zero-fills them)."""
+        cap, N, D = event_states.shape
+        if not self._needs_grad(event_states):
+            dtype = torch.bfloat16 if (torch.is_autocast_enabled("cuda") and
+                                       torch.get_autocast_dtype("cuda") == torch.bfloat16) else torch.float32
+            W = Level1Weights.from_module(self, dtype)
+            return level1_forward_packed(event_states, index, obj_mask, W,
+                                         out_dtype=event_states.dtype if event_states.dtype in
+                                         (torch.float32, dtype) else torch.float32)
+        x = self.proj_in(event_states)
+        kpm = None
+        if obj_mask is not None:
+            # batch row of each packed event; entries past the live count are clamped to a valid row
+            rows = index.rows[:cap].long().clamp(0, index.B - 1)
+            kpm = ~(obj_mask[rows] > 0.5)
+        for block in self.blocks:
+            if self.use_gradient_checkpointing and self.training:
+                x = torch.utils.checkpoint.checkpoint(block, x, kpm, use_reentrant=False)
+            else:
+                x = block(x, key_padding_mask=kpm)
+        return self.proj_out(self.norm(x))

@@ -28,7 +28,11 @@ from hclsm_amd.kernels.sparse_event_attn import (
     scatter_events_padded,
     gather_packed,
     scatter_packed,
+    gather_events_packed,
+    scatter_events_packed,
 )
+
+from hclsm_amd.kernels.level1_packed import Level1Weights, level1_forward_packed
 
 from hclsm_amd.kernels.event_attention import (
     event_attention,
@@ -95,6 +99,10 @@ __all__ = [
     "scatter_events_padded",
     "gather_packed",
     "scatter_packed",
+    "gather_events_packed",
+    "scatter_events_packed",
+    "Level1Weights",
+    "level1_forward_packed",
     "event_attention",
     "track_causal_event_attention",
     "slots_attention",

@@ -202,13 +202,15 @@ def pad_mask_from_index(idx: EventIndex, K: int, dtype=torch.float32) -> torch.T
     return (ar[None, :] < idx.counts[:, None]).to(dtype)
 
 
-def gather_packed(src: torch.Tensor, idx: EventIndex, capacity: int | None = None) -> torch.Tensor:
-    """(B, T, ...) -> (capacity, ...) packed event rows (first idx.total() valid); no host sync
-    when ``capacity`` is given."""
+def gather_packed(src: torch.Tensor, idx: EventIndex, capacity: int | None = None,
+                  zero_fill: bool = False) -> torch.Tensor:
+    """(B, T, ...) -> (capacity, ...) packed event rows (first idx.total() valid); no host sync.
+    Rows past the live count are left uninitialised, or zero with ``zero_fill``."""
     require_gpu("gather_packed", src)
     s = src.contiguous()
     cap = idx.B * idx.T if capacity is None else int(capacity)
-    out = torch.empty((cap,) + tuple(s.shape[2:]), dtype=s.dtype, device=s.device)
+    alloc = torch.zeros if zero_fill else torch.empty
+    out = alloc((cap,) + tuple(s.shape[2:]), dtype=s.dtype, device=s.device)
     rc = _lib.lib().hclsm_event_gather_packed(_lib.ptr(s), _lib.ptr(out), _row_bytes(s), idx.B, idx.T, cap,
                                               idx.ptr("rows"), idx.ptr("indices"), idx.ptr("stats"),
                                               _lib.stream_of(s))
@@ -216,22 +218,69 @@ def gather_packed(src: torch.Tensor, idx: EventIndex, capacity: int | None = Non
     return out
 
 
-def scatter_packed(base: torch.Tensor | None, packed: torch.Tensor, idx: EventIndex,
+def scatter_packed(base: torch.Tensor | None, packed: torch.Tensor | None, idx: EventIndex,
                    out: torch.Tensor | None = None) -> torch.Tensor:
     """out[b, t] = packed[offsets[b] + slot_of[b, t]] at events, base[b, t] elsewhere
-    (zeros if base is None)."""
+    (either one None reads as zeros)."""
     require_gpu("scatter_packed", base, packed)
-    p = packed.contiguous()
+    if base is None and packed is None:
+        raise ValueError("scatter_packed: base and packed are both None")
+    p = None if packed is None else packed.contiguous()
     b = None if base is None else base.contiguous()
+    like = p if p is not None else b
     if out is None:
-        out = torch.empty((idx.B, idx.T) + tuple(p.shape[1:]), dtype=p.dtype, device=p.device)
+        rest = tuple(p.shape[1:]) if p is not None else tuple(b.shape[2:])
+        out = torch.empty((idx.B, idx.T) + rest, dtype=like.dtype, device=like.device)
     rb = out.element_size()
     for s in out.shape[2:]:
         rb *= s
     rc = _lib.lib().hclsm_event_scatter_packed(_lib.ptr(b), _lib.ptr(p), _lib.ptr(out), rb, idx.B, idx.T,
-                                               idx.ptr("offsets"), idx.ptr("slot_of"), _lib.stream_of(p))
+                                               idx.ptr("offsets"), idx.ptr("slot_of"), _lib.stream_of(like))
     _lib.check(rc, "hclsm_event_scatter_packed")
     return out
+
+
+class _GatherPacked(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, states, idx):
+        ctx.idx = idx
+        ctx.like = torch.empty((0, 0) + tuple(states.shape[2:]), dtype=states.dtype, device=states.device)
+        return gather_packed(states, idx, zero_fill=True)
+
+    @staticmethod
+    def backward(ctx, g):
+        # d states[b, t] = g[offsets[b] + slot_of[b, t]] at events, 0 elsewhere
+        return scatter_packed(None, g.contiguous(), ctx.idx), None
+
+
+class _ScatterPacked(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, base, packed, idx):
+        ctx.idx = idx
+        if packed.dtype != base.dtype:
+            packed = packed.to(base.dtype)
+        return scatter_packed(base, packed, idx)
+
+    @staticmethod
+    def backward(ctx, g):
+        g = g.contiguous()
+        g_base = scatter_packed(g, None, ctx.idx)           # zero at replaced rows
+        g_packed = gather_packed(g, ctx.idx, zero_fill=True)
+        return g_base, g_packed, None
+
+
+def gather_events_packed(states: torch.Tensor, idx: EventIndex) -> torch.Tensor:
+    """Differentiable packed gather: (B, T, ...) -> (B*T, ...) with event e < idx.total() in row e
+    (rows ascending per batch row, batch rows in order) and zero rows after; no host sync."""
+    require_gpu("gather_events_packed", states)
+    return _GatherPacked.apply(states, idx)
+
+
+def scatter_events_packed(base: torch.Tensor, packed: torch.Tensor, idx: EventIndex) -> torch.Tensor:
+    """Differentiable packed scatter: base with out[b, t] = packed[offsets[b] + slot_of[b, t]] at
+    events; no host sync."""
+    require_gpu("scatter_events_packed", base, packed)
+    return _ScatterPacked.apply(base, packed, idx)
 
 
 # ---------------------------------------------------------------------------

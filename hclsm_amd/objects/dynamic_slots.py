@@ -85,7 +85,7 @@ class DynamicSlotAttention(nn.Module):
                 else:
                     slots = self._iteration_step(slots, k, v)
         else:
-            dtype = torch.bfloat16 if (torch.is_autocast_enabled() and torch.get_autocast_gpu_dtype() == torch.bfloat16) \
+            dtype = torch.bfloat16 if (torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16) \
                 else torch.float32
             W = SlotWeights.from_module(self, dtype)
             mode = SlotMode(logit_clamp=_LOGIT_CLAMP, renorm_eps=None, slot_clamp=_SLOT_CLAMP)

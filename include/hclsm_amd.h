@@ -300,6 +300,33 @@ int hclsm_slot_attention_forward(const HclsmSlotWeights* W, const float* inputs,
                                  float renorm_eps, float slot_clamp, int dtype, void* workspace,
                                  int64_t workspace_bytes, void* stream);
 
+/* Workspace bytes for hclsm_level1_forward. */
+int64_t hclsm_level1_forward_workspace(int64_t capacity, int64_t N, int64_t d_model, int64_t hidden, int dtype);
+
+/*
+ * Level1EventDynamics.forward on packed events, without host synchronisation.  Event e < *n_events
+ * (a device-side count, e.g. the event index's stats[0]) is rows e*N .. e*N+N-1 of ev [capacity*N, d_slot]
+ * (ev_dtype: F32 or dtype); the same rows of out [capacity*N, d_slot] (out_dtype: F32 or dtype) receive
+ *   x = ev proj_in^T; per layer x += MHA over the event's N slots (LN1 first; keys j with
+ *   obj_mask[ev_rows[e], j] <= 0.5 excluded; obj_mask [B, N] float32 nullable) and x += SwiGLU(LN2 x);
+ *   out = LN(x) proj_out^T.
+ * Rows of later events are untouched.  GEMM operands in `dtype` (F32 / BF16 / F16) with fp32
+ * accumulation; the residual stream is fp32.  d_model / n_heads in {16, 32, 64, 128}; d_slot, d_model,
+ * hidden multiples of 32 (4 for F32).  params: host array of 4 + 9 * n_layers device pointers:
+ *   proj_in [d_model, d_slot], norm_w [d_model], norm_b [d_model], proj_out [d_slot, d_model], then per
+ *   layer ln1_w, ln1_b [d_model], in_proj [3 d_model, d_model], out_proj [d_model, d_model], ln2_w,
+ *   ln2_b [d_model], w1 [hidden, d_model], w3 [hidden, d_model], w2 [d_model, hidden]
+ * (LayerNorm weights float32, the rest in `dtype`; no biases, as in the reference).  A query whose keys
+ * are all excluded gives NaN, as torch's softmax over all -inf does.
+ * Replaces: Level1EventDynamics.forward with EventTransformerBlock and SwiGLUFFN
+ *   (hclsm/dynamics/level1_event.py:17-133) on the events gathered by HierarchyManager.gather_events.
+ */
+int hclsm_level1_forward(const void* ev, int ev_dtype, void* out, int out_dtype, const int32_t* n_events,
+                         int64_t capacity, int64_t N, const int32_t* ev_rows, const float* obj_mask,
+                         int64_t d_slot, int64_t d_model, int64_t n_heads, int64_t hidden, int64_t n_layers,
+                         const void* const* params, float ln_eps, int dtype, void* workspace,
+                         int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

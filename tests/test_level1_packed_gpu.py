@@ -1,0 +1,163 @@
+"""GPU tests of the packed, sync-free Level-1 path: hclsm_level1_forward (one C call for
+Level1EventDynamics over the live events), the differentiable packed gather / scatter, and
+level1_events_packed (index, gather, Level-1, scatter and top-down gating without a host read).
+
+Parity: the Level-1 output of every live event against oracle/modules.py::level1_ref on the padded
+events (fp32: normwise 1e-5; bf16 compute: 2e-2); the whole packed step against the reference-shaped
+padded flow (gather_events with its K_max host read, Level-1, HierarchyManager.forward), outputs and
+gradients."""
+
+from __future__ import annotations
+
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import modules as om
+from oracle.ssm_scan import normwise_rel_err
+
+pytestmark = pytest.mark.gpu
+
+L1 = SimpleNamespace(d_model=256, n_layers=2, n_heads=4)     # HCLSMConfig.tiny() level1 (config.py:206)
+D_SLOT, D_L2 = 128, 384
+
+
+def _np(t):
+    return t.detach().double().cpu().numpy()
+
+
+def _sd(m):
+    return {k: _np(v) for k, v in m.state_dict().items()}
+
+
+def _case(B, T, N, seed, p=0.35, empty_row=True, dead=True):
+    g = torch.Generator().manual_seed(seed)
+    states = torch.randn(B, T, N, D_SLOT, generator=g)
+    mask = (torch.rand(B, T, generator=g) < p).float()
+    if empty_row and B > 1:
+        mask[1] = 0.0
+    obj = torch.ones(B, N)
+    if dead:
+        for b in range(B):
+            k = int(torch.randint(0, N // 2, (1,), generator=g))
+            obj[b, N - k:] = 0.0
+    return states.cuda(), mask.cuda(), obj.cuda()
+
+
+def _modules(seed):
+    from hclsm_amd.dynamics import HierarchyManager, Level1EventDynamics
+    torch.manual_seed(seed)
+    return HierarchyManager(D_SLOT, D_L2).cuda(), Level1EventDynamics(L1, D_SLOT).cuda()
+
+
+def _live_rows(out, idx):
+    """Packed rows of the live events, in (b, k) order, and the (b, k) list."""
+    counts = idx.counts.cpu().tolist()
+    offs = idx.offsets.cpu().tolist()
+    rows, bk = [], []
+    for b, c in enumerate(counts):
+        for k in range(c):
+            rows.append(offs[b] + k)
+            bk.append((b, k))
+    return out[rows], bk
+
+
+@pytest.mark.parametrize("B,T,N,seed", [(3, 7, 16, 0), (4, 12, 16, 1), (2, 5, 32, 2)])
+def test_level1_packed_matches_oracle_fp32(B, T, N, seed):
+    hm, l1 = _modules(seed)
+    states, mask, obj = _case(B, T, N, seed)
+    with torch.no_grad():
+        ev, idx = hm.gather_events_packed(states, mask)
+        out = l1.forward_packed(ev, idx, obj)
+        ev_pad, pad, K = hm.gather_events(states, mask)
+    ref = om.level1_ref(_np(ev_pad), _np(pad), _np(obj), _sd(l1), L1.n_layers, L1.n_heads)
+    got, bk = _live_rows(out, idx)
+    assert len(bk) == idx.total() and len(bk) > 0
+    want = np.stack([ref[b, k] for b, k in bk])
+    assert normwise_rel_err(_np(got), want) <= 1e-5
+
+
+def test_level1_packed_bf16_autocast():
+    hm, l1 = _modules(3)
+    states, mask, obj = _case(4, 16, 16, 3)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        ev, idx = hm.gather_events_packed(states, mask)
+        out = l1.forward_packed(ev, idx, obj)
+    with torch.no_grad():
+        ev_pad, pad, K = hm.gather_events(states, mask)
+    ref = om.level1_ref(_np(ev_pad), _np(pad), _np(obj), _sd(l1), L1.n_layers, L1.n_heads)
+    got, bk = _live_rows(out, idx)
+    assert out.dtype == torch.float32
+    assert normwise_rel_err(_np(got), np.stack([ref[b, k] for b, k in bk])) <= 2e-2
+
+
+def test_level1_packed_all_slots_dead_gives_nan_like_softmax():
+    """An event whose slots are all dead: every key excluded, softmax over all -inf -> NaN rows, as
+    nn.MultiheadAttention gives; other rows unaffected."""
+    hm, l1 = _modules(4)
+    states, mask, obj = _case(2, 6, 16, 4, empty_row=False, dead=False)
+    mask[:, 0] = 1.0
+    obj[1] = 0.0
+    with torch.no_grad():
+        ev, idx = hm.gather_events_packed(states, mask)
+        out = l1.forward_packed(ev, idx, obj)
+    got, bk = _live_rows(out, idx)
+    dead_rows = torch.tensor([b == 1 for b, _ in bk], device="cuda")
+    assert torch.isnan(got[dead_rows]).all()
+    assert torch.isfinite(got[~dead_rows]).all()
+
+
+def test_level1_packed_no_events():
+    hm, l1 = _modules(5)
+    states, mask, obj = _case(2, 6, 16, 5)
+    mask.zero_()
+    from hclsm_amd.dynamics import level1_events_packed
+    with torch.no_grad():
+        comb = level1_events_packed(hm, l1, states, mask, obj)
+    assert torch.equal(comb, states * obj[:, None, :, None])
+
+
+def _padded_flow(hm, l1, states, mask, obj, l2):
+    ev, pad, K = hm.gather_events(states, mask)
+    return hm(states, l1(ev, pad, obj), l2, mask, obj)
+
+
+def test_level1_events_packed_matches_padded_flow_without_host_sync():
+    from hclsm_amd.dynamics import level1_events_packed
+    hm, l1 = _modules(6)
+    states, mask, obj = _case(3, 10, 16, 6)
+    l2 = torch.randn(3, 4, D_L2, device="cuda")
+    with torch.no_grad():
+        want = _padded_flow(hm, l1, states, mask, obj, l2)
+        level1_events_packed(hm, l1, states, mask, obj, l2)   # warm caches (weights, workspace)
+        torch.cuda.synchronize()
+        torch.cuda.set_sync_debug_mode("error")
+        try:
+            got = level1_events_packed(hm, l1, states, mask, obj, l2)
+        finally:
+            torch.cuda.set_sync_debug_mode("default")
+    assert normwise_rel_err(_np(got), _np(want)) <= 1e-5
+
+
+def test_level1_events_packed_gradients_match_padded_flow():
+    from hclsm_amd.dynamics import level1_events_packed
+    hm, l1 = _modules(7)
+    states, mask, obj = _case(2, 8, 16, 7)
+    l2 = torch.randn(2, 3, D_L2, device="cuda")
+    w = torch.randn(2, 8, 16, D_SLOT, device="cuda")
+    xa = states.clone().requires_grad_()
+    (level1_events_packed(hm, l1, xa, mask, obj, l2) * w).sum().backward()
+    ga = {n: None if p.grad is None else p.grad.clone()
+          for n, p in list(hm.named_parameters()) + list(l1.named_parameters())}
+    hm.zero_grad()
+    l1.zero_grad()
+    xb = states.clone().requires_grad_()
+    (_padded_flow(hm, l1, xb, mask, obj, l2) * w).sum().backward()
+    assert normwise_rel_err(_np(xa.grad), _np(xb.grad)) <= 1e-5
+    for n, p in list(hm.named_parameters()) + list(l1.named_parameters()):
+        if p.grad is None:
+            assert ga[n] is None or ga[n].abs().sum() == 0, n
+            continue
+        assert normwise_rel_err(_np(ga[n]), _np(p.grad)) <= 1e-5, n
