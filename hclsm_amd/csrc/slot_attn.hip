@@ -294,6 +294,106 @@ linear_lds_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const t
   }
 }
 
+// 128x128 output tile per workgroup, 16-bit operands, for wide layers (N >= 768) with many rows: the tile's
+// A and W rows staged in LDS in K chunks of 64 (next chunk's global loads in flight), each wave a 64x64
+// quadrant (4 x 4 MFMA tiles), so every LDS fragment feeds four MFMAs and each staged byte eight times the
+// FLOPs of the 64x64 tile.  37 KB of LDS.
+constexpr int LB_KC = 64;
+constexpr int LB_LD = LB_KC + 8;   // pitch 144 B: the 16 rows of a fragment read hit distinct banks
+
+template <int DT, int OT>
+__global__ void __launch_bounds__(256)
+linear_lds128_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const typename MM<DT>::T* __restrict__ W,
+                     int64_t ldw, const float* __restrict__ bias, const float* __restrict__ resid, int64_t ldr,
+                     typename MM<OT>::T* __restrict__ Y, int64_t ldy, typename MM<DT>::T* __restrict__ Y2,
+                     int64_t ldy2, int64_t M, int64_t N, int64_t K, int relu, float clamp_v, LinExt ext) {
+  using A = MM<DT>;
+  using T = typename A::T;
+  static_assert(A::KPL == 8, "16-bit operands");
+  __shared__ __align__(16) T As[128 * LB_LD];
+  __shared__ __align__(16) T Bs[128 * LB_LD];
+  const int64_t tiles_n = (N + 127) / 128;
+  const int64_t tm = blockIdx.x / tiles_n, tn = blockIdx.x - tm * tiles_n;
+  M = ext_rows(ext, M);
+  if (tm * 128 >= M) return;   // the whole workgroup, before any barrier
+  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, g = lane >> 4, li = lane & 15;
+  const int wr = wid >> 1, wc = wid & 1;
+  // staging map: 128 rows x (KC / 8) 16-byte units = 1024 units per operand, 4 per thread
+  const T* pa[4];
+  const T* pb[4];
+  int soff[4], ucol[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int u = tid + 256 * i, r = u >> 3;
+    ucol[i] = (u & 7) * 8;
+    int64_t ra = tm * 128 + r, rb = tn * 128 + r;
+    ra = ra < M ? ra : M - 1;
+    rb = rb < N ? rb : N - 1;
+    pa[i] = X + ra * ldx + ucol[i];
+    pb[i] = W + rb * ldw + ucol[i];
+    soff[i] = r * LB_LD + ucol[i];
+  }
+  uint4 ra_[4], rb_[4];
+  auto fetch = [&](int64_t k0, int kc) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool in = ucol[i] < kc;
+      ra_[i] = in ? *reinterpret_cast<const uint4*>(pa[i] + k0) : make_uint4(0u, 0u, 0u, 0u);
+      rb_[i] = in ? *reinterpret_cast<const uint4*>(pb[i] + k0) : make_uint4(0u, 0u, 0u, 0u);
+    }
+  };
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  fetch(0, (int)(K < LB_KC ? K : LB_KC));
+  for (int64_t k0 = 0; k0 < K; k0 += LB_KC) {
+    const int kc = (int)(K - k0 < LB_KC ? K - k0 : LB_KC);
+    __syncthreads();   // the previous chunk is consumed
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      *reinterpret_cast<uint4*>(As + soff[i]) = ra_[i];
+      *reinterpret_cast<uint4*>(Bs + soff[i]) = rb_[i];
+    }
+    __syncthreads();
+    if (k0 + LB_KC < K) fetch(k0 + LB_KC, (int)(K - k0 - LB_KC < LB_KC ? K - k0 - LB_KC : LB_KC));
+    for (int s = 0; s < kc / 32; ++s) {
+      typename A::Op a[4], b[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        a[t] = A::load(As + (wr * 64 + 16 * t + li) * LB_LD + s * 32 + 8 * g);
+        b[t] = A::load(Bs + (wc * 64 + 16 * t + li) * LB_LD + s * 32 + 8 * g);
+      }
+#pragma unroll
+      for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+        for (int tj = 0; tj < 4; ++tj) acc[ti][tj] = A::mfma(a[ti], b[tj], acc[ti][tj]);
+    }
+  }
+  const int64_t r0 = tm * 128 + 64 * wr, c0 = tn * 128 + 64 * wc;
+#pragma unroll
+  for (int tj = 0; tj < 4; ++tj) {
+    const int64_t col = c0 + 16 * tj + li;
+    if (col >= N) continue;
+    const float bv = bias ? bias[col] : 0.f;
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t row = r0 + 16 * ti + 4 * g + r;
+        if (row >= M) continue;
+        float val = acc[ti][tj][r] + bv;
+        if (relu) val = fmaxf(val, 0.f);
+        val = ext_glu<DT>(ext, row, col, val);
+        if (resid) val += resid[row * ldr + col];
+        if (clamp_v > 0.f) val = fminf(fmaxf(val, -clamp_v), clamp_v);
+        Y[row * ldy + col] = MM<OT>::fromf(val);
+        if (Y2) Y2[row * ldy2 + col] = A::fromf(val);
+      }
+  }
+}
+
 // fp32 operands: the same 64x64 tile with A and W rows staged in LDS in K chunks of 64 floats (the next
 // chunk in flight), each wave a 32x32 quadrant of v_mfma_f32_16x16x4_f32.  The contraction is permuted
 // so that a lane's operands are float4 reads: in a 16-wide k block, lane group g owns k = 4g .. 4g+3 and
@@ -985,11 +1085,17 @@ static void launch_linear_quad(const void* x, int64_t ldx, const void* w, int64_
                                OutSplit os = OutSplit{0, 1, 0, 0, nullptr}, LinExt ext = kNoLinExt) {
   if constexpr (std::is_same_v<XT, typename MM<DT>::T>) {
     const unsigned grid = (unsigned)(((M + 63) / 64) * ((N + 63) / 64));
-    if constexpr (MM<DT>::KPL == 8)
-      hipLaunchKernelGGL((linear_lds_kernel<DT, OT>), dim3(grid), dim3(256), 0, st, (const typename MM<DT>::T*)x, ldx,
-                         (const typename MM<DT>::T*)w, ldw, bias, resid, ldr, (typename MM<OT>::T*)y, ldy,
-                         (typename MM<DT>::T*)y2, ldy2, M, N, K, relu, clamp, os, ext);
-    else if (os.yt == nullptr && al16(x) && al16(w) && ldx % 4 == 0 && ldw % 4 == 0)
+    const int64_t tiles128 = ((M + 127) / 128) * ((N + 127) / 128);
+    if constexpr (MM<DT>::KPL == 8) {
+      if (os.yt == nullptr && N >= 768 && tiles128 >= 512)
+        hipLaunchKernelGGL((linear_lds128_kernel<DT, OT>), dim3((unsigned)tiles128), dim3(256), 0, st,
+                           (const typename MM<DT>::T*)x, ldx, (const typename MM<DT>::T*)w, ldw, bias, resid, ldr,
+                           (typename MM<OT>::T*)y, ldy, (typename MM<DT>::T*)y2, ldy2, M, N, K, relu, clamp, ext);
+      else
+        hipLaunchKernelGGL((linear_lds_kernel<DT, OT>), dim3(grid), dim3(256), 0, st, (const typename MM<DT>::T*)x,
+                           ldx, (const typename MM<DT>::T*)w, ldw, bias, resid, ldr, (typename MM<OT>::T*)y, ldy,
+                           (typename MM<DT>::T*)y2, ldy2, M, N, K, relu, clamp, os, ext);
+    } else if (os.yt == nullptr && al16(x) && al16(w) && ldx % 4 == 0 && ldw % 4 == 0)
       hipLaunchKernelGGL((linear_lds_f32_kernel<OT>), dim3(grid), dim3(256), 0, st, (const float*)x, ldx,
                          (const float*)w, ldw, bias, resid, ldr, (typename MM<OT>::T*)y, ldy, (float*)y2, ldy2, M,
                          N, K, relu, clamp, ext);

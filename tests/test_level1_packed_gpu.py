@@ -161,3 +161,30 @@ def test_level1_events_packed_gradients_match_padded_flow():
             assert ga[n] is None or ga[n].abs().sum() == 0, n
             continue
         assert normwise_rel_err(_np(ga[n]), _np(p.grad)) <= 1e-5, n
+
+
+@pytest.mark.parametrize("autocast", [False, True])
+def test_level1_events_packed_small_preset_matches_padded_flow(autocast):
+    """The bench's small-preset shape (32 clips x T=64 x 32 slots, d_slot 192, d_model 384, 3 layers,
+    6 heads): large enough for the LDS-tiled GEMM kernels (64x64, 128x128, fp32) with device row counts
+    and the gated epilogue.  fp32: 1e-5 normwise against the padded flow; bf16 autocast: 2e-2."""
+    from hclsm_amd.dynamics import HierarchyManager, Level1EventDynamics, level1_events_packed
+    torch.manual_seed(8)
+    B, T, N, D, DL2 = 32, 64, 32, 192, 512
+    hm = HierarchyManager(D, DL2).cuda()
+    l1 = Level1EventDynamics(SimpleNamespace(d_model=384, n_layers=3, n_heads=6), D).cuda()
+    g = torch.Generator(device="cuda").manual_seed(9)
+    states = torch.randn(B, T, N, D, generator=g, device="cuda")
+    mask = (torch.rand(B, T, generator=g, device="cuda") < 0.15).float()
+    mask[:, 0] = 1.0
+    obj = (torch.rand(B, N, generator=g, device="cuda") < 0.8).float()
+    obj[:, 0] = 1.0
+    l2 = torch.randn(B, 4, DL2, generator=g, device="cuda")
+    with torch.no_grad():
+        want = _padded_flow(hm, l1, states, mask, obj, l2)
+        if autocast:
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                got = level1_events_packed(hm, l1, states, mask, obj, l2)
+        else:
+            got = level1_events_packed(hm, l1, states, mask, obj, l2)
+    assert normwise_rel_err(_np(got.float()), _np(want)) <= (2e-2 if autocast else 1e-5)

@@ -204,3 +204,24 @@ def test_large_linear_lds_tiles(dtype, tol):
                    stream=st)
     ref = np.clip(np.maximum(_np(x) @ _np(w).T + _np(b), 0) + _np(r), -2.0, 2.0)
     assert normwise_rel_err(_np(y), ref) <= tol
+
+
+@pytest.mark.parametrize("dtype,tol,M,N,K", [
+    (torch.bfloat16, 2e-2, 8200, 1040, 416),    # 128x128 LDS tiles: N >= 768, >= 512 tiles; ragged M, N; K tail
+    (torch.float16, 2e-2, 8200, 1040, 416),
+    (torch.float32, 1e-5, 2085, 1040, 420),     # fp32 LDS-staged tiles (float4 operands), K tail of 4
+])
+def test_large_linear_wide_tiles(dtype, tol, M, N, K):
+    """hclsm_linear at sizes that take the 128x128-tile 16-bit kernel and the fp32 LDS kernel, with bias,
+    ReLU, residual and clamp."""
+    from hclsm_amd.kernels import slot_iteration as si
+    g = torch.Generator().manual_seed(32)
+    x = torch.randn(M, K, generator=g).to(dtype)
+    w = (torch.randn(N, K, generator=g) / 16).to(dtype)
+    b = torch.randn(N, generator=g)
+    r = torch.randn(M, N, generator=g)
+    st = torch.cuda.current_stream().cuda_stream
+    y = si._linear(x.cuda(), w.cuda(), bias=b.cuda(), resid=r.cuda(), relu=True, clamp=2.0, out_dtype=torch.float32,
+                   stream=st)
+    ref = np.clip(np.maximum(_np(x) @ _np(w).T + _np(b), 0) + _np(r), -2.0, 2.0)
+    assert normwise_rel_err(_np(y), ref) <= tol
