@@ -26,6 +26,12 @@ adds tens of microseconds of Python dispatch per call, which is the size of the 
     hclsm_hip::slot_attention_forward(inputs, slots0, weights, n_iter, scale, logit_clamp, renorm_eps,
                                       slot_clamp, compute_dtype) -> slots fp32
         weights in the order of SLOT_WEIGHT_ORDER (dynamic_slots.py:98-164)
+    hclsm_hip::event_gather_packed(states, rows, indices, stats) -> (B*T, ...)
+        packed event rows, zero past the live count stats[0] (no host sync)
+    hclsm_hip::event_scatter_packed(base, packed, offsets, slot_of) -> (B, T, ...)
+    hclsm_hip::level1_forward(ev, stats, rows, obj_mask?, params, n_heads, ln_eps, compute_dtype) -> fp32
+        Level1EventDynamics over the live packed events (level1_event.py:17-133); params in the order of
+        Level1Weights (4 + 9 per layer); rows past the live count are zero
 """
 
 from __future__ import annotations
@@ -39,7 +45,9 @@ from hclsm_amd.kernels._common import require_gpu
 from hclsm_amd.kernels.event_attention import event_attention as _event_attention
 from hclsm_amd.kernels.slot_attention_kernel import _core_raw
 from hclsm_amd.kernels.slot_iteration import SlotMode, SlotWeights, slot_attention_forward as _slot_forward
-from hclsm_amd.kernels.sparse_event_attn import EventIndex, _gather_padded_raw, _mask_code, _scatter_padded_raw
+from hclsm_amd.kernels.level1_packed import Level1Weights, level1_forward_packed
+from hclsm_amd.kernels.sparse_event_attn import (EventIndex, _gather_padded_raw, _mask_code, _scatter_padded_raw,
+                                                 gather_packed, scatter_packed)
 from hclsm_amd.kernels.ssm_scan_bwd import scan_backward
 from hclsm_amd.kernels.ssm_scan_kernel import _block_forward, _scan_forward
 
@@ -190,3 +198,51 @@ def event_attention(q: Tensor, k: Tensor, v: Tensor, offsets: Tensor, indices: T
 @event_attention.register_fake
 def _(q, k, v, offsets, indices, key_pad, scale, mode, capacity):
     return q.new_empty((capacity, q.shape[2], q.shape[3]))
+
+
+@torch.library.custom_op("hclsm_hip::event_gather_packed", mutates_args=())
+def event_gather_packed(states: Tensor, rows: Tensor, indices: Tensor, stats: Tensor) -> Tensor:
+    idx = EventIndex(states.shape[0], states.shape[1], None, None, indices, rows, None, stats)
+    return gather_packed(states, idx, zero_fill=True)
+
+
+@event_gather_packed.register_fake
+def _(states, rows, indices, stats):
+    return states.new_empty((states.shape[0] * states.shape[1],) + tuple(states.shape[2:]))
+
+
+@torch.library.custom_op("hclsm_hip::event_scatter_packed", mutates_args=())
+def event_scatter_packed(base: Tensor, packed: Tensor, offsets: Tensor, slot_of: Tensor) -> Tensor:
+    B, T = slot_of.shape
+    idx = EventIndex(B, T, None, offsets, None, None, slot_of, None)
+    return scatter_packed(base, packed.to(base.dtype), idx)
+
+
+@event_scatter_packed.register_fake
+def _(base, packed, offsets, slot_of):
+    return torch.empty_like(base)
+
+
+@torch.library.custom_op("hclsm_hip::level1_forward", mutates_args=())
+def level1_forward(ev: Tensor, stats: Tensor, rows: Tensor, obj_mask: Optional[Tensor], params: list[Tensor],
+                   n_heads: int, ln_eps: float, compute_dtype: torch.dtype) -> Tensor:
+    if len(params) < 4 or (len(params) - 4) % 9:
+        raise ValueError("level1_forward: params are proj_in, norm.w, norm.b, proj_out, then 9 per layer")
+    n_layers = (len(params) - 4) // 9
+    mats = {0, 3} | {4 + 9 * l + j for l in range(n_layers) for j in (2, 3, 6, 7, 8)}
+    t = [p.detach().to(compute_dtype if i in mats else torch.float32).contiguous() for i, p in enumerate(params)]
+    d_model, d_slot = t[0].shape
+    hidden = t[10].shape[0] if n_layers else 32
+    W = Level1Weights(t, compute_dtype, d_slot, d_model, hidden, n_layers, int(n_heads), float(ln_eps))
+    cap, N = ev.shape[0], ev.shape[1]
+    B = obj_mask.shape[0] if obj_mask is not None else max(cap, 1)
+    idx = EventIndex(B, max(cap // max(B, 1), 1), None, None, None, rows, None, stats)
+    idx.B, idx.T = B, (cap + B - 1) // B if B else 1
+    out = level1_forward_packed(ev, idx, obj_mask, W, out_dtype=torch.float32)
+    live = torch.arange(cap, device=ev.device) < stats[0]          # device-side: rows past the count -> 0
+    return torch.where(live[:, None, None], out, out.new_zeros(()))
+
+
+@level1_forward.register_fake
+def _(ev, stats, rows, obj_mask, params, n_heads, ln_eps, compute_dtype):
+    return ev.new_empty(ev.shape, dtype=torch.float32)

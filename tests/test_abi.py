@@ -76,3 +76,25 @@ def test_scan_backward_argument_errors_before_launch(lib):
     assert f(*null13, 1, 4, 4, 65, 1, 0, None, 0, None) == -4
     assert f(*null13, 1, 1 << 20, 1 << 10, 16, 1, 0, None, 0, None) == -4   # 2^30 bf16 elements = 2 GiB
     assert f(*null13, 1, 4, 4, 4, 1, 0, None, 0, None) == -1
+
+
+def test_level1_forward_argument_errors_before_launch(lib):
+    f = lib.hclsm_level1_forward
+    ws = lib.hclsm_level1_forward_workspace
+    assert ws(-1, 4, 64, 256, 1) == -2
+    assert ws(4, 4, 64, 256, 9) == -3
+    assert ws(0, 4, 64, 256, 1) >= 0
+    args = dict(ev=None, evd=0, out=None, outd=0, n=None, cap=4, N=8, rows=None, om=None, ds=64, dm=64, H=4,
+                hid=256, L=1, params=None, eps=1e-5, dt=1, ws=None, wsb=0, st=None)
+
+    def call(**kw):
+        a = {**args, **kw}
+        return f(a["ev"], a["evd"], a["out"], a["outd"], a["n"], a["cap"], a["N"], a["rows"], a["om"], a["ds"], a["dm"],
+                 a["H"], a["hid"], a["L"], a["params"], a["eps"], a["dt"], a["ws"], a["wsb"], a["st"])
+    assert call(dm=60, H=4) == -4            # head dim 15: unsupported
+    assert call(dm=64, H=3) == -2            # d_model not a multiple of n_heads
+    assert call(dt=7) == -3                  # compute dtype
+    assert call(evd=2) == -3                 # ev dtype neither F32 nor the compute dtype
+    assert call(ds=48) == -4                 # d_slot not a multiple of 32 for 16-bit operands
+    assert call() == -1                      # NULL pointers
+    assert call(cap=0) == 0                  # nothing to do

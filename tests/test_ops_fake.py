@@ -41,6 +41,15 @@ def test_event_and_slot_ops_fake_shapes():
     assert s.shape == (2, 8, 64) and s.dtype == torch.float32
 
 
+def test_packed_level1_ops_fake_shapes():
+    i32 = torch.int32
+    assert OPS.event_gather_packed(_m(4, 9, 3, 5), _m(36, dt=i32), _m(36, dt=i32), _m(2, dt=i32)).shape == (36, 3, 5)
+    assert OPS.event_scatter_packed(_m(4, 9, 3, 5), _m(36, 3, 5), _m(5, dt=i32), _m(4, 9, dt=i32)).shape == (4, 9, 3, 5)
+    params = [_m(64, 32), _m(64), _m(64), _m(32, 64)] + [_m(1)] * 9
+    out = OPS.level1_forward(_m(36, 8, 32), _m(2, dt=i32), _m(36, dt=i32), _m(4, 8), params, 4, 1e-5, torch.bfloat16)
+    assert out.shape == (36, 8, 32) and out.dtype == torch.float32
+
+
 def test_ops_under_fake_tensor_mode():
     from torch._subclasses.fake_tensor import FakeTensorMode
     with FakeTensorMode():

@@ -80,3 +80,36 @@ def test_block_scan_op_equals_eager():
     y, y_pre = OPS.ssm_block_scan_fwd(z, dt_in, A_log, Bm, Cm, gate)
     assert torch.equal(y, ssm_block_scan(z, dt_in, A_log, Bm, Cm, gate))
     assert torch.allclose(y.float(), (y_pre.float() * torch.nn.functional.silu(gate.float())), rtol=1e-2, atol=1e-2)
+
+
+def test_packed_level1_ops_equal_eager():
+    """hclsm_hip::event_gather_packed / level1_forward / event_scatter_packed against the eager packed
+    path, and opcheck of their schemas and fake kernels."""
+    from types import SimpleNamespace
+    from hclsm_amd.dynamics import HierarchyManager, Level1EventDynamics
+    from hclsm_amd.kernels.level1_packed import Level1Weights
+    torch.manual_seed(12)
+    B, T, N, D = 3, 9, 8, 64
+    hm = HierarchyManager(D, 96).cuda()
+    l1 = Level1EventDynamics(SimpleNamespace(d_model=64, n_layers=2, n_heads=4), D).cuda()
+    g = torch.Generator().manual_seed(13)
+    states = torch.randn(B, T, N, D, generator=g).cuda()
+    mask = (torch.rand(B, T, generator=g) < 0.4).float().cuda()
+    obj = torch.ones(B, N, device="cuda")
+    obj[0, 5:] = 0.0
+    with torch.no_grad():
+        ev, idx = hm.gather_events_packed(states, mask)
+        want = l1.forward_packed(ev, idx, obj)
+        t = OPS.event_index(mask, 0)
+        evo = OPS.event_gather_packed(states, t[3], t[2], t[5])
+        assert torch.equal(evo, ev)
+        W = Level1Weights.from_module(l1, torch.float32)
+        got = OPS.level1_forward(evo, t[5], t[3], obj, W.tensors, 4, W.ln_eps, torch.float32)
+        n = idx.total()
+        assert torch.equal(got[:n], want[:n]) and got[n:].abs().sum() == 0
+        comb = OPS.event_scatter_packed(states, got, t[1], t[4])
+        assert torch.equal(comb, hm.forward_packed(states, want, idx))
+    torch.library.opcheck(OPS.event_gather_packed.default, (states, t[3], t[2], t[5]),
+                          test_utils=("test_schema", "test_faketensor"))
+    torch.library.opcheck(OPS.level1_forward.default, (evo, t[5], t[3], obj, W.tensors, 4, W.ln_eps, torch.float32),
+                          test_utils=("test_schema", "test_faketensor"))
