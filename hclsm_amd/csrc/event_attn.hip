@@ -158,8 +158,14 @@ event_attn_kernel(const typename AttnT<DT>::T* __restrict__ q, const typename At
 
     const int kt_end = (MODE == 0) ? qt : nqt - 1;   // MODE 0 = track-causal
     for (int kt = 0; kt <= kt_end; ++kt) {
+      // the tile's K and V rows are requested together, so their latencies overlap (segments here are
+      // short: one key tile is the common case)
       TT ke[QD];
       load_row<TT, QD>(row_ptr(k, kt * 16 + li) + g * QD, ke);
+      // V operand: keys j = kt*16 + 4g + r, columns NT*li .. NT*li + NT - 1
+      TT ve[4][NT];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) load_row<TT, NT>(row_ptr(v, kt * 16 + 4 * g + r) + NT * li, ve[r]);
       f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int c = 0; c < NCH; ++c) s4 = A::mfma(A::pack(ke + c * KPL), A::pack(qe + c * KPL), s4);
@@ -197,10 +203,6 @@ event_attn_kernel(const typename AttnT<DT>::T* __restrict__ q, const typename At
       psum += __shfl_xor(psum, 32, 64);
       l = l * alpha + psum;
       m = m_new;
-      // V operand: keys j = kt*16 + 4g + r, columns NT*li .. NT*li + NT - 1
-      TT ve[4][NT];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) load_row<TT, NT>(row_ptr(v, kt * 16 + 4 * g + r) + NT * li, ve[r]);
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         f32x4 o4 = {acc[0][nt] * alpha, acc[1][nt] * alpha, acc[2][nt] * alpha, acc[3][nt] * alpha};
