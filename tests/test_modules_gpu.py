@@ -276,3 +276,44 @@ def test_dynamic_slots_fused_forward_matches_oracle_and_grad_path():
     assert normwise_rel_err(_np(s_fused), ref) <= 1e-5
     assert normwise_rel_err(_np(s_grad), ref) <= 1e-5
     assert normwise_rel_err(_np(a_fused), _np(a_grad)) <= 1e-5
+
+
+def test_hot_path_from_reference_checkpoint_matches_oracle(tmp_path):
+    """step_N.pt with the reference's layout (distributed.py:295-304) -> build_hot_path -> Level-0 and
+    packed Level-1 forwards against oracle/modules.py with the checkpoint's weights."""
+    from hclsm_amd.checkpoint import build_hot_path, module_state, preset_config, read_model_state
+    from hclsm_amd.dynamics import HierarchyManager, Level0SSM, Level1EventDynamics
+    torch.manual_seed(21)
+    cfg = preset_config("tiny")
+    src = {"level0_ssm": Level0SSM(cfg.dynamics.level0, D_SLOT),
+           "level1_event": Level1EventDynamics(cfg.dynamics.level1, D_SLOT),
+           "hierarchy_manager": HierarchyManager(D_SLOT, cfg.dynamics.level2.d_model)}
+    from hclsm_amd.objects import DynamicSlotAttention
+    src["slot_attention"] = DynamicSlotAttention(cfg.objects, cfg.d_world)
+    with torch.no_grad():      # trained-looking A_log: spread over the clamp's range
+        for blk in list(src["level0_ssm"].object_blocks) + list(src["level0_ssm"].global_blocks):
+            blk.A_log.uniform_(-3.0, 0.5)
+    state = {f"{n}.{k}": v for n, m in src.items() for k, v in m.state_dict().items()}
+    path = tmp_path / "step_100.pt"
+    torch.save({"model": state, "optimizer": {}, "scheduler": None, "scaler": None, "global_step": 100,
+                "is_fsdp": False}, path)
+    mods = build_hot_path(path, cfg)
+    sd = read_model_state(path)
+    B, N, T = 2, 16, 8
+    x = torch.randn(B, N, T, D_SLOT, device="cuda")
+    mask = torch.ones(B, N, device="cuda")
+    with torch.no_grad():
+        out0 = mods["level0_ssm"](x, mask)
+    ref0 = om.level0_ssm_ref(_np(x), _np(mask), {k: _np(v) for k, v in module_state(sd, "level0_ssm").items()},
+                             cfg.dynamics.level0.n_blocks)
+    assert normwise_rel_err(_np(out0), ref0) <= 1e-5
+    states = torch.randn(B, T, N, D_SLOT, device="cuda")
+    em = torch.zeros(B, T, device="cuda")
+    em[:, [0, 3, 5]] = 1.0
+    with torch.no_grad():
+        ev, idx = mods["hierarchy_manager"].gather_events_packed(states, em)
+        out1 = mods["level1_event"].forward_packed(ev, idx, mask)
+    ref1 = om.level1_ref(_np(states[:, [0, 3, 5]]), None, _np(mask),
+                         {k: _np(v) for k, v in module_state(sd, "level1_event").items()},
+                         cfg.dynamics.level1.n_layers, cfg.dynamics.level1.n_heads)
+    assert normwise_rel_err(_np(out1[:6]).reshape(B, 3, N, D_SLOT), ref1) <= 1e-5
