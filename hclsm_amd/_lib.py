@@ -57,12 +57,16 @@ _SIGNATURES: dict[str, list] = {
     "hclsm_slot_attention_forward": [_c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64,
                                      _i64, _i64, _f32, _f32, _f32, _f32, _int, _c_void_p, _i64, _c_void_p],
     "hclsm_level1_forward_workspace": [_i64, _i64, _i64, _i64, _int],
+    "hclsm_relation_graph_workspace": [_i64, _i64, _i64, _i64, _int],
+    "hclsm_relation_graph_forward": [_c_void_p] * 4 + [_i64] * 5 + [_int, _c_void_p, _f32, _int, _c_void_p, _i64,
+                                                                    _c_void_p],
     "hclsm_level1_forward": [_c_void_p, _int, _c_void_p, _int, _c_void_p, _i64, _i64, _c_void_p, _c_void_p,
                              _i64, _i64, _i64, _i64, _i64, _c_void_p, _f32, _int, _c_void_p, _i64, _c_void_p],
 }
 _RESTYPES = {"hclsm_strerror": ctypes.c_char_p, "hclsm_slot_attn_core_workspace": ctypes.c_int64,
              "hclsm_ssm_scan_bwd_workspace": ctypes.c_int64,
-             "hclsm_slot_attention_workspace": ctypes.c_int64, "hclsm_level1_forward_workspace": ctypes.c_int64}
+             "hclsm_slot_attention_workspace": ctypes.c_int64, "hclsm_level1_forward_workspace": ctypes.c_int64,
+             "hclsm_relation_graph_workspace": ctypes.c_int64}
 
 
 class HclsmSlotWeights(ctypes.Structure):

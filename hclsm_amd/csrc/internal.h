@@ -5,13 +5,13 @@
 
 namespace hclsm {
 
-// Y[M, N] = A . W^T (+ resid) with A = X or LayerNorm(X) rows (ln != 0), the row count taken as
-// min(M, *m_dev * m_mul) when m_dev is set (read on the device), and, when glu is set, the
-// gated-linear epilogue val = silu(glu[row, col]) * val (glu in `dtype`, row stride ldg).
-// Defined in slot_attn.hip.
-int linear_rows(const void* x, int64_t ldx, int x_dtype, const void* w, int64_t ldw, const float* resid,
-                int64_t ldr, void* y, int64_t ldy, int y_dtype, int64_t M, int64_t N, int64_t K, int ln,
-                const float* ln_w, const float* ln_b, float ln_eps, const void* glu, int64_t ldg,
+// Y[M, N] = A . W^T (+ bias) (ReLU if relu) (+ resid) with A = X or LayerNorm(X) rows (ln != 0), the
+// row count taken as min(M, *m_dev * m_mul) when m_dev is set (read on the device), and, when glu is
+// set, the gated-linear epilogue val = silu(glu[row, col]) * val (glu in `dtype`, row stride ldg) before
+// the residual.  Defined in slot_attn.hip.
+int linear_rows(const void* x, int64_t ldx, int x_dtype, const void* w, int64_t ldw, const float* bias,
+                const float* resid, int64_t ldr, void* y, int64_t ldy, int y_dtype, int64_t M, int64_t N, int64_t K,
+                int ln, int relu, const float* ln_w, const float* ln_b, float ln_eps, const void* glu, int64_t ldg,
                 const int32_t* m_dev, int64_t m_mul, int dtype, hipStream_t st);
 
 // LayerNorm of M rows (row count min(M, *m_dev * m_mul) when m_dev is set), as hclsm_layer_norm.

@@ -96,8 +96,8 @@ extern "C" int hclsm_level1_forward(const void* ev, int ev_dtype, void* out, int
   // GEMM Y[R, n] = X[R, k] . W^T (+ resid) (gated by glu), rows of the live events only
   auto gemm = [&](const void* X, int xdt, const void* W, int64_t n, int64_t k, const float* resid, void* Y, int ydt,
                   const void* glu) {
-    return linear_rows(X, k, xdt, W, k, resid, n, Y, n, ydt, R, n, k, 0, nullptr, nullptr, ln_eps, glu, n, n_events,
-                       N, dtype, st);
+    return linear_rows(X, k, xdt, W, k, nullptr, resid, n, Y, n, ydt, R, n, k, 0, 0, nullptr, nullptr, ln_eps, glu, n,
+                       n_events, N, dtype, st);
   };
   auto norm = [&](const float* w, const float* b) {
     return layer_norm_rows(x, dm, w, b, xn, dm, R, dm, ln_eps, HCLSM_F32, dtype, n_events, N, st);

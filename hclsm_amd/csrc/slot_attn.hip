@@ -1162,12 +1162,12 @@ static int linear_impl(const void* x, int64_t ldx, int x_dtype, const void* w, i
 
 // Linear layer with a device-side row count and an optional gated-linear epilogue, for composite
 // entry points in other files (declared in internal.h).
-int linear_rows(const void* x, int64_t ldx, int x_dtype, const void* w, int64_t ldw, const float* resid,
-                int64_t ldr, void* y, int64_t ldy, int y_dtype, int64_t M, int64_t N, int64_t K, int ln,
-                const float* ln_w, const float* ln_b, float ln_eps, const void* glu, int64_t ldg,
+int linear_rows(const void* x, int64_t ldx, int x_dtype, const void* w, int64_t ldw, const float* bias,
+                const float* resid, int64_t ldr, void* y, int64_t ldy, int y_dtype, int64_t M, int64_t N, int64_t K,
+                int ln, int relu, const float* ln_w, const float* ln_b, float ln_eps, const void* glu, int64_t ldg,
                 const int32_t* m_dev, int64_t m_mul, int dtype, hipStream_t st) {
   if (glu && (x_dtype != dtype && x_dtype != HCLSM_F32)) return HCLSM_ERR_DTYPE;
-  return linear_impl(x, ldx, x_dtype, w, ldw, nullptr, resid, ldr, y, ldy, y_dtype, nullptr, 0, M, N, K, 0, 0.f, ln,
+  return linear_impl(x, ldx, x_dtype, w, ldw, bias, resid, ldr, y, ldy, y_dtype, nullptr, 0, M, N, K, relu, 0.f, ln,
                      ln_w, ln_b, ln_eps, dtype, st, LinExt{m_dev, m_mul, glu, ldg});
 }
 

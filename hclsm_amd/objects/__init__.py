@@ -1,5 +1,7 @@
-"""Counterpart of the reference's hclsm/objects/dynamic_slots.py on the hot path."""
+"""Counterparts of the reference's hclsm/objects modules on the hot path (slot attention) and next to it
+(relation graph)."""
 
 from hclsm_amd.objects.dynamic_slots import DynamicSlotAttention
+from hclsm_amd.objects.relation_graph import RelationGraph
 
-__all__ = ["DynamicSlotAttention"]
+__all__ = ["DynamicSlotAttention", "RelationGraph"]

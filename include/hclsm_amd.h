@@ -327,6 +327,32 @@ int hclsm_level1_forward(const void* ev, int ev_dtype, void* out, int out_dtype,
                          const void* const* params, float ln_eps, int dtype, void* workspace,
                          int64_t workspace_bytes, void* stream);
 
+/* Workspace bytes for hclsm_relation_graph_forward. */
+int64_t hclsm_relation_graph_workspace(int64_t frames, int64_t N, int64_t D, int64_t E, int dtype);
+
+/*
+ * RelationGraph.forward (GNN over object slots) for `frames` frames of N slots:
+ *   per round: edge features e_ij = ReLU(W2 ReLU(W1 LN([n_i; n_j; n_i - n_j; n_i * n_j]) + b1) + b2),
+ *   weights w_ij = sigmoid(we . e_ij + be) * alive_i * alive_j, agg_i = sum_j ReLU(Wm e_ij + bm) w_ij,
+ *   n_i += U2 ReLU(U1 [n_i; agg_i] + c1) + c2; causal_ij = sigmoid(c2' . ReLU(C1 e_ij + d1) + d2) * alive_i
+ *   * alive_j; finally nodes_out = n * alive.
+ * chunked != 0 gives the reference's N > 32 path semantics: edges recomputed from the current nodes every
+ * round and the causal edges from the final nodes; chunked == 0 the all-pairs path (causal edges from the
+ * last edges computed, which for n_rounds == 1 are those of the input nodes).
+ * nodes, nodes_out [frames, N, D], alive [frames, N] (nullable), causal [frames, N, N]: float32.
+ * params: host array of 18 device pointers in the module's parameter order (pair_norm.weight/bias [4D],
+ *   edge_mlp.0.weight [2E, 4D] / bias, edge_mlp.2.weight [E, 2E] / bias, edge_weight.weight [E] / bias [1],
+ *   msg_mlp.0.weight [D, E] / bias, update_mlp.0.weight [D, 2D] / bias, update_mlp.2.weight [D, D] / bias,
+ *   causal_mlp.0.weight [E/2, E] / bias, causal_mlp.2.weight [E/2] / bias [1]); matrices in `dtype`
+ *   (F32 / BF16 / F16), vectors float32.  D, E multiples of 32, E <= 192, N <= 128 (64 for F32).
+ * Replaces: RelationGraph.forward (hclsm/objects/relation_graph.py:68-193), called by the model on the
+ *   tracked slots (model.py:255-266).
+ */
+int hclsm_relation_graph_forward(const float* nodes, const float* alive, float* nodes_out, float* causal,
+                                 int64_t frames, int64_t N, int64_t D, int64_t E, int64_t n_rounds, int chunked,
+                                 const void* const* params, float ln_eps, int dtype, void* workspace,
+                                 int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
