@@ -298,6 +298,48 @@ def _bench_level1(dev, n, warmup):
                          "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4), "flops_per_call": flops}}
 
 
+def _bench_gnn(dev, n, warmup):
+    """Relation graph (GNN over slots) at the small preset (config.py:221-242): 32 clips x 64 frames =
+    2048 frames of 32 slots, d_slot 192, d_edge 96, 2 rounds, 80% live slots: hclsm_relation_graph_forward
+    (bf16 operands, and fp32) against the reference's math as torch ops on the GPU (the all-pairs path,
+    relation_graph.py:171-188, fp32)."""
+    import torch
+    from types import SimpleNamespace
+    from hclsm_amd.objects import RelationGraph
+    from hclsm_amd.kernels.relation_graph import GnnWeights, relation_graph_forward
+    torch.manual_seed(1008)
+    Fr, N, D, E, R = 2048, 32, 192, 96, 2
+    m = RelationGraph(SimpleNamespace(d_slot=D, d_edge=E, gnn_rounds=R, n_max_slots=N)).to(dev)
+    g = torch.Generator(device=dev).manual_seed(1009)
+    x = torch.randn(Fr, N, D, generator=g, device=dev)
+    alive = (torch.rand(Fr, N, generator=g, device=dev) < 0.8).float()
+    with torch.no_grad():
+        Wb, Wf = GnnWeights.from_module(m, torch.bfloat16), GnnWeights.from_module(m, torch.float32)
+        bf_med, _ = _event_timing(lambda: relation_graph_forward(x, alive, Wb, R), n, warmup)
+        f32_med, _ = _event_timing(lambda: relation_graph_forward(x, alive, Wf, R), n, warmup)
+        ref_med, _ = _event_timing(lambda: m._torch_forward(x, alive), max(n // 4, 3), 1)
+        ro, rc = m._torch_forward(x, alive)
+        ob, cb = relation_graph_forward(x, alive, Wb, R)
+        of, cf = relation_graph_forward(x, alive, Wf, R)
+        err = lambda a, b: float(((a - b).norm() / b.norm()).item())
+        errs = {"fp32_nodes": err(of, ro), "fp32_causal": err(cf, rc), "bf16_nodes": err(ob, ro), "bf16_causal": err(cb, rc)}
+    pairs = Fr * N * N
+    # per edge pass: Hadamard contraction (D x 2E), W2 (2E x E), messages (E x D) or causal (E x E/2, E/2);
+    # per-node P/Q projection (D x 4E); node update (2D x D, D x D)
+    per_pair_msg = D * 2 * E + 2 * E * E + E * D
+    per_pair_causal = D * 2 * E + 2 * E * E + E * (E // 2) + E // 2
+    flops = 2 * (R * pairs * per_pair_msg + pairs * per_pair_causal + (R + 1) * Fr * N * D * 4 * E
+                 + R * Fr * N * (2 * D * D + D * D))
+    tf = flops / bf_med / 1e12
+    return {"workload": "RelationGraph, small preset: 2048 frames x 32 slots, d_slot 192, d_edge 96, 2 rounds, 80% "
+                        "live slots",
+            "pairs": pairs, "fused_bf16_us": round(bf_med * 1e6, 2), "fused_fp32_us": round(f32_med * 1e6, 2),
+            "torch_reference_fp32_us": round(ref_med * 1e6, 2), "speedup_bf16": round(ref_med / bf_med, 2),
+            "speedup_fp32": round(ref_med / f32_med, 2), "normwise_vs_torch": errs,
+            "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4), "flops_per_call": flops}}
+
+
 def _bench_chain(dev, n, warmup):
     """Config 4: four chained scans at (1024, 1024, 768), S=16, bf16 (each fed the previous output),
     then the event index of a p=0.05 mask (t=0 forced) and causal event attention, 12 heads x 64."""
@@ -470,6 +512,7 @@ def main():
         out["block_scan"] = _bench_block_scan(dev, 50, 5)
         out["scan_bwd"] = _bench_scan_bwd(dev, 50, 5)
         out["level1"] = _bench_level1(dev, 30, 3)
+        out["gnn"] = _bench_gnn(dev, 20, 3)
     print(json.dumps(out), flush=True)
 
 

@@ -89,26 +89,43 @@ struct GnnArgs {
   float eps;
 };
 
-template <int DT, int NW>
+// Weight chunks are staged in LDS (shared by the workgroup's waves): KC columns of every output row
+// (KC a multiple of the fragment block KB; smaller KC when the widest layer would not fit).
+
+// sW[r * pitch + c] = W[r * ldw + k0 + c] for r < nrows, c < kc (16-byte units; kc a multiple of the unit)
+template <typename T, int NTH>
+__device__ __forceinline__ void stage_rows(const T* __restrict__ W, int ldw, int nrows, int k0, int kc, T* sW,
+                                           int pitch, int tid) {
+  constexpr int U = 16 / (int)sizeof(T);
+  const int upr = kc / U;
+  for (int u = tid; u < nrows * upr; u += NTH) {
+    const int r = u / upr, c = (u - r * upr) * U;
+    *reinterpret_cast<uint4*>(sW + r * pitch + c) = *reinterpret_cast<const uint4*>(W + (size_t)r * ldw + k0 + c);
+  }
+}
+
+template <int DT, int NW, int KC>
 __global__ void __launch_bounds__(64 * NW)
 gnn_edge_kernel(GnnArgs a) {
   using A = MM<DT>;
   using T = typename A::T;
-  constexpr int KE = GFrag<DT>::KE, KB = GFrag<DT>::KB;
-  constexpr int ROWS = 16 * NW;
+  constexpr int KE = GFrag<DT>::KE, KB = GFrag<DT>::KB, PW = KC + 8;
+  static_assert(KC % KB == 0, "chunk of whole fragment blocks");
+  constexpr int ROWS = 16 * NW, NTH = 64 * NW;
   extern __shared__ __align__(16) unsigned char smem[];
   const int N = a.N, NP = a.NP, D = a.D, E = a.E, H1 = 2 * E;
   const int LH = H1 + 8, LE = E + 8;     // LDS row pitches (elements)
-  T* sH = reinterpret_cast<T*>(smem);                                      // [ROWS][LH], then [ROWS][LE]
-  float* sw = reinterpret_cast<float*>(smem + (size_t)ROWS * LH * sizeof(T));   // [ROWS] edge weights
-  float* sst = sw + ROWS;                                                  // [ROWS][2] mu, rstd
-  float* sagg = sst + 2 * ROWS;                                            // [NW][D] per-wave message sums
-  const int G = ROWS / NP;                                                 // i-rows per workgroup (>= 1)
+  const int WR = (H1 > D ? H1 : D);      // most weight rows staged at once
+  T* sH = reinterpret_cast<T*>(smem);                                                  // [ROWS][LH], then [ROWS][LE]
+  T* sW = sH + (size_t)ROWS * LH;                                                      // [WR][PW] weight chunk
+  float* sw = reinterpret_cast<float*>(sW + (size_t)WR * PW);                          // [ROWS] edge weights
+  float* sst = sw + ROWS;                                                              // [ROWS][2] mu, rstd
+  float* sagg = sst + 2 * ROWS;                                                        // [NW][D] message sums
+  const int G = ROWS / NP;                                                             // i-rows per workgroup
   const int tiles_f = (N + G - 1) / G;
   const int f = blockIdx.x / tiles_f;
   const int i0 = (blockIdx.x - f * tiles_f) * G;
   const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, g = lane >> 4, li = lane & 15;
-  // this lane's operand row (li) and the rows of its accumulator entries (4g + rr) within the wave tile
   auto row_pair = [&](int row, int& i, int& j) {
     const int il = row / NP;
     i = i0 + il;
@@ -118,6 +135,28 @@ gnn_edge_kernel(GnnArgs a) {
   const float* Xf = a.X + (size_t)f * N * a.ldx;
   const float* alive = a.alive ? a.alive + (size_t)f * N : nullptr;
   auto pair_mask = [&](int i, int j) { return alive ? alive[i] * alive[j] : 1.f; };
+  // acc[t] += A-rows (this wave's 16) x W rows t*16 + li over K, W streamed through LDS in KC-column chunks;
+  // a_frag(k) gives this lane's KE operand elements at column k
+  auto gemm = [&](auto& acc, int NT, int NTMAX, const T* W, int K, auto a_frag) {
+    for (int k0 = 0; k0 < K; k0 += KC) {
+      const int kc = K - k0 < KC ? K - k0 : KC;
+      __syncthreads();   // the previous chunk is consumed
+      stage_rows<T, NTH>(W, K, NT * 16, k0, kc, sW, PW, tid);
+      __syncthreads();
+      for (int kb = 0; kb < kc; kb += KB) {
+        T op[KE];
+        a_frag(k0 + kb + KE * g, op);
+#pragma unroll
+        for (int t = 0; t < NTMAX; ++t) {
+          if (t < NT) {
+            T wb[KE];
+            frag_load<DT>(sW + (t * 16 + li) * PW + kb + KE * g, wb);
+            acc[t] = frag_mma<DT>(op, wb, acc[t]);
+          }
+        }
+      }
+    }
+  };
 
   // ---- A: Hadamard GEMM + pair statistics -> H1
   {
@@ -131,9 +170,7 @@ gnn_edge_kernel(GnnArgs a) {
     f32x4 acc[24];
 #pragma unroll
     for (int t = 0; t < 24; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const T* A4 = reinterpret_cast<const T*>(a.A4);
-    for (int kb = 0; kb < D; kb += KB) {
-      const int k = kb + KE * g;
+    gemm(acc, NT, 24, reinterpret_cast<const T*>(a.A4), D, [&](int k, T* op) {
       float vi[KE], vj[KE];
 #pragma unroll
       for (int e = 0; e < KE; e += 4) {
@@ -142,7 +179,6 @@ gnn_edge_kernel(GnnArgs a) {
         vi[e] = x4.x; vi[e + 1] = x4.y; vi[e + 2] = x4.z; vi[e + 3] = x4.w;
         vj[e] = y4.x; vj[e + 1] = y4.y; vj[e + 2] = y4.z; vj[e + 3] = y4.w;
       }
-      T op[KE];
 #pragma unroll
       for (int e = 0; e < KE; ++e) {
         const float pr = vi[e] * vj[e];
@@ -153,15 +189,7 @@ gnn_edge_kernel(GnnArgs a) {
         qj = fmaf(vj[e], vj[e], qj);
         op[e] = A::fromf(pr);
       }
-#pragma unroll
-      for (int t = 0; t < 24; ++t) {
-        if (t < NT) {
-          T wb[KE];
-          frag_load<DT>(A4 + (size_t)(t * 16 + li) * D + k, wb);
-          acc[t] = frag_mma<DT>(op, wb, acc[t]);
-        }
-      }
-    }
+    });
     // row sums over the four lane groups sharing the row
 #pragma unroll
     for (int m = 16; m < 64; m <<= 1) {
@@ -178,7 +206,7 @@ gnn_edge_kernel(GnnArgs a) {
       sst[2 * row] = mu;
       sst[2 * row + 1] = 1.f / sqrtf(fmaxf(m2 - mu * mu, 0.f) + a.eps);
     }
-    __syncthreads();   // statistics of every row are in LDS (the H1 region is written below, after this)
+    __syncthreads();   // statistics of every row are in LDS
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       const int orow = wid * 16 + 4 * g + rr;
@@ -191,13 +219,12 @@ gnn_edge_kernel(GnnArgs a) {
       for (int t = 0; t < 24; ++t) {
         if (t < NT) {
           const int o = t * 16 + li;
-          float v = fmaf(P[o] + Q[o] + acc[t][rr] - mu * a.r[o], rs, a.c[o]);
+          const float v = fmaf(P[o] + Q[o] + acc[t][rr] - mu * a.r[o], rs, a.c[o]);
           sH[(size_t)orow * LH + o] = A::fromf(ok ? fmaxf(v, 0.f) : 0.f);
         }
       }
     }
   }
-  __syncthreads();
 
   // ---- B: H1 W2^T + b2, ReLU -> edge features (written over H1 after everyone has read it)
   {
@@ -205,20 +232,8 @@ gnn_edge_kernel(GnnArgs a) {
     f32x4 acc[12];
 #pragma unroll
     for (int t = 0; t < 12; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const T* W2 = reinterpret_cast<const T*>(a.W2);
-    for (int kb = 0; kb < H1; kb += KB) {
-      const int k = kb + KE * g;
-      T op[KE];
-      frag_load<DT>(sH + (size_t)(wid * 16 + li) * LH + k, op);
-#pragma unroll
-      for (int t = 0; t < 12; ++t) {
-        if (t < NT) {
-          T wb[KE];
-          frag_load<DT>(W2 + (size_t)(t * 16 + li) * H1 + k, wb);
-          acc[t] = frag_mma<DT>(op, wb, acc[t]);
-        }
-      }
-    }
+    const T* hrow = sH + (size_t)(wid * 16 + li) * LH;
+    gemm(acc, NT, 12, reinterpret_cast<const T*>(a.W2), H1, [&](int k, T* op) { frag_load<DT>(hrow + k, op); });
     __syncthreads();   // H1 fully consumed
 #pragma unroll
     for (int t = 0; t < 12; ++t) {
@@ -232,84 +247,62 @@ gnn_edge_kernel(GnnArgs a) {
   }
   __syncthreads();
   const T* sE = sH;
+  const T* erow = sE + (size_t)(wid * 16 + li) * LE;
   // edge weight per row
-  for (int row = tid; row < ROWS; row += 64 * NW) {
+  for (int row = tid; row < ROWS; row += NTH) {
     int i, j;
     const bool ok = row_pair(row, i, j);
     float s = a.be[0];
     for (int o = 0; o < E; ++o) s = fmaf(A::tof(sE[(size_t)row * LE + o]), a.we[o], s);
     sw[row] = ok ? pair_mask(i, j) / (1.f + __expf(-s)) : 0.f;
   }
-  __syncthreads();
+  // (the first chunk staging of the next GEMM begins with a barrier: sw is complete before it is read)
 
   // ---- C: messages, summed over the wave's 16 pairs (one i-row: NP is a multiple of 16)
   if (a.agg) {
-    const int NT = D / 16;
+    const int NTALL = D / 16;
     const T* Wm = reinterpret_cast<const T*>(a.Wm);
-    for (int t0 = 0; t0 < NT; t0 += 12) {
+    for (int t0 = 0; t0 < NTALL; t0 += 12) {
+      const int NT = NTALL - t0 < 12 ? NTALL - t0 : 12;
       f32x4 acc[12];
 #pragma unroll
       for (int t = 0; t < 12; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-      for (int kb = 0; kb < E; kb += KB) {
-        const int k = kb + KE * g;
-        T op[KE];
-        frag_load<DT>(sE + (size_t)(wid * 16 + li) * LE + k, op);
-#pragma unroll
-        for (int t = 0; t < 12; ++t) {
-          if (t0 + t < NT) {
-            T wb[KE];
-            frag_load<DT>(Wm + (size_t)((t0 + t) * 16 + li) * E + k, wb);
-            acc[t] = frag_mma<DT>(op, wb, acc[t]);
-          }
-        }
-      }
+      gemm(acc, NT, 12, Wm + (size_t)t0 * 16 * E, E, [&](int k, T* op) { frag_load<DT>(erow + k, op); });
 #pragma unroll
       for (int t = 0; t < 12; ++t) {
-        if (t0 + t < NT) {
+        if (t < NT) {
           const int o = (t0 + t) * 16 + li;
-          float s = 0.f;
+          float sacc = 0.f;
 #pragma unroll
-          for (int rr = 0; rr < 4; ++rr) s = fmaf(fmaxf(acc[t][rr] + a.bm[o], 0.f), sw[wid * 16 + 4 * g + rr], s);
-          s += __shfl_xor(s, 16, 64);
-          s += __shfl_xor(s, 32, 64);
-          if (g == 0) sagg[wid * D + o] = s;
+          for (int rr = 0; rr < 4; ++rr)
+            sacc = fmaf(fmaxf(acc[t][rr] + a.bm[o], 0.f), sw[wid * 16 + 4 * g + rr], sacc);
+          sacc += __shfl_xor(sacc, 16, 64);
+          sacc += __shfl_xor(sacc, 32, 64);
+          if (g == 0) sagg[wid * D + o] = sacc;
         }
       }
     }
     __syncthreads();
     // agg[i] = sum of the partials of the NP/16 waves of row i, in wave order
     const int wpr = NP / 16;
-    for (int e = tid; e < G * D; e += 64 * NW) {
+    for (int e = tid; e < G * D; e += NTH) {
       const int il = e / D, o = e - il * D;
       const int i = i0 + il;
       if (i < N) {
-        float s = 0.f;
-        for (int w = 0; w < wpr; ++w) s += sagg[(il * wpr + w) * D + o];
-        a.agg[((size_t)f * N + i) * a.ldagg + o] = s;
+        float sacc = 0.f;
+        for (int w = 0; w < wpr; ++w) sacc += sagg[(il * wpr + w) * D + o];
+        a.agg[((size_t)f * N + i) * a.ldagg + o] = sacc;
       }
     }
   }
 
   // ---- D: causal edge probabilities
   if (a.causal) {
-    const int Eh = E / 2, NT = Eh / 16;
-    const T* C1 = reinterpret_cast<const T*>(a.C1);
+    const int NT = E / 32;
     f32x4 acc[6];
 #pragma unroll
     for (int t = 0; t < 6; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int kb = 0; kb < E; kb += KB) {
-      const int k = kb + KE * g;
-      T op[KE];
-      frag_load<DT>(sE + (size_t)(wid * 16 + li) * LE + k, op);
-#pragma unroll
-      for (int t = 0; t < 6; ++t) {
-        if (t < NT) {
-          T wb[KE];
-          frag_load<DT>(C1 + (size_t)(t * 16 + li) * E + k, wb);
-          acc[t] = frag_mma<DT>(op, wb, acc[t]);
-        }
-      }
-    }
+    gemm(acc, NT, 6, reinterpret_cast<const T*>(a.C1), E, [&](int k, T* op) { frag_load<DT>(erow + k, op); });
     float part[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < 6; ++t) {
@@ -403,24 +396,51 @@ static GnnWs gnn_ws(int64_t F, int64_t N, int64_t D, int64_t E, int es) {
   return w;
 }
 
-template <int DT, int NW>
-static int launch_edges(const GnnArgs& a, hipStream_t st) {
+template <int DT, int NW, int KC>
+static size_t edge_lds(const GnnArgs& a) {
   using T = typename MM<DT>::T;
-  constexpr int ROWS = 16 * NW;
-  const int G = ROWS / a.NP;
+  const int WR = 2 * a.E > a.D ? 2 * a.E : a.D;
+  return ((size_t)16 * NW * (2 * a.E + 8) + (size_t)WR * (KC + 8)) * sizeof(T) + (size_t)16 * NW * 3 * 4 +
+         (size_t)NW * a.D * 4;
+}
+
+template <int DT, int NW, int KC>
+static int launch_edges_kc(const GnnArgs& a, hipStream_t st) {
+  const int G = 16 * NW / a.NP;
   const int64_t tiles = (int64_t)a.F * ((a.N + G - 1) / G);
-  const size_t lds = (size_t)ROWS * (2 * a.E + 8) * sizeof(T) + (size_t)ROWS * 3 * 4 + (size_t)NW * a.D * 4;
-  if (lds > 160 * 1024) return HCLSM_ERR_UNSUPPORTED;
   static bool big_lds = false;   // allow more than the default 64 KB of dynamic LDS (idempotent)
   if (!big_lds) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gnn_edge_kernel<DT, NW>),
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gnn_edge_kernel<DT, NW, KC>),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (e != hipSuccess) return (int)e;
     big_lds = true;
   }
-  hipLaunchKernelGGL((gnn_edge_kernel<DT, NW>), dim3((unsigned)tiles), dim3(64 * NW), lds, st, a);
+  const size_t lds = edge_lds<DT, NW, KC>(a);
+  hipLaunchKernelGGL((gnn_edge_kernel<DT, NW, KC>), dim3((unsigned)tiles), dim3(64 * NW), lds, st, a);
   HCLSM_LAUNCH_CHECK();
   return 0;
+}
+
+// 16-bit operands: 128 pairs per workgroup, weight chunks of 64 columns (32 if the LDS would overflow);
+// fp32: 64 pairs, chunks of 16.
+constexpr size_t GNN_LDS_MAX = 160 * 1024;
+
+template <int DT>
+static bool edges_fit(const GnnArgs& a) {
+  if constexpr (DT == HCLSM_F32) return edge_lds<DT, 4, 16>(a) <= GNN_LDS_MAX;
+  else return edge_lds<DT, 8, 32>(a) <= GNN_LDS_MAX;
+}
+
+template <int DT>
+static int launch_edges(const GnnArgs& a, hipStream_t st) {
+  if constexpr (DT == HCLSM_F32) {
+    if (edge_lds<DT, 4, 16>(a) > GNN_LDS_MAX) return HCLSM_ERR_UNSUPPORTED;
+    return launch_edges_kc<DT, 4, 16>(a, st);
+  } else {
+    if (edge_lds<DT, 8, 64>(a) <= GNN_LDS_MAX) return launch_edges_kc<DT, 8, 64>(a, st);
+    if (edge_lds<DT, 8, 32>(a) <= GNN_LDS_MAX) return launch_edges_kc<DT, 8, 32>(a, st);
+    return HCLSM_ERR_UNSUPPORTED;
+  }
 }
 
 static int copy_rows(const float* x, int64_t ldx, const float* alive, float* y, int64_t ldy, int64_t rows, int64_t D,
@@ -433,6 +453,12 @@ static int copy_rows(const float* x, int64_t ldx, const float* alive, float* y, 
   return 0;
 }
 
+static GnnArgs a0_shape(int64_t F, int64_t N, int64_t D, int64_t E) {
+  GnnArgs a{};
+  a.F = (int)F; a.N = (int)N; a.NP = (int)((N + 15) / 16 * 16); a.D = (int)D; a.E = (int)E;
+  return a;
+}
+
 // params (module order): 0 pair_norm.w, 1 pair_norm.b, 2 edge_mlp.0.w, 3 edge_mlp.0.b, 4 edge_mlp.2.w,
 // 5 edge_mlp.2.b, 6 edge_weight.w, 7 edge_weight.b, 8 msg_mlp.0.w, 9 msg_mlp.0.b, 10 update_mlp.0.w,
 // 11 update_mlp.0.b, 12 update_mlp.2.w, 13 update_mlp.2.b, 14 causal_mlp.0.w, 15 causal_mlp.0.b,
@@ -442,7 +468,6 @@ static int gnn_forward(const float* nodes, const float* alive, float* nodes_out,
                        int64_t D, int64_t E, int64_t rounds, int chunked, const void* const* p, float eps,
                        char* ws, const GnnWs& L, hipStream_t st) {
   using T = typename MM<DT>::T;
-  constexpr int NW = DT == HCLSM_F32 ? 4 : 8;
   T* WPQ = reinterpret_cast<T*>(ws + L.wpq);
   T* A4 = reinterpret_cast<T*>(ws + L.a4);
   float* r = reinterpret_cast<float*>(ws + L.r);
@@ -475,7 +500,7 @@ static int gnn_forward(const float* nodes, const float* alive, float* nodes_out,
     if (e) return e;
     a.agg = msg ? XA + D : nullptr;
     a.causal = caus ? causal : nullptr;
-    return launch_edges<DT, NW>(a, st);
+    return launch_edges<DT>(a, st);
   };
   auto update = [&]() -> int {   // nodes += U2 ReLU(U1 [nodes; agg] + c1) + c2, in place in XA
     int e = linear_rows(XA, ld, HCLSM_F32, P(10), 2 * D, Pf(11), nullptr, 0, U, D, DT, R, D, 2 * D, 0, 1, nullptr,
@@ -507,9 +532,22 @@ static int gnn_forward(const float* nodes, const float* alive, float* nodes_out,
 
 using namespace hclsm;
 
-extern "C" int64_t hclsm_relation_graph_workspace(int64_t frames, int64_t N, int64_t D, int64_t E, int dtype) {
-  if (frames < 0 || N < 0 || D < 0 || E < 0) return HCLSM_ERR_SHAPE;
+// HCLSM_ERR_UNSUPPORTED for shapes outside the fused kernel: D, E multiples of 32, E <= 192, N <= 128
+// (64 for fp32 operands), and the workgroup's LDS tiles within 160 KB.
+static int gnn_check(int64_t N, int64_t D, int64_t E, int dtype) {
+  if (N < 0 || D <= 0 || E <= 0) return HCLSM_ERR_SHAPE;
   if (dtype != HCLSM_F32 && dtype != HCLSM_BF16 && dtype != HCLSM_F16) return HCLSM_ERR_DTYPE;
+  const int NW = dtype == HCLSM_F32 ? 4 : 8;
+  if (D % 32 || E % 32 || E > 192 || N > 16 * NW) return HCLSM_ERR_UNSUPPORTED;
+  const GnnArgs a = a0_shape(1, N, D, E);
+  const bool fit = dtype == HCLSM_F32 ? edges_fit<HCLSM_F32>(a) : edges_fit<HCLSM_BF16>(a);
+  return fit ? 0 : HCLSM_ERR_UNSUPPORTED;
+}
+
+extern "C" int64_t hclsm_relation_graph_workspace(int64_t frames, int64_t N, int64_t D, int64_t E, int dtype) {
+  if (frames < 0) return HCLSM_ERR_SHAPE;
+  const int c = gnn_check(N, D, E, dtype);
+  if (c) return c;
   return (int64_t)gnn_ws(frames, N, D, E, dtype == HCLSM_F32 ? 4 : 2).total;
 }
 
@@ -517,11 +555,9 @@ extern "C" int hclsm_relation_graph_forward(const float* nodes, const float* ali
                                             int64_t frames, int64_t N, int64_t D, int64_t E, int64_t rounds,
                                             int chunked, const void* const* params, float ln_eps, int dtype,
                                             void* workspace, int64_t workspace_bytes, void* stream) {
-  if (frames < 0 || N < 0 || D <= 0 || E <= 0 || rounds < 0) return HCLSM_ERR_SHAPE;
-  if (dtype != HCLSM_F32 && dtype != HCLSM_BF16 && dtype != HCLSM_F16) return HCLSM_ERR_DTYPE;
-  const int NW = dtype == HCLSM_F32 ? 4 : 8;
-  // operand granules of the MFMA fragments and tile bounds of the edge kernel
-  if (D % 32 || E % 32 || E > 192 || N > 16 * NW) return HCLSM_ERR_UNSUPPORTED;
+  if (frames < 0 || rounds < 0) return HCLSM_ERR_SHAPE;
+  const int chk = gnn_check(N, D, E, dtype);
+  if (chk) return chk;
   if (frames * N > 0x7fffffffLL) return HCLSM_ERR_SHAPE;
   if (frames == 0 || N == 0) return 0;
   if (!nodes || !nodes_out || !causal || !params || !workspace) return HCLSM_ERR_NULL;

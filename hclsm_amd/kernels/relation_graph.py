@@ -56,6 +56,12 @@ class GnnWeights:
         return W
 
 
+def fused_supported(N: int, d_slot: int, d_edge: int, dtype: torch.dtype) -> bool:
+    """Whether hclsm_relation_graph_forward takes this shape (D, E multiples of 32, E <= 192, N <= 128, or
+    64 with fp32 operands, within the kernel's LDS budget)."""
+    return int(_lib.lib().hclsm_relation_graph_workspace(1, N, d_slot, d_edge, _lib.dtype_code(dtype))) >= 0
+
+
 def relation_graph_forward(nodes: torch.Tensor, alive: torch.Tensor | None, W: GnnWeights, n_rounds: int,
                            chunked: bool | None = None) -> tuple[torch.Tensor, torch.Tensor]:
     """nodes (F, N, d_slot), alive (F, N) or None -> (nodes' (F, N, d_slot) fp32, causal (F, N, N) fp32).

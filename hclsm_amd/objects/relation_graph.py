@@ -4,7 +4,9 @@ Same parameters and names as the reference module (:23-66), so its state dict lo
 
 * Without autograd: one call of ``hclsm_relation_graph_forward`` (pair LayerNorm folded into the first
   edge layer, the edge MLP / weight / messages / causal head fused per pair tile on MFMA, node update on
-  the MFMA linear kernels); compute in fp32, or bf16 under a bf16 autocast.
+  the MFMA linear kernels); compute in fp32, or bf16 under a bf16 autocast.  Shapes outside that kernel
+  (fp32 operands with more than 64 slots, D or d_edge not multiples of 32, d_edge > 192) run the torch
+  path below on the GPU.
 * With autograd: the reference's math in torch ops on the GPU (both of its paths: all pairs for N <= 32,
   :171-188, source-chunked for N > 32, :150-170).
 """
@@ -15,7 +17,7 @@ import torch
 import torch.nn as nn
 
 from hclsm_amd.kernels._common import require_gpu
-from hclsm_amd.kernels.relation_graph import GnnWeights, relation_graph_forward
+from hclsm_amd.kernels.relation_graph import GnnWeights, fused_supported, relation_graph_forward
 
 
 class RelationGraph(nn.Module):
@@ -83,10 +85,10 @@ class RelationGraph(nn.Module):
     def forward(self, nodes: torch.Tensor, alive_mask: torch.Tensor | None = None):
         """nodes (B, N, d_slot), alive_mask (B, N) -> (updated nodes (B, N, d_slot), causal edges (B, N, N))."""
         require_gpu("RelationGraph", nodes, alive_mask)
-        if self._needs_grad(nodes):
-            return self._torch_forward(nodes, alive_mask)
         dtype = torch.bfloat16 if (torch.is_autocast_enabled("cuda") and
                                    torch.get_autocast_dtype("cuda") == torch.bfloat16) else torch.float32
+        if self._needs_grad(nodes) or not fused_supported(nodes.shape[1], self.d_slot, self.d_edge, dtype):
+            return self._torch_forward(nodes, alive_mask)
         W = GnnWeights.from_module(self, dtype)
         out, causal = relation_graph_forward(nodes, alive_mask, W, self.n_rounds, chunked=nodes.shape[1] > 32)
         return out.to(nodes.dtype), causal

@@ -327,7 +327,7 @@ int hclsm_level1_forward(const void* ev, int ev_dtype, void* out, int out_dtype,
                          const void* const* params, float ln_eps, int dtype, void* workspace,
                          int64_t workspace_bytes, void* stream);
 
-/* Workspace bytes for hclsm_relation_graph_forward. */
+/* Workspace bytes for hclsm_relation_graph_forward, or HCLSM_ERR_UNSUPPORTED for a shape outside it. */
 int64_t hclsm_relation_graph_workspace(int64_t frames, int64_t N, int64_t D, int64_t E, int dtype);
 
 /*
@@ -344,7 +344,8 @@ int64_t hclsm_relation_graph_workspace(int64_t frames, int64_t N, int64_t D, int
  *   edge_mlp.0.weight [2E, 4D] / bias, edge_mlp.2.weight [E, 2E] / bias, edge_weight.weight [E] / bias [1],
  *   msg_mlp.0.weight [D, E] / bias, update_mlp.0.weight [D, 2D] / bias, update_mlp.2.weight [D, D] / bias,
  *   causal_mlp.0.weight [E/2, E] / bias, causal_mlp.2.weight [E/2] / bias [1]); matrices in `dtype`
- *   (F32 / BF16 / F16), vectors float32.  D, E multiples of 32, E <= 192, N <= 128 (64 for F32).
+ *   (F32 / BF16 / F16), vectors float32.  D, E multiples of 32, E <= 192, N <= 128 (64 for F32), and the
+ *   workgroup tiles within 160 KB of LDS (hclsm_relation_graph_workspace says HCLSM_ERR_UNSUPPORTED otherwise).
  * Replaces: RelationGraph.forward (hclsm/objects/relation_graph.py:68-193), called by the model on the
  *   tracked slots (model.py:255-266).
  */

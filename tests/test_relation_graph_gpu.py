@@ -60,7 +60,7 @@ def test_relation_graph_fp32_matches_oracle(F, N, D, E, rounds, chunked):
     assert normwise_rel_err(_np(causal), rc) <= 1e-5
 
 
-@pytest.mark.parametrize("F,N,D,E,rounds,chunked", CASES[:2] + CASES[3:4])
+@pytest.mark.parametrize("F,N,D,E,rounds,chunked", CASES[:2] + CASES[3:4] + [(1, 128, 384, 192, 3, True)])
 def test_relation_graph_bf16_matches_oracle(F, N, D, E, rounds, chunked):
     from hclsm_amd.kernels.relation_graph import GnnWeights, relation_graph_forward
     m = _module(D, E, rounds, N, F + N + 1)
@@ -94,3 +94,10 @@ def test_module_paths_and_gradients():
     ob_, cb_ = m64._torch_forward(xb, alive.double().cpu())
     ((ob_ * w.double().cpu()).sum() + cb_.sum()).backward()
     assert normwise_rel_err(_np(xa.grad), xb.grad.numpy()) <= 1e-5
+
+
+def test_fused_shape_limits():
+    from hclsm_amd.kernels.relation_graph import fused_supported
+    assert fused_supported(128, 384, 192, torch.bfloat16)        # large preset (config.py:270): 32-column chunks
+    assert not fused_supported(128, 384, 192, torch.float32)     # fp32 tiles hold 64 pairs
+    assert not fused_supported(32, 200, 96, torch.bfloat16)      # D not a multiple of 32
