@@ -340,6 +340,61 @@ def _bench_gnn(dev, n, warmup):
                          "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4), "flops_per_call": flops}}
 
 
+def _bench_track(dev, n, warmup):
+    """Slot tracking loop at the small preset (model.py:229-252, slot_tracker.py): 32 clips x 64 frames x 32
+    slots, d_slot 192, 80% live slots: hclsm_slot_track_sequence (bf16 operands, with and without the GRU
+    carry, and fp32) against the reference's loop as torch ops on the GPU (fp32, GRU carry included)."""
+    import torch
+    from types import SimpleNamespace
+    from hclsm_amd.objects import SlotTracker, sinkhorn_matching
+    from hclsm_amd.kernels.slot_tracker import TrackerWeights, track_sequence
+    torch.manual_seed(1010)
+    B, T, N, D = 32, 64, 32, 192
+    m = SlotTracker(SimpleNamespace(d_slot=D, n_max_slots=N)).to(dev)
+    g = torch.Generator(device=dev).manual_seed(1011)
+    x = torch.randn(B, T, N, D, generator=g, device=dev)
+    alive = (torch.rand(B, T, N, generator=g, device=dev) < 0.8).float()
+
+    def reference_loop():
+        hidden = torch.zeros(B, N, D, device=dev)
+        tracked, al = [x[:, 0]], [alive[:, 0]]
+        for t in range(1, T):
+            cost = torch.clamp(m._torch_cost(tracked[-1], x[:, t], al[-1], alive[:, t]), -1e4, 1e4)
+            perm, conf = sinkhorn_matching(cost)
+            matched = (al[-1] > 0.5).float() * (alive[:, t] > 0.5).float().gather(1, perm) * (conf > 0.3).float()
+            re = x[:, t].gather(1, perm.unsqueeze(-1).expand(B, N, D))
+            h1 = m.hidden_gru(re.reshape(-1, D), hidden.reshape(-1, D)).reshape(B, N, D)
+            hidden = matched.unsqueeze(-1) * h1 + (1 - matched.unsqueeze(-1)) * re
+            tracked.append(re)
+            al.append(alive[:, t].gather(1, perm))
+        return torch.stack(tracked, 1), torch.stack(al, 1), hidden
+
+    with torch.no_grad():
+        Wb, Wf = TrackerWeights.from_module(m, torch.bfloat16), TrackerWeights.from_module(m, torch.float32)
+        bf_med, _ = _event_timing(lambda: track_sequence(x, alive, Wb), n, warmup)
+        bfh_med, _ = _event_timing(lambda: track_sequence(x, alive, Wb, with_hidden=True), n, warmup)
+        f32h_med, _ = _event_timing(lambda: track_sequence(x, alive, Wf, with_hidden=True), n, warmup)
+        ref_med, _ = _event_timing(reference_loop, 3, 1)
+        rt, ra, rh = reference_loop()
+        got = track_sequence(x, alive, Wf, with_hidden=True)
+        agree = float((got["tracked"] == rt).all(-1).float().mean().item())
+    pairs = B * (T - 1) * N * N
+    # pair MLP: |a - b| block of the first layer (D x D), second layer (D x D/4), score (D/4);
+    # per-node projections of the first layer's [a; b] blocks (2 x D x D per slot row)
+    flops = 2 * (pairs * (D * D + D * (D // 4) + D // 4) + B * T * N * 2 * D * D)
+    tf = flops / bf_med / 1e12
+    return {"workload": "slot tracking loop, small preset: 32 clips x 64 frames x 32 slots, d_slot 192, 80% live "
+                        "slots, 20 Sinkhorn iterations per frame",
+            "pairs": pairs, "fused_bf16_us": round(bf_med * 1e6, 2), "fused_bf16_with_gru_us": round(bfh_med * 1e6, 2),
+            "fused_fp32_with_gru_us": round(f32h_med * 1e6, 2), "torch_reference_fp32_us": round(ref_med * 1e6, 2),
+            "speedup_bf16_with_gru": round(ref_med / bfh_med, 2), "speedup_fp32_with_gru": round(ref_med / f32h_med, 2),
+            "fp32_tracked_rows_equal_to_torch": agree,
+            "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4), "flops_per_call": flops,
+                         "note": "whole call (cost launch + sequential Sinkhorn loop + gather) against the pair "
+                                 "MLP's flops"}}
+
+
 def _bench_chain(dev, n, warmup):
     """Config 4: four chained scans at (1024, 1024, 768), S=16, bf16 (each fed the previous output),
     then the event index of a p=0.05 mask (t=0 forced) and causal event attention, 12 heads x 64."""
@@ -513,6 +568,7 @@ def main():
         out["scan_bwd"] = _bench_scan_bwd(dev, 50, 5)
         out["level1"] = _bench_level1(dev, 30, 3)
         out["gnn"] = _bench_gnn(dev, 20, 3)
+        out["track"] = _bench_track(dev, 20, 3)
     print(json.dumps(out), flush=True)
 
 

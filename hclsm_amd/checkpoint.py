@@ -6,6 +6,8 @@ The reference trainer saves ``step_N.pt`` as ``{"model": state_dict, "optimizer"
 the reference's module trees and parameter names, so their slices of that state dict load unchanged:
 
     slot_attention.*, target_slot_attention.*  -> hclsm_amd.objects.DynamicSlotAttention (model.py:72, :123)
+    slot_tracker.*                             -> hclsm_amd.objects.SlotTracker           (model.py:74)
+    relation_graph.*                           -> hclsm_amd.objects.RelationGraph         (model.py:75)
     level0_ssm.*                               -> hclsm_amd.dynamics.Level0SSM            (model.py:82)
     level1_event.*                             -> hclsm_amd.dynamics.Level1EventDynamics  (model.py:89)
     hierarchy_manager.*                        -> hclsm_amd.dynamics.HierarchyManager     (model.py:91-93)
@@ -24,14 +26,14 @@ import torch
 
 # Hot-path fields of the reference presets (hclsm/config.py:193-290 and the dataclass defaults :31-83).
 PRESETS = {
-    "tiny": dict(d_world=256, d_slot=128, n_max_slots=16, n_iterations=3, d_state=32, n_blocks=2,
-                 l1=(256, 2, 4), l2_d_model=384),
-    "small": dict(d_world=384, d_slot=192, n_max_slots=32, n_iterations=5, d_state=48, n_blocks=3,
-                  l1=(384, 3, 6), l2_d_model=512),
-    "base": dict(d_world=768, d_slot=256, n_max_slots=64, n_iterations=7, d_state=64, n_blocks=4,
-                 l1=(512, 4, 8), l2_d_model=768),
-    "large": dict(d_world=1024, d_slot=384, n_max_slots=128, n_iterations=7, d_state=96, n_blocks=6,
-                  l1=(768, 6, 12), l2_d_model=1024),
+    "tiny": dict(d_world=256, d_slot=128, n_max_slots=16, n_iterations=3, d_edge=64, gnn_rounds=1, d_state=32,
+                 n_blocks=2, l1=(256, 2, 4), l2_d_model=384),
+    "small": dict(d_world=384, d_slot=192, n_max_slots=32, n_iterations=5, d_edge=96, gnn_rounds=2, d_state=48,
+                  n_blocks=3, l1=(384, 3, 6), l2_d_model=512),
+    "base": dict(d_world=768, d_slot=256, n_max_slots=64, n_iterations=7, d_edge=128, gnn_rounds=2, d_state=64,
+                 n_blocks=4, l1=(512, 4, 8), l2_d_model=768),
+    "large": dict(d_world=1024, d_slot=384, n_max_slots=128, n_iterations=7, d_edge=192, gnn_rounds=3, d_state=96,
+                  n_blocks=6, l1=(768, 6, 12), l2_d_model=1024),
 }
 
 _WRAPPER_PREFIXES = ("module.", "_orig_mod.", "_fsdp_wrapped_module.")
@@ -44,7 +46,8 @@ def preset_config(name: str) -> SimpleNamespace:
     return SimpleNamespace(
         d_world=p["d_world"],
         objects=SimpleNamespace(d_slot=p["d_slot"], n_max_slots=p["n_max_slots"], n_iterations=p["n_iterations"],
-                                existence_threshold=0.5, birth_threshold=0.7),
+                                existence_threshold=0.5, birth_threshold=0.7, d_edge=p["d_edge"],
+                                gnn_rounds=p["gnn_rounds"]),
         dynamics=SimpleNamespace(
             level0=SimpleNamespace(d_state=p["d_state"], n_blocks=p["n_blocks"], expand_ratio=2),
             level1=SimpleNamespace(d_model=d_model, n_layers=n_layers, n_heads=n_heads),
@@ -92,11 +95,13 @@ def build_hot_path(source, config, device="cuda", with_target: bool = False) -> 
     parameter of each module must be present with the reference's name and shape).  Returns a dict
     keyed by the reference's attribute names."""
     from hclsm_amd.dynamics import HierarchyManager, Level0SSM, Level1EventDynamics
-    from hclsm_amd.objects import DynamicSlotAttention
+    from hclsm_amd.objects import DynamicSlotAttention, RelationGraph, SlotTracker
     state = read_model_state(source)
     d_slot = config.objects.d_slot
     mods = {
         "slot_attention": DynamicSlotAttention(config.objects, config.d_world),
+        "slot_tracker": SlotTracker(config.objects),
+        "relation_graph": RelationGraph(config.objects),
         "level0_ssm": Level0SSM(config.dynamics.level0, d_slot),
         "level1_event": Level1EventDynamics(config.dynamics.level1, d_slot),
         "hierarchy_manager": HierarchyManager(d_slot, config.dynamics.level2.d_model),

@@ -24,45 +24,9 @@
 //                   D  (causal) sigmoid(c2 . ReLU(e C1^T + d1) + d2) * alive_i * alive_j -> causal[i, j]
 // The node update nodes += U2 ReLU(U1 [nodes; agg] + c1) + c2 runs on the MFMA linear kernels.
 #include "internal.h"
-#include "mfma.h"
+#include "pair_tile.h"
 
 namespace hclsm {
-
-// k-fragment of one lane per MFMA group: KE contiguous elements at kb + KE*g of a KB-wide block.
-// 16-bit: one v_mfma_f32_16x16x32 per block.  fp32: four v_mfma_f32_16x16x4 (MFMA e contracts k = 4g + e
-// across the lane groups: the contraction order is permuted, the sum is the same).
-template <int DT> struct GFrag;
-template <> struct GFrag<HCLSM_BF16> {
-  static constexpr int KE = 8, KB = 32;
-};
-template <> struct GFrag<HCLSM_F16> {
-  static constexpr int KE = 8, KB = 32;
-};
-template <> struct GFrag<HCLSM_F32> {
-  static constexpr int KE = 4, KB = 16;
-};
-
-template <int DT>
-__device__ __forceinline__ void frag_load(const typename MM<DT>::T* p, typename MM<DT>::T* e) {
-  if constexpr (DT == HCLSM_F32) {
-    const float4 v = *reinterpret_cast<const float4*>(p);
-    e[0] = v.x; e[1] = v.y; e[2] = v.z; e[3] = v.w;
-  } else {
-    *reinterpret_cast<uint4*>(e) = *reinterpret_cast<const uint4*>(p);
-  }
-}
-
-template <int DT>
-__device__ __forceinline__ f32x4 frag_mma(const typename MM<DT>::T* a, const typename MM<DT>::T* b, f32x4 acc) {
-  using A = MM<DT>;
-  if constexpr (DT == HCLSM_F32) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) acc = A::mfma(a[e], b[e], acc);
-    return acc;
-  } else {
-    return A::mfma(A::load(a), A::load(b), acc);
-  }
-}
 
 struct GnnArgs {
   const float* X;      // node features, row stride ldx
@@ -91,18 +55,6 @@ struct GnnArgs {
 
 // Weight chunks are staged in LDS (shared by the workgroup's waves): KC columns of every output row
 // (KC a multiple of the fragment block KB; smaller KC when the widest layer would not fit).
-
-// sW[r * pitch + c] = W[r * ldw + k0 + c] for r < nrows, c < kc (16-byte units; kc a multiple of the unit)
-template <typename T, int NTH>
-__device__ __forceinline__ void stage_rows(const T* __restrict__ W, int ldw, int nrows, int k0, int kc, T* sW,
-                                           int pitch, int tid) {
-  constexpr int U = 16 / (int)sizeof(T);
-  const int upr = kc / U;
-  for (int u = tid; u < nrows * upr; u += NTH) {
-    const int r = u / upr, c = (u - r * upr) * U;
-    *reinterpret_cast<uint4*>(sW + r * pitch + c) = *reinterpret_cast<const uint4*>(W + (size_t)r * ldw + k0 + c);
-  }
-}
 
 template <int DT, int NW, int KC>
 __global__ void __launch_bounds__(64 * NW)
@@ -135,27 +87,8 @@ gnn_edge_kernel(GnnArgs a) {
   const float* Xf = a.X + (size_t)f * N * a.ldx;
   const float* alive = a.alive ? a.alive + (size_t)f * N : nullptr;
   auto pair_mask = [&](int i, int j) { return alive ? alive[i] * alive[j] : 1.f; };
-  // acc[t] += A-rows (this wave's 16) x W rows t*16 + li over K, W streamed through LDS in KC-column chunks;
-  // a_frag(k) gives this lane's KE operand elements at column k
-  auto gemm = [&](auto& acc, int NT, int NTMAX, const T* W, int K, auto a_frag) {
-    for (int k0 = 0; k0 < K; k0 += KC) {
-      const int kc = K - k0 < KC ? K - k0 : KC;
-      __syncthreads();   // the previous chunk is consumed
-      stage_rows<T, NTH>(W, K, NT * 16, k0, kc, sW, PW, tid);
-      __syncthreads();
-      for (int kb = 0; kb < kc; kb += KB) {
-        T op[KE];
-        a_frag(k0 + kb + KE * g, op);
-#pragma unroll
-        for (int t = 0; t < NTMAX; ++t) {
-          if (t < NT) {
-            T wb[KE];
-            frag_load<DT>(sW + (t * 16 + li) * PW + kb + KE * g, wb);
-            acc[t] = frag_mma<DT>(op, wb, acc[t]);
-          }
-        }
-      }
-    }
+  auto gemm = [&](auto& acc, int NT, const T* W, int K, auto a_frag) {
+    tile_gemm<DT, KC, NTH>(acc, NT, W, K, K, sW, tid, a_frag);
   };
 
   // ---- A: Hadamard GEMM + pair statistics -> H1
@@ -170,7 +103,7 @@ gnn_edge_kernel(GnnArgs a) {
     f32x4 acc[24];
 #pragma unroll
     for (int t = 0; t < 24; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    gemm(acc, NT, 24, reinterpret_cast<const T*>(a.A4), D, [&](int k, T* op) {
+    gemm(acc, NT, reinterpret_cast<const T*>(a.A4), D, [&](int k, T* op) {
       float vi[KE], vj[KE];
 #pragma unroll
       for (int e = 0; e < KE; e += 4) {
@@ -233,7 +166,7 @@ gnn_edge_kernel(GnnArgs a) {
 #pragma unroll
     for (int t = 0; t < 12; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
     const T* hrow = sH + (size_t)(wid * 16 + li) * LH;
-    gemm(acc, NT, 12, reinterpret_cast<const T*>(a.W2), H1, [&](int k, T* op) { frag_load<DT>(hrow + k, op); });
+    gemm(acc, NT, reinterpret_cast<const T*>(a.W2), H1, [&](int k, T* op) { frag_load<DT>(hrow + k, op); });
     __syncthreads();   // H1 fully consumed
 #pragma unroll
     for (int t = 0; t < 12; ++t) {
@@ -267,7 +200,7 @@ gnn_edge_kernel(GnnArgs a) {
       f32x4 acc[12];
 #pragma unroll
       for (int t = 0; t < 12; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-      gemm(acc, NT, 12, Wm + (size_t)t0 * 16 * E, E, [&](int k, T* op) { frag_load<DT>(erow + k, op); });
+      gemm(acc, NT, Wm + (size_t)t0 * 16 * E, E, [&](int k, T* op) { frag_load<DT>(erow + k, op); });
 #pragma unroll
       for (int t = 0; t < 12; ++t) {
         if (t < NT) {
@@ -302,7 +235,7 @@ gnn_edge_kernel(GnnArgs a) {
     f32x4 acc[6];
 #pragma unroll
     for (int t = 0; t < 6; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    gemm(acc, NT, 6, reinterpret_cast<const T*>(a.C1), E, [&](int k, T* op) { frag_load<DT>(erow + k, op); });
+    gemm(acc, NT, reinterpret_cast<const T*>(a.C1), E, [&](int k, T* op) { frag_load<DT>(erow + k, op); });
     float part[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < 6; ++t) {

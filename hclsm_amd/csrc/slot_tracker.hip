@@ -1,0 +1,769 @@
+// Slot tracker for gfx950: SlotTracker of hclsm/objects/slot_tracker.py:46-158 and the frame-by-frame
+// tracking loop of hclsm/model.py:229-252.
+//
+// Matching cost of pair (i, j) (slot i of the earlier frame, slot j of the later one), slot_tracker.py:74-107:
+//   score = w3 . ReLU(W2 ReLU(W1 [a_i; b_j; |a_i - b_j|] + b1) + b2) + b3   (a, b clamped to [-50, 50])
+//   cost  = -(score - 1e4 [alive_a_i < 0.5] - 1e4 [alive_b_j < 0.5])
+// W1 [a; b; d] = W1a a + W1b b + W1c d: the first two terms are per-node projections (one GEMM over the
+// nodes), so only W1c |a_i - b_j| (K = D instead of 3D) is contracted per pair, on MFMA pair tiles whose
+// operand is formed on the fly; the second layer and the score follow in the same workgroup.
+//
+// Tracking loop.  Step t matches the tracked slots of frame t-1 (frame t-1 permuted by the previous step's
+// perm, alive permuted with them) against frame t.  Row i of that cost matrix is row perm_{t-1}[i] of the
+// cost between the unpermuted frames t-1 and t, penalties included.  So the pair MLP runs once, in one
+// launch, over every (t-1, t) frame pair of every clip; only the Sinkhorn matching is sequential in t: one
+// workgroup per clip loops over the frames with the previous perm and alive row in LDS.  The tracked slots
+// are gathered afterwards in one parallel pass.  The GRU hidden state (slot_tracker.py:137-158) does not
+// feed back into the matching; when it is wanted it is carried in a second loop, one GEMM and one gate
+// launch per frame, with the input-side GEMM done once for all frames.
+//
+// Sinkhorn (slot_tracker.py:15-43): log_alpha = -clamp(cost, -1e4, 1e4) * (1 / temperature), then n_iters
+// rounds of log-sum-exp normalisation over rows, then over columns, updated in place; perm = argmax over j
+// of exp(log_alpha) (lowest index on ties), confidence = that maximum.  A frame's matrix stays in
+// registers: each wave holds 32 rows, lane 8 rg + cg holds rows rg + 8r (r < 4) x columns cg + 8c
+// (c < CPL).  Row reductions run over the 8 lanes of a row group (DPP), column reductions over the 8 row
+// groups of the wave (DPP row rotate and the two permlane swaps) and, for N > 32, across the waves through
+// LDS, merging (max, sum) pairs.
+#include "internal.h"
+#include "pair_tile.h"
+
+namespace hclsm {
+
+constexpr float TRK_PENALTY = 1e4f;
+constexpr float TRK_COST_CLAMP = 1e4f;
+constexpr float TRK_SLOT_CLAMP = 50.f;
+
+// ------------------------------------------------------------------------------------------------ cost
+struct TrackCostArgs {
+  const float* S;      // clamped node rows [rows, D] fp32
+  const float* UV;     // [rows, 2D] fp32: W1a s + b1 | W1b s
+  const void* W1;      // match_mlp.0.weight [D, 3D] (operand dtype)
+  const void* W2;      // match_mlp.2.weight [D/4, D] (operand dtype)
+  const float* b2;     // [D/4]
+  const float* w3;     // match_mlp.4.weight [D/4]
+  const float* b3;     // [1]
+  const float* alive_a;   // alive of the a rows, indexed by node row, or null (all alive)
+  const float* alive_b;   // alive of the b rows, indexed by node row - boff
+  int64_t boff;
+  float* cost;         // [F, N, N]
+  int64_t pairs;       // F * N * N
+  int N, D;
+  int nt, tstride, fboff;   // cost frame f pairs node frames fa = (f / nt) * tstride + f % nt and fa + fboff
+};
+
+template <int DT, int NW, int KC>
+__global__ void __launch_bounds__(64 * NW)
+track_cost_kernel(TrackCostArgs a) {
+  using A = MM<DT>;
+  using T = typename A::T;
+  constexpr int KE = GFrag<DT>::KE;
+  constexpr int ROWS = 16 * NW, NTH = 64 * NW;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int N = a.N, D = a.D, LH = D + 8;
+  T* sH = reinterpret_cast<T*>(smem);    // [ROWS][LH] first hidden layer of the workgroup's pairs
+  T* sW = sH + (size_t)ROWS * LH;        // [D][KC + 8] weight chunk
+  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, g = lane >> 4, li = lane & 15;
+  const int64_t p0 = (int64_t)blockIdx.x * ROWS;
+  const int64_t NN = (int64_t)N * N;
+  // pair p (clamped into range) -> node rows of a_i and b_j
+  auto nodes_of = [&](int64_t p, int64_t& ra, int64_t& rb) {
+    p = p < a.pairs ? p : a.pairs - 1;
+    const int64_t f = p / NN;
+    const int rem = (int)(p - f * NN);
+    const int i = rem / N, j = rem - i * N;
+    const int64_t q = f / a.nt;
+    const int64_t fa = q * a.tstride + (f - q * a.nt);
+    ra = fa * N + i;
+    rb = (fa + a.fboff) * N + j;
+  };
+
+  // ---- first layer: ReLU(W1c |a_i - b_j| + U_i + V_j) -> sH
+  {
+    int64_t ra, rb;
+    nodes_of(p0 + wid * 16 + li, ra, rb);
+    const float* xa = a.S + ra * D;
+    const float* xb = a.S + rb * D;
+    const int NT = D / 16;
+    f32x4 acc[24];
+#pragma unroll
+    for (int t = 0; t < 24; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    tile_gemm<DT, KC, NTH>(acc, NT, reinterpret_cast<const T*>(a.W1) + 2 * D, 3 * D, D, sW, tid, [&](int k, T* op) {
+#pragma unroll
+      for (int e = 0; e < KE; e += 4) {
+        const float4 x4 = *reinterpret_cast<const float4*>(xa + k + e);
+        const float4 y4 = *reinterpret_cast<const float4*>(xb + k + e);
+        op[e] = A::fromf(fabsf(x4.x - y4.x));
+        op[e + 1] = A::fromf(fabsf(x4.y - y4.y));
+        op[e + 2] = A::fromf(fabsf(x4.z - y4.z));
+        op[e + 3] = A::fromf(fabsf(x4.w - y4.w));
+      }
+    });
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int orow = wid * 16 + 4 * g + rr;
+      int64_t rao, rbo;
+      nodes_of(p0 + orow, rao, rbo);
+      const float* U = a.UV + rao * 2 * D;
+      const float* V = a.UV + rbo * 2 * D + D;
+#pragma unroll
+      for (int t = 0; t < 24; ++t) {
+        if (t < NT) {
+          const int o = t * 16 + li;
+          sH[(size_t)orow * LH + o] = A::fromf(fmaxf(acc[t][rr] + U[o] + V[o], 0.f));
+        }
+      }
+    }
+  }
+
+  // ---- second layer and score (tile_gemm's first barrier orders the sH writes before these reads)
+  {
+    const int NT = D / 64;   // D/4 outputs in 16-wide tiles
+    f32x4 acc[6];
+#pragma unroll
+    for (int t = 0; t < 6; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const T* hrow = sH + (size_t)(wid * 16 + li) * LH;
+    tile_gemm<DT, KC, NTH>(acc, NT, reinterpret_cast<const T*>(a.W2), D, D, sW, tid,
+                           [&](int k, T* op) { frag_load<DT>(hrow + k, op); });
+    float part[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < 6; ++t) {
+      if (t < NT) {
+        const int o = t * 16 + li;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) part[rr] = fmaf(fmaxf(acc[t][rr] + a.b2[o], 0.f), a.w3[o], part[rr]);
+      }
+    }
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr)
+#pragma unroll
+      for (int m = 1; m < 16; m <<= 1) part[rr] += __shfl_xor(part[rr], m, 64);
+    if (li == 0) {
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int64_t p = p0 + wid * 16 + 4 * g + rr;
+        if (p < a.pairs) {
+          float s = part[rr] + a.b3[0];
+          if (a.alive_a) {
+            int64_t ra, rb;
+            nodes_of(p, ra, rb);
+            s = s - (a.alive_a[ra] < 0.5f ? TRK_PENALTY : 0.f);
+            s = s - (a.alive_b[rb - a.boff] < 0.5f ? TRK_PENALTY : 0.f);
+          }
+          a.cost[p] = -s;
+        }
+      }
+    }
+  }
+}
+
+// y[r, k] = clamp(x[r, k], -50, 50) (NaN passes through, as torch.clamp)
+__global__ void __launch_bounds__(256)
+trk_clamp_kernel(const float* __restrict__ x, float* __restrict__ y, int64_t n) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= n) return;
+  const float v = x[e];
+  y[e] = v < -TRK_SLOT_CLAMP ? -TRK_SLOT_CLAMP : (v > TRK_SLOT_CLAMP ? TRK_SLOT_CLAMP : v);
+}
+
+// --------------------------------------------------------------------------------------------- Sinkhorn
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, true);
+}
+
+// All-reduce over the 8 lanes of a row group (lane bits 0-2): quad xor 1, quad xor 2, half-row mirror.
+template <bool MAX>
+__device__ __forceinline__ float row_reduce(float v) {
+  if constexpr (MAX) {
+    v = fmaxf(v, dpp_f<0xb1>(v));
+    v = fmaxf(v, dpp_f<0x4e>(v));
+    return fmaxf(v, dpp_f<0x141>(v));
+  } else {
+    v += dpp_f<0xb1>(v);
+    v += dpp_f<0x4e>(v);
+    return v + dpp_f<0x141>(v);
+  }
+}
+
+// All-reduce over the 8 row groups of a wave (lane bits 3-5): row rotate by 8 (xor 8 within 16 lanes),
+// then permlane16 and permlane32 swaps (each hands every lane its partner's value across the 16 / 32 split).
+template <bool MAX>
+__device__ __forceinline__ float col_reduce(float v) {
+  auto op = [](float x, float y) { return MAX ? fmaxf(x, y) : x + y; };
+  v = op(v, dpp_f<0x128>(v));
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float lse_of(float m, float s) { return m == -INFINITY ? 0.f : m + __logf(s); }
+
+// n_iters rounds of row then column log-sum-exp normalisation of la in place.  W waves hold 32 rows each;
+// sred: [2][W][8 * CPL][2] floats of LDS (unused for W == 1).  Entries at -inf (padding) stay -inf.
+template <int CPL, int W>
+__device__ __forceinline__ void sinkhorn_regs(float (&la)[4][CPL], int n_iters, float* sred, int wid, int rg,
+                                              int cg) {
+  constexpr int NC = 8 * CPL;
+  for (int it = 0; it < n_iters; ++it) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float m = la[r][0];
+#pragma unroll
+      for (int c = 1; c < CPL; ++c) m = fmaxf(m, la[r][c]);
+      m = row_reduce<true>(m);
+      float s = 0.f;
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) s += __expf(la[r][c] - m);
+      s = row_reduce<false>(s);
+      const float l = lse_of(m, s);
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) la[r][c] -= l;
+    }
+    float cm[CPL], cs[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      float m = fmaxf(fmaxf(la[0][c], la[1][c]), fmaxf(la[2][c], la[3][c]));
+      m = col_reduce<true>(m);
+      float s = 0.f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s += __expf(la[r][c] - m);
+      cm[c] = m;
+      cs[c] = col_reduce<false>(s);
+    }
+    if constexpr (W > 1) {
+      float* buf = sred + (size_t)(it & 1) * W * NC * 2;
+      if (rg == 0) {
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+          buf[(wid * NC + cg + 8 * c) * 2] = cm[c];
+          buf[(wid * NC + cg + 8 * c) * 2 + 1] = cs[c];
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < W; ++w) M = fmaxf(M, buf[(w * NC + cg + 8 * c) * 2]);
+        float S = 0.f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+          const float mw = buf[(w * NC + cg + 8 * c) * 2];
+          if (mw != -INFINITY) S = fmaf(buf[(w * NC + cg + 8 * c) * 2 + 1], __expf(mw - M), S);
+        }
+        cm[c] = M;
+        cs[c] = S;
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const float l = lse_of(cm[c], cs[c]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) la[r][c] -= l;
+    }
+  }
+}
+
+// Per row r: (max over j < N of exp(la), its lowest j) over the whole row, in every lane of the row group.
+// The index is always in [0, N): a row with no comparable entry (all NaN) gives index 0, value NaN.
+template <int CPL>
+__device__ __forceinline__ void argmax_regs(const float (&la)[4][CPL], int N, int cg, float (&bv)[4], int (&bi)[4]) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float v = -1.f;
+    int id = 0;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const float e = expf(la[r][c]);
+      if (cg + 8 * c < N && e > v) {
+        v = e;
+        id = cg + 8 * c;
+      }
+    }
+    auto take = [&](float ov, int oi) {
+      if (ov > v || (ov == v && oi < id)) {
+        v = ov;
+        id = oi;
+      }
+    };
+    take(dpp_f<0xb1>(v), dpp_i<0xb1>(id));
+    take(dpp_f<0x4e>(v), dpp_i<0x4e>(id));
+    take(dpp_f<0x141>(v), dpp_i<0x141>(id));
+    bv[r] = v < 0.f ? __int_as_float(0x7fc00000) : v;
+    bi[r] = id;
+  }
+}
+
+// -log_alpha entry: clamp(cost, -1e4, 1e4) (NaN passes through), negated, times 1 / temperature
+__device__ __forceinline__ float la_of(float c, float inv_t) {
+  c = c < -TRK_COST_CLAMP ? -TRK_COST_CLAMP : (c > TRK_COST_CLAMP ? TRK_COST_CLAMP : c);
+  return -c * inv_t;
+}
+
+template <int CPL, int W>
+__device__ __forceinline__ void load_la(float (&la)[4][CPL], const float* cost, const int* src_row, int N,
+                                        float inv_t, int wid, int rg, int cg) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int i = 32 * wid + rg + 8 * r;
+    const float* row = i < N ? cost + (size_t)(src_row ? src_row[i] : i) * N : cost;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const int j = cg + 8 * c;
+      la[r][c] = (i < N && j < N) ? la_of(row[j], inv_t) : -INFINITY;
+    }
+  }
+}
+
+// SlotTracker.forward after the cost (slot_tracker.py:122-135) for one frame per workgroup.
+template <int CPL, int W>
+__global__ void __launch_bounds__(64 * W)
+track_match_kernel(const float* __restrict__ cost, const float* __restrict__ alive_a,
+                   const float* __restrict__ alive_b, int64_t* __restrict__ perm, float* __restrict__ matched,
+                   float* __restrict__ conf, int N, int n_iters, float inv_t) {
+  __shared__ float sred[W > 1 ? 2 * W * 8 * CPL * 2 : 1];
+  const int64_t f = blockIdx.x;
+  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, rg = lane >> 3, cg = lane & 7;
+  float la[4][CPL];
+  load_la<CPL, W>(la, cost + f * N * N, nullptr, N, inv_t, wid, rg, cg);
+  sinkhorn_regs<CPL, W>(la, n_iters, sred, wid, rg, cg);
+  float bv[4];
+  int bi[4];
+  argmax_regs<CPL>(la, N, cg, bv, bi);
+  if (cg == 0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = 32 * wid + rg + 8 * r;
+      if (i < N) {
+        const int64_t o = f * N + i;
+        const float at = alive_a ? (alive_a[o] > 0.5f ? 1.f : 0.f) : 1.f;
+        const float at1 = alive_b ? (alive_b[f * N + bi[r]] > 0.5f ? 1.f : 0.f) : 1.f;
+        perm[o] = bi[r];
+        matched[o] = at * at1 * (bv[r] > 0.3f ? 1.f : 0.f);
+        if (conf) conf[o] = bv[r];
+      }
+    }
+  }
+}
+
+// The matching half of the tracking loop (model.py:233-252) for one clip per workgroup.  C: cost between
+// the unpermuted frames t-1 and t, [clip][T-1][N][N]; alive [clip][T][N] (null: all alive).  Writes, for
+// t >= 1, perm32 / perm64 / matched / alive_out at [clip][t][i] (t = 0: identity, 0, alive of frame 0).
+template <int CPL, int W>
+__global__ void __launch_bounds__(64 * W)
+track_sequence_kernel(const float* __restrict__ C, const float* __restrict__ alive, int* __restrict__ perm32,
+                      int64_t* __restrict__ perm64, float* __restrict__ matched, float* __restrict__ alive_out,
+                      int T, int N, int n_iters, float inv_t) {
+  __shared__ float sred[W > 1 ? 2 * W * 8 * CPL * 2 : 1];
+  __shared__ int sperm[32 * W];      // perm of the previous step (rows of the tracked frame t-1)
+  __shared__ float salive[32 * W];   // alive of the tracked frame t-1
+  const int64_t b = blockIdx.x;
+  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, rg = lane >> 3, cg = lane & 7;
+  const int64_t base = b * T * N;
+  for (int i = tid; i < N; i += 64 * W) {
+    const float al = alive ? alive[base + i] : 1.f;
+    sperm[i] = i;
+    salive[i] = al;
+    perm32[base + i] = i;
+    if (perm64) perm64[base + i] = i;
+    matched[base + i] = 0.f;
+    if (alive_out) alive_out[base + i] = al;
+  }
+  __syncthreads();
+  for (int t = 1; t < T; ++t) {
+    float la[4][CPL];
+    load_la<CPL, W>(la, C + ((size_t)b * (T - 1) + (t - 1)) * N * N, sperm, N, inv_t, wid, rg, cg);
+    sinkhorn_regs<CPL, W>(la, n_iters, sred, wid, rg, cg);
+    float bv[4];
+    int bi[4];
+    argmax_regs<CPL>(la, N, cg, bv, bi);
+    __syncthreads();   // every lane has read sperm
+    if (cg == 0) {
+      const int64_t o = base + (int64_t)t * N;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = 32 * wid + rg + 8 * r;
+        if (i < N) {
+          const float a1 = alive ? alive[o + bi[r]] : 1.f;
+          perm32[o + i] = bi[r];
+          if (perm64) perm64[o + i] = bi[r];
+          matched[o + i] = (salive[i] > 0.5f ? 1.f : 0.f) * (a1 > 0.5f ? 1.f : 0.f) * (bv[r] > 0.3f ? 1.f : 0.f);
+          if (alive_out) alive_out[o + i] = a1;
+          salive[i] = a1;
+          sperm[i] = bi[r];
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ------------------------------------------------------------------------------------- reorder and GRU
+// y[row, k] = x[frame * N + perm[row], k] with frame = row / N; an index outside [0, N) gives a NaN row.
+template <typename I>
+__global__ void __launch_bounds__(256)
+trk_gather_kernel(const float* __restrict__ x, const I* __restrict__ perm, float* __restrict__ y, int64_t rows,
+                  int N, int D) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= rows * D) return;
+  const int64_t row = e / D;
+  const int k = (int)(e - row * D);
+  const int64_t p = (int64_t)perm[row];
+  y[e] = (p >= 0 && p < N) ? x[((row / N) * N + p) * D + k] : __int_as_float(0x7fc00000);
+}
+
+// torch.nn.GRUCell gates and the matched blend of SlotTracker.reorder_and_update (slot_tracker.py:150-156)
+// for rows (f, i), f < nf, i < N:
+//   gi = GI[f * sgi + pi] (pi = perm[f * sp + i], or i when perm is null), gh = GH[f * N + i] ([r; z; n]);
+//   h' = n + z (h - n), n = tanh(gi_n + r gh_n);  out = m h' + (1 - m) re, m = matched[f * sm + i],
+//   re = RE[f * sre + i], h = H[f * N + i].  In place (out == H) is allowed.
+__global__ void __launch_bounds__(256)
+trk_gru_gate_kernel(const float* __restrict__ GI, int64_t sgi, const int* __restrict__ perm, int64_t sp,
+                    const float* __restrict__ GH, const float* __restrict__ matched, int64_t sm,
+                    const float* __restrict__ RE, int64_t sre, const float* H, float* out, int64_t nf, int N,
+                    int D) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= nf * N * D) return;
+  const int64_t row = e / D;
+  const int k = (int)(e - row * D);
+  const int64_t f = row / N;
+  const int i = (int)(row - f * N);
+  const int pi = perm ? perm[f * sp + i] : i;
+  const float* gi = GI + (f * sgi + pi) * 3 * D;
+  const float* gh = GH + row * 3 * D;
+  const float r = 1.f / (1.f + expf(-(gi[k] + gh[k])));
+  const float z = 1.f / (1.f + expf(-(gi[D + k] + gh[D + k])));
+  const float n = tanhf(gi[2 * D + k] + r * gh[2 * D + k]);
+  const float h1 = n + z * (H[e] - n);
+  const float m = matched[f * sm + i];
+  out[e] = m * h1 + (1.f - m) * RE[(f * sre + i) * D + k];
+}
+
+// ------------------------------------------------------------------------------------------------ host
+static unsigned blocks256(int64_t n) { return (unsigned)((n + 255) / 256); }
+
+template <int DT, int NW, int KC>
+static size_t cost_lds(int D) {
+  return ((size_t)16 * NW * (D + 8) + (size_t)D * (KC + 8)) * sizeof(typename MM<DT>::T);
+}
+
+constexpr size_t TRK_LDS_MAX = 160 * 1024;
+
+template <int DT, int NW, int KC>
+static int launch_cost_kc(const TrackCostArgs& a, hipStream_t st) {
+  static bool big_lds = false;   // allow more than the default 64 KB of dynamic LDS (idempotent)
+  if (!big_lds) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&track_cost_kernel<DT, NW, KC>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)TRK_LDS_MAX);
+    if (e != hipSuccess) return (int)e;
+    big_lds = true;
+  }
+  const size_t lds = cost_lds<DT, NW, KC>(a.D);
+  const int64_t tiles = (a.pairs + 16 * NW - 1) / (16 * NW);
+  hipLaunchKernelGGL((track_cost_kernel<DT, NW, KC>), dim3((unsigned)tiles), dim3(64 * NW), lds, st, a);
+  HCLSM_LAUNCH_CHECK();
+  return 0;
+}
+
+// 16-bit operands: 128 pairs per workgroup, weight chunks of 64 columns (32 when the LDS would overflow);
+// fp32: 64 pairs, chunks of 16.
+template <int DT>
+static int launch_cost(const TrackCostArgs& a, hipStream_t st) {
+  if (a.pairs == 0) return 0;
+  if constexpr (DT == HCLSM_F32) {
+    return launch_cost_kc<DT, 4, 16>(a, st);
+  } else {
+    if (cost_lds<DT, 8, 64>(a.D) <= TRK_LDS_MAX) return launch_cost_kc<DT, 8, 64>(a, st);
+    return launch_cost_kc<DT, 8, 32>(a, st);
+  }
+}
+
+static int launch_cost_dt(int dtype, const TrackCostArgs& a, hipStream_t st) {
+  switch (dtype) {
+    case HCLSM_BF16: return launch_cost<HCLSM_BF16>(a, st);
+    case HCLSM_F16: return launch_cost<HCLSM_F16>(a, st);
+    default: return launch_cost<HCLSM_F32>(a, st);
+  }
+}
+
+static int clamp_rows(const float* x, float* y, int64_t n, hipStream_t st) {
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(trk_clamp_kernel, dim3(blocks256(n)), dim3(256), 0, st, x, y, n);
+  HCLSM_LAUNCH_CHECK();
+  return 0;
+}
+
+// Sinkhorn tile shape for N: (columns per lane, waves)
+template <typename F>
+static int with_tile(int64_t N, F&& fn) {
+  if (N <= 16) return fn(std::integral_constant<int, 2>{}, std::integral_constant<int, 1>{});
+  if (N <= 32) return fn(std::integral_constant<int, 4>{}, std::integral_constant<int, 1>{});
+  if (N <= 64) return fn(std::integral_constant<int, 8>{}, std::integral_constant<int, 2>{});
+  return fn(std::integral_constant<int, 16>{}, std::integral_constant<int, 4>{});
+}
+
+constexpr int64_t TRK_MAX_SLOTS = 128;
+
+// D a multiple of 64 (so D/4 fills 16-wide MFMA tiles) and at most 384 (24 accumulator tiles); the pair
+// tile of the widest supported D fits the LDS with 32-column chunks for every operand type.
+static int track_check(int64_t N, int64_t D, int dtype) {
+  if (N < 0 || D <= 0) return HCLSM_ERR_SHAPE;
+  if (dtype != HCLSM_F32 && dtype != HCLSM_BF16 && dtype != HCLSM_F16) return HCLSM_ERR_DTYPE;
+  if (D % 64 || D > 384) return HCLSM_ERR_UNSUPPORTED;
+  return 0;
+}
+
+static float inv_temperature(float temperature) { return 1.f / (temperature > 1e-6f ? temperature : 1e-6f); }
+
+static size_t al256t(size_t v) { return (v + 255) / 256 * 256; }
+
+struct SeqWs {
+  size_t s, uv, c, perm, matched, gi, gh, total;
+};
+
+static SeqWs seq_ws(int64_t B, int64_t T, int64_t N, int64_t D, bool hidden) {
+  SeqWs w{};
+  const size_t R = (size_t)B * T * N;
+  size_t o = 0;
+  w.s = o; o += al256t(R * D * 4);
+  w.uv = o; o += al256t(R * 2 * D * 4);
+  w.c = o; o += al256t((size_t)B * (T > 0 ? T - 1 : 0) * N * N * 4);
+  w.perm = o; o += al256t(R * 4);
+  w.matched = o; o += al256t(R * 4);
+  if (hidden) {
+    w.gi = o; o += al256t(R * 3 * D * 4);
+    w.gh = o; o += al256t((size_t)B * N * 3 * D * 4);
+  }
+  w.total = o;
+  return w;
+}
+
+}  // namespace hclsm
+
+using namespace hclsm;
+
+// ----------------------------------------------------------------------------------------------- C ABI
+extern "C" int64_t hclsm_slot_track_cost_workspace(int64_t frames, int64_t N, int64_t D, int dtype) {
+  if (frames < 0) return HCLSM_ERR_SHAPE;
+  const int c = track_check(N, D, dtype);
+  if (c) return c;
+  const size_t R = (size_t)2 * frames * N;
+  return (int64_t)(al256t(R * D * 4) + al256t(R * 2 * D * 4));
+}
+
+// params: match_mlp.0.weight, .0.bias, match_mlp.2.weight, .2.bias, match_mlp.4.weight, .4.bias
+extern "C" int hclsm_slot_track_cost(const float* slots_t, const float* slots_t1, const float* alive_t,
+                                     const float* alive_t1, float* cost, int64_t frames, int64_t N, int64_t D,
+                                     const void* const* params, int dtype, void* workspace, int64_t workspace_bytes,
+                                     void* stream) {
+  if (frames < 0) return HCLSM_ERR_SHAPE;
+  const int chk = track_check(N, D, dtype);
+  if (chk) return chk;
+  if (frames * N * N > 0x7fffffffLL * 64) return HCLSM_ERR_SHAPE;
+  if (frames == 0 || N == 0) return 0;
+  if (!slots_t || !slots_t1 || !cost || !params || !workspace) return HCLSM_ERR_NULL;
+  if ((alive_t == nullptr) != (alive_t1 == nullptr)) return HCLSM_ERR_NULL;
+  for (int i = 0; i < 6; ++i)
+    if (!params[i]) return HCLSM_ERR_NULL;
+  if (workspace_bytes < hclsm_slot_track_cost_workspace(frames, N, D, dtype)) return HCLSM_ERR_SHAPE;
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t FN = frames * N, R = 2 * FN;
+  char* ws = reinterpret_cast<char*>(workspace);
+  float* S = reinterpret_cast<float*>(ws);
+  float* UV = reinterpret_cast<float*>(ws + al256t((size_t)R * D * 4));
+  int rc;
+  if ((rc = clamp_rows(slots_t, S, FN * D, st))) return rc;
+  if ((rc = clamp_rows(slots_t1, S + FN * D, FN * D, st))) return rc;
+  const int es = dtype == HCLSM_F32 ? 4 : 2;
+  const char* W1 = reinterpret_cast<const char*>(params[0]);
+  const float* b1 = reinterpret_cast<const float*>(params[1]);
+  // U over the earlier frame's rows (with b1), V over the later frame's rows
+  if ((rc = linear_rows(S, D, HCLSM_F32, W1, 3 * D, b1, nullptr, 0, UV, 2 * D, HCLSM_F32, FN, D, D, 0, 0, nullptr,
+                        nullptr, 0.f, nullptr, 0, nullptr, 1, dtype, st)))
+    return rc;
+  if ((rc = linear_rows(S + FN * D, D, HCLSM_F32, W1 + (size_t)D * es, 3 * D, nullptr, nullptr, 0,
+                        UV + FN * 2 * D + D, 2 * D, HCLSM_F32, FN, D, D, 0, 0, nullptr, nullptr, 0.f, nullptr, 0,
+                        nullptr, 1, dtype, st)))
+    return rc;
+  TrackCostArgs a{};
+  a.S = S; a.UV = UV; a.W1 = params[0]; a.W2 = params[2];
+  a.b2 = reinterpret_cast<const float*>(params[3]);
+  a.w3 = reinterpret_cast<const float*>(params[4]);
+  a.b3 = reinterpret_cast<const float*>(params[5]);
+  a.alive_a = alive_t;
+  a.alive_b = alive_t1;
+  a.boff = FN;
+  a.cost = cost;
+  a.pairs = frames * N * N;
+  a.N = (int)N; a.D = (int)D;
+  a.nt = (int)frames; a.tstride = 0; a.fboff = (int)frames;
+  return launch_cost_dt(dtype, a, st);
+}
+
+extern "C" int hclsm_slot_track_match(const float* cost, const float* alive_t, const float* alive_t1,
+                                      int64_t* perm, float* matched, float* confidence, int64_t frames, int64_t N,
+                                      int64_t n_iters, float temperature, void* stream) {
+  if (frames < 0 || N < 0 || n_iters < 0) return HCLSM_ERR_SHAPE;
+  if (N > TRK_MAX_SLOTS) return HCLSM_ERR_UNSUPPORTED;
+  if (frames > 0x7fffffffLL || n_iters > 0x7fffffffLL) return HCLSM_ERR_SHAPE;
+  if (frames == 0 || N == 0) return 0;
+  if (!cost || !perm || !matched) return HCLSM_ERR_NULL;
+  hipStream_t st = (hipStream_t)stream;
+  const float inv_t = inv_temperature(temperature);
+  return with_tile(N, [&](auto cpl, auto w) {
+    constexpr int CPL = decltype(cpl)::value, W = decltype(w)::value;
+    hipLaunchKernelGGL((track_match_kernel<CPL, W>), dim3((unsigned)frames), dim3(64 * W), 0, st, cost, alive_t,
+                       alive_t1, perm, matched, confidence, (int)N, (int)n_iters, inv_t);
+    HCLSM_LAUNCH_CHECK();
+    return 0;
+  });
+}
+
+extern "C" int64_t hclsm_slot_track_reorder_update_workspace(int64_t frames, int64_t N, int64_t D, int dtype) {
+  if (frames < 0) return HCLSM_ERR_SHAPE;
+  const int c = track_check(N, D, dtype);
+  if (c) return c;
+  return (int64_t)(2 * al256t((size_t)frames * N * 3 * D * 4));
+}
+
+// params: hidden_gru.weight_ih, .weight_hh (operand dtype), .bias_ih, .bias_hh (fp32, nullable)
+extern "C" int hclsm_slot_track_reorder_update(const float* slots_t1, const int64_t* perm, const float* hidden_t,
+                                               const float* matched, float* reordered, float* hidden_t1,
+                                               int64_t frames, int64_t N, int64_t D, const void* const* params,
+                                               int dtype, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (frames < 0) return HCLSM_ERR_SHAPE;
+  const int chk = track_check(N, D, dtype);
+  if (chk) return chk;
+  if (frames * N * 3 * D > 0x7fffffffLL * 64) return HCLSM_ERR_SHAPE;
+  if (frames == 0 || N == 0) return 0;
+  if (!slots_t1 || !perm || !hidden_t || !matched || !reordered || !hidden_t1 || !params || !workspace)
+    return HCLSM_ERR_NULL;
+  if (!params[0] || !params[1]) return HCLSM_ERR_NULL;
+  if (workspace_bytes < hclsm_slot_track_reorder_update_workspace(frames, N, D, dtype)) return HCLSM_ERR_SHAPE;
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t R = frames * N;
+  char* ws = reinterpret_cast<char*>(workspace);
+  float* GI = reinterpret_cast<float*>(ws);
+  float* GH = reinterpret_cast<float*>(ws + al256t((size_t)R * 3 * D * 4));
+  const float* b_ih = reinterpret_cast<const float*>(params[2]);
+  const float* b_hh = reinterpret_cast<const float*>(params[3]);
+  hipLaunchKernelGGL((trk_gather_kernel<int64_t>), dim3(blocks256(R * D)), dim3(256), 0, st, slots_t1, perm,
+                     reordered, R, (int)N, (int)D);
+  HCLSM_LAUNCH_CHECK();
+  int rc;
+  if ((rc = linear_rows(reordered, D, HCLSM_F32, params[0], D, b_ih, nullptr, 0, GI, 3 * D, HCLSM_F32, R, 3 * D, D, 0,
+                        0, nullptr, nullptr, 0.f, nullptr, 0, nullptr, 1, dtype, st)))
+    return rc;
+  if ((rc = linear_rows(hidden_t, D, HCLSM_F32, params[1], D, b_hh, nullptr, 0, GH, 3 * D, HCLSM_F32, R, 3 * D, D, 0,
+                        0, nullptr, nullptr, 0.f, nullptr, 0, nullptr, 1, dtype, st)))
+    return rc;
+  hipLaunchKernelGGL(trk_gru_gate_kernel, dim3(blocks256(R * D)), dim3(256), 0, st, GI, (int64_t)N, nullptr,
+                     (int64_t)0, GH, matched, (int64_t)N, reordered, (int64_t)N, hidden_t, hidden_t1, frames, (int)N,
+                     (int)D);
+  HCLSM_LAUNCH_CHECK();
+  return 0;
+}
+
+extern "C" int64_t hclsm_slot_track_sequence_workspace(int64_t batch, int64_t T, int64_t N, int64_t D,
+                                                       int with_hidden, int dtype) {
+  if (batch < 0 || T < 0) return HCLSM_ERR_SHAPE;
+  const int c = track_check(N, D, dtype);
+  if (c) return c;
+  if (N > TRK_MAX_SLOTS) return HCLSM_ERR_UNSUPPORTED;
+  return (int64_t)seq_ws(batch, T, N, D, with_hidden != 0).total;
+}
+
+// params: the six match_mlp tensors, then hidden_gru.weight_ih, .weight_hh, .bias_ih, .bias_hh (only read
+// when hidden is wanted).
+extern "C" int hclsm_slot_track_sequence(const float* slots, const float* alive, float* tracked, float* alive_out,
+                                         int64_t* perm, float* matched, float* hidden, int64_t batch, int64_t T,
+                                         int64_t N, int64_t D, int64_t n_iters, float temperature,
+                                         const void* const* params, int dtype, void* workspace,
+                                         int64_t workspace_bytes, void* stream) {
+  if (batch < 0 || T < 0 || n_iters < 0) return HCLSM_ERR_SHAPE;
+  const int chk = track_check(N, D, dtype);
+  if (chk) return chk;
+  if (N > TRK_MAX_SLOTS) return HCLSM_ERR_UNSUPPORTED;
+  if (batch > 0x7fffffffLL || T > 0x7fffffffLL || n_iters > 0x7fffffffLL) return HCLSM_ERR_SHAPE;
+  if (batch * T * N * 3 * D > 0x7fffffffLL * 64) return HCLSM_ERR_SHAPE;
+  if (batch == 0 || T == 0 || N == 0) return 0;
+  if (!slots || !tracked || !params || !workspace) return HCLSM_ERR_NULL;
+  for (int i = 0; i < 6; ++i)
+    if (!params[i]) return HCLSM_ERR_NULL;
+  if (hidden && (!params[6] || !params[7])) return HCLSM_ERR_NULL;
+  const SeqWs L = seq_ws(batch, T, N, D, hidden != nullptr);
+  if (workspace_bytes < (int64_t)L.total) return HCLSM_ERR_SHAPE;
+  hipStream_t st = (hipStream_t)stream;
+  char* ws = reinterpret_cast<char*>(workspace);
+  float* S = reinterpret_cast<float*>(ws + L.s);
+  float* UV = reinterpret_cast<float*>(ws + L.uv);
+  float* C = reinterpret_cast<float*>(ws + L.c);
+  int* P = reinterpret_cast<int*>(ws + L.perm);
+  float* M = matched ? matched : reinterpret_cast<float*>(ws + L.matched);
+  const int64_t R = batch * T * N;
+  const int es = dtype == HCLSM_F32 ? 4 : 2;
+  int rc;
+  if (T > 1) {
+    // pair MLP over every (t-1, t) frame pair: U = W1a s + b1 and V = W1b s for every node row
+    if ((rc = clamp_rows(slots, S, R * D, st))) return rc;
+    const char* W1 = reinterpret_cast<const char*>(params[0]);
+    if ((rc = linear_rows(S, D, HCLSM_F32, W1, 3 * D, reinterpret_cast<const float*>(params[1]), nullptr, 0, UV,
+                          2 * D, HCLSM_F32, R, D, D, 0, 0, nullptr, nullptr, 0.f, nullptr, 0, nullptr, 1, dtype, st)))
+      return rc;
+    if ((rc = linear_rows(S, D, HCLSM_F32, W1 + (size_t)D * es, 3 * D, nullptr, nullptr, 0, UV + D, 2 * D, HCLSM_F32,
+                          R, D, D, 0, 0, nullptr, nullptr, 0.f, nullptr, 0, nullptr, 1, dtype, st)))
+      return rc;
+    TrackCostArgs a{};
+    a.S = S; a.UV = UV; a.W1 = params[0]; a.W2 = params[2];
+    a.b2 = reinterpret_cast<const float*>(params[3]);
+    a.w3 = reinterpret_cast<const float*>(params[4]);
+    a.b3 = reinterpret_cast<const float*>(params[5]);
+    a.alive_a = alive;
+    a.alive_b = alive;
+    a.boff = 0;
+    a.cost = C;
+    a.pairs = batch * (T - 1) * N * N;
+    a.N = (int)N; a.D = (int)D;
+    a.nt = (int)(T - 1); a.tstride = (int)T; a.fboff = 1;
+    if ((rc = launch_cost_dt(dtype, a, st))) return rc;
+  }
+  const float inv_t = inv_temperature(temperature);
+  rc = with_tile(N, [&](auto cpl, auto w) {
+    constexpr int CPL = decltype(cpl)::value, W = decltype(w)::value;
+    hipLaunchKernelGGL((track_sequence_kernel<CPL, W>), dim3((unsigned)batch), dim3(64 * W), 0, st, C, alive, P, perm,
+                       M, alive_out, (int)T, (int)N, (int)n_iters, inv_t);
+    HCLSM_LAUNCH_CHECK();
+    return 0;
+  });
+  if (rc) return rc;
+  hipLaunchKernelGGL((trk_gather_kernel<int>), dim3(blocks256(R * D)), dim3(256), 0, st, slots, P, tracked, R, (int)N,
+                     (int)D);
+  HCLSM_LAUNCH_CHECK();
+  if (!hidden) return 0;
+  // GRU carry (slot_tracker.py:150-156): hidden_0 = 0; for t >= 1 hidden_t = blend(GRU(tracked_t, hidden_{t-1}))
+  float* GI = reinterpret_cast<float*>(ws + L.gi);
+  float* GH = reinterpret_cast<float*>(ws + L.gh);
+  const float* b_ih = reinterpret_cast<const float*>(params[8]);
+  const float* b_hh = reinterpret_cast<const float*>(params[9]);
+  if ((rc = zero_fill_f32(hidden, batch * N * D, st))) return rc;
+  if (T < 2) return 0;
+  if ((rc = linear_rows(slots, D, HCLSM_F32, params[6], D, b_ih, nullptr, 0, GI, 3 * D, HCLSM_F32, R, 3 * D, D, 0, 0,
+                        nullptr, nullptr, 0.f, nullptr, 0, nullptr, 1, dtype, st)))
+    return rc;
+  const int64_t BN = batch * N;
+  for (int64_t t = 1; t < T; ++t) {
+    if ((rc = linear_rows(hidden, D, HCLSM_F32, params[7], D, b_hh, nullptr, 0, GH, 3 * D, HCLSM_F32, BN, 3 * D, D,
+                          0, 0, nullptr, nullptr, 0.f, nullptr, 0, nullptr, 1, dtype, st)))
+      return rc;
+    hipLaunchKernelGGL(trk_gru_gate_kernel, dim3(blocks256(BN * D)), dim3(256), 0, st, GI + t * N * 3 * D, T * N,
+                       P + t * N, T * N, GH, M + t * N, T * N, tracked + t * N * D, T * N, hidden, hidden, batch,
+                       (int)N, (int)D);
+    HCLSM_LAUNCH_CHECK();
+  }
+  return 0;
+}

@@ -1,7 +1,8 @@
 """Counterparts of the reference's hclsm/objects modules on the hot path (slot attention) and next to it
-(relation graph)."""
+(slot tracker, relation graph)."""
 
 from hclsm_amd.objects.dynamic_slots import DynamicSlotAttention
 from hclsm_amd.objects.relation_graph import RelationGraph
+from hclsm_amd.objects.slot_tracker import SlotTracker, sinkhorn_matching
 
-__all__ = ["DynamicSlotAttention", "RelationGraph"]
+__all__ = ["DynamicSlotAttention", "RelationGraph", "SlotTracker", "sinkhorn_matching"]

@@ -354,6 +354,77 @@ int hclsm_relation_graph_forward(const float* nodes, const float* alive, float* 
                                  const void* const* params, float ln_eps, int dtype, void* workspace,
                                  int64_t workspace_bytes, void* stream);
 
+/* ---- slot tracker (hclsm/objects/slot_tracker.py, tracking loop of hclsm/model.py:229-252) ----
+ * Shapes: D (d_slot) a multiple of 64 and at most 384; the Sinkhorn entries N <= 128.  The workspace
+ * queries return HCLSM_ERR_UNSUPPORTED outside these.  Slots, alive flags, costs and hidden states are
+ * float32; match_mlp.0.weight [D, 3D], match_mlp.2.weight [D/4, D], hidden_gru.weight_ih / weight_hh
+ * [3D, D] in `dtype` (F32 / BF16 / F16); biases and match_mlp.4.weight [D/4] float32. */
+
+/* Workspace bytes for hclsm_slot_track_cost. */
+int64_t hclsm_slot_track_cost_workspace(int64_t frames, int64_t N, int64_t D, int dtype);
+
+/*
+ * Matching cost between frames t and t1 for `frames` frame pairs of N slots:
+ *   cost_ij = -(w3 . ReLU(W2 ReLU(W1 [a_i; b_j; |a_i - b_j|] + b1) + b2) + b3
+ *              - 1e4 [alive_t_i < 0.5] - 1e4 [alive_t1_j < 0.5]),  a, b = slots clamped to [-50, 50].
+ * slots_t, slots_t1 [frames, N, D]; alive_t, alive_t1 [frames, N] (both NULL: no penalties); cost
+ * [frames, N, N] (not clamped).  params: 6 device pointers match_mlp.0.weight, .0.bias, .2.weight,
+ * .2.bias, .4.weight, .4.bias.
+ * Replaces: SlotTracker.compute_cost_matrix (hclsm/objects/slot_tracker.py:74-107).
+ */
+int hclsm_slot_track_cost(const float* slots_t, const float* slots_t1, const float* alive_t, const float* alive_t1,
+                          float* cost, int64_t frames, int64_t N, int64_t D, const void* const* params, int dtype,
+                          void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Sinkhorn matching of `frames` N x N costs: log_alpha = -clamp(cost, -1e4, 1e4) * (1 / max(temperature,
+ * 1e-6)), n_iters rounds of row then column log-sum-exp normalisation; perm [frames, N] int64 = argmax over
+ * j of exp(log_alpha) (lowest index on ties), confidence [frames, N] (nullable) its value, matched
+ * [frames, N] = [alive_t_i > 0.5] [alive_t1_perm_i > 0.5] [confidence > 0.3] (alive pointers nullable:
+ * alive).  No workspace.  N <= 128.
+ * Replaces: SlotTracker.forward after the cost (slot_tracker.py:122-135) and _sinkhorn_matching (:15-43).
+ */
+int hclsm_slot_track_match(const float* cost, const float* alive_t, const float* alive_t1, int64_t* perm,
+                           float* matched, float* confidence, int64_t frames, int64_t N, int64_t n_iters,
+                           float temperature, void* stream);
+
+/* Workspace bytes for hclsm_slot_track_reorder_update. */
+int64_t hclsm_slot_track_reorder_update_workspace(int64_t frames, int64_t N, int64_t D, int dtype);
+
+/*
+ * reordered[f, i] = slots_t1[f, perm[f, i]] (an index outside [0, N) gives a NaN row);
+ * hidden_t1 = m * GRUCell(reordered, hidden_t) + (1 - m) * reordered, m = matched[f, i].
+ * slots_t1, hidden_t, reordered, hidden_t1 [frames, N, D]; perm [frames, N] int64; matched [frames, N].
+ * params: 4 device pointers hidden_gru.weight_ih, .weight_hh, .bias_ih, .bias_hh (biases nullable).
+ * Replaces: SlotTracker.reorder_and_update (slot_tracker.py:137-158).
+ */
+int hclsm_slot_track_reorder_update(const float* slots_t1, const int64_t* perm, const float* hidden_t,
+                                    const float* matched, float* reordered, float* hidden_t1, int64_t frames,
+                                    int64_t N, int64_t D, const void* const* params, int dtype, void* workspace,
+                                    int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes for hclsm_slot_track_sequence (with_hidden != 0: room for the GRU carry). */
+int64_t hclsm_slot_track_sequence_workspace(int64_t batch, int64_t T, int64_t N, int64_t D, int with_hidden,
+                                            int dtype);
+
+/*
+ * The tracking loop over `batch` clips of T frames: frame 0 is kept; for t >= 1 the tracked slots of frame
+ * t-1 are matched against frame t (cost, Sinkhorn with n_iters / temperature, as the two entries above),
+ * frame t's slots and alive flags are reordered by the perm, and, when hidden is non-NULL, the GRU state
+ * is carried (hidden_0 = 0, blend as hclsm_slot_track_reorder_update).
+ * slots, tracked [batch, T, N, D]; alive, alive_out [batch, T, N] (nullable: all alive / not written);
+ * perm [batch, T, N] int64 and matched [batch, T, N] (nullable; frame 0: identity and 0); hidden
+ * [batch, N, D] (nullable), the state after the last frame.  params: 10 device pointers, the six of
+ * hclsm_slot_track_cost then the four of hclsm_slot_track_reorder_update (those only read when hidden is
+ * wanted).  The matching costs of every (t-1, t) frame pair are computed in one launch (the previous perm
+ * only reorders cost rows); one workgroup per clip runs the Sinkhorn steps in sequence.
+ * Replaces: the frame loop of HCLSMWorldModel.forward (hclsm/model.py:229-252) over self.slot_tracker.
+ */
+int hclsm_slot_track_sequence(const float* slots, const float* alive, float* tracked, float* alive_out,
+                              int64_t* perm, float* matched, float* hidden, int64_t batch, int64_t T, int64_t N,
+                              int64_t D, int64_t n_iters, float temperature, const void* const* params, int dtype,
+                              void* workspace, int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -98,3 +98,30 @@ def test_level1_forward_argument_errors_before_launch(lib):
     assert call(ds=48) == -4                 # d_slot not a multiple of 32 for 16-bit operands
     assert call() == -1                      # NULL pointers
     assert call(cap=0) == 0                  # nothing to do
+
+
+def test_slot_tracker_argument_errors_before_launch(lib):
+    assert lib.hclsm_slot_track_cost_workspace(-1, 32, 192, 1) == -2
+    assert lib.hclsm_slot_track_cost_workspace(2, 32, 96, 1) == -4       # d_slot not a multiple of 64
+    assert lib.hclsm_slot_track_cost_workspace(2, 32, 448, 0) == -4      # d_slot above 384
+    assert lib.hclsm_slot_track_cost_workspace(2, 32, 192, 9) == -3
+    assert lib.hclsm_slot_track_cost_workspace(2, 200, 192, 1) > 0        # the pair MLP has no slot limit
+    assert lib.hclsm_slot_track_sequence_workspace(2, 8, 129, 192, 0, 1) == -4   # Sinkhorn: N <= 128
+    assert lib.hclsm_slot_track_sequence_workspace(2, 8, 128, 192, 1, 1) > \
+        lib.hclsm_slot_track_sequence_workspace(2, 8, 128, 192, 0, 1)              # room for the GRU carry
+    f = lib.hclsm_slot_track_cost
+    assert f(None, None, None, None, None, 2, 32, 192, None, 1, None, 0, None) == -1
+    assert f(None, None, None, None, None, 0, 32, 192, None, 1, None, 0, None) == 0
+    assert f(None, None, None, None, None, 2, 32, 100, None, 1, None, 0, None) == -4
+    m = lib.hclsm_slot_track_match
+    assert m(None, None, None, None, None, None, 2, 129, 20, 0.05, None) == -4
+    assert m(None, None, None, None, None, None, 2, 32, -1, 0.05, None) == -2
+    assert m(None, None, None, None, None, None, 2, 32, 20, 0.05, None) == -1
+    assert m(None, None, None, None, None, None, 0, 32, 20, 0.05, None) == 0
+    s = lib.hclsm_slot_track_sequence
+    assert s(*[None] * 7, 2, 8, 32, 192, 20, 0.05, None, 1, None, 0, None) == -1
+    assert s(*[None] * 7, 2, 8, 32, 192, -1, 0.05, None, 1, None, 0, None) == -2
+    assert s(*[None] * 7, 2, 0, 32, 192, 20, 0.05, None, 1, None, 0, None) == 0
+    r = lib.hclsm_slot_track_reorder_update
+    assert r(*[None] * 6, 2, 32, 192, None, 1, None, 0, None) == -1
+    assert r(*[None] * 6, 2, 32, 64, None, 5, None, 0, None) == -3

@@ -14,11 +14,13 @@ def _reference_shaped_model_state(seed=0):
     """A model state dict with the reference's key layout for the hot-path modules (plus unrelated
     entries that must be ignored), from freshly initialised modules of the tiny preset."""
     from hclsm_amd.dynamics import HierarchyManager, Level0SSM, Level1EventDynamics
-    from hclsm_amd.objects import DynamicSlotAttention
+    from hclsm_amd.objects import DynamicSlotAttention, RelationGraph, SlotTracker
     torch.manual_seed(seed)
     cfg = preset_config("tiny")
     mods = {"slot_attention": DynamicSlotAttention(cfg.objects, cfg.d_world),
             "target_slot_attention": DynamicSlotAttention(cfg.objects, cfg.d_world),
+            "slot_tracker": SlotTracker(cfg.objects),
+            "relation_graph": RelationGraph(cfg.objects),
             "level0_ssm": Level0SSM(cfg.dynamics.level0, cfg.objects.d_slot),
             "level1_event": Level1EventDynamics(cfg.dynamics.level1, cfg.objects.d_slot),
             "hierarchy_manager": HierarchyManager(cfg.objects.d_slot, cfg.dynamics.level2.d_model)}
@@ -41,7 +43,8 @@ def test_build_hot_path_from_reference_checkpoint(tmp_path):
     path = tmp_path / "step_7.pt"
     torch.save(_checkpoint(state), path)
     mods = build_hot_path(path, cfg, device="cpu", with_target=True)
-    assert set(mods) == {"slot_attention", "target_slot_attention", "level0_ssm", "level1_event", "hierarchy_manager"}
+    assert set(mods) == {"slot_attention", "target_slot_attention", "slot_tracker", "relation_graph", "level0_ssm",
+                         "level1_event", "hierarchy_manager"}
     for name, m in mods.items():
         for k, v in m.state_dict().items():
             assert torch.equal(v, state[f"{name}.{k}"]), f"{name}.{k}"

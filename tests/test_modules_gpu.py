@@ -288,8 +288,10 @@ def test_hot_path_from_reference_checkpoint_matches_oracle(tmp_path):
     src = {"level0_ssm": Level0SSM(cfg.dynamics.level0, D_SLOT),
            "level1_event": Level1EventDynamics(cfg.dynamics.level1, D_SLOT),
            "hierarchy_manager": HierarchyManager(D_SLOT, cfg.dynamics.level2.d_model)}
-    from hclsm_amd.objects import DynamicSlotAttention
+    from hclsm_amd.objects import DynamicSlotAttention, RelationGraph, SlotTracker
     src["slot_attention"] = DynamicSlotAttention(cfg.objects, cfg.d_world)
+    src["slot_tracker"] = SlotTracker(cfg.objects)
+    src["relation_graph"] = RelationGraph(cfg.objects)
     with torch.no_grad():      # trained-looking A_log: spread over the clamp's range
         for blk in list(src["level0_ssm"].object_blocks) + list(src["level0_ssm"].global_blocks):
             blk.A_log.uniform_(-3.0, 0.5)
@@ -317,3 +319,15 @@ def test_hot_path_from_reference_checkpoint_matches_oracle(tmp_path):
                          {k: _np(v) for k, v in module_state(sd, "level1_event").items()},
                          cfg.dynamics.level1.n_layers, cfg.dynamics.level1.n_heads)
     assert normwise_rel_err(_np(out1[:6]).reshape(B, 3, N, D_SLOT), ref1) <= 1e-5
+    # object layer: tracker cost and relation graph with the checkpoint's weights
+    from oracle import objects as ob
+    a, b = torch.randn(B, N, D_SLOT, device="cuda"), torch.randn(B, N, D_SLOT, device="cuda")
+    al = torch.ones(B, N, device="cuda")
+    with torch.no_grad():
+        cost = mods["slot_tracker"].compute_cost_matrix(a, b, al, al)
+        nodes, causal = mods["relation_graph"](a, al)
+    pt = {k: _np(v) for k, v in module_state(sd, "slot_tracker").items()}
+    assert normwise_rel_err(_np(cost), ob.tracker_cost_ref(_np(a), _np(b), _np(al), _np(al), pt)) <= 1e-5
+    pg = {k: _np(v) for k, v in module_state(sd, "relation_graph").items()}
+    rn, rc = ob.relation_graph_ref(_np(a), _np(al), pg, cfg.objects.gnn_rounds)
+    assert normwise_rel_err(_np(nodes), rn) <= 1e-5 and normwise_rel_err(_np(causal), rc) <= 1e-5
