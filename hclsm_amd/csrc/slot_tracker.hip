@@ -19,11 +19,9 @@
 //
 // Sinkhorn (slot_tracker.py:15-43): log_alpha = -clamp(cost, -1e4, 1e4) * (1 / temperature), then n_iters
 // rounds of log-sum-exp normalisation over rows, then over columns, updated in place; perm = argmax over j
-// of exp(log_alpha) (lowest index on ties), confidence = that maximum.  A frame's matrix stays in
-// registers: each wave holds 32 rows, lane 8 rg + cg holds rows rg + 8r (r < 4) x columns cg + 8c
-// (c < CPL).  Row reductions run over the 8 lanes of a row group (DPP), column reductions over the 8 row
-// groups of the wave (DPP row rotate and the two permlane swaps) and, for N > 32, across the waves through
-// LDS, merging (max, sum) pairs.
+// of exp(log_alpha) (lowest index on ties), confidence = that maximum.  A frame's log_alpha lives in LDS
+// and is normalised in place; each half-step gives every lane CPL entries of one row (or column) and
+// reduces them in the lane and over the line's 8 lanes with DPP, one barrier between half-steps.
 #include "internal.h"
 #include "pair_tile.h"
 
@@ -156,6 +154,175 @@ track_cost_kernel(TrackCostArgs a) {
   }
 }
 
+// Weight-resident variant for 16-bit operands and D <= 192 (the pair tiles of the tiny and small presets):
+// a persistent workgroup stages W1c and W2 in LDS once, then walks blocks of 32 NW pairs.  The MFMAs take
+// the weights as the A operand and the pairs as the B operand, so lane (g, li) of a 16-output tile holds
+// outputs 4g .. 4g+3 of pair li: the U / V epilogue reads float4s, and the first layer's accumulators are,
+// without leaving registers, the second layer's B operand, with W2's columns stored in the matching order
+// (positions 8g .. 8g+7 of a 32-wide block hold k = 4g .. 4g+3 and 16 + 4g .. 16 + 4g+3).  Two 16-pair
+// tiles per wave share each weight fragment read from LDS.
+template <int DT, int D, int NW>
+__global__ void __launch_bounds__(64 * NW)
+track_cost_res_kernel(TrackCostArgs a) {
+  using A = MM<DT>;
+  using T = typename A::T;
+  static_assert(DT != HCLSM_F32 && D % 64 == 0 && D <= 192, "16-bit operands, D a multiple of 64 up to 192");
+  constexpr int NTH = 64 * NW, PT = 2, BLK = 16 * PT * NW;
+  constexpr int D4 = D / 4, PW = D + 8, NT = D / 16, NT2 = D4 / 16, NKB = D / 32;
+  extern __shared__ __align__(16) unsigned char smem[];
+  T* sW1 = reinterpret_cast<T*>(smem);                 // [D][PW] W1c, natural k order
+  T* sW2 = sW1 + D * PW;                               // [D4][PW] W2, k permuted within 32-wide blocks
+  float* sb2 = reinterpret_cast<float*>(sW2 + D4 * PW);
+  float* sw3 = sb2 + D4;
+  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, g = lane >> 4, li = lane & 15;
+  {
+    const T* W1 = reinterpret_cast<const T*>(a.W1);
+    for (int u = tid; u < D * (D / 8); u += NTH) {
+      const int r = u / (D / 8), c = (u - r * (D / 8)) * 8;
+      *reinterpret_cast<uint4*>(sW1 + r * PW + c) = *reinterpret_cast<const uint4*>(W1 + (size_t)r * 3 * D + 2 * D + c);
+    }
+    const T* W2 = reinterpret_cast<const T*>(a.W2);
+    for (int u = tid; u < D4 * (D / 8); u += NTH) {
+      const int r = u / (D / 8), q = (u - r * (D / 8)) * 8;
+      const int kb = q & ~31, gg = (q & 31) >> 3;
+      const uint2 lo = *reinterpret_cast<const uint2*>(W2 + (size_t)r * D + kb + 4 * gg);
+      const uint2 hi = *reinterpret_cast<const uint2*>(W2 + (size_t)r * D + kb + 16 + 4 * gg);
+      *reinterpret_cast<uint4*>(sW2 + r * PW + q) = make_uint4(lo.x, lo.y, hi.x, hi.y);
+    }
+    for (int u = tid; u < D4; u += NTH) {
+      sb2[u] = a.b2[u];
+      sw3[u] = a.w3[u];
+    }
+  }
+  __syncthreads();
+  const int N = a.N;
+  const int64_t NN = (int64_t)N * N;
+  auto nodes_of = [&](int64_t p, int64_t& ra, int64_t& rb) {
+    p = p < a.pairs ? p : a.pairs - 1;
+    const int64_t f = p / NN;
+    const int rem = (int)(p - f * NN);
+    const int i = rem / N, j = rem - i * N;
+    const int64_t q = f / a.nt;
+    const int64_t fa = q * a.tstride + (f - q * a.nt);
+    ra = fa * N + i;
+    rb = (fa + a.fboff) * N + j;
+  };
+  const int64_t nblk = (a.pairs + BLK - 1) / BLK;
+  for (int64_t blk = blockIdx.x; blk < nblk; blk += gridDim.x) {
+    const int64_t pw = blk * BLK + (int64_t)wid * 16 * PT;
+    int64_t ra[PT], rb[PT];
+#pragma unroll
+    for (int pt = 0; pt < PT; ++pt) nodes_of(pw + 16 * pt + li, ra[pt], rb[pt]);
+    // ---- first layer: acc[pt][t] = W1c rows 16t.. x |a - b| of the tile's pairs
+    f32x4 acc[PT][NT];
+#pragma unroll
+    for (int pt = 0; pt < PT; ++pt)
+#pragma unroll
+      for (int t = 0; t < NT; ++t) acc[pt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // raw rows of the next k-block are loaded while the current one is multiplied
+    float4 xr[PT][4];
+    auto load_k = [&](int kb) {
+#pragma unroll
+      for (int pt = 0; pt < PT; ++pt) {
+        const float* xa = a.S + ra[pt] * D + kb + 8 * g;
+        const float* xb = a.S + rb[pt] * D + kb + 8 * g;
+        xr[pt][0] = *reinterpret_cast<const float4*>(xa);
+        xr[pt][1] = *reinterpret_cast<const float4*>(xa + 4);
+        xr[pt][2] = *reinterpret_cast<const float4*>(xb);
+        xr[pt][3] = *reinterpret_cast<const float4*>(xb + 4);
+      }
+    };
+    load_k(0);
+#pragma unroll 1
+    for (int kb = 0; kb < D; kb += 32) {
+      T op[PT][8];
+#pragma unroll
+      for (int pt = 0; pt < PT; ++pt) {
+        const float4 x0 = xr[pt][0], x1 = xr[pt][1], y0 = xr[pt][2], y1 = xr[pt][3];
+        op[pt][0] = A::fromf(fabsf(x0.x - y0.x)); op[pt][1] = A::fromf(fabsf(x0.y - y0.y));
+        op[pt][2] = A::fromf(fabsf(x0.z - y0.z)); op[pt][3] = A::fromf(fabsf(x0.w - y0.w));
+        op[pt][4] = A::fromf(fabsf(x1.x - y1.x)); op[pt][5] = A::fromf(fabsf(x1.y - y1.y));
+        op[pt][6] = A::fromf(fabsf(x1.z - y1.z)); op[pt][7] = A::fromf(fabsf(x1.w - y1.w));
+      }
+      if (kb + 32 < D) load_k(kb + 32);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        T wf[8];
+        frag_load<DT>(sW1 + (16 * t + li) * PW + kb + 8 * g, wf);
+#pragma unroll
+        for (int pt = 0; pt < PT; ++pt) acc[pt][t] = frag_mma<DT>(wf, op[pt], acc[pt][t]);
+      }
+    }
+    // ---- epilogue: h = ReLU(acc + U_i + V_j) for outputs 16t + 4g + rr of pair li
+    // (in groups of 3 tiles: the scheduler would otherwise hoist every load of the epilogue at once)
+#pragma unroll
+    for (int pt = 0; pt < PT; ++pt) {
+      const float* U = a.UV + ra[pt] * 2 * D + 4 * g;
+      const float* V = a.UV + rb[pt] * 2 * D + D + 4 * g;
+#pragma unroll
+      for (int t0 = 0; t0 < NT; t0 += 3) {
+#pragma unroll
+        for (int t = t0; t < t0 + 3 && t < NT; ++t) {
+          const float4 u4 = *reinterpret_cast<const float4*>(U + 16 * t);
+          const float4 v4 = *reinterpret_cast<const float4*>(V + 16 * t);
+          acc[pt][t][0] = fmaxf(acc[pt][t][0] + u4.x + v4.x, 0.f);
+          acc[pt][t][1] = fmaxf(acc[pt][t][1] + u4.y + v4.y, 0.f);
+          acc[pt][t][2] = fmaxf(acc[pt][t][2] + u4.z + v4.z, 0.f);
+          acc[pt][t][3] = fmaxf(acc[pt][t][3] + u4.w + v4.w, 0.f);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    // ---- second layer: k-block kb takes tiles 2kb (k = 32kb + 4g + e) and 2kb + 1 (32kb + 16 + 4g + e)
+    f32x4 acc2[PT][NT2];
+#pragma unroll
+    for (int pt = 0; pt < PT; ++pt)
+#pragma unroll
+      for (int t = 0; t < NT2; ++t) acc2[pt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      T hb[PT][8];
+#pragma unroll
+      for (int pt = 0; pt < PT; ++pt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          hb[pt][e] = A::fromf(acc[pt][2 * kb][e]);
+          hb[pt][4 + e] = A::fromf(acc[pt][2 * kb + 1][e]);
+        }
+#pragma unroll
+      for (int t = 0; t < NT2; ++t) {
+        T wf[8];
+        frag_load<DT>(sW2 + (16 * t + li) * PW + 32 * kb + 8 * g, wf);
+#pragma unroll
+        for (int pt = 0; pt < PT; ++pt) acc2[pt][t] = frag_mma<DT>(wf, hb[pt], acc2[pt][t]);
+      }
+    }
+    // ---- score of pair li: sum over the second layer's outputs 16t + 4g + rr, then over the 4 lane groups
+#pragma unroll
+    for (int pt = 0; pt < PT; ++pt) {
+      float part = 0.f;
+#pragma unroll
+      for (int t = 0; t < NT2; ++t)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int o = 16 * t + 4 * g + rr;
+          part = fmaf(fmaxf(acc2[pt][t][rr] + sb2[o], 0.f), sw3[o], part);
+        }
+      part += __shfl_xor(part, 16, 64);
+      part += __shfl_xor(part, 32, 64);
+      const int64_t p = pw + 16 * pt + li;
+      if (g == 0 && p < a.pairs) {
+        float s = part + a.b3[0];
+        if (a.alive_a) {
+          s = s - (a.alive_a[ra[pt]] < 0.5f ? TRK_PENALTY : 0.f);
+          s = s - (a.alive_b[rb[pt] - a.boff] < 0.5f ? TRK_PENALTY : 0.f);
+        }
+        a.cost[p] = -s;
+      }
+    }
+  }
+}
+
 // y[r, k] = clamp(x[r, k], -50, 50) (NaN passes through, as torch.clamp)
 __global__ void __launch_bounds__(256)
 trk_clamp_kernel(const float* __restrict__ x, float* __restrict__ y, int64_t n) {
@@ -175,128 +342,104 @@ __device__ __forceinline__ int dpp_i(int v) {
   return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, true);
 }
 
+// max(m, x) without fmaxf's quieting of the operands: NaN is not a value the matching has to order
+__device__ __forceinline__ float max_sel(float m, float x) { return x > m ? x : m; }
+
+// log-sum-exp of a reduced (max, sum of exp(x - max)); a row or column of padding (max -inf) gives 0 so that
+// it stays -inf.  The sum is at least 1: the hardware log2 needs no range handling.
+__device__ __forceinline__ float lse_of(float m, float s) {
+  return m == -INFINITY ? 0.f : fmaf(__builtin_amdgcn_logf(s), HCLSM_LN2, m);
+}
+
 // All-reduce over the 8 lanes of a row group (lane bits 0-2): quad xor 1, quad xor 2, half-row mirror.
-template <bool MAX>
-__device__ __forceinline__ float row_reduce(float v) {
-  if constexpr (MAX) {
-    v = fmaxf(v, dpp_f<0xb1>(v));
-    v = fmaxf(v, dpp_f<0x4e>(v));
-    return fmaxf(v, dpp_f<0x141>(v));
-  } else {
-    v += dpp_f<0xb1>(v);
-    v += dpp_f<0x4e>(v);
-    return v + dpp_f<0x141>(v);
-  }
+__device__ __forceinline__ float group_max(float v) {
+  v = max_sel(v, dpp_f<0xb1>(v));
+  v = max_sel(v, dpp_f<0x4e>(v));
+  return max_sel(v, dpp_f<0x141>(v));
+}
+__device__ __forceinline__ float group_sum(float v) {
+  v += dpp_f<0xb1>(v);
+  v += dpp_f<0x4e>(v);
+  return v + dpp_f<0x141>(v);
 }
 
-// All-reduce over the 8 row groups of a wave (lane bits 3-5): row rotate by 8 (xor 8 within 16 lanes),
-// then permlane16 and permlane32 swaps (each hands every lane its partner's value across the 16 / 32 split).
-template <bool MAX>
-__device__ __forceinline__ float col_reduce(float v) {
-  auto op = [](float x, float y) { return MAX ? fmaxf(x, y) : x + y; };
-  v = op(v, dpp_f<0x128>(v));
-  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = op(__uint_as_float(r[0]), __uint_as_float(r[1]));
-  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return op(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-
-__device__ __forceinline__ float lse_of(float m, float s) { return m == -INFINITY ? 0.f : m + __logf(s); }
-
-// n_iters rounds of row then column log-sum-exp normalisation of la in place.  W waves hold 32 rows each;
-// sred: [2][W][8 * CPL][2] floats of LDS (unused for W == 1).  Entries at -inf (padding) stay -inf.
-template <int CPL, int W>
-__device__ __forceinline__ void sinkhorn_regs(float (&la)[4][CPL], int n_iters, float* sred, int wid, int rg,
-                                              int cg) {
-  constexpr int NC = 8 * CPL;
-  for (int it = 0; it < n_iters; ++it) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float m = la[r][0];
-#pragma unroll
-      for (int c = 1; c < CPL; ++c) m = fmaxf(m, la[r][c]);
-      m = row_reduce<true>(m);
-      float s = 0.f;
-#pragma unroll
-      for (int c = 0; c < CPL; ++c) s += __expf(la[r][c] - m);
-      s = row_reduce<false>(s);
-      const float l = lse_of(m, s);
-#pragma unroll
-      for (int c = 0; c < CPL; ++c) la[r][c] -= l;
-    }
-    float cm[CPL], cs[CPL];
-#pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-      float m = fmaxf(fmaxf(la[0][c], la[1][c]), fmaxf(la[2][c], la[3][c]));
-      m = col_reduce<true>(m);
-      float s = 0.f;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) s += __expf(la[r][c] - m);
-      cm[c] = m;
-      cs[c] = col_reduce<false>(s);
-    }
-    if constexpr (W > 1) {
-      float* buf = sred + (size_t)(it & 1) * W * NC * 2;
-      if (rg == 0) {
-#pragma unroll
-        for (int c = 0; c < CPL; ++c) {
-          buf[(wid * NC + cg + 8 * c) * 2] = cm[c];
-          buf[(wid * NC + cg + 8 * c) * 2 + 1] = cs[c];
-        }
-      }
-      __syncthreads();
-#pragma unroll
-      for (int c = 0; c < CPL; ++c) {
-        float M = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < W; ++w) M = fmaxf(M, buf[(w * NC + cg + 8 * c) * 2]);
-        float S = 0.f;
-#pragma unroll
-        for (int w = 0; w < W; ++w) {
-          const float mw = buf[(w * NC + cg + 8 * c) * 2];
-          if (mw != -INFINITY) S = fmaf(buf[(w * NC + cg + 8 * c) * 2 + 1], __expf(mw - M), S);
-        }
-        cm[c] = M;
-        cs[c] = S;
-      }
-    }
-#pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-      const float l = lse_of(cm[c], cs[c]);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) la[r][c] -= l;
-    }
-  }
-}
-
-// Per row r: (max over j < N of exp(la), its lowest j) over the whole row, in every lane of the row group.
-// The index is always in [0, N): a row with no comparable entry (all NaN) gives index 0, value NaN.
+// The N x N log_alpha of one frame lives in LDS (sL, row pitch SkTile::P) and is normalised in place, as
+// the reference does.  W = CPL waves of 64 lanes; lane 8 rg + cg of wave w handles line w 8 + rg of the
+// half-step (a row in the row step, a column in the column step) and its CPL entries cg CPL + c, so both
+// reductions are CPL values in the lane plus three DPP steps over the 8 lanes of the line, with one
+// barrier between half-steps.  The pitch makes the column reads of a wave hit 64 (or 32) distinct banks.
 template <int CPL>
-__device__ __forceinline__ void argmax_regs(const float (&la)[4][CPL], int N, int cg, float (&bv)[4], int (&bi)[4]) {
+struct SkTile {
+  static constexpr int W = CPL, NC = 8 * CPL, NTH = 64 * CPL;
+  static constexpr int P = CPL == 2 ? NC + 4 : CPL == 4 ? NC + 2 : NC + 1;
+};
+
+template <int CPL>
+__device__ __forceinline__ void lse_line(float (&v)[CPL]) {
+  float m = v[0];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    float v = -1.f;
-    int id = 0;
+  for (int c = 1; c < CPL; ++c) m = max_sel(m, v[c]);
+  m = group_max(m);
+  float s = __expf(v[0] - m);
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-      const float e = expf(la[r][c]);
-      if (cg + 8 * c < N && e > v) {
-        v = e;
-        id = cg + 8 * c;
-      }
-    }
-    auto take = [&](float ov, int oi) {
-      if (ov > v || (ov == v && oi < id)) {
-        v = ov;
-        id = oi;
-      }
-    };
-    take(dpp_f<0xb1>(v), dpp_i<0xb1>(id));
-    take(dpp_f<0x4e>(v), dpp_i<0x4e>(id));
-    take(dpp_f<0x141>(v), dpp_i<0x141>(id));
-    bv[r] = v < 0.f ? __int_as_float(0x7fc00000) : v;
-    bi[r] = id;
+  for (int c = 1; c < CPL; ++c) s += __expf(v[c] - m);
+  s = group_sum(s);
+  const float l = lse_of(m, s);
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) v[c] -= l;
+}
+
+// n_iters rounds of row then column log-sum-exp normalisation of sL in place.  Entries at -inf (padding)
+// stay -inf.  Every thread of the workgroup calls it; sL must be complete (a barrier after its writes).
+template <int CPL>
+__device__ __forceinline__ void sinkhorn_lds(float* sL, int n_iters, int line, int cg) {
+  constexpr int P = SkTile<CPL>::P;
+  float v[CPL];
+  for (int it = 0; it < n_iters; ++it) {
+    float* r = sL + line * P + cg * CPL;          // row `line`, columns cg CPL + c
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) v[c] = r[c];
+    lse_line<CPL>(v);
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) r[c] = v[c];
+    __syncthreads();
+    float* k = sL + (cg * CPL) * P + line;        // column `line`, rows cg CPL + c
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) v[c] = k[c * P];
+    lse_line<CPL>(v);
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) k[c * P] = v[c];
+    __syncthreads();
   }
+}
+
+// Row `line`: (max over j < N of exp(log_alpha), its lowest j), in every lane of the row's group.  The index
+// is always in [0, N): a row with no comparable entry (all NaN) gives index 0, value NaN.
+template <int CPL>
+__device__ __forceinline__ void argmax_row(const float* sL, int N, int line, int cg, float& bv, int& bi) {
+  constexpr int P = SkTile<CPL>::P;
+  const float* r = sL + line * P + cg * CPL;
+  float v = -1.f;
+  int id = 0;
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const float e = expf(r[c]);
+    if (cg * CPL + c < N && e > v) {
+      v = e;
+      id = cg * CPL + c;
+    }
+  }
+  auto take = [&](float ov, int oi) {
+    if (ov > v || (ov == v && oi < id)) {
+      v = ov;
+      id = oi;
+    }
+  };
+  take(dpp_f<0xb1>(v), dpp_i<0xb1>(id));
+  take(dpp_f<0x4e>(v), dpp_i<0x4e>(id));
+  take(dpp_f<0x141>(v), dpp_i<0x141>(id));
+  bv = v < 0.f ? __int_as_float(0x7fc00000) : v;
+  bi = id;
 }
 
 // -log_alpha entry: clamp(cost, -1e4, 1e4) (NaN passes through), negated, times 1 / temperature
@@ -305,101 +448,102 @@ __device__ __forceinline__ float la_of(float c, float inv_t) {
   return -c * inv_t;
 }
 
-template <int CPL, int W>
-__device__ __forceinline__ void load_la(float (&la)[4][CPL], const float* cost, const int* src_row, int N,
-                                        float inv_t, int wid, int rg, int cg) {
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int i = 32 * wid + rg + 8 * r;
-    const float* row = i < N ? cost + (size_t)(src_row ? src_row[i] : i) * N : cost;
-#pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-      const int j = cg + 8 * c;
-      la[r][c] = (i < N && j < N) ? la_of(row[j], inv_t) : -INFINITY;
-    }
-  }
-}
-
 // SlotTracker.forward after the cost (slot_tracker.py:122-135) for one frame per workgroup.
-template <int CPL, int W>
-__global__ void __launch_bounds__(64 * W)
+template <int CPL>
+__global__ void __launch_bounds__(64 * CPL)
 track_match_kernel(const float* __restrict__ cost, const float* __restrict__ alive_a,
                    const float* __restrict__ alive_b, int64_t* __restrict__ perm, float* __restrict__ matched,
                    float* __restrict__ conf, int N, int n_iters, float inv_t) {
-  __shared__ float sred[W > 1 ? 2 * W * 8 * CPL * 2 : 1];
+  using S = SkTile<CPL>;
+  __shared__ float sL[S::NC * S::P];
   const int64_t f = blockIdx.x;
-  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, rg = lane >> 3, cg = lane & 7;
-  float la[4][CPL];
-  load_la<CPL, W>(la, cost + f * N * N, nullptr, N, inv_t, wid, rg, cg);
-  sinkhorn_regs<CPL, W>(la, n_iters, sred, wid, rg, cg);
-  float bv[4];
-  int bi[4];
-  argmax_regs<CPL>(la, N, cg, bv, bi);
-  if (cg == 0) {
+  const int tid = threadIdx.x, line = (tid >> 6) * 8 + ((tid & 63) >> 3), cg = tid & 7;
+  const float* cf = cost + f * N * N;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = 32 * wid + rg + 8 * r;
-      if (i < N) {
-        const int64_t o = f * N + i;
-        const float at = alive_a ? (alive_a[o] > 0.5f ? 1.f : 0.f) : 1.f;
-        const float at1 = alive_b ? (alive_b[f * N + bi[r]] > 0.5f ? 1.f : 0.f) : 1.f;
-        perm[o] = bi[r];
-        matched[o] = at * at1 * (bv[r] > 0.3f ? 1.f : 0.f);
-        if (conf) conf[o] = bv[r];
-      }
-    }
+  for (int c = 0; c < CPL; ++c) {
+    const int j = cg * CPL + c;
+    sL[line * S::P + j] = (line < N && j < N) ? la_of(cf[(size_t)line * N + j], inv_t) : -INFINITY;
+  }
+  __syncthreads();
+  sinkhorn_lds<CPL>(sL, n_iters, line, cg);
+  float bv;
+  int bi;
+  argmax_row<CPL>(sL, N, line, cg, bv, bi);
+  if (cg == 0 && line < N) {
+    const int64_t o = f * N + line;
+    const float at = alive_a ? (alive_a[o] > 0.5f ? 1.f : 0.f) : 1.f;
+    const float at1 = alive_b ? (alive_b[f * N + bi] > 0.5f ? 1.f : 0.f) : 1.f;
+    perm[o] = bi;
+    matched[o] = at * at1 * (bv > 0.3f ? 1.f : 0.f);
+    if (conf) conf[o] = bv;
   }
 }
 
 // The matching half of the tracking loop (model.py:233-252) for one clip per workgroup.  C: cost between
 // the unpermuted frames t-1 and t, [clip][T-1][N][N]; alive [clip][T][N] (null: all alive).  Writes, for
 // t >= 1, perm32 / perm64 / matched / alive_out at [clip][t][i] (t = 0: identity, 0, alive of frame 0).
-template <int CPL, int W>
-__global__ void __launch_bounds__(64 * W)
+// The next frame pair's cost block is loaded into registers while the current step runs.
+template <int CPL>
+__global__ void __launch_bounds__(64 * CPL)
 track_sequence_kernel(const float* __restrict__ C, const float* __restrict__ alive, int* __restrict__ perm32,
                       int64_t* __restrict__ perm64, float* __restrict__ matched, float* __restrict__ alive_out,
                       int T, int N, int n_iters, float inv_t) {
-  __shared__ float sred[W > 1 ? 2 * W * 8 * CPL * 2 : 1];
-  __shared__ int sperm[32 * W];      // perm of the previous step (rows of the tracked frame t-1)
-  __shared__ float salive[32 * W];   // alive of the tracked frame t-1
+  using S = SkTile<CPL>;
+  constexpr int NC = S::NC, P = S::P;
+  __shared__ float sL[NC * P];     // log_alpha of the current step
+  __shared__ float sC[NC * P];     // cost block of the current frame pair (rows of the unpermuted frame)
+  __shared__ int sperm[NC];        // perm of the previous step (rows of the tracked frame t-1)
+  __shared__ float salive[NC];     // alive of the tracked frame t-1
   const int64_t b = blockIdx.x;
-  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, rg = lane >> 3, cg = lane & 7;
+  const int tid = threadIdx.x, line = (tid >> 6) * 8 + ((tid & 63) >> 3), cg = tid & 7;
   const int64_t base = b * T * N;
-  for (int i = tid; i < N; i += 64 * W) {
-    const float al = alive ? alive[base + i] : 1.f;
-    sperm[i] = i;
-    salive[i] = al;
-    perm32[base + i] = i;
-    if (perm64) perm64[base + i] = i;
-    matched[base + i] = 0.f;
-    if (alive_out) alive_out[base + i] = al;
+  if (cg == 0 && line < N) {
+    const float al = alive ? alive[base + line] : 1.f;
+    sperm[line] = line;
+    salive[line] = al;
+    perm32[base + line] = line;
+    if (perm64) perm64[base + line] = line;
+    matched[base + line] = 0.f;
+    if (alive_out) alive_out[base + line] = al;
   }
-  __syncthreads();
-  for (int t = 1; t < T; ++t) {
-    float la[4][CPL];
-    load_la<CPL, W>(la, C + ((size_t)b * (T - 1) + (t - 1)) * N * N, sperm, N, inv_t, wid, rg, cg);
-    sinkhorn_regs<CPL, W>(la, n_iters, sred, wid, rg, cg);
-    float bv[4];
-    int bi[4];
-    argmax_regs<CPL>(la, N, cg, bv, bi);
-    __syncthreads();   // every lane has read sperm
-    if (cg == 0) {
-      const int64_t o = base + (int64_t)t * N;
+  // this thread's slice of a cost block: row `line`, columns cg CPL + c
+  float pf[CPL];
+  auto prefetch = [&](int t) {
+    const float* ct = C + (((size_t)b * (T - 1) + (t - 1)) * N + (line < N ? line : 0)) * N;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = 32 * wid + rg + 8 * r;
-        if (i < N) {
-          const float a1 = alive ? alive[o + bi[r]] : 1.f;
-          perm32[o + i] = bi[r];
-          if (perm64) perm64[o + i] = bi[r];
-          matched[o + i] = (salive[i] > 0.5f ? 1.f : 0.f) * (a1 > 0.5f ? 1.f : 0.f) * (bv[r] > 0.3f ? 1.f : 0.f);
-          if (alive_out) alive_out[o + i] = a1;
-          salive[i] = a1;
-          sperm[i] = bi[r];
-        }
-      }
+    for (int c = 0; c < CPL; ++c) {
+      const int j = cg * CPL + c;
+      pf[c] = (line < N && j < N) ? ct[j] : 0.f;
+    }
+  };
+  if (T > 1) prefetch(1);
+  for (int t = 1; t < T; ++t) {
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) sC[line * P + cg * CPL + c] = pf[c];
+    __syncthreads();   // sC complete; the previous step's sperm / salive updates visible
+    if (t + 1 < T) prefetch(t + 1);
+    const float* src = sC + (line < N ? sperm[line] : 0) * P;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const int j = cg * CPL + c;
+      sL[line * P + j] = (line < N && j < N) ? la_of(src[j], inv_t) : -INFINITY;
     }
     __syncthreads();
+    sinkhorn_lds<CPL>(sL, n_iters, line, cg);
+    float bv;
+    int bi;
+    argmax_row<CPL>(sL, N, line, cg, bv, bi);
+    __syncthreads();   // every lane has read sperm, sC and sL
+    if (cg == 0 && line < N) {
+      const int64_t o = base + (int64_t)t * N;
+      const float a1 = alive ? alive[o + bi] : 1.f;
+      perm32[o + line] = bi;
+      if (perm64) perm64[o + line] = bi;
+      matched[o + line] = (salive[line] > 0.5f ? 1.f : 0.f) * (a1 > 0.5f ? 1.f : 0.f) * (bv > 0.3f ? 1.f : 0.f);
+      if (alive_out) alive_out[o + line] = a1;
+      salive[line] = a1;
+      sperm[line] = bi;
+    }
   }
 }
 
@@ -470,14 +614,41 @@ static int launch_cost_kc(const TrackCostArgs& a, hipStream_t st) {
   return 0;
 }
 
-// 16-bit operands: 128 pairs per workgroup, weight chunks of 64 columns (32 when the LDS would overflow);
-// fp32: 64 pairs, chunks of 16.
+template <int DT, int D, int NW>
+static int launch_cost_res(const TrackCostArgs& a, hipStream_t st) {
+  using T = typename MM<DT>::T;
+  constexpr size_t lds = ((size_t)D * (D + 8) + (size_t)(D / 4) * (D + 8)) * sizeof(T) + (size_t)(D / 4) * 8;
+  static int grid = 0;   // resident workgroups on the device (persistent kernel), found once
+  if (grid == 0) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&track_cost_res_kernel<DT, D, NW>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)TRK_LDS_MAX);
+    if (e != hipSuccess) return (int)e;
+    int dev = 0, cus = 0, per_cu = 0;
+    if ((e = hipGetDevice(&dev)) != hipSuccess) return (int)e;
+    if ((e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return (int)e;
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(
+                                                         &track_cost_res_kernel<DT, D, NW>), 64 * NW, lds);
+    if (e != hipSuccess) return (int)e;
+    grid = cus * (per_cu > 0 ? per_cu : 1);
+  }
+  const int64_t nblk = (a.pairs + 32 * NW - 1) / (32 * NW);
+  const unsigned g = (unsigned)(nblk < grid ? nblk : grid);
+  hipLaunchKernelGGL((track_cost_res_kernel<DT, D, NW>), dim3(g), dim3(64 * NW), lds, st, a);
+  HCLSM_LAUNCH_CHECK();
+  return 0;
+}
+
+// 16-bit operands: the weight-resident kernel for D <= 192; otherwise 128 pairs per workgroup with weight
+// chunks of 64 columns (32 when the LDS would overflow).  fp32: 64 pairs, chunks of 16.
 template <int DT>
 static int launch_cost(const TrackCostArgs& a, hipStream_t st) {
   if (a.pairs == 0) return 0;
   if constexpr (DT == HCLSM_F32) {
     return launch_cost_kc<DT, 4, 16>(a, st);
   } else {
+    if (a.D == 64) return launch_cost_res<DT, 64, 8>(a, st);
+    if (a.D == 128) return launch_cost_res<DT, 128, 8>(a, st);
+    if (a.D == 192) return launch_cost_res<DT, 192, 8>(a, st);
     if (cost_lds<DT, 8, 64>(a.D) <= TRK_LDS_MAX) return launch_cost_kc<DT, 8, 64>(a, st);
     return launch_cost_kc<DT, 8, 32>(a, st);
   }
@@ -498,13 +669,14 @@ static int clamp_rows(const float* x, float* y, int64_t n, hipStream_t st) {
   return 0;
 }
 
-// Sinkhorn tile shape for N: (columns per lane, waves)
+// Sinkhorn tile for N: CPL columns per lane and CPL waves (8 CPL >= N)
 template <typename F>
 static int with_tile(int64_t N, F&& fn) {
-  if (N <= 16) return fn(std::integral_constant<int, 2>{}, std::integral_constant<int, 1>{});
-  if (N <= 32) return fn(std::integral_constant<int, 4>{}, std::integral_constant<int, 1>{});
-  if (N <= 64) return fn(std::integral_constant<int, 8>{}, std::integral_constant<int, 2>{});
-  return fn(std::integral_constant<int, 16>{}, std::integral_constant<int, 4>{});
+  using std::integral_constant;
+  if (N <= 16) return fn(integral_constant<int, 2>{});
+  if (N <= 32) return fn(integral_constant<int, 4>{});
+  if (N <= 64) return fn(integral_constant<int, 8>{});
+  return fn(integral_constant<int, 16>{});
 }
 
 constexpr int64_t TRK_MAX_SLOTS = 128;
@@ -615,9 +787,9 @@ extern "C" int hclsm_slot_track_match(const float* cost, const float* alive_t, c
   if (!cost || !perm || !matched) return HCLSM_ERR_NULL;
   hipStream_t st = (hipStream_t)stream;
   const float inv_t = inv_temperature(temperature);
-  return with_tile(N, [&](auto cpl, auto w) {
-    constexpr int CPL = decltype(cpl)::value, W = decltype(w)::value;
-    hipLaunchKernelGGL((track_match_kernel<CPL, W>), dim3((unsigned)frames), dim3(64 * W), 0, st, cost, alive_t,
+  return with_tile(N, [&](auto cpl) {
+    constexpr int CPL = decltype(cpl)::value;
+    hipLaunchKernelGGL((track_match_kernel<CPL>), dim3((unsigned)frames), dim3(64 * CPL), 0, st, cost, alive_t,
                        alive_t1, perm, matched, confidence, (int)N, (int)n_iters, inv_t);
     HCLSM_LAUNCH_CHECK();
     return 0;
@@ -733,9 +905,9 @@ extern "C" int hclsm_slot_track_sequence(const float* slots, const float* alive,
     if ((rc = launch_cost_dt(dtype, a, st))) return rc;
   }
   const float inv_t = inv_temperature(temperature);
-  rc = with_tile(N, [&](auto cpl, auto w) {
-    constexpr int CPL = decltype(cpl)::value, W = decltype(w)::value;
-    hipLaunchKernelGGL((track_sequence_kernel<CPL, W>), dim3((unsigned)batch), dim3(64 * W), 0, st, C, alive, P, perm,
+  rc = with_tile(N, [&](auto cpl) {
+    constexpr int CPL = decltype(cpl)::value;
+    hipLaunchKernelGGL((track_sequence_kernel<CPL>), dim3((unsigned)batch), dim3(64 * CPL), 0, st, C, alive, P, perm,
                        M, alive_out, (int)T, (int)N, (int)n_iters, inv_t);
     HCLSM_LAUNCH_CHECK();
     return 0;
