@@ -260,6 +260,348 @@ gnn_edge_kernel(GnnArgs a) {
   }
 }
 
+// Weight-resident edge kernel for 16-bit operands at the preset shapes (D, E) = (64, 32), (128, 64), (192, 96).
+// A persistent workgroup stages A4, W2 and Wm (messages) and / or C1 (causal head) in LDS once; each wave then
+// owns whole source rows i (frame f), 32 targets j per chunk as two 16-pair MFMA tiles.
+//   A  A4 (n_i * n_j) with the weights as the A operand: lane (g, li) holds outputs 4g .. 4g+3 of each
+//      16-wide tile for pair li, so the pair statistics, P_i + Q_j and the normalisation stay in the lane.
+//   B  W2 H1: H1 is the B operand straight from A's accumulators (W2's columns stored in the matching order:
+//      positions 8g .. 8g+7 of a 32-wide block hold k = 4g .. 4g+3 and 16 + 4g .. 16 + 4g+3); edge weight.
+//   C  messages with the edge features as the A operand (pairs as rows), so the sum over j is four pairs in
+//      the lane, then the two tiles, then over the lane groups; Wm's columns in the same order as W2's.
+//   D  causal head with C1 as the A operand, the score reduced over the lane groups.
+// Node sums s, q come precomputed (nstat); only g = sum n_i n_j and h = sum (n_i n_j)^2 are per pair.
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(T lo, T hi) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+}
+
+template <int D, int E, bool MSG, bool CAUS>
+struct GnnRes {
+  static constexpr int H1 = 2 * E, PA = D + 8, PB = H1 + 8, PC = E + 8;
+  static constexpr size_t a4 = 0;
+  static constexpr size_t w2 = a4 + (size_t)H1 * PA * 2;
+  static constexpr size_t wm = w2 + (size_t)E * PB * 2;
+  static constexpr size_t c1 = wm + (MSG ? (size_t)D * PC * 2 : 0);
+  static constexpr size_t vec = c1 + (CAUS ? (size_t)(E / 2) * PC * 2 : 0);
+  // fp32 vectors: r, c [H1]; b2, we [E]; bm [D]; d1, cc2 [E/2]
+  static constexpr size_t r = vec, c = r + H1 * 4, b2 = c + H1 * 4, we = b2 + E * 4, bm = we + E * 4;
+  static constexpr size_t d1 = bm + (MSG ? D * 4 : 0), cc2 = d1 + (CAUS ? (E / 2) * 4 : 0);
+  static constexpr size_t total = cc2 + (CAUS ? (E / 2) * 4 : 0);
+};
+
+// rows x KC of W (row stride ldw) into sW (pitch P) with the columns of every 32-wide block permuted so that
+// positions 8g .. 8g+7 hold k = 4g .. 4g+3 and 16 + 4g .. 16 + 4g+3
+template <typename T, int NTH>
+__device__ __forceinline__ void stage_permuted(const T* __restrict__ W, int ldw, int rows, int K, T* sW, int P,
+                                               int tid) {
+  for (int u = tid; u < rows * (K / 8); u += NTH) {
+    const int rr = u / (K / 8), q = (u - rr * (K / 8)) * 8;
+    const int kb = q & ~31, gg = (q & 31) >> 3;
+    const uint2 lo = *reinterpret_cast<const uint2*>(W + (size_t)rr * ldw + kb + 4 * gg);
+    const uint2 hi = *reinterpret_cast<const uint2*>(W + (size_t)rr * ldw + kb + 16 + 4 * gg);
+    *reinterpret_cast<uint4*>(sW + rr * P + q) = make_uint4(lo.x, lo.y, hi.x, hi.y);
+  }
+}
+
+template <int DT, int D, int E, int NW, bool MSG, bool CAUS>
+__global__ void __launch_bounds__(64 * NW)
+gnn_edge_res_kernel(GnnArgs a, const float* __restrict__ nstat) {
+  using A = MM<DT>;
+  using T = typename A::T;
+  using L = GnnRes<D, E, MSG, CAUS>;
+  static_assert(DT != HCLSM_F32 && D % 32 == 0 && E % 32 == 0, "16-bit operands, D and E multiples of 32");
+  constexpr int NTH = 64 * NW, H1 = L::H1, PA = L::PA, PB = L::PB, PC = L::PC;
+  constexpr int NT1 = H1 / 16, NT2 = E / 16, NT3 = D / 16, NT4 = E / 32;
+  extern __shared__ __align__(16) unsigned char smem[];
+  T* sA4 = reinterpret_cast<T*>(smem + L::a4);
+  T* sW2 = reinterpret_cast<T*>(smem + L::w2);
+  T* sWm = reinterpret_cast<T*>(smem + L::wm);
+  T* sC1 = reinterpret_cast<T*>(smem + L::c1);
+  float* sr = reinterpret_cast<float*>(smem + L::r);
+  float* sc = reinterpret_cast<float*>(smem + L::c);
+  float* sb2 = reinterpret_cast<float*>(smem + L::b2);
+  float* swe = reinterpret_cast<float*>(smem + L::we);
+  float* sbm = reinterpret_cast<float*>(smem + L::bm);
+  float* sd1 = reinterpret_cast<float*>(smem + L::d1);
+  float* scc2 = reinterpret_cast<float*>(smem + L::cc2);
+  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, g = lane >> 4, li = lane & 15;
+  {
+    const T* A4 = reinterpret_cast<const T*>(a.A4);
+    for (int u = tid; u < H1 * (D / 8); u += NTH) {
+      const int rr = u / (D / 8), q = (u - rr * (D / 8)) * 8;
+      *reinterpret_cast<uint4*>(sA4 + rr * PA + q) = *reinterpret_cast<const uint4*>(A4 + (size_t)rr * D + q);
+    }
+    stage_permuted<T, NTH>(reinterpret_cast<const T*>(a.W2), H1, E, H1, sW2, PB, tid);
+    if constexpr (MSG) stage_permuted<T, NTH>(reinterpret_cast<const T*>(a.Wm), E, D, E, sWm, PC, tid);
+    if constexpr (CAUS) stage_permuted<T, NTH>(reinterpret_cast<const T*>(a.C1), E, E / 2, E, sC1, PC, tid);
+    for (int u = tid; u < H1; u += NTH) {
+      sr[u] = a.r[u];
+      sc[u] = a.c[u];
+    }
+    for (int u = tid; u < E; u += NTH) {
+      sb2[u] = a.b2[u];
+      swe[u] = a.we[u];
+    }
+    if constexpr (MSG)
+      for (int u = tid; u < D; u += NTH) sbm[u] = a.bm[u];
+    if constexpr (CAUS)
+      for (int u = tid; u < E / 2; u += NTH) {
+        sd1[u] = a.d1[u];
+        scc2[u] = a.cc2[u];
+      }
+  }
+  __syncthreads();
+  const int N = a.N;
+  const int64_t units = (int64_t)a.F * N;
+  const float inv4d = 1.f / (4.f * (float)D);
+  for (int64_t unit = (int64_t)blockIdx.x * NW + wid; unit < units; unit += (int64_t)gridDim.x * NW) {
+    const int64_t f = unit / N;
+    const int i = (int)(unit - f * N);
+    const int64_t rowi = f * N + i;
+    const float* xi = a.X + rowi * a.ldx;
+    const float ali = a.alive ? a.alive[rowi] : 1.f;
+    const float si = nstat[2 * rowi], qi = nstat[2 * rowi + 1];
+    float aggp[NT3];   // message partial sums for outputs 16t + li over this lane's pairs
+#pragma unroll
+    for (int t = 0; t < NT3; ++t) aggp[t] = 0.f;
+    for (int j0 = 0; j0 < N; j0 += 32) {
+      int jj[2];
+      const float* xj[2];
+#pragma unroll
+      for (int pt = 0; pt < 2; ++pt) {
+        const int j = j0 + 16 * pt + li;
+        jj[pt] = j;
+        xj[pt] = a.X + (f * N + (j < N ? j : N - 1)) * a.ldx;
+      }
+      // ---- A: Hadamard GEMM, pair statistics
+      f32x4 acc[2][NT1];
+#pragma unroll
+      for (int pt = 0; pt < 2; ++pt)
+#pragma unroll
+        for (int t = 0; t < NT1; ++t) acc[pt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+      float gs[2] = {0.f, 0.f}, hs[2] = {0.f, 0.f};
+      float4 xr[6];
+      auto load_k = [&](int kb) {
+        xr[0] = *reinterpret_cast<const float4*>(xi + kb + 8 * g);
+        xr[1] = *reinterpret_cast<const float4*>(xi + kb + 8 * g + 4);
+#pragma unroll
+        for (int pt = 0; pt < 2; ++pt) {
+          xr[2 + 2 * pt] = *reinterpret_cast<const float4*>(xj[pt] + kb + 8 * g);
+          xr[3 + 2 * pt] = *reinterpret_cast<const float4*>(xj[pt] + kb + 8 * g + 4);
+        }
+      };
+      load_k(0);
+#pragma unroll 1
+      for (int kb = 0; kb < D; kb += 32) {
+        T op[2][8];
+        const float vi[8] = {xr[0].x, xr[0].y, xr[0].z, xr[0].w, xr[1].x, xr[1].y, xr[1].z, xr[1].w};
+#pragma unroll
+        for (int pt = 0; pt < 2; ++pt) {
+          const float vj[8] = {xr[2 + 2 * pt].x, xr[2 + 2 * pt].y, xr[2 + 2 * pt].z, xr[2 + 2 * pt].w,
+                               xr[3 + 2 * pt].x, xr[3 + 2 * pt].y, xr[3 + 2 * pt].z, xr[3 + 2 * pt].w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float pr = vi[e] * vj[e];
+            gs[pt] += pr;
+            hs[pt] = fmaf(pr, pr, hs[pt]);
+            op[pt][e] = A::fromf(pr);
+          }
+        }
+        if (kb + 32 < D) load_k(kb + 32);
+#pragma unroll
+        for (int t = 0; t < NT1; ++t) {
+          T wf[8];
+          frag_load<DT>(sA4 + (16 * t + li) * PA + kb + 8 * g, wf);
+#pragma unroll
+          for (int pt = 0; pt < 2; ++pt) acc[pt][t] = frag_mma<DT>(wf, op[pt], acc[pt][t]);
+        }
+      }
+      // normalise: v = rstd (P_i + Q_j + acc - mu r) + c, ReLU (outputs 16t + 4g + rr of pair li)
+      const float* P = a.PQ + rowi * 2 * H1 + 4 * g;
+#pragma unroll
+      for (int pt = 0; pt < 2; ++pt) {
+        float gg = gs[pt], hh = hs[pt];
+        gg += __shfl_xor(gg, 16, 64);
+        gg += __shfl_xor(gg, 32, 64);
+        hh += __shfl_xor(hh, 16, 64);
+        hh += __shfl_xor(hh, 32, 64);
+        const int64_t rowj = f * N + (jj[pt] < N ? jj[pt] : N - 1);
+        const float qj = nstat[2 * rowj + 1];
+        const float mu = (2.f * si + gg) * inv4d;
+        const float m2 = (2.f * qi + 2.f * qj - 2.f * gg + hh) * inv4d;
+        const float rs = 1.f / sqrtf(fmaxf(m2 - mu * mu, 0.f) + a.eps);
+        const float* Q = a.PQ + rowj * 2 * H1 + H1 + 4 * g;
+#pragma unroll
+        for (int t0 = 0; t0 < NT1; t0 += 3) {
+#pragma unroll
+          for (int t = t0; t < t0 + 3 && t < NT1; ++t) {
+            const float4 p4 = *reinterpret_cast<const float4*>(P + 16 * t);
+            const float4 q4 = *reinterpret_cast<const float4*>(Q + 16 * t);
+            const float4 r4 = *reinterpret_cast<const float4*>(sr + 16 * t + 4 * g);
+            const float4 c4 = *reinterpret_cast<const float4*>(sc + 16 * t + 4 * g);
+            acc[pt][t][0] = fmaxf(fmaf(p4.x + q4.x + acc[pt][t][0] - mu * r4.x, rs, c4.x), 0.f);
+            acc[pt][t][1] = fmaxf(fmaf(p4.y + q4.y + acc[pt][t][1] - mu * r4.y, rs, c4.y), 0.f);
+            acc[pt][t][2] = fmaxf(fmaf(p4.z + q4.z + acc[pt][t][2] - mu * r4.z, rs, c4.z), 0.f);
+            acc[pt][t][3] = fmaxf(fmaf(p4.w + q4.w + acc[pt][t][3] - mu * r4.w, rs, c4.w), 0.f);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      // ---- B: edge features e = ReLU(W2 H1 + b2), rounded to the operand type as the next layers see them
+      f32x4 acc2[2][NT2];
+#pragma unroll
+      for (int pt = 0; pt < 2; ++pt)
+#pragma unroll
+        for (int t = 0; t < NT2; ++t) acc2[pt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < H1 / 32; ++kb) {
+        T hb[2][8];
+#pragma unroll
+        for (int pt = 0; pt < 2; ++pt)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            hb[pt][e] = A::fromf(acc[pt][2 * kb][e]);
+            hb[pt][4 + e] = A::fromf(acc[pt][2 * kb + 1][e]);
+          }
+#pragma unroll
+        for (int t = 0; t < NT2; ++t) {
+          T wf[8];
+          frag_load<DT>(sW2 + (16 * t + li) * PB + 32 * kb + 8 * g, wf);
+#pragma unroll
+          for (int pt = 0; pt < 2; ++pt) acc2[pt][t] = frag_mma<DT>(wf, hb[pt], acc2[pt][t]);
+        }
+      }
+      // edge features of pair li, outputs 16t + 4g + rr, as packed operand pairs (rr = 0,1 | 2,3)
+      uint32_t ebp[2][NT2][2];
+      float wgt[2];      // edge weight of pair li
+#pragma unroll
+      for (int pt = 0; pt < 2; ++pt) {
+        float s = 0.f;
+#pragma unroll
+        for (int t = 0; t < NT2; ++t) {
+          T ev[4];
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) {
+            const int o = 16 * t + 4 * g + rr;
+            ev[rr] = A::fromf(fmaxf(acc2[pt][t][rr] + sb2[o], 0.f));
+            s = fmaf(A::tof(ev[rr]), swe[o], s);
+          }
+          ebp[pt][t][0] = pack2<T>(ev[0], ev[1]);
+          ebp[pt][t][1] = pack2<T>(ev[2], ev[3]);
+        }
+        s += __shfl_xor(s, 16, 64);
+        s += __shfl_xor(s, 32, 64);
+        const int j = jj[pt];
+        const float alj = j < N ? (a.alive ? a.alive[f * N + j] : 1.f) : 0.f;
+        wgt[pt] = ali * alj / (1.f + __expf(-(s + a.be[0])));
+      }
+      // k-block kb of the edge features as an MFMA operand (tiles 2kb and 2kb + 1, in the permuted k order)
+      auto e_op = [&](int pt, int kb) {
+        return __builtin_bit_cast(typename A::Op, make_uint4(ebp[pt][2 * kb][0], ebp[pt][2 * kb][1],
+                                                            ebp[pt][2 * kb + 1][0], ebp[pt][2 * kb + 1][1]));
+      };
+      // ---- C: messages ReLU(Wm e + bm) * w summed over the pairs (outputs in two halves)
+      if constexpr (MSG) {
+        constexpr int HT = (NT3 + 1) / 2;
+#pragma unroll
+        for (int pt = 0; pt < 2; ++pt) {
+          float wr[4];   // weights of pairs 4g + rr of this tile
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) wr[rr] = __shfl(wgt[pt], 4 * g + rr, 64);
+#pragma unroll
+          for (int h0 = 0; h0 < NT3; h0 += HT) {
+            f32x4 acc3[HT];
+#pragma unroll
+            for (int t = 0; t < HT; ++t) acc3[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kb = 0; kb < E / 32; ++kb) {
+              const typename A::Op ea = e_op(pt, kb);
+#pragma unroll
+              for (int t = 0; t < HT; ++t) {
+                if (h0 + t < NT3)
+                  acc3[t] = A::mfma(ea, A::load(sWm + (16 * (h0 + t) + li) * PC + 32 * kb + 8 * g), acc3[t]);
+              }
+            }
+#pragma unroll
+            for (int t = 0; t < HT; ++t) {
+              if (h0 + t < NT3) {
+                const float bmo = sbm[16 * (h0 + t) + li];
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr)
+                  aggp[h0 + t] = fmaf(fmaxf(acc3[t][rr] + bmo, 0.f), wr[rr], aggp[h0 + t]);
+              }
+            }
+          }
+        }
+      }
+      // ---- D: causal edges
+      if constexpr (CAUS) {
+#pragma unroll
+        for (int pt = 0; pt < 2; ++pt) {
+          f32x4 acc4[NT4];
+#pragma unroll
+          for (int t = 0; t < NT4; ++t) acc4[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int kb = 0; kb < E / 32; ++kb) {
+            const typename A::Op hb = e_op(pt, kb);
+#pragma unroll
+            for (int t = 0; t < NT4; ++t)
+              acc4[t] = A::mfma(A::load(sC1 + (16 * t + li) * PC + 32 * kb + 8 * g), hb, acc4[t]);
+          }
+          float s = 0.f;
+#pragma unroll
+          for (int t = 0; t < NT4; ++t)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+              const int o = 16 * t + 4 * g + rr;
+              s = fmaf(fmaxf(acc4[t][rr] + sd1[o], 0.f), scc2[o], s);
+            }
+          s += __shfl_xor(s, 16, 64);
+          s += __shfl_xor(s, 32, 64);
+          const int j = jj[pt];
+          if (g == 0 && j < N) {
+            const float alj = a.alive ? a.alive[f * N + j] : 1.f;
+            a.causal[rowi * N + j] = ali * alj / (1.f + __expf(-(s + a.d2[0])));
+          }
+        }
+      }
+    }
+    if constexpr (MSG) {
+#pragma unroll
+      for (int t = 0; t < NT3; ++t) {
+        float v = aggp[t];
+        v += __shfl_xor(v, 16, 64);
+        v += __shfl_xor(v, 32, 64);
+        if (g == 0) a.agg[rowi * a.ldagg + 16 * t + li] = v;
+      }
+    }
+  }
+}
+
+// s = sum_k x[row, k], q = sum_k x[row, k]^2 for every row (one wave per row)
+__global__ void __launch_bounds__(256)
+gnn_node_stats_kernel(const float* __restrict__ x, int64_t ldx, float* __restrict__ st, int64_t rows, int D) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int lane = threadIdx.x & 63;
+  float s = 0.f, q = 0.f;
+  for (int k = lane; k < D; k += 64) {
+    const float v = x[row * ldx + k];
+    s += v;
+    q = fmaf(v, v, q);
+  }
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) {
+    s += __shfl_xor(s, m, 64);
+    q += __shfl_xor(q, m, 64);
+  }
+  if (lane == 0) {
+    st[2 * row] = s;
+    st[2 * row + 1] = q;
+  }
+}
+
 // [P-weights; Q-weights] (4E x D), A4 (2E x D) in the operand dtype, r and c (2E) in fp32, from W1 (2E x 4D,
 // operand dtype), b1, gamma, beta.  Grid: one workgroup per output row o < 2E.
 template <int DT>
@@ -309,7 +651,7 @@ gnn_copy_rows_kernel(const float* __restrict__ x, int64_t ldx, const float* __re
 }
 
 struct GnnWs {
-  size_t wpq, a4, r, c, pq, xa, u, total;
+  size_t wpq, a4, r, c, pq, xa, u, nstat, total;
 };
 
 static size_t al256g(size_t v) { return (v + 255) / 256 * 256; }
@@ -325,6 +667,7 @@ static GnnWs gnn_ws(int64_t F, int64_t N, int64_t D, int64_t E, int es) {
   w.pq = o; o += al256g(R * 4 * E * 4);
   w.xa = o; o += al256g(R * 2 * D * 4);
   w.u = o; o += al256g(R * D * es);
+  w.nstat = o; o += al256g(R * 2 * 4);
   w.total = o;
   return w;
 }
@@ -362,6 +705,59 @@ template <int DT>
 static bool edges_fit(const GnnArgs& a) {
   if constexpr (DT == HCLSM_F32) return edge_lds<DT, 4, 16>(a) <= GNN_LDS_MAX;
   else return edge_lds<DT, 8, 32>(a) <= GNN_LDS_MAX;
+}
+
+template <int DT, int D, int E, bool MSG, bool CAUS>
+static int launch_edges_res(const GnnArgs& a, const float* nstat, hipStream_t st) {
+  constexpr int NW = 8;
+  constexpr size_t lds = GnnRes<D, E, MSG, CAUS>::total;
+  static_assert(lds <= GNN_LDS_MAX, "resident weights exceed the LDS");
+  static int grid = 0;   // resident workgroups on the device (persistent kernel), found once
+  if (grid == 0) {
+    const void* fn = reinterpret_cast<const void*>(&gnn_edge_res_kernel<DT, D, E, NW, MSG, CAUS>);
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)GNN_LDS_MAX);
+    if (e != hipSuccess) return (int)e;
+    int dev = 0, cus = 0, per_cu = 0;
+    if ((e = hipGetDevice(&dev)) != hipSuccess) return (int)e;
+    if ((e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return (int)e;
+    if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 64 * NW, lds)) != hipSuccess) return (int)e;
+    grid = cus * (per_cu > 0 ? per_cu : 1);
+  }
+  const int64_t units = (int64_t)a.F * a.N;
+  const int64_t need = (units + NW - 1) / NW;
+  const unsigned g = (unsigned)(need < grid ? need : grid);
+  hipLaunchKernelGGL((gnn_edge_res_kernel<DT, D, E, NW, MSG, CAUS>), dim3(g), dim3(64 * NW), lds, st, a, nstat);
+  HCLSM_LAUNCH_CHECK();
+  return 0;
+}
+
+// The resident kernel for the preset shapes (messages and causal head in one pass when both fit the LDS,
+// otherwise one pass each over the same edges); 1 on a shape it does not cover.
+template <int DT, int D, int E>
+static int edges_res_shape(const GnnArgs& a, const float* nstat, hipStream_t st) {
+  const bool msg = a.agg != nullptr, caus = a.causal != nullptr;
+  if (msg && caus) {
+    if constexpr (GnnRes<D, E, true, true>::total <= GNN_LDS_MAX) {
+      return launch_edges_res<DT, D, E, true, true>(a, nstat, st);
+    } else {
+      GnnArgs m = a, c = a;
+      m.causal = nullptr;
+      c.agg = nullptr;
+      const int rc = launch_edges_res<DT, D, E, true, false>(m, nstat, st);
+      return rc ? rc : launch_edges_res<DT, D, E, false, true>(c, nstat, st);
+    }
+  }
+  if (msg) return launch_edges_res<DT, D, E, true, false>(a, nstat, st);
+  if (caus) return launch_edges_res<DT, D, E, false, true>(a, nstat, st);
+  return 0;
+}
+
+template <int DT>
+static int launch_edges_resident(const GnnArgs& a, const float* nstat, hipStream_t st) {
+  if (a.D == 64 && a.E == 32) return edges_res_shape<DT, 64, 32>(a, nstat, st);
+  if (a.D == 128 && a.E == 64) return edges_res_shape<DT, 128, 64>(a, nstat, st);
+  if (a.D == 192 && a.E == 96) return edges_res_shape<DT, 192, 96>(a, nstat, st);
+  return 1;
 }
 
 template <int DT>
@@ -408,6 +804,7 @@ static int gnn_forward(const float* nodes, const float* alive, float* nodes_out,
   float* PQ = reinterpret_cast<float*>(ws + L.pq);
   float* XA = reinterpret_cast<float*>(ws + L.xa);   // [F*N, 2D]: nodes | messages
   void* U = ws + L.u;                                // [F*N, D] hidden layer of the node update
+  float* nstat = reinterpret_cast<float*>(ws + L.nstat);   // [F*N][2] node sums and sums of squares
   const int64_t R = F * N, ld = 2 * D;
   auto P = [&](int i) { return p[i]; };
   auto Pf = [&](int i) { return reinterpret_cast<const float*>(p[i]); };
@@ -433,6 +830,13 @@ static int gnn_forward(const float* nodes, const float* alive, float* nodes_out,
     if (e) return e;
     a.agg = msg ? XA + D : nullptr;
     a.causal = caus ? causal : nullptr;
+    if constexpr (DT != HCLSM_F32) {
+      hipLaunchKernelGGL(gnn_node_stats_kernel, dim3((unsigned)((R + 3) / 4)), dim3(256), 0, st, XA, ld, nstat, R,
+                         (int)D);
+      HCLSM_LAUNCH_CHECK();
+      e = launch_edges_resident<DT>(a, nstat, st);
+      if (e != 1) return e;
+    }
     return launch_edges<DT>(a, st);
   };
   auto update = [&]() -> int {   // nodes += U2 ReLU(U1 [nodes; agg] + c1) + c2, in place in XA

@@ -160,12 +160,37 @@ __device__ __forceinline__ float ext_glu(const LinExt& e, int64_t row, int64_t c
 // K chunks of 128 (each global byte read once per workgroup), the next chunk's global loads in flight
 // while the current chunk is multiplied; each wave computes a 32x32 quadrant from LDS.  34 KB of LDS,
 // so several workgroups share a CU.
+// One 16-byte LDS unit (8 operand elements) of the A operand: loaded as is for 16-bit X, or as 8 fp32 values
+// rounded to the operand type when it is stored (fp32 X).
+template <int DT, typename XT>
+struct AUnit {
+  uint4 v;
+  __device__ __forceinline__ void load(const XT* p) { v = *reinterpret_cast<const uint4*>(p); }
+  __device__ __forceinline__ void zero() { v = make_uint4(0u, 0u, 0u, 0u); }
+  __device__ __forceinline__ uint4 get() const { return v; }
+};
+template <int DT>
+struct AUnit<DT, float> {
+  float4 lo, hi;
+  __device__ __forceinline__ void load(const float* p) {
+    lo = *reinterpret_cast<const float4*>(p);
+    hi = *reinterpret_cast<const float4*>(p + 4);
+  }
+  __device__ __forceinline__ void zero() { lo = hi = make_float4(0.f, 0.f, 0.f, 0.f); }
+  __device__ __forceinline__ uint4 get() const {
+    using A = MM<DT>;
+    typename A::T e[8] = {A::fromf(lo.x), A::fromf(lo.y), A::fromf(lo.z), A::fromf(lo.w),
+                          A::fromf(hi.x), A::fromf(hi.y), A::fromf(hi.z), A::fromf(hi.w)};
+    return *reinterpret_cast<const uint4*>(e);
+  }
+};
+
 constexpr int LT_KC = 128;
 constexpr int LT_LD = LT_KC + 8;   // LDS row pitch (elements): spreads the 16 rows of an operand over banks
 
-template <int DT, int OT>
+template <int DT, int OT, typename XT = typename MM<DT>::T>
 __global__ void __launch_bounds__(256)
-linear_lds_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const typename MM<DT>::T* __restrict__ W,
+linear_lds_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>::T* __restrict__ W,
                   int64_t ldw, const float* __restrict__ bias, const float* __restrict__ resid, int64_t ldr,
                   typename MM<OT>::T* __restrict__ Y, int64_t ldy, typename MM<DT>::T* __restrict__ Y2,
                   int64_t ldy2, int64_t M, int64_t N, int64_t K, int relu, float clamp_v, OutSplit os, LinExt ext) {
@@ -181,7 +206,7 @@ linear_lds_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const t
   const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, g = lane >> 4, li = lane & 15;
   const int wr = wid >> 1, wc = wid & 1;
   // staging map: 64 rows x (KC / 8) 16-byte units = 1024 units per operand, 4 per thread
-  const T* pa[4];
+  const XT* pa[4];
   const T* pb[4];
   int soff[4], ucol[4];
 #pragma unroll
@@ -195,12 +220,14 @@ linear_lds_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const t
     pb[i] = W + rb * ldw + ucol[i];
     soff[i] = r * LT_LD + ucol[i];
   }
-  uint4 ra_[4], rb_[4];
+  AUnit<DT, XT> ra_[4];
+  uint4 rb_[4];
   auto fetch = [&](int64_t k0, int kc) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const bool in = ucol[i] < kc;
-      ra_[i] = in ? *reinterpret_cast<const uint4*>(pa[i] + k0) : make_uint4(0u, 0u, 0u, 0u);
+      if (in) ra_[i].load(pa[i] + k0);
+      else ra_[i].zero();
       rb_[i] = in ? *reinterpret_cast<const uint4*>(pb[i] + k0) : make_uint4(0u, 0u, 0u, 0u);
     }
   };
@@ -215,7 +242,7 @@ linear_lds_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const t
     __syncthreads();   // the previous chunk is consumed
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      *reinterpret_cast<uint4*>(As + soff[i]) = ra_[i];
+      *reinterpret_cast<uint4*>(As + soff[i]) = ra_[i].get();
       *reinterpret_cast<uint4*>(Bs + soff[i]) = rb_[i];
     }
     __syncthreads();
@@ -301,9 +328,9 @@ linear_lds_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const t
 constexpr int LB_KC = 64;
 constexpr int LB_LD = LB_KC + 8;   // pitch 144 B: the 16 rows of a fragment read hit distinct banks
 
-template <int DT, int OT>
+template <int DT, int OT, typename XT = typename MM<DT>::T>
 __global__ void __launch_bounds__(256)
-linear_lds128_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const typename MM<DT>::T* __restrict__ W,
+linear_lds128_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>::T* __restrict__ W,
                      int64_t ldw, const float* __restrict__ bias, const float* __restrict__ resid, int64_t ldr,
                      typename MM<OT>::T* __restrict__ Y, int64_t ldy, typename MM<DT>::T* __restrict__ Y2,
                      int64_t ldy2, int64_t M, int64_t N, int64_t K, int relu, float clamp_v, LinExt ext) {
@@ -319,7 +346,7 @@ linear_lds128_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, cons
   const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, g = lane >> 4, li = lane & 15;
   const int wr = wid >> 1, wc = wid & 1;
   // staging map: 128 rows x (KC / 8) 16-byte units = 1024 units per operand, 4 per thread
-  const T* pa[4];
+  const XT* pa[4];
   const T* pb[4];
   int soff[4], ucol[4];
 #pragma unroll
@@ -333,12 +360,14 @@ linear_lds128_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, cons
     pb[i] = W + rb * ldw + ucol[i];
     soff[i] = r * LB_LD + ucol[i];
   }
-  uint4 ra_[4], rb_[4];
+  AUnit<DT, XT> ra_[4];
+  uint4 rb_[4];
   auto fetch = [&](int64_t k0, int kc) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const bool in = ucol[i] < kc;
-      ra_[i] = in ? *reinterpret_cast<const uint4*>(pa[i] + k0) : make_uint4(0u, 0u, 0u, 0u);
+      if (in) ra_[i].load(pa[i] + k0);
+      else ra_[i].zero();
       rb_[i] = in ? *reinterpret_cast<const uint4*>(pb[i] + k0) : make_uint4(0u, 0u, 0u, 0u);
     }
   };
@@ -353,7 +382,7 @@ linear_lds128_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, cons
     __syncthreads();   // the previous chunk is consumed
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      *reinterpret_cast<uint4*>(As + soff[i]) = ra_[i];
+      *reinterpret_cast<uint4*>(As + soff[i]) = ra_[i].get();
       *reinterpret_cast<uint4*>(Bs + soff[i]) = rb_[i];
     }
     __syncthreads();
@@ -1083,26 +1112,31 @@ static void launch_linear_quad(const void* x, int64_t ldx, const void* w, int64_
                                const float* resid, int64_t ldr, void* y, int64_t ldy, void* y2, int64_t ldy2,
                                int64_t M, int64_t N, int64_t K, int relu, float clamp, hipStream_t st,
                                OutSplit os = OutSplit{0, 1, 0, 0, nullptr}, LinExt ext = kNoLinExt) {
-  if constexpr (std::is_same_v<XT, typename MM<DT>::T>) {
+  constexpr bool direct = std::is_same_v<XT, typename MM<DT>::T>;
+  // fp32 X with 16-bit operands: the LDS kernels round X while staging it (callers check 16-byte rows)
+  constexpr bool cvt = MM<DT>::KPL == 8 && std::is_same_v<XT, float>;
+  if constexpr (direct || cvt) {
     const unsigned grid = (unsigned)(((M + 63) / 64) * ((N + 63) / 64));
     const int64_t tiles128 = ((M + 127) / 128) * ((N + 127) / 128);
     if constexpr (MM<DT>::KPL == 8) {
       if (os.yt == nullptr && N >= 768 && tiles128 >= 512)
-        hipLaunchKernelGGL((linear_lds128_kernel<DT, OT>), dim3((unsigned)tiles128), dim3(256), 0, st,
-                           (const typename MM<DT>::T*)x, ldx, (const typename MM<DT>::T*)w, ldw, bias, resid, ldr,
+        hipLaunchKernelGGL((linear_lds128_kernel<DT, OT, XT>), dim3((unsigned)tiles128), dim3(256), 0, st,
+                           (const XT*)x, ldx, (const typename MM<DT>::T*)w, ldw, bias, resid, ldr,
                            (typename MM<OT>::T*)y, ldy, (typename MM<DT>::T*)y2, ldy2, M, N, K, relu, clamp, ext);
       else
-        hipLaunchKernelGGL((linear_lds_kernel<DT, OT>), dim3(grid), dim3(256), 0, st, (const typename MM<DT>::T*)x,
+        hipLaunchKernelGGL((linear_lds_kernel<DT, OT, XT>), dim3(grid), dim3(256), 0, st, (const XT*)x, ldx,
+                           (const typename MM<DT>::T*)w, ldw, bias, resid, ldr, (typename MM<OT>::T*)y, ldy,
+                           (typename MM<DT>::T*)y2, ldy2, M, N, K, relu, clamp, os, ext);
+    } else if constexpr (direct) {
+      if (os.yt == nullptr && al16(x) && al16(w) && ldx % 4 == 0 && ldw % 4 == 0)
+        hipLaunchKernelGGL((linear_lds_f32_kernel<OT>), dim3(grid), dim3(256), 0, st, (const float*)x, ldx,
+                           (const float*)w, ldw, bias, resid, ldr, (typename MM<OT>::T*)y, ldy, (float*)y2, ldy2, M,
+                           N, K, relu, clamp, ext);
+      else
+        hipLaunchKernelGGL((linear_quad_kernel<DT, OT>), dim3(grid), dim3(256), 0, st, (const typename MM<DT>::T*)x,
                            ldx, (const typename MM<DT>::T*)w, ldw, bias, resid, ldr, (typename MM<OT>::T*)y, ldy,
                            (typename MM<DT>::T*)y2, ldy2, M, N, K, relu, clamp, os, ext);
-    } else if (os.yt == nullptr && al16(x) && al16(w) && ldx % 4 == 0 && ldw % 4 == 0)
-      hipLaunchKernelGGL((linear_lds_f32_kernel<OT>), dim3(grid), dim3(256), 0, st, (const float*)x, ldx,
-                         (const float*)w, ldw, bias, resid, ldr, (typename MM<OT>::T*)y, ldy, (float*)y2, ldy2, M,
-                         N, K, relu, clamp, ext);
-    else
-      hipLaunchKernelGGL((linear_quad_kernel<DT, OT>), dim3(grid), dim3(256), 0, st, (const typename MM<DT>::T*)x,
-                         ldx, (const typename MM<DT>::T*)w, ldw, bias, resid, ldr, (typename MM<OT>::T*)y, ldy,
-                         (typename MM<DT>::T*)y2, ldy2, M, N, K, relu, clamp, os, ext);
+    }
   }
 }
 
@@ -1112,7 +1146,8 @@ static void launch_linear_t(bool ln, const void* x, int64_t ldx, const void* w, 
                             int64_t N, int64_t K, int relu, float clamp, const float* lnw, const float* lnb,
                             float eps, hipStream_t st, LinExt ext = kNoLinExt) {
   const int64_t tiles32 = ((M + 31) / 32) * ((N + 31) / 32);
-  if (!ln && std::is_same_v<XT, typename MM<DT>::T> && tiles32 >= 2048) {
+  constexpr bool cvt = MM<DT>::KPL == 8 && std::is_same_v<XT, float>;
+  if (!ln && (std::is_same_v<XT, typename MM<DT>::T> || (cvt && al16(x) && ldx % 4 == 0)) && tiles32 >= 2048) {
     launch_linear_quad<DT, OT, XT>(x, ldx, w, ldw, bias, resid, ldr, y, ldy, y2, ldy2, M, N, K, relu, clamp, st,
                                    OutSplit{0, 1, 0, 0, nullptr}, ext);
     return;
