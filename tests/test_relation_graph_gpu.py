@@ -60,7 +60,8 @@ def test_relation_graph_fp32_matches_oracle(F, N, D, E, rounds, chunked):
     assert normwise_rel_err(_np(causal), rc) <= 1e-5
 
 
-@pytest.mark.parametrize("F,N,D,E,rounds,chunked", CASES[:2] + CASES[3:4] + [(1, 128, 384, 192, 3, True)])
+@pytest.mark.parametrize("F,N,D,E,rounds,chunked", CASES + [(1, 128, 384, 192, 3, True), (2, 40, 192, 96, 1, False),
+                                                     (2, 64, 256, 128, 2, True)])
 def test_relation_graph_bf16_matches_oracle(F, N, D, E, rounds, chunked):
     from hclsm_amd.kernels.relation_graph import GnnWeights, relation_graph_forward
     m = _module(D, E, rounds, N, F + N + 1)
