@@ -26,6 +26,8 @@
 #include "internal.h"
 #include "pair_tile.h"
 
+#include <utility>
+
 namespace hclsm {
 
 struct GnnArgs {
@@ -579,6 +581,344 @@ gnn_edge_res_kernel(GnnArgs a, const float* __restrict__ nstat) {
   }
 }
 
+// Chunk-streamed edge kernel for 16-bit operands at the base preset's shape (D, E) = (256, 128), whose weights
+// exceed the LDS: the same register-chained phases as gnn_edge_res_kernel, with one 16-pair tile per wave, and all
+// weights streamed through a double-buffered LDS ring in 64-column chunks (A4, then W2, then Wm and / or C1;
+// the schedule repeats every step, so the next chunk's global loads are always in flight while the current one
+// is multiplied; one barrier per chunk).  A workgroup owns NW consecutive source rows (one per wave) and steps
+// through the targets 16 at a time; the messages of a row are summed over the steps in registers.
+template <int D, int E, bool MSG, bool CAUS>
+struct GnnStr {
+  static constexpr int H1 = 2 * E, KS = 64, PS = KS + 8;
+  static constexpr int RMAX = H1 > D ? H1 : D;
+  static constexpr int NA = D / KS, NB = H1 / KS, NC = MSG ? E / KS : 0, ND = CAUS ? E / KS : 0;
+  static constexpr int NCH = NA + NB + NC + ND;
+  static constexpr size_t buf = (size_t)RMAX * PS * 2;   // one chunk buffer (bytes)
+  // fp32 vectors first: their offsets fit the 16-bit immediate of LDS reads
+  static constexpr size_t r = 0, c = r + H1 * 4, b2 = c + H1 * 4, we = b2 + E * 4, bm = we + E * 4;
+  static constexpr size_t d1 = bm + D * 4, cc2 = d1 + (E / 2) * 4;
+  static constexpr size_t buf0 = (cc2 + (E / 2) * 4 + 255) / 256 * 256, buf1 = buf0 + buf, total = buf1 + buf;
+};
+
+template <int N_, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  [&]<int... I>(std::integer_sequence<int, I...>) { (f(std::integral_constant<int, I>{}), ...); }
+  (std::make_integer_sequence<int, N_>{});
+}
+
+template <int DT, int D, int E, int NW, bool MSG, bool CAUS>
+__global__ void __launch_bounds__(64 * NW)
+gnn_edge_str_kernel(GnnArgs a, const float* __restrict__ nstat) {
+  using A = MM<DT>;
+  using T = typename A::T;
+  using L = GnnStr<D, E, MSG, CAUS>;
+  static_assert(DT != HCLSM_F32 && D % 64 == 0 && E % 64 == 0, "16-bit operands, D and E multiples of 64");
+  constexpr int NTH = 64 * NW, H1 = L::H1, KS = L::KS, PS = L::PS, NCH = L::NCH;
+  constexpr int NA = L::NA, NB = L::NB, NC = L::NC;
+  constexpr int NT1 = H1 / 16, NT2 = E / 16, NT3 = D / 16, NT4 = E / 32;
+  constexpr int UPT = (L::RMAX * (KS / 8) + NTH - 1) / NTH;   // 16-byte units per thread per chunk
+  extern __shared__ __align__(16) unsigned char smem[];
+  T* sbuf0 = reinterpret_cast<T*>(smem + L::buf0);
+  T* sbuf1 = reinterpret_cast<T*>(smem + L::buf1);
+  float* sr = reinterpret_cast<float*>(smem + L::r);
+  float* sc = reinterpret_cast<float*>(smem + L::c);
+  float* sb2 = reinterpret_cast<float*>(smem + L::b2);
+  float* swe = reinterpret_cast<float*>(smem + L::we);
+  float* sbm = reinterpret_cast<float*>(smem + L::bm);
+  float* sd1 = reinterpret_cast<float*>(smem + L::d1);
+  float* scc2 = reinterpret_cast<float*>(smem + L::cc2);
+  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, g = lane >> 4, li = lane & 15;
+  for (int u = tid; u < H1; u += NTH) {
+    sr[u] = a.r[u];
+    sc[u] = a.c[u];
+  }
+  for (int u = tid; u < E; u += NTH) {
+    sb2[u] = a.b2[u];
+    swe[u] = a.we[u];
+  }
+  for (int u = tid; u < D; u += NTH) sbm[u] = MSG ? a.bm[u] : 0.f;
+  for (int u = tid; u < E / 2; u += NTH) {
+    sd1[u] = CAUS ? a.d1[u] : 0.f;
+    scc2[u] = CAUS ? a.cc2[u] : 0.f;
+  }
+  // chunk ch of the periodic schedule: weight rows, their row stride, the first column, permuted or not
+  auto chunk_src = [&](int ch, const T*& W, int& rows, int& ld, int& k0, bool& perm) {
+    if (ch < NA) { W = reinterpret_cast<const T*>(a.A4); rows = H1; ld = D; k0 = ch * KS; perm = false; }
+    else if (ch < NA + NB) { W = reinterpret_cast<const T*>(a.W2); rows = E; ld = H1; k0 = (ch - NA) * KS; perm = true; }
+    else if (ch < NA + NB + NC) { W = reinterpret_cast<const T*>(a.Wm); rows = D; ld = E; k0 = (ch - NA - NB) * KS; perm = true; }
+    else { W = reinterpret_cast<const T*>(a.C1); rows = E / 2; ld = E; k0 = (ch - NA - NB - NC) * KS; perm = true; }
+  };
+  uint4 stg[UPT];
+  // The staging addresses are recomputed at every chunk from a copy of tid the compiler cannot see through:
+  // hoisted out of the loops, the addresses of every chunk of the schedule would stay live in registers.
+  auto opaque_tid = [&]() {
+    int t = tid;
+    asm volatile("" : "+v"(t));
+    return t;
+  };
+  auto load_chunk = [&](int ch) {
+    const T* W;
+    int rows, ld, k0;
+    bool perm;
+    chunk_src(ch, W, rows, ld, k0, perm);
+    const int t0 = opaque_tid();
+#pragma unroll
+    for (int q = 0; q < UPT; ++q) {
+      const int u = t0 + q * NTH, rr = u / (KS / 8), p = (u - rr * (KS / 8)) * 8;
+      if (rr < rows) {
+        const T* src = W + (size_t)rr * ld + k0;
+        if (perm) {
+          const int kb = p & ~31, gg = (p & 31) >> 3;
+          const uint2 lo = *reinterpret_cast<const uint2*>(src + kb + 4 * gg);
+          const uint2 hi = *reinterpret_cast<const uint2*>(src + kb + 16 + 4 * gg);
+          stg[q] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        } else {
+          stg[q] = *reinterpret_cast<const uint4*>(src + p);
+        }
+      }
+    }
+  };
+  auto store_chunk = [&](int ch, T* buf) {
+    const T* W;
+    int rows, ld, k0;
+    bool perm;
+    chunk_src(ch, W, rows, ld, k0, perm);
+    const int t0 = opaque_tid();
+#pragma unroll
+    for (int q = 0; q < UPT; ++q) {
+      const int u = t0 + q * NTH, rr = u / (KS / 8), p = (u - rr * (KS / 8)) * 8;
+      if (rr < rows) *reinterpret_cast<uint4*>(buf + rr * PS + p) = stg[q];
+    }
+  };
+  const int N = a.N;
+  const int64_t rows_all = (int64_t)a.F * N;
+  const int64_t groups = (rows_all + NW - 1) / NW;
+  const int steps = (N + 15) / 16;
+  const float inv4d = 1.f / (4.f * (float)D);
+  // prologue: chunk 0 of the schedule into buffer 0
+  load_chunk(0);
+  store_chunk(0, sbuf0);
+  __syncthreads();
+  int cur = 0;   // buffer holding the chunk about to be used (the schedule restarts with chunk 0 each step)
+  for (int64_t grp = blockIdx.x; grp < groups; grp += gridDim.x) {
+    const int64_t rowi_raw = grp * NW + wid;
+    const bool live_row = rowi_raw < rows_all;
+    const int64_t rowi = live_row ? rowi_raw : rows_all - 1;
+    const int64_t f = rowi / N;
+    const float* xi = a.X + rowi * a.ldx;
+    const float ali = a.alive ? a.alive[rowi] : 1.f;
+    const float si = nstat[2 * rowi], qi = nstat[2 * rowi + 1];
+    float aggp[NT3];
+#pragma unroll
+    for (int t = 0; t < NT3; ++t) aggp[t] = 0.f;
+    for (int st = 0; st < steps; ++st) {
+      const int j = st * 16 + li;
+      const int64_t rowj = f * N + (j < N ? j : N - 1);
+      const float* xj = a.X + rowj * a.ldx;
+      // accumulators of the four phases; each is cleared at its phase's first chunk (disjoint live ranges)
+      f32x4 acc[NT1], acc2[NT2], acc3[NT3], acc4[NT4];
+      float gs = 0.f, hs = 0.f, wgt = 0.f;
+      uint32_t ebp[NT2][2];
+      // node rows of the current A chunk (this lane's 2 x 8 columns of x_i and x_j), loaded one chunk ahead
+      float4 xr[8], xn[8];
+      auto load_x = [&](int kc, float4 (&d)[8]) {
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const int k = kc * KS + 32 * s2 + 8 * g;
+          d[4 * s2] = *reinterpret_cast<const float4*>(xi + k);
+          d[4 * s2 + 1] = *reinterpret_cast<const float4*>(xi + k + 4);
+          d[4 * s2 + 2] = *reinterpret_cast<const float4*>(xj + k);
+          d[4 * s2 + 3] = *reinterpret_cast<const float4*>(xj + k + 4);
+        }
+      };
+      load_x(0, xr);
+      auto e_op = [&](int kb) {
+        return __builtin_bit_cast(typename A::Op, make_uint4(ebp[2 * kb][0], ebp[2 * kb][1], ebp[2 * kb + 1][0],
+                                                            ebp[2 * kb + 1][1]));
+      };
+      static_for<NCH>([&](auto chc) {
+        constexpr int ch = decltype(chc)::value;
+        const T* sb = cur ? sbuf1 : sbuf0;
+        load_chunk(ch + 1 < NCH ? ch + 1 : 0);   // the next chunk of the schedule, in flight
+        if constexpr (ch < NA) {
+          // ---- A: Hadamard GEMM over columns [64 ch, 64 ch + 64)
+          if constexpr (ch == 0) {
+#pragma unroll
+            for (int t = 0; t < NT1; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+          }
+          if constexpr (ch + 1 < NA) load_x(ch + 1, xn);
+#pragma unroll
+          for (int s = 0; s < 2; ++s) {
+            const float4 x0 = xr[4 * s], x1 = xr[4 * s + 1], y0 = xr[4 * s + 2], y1 = xr[4 * s + 3];
+            const float vi[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            const float vj[8] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w};
+            T op[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const float pr = vi[e] * vj[e];
+              gs += pr;
+              hs = fmaf(pr, pr, hs);
+              op[e] = A::fromf(pr);
+            }
+            const typename A::Op opv = A::load(op);
+#pragma unroll
+            for (int t = 0; t < NT1; ++t) {
+              acc[t] = A::mfma(A::load(sb + (16 * t + li) * PS + 32 * s + 8 * g), opv, acc[t]);
+              if ((t & 3) == 3) __builtin_amdgcn_sched_barrier(0);   // at most 4 fragments in flight
+            }
+          }
+          if constexpr (ch + 1 < NA) {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) xr[q] = xn[q];
+          }
+          if constexpr (ch == NA - 1) {
+            // normalise: v = rstd (P_i + Q_j + acc - mu r) + c, ReLU (outputs 16t + 4g + rr of pair li)
+            gs += __shfl_xor(gs, 16, 64);
+            gs += __shfl_xor(gs, 32, 64);
+            hs += __shfl_xor(hs, 16, 64);
+            hs += __shfl_xor(hs, 32, 64);
+            const float qj = nstat[2 * rowj + 1];
+            const float mu = (2.f * si + gs) * inv4d;
+            const float m2 = (2.f * qi + 2.f * qj - 2.f * gs + hs) * inv4d;
+            const float rs = 1.f / sqrtf(fmaxf(m2 - mu * mu, 0.f) + a.eps);
+            const float* P = a.PQ + rowi * 2 * H1 + 4 * g;
+            const float* Q = a.PQ + rowj * 2 * H1 + H1 + 4 * g;
+#pragma unroll
+            for (int t0 = 0; t0 < NT1; t0 += 4) {
+#pragma unroll
+              for (int t = t0; t < t0 + 4 && t < NT1; ++t) {
+                const float4 p4 = *reinterpret_cast<const float4*>(P + 16 * t);
+                const float4 q4 = *reinterpret_cast<const float4*>(Q + 16 * t);
+                const float4 r4 = *reinterpret_cast<const float4*>(sr + 16 * t + 4 * g);
+                const float4 c4 = *reinterpret_cast<const float4*>(sc + 16 * t + 4 * g);
+                acc[t][0] = fmaxf(fmaf(p4.x + q4.x + acc[t][0] - mu * r4.x, rs, c4.x), 0.f);
+                acc[t][1] = fmaxf(fmaf(p4.y + q4.y + acc[t][1] - mu * r4.y, rs, c4.y), 0.f);
+                acc[t][2] = fmaxf(fmaf(p4.z + q4.z + acc[t][2] - mu * r4.z, rs, c4.z), 0.f);
+                acc[t][3] = fmaxf(fmaf(p4.w + q4.w + acc[t][3] - mu * r4.w, rs, c4.w), 0.f);
+              }
+              __builtin_amdgcn_sched_barrier(0);
+            }
+          }
+        } else if constexpr (ch < NA + NB) {
+          // ---- B: W2 H1 over H1 columns [64 (ch - NA), +64): k-blocks kb take acc tiles 2kb, 2kb + 1
+          constexpr int cb = ch - NA;
+          if constexpr (cb == 0) {
+#pragma unroll
+            for (int t = 0; t < NT2; ++t) acc2[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+          }
+#pragma unroll
+          for (int s = 0; s < 2; ++s) {
+            const int kb = 2 * cb + s;
+            T hb[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              hb[e] = A::fromf(acc[2 * kb][e]);
+              hb[4 + e] = A::fromf(acc[2 * kb + 1][e]);
+            }
+            const typename A::Op hv = A::load(hb);
+#pragma unroll
+            for (int t = 0; t < NT2; ++t) {
+              acc2[t] = A::mfma(A::load(sb + (16 * t + li) * PS + 32 * s + 8 * g), hv, acc2[t]);
+              if ((t & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+            }
+          }
+          if constexpr (ch == NA + NB - 1) {
+            float sw = 0.f;
+#pragma unroll
+            for (int t = 0; t < NT2; ++t) {
+              T ev[4];
+#pragma unroll
+              for (int rr = 0; rr < 4; ++rr) {
+                const int o = 16 * t + 4 * g + rr;
+                ev[rr] = A::fromf(fmaxf(acc2[t][rr] + sb2[o], 0.f));
+                sw = fmaf(A::tof(ev[rr]), swe[o], sw);
+              }
+              ebp[t][0] = pack2<T>(ev[0], ev[1]);
+              ebp[t][1] = pack2<T>(ev[2], ev[3]);
+            }
+            sw += __shfl_xor(sw, 16, 64);
+            sw += __shfl_xor(sw, 32, 64);
+            const float alj = j < N ? (a.alive ? a.alive[rowj] : 1.f) : 0.f;
+            wgt = ali * alj / (1.f + __expf(-(sw + a.be[0])));
+          }
+        } else if constexpr (ch < NA + NB + NC) {
+          // ---- C: messages over edge-feature columns [64 (ch - NA - NB), +64); pairs as the A operand
+          constexpr int cc = ch - NA - NB;
+          if constexpr (cc == 0) {
+#pragma unroll
+            for (int t = 0; t < NT3; ++t) acc3[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+          }
+#pragma unroll
+          for (int s = 0; s < 2; ++s) {
+            const typename A::Op ea = e_op(2 * cc + s);
+#pragma unroll
+            for (int t = 0; t < NT3; ++t) {
+              acc3[t] = A::mfma(ea, A::load(sb + (16 * t + li) * PS + 32 * s + 8 * g), acc3[t]);
+              if ((t & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+            }
+          }
+          if constexpr (ch == NA + NB + NC - 1) {
+            float wr[4];   // weights of pairs 4g + rr
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) wr[rr] = __shfl(wgt, 4 * g + rr, 64);
+#pragma unroll
+            for (int t = 0; t < NT3; ++t) {
+              const float bmo = sbm[16 * t + li];
+#pragma unroll
+              for (int rr = 0; rr < 4; ++rr) aggp[t] = fmaf(fmaxf(acc3[t][rr] + bmo, 0.f), wr[rr], aggp[t]);
+            }
+          }
+        } else {
+          // ---- D: causal head over edge-feature columns [64 (ch - NA - NB - NC), +64)
+          constexpr int cd = ch - NA - NB - NC;
+          if constexpr (cd == 0) {
+#pragma unroll
+            for (int t = 0; t < NT4; ++t) acc4[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+          }
+#pragma unroll
+          for (int s = 0; s < 2; ++s) {
+            const typename A::Op hb = e_op(2 * cd + s);
+#pragma unroll
+            for (int t = 0; t < NT4; ++t) {
+              acc4[t] = A::mfma(A::load(sb + (16 * t + li) * PS + 32 * s + 8 * g), hb, acc4[t]);
+              if ((t & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+            }
+          }
+          if constexpr (ch == NCH - 1) {
+            float s = 0.f;
+#pragma unroll
+            for (int t = 0; t < NT4; ++t)
+#pragma unroll
+              for (int rr = 0; rr < 4; ++rr) {
+                const int o = 16 * t + 4 * g + rr;
+                s = fmaf(fmaxf(acc4[t][rr] + sd1[o], 0.f), scc2[o], s);
+              }
+            s += __shfl_xor(s, 16, 64);
+            s += __shfl_xor(s, 32, 64);
+            if (g == 0 && j < N && live_row) {
+              const float alj = a.alive ? a.alive[rowj] : 1.f;
+              a.causal[rowi * N + j] = ali * alj / (1.f + __expf(-(s + a.d2[0])));
+            }
+          }
+        }
+        // the other buffer was last read in the previous chunk, before the barrier that ended it
+        store_chunk(ch + 1 < NCH ? ch + 1 : 0, cur ? sbuf0 : sbuf1);
+        __syncthreads();
+        cur ^= 1;
+      });
+    }
+    if constexpr (MSG) {
+#pragma unroll
+      for (int t = 0; t < NT3; ++t) {
+        float v = aggp[t];
+        v += __shfl_xor(v, 16, 64);
+        v += __shfl_xor(v, 32, 64);
+        if (g == 0 && live_row) a.agg[rowi * a.ldagg + 16 * t + li] = v;
+      }
+    }
+  }
+}
+
 // s = sum_k x[row, k], q = sum_k x[row, k]^2 for every row (one wave per row)
 __global__ void __launch_bounds__(256)
 gnn_node_stats_kernel(const float* __restrict__ x, int64_t ldx, float* __restrict__ st, int64_t rows, int D) {
@@ -752,8 +1092,41 @@ static int edges_res_shape(const GnnArgs& a, const float* nstat, hipStream_t st)
   return 0;
 }
 
+template <int DT, int D, int E, bool MSG, bool CAUS>
+static int launch_edges_str(const GnnArgs& a, const float* nstat, hipStream_t st) {
+  constexpr int NW = 4;   // one wave per SIMD: the accumulators can use the AGPRs
+  constexpr size_t lds = GnnStr<D, E, MSG, CAUS>::total;
+  static_assert(lds <= GNN_LDS_MAX, "chunk buffers exceed the LDS");
+  static int grid = 0;   // resident workgroups on the device (persistent kernel), found once
+  if (grid == 0) {
+    const void* fn = reinterpret_cast<const void*>(&gnn_edge_str_kernel<DT, D, E, NW, MSG, CAUS>);
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)GNN_LDS_MAX);
+    if (e != hipSuccess) return (int)e;
+    int dev = 0, cus = 0, per_cu = 0;
+    if ((e = hipGetDevice(&dev)) != hipSuccess) return (int)e;
+    if ((e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return (int)e;
+    if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 64 * NW, lds)) != hipSuccess) return (int)e;
+    grid = cus * (per_cu > 0 ? per_cu : 1);
+  }
+  const int64_t groups = ((int64_t)a.F * a.N + NW - 1) / NW;
+  const unsigned g = (unsigned)(groups < grid ? groups : grid);
+  hipLaunchKernelGGL((gnn_edge_str_kernel<DT, D, E, NW, MSG, CAUS>), dim3(g), dim3(64 * NW), lds, st, a, nstat);
+  HCLSM_LAUNCH_CHECK();
+  return 0;
+}
+
+template <int DT, int D, int E>
+static int edges_str_shape(const GnnArgs& a, const float* nstat, hipStream_t st) {
+  const bool msg = a.agg != nullptr, caus = a.causal != nullptr;
+  if (msg && caus) return launch_edges_str<DT, D, E, true, true>(a, nstat, st);
+  if (msg) return launch_edges_str<DT, D, E, true, false>(a, nstat, st);
+  if (caus) return launch_edges_str<DT, D, E, false, true>(a, nstat, st);
+  return 0;
+}
+
 template <int DT>
 static int launch_edges_resident(const GnnArgs& a, const float* nstat, hipStream_t st) {
+  if (a.D == 256 && a.E == 128) return edges_str_shape<DT, 256, 128>(a, nstat, st);
   if (a.D == 64 && a.E == 32) return edges_res_shape<DT, 64, 32>(a, nstat, st);
   if (a.D == 128 && a.E == 64) return edges_res_shape<DT, 128, 64>(a, nstat, st);
   if (a.D == 192 && a.E == 96) return edges_res_shape<DT, 192, 96>(a, nstat, st);
