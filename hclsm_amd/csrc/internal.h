@@ -28,3 +28,16 @@ int attn_slots_packed(const void* q, const void* k, const void* v, int64_t ldi, 
                       const int32_t* seg_rows, float scale, int dtype, hipStream_t st);
 
 }  // namespace hclsm
+
+#include <atomic>
+
+namespace hclsm {
+
+constexpr int HCLSM_MAX_DEVICES = 64;
+
+// Once per device and call site: raise the kernel's dynamic-LDS limit to max_lds (when max_lds > 0) and find how
+// many workgroups of `threads` threads using `lds` bytes the device holds at once (multiprocessors x occupancy).
+// cache: the call site's per-device slots (0 = not set up).  *grid gets the count.  Defined in launch.hip.
+int device_launch_setup(const void* fn, int threads, size_t lds, int max_lds, std::atomic<int>* cache, int* grid);
+
+}  // namespace hclsm

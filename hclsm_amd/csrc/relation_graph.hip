@@ -1024,14 +1024,12 @@ template <int DT, int NW, int KC>
 static int launch_edges_kc(const GnnArgs& a, hipStream_t st) {
   const int G = 16 * NW / a.NP;
   const int64_t tiles = (int64_t)a.F * ((a.N + G - 1) / G);
-  static bool big_lds = false;   // allow more than the default 64 KB of dynamic LDS (idempotent)
-  if (!big_lds) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gnn_edge_kernel<DT, NW, KC>),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    if (e != hipSuccess) return (int)e;
-    big_lds = true;
-  }
   const size_t lds = edge_lds<DT, NW, KC>(a);
+  static std::atomic<int> setup[HCLSM_MAX_DEVICES];   // more than the default 64 KB of dynamic LDS, per device
+  int unused;
+  const int se = device_launch_setup(reinterpret_cast<const void*>(&gnn_edge_kernel<DT, NW, KC>), 64 * NW, lds,
+                                     160 * 1024, setup, &unused);
+  if (se) return se;
   hipLaunchKernelGGL((gnn_edge_kernel<DT, NW, KC>), dim3((unsigned)tiles), dim3(64 * NW), lds, st, a);
   HCLSM_LAUNCH_CHECK();
   return 0;
@@ -1052,17 +1050,11 @@ static int launch_edges_res(const GnnArgs& a, const float* nstat, hipStream_t st
   constexpr int NW = 8;
   constexpr size_t lds = GnnRes<D, E, MSG, CAUS>::total;
   static_assert(lds <= GNN_LDS_MAX, "resident weights exceed the LDS");
-  static int grid = 0;   // resident workgroups on the device (persistent kernel), found once
-  if (grid == 0) {
-    const void* fn = reinterpret_cast<const void*>(&gnn_edge_res_kernel<DT, D, E, NW, MSG, CAUS>);
-    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)GNN_LDS_MAX);
-    if (e != hipSuccess) return (int)e;
-    int dev = 0, cus = 0, per_cu = 0;
-    if ((e = hipGetDevice(&dev)) != hipSuccess) return (int)e;
-    if ((e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return (int)e;
-    if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 64 * NW, lds)) != hipSuccess) return (int)e;
-    grid = cus * (per_cu > 0 ? per_cu : 1);
-  }
+  static std::atomic<int> setup[HCLSM_MAX_DEVICES];   // resident workgroups per device (persistent kernel)
+  int grid = 0;
+  const int se = device_launch_setup(reinterpret_cast<const void*>(&gnn_edge_res_kernel<DT, D, E, NW, MSG, CAUS>),
+                                     64 * NW, lds, (int)GNN_LDS_MAX, setup, &grid);
+  if (se) return se;
   const int64_t units = (int64_t)a.F * a.N;
   const int64_t need = (units + NW - 1) / NW;
   const unsigned g = (unsigned)(need < grid ? need : grid);
@@ -1097,17 +1089,11 @@ static int launch_edges_str(const GnnArgs& a, const float* nstat, hipStream_t st
   constexpr int NW = 4;   // one wave per SIMD: the accumulators can use the AGPRs
   constexpr size_t lds = GnnStr<D, E, MSG, CAUS>::total;
   static_assert(lds <= GNN_LDS_MAX, "chunk buffers exceed the LDS");
-  static int grid = 0;   // resident workgroups on the device (persistent kernel), found once
-  if (grid == 0) {
-    const void* fn = reinterpret_cast<const void*>(&gnn_edge_str_kernel<DT, D, E, NW, MSG, CAUS>);
-    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)GNN_LDS_MAX);
-    if (e != hipSuccess) return (int)e;
-    int dev = 0, cus = 0, per_cu = 0;
-    if ((e = hipGetDevice(&dev)) != hipSuccess) return (int)e;
-    if ((e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return (int)e;
-    if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 64 * NW, lds)) != hipSuccess) return (int)e;
-    grid = cus * (per_cu > 0 ? per_cu : 1);
-  }
+  static std::atomic<int> setup[HCLSM_MAX_DEVICES];   // resident workgroups per device (persistent kernel)
+  int grid = 0;
+  const int se = device_launch_setup(reinterpret_cast<const void*>(&gnn_edge_str_kernel<DT, D, E, NW, MSG, CAUS>),
+                                     64 * NW, lds, (int)GNN_LDS_MAX, setup, &grid);
+  if (se) return se;
   const int64_t groups = ((int64_t)a.F * a.N + NW - 1) / NW;
   const unsigned g = (unsigned)(groups < grid ? groups : grid);
   hipLaunchKernelGGL((gnn_edge_str_kernel<DT, D, E, NW, MSG, CAUS>), dim3(g), dim3(64 * NW), lds, st, a, nstat);

@@ -600,14 +600,12 @@ constexpr size_t TRK_LDS_MAX = 160 * 1024;
 
 template <int DT, int NW, int KC>
 static int launch_cost_kc(const TrackCostArgs& a, hipStream_t st) {
-  static bool big_lds = false;   // allow more than the default 64 KB of dynamic LDS (idempotent)
-  if (!big_lds) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&track_cost_kernel<DT, NW, KC>),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)TRK_LDS_MAX);
-    if (e != hipSuccess) return (int)e;
-    big_lds = true;
-  }
   const size_t lds = cost_lds<DT, NW, KC>(a.D);
+  static std::atomic<int> setup[HCLSM_MAX_DEVICES];   // more than the default 64 KB of dynamic LDS, per device
+  int unused;
+  const int se = device_launch_setup(reinterpret_cast<const void*>(&track_cost_kernel<DT, NW, KC>), 64 * NW, lds,
+                                     (int)TRK_LDS_MAX, setup, &unused);
+  if (se) return se;
   const int64_t tiles = (a.pairs + 16 * NW - 1) / (16 * NW);
   hipLaunchKernelGGL((track_cost_kernel<DT, NW, KC>), dim3((unsigned)tiles), dim3(64 * NW), lds, st, a);
   HCLSM_LAUNCH_CHECK();
@@ -618,19 +616,11 @@ template <int DT, int D, int NW>
 static int launch_cost_res(const TrackCostArgs& a, hipStream_t st) {
   using T = typename MM<DT>::T;
   constexpr size_t lds = ((size_t)D * (D + 8) + (size_t)(D / 4) * (D + 8)) * sizeof(T) + (size_t)(D / 4) * 8;
-  static int grid = 0;   // resident workgroups on the device (persistent kernel), found once
-  if (grid == 0) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&track_cost_res_kernel<DT, D, NW>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)TRK_LDS_MAX);
-    if (e != hipSuccess) return (int)e;
-    int dev = 0, cus = 0, per_cu = 0;
-    if ((e = hipGetDevice(&dev)) != hipSuccess) return (int)e;
-    if ((e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return (int)e;
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(
-                                                         &track_cost_res_kernel<DT, D, NW>), 64 * NW, lds);
-    if (e != hipSuccess) return (int)e;
-    grid = cus * (per_cu > 0 ? per_cu : 1);
-  }
+  static std::atomic<int> setup[HCLSM_MAX_DEVICES];   // resident workgroups per device (persistent kernel)
+  int grid = 0;
+  const int se = device_launch_setup(reinterpret_cast<const void*>(&track_cost_res_kernel<DT, D, NW>), 64 * NW, lds,
+                                     (int)TRK_LDS_MAX, setup, &grid);
+  if (se) return se;
   const int64_t nblk = (a.pairs + 32 * NW - 1) / (32 * NW);
   const unsigned g = (unsigned)(nblk < grid ? nblk : grid);
   hipLaunchKernelGGL((track_cost_res_kernel<DT, D, NW>), dim3(g), dim3(64 * NW), lds, st, a);
