@@ -160,6 +160,69 @@ __device__ __forceinline__ float ext_glu(const LinExt& e, int64_t row, int64_t c
 // K chunks of 128 (each global byte read once per workgroup), the next chunk's global loads in flight
 // while the current chunk is multiplied; each wave computes a 32x32 quadrant from LDS.  34 KB of LDS,
 // so several workgroups share a CU.
+// Epilogue of four consecutive output columns col .. col+3 of one row (columns past N skipped):
+// val = acc + bias, ReLU, gated-linear factor, + resid, clamp; stored to Y (and Y2).  With vec, every
+// row of Y / Y2 / resid / glu starts 16-byte aligned and the four columns are in range: one vector access each.
+template <int DT, int OT>
+__device__ __forceinline__ bool lin_vec4_ok(const void* Y, int64_t ldy, const void* Y2, int64_t ldy2,
+                                            const float* resid, int64_t ldr, const LinExt& e) {
+  auto al = [](const void* p, int64_t ld, int es) {
+    return p == nullptr || ((((uintptr_t)p) & 15) == 0 && (ld * es) % 16 == 0);
+  };
+  return al(Y, ldy, (int)sizeof(typename MM<OT>::T)) && al(Y2, ldy2, (int)sizeof(typename MM<DT>::T)) &&
+         al(resid, ldr, 4) && al(e.glu, e.ldg, (int)sizeof(typename MM<DT>::T));
+}
+
+template <int DT, int OT>
+__device__ __forceinline__ void lin_epilogue4(const f32x4& acc, const float (&bv)[4], int64_t row, int64_t col,
+                                              int64_t N, int relu, float clamp_v, const float* __restrict__ resid,
+                                              int64_t ldr, typename MM<OT>::T* __restrict__ Y, int64_t ldy,
+                                              typename MM<DT>::T* __restrict__ Y2, int64_t ldy2, const LinExt& e,
+                                              bool vec) {
+  using TD = typename MM<DT>::T;
+  using TO = typename MM<OT>::T;
+  float v[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    v[r] = acc[r] + bv[r];
+    if (relu) v[r] = fmaxf(v[r], 0.f);
+  }
+  if (vec && col + 3 < N) {
+    if (e.glu) {
+      TD gv[4];
+      *reinterpret_cast<uint2*>(gv) = *reinterpret_cast<const uint2*>(reinterpret_cast<const TD*>(e.glu) + row * e.ldg + col);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = silu_f(Cvt<TD>::f(gv[r])) * v[r];
+    }
+    if (resid) {
+      const float4 rv = *reinterpret_cast<const float4*>(resid + row * ldr + col);
+      v[0] += rv.x; v[1] += rv.y; v[2] += rv.z; v[3] += rv.w;
+    }
+    if (clamp_v > 0.f) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = fminf(fmaxf(v[r], -clamp_v), clamp_v);
+    }
+    TO o[4] = {MM<OT>::fromf(v[0]), MM<OT>::fromf(v[1]), MM<OT>::fromf(v[2]), MM<OT>::fromf(v[3])};
+    if constexpr (sizeof(TO) == 4) *reinterpret_cast<float4*>(Y + row * ldy + col) = *reinterpret_cast<float4*>(o);
+    else *reinterpret_cast<uint2*>(Y + row * ldy + col) = *reinterpret_cast<uint2*>(o);
+    if (Y2) {
+      TD o2[4] = {MM<DT>::fromf(v[0]), MM<DT>::fromf(v[1]), MM<DT>::fromf(v[2]), MM<DT>::fromf(v[3])};
+      if constexpr (sizeof(TD) == 4) *reinterpret_cast<float4*>(Y2 + row * ldy2 + col) = *reinterpret_cast<float4*>(o2);
+      else *reinterpret_cast<uint2*>(Y2 + row * ldy2 + col) = *reinterpret_cast<uint2*>(o2);
+    }
+    return;
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    if (col + r >= N) break;
+    float val = ext_glu<DT>(e, row, col + r, v[r]);
+    if (resid) val += resid[row * ldr + col + r];
+    if (clamp_v > 0.f) val = fminf(fmaxf(val, -clamp_v), clamp_v);
+    Y[row * ldy + col + r] = MM<OT>::fromf(val);
+    if (Y2) Y2[row * ldy2 + col + r] = MM<DT>::fromf(val);
+  }
+}
+
 // One 16-byte LDS unit (8 operand elements) of the A operand: loaded as is for 16-bit X, or as 8 fp32 values
 // rounded to the operand type when it is stored (fp32 X).
 template <int DT, typename XT>
@@ -252,10 +315,11 @@ linear_lds_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>::
       const typename A::Op a1 = A::load(As + (wr * 32 + 16 + li) * LT_LD + s * 32 + 8 * g);
       const typename A::Op b0 = A::load(Bs + (wc * 32 + li) * LT_LD + s * 32 + 8 * g);
       const typename A::Op b1 = A::load(Bs + (wc * 32 + 16 + li) * LT_LD + s * 32 + 8 * g);
-      acc[0][0] = A::mfma(a0, b0, acc[0][0]);
-      acc[0][1] = A::mfma(a0, b1, acc[0][1]);
-      acc[1][0] = A::mfma(a1, b0, acc[1][0]);
-      acc[1][1] = A::mfma(a1, b1, acc[1][1]);
+      // weights as the A operand: acc[ti][tj][r] = out[row 16 ti + li][col 16 tj + 4g + r]
+      acc[0][0] = A::mfma(b0, a0, acc[0][0]);
+      acc[0][1] = A::mfma(b1, a0, acc[0][1]);
+      acc[1][0] = A::mfma(b0, a1, acc[1][0]);
+      acc[1][1] = A::mfma(b1, a1, acc[1][1]);
     }
   }
   const int64_t r0 = tm * 64 + 32 * wr, c0 = tn * 64 + 32 * wc;
@@ -266,21 +330,21 @@ linear_lds_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>::
     T* Ts = As;
     __syncthreads();   // the last chunk is consumed
 #pragma unroll
-    for (int tj = 0; tj < 2; ++tj) {
-      const int64_t col = c0 + 16 * tj + li;
-      const float bv = (bias && col < N) ? bias[col] : 0.f;
+    for (int tj = 0; tj < 2; ++tj)
 #pragma unroll
-      for (int ti = 0; ti < 2; ++ti)
+      for (int r = 0; r < 4; ++r) {
+        const int64_t col = c0 + 16 * tj + 4 * g + r;
+        const float bv = (bias && col < N) ? bias[col] : 0.f;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int64_t row = r0 + 16 * ti + 4 * g + r;
+        for (int ti = 0; ti < 2; ++ti) {
+          const int64_t row = r0 + 16 * ti + li;
           float val = acc[ti][tj][r] + bv;
           if (relu) val = fmaxf(val, 0.f);
           if (resid && row < M && col < N) val += resid[row * ldr + col];
           if (clamp_v > 0.f) val = fminf(fmaxf(val, -clamp_v), clamp_v);
-          Ts[(32 * wc + 16 * tj + li) * TP + 32 * wr + 16 * ti + 4 * g + r] = MM<OT>::fromf(val);
+          Ts[(32 * wc + 16 * tj + 4 * g + r) * TP + 32 * wr + 16 * ti + li] = MM<OT>::fromf(val);
         }
-    }
+      }
     __syncthreads();
     typename MM<OT>::T* yt = reinterpret_cast<typename MM<OT>::T*>(os.yt);
     for (int i = tid; i < 64 * 64; i += 256) {
@@ -293,31 +357,40 @@ linear_lds_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>::
     }
     return;
   }
+  const bool vec = os.yt == nullptr && lin_vec4_ok<DT, OT>(Y, ldy, Y2, ldy2, resid, ldr, ext);
 #pragma unroll
   for (int tj = 0; tj < 2; ++tj) {
-    const int64_t col = c0 + 16 * tj + li;
-    if (col >= N) continue;
-    const float bv = bias ? bias[col] : 0.f;
+    const int64_t col = c0 + 16 * tj + 4 * g;
+    float bv[4];
 #pragma unroll
-    for (int ti = 0; ti < 2; ++ti)
+    for (int r = 0; r < 4; ++r) bv[r] = (bias && col + r < N) ? bias[col + r] : 0.f;
+#pragma unroll
+    for (int ti = 0; ti < 2; ++ti) {
+      const int64_t row = r0 + 16 * ti + li;
+      if (row >= M || col >= N) continue;
+      if (os.yt == nullptr) {
+        lin_epilogue4<DT, OT>(acc[ti][tj], bv, row, col, N, relu, clamp_v, resid, ldr, Y, ldy, Y2, ldy2, ext, vec);
+        continue;
+      }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int64_t row = r0 + 16 * ti + 4 * g + r;
-        if (row >= M) continue;
-        float val = acc[ti][tj][r] + bv;
+        const int64_t cr = col + r;
+        if (cr >= N) break;
+        float val = acc[ti][tj][r] + bv[r];
         if (relu) val = fmaxf(val, 0.f);
-        val = ext_glu<DT>(ext, row, col, val);
-        if (resid) val += resid[row * ldr + col];
+        val = ext_glu<DT>(ext, row, cr, val);
+        if (resid) val += resid[row * ldr + cr];
         if (clamp_v > 0.f) val = fminf(fmaxf(val, -clamp_v), clamp_v);
-        if (os.yt != nullptr && col >= os.col) {
+        if (cr >= os.col) {
           const int64_t fr = row / os.frame_rows, rr = row - fr * os.frame_rows;
-          reinterpret_cast<typename MM<OT>::T*>(os.yt)[fr * os.bstride + (col - os.col) * os.ldyt + rr] =
+          reinterpret_cast<typename MM<OT>::T*>(os.yt)[fr * os.bstride + (cr - os.col) * os.ldyt + rr] =
               MM<OT>::fromf(val);
         } else {
-          Y[row * ldy + col] = MM<OT>::fromf(val);
+          Y[row * ldy + cr] = MM<OT>::fromf(val);
         }
-        if (Y2) Y2[row * ldy2 + col] = A::fromf(val);
+        if (Y2) Y2[row * ldy2 + cr] = A::fromf(val);
       }
+    }
   }
 }
 
@@ -394,32 +467,28 @@ linear_lds128_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT
         a[t] = A::load(As + (wr * 64 + 16 * t + li) * LB_LD + s * 32 + 8 * g);
         b[t] = A::load(Bs + (wc * 64 + 16 * t + li) * LB_LD + s * 32 + 8 * g);
       }
+      // weights as the A operand: acc[ti][tj][r] = out[row 16 ti + li][col 16 tj + 4g + r], so a lane's four
+      // values are consecutive columns of one row (vector epilogue)
 #pragma unroll
       for (int ti = 0; ti < 4; ++ti)
 #pragma unroll
-        for (int tj = 0; tj < 4; ++tj) acc[ti][tj] = A::mfma(a[ti], b[tj], acc[ti][tj]);
+        for (int tj = 0; tj < 4; ++tj) acc[ti][tj] = A::mfma(b[tj], a[ti], acc[ti][tj]);
     }
   }
   const int64_t r0 = tm * 128 + 64 * wr, c0 = tn * 128 + 64 * wc;
+  const bool vec = lin_vec4_ok<DT, OT>(Y, ldy, Y2, ldy2, resid, ldr, ext);
 #pragma unroll
   for (int tj = 0; tj < 4; ++tj) {
-    const int64_t col = c0 + 16 * tj + li;
-    if (col >= N) continue;
-    const float bv = bias ? bias[col] : 0.f;
+    const int64_t col = c0 + 16 * tj + 4 * g;
+    float bv[4];
 #pragma unroll
-    for (int ti = 0; ti < 4; ++ti)
+    for (int r = 0; r < 4; ++r) bv[r] = (bias && col + r < N) ? bias[col + r] : 0.f;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t row = r0 + 16 * ti + 4 * g + r;
-        if (row >= M) continue;
-        float val = acc[ti][tj][r] + bv;
-        if (relu) val = fmaxf(val, 0.f);
-        val = ext_glu<DT>(ext, row, col, val);
-        if (resid) val += resid[row * ldr + col];
-        if (clamp_v > 0.f) val = fminf(fmaxf(val, -clamp_v), clamp_v);
-        Y[row * ldy + col] = MM<OT>::fromf(val);
-        if (Y2) Y2[row * ldy2 + col] = A::fromf(val);
-      }
+    for (int ti = 0; ti < 4; ++ti) {
+      const int64_t row = r0 + 16 * ti + li;
+      if (row >= M || col >= N) continue;
+      lin_epilogue4<DT, OT>(acc[ti][tj], bv, row, col, N, relu, clamp_v, resid, ldr, Y, ldy, Y2, ldy2, ext, vec);
+    }
   }
 }
 
