@@ -190,7 +190,9 @@ __device__ __forceinline__ void lin_epilogue4(const f32x4& acc, const float (&bv
   if (vec && col + 3 < N) {
     if (e.glu) {
       TD gv[4];
-      *reinterpret_cast<uint2*>(gv) = *reinterpret_cast<const uint2*>(reinterpret_cast<const TD*>(e.glu) + row * e.ldg + col);
+      const TD* gp = reinterpret_cast<const TD*>(e.glu) + row * e.ldg + col;
+      if constexpr (sizeof(TD) == 4) *reinterpret_cast<float4*>(gv) = *reinterpret_cast<const float4*>(gp);
+      else *reinterpret_cast<uint2*>(gv) = *reinterpret_cast<const uint2*>(gp);
 #pragma unroll
       for (int r = 0; r < 4; ++r) v[r] = silu_f(Cvt<TD>::f(gv[r])) * v[r];
     }
@@ -564,33 +566,29 @@ linear_lds_f32_kernel(const float* __restrict__ X, int64_t ldx, const float* __r
       for (int ti = 0; ti < 2; ++ti)
 #pragma unroll
         for (int tj = 0; tj < 2; ++tj) {
-          acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[ti].x, b[tj].x, acc[ti][tj], 0, 0, 0);
-          acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[ti].y, b[tj].y, acc[ti][tj], 0, 0, 0);
-          acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[ti].z, b[tj].z, acc[ti][tj], 0, 0, 0);
-          acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[ti].w, b[tj].w, acc[ti][tj], 0, 0, 0);
+          // weights as the A operand: acc[ti][tj][r] = out[row 16 ti + li][col 16 tj + 4g + r]
+          acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x4f32(b[tj].x, a[ti].x, acc[ti][tj], 0, 0, 0);
+          acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x4f32(b[tj].y, a[ti].y, acc[ti][tj], 0, 0, 0);
+          acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x4f32(b[tj].z, a[ti].z, acc[ti][tj], 0, 0, 0);
+          acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x4f32(b[tj].w, a[ti].w, acc[ti][tj], 0, 0, 0);
         }
     }
   }
   const int64_t r0 = tm * 64 + 32 * wr, c0 = tn * 64 + 32 * wc;
+  const bool vec = lin_vec4_ok<HCLSM_F32, OT>(Y, ldy, Y2, ldy2, resid, ldr, ext);
 #pragma unroll
   for (int tj = 0; tj < 2; ++tj) {
-    const int64_t col = c0 + 16 * tj + li;
-    if (col >= N) continue;
-    const float bv = bias ? bias[col] : 0.f;
+    const int64_t col = c0 + 16 * tj + 4 * g;
+    float bv[4];
 #pragma unroll
-    for (int ti = 0; ti < 2; ++ti)
+    for (int r = 0; r < 4; ++r) bv[r] = (bias && col + r < N) ? bias[col + r] : 0.f;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t row = r0 + 16 * ti + 4 * g + r;
-        if (row >= M) continue;
-        float val = acc[ti][tj][r] + bv;
-        if (relu) val = fmaxf(val, 0.f);
-        val = ext_glu<HCLSM_F32>(ext, row, col, val);
-        if (resid) val += resid[row * ldr + col];
-        if (clamp_v > 0.f) val = fminf(fmaxf(val, -clamp_v), clamp_v);
-        Y[row * ldy + col] = MM<OT>::fromf(val);
-        if (Y2) Y2[row * ldy2 + col] = val;
-      }
+    for (int ti = 0; ti < 2; ++ti) {
+      const int64_t row = r0 + 16 * ti + li;
+      if (row >= M || col >= N) continue;
+      lin_epilogue4<HCLSM_F32, OT>(acc[ti][tj], bv, row, col, N, relu, clamp_v, resid, ldr, Y, ldy, Y2, ldy2, ext,
+                                   vec);
+    }
   }
 }
 
