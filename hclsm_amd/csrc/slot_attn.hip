@@ -160,6 +160,15 @@ __device__ __forceinline__ float ext_glu(const LinExt& e, int64_t row, int64_t c
 // K chunks of 128 (each global byte read once per workgroup), the next chunk's global loads in flight
 // while the current chunk is multiplied; each wave computes a 32x32 quadrant from LDS.  34 KB of LDS,
 // so several workgroups share a CU.
+// Workgroup -> tile order that keeps consecutive tiles (which share rows of X) on one XCD: the dispatcher
+// deals workgroups to the 8 XCDs in turn, so XCD x receives blocks x, x + 8, ...; they take the x-th contiguous
+// share of the tiles (the first G % 8 XCDs one tile more).
+__device__ __forceinline__ int64_t xcd_tile(int64_t bid, int64_t G) {
+  constexpr int64_t NX = 8;
+  const int64_t x = bid % NX, k = bid / NX, per = G / NX, r = G % NX;
+  return x * per + (x < r ? x : r) + k;
+}
+
 // Epilogue of four consecutive output columns col .. col+3 of one row (columns past N skipped):
 // val = acc + bias, ReLU, gated-linear factor, + resid, clamp; stored to Y (and Y2).  With vec, every
 // row of Y / Y2 / resid / glu starts 16-byte aligned and the four columns are in range: one vector access each.
@@ -265,7 +274,9 @@ linear_lds_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>::
   __shared__ __align__(16) T As[64 * LT_LD];
   __shared__ __align__(16) T Bs[64 * LT_LD];
   const int64_t tiles_n = (N + 63) / 64;
-  const int64_t tm = blockIdx.x / tiles_n, tn = blockIdx.x - tm * tiles_n;
+  // (a device-side row count leaves only the leading tiles live: keep them spread over the XCDs)
+  const int64_t tile = ext.m_dev ? (int64_t)blockIdx.x : xcd_tile(blockIdx.x, gridDim.x);
+  const int64_t tm = tile / tiles_n, tn = tile - tm * tiles_n;
   M = ext_rows(ext, M);
   if (tm * 64 >= M) return;   // the whole workgroup, before any barrier
   const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, g = lane >> 4, li = lane & 15;
@@ -415,7 +426,9 @@ linear_lds128_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT
   __shared__ __align__(16) T As[128 * LB_LD];
   __shared__ __align__(16) T Bs[128 * LB_LD];
   const int64_t tiles_n = (N + 127) / 128;
-  const int64_t tm = blockIdx.x / tiles_n, tn = blockIdx.x - tm * tiles_n;
+  // (a device-side row count leaves only the leading tiles live: keep them spread over the XCDs)
+  const int64_t tile = ext.m_dev ? (int64_t)blockIdx.x : xcd_tile(blockIdx.x, gridDim.x);
+  const int64_t tm = tile / tiles_n, tn = tile - tm * tiles_n;
   M = ext_rows(ext, M);
   if (tm * 128 >= M) return;   // the whole workgroup, before any barrier
   const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, g = lane >> 4, li = lane & 15;
@@ -510,7 +523,9 @@ linear_lds_f32_kernel(const float* __restrict__ X, int64_t ldx, const float* __r
   __shared__ __align__(16) float As[64 * LF_LD];
   __shared__ __align__(16) float Bs[64 * LF_LD];
   const int64_t tiles_n = (N + 63) / 64;
-  const int64_t tm = blockIdx.x / tiles_n, tn = blockIdx.x - tm * tiles_n;
+  // (a device-side row count leaves only the leading tiles live: keep them spread over the XCDs)
+  const int64_t tile = ext.m_dev ? (int64_t)blockIdx.x : xcd_tile(blockIdx.x, gridDim.x);
+  const int64_t tm = tile / tiles_n, tn = tile - tm * tiles_n;
   M = ext_rows(ext, M);
   if (tm * 64 >= M) return;   // the whole workgroup, before any barrier
   const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, g = lane >> 4, li = lane & 15;
