@@ -102,3 +102,17 @@ def test_fused_shape_limits():
     assert fused_supported(128, 384, 192, torch.bfloat16)        # large preset (config.py:270): 32-column chunks
     assert not fused_supported(128, 384, 192, torch.float32)     # fp32 tiles hold 64 pairs
     assert not fused_supported(32, 200, 96, torch.bfloat16)      # D not a multiple of 32
+
+
+@pytest.mark.parametrize("F,N,D,E,rounds,chunked", [CASES[0], CASES[1], (2, 64, 256, 128, 2, True), CASES[4]])
+def test_relation_graph_fp16_matches_oracle(F, N, D, E, rounds, chunked):
+    """fp16 operands through the same kernels (resident, streamed and chunked variants)."""
+    from hclsm_amd.kernels.relation_graph import GnnWeights, relation_graph_forward
+    m = _module(D, E, rounds, N, F + N + 2)
+    x, alive = _inputs(F, N, D, seed=N + D + 2)
+    W = GnnWeights.from_module(m, torch.float16)
+    out, causal = relation_graph_forward(x, alive, W, rounds, chunked=chunked)
+    p = {k: _np(v) for k, v in m.state_dict().items()}
+    ref, rc = ob.relation_graph_ref(_np(x), _np(alive), p, rounds, chunked=chunked)
+    assert normwise_rel_err(_np(out), ref) <= 1e-2
+    assert normwise_rel_err(_np(causal), rc) <= 1e-2

@@ -277,3 +277,27 @@ def test_shape_limits():
     assert not track_supported(129, 192, torch.float32, sequence=True)
     assert not track_supported(32, 96, torch.float32)
     assert not track_supported(32, 448, torch.bfloat16)
+
+
+@pytest.mark.parametrize("F,N,D", [COST_CASES[1], COST_CASES[3], COST_CASES[4]])
+def test_cost_fp16_matches_oracle(F, N, D):
+    """fp16 operands: the weight-resident kernel (D <= 192) and the chunked one."""
+    from hclsm_amd.kernels.slot_tracker import TrackerWeights, track_cost
+    m = _module(D, N, seed=F + N + D + 3)
+    a, b, at, at1 = _slots(F, N, D, seed=N + D + 3)
+    W = TrackerWeights.from_module(m, torch.float16)
+    cost = track_cost(a, b, at, at1, W)
+    ref = ob.tracker_cost_ref(_np(a), _np(b), _np(at), _np(at1), _params(m))
+    _check_cost(_np(cost), ref, _np(at), _np(at1), 1e-2)
+
+
+def test_sequence_fp16_matches_oracle():
+    from hclsm_amd.kernels.slot_tracker import TrackerWeights, track_sequence
+    B, T, N, D = 2, 5, 32, 192
+    m = _module(D, N, seed=31, discriminative=True)
+    x, alive = _clip(B, T, N, D, seed=32)
+    W = TrackerWeights.from_module(m, torch.float16)
+    r = track_sequence(x, alive, W, with_hidden=True)
+    rt, ra, rh = ob.track_sequence_ref(_np(x), _np(alive), _params(m))
+    assert (_np(r["tracked"]) == rt).all() and (_np(r["alive"]) == ra).all()
+    assert normwise_rel_err(_np(r["hidden"]), rh) <= 1e-2
