@@ -32,6 +32,12 @@ adds tens of microseconds of Python dispatch per call, which is the size of the 
     hclsm_hip::level1_forward(ev, stats, rows, obj_mask?, params, n_heads, ln_eps, compute_dtype) -> fp32
         Level1EventDynamics over the live packed events (level1_event.py:17-133); params in the order of
         Level1Weights (4 + 9 per layer); rows past the live count are zero
+    hclsm_hip::relation_graph_forward(nodes, alive?, params, n_rounds, chunked, ln_eps, compute_dtype)
+        -> (nodes', causal) fp32: RelationGraph.forward (objects/relation_graph.py:68-193); params in the
+        module's state-dict order (18 tensors)
+    hclsm_hip::slot_track_sequence(slots, alive?, params, with_hidden, n_iters, temperature, compute_dtype)
+        -> (tracked, alive', perm, matched, hidden): the tracking loop of model.py:229-252 over
+        SlotTracker's 10 tensors (state-dict order); alive' is empty without alive, hidden without with_hidden
 """
 
 from __future__ import annotations
@@ -46,6 +52,8 @@ from hclsm_amd.kernels.event_attention import event_attention as _event_attentio
 from hclsm_amd.kernels.slot_attention_kernel import _core_raw
 from hclsm_amd.kernels.slot_iteration import SlotMode, SlotWeights, slot_attention_forward as _slot_forward
 from hclsm_amd.kernels.level1_packed import Level1Weights, level1_forward_packed
+from hclsm_amd.kernels.relation_graph import GNN_PARAM_ORDER, GnnWeights, relation_graph_forward as _gnn_forward
+from hclsm_amd.kernels.slot_tracker import TRACK_PARAM_ORDER, TrackerWeights, track_sequence as _track_sequence
 from hclsm_amd.kernels.sparse_event_attn import (EventIndex, _gather_padded_raw, _mask_code, _scatter_padded_raw,
                                                  gather_packed, scatter_packed)
 from hclsm_amd.kernels.ssm_scan_bwd import scan_backward
@@ -246,3 +254,44 @@ def level1_forward(ev: Tensor, stats: Tensor, rows: Tensor, obj_mask: Optional[T
 @level1_forward.register_fake
 def _(ev, stats, rows, obj_mask, params, n_heads, ln_eps, compute_dtype):
     return ev.new_empty(ev.shape, dtype=torch.float32)
+
+
+# --------------------------------------------------------------------------- object layer
+
+@torch.library.custom_op("hclsm_hip::relation_graph_forward", mutates_args=())
+def relation_graph_forward(nodes: Tensor, alive: Optional[Tensor], params: list[Tensor], n_rounds: int,
+                           chunked: bool, ln_eps: float, compute_dtype: torch.dtype) -> tuple[Tensor, Tensor]:
+    if len(params) != len(GNN_PARAM_ORDER):
+        raise ValueError(f"relation_graph_forward: {len(GNN_PARAM_ORDER)} parameters in state-dict order")
+    W = GnnWeights.from_dict(dict(zip(GNN_PARAM_ORDER, params)), compute_dtype, float(ln_eps), nodes.device)
+    return _gnn_forward(nodes, alive, W, int(n_rounds), chunked=bool(chunked))
+
+
+@relation_graph_forward.register_fake
+def _(nodes, alive, params, n_rounds, chunked, ln_eps, compute_dtype):
+    F, N, D = nodes.shape
+    return nodes.new_empty((F, N, D), dtype=torch.float32), nodes.new_empty((F, N, N), dtype=torch.float32)
+
+
+@torch.library.custom_op("hclsm_hip::slot_track_sequence", mutates_args=())
+def slot_track_sequence(slots: Tensor, alive: Optional[Tensor], params: list[Tensor], with_hidden: bool,
+                        n_iters: int, temperature: float,
+                        compute_dtype: torch.dtype) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    if len(params) != len(TRACK_PARAM_ORDER):
+        raise ValueError(f"slot_track_sequence: {len(TRACK_PARAM_ORDER)} parameters in state-dict order")
+    W = TrackerWeights.from_dict(dict(zip(TRACK_PARAM_ORDER, params)), compute_dtype, slots.device)
+    r = _track_sequence(slots, alive, W, with_hidden=bool(with_hidden), n_iters=int(n_iters),
+                        temperature=float(temperature))
+    empty = slots.new_empty((0,), dtype=torch.float32)
+    return (r["tracked"], r["alive"] if r["alive"] is not None else empty, r["perm"], r["matched"],
+            r["hidden"] if r["hidden"] is not None else empty)
+
+
+@slot_track_sequence.register_fake
+def _(slots, alive, params, with_hidden, n_iters, temperature, compute_dtype):
+    B, T, N, D = slots.shape
+    f32 = dict(dtype=torch.float32)
+    return (slots.new_empty((B, T, N, D), **f32),
+            slots.new_empty((B, T, N) if alive is not None else (0,), **f32),
+            slots.new_empty((B, T, N), dtype=torch.int64), slots.new_empty((B, T, N), **f32),
+            slots.new_empty((B, N, D) if with_hidden else (0,), **f32))

@@ -56,3 +56,14 @@ def test_ops_under_fake_tensor_mode():
         x = torch.empty(2, 8, 32)
         y, _ = OPS.ssm_scan_fwd(x, x, torch.empty(32, 16), torch.empty(2, 8, 16), torch.empty(2, 8, 16), None, 0, False)
         assert y.shape == (2, 8, 32)
+
+
+def test_object_layer_ops_fake_shapes():
+    nodes, causal = OPS.relation_graph_forward(_m(6, 16, 64), _m(6, 16), [_m(1)] * 18, 2, False, 1e-5, torch.bfloat16)
+    assert nodes.shape == (6, 16, 64) and causal.shape == (6, 16, 16) and causal.dtype == torch.float32
+    t, a, p, mt, h = OPS.slot_track_sequence(_m(2, 5, 16, 64), _m(2, 5, 16), [_m(1)] * 10, True, 20, 0.05,
+                                             torch.bfloat16)
+    assert [tuple(x.shape) for x in (t, a, p, mt, h)] == [(2, 5, 16, 64), (2, 5, 16), (2, 5, 16), (2, 5, 16), (2, 16, 64)]
+    assert p.dtype == torch.int64
+    _, a0, _, _, h0 = OPS.slot_track_sequence(_m(2, 5, 16, 64), None, [_m(1)] * 10, False, 20, 0.05, torch.float32)
+    assert a0.shape == (0,) and h0.shape == (0,)

@@ -113,3 +113,32 @@ def test_packed_level1_ops_equal_eager():
                           test_utils=("test_schema", "test_faketensor"))
     torch.library.opcheck(OPS.level1_forward.default, (evo, t[5], t[3], obj, W.tensors, 4, W.ln_eps, torch.float32),
                           test_utils=("test_schema", "test_faketensor"))
+
+
+def test_object_layer_ops_equal_eager():
+    """hclsm_hip::relation_graph_forward / slot_track_sequence against the module calls, and opcheck of their
+    schemas and fake kernels."""
+    from types import SimpleNamespace
+    from hclsm_amd.objects import RelationGraph, SlotTracker
+    torch.manual_seed(14)
+    cfg = SimpleNamespace(d_slot=64, d_edge=32, gnn_rounds=2, n_max_slots=16)
+    rg, trk = RelationGraph(cfg).cuda(), SlotTracker(cfg).cuda()
+    g = torch.Generator().manual_seed(15)
+    nodes = torch.randn(4, 16, 64, generator=g).cuda()
+    alive = (torch.rand(4, 16, generator=g) > 0.25).float().cuda()
+    slots = torch.randn(2, 5, 16, 64, generator=g).cuda()
+    salive = (torch.rand(2, 5, 16, generator=g) > 0.2).float().cuda()
+    gp = [p.detach() for p in rg.state_dict().values()]
+    tp = [p.detach() for p in trk.state_dict().values()]
+    with torch.no_grad():
+        wn, wc = rg(nodes, alive)
+        gn, gc = OPS.relation_graph_forward(nodes, alive, gp, 2, False, rg.pair_norm.eps, torch.float32)
+        assert torch.equal(gn, wn) and torch.equal(gc, wc)
+        wt, wa, wh = trk.track(slots, salive, return_hidden=True)
+        t, a, p, mt, h = OPS.slot_track_sequence(slots, salive, tp, True, 20, 0.05, torch.float32)
+        assert torch.equal(t, wt) and torch.equal(a, wa) and torch.equal(h, wh)
+        assert torch.equal(torch.gather(slots, 2, p[..., None].expand_as(slots)), t)
+    torch.library.opcheck(OPS.relation_graph_forward.default, (nodes, alive, gp, 2, False, 1e-5, torch.float32),
+                          test_utils=("test_schema", "test_faketensor"))
+    torch.library.opcheck(OPS.slot_track_sequence.default, (slots, salive, tp, True, 20, 0.05, torch.float32),
+                          test_utils=("test_schema", "test_faketensor"))
