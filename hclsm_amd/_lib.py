@@ -38,6 +38,9 @@ _SIGNATURES: dict[str, list] = {
     "hclsm_event_gather_packed": [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64] + [_c_void_p] * 3 + [_c_void_p],
     "hclsm_event_scatter": [_c_void_p] * 3 + [_i64] * 4 + [_c_void_p, _c_void_p],
     "hclsm_event_scatter_packed": [_c_void_p] * 3 + [_i64] * 3 + [_c_void_p, _c_void_p, _c_void_p],
+    "hclsm_event_top_down_workspace": [_i64, _i64],
+    "hclsm_event_top_down": [_c_void_p] * 4 + [_i64, _c_void_p, _i64, _i64] + [_c_void_p] * 4 + [_i64] +
+                            [_c_void_p] * 2 + [_i64] * 4 + [_int, _c_void_p, _i64, _c_void_p],
     "hclsm_event_attention": [_c_void_p] * 8 + [_i64] * 5 + [_f32, _int, _int, _c_void_p],
     "hclsm_layer_norm": [_c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _f32, _int, _int,
                          _c_void_p],
@@ -75,7 +78,8 @@ _RESTYPES = {"hclsm_strerror": ctypes.c_char_p, "hclsm_slot_attn_core_workspace"
              "hclsm_slot_attention_workspace": ctypes.c_int64, "hclsm_level1_forward_workspace": ctypes.c_int64,
              "hclsm_relation_graph_workspace": ctypes.c_int64, "hclsm_slot_track_cost_workspace": ctypes.c_int64,
              "hclsm_slot_track_reorder_update_workspace": ctypes.c_int64,
-             "hclsm_slot_track_sequence_workspace": ctypes.c_int64}
+             "hclsm_slot_track_sequence_workspace": ctypes.c_int64,
+             "hclsm_event_top_down_workspace": ctypes.c_int64}
 
 
 class HclsmSlotWeights(ctypes.Structure):

@@ -60,7 +60,9 @@ __device__ __forceinline__ void stage_rows(const T* __restrict__ W, int ldw, int
 // stride ldw) is staged through sW (pitch KC + 8) in KC-column chunks; a_frag(k, op) gives this lane's KE
 // operand elements at column k (k = kb + KE*g of the current block).  Every thread of the workgroup calls
 // it (it holds barriers); the first barrier also orders any LDS writes made before the call.
-template <int DT, int KC, int NTH, int NTMAX, typename AF>
+// Output layout: acc[t][r] is operand row 4g + r, W row t*16 + li; with WA (W as the MFMA's A operand) it is
+// operand row li, W row t*16 + 4g + r, so a lane holds four consecutive outputs of one operand row.
+template <int DT, int KC, int NTH, int NTMAX, bool WA = false, typename AF>
 __device__ __forceinline__ void tile_gemm(f32x4 (&acc)[NTMAX], int NT, const typename MM<DT>::T* W, int ldw, int K,
                                           typename MM<DT>::T* sW, int tid, AF&& a_frag) {
   using T = typename MM<DT>::T;
@@ -80,7 +82,7 @@ __device__ __forceinline__ void tile_gemm(f32x4 (&acc)[NTMAX], int NT, const typ
         if (t < NT) {
           T wb[KE];
           frag_load<DT>(sW + (t * 16 + li) * PW + kb + KE * g, wb);
-          acc[t] = frag_mma<DT>(op, wb, acc[t]);
+          acc[t] = WA ? frag_mma<DT>(wb, op, acc[t]) : frag_mma<DT>(op, wb, acc[t]);
         }
       }
     }

@@ -1,10 +1,14 @@
 """Hierarchy manager on MI355X: counterpart of hclsm/dynamics/hierarchy_manager.py.
 
 gather_events / scatter_events run on the device-built int32 event index and the byte-exact
-gather / scatter kernels (rule mask > 0.5, ascending event order, exact zero padding); the
-top-down gating of forward() is unchanged torch math.  gather_events still returns K_max as a
-Python int, as the reference does (:63), which costs one host read of the index statistics;
-the packed counterparts (gather_events_packed, forward_packed, level1_events_packed) need none.
+gather / scatter kernels (rule mask > 0.5, ascending event order, exact zero padding).  Without
+autograd, forward() and forward_packed() on fp32 states are one hclsm_event_top_down call: the
+scatter, the Level-2 top-down gate and its blend, and the alive mask in one pass over the rows, the
+gate GEMM in fp32, or in bf16 / fp16 operands under an autocast of that type.  With autograd (or
+shapes outside that kernel) the gating is the reference's torch math.  gather_events still returns
+K_max as a Python int, as the reference does (:63), which costs one host read of the index
+statistics; the packed counterparts (gather_events_packed, forward_packed, level1_events_packed)
+need none.
 """
 
 from __future__ import annotations
@@ -15,6 +19,7 @@ import torch.nn as nn
 from hclsm_amd.kernels.sparse_event_attn import (EventIndex, build_event_index, gather_events_packed,
                                                  gather_events_padded, pad_mask_from_index,
                                                  scatter_events_packed, scatter_events_padded)
+from hclsm_amd.kernels.top_down import TopDownWeights, event_top_down, top_down_supported
 
 
 class HierarchyManager(nn.Module):
@@ -39,8 +44,31 @@ class HierarchyManager(nn.Module):
         return scatter_events_padded(base_states, event_updates, idx)
 
     def forward(self, level0_states, level1_states, level2_context, event_mask, obj_mask=None):
+        if self._fused_ok(level0_states, level1_states, level2_context, obj_mask):
+            idx = build_event_index(event_mask, "gt_half")
+            return self._fused(level0_states, level1_states, idx, level2_context, obj_mask,
+                               kpad=max(level1_states.shape[1], 1))
         combined = self.scatter_events(level0_states, level1_states, event_mask)      # :143
         return self._top_down(combined, level2_context, obj_mask)
+
+    # ---- fused output step (hclsm_event_top_down)
+
+    def _fused_ok(self, level0_states, level1_states, level2_context, obj_mask) -> bool:
+        xs = (level0_states, level1_states, level2_context, obj_mask)
+        if torch.is_grad_enabled() and (any(x is not None and x.requires_grad for x in xs) or
+                                        any(p.requires_grad for p in self.parameters())):
+            return False
+        if not level0_states.is_cuda or level0_states.dtype != torch.float32 or level1_states.shape[1] == 0:
+            return False
+        dl2 = None if level2_context is None else level2_context.shape[-1]
+        return top_down_supported(level0_states.shape[-1], dl2)
+
+    def _fused(self, level0_states, level1_states, idx, level2_context, obj_mask, kpad):
+        dtype = torch.float32
+        if torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") in (torch.bfloat16, torch.float16):
+            dtype = torch.get_autocast_dtype("cuda")
+        W = TopDownWeights.from_module(self, dtype) if level2_context is not None else None
+        return event_top_down(level0_states, level1_states, idx, W, level2_context, obj_mask, kpad=kpad)
 
     def _top_down(self, combined, level2_context, obj_mask):
         if level2_context is not None:                                                # :146-156
@@ -63,6 +91,8 @@ class HierarchyManager(nn.Module):
     def forward_packed(self, level0_states, level1_packed, index: EventIndex, level2_context=None,
                        obj_mask=None):
         """forward() with Level-1 outputs in the packed layout of gather_events_packed."""
+        if self._fused_ok(level0_states, level1_packed, level2_context, obj_mask):
+            return self._fused(level0_states, level1_packed, index, level2_context, obj_mask, kpad=0)
         combined = scatter_events_packed(level0_states, level1_packed, index)
         return self._top_down(combined, level2_context, obj_mask)
 

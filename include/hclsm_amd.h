@@ -171,6 +171,31 @@ int hclsm_event_scatter_packed(const void* base, const void* packed, void* out, 
                                void* stream);
 
 /*
+ * Hierarchy manager output step: HierarchyManager.forward (hierarchy_manager.py:120-162) after the
+ * Level-1 pass, fused.  All states fp32, rows of D floats, 16-byte aligned:
+ *   level0  [B, T, N, D]; events: the Level-1 rows, packed [capacity, N, D] at offsets[b] + slot_of[b, t]
+ *   (kpad == 0) or padded [B, kpad, N, D] at slot_of[b, t] < kpad (kpad > 0; later events keep level0).
+ *   combined = event row at events, level0 elsewhere (the scatter, :143).
+ *   With level2_context [B, S2, DL2] (nullable):
+ *     l2 = W_l2 mean_s(level2_context)   (W_l2 = l2_to_l1.weight [D, DL2], :147-152)
+ *     gate = sigmoid(W_gate [combined; l2] + b_gate)   (W_gate [D, 2D], b_gate [D] nullable, :153-154)
+ *     combined = gate * l2 + (1 - gate) * combined   (:155)
+ *   the gate GEMM runs in `dtype` (f32 / bf16 / f16 operands, fp32 accumulation) on W_gate_x, a copy of
+ *   W_gate[:, :D] in that type with row stride ldw (for f32 it may be W_gate itself, ldw = 2D); l2 and the
+ *   Level-2 half of the gate are fp32.
+ *   out = combined * obj_mask[b, n] (obj_mask [B, N] nullable, :159-160).  out may alias level0.
+ * ws: hclsm_event_top_down_workspace(B, D) bytes, 16-byte aligned (needed with a level2_context).
+ * D a multiple of 32 up to 384 (HCLSM_ERR_UNSUPPORTED otherwise).
+ */
+int64_t hclsm_event_top_down_workspace(int64_t B, int64_t D);
+int hclsm_event_top_down(const float* level0, const float* events, const int32_t* offsets,
+                         const int32_t* slot_of, int64_t kpad, const float* level2_context, int64_t S2,
+                         int64_t DL2, const float* W_l2, const float* W_gate, const float* b_gate,
+                         const void* W_gate_x, int64_t ldw, const float* obj_mask, float* out, int64_t B,
+                         int64_t T, int64_t N, int64_t D, int dtype, void* ws, int64_t ws_bytes,
+                         void* stream);
+
+/*
  * Variable-length attention over event segments, on MFMA.
  *   q, k, v   [nseg, T, H, dh]  element type `dtype` (bf16 / f16 / f32), contiguous
  *   offsets   [nseg+1], indices [>= offsets[nseg]]  int32 (an event index: segment p is the rows

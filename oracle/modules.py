@@ -8,13 +8,14 @@ state dicts):
   event_block_ref           hclsm/dynamics/level1_event.py:44-54 (MHA over slots + SwiGLU)
   level1_ref                hclsm/dynamics/level1_event.py:85-133
   event_mask_rule_ref       hclsm/dynamics/event_detector.py:160-170
+  hierarchy_forward_ref     hclsm/dynamics/hierarchy_manager.py:120-162 (scatter, Level-2 gate, alive mask)
 """
 
 from __future__ import annotations
 
 import numpy as np
 
-from oracle.events import slots_attention
+from oracle.events import scatter, slots_attention
 from oracle.slot_attention import layer_norm, sigmoid
 from oracle.ssm_scan import ssm_scan_ref
 
@@ -110,3 +111,24 @@ def event_mask_rule_ref(probs, threshold_logit):
     if mask.shape[1] and hard.sum(1).min() == 0:
         mask[:, 0] = 1.0
     return mask
+
+
+def hierarchy_forward_ref(level0, level1, index, w_l2, w_gate, b_gate=None, level2_context=None, obj_mask=None):
+    """HierarchyManager.forward (hierarchy_manager.py:120-162).  level0 (B, T, N, D); level1 (B, K, N, D) padded
+    Level-1 rows; index an oracle.events.event_index of the mask; w_l2 = l2_to_l1.weight (D, d_l2);
+    w_gate / b_gate = gate_l2_l0.0 (D, 2D) / (D,).
+      combined = scatter of the Level-1 rows into level0                         (:143)
+      l2 = l2_to_l1(mean over summaries of level2_context), broadcast           (:147-152)
+      gate = sigmoid(W_gate [combined; l2] + b_gate)                             (:153-154)
+      combined = gate * l2 + (1 - gate) * combined                               (:155)
+      out = combined * obj_mask[b, None, n, None]                                (:159-160)"""
+    combined = scatter(np.asarray(level0, np.float64), np.asarray(level1, np.float64), index)
+    if level2_context is not None:
+        ctx = np.asarray(level2_context, np.float64)
+        l2 = _lin(ctx.mean(axis=1), w_l2)                                        # (B, D)
+        l2b = np.broadcast_to(l2[:, None, None, :], combined.shape)
+        gate = sigmoid(_lin(np.concatenate([combined, l2b], axis=-1), w_gate, b_gate))
+        combined = gate * l2b + (1.0 - gate) * combined
+    if obj_mask is not None:
+        combined = combined * np.asarray(obj_mask, np.float64)[:, None, :, None]
+    return combined

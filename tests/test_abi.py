@@ -125,3 +125,29 @@ def test_slot_tracker_argument_errors_before_launch(lib):
     r = lib.hclsm_slot_track_reorder_update
     assert r(*[None] * 6, 2, 32, 192, None, 1, None, 0, None) == -1
     assert r(*[None] * 6, 2, 32, 64, None, 5, None, 0, None) == -3
+
+
+def test_top_down_argument_errors_before_launch(lib):
+    assert lib.hclsm_event_top_down_workspace(-1, 192) == -2
+    assert lib.hclsm_event_top_down_workspace(32, 192) == 2 * 32 * 192 * 4
+    f = lib.hclsm_event_top_down
+    P = 256   # stand-in address: every call below returns before anything is launched
+
+    def call(B=2, T=8, N=32, D=192, dtype=1, ev=P, kpad=0, offs=P, ctx=None, S2=4, DL2=512, wx=P, ldw=192,
+             ws=P, ws_bytes=1 << 20):
+        return f(P, ev, offs, P, kpad, ctx, S2, DL2, P, P, None, wx, ldw, None, P, B, T, N, D, dtype, ws,
+                 ws_bytes, None)
+    assert call(B=-1) == -2
+    assert call(kpad=-1) == -2
+    assert call(dtype=9) == -3
+    assert call(D=100) == -4                              # d_slot not a multiple of 32
+    assert call(D=416) == -4                              # d_slot above 384
+    assert call(B=0) == 0                                 # nothing to do
+    assert call(ev=None) == -1
+    assert call(offs=None) == -1                          # packed rows need the offsets
+    assert call(ctx=P, S2=0) == -2
+    assert call(ctx=P, DL2=16384) == -4                   # the prologue's vectors exceed 64 KB of LDS
+    assert call(ctx=P, wx=None) == -1
+    assert call(ctx=P, ldw=100) == -2
+    assert call(ctx=P, ws_bytes=16) == -2
+    assert call(ctx=P, wx=P + 2) == -4                    # operand rows must be 16-byte aligned

@@ -71,3 +71,62 @@ def test_event_mask_rule_cases():
     np.testing.assert_array_equal(m, [[0, 1, 0], [1, 0, 1]])
     probs2 = np.array([[0.1, 0.2, 0.3], [0.1, 0.9, 0.1]])   # row 0 empty -> column 0 set in every row
     np.testing.assert_array_equal(om.event_mask_rule_ref(probs2, tl), [[1, 0, 0], [1, 1, 0]])
+
+
+def _hier_case(B=3, T=9, N=5, D=8, DL2=12, S2=3, p=0.4, seed=0):
+    g = np.random.default_rng(seed)
+    mask = (g.random((B, T)) < p).astype(np.float32)
+    mask[0, :] = 1.0            # a clip whose every frame is an event
+    mask[1, :] = 0.0            # a clip with none
+    K = max(int(mask.sum(axis=1).max()), 1)
+    return (g.standard_normal((B, T, N, D)), g.standard_normal((B, K, N, D)), mask,
+            g.standard_normal((B, S2, DL2)), (g.random((B, N)) < 0.7).astype(np.float64))
+
+
+def test_hierarchy_forward_against_torch_modules():
+    """hierarchy_manager.py:120-162 built from nn.Linear / nn.Sigmoid with the same weights, the scatter as a
+    loop over each clip's events in ascending t."""
+    from oracle.events import event_index
+    torch.manual_seed(1)
+    level0, level1, mask, ctx, obj = _hier_case()
+    B, T, N, D = level0.shape
+    l2_to_l1 = nn.Linear(ctx.shape[2], D, bias=False).double()
+    gate = nn.Sequential(nn.Linear(2 * D, D), nn.Sigmoid()).double()
+    comb = torch.tensor(level0)
+    for b in range(B):
+        for k, t in enumerate(np.nonzero(mask[b] > 0.5)[0]):
+            comb[b, t] = torch.tensor(level1[b, k])
+    l2b = l2_to_l1(torch.tensor(ctx).mean(dim=1))[:, None, None, :].expand_as(comb)
+    gv = gate(torch.cat([comb, l2b], dim=-1))
+    want = ((gv * l2b + (1 - gv) * comb) * torch.tensor(obj)[:, None, :, None]).detach().numpy()
+    got = om.hierarchy_forward_ref(level0, level1, event_index(mask), l2_to_l1.weight.detach().numpy(),
+                                   gate[0].weight.detach().numpy(), gate[0].bias.detach().numpy(), ctx, obj)
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+def test_hierarchy_forward_closed_forms():
+    from oracle.events import event_index, scatter
+    level0, level1, mask, ctx, obj = _hier_case(seed=2)
+    B, T, N, D = level0.shape
+    idx = event_index(mask)
+    comb = scatter(level0, level1, idx)
+    w_l2 = np.eye(D, ctx.shape[2])                  # l2 = the first D entries of the mean context
+    l2 = ctx.mean(axis=1)[:, :D][:, None, None, :]
+    w0 = np.zeros((D, 2 * D))
+    # no context: the scatter times the alive mask
+    np.testing.assert_array_equal(om.hierarchy_forward_ref(level0, level1, idx, w_l2, w0, None, None, obj),
+                                  comb * obj[:, None, :, None])
+    # a gate of exactly 1/2
+    half = om.hierarchy_forward_ref(level0, level1, idx, w_l2, w0, np.zeros(D), ctx, None)
+    np.testing.assert_allclose(half, 0.5 * (comb + l2), rtol=1e-14, atol=1e-14)
+    # saturated gates select the Level-2 context or the scattered states
+    hi = om.hierarchy_forward_ref(level0, level1, idx, w_l2, w0, np.full(D, 60.0), ctx, obj)
+    np.testing.assert_allclose(hi, np.broadcast_to(l2, comb.shape) * obj[:, None, :, None], atol=1e-20)
+    lo = om.hierarchy_forward_ref(level0, level1, idx, w_l2, w0, np.full(D, -60.0), ctx, obj)
+    np.testing.assert_allclose(lo, comb * obj[:, None, :, None], rtol=1e-12, atol=1e-20)
+    # only the combined half of W_gate sees the states: a gate on channel j from state channel j alone
+    w = np.zeros((D, 2 * D))
+    w[np.arange(D), np.arange(D)] = 1.0
+    diag = om.hierarchy_forward_ref(level0, level1, idx, w_l2, w, None, ctx, None)
+    s = 1.0 / (1.0 + np.exp(-comb))
+    np.testing.assert_allclose(diag, s * l2 + (1 - s) * comb, rtol=1e-13, atol=1e-13)
