@@ -55,10 +55,10 @@ class TopDownWeights:
 
 
 def top_down_supported(d_slot: int, level2_dim: int | None = None) -> bool:
-    """Shapes hclsm_event_top_down takes: d_slot a multiple of 32 up to 384 (and d_l2 + d_slot <= 16384)."""
+    """Shapes hclsm_event_top_down takes: d_slot a multiple of 32 up to 384, d_l2 up to 16384."""
     if d_slot % 32 != 0 or not 0 < d_slot <= 384:
         return False
-    return level2_dim is None or level2_dim + d_slot <= 16384
+    return level2_dim is None or 0 < level2_dim <= 16384
 
 
 def event_top_down(level0: torch.Tensor, events: torch.Tensor, idx: EventIndex, W: TopDownWeights | None,

@@ -185,7 +185,7 @@ int hclsm_event_scatter_packed(const void* base, const void* packed, void* out, 
  *   Level-2 half of the gate are fp32.
  *   out = combined * obj_mask[b, n] (obj_mask [B, N] nullable, :159-160).  out may alias level0.
  * ws: hclsm_event_top_down_workspace(B, D) bytes, 16-byte aligned (needed with a level2_context).
- * D a multiple of 32 up to 384 (HCLSM_ERR_UNSUPPORTED otherwise).
+ * D a multiple of 32 up to 384, DL2 up to 16384 (HCLSM_ERR_UNSUPPORTED otherwise).
  */
 int64_t hclsm_event_top_down_workspace(int64_t B, int64_t D);
 int hclsm_event_top_down(const float* level0, const float* events, const int32_t* offsets,

@@ -146,7 +146,7 @@ def test_top_down_argument_errors_before_launch(lib):
     assert call(ev=None) == -1
     assert call(offs=None) == -1                          # packed rows need the offsets
     assert call(ctx=P, S2=0) == -2
-    assert call(ctx=P, DL2=16384) == -4                   # the prologue's vectors exceed 64 KB of LDS
+    assert call(ctx=P, DL2=16385) == -4                   # the mean context exceeds 64 KB of LDS
     assert call(ctx=P, wx=None) == -1
     assert call(ctx=P, ldw=100) == -2
     assert call(ctx=P, ws_bytes=16) == -2
