@@ -10,8 +10,9 @@
 //     qkv = xn . in_proj^T
 //     o   = softmax(q k^T / sqrt(dh), keys of dead slots excluded) v, per event and head   :49-51
 //     x  += o . out_proj^T                                (residual in the GEMM epilogue)
-//     xn  = LN2(x);  h1 = xn . w1^T
-//     g   = silu(h1) * (xn . w3^T)                        (gated-linear epilogue)          :17-28
+//     xn  = LN2(x)
+//     g   = silu(xn . w1^T) * (xn . w3^T)                 (one GEMM over interleaved w1 / w3 rows whose
+//                                                          epilogue pairs the products; fp32: two GEMMs) :17-28
 //     x  += g . w2^T
 //   out = LN(x) . proj_out^T                                                                 :124-128
 //
@@ -112,8 +113,15 @@ extern "C" int hclsm_level1_forward(const void* ev, int ev_dtype, void* out, int
                                 (int)n_heads, (int)dh, obj_mask, ev_rows, scale, dtype, st));
     HCLSM_TRY(gemm(o, dtype, P(b + 3), dm, dm, x, x, HCLSM_F32, nullptr));
     HCLSM_TRY(norm(Pf(b + 4), Pf(b + 5)));
-    HCLSM_TRY(gemm(xn, dtype, P(b + 6), hidden, dm, nullptr, h1, dtype, nullptr));
-    HCLSM_TRY(gemm(xn, dtype, P(b + 7), hidden, dm, nullptr, g, dtype, h1));
+    // g = silu(xn . w1^T) * (xn . w3^T): one paired GEMM for 16-bit operands, else two GEMMs through h1
+    rc = linear_glu_rows(xn, dm, dtype, P(b + 6), P(b + 7), dm, g, hidden, dtype, R, hidden, dm, n_events, N, dtype,
+                         st);
+    if (rc == HCLSM_ERR_UNSUPPORTED) {
+      HCLSM_TRY(gemm(xn, dtype, P(b + 6), hidden, dm, nullptr, h1, dtype, nullptr));
+      HCLSM_TRY(gemm(xn, dtype, P(b + 7), hidden, dm, nullptr, g, dtype, h1));
+    } else if (rc) {
+      return rc;
+    }
     HCLSM_TRY(gemm(g, dtype, P(b + 8), dm, hidden, x, x, HCLSM_F32, nullptr));
   }
   HCLSM_TRY(norm(Pf(1), Pf(2)));

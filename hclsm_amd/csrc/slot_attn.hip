@@ -141,8 +141,28 @@ struct LinExt {
   int64_t m_mul;
   const void* glu;
   int64_t ldg;
+  const void* w3;   // paired gated-linear GEMM (16-bit LDS kernels): see w_row
 };
-constexpr LinExt kNoLinExt{nullptr, 1, nullptr, 0};
+constexpr LinExt kNoLinExt{nullptr, 1, nullptr, 0, nullptr};
+
+// Weight row of GEMM column j.  With e.w3 set the GEMM is 2H columns wide and its 16-column tiles alternate
+// between W (= w1) and e.w3: column j is row 16 (j / 32) + j % 16 of w1 for j % 32 < 16, of w3 otherwise.  A
+// wave's tile pair (2u, 2u + 1) then holds h1 and h3 of the same 16 outputs, and the epilogue writes
+// silu(h1) * h3 to output columns 16u .. 16u + 15 (SwiGLU without h1 ever leaving the registers).
+template <typename T>
+__device__ __forceinline__ const T* w_row(const T* W, const LinExt& e, int64_t j, int64_t ldw) {
+  if (e.w3 == nullptr) return W + j * ldw;
+  const int64_t r = ((j >> 5) << 4) + (j & 15);
+  return ((j & 16) ? reinterpret_cast<const T*>(e.w3) : W) + r * ldw;
+}
+
+// Epilogue of a (w1, w3) tile pair: four consecutive outputs col .. col+3 of one row, col a multiple of 4 in
+// the H-wide output.
+template <int DT, int OT>
+__device__ __forceinline__ void glu_pair_epilogue(const f32x4& h1, const f32x4& h3, int64_t row, int64_t col,
+                                                  int64_t H, const float* resid, int64_t ldr,
+                                                  typename MM<OT>::T* Y, int64_t ldy, typename MM<DT>::T* Y2,
+                                                  int64_t ldy2, bool vec);
 
 __device__ __forceinline__ int64_t ext_rows(const LinExt& e, int64_t M) {
   if (e.m_dev == nullptr) return M;
@@ -234,6 +254,18 @@ __device__ __forceinline__ void lin_epilogue4(const f32x4& acc, const float (&bv
   }
 }
 
+template <int DT, int OT>
+__device__ __forceinline__ void glu_pair_epilogue(const f32x4& h1, const f32x4& h3, int64_t row, int64_t col,
+                                                  int64_t H, const float* resid, int64_t ldr,
+                                                  typename MM<OT>::T* Y, int64_t ldy, typename MM<DT>::T* Y2,
+                                                  int64_t ldy2, bool vec) {
+  f32x4 v;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) v[r] = silu_f(h1[r]) * h3[r];
+  const float zero[4] = {0.f, 0.f, 0.f, 0.f};
+  lin_epilogue4<DT, OT>(v, zero, row, col, H, 0, 0.f, resid, ldr, Y, ldy, Y2, ldy2, kNoLinExt, vec);
+}
+
 // One 16-byte LDS unit (8 operand elements) of the A operand: loaded as is for 16-bit X, or as 8 fp32 values
 // rounded to the operand type when it is stored (fp32 X).
 template <int DT, typename XT>
@@ -293,7 +325,7 @@ linear_lds_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>::
     ra = ra < M ? ra : M - 1;
     rb = rb < N ? rb : N - 1;
     pa[i] = X + ra * ldx + ucol[i];
-    pb[i] = W + rb * ldw + ucol[i];
+    pb[i] = w_row(W, ext, rb, ldw) + ucol[i];
     soff[i] = r * LT_LD + ucol[i];
   }
   AUnit<DT, XT> ra_[4];
@@ -367,6 +399,17 @@ linear_lds_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>::
         const int64_t fr = row / os.frame_rows, rr = row - fr * os.frame_rows;
         yt[fr * os.bstride + (col - os.col) * os.ldyt + rr] = Ts[c * TP + rl];
       }
+    }
+    return;
+  }
+  if (ext.w3 != nullptr) {   // (w1, w3) tile pair: the wave's two column tiles (c0 a multiple of 32)
+    const int64_t H = N / 2, col = c0 / 2 + 4 * g;
+    const bool v4 = lin_vec4_ok<DT, OT>(Y, ldy, Y2, ldy2, resid, ldr, kNoLinExt);
+#pragma unroll
+    for (int ti = 0; ti < 2; ++ti) {
+      const int64_t row = r0 + 16 * ti + li;
+      if (row < M && col < H)
+        glu_pair_epilogue<DT, OT>(acc[ti][0], acc[ti][1], row, col, H, resid, ldr, Y, ldy, Y2, ldy2, v4);
     }
     return;
   }
@@ -445,7 +488,7 @@ linear_lds128_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT
     ra = ra < M ? ra : M - 1;
     rb = rb < N ? rb : N - 1;
     pa[i] = X + ra * ldx + ucol[i];
-    pb[i] = W + rb * ldw + ucol[i];
+    pb[i] = w_row(W, ext, rb, ldw) + ucol[i];
     soff[i] = r * LB_LD + ucol[i];
   }
   AUnit<DT, XT> ra_[4];
@@ -491,6 +534,21 @@ linear_lds128_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT
     }
   }
   const int64_t r0 = tm * 128 + 64 * wr, c0 = tn * 128 + 64 * wc;
+  if (ext.w3 != nullptr) {   // (w1, w3) tile pairs (0, 1) and (2, 3) of the wave's 64 columns
+    const int64_t H = N / 2;
+    const bool v4 = lin_vec4_ok<DT, OT>(Y, ldy, Y2, ldy2, resid, ldr, kNoLinExt);
+#pragma unroll
+    for (int tj = 0; tj < 4; tj += 2) {
+      const int64_t col = (c0 + 16 * tj) / 2 + 4 * g;
+#pragma unroll
+      for (int ti = 0; ti < 4; ++ti) {
+        const int64_t row = r0 + 16 * ti + li;
+        if (row < M && col < H)
+          glu_pair_epilogue<DT, OT>(acc[ti][tj], acc[ti][tj + 1], row, col, H, resid, ldr, Y, ldy, Y2, ldy2, v4);
+      }
+    }
+    return;
+  }
   const bool vec = lin_vec4_ok<DT, OT>(Y, ldy, Y2, ldy2, resid, ldr, ext);
 #pragma unroll
   for (int tj = 0; tj < 4; ++tj) {
@@ -1286,6 +1344,37 @@ int linear_rows(const void* x, int64_t ldx, int x_dtype, const void* w, int64_t 
   if (glu && (x_dtype != dtype && x_dtype != HCLSM_F32)) return HCLSM_ERR_DTYPE;
   return linear_impl(x, ldx, x_dtype, w, ldw, bias, resid, ldr, y, ldy, y_dtype, nullptr, 0, M, N, K, relu, 0.f, ln,
                      ln_w, ln_b, ln_eps, dtype, st, LinExt{m_dev, m_mul, glu, ldg});
+}
+
+// SwiGLU input layer Y[M, H] = silu(X . w1^T) * (X . w3^T) as one GEMM over 2H interleaved columns (w_row),
+// 16-bit operands only (HCLSM_ERR_UNSUPPORTED otherwise: the caller runs two GEMMs).  Declared in internal.h.
+int linear_glu_rows(const void* x, int64_t ldx, int x_dtype, const void* w1, const void* w3, int64_t ldw, void* y,
+                    int64_t ldy, int y_dtype, int64_t M, int64_t H, int64_t K, const int32_t* m_dev, int64_t m_mul,
+                    int dtype, hipStream_t st) {
+  if (M < 0 || H < 0 || K < 0) return HCLSM_ERR_SHAPE;
+  if (M == 0 || H == 0) return 0;
+  if (!x || !w1 || !w3 || !y) return HCLSM_ERR_NULL;
+  if (dtype == HCLSM_F32 || H % 16 != 0 || K % 32 != 0 || K == 0) return HCLSM_ERR_UNSUPPORTED;
+  if (!al16(w1) || !al16(w3) || ldw % 8) return HCLSM_ERR_UNSUPPORTED;
+  if (x_dtype == dtype ? (!al16(x) || ldx % 8) : (x_dtype != HCLSM_F32 || !al16(x) || ldx % 4))
+    return HCLSM_ERR_UNSUPPORTED;
+  const LinExt ext{m_dev, m_mul, nullptr, 0, w3};
+  const int64_t N = 2 * H;
+#define HCLSM_GLU2(D, O, XD, XT)                                                                             \
+  if (dtype == D && y_dtype == O && x_dtype == XD) {                                                         \
+    launch_linear_quad<D, O, XT>(x, ldx, w1, ldw, nullptr, nullptr, 0, y, ldy, nullptr, 0, M, N, K, 0, 0.f, st, \
+                                 OutSplit{0, 1, 0, 0, nullptr}, ext);                                        \
+    HCLSM_LAUNCH_CHECK();                                                                                    \
+    return 0;                                                                                                \
+  }
+  HCLSM_GLU2(HCLSM_BF16, HCLSM_BF16, HCLSM_BF16, uint16_t)
+  HCLSM_GLU2(HCLSM_BF16, HCLSM_F32, HCLSM_BF16, uint16_t)
+  HCLSM_GLU2(HCLSM_BF16, HCLSM_BF16, HCLSM_F32, float)
+  HCLSM_GLU2(HCLSM_F16, HCLSM_F16, HCLSM_F16, _Float16)
+  HCLSM_GLU2(HCLSM_F16, HCLSM_F32, HCLSM_F16, _Float16)
+  HCLSM_GLU2(HCLSM_F16, HCLSM_F16, HCLSM_F32, float)
+#undef HCLSM_GLU2
+  return HCLSM_ERR_DTYPE;
 }
 
 static int gru_impl(const void* x, int64_t ldx, const void* hb, int64_t ldhb, const float* h, int64_t ldh,

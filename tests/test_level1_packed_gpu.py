@@ -93,6 +93,22 @@ def test_level1_packed_bf16_autocast():
     assert normwise_rel_err(_np(got), np.stack([ref[b, k] for b, k in bk])) <= 2e-2
 
 
+def test_level1_packed_bf16_autocast_wide_tiles():
+    """A capacity of 65,536 rows: the paired SwiGLU GEMM (w1 / w3 interleaved, one launch) runs on the
+    128x128-tile kernel, the other layers on their usual kernels; against the oracle at the bf16 bar."""
+    hm, l1 = _modules(11)
+    states, mask, obj = _case(16, 128, 32, 11, p=0.1)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        ev, idx = hm.gather_events_packed(states, mask)
+        out = l1.forward_packed(ev, idx, obj)
+    with torch.no_grad():
+        ev_pad, pad, K = hm.gather_events(states, mask)
+    ref = om.level1_ref(_np(ev_pad), _np(pad), _np(obj), _sd(l1), L1.n_layers, L1.n_heads)
+    got, bk = _live_rows(out, idx)
+    assert ev.shape[0] * ev.shape[1] == 65536
+    assert normwise_rel_err(_np(got), np.stack([ref[b, k] for b, k in bk])) <= 2e-2
+
+
 def test_level1_packed_all_slots_dead_gives_nan_like_softmax():
     """An event whose slots are all dead: every key excluded, softmax over all -inf -> NaN rows, as
     nn.MultiheadAttention gives; other rows unaffected."""
