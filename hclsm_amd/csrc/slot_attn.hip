@@ -1461,16 +1461,123 @@ layer_norm_kernel(const typename MM<DTI>::T* __restrict__ x, int64_t ldx, const 
   }
 }
 
+// 4 consecutive elements as fp32 (one 16-byte load for fp32, 8 bytes for 16-bit types) and back
+template <int DT>
+__device__ __forceinline__ float4 ln_load4(const typename MM<DT>::T* p) {
+  if constexpr (DT == HCLSM_F32) {
+    return *reinterpret_cast<const float4*>(p);
+  } else {
+    typename MM<DT>::T e[4];
+    *reinterpret_cast<uint2*>(e) = *reinterpret_cast<const uint2*>(p);
+    return make_float4(MM<DT>::tof(e[0]), MM<DT>::tof(e[1]), MM<DT>::tof(e[2]), MM<DT>::tof(e[3]));
+  }
+}
+template <int DT>
+__device__ __forceinline__ void ln_store4(typename MM<DT>::T* p, float4 v) {
+  if constexpr (DT == HCLSM_F32) {
+    *reinterpret_cast<float4*>(p) = v;
+  } else {
+    typename MM<DT>::T e[4] = {MM<DT>::fromf(v.x), MM<DT>::fromf(v.y), MM<DT>::fromf(v.z), MM<DT>::fromf(v.w)};
+    *reinterpret_cast<uint2*>(p) = *reinterpret_cast<const uint2*>(e);
+  }
+}
+
+// LayerNorm for rows of D = 4u elements (u <= 64 * VPL 4-element units) starting 16-byte (fp32) / 8-byte aligned:
+// one wave per row, lane l holding units l, l + 64, ... in registers, every load issued before the reductions.
+// Same two-pass statistics as layer_norm_kernel.
+template <int DTI, int DTO, int VPL>
+__global__ void __launch_bounds__(256)
+layer_norm_vec_kernel(const typename MM<DTI>::T* __restrict__ x, int64_t ldx, const float* __restrict__ w,
+                      const float* __restrict__ b, typename MM<DTO>::T* __restrict__ y, int64_t ldy, int64_t M,
+                      int D, float eps, LinExt ext) {
+  const int lane = threadIdx.x & 63;
+  M = ext_rows(ext, M);
+  const int U = D >> 2;
+  // rows walked with the grid's stride (the grid may be smaller than M / 4 with a device-side row count)
+  for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < M; row += (int64_t)gridDim.x * 4) {
+    const typename MM<DTI>::T* xr = x + row * ldx;
+    float4 v[VPL];
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      const int u = lane + 64 * j;
+      v[j] = u < U ? ln_load4<DTI>(xr + 4 * u) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+    const float mean = s / (float)D;
+    float q = 0.f;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      if (lane + 64 * j < U) {
+        const float a = v[j].x - mean, c = v[j].y - mean, d = v[j].z - mean, e = v[j].w - mean;
+        q += (a * a + c * c) + (d * d + e * e);
+      }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o, 64);
+    const float rstd = 1.f / sqrtf(q / (float)D + eps);
+    typename MM<DTO>::T* yr = y + row * ldy;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      const int u = lane + 64 * j;
+      if (u < U) {
+        float4 t = make_float4((v[j].x - mean) * rstd, (v[j].y - mean) * rstd, (v[j].z - mean) * rstd,
+                               (v[j].w - mean) * rstd);
+        if (w) {
+          const float4 wv = *reinterpret_cast<const float4*>(w + 4 * u);
+          t.x *= wv.x; t.y *= wv.y; t.z *= wv.z; t.w *= wv.w;
+        }
+        if (b) {
+          const float4 bv = *reinterpret_cast<const float4*>(b + 4 * u);
+          t.x += bv.x; t.y += bv.y; t.z += bv.z; t.w += bv.w;
+        }
+        ln_store4<DTO>(yr + 4 * u, t);
+      }
+    }
+  }
+}
+
 static int ln_impl(const void* x, int64_t ldx, const float* w, const float* b, void* y, int64_t ldy, int64_t M,
                    int64_t D, float eps, int in_dtype, int out_dtype, hipStream_t st, LinExt ext = kNoLinExt) {
   if (M < 0 || D < 0 || D > 0x7fffffff) return HCLSM_ERR_SHAPE;
   if (M == 0 || D == 0) return 0;
   if (!x || !y) return HCLSM_ERR_NULL;
   const unsigned grid = (unsigned)((M + 3) / 4);
+  // vector kernel: D a multiple of 4 up to 1024, rows and weights aligned for 4-element accesses
+  const int ies = in_dtype == HCLSM_F32 ? 4 : 2, oes = out_dtype == HCLSM_F32 ? 4 : 2;
+  const bool vec = D % 4 == 0 && D <= 1024 && ((uintptr_t)x % (4 * ies)) == 0 && ((uintptr_t)y % (4 * oes)) == 0 &&
+                   (ldx * ies) % (4 * ies) == 0 && (ldy * oes) % (4 * oes) == 0 && ((uintptr_t)w % 16) == 0 &&
+                   ((uintptr_t)b % 16) == 0;
+  const int vpl = D <= 256 ? 1 : D <= 512 ? 2 : 4;
+  // device row count: at most what the device holds at once (the vector kernel walks the rows); every
+  // instantiation has the same occupancy, so one of each width stands for all element types
+  unsigned vgrid = grid;
+  if (vec && ext.m_dev) {
+    static std::atomic<int> cache[3][HCLSM_MAX_DEVICES];
+    const void* fn = vpl == 1 ? (const void*)layer_norm_vec_kernel<HCLSM_F32, HCLSM_BF16, 1>
+                   : vpl == 2 ? (const void*)layer_norm_vec_kernel<HCLSM_F32, HCLSM_BF16, 2>
+                              : (const void*)layer_norm_vec_kernel<HCLSM_F32, HCLSM_BF16, 4>;
+    int slots = 0;
+    if (device_launch_setup(fn, 256, 0, 0, cache[vpl >> 1], &slots) == 0 && slots > 0 && (unsigned)slots < grid)
+      vgrid = (unsigned)slots;
+  }
 #define HCLSM_LN(I, O)                                                                                     \
   if (in_dtype == I && out_dtype == O) {                                                                   \
-    hipLaunchKernelGGL((layer_norm_kernel<I, O>), dim3(grid), dim3(256), 0, st, (const MM<I>::T*)x, ldx, w, b, \
-                       (MM<O>::T*)y, ldy, M, (int)D, eps, ext);                                            \
+    if (vec && vpl == 1)                                                                                   \
+      hipLaunchKernelGGL((layer_norm_vec_kernel<I, O, 1>), dim3(vgrid), dim3(256), 0, st, (const MM<I>::T*)x, \
+                         ldx, w, b, (MM<O>::T*)y, ldy, M, (int)D, eps, ext);                               \
+    else if (vec && vpl == 2)                                                                              \
+      hipLaunchKernelGGL((layer_norm_vec_kernel<I, O, 2>), dim3(vgrid), dim3(256), 0, st, (const MM<I>::T*)x, \
+                         ldx, w, b, (MM<O>::T*)y, ldy, M, (int)D, eps, ext);                               \
+    else if (vec)                                                                                          \
+      hipLaunchKernelGGL((layer_norm_vec_kernel<I, O, 4>), dim3(vgrid), dim3(256), 0, st, (const MM<I>::T*)x, \
+                         ldx, w, b, (MM<O>::T*)y, ldy, M, (int)D, eps, ext);                               \
+    else                                                                                                   \
+      hipLaunchKernelGGL((layer_norm_kernel<I, O>), dim3(grid), dim3(256), 0, st, (const MM<I>::T*)x, ldx, w, \
+                         b, (MM<O>::T*)y, ldy, M, (int)D, eps, ext);                                       \
     HCLSM_LAUNCH_CHECK();                                                                                  \
     return 0;                                                                                              \
   }

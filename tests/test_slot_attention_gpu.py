@@ -225,3 +225,25 @@ def test_large_linear_wide_tiles(dtype, tol, M, N, K):
                    stream=st)
     ref = np.clip(np.maximum(_np(x) @ _np(w).T + _np(b), 0) + _np(r), -2.0, 2.0)
     assert normwise_rel_err(_np(y), ref) <= tol
+
+
+@pytest.mark.parametrize("D,pad", [(96, 0), (384, 0), (384, 4), (1000, 0), (1024, 0), (97, 0), (384, 1), (1030, 0),
+                                   (4, 0)])
+@pytest.mark.parametrize("io", [(torch.float32, torch.float32), (torch.float32, torch.bfloat16),
+                                (torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16)])
+def test_layer_norm_rows(D, pad, io):
+    """hclsm_layer_norm over row widths taking the vector kernel (D % 4 == 0, D <= 1024, aligned rows: one, two
+    or four 4-element units per lane) and the scalar one (odd widths, unaligned row strides, D > 1024), rows
+    with a large common offset, against the float64 LayerNorm."""
+    from hclsm_amd.kernels import slot_iteration as si
+    din, dout = io
+    g = torch.Generator().manual_seed(D + pad)
+    M, ldx = 37, D + pad
+    x = (torch.randn(M, ldx, generator=g) * 0.5 + 20.0).to(din)
+    w, b = torch.rand(D, generator=g) + 0.5, torch.randn(D, generator=g)
+    print(f"layer_norm D={D} pad={pad} io={io}", flush=True)
+    y = si._ln(x.cuda(), ldx, M, D, w.cuda(), b.cuda(), dout, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    want = sa.layer_norm(_np(x[:, :D]), _np(w), _np(b))
+    tol = 1e-5 if dout == torch.float32 and din == torch.float32 else 8e-3
+    assert normwise_rel_err(_np(y), want) <= tol
