@@ -15,8 +15,8 @@ int linear_rows(const void* x, int64_t ldx, int x_dtype, const void* w, int64_t 
                 const int32_t* m_dev, int64_t m_mul, int dtype, hipStream_t st);
 
 // SwiGLU input layer Y[M, H] = silu(X . w1^T) * (X . w3^T) (w1, w3 [H, K] with row stride ldw) as one GEMM
-// whose epilogue pairs the two products; row count as linear_rows.  16-bit operands only: HCLSM_ERR_UNSUPPORTED
-// for fp32 or shapes it does not take (H % 16, K % 32, alignment), where the caller runs two GEMMs instead.
+// whose epilogue pairs the two products; row count as linear_rows.  HCLSM_ERR_UNSUPPORTED for shapes it does not
+// take (H % 16; K % 32 for 16-bit operands, K % 4 for fp32; 16-byte alignment), where the caller runs two GEMMs.
 // Defined in slot_attn.hip.
 int linear_glu_rows(const void* x, int64_t ldx, int x_dtype, const void* w1, const void* w3, int64_t ldw, void* y,
                     int64_t ldy, int y_dtype, int64_t M, int64_t H, int64_t K, const int32_t* m_dev, int64_t m_mul,

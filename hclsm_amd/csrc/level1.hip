@@ -12,7 +12,7 @@
 //     x  += o . out_proj^T                                (residual in the GEMM epilogue)
 //     xn  = LN2(x)
 //     g   = silu(xn . w1^T) * (xn . w3^T)                 (one GEMM over interleaved w1 / w3 rows whose
-//                                                          epilogue pairs the products; fp32: two GEMMs) :17-28
+//                                                          epilogue pairs the products)                   :17-28
 //     x  += g . w2^T
 //   out = LN(x) . proj_out^T                                                                 :124-128
 //
@@ -113,7 +113,7 @@ extern "C" int hclsm_level1_forward(const void* ev, int ev_dtype, void* out, int
                                 (int)n_heads, (int)dh, obj_mask, ev_rows, scale, dtype, st));
     HCLSM_TRY(gemm(o, dtype, P(b + 3), dm, dm, x, x, HCLSM_F32, nullptr));
     HCLSM_TRY(norm(Pf(b + 4), Pf(b + 5)));
-    // g = silu(xn . w1^T) * (xn . w3^T): one paired GEMM for 16-bit operands, else two GEMMs through h1
+    // g = silu(xn . w1^T) * (xn . w3^T): one paired GEMM, or two GEMMs through h1 where it does not apply
     rc = linear_glu_rows(xn, dm, dtype, P(b + 6), P(b + 7), dm, g, hidden, dtype, R, hidden, dm, n_events, N, dtype,
                          st);
     if (rc == HCLSM_ERR_UNSUPPORTED) {

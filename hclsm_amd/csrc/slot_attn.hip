@@ -141,11 +141,11 @@ struct LinExt {
   int64_t m_mul;
   const void* glu;
   int64_t ldg;
-  const void* w3;   // paired gated-linear GEMM (16-bit LDS kernels): see w_row
+  const void* w3;   // paired gated-linear GEMM (LDS kernels): see w_row
 };
 constexpr LinExt kNoLinExt{nullptr, 1, nullptr, 0, nullptr};
 
-// Weight row of GEMM column j.  With e.w3 set the GEMM is 2H columns wide and its 16-column tiles alternate
+// Weight row of GEMM column j.  With e.w3 set (LDS kernels) the GEMM is 2H columns wide and its 16-column tiles alternate
 // between W (= w1) and e.w3: column j is row 16 (j / 32) + j % 16 of w1 for j % 32 < 16, of w3 otherwise.  A
 // wave's tile pair (2u, 2u + 1) then holds h1 and h3 of the same 16 outputs, and the epilogue writes
 // silu(h1) * h3 to output columns 16u .. 16u + 15 (SwiGLU without h1 ever leaving the registers).
@@ -600,7 +600,7 @@ linear_lds_f32_kernel(const float* __restrict__ X, int64_t ldx, const float* __r
     ra = ra < M ? ra : M - 1;
     rb = rb < N ? rb : N - 1;
     pa[i] = X + ra * ldx + ucol[i];
-    pb[i] = W + rb * ldw + ucol[i];
+    pb[i] = w_row(W, ext, rb, ldw) + ucol[i];
     soff[i] = r * LF_LD + ucol[i];
   }
   float4 ra_[4], rb_[4];
@@ -648,6 +648,17 @@ linear_lds_f32_kernel(const float* __restrict__ X, int64_t ldx, const float* __r
     }
   }
   const int64_t r0 = tm * 64 + 32 * wr, c0 = tn * 64 + 32 * wc;
+  if (ext.w3 != nullptr) {   // (w1, w3) tile pair: the wave's two column tiles (c0 a multiple of 32)
+    const int64_t H = N / 2, col = c0 / 2 + 4 * g;
+    const bool v4 = lin_vec4_ok<HCLSM_F32, OT>(Y, ldy, Y2, ldy2, resid, ldr, kNoLinExt);
+#pragma unroll
+    for (int ti = 0; ti < 2; ++ti) {
+      const int64_t row = r0 + 16 * ti + li;
+      if (row < M && col < H)
+        glu_pair_epilogue<HCLSM_F32, OT>(acc[ti][0], acc[ti][1], row, col, H, resid, ldr, Y, ldy, Y2, ldy2, v4);
+    }
+    return;
+  }
   const bool vec = lin_vec4_ok<HCLSM_F32, OT>(Y, ldy, Y2, ldy2, resid, ldr, ext);
 #pragma unroll
   for (int tj = 0; tj < 2; ++tj) {
@@ -1346,18 +1357,24 @@ int linear_rows(const void* x, int64_t ldx, int x_dtype, const void* w, int64_t 
                      ln_w, ln_b, ln_eps, dtype, st, LinExt{m_dev, m_mul, glu, ldg});
 }
 
-// SwiGLU input layer Y[M, H] = silu(X . w1^T) * (X . w3^T) as one GEMM over 2H interleaved columns (w_row),
-// 16-bit operands only (HCLSM_ERR_UNSUPPORTED otherwise: the caller runs two GEMMs).  Declared in internal.h.
+// SwiGLU input layer Y[M, H] = silu(X . w1^T) * (X . w3^T) as one GEMM over 2H interleaved columns (w_row) on
+// the LDS kernels (HCLSM_ERR_UNSUPPORTED for shapes or alignments they do not take: the caller runs two GEMMs).
+// Declared in internal.h.
 int linear_glu_rows(const void* x, int64_t ldx, int x_dtype, const void* w1, const void* w3, int64_t ldw, void* y,
                     int64_t ldy, int y_dtype, int64_t M, int64_t H, int64_t K, const int32_t* m_dev, int64_t m_mul,
                     int dtype, hipStream_t st) {
   if (M < 0 || H < 0 || K < 0) return HCLSM_ERR_SHAPE;
   if (M == 0 || H == 0) return 0;
   if (!x || !w1 || !w3 || !y) return HCLSM_ERR_NULL;
-  if (dtype == HCLSM_F32 || H % 16 != 0 || K % 32 != 0 || K == 0) return HCLSM_ERR_UNSUPPORTED;
-  if (!al16(w1) || !al16(w3) || ldw % 8) return HCLSM_ERR_UNSUPPORTED;
-  if (x_dtype == dtype ? (!al16(x) || ldx % 8) : (x_dtype != HCLSM_F32 || !al16(x) || ldx % 4))
-    return HCLSM_ERR_UNSUPPORTED;
+  if (H % 16 != 0 || K == 0) return HCLSM_ERR_UNSUPPORTED;
+  if (dtype == HCLSM_F32) {   // the fp32 LDS kernel: 16-byte rows
+    if (x_dtype != HCLSM_F32 || K % 4 || !al16(x) || !al16(w1) || !al16(w3) || ldx % 4 || ldw % 4)
+      return HCLSM_ERR_UNSUPPORTED;
+  } else {
+    if (K % 32 != 0 || !al16(w1) || !al16(w3) || ldw % 8) return HCLSM_ERR_UNSUPPORTED;
+    if (x_dtype == dtype ? (!al16(x) || ldx % 8) : (x_dtype != HCLSM_F32 || !al16(x) || ldx % 4))
+      return HCLSM_ERR_UNSUPPORTED;
+  }
   const LinExt ext{m_dev, m_mul, nullptr, 0, w3};
   const int64_t N = 2 * H;
 #define HCLSM_GLU2(D, O, XD, XT)                                                                             \
@@ -1373,6 +1390,7 @@ int linear_glu_rows(const void* x, int64_t ldx, int x_dtype, const void* w1, con
   HCLSM_GLU2(HCLSM_F16, HCLSM_F16, HCLSM_F16, _Float16)
   HCLSM_GLU2(HCLSM_F16, HCLSM_F32, HCLSM_F16, _Float16)
   HCLSM_GLU2(HCLSM_F16, HCLSM_F16, HCLSM_F32, float)
+  HCLSM_GLU2(HCLSM_F32, HCLSM_F32, HCLSM_F32, float)
 #undef HCLSM_GLU2
   return HCLSM_ERR_DTYPE;
 }
