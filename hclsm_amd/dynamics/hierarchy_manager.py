@@ -83,8 +83,8 @@ class HierarchyManager(nn.Module):
     # ---- packed, sync-free counterparts (no K_max host read)
 
     def gather_events_packed(self, states: torch.Tensor, event_mask: torch.Tensor):
-        """(B, T, N, D) -> (packed event states (B*T, N, D), index): event e < index.total() in row e,
-        zero rows after.  Differentiable; no host sync."""
+        """(B, T, N, D) -> (packed event states (B*T, N, D), index): event e < index.total() in row e; the rows
+        after are zero in grad mode, unspecified otherwise.  Differentiable; no host sync."""
         idx = build_event_index(event_mask, "gt_half")
         return gather_events_packed(states, idx), idx
 

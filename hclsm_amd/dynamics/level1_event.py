@@ -99,7 +99,7 @@ class Level1EventDynamics(nn.Module):
 
         Without autograd this is one C call (hclsm_level1_forward, compute in fp32, or bf16 under a
         bf16 autocast).  With autograd it is this module's ops over all capacity rows, so the rows past
-        the live count must be finite (gather_events_packed zero-fills them)."""
+        the live count must be finite (gather_events_packed zero-fills them in grad mode)."""
         cap, N, D = event_states.shape
         if not self._needs_grad(event_states):
             dtype = torch.bfloat16 if (torch.is_autocast_enabled("cuda") and

@@ -242,15 +242,15 @@ def scatter_packed(base: torch.Tensor | None, packed: torch.Tensor | None, idx: 
 
 class _GatherPacked(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, states, idx):
+    def forward(ctx, states, idx, zero_fill):
         ctx.idx = idx
         ctx.like = torch.empty((0, 0) + tuple(states.shape[2:]), dtype=states.dtype, device=states.device)
-        return gather_packed(states, idx, zero_fill=True)
+        return gather_packed(states, idx, zero_fill=zero_fill)
 
     @staticmethod
     def backward(ctx, g):
         # d states[b, t] = g[offsets[b] + slot_of[b, t]] at events, 0 elsewhere
-        return scatter_packed(None, g.contiguous(), ctx.idx), None
+        return scatter_packed(None, g.contiguous(), ctx.idx), None, None
 
 
 class _ScatterPacked(torch.autograd.Function):
@@ -271,9 +271,12 @@ class _ScatterPacked(torch.autograd.Function):
 
 def gather_events_packed(states: torch.Tensor, idx: EventIndex) -> torch.Tensor:
     """Differentiable packed gather: (B, T, ...) -> (B*T, ...) with event e < idx.total() in row e
-    (rows ascending per batch row, batch rows in order) and zero rows after; no host sync."""
+    (rows ascending per batch row, batch rows in order); no host sync.  In grad mode the rows after the live
+    count are zero (torch ops over all capacity rows then stay finite, and so do their weight gradients);
+    otherwise they are unspecified: the C entry points read the live rows only, and every row op and
+    per-event attention keeps a later row to itself."""
     require_gpu("gather_events_packed", states)
-    return _GatherPacked.apply(states, idx)
+    return _GatherPacked.apply(states, idx, torch.is_grad_enabled())
 
 
 def scatter_events_packed(base: torch.Tensor, packed: torch.Tensor, idx: EventIndex) -> torch.Tensor:

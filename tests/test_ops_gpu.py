@@ -102,10 +102,11 @@ def test_packed_level1_ops_equal_eager():
         want = l1.forward_packed(ev, idx, obj)
         t = OPS.event_index(mask, 0)
         evo = OPS.event_gather_packed(states, t[3], t[2], t[5])
-        assert torch.equal(evo, ev)
+        n = idx.total()
+        # live rows equal; the op zero-fills the rest (the eager gather does so only in grad mode)
+        assert torch.equal(evo[:n], ev[:n]) and evo[n:].abs().sum() == 0
         W = Level1Weights.from_module(l1, torch.float32)
         got = OPS.level1_forward(evo, t[5], t[3], obj, W.tensors, 4, W.ln_eps, torch.float32)
-        n = idx.total()
         assert torch.equal(got[:n], want[:n]) and got[n:].abs().sum() == 0
         comb = OPS.event_scatter_packed(states, got, t[1], t[4])
         assert torch.equal(comb, hm.forward_packed(states, want, idx))
