@@ -1502,12 +1502,13 @@ __device__ __forceinline__ void ln_store4(typename MM<DT>::T* p, float4 v) {
 
 // LayerNorm for rows of D = 4u elements (u <= 64 * VPL 4-element units) starting 16-byte (fp32) / 8-byte aligned:
 // one wave per row, lane l holding units l, l + 64, ... in registers, every load issued before the reductions.
-// Same two-pass statistics as layer_norm_kernel.
+// Same two-pass statistics as layer_norm_kernel.  With xc the input rows are also written, in the output type,
+// to xc (row stride ldy).
 template <int DTI, int DTO, int VPL>
 __global__ void __launch_bounds__(256)
 layer_norm_vec_kernel(const typename MM<DTI>::T* __restrict__ x, int64_t ldx, const float* __restrict__ w,
                       const float* __restrict__ b, typename MM<DTO>::T* __restrict__ y, int64_t ldy, int64_t M,
-                      int D, float eps, LinExt ext) {
+                      int D, float eps, LinExt ext, typename MM<DTO>::T* __restrict__ xc) {
   const int lane = threadIdx.x & 63;
   M = ext_rows(ext, M);
   const int U = D >> 2;
@@ -1553,16 +1554,42 @@ layer_norm_vec_kernel(const typename MM<DTI>::T* __restrict__ x, int64_t ldx, co
           t.x += bv.x; t.y += bv.y; t.z += bv.z; t.w += bv.w;
         }
         ln_store4<DTO>(yr + 4 * u, t);
+        if (xc) ln_store4<DTO>(xc + row * ldy + 4 * u, v[j]);   // the input row itself, in the output type
       }
     }
   }
 }
 
+template <int DT>
+__global__ void __launch_bounds__(256)
+convert_f32_kernel(const float* __restrict__ src, typename MM<DT>::T* __restrict__ dst, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = MM<DT>::fromf(src[i]);
+}
+
+static int convert_f32(const float* src, void* dst, int64_t n, int dtype, hipStream_t st) {
+  if (n <= 0) return 0;
+  int64_t g = (n + 255) / 256;
+  g = g > 4096 ? 4096 : g;
+  if (dtype == HCLSM_BF16)
+    hipLaunchKernelGGL(convert_f32_kernel<HCLSM_BF16>, dim3((unsigned)g), dim3(256), 0, st, src, (uint16_t*)dst, n);
+  else if (dtype == HCLSM_F16)
+    hipLaunchKernelGGL(convert_f32_kernel<HCLSM_F16>, dim3((unsigned)g), dim3(256), 0, st, src, (_Float16*)dst, n);
+  else
+    hipLaunchKernelGGL(convert_f32_kernel<HCLSM_F32>, dim3((unsigned)g), dim3(256), 0, st, src, (float*)dst, n);
+  HCLSM_LAUNCH_CHECK();
+  return 0;
+}
+
+// LayerNorm of M rows; with xc (fp32 input rows with ldx == D only) the input is also copied to xc in the output
+// type, in the same pass where the vector kernel runs.
 static int ln_impl(const void* x, int64_t ldx, const float* w, const float* b, void* y, int64_t ldy, int64_t M,
-                   int64_t D, float eps, int in_dtype, int out_dtype, hipStream_t st, LinExt ext = kNoLinExt) {
+                   int64_t D, float eps, int in_dtype, int out_dtype, hipStream_t st, LinExt ext = kNoLinExt,
+                   void* xc = nullptr) {
   if (M < 0 || D < 0 || D > 0x7fffffff) return HCLSM_ERR_SHAPE;
   if (M == 0 || D == 0) return 0;
   if (!x || !y) return HCLSM_ERR_NULL;
+  if (xc && (in_dtype != HCLSM_F32 || ldx != D || ldy != D || ext.m_dev)) return HCLSM_ERR_UNSUPPORTED;
   const unsigned grid = (unsigned)((M + 3) / 4);
   // vector kernel: D a multiple of 4 up to 1024, rows and weights aligned for 4-element accesses
   const int ies = in_dtype == HCLSM_F32 ? 4 : 2, oes = out_dtype == HCLSM_F32 ? 4 : 2;
@@ -1586,17 +1613,18 @@ static int ln_impl(const void* x, int64_t ldx, const float* w, const float* b, v
   if (in_dtype == I && out_dtype == O) {                                                                   \
     if (vec && vpl == 1)                                                                                   \
       hipLaunchKernelGGL((layer_norm_vec_kernel<I, O, 1>), dim3(vgrid), dim3(256), 0, st, (const MM<I>::T*)x, \
-                         ldx, w, b, (MM<O>::T*)y, ldy, M, (int)D, eps, ext);                               \
+                         ldx, w, b, (MM<O>::T*)y, ldy, M, (int)D, eps, ext, (MM<O>::T*)xc);               \
     else if (vec && vpl == 2)                                                                              \
       hipLaunchKernelGGL((layer_norm_vec_kernel<I, O, 2>), dim3(vgrid), dim3(256), 0, st, (const MM<I>::T*)x, \
-                         ldx, w, b, (MM<O>::T*)y, ldy, M, (int)D, eps, ext);                               \
+                         ldx, w, b, (MM<O>::T*)y, ldy, M, (int)D, eps, ext, (MM<O>::T*)xc);               \
     else if (vec)                                                                                          \
       hipLaunchKernelGGL((layer_norm_vec_kernel<I, O, 4>), dim3(vgrid), dim3(256), 0, st, (const MM<I>::T*)x, \
-                         ldx, w, b, (MM<O>::T*)y, ldy, M, (int)D, eps, ext);                               \
+                         ldx, w, b, (MM<O>::T*)y, ldy, M, (int)D, eps, ext, (MM<O>::T*)xc);               \
     else                                                                                                   \
       hipLaunchKernelGGL((layer_norm_kernel<I, O>), dim3(grid), dim3(256), 0, st, (const MM<I>::T*)x, ldx, w, \
                          b, (MM<O>::T*)y, ldy, M, (int)D, eps, ext);                                       \
     HCLSM_LAUNCH_CHECK();                                                                                  \
+    if (xc && !vec) return convert_f32((const float*)x, xc, M * D, out_dtype, st);                         \
     return 0;                                                                                              \
   }
   HCLSM_LN(HCLSM_F32, HCLSM_F32)
@@ -1698,43 +1726,24 @@ extern "C" int64_t hclsm_slot_attention_workspace(int64_t B, int64_t N, int64_t 
   return (int64_t)slot_ws_layout(B, N, M, d, hidden, dtype == HCLSM_F32 ? 4 : 2, true, d_in).total;
 }
 
-template <int DT>
-__global__ void __launch_bounds__(256)
-convert_f32_kernel(const float* __restrict__ src, typename MM<DT>::T* __restrict__ dst, int64_t n) {
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = MM<DT>::fromf(src[i]);
-}
-
-static int convert_f32(const float* src, void* dst, int64_t n, int dtype, hipStream_t st) {
-  if (n <= 0) return 0;
-  int64_t g = (n + 255) / 256;
-  g = g > 4096 ? 4096 : g;
-  if (dtype == HCLSM_BF16)
-    hipLaunchKernelGGL(convert_f32_kernel<HCLSM_BF16>, dim3((unsigned)g), dim3(256), 0, st, src, (uint16_t*)dst, n);
-  else if (dtype == HCLSM_F16)
-    hipLaunchKernelGGL(convert_f32_kernel<HCLSM_F16>, dim3((unsigned)g), dim3(256), 0, st, src, (_Float16*)dst, n);
-  else
-    hipLaunchKernelGGL(convert_f32_kernel<HCLSM_F32>, dim3((unsigned)g), dim3(256), 0, st, src, (float*)dst, n);
-  HCLSM_LAUNCH_CHECK();
-  return 0;
-}
 
 // One iteration (dynamic_slots.py:98-131).  slots_in fp32 and sb (the same slots in `dtype`) are
 // read; slots_out (may alias slots_in: it is written by the last launch, after every read) and
 // sb (rewritten with the new slots in `dtype`) are produced.
-static int slot_iteration_impl(const HclsmSlotWeights* W, const float* slots_in, void* sb, const void* k,
-                               int64_t ldk, int64_t k_bstride, const void* v, int64_t ldv, int64_t v_bstride,
-                               bool v_transposed, float* slots_out, int64_t B, int64_t N, int64_t M, int64_t d,
-                               int64_t hidden, float scale, float logit_clamp, float renorm_eps, float slot_clamp,
-                               int dtype, char* ws, const SlotWs& L, hipStream_t st) {
+static int slot_iteration_impl(const HclsmSlotWeights* W, const float* slots_in, void* sb, bool make_sb,
+                               const void* k, int64_t ldk, int64_t k_bstride, const void* v, int64_t ldv,
+                               int64_t v_bstride, bool v_transposed, float* slots_out, int64_t B, int64_t N, int64_t M,
+                               int64_t d, int64_t hidden, float scale, float logit_clamp, float renorm_eps,
+                               float slot_clamp, int dtype, char* ws, const SlotWs& L, hipStream_t st) {
   const int64_t rows = B * N;
   void* q = ws + L.q;
   void* upd = ws + L.upd;
   float* h = reinterpret_cast<float*>(ws + L.h);
   void* m1 = ws + L.m1;
   void* xn = ws + L.xn;
-  // q = LN_pre(slots) W_q^T
-  int rc = ln_impl(slots_in, d, W->ln_pre_w, W->ln_pre_b, xn, d, rows, d, 1e-5f, HCLSM_F32, dtype, st);
+  // q = LN_pre(slots) W_q^T; with make_sb the same pass writes sb (the slots in dtype)
+  int rc = ln_impl(slots_in, d, W->ln_pre_w, W->ln_pre_b, xn, d, rows, d, 1e-5f, HCLSM_F32, dtype, st, kNoLinExt,
+                   make_sb ? sb : nullptr);
   if (rc) return rc;
   rc = linear_impl(xn, d, dtype, W->w_q, d, nullptr, nullptr, 0, q, d, dtype, nullptr, 0, rows, d, d, 0, 0.f, 0,
                    nullptr, nullptr, 0.f, dtype, st);
@@ -1788,10 +1797,8 @@ extern "C" int hclsm_slot_attention_iteration(const HclsmSlotWeights* W, const f
   if (B == 0 || N == 0) return 0;
   hipStream_t st = (hipStream_t)stream;
   char* ws = reinterpret_cast<char*>(workspace);
-  rc = convert_f32(slots_in, ws + L.sb, B * N * d, dtype, st);
-  if (rc) return rc;
-  return slot_iteration_impl(W, slots_in, ws + L.sb, k, ldkv, kv_bstride, v, ldkv, kv_bstride, false, slots_out, B,
-                             N, M, d, hidden, scale, logit_clamp, renorm_eps, slot_clamp, dtype, ws, L, st);
+  return slot_iteration_impl(W, slots_in, ws + L.sb, true, k, ldkv, kv_bstride, v, ldkv, kv_bstride, false, slots_out,
+                             B, N, M, d, hidden, scale, logit_clamp, renorm_eps, slot_clamp, dtype, ws, L, st);
 }
 
 extern "C" int hclsm_slot_attention_forward(const HclsmSlotWeights* W, const float* inputs, int64_t d_in,
@@ -1832,11 +1839,9 @@ extern "C" int hclsm_slot_attention_forward(const HclsmSlotWeights* W, const flo
   }
   (void)esize;
   const void* k = kv;
-  rc = convert_f32(slots0, ws + L.sb, B * N * d, dtype, st);
-  if (rc) return rc;
   if (n_iter == 0) return (int)hipMemcpyAsync(slots_out, slots0, (size_t)B * N * d * 4, hipMemcpyDeviceToDevice, st);
   for (int64_t it = 0; it < n_iter; ++it) {
-    rc = slot_iteration_impl(W, it == 0 ? slots0 : slots_out, ws + L.sb, k, d, M * d, vt, Mp, d * Mp, true,
+    rc = slot_iteration_impl(W, it == 0 ? slots0 : slots_out, ws + L.sb, it == 0, k, d, M * d, vt, Mp, d * Mp, true,
                              slots_out, B, N, M, d, hidden, scale, logit_clamp, renorm_eps, slot_clamp, dtype, ws, L,
                              st);
     if (rc) return rc;
