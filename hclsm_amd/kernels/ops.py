@@ -29,6 +29,11 @@ adds tens of microseconds of Python dispatch per call, which is the size of the 
     hclsm_hip::event_gather_packed(states, rows, indices, stats) -> (B*T, ...)
         packed event rows, zero past the live count stats[0] (no host sync)
     hclsm_hip::event_scatter_packed(base, packed, offsets, slot_of) -> (B, T, ...)
+    hclsm_hip::event_top_down(level0, events, offsets, slot_of, kpad, level2_context?, obj_mask?, params,
+                              compute_dtype) -> fp32 (B, T, N, D)
+        HierarchyManager.forward after the Level-1 pass (hierarchy_manager.py:120-162): scatter, Level-2 gate
+        and alive mask; events packed (kpad = 0) or padded (B, kpad, N, D); params = l2_to_l1.weight,
+        gate_l2_l0.0.weight[, gate_l2_l0.0.bias]
     hclsm_hip::level1_forward(ev, stats, rows, obj_mask?, params, n_heads, ln_eps, compute_dtype) -> fp32
         Level1EventDynamics over the live packed events (level1_event.py:17-133); params in the order of
         Level1Weights (4 + 9 per layer); rows past the live count are zero
@@ -57,6 +62,7 @@ from hclsm_amd.kernels.slot_tracker import TRACK_PARAM_ORDER, TrackerWeights, tr
 from hclsm_amd.kernels.sparse_event_attn import (EventIndex, _gather_padded_raw, _mask_code, _scatter_padded_raw,
                                                  gather_packed, scatter_packed)
 from hclsm_amd.kernels.ssm_scan_bwd import scan_backward
+from hclsm_amd.kernels.top_down import TopDownWeights, event_top_down as _event_top_down
 from hclsm_amd.kernels.ssm_scan_kernel import _block_forward, _scan_forward
 
 Tensor = torch.Tensor
@@ -229,6 +235,25 @@ def event_scatter_packed(base: Tensor, packed: Tensor, offsets: Tensor, slot_of:
 @event_scatter_packed.register_fake
 def _(base, packed, offsets, slot_of):
     return torch.empty_like(base)
+
+
+@torch.library.custom_op("hclsm_hip::event_top_down", mutates_args=())
+def event_top_down(level0: Tensor, events: Tensor, offsets: Tensor, slot_of: Tensor, kpad: int,
+                   level2_context: Optional[Tensor], obj_mask: Optional[Tensor], params: list[Tensor],
+                   compute_dtype: torch.dtype) -> Tensor:
+    B, T = slot_of.shape
+    idx = EventIndex(B, T, None, offsets, None, None, slot_of, None)
+    W = None
+    if level2_context is not None:
+        if len(params) not in (2, 3):
+            raise ValueError("event_top_down: params are l2_to_l1.weight, gate_l2_l0.0.weight[, its bias]")
+        W = TopDownWeights.from_tensors(params[0], params[1], params[2] if len(params) == 3 else None, compute_dtype)
+    return _event_top_down(level0, events, idx, W, level2_context, obj_mask, kpad=int(kpad))
+
+
+@event_top_down.register_fake
+def _(level0, events, offsets, slot_of, kpad, level2_context, obj_mask, params, compute_dtype):
+    return torch.empty(level0.shape, dtype=torch.float32, device=level0.device)
 
 
 @torch.library.custom_op("hclsm_hip::level1_forward", mutates_args=())

@@ -33,6 +33,23 @@ class TopDownWeights:
         return (dtype,) + tuple((p.data_ptr(), p._version) for p in m.parameters())
 
     @classmethod
+    def from_tensors(cls, w_l2: torch.Tensor, w_gate: torch.Tensor, b_gate: torch.Tensor | None,
+                     dtype: torch.dtype = torch.float32) -> "TopDownWeights":
+        """From l2_to_l1.weight (D, d_l2), gate_l2_l0.0.weight (D, 2D) and its bias (D,) or None."""
+        D = w_gate.shape[0]
+        if tuple(w_gate.shape) != (D, 2 * D) or w_l2.dim() != 2 or w_l2.shape[0] != D:
+            raise ValueError(f"gate weight must be (D, 2D) and l2_to_l1 (D, d_l2); got {tuple(w_gate.shape)}, "
+                             f"{tuple(w_l2.shape)}")
+        w_gate = w_gate.detach().float().contiguous()
+        b_gate = None if b_gate is None else b_gate.detach().float().contiguous()
+        w_l2 = w_l2.detach().float().contiguous()
+        if dtype == torch.float32:
+            w_x, ldw = w_gate, 2 * D
+        else:
+            w_x, ldw = w_gate[:, :D].to(dtype).contiguous(), D
+        return cls(w_l2, w_gate, b_gate, w_x, ldw, dtype, D)
+
+    @classmethod
     def from_module(cls, m, dtype: torch.dtype = torch.float32) -> "TopDownWeights":
         """From a HierarchyManager-shaped module (attribute names of hierarchy_manager.py:27-40); cached on the
         module until a parameter changes."""
@@ -40,16 +57,8 @@ class TopDownWeights:
         hit = getattr(m, "_hclsm_top_down_weights", None)
         if hit is not None and hit[0] == key:
             return hit[1]
-        D = m.d_slot
         lin = m.gate_l2_l0[0]
-        w_gate = lin.weight.detach().float().contiguous()
-        b_gate = None if lin.bias is None else lin.bias.detach().float().contiguous()
-        w_l2 = m.l2_to_l1.weight.detach().float().contiguous()
-        if dtype == torch.float32:
-            w_x, ldw = w_gate, 2 * D
-        else:
-            w_x, ldw = w_gate[:, :D].to(dtype).contiguous(), D
-        W = cls(w_l2, w_gate, b_gate, w_x, ldw, dtype, D)
+        W = cls.from_tensors(m.l2_to_l1.weight, lin.weight, lin.bias, dtype)
         m._hclsm_top_down_weights = (key, W)
         return W
 

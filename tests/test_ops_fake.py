@@ -48,6 +48,9 @@ def test_packed_level1_ops_fake_shapes():
     params = [_m(64, 32), _m(64), _m(64), _m(32, 64)] + [_m(1)] * 9
     out = OPS.level1_forward(_m(36, 8, 32), _m(2, dt=i32), _m(36, dt=i32), _m(4, 8), params, 4, 1e-5, torch.bfloat16)
     assert out.shape == (36, 8, 32) and out.dtype == torch.float32
+    td = OPS.event_top_down(_m(4, 9, 3, 64), _m(36, 3, 64), _m(5, dt=i32), _m(4, 9, dt=i32), 0, _m(4, 2, 96),
+                            _m(4, 3), [_m(64, 96), _m(64, 128), _m(64)], torch.bfloat16)
+    assert td.shape == (4, 9, 3, 64) and td.dtype == torch.float32
 
 
 def test_ops_under_fake_tensor_mode():

@@ -110,6 +110,14 @@ def test_packed_level1_ops_equal_eager():
         assert torch.equal(got[:n], want[:n]) and got[n:].abs().sum() == 0
         comb = OPS.event_scatter_packed(states, got, t[1], t[4])
         assert torch.equal(comb, hm.forward_packed(states, want, idx))
+        # the whole output step: against the module's fused call, and the padded-row form
+        l2 = torch.randn(B, 3, 96, generator=g).cuda()
+        td_params = [p.detach() for p in (hm.l2_to_l1.weight, hm.gate_l2_l0[0].weight, hm.gate_l2_l0[0].bias)]
+        td = OPS.event_top_down(states, got, t[1], t[4], 0, l2, obj, td_params, torch.float32)
+        assert torch.equal(td, hm.forward_packed(states, got, idx, l2, obj))
+    torch.library.opcheck(OPS.event_top_down.default,
+                          (states, got, t[1], t[4], 0, l2, obj, td_params, torch.float32),
+                          test_utils=("test_schema", "test_faketensor"))
     torch.library.opcheck(OPS.event_gather_packed.default, (states, t[3], t[2], t[5]),
                           test_utils=("test_schema", "test_faketensor"))
     torch.library.opcheck(OPS.level1_forward.default, (evo, t[5], t[3], obj, W.tensors, 4, W.ln_eps, torch.float32),
