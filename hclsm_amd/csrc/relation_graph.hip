@@ -919,17 +919,29 @@ gnn_edge_str_kernel(GnnArgs a, const float* __restrict__ nstat) {
   }
 }
 
-// s = sum_k x[row, k], q = sum_k x[row, k]^2 for every row (one wave per row)
+// s = sum_k x[row, k], q = sum_k x[row, k]^2 for every row (one wave per row); float4 loads, all of a lane's
+// in flight at once, when vec (D and ldx multiples of 4, x 16-byte aligned)
 __global__ void __launch_bounds__(256)
-gnn_node_stats_kernel(const float* __restrict__ x, int64_t ldx, float* __restrict__ st, int64_t rows, int D) {
+gnn_node_stats_kernel(const float* __restrict__ x, int64_t ldx, float* __restrict__ st, int64_t rows, int D,
+                      int vec) {
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int lane = threadIdx.x & 63;
   float s = 0.f, q = 0.f;
-  for (int k = lane; k < D; k += 64) {
-    const float v = x[row * ldx + k];
-    s += v;
-    q = fmaf(v, v, q);
+  if (vec) {
+    const float4* xr = reinterpret_cast<const float4*>(x + row * ldx);
+#pragma unroll 4
+    for (int u = lane; u < D / 4; u += 64) {
+      const float4 v = xr[u];
+      s += (v.x + v.y) + (v.z + v.w);
+      q = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, q))));
+    }
+  } else {
+    for (int k = lane; k < D; k += 64) {
+      const float v = x[row * ldx + k];
+      s += v;
+      q = fmaf(v, v, q);
+    }
   }
 #pragma unroll
   for (int m = 32; m > 0; m >>= 1) {
@@ -980,14 +992,24 @@ gnn_prep_kernel(const typename MM<DT>::T* __restrict__ W1, const float* __restri
   }
 }
 
-// y[row * ldy + k] = x[row * ldx + k] * alive[row] for k < D (alive nullable).
+// y[row * ldy + k] = x[row * ldx + k] * alive[row] for k < D (alive nullable); VW = 4: float4 units (D, ldx,
+// ldy multiples of 4, x and y 16-byte aligned).
+template <int VW>
 __global__ void __launch_bounds__(256)
 gnn_copy_rows_kernel(const float* __restrict__ x, int64_t ldx, const float* __restrict__ alive,
                      float* __restrict__ y, int64_t ldy, int64_t rows, int D) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= rows * D) return;
-  const int64_t row = e / D, k = e - row * D;
-  y[row * ldy + k] = x[row * ldx + k] * (alive ? alive[row] : 1.f);
+  const int DU = D / VW;
+  if (e >= rows * DU) return;
+  const int64_t row = e / DU, k = (e - row * DU) * VW;
+  const float a = alive ? alive[row] : 1.f;
+  if constexpr (VW == 4) {
+    float4 v = *reinterpret_cast<const float4*>(x + row * ldx + k);
+    v.x *= a; v.y *= a; v.z *= a; v.w *= a;
+    *reinterpret_cast<float4*>(y + row * ldy + k) = v;
+  } else {
+    y[row * ldy + k] = x[row * ldx + k] * a;
+  }
 }
 
 struct GnnWs {
@@ -1135,8 +1157,13 @@ static int copy_rows(const float* x, int64_t ldx, const float* alive, float* y, 
                      hipStream_t st) {
   const int64_t n = rows * D;
   if (n == 0) return 0;
-  hipLaunchKernelGGL(gnn_copy_rows_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, ldx, alive, y, ldy,
-                     rows, (int)D);
+  const bool vec = D % 4 == 0 && ldx % 4 == 0 && ldy % 4 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)y & 15) == 0;
+  if (vec)
+    hipLaunchKernelGGL(gnn_copy_rows_kernel<4>, dim3((unsigned)((n / 4 + 255) / 256)), dim3(256), 0, st, x, ldx, alive,
+                       y, ldy, rows, (int)D);
+  else
+    hipLaunchKernelGGL(gnn_copy_rows_kernel<1>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, ldx, alive, y,
+                       ldy, rows, (int)D);
   HCLSM_LAUNCH_CHECK();
   return 0;
 }
@@ -1190,8 +1217,9 @@ static int gnn_forward(const float* nodes, const float* alive, float* nodes_out,
     a.agg = msg ? XA + D : nullptr;
     a.causal = caus ? causal : nullptr;
     if constexpr (DT != HCLSM_F32) {
+      const int vec = D % 4 == 0 && ld % 4 == 0 && ((uintptr_t)XA & 15) == 0;
       hipLaunchKernelGGL(gnn_node_stats_kernel, dim3((unsigned)((R + 3) / 4)), dim3(256), 0, st, XA, ld, nstat, R,
-                         (int)D);
+                         (int)D, vec);
       HCLSM_LAUNCH_CHECK();
       e = launch_edges_resident<DT>(a, nstat, st);
       if (e != 1) return e;
