@@ -323,13 +323,23 @@ track_cost_res_kernel(TrackCostArgs a) {
   }
 }
 
-// y[r, k] = clamp(x[r, k], -50, 50) (NaN passes through, as torch.clamp)
+// y[r, k] = clamp(x[r, k], -50, 50) (NaN passes through, as torch.clamp); VW = 4: float4 units (n a multiple of
+// 4, x and y 16-byte aligned)
+__device__ __forceinline__ float trk_clamp1(float v) {
+  return v < -TRK_SLOT_CLAMP ? -TRK_SLOT_CLAMP : (v > TRK_SLOT_CLAMP ? TRK_SLOT_CLAMP : v);
+}
+template <int VW>
 __global__ void __launch_bounds__(256)
 trk_clamp_kernel(const float* __restrict__ x, float* __restrict__ y, int64_t n) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= n) return;
-  const float v = x[e];
-  y[e] = v < -TRK_SLOT_CLAMP ? -TRK_SLOT_CLAMP : (v > TRK_SLOT_CLAMP ? TRK_SLOT_CLAMP : v);
+  if (e >= n / VW) return;
+  if constexpr (VW == 4) {
+    float4 v = reinterpret_cast<const float4*>(x)[e];
+    v.x = trk_clamp1(v.x); v.y = trk_clamp1(v.y); v.z = trk_clamp1(v.z); v.w = trk_clamp1(v.w);
+    reinterpret_cast<float4*>(y)[e] = v;
+  } else {
+    y[e] = trk_clamp1(x[e]);
+  }
 }
 
 // --------------------------------------------------------------------------------------------- Sinkhorn
@@ -549,17 +559,28 @@ track_sequence_kernel(const float* __restrict__ C, const float* __restrict__ ali
 
 // ------------------------------------------------------------------------------------- reorder and GRU
 // y[row, k] = x[frame * N + perm[row], k] with frame = row / N; an index outside [0, N) gives a NaN row.
-template <typename I>
+// VW = 4: four consecutive k per thread (D a multiple of 4; x and y 16-byte aligned).
+template <typename I, int VW>
 __global__ void __launch_bounds__(256)
 trk_gather_kernel(const float* __restrict__ x, const I* __restrict__ perm, float* __restrict__ y, int64_t rows,
                   int N, int D) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= rows * D) return;
-  const int64_t row = e / D;
-  const int k = (int)(e - row * D);
+  const int DU = D / VW;
+  if (e >= rows * DU) return;
+  const int64_t row = e / DU;
+  const int k = (int)(e - row * DU) * VW;
   const int64_t p = (int64_t)perm[row];
-  y[e] = (p >= 0 && p < N) ? x[((row / N) * N + p) * D + k] : __int_as_float(0x7fc00000);
+  const float nan = __int_as_float(0x7fc00000);
+  const bool in = p >= 0 && p < N;
+  const float* src = x + ((row / N) * N + (in ? p : 0)) * D + k;
+  if constexpr (VW == 4) {
+    *reinterpret_cast<float4*>(y + row * D + k) =
+        in ? *reinterpret_cast<const float4*>(src) : make_float4(nan, nan, nan, nan);
+  } else {
+    y[row * D + k] = in ? *src : nan;
+  }
 }
+
 
 // torch.nn.GRUCell gates and the matched blend of SlotTracker.reorder_and_update (slot_tracker.py:150-156)
 // for rows (f, i), f < nf, i < N:
@@ -590,6 +611,17 @@ trk_gru_gate_kernel(const float* __restrict__ GI, int64_t sgi, const int* __rest
 
 // ------------------------------------------------------------------------------------------------ host
 static unsigned blocks256(int64_t n) { return (unsigned)((n + 255) / 256); }
+
+template <typename I>
+static void launch_gather(const float* x, const I* perm, float* y, int64_t rows, int64_t N, int64_t D,
+                          hipStream_t st) {
+  if (D % 4 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)y & 15) == 0)
+    hipLaunchKernelGGL((trk_gather_kernel<I, 4>), dim3(blocks256(rows * D / 4)), dim3(256), 0, st, x, perm, y, rows,
+                       (int)N, (int)D);
+  else
+    hipLaunchKernelGGL((trk_gather_kernel<I, 1>), dim3(blocks256(rows * D)), dim3(256), 0, st, x, perm, y, rows,
+                       (int)N, (int)D);
+}
 
 template <int DT, int NW, int KC>
 static size_t cost_lds(int D) {
@@ -654,7 +686,10 @@ static int launch_cost_dt(int dtype, const TrackCostArgs& a, hipStream_t st) {
 
 static int clamp_rows(const float* x, float* y, int64_t n, hipStream_t st) {
   if (n == 0) return 0;
-  hipLaunchKernelGGL(trk_clamp_kernel, dim3(blocks256(n)), dim3(256), 0, st, x, y, n);
+  if (n % 4 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)y & 15) == 0)
+    hipLaunchKernelGGL(trk_clamp_kernel<4>, dim3(blocks256(n / 4)), dim3(256), 0, st, x, y, n);
+  else
+    hipLaunchKernelGGL(trk_clamp_kernel<1>, dim3(blocks256(n)), dim3(256), 0, st, x, y, n);
   HCLSM_LAUNCH_CHECK();
   return 0;
 }
@@ -814,8 +849,7 @@ extern "C" int hclsm_slot_track_reorder_update(const float* slots_t1, const int6
   float* GH = reinterpret_cast<float*>(ws + al256t((size_t)R * 3 * D * 4));
   const float* b_ih = reinterpret_cast<const float*>(params[2]);
   const float* b_hh = reinterpret_cast<const float*>(params[3]);
-  hipLaunchKernelGGL((trk_gather_kernel<int64_t>), dim3(blocks256(R * D)), dim3(256), 0, st, slots_t1, perm,
-                     reordered, R, (int)N, (int)D);
+  launch_gather<int64_t>(slots_t1, perm, reordered, R, N, D, st);
   HCLSM_LAUNCH_CHECK();
   int rc;
   if ((rc = linear_rows(reordered, D, HCLSM_F32, params[0], D, b_ih, nullptr, 0, GI, 3 * D, HCLSM_F32, R, 3 * D, D, 0,
@@ -903,8 +937,7 @@ extern "C" int hclsm_slot_track_sequence(const float* slots, const float* alive,
     return 0;
   });
   if (rc) return rc;
-  hipLaunchKernelGGL((trk_gather_kernel<int>), dim3(blocks256(R * D)), dim3(256), 0, st, slots, P, tracked, R, (int)N,
-                     (int)D);
+  launch_gather<int>(slots, P, tracked, R, N, D, st);
   HCLSM_LAUNCH_CHECK();
   if (!hidden) return 0;
   // GRU carry (slot_tracker.py:150-156): hidden_0 = 0; for t >= 1 hidden_t = blend(GRU(tracked_t, hidden_{t-1}))
