@@ -12,9 +12,9 @@ Infinity Cache, so the timed loop rotates over NSETS distinct input/output sets
 
 Prints ONE JSON line.  `value` is the scan's algorithmic bytes / average step time
 (GB/s); `roofline` prices the same kernel against MI355X's 8 TB/s HBM peak with the
-per-launch duration measured by HIP events; `cpu_baseline` times the numpy oracle
-(float32, the reference's sequential_ssm_scan semantics in raw mode) on a bounded
-sample of the same workload on the host cores.
+per-launch duration measured by HIP events; `cpu_baseline` times the reference's sequential scan loop
+written with the same torch ops on the CPU (oracle/torch_cpu.py, raw mode) on the whole
+config-1 input, on the host cores.
 """
 
 from __future__ import annotations
