@@ -2,7 +2,7 @@
 //
 // A "segment" p is a list of rows of a [P, T, H, dh] tensor given by int32
 // offsets/indices (the event index): rows (p, indices[offsets[p] + i]), i < L_p.
-//   TRACK_CAUSAL: query i attends keys j <= i of its segment (BASELINE config 3/4).
+//   TRACK_CAUSAL: query i attends keys j <= i of its segment (benchmark config 3/4).
 //   SLOTS:        query i attends every key j of its segment not flagged in
 //                 key_pad[p, j] (the N x N attention of Level-1, level1_event.py:37-52).
 //

@@ -14,7 +14,7 @@ linear over the concatenated [W_k; W_v]) and runs n_iter iterations (dynamic_slo
 Slots are carried in fp32 between steps; every MFMA operand is in the compute dtype
 (bf16 for the benchmark configuration, fp32 for reference-precision runs).  Semantics
 are selected by ``SlotMode``: the reference module's clamps (logits +-30 :118, slots
-+-50 :130, MLP hidden 4*d), or BASELINE config 2 (no clamps, +1e-8 renormalised weighted
++-50 :130, MLP hidden 4*d), or benchmark config 2 (no clamps, +1e-8 renormalised weighted
 mean, MLP hidden 768).
 """
 
@@ -37,7 +37,7 @@ class SlotMode:
 
 
 REFERENCE_MODE = SlotMode(logit_clamp=30.0, renorm_eps=None, slot_clamp=50.0)   # dynamic_slots.py:118,130
-CONFIG2_MODE = SlotMode(logit_clamp=None, renorm_eps=1e-8, slot_clamp=None)
+CONFIG2_MODE = SlotMode(logit_clamp=None, renorm_eps=1e-8, slot_clamp=None)     # benchmark config 2
 
 _WEIGHT_KEYS = ("w_q", "w_ih", "w_hh", "w1", "w2", "w_k", "w_v")
 _F32_KEYS = ("ln_pre_w", "ln_pre_b", "b_ih", "b_hh", "ln_mlp_w", "ln_mlp_b", "b1", "b2", "ln_in_w", "ln_in_b")

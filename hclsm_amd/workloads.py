@@ -58,7 +58,7 @@ def xavier_uniform(shape, generator):
 
 
 def slot_config(B=32, M=196, N=32, d=384, hidden=768, seed=1002, wdtype=torch.bfloat16):
-    """BASELINE config 2: tokens = LayerNorm(randn(B, M, d)) (no affine); mu ~ 0.1 N(0,1);
+    """benchmark config 2: tokens = LayerNorm(randn(B, M, d)) (no affine); mu ~ 0.1 N(0,1);
     slots0 = mu + 0.5 N(0,1); Xavier-uniform W_q, W_k, W_v (d x d), GRU W_ih, W_hh (3d x d),
     MLP d -> hidden -> d; biases 0, LayerNorm weight 1 / bias 0; matrices rounded to ``wdtype``.
     Returns (inputs, slots0, weights) as CPU tensors (weights already rounded, stored fp32)."""

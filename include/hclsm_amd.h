@@ -38,7 +38,7 @@ extern "C" {
 #define HCLSM_EVENT_NONZERO 1 /* mask != 0 (NaN is an event): sparse_event_attn.py:65 */
 
 /* event attention modes */
-#define HCLSM_ATTN_TRACK_CAUSAL 0 /* causal over the events of one track (BASELINE configs 3/4) */
+#define HCLSM_ATTN_TRACK_CAUSAL 0 /* causal over the events of one track (benchmark configs 3/4) */
 #define HCLSM_ATTN_SLOTS        1 /* all rows of a segment, key padding (level1_event.py:37-52) */
 
 /* SSM scan clamp modes */

@@ -20,7 +20,7 @@ Gather / scatter (byte moves, bit-exact):
 
 Event attention (float):
   * "track_causal": per track, causal softmax attention among that track's event rows
-    (BASELINE config 3/4 semantics).
+    (the benchmark's config 3/4 semantics).
   * "slots": per (row, head), attention across the N slot rows with a key padding mask --
     the core of nn.MultiheadAttention in EventTransformerBlock (dynamics/level1_event.py:37-52),
     without its projections.

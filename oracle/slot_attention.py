@@ -11,7 +11,7 @@ Iteration (reference hclsm/objects/dynamic_slots.py:98-131, DynamicSlotAttention
   q       = sn W_q^T                                               :112
   logits  = q k^T * scale, optionally clamped to +-logit_clamp     :116-118
   attn    = softmax over slots                                     :119
-  attn    = (attn + eps) / sum_tokens(attn + eps)   if renorm_eps  (BASELINE config 2's weighted mean)
+  attn    = (attn + eps) / sum_tokens(attn + eps)   if renorm_eps  (benchmark config 2's weighted mean)
   updates = attn v                                                 :121
   slots   = GRUCell(updates, slots)                                :123-126 (torch GRUCell equations)
   slots   = slots + MLP(LayerNorm(slots))                          :128 (Linear, ReLU, Linear)

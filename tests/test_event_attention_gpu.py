@@ -36,7 +36,7 @@ def _run_causal(q, k, v, m, out="packed"):
 
 
 def test_config3_bf16():
-    """1024 tracks, T=64, 6 heads x 64, p=0.15 with t=0 forced."""
+    """benchmark config 3: 1024 tracks, T=64, 6 heads x 64, p=0.15 with t=0 forced."""
     q, k, v, m = _data(1024, 64, 6, 64, torch.bfloat16, 0.15, seed=1003)
     o, _ = _run_causal(q, k, v, m)
     i = ev.event_index(m.numpy())

@@ -146,7 +146,7 @@ def test_iteration_matches_oracle(mode_name, dtype, tol):
 
 
 def test_config2_forward_bf16():
-    """32 frames x 196 tokens x 384, 32 slots, 3 iterations, MLP 768, bf16 weights."""
+    """benchmark config 2: 32 frames x 196 tokens x 384, 32 slots, 3 iterations, MLP 768, bf16 weights."""
     from hclsm_amd.kernels import slot_iteration as si
     from hclsm_amd.workloads import slot_config
     tokens, slots0, w = slot_config()
