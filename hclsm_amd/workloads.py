@@ -86,3 +86,26 @@ def slot_flops(B=32, M=196, N=32, d=384, hidden=768, n_iter=3):
           + 2 * B * N * d * 3 * d * 2   # GRU W_ih, W_hh
           + 2 * B * N * d * hidden * 2)  # MLP
     return kv + n_iter * it
+
+
+def chain_config(device, seed=1004, H=12, dh=64, p_event=0.05):
+    """benchmark config 4, drawn on ``device`` (3.2 G values; a CPU draw of this size takes minutes) from
+    ``torch.Generator(device).manual_seed(1004)`` in this order: x0 = N(0,1) (1024, 1024, 768);
+    dt = softplus(-2 + 0.5 N(0,1)); A_log ~ U(0, ln 16) (768, 16); B, C = N(0,1)/4 (1024, 1024, 16);
+    D = N(0,1) (768); event mask = U(0,1) < p_event with t=0 forced, (1024, 1024) fp32; q, k, v = N(0,1)
+    (1024, 1024, H, dh).  Scan tensors and q, k, v in bf16; A_log, D and the mask fp32."""
+    N, T, Dn, S = 1024, 1024, 768, 16
+    g = torch.Generator(device=device).manual_seed(seed)
+    bf = torch.bfloat16
+    out = dict(x=torch.randn(N, T, Dn, generator=g, device=device).to(bf))
+    out["dt"] = F.softplus(-2 + 0.5 * torch.randn(N, T, Dn, generator=g, device=device)).to(bf)
+    out["A_log"] = torch.rand(Dn, S, generator=g, device=device) * math.log(16.0)
+    out["B"] = (torch.randn(N, T, S, generator=g, device=device) / 4).to(bf)
+    out["C"] = (torch.randn(N, T, S, generator=g, device=device) / 4).to(bf)
+    out["D"] = torch.randn(Dn, generator=g, device=device)
+    m = (torch.rand(N, T, generator=g, device=device) < p_event).float()
+    m[:, 0] = 1
+    out["mask"] = m
+    for name in ("q", "k", "v"):
+        out[name] = torch.randn(N, T, H, dh, generator=g, device=device).to(bf)
+    return out

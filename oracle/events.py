@@ -145,22 +145,30 @@ def track_causal_attention(q, k, v, index, scale=None):
     """q, k, v: (tracks, T, H, dh) (any float dtype, upcast to float64).
     Returns packed O (total, H, dh) float64: for each track, causal attention among its
     event rows in ascending order."""
-    q = np.asarray(q, np.float64)
-    k = np.asarray(k, np.float64)
-    v = np.asarray(v, np.float64)
-    nb, T, H, dh = q.shape
+    q, k, v = (np.asarray(t) for t in (q, k, v))
+    rows, ts = index["rows"], index["indices"]
+    return track_causal_attention_packed(q[rows, ts], k[rows, ts], v[rows, ts], index["offsets"], scale)
+
+
+def track_causal_attention_packed(qp, kp, vp, offsets, scale=None):
+    """The same on packed event rows: qp, kp, vp (total, H, dh), track b owning rows
+    offsets[b] .. offsets[b+1]-1 in ascending t (the gather_packed order)."""
+    q = np.asarray(qp, np.float64)
+    k = np.asarray(kp, np.float64)
+    v = np.asarray(vp, np.float64)
+    total, H, dh = q.shape
     if scale is None:
         scale = dh ** -0.5
-    out = np.zeros((index["total"], H, dh))
-    for b in range(nb):
-        o, c = int(index["offsets"][b]), int(index["counts"][b])
+    out = np.zeros((total, H, dh))
+    for b in range(len(offsets) - 1):
+        o, c = int(offsets[b]), int(offsets[b + 1]) - int(offsets[b])
         if c == 0:
             continue
-        ts = index["indices"][o:o + c]
-        Q, Kk, V = q[b, ts], k[b, ts], v[b, ts]          # (c, H, dh)
+        Q, Kk, V = q[o:o + c], k[o:o + c], v[o:o + c]      # (c, H, dh)
+        causal = np.tril(np.ones((c, c), bool))
         for h in range(H):
             s = Q[:, h] @ Kk[:, h].T * scale               # (c, c)
-            s = np.where(np.tril(np.ones((c, c), bool)), s, -np.inf)
+            s = np.where(causal, s, -np.inf)
             out[o:o + c, h] = _softmax_rows(s) @ V[:, h]
     return out
 
