@@ -130,6 +130,27 @@ def build_event_index(event_mask: torch.Tensor, rule: str = "gt_half") -> EventI
     return idx
 
 
+def _check_grid(fn: str, name: str, t: torch.Tensor, idx: EventIndex) -> None:
+    """A (B, T, ...) tensor must match the (B, T) of the event index it is used with."""
+    if t.dim() < 2 or tuple(t.shape[:2]) != (idx.B, idx.T):
+        raise ValueError(f"{fn}: {name} must be ({idx.B}, {idx.T}, ...) to match the event index, "
+                         f"got {tuple(t.shape)}")
+
+
+def _check_rows(fn: str, a_name: str, a_row, b_name: str, b_row) -> None:
+    if tuple(a_row) != tuple(b_row):
+        raise ValueError(f"{fn}: the rows of {a_name} {tuple(a_row)} and {b_name} {tuple(b_row)} differ")
+
+
+def _check_packed_rows(fn: str, packed: torch.Tensor, idx: EventIndex) -> None:
+    """Packed rows are read at offsets[b] + slot_of[b, t] < total: a tensor with fewer than B*T rows
+    must hold at least total rows (one host read of the device-side total, only in that case)."""
+    if packed.dim() < 1:
+        raise ValueError(f"{fn}: packed must be (rows, ...), got a 0-d tensor")
+    if packed.shape[0] < idx.B * idx.T and packed.shape[0] < idx.total():
+        raise ValueError(f"{fn}: packed has {packed.shape[0]} rows but the event index holds {idx.total()} events")
+
+
 def _row_bytes(t: torch.Tensor) -> int:
     n = 1
     for s in t.shape[2:]:
@@ -188,12 +209,20 @@ class _ScatterPadded(torch.autograd.Function):
 def gather_events_padded(states: torch.Tensor, idx: EventIndex, K: int) -> torch.Tensor:
     """(B, T, ...) -> (B, K, ...) event rows, ascending, zero rows past each row's count."""
     require_gpu("gather_events_padded", states)
+    _check_grid("gather_events_padded", "states", states, idx)
+    if int(K) < 0:
+        raise ValueError(f"gather_events_padded: K must be >= 0, got {K}")
     return _GatherPadded.apply(states, idx, int(K))
 
 
 def scatter_events_padded(base: torch.Tensor, updates: torch.Tensor, idx: EventIndex) -> torch.Tensor:
     """out = base with out[b, t] = updates[b, slot_of[b,t]] for event rows whose slot < K."""
     require_gpu("scatter_events_padded", base, updates)
+    _check_grid("scatter_events_padded", "base", base, idx)
+    if updates.dim() != base.dim() or updates.shape[0] != idx.B:
+        raise ValueError(f"scatter_events_padded: updates must be ({idx.B}, K) + {tuple(base.shape[2:])}, "
+                         f"got {tuple(updates.shape)}")
+    _check_rows("scatter_events_padded", "updates", updates.shape[2:], "base", base.shape[2:])
     return _ScatterPadded.apply(base, updates, idx, int(updates.shape[1]))
 
 
@@ -207,8 +236,11 @@ def gather_packed(src: torch.Tensor, idx: EventIndex, capacity: int | None = Non
     """(B, T, ...) -> (capacity, ...) packed event rows (first idx.total() valid); no host sync.
     Rows past the live count are left uninitialised, or zero with ``zero_fill``."""
     require_gpu("gather_packed", src)
+    _check_grid("gather_packed", "src", src, idx)
     s = src.contiguous()
     cap = idx.B * idx.T if capacity is None else int(capacity)
+    if cap < 0:
+        raise ValueError(f"gather_packed: capacity must be >= 0, got {cap}")
     alloc = torch.zeros if zero_fill else torch.empty
     out = alloc((cap,) + tuple(s.shape[2:]), dtype=s.dtype, device=s.device)
     rc = _lib.lib().hclsm_event_gather_packed(_lib.ptr(s), _lib.ptr(out), _row_bytes(s), idx.B, idx.T, cap,
@@ -228,9 +260,24 @@ def scatter_packed(base: torch.Tensor | None, packed: torch.Tensor | None, idx: 
     p = None if packed is None else packed.contiguous()
     b = None if base is None else base.contiguous()
     like = p if p is not None else b
+    if b is not None:
+        _check_grid("scatter_packed", "base", b, idx)
+    if p is not None:
+        _check_packed_rows("scatter_packed", p, idx)
+        if b is not None:
+            _check_rows("scatter_packed", "packed", p.shape[1:], "base", b.shape[2:])
+    if b is not None and p is not None and b.dtype != p.dtype:
+        raise TypeError(f"scatter_packed: base and packed must share a dtype, got {b.dtype} and {p.dtype}")
     if out is None:
         rest = tuple(p.shape[1:]) if p is not None else tuple(b.shape[2:])
         out = torch.empty((idx.B, idx.T) + rest, dtype=like.dtype, device=like.device)
+    else:
+        require_gpu("scatter_packed", out, like)
+        _check_grid("scatter_packed", "out", out, idx)
+        _check_rows("scatter_packed", "out", out.shape[2:], "packed" if p is not None else "base",
+                    p.shape[1:] if p is not None else b.shape[2:])
+        if out.dtype != like.dtype or not out.is_contiguous():
+            raise ValueError("scatter_packed: out must be contiguous and typed like its inputs")
     rb = out.element_size()
     for s in out.shape[2:]:
         rb *= s
@@ -276,6 +323,7 @@ def gather_events_packed(states: torch.Tensor, idx: EventIndex) -> torch.Tensor:
     otherwise they are unspecified: the C entry points read the live rows only, and every row op and
     per-event attention keeps a later row to itself."""
     require_gpu("gather_events_packed", states)
+    _check_grid("gather_events_packed", "states", states, idx)
     return _GatherPacked.apply(states, idx, torch.is_grad_enabled())
 
 
@@ -283,6 +331,9 @@ def scatter_events_packed(base: torch.Tensor, packed: torch.Tensor, idx: EventIn
     """Differentiable packed scatter: base with out[b, t] = packed[offsets[b] + slot_of[b, t]] at
     events; no host sync."""
     require_gpu("scatter_events_packed", base, packed)
+    _check_grid("scatter_events_packed", "base", base, idx)
+    _check_packed_rows("scatter_events_packed", packed, idx)
+    _check_rows("scatter_events_packed", "packed", packed.shape[1:], "base", base.shape[2:])
     return _ScatterPacked.apply(base, packed, idx)
 
 

@@ -157,3 +157,45 @@ def test_hierarchy_gather_count():
     mask[:, 2] = 1.0
     mask[:, 5] = 1.0
     assert build_event_index(mask).kmax() == 2
+
+
+def test_wrappers_reject_tensors_that_do_not_match_the_index():
+    """Every gather / scatter wrapper checks its tensors against the event index on the host, before
+    any launch: a (B, T) mismatch, a row-shape mismatch or too few packed rows raise ValueError."""
+    from hclsm_amd.kernels import sparse_event_attn as sea
+    m = _mask(4, 10, 0.5, seed=31, force0=True).cuda()
+    idx = sea.build_event_index(m)
+    total = idx.total()
+    good = torch.randn(4, 10, 3, 8, device="cuda")
+    wrong_b = torch.randn(5, 10, 3, 8, device="cuda")
+    wrong_t = torch.randn(4, 9, 3, 8, device="cuda")
+    for bad in (wrong_b, wrong_t):
+        with pytest.raises(ValueError):
+            sea.gather_events_padded(bad, idx, 3)
+        with pytest.raises(ValueError):
+            sea.gather_packed(bad, idx)
+        with pytest.raises(ValueError):
+            sea.gather_events_packed(bad, idx)
+        with pytest.raises(ValueError):
+            sea.scatter_events_padded(bad, torch.zeros(bad.shape[0], 3, 3, 8, device="cuda"), idx)
+        with pytest.raises(ValueError):
+            sea.scatter_packed(bad, torch.zeros(total, 3, 8, device="cuda"), idx)
+        with pytest.raises(ValueError):
+            sea.scatter_events_packed(bad, torch.zeros(total, 3, 8, device="cuda"), idx)
+    # updates with another row shape or batch size
+    with pytest.raises(ValueError):
+        sea.scatter_events_padded(good, torch.zeros(4, 3, 3, 7, device="cuda"), idx)
+    with pytest.raises(ValueError):
+        sea.scatter_events_padded(good, torch.zeros(3, 3, 3, 8, device="cuda"), idx)
+    # packed with fewer rows than events, or another row shape
+    with pytest.raises(ValueError):
+        sea.scatter_packed(good, torch.zeros(total - 1, 3, 8, device="cuda"), idx)
+    with pytest.raises(ValueError):
+        sea.scatter_events_packed(good, torch.zeros(total - 1, 3, 8, device="cuda"), idx)
+    with pytest.raises(ValueError):
+        sea.scatter_packed(good, torch.zeros(total, 3, 7, device="cuda"), idx)
+    with pytest.raises(ValueError):
+        sea.gather_events_padded(good, idx, -1)
+    # the matching calls still work, and exactly total packed rows suffice
+    out = sea.scatter_packed(good, sea.gather_packed(good, idx)[:total].contiguous(), idx)
+    assert torch.equal(out, good)
