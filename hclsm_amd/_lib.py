@@ -16,7 +16,7 @@ import torch  # noqa: F401  (must precede the CDLL load, see module docstring)
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libhclsm_amd.so"
 
 F32, BF16, F16, U8 = 0, 1, 2, 3
-SCAN_RAW, SCAN_MODEL = 0, 1
+SCAN_RAW, SCAN_MODEL, SCAN_BLOCK = 0, 1, 2
 EVENT_GT_HALF, EVENT_NONZERO = 0, 1
 ATTN_TRACK_CAUSAL, ATTN_SLOTS = 0, 1
 

@@ -50,6 +50,17 @@ template <> struct Elem<HCLSM_F16> {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// softplus(v) = max(v, 0) + log1p(exp(-|v|)), torch's threshold 20 kept.  log1p(e) for e in (0, 1] as
+// log(u) * e / (u - 1) with u = 1 + e (the rounding of u cancels to first order; e / (u - 1) = 1
+// when u rounds to 1).
+__device__ __forceinline__ float softplus_f(float v) {
+  const float e = __expf(-fabsf(v));
+  const float u = 1.f + e;
+  const float d = u - 1.f;
+  const float l = d == 0.f ? e : __logf(u) * (e * __builtin_amdgcn_rcpf(d));
+  return v > 20.f ? v : fmaxf(v, 0.f) + l;
+}
+
 // x * sigmoid(x) (torch.nn.functional.silu).
 __device__ __forceinline__ float silu_f(float g) { return g * __builtin_amdgcn_rcpf(1.f + __expf(-g)); }
 

@@ -22,22 +22,12 @@ namespace hclsm {
 // Internal mode of hclsm_ssm_block_scan_fwd: the MODEL clamps, dt = softplus(dt input) before
 // its clamp, and the output multiplied by silu(gate) -- the SimplifiedSSMBlock epilogues
 // (level0_ssm.py:73, :76, :103) fused into the scan.
-constexpr int SCAN_BLOCK = 2;
+constexpr int SCAN_BLOCK = HCLSM_SCAN_BLOCK;
 struct ScanEpi {
   const void* gate;   // [batch][T][d_inner], I/O type; required in SCAN_BLOCK
   void* y_pre;        // optional: the scan output before gating (kept for the backward)
 };
 
-// softplus(v) = max(v, 0) + log1p(exp(-|v|)), torch's threshold 20 kept.  log1p(e) for e in (0, 1] as
-// log(u) * e / (u - 1) with u = 1 + e (the rounding of u cancels to first order; e / (u - 1) = 1
-// when u rounds to 1).
-__device__ __forceinline__ float softplus_f(float v) {
-  const float e = __expf(-fabsf(v));
-  const float u = 1.f + e;
-  const float d = u - 1.f;
-  const float l = d == 0.f ? e : __logf(u) * (e * __builtin_amdgcn_rcpf(d));
-  return v > 20.f ? v : fmaxf(v, 0.f) + l;
-}
 
 template <int MODE>
 __device__ __forceinline__ float scan_dt(float v) {
@@ -49,6 +39,10 @@ __device__ __forceinline__ float scan_dt(float v) {
 
 constexpr int SCAN_TCHUNK = 8;
 constexpr int SCAN_MAX_BLOCK = 256;
+// Generic kernel: one lane per channel holds up to 32 states; larger d_state splits a channel's
+// states over 2 or 4 adjacent lanes (64 / 128 padded states), whose output partials are summed by
+// lane exchange, so no lane keeps more than 32 states and 32 gate exponents in registers.
+constexpr int scan_lanes_per_channel(int SP) { return SP > 32 ? SP / 32 : 1; }
 
 template <int DT, int SP, int MODE>
 __global__ void __launch_bounds__(SCAN_MAX_BLOCK)
@@ -64,19 +58,25 @@ ssm_scan_fwd_kernel(const typename Elem<DT>::T* __restrict__ x,
   using E = Elem<DT>;
   using TT = typename E::T;
   constexpr int TC = SCAN_TCHUNK;
+  constexpr int LPC = scan_lanes_per_channel(SP);   // adjacent lanes sharing one channel
+  constexpr int SPL = SP / LPC;                      // states per lane
   // B_t / C_t rows of the current and the next chunk, fp32, zero-padded to SP.
   __shared__ float4 sB[2][TC][SP / 4];
   __shared__ float4 sC[2][TC][SP / 4];
 
   const int n = blockIdx.x;
-  const int d = blockIdx.y * blockDim.x + threadIdx.x;
+  const int lt = blockIdx.y * blockDim.x + threadIdx.x;
+  const int d = lt / LPC;
+  const int sbase = (lt % LPC) * SPL;   // this lane's first state
   const bool act = d < Dn;
+  const bool writer = act && sbase == 0;   // one lane per channel stores y
   const int dd = act ? d : 0;  // inactive lanes read a valid address and store nothing
 
   // gate exponent per state in log2 units: A[d,s] * log2(e); padded states get 0
-  float a2[SP];
+  float a2[SPL];
 #pragma unroll
-  for (int s = 0; s < SP; ++s) {
+  for (int i = 0; i < SPL; ++i) {
+    const int s = sbase + i;
     float a = 0.f;
     {
       // unconditional load of a valid element, then select: no divergent branch
@@ -84,14 +84,14 @@ ssm_scan_fwd_kernel(const typename Elem<DT>::T* __restrict__ x,
       if (MODE != HCLSM_SCAN_RAW) e = fminf(fmaxf(e, 1e-6f), 1.0f);
       a = (s < S) ? -e * HCLSM_LOG2E : 0.f;
     }
-    a2[s] = a;
+    a2[i] = a;
   }
   const bool has_d = Dskip != nullptr;
   const float dsk = has_d ? Dskip[dd] : 0.f;
 
-  float h[SP];
+  float h[SPL];
 #pragma unroll
-  for (int s = 0; s < SP; ++s) h[s] = 0.f;
+  for (int i = 0; i < SPL; ++i) h[i] = 0.f;
 
   const size_t row0 = (size_t)n * T;
   const TT* xp = x + row0 * Dn + dd;
@@ -157,20 +157,22 @@ ssm_scan_fwd_kernel(const typename Elem<DT>::T* __restrict__ x,
     const float u = dtv * xval;
     float y0 = 0.f, y1 = 0.f;
 #pragma unroll
-    for (int q = 0; q < SP / 4; ++q) {
-      const float4 b4 = sB[buf][j][q];
-      const float4 c4 = sC[buf][j][q];
+    for (int q = 0; q < SPL / 4; ++q) {
+      const float4 b4 = sB[buf][j][sbase / 4 + q];
+      const float4 c4 = sC[buf][j][sbase / 4 + q];
       const float bb[4] = {b4.x, b4.y, b4.z, b4.w};
       const float cc[4] = {c4.x, c4.y, c4.z, c4.w};
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int s = 4 * q + r;
-        const float g = fast_exp2(dtv * a2[s]);
-        h[s] = fmaf(g, h[s], u * bb[r]);
-        if (r & 1) y1 = fmaf(h[s], cc[r], y1); else y0 = fmaf(h[s], cc[r], y0);
+        const int i = 4 * q + r;
+        const float g = fast_exp2(dtv * a2[i]);
+        h[i] = fmaf(g, h[i], u * bb[r]);
+        if (r & 1) y1 = fmaf(h[i], cc[r], y1); else y0 = fmaf(h[i], cc[r], y0);
       }
     }
     float yv = y0 + y1;
+    if constexpr (LPC >= 2) yv += __shfl_xor(yv, 1, 64);   // sum over the channel's lanes
+    if constexpr (LPC >= 4) yv += __shfl_xor(yv, 2, 64);
     if (has_d) yv = fmaf(dsk, xval, yv);
     return yv;
   };
@@ -194,7 +196,7 @@ ssm_scan_fwd_kernel(const typename Elem<DT>::T* __restrict__ x,
 #pragma unroll
       for (int j = 0; j < TC; ++j) {
         const float yv = step(buf, j, xv[j], dv[j]);
-        if (act) store_y(t0 + j, yv);
+        if (writer) store_y(t0 + j, yv);
       }
     } else {
       for (int j = 0; j < T - t0; ++j) {
@@ -202,7 +204,7 @@ ssm_scan_fwd_kernel(const typename Elem<DT>::T* __restrict__ x,
 #pragma unroll
         for (int k = 0; k < TC; ++k) if (k == j) { xj = xv[k]; dj = dv[k]; }
         const float yv = step(buf, j, xj, dj);
-        if (act) store_y(t0 + j, yv);
+        if (writer) store_y(t0 + j, yv);
       }
     }
     if (more) {
@@ -216,8 +218,8 @@ ssm_scan_fwd_kernel(const typename Elem<DT>::T* __restrict__ x,
   if (h_final != nullptr && act) {
     float* hp = h_final + ((size_t)n * Dn + d) * S;
 #pragma unroll
-    for (int s = 0; s < SP; ++s)
-      if (s < S) hp[s] = h[s];
+    for (int i = 0; i < SPL; ++i)
+      if (sbase + i < S) hp[sbase + i] = h[i];
   }
 }
 
@@ -640,8 +642,9 @@ static int launch_scan(const void* x, const void* dt, const float* A_log, const 
                        const void* C, const float* Dskip, void* y, float* h_final,
                        int64_t batch, int64_t T, int64_t Dn, int64_t S, hipStream_t st, ScanEpi epi) {
   using TT = typename Elem<DT>::T;
-  const int block = (Dn % 256 == 0) ? 256 : (Dn % 128 == 0 ? 128 : 64);
-  dim3 grid((unsigned)batch, (unsigned)((Dn + block - 1) / block));
+  const int64_t lanes = Dn * scan_lanes_per_channel(SP);
+  const int block = (lanes % 256 == 0) ? 256 : (lanes % 128 == 0 ? 128 : 64);
+  dim3 grid((unsigned)batch, (unsigned)((lanes + block - 1) / block));
   hipLaunchKernelGGL((ssm_scan_fwd_kernel<DT, SP, MODE>), grid, dim3(block), 0, st,
                      (const TT*)x, (const TT*)dt, A_log, (const TT*)B, (const TT*)C, Dskip,
                      (TT*)y, h_final, (int)T, (int)Dn, (int)S, epi);
@@ -681,7 +684,8 @@ static int dispatch_sp(int mode, const void* x, const void* dt, const float* A_l
   if (S <= 8) return dispatch_mode<DT, 8>(mode, x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, S, st, epi);
   if (S <= 16) return dispatch_mode<DT, 16>(mode, x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, S, st, epi);
   if (S <= 32) return dispatch_mode<DT, 32>(mode, x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, S, st, epi);
-  return dispatch_mode<DT, 64>(mode, x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, S, st, epi);
+  if (S <= 64) return dispatch_mode<DT, 64>(mode, x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, S, st, epi);
+  return dispatch_mode<DT, 128>(mode, x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, S, st, epi);
 }
 
 static int scan_entry(int mode, const void* x, const void* dt, const float* A_log, const void* B, const void* C,
@@ -689,8 +693,8 @@ static int scan_entry(int mode, const void* x, const void* dt, const float* A_lo
                       int64_t d_state, int dtype, hipStream_t st, ScanEpi epi) {
   if (batch < 0 || T < 0 || d_inner < 0 || d_state < 1) return HCLSM_ERR_SHAPE;
   if (batch > 0x7fffffffLL || T > 0x7fffffffLL || d_inner > 0x7fffffffLL) return HCLSM_ERR_SHAPE;
-  if ((d_inner + 63) / 64 > 65535) return HCLSM_ERR_SHAPE;
-  if (d_state > 64) return HCLSM_ERR_UNSUPPORTED;
+  if ((d_inner * 4 + 63) / 64 > 65535) return HCLSM_ERR_SHAPE;
+  if (d_state > 128) return HCLSM_ERR_UNSUPPORTED;
   if (dtype != HCLSM_F32 && dtype != HCLSM_BF16 && dtype != HCLSM_F16) return HCLSM_ERR_DTYPE;
   if (batch == 0 || T == 0 || d_inner == 0) {
     // nothing to scan; h_final (if any) is the zero initial state

@@ -8,7 +8,7 @@
 //   gA[d,s] = sum_{n,t} g_arg dt   with g_arg = gh_t h_{t-1} exp(dt A)
 // (model mode: each clamp passes gradient only inside its closed interval).
 //
-// Mapping: one lane owns channel d of sequence n and SG <= 8 of its states (G = d_state/SG lanes
+// Mapping: one lane owns channel d of sequence n and SG <= 16 of its states (G = d_state/SG lanes
 // per channel, adjacent); a workgroup holds up to 384 lanes of one sequence's channels.  Pass 1
 // recomputes h forward and writes the state at every chunk start (chunks of K = 32/SG steps) to a
 // checkpoint buffer.  Pass 2 walks the chunks backwards: it recomputes the chunk's states into
@@ -22,7 +22,7 @@
 namespace hclsm {
 
 // States per lane: all of a channel's states up to 16 (G = SP / SG adjacent lanes per channel for
-// d_state 32 / 64).  Chunks of K = 64 / SG steps: the chunk's recomputed states (64 floats) stay in
+// d_state 32 / 64 / 128).  Chunks of K = 64 / SG steps: the chunk's recomputed states (64 floats) stay in
 // registers.
 constexpr int bwd_sg(int SP) { return SP < 16 ? SP : 16; }
 constexpr int bwd_k(int SP) { return 64 / bwd_sg(SP); }
@@ -164,7 +164,7 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
   for (int j = 0; j < SG; ++j) {
     const int s = s0 + j;
     const float e = expf(A_log[(size_t)dd * S + (s < S ? s : S - 1)]);
-    const float ec = (MODE == HCLSM_SCAN_MODEL) ? fminf(fmaxf(e, 1e-6f), 1.0f) : e;
+    const float ec = (MODE != HCLSM_SCAN_RAW) ? fminf(fmaxf(e, 1e-6f), 1.0f) : e;
     a2[j] = (s < S) ? -ec * HCLSM_LOG2E : 0.f;
   }
   const float dsk = Dskip ? Dskip[dd] : 0.f;
@@ -202,9 +202,10 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
     for (int j = 0; j < SG; ++j) o[j] = src[r][s0 + j];
   };
   // dt as the recurrence uses it; 0 for a missing step (its raw dt reads 0, which the model clamp
-  // would lift to 1e-3)
+  // would lift to 1e-3).  BLOCK mode: dt = clamp(softplus(input)) in fp32, as the block forward.
   auto dt_of = [&](float v, bool live) {
     if constexpr (MODE == HCLSM_SCAN_MODEL) return live ? fminf(fmaxf(v, 1e-3f), 1.0f) : 0.f;
+    else if constexpr (MODE == HCLSM_SCAN_BLOCK) return live ? fminf(fmaxf(softplus_f(v), 1e-3f), 1.0f) : 0.f;
     else return v;
   };
   auto ld_chunk = [&](int c, float* xo, float* dto) {
@@ -333,6 +334,10 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
       gda2 = group_sum<G>(gda2);
       float gdv = fmaf(gda2, HCLSM_LN2, q * xv);
       if (MODE == HCLSM_SCAN_MODEL && !(draw >= 1e-3f && draw <= 1.0f)) gdv = 0.f;
+      if constexpr (MODE == HCLSM_SCAN_BLOCK) {   // through the clamp (closed interval) and softplus
+        const float sp = softplus_f(draw);
+        gdv = (sp >= 1e-3f && sp <= 1.0f) ? gdv * __builtin_amdgcn_rcpf(1.f + __expf(-draw)) : 0.f;
+      }
       const int so = (i < len) ? (int)((unsigned)t * pitch) : slab;   // a missing step stores nothing
       buf_st<DT>(fmaf(q, dtv, dsk * gyv), rgx, vo_st, so);
       buf_st<DT>(gdv, rgdt, vo_st, so);
@@ -410,14 +415,16 @@ ssm_scan_bwd_finalize(const float* __restrict__ gbc, const float* __restrict__ g
     const int64_t dd = i / S, s = i - dd * S;
     const float e = expf(A_log[i]);
     float dadl = -e;                          // d(-exp(A_log))/dA_log
-    if (MODE == HCLSM_SCAN_MODEL && !(e >= 1e-6f && e <= 1.0f)) dadl = 0.f;
+    if (MODE != HCLSM_SCAN_RAW && !(e >= 1e-6f && e <= 1.0f)) dadl = 0.f;
     gA_log[i] = ga_sum[dd * SP + s] * dadl;
   }
   if (gD)
     for (int64_t dd = tid0; dd < Dn; dd += stride) gD[dd] = gd_sum[dd];
 }
 
-static int64_t sp_of(int64_t S) { return S <= 4 ? 4 : S <= 8 ? 8 : S <= 16 ? 16 : S <= 32 ? 32 : 64; }
+static int64_t sp_of(int64_t S) {
+  return S <= 4 ? 4 : S <= 8 ? 8 : S <= 16 ? 16 : S <= 32 ? 32 : S <= 64 ? 64 : 128;
+}
 
 struct BwdWs {
   size_t ck, gbc, ga, gd, ga_sum, gd_sum, total;
@@ -488,7 +495,7 @@ static int launch_bwd(const void* x, const void* dt, const float* A_log, const v
 using namespace hclsm;
 
 extern "C" int64_t hclsm_ssm_scan_bwd_workspace(int64_t batch, int64_t T, int64_t d_inner, int64_t d_state) {
-  if (batch < 0 || T < 0 || d_inner < 0 || d_state < 1 || d_state > 64) return HCLSM_ERR_SHAPE;
+  if (batch < 0 || T < 0 || d_inner < 0 || d_state < 1 || d_state > 128) return HCLSM_ERR_SHAPE;
   return (int64_t)bwd_ws(batch, T, d_inner, d_state).total;
 }
 
@@ -498,10 +505,10 @@ extern "C" int hclsm_ssm_scan_bwd(const void* x, const void* dt, const float* A_
                                   int dtype, int mode, void* workspace, int64_t workspace_bytes, void* stream) {
   if (batch < 0 || T < 0 || d_inner < 0 || d_state < 1) return HCLSM_ERR_SHAPE;
   if (batch > 0x7fffffffLL || T > 0x7fffffffLL || d_inner > 0x7fffffffLL) return HCLSM_ERR_SHAPE;
-  if (d_state > 64) return HCLSM_ERR_UNSUPPORTED;
+  if (d_state > 128) return HCLSM_ERR_UNSUPPORTED;
   // per-sequence slabs are addressed through 32-bit buffer offsets
   if (T * d_inner * (dtype == HCLSM_F32 ? 4 : 2) >= (1LL << 31)) return HCLSM_ERR_UNSUPPORTED;
-  if (mode != HCLSM_SCAN_RAW && mode != HCLSM_SCAN_MODEL) return HCLSM_ERR_MODE;
+  if (mode != HCLSM_SCAN_RAW && mode != HCLSM_SCAN_MODEL && mode != HCLSM_SCAN_BLOCK) return HCLSM_ERR_MODE;
   if (dtype != HCLSM_F32 && dtype != HCLSM_BF16 && dtype != HCLSM_F16) return HCLSM_ERR_DTYPE;
   hipStream_t st = (hipStream_t)stream;
   if (batch == 0 || T == 0 || d_inner == 0) {
@@ -523,11 +530,14 @@ extern "C" int hclsm_ssm_scan_bwd(const void* x, const void* dt, const float* A_
     if (mode == HCLSM_SCAN_RAW)                                                                              \
       return launch_bwd<DT_, SP_, HCLSM_SCAN_RAW>(x, dt, A_log, B, C, Dskip, gy, gx, gdt, gA_log, gB, gC, gD, ws, L, \
                                                   batch, T, d_inner, d_state, st);                           \
+    if (mode == HCLSM_SCAN_BLOCK)                                                                            \
+      return launch_bwd<DT_, SP_, HCLSM_SCAN_BLOCK>(x, dt, A_log, B, C, Dskip, gy, gx, gdt, gA_log, gB, gC, gD, ws, \
+                                                    L, batch, T, d_inner, d_state, st);                      \
     return launch_bwd<DT_, SP_, HCLSM_SCAN_MODEL>(x, dt, A_log, B, C, Dskip, gy, gx, gdt, gA_log, gB, gC, gD, ws, L, \
                                                   batch, T, d_inner, d_state, st);                           \
   }
 #define HCLSM_BWD_DT(DT_) \
-  HCLSM_BWD(DT_, 4) HCLSM_BWD(DT_, 8) HCLSM_BWD(DT_, 16) HCLSM_BWD(DT_, 32) HCLSM_BWD(DT_, 64)
+  HCLSM_BWD(DT_, 4) HCLSM_BWD(DT_, 8) HCLSM_BWD(DT_, 16) HCLSM_BWD(DT_, 32) HCLSM_BWD(DT_, 64) HCLSM_BWD(DT_, 128)
   if (dtype == HCLSM_F32) { HCLSM_BWD_DT(HCLSM_F32) }
   if (dtype == HCLSM_BF16) { HCLSM_BWD_DT(HCLSM_BF16) }
   if (dtype == HCLSM_F16) { HCLSM_BWD_DT(HCLSM_F16) }

@@ -166,8 +166,9 @@ def _block_forward(z, dt_in, A_log, B, C, gate, want_pre: bool):
 
 
 class _HipSSMBlockScan(torch.autograd.Function):
-    """Fused block scan forward on HIP; backward = HIP reverse scan (model mode) plus the chain rule
-    through softplus / clamp (torch's clamp passes gradient inside the closed interval) and silu."""
+    """Fused block scan forward on HIP; backward = HIP reverse scan in block mode (dt recomputed as
+    clamp(softplus(dt_in)) in fp32 exactly as the forward kernel does, gradient returned with respect to
+    dt_in through the clamp -- closed interval, as torch's clamp -- and softplus) plus the silu chain rule."""
 
     @staticmethod
     def forward(ctx, z, dt_in, A_log, B, C, gate):
@@ -180,18 +181,13 @@ class _HipSSMBlockScan(torch.autograd.Function):
     @staticmethod
     def backward(ctx, g):
         from hclsm_amd.kernels.ssm_scan_bwd import scan_backward
-        import torch.nn.functional as F
         z, dt_in, A_log, B, C, gate, y_pre = ctx.saved_tensors
         gf, gatef = g.float(), gate.float()
         sg = torch.sigmoid(gatef)
         g_y = gf * gatef * sg
         g_gate = gf * y_pre.float() * sg * (1.0 + gatef * (1.0 - sg))
-        dtf = dt_in.float()
-        sp = F.softplus(dtf)
-        dt = sp.clamp(1e-3, 1.0)
-        grads = scan_backward(z, dt.to(y_pre.dtype), A_log, B, C, None, g_y.to(y_pre.dtype), _lib.SCAN_MODEL)
-        g_dt_in = grads["dt"].float() * torch.sigmoid(dtf) * ((sp >= 1e-3) & (sp <= 1.0)).to(torch.float32)
-        return (grads["x"].to(z.dtype), g_dt_in.to(dt_in.dtype), grads["A_log"], grads["B"].to(B.dtype),
+        grads = scan_backward(z, dt_in.to(y_pre.dtype), A_log, B, C, None, g_y.to(y_pre.dtype), _lib.SCAN_BLOCK)
+        return (grads["x"].to(z.dtype), grads["dt"].to(dt_in.dtype), grads["A_log"], grads["B"].to(B.dtype),
                 grads["C"].to(C.dtype), g_gate.to(gate.dtype))
 
 

@@ -44,12 +44,14 @@ extern "C" {
 /* SSM scan clamp modes */
 #define HCLSM_SCAN_RAW   0  /* A=-exp(A_log), no clamps: ssm_scan_kernel.py:191, :255 */
 #define HCLSM_SCAN_MODEL 1  /* clamps of ssm_scan_kernel.py:63,68,77 and level0_ssm.py:76,82,96 */
+#define HCLSM_SCAN_BLOCK 2  /* hclsm_ssm_scan_bwd only: MODEL with dt = clamp(softplus(dt input), 1e-3, 1) inside
+                               the kernel, as hclsm_ssm_block_scan_fwd computes it (level0_ssm.py:76) */
 
 /* argument errors (negative) */
 #define HCLSM_ERR_NULL        (-1) /* a required pointer is NULL */
 #define HCLSM_ERR_SHAPE       (-2) /* a size is negative, zero where not allowed, or too large */
 #define HCLSM_ERR_DTYPE       (-3) /* unknown element-type code */
-#define HCLSM_ERR_UNSUPPORTED (-4) /* valid but not implemented (e.g. d_state > 64) */
+#define HCLSM_ERR_UNSUPPORTED (-4) /* valid but not implemented (e.g. d_state > 128) */
 #define HCLSM_ERR_MODE        (-5) /* unknown mode code */
 
 /* Version of this ABI (HCLSM_ABI_VERSION of the built library). */
@@ -68,7 +70,7 @@ const char* hclsm_strerror(int code);
  *   A_log    : [d_inner, d_state]    float32
  *   Dskip    : [d_inner]             float32, nullable
  *   h_final  : [batch, d_inner, d_state] float32, nullable (state after the last step)
- * State and arithmetic are float32; 1 <= d_state <= 64.
+ * State and arithmetic are float32; 1 <= d_state <= 128.
  * Replaces: ssm_scan_fn / fused_ssm_scan_triton / _TritonSSMScan.forward
  *   (hclsm/kernels/ssm_scan_kernel.py:394-421, :379-387, :294-319) in RAW mode and
  *   sequential_ssm_scan (ssm_scan_kernel.py:42-86) in MODEL mode.
@@ -102,7 +104,10 @@ int64_t hclsm_ssm_scan_bwd_workspace(int64_t batch, int64_t T, int64_t d_inner, 
  * Selective SSM scan, backward: gradients of sum(gy * y) for the forward of hclsm_ssm_scan_fwd with the
  * same arguments and mode.  gy, gx, gdt [batch, T, d_inner] and gB, gC [batch, T, d_state] in `dtype`;
  * gA_log [d_inner, d_state] float32; gD [d_inner] float32 (nullable; Dskip nullable as in the forward).
- * MODEL mode passes gradient through each clamp only inside its closed interval.  Chunk checkpoints and
+ * MODEL mode passes gradient through each clamp only inside its closed interval.  BLOCK mode takes the
+ * block's dt input (before softplus) as `dt`, recomputes dt = clamp(softplus(dt), 1e-3, 1) in fp32 exactly as
+ * the fused block forward does, and returns in gdt the gradient with respect to that input (through the clamp,
+ * closed interval, and softplus).  Chunk checkpoints and
  * partial sums live in `workspace` (>= hclsm_ssm_scan_bwd_workspace bytes).  Four launches at most.
  * Deterministic (no float atomics).  One sequence's [T, d_inner] slab must be < 2^31 bytes
  * (HCLSM_ERR_UNSUPPORTED otherwise).

@@ -62,7 +62,7 @@ def test_argument_errors_before_launch(lib):
     assert f(None, None, None, None, None, None, None, None, -1, 4, 4, 4, 0, 0, None) == -2
     assert f(None, None, None, None, None, None, None, None, 1, 4, 4, 4, 7, 0, None) == -3
     assert f(None, None, None, None, None, None, None, None, 1, 4, 4, 4, 0, 9, None) == -5
-    assert f(None, None, None, None, None, None, None, None, 1, 4, 4, 65, 0, 0, None) == -4
+    assert f(None, None, None, None, None, None, None, None, 1, 4, 4, 129, 0, 0, None) == -4
     assert f(None, None, None, None, None, None, None, None, 1, 4, 4, 4, 0, 0, None) == -1
     # empty problem: nothing to launch, success
     assert f(None, None, None, None, None, None, None, None, 0, 4, 4, 4, 0, 0, None) == 0
@@ -73,7 +73,8 @@ def test_scan_backward_argument_errors_before_launch(lib):
     null13 = [None] * 13
     # bad mode, oversized d_state, a per-sequence slab past 32-bit buffer offsets, NULL pointers
     assert f(*null13, 1, 4, 4, 4, 1, 7, None, 0, None) == -5
-    assert f(*null13, 1, 4, 4, 65, 1, 0, None, 0, None) == -4
+    assert f(*null13, 1, 4, 4, 4, 1, 2, None, 0, None) == -1   # block mode is accepted
+    assert f(*null13, 1, 4, 4, 129, 1, 0, None, 0, None) == -4
     assert f(*null13, 1, 1 << 20, 1 << 10, 16, 1, 0, None, 0, None) == -4   # 2^30 bf16 elements = 2 GiB
     assert f(*null13, 1, 4, 4, 4, 1, 0, None, 0, None) == -1
 
@@ -151,3 +152,4 @@ def test_top_down_argument_errors_before_launch(lib):
     assert call(ctx=P, ldw=100) == -2
     assert call(ctx=P, ws_bytes=16) == -2
     assert call(ctx=P, wx=P + 2) == -4                    # operand rows must be 16-byte aligned
+

@@ -36,7 +36,8 @@ def _np(t):
 
 
 @pytest.mark.parametrize("N,T,Dn,S", [(2, 16, 32, 8), (1, 8, 64, 16), (4, 32, 16, 4), (3, 37, 384, 16),
-                                      (2, 19, 70, 5), (1, 12, 40, 32), (1, 9, 24, 64), (2, 70, 300, 16)])
+                                      (2, 19, 70, 5), (1, 12, 40, 32), (1, 9, 24, 64), (2, 70, 300, 16),
+                                      (2, 11, 40, 96), (1, 70, 24, 128)])   # up to the large preset's d_state
 @pytest.mark.parametrize("mode", ["raw", "model"])
 def test_backward_fp32(N, T, Dn, S, mode):
     from hclsm_amd.kernels.ssm_scan_kernel import fused_ssm_scan_hip

@@ -151,8 +151,8 @@ def test_empty_and_errors():
     from hclsm_amd._lib import HipKernelError
     xg = torch.zeros(1, 2, 8, device="cuda")
     with pytest.raises(HipKernelError, match="not supported"):
-        ssm_scan_fn(xg, xg, torch.zeros(8, 65, device="cuda"), torch.zeros(1, 2, 65, device="cuda"),
-                    torch.zeros(1, 2, 65, device="cuda"))
+        ssm_scan_fn(xg, xg, torch.zeros(8, 129, device="cuda"), torch.zeros(1, 2, 129, device="cuda"),
+                    torch.zeros(1, 2, 129, device="cuda"))
 
 
 def test_backend_semantics():
@@ -283,3 +283,71 @@ def test_block_scan_gradients_match_float64_autograd():
     ((torch.stack(ys, 1) * F.silu(r[5])) * w).sum().backward()
     for got, ref, name in zip(ins, r, ("z", "dt_in", "A_log", "B", "C", "gate")):
         assert normwise_rel_err(_np(got.grad), _np(ref.grad)) <= 1e-5, name
+
+
+def test_block_scan_bf16_gradient_at_the_lower_dt_clamp():
+    """bf16 dt_in = -6.90625 gives softplus = 1.0006e-3 in fp32: inside the clamp's closed interval
+    [1e-3, 1], so dt_in receives gradient (dt = softplus), although the value rounded to bf16
+    (0.000999451) would sit below it.  The backward recomputes clamp(softplus(dt_in)) in fp32 as the
+    forward does; the float64 reference of the same math on the bf16 inputs must agree."""
+    import torch.nn.functional as F
+    from hclsm_amd.kernels import ssm_block_scan
+    g = torch.Generator().manual_seed(78)
+    N, T, Dn, S = 2, 16, 64, 16
+    bf = torch.bfloat16
+    z, gate = (torch.randn(N, T, Dn, generator=g).to(bf) for _ in range(2))
+    dt_in = torch.full((N, T, Dn), -6.90625).to(bf)
+    dt_in[:, :, ::2] = torch.tensor(-7.5).to(bf)          # below the clamp: no gradient there
+    A_log = -torch.rand(Dn, S, generator=g) * 0.5
+    Bm, Cm = ((torch.randn(N, T, S, generator=g) / 4).to(bf) for _ in range(2))
+    w = torch.randn(N, T, Dn, generator=g)
+    ins = [t.cuda().requires_grad_() for t in (z, dt_in, A_log, Bm, Cm, gate)]
+    (ssm_block_scan(*ins).float() * w.cuda()).sum().backward()
+    r = [t.double().clone().requires_grad_() for t in (z, dt_in, A_log, Bm, Cm, gate)]
+    sp = F.softplus(r[1])
+    assert bool(((sp[:, :, 1::2] >= 1e-3) & (sp[:, :, 1::2] < 1.0034e-3)).all())
+    dt = sp.clamp(1e-3, 1.0)
+    A = -torch.exp(r[2]).clamp(1e-6, 1.0)
+    h = torch.zeros(N, Dn, S, dtype=torch.float64)
+    ys = []
+    for t in range(T):
+        h = torch.exp(dt[:, t, :, None] * A) * h + (dt[:, t] * r[0][:, t])[:, :, None] * r[3][:, t, None, :]
+        ys.append((h * r[4][:, t, None, :]).sum(-1))
+    ((torch.stack(ys, 1) * F.silu(r[5])) * w.double()).sum().backward()
+    gd = ins[1].grad.float().cpu()
+    assert bool((gd[:, :, 1::2] != 0).all()) and bool((gd[:, :, ::2] == 0).all())
+    for got, ref, name in zip(ins, r, ("z", "dt_in", "A_log", "B", "C", "gate")):
+        assert normwise_rel_err(_np(got.grad), _np(ref.grad)) <= LOWP_TOL, name
+
+
+@pytest.mark.parametrize("S", [96, 128])
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, FP32_TOL), (torch.bfloat16, LOWP_TOL)])
+def test_large_d_state_forward(S, dtype, tol):
+    """d_state up to 128 (the large preset uses 96): the generic kernel splits a channel's states over
+    adjacent lanes."""
+    for mode in ("raw", "model"):
+        d = _inputs(3, 21, 70, S, dtype=dtype, seed=S + 1, dt_kind="ref_test" if mode == "model" else "softplus")
+        y, h = _run(d, mode, True, want_h=True)
+        ref, href = ssm_scan_ref(_np(d["x"]), _np(d["dt"]), _np(d["A_log"]), _np(d["B"]), _np(d["C"]),
+                                 D=_np(d["D"]), clamp_mode=mode, return_h_final=True)
+        assert normwise_rel_err(_np(y), ref) <= tol, mode
+        assert normwise_rel_err(_np(h), href) <= max(tol, 1e-5), mode
+
+
+def test_large_preset_level0_block_runs():
+    """The large preset's SimplifiedSSMBlock shape (d_state 96): forward and backward run on the HIP
+    kernels and the block output matches the oracle."""
+    from oracle.modules import block_scan_ref
+    from hclsm_amd.kernels import ssm_block_scan
+    g = torch.Generator().manual_seed(96)
+    N, T, Dn, S = 2, 12, 96, 96
+    z, gate = (torch.randn(N, T, Dn, generator=g) for _ in range(2))
+    dt_in = torch.randn(N, T, Dn, generator=g) * 2 - 1
+    A_log = -torch.rand(Dn, S, generator=g) * 0.5
+    Bm, Cm = (torch.randn(N, T, S, generator=g) / 4 for _ in range(2))
+    ins = [t.cuda().requires_grad_() for t in (z, dt_in, A_log, Bm, Cm, gate)]
+    y = ssm_block_scan(*ins)
+    ref = block_scan_ref(*(_np(t) for t in (z, dt_in, A_log, Bm, Cm, gate)))
+    assert normwise_rel_err(_np(y), ref) <= FP32_TOL
+    y.sum().backward()
+    assert all(bool(torch.isfinite(t.grad).all()) for t in ins)
