@@ -59,6 +59,8 @@ _SIGNATURES: dict[str, list] = {
                                        _i64, _c_void_p],
     "hclsm_slot_attention_forward": [_c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64,
                                      _i64, _i64, _f32, _f32, _f32, _f32, _int, _c_void_p, _i64, _c_void_p],
+    "hclsm_slot_attention_forward_noalloc": [_c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i64, _i64,
+                                             _i64, _i64, _i64, _f32, _f32, _f32, _f32, _int, _c_void_p],
     "hclsm_level1_forward_workspace": [_i64, _i64, _i64, _i64, _int],
     "hclsm_relation_graph_workspace": [_i64, _i64, _i64, _i64, _int],
     "hclsm_relation_graph_forward": [_c_void_p] * 4 + [_i64] * 5 + [_int, _c_void_p, _f32, _int, _c_void_p, _i64,

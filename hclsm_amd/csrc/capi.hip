@@ -50,6 +50,8 @@ extern "C" const char* hclsm_strerror(int code) {
     case HCLSM_ERR_DTYPE: return "hclsm: unknown element-type code";
     case HCLSM_ERR_UNSUPPORTED: return "hclsm: argument combination not supported by this build";
     case HCLSM_ERR_MODE: return "hclsm: unknown mode code";
+    case HCLSM_ERR_SCRATCH:
+      return "hclsm: the call needs more workspace than the allocation-free entry point's static scratch array";
     default: break;
   }
   if (code > 0) return hipGetErrorString((hipError_t)code);

@@ -17,6 +17,8 @@
 // core_update     grid (frame, 64-column block of D): attn (A operand, row-major in HBM) times
 //                 v staged transposed through LDS in 32-token chunks; optional
 //                 renormalisation (attn + eps) / sum_m (attn + eps) folded into the epilogue.
+#include <mutex>
+
 #include "mfma.h"
 #include "internal.h"
 
@@ -1801,11 +1803,10 @@ extern "C" int hclsm_slot_attention_iteration(const HclsmSlotWeights* W, const f
                              B, N, M, d, hidden, scale, logit_clamp, renorm_eps, slot_clamp, dtype, ws, L, st);
 }
 
-extern "C" int hclsm_slot_attention_forward(const HclsmSlotWeights* W, const float* inputs, int64_t d_in,
-                                            const float* slots0, float* slots_out, int64_t B, int64_t N, int64_t M,
-                                            int64_t d, int64_t hidden, int64_t n_iter, float scale, float logit_clamp,
-                                            float renorm_eps, float slot_clamp, int dtype, void* workspace,
-                                            int64_t workspace_bytes, void* stream) {
+static int slot_forward_impl(const HclsmSlotWeights* W, const float* inputs, int64_t d_in, const float* slots0,
+                             float* slots_out, int64_t B, int64_t N, int64_t M, int64_t d, int64_t hidden,
+                             int64_t n_iter, float scale, float logit_clamp, float renorm_eps, float slot_clamp,
+                             int dtype, void* workspace, int64_t workspace_bytes, void* stream) {
   SlotWs L;
   int rc = check_slot_args(W, B, N, M, d, hidden, dtype, workspace, workspace_bytes, true, &L, d_in);
   if (rc) return rc;
@@ -1847,4 +1848,60 @@ extern "C" int hclsm_slot_attention_forward(const HclsmSlotWeights* W, const flo
     if (rc) return rc;
   }
   return 0;
+}
+
+extern "C" int hclsm_slot_attention_forward(const HclsmSlotWeights* W, const float* inputs, int64_t d_in,
+                                            const float* slots0, float* slots_out, int64_t B, int64_t N, int64_t M,
+                                            int64_t d, int64_t hidden, int64_t n_iter, float scale, float logit_clamp,
+                                            float renorm_eps, float slot_clamp, int dtype, void* workspace,
+                                            int64_t workspace_bytes, void* stream) {
+  return slot_forward_impl(W, inputs, d_in, slots0, slots_out, B, N, M, d, hidden, n_iter, scale, logit_clamp,
+                           renorm_eps, slot_clamp, dtype, workspace, workspace_bytes, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free forward: the same launches, with the workspace in a static device array.
+//
+// `scratch` is a file-scope device array: every GPU the library runs on holds its own copy, at its
+// own address, from the code object's load until the process ends.  Its host-side name is not a device
+// address, so host code only ever passes scratch_ptr[dev], the address hipGetSymbolAddress returns with
+// that device current.  The forward needs no zeroed memory (every workspace region is written before it
+// is read), so nothing is cleared between calls.  Calls that overlap on one GPU share the array and race.
+
+static __device__ __align__(256) unsigned char scratch[HCLSM_SLOT_NOALLOC_SCRATCH_BYTES];
+
+static std::mutex scratch_mu;
+static void* scratch_ptr[HCLSM_MAX_DEVICES];
+
+// Device address of the current device's scratch array, looked up once per device.
+static int current_scratch(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= HCLSM_MAX_DEVICES) return HCLSM_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (p == nullptr) return HCLSM_ERR_NULL;
+    scratch_ptr[dev] = p;
+  }
+  *out = scratch_ptr[dev];
+  return 0;
+}
+
+extern "C" int hclsm_slot_attention_forward_noalloc(const HclsmSlotWeights* W, const float* inputs, int64_t d_in,
+                                                    const float* slots0, float* slots_out, int64_t B, int64_t N,
+                                                    int64_t M, int64_t d, int64_t hidden, int64_t n_iter, float scale,
+                                                    float logit_clamp, float renorm_eps, float slot_clamp, int dtype,
+                                                    void* stream) {
+  if (B < 0 || N < 0 || M < 0 || d_in < 0 || d < 0 || hidden < 0) return HCLSM_ERR_SHAPE;
+  const int64_t need = (int64_t)slot_ws_layout(B, N, M, d, hidden, dtype == HCLSM_F32 ? 4 : 2, true, d_in).total;
+  if (need > HCLSM_SLOT_NOALLOC_SCRATCH_BYTES) return HCLSM_ERR_SCRATCH;
+  void* ws = nullptr;
+  const int rc = current_scratch(&ws);
+  if (rc) return rc;
+  return slot_forward_impl(W, inputs, d_in, slots0, slots_out, B, N, M, d, hidden, n_iter, scale, logit_clamp,
+                           renorm_eps, slot_clamp, dtype, ws, HCLSM_SLOT_NOALLOC_SCRATCH_BYTES, stream);
 }

@@ -53,6 +53,7 @@ extern "C" {
 #define HCLSM_ERR_DTYPE       (-3) /* unknown element-type code */
 #define HCLSM_ERR_UNSUPPORTED (-4) /* valid but not implemented (e.g. d_state > 128) */
 #define HCLSM_ERR_MODE        (-5) /* unknown mode code */
+#define HCLSM_ERR_SCRATCH     (-6) /* the call needs more than an allocation-free entry point's static scratch */
 
 /* Version of this ABI (HCLSM_ABI_VERSION of the built library). */
 int hclsm_abi_version(void);
@@ -329,6 +330,22 @@ int hclsm_slot_attention_forward(const HclsmSlotWeights* W, const float* inputs,
                                  int64_t d, int64_t hidden, int64_t n_iter, float scale, float logit_clamp,
                                  float renorm_eps, float slot_clamp, int dtype, void* workspace,
                                  int64_t workspace_bytes, void* stream);
+
+/*
+ * Allocation-free variant of hclsm_slot_attention_forward: the same arguments and launches, with the workspace
+ * taken from a static device array of HCLSM_SLOT_NOALLOC_SCRATCH_BYTES in the library (one copy per GPU, held
+ * until the process ends) instead of a caller buffer.  No allocation, free or synchronisation, so the call may
+ * run under HIP graph capture.  A shape whose hclsm_slot_attention_workspace exceeds the array returns
+ * HCLSM_ERR_SCRATCH before any launch (config 2, B=32 M=196 d=384 bf16, needs about 22 MB).  Calls that overlap
+ * on one GPU (two streams, two threads) share the array and race; serialise them.
+ * No counterpart in the reference: it is for callers that cannot allocate device memory (graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).
+ */
+#define HCLSM_SLOT_NOALLOC_SCRATCH_BYTES (64LL << 20)
+int hclsm_slot_attention_forward_noalloc(const HclsmSlotWeights* W, const float* inputs, int64_t d_in,
+                                         const float* slots0, float* slots_out, int64_t B, int64_t N, int64_t M,
+                                         int64_t d, int64_t hidden, int64_t n_iter, float scale, float logit_clamp,
+                                         float renorm_eps, float slot_clamp, int dtype, void* stream);
 
 /* Workspace bytes for hclsm_level1_forward. */
 int64_t hclsm_level1_forward_workspace(int64_t capacity, int64_t N, int64_t d_model, int64_t hidden, int dtype);

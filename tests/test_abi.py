@@ -51,7 +51,7 @@ def test_every_declared_symbol_is_exported(lib):
 def test_version_and_strerror(lib):
     from hclsm_amd import _lib
     assert lib.hclsm_abi_version() == 1
-    for code in (0, -1, -2, -3, -4, -5):
+    for code in (0, -1, -2, -3, -4, -5, -6):
         assert _lib.strerror(code)
     assert "unknown" in _lib.strerror(-999)
 
@@ -153,3 +153,12 @@ def test_top_down_argument_errors_before_launch(lib):
     assert call(ctx=P, ws_bytes=16) == -2
     assert call(ctx=P, wx=P + 2) == -4                    # operand rows must be 16-byte aligned
 
+
+def test_noalloc_forward_rejects_oversized_shapes_before_launch(lib):
+    """hclsm_slot_attention_forward_noalloc: a shape whose workspace exceeds the static scratch array
+    (64 MiB) returns HCLSM_ERR_SCRATCH (-6) on the host; negative sizes return HCLSM_ERR_SHAPE."""
+    f = lib.hclsm_slot_attention_forward_noalloc
+    need = lib.hclsm_slot_attention_workspace(512, 32, 196, 384, 384, 768, 1)
+    assert need > (64 << 20)
+    assert f(None, None, 384, None, None, 512, 32, 196, 384, 768, 3, 0.05, 0.0, 1e-8, 0.0, 1, None) == -6
+    assert f(None, None, 384, None, None, -1, 32, 196, 384, 768, 3, 0.05, 0.0, 1e-8, 0.0, 1, None) == -2
