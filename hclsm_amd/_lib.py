@@ -67,6 +67,8 @@ _SIGNATURES: dict[str, list] = {
                                                                     _c_void_p],
     "hclsm_level1_forward": [_c_void_p, _int, _c_void_p, _int, _c_void_p, _i64, _i64, _c_void_p, _c_void_p,
                              _i64, _i64, _i64, _i64, _i64, _c_void_p, _f32, _int, _c_void_p, _i64, _c_void_p],
+    "hclsm_gnn_message_pass_workspace": [_i64, _i64, _i64, _i64, _int],
+    "hclsm_gnn_message_pass": [_c_void_p] * 4 + [_i64] * 7 + [_c_void_p, _int, _c_void_p, _i64, _c_void_p],
     "hclsm_slot_track_cost_workspace": [_i64, _i64, _i64, _int],
     "hclsm_slot_track_cost": [_c_void_p] * 5 + [_i64] * 3 + [_c_void_p, _int, _c_void_p, _i64, _c_void_p],
     "hclsm_slot_track_match": [_c_void_p] * 6 + [_i64] * 3 + [_f32, _c_void_p],
@@ -81,7 +83,7 @@ _RESTYPES = {"hclsm_strerror": ctypes.c_char_p, "hclsm_slot_attn_core_workspace"
              "hclsm_relation_graph_workspace": ctypes.c_int64, "hclsm_slot_track_cost_workspace": ctypes.c_int64,
              "hclsm_slot_track_reorder_update_workspace": ctypes.c_int64,
              "hclsm_slot_track_sequence_workspace": ctypes.c_int64,
-             "hclsm_event_top_down_workspace": ctypes.c_int64}
+             "hclsm_event_top_down_workspace": ctypes.c_int64, "hclsm_gnn_message_pass_workspace": ctypes.c_int64}
 
 
 class HclsmSlotWeights(ctypes.Structure):

@@ -51,7 +51,10 @@ struct GnnArgs {
   float* agg;          // messages summed over j, row stride ldagg (null: not wanted)
   int64_t ldagg;
   float* causal;       // [F, N, N] or null
+  float* edges;        // [F, N, enj, E] fp32 edge features of the targets j in [ej0, ej0 + enj), or null
+  int ej0, enj;
   int F, N, NP, D, E;  // NP = N rounded up to 16 (pairs of a padded i-row)
+  int norm;            // 1: pair LayerNorm folded in (RelationGraph); 0: no pair norm (gnn_message_pass)
   float eps;
 };
 
@@ -138,8 +141,8 @@ gnn_edge_kernel(GnnArgs a) {
       const float inv = 1.f / (4.f * (float)D);
       const float mu = (2.f * si + gs) * inv;
       const float m2 = (2.f * qi + 2.f * qj - 2.f * gs + hs) * inv;
-      sst[2 * row] = mu;
-      sst[2 * row + 1] = 1.f / sqrtf(fmaxf(m2 - mu * mu, 0.f) + a.eps);
+      sst[2 * row] = a.norm ? mu : 0.f;
+      sst[2 * row + 1] = a.norm ? 1.f / sqrtf(fmaxf(m2 - mu * mu, 0.f) + a.eps) : 1.f;
     }
     __syncthreads();   // statistics of every row are in LDS
 #pragma unroll
@@ -183,6 +186,14 @@ gnn_edge_kernel(GnnArgs a) {
   __syncthreads();
   const T* sE = sH;
   const T* erow = sE + (size_t)(wid * 16 + li) * LE;
+  if (a.edges) {   // edge features of the output window, as the next layers see them
+    for (int e = tid; e < ROWS * E; e += NTH) {
+      const int row = e / E, o = e - row * E;
+      int i, j;
+      if (row_pair(row, i, j) && j >= a.ej0 && j < a.ej0 + a.enj)
+        a.edges[(((size_t)f * N + i) * a.enj + (j - a.ej0)) * E + o] = A::tof(sE[(size_t)row * LE + o]);
+    }
+  }
   // edge weight per row
   for (int row = tid; row < ROWS; row += NTH) {
     int i, j;
@@ -430,9 +441,9 @@ gnn_edge_res_kernel(GnnArgs a, const float* __restrict__ nstat) {
         hh += __shfl_xor(hh, 32, 64);
         const int64_t rowj = f * N + (jj[pt] < N ? jj[pt] : N - 1);
         const float qj = nstat[2 * rowj + 1];
-        const float mu = (2.f * si + gg) * inv4d;
+        const float mu = a.norm ? (2.f * si + gg) * inv4d : 0.f;
         const float m2 = (2.f * qi + 2.f * qj - 2.f * gg + hh) * inv4d;
-        const float rs = 1.f / sqrtf(fmaxf(m2 - mu * mu, 0.f) + a.eps);
+        const float rs = a.norm ? 1.f / sqrtf(fmaxf(m2 - mu * mu, 0.f) + a.eps) : 1.f;
         const float* Q = a.PQ + rowj * 2 * H1 + H1 + 4 * g;
 #pragma unroll
         for (int t0 = 0; t0 < NT1; t0 += 3) {
@@ -491,6 +502,10 @@ gnn_edge_res_kernel(GnnArgs a, const float* __restrict__ nstat) {
           }
           ebp[pt][t][0] = pack2<T>(ev[0], ev[1]);
           ebp[pt][t][1] = pack2<T>(ev[2], ev[3]);
+          const int je = jj[pt] - a.ej0;
+          if (a.edges && jj[pt] < N && je >= 0 && je < a.enj)
+            *reinterpret_cast<float4*>(a.edges + (rowi * a.enj + je) * E + 16 * t + 4 * g) =
+                make_float4(A::tof(ev[0]), A::tof(ev[1]), A::tof(ev[2]), A::tof(ev[3]));
         }
         s += __shfl_xor(s, 16, 64);
         s += __shfl_xor(s, 32, 64);
@@ -778,9 +793,9 @@ gnn_edge_str_kernel(GnnArgs a, const float* __restrict__ nstat) {
             hs += __shfl_xor(hs, 16, 64);
             hs += __shfl_xor(hs, 32, 64);
             const float qj = nstat[2 * rowj + 1];
-            const float mu = (2.f * si + gs) * inv4d;
+            const float mu = a.norm ? (2.f * si + gs) * inv4d : 0.f;
             const float m2 = (2.f * qi + 2.f * qj - 2.f * gs + hs) * inv4d;
-            const float rs = 1.f / sqrtf(fmaxf(m2 - mu * mu, 0.f) + a.eps);
+            const float rs = a.norm ? 1.f / sqrtf(fmaxf(m2 - mu * mu, 0.f) + a.eps) : 1.f;
             const float* P = a.PQ + rowi * 2 * H1 + 4 * g;
             const float* Q = a.PQ + rowj * 2 * H1 + H1 + 4 * g;
 #pragma unroll
@@ -835,6 +850,10 @@ gnn_edge_str_kernel(GnnArgs a, const float* __restrict__ nstat) {
               }
               ebp[t][0] = pack2<T>(ev[0], ev[1]);
               ebp[t][1] = pack2<T>(ev[2], ev[3]);
+              const int je = j - a.ej0;
+              if (a.edges && live_row && j < N && je >= 0 && je < a.enj)
+                *reinterpret_cast<float4*>(a.edges + (rowi * a.enj + je) * E + 16 * t + 4 * g) =
+                    make_float4(A::tof(ev[0]), A::tof(ev[1]), A::tof(ev[2]), A::tof(ev[3]));
             }
             sw += __shfl_xor(sw, 16, 64);
             sw += __shfl_xor(sw, 32, 64);
@@ -966,14 +985,15 @@ gnn_prep_kernel(const typename MM<DT>::T* __restrict__ W1, const float* __restri
   const typename A::T* w = W1 + (size_t)o * 4 * D;
   float sr = 0.f, sc = 0.f;
   for (int k = threadIdx.x; k < D; k += blockDim.x) {
-    const float w1 = A::tof(w[k]) * gam[k], w2 = A::tof(w[D + k]) * gam[D + k];
-    const float w3 = A::tof(w[2 * D + k]) * gam[2 * D + k], w4 = A::tof(w[3 * D + k]) * gam[3 * D + k];
+    auto gm = [&](int i) { return gam ? gam[i] : 1.f; };   // no pair norm: gamma 1, beta 0
+    const float w1 = A::tof(w[k]) * gm(k), w2 = A::tof(w[D + k]) * gm(D + k);
+    const float w3 = A::tof(w[2 * D + k]) * gm(2 * D + k), w4 = A::tof(w[3 * D + k]) * gm(3 * D + k);
     WPQ[(size_t)o * D + k] = A::fromf(w1 + w3);
     WPQ[(size_t)(H1 + o) * D + k] = A::fromf(w2 - w3);
     A4[(size_t)o * D + k] = A::fromf(w4);
     sr += w1 + w2 + w3 + w4;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) sc = fmaf(A::tof(w[q * D + k]), bet[q * D + k], sc);
+    for (int q = 0; q < 4; ++q) sc = fmaf(A::tof(w[q * D + k]), bet ? bet[q * D + k] : 0.f, sc);
   }
   __shared__ float red[2][256];
   red[0][threadIdx.x] = sr;
@@ -1174,48 +1194,50 @@ static GnnArgs a0_shape(int64_t F, int64_t N, int64_t D, int64_t E) {
   return a;
 }
 
-// params (module order): 0 pair_norm.w, 1 pair_norm.b, 2 edge_mlp.0.w, 3 edge_mlp.0.b, 4 edge_mlp.2.w,
-// 5 edge_mlp.2.b, 6 edge_weight.w, 7 edge_weight.b, 8 msg_mlp.0.w, 9 msg_mlp.0.b, 10 update_mlp.0.w,
-// 11 update_mlp.0.b, 12 update_mlp.2.w, 13 update_mlp.2.b, 14 causal_mlp.0.w, 15 causal_mlp.0.b,
-// 16 causal_mlp.2.w, 17 causal_mlp.2.b
+// One GNN call's workspace views and the steps shared by RelationGraph.forward and gnn_message_pass: the node
+// projections P | Q, the edge pass (messages and / or causal edges and / or edge features), the node update.
 template <int DT>
-static int gnn_forward(const float* nodes, const float* alive, float* nodes_out, float* causal, int64_t F, int64_t N,
-                       int64_t D, int64_t E, int64_t rounds, int chunked, const void* const* p, float eps,
-                       char* ws, const GnnWs& L, hipStream_t st) {
+struct GnnRun {
   using T = typename MM<DT>::T;
-  T* WPQ = reinterpret_cast<T*>(ws + L.wpq);
-  T* A4 = reinterpret_cast<T*>(ws + L.a4);
-  float* r = reinterpret_cast<float*>(ws + L.r);
-  float* c = reinterpret_cast<float*>(ws + L.c);
-  float* PQ = reinterpret_cast<float*>(ws + L.pq);
-  float* XA = reinterpret_cast<float*>(ws + L.xa);   // [F*N, 2D]: nodes | messages
-  void* U = ws + L.u;                                // [F*N, D] hidden layer of the node update
-  float* nstat = reinterpret_cast<float*>(ws + L.nstat);   // [F*N][2] node sums and sums of squares
-  const int64_t R = F * N, ld = 2 * D;
-  auto P = [&](int i) { return p[i]; };
-  auto Pf = [&](int i) { return reinterpret_cast<const float*>(p[i]); };
-  int rc;
-#define HCLSM_TRY(call) \
-  do {                  \
-    rc = (call);        \
-    if (rc) return rc;  \
-  } while (0)
-  hipLaunchKernelGGL((gnn_prep_kernel<DT>), dim3((unsigned)(2 * E)), dim3(256), 0, st, (const T*)P(2), Pf(3), Pf(0),
-                     Pf(1), WPQ, A4, r, c, (int)D, (int)E);
-  HCLSM_LAUNCH_CHECK();
-  HCLSM_TRY(copy_rows(nodes, D, nullptr, XA, ld, R, D, st));
   GnnArgs a{};
-  a.X = XA; a.ldx = ld; a.PQ = PQ; a.A4 = A4; a.r = r; a.c = c;
-  a.W2 = P(4); a.b2 = Pf(5); a.we = Pf(6); a.be = Pf(7); a.Wm = P(8); a.bm = Pf(9);
-  a.C1 = P(14); a.d1 = Pf(15); a.cc2 = Pf(16); a.d2 = Pf(17);
-  a.alive = alive; a.ldagg = ld;
-  a.F = (int)F; a.N = (int)N; a.NP = (int)((N + 15) / 16 * 16); a.D = (int)D; a.E = (int)E; a.eps = eps;
-  auto edges = [&](bool msg, bool caus) -> int {
+  T* WPQ;
+  T* A4;
+  float* r;
+  float* c;
+  float* PQ;
+  float* XA;      // [F*N, 2D]: nodes | messages
+  void* U;        // [F*N, D] hidden layer of the node update
+  float* nstat;   // [F*N][2] node sums and sums of squares
+  int64_t R, D, E, ld;
+  const void* u1;
+  const float* c1;
+  const void* u2;
+  const float* c2;
+  hipStream_t st;
+
+  GnnRun(char* ws, const GnnWs& L, int64_t F, int64_t N, int64_t D_, int64_t E_, const float* alive, hipStream_t s)
+      : WPQ(reinterpret_cast<T*>(ws + L.wpq)), A4(reinterpret_cast<T*>(ws + L.a4)),
+        r(reinterpret_cast<float*>(ws + L.r)), c(reinterpret_cast<float*>(ws + L.c)),
+        PQ(reinterpret_cast<float*>(ws + L.pq)), XA(reinterpret_cast<float*>(ws + L.xa)), U(ws + L.u),
+        nstat(reinterpret_cast<float*>(ws + L.nstat)), R(F * N), D(D_), E(E_), ld(2 * D_), st(s) {
+    a.X = XA; a.ldx = ld; a.PQ = PQ; a.A4 = A4; a.r = r; a.c = c;
+    a.alive = alive; a.ldagg = ld;
+    a.F = (int)F; a.N = (int)N; a.NP = (int)((N + 15) / 16 * 16); a.D = (int)D_; a.E = (int)E_;
+  }
+  // W1 = edge_mlp.0.weight [2E, 4D] folded into P | Q weights, A4, r, c (gamma / beta null: no pair norm)
+  int prep(const void* W1, const float* b1, const float* gam, const float* bet) {
+    hipLaunchKernelGGL((gnn_prep_kernel<DT>), dim3((unsigned)(2 * E)), dim3(256), 0, st, (const T*)W1, b1, gam, bet,
+                       WPQ, A4, r, c, (int)D, (int)E);
+    HCLSM_LAUNCH_CHECK();
+    return 0;
+  }
+  int edges(bool msg, float* causal, float* edges_out) {
     int e = linear_rows(XA, ld, HCLSM_F32, WPQ, D, nullptr, nullptr, 0, PQ, 4 * E, HCLSM_F32, R, 4 * E, D, 0, 0,
-                        nullptr, nullptr, eps, nullptr, 0, nullptr, 1, DT, st);
+                        nullptr, nullptr, a.eps, nullptr, 0, nullptr, 1, DT, st);
     if (e) return e;
     a.agg = msg ? XA + D : nullptr;
-    a.causal = caus ? causal : nullptr;
+    a.causal = causal;
+    a.edges = edges_out;
     if constexpr (DT != HCLSM_F32) {
       const int vec = D % 4 == 0 && ld % 4 == 0 && ((uintptr_t)XA & 15) == 0;
       hipLaunchKernelGGL(gnn_node_stats_kernel, dim3((unsigned)((R + 3) / 4)), dim3(256), 0, st, XA, ld, nstat, R,
@@ -1225,32 +1247,84 @@ static int gnn_forward(const float* nodes, const float* alive, float* nodes_out,
       if (e != 1) return e;
     }
     return launch_edges<DT>(a, st);
-  };
-  auto update = [&]() -> int {   // nodes += U2 ReLU(U1 [nodes; agg] + c1) + c2, in place in XA
-    int e = linear_rows(XA, ld, HCLSM_F32, P(10), 2 * D, Pf(11), nullptr, 0, U, D, DT, R, D, 2 * D, 0, 1, nullptr,
-                        nullptr, eps, nullptr, 0, nullptr, 1, DT, st);
+  }
+  // nodes += U2 ReLU(U1 [nodes; agg] + c1) + c2, in place in XA
+  int update() {
+    int e = linear_rows(XA, ld, HCLSM_F32, u1, 2 * D, c1, nullptr, 0, U, D, DT, R, D, 2 * D, 0, 1, nullptr, nullptr,
+                        a.eps, nullptr, 0, nullptr, 1, DT, st);
     if (e) return e;
-    return linear_rows(U, D, DT, P(12), D, Pf(13), XA, ld, XA, ld, HCLSM_F32, R, D, D, 0, 0, nullptr, nullptr, eps,
-                       nullptr, 0, nullptr, 1, DT, st);
-  };
+    return linear_rows(U, D, DT, u2, D, c2, XA, ld, XA, ld, HCLSM_F32, R, D, D, 0, 0, nullptr, nullptr, a.eps, nullptr,
+                       0, nullptr, 1, DT, st);
+  }
+};
+
+#define HCLSM_TRY(call) \
+  do {                  \
+    const int rc_ = (call); \
+    if (rc_) return rc_;    \
+  } while (0)
+
+// params (module order): 0 pair_norm.w, 1 pair_norm.b, 2 edge_mlp.0.w, 3 edge_mlp.0.b, 4 edge_mlp.2.w,
+// 5 edge_mlp.2.b, 6 edge_weight.w, 7 edge_weight.b, 8 msg_mlp.0.w, 9 msg_mlp.0.b, 10 update_mlp.0.w,
+// 11 update_mlp.0.b, 12 update_mlp.2.w, 13 update_mlp.2.b, 14 causal_mlp.0.w, 15 causal_mlp.0.b,
+// 16 causal_mlp.2.w, 17 causal_mlp.2.b
+template <int DT>
+static int gnn_forward(const float* nodes, const float* alive, float* nodes_out, float* causal, int64_t F, int64_t N,
+                       int64_t D, int64_t E, int64_t rounds, int chunked, const void* const* p, float eps,
+                       char* ws, const GnnWs& L, hipStream_t st) {
+  auto Pf = [&](int i) { return reinterpret_cast<const float*>(p[i]); };
+  GnnRun<DT> g(ws, L, F, N, D, E, alive, st);
+  g.a.W2 = p[4]; g.a.b2 = Pf(5); g.a.we = Pf(6); g.a.be = Pf(7); g.a.Wm = p[8]; g.a.bm = Pf(9);
+  g.a.C1 = p[14]; g.a.d1 = Pf(15); g.a.cc2 = Pf(16); g.a.d2 = Pf(17);
+  g.a.eps = eps;
+  g.a.norm = 1;
+  g.u1 = p[10]; g.c1 = Pf(11); g.u2 = p[12]; g.c2 = Pf(13);
+  HCLSM_TRY(g.prep(p[2], Pf(3), Pf(0), Pf(1)));
+  HCLSM_TRY(copy_rows(nodes, D, nullptr, g.XA, g.ld, g.R, D, st));
   // Round structure (relation_graph.py:150-188): the all-pairs path (N <= 32) computes the edges of the
   // input nodes, recomputes them after a round only when rounds > 1, and takes the causal edges from the
   // last edges computed; the chunked path recomputes the edges every round and takes the causal edges
   // from the final nodes.  Both coincide except for rounds == 1.
   if (rounds == 0) {
-    HCLSM_TRY(edges(false, true));
+    HCLSM_TRY(g.edges(false, causal, nullptr));
   } else {
-    HCLSM_TRY(edges(true, rounds == 1 && !chunked));
+    HCLSM_TRY(g.edges(true, rounds == 1 && !chunked ? causal : nullptr, nullptr));
     for (int64_t rd = 0; rd < rounds; ++rd) {
-      HCLSM_TRY(update());
-      if (rd + 1 < rounds) HCLSM_TRY(edges(true, false));
+      HCLSM_TRY(g.update());
+      if (rd + 1 < rounds) HCLSM_TRY(g.edges(true, nullptr, nullptr));
     }
-    if (rounds > 1 || chunked) HCLSM_TRY(edges(false, true));
+    if (rounds > 1 || chunked) HCLSM_TRY(g.edges(false, causal, nullptr));
   }
-  HCLSM_TRY(copy_rows(XA, ld, alive, nodes_out, D, R, D, st));
-#undef HCLSM_TRY
+  HCLSM_TRY(copy_rows(g.XA, g.ld, alive, nodes_out, D, g.R, D, st));
   return 0;
 }
+
+// gnn_message_pass (hclsm/kernels/gnn_message_pass.py:38-100): no pair norm, no causal head; every round
+// computes the edges of the current nodes, the messages and the update, and the last round's edge features of
+// the targets [ej0, ej0 + enj) are written out.  params: 0 edge_mlp.0.w [2E, 4D], 1 edge_mlp.0.b, 2 edge_mlp.2.w
+// [E, 2E], 3 edge_mlp.2.b, 4 edge_weight.w [E], 5 edge_weight.b [1], 6 msg_mlp.0.w [D, E], 7 msg_mlp.0.b,
+// 8 update_mlp.0.w [D, 2D], 9 update_mlp.0.b, 10 update_mlp.2.w [D, D], 11 update_mlp.2.b
+template <int DT>
+static int gnn_mp_forward(const float* nodes, const float* alive, float* nodes_out, float* edges_out, int64_t F,
+                          int64_t N, int64_t D, int64_t E, int64_t rounds, int64_t ej0, int64_t enj,
+                          const void* const* p, char* ws, const GnnWs& L, hipStream_t st) {
+  auto Pf = [&](int i) { return reinterpret_cast<const float*>(p[i]); };
+  GnnRun<DT> g(ws, L, F, N, D, E, alive, st);
+  g.a.W2 = p[2]; g.a.b2 = Pf(3); g.a.we = Pf(4); g.a.be = Pf(5); g.a.Wm = p[6]; g.a.bm = Pf(7);
+  g.a.norm = 0;
+  g.a.ej0 = (int)ej0;
+  g.a.enj = (int)enj;
+  g.u1 = p[8]; g.c1 = Pf(9); g.u2 = p[10]; g.c2 = Pf(11);
+  HCLSM_TRY(g.prep(p[0], Pf(1), nullptr, nullptr));
+  HCLSM_TRY(copy_rows(nodes, D, nullptr, g.XA, g.ld, g.R, D, st));
+  for (int64_t rd = 0; rd < rounds; ++rd) {
+    HCLSM_TRY(g.edges(true, nullptr, rd + 1 == rounds && enj > 0 ? edges_out : nullptr));
+    HCLSM_TRY(g.update());
+  }
+  HCLSM_TRY(copy_rows(g.XA, g.ld, alive, nodes_out, D, g.R, D, st));
+  return 0;
+}
+#undef HCLSM_TRY
 
 }  // namespace hclsm
 
@@ -1302,5 +1376,53 @@ extern "C" int hclsm_relation_graph_forward(const float* nodes, const float* ali
     default:
       return gnn_forward<HCLSM_F32>(nodes, alive, nodes_out, causal, frames, N, D, E, rounds, chunked, params, ln_eps,
                                     ws, L, st);
+  }
+}
+
+// HCLSM_ERR_UNSUPPORTED outside the message-pass kernels: D, E multiples of 16 (fp32) or 32 (16-bit operands),
+// E <= 192, N <= 64 (fp32) or 128, and the workgroup's LDS tiles within 160 KB.
+static int gnn_mp_check(int64_t N, int64_t D, int64_t E, int dtype) {
+  if (N < 0 || D <= 0 || E <= 0) return HCLSM_ERR_SHAPE;
+  if (dtype != HCLSM_F32 && dtype != HCLSM_BF16 && dtype != HCLSM_F16) return HCLSM_ERR_DTYPE;
+  const int NW = dtype == HCLSM_F32 ? 4 : 8, mult = dtype == HCLSM_F32 ? 16 : 32;
+  if (D % mult || E % mult || E > 192 || N > 16 * NW) return HCLSM_ERR_UNSUPPORTED;
+  const GnnArgs a = a0_shape(1, N, D, E);
+  const bool fit = dtype == HCLSM_F32 ? edges_fit<HCLSM_F32>(a) : edges_fit<HCLSM_BF16>(a);
+  return fit ? 0 : HCLSM_ERR_UNSUPPORTED;
+}
+
+extern "C" int64_t hclsm_gnn_message_pass_workspace(int64_t frames, int64_t N, int64_t D, int64_t E, int dtype) {
+  if (frames < 0) return HCLSM_ERR_SHAPE;
+  const int c = gnn_mp_check(N, D, E, dtype);
+  if (c) return c;
+  return (int64_t)gnn_ws(frames, N, D, E, dtype == HCLSM_F32 ? 4 : 2).total;
+}
+
+extern "C" int hclsm_gnn_message_pass(const float* nodes, const float* alive, float* nodes_out, float* edges_out,
+                                      int64_t frames, int64_t N, int64_t D, int64_t E, int64_t rounds, int64_t ej0,
+                                      int64_t enj, const void* const* params, int dtype, void* workspace,
+                                      int64_t workspace_bytes, void* stream) {
+  if (frames < 0 || rounds < 0 || ej0 < 0 || enj < 0 || ej0 + enj > N) return HCLSM_ERR_SHAPE;
+  const int chk = gnn_mp_check(N, D, E, dtype);
+  if (chk) return chk;
+  if (frames * N > 0x7fffffffLL || frames * N * (enj > 0 ? enj : 1) * E > (1LL << 40)) return HCLSM_ERR_SHAPE;
+  if (frames == 0 || N == 0) return 0;
+  if (!nodes || !nodes_out || !params || !workspace || (enj > 0 && rounds > 0 && !edges_out)) return HCLSM_ERR_NULL;
+  for (int i = 0; i < 12; ++i)
+    if (!params[i]) return HCLSM_ERR_NULL;
+  const GnnWs L = gnn_ws(frames, N, D, E, dtype == HCLSM_F32 ? 4 : 2);
+  if (workspace_bytes < (int64_t)L.total) return HCLSM_ERR_SHAPE;
+  char* ws = reinterpret_cast<char*>(workspace);
+  hipStream_t st = (hipStream_t)stream;
+  switch (dtype) {
+    case HCLSM_BF16:
+      return gnn_mp_forward<HCLSM_BF16>(nodes, alive, nodes_out, edges_out, frames, N, D, E, rounds, ej0, enj, params,
+                                        ws, L, st);
+    case HCLSM_F16:
+      return gnn_mp_forward<HCLSM_F16>(nodes, alive, nodes_out, edges_out, frames, N, D, E, rounds, ej0, enj, params,
+                                       ws, L, st);
+    default:
+      return gnn_mp_forward<HCLSM_F32>(nodes, alive, nodes_out, edges_out, frames, N, D, E, rounds, ej0, enj, params,
+                                       ws, L, st);
   }
 }

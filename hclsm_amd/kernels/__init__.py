@@ -46,7 +46,21 @@ from hclsm_amd.kernels.slot_attention_kernel import (
     naive_slot_attention,
     compiled_slot_attention,
     fused_slot_attention_triton,
+    TRITON_AVAILABLE,
 )
+from hclsm_amd.kernels.gnn_message_pass import (
+    gnn_message_pass_fn,
+    naive_gnn_message_pass,
+    optimized_gnn_message_pass,
+    chunked_gnn_message_pass,
+)
+from hclsm_amd.kernels.hierarchical_state import (
+    hierarchical_state_fn,
+    hierarchical_state_naive,
+    hierarchical_state_fused,
+    hierarchical_state_streamed,
+)
+from hclsm_amd.kernels._common import HipFallbackWarning
 from hclsm_amd.kernels.slot_iteration import (
     SlotMode,
     SlotWeights,
@@ -56,7 +70,6 @@ from hclsm_amd.kernels.slot_iteration import (
     slot_attention_forward,
 )
 
-TRITON_AVAILABLE = False
 
 
 def _hip_available() -> bool:
@@ -106,6 +119,15 @@ __all__ = [
     "event_attention",
     "track_causal_event_attention",
     "slots_attention",
+    "gnn_message_pass_fn",
+    "naive_gnn_message_pass",
+    "optimized_gnn_message_pass",
+    "chunked_gnn_message_pass",
+    "hierarchical_state_fn",
+    "hierarchical_state_naive",
+    "hierarchical_state_fused",
+    "hierarchical_state_streamed",
+    "HipFallbackWarning",
     "TRITON_AVAILABLE",
     "HIP_AVAILABLE",
     "ops",

@@ -32,3 +32,22 @@ def common_float_dtype(*tensors: torch.Tensor) -> torch.dtype:
         if dt in (torch.float32, torch.bfloat16, torch.float16):
             return dt
     return torch.float32
+
+
+class HipFallbackWarning(UserWarning):
+    """A call ran the reference's math as torch ops on the GPU instead of an hclsm_amd kernel (autograd through a
+    forward-only kernel, or a module structure / shape the kernel does not take)."""
+
+
+_WARNED: set = set()
+
+
+def warn_fallback(fn_name: str, reason: str) -> None:
+    """Warn (once per function and reason) that fn_name is running torch ops instead of its HIP kernel."""
+    import warnings
+    key = (fn_name, reason)
+    if key in _WARNED:
+        return
+    _WARNED.add(key)
+    warnings.warn(f"hclsm_amd.{fn_name}: running the reference math as torch ops on the GPU: {reason}",
+                  HipFallbackWarning, stacklevel=3)

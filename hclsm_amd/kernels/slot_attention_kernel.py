@@ -26,6 +26,9 @@ from hclsm_amd.kernels._common import common_float_dtype, require_gpu
 
 _EPS_BACKENDS = ("auto", "triton", "hip")
 
+# The reference exports this flag from this module (:14-20); there is no Triton path here.
+TRITON_AVAILABLE = False
+
 
 def _core_raw(Q, K, V, scale, denom_eps, logit_clamp=None, renorm_eps=None, want_attn=True,
               attn_dtype=None):

@@ -401,6 +401,29 @@ int hclsm_relation_graph_forward(const float* nodes, const float* alive, float* 
                                  const void* const* params, float ln_eps, int dtype, void* workspace,
                                  int64_t workspace_bytes, void* stream);
 
+/* Workspace bytes for hclsm_gnn_message_pass, or HCLSM_ERR_UNSUPPORTED for a shape outside it. */
+int64_t hclsm_gnn_message_pass_workspace(int64_t frames, int64_t N, int64_t D, int64_t E, int dtype);
+
+/*
+ * GNN message passing over the N slots of `frames` frames, n_rounds rounds of:
+ *   e_ij = ReLU(W2 ReLU(W1 [n_i; n_j; n_i - n_j; n_i * n_j] + b1) + b2)      (no pair norm)
+ *   w_ij = sigmoid(we . e_ij + be) * alive_i * alive_j
+ *   agg_i = sum_j ReLU(Wm e_ij + bm) w_ij,   n_i += U2 ReLU(U1 [n_i; agg_i] + c1) + c2
+ * then nodes_out = n * alive.  The last round's edge features of the targets j in [ej0, ej0 + enj) go to
+ * edges_out [frames, N, enj, E] float32 (as the next layer sees them: rounded to `dtype` for 16-bit operands).
+ * nodes, nodes_out [frames, N, D], alive [frames, N] (nullable): float32.  params: host array of 12 device
+ * pointers edge_mlp.0.weight [2E, 4D] / .bias, edge_mlp.2.weight [E, 2E] / .bias, edge_weight.weight [E] /
+ * .bias [1], msg_mlp.0.weight [D, E] / .bias, update_mlp.0.weight [D, 2D] / .bias, update_mlp.2.weight [D, D] /
+ * .bias; matrices in `dtype` (F32 / BF16 / F16), vectors float32, none nullable.  D, E multiples of 16 (F32) or 32,
+ * E <= 192, N <= 64 (F32) or 128.
+ * Replaces: naive_gnn_message_pass / optimized_gnn_message_pass (all pairs, enj = N) and
+ *   chunked_gnn_message_pass (edges of the last target chunk) of hclsm/kernels/gnn_message_pass.py:38-243.
+ */
+int hclsm_gnn_message_pass(const float* nodes, const float* alive, float* nodes_out, float* edges_out,
+                           int64_t frames, int64_t N, int64_t D, int64_t E, int64_t n_rounds, int64_t ej0,
+                           int64_t enj, const void* const* params, int dtype, void* workspace,
+                           int64_t workspace_bytes, void* stream);
+
 /* ---- slot tracker (hclsm/objects/slot_tracker.py, tracking loop of hclsm/model.py:229-252) ----
  * Shapes: D (d_slot) a multiple of 64 and at most 384; the Sinkhorn entries N <= 128.  The workspace
  * queries return HCLSM_ERR_UNSUPPORTED outside these.  Slots, alive flags, costs and hidden states are

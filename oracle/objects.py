@@ -11,6 +11,8 @@ Numpy float64 restatements taking parameters as plain arrays (names as in the re
   tracker_forward_ref  :112-138 (perm, matched)
   reorder_update_ref   :140-158 (gather by perm, GRUCell carry, unmatched rows take the new slot)
   track_sequence_ref   the frame loop of hclsm/model.py:229-252 (tracked slots and alive masks)
+  gnn_message_pass_ref hclsm/kernels/gnn_message_pass.py:38-100 and :168-243 (no pair norm, no causal head;
+                       edge features of the last round, or of its last target chunk)
 """
 
 from __future__ import annotations
@@ -159,3 +161,24 @@ def track_sequence_ref(slots, alive, p):
         tracked.append(re)
         al.append(np.take_along_axis(alive[:, t], perm, axis=1))
     return np.stack(tracked, 1), np.stack(al, 1), hidden
+
+
+def gnn_message_pass_ref(nodes, alive, p, n_rounds, chunk_size=None):
+    """naive_gnn_message_pass (gnn_message_pass.py:38-100) -> (nodes (F, N, D), edge features of the last round
+    (F, N, N, E), or None for no rounds).  With chunk_size, the edge features of the last chunk of targets
+    (F, N, C, E), as chunked_gnn_message_pass keeps them (:225-227); the nodes are the same.  p: the
+    parameters edge_mlp.0 / .2, edge_weight, msg_mlp.0, update_mlp.0 / .2 (.weight / .bias)."""
+    x = _f(nodes)
+    F, N, D = x.shape
+    mask = np.ones((F, N, N)) if alive is None else _f(alive)[:, :, None] * _f(alive)[:, None, :]
+    e = None
+    for _ in range(n_rounds):
+        pf = pair_features(x, x)
+        e = _relu(_lin(_relu(_lin(pf, p, "edge_mlp.0")), p, "edge_mlp.2"))
+        w = sigmoid(_lin(e, p, "edge_weight")[..., 0]) * mask
+        x = _update(x, _messages(e, w, p), p)
+    if alive is not None:
+        x = x * _f(alive)[:, :, None]
+    if e is not None and chunk_size is not None:
+        e = e[:, :, ((N - 1) // chunk_size) * chunk_size:]
+    return x, e

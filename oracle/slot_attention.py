@@ -21,7 +21,7 @@ Config-2 mode:  no clamps, renorm_eps=1e-8, MLP hidden 768.
 
 Forward up to the iterations (dynamic_slots.py:149-164): k, v = LN_in(inputs) W_k^T, W_v^T,
 then n_iter iterations from the given initial slots (the Gaussian draw of _init_slots :86-96
-is the caller's; existence head and slot birth :166-199 are outside this path).
+is the caller's).  dynamic_slots_forward_ref adds the existence head and slot birth (:166-199).
 All float64.
 """
 
@@ -116,3 +116,31 @@ def slot_attention_forward(inputs, slots0, W, n_iter, **mode):
     for _ in range(n_iter):
         s = slot_iteration(s, k, v, W64, **mode)
     return s
+
+
+def dynamic_slots_forward_ref(inputs, slots0, W, n_iter, existence_threshold, birth_threshold, scale=None):
+    """DynamicSlotAttention.forward (dynamic_slots.py:149-199) from given initial slots (the _init_slots draw
+    is the caller's), reference mode (logits +-30, slots +-50): the iterations, the existence head
+    (:167-168) and slot birth (:180-199: the residual |1 - sum over slots of the unclamped softmax| per
+    token; for each clip whose largest residual exceeds birth_threshold and that has a dormant slot, alive <
+    existence_threshold, the first dormant slot becomes birth_proj(inputs[b, token of the largest residual],
+    the first such token on ties).  Extra W keys: e1_w, e1_b, e2_w, e2_b (existence_head.0 / .2), birth_w,
+    birth_b.  Returns (slots (B, N, d), alive (B, N))."""
+    W64 = {n: np.asarray(a, np.float64) for n, a in W.items()}
+    x_in = np.asarray(inputs, np.float64)
+    d = W64["w_q"].shape[0]
+    scale = d ** -0.5 if scale is None else scale
+    s = slot_attention_forward(x_in, slots0, W64, n_iter, scale=scale, logit_clamp=30.0, slot_clamp=50.0)
+    h = np.maximum(s @ W64["e1_w"].T + W64["e1_b"], 0.0)
+    alive = sigmoid((h @ W64["e2_w"].T + W64["e2_b"])[..., 0])
+    k = layer_norm(x_in, W64["ln_in_w"], W64["ln_in_b"]) @ W64["w_k"].T
+    q = layer_norm(s, W64["ln_pre_w"], W64["ln_pre_b"]) @ W64["w_q"].T
+    _, attn = slot_attention_core(q, k, k, scale=scale)
+    residual = np.abs(1.0 - attn.sum(axis=1))                                  # (B, M)
+    out = s.copy()
+    for b in range(s.shape[0]):
+        dormant = np.nonzero(alive[b] < existence_threshold)[0]
+        if residual[b].max() > birth_threshold and dormant.size:
+            tok = int(np.argmax(residual[b]))
+            out[b, dormant[0]] = x_in[b, tok] @ W64["birth_w"].T + W64["birth_b"]
+    return out, alive

@@ -278,6 +278,60 @@ def test_dynamic_slots_fused_forward_matches_oracle_and_grad_path():
     assert normwise_rel_err(_np(a_fused), _np(a_grad)) <= 1e-5
 
 
+def _dyn_weights(m):
+    W = {"ln_in_w": m.norm_input.weight, "ln_in_b": m.norm_input.bias, "w_k": m.project_k.weight,
+         "w_v": m.project_v.weight, "ln_pre_w": m.norm_pre_attn.weight, "ln_pre_b": m.norm_pre_attn.bias,
+         "w_q": m.project_q.weight, "w_ih": m.gru.weight_ih, "w_hh": m.gru.weight_hh, "b_ih": m.gru.bias_ih,
+         "b_hh": m.gru.bias_hh, "ln_mlp_w": m.norm_slots.weight, "ln_mlp_b": m.norm_slots.bias,
+         "w1": m.mlp[0].weight, "b1": m.mlp[0].bias, "w2": m.mlp[2].weight, "b2": m.mlp[2].bias,
+         "e1_w": m.existence_head[0].weight, "e1_b": m.existence_head[0].bias, "e2_w": m.existence_head[2].weight,
+         "e2_b": m.existence_head[2].bias, "birth_w": m.birth_proj.weight, "birth_b": m.birth_proj.bias}
+    return {k: _np(v) for k, v in W.items()}
+
+
+@pytest.mark.parametrize("grad", [False, True])
+def test_dynamic_slots_birth_matches_oracle(grad):
+    """Slot birth (dynamic_slots.py:180-199) on, in the fused no-grad path and the autograd path, against
+    oracle/slot_attention.py::dynamic_slots_forward_ref: one input token (the residual's argmax is token 0
+    exactly), a birth threshold every clip exceeds, an existence threshold between two alive values of every
+    clip (so some slots are dormant and the decision is far from rounding); then a threshold no residual
+    reaches (the residual is rounding noise) leaves the slots as the iterations made them."""
+    from hclsm_amd.objects import DynamicSlotAttention
+    torch.manual_seed(31)
+    m = DynamicSlotAttention(TINY.objects, TINY.d_world).cuda()
+    x = torch.randn(4, 1, TINY.d_world, device="cuda")
+    W = _dyn_weights(m)
+    torch.manual_seed(32)
+    with torch.no_grad():
+        slots0 = m._init_slots(4, "cuda")
+    _, alive_ref = sa.dynamic_slots_forward_ref(_np(x), _np(slots0), W, m.n_iterations, 0.0, 10.0)
+    a = np.sort(alive_ref, axis=1)
+    gaps = a[:, 1:] - a[:, :-1]
+    k = int(np.argmax(gaps.min(axis=0)))              # the rank whose gap is widest in the worst clip
+    thr = float(np.clip(0.5 * (a[:, k].max() + a[:, k + 1].min()), 1e-6, 1 - 1e-6))
+    if not (a[:, k].max() + 1e-4 < thr < a[:, k + 1].min() - 1e-4):
+        thr = float(np.median(alive_ref))
+    m.existence_threshold = thr
+    m.birth_threshold = -1.0
+    ref, _ = sa.dynamic_slots_forward_ref(_np(x), _np(slots0), W, m.n_iterations, thr, -1.0)
+    torch.manual_seed(32)
+    with torch.set_grad_enabled(grad):
+        s, alive = m(x)
+    assert normwise_rel_err(_np(alive), alive_ref) <= 1e-5
+    assert normwise_rel_err(_np(s), ref) <= 1e-5
+    born = np.abs(ref - sa.dynamic_slots_forward_ref(_np(x), _np(slots0), W, m.n_iterations, thr, 10.0)[0])
+    assert (born.max(axis=-1) > 1e-3).sum() >= 1     # at least one slot was born
+    m.birth_threshold = 1e-3
+    torch.manual_seed(32)
+    with torch.set_grad_enabled(grad):
+        s2, _ = m(torch.randn(4, 9, TINY.d_world, device="cuda"))
+    torch.manual_seed(32)
+    m.birth_threshold = 10.0
+    with torch.set_grad_enabled(grad):
+        s3, _ = m(torch.randn(4, 9, TINY.d_world, device="cuda"))
+    assert torch.isfinite(s2).all() and torch.equal(s2, s3)
+
+
 def test_hot_path_from_reference_checkpoint_matches_oracle(tmp_path):
     """step_N.pt with the reference's layout (distributed.py:295-304) -> build_hot_path -> Level-0 and
     packed Level-1 forwards against oracle/modules.py with the checkpoint's weights."""

@@ -150,3 +150,50 @@ def test_tracker_identity_frames_and_dead_penalty():
     base = ob.tracker_cost_ref(s, s, np.ones_like(alive), np.ones_like(alive), p)
     assert np.allclose(cost[0, 4, :4] - base[0, 4, :4], 1e4) and np.allclose(cost[0, :4, 4] - base[0, :4, 4], 1e4)
     assert np.allclose(cost[0, 4, 4] - base[0, 4, 4], 2e4)
+
+
+def _loop_mp_round(x, p, mask):
+    """One gnn_message_pass round (no pair norm) element by element: (new nodes, edge features)."""
+    F, N, D = x.shape
+    relu = lambda v: np.maximum(v, 0)
+    out = np.empty_like(x)
+    e_all = np.empty((F, N, N, p["edge_mlp.2.weight"].shape[0]))
+    for f in range(F):
+        for i in range(N):
+            agg = np.zeros(D)
+            for j in range(N):
+                pf = np.concatenate([x[f, i], x[f, j], x[f, i] - x[f, j], x[f, i] * x[f, j]])
+                e = relu(p["edge_mlp.2.weight"] @ relu(p["edge_mlp.0.weight"] @ pf + p["edge_mlp.0.bias"])
+                         + p["edge_mlp.2.bias"])
+                e_all[f, i, j] = e
+                w = 1 / (1 + np.exp(-(p["edge_weight.weight"][0] @ e + p["edge_weight.bias"][0]))) * mask[f, i, j]
+                agg += relu(p["msg_mlp.0.weight"] @ e + p["msg_mlp.0.bias"]) * w
+            u = relu(p["update_mlp.0.weight"] @ np.concatenate([x[f, i], agg]) + p["update_mlp.0.bias"])
+            out[f, i] = x[f, i] + p["update_mlp.2.weight"] @ u + p["update_mlp.2.bias"]
+    return out, e_all
+
+
+def test_gnn_message_pass_matches_loop_restatement_and_chunk_window():
+    """gnn_message_pass_ref against the element-wise loop (2 rounds: edges of the second round come from the
+    once-updated nodes), the chunked form's last-chunk window, and zero rounds."""
+    D, E, F, N = 6, 4, 2, 5
+    p = _gnn_params(D, E, 6)
+    x = np.random.default_rng(7).standard_normal((F, N, D))
+    alive = np.array([[1, 1, 0, 1, 1], [1, 0.5, 1, 1, 1]], np.float64)   # a fractional alive value too
+    mask = alive[:, :, None] * alive[:, None, :]
+    x1, _ = _loop_mp_round(x, p, mask)
+    x2, e1 = _loop_mp_round(x1, p, mask)
+    got, e = ob.gnn_message_pass_ref(x, alive, p, 2)
+    np.testing.assert_allclose(got, x2 * alive[..., None], rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(e, e1, rtol=1e-12, atol=1e-12)
+    gc, ec = ob.gnn_message_pass_ref(x, alive, p, 2, chunk_size=2)
+    np.testing.assert_array_equal(gc, got)
+    np.testing.assert_allclose(ec, e1[:, :, 4:], rtol=1e-12, atol=1e-12)   # last chunk of targets: [4, 5)
+    g0, e0 = ob.gnn_message_pass_ref(x, alive, p, 0)
+    assert e0 is None
+    np.testing.assert_array_equal(g0, x * alive[..., None])
+    # the pair norm is the only difference from RelationGraph: with an identity-like norm removed, the
+    # relation graph's edges differ, so a stray LayerNorm in the message pass would be caught above
+    rg, _ = ob.relation_graph_ref(x, alive, p, 1, chunked=True)
+    mp, _ = ob.gnn_message_pass_ref(x, alive, p, 1)
+    assert np.abs(rg - mp).max() > 1e-3

@@ -120,3 +120,66 @@ def test_logit_clamp_binds_and_renorm_rows_sum_to_one():
     attn = a_clamped + 1e-8
     attn = attn / attn.sum(-1, keepdims=True)
     np.testing.assert_allclose(attn.sum(-1), 1.0, rtol=1e-12)
+
+
+def _birth_case(M, seed=8):
+    """Float64 torch modules for dynamic_slots_forward_ref and the oracle's W dict of the same weights."""
+    torch.manual_seed(seed)
+    d, d_in, B, N = 16, 12, 3, 6
+    mods = dict(ln_in=nn.LayerNorm(d_in), ln_pre=nn.LayerNorm(d), wq=nn.Linear(d, d, bias=False),
+                wk=nn.Linear(d_in, d, bias=False), wv=nn.Linear(d_in, d, bias=False), gru=nn.GRUCell(d, d),
+                ln_mlp=nn.LayerNorm(d), mlp=nn.Sequential(nn.Linear(d, 4 * d), nn.ReLU(), nn.Linear(4 * d, d)),
+                head=nn.Sequential(nn.Linear(d, d // 4), nn.ReLU(), nn.Linear(d // 4, 1)), birth=nn.Linear(d_in, d))
+    mods = {k: m.double() for k, m in mods.items()}
+    W = dict(ln_in_w=mods["ln_in"].weight, ln_in_b=mods["ln_in"].bias, ln_pre_w=mods["ln_pre"].weight,
+             ln_pre_b=mods["ln_pre"].bias, w_q=mods["wq"].weight, w_k=mods["wk"].weight, w_v=mods["wv"].weight,
+             w_ih=mods["gru"].weight_ih, w_hh=mods["gru"].weight_hh, b_ih=mods["gru"].bias_ih,
+             b_hh=mods["gru"].bias_hh, ln_mlp_w=mods["ln_mlp"].weight, ln_mlp_b=mods["ln_mlp"].bias,
+             w1=mods["mlp"][0].weight, b1=mods["mlp"][0].bias, w2=mods["mlp"][2].weight, b2=mods["mlp"][2].bias,
+             e1_w=mods["head"][0].weight, e1_b=mods["head"][0].bias, e2_w=mods["head"][2].weight,
+             e2_b=mods["head"][2].bias, birth_w=mods["birth"].weight, birth_b=mods["birth"].bias)
+    W = {k: v.detach().numpy() for k, v in W.items()}
+    x = torch.randn(B, M, d_in, dtype=torch.float64)
+    s0 = torch.randn(B, N, d, dtype=torch.float64)
+    return mods, W, x, s0
+
+
+def test_dynamic_slots_forward_and_birth_against_torch_modules():
+    """dynamic_slots.py:149-199 with torch modules: the iterations, the existence head, and birth at the first
+    dormant slot from birth_proj(inputs[b, argmax residual]) -- M = 1 token, so the residual's argmax is 0 and
+    the birth decision is exact; thresholds that make every / no clip give birth."""
+    mods, W, x, s0 = _birth_case(M=1)
+    with torch.no_grad():
+        xn = mods["ln_in"](x)
+        k, v = mods["wk"](xn), mods["wv"](xn)
+        s = s0
+        for _ in range(2):
+            s = _torch_iteration(s, k, v, (mods["ln_pre"], mods["wq"], mods["gru"], mods["ln_mlp"], mods["mlp"]),
+                                 30.0, None, 50.0)
+        alive = torch.sigmoid(mods["head"](s).squeeze(-1))
+        born = mods["birth"](x[:, 0])
+    thr = float(alive.median())                        # some slots dormant in some clips
+    got, got_alive = sa.dynamic_slots_forward_ref(x.numpy(), s0.numpy(), W, 2, thr, -1.0)
+    np.testing.assert_allclose(got_alive, alive.numpy(), rtol=1e-12, atol=1e-14)
+    want = s.clone()
+    births = 0
+    for b in range(x.shape[0]):
+        dormant = torch.nonzero(alive[b] < thr).flatten()
+        if len(dormant):
+            want[b, dormant[0]] = born[b]
+            births += 1
+    assert births >= 2
+    np.testing.assert_allclose(got, want.numpy(), rtol=1e-10, atol=1e-12)
+    none, _ = sa.dynamic_slots_forward_ref(x.numpy(), s0.numpy(), W, 2, thr, 2.0)      # residual <= 1: no birth
+    np.testing.assert_allclose(none, s.numpy(), rtol=1e-10, atol=1e-12)
+    none, _ = sa.dynamic_slots_forward_ref(x.numpy(), s0.numpy(), W, 2, 0.0, -1.0)     # nothing dormant
+    np.testing.assert_allclose(none, s.numpy(), rtol=1e-10, atol=1e-12)
+
+
+def test_birth_residual_is_rounding_noise():
+    """The residual |1 - sum over slots of a softmax over slots| is rounding noise (every token's column sums to
+    one), so a birth threshold above ~1e-12 never fires -- the decision the reference takes in practice."""
+    mods, W, x, s0 = _birth_case(M=9, seed=9)
+    got, alive = sa.dynamic_slots_forward_ref(x.numpy(), s0.numpy(), W, 1, 1.0, 1e-9)
+    plain, _ = sa.dynamic_slots_forward_ref(x.numpy(), s0.numpy(), W, 1, 0.0, 1e-9)
+    np.testing.assert_array_equal(got, plain)
