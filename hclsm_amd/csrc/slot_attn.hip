@@ -1198,6 +1198,206 @@ core_update_kernel(const typename MM<DT>::T* __restrict__ P, int64_t Mp, const f
   }
 }
 
+// Fused attention core for the iteration (16-bit operands, v given transposed per frame: vt[b][d][Mp]), one launch
+// per iteration: grid (frame, column block of D / NCB columns), 8 waves.  Each column block of a frame recomputes
+// the frame's logits and softmax (k is read from L2 by the frame's NCB workgroups), so the probabilities never leave
+// the workgroup and no second launch or global round trip is needed.  Every global load of the kernel is issued at
+// its start -- the wave's k tiles, its v^T column tiles and q (staged in LDS) -- so the kernel waits on memory once:
+// measured on MI355X, each dependent round of global loads costs ~1.5 us here, more than the arithmetic.
+//   phase 1 wave w: token tiles w and w + 8: S = q k^T as NT MFMA tiles (slots as rows, 16 tokens as columns),
+//           softmax over the slots of each token column in registers (the NT*4 values of a lane, then the four lane
+//           groups), P (zero for tokens m >= M) to LDS, per-slot sums of P for the renormalisation.
+//   phase 2 wave w: column tiles w, w + 8, ... of the block for every slot: P (A operand, LDS) times the v^T rows
+//           held in registers (tokens m >= M zeroed); epilogue (acc + eps sum_m v) / (sum_m P + M eps).
+// Limits: M <= 256 (two token tiles per wave, eight 32-token blocks of v^T).
+constexpr int CF_WAVES = 8;
+constexpr int CF_MAXM = 256;
+
+template <int DT, int NT, int DD, int NCB>
+__global__ void __launch_bounds__(64 * CF_WAVES)
+core_fused_t_kernel(const typename MM<DT>::T* __restrict__ q, const typename MM<DT>::T* __restrict__ k,
+                    const typename MM<DT>::T* __restrict__ vt, int64_t Mp, typename MM<DT>::T* __restrict__ out,
+                    CoreArgs a) {
+  using A = MM<DT>;
+  using TT = typename A::T;
+  static_assert(A::KPL == 8 && DD % (16 * NCB) == 0, "16-bit operands, whole 16-column tiles per block");
+  constexpr int NW = CF_WAVES, NKB = DD / 32, NS = NT * 16, QP = DD + 8, NCT = DD / NCB / 16;
+  constexpr int CTW = (NCT + NW - 1) / NW, TPW = CF_MAXM / 16 / NW, VB = CF_MAXM / 32;
+  extern __shared__ __align__(16) unsigned char smem[];
+  TT* sq = reinterpret_cast<TT*>(smem);                                  // [NS][QP]
+  TT* sp = sq + NS * QP;                                                 // [NS][Mp + 8] probabilities
+  float* srs = reinterpret_cast<float*>(sp + (size_t)NS * (Mp + 8));     // [NW][NS] per-wave sums of P
+  const int PP = (int)Mp + 8;
+  const int64_t b = blockIdx.x;
+  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, g = lane >> 4, li = lane & 15;
+  const int MT = (int)((a.M + 15) / 16), MPT = (int)(Mp / 16), NVB = (int)(Mp / 32);
+  // ---- every global load first: k tiles, v^T column tiles, q
+  const TT* kf = k + b * a.kb;
+  uint4 kr[TPW][NKB];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) {
+    const int t = wid + NW * j;
+    if (t < MT) {
+      int m = t * 16 + li;
+      m = m < a.M ? m : a.M - 1;
+      const TT* kp = kf + (int64_t)m * a.ldk + 8 * g;
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) kr[j][kb] = *reinterpret_cast<const uint4*>(kp + 32 * kb);
+    }
+  }
+  uint4 vr[CTW][VB];
+#pragma unroll
+  for (int c = 0; c < CTW; ++c) {
+    const int ct = wid + NW * c;
+    if (ct < NCT) {
+      const TT* vp = vt + b * a.vb + (int64_t)(blockIdx.y * (DD / NCB) + ct * 16 + li) * Mp + 8 * g;
+#pragma unroll
+      for (int i = 0; i < VB; ++i)
+        if (i < NVB) vr[c][i] = *reinterpret_cast<const uint4*>(vp + 32 * i);
+    }
+  }
+  for (int u = tid; u < NS * (DD / 8); u += 64 * NW) {   // rows n >= N repeat row N - 1 (their logits are masked)
+    const int n = u / (DD / 8), c = (u - n * (DD / 8)) * 8;
+    const int nc = n < a.N ? n : a.N - 1;
+    *reinterpret_cast<uint4*>(sq + n * QP + c) = *reinterpret_cast<const uint4*>(q + b * a.qb + (int64_t)nc * a.ldq + c);
+  }
+  __syncthreads();
+  // ---- phase 1: logits, softmax over slots, P to LDS
+  float rs[NT][4];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) rs[nt][r] = 0.f;
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) {
+    const int t = wid + NW * j;
+    if (t >= MPT) break;
+    const int m = t * 16 + li;
+    if (t >= MT) {   // the padding tile past the last token tile: zero probabilities
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sp[(nt * 16 + 4 * g + r) * PP + m] = A::fromf(0.f);
+      continue;
+    }
+    f32x4 acc[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      const typename A::Op kv = __builtin_bit_cast(typename A::Op, kr[j][kb]);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)   // acc[nt][r] = logit[n = 16nt + 4g + r][m]
+        acc[nt] = A::mfma(A::load(sq + (nt * 16 + li) * QP + 32 * kb + 8 * g), kv, acc[nt]);
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float sv = acc[nt][r] * a.scale;
+        if (a.logit_clamp > 0.f) sv = fminf(fmaxf(sv, -a.logit_clamp), a.logit_clamp);
+        sv = (nt * 16 + 4 * g + r < a.N) ? sv : -INFINITY;
+        acc[nt][r] = sv;
+        mx = fmaxf(mx, sv);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    float sum = 0.f;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float e = __expf(acc[nt][r] - mx);
+        acc[nt][r] = e;
+        sum += e;
+      }
+    sum += __shfl_xor(sum, 16, 64);
+    sum += __shfl_xor(sum, 32, 64);
+    const float inv = m < a.M ? 1.f / (sum + a.denom_eps) : 0.f;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float pv = acc[nt][r] * inv;
+        rs[nt][r] += pv;
+        sp[(nt * 16 + 4 * g + r) * PP + m] = A::fromf(pv);
+      }
+  }
+  // per-slot sums over this wave's tokens (the 16 lanes of a lane group hold 16 tokens)
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v = rs[nt][r];
+      v += __shfl_xor(v, 1, 64);
+      v += __shfl_xor(v, 2, 64);
+      v += __shfl_xor(v, 4, 64);
+      v += __shfl_xor(v, 8, 64);
+      if (li == 0) srs[wid * NS + nt * 16 + 4 * g + r] = v;
+    }
+  __syncthreads();
+  // ---- phase 2: this wave's column tiles
+  const bool renorm = a.renorm_eps >= 0.f;
+  float rinv[NT][4];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float t = (float)a.M * a.renorm_eps;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) t += srs[w * NS + nt * 16 + 4 * g + r];
+      rinv[nt][r] = renorm ? 1.f / t : 1.f;
+    }
+#pragma unroll
+  for (int c = 0; c < CTW; ++c) {
+    const int ct = wid + NW * c;
+    if (ct >= NCT) break;
+    const int d = blockIdx.y * (DD / NCB) + ct * 16 + li;
+    f32x4 acc[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float cs = 0.f;
+#pragma unroll
+    for (int i = 0; i < VB; ++i) {
+      if (i >= NVB) break;
+      const int m0 = 32 * i;
+      uint4 raw = vr[c][i];
+      if (m0 + 32 > a.M) {   // tokens past M: v^T columns are not initialised, zero them
+        TT e[8];
+        *reinterpret_cast<uint4*>(e) = raw;
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj)
+          if (m0 + 8 * g + jj >= a.M) e[jj] = A::fromf(0.f);
+        raw = *reinterpret_cast<uint4*>(e);
+      }
+      if (renorm) {
+        TT e[8];
+        *reinterpret_cast<uint4*>(e) = raw;
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) cs += A::tof(e[jj]);
+      }
+      const typename A::Op bv = __builtin_bit_cast(typename A::Op, raw);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) acc[nt] = A::mfma(A::load(sp + (nt * 16 + li) * PP + m0 + 8 * g), bv, acc[nt]);
+    }
+    cs += __shfl_xor(cs, 16, 64);
+    cs += __shfl_xor(cs, 32, 64);
+    const float epsv = renorm ? a.renorm_eps * cs : 0.f;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int n = nt * 16 + 4 * g + r;
+        if (n < a.N) out[b * a.ob + (int64_t)n * a.ldo + d] = A::fromf((acc[nt][r] + epsv) * rinv[nt][r]);
+      }
+  }
+}
+
+static size_t core_fused_lds(int NT, int64_t D, int64_t Mp, int esize) {
+  return ((size_t)NT * 16 * (D + 8) + (size_t)NT * 16 * (Mp + 8)) * esize + (size_t)CF_WAVES * NT * 16 * 4;
+}
+
 static bool al16(const void* p) { return (((uintptr_t)p) & 15) == 0; }
 
 static size_t core_ws_bytes(int64_t B, int64_t N, int64_t M, int esize) {
@@ -1247,6 +1447,43 @@ static int launch_core(const void* q, int64_t ldq, int64_t qbs, const void* k, i
   HCLSM_CORE(HCLSM_F32, HCLSM_F32)
 #undef HCLSM_CORE
   return HCLSM_ERR_DTYPE;
+}
+
+// The fused core (16-bit operands, v transposed) when the shape fits its instantiations; 1 otherwise.  Column
+// blocks per frame: 128-column blocks for D = 384 / 256, one block for D = 192 / 128.
+static int launch_core_fused(const void* q, int64_t ldq, int64_t qbs, const void* k, int64_t ldk, int64_t kbs,
+                             const void* vt, int64_t vbs, void* out, int64_t ldo, int64_t obs, int64_t B, int64_t N,
+                             int64_t M, int64_t D, float scale, float denom_eps, float logit_clamp, float renorm_eps,
+                             int dtype, hipStream_t st) {
+  if (dtype != HCLSM_BF16 && dtype != HCLSM_F16) return 1;
+  if (N < 1 || N > 32 || M < 1 || M > CF_MAXM || (D != 128 && D != 192 && D != 256 && D != 384)) return 1;
+  if (B > 65535) return 1;
+  const int NT = N <= 16 ? 1 : 2;
+  const int64_t Mp = (M + 31) / 32 * 32;
+  const size_t lds = core_fused_lds(NT, D, Mp, 2);
+  if (lds > 64 * 1024) return 1;
+  CoreArgs a;
+  a.ldq = ldq; a.ldk = ldk; a.ldv = 0; a.ldo = ldo;
+  a.qb = qbs; a.kb = kbs; a.vb = vbs; a.ob = obs;
+  a.N = (int)N; a.M = (int)M; a.D = (int)D;
+  a.NT = NT;
+  a.MT = (int)((M + 15) / 16);
+  a.scale = scale; a.denom_eps = denom_eps; a.logit_clamp = logit_clamp; a.renorm_eps = renorm_eps;
+#define HCLSM_CF(DT_, NT_, DD_, NCB_)                                                                           \
+  if (dtype == DT_ && NT == NT_ && D == DD_) {                                                                 \
+    hipLaunchKernelGGL((core_fused_t_kernel<DT_, NT_, DD_, NCB_>), dim3((unsigned)B, NCB_), dim3(64 * CF_WAVES), \
+                       lds, st, (const MM<DT_>::T*)q, (const MM<DT_>::T*)k, (const MM<DT_>::T*)vt, Mp,           \
+                       (MM<DT_>::T*)out, a);                                                                   \
+    HCLSM_LAUNCH_CHECK();                                                                                      \
+    return 0;                                                                                                  \
+  }
+#define HCLSM_CF_D(DT_, NT_) \
+  HCLSM_CF(DT_, NT_, 128, 1) HCLSM_CF(DT_, NT_, 192, 1) HCLSM_CF(DT_, NT_, 256, 2) HCLSM_CF(DT_, NT_, 384, 3)
+  HCLSM_CF_D(HCLSM_BF16, 1) HCLSM_CF_D(HCLSM_BF16, 2)
+  HCLSM_CF_D(HCLSM_F16, 1) HCLSM_CF_D(HCLSM_F16, 2)
+#undef HCLSM_CF_D
+#undef HCLSM_CF
+  return 1;
 }
 
 static int check_core(const void* q, int64_t ldq, int64_t qbs, const void* k, int64_t ldk, int64_t kbs, int64_t B,
@@ -1750,9 +1987,13 @@ static int slot_iteration_impl(const HclsmSlotWeights* W, const float* slots_in,
   rc = linear_impl(xn, d, dtype, W->w_q, d, nullptr, nullptr, 0, q, d, dtype, nullptr, 0, rows, d, d, 0, 0.f, 0,
                    nullptr, nullptr, 0.f, dtype, st);
   if (rc) return rc;
-  // updates = attention core (logits, softmax over slots, [renorm], attn v)
-  rc = launch_core(q, d, N * d, k, ldk, k_bstride, v, ldv, v_bstride, upd, d, N * d, nullptr, dtype, B, N, M, d,
-                   scale, 0.f, logit_clamp, renorm_eps, dtype, ws + L.core, st, v_transposed);
+  // updates = attention core (logits, softmax over slots, [renorm], attn v): one fused launch when v is transposed
+  rc = v_transposed ? launch_core_fused(q, d, N * d, k, ldk, k_bstride, v, v_bstride, upd, d, N * d, B, N, M, d, scale,
+                                        0.f, logit_clamp, renorm_eps, dtype, st)
+                    : 1;
+  if (rc == 1)
+    rc = launch_core(q, d, N * d, k, ldk, k_bstride, v, ldv, v_bstride, upd, d, N * d, nullptr, dtype, B, N, M, d,
+                     scale, 0.f, logit_clamp, renorm_eps, dtype, ws + L.core, st, v_transposed);
   if (rc) return rc;
   // h = GRUCell(updates, slots)
   rc = gru_impl(upd, d, sb, d, slots_in, d, W->w_ih, W->w_hh, W->b_ih, W->b_hh, h, d, nullptr, 0, rows, d, d, dtype,

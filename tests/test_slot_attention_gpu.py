@@ -188,6 +188,36 @@ def test_forward_two_launch_iteration_matches_oracle(mode_name, dtype, B, N, M, 
     assert err <= 2e-2, f"{mode_name} {dtype}: {err:.3e}"
 
 
+@pytest.mark.parametrize("mode_name,dtype,B,N,M,d", [
+    ("config2", torch.bfloat16, 3, 32, 196, 384),    # config 2's per-frame shape: 3 column blocks of 128
+    ("reference", torch.bfloat16, 2, 5, 1, 384),     # one token, a partial slot tile
+    ("config2", torch.float16, 2, 16, 256, 256),     # the longest token count the fused core takes
+    ("reference", torch.bfloat16, 4, 17, 31, 192),   # one column block, two slot tiles, ragged tokens
+    ("config2", torch.bfloat16, 2, 32, 257, 128),    # past the fused core's token limit: the two-launch core
+])
+def test_fused_attention_core_shapes(mode_name, dtype, B, N, M, d):
+    """The iteration's attention core (one launch per iteration for 16-bit operands, N <= 32, M <= 256,
+    d in {128, 192, 256, 384}) inside the forward, against the oracle."""
+    from hclsm_amd.kernels import slot_iteration as si
+    from hclsm_amd.workloads import xavier_uniform
+    g = torch.Generator().manual_seed(B * 1000 + N * 10 + M)
+    w = _weights(d, 2 * d, seed=N + d)
+    w["w_k"] = xavier_uniform((d, d), g)
+    w["w_v"] = xavier_uniform((d, d), g)
+    w["ln_in_w"] = torch.ones(d)
+    w["ln_in_b"] = torch.zeros(d)
+    w = {n: t.to(dtype).float() if n in si._WEIGHT_KEYS else t for n, t in w.items()}
+    W = si.SlotWeights.from_dict(w, dtype)
+    tokens = torch.randn(B, M, d, generator=g)
+    slots0 = torch.randn(B, N, d, generator=g) * 0.5
+    mode = si.REFERENCE_MODE if mode_name == "reference" else si.CONFIG2_MODE
+    out = si.slot_attention_forward(tokens.cuda(), slots0.cuda(), W, 2, mode)
+    ref = sa.slot_attention_forward(tokens.numpy(), slots0.numpy(), {n: _np(t) for n, t in w.items()}, 2,
+                                    logit_clamp=mode.logit_clamp, renorm_eps=mode.renorm_eps, slot_clamp=mode.slot_clamp)
+    err = normwise_rel_err(_np(out), ref)
+    assert err <= 2e-2, f"{mode_name} {dtype} N={N} M={M} d={d}: {err:.3e}"
+
+
 @pytest.mark.parametrize("dtype,tol", [(torch.bfloat16, 2e-2), (torch.float16, 2e-2)])
 def test_large_linear_lds_tiles(dtype, tol):
     """hclsm_linear at a size that takes the LDS-staged 64x64-tile kernel (>= 2048 32x32 tiles), with
