@@ -432,11 +432,19 @@ static int launch_scan_sgpr(const void* x, const void* dt, const float* A_log, c
 //   A operand (lane l: k = 4*(l/32) .. +3 of row l%32) = (b_s, b_s, 0, 0) with
 //   s = s(row), when the row's half c(row) matches the lane's k half, else 0.
 // Both products are exact in fp32, so the state keeps fp32 accuracy; the
-// matrix core replaces one multiply and turns the FMA into a multiply, which
-// lowers the VALU work per state update from ~5.4 to ~4.4 instructions on
-// this VALU-bound loop.  Each lane needs b_s for a lane-dependent s, so the B
-// row is read with a per-lane 2-byte load; the C row is uniform and goes
-// through scalar loads.
+// matrix core replaces one multiply and turns the FMA into a multiply.  Each
+// lane needs b_s for a lane-dependent s, so the B row is read with a per-lane
+// 2-byte load; the C row is uniform and goes through scalar loads, unpacked on
+// the scalar unit.
+//
+// The loop is bound by VALU issue: per state update one multiply for the
+// exponent, one v_exp_f32 (about three FMA issue slots on gfx950), one
+// multiply for the decay and one FMA for the readout.  The gates of step t+1
+// are computed between the state update of step t and its readout, so the
+// exponentials cover the matrix-core latency and no exp result is consumed
+// by the next instruction.  Moving the readout onto the matrix core (bf16 h,
+// two 16x16x32 products per channel) issues fewer VALU instructions but ran
+// slower here, as did one barrier-synchronised workgroup per CU.
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
@@ -462,7 +470,7 @@ ssm_scan_fwd_mfma_kernel(const uint16_t* __restrict__ x, const uint16_t* __restr
   for (int k = 0; k < DPL; ++k) {
 #pragma unroll
     for (int s = 0; s < SP; ++s) {
-      float e = expf(A_log[(size_t)(d0 + k) * SP + s]);
+      float e = fast_exp2(A_log[(size_t)(d0 + k) * SP + s] * HCLSM_LOG2E);
       if (MODE != HCLSM_SCAN_RAW) e = fminf(fmaxf(e, 1e-6f), 1.0f);
       a2[k][s] = -e * HCLSM_LOG2E;
     }
@@ -520,33 +528,53 @@ ssm_scan_fwd_mfma_kernel(const uint16_t* __restrict__ x, const uint16_t* __restr
 #pragma unroll
   for (int i = 0; i < 8; ++i) cw[i] = cw0[i];
 
-  auto step = [&](int t, uint32_t xw, uint32_t dw, uint16_t bb, uint32_t gw) {
+  // Gates are computed one step ahead, between the state update of step t and its readout, so the
+  // exponentials fill the matrix-core latency of the update and each exp result is consumed a step later.
+  float gt[DPL][SP];
+  float dtc[DPL];
+  auto gates = [&](uint32_t dw) {
+#pragma unroll
+    for (int k = 0; k < DPL; ++k) {
+      dtc[k] = scan_dt<MODE>(__uint_as_float(k == 0 ? dw << 16 : dw & 0xffff0000u));
+#pragma unroll
+      for (int s = 0; s < SP; ++s) gt[k][s] = dtc[k] * a2[k][s];
+#pragma unroll
+      for (int s = 0; s < SP; ++s) gt[k][s] = fast_exp2(gt[k][s]);
+    }
+  };
+
+  auto step = [&](int t, uint32_t xw, uint32_t dw_next, uint16_t bb, uint32_t gw) {
     const int tn = t + 1 < T ? t + 1 : T - 1;
     uint32_t cwn[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) cwn[i] = cw0[(size_t)tn * 8 + i];
     const short ab = a_on ? (short)bb : (short)0;
     const s16x4_t aop = {ab, ab, 0, 0};
-    float yo[DPL];
+    float xs[DPL];
 #pragma unroll
     for (int k = 0; k < DPL; ++k) {
-      const float xs = __uint_as_float(k == 0 ? xw << 16 : xw & 0xffff0000u);
-      float dtv = __uint_as_float(k == 0 ? dw << 16 : dw & 0xffff0000u);
-      dtv = scan_dt<MODE>(dtv);
-      const float u = dtv * xs;
+      xs[k] = __uint_as_float(k == 0 ? xw << 16 : xw & 0xffff0000u);
+      const float u = dtc[k] * xs[k];
       const uint32_t uhi = __float_as_uint(u) & 0xffff0000u;
       const float ulo = u - __uint_as_float(uhi);
       const s16x4_t bop = {(short)(uhi >> 16), (short)(__float_as_uint(ulo) >> 16), 0, 0};
 #pragma unroll
-      for (int s = 0; s < SP; ++s) h[k][s] *= fast_exp2(dtv * a2[k][s]);
+      for (int s = 0; s < SP; ++s) h[k][s] *= gt[k][s];
       h[k] = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(aop, bop, h[k], 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    gates(dw_next);
+    __builtin_amdgcn_sched_barrier(0);
+    float yo[DPL];
+#pragma unroll
+    for (int k = 0; k < DPL; ++k) {
       float y0 = 0.f, y1 = 0.f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         y0 = fmaf(h[k][2 * i], __uint_as_float(cw[i] << 16), y0);
         y1 = fmaf(h[k][2 * i + 1], __uint_as_float(cw[i] & 0xffff0000u), y1);
       }
-      yo[k] = fmaf(dsk[k], xs, y0 + y1);
+      yo[k] = fmaf(dsk[k], xs[k], y0 + y1);
     }
     if constexpr (MODE == SCAN_BLOCK) {
       if constexpr (DPL == 2)
@@ -565,13 +593,14 @@ ssm_scan_fwd_mfma_kernel(const uint16_t* __restrict__ x, const uint16_t* __restr
   };
 
   load(0, xv, dv, bv, gv);
+  gates(dv[0]);
   const int tfull = T - T % TC;
   for (int t0 = 0; t0 < tfull; t0 += TC) {
     uint32_t xn[TC], dn[TC], gn[GC];
     uint16_t bn[TC];
     load(t0 + TC, xn, dn, bn, gn);
 #pragma unroll
-    for (int j = 0; j < TC; ++j) step(t0 + j, xv[j], dv[j], bv[j], gv[j < GC ? j : 0]);
+    for (int j = 0; j < TC; ++j) step(t0 + j, xv[j], j + 1 < TC ? dv[j + 1] : dn[0], bv[j], gv[j < GC ? j : 0]);
 #pragma unroll
     for (int j = 0; j < TC; ++j) { xv[j] = xn[j]; dv[j] = dn[j]; bv[j] = bn[j]; }
 #pragma unroll
@@ -579,7 +608,7 @@ ssm_scan_fwd_mfma_kernel(const uint16_t* __restrict__ x, const uint16_t* __restr
   }
 #pragma unroll
   for (int j = 0; j < TC - 1; ++j)
-    if (tfull + j < T) step(tfull + j, xv[j], dv[j], bv[j], gv[j < GC ? j : 0]);
+    if (tfull + j < T) step(tfull + j, xv[j], dv[j + 1], bv[j], gv[j < GC ? j : 0]);
 
   if (h_final != nullptr && act) {
 #pragma unroll
