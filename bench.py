@@ -31,6 +31,8 @@ sys.path.insert(0, ROOT)
 METRIC = "SSM scan GB/s (% of HBM peak) + slot-attn/event-attn tokens/s, small preset, 1 GPU"
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+MI355X_SIMDS = 1024          # 256 CUs x 4 SIMDs
+PEAK_CLOCK_GHZ = 2.4
 NSETS = 4
 
 
@@ -47,14 +49,32 @@ def _parse():
     return p.parse_args()
 
 
-def _traffic_from_profile():
-    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if present."""
-    path = os.path.join(ROOT, "profiles", "ssm_scan_cfg1_traffic.json")
+def _scan_counters():
+    """Per-launch rocprofv3 counters of the config-1 scan (HBM traffic, VALU instructions) from the committed
+    summary of the counter passes over this bench, if present."""
+    path = os.path.join(ROOT, "profiles", "ssm_scan_fwd_counters.json")
     try:
         with open(path) as f:
-            return json.load(f).get("hbm_bytes_per_launch")
+            return json.load(f)
     except (OSError, ValueError):
+        return {}
+
+
+def _valu_roofline(ctr, avg_s):
+    """The scan is VALU-issue bound.  SQ_ACTIVE_INST_VALU counts VALU activity in units of four cycles
+    (rocprofv3's VALUBusy = 400 * SQ_ACTIVE_INST_VALU / SIMDs / cycles); per SIMD and launch that is the
+    busy time the instruction stream needs, priced here against the measured launch time at the peak
+    engine clock: frac = busy cycles per SIMD / (launch seconds x 2.4 GHz)."""
+    if not ctr.get("sq_active_inst_valu_per_launch"):
         return None
+    busy = ctr["sq_active_inst_valu_per_launch"] * 4 / MI355X_SIMDS
+    ach = busy / avg_s / 1e9
+    return {"bound": "valu", "achieved": round(ach, 4), "peak": PEAK_CLOCK_GHZ,
+            "unit": "G VALU-busy cycles/s per SIMD", "frac": round(ach / PEAK_CLOCK_GHZ, 4),
+            "valu_busy_cycles_per_simd": round(busy, 1),
+            "valu_instr_per_launch": ctr["valu_instr_per_launch"],
+            "trans_instr_per_launch": ctr["trans_instr_per_launch"],
+            "counter_valu_busy_pct": ctr.get("valu_busy_pct"), "source": ctr.get("source")}
 
 
 def _cpu_threads():
@@ -143,7 +163,7 @@ def _bench_slot(dev, n, warmup, cpu):
 def _bench_events(dev, n, warmup, cpu):
     """Config 3: event index + per-track causal attention, 1024 tracks x T=64, 6 x 64 heads, p=0.15."""
     import torch
-    from hclsm_amd.kernels.event_attention import event_attention
+    from hclsm_amd.kernels.event_attention import track_causal_event_attention
     from hclsm_amd.kernels.sparse_event_attn import build_event_index
     g = torch.Generator().manual_seed(1003)
     q, k, v = (torch.randn(1024, 64, 6, 64, generator=g).to(torch.bfloat16).to(dev) for _ in range(3))
@@ -153,12 +173,11 @@ def _bench_events(dev, n, warmup, cpu):
     total = build_event_index(m).total()
 
     def step():
-        idx = build_event_index(m)
-        event_attention(q, k, v, idx, capacity=total)
+        track_causal_event_attention(q, k, v, m, capacity=total)
     med, avg = _event_timing(step, n, warmup)
     nbytes = total * 6 * 64 * 2 * 4 + m.numel() * 4 + (1025 + 2 * total + 2 * 65536) * 4
     res = {"workload": "config 3: 1024 tracks x T=64, 6 heads x 64, p=0.15 (t=0 forced), bf16, "
-                        "index build + causal event attention, packed output",
+                        "index build + causal event attention, packed output (one library call)",
             "events": total, "metric": "event-tokens/s", "value": round(total / med, 1),
             "grid_tokens_per_s": round(65536 / med, 1), "median_us": round(med * 1e6, 2),
             "roofline": {"bound": "hbm", "achieved": round(nbytes / med / 1e9, 2), "peak": HBM_PEAK_GBS,
@@ -395,25 +414,46 @@ def _bench_track(dev, n, warmup):
                                  "MLP's flops"}}
 
 
-def _bench_chain(dev, n, warmup):
+def _bench_scan_context(dev, n, warmup):
+    """The reference's published scan shapes (docs/benchmarks.md:16-19: T4, Triton 0.16 / 1.83 ms,
+    sequential loop 6.22 / 69.64 ms), drawn as scripts/benchmark_kernels.py:132-136 draws them (fp32:
+    x ~ N(0,1), dt ~ U(0,1) + 0.01, A_log, B, C ~ N(0,1)) and timed the same way (events around each
+    ssm_scan_fn call, default backend).  Context only: other hardware, and not this bench's metric."""
+    import torch
+    from hclsm_amd.kernels import ssm_scan_fn
+    rows = []
+    for name, BN, T, Dn, S, t4_triton, t4_seq in (("tiny", 128, 16, 256, 32, 0.16, 6.22),
+                                                  ("base", 512, 16, 512, 64, 1.83, 69.64)):
+        g = torch.Generator(device=dev).manual_seed(7)
+        x = torch.randn(BN, T, Dn, generator=g, device=dev)
+        dt = torch.rand(BN, T, Dn, generator=g, device=dev).abs() + 0.01
+        A_log = torch.randn(Dn, S, generator=g, device=dev)
+        Bp = torch.randn(BN, T, S, generator=g, device=dev)
+        C = torch.randn(BN, T, S, generator=g, device=dev)
+        med, avg = _event_timing(lambda: ssm_scan_fn(x, dt, A_log, Bp, C), n, warmup)
+        rows.append({"config": name, "shape": {"BN": BN, "T": T, "d_inner": Dn, "d_state": S}, "dtype": "f32",
+                     "ms_per_call": round(med * 1e3, 4), "mean_ms": round(avg * 1e3, 4),
+                     "reference_published_ms": {"triton_t4": t4_triton, "sequential_t4": t4_seq}})
+    return rows
+
+
+def _bench_chain(dev, n, warmup, cpu):
     """Config 4: four chained scans at (1024, 1024, 768), S=16, bf16 (each fed the previous output),
-    then the event index of a p=0.05 mask (t=0 forced) and causal event attention, 12 heads x 64."""
+    then the event index of a p=0.05 mask (t=0 forced) and causal event attention, 12 heads x 64
+    (hclsm_amd.workloads.chain_config's draw)."""
     import torch
     from hclsm_amd import _lib
-    from hclsm_amd.kernels.event_attention import event_attention
+    from hclsm_amd.kernels.event_attention import track_causal_event_attention
     from hclsm_amd.kernels.sparse_event_attn import build_event_index
-    from hclsm_amd.workloads import scan_algorithmic_bytes
+    from hclsm_amd.workloads import chain_config, scan_algorithmic_bytes
     from oracle.ssm_scan import normwise_rel_err, ssm_scan_ref
     L = _lib.lib()
-    N, T, Dn, S = 1024, 1024, 768, 16
-    g = torch.Generator(device=dev).manual_seed(1004)
-    bf = torch.bfloat16
-    x0 = torch.randn(N, T, Dn, generator=g, device=dev).to(bf)
-    dt = torch.nn.functional.softplus(-2 + 0.5 * torch.randn(N, T, Dn, generator=g, device=dev)).to(bf)
-    A_log = torch.rand(Dn, S, generator=g, device=dev) * float(torch.log(torch.tensor(16.0)))
-    Bm = (torch.randn(N, T, S, generator=g, device=dev) / 4).to(bf)
-    Cm = (torch.randn(N, T, S, generator=g, device=dev) / 4).to(bf)
-    Dv = torch.randn(Dn, generator=g, device=dev)
+    c = chain_config(dev)
+    x0, dt, A_log, Bm, Cm, Dv, m = (c[k] for k in ("x", "dt", "A_log", "B", "C", "D", "mask"))
+    q, k, v = c["q"], c["k"], c["v"]
+    N, T, Dn = x0.shape
+    S = Bm.shape[2]
+    H, dh = q.shape[2], q.shape[3]
     ys = [torch.empty_like(x0), torch.empty_like(x0)]
     stream = torch.cuda.current_stream(dev).cuda_stream
 
@@ -429,14 +469,10 @@ def _bench_chain(dev, n, warmup):
         scan(ys[1], ys[0])
         scan(ys[0], ys[1])
 
-    m = (torch.rand(N, T, generator=g, device=dev) < 0.05).float()
-    m[:, 0] = 1
-    H, dh = 12, 64
-    q, k, v = (torch.randn(N, T, H, dh, generator=g, device=dev).to(bf) for _ in range(3))
     total = build_event_index(m).total()
 
     def attn():
-        event_attention(q, k, v, build_event_index(m), capacity=total)
+        track_causal_event_attention(q, k, v, m, capacity=total)
 
     # parity spot check of the first scan on 2 sequences
     scan(x0, ys[0])
@@ -449,14 +485,38 @@ def _bench_chain(dev, n, warmup):
     s_med, _ = _event_timing(scans, n, warmup)
     a_med, _ = _event_timing(attn, n, warmup)
     sb = scan_algorithmic_bytes(N, T, Dn, S, 2)
+    # q, k, v read and o written once per event; the mask; the index tables (offsets, packed indices and
+    # positions, the two (N, T) maps)
     ab = total * H * dh * 2 * 4 + m.numel() * 4 + (N + 1 + 2 * total + 2 * N * T) * 4
-    return {"workload": "config 4: 4 chained scans (1024 seq x T=1024 x 768, S=16, bf16, raw + skip), then "
-                        "index + causal event attention (p=0.05, t=0 forced, 12 heads x 64, packed output)",
-            "chain_ms": round((s_med + a_med) * 1e3, 4), "scan_us_each": round(s_med / 4 * 1e6, 1),
-            "scan_gbs": round(4 * sb / s_med / 1e9, 1), "scan_frac": round(4 * sb / s_med / 1e9 / HBM_PEAK_GBS, 4),
-            "scan_bytes_each": sb, "events": total, "attn_us": round(a_med * 1e6, 2),
-            "event_tokens_per_s": round(total / a_med, 1), "attn_gbs": round(ab / a_med / 1e9, 1),
-            "scan_parity_normwise_err": err}
+    res = {"workload": "config 4: 4 chained scans (1024 seq x T=1024 x 768, S=16, bf16, raw + skip), then "
+                       "index + causal event attention (p=0.05, t=0 forced, 12 heads x 64, packed output)",
+           "metric": "chain ms (lower is better)", "chain_ms": round((s_med + a_med) * 1e3, 4),
+           "scan_us_each": round(s_med / 4 * 1e6, 1), "scan_bytes_each": sb, "events": total,
+           "attn_us": round(a_med * 1e6, 2), "event_tokens_per_s": round(total / a_med, 1),
+           "scan_roofline": {"bound": "hbm", "achieved": round(4 * sb / s_med / 1e9, 2), "peak": HBM_PEAK_GBS,
+                             "unit": "GB/s", "frac": round(4 * sb / s_med / 1e9 / HBM_PEAK_GBS, 4),
+                             "bytes_per_call": sb, "kernel": "ssm_scan_fwd_mfma_kernel<raw,TC=8,DPL=2>"},
+           "attn_roofline": {"bound": "hbm", "achieved": round(ab / a_med / 1e9, 2), "peak": HBM_PEAK_GBS,
+                             "unit": "GB/s", "frac": round(ab / a_med / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_call": ab,
+                             "kernel": "event_attn_kernel<bf16, causal per track> + index build"},
+           "scan_parity_normwise_err": err}
+    if cpu:
+        from oracle.torch_cpu import event_attention_torch, scan_torch
+        cores, model = _cpu_threads()
+        tp = 64
+        xc, dtc, Bc, Cc = (t[:, :tp].cpu() for t in (x0, dt, Bm, Cm))
+        Ac, Dc = A_log.cpu(), Dv.cpu()
+        t_scan = _cpu_time(lambda: scan_torch(xc, dtc, Ac, Bc, Cc, D=Dc, clamp_mode="raw"), 1)
+        qc, kc, vc, mc = (t.cpu() for t in (q, k, v, m))
+        t_attn = _cpu_time(lambda: event_attention_torch(qc, kc, vc, mc), 1)
+        chain_s = 4 * t_scan * (T / tp) + t_attn
+        res["cpu_baseline"] = {
+            "value": round(chain_s * 1e3, 1), "unit": "ms per chain (extrapolated)", "cores": cores, "kind": "port",
+            "sample": f"one scan over the first {tp} of {T} steps of the 1024 x 768 input (the reference's sequential "
+                      f"loop as torch CPU ops, oracle/torch_cpu.py): {t_scan:.3f} s, extrapolated linearly in T to "
+                      f"4 scans of {T} steps; the event attention (per-track nonzero gather + causal SDPA, "
+                      f"oracle/torch_cpu.py) on the full config: {t_attn:.3f} s; {cores} threads on {model}"}
+    return res
 
 
 def main():
@@ -535,6 +595,7 @@ def main():
         del src, dst
 
     achieved = nbytes / avg / 1e9
+    ctr = _scan_counters()
     out = {
         "metric": METRIC,
         "value": round(nbytes * args.steps / wall / 1e9, 2),
@@ -553,17 +614,20 @@ def main():
                    "io_dtype": "bf16", "input_sets_rotated": NSETS,
                    "algorithmic_bytes_per_step": nbytes, "parity_normwise_err": err},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic_from_profile(),
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": ctr.get("hbm_bytes_per_launch"),
+                     "traffic_source": ctr.get("source"),
                      "kernel": "ssm_scan_fwd_mfma_kernel<raw,TC=8,DPL=2>",
                      "avg_launch_us": round(avg * 1e6, 3), "median_launch_us": round(med * 1e6, 3),
                      "p10_launch_us": round(p10 * 1e6, 3), "p90_launch_us": round(p90 * 1e6, 3)},
+        "roofline_valu": _valu_roofline(ctr, avg),
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = _cpu_baseline(d)
     if not args.no_extra:
         out["slot_attn"] = _bench_slot(dev, 100, 10, not args.no_cpu_baseline)
         out["event_attn"] = _bench_events(dev, 100, 10, not args.no_cpu_baseline)
-        out["chain"] = _bench_chain(dev, 20, 3)
+        out["chain"] = _bench_chain(dev, 20, 3, not args.no_cpu_baseline)
+        out["scan_context"] = _bench_scan_context(dev, 30, 10)
         out["block_scan"] = _bench_block_scan(dev, 50, 5)
         out["scan_bwd"] = _bench_scan_bwd(dev, 50, 5)
         out["level1"] = _bench_level1(dev, 30, 3)

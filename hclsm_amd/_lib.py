@@ -42,6 +42,7 @@ _SIGNATURES: dict[str, list] = {
     "hclsm_event_top_down": [_c_void_p] * 4 + [_i64, _c_void_p, _i64, _i64] + [_c_void_p] * 4 + [_i64] +
                             [_c_void_p] * 2 + [_i64] * 4 + [_int, _c_void_p, _i64, _c_void_p],
     "hclsm_event_attention": [_c_void_p] * 8 + [_i64] * 5 + [_f32, _int, _int, _c_void_p],
+    "hclsm_track_causal_attention": [_c_void_p, _int, _int] + [_c_void_p] * 4 + [_i64] * 5 + [_f32, _int, _c_void_p, _c_void_p],
     "hclsm_layer_norm": [_c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _f32, _int, _int,
                          _c_void_p],
     "hclsm_linear": [_c_void_p, _i64, _int, _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _c_void_p, _i64, _int,

@@ -102,13 +102,26 @@ struct AttnExt {
   const int32_t* seg_rows;
 };
 
+// MODE 3 (track-causal, packed output, index built in the launch): track p's events are read from row p of
+// the mask (rule as hclsm_event_index), its packed offset is the sum of counts[0, p) (row counts from an
+// earlier launch), and the head-0 wave of each track writes the track's part of the index tables
+// (offsets, indices, rows, slot_of); wave 0 also writes stats {total, largest count} and offsets[nseg].
+struct AttnIdx {
+  const void* mask;
+  int mask_dtype, rule;
+  const int32_t* counts;
+  int32_t *offsets, *indices, *rows, *slot_of, *stats;
+};
+constexpr int ATTN_IDX_TMAX = 1024;   // MODE 3: timesteps per track held in LDS
+
 template <int DT, int DH, int MODE>
 __global__ void __launch_bounds__(64 * ATTN_WAVES)
 event_attn_kernel(const typename AttnT<DT>::T* __restrict__ q, const typename AttnT<DT>::T* __restrict__ k,
                   const typename AttnT<DT>::T* __restrict__ v, typename AttnT<DT>::T* __restrict__ out_packed,
                   typename AttnT<DT>::T* __restrict__ out_grid, const int32_t* __restrict__ offsets,
                   const int32_t* __restrict__ indices, const uint8_t* __restrict__ key_pad,
-                  int64_t nseg, int64_t T, int H, int64_t capacity, float scale_log2, AttnExt ex) {
+                  int64_t nseg, int64_t T, int H, int64_t capacity, float scale_log2, AttnExt ex,
+                  AttnIdx ix) {
   using A = AttnT<DT>;
   using TT = typename A::T;
   constexpr int QD = DH / 4;          // contiguous head columns per lane
@@ -118,13 +131,70 @@ event_attn_kernel(const typename AttnT<DT>::T* __restrict__ q, const typename At
   static_assert(DH % 16 == 0, "head dim must be a multiple of 16");
 
   const int64_t wave = (int64_t)blockIdx.x * ATTN_WAVES + (threadIdx.x >> 6);
+  __shared__ int32_t s_idx[MODE == 3 ? ATTN_WAVES * ATTN_IDX_TMAX : 1];
   if (wave >= nseg * H) return;  // whole wave exits
   const int64_t p = wave / H;
   const int h = (int)(wave - p * H);
   const int lane = threadIdx.x & 63, g = lane >> 4, li = lane & 15;
   int64_t base;
   int L;
-  if constexpr (MODE == 2) {
+  int32_t* sidx = s_idx + (MODE == 3 ? (threadIdx.x >> 6) * ATTN_IDX_TMAX : 0);
+  if constexpr (MODE == 3) {
+    // events of row p, ascending, into this wave's LDS list (the head-0 wave also fills the tables)
+    const bool hw = h == 0;
+    int run = 0;
+    for (int64_t t0 = 0; t0 < T; t0 += 64) {
+      const int64_t t = t0 + lane;
+      const bool ev = t < T && is_event(ix.mask, ix.mask_dtype, p * T + (t < T ? t : T - 1), ix.rule);
+      const uint64_t bal = __ballot(ev);
+      const int r = run + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                        __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+      if (ev) sidx[r] = (int32_t)t;
+      if (hw && t < T && ix.slot_of) ix.slot_of[p * T + t] = ev ? r : -1;
+      run += __popcll(bal);
+    }
+    // packed offset: events of rows 0 .. p-1
+    int32_t pre = 0;
+    for (int64_t i0 = lane; i0 < p; i0 += 64 * 8) {
+      int32_t c[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) c[u] = i0 + 64 * u < p ? ix.counts[i0 + 64 * u] : 0;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) pre += c[u];
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) pre += __shfl_xor(pre, o, 64);
+    base = pre;
+    L = run;
+    __builtin_amdgcn_wave_barrier();   // the list is read back by other lanes of this wave
+    if (hw) {
+      for (int e = lane; e < L; e += 64) {
+        ix.indices[pre + e] = sidx[e];
+        if (ix.rows) ix.rows[pre + e] = (int32_t)p;
+      }
+      if (lane == 0) {
+        ix.offsets[p] = pre;
+        if (p == nseg - 1) ix.offsets[nseg] = pre + L;
+      }
+    }
+    if (wave == 0) {   // totals over every row
+      int32_t tot = 0, mx = 0;
+      for (int64_t i0 = lane; i0 < nseg; i0 += 64 * 8) {
+        int32_t c[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) c[u] = i0 + 64 * u < nseg ? ix.counts[i0 + 64 * u] : 0;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) { tot += c[u]; mx = c[u] > mx ? c[u] : mx; }
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        tot += __shfl_xor(tot, o, 64);
+        const int u = __shfl_xor(mx, o, 64);
+        mx = u > mx ? u : mx;
+      }
+      if (lane == 0) { ix.stats[0] = tot; ix.stats[1] = mx; }
+    }
+  } else if constexpr (MODE == 2) {
     if (p >= *ex.nseg_dev) return;
     base = p * T;
     L = (int)T;
@@ -138,7 +208,7 @@ event_attn_kernel(const typename AttnT<DT>::T* __restrict__ q, const typename At
   auto row_ptr = [&](const TT* t, int i) -> const TT* {
     const int ic = i < L ? i : L - 1;  // clamp: always a valid row of this segment
     if constexpr (MODE == 2) return t + (base + ic) * ldi + (int64_t)h * DH;
-    int64_t tr = indices[base + ic];
+    int64_t tr = MODE == 3 ? sidx[ic] : indices[base + ic];
     tr = tr < 0 ? 0 : (tr >= T ? T - 1 : tr);
     return t + ((int64_t)p * T + tr) * rstride + (int64_t)h * DH;
   };
@@ -156,7 +226,7 @@ event_attn_kernel(const typename AttnT<DT>::T* __restrict__ q, const typename At
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) acc[r][nt] = 0.f;
 
-    const int kt_end = (MODE == 0) ? qt : nqt - 1;   // MODE 0 = track-causal
+    const int kt_end = (MODE == 0 || MODE == 3) ? qt : nqt - 1;   // MODE 0 / 3 = track-causal
     for (int kt = 0; kt <= kt_end; ++kt) {
       // the tile's K and V rows are requested together, so their latencies overlap (segments here are
       // short: one key tile is the common case)
@@ -176,7 +246,7 @@ event_attn_kernel(const typename AttnT<DT>::T* __restrict__ q, const typename At
       for (int r = 0; r < 4; ++r) {
         const int j = kt * 16 + 4 * g + r;
         bool ok = (i < L) && (j < L);
-        if (MODE == 0) ok = ok && (j <= i);
+        if (MODE == 0 || MODE == 3) ok = ok && (j <= i);
         else if (MODE == 2) ok = ok && (om == nullptr || om[j < L ? j : L - 1] > 0.5f);
         else if (key_pad != nullptr) {
           int64_t tj = indices[base + (j < L ? j : L - 1)];
@@ -229,7 +299,7 @@ event_attn_kernel(const typename AttnT<DT>::T* __restrict__ q, const typename At
 #pragma unroll
         for (int e = 0; e < QD; ++e) dst[e] = o[e];
       }
-      if (MODE != 2 && out_grid) {
+      if (MODE < 2 && out_grid) {
         int64_t tr = indices[base + i];
         tr = tr < 0 ? 0 : (tr >= T ? T - 1 : tr);
         TT* dst = out_grid + ((int64_t)p * T + tr) * rstride + (int64_t)h * DH + g * QD;
@@ -251,13 +321,38 @@ static int launch_attn(int mode, const void* q, const void* k, const void* v, vo
   if (mode == HCLSM_ATTN_TRACK_CAUSAL)
     hipLaunchKernelGGL((event_attn_kernel<DT, DH, 0>), dim3(grid), dim3(64 * ATTN_WAVES), 0, st, (const TT*)q,
                        (const TT*)k, (const TT*)v, (TT*)outp, (TT*)outg, offsets, indices, kp, nseg, T, H, cap, sl2,
-                       AttnExt{});
+                       AttnExt{}, AttnIdx{});
   else
     hipLaunchKernelGGL((event_attn_kernel<DT, DH, 1>), dim3(grid), dim3(64 * ATTN_WAVES), 0, st, (const TT*)q,
                        (const TT*)k, (const TT*)v, (TT*)outp, (TT*)outg, offsets, indices, kp, nseg, T, H, cap, sl2,
-                       AttnExt{});
+                       AttnExt{}, AttnIdx{});
   HCLSM_LAUNCH_CHECK();
   return 0;
+}
+
+// MODE 3 launch (track-causal, packed, index built in the launch; T <= ATTN_IDX_TMAX).
+template <int DT, int DH>
+static int launch_attn_idx(const void* q, const void* k, const void* v, void* outp, int64_t nseg, int64_t T, int H,
+                           int64_t cap, float scale, const AttnIdx& ix, hipStream_t st) {
+  using TT = typename AttnT<DT>::T;
+  const unsigned grid = (unsigned)((nseg * H + ATTN_WAVES - 1) / ATTN_WAVES);
+  hipLaunchKernelGGL((event_attn_kernel<DT, DH, 3>), dim3(grid), dim3(64 * ATTN_WAVES), 0, st, (const TT*)q,
+                     (const TT*)k, (const TT*)v, (TT*)outp, (TT*)nullptr, nullptr, nullptr, nullptr, nseg, T, H, cap,
+                     scale * HCLSM_LOG2E, AttnExt{}, ix);
+  HCLSM_LAUNCH_CHECK();
+  return 0;
+}
+
+template <int DT>
+static int dispatch_idx(int dh, const void* q, const void* k, const void* v, void* outp, int64_t nseg, int64_t T,
+                        int H, int64_t cap, float scale, const AttnIdx& ix, hipStream_t st) {
+  switch (dh) {
+    case 16: return launch_attn_idx<DT, 16>(q, k, v, outp, nseg, T, H, cap, scale, ix, st);
+    case 32: return launch_attn_idx<DT, 32>(q, k, v, outp, nseg, T, H, cap, scale, ix, st);
+    case 64: return launch_attn_idx<DT, 64>(q, k, v, outp, nseg, T, H, cap, scale, ix, st);
+    case 128: return launch_attn_idx<DT, 128>(q, k, v, outp, nseg, T, H, cap, scale, ix, st);
+    default: return HCLSM_ERR_UNSUPPORTED;
+  }
 }
 
 template <int DT>
@@ -289,7 +384,7 @@ int attn_slots_packed(const void* q, const void* k, const void* v, int64_t ldi, 
     using TT = typename AttnT<DT_>::T;                                                                       \
     hipLaunchKernelGGL((event_attn_kernel<DT_, DH_, 2>), dim3(grid), dim3(64 * ATTN_WAVES), 0, st, (const TT*)q, \
                        (const TT*)k, (const TT*)v, (TT*)out, (TT*)nullptr, nullptr, nullptr, nullptr, cap, N, H,   \
-                       cap * N, sl2, ex);                                                                    \
+                       cap * N, sl2, ex, AttnIdx{});                                                         \
     HCLSM_LAUNCH_CHECK();                                                                                    \
     return 0;                                                                                                \
   }
@@ -314,6 +409,7 @@ extern "C" int hclsm_event_attention(const void* q, const void* k, const void* v
   if (dtype != HCLSM_F32 && dtype != HCLSM_BF16 && dtype != HCLSM_F16) return HCLSM_ERR_DTYPE;
   if (dh != 16 && dh != 32 && dh != 64 && dh != 128) return HCLSM_ERR_UNSUPPORTED;
   if (nseg == 0 || H == 0 || T == 0) return 0;
+  if (!out_grid && capacity == 0) return 0;   // a packed output of no rows: nothing to write
   if (!q || !k || !v || !offsets || !indices || (!out_packed && !out_grid)) return HCLSM_ERR_NULL;
   hipStream_t st = (hipStream_t)stream;
   switch (dtype) {
@@ -324,4 +420,44 @@ extern "C" int hclsm_event_attention(const void* q, const void* k, const void* v
     default:
       return dispatch_dh<HCLSM_F32>((int)dh, mode, q, k, v, out_packed, out_grid, offsets, indices, key_pad, nseg, T, (int)H, capacity, scale, st);
   }
+}
+
+// Index build and per-track causal attention in one call, on `stream`.  For T <= ATTN_IDX_TMAX (with
+// heads and a packed output to write) two launches: the row counts, then the attention, whose waves read
+// their track's events straight from the mask, take the packed offset from the counts and fill the index
+// tables as they go.  Otherwise hclsm_event_index, then hclsm_event_attention over its tables.
+extern "C" int hclsm_track_causal_attention(const void* mask, int mask_dtype, int rule, const void* q,
+                                            const void* k, const void* v, void* out_packed, int64_t B,
+                                            int64_t T, int64_t H, int64_t dh, int64_t capacity, float scale,
+                                            int dtype, int32_t* tables, void* stream) {
+  using namespace hclsm;
+  if (B < 0 || T < 0 || H < 0 || dh < 0 || capacity < 0 || B * T > 0x7fffffffLL) return HCLSM_ERR_SHAPE;
+  if (mask_dtype < HCLSM_F32 || mask_dtype > HCLSM_U8) return HCLSM_ERR_DTYPE;
+  if (dtype != HCLSM_F32 && dtype != HCLSM_BF16 && dtype != HCLSM_F16) return HCLSM_ERR_DTYPE;
+  if (rule != HCLSM_EVENT_GT_HALF && rule != HCLSM_EVENT_NONZERO) return HCLSM_ERR_MODE;
+  if (dh != 16 && dh != 32 && dh != 64 && dh != 128) return HCLSM_ERR_UNSUPPORTED;
+  if (!tables) return HCLSM_ERR_NULL;
+  const int64_t cap = B * T > 1 ? B * T : 1;
+  int32_t* stats = tables;
+  int32_t* counts = stats + 2;
+  int32_t* offsets = counts + B;
+  int32_t* indices = offsets + B + 1;
+  int32_t* rows = indices + cap;
+  int32_t* slot_of = rows + cap;
+  if (B > 0 && T > 0 && T <= ATTN_IDX_TMAX && H > 0 && capacity > 0) {
+    if (!mask || !q || !k || !v || !out_packed) return HCLSM_ERR_NULL;
+    hipStream_t st = (hipStream_t)stream;
+    int rc = event_counts(mask, mask_dtype, B, T, rule, counts, st);
+    if (rc) return rc;
+    const AttnIdx ix{mask, mask_dtype, rule, counts, offsets, indices, rows, slot_of, stats};
+    switch (dtype) {
+      case HCLSM_BF16: return dispatch_idx<HCLSM_BF16>((int)dh, q, k, v, out_packed, B, T, (int)H, capacity, scale, ix, st);
+      case HCLSM_F16: return dispatch_idx<HCLSM_F16>((int)dh, q, k, v, out_packed, B, T, (int)H, capacity, scale, ix, st);
+      default: return dispatch_idx<HCLSM_F32>((int)dh, q, k, v, out_packed, B, T, (int)H, capacity, scale, ix, st);
+    }
+  }
+  const int rc = hclsm_event_index(mask, mask_dtype, B, T, rule, counts, offsets, indices, rows, slot_of, stats, stream);
+  if (rc) return rc;
+  return hclsm_event_attention(q, k, v, out_packed, nullptr, offsets, indices, nullptr, B, T, H, dh, capacity, scale,
+                               dtype, HCLSM_ATTN_TRACK_CAUSAL, stream);
 }

@@ -13,21 +13,9 @@
 // Gather / scatter are byte moves over 16/4/2/1-byte units chosen from the row
 // size and pointer alignment; every unit looks its source up in the int32 tables,
 // so non-event rows are copied exactly and padded rows are exact zeros.
-#include "common.h"
+#include "internal.h"
 
 namespace hclsm {
-
-__device__ __forceinline__ bool is_event(const void* mask, int mdt, int64_t i, int rule) {
-  float v;
-  switch (mdt) {
-    case HCLSM_F32: v = reinterpret_cast<const float*>(mask)[i]; break;
-    case HCLSM_BF16: v = bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(mask)[i]); break;
-    case HCLSM_F16: v = (float)reinterpret_cast<const _Float16*>(mask)[i]; break;
-    default: return reinterpret_cast<const uint8_t*>(mask)[i] != 0;
-  }
-  if (rule == HCLSM_EVENT_GT_HALF) return v > 0.5f;
-  return !(v == 0.0f);  // NaN counts as an event, like torch.nonzero
-}
 
 constexpr int EV_WAVES = 4;  // rows (waves) per workgroup in count / fill
 
@@ -44,6 +32,15 @@ event_count_kernel(const void* __restrict__ mask, int mdt, int64_t B, int64_t T,
     c += __popcll(__ballot(ev));
   }
   if (lane == 0) counts[b] = c;
+}
+
+// Row counts of a [B, T] mask alone (composite entry points that build the rest of the index later).
+int event_counts(const void* mask, int mdt, int64_t B, int64_t T, int rule, int32_t* counts, hipStream_t st) {
+  if (B <= 0) return 0;
+  const unsigned g = (unsigned)((B + EV_WAVES - 1) / EV_WAVES);
+  hipLaunchKernelGGL(event_count_kernel, dim3(g), dim3(64 * EV_WAVES), 0, st, mask, mdt, B, T, rule, counts);
+  HCLSM_LAUNCH_CHECK();
+  return 0;
 }
 
 constexpr int SCAN_THREADS = 1024;
@@ -164,8 +161,18 @@ event_fill_prefix_kernel(const void* __restrict__ mask, int mdt, int64_t B, int6
   __shared__ int32_t red[EV_WAVES];
   const int64_t b0 = (int64_t)blockIdx.x * EV_WAVES;
   const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
+  // counts[0, b0): 8 loads per thread in flight per round (a later workgroup reads up to 16384 counts)
   int32_t s = 0;
-  for (int64_t i = tid; i < b0; i += 64 * EV_WAVES) s += counts[i];
+  for (int64_t i0 = tid; i0 < b0; i0 += 8 * 64 * EV_WAVES) {
+    int32_t c[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t i = i0 + (int64_t)u * 64 * EV_WAVES;
+      c[u] = i < b0 ? counts[i] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s += c[u];
+  }
   const int32_t prefix = block_sum(s, red);
   const int64_t b = b0 + wid;
   int32_t off = prefix;
@@ -191,10 +198,18 @@ event_fill_prefix_kernel(const void* __restrict__ mask, int mdt, int64_t B, int6
   }
   if (blockIdx.x == gridDim.x - 1) {   // totals: every row count, summed and maxed by this workgroup
     int32_t t = 0, m = 0;
-    for (int64_t i = tid; i < B; i += 64 * EV_WAVES) {
-      const int32_t c = counts[i];
-      t += c;
-      m = c > m ? c : m;
+    for (int64_t i0 = tid; i0 < B; i0 += 8 * 64 * EV_WAVES) {
+      int32_t c[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int64_t i = i0 + (int64_t)u * 64 * EV_WAVES;
+        c[u] = i < B ? counts[i] : 0;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        t += c[u];
+        m = c[u] > m ? c[u] : m;
+      }
     }
     const int32_t total = block_sum(t, red);
 #pragma unroll

@@ -5,6 +5,21 @@
 
 namespace hclsm {
 
+// Event rule of mask element i (mask dtype mdt: F32 / BF16 / F16 / U8): GT_HALF is v > 0.5, NONZERO
+// v != 0 (NaN counts, as torch.nonzero); U8 masks: any nonzero byte.
+__device__ __forceinline__ bool is_event(const void* mask, int mdt, int64_t i, int rule) {
+  float v;
+  switch (mdt) {
+    case HCLSM_F32: v = reinterpret_cast<const float*>(mask)[i]; break;
+    case HCLSM_BF16: v = bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(mask)[i]); break;
+    case HCLSM_F16: v = (float)reinterpret_cast<const _Float16*>(mask)[i]; break;
+    default: return reinterpret_cast<const uint8_t*>(mask)[i] != 0;
+  }
+  if (rule == HCLSM_EVENT_GT_HALF) return v > 0.5f;
+  return !(v == 0.0f);  // NaN counts as an event, like torch.nonzero
+}
+
+
 // Y[M, N] = A . W^T (+ bias) (ReLU if relu) (+ resid) with A = X or LayerNorm(X) rows (ln != 0), the
 // row count taken as min(M, *m_dev * m_mul) when m_dev is set (read on the device), and, when glu is
 // set, the gated-linear epilogue val = silu(glu[row, col]) * val (glu in `dtype`, row stride ldg) before
@@ -31,6 +46,9 @@ int layer_norm_rows(const void* x, int64_t ldx, const float* w, const float* b, 
 // Attention among the N rows of each of cap uniform segments (the first *nseg_dev live): rows p*N + i
 // of q / k / v (row stride ldi) and out (row stride ldo), H heads of dh columns; key j of segment p is
 // excluded when obj_mask[seg_rows[p] * N + j] <= 0.5 (obj_mask nullable).  Defined in event_attn.hip.
+// event_count_kernel over a [B, T] mask: counts[b] = events of row b (events.hip).
+int event_counts(const void* mask, int mdt, int64_t B, int64_t T, int rule, int32_t* counts, hipStream_t st);
+
 int attn_slots_packed(const void* q, const void* k, const void* v, int64_t ldi, void* out, int64_t ldo,
                       const int32_t* nseg_dev, int64_t cap, int64_t N, int H, int dh, const float* obj_mask,
                       const int32_t* seg_rows, float scale, int dtype, hipStream_t st);

@@ -20,9 +20,10 @@ import torch
 
 from hclsm_amd import _lib
 from hclsm_amd.kernels._common import require_gpu
-from hclsm_amd.kernels.sparse_event_attn import EventIndex, build_event_index
+from hclsm_amd.kernels.sparse_event_attn import EventIndex, _mask_code, build_event_index
 
 _MODES = {"track_causal": _lib.ATTN_TRACK_CAUSAL, "slots": _lib.ATTN_SLOTS}
+_RULES = {"gt_half": _lib.EVENT_GT_HALF, "nonzero": _lib.EVENT_NONZERO}
 
 
 def _check_qkv(q, k, v):
@@ -77,11 +78,33 @@ def event_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, index: Ev
     return result
 
 
-def track_causal_event_attention(q, k, v, event_mask, scale=None, out="packed", rule="gt_half"):
+def track_causal_event_attention(q, k, v, event_mask, scale=None, out="packed", rule="gt_half", capacity=None):
     """Per-track causal attention among the event timesteps of ``event_mask`` (P, T).
-    Returns (packed output, event index)."""
-    idx = build_event_index(event_mask, rule)
-    return event_attention(q, k, v, idx, "track_causal", scale=scale, out=out), idx
+    Returns (packed output, event index).  With out="packed" and a known ``capacity`` (rows of the packed
+    output; events past it are dropped) the index build and the attention are one library call
+    (hclsm_track_causal_attention) with no host synchronisation; otherwise the index is built first and
+    the output sized by its total (one host read)."""
+    if out != "packed" or capacity is None:
+        idx = build_event_index(event_mask, rule)
+        return event_attention(q, k, v, idx, "track_causal", scale=scale, out=out, capacity=capacity), idx
+    require_gpu("track_causal_event_attention", q, k, v, event_mask)
+    _check_qkv(q, k, v)
+    P, T, H, dh = q.shape
+    if tuple(event_mask.shape) != (P, T):
+        raise ValueError(f"event_mask must be ({P}, {T}) to match q, got {tuple(event_mask.shape)}")
+    cap = int(capacity)
+    if cap < 0:
+        raise ValueError(f"capacity must be >= 0, got {cap}")
+    m, code = _mask_code(event_mask.detach().contiguous())
+    qc, kc, vc = q.contiguous(), k.contiguous(), v.contiguous()
+    idx = EventIndex.allocate(P, T, q.device)
+    outp = torch.empty((cap, H, dh), dtype=q.dtype, device=q.device)
+    rc = _lib.lib().hclsm_track_causal_attention(
+        m.data_ptr(), code, _RULES[rule], qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), outp.data_ptr(), P, T, H, dh,
+        cap, float(dh ** -0.5 if scale is None else scale), _lib.dtype_code(q.dtype), idx.ptr("stats"),
+        _lib.stream_of(qc))
+    _lib.check(rc, "hclsm_track_causal_attention")
+    return outp, idx
 
 
 _DENSE_CACHE: dict = {}

@@ -57,16 +57,24 @@ class EventIndex:
         self._buf = None
         self._off: dict = {}
 
+    _LAYOUTS: dict = {}
+
     @classmethod
     def allocate(cls, B: int, T: int, device) -> "EventIndex":
-        cap = max(B * T, 1)
-        sizes = dict(stats=2, counts=B, offsets=B + 1, indices=cap, rows=cap, slot_of=B * T)
+        lay = cls._LAYOUTS.get((B, T))
+        if lay is None:
+            cap = max(B * T, 1)
+            sizes = dict(stats=2, counts=B, offsets=B + 1, indices=cap, rows=cap, slot_of=B * T)
+            off, o = {}, 0
+            for n in cls._NAMES:
+                off[n] = (o, sizes[n])
+                o += sizes[n]
+            if len(cls._LAYOUTS) > 256:
+                cls._LAYOUTS.clear()
+            lay = cls._LAYOUTS[(B, T)] = (off, o)
         idx = cls(B, T)
-        o = 0
-        for n in cls._NAMES:
-            idx._off[n] = (o, sizes[n])
-            o += sizes[n]
-        idx._buf = torch.empty(o, dtype=torch.int32, device=device)
+        idx._off = lay[0]            # shared, read-only
+        idx._buf = torch.empty(lay[1], dtype=torch.int32, device=device)
         idx._base = idx._buf.data_ptr()
         return idx
 

@@ -224,6 +224,18 @@ int hclsm_event_attention(const void* q, const void* k, const void* v, void* out
                           float scale, int dtype, int mode, void* stream);
 
 /*
+ * hclsm_event_index of a [B, T] mask followed by hclsm_event_attention in HCLSM_ATTN_TRACK_CAUSAL mode
+ * with a packed output ([capacity, H, dh]), in one call on one stream.  `tables` is one int32 buffer
+ * holding the index in this order: stats [2], counts [B], offsets [B+1], indices [max(B*T,1)],
+ * rows [max(B*T,1)], slot_of [B*T]; it is left filled for later gathers and scatters.
+ * Replaces: the index construction and attention of the per-track causal event attention of the
+ *   benchmark configuration (sparse_event_attn.py:153-188, hierarchy_manager.py:42-77) as one host call.
+ */
+int hclsm_track_causal_attention(const void* mask, int mask_dtype, int rule, const void* q, const void* k,
+                                 const void* v, void* out_packed, int64_t B, int64_t T, int64_t H, int64_t dh,
+                                 int64_t capacity, float scale, int dtype, int32_t* tables, void* stream);
+
+/*
  * LayerNorm over the last dimension of a [M, D] row-major tensor (row strides ldx / ldy):
  *   y = (x - mean) / sqrt(var + eps) * w + b, population variance, fp32 statistics.
  * w, b: [D] float32, nullable (then 1 / 0).  (in, out) dtype pairs: (F32,F32) (F32,BF16) (BF16,BF16)

@@ -113,3 +113,33 @@ def test_against_torch_sdpa_on_gpu():
         qq, kk, vv = (t[b, ts].permute(1, 0, 2).cuda() for t in (q, k, v))
         ref = F.scaled_dot_product_attention(qq, kk, vv, is_causal=True).permute(1, 0, 2)
         assert torch.allclose(o[offs[b]:offs[b + 1]], ref, rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.parametrize("P,T,H,dh,p,dtype", [(1024, 64, 6, 64, 0.15, torch.bfloat16), (37, 300, 2, 32, 0.3, torch.float32),
+                                              (5, 1, 1, 16, 1.0, torch.float16), (64, 128, 4, 64, 0.0, torch.bfloat16),
+                                              (8, 1024, 3, 64, 0.05, torch.bfloat16), (700, 16, 2, 128, 0.5, torch.float32),
+                                              (3, 1500, 1, 16, 0.3, torch.bfloat16)])
+def test_one_call_matches_two_calls(P, T, H, dh, p, dtype):
+    """hclsm_track_causal_attention (index + attention in one call, capacity given: for T <= 1024 the row
+    counts, then the attention building each track's event list from the mask and filling the tables; past
+    that the separate index build) against the index build followed by hclsm_event_attention: identical
+    packed output and identical index tables; with a capacity below the event total the rows past it are
+    not written."""
+    from hclsm_amd.kernels.event_attention import event_attention, track_causal_event_attention
+    from hclsm_amd.kernels.sparse_event_attn import build_event_index
+    q, k, v, m = _data(P, T, H, dh, dtype, p, seed=P + T)
+    q, k, v, m = q.cuda(), k.cuda(), v.cuda(), m.cuda()
+    ref_idx = build_event_index(m)
+    total = ref_idx.total()
+    ref = event_attention(q, k, v, ref_idx, capacity=total)
+    o, idx = track_causal_event_attention(q, k, v, m, capacity=total)
+    torch.cuda.synchronize()
+    assert o.shape == (total, H, dh) and torch.equal(o, ref)
+    for name in ("counts", "offsets", "slot_of", "stats"):
+        assert torch.equal(getattr(idx, name), getattr(ref_idx, name)), name
+    assert torch.equal(idx.indices[:total], ref_idx.indices[:total])
+    assert torch.equal(idx.rows[:total], ref_idx.rows[:total])
+    if total > 1:
+        cut = total // 2
+        o2, _ = track_causal_event_attention(q, k, v, m, capacity=cut)
+        assert o2.shape == (cut, H, dh) and torch.equal(o2, ref[:cut])

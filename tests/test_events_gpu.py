@@ -43,6 +43,52 @@ def test_index_bit_exact(B, T, p):
     _check_index(_mask(B, T, p, seed=B + T, force0=(p == 0.15)))
 
 
+def _index_equal(idx, ref):
+    total = ref.total()
+    for name in ("counts", "offsets", "slot_of", "stats"):
+        assert torch.equal(getattr(idx, name), getattr(ref, name)), name
+    for name in ("indices", "rows"):            # entries past the total are unwritten capacity
+        assert torch.equal(getattr(idx, name)[:total], getattr(ref, name)[:total]), name
+
+
+@pytest.mark.parametrize("B,T,p", [(1, 4, 1.0), (63, 8, 0.5), (65, 16, 0.5), (200, 32, 0.3), (129, 64, 1.0),
+                                   (1024, 64, 0.15), (4096, 64, 0.1), (4000, 4, 0.7), (3000, 16, 0.0),
+                                   (2049, 32, 0.6), (4097, 64, 0.2), (10, 60, 0.5)])
+def test_one_call_index(B, T, p):
+    """The index hclsm_track_causal_attention leaves in its table buffer: the same tables as
+    build_event_index, which is checked against the oracle; empty and full masks, ragged sizes."""
+    from hclsm_amd.kernels.event_attention import track_causal_event_attention
+    from hclsm_amd.kernels.sparse_event_attn import build_event_index
+    m = _mask(B, T, p, seed=B + T, force0=(p == 0.15)).cuda()
+    q = torch.zeros(B, T, 1, 16, dtype=torch.bfloat16, device="cuda")
+    ref, _ = _check_index(m.cpu())
+    _, idx = track_causal_event_attention(q, q, q, m, capacity=max(ref.total(), 1))
+    _index_equal(idx, build_event_index(m))
+
+
+@pytest.mark.parametrize("B,T", [(1024, 64), (77, 16)])
+def test_one_call_index_nonzero_rule_and_misaligned_mask(B, T):
+    """The one-call index under rule "nonzero" (negative, NaN and tiny values count), and from a mask whose
+    storage is not 16-byte aligned: both bit-exact against build_event_index."""
+    from hclsm_amd.kernels.event_attention import track_causal_event_attention
+    from hclsm_amd.kernels.sparse_event_attn import build_event_index
+    q = torch.zeros(B, T, 1, 16, dtype=torch.bfloat16, device="cuda")
+    m = _mask(B, T, 0.3, seed=B)
+    m = m * torch.where(torch.rand(B, T, generator=torch.Generator().manual_seed(1)) < 0.5, -1e-3, 1.0)
+    m[0, 1] = float("nan")
+    _check_index(m, rule="nonzero")
+    mg = m.cuda()
+    _, idx = track_causal_event_attention(q, q, q, mg, rule="nonzero", capacity=B * T)
+    _index_equal(idx, build_event_index(mg, "nonzero"))
+    m2 = _mask(B, T, 0.4, seed=B + 1).cuda()
+    buf = torch.zeros(B * T + 1, device="cuda")
+    mis = buf[1:].view(B, T)
+    mis.copy_(m2)
+    assert mis.data_ptr() % 16 != 0
+    _, idx2 = track_causal_event_attention(q, q, q, mis, capacity=B * T)
+    _index_equal(idx2, build_event_index(m2))
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.bool, torch.uint8])
 def test_index_mask_dtypes(dtype):
     _check_index(_mask(33, 70, 0.3, seed=2), dtype=dtype)
