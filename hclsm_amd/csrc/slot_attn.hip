@@ -29,6 +29,20 @@ template <> struct Cvt<float> { static __device__ __forceinline__ float f(float 
 template <> struct Cvt<uint16_t> { static __device__ __forceinline__ float f(uint16_t v) { return bf16_bits_to_f32(v); } };
 template <> struct Cvt<_Float16> { static __device__ __forceinline__ float f(_Float16 v) { return (float)v; } };
 
+// Eight consecutive elements as floats with 16-byte loads (p 16-byte aligned for 16-bit XT, 32-byte for float).
+template <typename XT>
+__device__ __forceinline__ void load8f(const XT* p, float* o) {
+  if constexpr (std::is_same_v<XT, float>) {
+    const float4 u = reinterpret_cast<const float4*>(p)[0], v = reinterpret_cast<const float4*>(p)[1];
+    o[0] = u.x; o[1] = u.y; o[2] = u.z; o[3] = u.w; o[4] = v.x; o[5] = v.y; o[6] = v.z; o[7] = v.w;
+  } else {
+    const uint4 u = *reinterpret_cast<const uint4*>(p);
+    const XT* e = reinterpret_cast<const XT*>(&u);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = Cvt<XT>::f(e[i]);
+  }
+}
+
 // Operand of one 32-wide K block for this lane (8 elements at k0 + 8g), converted to DT.
 template <int DT, typename XT>
 __device__ __forceinline__ typename MM<DT>::Op load_op(const XT* p) {
@@ -831,6 +845,169 @@ linear_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>::T* _
 }
 
 // ---------------------------------------------------------------------------
+// Small-M linear layer (16-bit operands) with every K block of a wave requested at once: the 4 waves
+// of a 32 x 32 output tile split K in blocks of 32 (wave w: blocks w, w + 4, ...; KB per wave), each
+// lane holding its 8 elements of every block for two rows and two columns, so the loads take one
+// latency round instead of one per block.  With LN the row statistics of X come from the same
+// registers (mean, then the centred sum of squares: two passes, two barriers) and the operands are
+// normalised in place: LN(X) W^T with no separate LayerNorm launch.  xout (nullable): the workgroups
+// of column tile 0 also store X rounded to DT.
+template <int DT, int OT, typename XT, bool LN, int KB>
+__global__ void __launch_bounds__(256)
+linear_kreg_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>::T* __restrict__ W, int64_t ldw,
+                   const float* __restrict__ bias, const float* __restrict__ resid, int64_t ldr,
+                   typename MM<OT>::T* __restrict__ Y, int64_t ldy, typename MM<DT>::T* __restrict__ Y2,
+                   int64_t ldy2, int64_t M, int64_t N, int64_t K, int relu, float clamp_v,
+                   const float* __restrict__ lnw, const float* __restrict__ lnb, float ln_eps,
+                   typename MM<DT>::T* __restrict__ xout, int64_t ldxo) {
+  using A = MM<DT>;
+  constexpr int KPL = A::KPL;
+  constexpr int BLK = 4 * KPL;
+  static_assert(KPL == 8, "16-bit operands");
+  __shared__ float red[4][2][2][4][64];   // 16 KB
+  __shared__ float stat[2][4][2][16];     // [pass][wave][row tile][li]
+  const int64_t tiles_n = (N + 31) / 32;
+  const int64_t tm = blockIdx.x / tiles_n, tn = blockIdx.x - tm * tiles_n;
+  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, g = lane >> 4, li = lane & 15;
+  const int nblk = (int)(K / BLK);
+  const XT* pa[2];
+  const typename A::T* pb[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    int64_t r = tm * 32 + 16 * t + li;
+    r = r < M ? r : M - 1;
+    pa[t] = X + r * ldx + KPL * g;
+    int64_t c = tn * 32 + 16 * t + li;
+    c = c < N ? c : N - 1;
+    pb[t] = W + c * ldw + KPL * g;
+  }
+  // 1. every operand of this wave's blocks (block index clamped; blocks past nblk are skipped below)
+  float xa[LN ? KB : 1][2][KPL];
+  typename A::Op ao[LN ? 1 : KB][2], bo[KB][2];
+  float lw[LN ? KB : 1][KPL], lb[LN ? KB : 1][KPL];
+#pragma unroll
+  for (int i = 0; i < KB; ++i) {
+    const int sb = wid + 4 * i < nblk ? wid + 4 * i : nblk - 1;
+    const int64_t k0 = (int64_t)sb * BLK;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      if constexpr (LN) {
+        load8f<XT>(pa[t] + k0, xa[i][t]);
+      } else {
+        ao[i][t] = load_op<DT, XT>(pa[t] + k0);
+      }
+      bo[i][t] = A::load(pb[t] + k0);
+    }
+    if constexpr (LN) {
+      if (lnw) load8f<float>(lnw + k0 + KPL * g, lw[i]);
+      else
+#pragma unroll
+        for (int e = 0; e < KPL; ++e) lw[i][e] = 1.f;
+      if (lnb) load8f<float>(lnb + k0 + KPL * g, lb[i]);
+      else
+#pragma unroll
+        for (int e = 0; e < KPL; ++e) lb[i][e] = 0.f;
+    }
+  }
+  float mean[2] = {0.f, 0.f}, rstd[2] = {1.f, 1.f};
+  if constexpr (LN) {
+    // 2. row mean, then the centred sum of squares, over this lane's values, the 4 lane groups and the waves
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        float sacc = 0.f;
+#pragma unroll
+        for (int i = 0; i < KB; ++i) {
+          if (wid + 4 * i >= nblk) continue;
+#pragma unroll
+          for (int e = 0; e < KPL; ++e) {
+            const float dv = pass == 0 ? xa[i][t][e] : xa[i][t][e] - mean[t];
+            sacc += pass == 0 ? dv : dv * dv;
+          }
+        }
+        sacc += __shfl_xor(sacc, 16, 64);
+        sacc += __shfl_xor(sacc, 32, 64);
+        if (g == 0) stat[pass][wid][t][li] = sacc;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const float tot = stat[pass][0][t][li] + stat[pass][1][t][li] + stat[pass][2][t][li] + stat[pass][3][t][li];
+        if (pass == 0) mean[t] = tot / (float)K;
+        else rstd[t] = rsqrtf(tot / (float)K + ln_eps);
+      }
+    }
+    if (xout != nullptr && tn == 0) {   // X in DT, rows of this tile
+#pragma unroll
+      for (int i = 0; i < KB; ++i) {
+        if (wid + 4 * i >= nblk) continue;
+        const int64_t k0 = (int64_t)(wid + 4 * i) * BLK + KPL * g;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int64_t row = tm * 32 + 16 * t + li;
+          if (row >= M) continue;
+          typename A::T e8[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) e8[e] = A::fromf(xa[i][t][e]);
+          *reinterpret_cast<uint4*>(xout + row * ldxo + k0) = *reinterpret_cast<uint4*>(e8);
+        }
+      }
+    }
+  }
+  // 3. the products
+  f32x4 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < KB; ++i) {
+    if (wid + 4 * i >= nblk) continue;
+    typename A::Op a[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      if constexpr (LN) {
+        typename A::T e8[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) e8[e] = A::fromf((xa[i][t][e] - mean[t]) * rstd[t] * lw[i][e] + lb[i][e]);
+        a[t] = __builtin_bit_cast(typename A::Op, *reinterpret_cast<uint4*>(e8));
+      } else {
+        a[t] = ao[i][t];
+      }
+    }
+    acc[0][0] = A::mfma(a[0], bo[i][0], acc[0][0]);
+    acc[0][1] = A::mfma(a[0], bo[i][1], acc[0][1]);
+    acc[1][0] = A::mfma(a[1], bo[i][0], acc[1][0]);
+    acc[1][1] = A::mfma(a[1], bo[i][1], acc[1][1]);
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[wid][i][j][r][lane] = acc[i][j][r];
+  __syncthreads();
+  // 1024 outputs, 4 per thread: thread -> (ti, tj) = wave index, lane, all four r
+  const int ti = wid >> 1, tj = wid & 1;
+  const int64_t col = tn * 32 + 16 * tj + li;
+  if (col >= N) return;
+  const float bv = bias ? bias[col] : 0.f;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int64_t row = tm * 32 + 16 * ti + 4 * g + r;
+    if (row >= M) continue;
+    float val = red[0][ti][tj][r][lane] + red[1][ti][tj][r][lane] + red[2][ti][tj][r][lane] +
+                red[3][ti][tj][r][lane] + bv;
+    if (relu) val = fmaxf(val, 0.f);
+    if (resid) val += resid[row * ldr + col];
+    if (clamp_v > 0.f) val = fminf(fmaxf(val, -clamp_v), clamp_v);
+    Y[row * ldy + col] = MM<OT>::fromf(val);
+    if (Y2) Y2[row * ldy2 + col] = A::fromf(val);
+  }
+}
+
+// ---------------------------------------------------------------------------
 template <int DT>
 __global__ void __launch_bounds__(256)
 gru_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const typename MM<DT>::T* __restrict__ Hb,
@@ -1530,17 +1707,57 @@ static void launch_linear_quad(const void* x, int64_t ldx, const void* w, int64_
   }
 }
 
+// linear_kreg_kernel with KB = the smallest instantiated count of blocks per wave covering K; false
+// (nothing launched) past the largest.
+template <int DT, int OT, typename XT, bool LN>
+static bool launch_linear_kreg(const void* x, int64_t ldx, const void* w, int64_t ldw, const float* bias,
+                               const float* resid, int64_t ldr, void* y, int64_t ldy, void* y2, int64_t ldy2,
+                               int64_t M, int64_t N, int64_t K, int relu, float clamp, const float* lnw,
+                               const float* lnb, float eps, void* xout, int64_t ldxo, hipStream_t st) {
+  const int64_t nblk = K / 32;
+  const int need = (int)((nblk + 3) / 4);
+  const unsigned grid = (unsigned)(((M + 31) / 32) * ((N + 31) / 32));
+  using TT = typename MM<DT>::T;
+#define HCLSM_KREG(KBV)                                                                                      \
+  if (need <= KBV) {                                                                                         \
+    hipLaunchKernelGGL((linear_kreg_kernel<DT, OT, XT, LN, KBV>), dim3(grid), dim3(256), 0, st, (const XT*)x, ldx, \
+                       (const TT*)w, ldw, bias, resid, ldr, (typename MM<OT>::T*)y, ldy, (TT*)y2, ldy2, M, N, K,   \
+                       relu, clamp, lnw, lnb, eps, (TT*)xout, ldxo);                                         \
+    return true;                                                                                             \
+  }
+  HCLSM_KREG(1) HCLSM_KREG(2) HCLSM_KREG(3)
+  if constexpr (!LN) {   // with LN the raw rows, gamma and beta stay in registers too: K <= 384 only
+    HCLSM_KREG(4) HCLSM_KREG(6) HCLSM_KREG(8)
+  }
+#undef HCLSM_KREG
+  return false;
+}
+
 template <int DT, int OT, typename XT>
 static void launch_linear_t(bool ln, const void* x, int64_t ldx, const void* w, int64_t ldw, const float* bias,
                             const float* resid, int64_t ldr, void* y, int64_t ldy, void* y2, int64_t ldy2, int64_t M,
                             int64_t N, int64_t K, int relu, float clamp, const float* lnw, const float* lnb,
-                            float eps, hipStream_t st, LinExt ext = kNoLinExt) {
+                            float eps, hipStream_t st, LinExt ext = kNoLinExt, void* xout = nullptr,
+                            int64_t ldxo = 0) {
   const int64_t tiles32 = ((M + 31) / 32) * ((N + 31) / 32);
   constexpr bool cvt = MM<DT>::KPL == 8 && std::is_same_v<XT, float>;
   if (!ln && (std::is_same_v<XT, typename MM<DT>::T> || (cvt && al16(x) && ldx % 4 == 0)) && tiles32 >= 2048) {
     launch_linear_quad<DT, OT, XT>(x, ldx, w, ldw, bias, resid, ldr, y, ldy, y2, ldy2, M, N, K, relu, clamp, st,
                                    OutSplit{0, 1, 0, 0, nullptr}, ext);
     return;
+  }
+  // 16-bit operands, K <= 1024, no device-side row count or gate: every K block in flight at once
+  if constexpr (MM<DT>::KPL == 8) {
+    const bool xok = std::is_same_v<XT, float> ? (al16(x) && ldx % 4 == 0) : (al16(x) && ldx % 8 == 0);
+    const bool lnok = !ln || ((lnw == nullptr || al16(lnw)) && (lnb == nullptr || al16(lnb)));
+    const bool xo_ok = xout == nullptr || (ln && al16(xout) && ldxo % 8 == 0);
+    if (ext.m_dev == nullptr && ext.glu == nullptr && K <= 1024 && xok && lnok && xo_ok) {
+      const bool done = ln ? launch_linear_kreg<DT, OT, XT, true>(x, ldx, w, ldw, bias, resid, ldr, y, ldy, y2, ldy2, M,
+                                                                 N, K, relu, clamp, lnw, lnb, eps, xout, ldxo, st)
+                           : launch_linear_kreg<DT, OT, XT, false>(x, ldx, w, ldw, bias, resid, ldr, y, ldy, y2, ldy2,
+                                                                  M, N, K, relu, clamp, lnw, lnb, eps, nullptr, 0, st);
+      if (done) return;
+    }
   }
   const unsigned grid = (unsigned)tiles32;
   if (ln)
@@ -1556,7 +1773,8 @@ static void launch_linear_t(bool ln, const void* x, int64_t ldx, const void* w, 
 static int linear_impl(const void* x, int64_t ldx, int x_dtype, const void* w, int64_t ldw, const float* bias,
                        const float* resid, int64_t ldr, void* y, int64_t ldy, int y_dtype, void* y2, int64_t ldy2,
                        int64_t M, int64_t N, int64_t K, int relu, float clamp, int ln, const float* lnw,
-                       const float* lnb, float ln_eps, int dtype, hipStream_t st, LinExt ext = kNoLinExt) {
+                       const float* lnb, float ln_eps, int dtype, hipStream_t st, LinExt ext = kNoLinExt,
+                       void* xout = nullptr, int64_t ldxo = 0) {
   if (M < 0 || N < 0 || K < 0) return HCLSM_ERR_SHAPE;
   if (M == 0 || N == 0) return 0;
   if (!x || !w || !y) return HCLSM_ERR_NULL;
@@ -1568,7 +1786,7 @@ static int linear_impl(const void* x, int64_t ldx, int x_dtype, const void* w, i
 #define HCLSM_LIN(D, O, XD, XT)                                                                              \
   if (dtype == D && y_dtype == O && x_dtype == XD) {                                                         \
     launch_linear_t<D, O, XT>(LNf, x, ldx, w, ldw, bias, resid, ldr, y, ldy, y2, ldy2, M, N, K, relu, clamp, lnw, \
-                              lnb, ln_eps, st, ext);                                                         \
+                              lnb, ln_eps, st, ext, xout, ldxo);                                             \
     HCLSM_LAUNCH_CHECK();                                                                                    \
     return 0;                                                                                                \
   }
@@ -1969,6 +2187,40 @@ extern "C" int64_t hclsm_slot_attention_workspace(int64_t B, int64_t N, int64_t 
 // One iteration (dynamic_slots.py:98-131).  slots_in fp32 and sb (the same slots in `dtype`) are
 // read; slots_out (may alias slots_in: it is written by the last launch, after every read) and
 // sb (rewritten with the new slots in `dtype`) are produced.
+// LN(x) W^T (+ bias) (ReLU) for fp32 x in one launch (linear_kreg_kernel: row statistics from the registers
+// holding the rows); xout (nullable) receives x rounded to dtype.  *taken = false, launching nothing, when
+// the shapes do not fit it: 16-bit dtype, K <= 384 a multiple of 32, 16-byte aligned rows and LN weights.
+static int linear_ln_fold(const float* x, int64_t ldx, const void* w, int64_t ldw, const float* bias, void* y,
+                          int64_t ldy, int64_t M, int64_t N, int64_t K, int relu, const float* lnw, const float* lnb,
+                          float eps, void* xout, int64_t ldxo, int dtype, hipStream_t st, bool* taken) {
+  *taken = false;
+  // the LN variant keeps the rows, gamma and beta in registers (two workgroups per CU): taken only when the
+  // tiles fit one such round on the device, where it beats a LayerNorm launch plus the linear layer
+  const int64_t tiles = ((M + 31) / 32) * ((N + 31) / 32);
+  static std::atomic<int> cu_count[HCLSM_MAX_DEVICES];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= HCLSM_MAX_DEVICES) return 0;
+  int cus = cu_count[dev].load(std::memory_order_relaxed);
+  if (cus == 0) {
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return 0;
+    cu_count[dev].store(cus, std::memory_order_relaxed);
+  }
+  if (tiles > 2 * (int64_t)cus) return 0;
+  if ((dtype != HCLSM_BF16 && dtype != HCLSM_F16) || M <= 0 || N <= 0 || K <= 0 || K % 32 || K > 384 || !al16(x) ||
+      ldx % 4 || !al16(w) || ldw % 8 || (lnw && !al16(lnw)) || (lnb && !al16(lnb)) ||
+      (xout && (!al16(xout) || ldxo % 8)) || !al16(y) || ldy % 8)
+    return 0;
+  *taken = true;
+  if (dtype == HCLSM_BF16)
+    launch_linear_kreg<HCLSM_BF16, HCLSM_BF16, float, true>(x, ldx, w, ldw, bias, nullptr, 0, y, ldy, nullptr, 0, M, N,
+                                                            K, relu, 0.f, lnw, lnb, eps, xout, ldxo, st);
+  else
+    launch_linear_kreg<HCLSM_F16, HCLSM_F16, float, true>(x, ldx, w, ldw, bias, nullptr, 0, y, ldy, nullptr, 0, M, N,
+                                                          K, relu, 0.f, lnw, lnb, eps, xout, ldxo, st);
+  HCLSM_LAUNCH_CHECK();
+  return 0;
+}
+
 static int slot_iteration_impl(const HclsmSlotWeights* W, const float* slots_in, void* sb, bool make_sb,
                                const void* k, int64_t ldk, int64_t k_bstride, const void* v, int64_t ldv,
                                int64_t v_bstride, bool v_transposed, float* slots_out, int64_t B, int64_t N, int64_t M,
@@ -1981,12 +2233,18 @@ static int slot_iteration_impl(const HclsmSlotWeights* W, const float* slots_in,
   void* m1 = ws + L.m1;
   void* xn = ws + L.xn;
   // q = LN_pre(slots) W_q^T; with make_sb the same pass writes sb (the slots in dtype)
-  int rc = ln_impl(slots_in, d, W->ln_pre_w, W->ln_pre_b, xn, d, rows, d, 1e-5f, HCLSM_F32, dtype, st, kNoLinExt,
-                   make_sb ? sb : nullptr);
+  bool folded = false;
+  int rc = linear_ln_fold(slots_in, d, W->w_q, d, nullptr, q, d, rows, d, d, 0, W->ln_pre_w, W->ln_pre_b, 1e-5f,
+                          make_sb ? sb : nullptr, d, dtype, st, &folded);
   if (rc) return rc;
-  rc = linear_impl(xn, d, dtype, W->w_q, d, nullptr, nullptr, 0, q, d, dtype, nullptr, 0, rows, d, d, 0, 0.f, 0,
-                   nullptr, nullptr, 0.f, dtype, st);
-  if (rc) return rc;
+  if (!folded) {
+    rc = ln_impl(slots_in, d, W->ln_pre_w, W->ln_pre_b, xn, d, rows, d, 1e-5f, HCLSM_F32, dtype, st, kNoLinExt,
+                 make_sb ? sb : nullptr);
+    if (rc) return rc;
+    rc = linear_impl(xn, d, dtype, W->w_q, d, nullptr, nullptr, 0, q, d, dtype, nullptr, 0, rows, d, d, 0, 0.f, 0,
+                     nullptr, nullptr, 0.f, dtype, st);
+    if (rc) return rc;
+  }
   // updates = attention core (logits, softmax over slots, [renorm], attn v): one fused launch when v is transposed
   rc = v_transposed ? launch_core_fused(q, d, N * d, k, ldk, k_bstride, v, v_bstride, upd, d, N * d, B, N, M, d, scale,
                                         0.f, logit_clamp, renorm_eps, dtype, st)
@@ -2000,11 +2258,16 @@ static int slot_iteration_impl(const HclsmSlotWeights* W, const float* slots_in,
                 st);
   if (rc) return rc;
   // m1 = ReLU(LN_mlp(h) W1^T + b1)
-  rc = ln_impl(h, d, W->ln_mlp_w, W->ln_mlp_b, xn, d, rows, d, 1e-5f, HCLSM_F32, dtype, st);
+  rc = linear_ln_fold(h, d, W->w1, d, W->b1, m1, hidden, rows, hidden, d, 1, W->ln_mlp_w, W->ln_mlp_b, 1e-5f, nullptr,
+                      0, dtype, st, &folded);
   if (rc) return rc;
-  rc = linear_impl(xn, d, dtype, W->w1, d, W->b1, nullptr, 0, m1, hidden, dtype, nullptr, 0, rows, hidden, d, 1, 0.f,
-                   0, nullptr, nullptr, 0.f, dtype, st);
-  if (rc) return rc;
+  if (!folded) {
+    rc = ln_impl(h, d, W->ln_mlp_w, W->ln_mlp_b, xn, d, rows, d, 1e-5f, HCLSM_F32, dtype, st);
+    if (rc) return rc;
+    rc = linear_impl(xn, d, dtype, W->w1, d, W->b1, nullptr, 0, m1, hidden, dtype, nullptr, 0, rows, hidden, d, 1, 0.f,
+                     0, nullptr, nullptr, 0.f, dtype, st);
+    if (rc) return rc;
+  }
   // slots_out = clamp(h + m1 W2^T + b2); sb = the same in dtype
   return linear_impl(m1, hidden, dtype, W->w2, hidden, W->b2, h, d, slots_out, d, HCLSM_F32, sb, d, rows, d, hidden, 0,
                      slot_clamp, 0, nullptr, nullptr, 0.f, dtype, st);
