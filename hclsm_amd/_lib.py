@@ -55,6 +55,7 @@ _SIGNATURES: dict[str, list] = {
                              _i64, _i64, _c_void_p, _int, _i64, _i64, _i64, _i64, _f32, _f32, _f32, _f32,
                              _int, _c_void_p, _i64, _c_void_p],
     "hclsm_slot_attention_workspace": [_i64, _i64, _i64, _i64, _i64, _i64, _int],
+    "hclsm_slot_attention_k_offset": [_i64, _i64, _i64, _i64, _i64, _i64, _int],
     "hclsm_slot_attention_iteration": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _c_void_p,
                                        _i64, _i64, _i64, _i64, _i64, _f32, _f32, _f32, _f32, _int, _c_void_p,
                                        _i64, _c_void_p],
@@ -80,7 +81,7 @@ _SIGNATURES: dict[str, list] = {
 }
 _RESTYPES = {"hclsm_strerror": ctypes.c_char_p, "hclsm_slot_attn_core_workspace": ctypes.c_int64,
              "hclsm_ssm_scan_bwd_workspace": ctypes.c_int64,
-             "hclsm_slot_attention_workspace": ctypes.c_int64, "hclsm_level1_forward_workspace": ctypes.c_int64,
+             "hclsm_slot_attention_workspace": ctypes.c_int64, "hclsm_slot_attention_k_offset": ctypes.c_int64, "hclsm_level1_forward_workspace": ctypes.c_int64,
              "hclsm_relation_graph_workspace": ctypes.c_int64, "hclsm_slot_track_cost_workspace": ctypes.c_int64,
              "hclsm_slot_track_reorder_update_workspace": ctypes.c_int64,
              "hclsm_slot_track_sequence_workspace": ctypes.c_int64,

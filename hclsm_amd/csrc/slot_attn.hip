@@ -2354,6 +2354,13 @@ static int slot_forward_impl(const HclsmSlotWeights* W, const float* inputs, int
   return 0;
 }
 
+extern "C" int64_t hclsm_slot_attention_k_offset(int64_t B, int64_t N, int64_t M, int64_t d_in, int64_t d,
+                                                 int64_t hidden, int dtype) {
+  if (B < 0 || N < 0 || M < 1 || d < 1 || hidden < 1 || d_in < 1) return HCLSM_ERR_SHAPE;
+  if (dtype != HCLSM_BF16 && dtype != HCLSM_F16 && dtype != HCLSM_F32) return HCLSM_ERR_DTYPE;
+  return (int64_t)slot_ws_layout(B, N, M, d, hidden, dtype == HCLSM_F32 ? 4 : 2, true, d_in).kv;
+}
+
 extern "C" int hclsm_slot_attention_forward(const HclsmSlotWeights* W, const float* inputs, int64_t d_in,
                                             const float* slots0, float* slots_out, int64_t B, int64_t N, int64_t M,
                                             int64_t d, int64_t hidden, int64_t n_iter, float scale, float logit_clamp,

@@ -16,6 +16,7 @@ from __future__ import annotations
 import torch
 import torch.nn as nn
 
+from hclsm_amd.kernels._common import warn_fallback
 from hclsm_amd.kernels.sparse_event_attn import (EventIndex, build_event_index, gather_events_packed,
                                                  gather_events_padded, pad_mask_from_index,
                                                  scatter_events_packed, scatter_events_padded)
@@ -57,6 +58,7 @@ class HierarchyManager(nn.Module):
         xs = (level0_states, level1_states, level2_context, obj_mask)
         if torch.is_grad_enabled() and (any(x is not None and x.requires_grad for x in xs) or
                                         any(p.requires_grad for p in self.parameters())):
+            warn_fallback("HierarchyManager", "autograd (the fused top-down output step has no backward)")
             return False
         if not level0_states.is_cuda or level0_states.dtype != torch.float32 or level1_states.shape[1] == 0:
             return False

@@ -13,6 +13,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from hclsm_amd.kernels._common import warn_fallback
 from hclsm_amd.kernels.event_attention import slots_attention
 from hclsm_amd.kernels.level1_packed import Level1Weights, level1_forward_packed
 from hclsm_amd.kernels.sparse_event_attn import EventIndex
@@ -108,6 +109,8 @@ class Level1EventDynamics(nn.Module):
             return level1_forward_packed(event_states, index, obj_mask, W,
                                          out_dtype=event_states.dtype if event_states.dtype in
                                          (torch.float32, dtype) else torch.float32)
+        warn_fallback("Level1EventDynamics.forward_packed", "autograd (projections, LayerNorms and SwiGLU as torch "
+                                                            "ops around the HIP attention core)")
         x = self.proj_in(event_states)
         kpm = None
         if obj_mask is not None:

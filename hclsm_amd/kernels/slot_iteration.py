@@ -169,10 +169,10 @@ def slot_attention_iteration(slots: torch.Tensor, k: torch.Tensor, v: torch.Tens
 
 
 def slot_attention_forward(inputs: torch.Tensor, slots0: torch.Tensor, W: SlotWeights, n_iter: int,
-                           mode: SlotMode = REFERENCE_MODE, scale: float | None = None) -> torch.Tensor:
+                           mode: SlotMode = REFERENCE_MODE, scale: float | None = None, return_k: bool = False):
     """k, v = LN_in(inputs) W_k^T, W_v^T (one MFMA linear over [W_k; W_v]), then n_iter iterations
-    from slots0.  inputs (B, M, d_in), slots0 (B, N, d).  Returns slots (B, N, d) fp32.
-    One C call (3 + 8 * n_iter launches), no host synchronisation."""
+    from slots0.  inputs (B, M, d_in), slots0 (B, N, d).  Returns slots (B, N, d) fp32, and with
+    return_k also a copy of the keys k (B, M, d) in W.dtype.  One C call, no host synchronisation."""
     require_gpu("slot_attention_forward", inputs, slots0)
     B, M, d_in = inputs.shape
     N, d = slots0.shape[1], W.d
@@ -191,4 +191,11 @@ def slot_attention_forward(inputs: torch.Tensor, slots0: torch.Tensor, W: SlotWe
                                         W.hidden, int(n_iter), float(scale), lc, re, sc, code, _lib.ptr(ws),
                                         ws.numel(), _lib.stream_of(x))
     _lib.check(rc, "hclsm_slot_attention_forward")
-    return out
+    if not return_k:
+        return out
+    off = int(L.hclsm_slot_attention_k_offset(B, N, M, d_in, d, W.hidden, code))
+    if off < 0:
+        _lib.check(off, "hclsm_slot_attention_k_offset")
+    nb = B * M * d * torch.tensor([], dtype=W.dtype).element_size()
+    k = ws[off:off + nb].view(W.dtype).view(B, M, d).clone()
+    return out, k

@@ -3,11 +3,12 @@
 Same parameters and names as the reference module (:47-82), so its state dict loads unchanged.
 
 * Without autograd (inference, torch.no_grad): the k/v projections and all n_iterations run as
-  one call of the fused C entry ``hclsm_slot_attention_forward`` (MFMA GEMMs, two-launch
-  attention core, fused GRU) with the reference's in-model semantics: logits clamped to +-30,
-  MLP hidden 4*d, slots clamped to +-50.  Compute dtype fp32, or bf16 under a bf16 autocast.
+  one call of the fused C entry ``hclsm_slot_attention_forward`` (MFMA GEMMs, fused attention
+  core, fused GRU) with the reference's in-model semantics: logits clamped to +-30, MLP hidden
+  4*d, slots clamped to +-50.  Compute dtype fp32, or bf16 under a bf16 autocast.  The keys it
+  computed are reused for the birth attention.
 * With autograd (training): the iteration is torch LayerNorm / Linear / GRUCell around the HIP
-  slot-attention core (differentiable, logit clamp included).
+  slot-attention core (differentiable, logit clamp included), with a HipFallbackWarning.
 Slot initialisation draws from the global RNG as the reference does (:86-96); slot birth
 (:180-199) is vectorised without the reference's host synchronisation and Python loop.
 """
@@ -18,6 +19,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from hclsm_amd.kernels._common import warn_fallback
 from hclsm_amd.kernels.slot_attention_kernel import slot_attention_core
 from hclsm_amd.kernels.slot_iteration import SlotMode, SlotWeights, slot_attention_forward
 
@@ -77,6 +79,8 @@ class DynamicSlotAttention(nn.Module):
         B, M, _ = inputs.shape
         slots = self._init_slots(B, inputs.device)
         if self._needs_grad(inputs):
+            warn_fallback("DynamicSlotAttention", "autograd (LayerNorm / Linear / GRUCell as torch ops around the "
+                                                  "HIP attention core; the fused forward has no backward)")
             x = self.norm_input(inputs)
             k, v = self.project_k(x), self.project_v(x)
             for _ in range(self.n_iterations):
@@ -89,14 +93,14 @@ class DynamicSlotAttention(nn.Module):
                 else torch.float32
             W = SlotWeights.from_module(self, dtype)
             mode = SlotMode(logit_clamp=_LOGIT_CLAMP, renorm_eps=None, slot_clamp=_SLOT_CLAMP)
-            slots = slot_attention_forward(inputs.float(), slots.float(), W, self.n_iterations, mode,
-                                           scale=self.scale).to(inputs.dtype)
-            x = self.norm_input(inputs)
-            k = self.project_k(x)
+            slots, k = slot_attention_forward(inputs.float(), slots.float(), W, self.n_iterations, mode,
+                                              scale=self.scale, return_k=True)
+            slots = slots.to(inputs.dtype)
         alive = torch.sigmoid(self.existence_head(slots).squeeze(-1))              # :167-168
         final_attn = None
         with torch.no_grad():
             q = self.project_q(self.norm_pre_attn(slots))
+            k = k.to(q.dtype)
             _, attn = slot_attention_core(q.detach(), k.detach(), k.detach(), scale=self.scale)   # :172-177
             if return_attention:
                 final_attn = attn

@@ -6,9 +6,9 @@ Same parameters and names as the reference module (:23-66), so its state dict lo
   edge layer, the edge MLP / weight / messages / causal head fused per pair tile on MFMA, node update on
   the MFMA linear kernels); compute in fp32, or bf16 under a bf16 autocast.  Shapes outside that kernel
   (fp32 operands with more than 64 slots, D or d_edge not multiples of 32, d_edge > 192) run the torch
-  path below on the GPU.
+  path below on the GPU, with a HipFallbackWarning.
 * With autograd: the reference's math in torch ops on the GPU (both of its paths: all pairs for N <= 32,
-  :171-188, source-chunked for N > 32, :150-170).
+  :171-188, source-chunked for N > 32, :150-170), with a HipFallbackWarning.
 """
 
 from __future__ import annotations
@@ -16,7 +16,7 @@ from __future__ import annotations
 import torch
 import torch.nn as nn
 
-from hclsm_amd.kernels._common import require_gpu
+from hclsm_amd.kernels._common import require_gpu, warn_fallback
 from hclsm_amd.kernels.relation_graph import GnnWeights, fused_supported, relation_graph_forward
 
 
@@ -87,7 +87,12 @@ class RelationGraph(nn.Module):
         require_gpu("RelationGraph", nodes, alive_mask)
         dtype = torch.bfloat16 if (torch.is_autocast_enabled("cuda") and
                                    torch.get_autocast_dtype("cuda") == torch.bfloat16) else torch.float32
-        if self._needs_grad(nodes) or not fused_supported(nodes.shape[1], self.d_slot, self.d_edge, dtype):
+        if self._needs_grad(nodes):
+            warn_fallback("RelationGraph", "autograd (the fused edge and node kernels have no backward)")
+            return self._torch_forward(nodes, alive_mask)
+        if not fused_supported(nodes.shape[1], self.d_slot, self.d_edge, dtype):
+            warn_fallback("RelationGraph", f"shape outside the fused kernels (N={nodes.shape[1]}, d_slot={self.d_slot}, "
+                                           f"d_edge={self.d_edge}, {dtype})")
             return self._torch_forward(nodes, alive_mask)
         W = GnnWeights.from_module(self, dtype)
         out, causal = relation_graph_forward(nodes, alive_mask, W, self.n_rounds, chunked=nodes.shape[1] > 32)

@@ -7,7 +7,7 @@ unchanged.
   (B, N, N, 3D) pair tensor, Sinkhorn in registers, fused gather + GRU gates); compute in fp32, or bf16
   under a bf16 autocast.  ``track`` runs the whole frame loop of hclsm/model.py:229-252 in one call.
 * With autograd, or for shapes outside those kernels (d_slot not a multiple of 64 or above 384, more than
-  128 slots): the reference's math in torch ops on the GPU.
+  128 slots): the reference's math in torch ops on the GPU, with a HipFallbackWarning.
 """
 
 from __future__ import annotations
@@ -15,7 +15,7 @@ from __future__ import annotations
 import torch
 import torch.nn as nn
 
-from hclsm_amd.kernels._common import require_gpu
+from hclsm_amd.kernels._common import require_gpu, warn_fallback
 from hclsm_amd.kernels.slot_tracker import (SINKHORN_ITERS, SINKHORN_TEMPERATURE, TrackerWeights, track_cost,
                                             track_match, track_reorder_update, track_sequence, track_supported)
 
@@ -57,8 +57,14 @@ class SlotTracker(nn.Module):
         return any(x is not None and x.requires_grad for x in xs) or any(p.requires_grad for p in self.parameters())
 
     def _fused(self, N: int, *xs, sequence: bool = False) -> TrackerWeights | None:
+        """The kernels' weights, or None (with a HipFallbackWarning) when this call runs torch ops."""
         dtype = self._dtype()
-        if self._needs_grad(*xs) or not track_supported(N, self.d_slot, dtype, sequence):
+        if self._needs_grad(*xs):
+            warn_fallback("SlotTracker", "autograd (the fused cost, match and GRU kernels have no backward)")
+            return None
+        if not track_supported(N, self.d_slot, dtype, sequence):
+            warn_fallback("SlotTracker", f"shape outside the fused kernels (N={N}, d_slot={self.d_slot}, {dtype}"
+                                         f"{', sequence' if sequence else ''})")
             return None
         return TrackerWeights.from_module(self, dtype)
 
@@ -88,6 +94,8 @@ class SlotTracker(nn.Module):
         if not cost.requires_grad and cost.shape[1] <= 128:
             perm, matched, _ = track_match(cost, alive_t, alive_t1)
             return perm, matched
+        warn_fallback("SlotTracker", "Sinkhorn matching as torch ops (autograd through the cost, or more than "
+                                     "128 slots)")
         perm, confidence = sinkhorn_matching(torch.clamp(cost, -1e4, 1e4))
         matched = ((alive_t > 0.5).float() * (alive_t1 > 0.5).float().gather(1, perm) *
                    (confidence > 0.3).float())

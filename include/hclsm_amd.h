@@ -320,6 +320,15 @@ int64_t hclsm_slot_attention_workspace(int64_t B, int64_t N, int64_t M, int64_t 
                                        int dtype);
 
 /*
+ * Byte offset, inside the workspace of hclsm_slot_attention_forward, of the token keys it computed:
+ * k = LN_in(inputs) W_k^T as [B*M, d] row-major in `dtype`, valid after the forward until the workspace is
+ * reused (or a negative error code).  Lets a caller reuse the keys (slot birth, dynamic_slots.py:170-177)
+ * instead of recomputing norm_input + project_k.
+ */
+int64_t hclsm_slot_attention_k_offset(int64_t B, int64_t N, int64_t M, int64_t d_in, int64_t d, int64_t hidden,
+                                      int dtype);
+
+/*
  * One slot-attention iteration (objects/dynamic_slots.py:98-131) for B frames of N slots:
  *   q = LN_pre(slots) W_q^T; attention core (logit clamp, renorm as above); GRUCell; slots + MLP(LN(.));
  *   clamp to +-slot_clamp if slot_clamp > 0.  slots_in / slots_out [B, N, d] float32 (may alias);
