@@ -91,3 +91,32 @@ def test_presets_match_reference_configs():
         c = preset_config(name)
         assert (c.objects.d_slot, c.objects.n_max_slots) == (d_slot, slots)
         assert (c.dynamics.level1.d_model, c.dynamics.level1.n_layers, c.dynamics.level1.n_heads) == l1
+
+
+@pytest.mark.parametrize("preset", ["tiny", "small", "base", "large"])
+def test_module_trees_match_the_reference_modules(preset):
+    """State-dict keys and shapes of every hot-path module, and the preset's hot-path config fields, against
+    the reference's own modules built from its presets (tests/golden/reference_state_names.json, written by
+    tests/golden/make_reference_state_names.py from hclsm/config.py and the reference module classes)."""
+    import json
+    from pathlib import Path
+    from hclsm_amd.checkpoint import PRESETS
+    from hclsm_amd.dynamics import HierarchyManager, Level0SSM, Level1EventDynamics
+    from hclsm_amd.objects import DynamicSlotAttention, RelationGraph, SlotTracker
+    ref = json.loads((Path(__file__).resolve().parent / "golden" / "reference_state_names.json").read_text())[preset]
+    p = PRESETS[preset]
+    rc = ref["config"]
+    assert {k: p[k] for k in ("d_world", "d_slot", "n_max_slots", "n_iterations", "d_edge", "gnn_rounds", "d_state",
+                              "n_blocks", "l2_d_model")} == {k: rc[k] for k in ("d_world", "d_slot", "n_max_slots",
+                                                                              "n_iterations", "d_edge", "gnn_rounds",
+                                                                              "d_state", "n_blocks", "l2_d_model")}
+    assert list(p["l1"]) == rc["l1"] and rc["expand_ratio"] == 2
+    cfg = preset_config(preset)
+    ob, dy = cfg.objects, cfg.dynamics
+    mods = {"slot_attention": DynamicSlotAttention(ob, cfg.d_world), "slot_tracker": SlotTracker(ob),
+            "relation_graph": RelationGraph(ob), "level0_ssm": Level0SSM(dy.level0, ob.d_slot),
+            "level1_event": Level1EventDynamics(dy.level1, ob.d_slot),
+            "hierarchy_manager": HierarchyManager(ob.d_slot, dy.level2.d_model)}
+    for name, m in mods.items():
+        got = {k: list(v.shape) for k, v in m.state_dict().items()}
+        assert got == ref["modules"][name], name

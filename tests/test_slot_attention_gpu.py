@@ -165,9 +165,9 @@ def test_config2_forward_bf16():
     ("reference", torch.float16, 2, 16, 33, 64, 64, 256),
     ("config2", torch.float16, 4, 32, 196, 128, 160, 384),
 ])
-def test_forward_two_launch_iteration_matches_oracle(mode_name, dtype, B, N, M, d, d_in, hidden):
-    """hclsm_slot_attention_forward with 16-bit operands runs each iteration as two launches
-    (attention block per frame, GRU + MLP block per 16 rows); result against the oracle."""
+def test_forward_iteration_matches_oracle(mode_name, dtype, B, N, M, d, d_in, hidden):
+    """hclsm_slot_attention_forward with 16-bit operands (per iteration: LayerNorm-folded q projection,
+    attention core, GRU, MLP), partial tiles and ragged token counts; result against the oracle."""
     from hclsm_amd.kernels import slot_iteration as si
     from hclsm_amd.workloads import xavier_uniform
     g = torch.Generator().manual_seed(B * 100 + N + M)
