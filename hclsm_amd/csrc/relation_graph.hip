@@ -317,7 +317,7 @@ __device__ __forceinline__ void stage_permuted(const T* __restrict__ W, int ldw,
   }
 }
 
-template <int DT, int D, int E, int NW, bool MSG, bool CAUS>
+template <int DT, int D, int E, int NW, bool MSG, bool CAUS, bool MP>
 __global__ void __launch_bounds__(64 * NW)
 gnn_edge_res_kernel(GnnArgs a, const float* __restrict__ nstat) {
   using A = MM<DT>;
@@ -441,9 +441,9 @@ gnn_edge_res_kernel(GnnArgs a, const float* __restrict__ nstat) {
         hh += __shfl_xor(hh, 32, 64);
         const int64_t rowj = f * N + (jj[pt] < N ? jj[pt] : N - 1);
         const float qj = nstat[2 * rowj + 1];
-        const float mu = a.norm ? (2.f * si + gg) * inv4d : 0.f;
+        const float mu = MP ? 0.f : (2.f * si + gg) * inv4d;
         const float m2 = (2.f * qi + 2.f * qj - 2.f * gg + hh) * inv4d;
-        const float rs = a.norm ? 1.f / sqrtf(fmaxf(m2 - mu * mu, 0.f) + a.eps) : 1.f;
+        const float rs = MP ? 1.f : 1.f / sqrtf(fmaxf(m2 - mu * mu, 0.f) + a.eps);
         const float* Q = a.PQ + rowj * 2 * H1 + H1 + 4 * g;
 #pragma unroll
         for (int t0 = 0; t0 < NT1; t0 += 3) {
@@ -503,7 +503,7 @@ gnn_edge_res_kernel(GnnArgs a, const float* __restrict__ nstat) {
           ebp[pt][t][0] = pack2<T>(ev[0], ev[1]);
           ebp[pt][t][1] = pack2<T>(ev[2], ev[3]);
           const int je = jj[pt] - a.ej0;
-          if (a.edges && jj[pt] < N && je >= 0 && je < a.enj)
+          if (MP && a.edges && jj[pt] < N && je >= 0 && je < a.enj)
             *reinterpret_cast<float4*>(a.edges + (rowi * a.enj + je) * E + 16 * t + 4 * g) =
                 make_float4(A::tof(ev[0]), A::tof(ev[1]), A::tof(ev[2]), A::tof(ev[3]));
         }
@@ -621,7 +621,7 @@ __device__ __forceinline__ void static_for(F&& f) {
   (std::make_integer_sequence<int, N_>{});
 }
 
-template <int DT, int D, int E, int NW, bool MSG, bool CAUS>
+template <int DT, int D, int E, int NW, bool MSG, bool CAUS, bool MP>
 __global__ void __launch_bounds__(64 * NW)
 gnn_edge_str_kernel(GnnArgs a, const float* __restrict__ nstat) {
   using A = MM<DT>;
@@ -793,9 +793,9 @@ gnn_edge_str_kernel(GnnArgs a, const float* __restrict__ nstat) {
             hs += __shfl_xor(hs, 16, 64);
             hs += __shfl_xor(hs, 32, 64);
             const float qj = nstat[2 * rowj + 1];
-            const float mu = a.norm ? (2.f * si + gs) * inv4d : 0.f;
+            const float mu = MP ? 0.f : (2.f * si + gs) * inv4d;
             const float m2 = (2.f * qi + 2.f * qj - 2.f * gs + hs) * inv4d;
-            const float rs = a.norm ? 1.f / sqrtf(fmaxf(m2 - mu * mu, 0.f) + a.eps) : 1.f;
+            const float rs = MP ? 1.f : 1.f / sqrtf(fmaxf(m2 - mu * mu, 0.f) + a.eps);
             const float* P = a.PQ + rowi * 2 * H1 + 4 * g;
             const float* Q = a.PQ + rowj * 2 * H1 + H1 + 4 * g;
 #pragma unroll
@@ -851,7 +851,7 @@ gnn_edge_str_kernel(GnnArgs a, const float* __restrict__ nstat) {
               ebp[t][0] = pack2<T>(ev[0], ev[1]);
               ebp[t][1] = pack2<T>(ev[2], ev[3]);
               const int je = j - a.ej0;
-              if (a.edges && live_row && j < N && je >= 0 && je < a.enj)
+              if (MP && a.edges && live_row && j < N && je >= 0 && je < a.enj)
                 *reinterpret_cast<float4*>(a.edges + (rowi * a.enj + je) * E + 16 * t + 4 * g) =
                     make_float4(A::tof(ev[0]), A::tof(ev[1]), A::tof(ev[2]), A::tof(ev[3]));
             }
@@ -1087,20 +1087,20 @@ static bool edges_fit(const GnnArgs& a) {
   else return edge_lds<DT, 8, 32>(a) <= GNN_LDS_MAX;
 }
 
-template <int DT, int D, int E, bool MSG, bool CAUS>
+template <int DT, int D, int E, bool MSG, bool CAUS, bool MP = false>
 static int launch_edges_res(const GnnArgs& a, const float* nstat, hipStream_t st) {
   constexpr int NW = 8;
   constexpr size_t lds = GnnRes<D, E, MSG, CAUS>::total;
   static_assert(lds <= GNN_LDS_MAX, "resident weights exceed the LDS");
   static std::atomic<int> setup[HCLSM_MAX_DEVICES];   // resident workgroups per device (persistent kernel)
   int grid = 0;
-  const int se = device_launch_setup(reinterpret_cast<const void*>(&gnn_edge_res_kernel<DT, D, E, NW, MSG, CAUS>),
+  const int se = device_launch_setup(reinterpret_cast<const void*>(&gnn_edge_res_kernel<DT, D, E, NW, MSG, CAUS, MP>),
                                      64 * NW, lds, (int)GNN_LDS_MAX, setup, &grid);
   if (se) return se;
   const int64_t units = (int64_t)a.F * a.N;
   const int64_t need = (units + NW - 1) / NW;
   const unsigned g = (unsigned)(need < grid ? need : grid);
-  hipLaunchKernelGGL((gnn_edge_res_kernel<DT, D, E, NW, MSG, CAUS>), dim3(g), dim3(64 * NW), lds, st, a, nstat);
+  hipLaunchKernelGGL((gnn_edge_res_kernel<DT, D, E, NW, MSG, CAUS, MP>), dim3(g), dim3(64 * NW), lds, st, a, nstat);
   HCLSM_LAUNCH_CHECK();
   return 0;
 }
@@ -1110,6 +1110,9 @@ static int launch_edges_res(const GnnArgs& a, const float* nstat, hipStream_t st
 template <int DT, int D, int E>
 static int edges_res_shape(const GnnArgs& a, const float* nstat, hipStream_t st) {
   const bool msg = a.agg != nullptr, caus = a.causal != nullptr;
+  // gnn_message_pass (no pair norm, edge-feature output, messages without the causal head) is an instantiation
+  // of its own: with the norm switch and the edge stores as run-time branches the other variants spill.
+  if (!a.norm) return msg && !caus ? launch_edges_res<DT, D, E, true, false, true>(a, nstat, st) : 1;
   if (msg && caus) {
     if constexpr (GnnRes<D, E, true, true>::total <= GNN_LDS_MAX) {
       return launch_edges_res<DT, D, E, true, true>(a, nstat, st);
@@ -1126,19 +1129,19 @@ static int edges_res_shape(const GnnArgs& a, const float* nstat, hipStream_t st)
   return 0;
 }
 
-template <int DT, int D, int E, bool MSG, bool CAUS>
+template <int DT, int D, int E, bool MSG, bool CAUS, bool MP = false>
 static int launch_edges_str(const GnnArgs& a, const float* nstat, hipStream_t st) {
   constexpr int NW = 4;   // one wave per SIMD: the accumulators can use the AGPRs
   constexpr size_t lds = GnnStr<D, E, MSG, CAUS>::total;
   static_assert(lds <= GNN_LDS_MAX, "chunk buffers exceed the LDS");
   static std::atomic<int> setup[HCLSM_MAX_DEVICES];   // resident workgroups per device (persistent kernel)
   int grid = 0;
-  const int se = device_launch_setup(reinterpret_cast<const void*>(&gnn_edge_str_kernel<DT, D, E, NW, MSG, CAUS>),
+  const int se = device_launch_setup(reinterpret_cast<const void*>(&gnn_edge_str_kernel<DT, D, E, NW, MSG, CAUS, MP>),
                                      64 * NW, lds, (int)GNN_LDS_MAX, setup, &grid);
   if (se) return se;
   const int64_t groups = ((int64_t)a.F * a.N + NW - 1) / NW;
   const unsigned g = (unsigned)(groups < grid ? groups : grid);
-  hipLaunchKernelGGL((gnn_edge_str_kernel<DT, D, E, NW, MSG, CAUS>), dim3(g), dim3(64 * NW), lds, st, a, nstat);
+  hipLaunchKernelGGL((gnn_edge_str_kernel<DT, D, E, NW, MSG, CAUS, MP>), dim3(g), dim3(64 * NW), lds, st, a, nstat);
   HCLSM_LAUNCH_CHECK();
   return 0;
 }
@@ -1146,6 +1149,7 @@ static int launch_edges_str(const GnnArgs& a, const float* nstat, hipStream_t st
 template <int DT, int D, int E>
 static int edges_str_shape(const GnnArgs& a, const float* nstat, hipStream_t st) {
   const bool msg = a.agg != nullptr, caus = a.causal != nullptr;
+  if (!a.norm) return msg && !caus ? launch_edges_str<DT, D, E, true, false, true>(a, nstat, st) : 1;
   if (msg && caus) return launch_edges_str<DT, D, E, true, true>(a, nstat, st);
   if (msg) return launch_edges_str<DT, D, E, true, false>(a, nstat, st);
   if (caus) return launch_edges_str<DT, D, E, false, true>(a, nstat, st);
