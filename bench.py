@@ -36,6 +36,9 @@ PEAK_CLOCK_GHZ = 2.4
 NSETS = 4
 
 
+LEGS = ("slot", "events", "chain", "context", "block", "bwd", "level1", "gnn", "track")
+
+
 def _parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
@@ -43,6 +46,9 @@ def _parse():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extra", action="store_true", help="time only the config-1 scan (configs 2-4 skipped)")
+    p.add_argument("--legs", default=",".join(LEGS),
+                   help="comma-separated sub-benchmarks to run after the metric (default: all of "
+                        + ",".join(LEGS) + ")")
     p.add_argument("--copy-calibration", action="store_true",
                    help="after the timed loop, run a 1 GiB device-to-device copy 5 times (a kernel of "
                         "known traffic for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE counters)")
@@ -163,7 +169,7 @@ def _bench_slot(dev, n, warmup, cpu):
 def _bench_events(dev, n, warmup, cpu):
     """Config 3: event index + per-track causal attention, 1024 tracks x T=64, 6 x 64 heads, p=0.15."""
     import torch
-    from hclsm_amd.kernels.event_attention import track_causal_event_attention
+    from hclsm_amd.kernels.event_attention import TrackCausalPlan
     from hclsm_amd.kernels.sparse_event_attn import build_event_index
     g = torch.Generator().manual_seed(1003)
     q, k, v = (torch.randn(1024, 64, 6, 64, generator=g).to(torch.bfloat16).to(dev) for _ in range(3))
@@ -171,13 +177,12 @@ def _bench_events(dev, n, warmup, cpu):
     m[:, 0] = 1
     m = m.to(dev)
     total = build_event_index(m).total()
-
-    def step():
-        track_causal_event_attention(q, k, v, m, capacity=total)
+    step = TrackCausalPlan(q, k, v, m, capacity=total)   # checks and buffers once; each step is the library call
     med, avg = _event_timing(step, n, warmup)
     nbytes = total * 6 * 64 * 2 * 4 + m.numel() * 4 + (1025 + 2 * total + 2 * 65536) * 4
     res = {"workload": "config 3: 1024 tracks x T=64, 6 heads x 64, p=0.15 (t=0 forced), bf16, "
-                        "index build + causal event attention, packed output (one library call)",
+                        "index build + causal event attention, packed output (one library call per step through "
+                        "TrackCausalPlan: arguments checked and output / index buffers allocated once)",
             "events": total, "metric": "event-tokens/s", "value": round(total / med, 1),
             "grid_tokens_per_s": round(65536 / med, 1), "median_us": round(med * 1e6, 2),
             "roofline": {"bound": "hbm", "achieved": round(nbytes / med / 1e9, 2), "peak": HBM_PEAK_GBS,
@@ -443,7 +448,7 @@ def _bench_chain(dev, n, warmup, cpu):
     (hclsm_amd.workloads.chain_config's draw)."""
     import torch
     from hclsm_amd import _lib
-    from hclsm_amd.kernels.event_attention import track_causal_event_attention
+    from hclsm_amd.kernels.event_attention import TrackCausalPlan
     from hclsm_amd.kernels.sparse_event_attn import build_event_index
     from hclsm_amd.workloads import chain_config, scan_algorithmic_bytes
     from oracle.ssm_scan import normwise_rel_err, ssm_scan_ref
@@ -470,9 +475,7 @@ def _bench_chain(dev, n, warmup, cpu):
         scan(ys[0], ys[1])
 
     total = build_event_index(m).total()
-
-    def attn():
-        track_causal_event_attention(q, k, v, m, capacity=total)
+    attn = TrackCausalPlan(q, k, v, m, capacity=total)
 
     # parity spot check of the first scan on 2 sequences
     scan(x0, ys[0])
@@ -495,7 +498,7 @@ def _bench_chain(dev, n, warmup, cpu):
            "attn_us": round(a_med * 1e6, 2), "event_tokens_per_s": round(total / a_med, 1),
            "scan_roofline": {"bound": "hbm", "achieved": round(4 * sb / s_med / 1e9, 2), "peak": HBM_PEAK_GBS,
                              "unit": "GB/s", "frac": round(4 * sb / s_med / 1e9 / HBM_PEAK_GBS, 4),
-                             "bytes_per_call": sb, "kernel": "ssm_scan_fwd_mfma_kernel<raw,TC=8,DPL=2>"},
+                             "bytes_per_call": sb, "kernel": "ssm_scan_fwd_mfma_kernel<raw,TC=2,DPL=2>"},
            "attn_roofline": {"bound": "hbm", "achieved": round(ab / a_med / 1e9, 2), "peak": HBM_PEAK_GBS,
                              "unit": "GB/s", "frac": round(ab / a_med / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_call": ab,
                              "kernel": "event_attn_kernel<bf16, causal per track> + index build"},
@@ -616,7 +619,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": ctr.get("hbm_bytes_per_launch"),
                      "traffic_source": ctr.get("source"),
-                     "kernel": "ssm_scan_fwd_mfma_kernel<raw,TC=8,DPL=2>",
+                     "kernel": "ssm_scan_fwd_mfma_kernel<raw,TC=4,DPL=2>",
                      "avg_launch_us": round(avg * 1e6, 3), "median_launch_us": round(med * 1e6, 3),
                      "p10_launch_us": round(p10 * 1e6, 3), "p90_launch_us": round(p90 * 1e6, 3)},
         "roofline_valu": _valu_roofline(ctr, avg),
@@ -624,15 +627,24 @@ def main():
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = _cpu_baseline(d)
     if not args.no_extra:
-        out["slot_attn"] = _bench_slot(dev, 100, 10, not args.no_cpu_baseline)
-        out["event_attn"] = _bench_events(dev, 100, 10, not args.no_cpu_baseline)
-        out["chain"] = _bench_chain(dev, 20, 3, not args.no_cpu_baseline)
-        out["scan_context"] = _bench_scan_context(dev, 30, 10)
-        out["block_scan"] = _bench_block_scan(dev, 50, 5)
-        out["scan_bwd"] = _bench_scan_bwd(dev, 50, 5)
-        out["level1"] = _bench_level1(dev, 30, 3)
-        out["gnn"] = _bench_gnn(dev, 20, 3)
-        out["track"] = _bench_track(dev, 20, 3)
+        legs = set(args.legs.split(",")) if args.legs else set()
+        unknown = legs - set(LEGS)
+        if unknown:
+            raise SystemExit(f"bench.py: unknown --legs {sorted(unknown)}; choose from {','.join(LEGS)}")
+        cpu = not args.no_cpu_baseline
+        runs = {"slot": ("slot_attn", lambda: _bench_slot(dev, 100, 10, cpu)),
+                "events": ("event_attn", lambda: _bench_events(dev, 100, 10, cpu)),
+                "chain": ("chain", lambda: _bench_chain(dev, 20, 3, cpu)),
+                "context": ("scan_context", lambda: _bench_scan_context(dev, 30, 10)),
+                "block": ("block_scan", lambda: _bench_block_scan(dev, 50, 5)),
+                "bwd": ("scan_bwd", lambda: _bench_scan_bwd(dev, 50, 5)),
+                "level1": ("level1", lambda: _bench_level1(dev, 30, 3)),
+                "gnn": ("gnn", lambda: _bench_gnn(dev, 20, 3)),
+                "track": ("track", lambda: _bench_track(dev, 20, 3))}
+        for leg in LEGS:
+            if leg in legs:
+                key, fn = runs[leg]
+                out[key] = fn()
     print(json.dumps(out), flush=True)
 
 

@@ -148,6 +148,13 @@ def dtype_code(dt: torch.dtype) -> int:
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
+def stream_of_device(device_index: int) -> int:
+    """hipStream_t of torch's current stream on a device given by index."""
+    if _raw_stream is not None:
+        return _raw_stream(device_index)
+    return torch.cuda.current_stream(device_index).cuda_stream
+
+
 def stream_of(t: torch.Tensor) -> int:
     """hipStream_t of torch's current stream on t's device."""
     if _raw_stream is not None:

@@ -33,6 +33,9 @@ HIPCC_FLAGS = [
 # VALU ops every step; the VGPR form of MFMA avoids an AGPR<->VGPR copy of all 16 states.
 FILE_FLAGS = {
     "ssm_scan.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    # The attention's score and output tiles are consumed by VALU code right after each MFMA; in the VGPR
+    # form they need no AGPR copies and the kernel takes fewer registers (more waves per SIMD).
+    "event_attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 
 

@@ -65,5 +65,7 @@ constexpr int HCLSM_MAX_DEVICES = 64;
 // many workgroups of `threads` threads using `lds` bytes the device holds at once (multiprocessors x occupancy).
 // cache: the call site's per-device slots (0 = not set up).  *grid gets the count.  Defined in launch.hip.
 int device_launch_setup(const void* fn, int threads, size_t lds, int max_lds, std::atomic<int>* cache, int* grid);
+// Compute units of the current device (cached per device).  Defined in launch.hip.
+int device_cus(int* cus);
 
 }  // namespace hclsm

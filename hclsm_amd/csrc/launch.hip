@@ -22,4 +22,19 @@ int device_launch_setup(const void* fn, int threads, size_t lds, int max_lds, st
   return 0;
 }
 
+int device_cus(int* cus) {
+  static std::atomic<int> cache[HCLSM_MAX_DEVICES];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= HCLSM_MAX_DEVICES) return HCLSM_ERR_UNSUPPORTED;
+  int c = cache[dev].load(std::memory_order_relaxed);
+  if (c == 0) {
+    if ((e = hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return (int)e;
+    cache[dev].store(c, std::memory_order_relaxed);
+  }
+  *cus = c;
+  return 0;
+}
+
 }  // namespace hclsm

@@ -1627,7 +1627,9 @@ static int launch_core(const void* q, int64_t ldq, int64_t qbs, const void* k, i
 }
 
 // The fused core (16-bit operands, v transposed) when the shape fits its instantiations; 1 otherwise.  Column
-// blocks per frame: 128-column blocks for D = 384 / 256, one block for D = 192 / 128.
+// blocks per frame: eight 48-column blocks for D = 384 (config 2: 256 workgroups, one per CU; each block
+// recomputes the frame's logits, and against three 128-column blocks the wider grid still wins by ~2.5 us per
+// forward), 128-column blocks for D = 256, one block for D = 192 / 128.
 static int launch_core_fused(const void* q, int64_t ldq, int64_t qbs, const void* k, int64_t ldk, int64_t kbs,
                              const void* vt, int64_t vbs, void* out, int64_t ldo, int64_t obs, int64_t B, int64_t N,
                              int64_t M, int64_t D, float scale, float denom_eps, float logit_clamp, float renorm_eps,
@@ -1655,7 +1657,7 @@ static int launch_core_fused(const void* q, int64_t ldq, int64_t qbs, const void
     return 0;                                                                                                  \
   }
 #define HCLSM_CF_D(DT_, NT_) \
-  HCLSM_CF(DT_, NT_, 128, 1) HCLSM_CF(DT_, NT_, 192, 1) HCLSM_CF(DT_, NT_, 256, 2) HCLSM_CF(DT_, NT_, 384, 3)
+  HCLSM_CF(DT_, NT_, 128, 1) HCLSM_CF(DT_, NT_, 192, 1) HCLSM_CF(DT_, NT_, 256, 2) HCLSM_CF(DT_, NT_, 384, 8)
   HCLSM_CF_D(HCLSM_BF16, 1) HCLSM_CF_D(HCLSM_BF16, 2)
   HCLSM_CF_D(HCLSM_F16, 1) HCLSM_CF_D(HCLSM_F16, 2)
 #undef HCLSM_CF_D
@@ -2197,14 +2199,8 @@ static int linear_ln_fold(const float* x, int64_t ldx, const void* w, int64_t ld
   // the LN variant keeps the rows, gamma and beta in registers (two workgroups per CU): taken only when the
   // tiles fit one such round on the device, where it beats a LayerNorm launch plus the linear layer
   const int64_t tiles = ((M + 31) / 32) * ((N + 31) / 32);
-  static std::atomic<int> cu_count[HCLSM_MAX_DEVICES];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= HCLSM_MAX_DEVICES) return 0;
-  int cus = cu_count[dev].load(std::memory_order_relaxed);
-  if (cus == 0) {
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return 0;
-    cu_count[dev].store(cus, std::memory_order_relaxed);
-  }
+  int cus = 0;
+  if (device_cus(&cus) != 0 || cus <= 0) return 0;
   if (tiles > 2 * (int64_t)cus) return 0;
   if ((dtype != HCLSM_BF16 && dtype != HCLSM_F16) || M <= 0 || N <= 0 || K <= 0 || K % 32 || K > 384 || !al16(x) ||
       ldx % 4 || !al16(w) || ldw % 8 || (lnw && !al16(lnw)) || (lnb && !al16(lnb)) ||

@@ -15,7 +15,7 @@
 // For bf16 I/O with d_state 16 the rank-1 input term dt*x*B and its add into h
 // run on the matrix core instead (ssm_scan_fwd_mfma_kernel below), which leaves
 // mul, exp, mul, fma per state update on the VALU.
-#include "common.h"
+#include "internal.h"
 
 namespace hclsm {
 
@@ -596,6 +596,17 @@ ssm_scan_fwd_mfma_kernel(const uint16_t* __restrict__ x, const uint16_t* __restr
   gates(dv[0]);
   const int tfull = T - T % TC;
   for (int t0 = 0; t0 < tfull; t0 += TC) {
+    // Issue priority falls with progress, by quarters of T.  The waves of a SIMD start together; with
+    // equal priorities the sequencer issues oldest-first, so they would run almost one after another and
+    // leave the last wave of each SIMD alone -- at about half the issue rate -- for the last third of the
+    // launch.  A wave that gets a quarter ahead now yields to the others, and they finish close together.
+    {
+      const int pr = (4 * t0) / T;
+      if (pr == 0) __builtin_amdgcn_s_setprio(3);
+      else if (pr == 1) __builtin_amdgcn_s_setprio(2);
+      else if (pr == 2) __builtin_amdgcn_s_setprio(1);
+      else __builtin_amdgcn_s_setprio(0);
+    }
     uint32_t xn[TC], dn[TC], gn[GC];
     uint16_t bn[TC];
     load(t0 + TC, xn, dn, bn, gn);
@@ -651,9 +662,24 @@ static int try_scan_sgpr(const void* x, const void* dt, const float* A_log, cons
   }
   if constexpr (DT == HCLSM_BF16) {
     if (S == 16 && T * Dn * 2 < 0x7fffffffLL) {
-      constexpr int TCM = MODE == SCAN_BLOCK ? 4 : 8;   // the gate prefetch costs registers: shorter chunks
-      if (pair) return launch_scan_mfma<MODE, TCM, 2>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, st, epi);
-      return launch_scan_mfma<MODE, TCM, 1>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, st, epi);
+      // Steps per prefetched chunk: 4 while the grid is at most one round of three waves per SIMD (131 VGPRs,
+      // three waves fit); past that 2 (120 VGPRs: four waves per SIMD, fewer rounds).  Measured on MI355X
+      // (same-run A/B against 8-step chunks): config 1 (three waves per SIMD) 65.7 -> 64.2 us with 4, 65.5 with
+      // 2; config 4 (six per SIMD) 1833 -> 1795 us with 2, 1822 with 4.
+      if constexpr (MODE == SCAN_BLOCK) {   // the gate prefetch costs registers: 4-step chunks throughout
+        if (pair) return launch_scan_mfma<MODE, 4, 2>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, st, epi);
+        return launch_scan_mfma<MODE, 4, 1>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, st, epi);
+      } else {
+        int cus = 0;
+        const int rc = device_cus(&cus);
+        if (rc) return rc;
+        const int64_t waves = batch * ((Dn / (pair ? 2 : 1) + 63) / 64);
+        const bool many = waves > 3 * 4 * (int64_t)cus;   // more than three waves per SIMD
+        if (pair && many) return launch_scan_mfma<MODE, 2, 2>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, st, epi);
+        if (pair) return launch_scan_mfma<MODE, 4, 2>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, st, epi);
+        if (many) return launch_scan_mfma<MODE, 2, 1>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, st, epi);
+        return launch_scan_mfma<MODE, 4, 1>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, st, epi);
+      }
     }
     HCLSM_SCAN_SGPR(4)
     HCLSM_SCAN_SGPR(8)

@@ -124,12 +124,17 @@ template <int N_, int MASK_LO> struct RSCount {  // values left per lane after R
 };
 
 struct BwdArgs {
-  int T, Dn, S, nchunk, DW;
-  int64_t ld_ck;  // floats per (n, chunk) checkpoint slab = Dn * SP
+  int T, Dn, S, nchunk, nck, DW;   // nck = checkpoints per sequence = ceil(nchunk / BWD_CKR)
+  int64_t ld_ck;  // floats per (n, checkpoint) slab = Dn * SP
 };
 
 // Steps of B / C rows staged in LDS at a time (a multiple of every chunk length K).
 constexpr int BWD_WT = 64;
+// Chunks per checkpoint: pass 1 stores the state at the start of every BWD_CKR-th chunk, and pass 2 steps
+// forward from there to the start of the chunks in between.  Checkpoints are the largest HBM stream of the
+// backward (16 fp32 states per channel per chunk, written and read back); every other chunk halves it for
+// one extra forward chunk in two.  The chunks of a checkpoint share one B / C window.
+constexpr int BWD_CKR = 2;
 
 template <int DT, int SP, int MODE>
 __global__ void __launch_bounds__(BWD_MAX_THREADS)
@@ -146,6 +151,7 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
   constexpr int VL = RSCount<SG, G>::value;       // values per lane after reduce-scattering gB (then gC)
   constexpr int WMAX = BWD_MAX_THREADS / 64;
   static_assert(BWD_WT % K == 0, "an LDS window holds whole chunks");
+  static_assert((BWD_WT / K) % BWD_CKR == 0, "the chunks of a checkpoint share one LDS window");
   __shared__ float red[K][WMAX][2 * SP];           // per-chunk wave partials of gB | gC
   __shared__ __align__(16) float sB[BWD_WT][SP];   // B / C rows of the current window, fp32; states >= S
   __shared__ __align__(16) float sC[BWD_WT][SP];   // and steps >= T are zero
@@ -216,7 +222,7 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
       dto[i] = buf_ld<DT>(rdt, vo, so);
     }
   };
-  float* ck = ckpt + (size_t)n * a.nchunk * a.ld_ck + (size_t)dd * SP + s0;
+  float* ck = ckpt + (size_t)n * a.nck * a.ld_ck + (size_t)dd * SP + s0;
 
   // ---- pass 1: forward recompute, checkpoint at every chunk start; the next chunk's x / dt are in
   // flight while a chunk is stepped
@@ -238,9 +244,9 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
       }
       float xn[K], dn[K];
       ld_chunk(c + 1, xn, dn);
-      if (act)
+      if (act && c % BWD_CKR == 0)
 #pragma unroll
-        for (int j = 0; j < SG; ++j) ck[(size_t)c * a.ld_ck + j] = h[j];
+        for (int j = 0; j < SG; ++j) ck[(size_t)(c / BWD_CKR) * a.ld_ck + j] = h[j];
 #pragma unroll
       for (int i = 0; i < K; ++i) {
         const float dtv = dt_of(dc[i], i < len);
@@ -267,7 +273,7 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
     const int w0 = t0 / BWD_WT * BWD_WT;
     float hc[SG], xs[K], ds[K], gs[K];
 #pragma unroll
-    for (int j = 0; j < SG; ++j) hc[j] = act ? ck[(size_t)c * a.ld_ck + j] : 0.f;
+    for (int j = 0; j < SG; ++j) hc[j] = act ? ck[(size_t)(c / BWD_CKR) * a.ld_ck + j] : 0.f;
     ld_chunk(c, xs, ds);
 #pragma unroll
     for (int i = 0; i < K; ++i) {
@@ -278,6 +284,20 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
       stage(w0, true);
       __syncthreads();
       wcur = w0;
+    }
+    // from the checkpoint to this chunk's start: the chunks in between, forward (full chunks, same window)
+    for (int cc = c - c % BWD_CKR; cc < c; ++cc) {
+      float xr[K], dr[K];
+      ld_chunk(cc, xr, dr);
+#pragma unroll
+      for (int i = 0; i < K; ++i) {
+        const float dtv = dt_of(dr[i], true);
+        const float u = dtv * xr[i];
+        float bv[SG];
+        row(sB, cc * K + i - w0, bv);
+#pragma unroll
+        for (int j = 0; j < SG; ++j) hc[j] = fmaf(fast_exp2(dtv * a2[j]), hc[j], u * bv[j]);
+      }
     }
     // recompute the chunk's states h_{t0+i} into hk (registers; the starting state goes to LDS) and
     // reduce gC_t = sum_d gy_t h_t over the wave's channels on the way (gy = 0 on inactive lanes and
@@ -428,7 +448,7 @@ static int64_t sp_of(int64_t S) {
 
 struct BwdWs {
   size_t ck, gbc, ga, gd, ga_sum, gd_sum, total;
-  int nchunk;
+  int nchunk, nck;
   BwdGrid grid;
 };
 
@@ -441,7 +461,8 @@ static BwdWs bwd_ws(int64_t N, int64_t T, int64_t Dn, int64_t S) {
   w.grid = bwd_grid(Dn, (int)(SP / SG));
   auto al = [](size_t v) { return (v + 255) / 256 * 256; };
   size_t o = 0;
-  w.ck = o; o += al((size_t)N * w.nchunk * Dn * SP * 4);
+  w.nck = (w.nchunk + BWD_CKR - 1) / BWD_CKR;
+  w.ck = o; o += al((size_t)N * w.nck * Dn * SP * 4);
   w.gbc = o; o += al((size_t)w.grid.nblk * N * T * 2 * SP * 4);
   w.ga = o; o += al((size_t)N * Dn * SP * 4);
   w.gd = o; o += al((size_t)N * Dn * 4);
@@ -463,7 +484,7 @@ static int launch_bwd(const void* x, const void* dt, const float* A_log, const v
   int threads = DW * G;
   threads = (threads + 63) / 64 * 64;
   BwdArgs a;
-  a.T = (int)T; a.Dn = (int)Dn; a.S = (int)S; a.nchunk = L.nchunk; a.DW = DW;
+  a.T = (int)T; a.Dn = (int)Dn; a.S = (int)S; a.nchunk = L.nchunk; a.nck = L.nck; a.DW = DW;
   a.ld_ck = Dn * SP;
   float* gbc = reinterpret_cast<float*>(ws + L.gbc);
   hipLaunchKernelGGL((ssm_scan_bwd_kernel<DT, SP, MODE>), dim3((unsigned)N, (unsigned)nblk_d), dim3(threads), 0, st,

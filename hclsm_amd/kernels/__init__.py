@@ -35,6 +35,7 @@ from hclsm_amd.kernels.sparse_event_attn import (
 from hclsm_amd.kernels.level1_packed import Level1Weights, level1_forward_packed
 
 from hclsm_amd.kernels.event_attention import (
+    TrackCausalPlan,
     event_attention,
     track_causal_event_attention,
     slots_attention,
@@ -118,6 +119,7 @@ __all__ = [
     "level1_forward_packed",
     "event_attention",
     "track_causal_event_attention",
+    "TrackCausalPlan",
     "slots_attention",
     "gnn_message_pass_fn",
     "naive_gnn_message_pass",

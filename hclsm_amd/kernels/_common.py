@@ -43,11 +43,13 @@ _WARNED: set = set()
 
 
 def warn_fallback(fn_name: str, reason: str) -> None:
-    """Warn (once per function and reason) that fn_name is running torch ops instead of its HIP kernel."""
+    """Warn (once per function and reason) that fn_name is running torch ops instead of its HIP kernel.  The
+    pair is recorded only after the warning was issued, so under ``warnings.simplefilter("error",
+    HipFallbackWarning)`` every such call raises."""
     import warnings
     key = (fn_name, reason)
     if key in _WARNED:
         return
-    _WARNED.add(key)
     warnings.warn(f"hclsm_amd.{fn_name}: running the reference math as torch ops on the GPU: {reason}",
                   HipFallbackWarning, stacklevel=3)
+    _WARNED.add(key)

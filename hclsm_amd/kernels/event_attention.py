@@ -78,33 +78,90 @@ def event_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, index: Ev
     return result
 
 
-def track_causal_event_attention(q, k, v, event_mask, scale=None, out="packed", rule="gt_half", capacity=None):
+def track_causal_event_attention(q, k, v, event_mask, scale=None, out="packed", rule="gt_half", capacity=None,
+                                 *, out_packed=None, index=None):
     """Per-track causal attention among the event timesteps of ``event_mask`` (P, T).
     Returns (packed output, event index).  With out="packed" and a known ``capacity`` (rows of the packed
     output; events past it are dropped) the index build and the attention are one library call
     (hclsm_track_causal_attention) with no host synchronisation; otherwise the index is built first and
-    the output sized by its total (one host read)."""
-    if out != "packed" or capacity is None:
+    the output sized by its total (one host read).
+
+    A loop over steps of one shape can pass back the buffers of an earlier call: ``out_packed`` (a
+    contiguous (capacity, H, dh) tensor of q's dtype; capacity defaults to its rows) and ``index`` (an
+    EventIndex of this (P, T) from EventIndex.allocate or an earlier call, rewritten in place).  Nothing
+    is allocated then."""
+    if out != "packed" or (capacity is None and out_packed is None):
         idx = build_event_index(event_mask, rule)
         return event_attention(q, k, v, idx, "track_causal", scale=scale, out=out, capacity=capacity), idx
-    require_gpu("track_causal_event_attention", q, k, v, event_mask)
+    require_gpu("track_causal_event_attention", q, k, v, event_mask, out_packed)
     _check_qkv(q, k, v)
     P, T, H, dh = q.shape
     if tuple(event_mask.shape) != (P, T):
         raise ValueError(f"event_mask must be ({P}, {T}) to match q, got {tuple(event_mask.shape)}")
-    cap = int(capacity)
+    cap = int(capacity) if capacity is not None else out_packed.shape[0]
     if cap < 0:
         raise ValueError(f"capacity must be >= 0, got {cap}")
     m, code = _mask_code(event_mask.detach().contiguous())
     qc, kc, vc = q.contiguous(), k.contiguous(), v.contiguous()
-    idx = EventIndex.allocate(P, T, q.device)
-    outp = torch.empty((cap, H, dh), dtype=q.dtype, device=q.device)
+    if index is None:
+        idx = EventIndex.allocate(P, T, q.device)
+    elif index._buf is None or (index.B, index.T) != (P, T) or index._buf.device != q.device:
+        raise ValueError(f"index must be an EventIndex.allocate({P}, {T}) buffer on {q.device}")
+    else:
+        idx = index
+    if out_packed is None:
+        outp = torch.empty((cap, H, dh), dtype=q.dtype, device=q.device)
+    elif (out_packed.dtype != q.dtype or not out_packed.is_contiguous() or out_packed.dim() != 3
+          or tuple(out_packed.shape[1:]) != (H, dh) or out_packed.shape[0] < cap):
+        raise ValueError(f"out_packed must be a contiguous ({cap}, {H}, {dh}) {q.dtype} tensor")
+    else:
+        outp = out_packed
     rc = _lib.lib().hclsm_track_causal_attention(
         m.data_ptr(), code, _RULES[rule], qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), outp.data_ptr(), P, T, H, dh,
         cap, float(dh ** -0.5 if scale is None else scale), _lib.dtype_code(q.dtype), idx.ptr("stats"),
         _lib.stream_of(qc))
     _lib.check(rc, "hclsm_track_causal_attention")
     return outp, idx
+
+
+class TrackCausalPlan:
+    """track_causal_event_attention prepared for a loop over steps of one shape (a serving loop): the tensors
+    are checked and the output and index buffers allocated once, and each call is the one library call
+    (hclsm_track_causal_attention) on torch's current stream, reading whatever q, k, v and the mask hold at
+    that moment.  The caller keeps those tensors alive and updates them in place between calls.
+
+        plan = TrackCausalPlan(q, k, v, event_mask, capacity)
+        out, index = plan()      # the same (out, index) objects every call
+    """
+
+    def __init__(self, q, k, v, event_mask, capacity, scale=None, rule="gt_half"):
+        require_gpu("TrackCausalPlan", q, k, v, event_mask)
+        _check_qkv(q, k, v)
+        P, T, H, dh = q.shape
+        if tuple(event_mask.shape) != (P, T):
+            raise ValueError(f"event_mask must be ({P}, {T}) to match q, got {tuple(event_mask.shape)}")
+        if not (q.is_contiguous() and k.is_contiguous() and v.is_contiguous() and event_mask.is_contiguous()):
+            raise ValueError("TrackCausalPlan binds device pointers: q, k, v and the mask must be contiguous")
+        cap = int(capacity)
+        if cap < 0:
+            raise ValueError(f"capacity must be >= 0, got {cap}")
+        m, code = _mask_code(event_mask.detach())
+        if m.data_ptr() != event_mask.data_ptr():
+            raise TypeError("TrackCausalPlan needs a float32, bfloat16, float16, bool or uint8 mask")
+        self.out = torch.empty((cap, H, dh), dtype=q.dtype, device=q.device)
+        self.index = EventIndex.allocate(P, T, q.device)
+        self._keep = (q, k, v, event_mask)
+        self._fn = _lib.lib().hclsm_track_causal_attention
+        self._dev = q.get_device()
+        self._args = (m.data_ptr(), code, _RULES[rule], q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                      self.out.data_ptr(), P, T, H, dh, cap, float(dh ** -0.5 if scale is None else scale),
+                      _lib.dtype_code(q.dtype), self.index.ptr("stats"))
+
+    def __call__(self):
+        rc = self._fn(*self._args, _lib.stream_of_device(self._dev))
+        if rc:
+            _lib.check(rc, "hclsm_track_causal_attention")
+        return self.out, self.index
 
 
 _DENSE_CACHE: dict = {}

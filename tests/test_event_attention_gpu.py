@@ -143,3 +143,53 @@ def test_one_call_matches_two_calls(P, T, H, dh, p, dtype):
         cut = total // 2
         o2, _ = track_causal_event_attention(q, k, v, m, capacity=cut)
         assert o2.shape == (cut, H, dh) and torch.equal(o2, ref[:cut])
+
+
+def test_one_call_reuses_buffers():
+    """Passing back the output and the index of an earlier call: a second mask of the same shape gives the
+    same result as fresh buffers, written into the same memory; mismatched buffers raise before any launch."""
+    from hclsm_amd.kernels.event_attention import track_causal_event_attention
+    from hclsm_amd.kernels.sparse_event_attn import EventIndex, build_event_index
+    P, T, H, dh = 96, 80, 3, 64
+    q, k, v, m = (t.cuda() for t in _data(P, T, H, dh, torch.bfloat16, 0.3, seed=11))
+    _, _, _, m2 = (t.cuda() for t in _data(P, T, H, dh, torch.bfloat16, 0.2, seed=12))
+    cap = P * T
+    o, idx = track_causal_event_attention(q, k, v, m, capacity=cap)
+    ptr_o, ptr_i = o.data_ptr(), idx.ptr("stats")
+    o2, idx2 = track_causal_event_attention(q, k, v, m2, out_packed=o, index=idx)
+    ref, ref_idx = track_causal_event_attention(q, k, v, m2, capacity=cap)
+    torch.cuda.synchronize()
+    total = build_event_index(m2).total()
+    assert o2.data_ptr() == ptr_o and idx2.ptr("stats") == ptr_i
+    assert torch.equal(o2[:total], ref[:total])
+    for name in ("counts", "offsets", "slot_of", "stats"):
+        assert torch.equal(getattr(idx2, name), getattr(ref_idx, name)), name
+    with pytest.raises(ValueError):
+        track_causal_event_attention(q, k, v, m2, out_packed=o[:, :, :32], index=idx)
+    with pytest.raises(ValueError):
+        track_causal_event_attention(q, k, v, m2, out_packed=o, index=EventIndex.allocate(P, T + 1, q.device))
+
+
+def test_plan_matches_the_function_and_follows_updates():
+    """TrackCausalPlan: the same output and tables as track_causal_event_attention, written into the same
+    buffers each call, and a mask / q updated in place between calls is what the next call reads."""
+    from hclsm_amd.kernels.event_attention import TrackCausalPlan, track_causal_event_attention
+    P, T, H, dh = 200, 64, 6, 64
+    q, k, v, m = (t.cuda() for t in _data(P, T, H, dh, torch.bfloat16, 0.15, seed=31))
+    cap = P * T
+    plan = TrackCausalPlan(q, k, v, m, capacity=cap)
+    for step in range(3):
+        if step:
+            _, _, _, m_new = _data(P, T, H, dh, torch.bfloat16, 0.1 * step, seed=40 + step)
+            m.copy_(m_new.cuda())
+            q.mul_(0.5)
+        out, idx = plan()
+        ref, ref_idx = track_causal_event_attention(q, k, v, m, capacity=cap)
+        torch.cuda.synchronize()
+        total = int(ref_idx.stats[0])
+        assert out.data_ptr() == plan.out.data_ptr() and idx is plan.index
+        assert torch.equal(out[:total], ref[:total])
+        for name in ("counts", "offsets", "slot_of", "stats"):
+            assert torch.equal(getattr(idx, name), getattr(ref_idx, name)), name
+    with pytest.raises(ValueError):
+        TrackCausalPlan(q[:, :, :, :32], k[:, :, :, :32], v[:, :, :, :32], m, capacity=cap)
