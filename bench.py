@@ -12,9 +12,14 @@ Infinity Cache, so the timed loop rotates over NSETS distinct input/output sets
 
 Prints ONE JSON line.  `value` is the scan's algorithmic bytes / average step time
 (GB/s); `roofline` prices the same kernel against MI355X's 8 TB/s HBM peak with the
-per-launch duration measured by HIP events; `cpu_baseline` times the reference's sequential scan loop
+per-launch duration measured by HIP events; `roofline_valu` prices it against its VALU issue
+budget from the committed counter run; `cpu_baseline` times the reference's sequential scan loop
 written with the same torch ops on the CPU (oracle/torch_cpu.py, raw mode) on the whole
 config-1 input, on the host cores.
+
+Sub-objects (`--legs`, default all): configs 2, 3 and 4, the scan at the reference's published
+shapes, and the widened rows (block scan, scan backward, Level-1, relation graph, tracking loop).
+Configs 2 and 3 rotate over SLOT_SETS / EVENT_SETS input sets for the same reason as the scan.
 """
 
 from __future__ import annotations
@@ -37,6 +42,8 @@ NSETS = 4
 
 
 LEGS = ("slot", "events", "chain", "context", "block", "bwd", "level1", "gnn", "track")
+SLOT_SETS = 64     # config-2 token / slot sets rotated over the timed steps (9.6 MB of tokens each)
+EVENT_SETS = 16    # config-3 q / k / v sets rotated over the timed steps (24 MB of event rows each)
 
 
 def _parse():
@@ -124,7 +131,9 @@ def _cpu_baseline(d, reps=3):
                       f"(oracle/torch_cpu.py), {cores} threads on {model}, median of {reps}: {med:.3f} s"}
 
 
-def _event_timing(fn, n, warmup):
+def _event_timing(fn, n, warmup, spread=None):
+    """Median and mean seconds per fn() call over n calls timed with HIP events on the current stream, after
+    `warmup` calls.  With a dict as `spread`, p10 / p90 (us) are added to it."""
     import torch
     for _ in range(warmup):
         fn()
@@ -136,7 +145,20 @@ def _event_timing(fn, n, warmup):
         b.record()
     torch.cuda.synchronize()
     ts = sorted(a.elapsed_time(b) * 1e-3 for a, b in evs)
+    if spread is not None:
+        spread["p10_us"] = round(ts[len(ts) // 10] * 1e6, 2)
+        spread["p90_us"] = round(ts[(len(ts) * 9) // 10] * 1e6, 2)
     return ts[len(ts) // 2], sum(ts) / len(ts)
+
+
+def _rotating(fns):
+    """One callable that runs fns[0], fns[1], ... in turn: steps over distinct input sets."""
+    state = [0]
+
+    def step():
+        fns[state[0] % len(fns)]()
+        state[0] += 1
+    return step
 
 
 def _bench_slot(dev, n, warmup, cpu):
@@ -147,11 +169,16 @@ def _bench_slot(dev, n, warmup, cpu):
     tokens, slots0, w = slot_config()
     W = si.SlotWeights.from_dict(w, torch.bfloat16, dev)
     tk, s0 = tokens.to(dev), slots0.to(dev)
-    med, avg = _event_timing(lambda: si.slot_attention_forward(tk, s0, W, 3, si.CONFIG2_MODE), n, warmup)
+    # distinct token / slot sets per step (> 512 MB in all), so that the 256 MB MALL does not serve the inputs
+    sets = [(torch.roll(tk, r, 0).contiguous(), torch.roll(s0, r, 0).contiguous()) for r in range(SLOT_SETS)]
+    step = _rotating([lambda a=a, b=b: si.slot_attention_forward(a, b, W, 3, si.CONFIG2_MODE) for a, b in sets])
+    spread = {}
+    med, avg = _event_timing(step, n, warmup, spread)
     fl = slot_flops()
     ntok = tokens.shape[0] * tokens.shape[1]
     res = {"workload": "config 2: 32 frames x 196 tokens x 384, 32 slots, 3 iterations, MLP 768, bf16 MFMA",
-           "metric": "tokens/s", "value": round(ntok / med, 1), "median_us": round(med * 1e6, 2),
+           "metric": "tokens/s", "value": round(ntok / med, 1), "median_us": round(med * 1e6, 2), **spread,
+           "input_sets_rotated": SLOT_SETS,
            "roofline": {"bound": "mfma", "achieved": round(fl / med / 1e12, 3), "peak": 2500.0,
                         "unit": "TFLOP/s", "frac": round(fl / med / 1e12 / 2500.0, 5), "flops_per_call": fl}}
     if cpu:
@@ -177,14 +204,21 @@ def _bench_events(dev, n, warmup, cpu):
     m[:, 0] = 1
     m = m.to(dev)
     total = build_event_index(m).total()
-    step = TrackCausalPlan(q, k, v, m, capacity=total)   # checks and buffers once; each step is the library call
-    med, avg = _event_timing(step, n, warmup)
+    # distinct q / k / v sets per step (the event rows of all sets exceed the 256 MB MALL); one prepared call
+    # each (checks and buffers once; each step is the library call)
+    plans = [TrackCausalPlan(q, k, v, m, capacity=total)]
+    for r in range(1, EVENT_SETS):
+        qr, kr, vr = (torch.roll(t, r, 0).contiguous() for t in (q, k, v))
+        plans.append(TrackCausalPlan(qr, kr, vr, m, capacity=total))
+    spread = {}
+    med, avg = _event_timing(_rotating(plans), n, warmup, spread)
     nbytes = total * 6 * 64 * 2 * 4 + m.numel() * 4 + (1025 + 2 * total + 2 * 65536) * 4
     res = {"workload": "config 3: 1024 tracks x T=64, 6 heads x 64, p=0.15 (t=0 forced), bf16, "
                         "index build + causal event attention, packed output (one library call per step through "
                         "TrackCausalPlan: arguments checked and output / index buffers allocated once)",
             "events": total, "metric": "event-tokens/s", "value": round(total / med, 1),
-            "grid_tokens_per_s": round(65536 / med, 1), "median_us": round(med * 1e6, 2),
+            "grid_tokens_per_s": round(65536 / med, 1), "median_us": round(med * 1e6, 2), **spread,
+            "input_sets_rotated": EVENT_SETS,
             "roofline": {"bound": "hbm", "achieved": round(nbytes / med / 1e9, 2), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(nbytes / med / 1e9 / HBM_PEAK_GBS, 5),
                          "bytes_per_call": nbytes}}
