@@ -56,6 +56,9 @@ def _parse():
     p.add_argument("--legs", default=",".join(LEGS),
                    help="comma-separated sub-benchmarks to run after the metric (default: all of "
                         + ",".join(LEGS) + ")")
+    p.add_argument("--no-counters", action="store_true",
+                   help="take the scan's HBM traffic and VALU counts from the committed counter summary "
+                        "(profiles/ssm_scan_fwd_counters.json) instead of rocprofv3 passes in this run")
     p.add_argument("--copy-calibration", action="store_true",
                    help="after the timed loop, run a 1 GiB device-to-device copy 5 times (a kernel of "
                         "known traffic for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE counters)")
@@ -71,6 +74,69 @@ def _scan_counters():
             return json.load(f)
     except (OSError, ValueError):
         return {}
+
+
+# rocprofv3 counter passes over this script's scan alone (each pass a child process of its own)
+_PMC_PASSES = (("FETCH_SIZE",), ("WRITE_SIZE",), ("SQ_ACTIVE_INST_VALU", "SQ_INSTS_VALU", "SQ_INSTS_VALU_TRANS_F32"))
+_SCAN_GRID = 196608   # config-1 launch: 1024 sequences x 3 channel blocks x 64 lanes
+_COPY_GRID = 131072   # the 1 GiB device copy of --copy-calibration
+
+
+def _measure_counters(timeout_s=180):
+    """The config-1 scan's counters measured in this run: each pass of _PMC_PASSES runs
+    `rocprofv3 --pmc ... -- python bench.py --no-extra --copy-calibration` as a child process (one pass per
+    run, as the counter blocks require), and per-dispatch averages are read from its counter_collection.csv.
+    FETCH_SIZE / WRITE_SIZE (KiB per dispatch) are scaled by what the same counter reads for the 1 GiB copy.
+    Returns {} when rocprofv3 is absent or a pass fails; the caller then uses the committed summary."""
+    import csv
+    import glob
+    import shutil
+    import subprocess
+    import tempfile
+    exe = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    if not os.path.exists(exe):
+        return {}
+    tmp = tempfile.mkdtemp(prefix="hclsm_pmc_", dir=os.environ.get("TMPDIR") or "/tmp")
+    vals = {}
+    try:
+        for i, counters in enumerate(_PMC_PASSES):
+            out = os.path.join(tmp, f"p{i}")
+            cmd = [exe, "--pmc", *counters, "-d", out, "-o", "run", "--output-format", "csv", "--",
+                   sys.executable, os.path.abspath(__file__), "--steps", "20", "--warmup", "2", "--no-cpu-baseline",
+                   "--no-extra", "--no-counters"]
+            if counters[0] in ("FETCH_SIZE", "WRITE_SIZE"):
+                cmd.append("--copy-calibration")
+            try:
+                subprocess.run(cmd, cwd=tmp, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL,
+                               timeout=timeout_s, check=False)
+            except subprocess.TimeoutExpired:
+                return {}
+            files = glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True)
+            if not files:
+                return {}
+            acc = {}
+            with open(files[0]) as f:
+                for r in csv.DictReader(f):
+                    name, grid = r["Kernel_Name"], int(float(r.get("Grid_Size", 0) or 0))
+                    kind = ("scan" if "ssm_scan_fwd_mfma_kernel" in name and grid == _SCAN_GRID else
+                            "copy" if "copyBuffer" in name and grid == _COPY_GRID else None)
+                    if kind:
+                        acc.setdefault((kind, r["Counter_Name"]), []).append(float(r["Counter_Value"]))
+            for (kind, c), v in acc.items():
+                vals[(kind, c)] = sum(v) / len(v)
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    res = {"source": "rocprofv3 --pmc passes of this run (bench.py --no-extra --copy-calibration as a child)"}
+    for c in ("FETCH_SIZE", "WRITE_SIZE"):
+        if ("scan", c) in vals and vals.get(("copy", c)):
+            res[c.lower() + "_bytes"] = int(round(vals[("scan", c)] * (1 << 30) / vals[("copy", c)]))
+    if "fetch_size_bytes" in res and "write_size_bytes" in res:
+        res["hbm_bytes_per_launch"] = res["fetch_size_bytes"] + res["write_size_bytes"]
+    for c, k in (("SQ_ACTIVE_INST_VALU", "sq_active_inst_valu_per_launch"), ("SQ_INSTS_VALU", "valu_instr_per_launch"),
+                 ("SQ_INSTS_VALU_TRANS_F32", "trans_instr_per_launch")):
+        if ("scan", c) in vals:
+            res[k] = int(round(vals[("scan", c)]))
+    return res
 
 
 def _valu_roofline(ctr, avg_s):
@@ -633,6 +699,10 @@ def main():
 
     achieved = nbytes / avg / 1e9
     ctr = _scan_counters()
+    if not args.no_counters:
+        live = _measure_counters()
+        if "hbm_bytes_per_launch" in live and "sq_active_inst_valu_per_launch" in live:
+            ctr = live
     out = {
         "metric": METRIC,
         "value": round(nbytes * args.steps / wall / 1e9, 2),
