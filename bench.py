@@ -82,7 +82,7 @@ _SCAN_GRID = 196608   # config-1 launch: 1024 sequences x 3 channel blocks x 64 
 _COPY_GRID = 131072   # the 1 GiB device copy of --copy-calibration
 
 
-def _measure_counters(timeout_s=180):
+def _measure_counters(timeout_s=90):
     """The config-1 scan's counters measured in this run: each pass of _PMC_PASSES runs
     `rocprofv3 --pmc ... -- python bench.py --no-extra --copy-calibration` as a child process (one pass per
     run, as the counter blocks require), and per-dispatch averages are read from its counter_collection.csv.
