@@ -193,3 +193,21 @@ def test_plan_matches_the_function_and_follows_updates():
             assert torch.equal(getattr(idx, name), getattr(ref_idx, name)), name
     with pytest.raises(ValueError):
         TrackCausalPlan(q[:, :, :, :32], k[:, :, :, :32], v[:, :, :, :32], m, capacity=cap)
+
+
+@pytest.mark.parametrize("mdtype", [torch.bool, torch.uint8, torch.bfloat16])
+def test_plan_mask_dtypes(mdtype):
+    """TrackCausalPlan over bool / uint8 / bf16 masks gives the fp32-mask result; a float64 mask, which the
+    plan cannot bind without a copy, raises."""
+    from hclsm_amd.kernels.event_attention import TrackCausalPlan, track_causal_event_attention
+    P, T, H, dh = 40, 48, 2, 32
+    q, k, v, m = (t.cuda() for t in _data(P, T, H, dh, torch.float32, 0.3, seed=77))
+    cap = P * T
+    ref, ref_idx = track_causal_event_attention(q, k, v, m, capacity=cap)
+    out, idx = TrackCausalPlan(q, k, v, (m > 0.5).to(mdtype).contiguous(), capacity=cap)()
+    torch.cuda.synchronize()
+    total = int(ref_idx.stats[0])
+    assert torch.equal(out[:total], ref[:total])
+    assert torch.equal(idx.offsets, ref_idx.offsets)
+    with pytest.raises(TypeError):
+        TrackCausalPlan(q, k, v, m.double(), capacity=cap)
