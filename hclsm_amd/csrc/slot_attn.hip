@@ -881,6 +881,21 @@ linear_kreg_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>:
     c = c < N ? c : N - 1;
     pb[t] = W + c * ldw + KPL * g;
   }
+  // 0. the epilogue's bias and residual values of this thread's four outputs, requested first so that their
+  // latency overlaps the operand loads instead of following the reduction
+  const int ti = wid >> 1, tj = wid & 1;
+  const int64_t col = tn * 32 + 16 * tj + li;
+  float bv = 0.f, rv[4] = {0.f, 0.f, 0.f, 0.f};
+  if (col < N) {
+    if (bias) bv = bias[col];
+    if (resid) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t row = tm * 32 + 16 * ti + 4 * g + r;
+        if (row < M) rv[r] = resid[row * ldr + col];
+      }
+    }
+  }
   // 1. every operand of this wave's blocks (block index clamped; blocks past nblk are skipped below)
   float xa[LN ? KB : 1][2][KPL];
   typename A::Op ao[LN ? 1 : KB][2], bo[KB][2];
@@ -989,10 +1004,7 @@ linear_kreg_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>:
       for (int r = 0; r < 4; ++r) red[wid][i][j][r][lane] = acc[i][j][r];
   __syncthreads();
   // 1024 outputs, 4 per thread: thread -> (ti, tj) = wave index, lane, all four r
-  const int ti = wid >> 1, tj = wid & 1;
-  const int64_t col = tn * 32 + 16 * tj + li;
   if (col >= N) return;
-  const float bv = bias ? bias[col] : 0.f;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int64_t row = tm * 32 + 16 * ti + 4 * g + r;
@@ -1000,7 +1012,7 @@ linear_kreg_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>:
     float val = red[0][ti][tj][r][lane] + red[1][ti][tj][r][lane] + red[2][ti][tj][r][lane] +
                 red[3][ti][tj][r][lane] + bv;
     if (relu) val = fmaxf(val, 0.f);
-    if (resid) val += resid[row * ldr + col];
+    if (resid) val += rv[r];
     if (clamp_v > 0.f) val = fminf(fmaxf(val, -clamp_v), clamp_v);
     Y[row * ldy + col] = MM<OT>::fromf(val);
     if (Y2) Y2[row * ldy2 + col] = A::fromf(val);
@@ -1029,6 +1041,19 @@ gru_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const typename
   for (int t = 0; t < 2; ++t) {
     const int64_t r = tm * 32 + 16 * t + li;
     rows[t] = r < M ? r : M - 1;
+  }
+  // the epilogue's biases and previous hidden state for this thread's two outputs, requested first
+  const int64_t col = tn * 16 + li;
+  const int t_e = wid >> 1;
+  float bir = 0.f, biz = 0.f, bin = 0.f, bhr = 0.f, bhz = 0.f, bhn = 0.f, hv[2] = {0.f, 0.f};
+  if (col < H) {
+    if (bih) { bir = bih[col]; biz = bih[H + col]; bin = bih[2 * H + col]; }
+    if (bhh) { bhr = bhh[col]; bhz = bhh[H + col]; bhn = bhh[2 * H + col]; }
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      const int64_t row = tm * 32 + 16 * t_e + 4 * g + 2 * (wid & 1) + rr;
+      if (row < M) hv[rr] = Hf[row * ldh + col];
+    }
   }
   f32x4 acc[2][6];
 #pragma unroll
@@ -1075,11 +1100,8 @@ gru_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const typename
       for (int r = 0; r < 4; ++r) red[wid][t][q][r][lane] = acc[t][q][r];
   __syncthreads();
   // 512 outputs (32 rows x 16 cols): thread -> (t = wid >> 1, r pair = 2 * (wid & 1) .. +1), lane
-  const int64_t col = tn * 16 + li;
   if (col >= H) return;
-  const float bir = bih ? bih[col] : 0.f, biz = bih ? bih[H + col] : 0.f, bin = bih ? bih[2 * H + col] : 0.f;
-  const float bhr = bhh ? bhh[col] : 0.f, bhz = bhh ? bhh[H + col] : 0.f, bhn = bhh ? bhh[2 * H + col] : 0.f;
-  const int t = wid >> 1;
+  const int t = t_e;
 #pragma unroll
   for (int rr = 0; rr < 2; ++rr) {
     const int r = 2 * (wid & 1) + rr;
@@ -1092,8 +1114,7 @@ gru_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const typename
     const float rg = sigmoid_f(gsum[0] + bir + gsum[3] + bhr);
     const float zg = sigmoid_f(gsum[1] + biz + gsum[4] + bhz);
     const float ng = tanh_f(gsum[2] + bin + rg * (gsum[5] + bhn));
-    const float hv = Hf[row * ldh + col];
-    const float o = (1.f - zg) * ng + zg * hv;
+    const float o = (1.f - zg) * ng + zg * hv[rr];
     out[row * ldo + col] = o;
     if (out2) out2[row * ldo2 + col] = A::fromf(o);
   }
