@@ -106,10 +106,15 @@ def _measure_counters(timeout_s=90):
                    "--no-extra", "--no-counters"]
             if counters[0] in ("FETCH_SIZE", "WRITE_SIZE"):
                 cmd.append("--copy-calibration")
+            # own process group, so that a pass past its limit is ended together with the program it profiles
+            proc = subprocess.Popen(cmd, cwd=tmp, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL,
+                                    start_new_session=True)
             try:
-                subprocess.run(cmd, cwd=tmp, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL,
-                               timeout=timeout_s, check=False)
+                proc.wait(timeout=timeout_s)
             except subprocess.TimeoutExpired:
+                import signal
+                os.killpg(proc.pid, signal.SIGKILL)
+                proc.wait()
                 return {}
             files = glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True)
             if not files:
