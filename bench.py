@@ -544,6 +544,17 @@ def _bench_scan_context(dev, n, warmup):
         rows.append({"config": name, "shape": {"BN": BN, "T": T, "d_inner": Dn, "d_state": S}, "dtype": "f32",
                      "ms_per_call": round(med * 1e3, 4), "mean_ms": round(avg * 1e3, 4),
                      "reference_published_ms": {"triton_t4": t4_triton, "sequential_t4": t4_seq}})
+    # config 0 (the fp32 parity config, 128 x 16 x 256, S=16, raw + D), through ssm_scan_fn as a caller
+    # would call it: launch-bound, so the time is mostly the call's host path
+    from hclsm_amd.workloads import scan_algorithmic_bytes, scan_config
+    c0 = {k: v.to(dev) for k, v in scan_config(0).items()}
+    med, avg = _event_timing(lambda: ssm_scan_fn(c0["x"], c0["dt"], c0["A_log"], c0["B"], c0["C"], D=c0["D"]), n,
+                             warmup)
+    N0, T0, D0 = c0["x"].shape
+    b0 = scan_algorithmic_bytes(N0, T0, D0, c0["B"].shape[2], 4)
+    rows.append({"config": "config 0", "shape": {"BN": N0, "T": T0, "d_inner": D0, "d_state": c0["B"].shape[2]},
+                 "dtype": "f32", "ms_per_call": round(med * 1e3, 4), "mean_ms": round(avg * 1e3, 4),
+                 "algorithmic_bytes": b0, "gbs": round(b0 / med / 1e9, 1)})
     return rows
 
 
