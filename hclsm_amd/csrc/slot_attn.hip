@@ -1411,11 +1411,27 @@ core_update_kernel(const typename MM<DT>::T* __restrict__ P, int64_t Mp, const f
 constexpr int CF_WAVES = 8;
 constexpr int CF_MAXM = 256;
 
-template <int DT, int NT, int DD, int NCB>
+//
+// With LNQ the query side is formed in the kernel: `q` is unused, the workgroup reads its frame's fp32 slot rows
+// (ln.s), takes their LayerNorm (two-pass mean and variance over a wave per row) into the LDS tile that holds q
+// otherwise, and `k` holds k Wq (the keys already multiplied by the query weight): (LN(s) Wq^T) k^T = LN(s) (k Wq)^T,
+// so the iteration needs no q projection.  ln.sb_out (nullable) receives the slot rows in the operand type (the
+// column-block-0 workgroup of each frame writes them).
+struct LnqArgs {
+  const float* s;        // [B][N][D] slot rows: row stride ld, frame stride fb
+  int64_t ld, fb;
+  const float* w;        // LayerNorm gamma / beta (nullable)
+  const float* b;
+  float eps;
+  void* sb_out;          // [B][N][D] in the operand type: row stride ldsb, frame stride sbb (nullable)
+  int64_t ldsb, sbb;
+};
+
+template <int DT, int NT, int DD, int NCB, bool LNQ>
 __global__ void __launch_bounds__(64 * CF_WAVES)
 core_fused_t_kernel(const typename MM<DT>::T* __restrict__ q, const typename MM<DT>::T* __restrict__ k,
                     const typename MM<DT>::T* __restrict__ vt, int64_t Mp, typename MM<DT>::T* __restrict__ out,
-                    CoreArgs a) {
+                    CoreArgs a, LnqArgs ln) {
   using A = MM<DT>;
   using TT = typename A::T;
   static_assert(A::KPL == 8 && DD % (16 * NCB) == 0, "16-bit operands, whole 16-column tiles per block");
@@ -1454,10 +1470,58 @@ core_fused_t_kernel(const typename MM<DT>::T* __restrict__ q, const typename MM<
         if (i < NVB) vr[c][i] = *reinterpret_cast<const uint4*>(vp + 32 * i);
     }
   }
-  for (int u = tid; u < NS * (DD / 8); u += 64 * NW) {   // rows n >= N repeat row N - 1 (their logits are masked)
-    const int n = u / (DD / 8), c = (u - n * (DD / 8)) * 8;
-    const int nc = n < a.N ? n : a.N - 1;
-    *reinterpret_cast<uint4*>(sq + n * QP + c) = *reinterpret_cast<const uint4*>(q + b * a.qb + (int64_t)nc * a.ldq + c);
+  if constexpr (LNQ) {
+    // LayerNorm of the frame's slot rows into sq: wave w takes rows w, w + NW, ...; lane l holds elements
+    // l + 64 e.  Rows n >= N repeat row N - 1 (their logits are masked).
+    constexpr int EPL = DD / 64, RPW = NS / NW;
+    static_assert(DD % 64 == 0 && NS % NW == 0, "whole rows per wave");
+    float xs[RPW][EPL];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      const int n = wid + NW * r;
+      const int nc = n < a.N ? n : a.N - 1;
+      const float* sp_ = ln.s + b * ln.fb + (int64_t)nc * ln.ld + lane;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) xs[r][e] = sp_[64 * e];
+    }
+    float gw[EPL], gb[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      gw[e] = ln.w ? ln.w[lane + 64 * e] : 1.f;
+      gb[e] = ln.b ? ln.b[lane + 64 * e] : 0.f;
+    }
+    TT* sbo = (ln.sb_out != nullptr && blockIdx.y == 0) ? reinterpret_cast<TT*>(ln.sb_out) + b * ln.sbb : nullptr;
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      const int n = wid + NW * r;
+      float s1 = 0.f;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) s1 += xs[r][e];
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) s1 += __shfl_xor(s1, o, 64);
+      const float mean = s1 * (1.f / (float)DD);
+      float s2 = 0.f;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        const float dv = xs[r][e] - mean;
+        s2 += dv * dv;
+      }
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) s2 += __shfl_xor(s2, o, 64);
+      const float rstd = 1.f / sqrtf(s2 * (1.f / (float)DD) + ln.eps);
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        sq[n * QP + lane + 64 * e] = A::fromf((xs[r][e] - mean) * rstd * gw[e] + gb[e]);
+        if (sbo != nullptr && n < a.N) sbo[(int64_t)n * ln.ldsb + lane + 64 * e] = A::fromf(xs[r][e]);
+      }
+    }
+  } else {
+    for (int u = tid; u < NS * (DD / 8); u += 64 * NW) {   // rows n >= N repeat row N - 1 (their logits are masked)
+      const int n = u / (DD / 8), c = (u - n * (DD / 8)) * 8;
+      const int nc = n < a.N ? n : a.N - 1;
+      *reinterpret_cast<uint4*>(sq + n * QP + c) =
+          *reinterpret_cast<const uint4*>(q + b * a.qb + (int64_t)nc * a.ldq + c);
+    }
   }
   __syncthreads();
   // ---- phase 1: logits, softmax over slots, P to LDS
@@ -1651,17 +1715,23 @@ static int launch_core(const void* q, int64_t ldq, int64_t qbs, const void* k, i
 // blocks per frame: eight 48-column blocks for D = 384 (config 2: 256 workgroups, one per CU; each block
 // recomputes the frame's logits, and against three 128-column blocks the wider grid still wins by ~2.5 us per
 // forward), 128-column blocks for D = 256, one block for D = 192 / 128.
+static bool core_fused_fits(int64_t B, int64_t N, int64_t M, int64_t D, int dtype) {
+  if (dtype != HCLSM_BF16 && dtype != HCLSM_F16) return false;
+  if (N < 1 || N > 32 || M < 1 || M > CF_MAXM || (D != 128 && D != 192 && D != 256 && D != 384)) return false;
+  if (B > 65535) return false;
+  return core_fused_lds(N <= 16 ? 1 : 2, D, (M + 31) / 32 * 32, 2) <= 64 * 1024;
+}
+
+// lnq (nullable): the LNQ form (q formed in the kernel from the slot rows; k holds k Wq).
 static int launch_core_fused(const void* q, int64_t ldq, int64_t qbs, const void* k, int64_t ldk, int64_t kbs,
                              const void* vt, int64_t vbs, void* out, int64_t ldo, int64_t obs, int64_t B, int64_t N,
                              int64_t M, int64_t D, float scale, float denom_eps, float logit_clamp, float renorm_eps,
-                             int dtype, hipStream_t st) {
-  if (dtype != HCLSM_BF16 && dtype != HCLSM_F16) return 1;
-  if (N < 1 || N > 32 || M < 1 || M > CF_MAXM || (D != 128 && D != 192 && D != 256 && D != 384)) return 1;
-  if (B > 65535) return 1;
+                             int dtype, hipStream_t st, const LnqArgs* lnq = nullptr) {
+  if (!core_fused_fits(B, N, M, D, dtype)) return 1;
   const int NT = N <= 16 ? 1 : 2;
   const int64_t Mp = (M + 31) / 32 * 32;
   const size_t lds = core_fused_lds(NT, D, Mp, 2);
-  if (lds > 64 * 1024) return 1;
+  const LnqArgs ln = lnq ? *lnq : LnqArgs{nullptr, 0, 0, nullptr, nullptr, 0.f, nullptr, 0, 0};
   CoreArgs a;
   a.ldq = ldq; a.ldk = ldk; a.ldv = 0; a.ldo = ldo;
   a.qb = qbs; a.kb = kbs; a.vb = vbs; a.ob = obs;
@@ -1671,9 +1741,14 @@ static int launch_core_fused(const void* q, int64_t ldq, int64_t qbs, const void
   a.scale = scale; a.denom_eps = denom_eps; a.logit_clamp = logit_clamp; a.renorm_eps = renorm_eps;
 #define HCLSM_CF(DT_, NT_, DD_, NCB_)                                                                           \
   if (dtype == DT_ && NT == NT_ && D == DD_) {                                                                 \
-    hipLaunchKernelGGL((core_fused_t_kernel<DT_, NT_, DD_, NCB_>), dim3((unsigned)B, NCB_), dim3(64 * CF_WAVES), \
-                       lds, st, (const MM<DT_>::T*)q, (const MM<DT_>::T*)k, (const MM<DT_>::T*)vt, Mp,           \
-                       (MM<DT_>::T*)out, a);                                                                   \
+    if (lnq)                                                                                                   \
+      hipLaunchKernelGGL((core_fused_t_kernel<DT_, NT_, DD_, NCB_, true>), dim3((unsigned)B, NCB_),            \
+                         dim3(64 * CF_WAVES), lds, st, (const MM<DT_>::T*)q, (const MM<DT_>::T*)k,            \
+                         (const MM<DT_>::T*)vt, Mp, (MM<DT_>::T*)out, a, ln);                                  \
+    else                                                                                                       \
+      hipLaunchKernelGGL((core_fused_t_kernel<DT_, NT_, DD_, NCB_, false>), dim3((unsigned)B, NCB_),           \
+                         dim3(64 * CF_WAVES), lds, st, (const MM<DT_>::T*)q, (const MM<DT_>::T*)k,            \
+                         (const MM<DT_>::T*)vt, Mp, (MM<DT_>::T*)out, a, ln);                                  \
     HCLSM_LAUNCH_CHECK();                                                                                      \
     return 0;                                                                                                  \
   }
@@ -2176,8 +2251,32 @@ extern "C" int hclsm_slot_attn_core(const void* q, int64_t ldq, int64_t q_bstrid
 
 static size_t al256(size_t x) { return (x + 255) / 256 * 256; }
 
+// dst[c][r] = src[r][c] for 16-bit elements, 32 x 32 tiles through LDS.
+__global__ void __launch_bounds__(256) transpose16_kernel(const uint16_t* __restrict__ src, int64_t lds,
+                                                          uint16_t* __restrict__ dst, int64_t ldd, int64_t R,
+                                                          int64_t C) {
+  __shared__ uint16_t tile[32][34];
+  const int64_t c0 = (int64_t)blockIdx.x * 32, r0 = (int64_t)blockIdx.y * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  for (int i = ty; i < 32; i += 8)
+    if (r0 + i < R && c0 + tx < C) tile[i][tx] = src[(r0 + i) * lds + c0 + tx];
+  __syncthreads();
+  for (int i = ty; i < 32; i += 8)
+    if (c0 + i < C && r0 + tx < R) dst[(c0 + i) * ldd + r0 + tx] = tile[tx][i];
+}
+
+static int transpose_16(const void* src, int64_t lds, void* dst, int64_t ldd, int64_t R, int64_t C, hipStream_t st) {
+  if (R <= 0 || C <= 0) return 0;
+  if ((R + 31) / 32 > 65535) return HCLSM_ERR_SHAPE;
+  hipLaunchKernelGGL(transpose16_kernel, dim3((unsigned)((C + 31) / 32), (unsigned)((R + 31) / 32)), dim3(256), 0, st,
+                     (const uint16_t*)src, lds, (uint16_t*)dst, ldd, R, C);
+  HCLSM_LAUNCH_CHECK();
+  return 0;
+}
+
 struct SlotWs {
-  size_t q, core, upd, h, sb, m1, sfa, kv, vt, xn, xin, total;
+  size_t q, core, upd, h, sb, m1, sfa, kv, vt, xn, xin, kq, wqt, total;
+  bool has_kq;
 };
 
 static SlotWs slot_ws_layout(int64_t B, int64_t N, int64_t M, int64_t d, int64_t hidden, int esize, bool with_kv,
@@ -2196,6 +2295,11 @@ static SlotWs slot_ws_layout(int64_t B, int64_t N, int64_t M, int64_t d, int64_t
   w.sfa = o; o += al256(rows * d * 4);
   w.kv = o; o += with_kv ? al256((size_t)B * M * d * esize) : 0;
   w.vt = o; o += with_kv ? al256((size_t)B * d * ((M + 31) / 32 * 32) * esize) : 0;
+  // 16-bit forward: k Wq (the keys times the query weight) and Wq^T, for the fused core's LNQ form
+  const bool kq = with_kv && esize == 2;
+  w.has_kq = kq;
+  w.kq = o; o += kq ? al256((size_t)B * M * d * esize) : 0;
+  w.wqt = o; o += kq ? al256((size_t)d * d * esize) : 0;
   w.total = o;
   return w;
 }
@@ -2238,34 +2342,46 @@ static int linear_ln_fold(const float* x, int64_t ldx, const void* w, int64_t ld
   return 0;
 }
 
+// kq (nullable; v transposed, shapes the fused core takes): k Wq with the same strides as k, and the iteration
+// runs no q projection (the fused core's LNQ form).
 static int slot_iteration_impl(const HclsmSlotWeights* W, const float* slots_in, void* sb, bool make_sb,
                                const void* k, int64_t ldk, int64_t k_bstride, const void* v, int64_t ldv,
                                int64_t v_bstride, bool v_transposed, float* slots_out, int64_t B, int64_t N, int64_t M,
                                int64_t d, int64_t hidden, float scale, float logit_clamp, float renorm_eps,
-                               float slot_clamp, int dtype, char* ws, const SlotWs& L, hipStream_t st) {
+                               float slot_clamp, int dtype, char* ws, const SlotWs& L, hipStream_t st,
+                               const void* kq = nullptr) {
   const int64_t rows = B * N;
   void* q = ws + L.q;
   void* upd = ws + L.upd;
   float* h = reinterpret_cast<float*>(ws + L.h);
   void* m1 = ws + L.m1;
   void* xn = ws + L.xn;
-  // q = LN_pre(slots) W_q^T; with make_sb the same pass writes sb (the slots in dtype)
   bool folded = false;
-  int rc = linear_ln_fold(slots_in, d, W->w_q, d, nullptr, q, d, rows, d, d, 0, W->ln_pre_w, W->ln_pre_b, 1e-5f,
-                          make_sb ? sb : nullptr, d, dtype, st, &folded);
-  if (rc) return rc;
-  if (!folded) {
-    rc = ln_impl(slots_in, d, W->ln_pre_w, W->ln_pre_b, xn, d, rows, d, 1e-5f, HCLSM_F32, dtype, st, kNoLinExt,
-                 make_sb ? sb : nullptr);
+  int rc = 1;
+  if (kq != nullptr) {
+    // updates = core(LN_pre(slots), k Wq, v^T); with make_sb the core also writes sb (the slots in dtype)
+    const LnqArgs ln{slots_in, d, N * d, W->ln_pre_w, W->ln_pre_b, 1e-5f, make_sb ? sb : nullptr, d, N * d};
+    rc = launch_core_fused(nullptr, d, N * d, kq, ldk, k_bstride, v, v_bstride, upd, d, N * d, B, N, M, d, scale, 0.f,
+                           logit_clamp, renorm_eps, dtype, st, &ln);
+    if (rc == 1) return HCLSM_ERR_UNSUPPORTED;   // the caller checked core_fused_fits
+  } else {
+    // q = LN_pre(slots) W_q^T; with make_sb the same pass writes sb (the slots in dtype)
+    rc = linear_ln_fold(slots_in, d, W->w_q, d, nullptr, q, d, rows, d, d, 0, W->ln_pre_w, W->ln_pre_b, 1e-5f,
+                        make_sb ? sb : nullptr, d, dtype, st, &folded);
     if (rc) return rc;
-    rc = linear_impl(xn, d, dtype, W->w_q, d, nullptr, nullptr, 0, q, d, dtype, nullptr, 0, rows, d, d, 0, 0.f, 0,
-                     nullptr, nullptr, 0.f, dtype, st);
-    if (rc) return rc;
+    if (!folded) {
+      rc = ln_impl(slots_in, d, W->ln_pre_w, W->ln_pre_b, xn, d, rows, d, 1e-5f, HCLSM_F32, dtype, st, kNoLinExt,
+                   make_sb ? sb : nullptr);
+      if (rc) return rc;
+      rc = linear_impl(xn, d, dtype, W->w_q, d, nullptr, nullptr, 0, q, d, dtype, nullptr, 0, rows, d, d, 0, 0.f, 0,
+                       nullptr, nullptr, 0.f, dtype, st);
+      if (rc) return rc;
+    }
+    // updates = attention core (logits, softmax over slots, [renorm], attn v): one fused launch when v is transposed
+    rc = v_transposed ? launch_core_fused(q, d, N * d, k, ldk, k_bstride, v, v_bstride, upd, d, N * d, B, N, M, d,
+                                          scale, 0.f, logit_clamp, renorm_eps, dtype, st)
+                      : 1;
   }
-  // updates = attention core (logits, softmax over slots, [renorm], attn v): one fused launch when v is transposed
-  rc = v_transposed ? launch_core_fused(q, d, N * d, k, ldk, k_bstride, v, v_bstride, upd, d, N * d, B, N, M, d, scale,
-                                        0.f, logit_clamp, renorm_eps, dtype, st)
-                    : 1;
   if (rc == 1)
     rc = launch_core(q, d, N * d, k, ldk, k_bstride, v, ldv, v_bstride, upd, d, N * d, nullptr, dtype, B, N, M, d,
                      scale, 0.f, logit_clamp, renorm_eps, dtype, ws + L.core, st, v_transposed);
@@ -2362,10 +2478,20 @@ static int slot_forward_impl(const HclsmSlotWeights* W, const float* inputs, int
   (void)esize;
   const void* k = kv;
   if (n_iter == 0) return (int)hipMemcpyAsync(slots_out, slots0, (size_t)B * N * d * 4, hipMemcpyDeviceToDevice, st);
+  // k Wq = k (Wq^T)^T once per call, so that no iteration projects the slots to queries
+  const void* kq = nullptr;
+  if (L.has_kq && core_fused_fits(B, N, M, d, dtype)) {
+    rc = transpose_16(W->w_q, d, ws + L.wqt, d, d, d, st);
+    if (rc) return rc;
+    rc = linear_impl(kv, d, dtype, ws + L.wqt, d, nullptr, nullptr, 0, ws + L.kq, d, dtype, nullptr, 0, B * M, d, d,
+                     0, 0.f, 0, nullptr, nullptr, 0.f, dtype, st);
+    if (rc) return rc;
+    kq = ws + L.kq;
+  }
   for (int64_t it = 0; it < n_iter; ++it) {
     rc = slot_iteration_impl(W, it == 0 ? slots0 : slots_out, ws + L.sb, it == 0, k, d, M * d, vt, Mp, d * Mp, true,
                              slots_out, B, N, M, d, hidden, scale, logit_clamp, renorm_eps, slot_clamp, dtype, ws, L,
-                             st);
+                             st, kq);
     if (rc) return rc;
   }
   return 0;
