@@ -1020,17 +1020,20 @@ linear_kreg_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>:
 }
 
 // ---------------------------------------------------------------------------
-template <int DT>
+// GH: the hidden-side products come precomputed in gh ([M][3H] fp32, row stride ldgh, without b_hh); Hb and Whh
+// are not read.
+template <int DT, bool GH>
 __global__ void __launch_bounds__(256)
 gru_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const typename MM<DT>::T* __restrict__ Hb,
            int64_t ldhb, const float* __restrict__ Hf, int64_t ldh, const typename MM<DT>::T* __restrict__ Wih,
            const typename MM<DT>::T* __restrict__ Whh, const float* __restrict__ bih, const float* __restrict__ bhh,
            float* __restrict__ out, int64_t ldo, typename MM<DT>::T* __restrict__ out2, int64_t ldo2, int64_t M,
-           int64_t H, int64_t Kx) {
+           int64_t H, int64_t Kx, const float* __restrict__ gh, int64_t ldgh) {
   using A = MM<DT>;
   constexpr int KPL = A::KPL;
   constexpr int BLK = 4 * KPL;
-  __shared__ float red[4][2][6][4][64];  // 48 KB
+  constexpr int NQ = GH ? 3 : 6;         // products formed here
+  __shared__ float red[4][2][NQ][4][64];  // 48 KB (24 KB with GH)
   const int64_t tiles_n = (H + 15) / 16;
   const int64_t tm = blockIdx.x / tiles_n, tn = blockIdx.x - tm * tiles_n;
   const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, g = lane >> 4, li = lane & 15;
@@ -1046,20 +1049,27 @@ gru_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const typename
   const int64_t col = tn * 16 + li;
   const int t_e = wid >> 1;
   float bir = 0.f, biz = 0.f, bin = 0.f, bhr = 0.f, bhz = 0.f, bhn = 0.f, hv[2] = {0.f, 0.f};
+  float ghv[2][3] = {{0.f, 0.f, 0.f}, {0.f, 0.f, 0.f}};
   if (col < H) {
     if (bih) { bir = bih[col]; biz = bih[H + col]; bin = bih[2 * H + col]; }
     if (bhh) { bhr = bhh[col]; bhz = bhh[H + col]; bhn = bhh[2 * H + col]; }
 #pragma unroll
     for (int rr = 0; rr < 2; ++rr) {
       const int64_t row = tm * 32 + 16 * t_e + 4 * g + 2 * (wid & 1) + rr;
-      if (row < M) hv[rr] = Hf[row * ldh + col];
+      if (row < M) {
+        hv[rr] = Hf[row * ldh + col];
+        if constexpr (GH) {
+#pragma unroll
+          for (int q = 0; q < 3; ++q) ghv[rr][q] = gh[row * ldgh + q * H + col];
+        }
+      }
     }
   }
-  f32x4 acc[2][6];
+  f32x4 acc[2][NQ];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 6; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < NQ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   {
     const typename A::T* pa[2] = {X + rows[0] * ldx + KPL * g, X + rows[1] * ldx + KPL * g};
     const typename A::T* pw[3] = {Wih + colr * Kx + KPL * g, Wih + (H + colr) * Kx + KPL * g,
@@ -1076,7 +1086,7 @@ gru_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const typename
       }
     }
   }
-  {
+  if constexpr (!GH) {
     const typename A::T* pa[2] = {Hb + rows[0] * ldhb + KPL * g, Hb + rows[1] * ldhb + KPL * g};
     const typename A::T* pw[3] = {Whh + colr * H + KPL * g, Whh + (H + colr) * H + KPL * g,
                                   Whh + (2 * H + colr) * H + KPL * g};
@@ -1095,7 +1105,7 @@ gru_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const typename
 #pragma unroll
   for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int q = 0; q < 6; ++q)
+    for (int q = 0; q < NQ; ++q)
 #pragma unroll
       for (int r = 0; r < 4; ++r) red[wid][t][q][r][lane] = acc[t][q][r];
   __syncthreads();
@@ -1109,8 +1119,12 @@ gru_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const typename
     if (row >= M) continue;
     float gsum[6];
 #pragma unroll
-    for (int q = 0; q < 6; ++q)
+    for (int q = 0; q < NQ; ++q)
       gsum[q] = red[0][t][q][r][lane] + red[1][t][q][r][lane] + red[2][t][q][r][lane] + red[3][t][q][r][lane];
+    if constexpr (GH) {
+#pragma unroll
+      for (int q = 0; q < 3; ++q) gsum[3 + q] = ghv[rr][q];
+    }
     const float rg = sigmoid_f(gsum[0] + bir + gsum[3] + bhr);
     const float zg = sigmoid_f(gsum[1] + biz + gsum[4] + bhz);
     const float ng = tanh_f(gsum[2] + bin + rg * (gsum[5] + bhn));
@@ -1425,9 +1439,14 @@ struct LnqArgs {
   float eps;
   void* sb_out;          // [B][N][D] in the operand type: row stride ldsb, frame stride sbb (nullable)
   int64_t ldsb, sbb;
+  const void* whh;       // GH: GRU hidden weights [3D][D] (operand type)
+  float* gh;             // GH: s W_hh^T, [B][N][3D] fp32 (row stride 3D), without the bias
 };
 
-template <int DT, int NT, int DD, int NCB, bool LNQ>
+// With GH (LNQ only) the workgroup also forms the GRU's hidden-side product for its frame's rows and its column
+// block of each of the three gates, s W_hh^T with s the slot rows in the operand type (the same operand the GRU
+// would multiply): phase 3, after attn.V, from the slot rows written to the q tile once the logits are done.
+template <int DT, int NT, int DD, int NCB, bool LNQ, bool GH>
 __global__ void __launch_bounds__(64 * CF_WAVES)
 core_fused_t_kernel(const typename MM<DT>::T* __restrict__ q, const typename MM<DT>::T* __restrict__ k,
                     const typename MM<DT>::T* __restrict__ vt, int64_t Mp, typename MM<DT>::T* __restrict__ out,
@@ -1470,10 +1489,12 @@ core_fused_t_kernel(const typename MM<DT>::T* __restrict__ q, const typename MM<
         if (i < NVB) vr[c][i] = *reinterpret_cast<const uint4*>(vp + 32 * i);
     }
   }
+  static_assert(!GH || LNQ, "the hidden-side product takes the slot rows of the LNQ form");
+  constexpr int EPL = DD / 64, RPW = NS / NW;
+  TT xh[GH ? RPW : 1][GH ? EPL : 1];   // GH: the slot rows in the operand type, written to sq after phase 1
   if constexpr (LNQ) {
     // LayerNorm of the frame's slot rows into sq: wave w takes rows w, w + NW, ...; lane l holds elements
     // l + 64 e.  Rows n >= N repeat row N - 1 (their logits are masked).
-    constexpr int EPL = DD / 64, RPW = NS / NW;
     static_assert(DD % 64 == 0 && NS % NW == 0, "whole rows per wave");
     float xs[RPW][EPL];
 #pragma unroll
@@ -1513,6 +1534,7 @@ core_fused_t_kernel(const typename MM<DT>::T* __restrict__ q, const typename MM<
       for (int e = 0; e < EPL; ++e) {
         sq[n * QP + lane + 64 * e] = A::fromf((xs[r][e] - mean) * rstd * gw[e] + gb[e]);
         if (sbo != nullptr && n < a.N) sbo[(int64_t)n * ln.ldsb + lane + 64 * e] = A::fromf(xs[r][e]);
+        if constexpr (GH) xh[r][e] = A::fromf(xs[r][e]);
       }
     }
   } else {
@@ -1599,6 +1621,28 @@ core_fused_t_kernel(const typename MM<DT>::T* __restrict__ q, const typename MM<
       if (li == 0) srs[wid * NS + nt * 16 + 4 * g + r] = v;
     }
   __syncthreads();
+  // GH: the logits are done with sq; it now takes the slot rows, and the W_hh rows of this wave's gate column tiles
+  // are requested before phase 2 so that they arrive while it runs.
+  constexpr int GCB = DD / NCB, GT = GH ? 3 * GCB / 16 : 0, GPW = GH ? (GT + NW - 1) / NW : 1;
+  uint4 wr[GPW][GH ? NKB : 1];
+  if constexpr (GH) {
+    static_assert((3 * GCB) % 16 == 0 && GCB % 16 == 0, "whole 16-column gate tiles");
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) sq[(wid + NW * r) * QP + lane + 64 * e] = xh[r][e];
+    const TT* whh = reinterpret_cast<const TT*>(ln.whh);
+#pragma unroll
+    for (int c = 0; c < GPW; ++c) {
+      const int ct = wid + NW * c;
+      if (ct < GT) {
+        const int j = (ct / (GCB / 16)) * DD + blockIdx.y * GCB + (ct % (GCB / 16)) * 16 + li;
+        const TT* wp = whh + (int64_t)j * DD + 8 * g;
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) wr[c][kb] = *reinterpret_cast<const uint4*>(wp + 32 * kb);
+      }
+    }
+  }
   // ---- phase 2: this wave's column tiles
   const bool renorm = a.renorm_eps >= 0.f;
   float rinv[NT][4];
@@ -1653,6 +1697,33 @@ core_fused_t_kernel(const typename MM<DT>::T* __restrict__ q, const typename MM<
         const int n = nt * 16 + 4 * g + r;
         if (n < a.N) out[b * a.ob + (int64_t)n * a.ldo + d] = A::fromf((acc[nt][r] + epsv) * rinv[nt][r]);
       }
+  }
+  if constexpr (GH) {
+    // ---- phase 3: gh[n][j] = sum_i s[n][i] W_hh[j][i] for this wave's gate column tiles
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < GPW; ++c) {
+      const int ct = wid + NW * c;
+      if (ct >= GT) break;
+      const int j = (ct / (GCB / 16)) * DD + blockIdx.y * GCB + (ct % (GCB / 16)) * 16 + li;
+      f32x4 acc[NT];
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+        const typename A::Op bq = __builtin_bit_cast(typename A::Op, wr[c][kb]);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[nt] = A::mfma(A::load(sq + (nt * 16 + li) * QP + 32 * kb + 8 * g), bq, acc[nt]);
+      }
+      float* ghf = ln.gh + b * (int64_t)a.N * (3 * DD);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int n = nt * 16 + 4 * g + r;
+          if (n < a.N) ghf[(int64_t)n * (3 * DD) + j] = acc[nt][r];
+        }
+    }
   }
 }
 
@@ -1715,6 +1786,11 @@ static int launch_core(const void* q, int64_t ldq, int64_t qbs, const void* k, i
 // blocks per frame: eight 48-column blocks for D = 384 (config 2: 256 workgroups, one per CU; each block
 // recomputes the frame's logits, and against three 128-column blocks the wider grid still wins by ~2.5 us per
 // forward), 128-column blocks for D = 256, one block for D = 192 / 128.
+// Column blocks per frame of the fused core for D (the launcher's instantiations).
+static constexpr int cf_ncb(int64_t D) { return D == 384 ? 8 : D == 256 ? 2 : 1; }
+// The GH form holds each wave's W_hh tiles in registers: at most two 16-column gate tiles per wave.
+static constexpr bool cf_gh_fits(int64_t D, int ncb) { return (3 * D / ncb / 16 + CF_WAVES - 1) / CF_WAVES <= 2; }
+
 static bool core_fused_fits(int64_t B, int64_t N, int64_t M, int64_t D, int dtype) {
   if (dtype != HCLSM_BF16 && dtype != HCLSM_F16) return false;
   if (N < 1 || N > 32 || M < 1 || M > CF_MAXM || (D != 128 && D != 192 && D != 256 && D != 384)) return false;
@@ -1731,7 +1807,7 @@ static int launch_core_fused(const void* q, int64_t ldq, int64_t qbs, const void
   const int NT = N <= 16 ? 1 : 2;
   const int64_t Mp = (M + 31) / 32 * 32;
   const size_t lds = core_fused_lds(NT, D, Mp, 2);
-  const LnqArgs ln = lnq ? *lnq : LnqArgs{nullptr, 0, 0, nullptr, nullptr, 0.f, nullptr, 0, 0};
+  const LnqArgs ln = lnq ? *lnq : LnqArgs{nullptr, 0, 0, nullptr, nullptr, 0.f, nullptr, 0, 0, nullptr, nullptr};
   CoreArgs a;
   a.ldq = ldq; a.ldk = ldk; a.ldv = 0; a.ldo = ldo;
   a.qb = qbs; a.kb = kbs; a.vb = vbs; a.ob = obs;
@@ -1741,19 +1817,27 @@ static int launch_core_fused(const void* q, int64_t ldq, int64_t qbs, const void
   a.scale = scale; a.denom_eps = denom_eps; a.logit_clamp = logit_clamp; a.renorm_eps = renorm_eps;
 #define HCLSM_CF(DT_, NT_, DD_, NCB_)                                                                           \
   if (dtype == DT_ && NT == NT_ && D == DD_) {                                                                 \
-    if (lnq)                                                                                                   \
-      hipLaunchKernelGGL((core_fused_t_kernel<DT_, NT_, DD_, NCB_, true>), dim3((unsigned)B, NCB_),            \
+    if (lnq && ln.gh) {                                                                                        \
+      if constexpr (cf_gh_fits(DD_, NCB_))                                                                     \
+        hipLaunchKernelGGL((core_fused_t_kernel<DT_, NT_, DD_, NCB_, true, true>), dim3((unsigned)B, NCB_),    \
+                           dim3(64 * CF_WAVES), lds, st, (const MM<DT_>::T*)q, (const MM<DT_>::T*)k,          \
+                           (const MM<DT_>::T*)vt, Mp, (MM<DT_>::T*)out, a, ln);                                \
+      else                                                                                                     \
+        return 1;                                                                                              \
+    } else if (lnq)                                                                                            \
+      hipLaunchKernelGGL((core_fused_t_kernel<DT_, NT_, DD_, NCB_, true, false>), dim3((unsigned)B, NCB_),     \
                          dim3(64 * CF_WAVES), lds, st, (const MM<DT_>::T*)q, (const MM<DT_>::T*)k,            \
                          (const MM<DT_>::T*)vt, Mp, (MM<DT_>::T*)out, a, ln);                                  \
     else                                                                                                       \
-      hipLaunchKernelGGL((core_fused_t_kernel<DT_, NT_, DD_, NCB_, false>), dim3((unsigned)B, NCB_),           \
+      hipLaunchKernelGGL((core_fused_t_kernel<DT_, NT_, DD_, NCB_, false, false>), dim3((unsigned)B, NCB_),    \
                          dim3(64 * CF_WAVES), lds, st, (const MM<DT_>::T*)q, (const MM<DT_>::T*)k,            \
                          (const MM<DT_>::T*)vt, Mp, (MM<DT_>::T*)out, a, ln);                                  \
     HCLSM_LAUNCH_CHECK();                                                                                      \
     return 0;                                                                                                  \
   }
 #define HCLSM_CF_D(DT_, NT_) \
-  HCLSM_CF(DT_, NT_, 128, 1) HCLSM_CF(DT_, NT_, 192, 1) HCLSM_CF(DT_, NT_, 256, 2) HCLSM_CF(DT_, NT_, 384, 8)
+  HCLSM_CF(DT_, NT_, 128, cf_ncb(128)) HCLSM_CF(DT_, NT_, 192, cf_ncb(192)) HCLSM_CF(DT_, NT_, 256, cf_ncb(256)) \
+  HCLSM_CF(DT_, NT_, 384, cf_ncb(384))
   HCLSM_CF_D(HCLSM_BF16, 1) HCLSM_CF_D(HCLSM_BF16, 2)
   HCLSM_CF_D(HCLSM_F16, 1) HCLSM_CF_D(HCLSM_F16, 2)
 #undef HCLSM_CF_D
@@ -1950,22 +2034,30 @@ int linear_glu_rows(const void* x, int64_t ldx, int x_dtype, const void* w1, con
   return HCLSM_ERR_DTYPE;
 }
 
+// gh (nullable): the hidden-side products s W_hh^T precomputed ([M][3H] fp32, row stride ldgh); hb and w_hh are
+// then not read.
 static int gru_impl(const void* x, int64_t ldx, const void* hb, int64_t ldhb, const float* h, int64_t ldh,
                     const void* w_ih, const void* w_hh, const float* b_ih, const float* b_hh, float* out, int64_t ldo,
-                    void* out2, int64_t ldo2, int64_t M, int64_t H, int64_t Kx, int dtype, hipStream_t st) {
+                    void* out2, int64_t ldo2, int64_t M, int64_t H, int64_t Kx, int dtype, hipStream_t st,
+                    const float* gh = nullptr, int64_t ldgh = 0) {
   if (M < 0 || H < 0 || Kx < 0) return HCLSM_ERR_SHAPE;
   if (M == 0 || H == 0) return 0;
-  if (!x || !hb || !h || !w_ih || !w_hh || !out) return HCLSM_ERR_NULL;
+  if (!x || (!hb && !gh) || !h || !w_ih || (!w_hh && !gh) || !out) return HCLSM_ERR_NULL;
   const int kpl = dtype == HCLSM_F32 ? 1 : 8;
   if (Kx % (4 * kpl) || H % (4 * kpl)) return HCLSM_ERR_UNSUPPORTED;
-  if (kpl == 8 && (!al16(x) || !al16(hb) || !al16(w_ih) || !al16(w_hh) || ldx % 8 || ldhb % 8))
-    return HCLSM_ERR_UNSUPPORTED;
+  if (kpl == 8 && (!al16(x) || !al16(w_ih) || ldx % 8)) return HCLSM_ERR_UNSUPPORTED;
+  if (kpl == 8 && !gh && (!al16(hb) || !al16(w_hh) || ldhb % 8)) return HCLSM_ERR_UNSUPPORTED;
   const unsigned grid = (unsigned)(((M + 31) / 32) * ((H + 15) / 16));
 #define HCLSM_GRU(D)                                                                                        \
   if (dtype == D) {                                                                                         \
-    hipLaunchKernelGGL((gru_kernel<D>), dim3(grid), dim3(256), 0, st, (const MM<D>::T*)x, ldx,               \
-                       (const MM<D>::T*)hb, ldhb, h, ldh, (const MM<D>::T*)w_ih, (const MM<D>::T*)w_hh, b_ih, \
-                       b_hh, out, ldo, (MM<D>::T*)out2, ldo2, M, H, Kx);                                    \
+    if (gh)                                                                                                 \
+      hipLaunchKernelGGL((gru_kernel<D, true>), dim3(grid), dim3(256), 0, st, (const MM<D>::T*)x, ldx,       \
+                         (const MM<D>::T*)hb, ldhb, h, ldh, (const MM<D>::T*)w_ih, (const MM<D>::T*)w_hh, b_ih, \
+                         b_hh, out, ldo, (MM<D>::T*)out2, ldo2, M, H, Kx, gh, ldgh);                        \
+    else                                                                                                    \
+      hipLaunchKernelGGL((gru_kernel<D, false>), dim3(grid), dim3(256), 0, st, (const MM<D>::T*)x, ldx,      \
+                         (const MM<D>::T*)hb, ldhb, h, ldh, (const MM<D>::T*)w_ih, (const MM<D>::T*)w_hh, b_ih, \
+                         b_hh, out, ldo, (MM<D>::T*)out2, ldo2, M, H, Kx, gh, ldgh);                        \
     HCLSM_LAUNCH_CHECK();                                                                                   \
     return 0;                                                                                               \
   }
@@ -2275,7 +2367,7 @@ static int transpose_16(const void* src, int64_t lds, void* dst, int64_t ldd, in
 }
 
 struct SlotWs {
-  size_t q, core, upd, h, sb, m1, sfa, kv, vt, xn, xin, kq, wqt, total;
+  size_t q, core, upd, h, sb, m1, sfa, kv, vt, xn, xin, kq, wqt, gh, total;
   bool has_kq;
 };
 
@@ -2300,6 +2392,7 @@ static SlotWs slot_ws_layout(int64_t B, int64_t N, int64_t M, int64_t d, int64_t
   w.has_kq = kq;
   w.kq = o; o += kq ? al256((size_t)B * M * d * esize) : 0;
   w.wqt = o; o += kq ? al256((size_t)d * d * esize) : 0;
+  w.gh = o; o += kq ? al256(rows * 3 * d * 4) : 0;   // the GRU's hidden-side products, formed by the fused core
   w.total = o;
   return w;
 }
@@ -2358,9 +2451,12 @@ static int slot_iteration_impl(const HclsmSlotWeights* W, const float* slots_in,
   void* xn = ws + L.xn;
   bool folded = false;
   int rc = 1;
+  // GH: the fused core also forms the GRU's hidden-side products (then no iteration needs the slots in dtype)
+  float* gh = (kq != nullptr && cf_gh_fits(d, cf_ncb(d))) ? reinterpret_cast<float*>(ws + L.gh) : nullptr;
   if (kq != nullptr) {
     // updates = core(LN_pre(slots), k Wq, v^T); with make_sb the core also writes sb (the slots in dtype)
-    const LnqArgs ln{slots_in, d, N * d, W->ln_pre_w, W->ln_pre_b, 1e-5f, make_sb ? sb : nullptr, d, N * d};
+    const LnqArgs ln{slots_in, d,       N * d, W->ln_pre_w, W->ln_pre_b, 1e-5f, (make_sb && !gh) ? sb : nullptr,
+                     d,        N * d,   W->w_hh, gh};
     rc = launch_core_fused(nullptr, d, N * d, kq, ldk, k_bstride, v, v_bstride, upd, d, N * d, B, N, M, d, scale, 0.f,
                            logit_clamp, renorm_eps, dtype, st, &ln);
     if (rc == 1) return HCLSM_ERR_UNSUPPORTED;   // the caller checked core_fused_fits
@@ -2388,7 +2484,7 @@ static int slot_iteration_impl(const HclsmSlotWeights* W, const float* slots_in,
   if (rc) return rc;
   // h = GRUCell(updates, slots)
   rc = gru_impl(upd, d, sb, d, slots_in, d, W->w_ih, W->w_hh, W->b_ih, W->b_hh, h, d, nullptr, 0, rows, d, d, dtype,
-                st);
+                st, gh, 3 * d);
   if (rc) return rc;
   // m1 = ReLU(LN_mlp(h) W1^T + b1)
   rc = linear_ln_fold(h, d, W->w1, d, W->b1, m1, hidden, rows, hidden, d, 1, W->ln_mlp_w, W->ln_mlp_b, 1e-5f, nullptr,
@@ -2402,8 +2498,8 @@ static int slot_iteration_impl(const HclsmSlotWeights* W, const float* slots_in,
     if (rc) return rc;
   }
   // slots_out = clamp(h + m1 W2^T + b2); sb = the same in dtype
-  return linear_impl(m1, hidden, dtype, W->w2, hidden, W->b2, h, d, slots_out, d, HCLSM_F32, sb, d, rows, d, hidden, 0,
-                     slot_clamp, 0, nullptr, nullptr, 0.f, dtype, st);
+  return linear_impl(m1, hidden, dtype, W->w2, hidden, W->b2, h, d, slots_out, d, HCLSM_F32, gh ? nullptr : sb, d, rows,
+                     d, hidden, 0, slot_clamp, 0, nullptr, nullptr, 0.f, dtype, st);
 }
 
 static int check_slot_args(const HclsmSlotWeights* W, int64_t B, int64_t N, int64_t M, int64_t d, int64_t hidden,
