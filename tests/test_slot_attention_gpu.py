@@ -166,8 +166,9 @@ def test_config2_forward_bf16():
     ("config2", torch.float16, 4, 32, 196, 128, 160, 384),
 ])
 def test_forward_iteration_matches_oracle(mode_name, dtype, B, N, M, d, d_in, hidden):
-    """hclsm_slot_attention_forward with 16-bit operands (per iteration: LayerNorm-folded q projection,
-    attention core, GRU, MLP), partial tiles and ragged token counts; result against the oracle."""
+    """hclsm_slot_attention_forward with 16-bit operands (per iteration: the attention core, the GRU, the MLP;
+    the q projection is folded into k Wq where the fused core takes the shape, and kept otherwise), partial tiles
+    and ragged token counts; result against the oracle."""
     from hclsm_amd.kernels import slot_iteration as si
     from hclsm_amd.workloads import xavier_uniform
     g = torch.Generator().manual_seed(B * 100 + N + M)
@@ -189,15 +190,16 @@ def test_forward_iteration_matches_oracle(mode_name, dtype, B, N, M, d, d_in, hi
 
 
 @pytest.mark.parametrize("mode_name,dtype,B,N,M,d", [
-    ("config2", torch.bfloat16, 3, 32, 196, 384),    # config 2's per-frame shape: 3 column blocks of 128
-    ("reference", torch.bfloat16, 2, 5, 1, 384),     # one token, a partial slot tile
+    ("config2", torch.bfloat16, 3, 32, 196, 384),    # config 2's per-frame shape: 8 column blocks of 48, GRU hidden side in the core
+    ("reference", torch.bfloat16, 2, 5, 1, 384),     # one token, a partial slot tile (one 16-slot tile, hidden side in the core)
     ("config2", torch.float16, 2, 16, 256, 256),     # the longest token count the fused core takes
     ("reference", torch.bfloat16, 4, 17, 31, 192),   # one column block, two slot tiles, ragged tokens
     ("config2", torch.bfloat16, 2, 32, 257, 128),    # past the fused core's token limit: the two-launch core
 ])
 def test_fused_attention_core_shapes(mode_name, dtype, B, N, M, d):
     """The iteration's attention core (one launch per iteration for 16-bit operands, N <= 32, M <= 256,
-    d in {128, 192, 256, 384}) inside the forward, against the oracle."""
+    d in {128, 192, 256, 384}: the slot LayerNorm formed in the core against k Wq, and at d = 384 the GRU's
+    hidden-side products too) inside the forward, against the oracle."""
     from hclsm_amd.kernels import slot_iteration as si
     from hclsm_amd.workloads import xavier_uniform
     g = torch.Generator().manual_seed(B * 1000 + N * 10 + M)
