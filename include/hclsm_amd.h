@@ -357,7 +357,7 @@ int hclsm_slot_attention_forward(const HclsmSlotWeights* W, const float* inputs,
  * taken from a static device array of HCLSM_SLOT_NOALLOC_SCRATCH_BYTES in the library (one copy per GPU, held
  * until the process ends) instead of a caller buffer.  No allocation, free or synchronisation, so the call may
  * run under HIP graph capture.  A shape whose hclsm_slot_attention_workspace exceeds the array returns
- * HCLSM_ERR_SCRATCH before any launch (config 2, B=32 M=196 d=384 bf16, needs about 22 MB).  Calls that overlap
+ * HCLSM_ERR_SCRATCH before any launch (config 2, B=32 M=196 d=384 bf16, needs about 33 MB).  Calls that overlap
  * on one GPU (two streams, two threads) share the array and race; serialise them.
  * No counterpart in the reference: it is for callers that cannot allocate device memory (graph capture, tight
  * serving loops, harnesses that forbid hipMalloc).
