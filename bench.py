@@ -12,10 +12,14 @@ Infinity Cache, so the timed loop rotates over NSETS distinct input/output sets
 
 Prints ONE JSON line.  `value` is the scan's algorithmic bytes / average step time
 (GB/s); `roofline` prices the same kernel against MI355X's 8 TB/s HBM peak with the
-per-launch duration measured by HIP events; `roofline_valu` prices it against its VALU issue
-budget from the committed counter run; `cpu_baseline` times the reference's sequential scan loop
+average launch time of the timed region (one pair of HIP events on the launch stream around
+the K launches; per-launch percentiles come from a second, untimed loop with an event pair
+around each launch); `roofline_valu` prices it against its VALU issue budget from counters
+measured in the run (rocprofv3 --pmc passes of this script as child processes; the committed
+summary when rocprofv3 is absent); `cpu_baseline` times the reference's sequential scan loop
 written with the same torch ops on the CPU (oracle/torch_cpu.py, raw mode) on the whole
-config-1 input, on the host cores.
+config-1 input, on the host cores.  Every leg is timed the same way: one event pair around
+its timed calls.
 
 Sub-objects (`--legs`, default all): configs 2, 3 and 4, the scan at the reference's published
 shapes, and the widened rows (block scan, scan backward, Level-1, relation graph, tracking loop).
@@ -39,6 +43,7 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 MI355X_SIMDS = 1024          # 256 CUs x 4 SIMDs
 PEAK_CLOCK_GHZ = 2.4
 NSETS = 4
+STEADY_LAUNCHES = 300   # untimed, then timed, launches of the steady-state figure
 
 
 LEGS = ("slot", "events", "chain", "context", "block", "bwd", "level1", "gnn", "track")
@@ -52,7 +57,8 @@ def _parse():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--no-extra", action="store_true", help="time only the config-1 scan (configs 2-4 skipped)")
+    p.add_argument("--no-extra", action="store_true",
+                   help="time only the config-1 scan's K steps (configs 2-4 and the steady-state figure skipped)")
     p.add_argument("--legs", default=",".join(LEGS),
                    help="comma-separated sub-benchmarks to run after the metric (default: all of "
                         + ",".join(LEGS) + ")")
@@ -144,7 +150,7 @@ def _measure_counters(timeout_s=90):
     return res
 
 
-def _valu_roofline(ctr, avg_s):
+def _valu_roofline(ctr, avg_s, steady_s=None):
     """The scan is VALU-issue bound.  SQ_ACTIVE_INST_VALU counts VALU activity in units of four cycles
     (rocprofv3's VALUBusy = 400 * SQ_ACTIVE_INST_VALU / SIMDs / cycles); per SIMD and launch that is the
     busy time the instruction stream needs, priced here against the measured launch time at the peak
@@ -158,7 +164,8 @@ def _valu_roofline(ctr, avg_s):
             "valu_busy_cycles_per_simd": round(busy, 1),
             "valu_instr_per_launch": ctr["valu_instr_per_launch"],
             "trans_instr_per_launch": ctr["trans_instr_per_launch"],
-            "counter_valu_busy_pct": ctr.get("valu_busy_pct"), "source": ctr.get("source")}
+            "counter_valu_busy_pct": ctr.get("valu_busy_pct"), "source": ctr.get("source"),
+            "steady_state_frac": None if steady_s is None else round(busy / steady_s / 1e9 / PEAK_CLOCK_GHZ, 4)}
 
 
 def _cpu_threads():
@@ -203,23 +210,33 @@ def _cpu_baseline(d, reps=3):
 
 
 def _event_timing(fn, n, warmup, spread=None):
-    """Median and mean seconds per fn() call over n calls timed with HIP events on the current stream, after
-    `warmup` calls.  With a dict as `spread`, p10 / p90 (us) are added to it."""
+    """Seconds per fn() call: after `warmup` calls, n calls timed as one region between two HIP events on the
+    current stream.  No event is recorded between the calls (each record adds a marker packet and a gap on the
+    GPU's timeline).  With a dict as `spread`, a second, untimed loop of n calls with an event pair around each
+    adds the per-call median / p10 / p90 (us) to it."""
     import torch
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
-    for a, b in evs:
-        a.record()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(n):
         fn()
-        b.record()
+    e1.record()
     torch.cuda.synchronize()
-    ts = sorted(a.elapsed_time(b) * 1e-3 for a, b in evs)
+    t = e0.elapsed_time(e1) * 1e-3 / n
     if spread is not None:
-        spread["p10_us"] = round(ts[len(ts) // 10] * 1e6, 2)
-        spread["p90_us"] = round(ts[(len(ts) * 9) // 10] * 1e6, 2)
-    return ts[len(ts) // 2], sum(ts) / len(ts)
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+        for a, b in evs:
+            a.record()
+            fn()
+            b.record()
+        torch.cuda.synchronize()
+        ts = sorted(a.elapsed_time(b) * 1e-3 for a, b in evs)
+        spread["per_call_median_us"] = round(ts[len(ts) // 2] * 1e6, 2)
+        spread["per_call_p10_us"] = round(ts[len(ts) // 10] * 1e6, 2)
+        spread["per_call_p90_us"] = round(ts[(len(ts) * 9) // 10] * 1e6, 2)
+    return t
 
 
 def _rotating(fns):
@@ -244,14 +261,14 @@ def _bench_slot(dev, n, warmup, cpu):
     sets = [(torch.roll(tk, r, 0).contiguous(), torch.roll(s0, r, 0).contiguous()) for r in range(SLOT_SETS)]
     step = _rotating([lambda a=a, b=b: si.slot_attention_forward(a, b, W, 3, si.CONFIG2_MODE) for a, b in sets])
     spread = {}
-    med, avg = _event_timing(step, n, warmup, spread)
+    t = _event_timing(step, n, warmup, spread)
     fl = slot_flops()
     ntok = tokens.shape[0] * tokens.shape[1]
     res = {"workload": "config 2: 32 frames x 196 tokens x 384, 32 slots, 3 iterations, MLP 768, bf16 MFMA",
-           "metric": "tokens/s", "value": round(ntok / med, 1), "median_us": round(med * 1e6, 2), **spread,
+           "metric": "tokens/s", "value": round(ntok / t, 1), "us_per_call": round(t * 1e6, 2), **spread,
            "input_sets_rotated": SLOT_SETS,
-           "roofline": {"bound": "mfma", "achieved": round(fl / med / 1e12, 3), "peak": 2500.0,
-                        "unit": "TFLOP/s", "frac": round(fl / med / 1e12 / 2500.0, 5), "flops_per_call": fl}}
+           "roofline": {"bound": "mfma", "achieved": round(fl / t / 1e12, 3), "peak": 2500.0,
+                        "unit": "TFLOP/s", "frac": round(fl / t / 1e12 / 2500.0, 5), "flops_per_call": fl}}
     if cpu:
         from oracle.torch_cpu import slot_forward_torch
         cores, model = _cpu_threads()
@@ -282,16 +299,16 @@ def _bench_events(dev, n, warmup, cpu):
         qr, kr, vr = (torch.roll(t, r, 0).contiguous() for t in (q, k, v))
         plans.append(TrackCausalPlan(qr, kr, vr, m, capacity=total))
     spread = {}
-    med, avg = _event_timing(_rotating(plans), n, warmup, spread)
+    t = _event_timing(_rotating(plans), n, warmup, spread)
     nbytes = total * 6 * 64 * 2 * 4 + m.numel() * 4 + (1025 + 2 * total + 2 * 65536) * 4
     res = {"workload": "config 3: 1024 tracks x T=64, 6 heads x 64, p=0.15 (t=0 forced), bf16, "
                         "index build + causal event attention, packed output (one library call per step through "
                         "TrackCausalPlan: arguments checked and output / index buffers allocated once)",
-            "events": total, "metric": "event-tokens/s", "value": round(total / med, 1),
-            "grid_tokens_per_s": round(65536 / med, 1), "median_us": round(med * 1e6, 2), **spread,
+            "events": total, "metric": "event-tokens/s", "value": round(total / t, 1),
+            "grid_tokens_per_s": round(65536 / t, 1), "us_per_call": round(t * 1e6, 2), **spread,
             "input_sets_rotated": EVENT_SETS,
-            "roofline": {"bound": "hbm", "achieved": round(nbytes / med / 1e9, 2), "peak": HBM_PEAK_GBS,
-                         "unit": "GB/s", "frac": round(nbytes / med / 1e9 / HBM_PEAK_GBS, 5),
+            "roofline": {"bound": "hbm", "achieved": round(nbytes / t / 1e9, 2), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 5),
                          "bytes_per_call": nbytes}}
     if cpu:
         from oracle.torch_cpu import event_attention_torch
@@ -321,19 +338,19 @@ def _bench_block_scan(dev, n, warmup):
     A_log = -torch.rand(Dn, S, generator=g, device=dev) * 0.5
     Bm, Cm = ((torch.randn(N, T, S, generator=g, device=dev) / 4).to(bf) for _ in range(2))
     with torch.no_grad():
-        fused_med, _ = _event_timing(lambda: ssm_block_scan(z, dt_in, A_log, Bm, Cm, gate), n, warmup)
+        fused_t = _event_timing(lambda: ssm_block_scan(z, dt_in, A_log, Bm, Cm, gate), n, warmup)
 
         def unfused():
             dt = F.softplus(dt_in).clamp(1e-3, 1.0)
             return ssm_scan_fn(z, dt, A_log, Bm, Cm, backend="sequential") * F.silu(gate)
-        unfused_med, _ = _event_timing(unfused, n, warmup)
+        unfused_t = _event_timing(unfused, n, warmup)
         err = float((ssm_block_scan(z, dt_in, A_log, Bm, Cm, gate).float() - unfused().float()).abs().max()
                     / unfused().float().abs().max())
     nbytes = scan_algorithmic_bytes(N, T, Dn, S, 2, with_D=False) + N * T * Dn * 2   # + the gate read
     return {"workload": "Level-0 block scan, config-1 shape (1024 x 64 x 384, S=16, bf16): fused epilogues vs "
                         "softplus/clamp + scan + silu + product",
-            "fused_us": round(fused_med * 1e6, 2), "unfused_us": round(unfused_med * 1e6, 2),
-            "speedup": round(unfused_med / fused_med, 3), "fused_gbs": round(nbytes / fused_med / 1e9, 1),
+            "fused_us": round(fused_t * 1e6, 2), "unfused_us": round(unfused_t * 1e6, 2),
+            "speedup": round(unfused_t / fused_t, 3), "fused_gbs": round(nbytes / fused_t / 1e9, 1),
             "fused_vs_unfused_normwise": err}
 
 
@@ -364,13 +381,13 @@ def _bench_scan_bwd(dev, n, warmup):
                                   _lib.BF16, _lib.SCAN_RAW, ws.data_ptr(), ws.numel(), st)
         if rc:
             raise RuntimeError(_lib.strerror(rc))
-    med, _ = _event_timing(step, n, warmup)
+    t = _event_timing(step, n, warmup)
     nbytes = 2 * (N * T * Dn * 5 + N * T * S * 4) + 4 * (Dn * S + Dn) * 2
     return {"workload": "scan backward, config-1 shape (1024 x 64 x 384, S=16, bf16, raw + D), one C call "
                         "(checkpoint pass, reverse pass, finalize)",
-            "median_us": round(med * 1e6, 2), "workspace_bytes": wsb,
-            "roofline": {"bound": "hbm", "achieved": round(nbytes / med / 1e9, 1), "peak": HBM_PEAK_GBS,
-                         "unit": "GB/s", "frac": round(nbytes / med / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_call": nbytes}}
+            "us_per_call": round(t * 1e6, 2), "workspace_bytes": wsb,
+            "roofline": {"bound": "hbm", "achieved": round(nbytes / t / 1e9, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_call": nbytes}}
 
 
 def _bench_level1(dev, n, warmup):
@@ -404,24 +421,24 @@ def _bench_level1(dev, n, warmup):
         return hm(states, l1(ev, pad, obj), l2, mask, obj)
     with torch.no_grad():
         E = int(mask.sum().item())
-        f32_med, _ = _event_timing(packed, n, warmup)
+        f32_t = _event_timing(packed, n, warmup)
         ref = padded()
         err32 = float(((packed() - ref).norm() / ref.norm()).item())
         with torch.autocast("cuda", dtype=torch.bfloat16):
-            bf_med, _ = _event_timing(packed, n, warmup)
+            bf_t = _event_timing(packed, n, warmup)
             out_bf = packed()
         errbf = float(((out_bf.float() - ref).norm() / ref.norm()).item())
-        pad_med, _ = _event_timing(padded, n, warmup)
+        pad_t = _event_timing(padded, n, warmup)
     dm, L, H = cfg.d_model, cfg.n_layers, cfg.n_heads
     flops = E * N * (2 * D * dm + L * (2 * dm * 3 * dm + 2 * dm * dm + 3 * 2 * dm * hid) + 2 * dm * D) \
         + E * L * 2 * 2 * N * N * dm
-    tf = flops / bf_med / 1e12
+    tf = flops / bf_t / 1e12
     return {"workload": "Level-1 step, small preset: 32 clips x T=64 x 32 slots (d_slot 192), p=0.15 events (t=0 "
                         "forced), d_model 384, 3 layers, 6 heads, SwiGLU 1536, Level-2 gating; packed and sync-free "
                         "vs the padded flow",
             "events": E, "rows": E * N,
-            "packed_bf16_us": round(bf_med * 1e6, 2), "packed_fp32_us": round(f32_med * 1e6, 2),
-            "padded_fp32_us": round(pad_med * 1e6, 2), "speedup_bf16_vs_padded": round(pad_med / bf_med, 3),
+            "packed_bf16_us": round(bf_t * 1e6, 2), "packed_fp32_us": round(f32_t * 1e6, 2),
+            "padded_fp32_us": round(pad_t * 1e6, 2), "speedup_bf16_vs_padded": round(pad_t / bf_t, 3),
             "packed_fp32_vs_padded_normwise": err32, "packed_bf16_vs_padded_normwise": errbf,
             "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4), "flops_per_call": flops}}
@@ -444,9 +461,9 @@ def _bench_gnn(dev, n, warmup):
     alive = (torch.rand(Fr, N, generator=g, device=dev) < 0.8).float()
     with torch.no_grad():
         Wb, Wf = GnnWeights.from_module(m, torch.bfloat16), GnnWeights.from_module(m, torch.float32)
-        bf_med, _ = _event_timing(lambda: relation_graph_forward(x, alive, Wb, R), n, warmup)
-        f32_med, _ = _event_timing(lambda: relation_graph_forward(x, alive, Wf, R), n, warmup)
-        ref_med, _ = _event_timing(lambda: m._torch_forward(x, alive), max(n // 4, 3), 1)
+        bf_t = _event_timing(lambda: relation_graph_forward(x, alive, Wb, R), n, warmup)
+        f32_t = _event_timing(lambda: relation_graph_forward(x, alive, Wf, R), n, warmup)
+        ref_t = _event_timing(lambda: m._torch_forward(x, alive), max(n // 4, 3), 1)
         ro, rc = m._torch_forward(x, alive)
         ob, cb = relation_graph_forward(x, alive, Wb, R)
         of, cf = relation_graph_forward(x, alive, Wf, R)
@@ -459,12 +476,12 @@ def _bench_gnn(dev, n, warmup):
     per_pair_causal = D * 2 * E + 2 * E * E + E * (E // 2) + E // 2
     flops = 2 * (R * pairs * per_pair_msg + pairs * per_pair_causal + (R + 1) * Fr * N * D * 4 * E
                  + R * Fr * N * (2 * D * D + D * D))
-    tf = flops / bf_med / 1e12
+    tf = flops / bf_t / 1e12
     return {"workload": "RelationGraph, small preset: 2048 frames x 32 slots, d_slot 192, d_edge 96, 2 rounds, 80% "
                         "live slots",
-            "pairs": pairs, "fused_bf16_us": round(bf_med * 1e6, 2), "fused_fp32_us": round(f32_med * 1e6, 2),
-            "torch_reference_fp32_us": round(ref_med * 1e6, 2), "speedup_bf16": round(ref_med / bf_med, 2),
-            "speedup_fp32": round(ref_med / f32_med, 2), "normwise_vs_torch": errs,
+            "pairs": pairs, "fused_bf16_us": round(bf_t * 1e6, 2), "fused_fp32_us": round(f32_t * 1e6, 2),
+            "torch_reference_fp32_us": round(ref_t * 1e6, 2), "speedup_bf16": round(ref_t / bf_t, 2),
+            "speedup_fp32": round(ref_t / f32_t, 2), "normwise_vs_torch": errs,
             "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4), "flops_per_call": flops}}
 
@@ -500,10 +517,10 @@ def _bench_track(dev, n, warmup):
 
     with torch.no_grad():
         Wb, Wf = TrackerWeights.from_module(m, torch.bfloat16), TrackerWeights.from_module(m, torch.float32)
-        bf_med, _ = _event_timing(lambda: track_sequence(x, alive, Wb), n, warmup)
-        bfh_med, _ = _event_timing(lambda: track_sequence(x, alive, Wb, with_hidden=True), n, warmup)
-        f32h_med, _ = _event_timing(lambda: track_sequence(x, alive, Wf, with_hidden=True), n, warmup)
-        ref_med, _ = _event_timing(reference_loop, 3, 1)
+        bf_t = _event_timing(lambda: track_sequence(x, alive, Wb), n, warmup)
+        bfh_t = _event_timing(lambda: track_sequence(x, alive, Wb, with_hidden=True), n, warmup)
+        f32h_t = _event_timing(lambda: track_sequence(x, alive, Wf, with_hidden=True), n, warmup)
+        ref_t = _event_timing(reference_loop, 3, 1)
         rt, ra, rh = reference_loop()
         got = track_sequence(x, alive, Wf, with_hidden=True)
         agree = float((got["tracked"] == rt).all(-1).float().mean().item())
@@ -511,12 +528,12 @@ def _bench_track(dev, n, warmup):
     # pair MLP: |a - b| block of the first layer (D x D), second layer (D x D/4), score (D/4);
     # per-node projections of the first layer's [a; b] blocks (2 x D x D per slot row)
     flops = 2 * (pairs * (D * D + D * (D // 4) + D // 4) + B * T * N * 2 * D * D)
-    tf = flops / bf_med / 1e12
+    tf = flops / bf_t / 1e12
     return {"workload": "slot tracking loop, small preset: 32 clips x 64 frames x 32 slots, d_slot 192, 80% live "
                         "slots, 20 Sinkhorn iterations per frame",
-            "pairs": pairs, "fused_bf16_us": round(bf_med * 1e6, 2), "fused_bf16_with_gru_us": round(bfh_med * 1e6, 2),
-            "fused_fp32_with_gru_us": round(f32h_med * 1e6, 2), "torch_reference_fp32_us": round(ref_med * 1e6, 2),
-            "speedup_bf16_with_gru": round(ref_med / bfh_med, 2), "speedup_fp32_with_gru": round(ref_med / f32h_med, 2),
+            "pairs": pairs, "fused_bf16_us": round(bf_t * 1e6, 2), "fused_bf16_with_gru_us": round(bfh_t * 1e6, 2),
+            "fused_fp32_with_gru_us": round(f32h_t * 1e6, 2), "torch_reference_fp32_us": round(ref_t * 1e6, 2),
+            "speedup_bf16_with_gru": round(ref_t / bfh_t, 2), "speedup_fp32_with_gru": round(ref_t / f32h_t, 2),
             "fp32_tracked_rows_equal_to_torch": agree,
             "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4), "flops_per_call": flops,
@@ -527,8 +544,8 @@ def _bench_track(dev, n, warmup):
 def _bench_scan_context(dev, n, warmup):
     """The reference's published scan shapes (docs/benchmarks.md:16-19: T4, Triton 0.16 / 1.83 ms,
     sequential loop 6.22 / 69.64 ms), drawn as scripts/benchmark_kernels.py:132-136 draws them (fp32:
-    x ~ N(0,1), dt ~ U(0,1) + 0.01, A_log, B, C ~ N(0,1)) and timed the same way (events around each
-    ssm_scan_fn call, default backend).  Context only: other hardware, and not this bench's metric."""
+    x ~ N(0,1), dt ~ U(0,1) + 0.01, A_log, B, C ~ N(0,1)) and timed as the other legs (one event pair around
+    n ssm_scan_fn calls, default backend).  Context only: other hardware, and not this bench's metric."""
     import torch
     from hclsm_amd.kernels import ssm_scan_fn
     rows = []
@@ -540,21 +557,21 @@ def _bench_scan_context(dev, n, warmup):
         A_log = torch.randn(Dn, S, generator=g, device=dev)
         Bp = torch.randn(BN, T, S, generator=g, device=dev)
         C = torch.randn(BN, T, S, generator=g, device=dev)
-        med, avg = _event_timing(lambda: ssm_scan_fn(x, dt, A_log, Bp, C), n, warmup)
+        t = _event_timing(lambda: ssm_scan_fn(x, dt, A_log, Bp, C), n, warmup)
         rows.append({"config": name, "shape": {"BN": BN, "T": T, "d_inner": Dn, "d_state": S}, "dtype": "f32",
-                     "ms_per_call": round(med * 1e3, 4), "mean_ms": round(avg * 1e3, 4),
+                     "ms_per_call": round(t * 1e3, 4),
                      "reference_published_ms": {"triton_t4": t4_triton, "sequential_t4": t4_seq}})
     # config 0 (the fp32 parity config, 128 x 16 x 256, S=16, raw + D), through ssm_scan_fn as a caller
     # would call it: launch-bound, so the time is mostly the call's host path
     from hclsm_amd.workloads import scan_algorithmic_bytes, scan_config
     c0 = {k: v.to(dev) for k, v in scan_config(0).items()}
-    med, avg = _event_timing(lambda: ssm_scan_fn(c0["x"], c0["dt"], c0["A_log"], c0["B"], c0["C"], D=c0["D"]), n,
+    t = _event_timing(lambda: ssm_scan_fn(c0["x"], c0["dt"], c0["A_log"], c0["B"], c0["C"], D=c0["D"]), n,
                              warmup)
     N0, T0, D0 = c0["x"].shape
     b0 = scan_algorithmic_bytes(N0, T0, D0, c0["B"].shape[2], 4)
     rows.append({"config": "config 0", "shape": {"BN": N0, "T": T0, "d_inner": D0, "d_state": c0["B"].shape[2]},
-                 "dtype": "f32", "ms_per_call": round(med * 1e3, 4), "mean_ms": round(avg * 1e3, 4),
-                 "algorithmic_bytes": b0, "gbs": round(b0 / med / 1e9, 1)})
+                 "dtype": "f32", "ms_per_call": round(t * 1e3, 4),
+                 "algorithmic_bytes": b0, "gbs": round(b0 / t / 1e9, 1)})
     return rows
 
 
@@ -601,22 +618,22 @@ def _bench_chain(dev, n, warmup, cpu):
     err = normwise_rel_err(ys[0][sel].float().cpu().numpy(), ref)
     if not err <= 2e-2:
         raise SystemExit(f"bench.py: config-4 scan parity failed (normwise {err:.3e})")
-    s_med, _ = _event_timing(scans, n, warmup)
-    a_med, _ = _event_timing(attn, n, warmup)
+    s_t = _event_timing(scans, n, warmup)
+    a_t = _event_timing(attn, n, warmup)
     sb = scan_algorithmic_bytes(N, T, Dn, S, 2)
     # q, k, v read and o written once per event; the mask; the index tables (offsets, packed indices and
     # positions, the two (N, T) maps)
     ab = total * H * dh * 2 * 4 + m.numel() * 4 + (N + 1 + 2 * total + 2 * N * T) * 4
     res = {"workload": "config 4: 4 chained scans (1024 seq x T=1024 x 768, S=16, bf16, raw + skip), then "
                        "index + causal event attention (p=0.05, t=0 forced, 12 heads x 64, packed output)",
-           "metric": "chain ms (lower is better)", "chain_ms": round((s_med + a_med) * 1e3, 4),
-           "scan_us_each": round(s_med / 4 * 1e6, 1), "scan_bytes_each": sb, "events": total,
-           "attn_us": round(a_med * 1e6, 2), "event_tokens_per_s": round(total / a_med, 1),
-           "scan_roofline": {"bound": "hbm", "achieved": round(4 * sb / s_med / 1e9, 2), "peak": HBM_PEAK_GBS,
-                             "unit": "GB/s", "frac": round(4 * sb / s_med / 1e9 / HBM_PEAK_GBS, 4),
+           "metric": "chain ms (lower is better)", "chain_ms": round((s_t + a_t) * 1e3, 4),
+           "scan_us_each": round(s_t / 4 * 1e6, 1), "scan_bytes_each": sb, "events": total,
+           "attn_us": round(a_t * 1e6, 2), "event_tokens_per_s": round(total / a_t, 1),
+           "scan_roofline": {"bound": "hbm", "achieved": round(4 * sb / s_t / 1e9, 2), "peak": HBM_PEAK_GBS,
+                             "unit": "GB/s", "frac": round(4 * sb / s_t / 1e9 / HBM_PEAK_GBS, 4),
                              "bytes_per_call": sb, "kernel": "ssm_scan_fwd_mfma_kernel<raw,TC=2,DPL=2>"},
-           "attn_roofline": {"bound": "hbm", "achieved": round(ab / a_med / 1e9, 2), "peak": HBM_PEAK_GBS,
-                             "unit": "GB/s", "frac": round(ab / a_med / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_call": ab,
+           "attn_roofline": {"bound": "hbm", "achieved": round(ab / a_t / 1e9, 2), "peak": HBM_PEAK_GBS,
+                             "unit": "GB/s", "frac": round(ab / a_t / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_call": ab,
                              "kernel": "event_attn_kernel<bf16, causal per track> + index build"},
            "scan_parity_normwise_err": err}
     if cpu:
@@ -681,19 +698,42 @@ def main():
         launch(sets[i % NSETS])
     torch.cuda.synchronize()
 
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    # the timed region: K launches between two HIP events on the launch stream, no event recorded between the
+    # launches (each record adds a marker packet and a gap on the GPU's timeline)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    e0.record()
+    for i in range(args.steps):
+        launch(sets[i % NSETS])
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    avg = e0.elapsed_time(e1) * 1e-3 / args.steps   # seconds per launch, launch to launch on the GPU
+    # spread: a second, untimed loop of K launches with an event pair around each
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
     for i, (a, b) in enumerate(evs):
         a.record()
         launch(sets[i % NSETS])
         b.record()
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    durs = sorted(a.elapsed_time(b) * 1e-3 for a, b in evs)   # seconds per launch
-    avg = sum(durs) / len(durs)
+    durs = sorted(a.elapsed_time(b) * 1e-3 for a, b in evs)
     med = durs[len(durs) // 2]
     p10, p90 = durs[len(durs) // 10], durs[(len(durs) * 9) // 10]
+    # steady state: in a fresh process the launch time falls over the first few hundred launches (70 -> 64 us on
+    # one box over ~400), so a short W / K window times part of that descent.  300 more launches, then 300 timed as
+    # one region; reported beside the roofline, not as it.
+    steady = None
+    if not args.no_extra:
+        for i in range(STEADY_LAUNCHES):
+            launch(sets[i % NSETS])
+        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record()
+        for i in range(STEADY_LAUNCHES):
+            launch(sets[i % NSETS])
+        s1.record()
+        torch.cuda.synchronize()
+        steady = s0.elapsed_time(s1) * 1e-3 / STEADY_LAUNCHES
 
     # correctness spot check of the last output against the oracle (8 sequences)
     from oracle.ssm_scan import normwise_rel_err, ssm_scan_ref
@@ -740,9 +780,14 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": ctr.get("hbm_bytes_per_launch"),
                      "traffic_source": ctr.get("source"),
                      "kernel": "ssm_scan_fwd_mfma_kernel<raw,TC=4,DPL=2>",
-                     "avg_launch_us": round(avg * 1e6, 3), "median_launch_us": round(med * 1e6, 3),
-                     "p10_launch_us": round(p10 * 1e6, 3), "p90_launch_us": round(p90 * 1e6, 3)},
-        "roofline_valu": _valu_roofline(ctr, avg),
+                     "avg_launch_us": round(avg * 1e6, 3),
+                     "per_launch_events": {"median_us": round(med * 1e6, 3), "p10_us": round(p10 * 1e6, 3),
+                                           "p90_us": round(p90 * 1e6, 3)},
+                     "steady_state": None if steady is None else {
+                         "launches_before": args.warmup + 2 * args.steps + STEADY_LAUNCHES,
+                         "us_per_launch": round(steady * 1e6, 3), "achieved": round(nbytes / steady / 1e9, 2),
+                         "frac": round(nbytes / steady / 1e9 / HBM_PEAK_GBS, 4)}},
+        "roofline_valu": _valu_roofline(ctr, avg, steady),
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = _cpu_baseline(d)
@@ -765,6 +810,7 @@ def main():
             if leg in legs:
                 key, fn = runs[leg]
                 out[key] = fn()
+
     print(json.dumps(out), flush=True)
 
 
