@@ -193,6 +193,7 @@ def test_forward_iteration_matches_oracle(mode_name, dtype, B, N, M, d, d_in, hi
     ("config2", torch.bfloat16, 3, 32, 196, 384),    # config 2's per-frame shape: 8 column blocks of 48, GRU hidden side in the core
     ("reference", torch.bfloat16, 2, 5, 1, 384),     # one token, a partial slot tile (one 16-slot tile, hidden side in the core)
     ("config2", torch.float16, 2, 16, 256, 256),     # the longest token count the fused core takes
+    ("config2", torch.float16, 2, 32, 100, 384),     # fp16 operands with the hidden side in the core
     ("reference", torch.bfloat16, 4, 17, 31, 192),   # one column block, two slot tiles, ragged tokens
     ("config2", torch.bfloat16, 2, 32, 257, 128),    # past the fused core's token limit: the two-launch core
 ])
