@@ -48,7 +48,7 @@ STEADY_LAUNCHES = 300   # untimed, then timed, launches of the steady-state figu
 
 LEGS = ("slot", "events", "chain", "context", "block", "bwd", "level1", "gnn", "track")
 SLOT_SETS = 64     # config-2 token / slot sets rotated over the timed steps (9.6 MB of tokens each)
-EVENT_SETS = 16    # config-3 q / k / v sets rotated over the timed steps (24 MB of event rows each)
+EVENT_SETS = 24    # config-3 q / k / v sets rotated over the timed steps (24 MB of event rows each, > 512 MB in all)
 
 
 def _parse():
