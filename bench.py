@@ -545,7 +545,8 @@ def _bench_scan_context(dev, n, warmup):
     """The reference's published scan shapes (docs/benchmarks.md:16-19: T4, Triton 0.16 / 1.83 ms,
     sequential loop 6.22 / 69.64 ms), drawn as scripts/benchmark_kernels.py:132-136 draws them (fp32:
     x ~ N(0,1), dt ~ U(0,1) + 0.01, A_log, B, C ~ N(0,1)) and timed as the other legs (one event pair around
-    n ssm_scan_fn calls, default backend).  Context only: other hardware, and not this bench's metric."""
+    n ssm_scan_fn calls, default backend); config 0; and the reference's published slot-attention shapes.
+    Context only: other hardware, and not this bench's metric."""
     import torch
     from hclsm_amd.kernels import ssm_scan_fn
     rows = []
@@ -572,6 +573,24 @@ def _bench_scan_context(dev, n, warmup):
     rows.append({"config": "config 0", "shape": {"BN": N0, "T": T0, "d_inner": D0, "d_state": c0["B"].shape[2]},
                  "dtype": "f32", "ms_per_call": round(t * 1e3, 4),
                  "algorithmic_bytes": b0, "gbs": round(b0 / t / 1e9, 1)})
+    # the reference's published slot-attention shapes (docs/benchmarks.md:27-30: T4, naive / Triton), drawn as
+    # scripts/benchmark_kernels.py:79-90 draws them (B = min(batch_size, 16); Q (B, N, D), K, V (B, M, D) fp32
+    # randn); one timed call is n_iterations calls of slot_attention_fn with the default backend
+    from hclsm_amd.kernels import slot_attention_fn
+    for name, B, N, M, D, it, t4_naive, t4_triton in (("slot tiny", 16, 16, 196, 128, 3, 0.29, 0.45),
+                                                      ("slot base", 2, 64, 196, 256, 7, 1.62, 3.64)):
+        g = torch.Generator(device=dev).manual_seed(9)
+        Q = torch.randn(B, N, D, generator=g, device=dev)
+        K = torch.randn(B, M, D, generator=g, device=dev)
+        V = torch.randn(B, M, D, generator=g, device=dev)
+
+        def run(Q=Q, K=K, V=V, it=it):
+            for _ in range(it):
+                slot_attention_fn(Q, K, V)
+        t = _event_timing(run, n, warmup)
+        rows.append({"config": name, "shape": {"B": B, "N": N, "M": M, "D": D, "iterations": it}, "dtype": "f32",
+                     "ms_per_call": round(t * 1e3, 4),
+                     "reference_published_ms": {"naive_t4": t4_naive, "triton_t4": t4_triton}})
     return rows
 
 

@@ -30,6 +30,9 @@ _EPS_BACKENDS = ("auto", "triton", "hip")
 TRITON_AVAILABLE = False
 
 
+_WS_BYTES: dict = {}   # (B, N, M, dtype code) -> hclsm_slot_attn_core_workspace
+
+
 def _core_raw(Q, K, V, scale, denom_eps, logit_clamp=None, renorm_eps=None, want_attn=True,
               attn_dtype=None):
     B, N, D = Q.shape
@@ -40,8 +43,15 @@ def _core_raw(Q, K, V, scale, denom_eps, logit_clamp=None, renorm_eps=None, want
     at = attn_dtype or io
     attn = torch.empty((B, N, M), dtype=at, device=Q.device) if want_attn else None
     L = _lib.lib()
-    wsb = L.hclsm_slot_attn_core_workspace(B, N, M, _lib.dtype_code(io))
-    ws = torch.empty(max(int(wsb), 16), dtype=torch.uint8, device=Q.device)
+    key = (B, N, M, _lib.dtype_code(io))
+    wsb = _WS_BYTES.get(key)
+    if wsb is None:
+        wsb = int(L.hclsm_slot_attn_core_workspace(*key))
+        _lib.check(wsb if wsb < 0 else 0, "hclsm_slot_attn_core_workspace")
+        if len(_WS_BYTES) > 256:
+            _WS_BYTES.clear()
+        _WS_BYTES[key] = wsb
+    ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=Q.device)
     rc = L.hclsm_slot_attn_core(
         _lib.ptr(q), D, N * D, _lib.ptr(k), D, M * D, _lib.ptr(v), D, M * D, _lib.ptr(out), D, N * D,
         _lib.ptr(attn), _lib.dtype_code(at), B, N, M, D, float(scale), float(denom_eps),
@@ -97,7 +107,10 @@ def _run(Q, K, V, scale, denom_eps):
     _check(Q, K, V)
     if scale is None:
         scale = Q.shape[-1] ** -0.5
-    return _SlotAttnCore.apply(Q, K, V, float(scale), float(denom_eps))
+    if torch.is_grad_enabled() and (Q.requires_grad or K.requires_grad or V.requires_grad):
+        return _SlotAttnCore.apply(Q, K, V, float(scale), float(denom_eps))
+    out, attn = _core_raw(Q, K, V, float(scale), float(denom_eps))   # nothing to differentiate: no graph node
+    return out.to(Q.dtype), attn.to(Q.dtype)
 
 
 def naive_slot_attention(Q, K, V, scale=None):
