@@ -1410,6 +1410,89 @@ core_update_kernel(const typename MM<DT>::T* __restrict__ P, int64_t Mp, const f
   }
 }
 
+// attn @ v for fp32 operands on a narrow grid (few frames): grid (frame, 16-column tile), the 4 waves splitting the
+// token steps (4 tokens per 16x16x4 product, step t to wave t % 4) and meeting in LDS.  v is read in place: for
+// fp32 a lane's B operand is one element, v[m][d], and the 16 lanes of a lane group read 16 consecutive columns.
+// Same output as core_update_kernel: (sum_m attn v + renorm_eps sum_m v) / (sum_m attn + M renorm_eps) when
+// renormalising.
+__global__ void __launch_bounds__(256)
+core_update_narrow_kernel(const float* __restrict__ P, int64_t Mp, const float* __restrict__ part,
+                          const float* __restrict__ v, float* __restrict__ out, CoreArgs a) {
+  using A = MM<HCLSM_F32>;
+  __shared__ float red[4][CORE_MAX_NT][4][64];   // 32 KB
+  __shared__ float csum[4][16];
+  __shared__ float rinv[CORE_MAX_NT * 16];
+  const int64_t b = blockIdx.x;
+  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, g = lane >> 4, li = lane & 15;
+  const int d = blockIdx.y * 16 + li;
+  const int dc = d < a.D ? d : a.D - 1;
+  const bool renorm = a.renorm_eps >= 0.f;
+  if (tid < a.NT * 16) {
+    float sr = 1.f;
+    if (renorm && tid < a.N) {
+      float t = 0.f;
+      for (int j = 0; j < a.MT; ++j) t += part[(b * a.MT + j) * a.N + tid];
+      sr = 1.f / (t + (float)a.M * a.renorm_eps);
+    }
+    rinv[tid] = sr;
+  }
+  f32x4 acc[CORE_MAX_NT];
+#pragma unroll
+  for (int nt = 0; nt < CORE_MAX_NT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const float* vb = v + b * a.vb + dc;
+  const float* pb = P + b * (int64_t)a.N * Mp;
+  int prow[CORE_MAX_NT];
+#pragma unroll
+  for (int nt = 0; nt < CORE_MAX_NT; ++nt) {
+    const int n = nt * 16 + li;
+    prow[nt] = n < a.N ? n : a.N - 1;
+  }
+  float cs = 0.f;
+  const int steps = (int)(Mp / 4);
+  for (int t0 = wid; t0 < steps; t0 += 8) {   // two steps per round, both loads issued first
+    float vv[2], pv[2][CORE_MAX_NT];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int t = t0 + 4 * u;
+      const int m = 4 * t + g;
+      const bool live = t < steps && m < a.M;
+      vv[u] = live ? vb[(int64_t)m * a.ldv] : 0.f;
+#pragma unroll
+      for (int nt = 0; nt < CORE_MAX_NT; ++nt)
+        pv[u][nt] = (nt < a.NT && t < steps) ? pb[(int64_t)prow[nt] * Mp + m] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      cs += vv[u];
+#pragma unroll
+      for (int nt = 0; nt < CORE_MAX_NT; ++nt)
+        if (nt < a.NT) acc[nt] = A::mfma(pv[u][nt], vv[u], acc[nt]);
+    }
+  }
+  cs += __shfl_xor(cs, 16, 64);
+  cs += __shfl_xor(cs, 32, 64);
+  if (g == 0) csum[wid][li] = cs;
+#pragma unroll
+  for (int nt = 0; nt < CORE_MAX_NT; ++nt)
+    if (nt < a.NT)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[wid][nt][r][lane] = acc[nt][r];
+  __syncthreads();
+  if (d >= a.D) return;
+  const float epsv = renorm ? a.renorm_eps * (csum[0][li] + csum[1][li] + csum[2][li] + csum[3][li]) : 0.f;
+  // outputs (slot n, column d): wave w takes slot tiles w, w + 4, ...
+  for (int nt = wid; nt < a.NT; nt += 4) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int n = nt * 16 + 4 * g + r;
+      if (n < a.N) {
+        const float sacc = red[0][nt][r][lane] + red[1][nt][r][lane] + red[2][nt][r][lane] + red[3][nt][r][lane];
+        out[b * a.ob + (int64_t)n * a.ldo + d] = (sacc + epsv) * rinv[n];
+      }
+    }
+  }
+}
+
 // Fused attention core for the iteration (16-bit operands, v given transposed per frame: vt[b][d][Mp]), one launch
 // per iteration: grid (frame, column block of D / NCB columns), 8 waves.  Each column block of a frame recomputes
 // the frame's logits and softmax (k is read from L2 by the frame's NCB workgroups), so the probabilities never leave
@@ -1740,6 +1823,22 @@ static size_t core_ws_bytes(int64_t B, int64_t N, int64_t M, int esize) {
   return p + (size_t)B * MT * N * 4;
 }
 
+// attn @ v with v in place (not transposed): the narrow-grid fp32 kernel when the 64-column grid would fill fewer
+// than half of a 256-CU device, else core_update_kernel.
+template <int DT>
+static void launch_update_plain(const typename MM<DT>::T* P, int64_t Mp, const float* part, const typename MM<DT>::T* v,
+                                typename MM<DT>::T* out, const CoreArgs& a, int64_t B, int64_t D, dim3 g2,
+                                hipStream_t st) {
+  if constexpr (DT == HCLSM_F32) {
+    if (B * ((D + CORE_DB - 1) / CORE_DB) < 128) {
+      hipLaunchKernelGGL(core_update_narrow_kernel, dim3((unsigned)B, (unsigned)((D + 15) / 16)), dim3(256), 0, st, P,
+                         Mp, part, v, out, a);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((core_update_kernel<DT>), g2, dim3(256), 0, st, P, Mp, part, v, out, a);
+}
+
 static int launch_core(const void* q, int64_t ldq, int64_t qbs, const void* k, int64_t ldk, int64_t kbs,
                        const void* v, int64_t ldv, int64_t vbs, void* out, int64_t ldo, int64_t obs, void* attn,
                        int attn_dtype, int64_t B, int64_t N, int64_t M, int64_t D, float scale, float denom_eps,
@@ -1768,8 +1867,7 @@ static int launch_core(const void* q, int64_t ldq, int64_t qbs, const void* k, i
       hipLaunchKernelGGL((core_update_t_kernel<D_>), g2, dim3(256), 0, st, (const MM<D_>::T*)ws, Mp, part,   \
                          (const MM<D_>::T*)v, (MM<D_>::T*)out, a);                                           \
     else                                                                                                     \
-      hipLaunchKernelGGL((core_update_kernel<D_>), g2, dim3(256), 0, st, (const MM<D_>::T*)ws, Mp, part,     \
-                         (const MM<D_>::T*)v, (MM<D_>::T*)out, a);                                           \
+      launch_update_plain<D_>((const MM<D_>::T*)ws, Mp, part, (const MM<D_>::T*)v, (MM<D_>::T*)out, a, B, D, g2, st); \
     HCLSM_LAUNCH_CHECK();                                                                                    \
     return 0;                                                                                                \
   }
