@@ -1147,15 +1147,16 @@ constexpr int CORE_MAX_NT = 8;  // up to 128 slots
 // P: [B][N][Mp] (Mp = 32 * ceil(M/32)) softmax in DT, zero for m >= M.  part: [B][MT][N] fp32.
 // Grid (frame, 16-token tile); the 4 waves split the D blocks, partial logits meet in LDS and
 // wave 0 finishes the softmax over slots.
-template <int DT, int AT>
-__global__ void __launch_bounds__(256)
+// NWL waves split the contraction (8 for fp32 on a grid that fills few CUs: half the blocks per wave).
+template <int DT, int AT, int NWL = 4>
+__global__ void __launch_bounds__(64 * NWL)
 core_logits_kernel(const typename MM<DT>::T* __restrict__ q, const typename MM<DT>::T* __restrict__ k,
                    typename MM<DT>::T* __restrict__ P, int64_t Mp, float* __restrict__ part,
                    typename MM<AT>::T* __restrict__ attn_out, CoreArgs a) {
   using A = MM<DT>;
   constexpr int KPL = A::KPL;
   constexpr int BLK = 4 * KPL;
-  __shared__ float red[4][CORE_MAX_NT][4][64];   // 32 KB
+  __shared__ float red[NWL][CORE_MAX_NT][4][64];   // 32 KB (64 KB with eight waves)
   const int64_t b = blockIdx.x;
   const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, li = lane & 15;
   const int mt = blockIdx.y;
@@ -1174,7 +1175,7 @@ core_logits_kernel(const typename MM<DT>::T* __restrict__ q, const typename MM<D
     qrow[nt] = q + b * a.qb + (int64_t)n * a.ldq + KPL * g;
   }
 #pragma unroll 2
-  for (int s = wid; s < nblk; s += 4) {
+  for (int s = wid; s < nblk; s += NWL) {
     const typename A::Op kb_ = A::load(kp + (int64_t)s * BLK);
 #pragma unroll
     for (int nt = 0; nt < CORE_MAX_NT; ++nt) {
@@ -1195,8 +1196,12 @@ core_logits_kernel(const typename MM<DT>::T* __restrict__ q, const typename MM<D
   for (int nt = 0; nt < CORE_MAX_NT; ++nt)
     if (nt < a.NT)
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        acc[nt][r] = red[0][nt][r][lane] + red[1][nt][r][lane] + red[2][nt][r][lane] + red[3][nt][r][lane];
+      for (int r = 0; r < 4; ++r) {
+        float t = 0.f;
+#pragma unroll
+        for (int w = 0; w < NWL; ++w) t += red[w][nt][r][lane];
+        acc[nt][r] = t;
+      }
   // softmax over slots for column m: values over (nt, r) in-lane and over g across lanes
   float mx = -INFINITY;
 #pragma unroll
@@ -1860,8 +1865,12 @@ static int launch_core(const void* q, int64_t ldq, int64_t qbs, const void* k, i
   dim3 g2((unsigned)B, (unsigned)((D + CORE_DB - 1) / CORE_DB));
 #define HCLSM_CORE(D_, A_)                                                                                   \
   if (dtype == D_ && (attn == nullptr ? A_ == D_ : attn_dtype == A_)) {                                      \
-    hipLaunchKernelGGL((core_logits_kernel<D_, A_>), g1, dim3(256), 0, st, (const MM<D_>::T*)q,             \
-                       (const MM<D_>::T*)k, (MM<D_>::T*)ws, Mp, part, (MM<A_>::T*)attn, a);                  \
+    if (D_ == HCLSM_F32 && B * (Mp / 16) < 128)                                                              \
+      hipLaunchKernelGGL((core_logits_kernel<D_, A_, 8>), g1, dim3(512), 0, st, (const MM<D_>::T*)q,         \
+                         (const MM<D_>::T*)k, (MM<D_>::T*)ws, Mp, part, (MM<A_>::T*)attn, a);                \
+    else                                                                                                     \
+      hipLaunchKernelGGL((core_logits_kernel<D_, A_>), g1, dim3(256), 0, st, (const MM<D_>::T*)q,           \
+                         (const MM<D_>::T*)k, (MM<D_>::T*)ws, Mp, part, (MM<A_>::T*)attn, a);                \
     HCLSM_LAUNCH_CHECK();                                                                                    \
     if (v_transposed)                                                                                        \
       hipLaunchKernelGGL((core_update_t_kernel<D_>), g2, dim3(256), 0, st, (const MM<D_>::T*)ws, Mp, part,   \
