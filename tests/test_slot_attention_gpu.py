@@ -19,7 +19,8 @@ def _np(t):
     return t.detach().float().cpu().numpy().astype(np.float64)
 
 
-@pytest.mark.parametrize("B,N,M,D", [(2, 16, 64, 128), (1, 8, 32, 64), (4, 32, 196, 256), (3, 32, 196, 384)])
+@pytest.mark.parametrize("B,N,M,D", [(2, 16, 64, 128), (1, 8, 32, 64), (4, 32, 196, 256), (3, 32, 196, 384),
+                                     (48, 32, 196, 384)])   # the last fills the device: the wide-grid kernels
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
 def test_core_matches_oracle(B, N, M, D, dtype, tol):
     from hclsm_amd.kernels import naive_slot_attention, slot_attention_fn
