@@ -190,6 +190,36 @@ def test_forward_iteration_matches_oracle(mode_name, dtype, B, N, M, d, d_in, hi
     assert err <= 2e-2, f"{mode_name} {dtype}: {err:.3e}"
 
 
+@pytest.mark.parametrize("mode_name,dtype,tol,B,N,M,d,hidden", [
+    ("config2", torch.bfloat16, 2e-2, 4, 32, 196, 384, 768),   # the 16-bit forward with the LayerNorm in the core
+    ("reference", torch.float32, 1e-5, 2, 8, 40, 128, 256),    # fp32: LayerNorm launches and the q projection
+])
+def test_forward_without_layernorm_affine(mode_name, dtype, tol, B, N, M, d, hidden):
+    """hclsm_slot_attention_forward with every LayerNorm weight and bias pointer NULL (the C ABI's "no affine"):
+    the result of the oracle with weights 1 and biases 0."""
+    from hclsm_amd.kernels import slot_iteration as si
+    from hclsm_amd.workloads import xavier_uniform
+    g = torch.Generator().manual_seed(B * 10 + d)
+    w = _weights(d, hidden, seed=d + N)
+    w["w_k"] = xavier_uniform((d, d), g)
+    w["w_v"] = xavier_uniform((d, d), g)
+    w = {n: t.to(dtype).float() if n in si._WEIGHT_KEYS else t for n, t in w.items()}
+    ln_keys = ("ln_pre_w", "ln_pre_b", "ln_mlp_w", "ln_mlp_b", "ln_in_w", "ln_in_b")
+    W = si.SlotWeights.from_dict({n: (None if n in ln_keys else t) for n, t in w.items()}, dtype)
+    assert not any(n in W.t for n in ln_keys)
+    ref_w = {n: _np(t) for n, t in w.items() if n not in ln_keys}
+    for n in ln_keys:
+        ref_w[n] = np.ones(d) if n.endswith("_w") else np.zeros(d)
+    tokens = torch.randn(B, M, d, generator=g)
+    slots0 = torch.randn(B, N, d, generator=g) * 0.5
+    mode = si.REFERENCE_MODE if mode_name == "reference" else si.CONFIG2_MODE
+    out = si.slot_attention_forward(tokens.cuda(), slots0.cuda(), W, 2, mode)
+    ref = sa.slot_attention_forward(tokens.numpy(), slots0.numpy(), ref_w, 2, logit_clamp=mode.logit_clamp,
+                                    renorm_eps=mode.renorm_eps, slot_clamp=mode.slot_clamp)
+    err = normwise_rel_err(_np(out), ref)
+    assert err <= tol, f"{mode_name} {dtype}: {err:.3e}"
+
+
 @pytest.mark.parametrize("mode_name,dtype,B,N,M,d", [
     ("config2", torch.bfloat16, 3, 32, 196, 384),    # config 2's per-frame shape: 8 column blocks of 48, GRU hidden side in the core
     ("reference", torch.bfloat16, 2, 5, 1, 384),     # one token, a partial slot tile (one 16-slot tile, hidden side in the core)
