@@ -14,9 +14,10 @@ Prints ONE JSON line.  `value` is the scan's algorithmic bytes / average step ti
 (GB/s); `roofline` prices the same kernel against MI355X's 8 TB/s HBM peak with the
 average launch time of the timed region (one pair of HIP events on the launch stream around
 the K launches; per-launch percentiles come from a second, untimed loop with an event pair
-around each launch); `roofline_valu` prices it against its VALU issue budget from counters
-measured in the run (rocprofv3 --pmc passes of this script as child processes; the committed
-summary when rocprofv3 is absent); `cpu_baseline` times the reference's sequential scan loop
+around each launch); `roofline_valu` prices its instruction counts (rocprofv3 --pmc passes of
+this script as child processes; the committed summary when rocprofv3 is absent) at the SIMD issue
+costs that a probe kernel (hclsm_issue_probe) measures in the same run, and sets that floor against
+the measured launch time; `cpu_baseline` times the reference's sequential scan loop
 written with the same torch ops on the CPU (oracle/torch_cpu.py, raw mode) on the whole
 config-1 input, on the host cores.  Every leg is timed the same way: one event pair around
 its timed calls.
@@ -65,6 +66,8 @@ def _parse():
     p.add_argument("--no-counters", action="store_true",
                    help="take the scan's HBM traffic and VALU counts from the committed counter summary "
                         "(profiles/ssm_scan_fwd_counters.json) instead of rocprofv3 passes in this run")
+    p.add_argument("--no-probe", action="store_true",
+                   help="skip the VALU issue-rate probe (hclsm_issue_probe) that prices the scan's instruction counts")
     p.add_argument("--copy-calibration", action="store_true",
                    help="after the timed loop, run a 1 GiB device-to-device copy 5 times (a kernel of "
                         "known traffic for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE counters)")
@@ -83,7 +86,8 @@ def _scan_counters():
 
 
 # rocprofv3 counter passes over this script's scan alone (each pass a child process of its own)
-_PMC_PASSES = (("FETCH_SIZE",), ("WRITE_SIZE",), ("SQ_ACTIVE_INST_VALU", "SQ_INSTS_VALU", "SQ_INSTS_VALU_TRANS_F32"))
+_PMC_PASSES = (("FETCH_SIZE",), ("WRITE_SIZE",), ("SQ_ACTIVE_INST_VALU", "SQ_INSTS_VALU", "SQ_INSTS_VALU_TRANS_F32",
+                                                  "SQ_INSTS_MFMA"))
 _SCAN_GRID = 196608   # config-1 launch: 1024 sequences x 3 channel blocks x 64 lanes
 _COPY_GRID = 131072   # the 1 GiB device copy of --copy-calibration
 
@@ -109,7 +113,7 @@ def _measure_counters(timeout_s=90):
             out = os.path.join(tmp, f"p{i}")
             cmd = [exe, "--pmc", *counters, "-d", out, "-o", "run", "--output-format", "csv", "--",
                    sys.executable, os.path.abspath(__file__), "--steps", "20", "--warmup", "2", "--no-cpu-baseline",
-                   "--no-extra", "--no-counters"]
+                   "--no-extra", "--no-counters", "--no-probe"]
             if counters[0] in ("FETCH_SIZE", "WRITE_SIZE"):
                 cmd.append("--copy-calibration")
             # own process group, so that a pass past its limit is ended together with the program it profiles
@@ -144,28 +148,71 @@ def _measure_counters(timeout_s=90):
     if "fetch_size_bytes" in res and "write_size_bytes" in res:
         res["hbm_bytes_per_launch"] = res["fetch_size_bytes"] + res["write_size_bytes"]
     for c, k in (("SQ_ACTIVE_INST_VALU", "sq_active_inst_valu_per_launch"), ("SQ_INSTS_VALU", "valu_instr_per_launch"),
-                 ("SQ_INSTS_VALU_TRANS_F32", "trans_instr_per_launch")):
+                 ("SQ_INSTS_VALU_TRANS_F32", "trans_instr_per_launch"), ("SQ_INSTS_MFMA", "mfma_instr_per_launch")):
         if ("scan", c) in vals:
             res[k] = int(round(vals[("scan", c)]))
     return res
 
 
-def _valu_roofline(ctr, avg_s, steady_s=None):
-    """The scan is VALU-issue bound.  SQ_ACTIVE_INST_VALU counts VALU activity in units of four cycles
-    (rocprofv3's VALUBusy = 400 * SQ_ACTIVE_INST_VALU / SIMDs / cycles); per SIMD and launch that is the
-    busy time the instruction stream needs, priced here against the measured launch time at the peak
-    engine clock: frac = busy cycles per SIMD / (launch seconds x 2.4 GHz)."""
-    if not ctr.get("sq_active_inst_valu_per_launch"):
+_PROBE_INSTR = {0: 32, 1: 32, 2: 128}   # instructions per iteration of hclsm_issue_probe kinds fma / exp / mix 1:3
+
+
+def _issue_probe(L, dev):
+    """Issue costs of the SIMD measured in this run (hclsm_issue_probe): seconds per wave-instruction per SIMD for
+    v_fma_f32, v_exp_f32 and the 1 exp : 3 FMA mix, each at 3 waves per SIMD (the config-1 scan's occupancy) and
+    at 8, the lower of the two kept.  Each figure is the median of 3 launches of about 3 ms."""
+    import torch
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    simds = 4 * cus
+    sink = torch.zeros(8 * simds * 64, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    res = {"simds": simds}
+    for kind, name in ((0, "fma"), (1, "exp"), (2, "mix_1exp_3fma")):
+        best = None
+        for w in (3, 8):
+            iters = max(8, int(4e6 / (_PROBE_INSTR[kind] * w)))
+            run = lambda: L.hclsm_issue_probe(kind, w * simds, iters, sink.data_ptr(), stream)
+            if run() or run():
+                raise RuntimeError("hclsm_issue_probe failed")
+            ts = []
+            for _ in range(3):
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                run()
+                b.record()
+                torch.cuda.synchronize()
+                ts.append(a.elapsed_time(b) * 1e-3)
+            per = sorted(ts)[1] / (w * iters * _PROBE_INSTR[kind])
+            res[f"{name}_ns_w{w}"] = round(per * 1e9, 4)
+            best = per if best is None else min(best, per)
+        res[f"{name}_ns"] = round(best * 1e9, 4)
+    return res
+
+
+def _valu_roofline(ctr, avg_s, steady_s, probe):
+    """The scan is bound by VALU issue.  Its instruction stream, priced at the issue costs the probe measured in
+    this run, gives the shortest launch the SIMDs could issue it in:
+        floor = [(VALU - transcendental - MFMA) x t_fma + transcendental x t_exp] / SIMDs  x  m,
+    with counts per launch from the counter passes (SQ_INSTS_VALU, SQ_INSTS_VALU_TRANS_F32, SQ_INSTS_MFMA;
+    matrix-core products are left unpriced, as they overlap VALU work) and m = min(1, 4 t_mix / (3 t_fma + t_exp)),
+    the probe's measured 1 exp : 3 FMA mix against the sum of its parts (m < 1 if the two classes overlap).
+    frac = floor / measured launch time; below 1 unless the kernel issues faster than the probe's own streams."""
+    if not probe or not ctr.get("valu_instr_per_launch") or not ctr.get("trans_instr_per_launch"):
         return None
-    busy = ctr["sq_active_inst_valu_per_launch"] * 4 / MI355X_SIMDS
-    ach = busy / avg_s / 1e9
-    return {"bound": "valu", "achieved": round(ach, 4), "peak": PEAK_CLOCK_GHZ,
-            "unit": "G VALU-busy cycles/s per SIMD", "frac": round(ach / PEAK_CLOCK_GHZ, 4),
-            "valu_busy_cycles_per_simd": round(busy, 1),
-            "valu_instr_per_launch": ctr["valu_instr_per_launch"],
-            "trans_instr_per_launch": ctr["trans_instr_per_launch"],
-            "counter_valu_busy_pct": ctr.get("valu_busy_pct"), "source": ctr.get("source"),
-            "steady_state_frac": None if steady_s is None else round(busy / steady_s / 1e9 / PEAK_CLOCK_GHZ, 4)}
+    simds = probe["simds"]
+    t_fma, t_exp, t_mix = probe["fma_ns"] * 1e-9, probe["exp_ns"] * 1e-9, probe["mix_1exp_3fma_ns"] * 1e-9
+    mfma = ctr.get("mfma_instr_per_launch") or 0
+    trans = ctr["trans_instr_per_launch"]
+    other = ctr["valu_instr_per_launch"] - trans - mfma
+    m = min(1.0, 4 * t_mix / (3 * t_fma + t_exp))
+    floor = (other * t_fma + trans * t_exp) / simds * m
+    return {"bound": "valu", "achieved": round(floor * 1e6, 3), "peak": round(avg_s * 1e6, 3),
+            "unit": "us per launch: issue floor of the counted instructions (achieved) vs measured (peak)",
+            "frac": round(floor / avg_s, 4),
+            "steady_state_frac": None if steady_s is None else round(floor / steady_s, 4),
+            "floor_us": round(floor * 1e6, 3), "mix_factor": round(m, 4),
+            "counts_per_launch": {"valu": ctr["valu_instr_per_launch"], "trans": trans, "mfma": mfma},
+            "issue_probe": probe, "source": ctr.get("source")}
 
 
 def _cpu_threads():
@@ -772,6 +819,7 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
+    probe = None if args.no_probe else _issue_probe(L, dev)
     achieved = nbytes / avg / 1e9
     ctr = _scan_counters()
     if not args.no_counters:
@@ -806,7 +854,7 @@ def main():
                          "launches_before": args.warmup + 2 * args.steps + STEADY_LAUNCHES,
                          "us_per_launch": round(steady * 1e6, 3), "achieved": round(nbytes / steady / 1e9, 2),
                          "frac": round(nbytes / steady / 1e9 / HBM_PEAK_GBS, 4)}},
-        "roofline_valu": _valu_roofline(ctr, avg, steady),
+        "roofline_valu": _valu_roofline(ctr, avg, steady, probe),
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = _cpu_baseline(d)

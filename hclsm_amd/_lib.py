@@ -78,6 +78,7 @@ _SIGNATURES: dict[str, list] = {
     "hclsm_slot_track_reorder_update": [_c_void_p] * 6 + [_i64] * 3 + [_c_void_p, _int, _c_void_p, _i64, _c_void_p],
     "hclsm_slot_track_sequence_workspace": [_i64, _i64, _i64, _i64, _int, _int],
     "hclsm_slot_track_sequence": [_c_void_p] * 7 + [_i64] * 5 + [_f32, _c_void_p, _int, _c_void_p, _i64, _c_void_p],
+    "hclsm_issue_probe": [_int, _i64, _int, _c_void_p, _c_void_p],
 }
 _RESTYPES = {"hclsm_strerror": ctypes.c_char_p, "hclsm_slot_attn_core_workspace": ctypes.c_int64,
              "hclsm_ssm_scan_bwd_workspace": ctypes.c_int64,

@@ -516,6 +516,20 @@ int hclsm_slot_track_sequence(const float* slots, const float* alive, float* tra
                               int64_t D, int64_t n_iters, float temperature, const void* const* params, int dtype,
                               void* workspace, int64_t workspace_bytes, void* stream);
 
+/*
+ * VALU issue-rate probe (measurement support; no counterpart in the reference, whose kernels have no
+ * roofline).  Launches `waves` one-wave workgroups; each runs `iters` iterations of a fixed block of
+ * independent VALU instructions of one class on eight register chains:
+ *   kind 0: 32 v_fma_f32;  kind 1: 32 v_exp_f32;
+ *   kind 2: 32 v_exp_f32 + 96 v_fma_f32, one exp then three FMAs (the scan's essential mix per update);
+ *   kind 3: the same 128 in blocks of 8 exps then 24 FMAs.
+ * With waves = w x (4 x compute units), the launch time / (w x iters x instructions per iteration) is a
+ * SIMD's time per instruction of that class at w waves per SIMD: the issue costs that price the scan's
+ * instruction counts in the benchmark's VALU roofline.  sink: device float[waves x 64], never written for
+ * the values the kernel computes (it keeps the chains live).  HCLSM_ERR_MODE for an unknown kind.
+ */
+int hclsm_issue_probe(int kind, int64_t waves, int iters, float* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
