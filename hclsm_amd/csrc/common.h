@@ -61,6 +61,23 @@ __device__ __forceinline__ float softplus_f(float v) {
   return v > 20.f ? v : fmaxf(v, 0.f) + l;
 }
 
+// Max / sum over the four lanes {l, l^16, l^32, l^48} (one per 16-lane row of the wave), with gfx950's row-swap
+// permutes (VALU, no LDS round trip).  permlane16_swap of (x, x) leaves, in every lane, its own row's value and
+// its neighbour row's in the two results, in row order; permlane32_swap does the same for the two halves.  The
+// combination order is the same in every lane, so all four lanes get bit-identical sums.
+__device__ __forceinline__ float rows4_max(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float rows4_sum(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // x * sigmoid(x) (torch.nn.functional.silu).
 __device__ __forceinline__ float silu_f(float g) { return g * __builtin_amdgcn_rcpf(1.f + __expf(-g)); }
 

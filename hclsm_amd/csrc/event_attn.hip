@@ -20,7 +20,7 @@
 // per key and its output is dh/4 contiguous elements: every global access of the
 // kernel is a contiguous per-lane vector, and no LDS or barrier is needed.
 // Softmax statistics (max, sum) are per query: reduced over r in-lane and over
-// the four lanes {i, i+16, i+32, i+48} with two xor shuffles.
+// the four lanes {i, i+16, i+32, i+48} with the row-swap permutes (rows4_max / rows4_sum).
 #include "internal.h"
 
 namespace hclsm {
@@ -84,6 +84,16 @@ template <> struct AttnT<HCLSM_F32> {
 };
 
 constexpr int ATTN_WAVES = 4;
+
+// Output element acc / l: a rounded fp32 product, then the conversion.  The empty asm statement keeps the
+// compiler from fusing the two into one mixed-precision FMA (a single rounding) in some kernels and not in
+// others, so every kernel here writes the same bits for the same tile.
+template <typename A>
+__device__ __forceinline__ typename A::T attn_out(float acc, float inv) {
+  float y = acc * inv;
+  asm volatile("" : "+v"(y));
+  return A::from(y);
+}
 
 // Load n contiguous elements (n a compile-time constant) from p into e[].
 template <typename T, int N>
@@ -256,8 +266,7 @@ event_attn_kernel(const typename AttnT<DT>::T* __restrict__ q, const typename At
         s[r] = ok ? s4[r] * scale_log2 : -INFINITY;
         tmax = fmaxf(tmax, s[r]);
       }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      tmax = rows4_max(tmax);
       const float m_new = fmaxf(m, tmax);
       float pr[4], psum = 0.f;
       float alpha = 1.f;
@@ -269,8 +278,7 @@ event_attn_kernel(const typename AttnT<DT>::T* __restrict__ q, const typename At
 #pragma unroll
         for (int r = 0; r < 4; ++r) pr[r] = 0.f;
       }
-      psum += __shfl_xor(psum, 16, 64);
-      psum += __shfl_xor(psum, 32, 64);
+      psum = rows4_sum(psum);
       l = l * alpha + psum;
       m = m_new;
 #pragma unroll
@@ -293,7 +301,7 @@ event_attn_kernel(const typename AttnT<DT>::T* __restrict__ q, const typename At
 #pragma unroll
       for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) o[r * NT + nt] = A::from(acc[r][nt] * inv);
+        for (int nt = 0; nt < NT; ++nt) o[r * NT + nt] = attn_out<A>(acc[r][nt], inv);
       if (out_packed && base + i < capacity) {
         TT* dst = out_packed + (base + i) * ldo + (int64_t)h * DH + g * QD;
 #pragma unroll
@@ -310,6 +318,238 @@ event_attn_kernel(const typename AttnT<DT>::T* __restrict__ q, const typename At
   }
 }
 
+// ---------------------------------------------------------------------------
+// Track-causal attention over long tracks (T > ATTN_PAIR_MIN_T) from a prebuilt index (mode 0, packed output),
+// with the K/V rows that get re-read staged in LDS.
+//
+// One workgroup holds two (track, head) units, each served by a pair of waves.  A track of n 16-row query
+// tiles reads key tile kt once for every query tile qt >= kt; tiles 0 .. n-2 are read again, the last tile
+// only once.  The pair therefore first copies rows 0 .. 16(n-1) - 1 of its unit's K and V (at most CAP rows)
+// from HBM into LDS, once, then both waves take their share of the query tiles and read those key tiles from
+// LDS; the last key tile, and any past CAP, come from global memory as in event_attn_kernel.  Every K/V row
+// then crosses HBM once (n(n+1)/2 tile reads per track otherwise, of which L2 keeps about half at config 4).
+// The two waves split the query tiles so that their key-tile counts match: counting tiles back from the last
+// one, a wave takes those at positions 0 and 3 (mod 4), the other those at 1 and 2 (n = 4: tiles 3, 0 against
+// 2, 1, 5 key tiles each).  Per tile the arithmetic is event_attn_kernel's, in the same order, so the outputs
+// are identical.
+//
+// LDS rows are stored swizzled (pair_swz), so that the K operand reads (16 rows, the same two chunks each) and
+// the V operand reads (four rows of consecutive chunks) spread over the banks.
+constexpr int ATTN_PAIR_MIN_T = 64;     // tracks of at most 64 steps (<= 4 query tiles) stay on event_attn_kernel
+constexpr int PAIR_KV_BYTES = 6144;     // per unit and tensor: 48 rows of a 64-column 16-bit head
+
+// Chunk index of (row, chunk) in a unit's LDS rows.  The chunk is XORed with the row's low bits, and rows 2m, 2m+1
+// trade places when bits 2 and 3 of the row differ, so that in one 256-byte bank cycle the K reads (rows R and R+8,
+// same chunks) and the V reads (rows R and R+4, whole rows) fall in different halves of the banks.
+__device__ __forceinline__ int pair_swz(int row, int chunk, int cpr) {
+  const int prow = row ^ (((row >> 2) ^ (row >> 3)) & 1);
+  return prow * cpr + (chunk ^ (row & (cpr - 1)));
+}
+template <int NB> struct LdsWord;
+template <> struct LdsWord<4> { using T = uint32_t; };
+template <> struct LdsWord<8> { using T = uint2; };
+template <> struct LdsWord<16> { using T = uint4; };
+
+template <int DT, int DH>
+__global__ void __launch_bounds__(256, 5)
+event_attn_pair_kernel(const typename AttnT<DT>::T* __restrict__ q, const typename AttnT<DT>::T* __restrict__ k,
+                       const typename AttnT<DT>::T* __restrict__ v, typename AttnT<DT>::T* __restrict__ out_packed,
+                       const int32_t* __restrict__ offsets, const int32_t* __restrict__ indices, int64_t nseg,
+                       int64_t T, int H, int64_t capacity, float scale_log2) {
+  using A = AttnT<DT>;
+  using TT = typename A::T;
+  constexpr int QD = DH / 4;
+  constexpr int NT = DH / 16;
+  constexpr int KPL = A::KPL;
+  constexpr int NCH = QD / KPL;
+  constexpr int ROWB = DH * (int)sizeof(TT);          // bytes of one head row
+  constexpr int CPR = ROWB / 16;                        // 16-byte chunks per row
+  constexpr int CAP = PAIR_KV_BYTES / ROWB;             // rows staged per unit
+  static_assert((CPR & (CPR - 1)) == 0, "chunks per row: a power of two");
+  static_assert(CAP % 2 == 0, "pair_swz trades rows in pairs");
+  static_assert(QD * (int)sizeof(TT) % 16 == 0 && 16 % (NT * (int)sizeof(TT)) == 0, "operand widths");
+
+  __shared__ __attribute__((aligned(16))) uint8_t s_kv[2][2][PAIR_KV_BYTES];   // [unit][K, V]
+
+  const int wv = threadIdx.x >> 6, pr = wv >> 1, half = wv & 1;
+  const int lane = threadIdx.x & 63, g = lane >> 4, li = lane & 15;
+  const int64_t unit = (int64_t)blockIdx.x * 2 + pr;
+  const bool live = unit < nseg * H;
+  const int64_t p = live ? unit / H : 0;
+  const int h = live ? (int)(unit - p * H) : 0;
+  int64_t base = 0;
+  int L = 0;
+  if (live) {
+    base = offsets[p];
+    L = offsets[p + 1] - (int32_t)base;
+  }
+
+  const int64_t rstride = (int64_t)H * DH;
+  auto row_of = [&](int i) -> int64_t {   // time step of the segment's row i (clamped to a valid row)
+    const int ic = i < L ? i : L - 1;
+    const int64_t tr = indices[base + ic];
+    return tr < 0 ? 0 : (tr >= T ? T - 1 : tr);
+  };
+  auto gptr = [&](const TT* t, int i) -> const TT* { return t + (p * T + row_of(i)) * rstride + (int64_t)h * DH; };
+
+  // stage rows 0 .. Ls - 1 of K and V, 16-byte chunks over the pair's 128 lanes: at most CAP rows, and not
+  // the last key tile, which only the last query tile reads
+  const int nqt = (L + 15) >> 4;
+  const int Ls = (nqt - 1) * 16 < CAP ? (nqt - 1) * 16 : CAP;
+  {
+    const int lt = half * 64 + lane;
+    uint8_t* sk = s_kv[pr][0];
+    uint8_t* sv = s_kv[pr][1];
+    auto gchunk = [&](const TT* t, int c) -> uint4 {
+      const int row = c / CPR, ch = c - row * CPR;
+      const int64_t go = (p * T + row_of(row)) * rstride + (int64_t)h * DH;
+      return *reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(t + go) + ch * 16);
+    };
+    auto put = [&](uint8_t* dst, int c, uint4 w) {
+      const int row = c / CPR, ch = c - row * CPR;
+      *reinterpret_cast<uint4*>(dst + pair_swz(row, ch, CPR) * 16) = w;
+    };
+    const int nch = Ls * CPR;
+    for (int c0 = lt; c0 < nch; c0 += 256) {   // two chunks of K and of V in flight per lane
+      const int c1 = c0 + 128;
+      const bool two = c1 < nch;
+      const uint4 k0 = gchunk(k, c0), v0 = gchunk(v, c0);
+      const uint4 k1 = gchunk(k, two ? c1 : c0), v1 = gchunk(v, two ? c1 : c0);
+      put(sk, c0, k0);
+      put(sv, c0, v0);
+      if (two) {
+        put(sk, c1, k1);
+        put(sv, c1, v1);
+      }
+    }
+  }
+  __syncthreads();   // staged rows of both units
+  if (!live || L <= 0) return;
+
+  const uint8_t* sk = s_kv[pr][0];
+  const uint8_t* sv = s_kv[pr][1];
+  constexpr int EPC = 16 / (int)sizeof(TT);   // elements per 16-byte chunk
+  using VW = typename LdsWord<NT * (int)sizeof(TT)>::T;
+  // K operand (QD elements of row i from element e0) and V operand (NT elements of row i from element e0,
+  // inside one chunk).  A key tile whose rows all lie below CAP reads LDS, any other tile global memory (the
+  // choice is uniform over the wave).
+  auto ld_k = [&](bool lds, int i, int e0, TT* e) {
+    if (lds) {
+      const int ic = i < L ? i : L - 1;
+#pragma unroll
+      for (int c = 0; c < QD / EPC; ++c) {
+        const uint4 w = *reinterpret_cast<const uint4*>(sk + pair_swz(ic, e0 / EPC + c, CPR) * 16);
+        __builtin_memcpy(e + c * EPC, &w, 16);
+      }
+    } else {
+      load_row<TT, QD>(gptr(k, i) + e0, e);
+    }
+  };
+  auto ld_v = [&](bool lds, int i, int e0, TT* e) {
+    if (lds) {
+      const int ic = i < L ? i : L - 1;
+      const VW w = *reinterpret_cast<const VW*>(sv + pair_swz(ic, e0 / EPC, CPR) * 16 + (e0 % EPC) * (int)sizeof(TT));
+      __builtin_memcpy(e, &w, sizeof(VW));
+    } else {
+      load_row<TT, NT>(gptr(v, i) + e0, e);
+    }
+  };
+
+  for (int back = 0; back < nqt; ++back) {
+    const int pos = back & 3;
+    if (((pos == 0 || pos == 3) ? 0 : 1) != half) continue;
+    const int qt = nqt - 1 - back;
+    const int i = qt * 16 + li;
+    TT qe[QD];
+    load_row<TT, QD>(gptr(q, i) + g * QD, qe);
+    float m = -INFINITY, l = 0.f;
+    float acc[4][NT];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) acc[r][nt] = 0.f;
+    for (int kt = 0; kt <= qt; ++kt) {
+      const bool lds = (kt + 1) * 16 <= Ls;
+      TT ke[QD];
+      ld_k(lds, kt * 16 + li, g * QD, ke);
+      TT ve[4][NT];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ld_v(lds, kt * 16 + 4 * g + r, NT * li, ve[r]);
+      f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) s4 = A::mfma(A::pack(ke + c * KPL), A::pack(qe + c * KPL), s4);
+      float s[4];
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = kt * 16 + 4 * g + r;
+        const bool ok = (i < L) && (j < L) && (j <= i);
+        s[r] = ok ? s4[r] * scale_log2 : -INFINITY;
+        tmax = fmaxf(tmax, s[r]);
+      }
+      tmax = rows4_max(tmax);
+      const float m_new = fmaxf(m, tmax);
+      float prb[4], psum = 0.f;
+      float alpha = 1.f;
+      if (m_new != -INFINITY) {
+        alpha = fast_exp2(m - m_new);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) { prb[r] = fast_exp2(s[r] - m_new); psum += prb[r]; }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) prb[r] = 0.f;
+      }
+      psum = rows4_sum(psum);
+      l = l * alpha + psum;
+      m = m_new;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        f32x4 o4 = {acc[0][nt] * alpha, acc[1][nt] * alpha, acc[2][nt] * alpha, acc[3][nt] * alpha};
+        if constexpr (KPL == 4) {
+          TT a_e[4] = {ve[0][nt], ve[1][nt], ve[2][nt], ve[3][nt]};
+          o4 = A::mfma(A::pack(a_e), A::pack_f(prb), o4);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o4 = A::mfma(ve[r][nt], prb[r], o4);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r][nt] = o4[r];
+      }
+    }
+    if (i < L && base + i < capacity) {
+      const float inv = 1.f / l;
+      TT o[QD];
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) o[r * NT + nt] = attn_out<A>(acc[r][nt], inv);
+      TT* dst = out_packed + (base + i) * rstride + (int64_t)h * DH + g * QD;
+#pragma unroll
+      for (int e = 0; e < QD; ++e) dst[e] = o[e];
+    }
+  }
+}
+
+// The staged-K/V kernel takes 16-bit heads of 32..128 columns and fp32 heads of 16..64, with 16-byte aligned
+// q / k / v (each row's head slice is then a whole number of 16-byte chunks).
+template <int DT, int DH>
+constexpr bool pair_ok() {
+  return DT == HCLSM_F32 ? (DH >= 16 && DH <= 64) : (DH >= 32 && DH <= 128);
+}
+static inline bool al16(const void* a) { return (((uintptr_t)a) & 15) == 0; }
+
+template <int DT, int DH>
+static int launch_attn_pair(const void* q, const void* k, const void* v, void* outp, const int32_t* offsets,
+                            const int32_t* indices, int64_t nseg, int64_t T, int H, int64_t cap, float scale,
+                            hipStream_t st) {
+  using TT = typename AttnT<DT>::T;
+  const unsigned grid = (unsigned)((nseg * H + 1) / 2);
+  hipLaunchKernelGGL((event_attn_pair_kernel<DT, DH>), dim3(grid), dim3(256), 0, st, (const TT*)q, (const TT*)k,
+                     (const TT*)v, (TT*)outp, offsets, indices, nseg, T, H, cap, scale * HCLSM_LOG2E);
+  HCLSM_LAUNCH_CHECK();
+  return 0;
+}
+
 template <int DT, int DH>
 static int launch_attn(int mode, const void* q, const void* k, const void* v, void* outp, void* outg,
                        const int32_t* offsets, const int32_t* indices, const uint8_t* kp, int64_t nseg,
@@ -318,6 +558,11 @@ static int launch_attn(int mode, const void* q, const void* k, const void* v, vo
   const int64_t waves = nseg * H;
   const unsigned grid = (unsigned)((waves + ATTN_WAVES - 1) / ATTN_WAVES);
   const float sl2 = scale * HCLSM_LOG2E;
+  if constexpr (pair_ok<DT, DH>()) {
+    if (mode == HCLSM_ATTN_TRACK_CAUSAL && T > ATTN_PAIR_MIN_T && outp && !outg && al16(q) && al16(k) && al16(v) &&
+        al16(outp))
+      return launch_attn_pair<DT, DH>(q, k, v, outp, offsets, indices, nseg, T, H, cap, scale, st);
+  }
   if (mode == HCLSM_ATTN_TRACK_CAUSAL)
     hipLaunchKernelGGL((event_attn_kernel<DT, DH, 0>), dim3(grid), dim3(64 * ATTN_WAVES), 0, st, (const TT*)q,
                        (const TT*)k, (const TT*)v, (TT*)outp, (TT*)outg, offsets, indices, kp, nseg, T, H, cap, sl2,
@@ -330,7 +575,7 @@ static int launch_attn(int mode, const void* q, const void* k, const void* v, vo
   return 0;
 }
 
-// MODE 3 launch (track-causal, packed, index built in the launch; T <= ATTN_IDX_TMAX).
+// MODE 3 launch (track-causal, packed, index built in the launch; T <= ATTN_PAIR_MIN_T).
 template <int DT, int DH>
 static int launch_attn_idx(const void* q, const void* k, const void* v, void* outp, int64_t nseg, int64_t T, int H,
                            int64_t cap, float scale, const AttnIdx& ix, hipStream_t st) {
@@ -422,10 +667,12 @@ extern "C" int hclsm_event_attention(const void* q, const void* k, const void* v
   }
 }
 
-// Index build and per-track causal attention in one call, on `stream`.  For T <= ATTN_IDX_TMAX (with
-// heads and a packed output to write) two launches: the row counts, then the attention, whose waves read
-// their track's events straight from the mask, take the packed offset from the counts and fill the index
-// tables as they go.  Otherwise hclsm_event_index, then hclsm_event_attention over its tables.
+// Index build and per-track causal attention in one call, on `stream`.  For T <= ATTN_PAIR_MIN_T (with heads
+// and a packed output to write) two launches: the row counts, then the attention, whose waves read their
+// track's events straight from the mask, take the packed offset from the counts and fill the index tables as
+// they go.  Longer tracks: hclsm_event_index, then hclsm_event_attention over its tables, which stages the
+// re-read K/V rows in LDS (event_attn_pair_kernel); there every head of a track would otherwise rank the same
+// mask row again.
 extern "C" int hclsm_track_causal_attention(const void* mask, int mask_dtype, int rule, const void* q,
                                             const void* k, const void* v, void* out_packed, int64_t B,
                                             int64_t T, int64_t H, int64_t dh, int64_t capacity, float scale,
@@ -444,7 +691,7 @@ extern "C" int hclsm_track_causal_attention(const void* mask, int mask_dtype, in
   int32_t* indices = offsets + B + 1;
   int32_t* rows = indices + cap;
   int32_t* slot_of = rows + cap;
-  if (B > 0 && T > 0 && T <= ATTN_IDX_TMAX && H > 0 && capacity > 0) {
+  if (B > 0 && T > 0 && T <= ATTN_PAIR_MIN_T && H > 0 && capacity > 0) {
     if (!mask || !q || !k || !v || !out_packed) return HCLSM_ERR_NULL;
     hipStream_t st = (hipStream_t)stream;
     int rc = event_counts(mask, mask_dtype, B, T, rule, counts, st);

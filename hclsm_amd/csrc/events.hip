@@ -3,7 +3,8 @@
 // Index build (bit-exact, ascending t within each row) with no host synchronisation.  For
 // B <= 16384 rows: event_count_kernel, then event_fill_prefix_kernel (below), which folds the prefix
 // sum into the fill.  Larger B, three launches:
-//   1. event_count_kernel : one wave per row; 64 timesteps per ballot, popcount.
+//   1. event_count_kernel : one wave per row; 64 timesteps per ballot, popcount (the mask loads of up to
+//                           1024 steps issued together).
 //   2. event_scan_kernel  : one workgroup; exclusive prefix sum of the counts over
 //                           tiles of 4096 rows with a running carry; also total
 //                           and max count (stats[0], stats[1]).
@@ -26,10 +27,11 @@ event_count_kernel(const void* __restrict__ mask, int mdt, int64_t B, int64_t T,
   const int lane = threadIdx.x & 63;
   if (b >= B) return;  // whole wave exits together
   int c = 0;
-  for (int64_t t0 = 0; t0 < T; t0 += 64) {
-    const int64_t t = t0 + lane;
-    const bool ev = (t < T) && is_event(mask, mdt, b * T + (t < T ? t : 0), rule);
-    c += __popcll(__ballot(ev));
+  for (int64_t t0 = 0; t0 < T; t0 += 64 * MASK_BLOCKS) {
+    bool ev[MASK_BLOCKS];
+    mask_events<MASK_BLOCKS>(mask, mdt, b, T, t0, lane, rule, ev);
+#pragma unroll
+    for (int u = 0; u < MASK_BLOCKS; ++u) c += __popcll(__ballot(ev[u]));
   }
   if (lane == 0) counts[b] = c;
 }
@@ -110,6 +112,33 @@ event_scan_kernel(const int32_t* __restrict__ counts, int64_t B, int32_t* __rest
   }
 }
 
+// One wave writes row b's part of the tables: slot_of[b, t] (rank among the row's events or -1), and for event
+// rank r, indices[off + r] = t and rows[off + r] = b.
+__device__ __forceinline__ void fill_row(const void* mask, int mdt, int64_t b, int64_t T, int rule, int lane, int32_t off,
+                                         int32_t* __restrict__ indices, int32_t* __restrict__ rows,
+                                         int32_t* __restrict__ slot_of) {
+  int32_t run = 0;
+  for (int64_t t0 = 0; t0 < T; t0 += 64 * MASK_BLOCKS) {
+    bool ev[MASK_BLOCKS];
+    mask_events<MASK_BLOCKS>(mask, mdt, b, T, t0, lane, rule, ev);
+#pragma unroll
+    for (int u = 0; u < MASK_BLOCKS; ++u) {
+      const int64_t t = t0 + 64 * u + lane;
+      const uint64_t bal = __ballot(ev[u]);
+      const int32_t rank = (int32_t)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                             __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+      if (t < T) {
+        if (slot_of) slot_of[b * T + t] = ev[u] ? run + rank : -1;
+        if (ev[u]) {
+          indices[off + run + rank] = (int32_t)t;
+          if (rows) rows[off + run + rank] = (int32_t)b;
+        }
+      }
+      run += __popcll(bal);
+    }
+  }
+}
+
 __global__ void __launch_bounds__(64 * EV_WAVES)
 event_fill_kernel(const void* __restrict__ mask, int mdt, int64_t B, int64_t T, int rule,
                   const int32_t* __restrict__ offsets, int32_t* __restrict__ indices,
@@ -118,23 +147,7 @@ event_fill_kernel(const void* __restrict__ mask, int mdt, int64_t B, int64_t T, 
   const int lane = threadIdx.x & 63;
   if (b >= B) return;
   const int32_t off = offsets[b];
-  int32_t run = 0;
-  for (int64_t t0 = 0; t0 < T; t0 += 64) {
-    const int64_t t = t0 + lane;
-    const bool ev = (t < T) && is_event(mask, mdt, b * T + (t < T ? t : 0), rule);
-    const uint64_t bal = __ballot(ev);
-    const int32_t rank = (int32_t)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
-                                                           __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
-    if (t < T) {
-      const int32_t slot = ev ? run + rank : -1;
-      if (slot_of) slot_of[b * T + t] = slot;
-      if (ev) {
-        indices[off + run + rank] = (int32_t)t;
-        if (rows) rows[off + run + rank] = (int32_t)b;
-      }
-    }
-    run += __popcll(bal);
-  }
+  fill_row(mask, mdt, b, T, rule, lane, off, indices, rows, slot_of);
 }
 
 // Fill with the prefix sum folded in (B <= PREFIX_MAX_ROWS): each workgroup sums counts[0, b0) of
@@ -179,22 +192,7 @@ event_fill_prefix_kernel(const void* __restrict__ mask, int mdt, int64_t B, int6
   for (int w = 0; w < wid; ++w) off += (b0 + w < B) ? counts[b0 + w] : 0;
   if (b < B) {
     if (lane == 0) offsets[b] = off;
-    int32_t run = 0;
-    for (int64_t t0 = 0; t0 < T; t0 += 64) {
-      const int64_t t = t0 + lane;
-      const bool ev = (t < T) && is_event(mask, mdt, b * T + (t < T ? t : 0), rule);
-      const uint64_t bal = __ballot(ev);
-      const int32_t rank = (int32_t)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
-                                                             __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
-      if (t < T) {
-        if (slot_of) slot_of[b * T + t] = ev ? run + rank : -1;
-        if (ev) {
-          indices[off + run + rank] = (int32_t)t;
-          if (rows) rows[off + run + rank] = (int32_t)b;
-        }
-      }
-      run += __popcll(bal);
-    }
+    fill_row(mask, mdt, b, T, rule, lane, off, indices, rows, slot_of);
   }
   if (blockIdx.x == gridDim.x - 1) {   // totals: every row count, summed and maxed by this workgroup
     int32_t t = 0, m = 0;

@@ -19,6 +19,48 @@ __device__ __forceinline__ bool is_event(const void* mask, int mdt, int64_t i, i
   return !(v == 0.0f);  // NaN counts as an event, like torch.nonzero
 }
 
+// Event flags of U blocks of 64 steps of mask row `row` (step t0 + 64u + lane of block u; steps past T are not
+// events), by the rule of is_event.  Every load is issued before any flag is formed, so a row of up to 64 U
+// steps costs one memory round trip instead of one per block.
+template <int U>
+__device__ __forceinline__ void mask_events(const void* mask, int mdt, int64_t row, int64_t T, int64_t t0, int lane,
+                                            int rule, bool* ev) {
+  float v[U];
+  const int64_t base = row * T;
+  switch (mdt) {
+    case HCLSM_F32: {
+      const float* m = reinterpret_cast<const float*>(mask) + base;
+#pragma unroll
+      for (int u = 0; u < U; ++u) { const int64_t t = t0 + 64 * u + lane; v[u] = t < T ? m[t] : 0.f; }
+      break;
+    }
+    case HCLSM_BF16: {
+      const uint16_t* m = reinterpret_cast<const uint16_t*>(mask) + base;
+#pragma unroll
+      for (int u = 0; u < U; ++u) { const int64_t t = t0 + 64 * u + lane; v[u] = t < T ? bf16_bits_to_f32(m[t]) : 0.f; }
+      break;
+    }
+    case HCLSM_F16: {
+      const _Float16* m = reinterpret_cast<const _Float16*>(mask) + base;
+#pragma unroll
+      for (int u = 0; u < U; ++u) { const int64_t t = t0 + 64 * u + lane; v[u] = t < T ? (float)m[t] : 0.f; }
+      break;
+    }
+    default: {   // U8: any nonzero byte is an event, whatever the rule
+      const uint8_t* m = reinterpret_cast<const uint8_t*>(mask) + base;
+#pragma unroll
+      for (int u = 0; u < U; ++u) { const int64_t t = t0 + 64 * u + lane; v[u] = (t < T && m[t] != 0) ? 1.f : 0.f; }
+      break;
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const bool in = t0 + 64 * u + lane < T;
+    ev[u] = in && (rule == HCLSM_EVENT_GT_HALF && mdt != HCLSM_U8 ? v[u] > 0.5f : !(v[u] == 0.0f));
+  }
+}
+constexpr int MASK_BLOCKS = 16;   // blocks of 64 steps per mask_events call in the index kernels
+
 
 // Y[M, N] = A . W^T (+ bias) (ReLU if relu) (+ resid) with A = X or LayerNorm(X) rows (ln != 0), the
 // row count taken as min(M, *m_dev * m_mul) when m_dev is set (read on the device), and, when glu is
