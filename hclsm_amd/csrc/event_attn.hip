@@ -123,6 +123,9 @@ struct AttnIdx {
   int32_t *offsets, *indices, *rows, *slot_of, *stats;
 };
 constexpr int ATTN_IDX_TMAX = 1024;   // MODE 3: timesteps per track held in LDS
+// MODE 3: every wave sums the counts of the tracks before its own (P^2 H / 2 loads over a launch), so it is taken
+// only up to this many tracks; more take the index build (one prefix per workgroup of rows) and mode 0.
+constexpr int64_t ATTN_IDX_MAX_TRACKS = 4096;
 
 template <int DT, int DH, int MODE>
 __global__ void __launch_bounds__(64 * ATTN_WAVES)
@@ -667,8 +670,8 @@ extern "C" int hclsm_event_attention(const void* q, const void* k, const void* v
   }
 }
 
-// Index build and per-track causal attention in one call, on `stream`.  For T <= ATTN_PAIR_MIN_T (with heads
-// and a packed output to write) two launches: the row counts, then the attention, whose waves read their
+// Index build and per-track causal attention in one call, on `stream`.  For T <= ATTN_PAIR_MIN_T and at most
+// ATTN_IDX_MAX_TRACKS tracks (with heads and a packed output to write) two launches: the row counts, then the attention, whose waves read their
 // track's events straight from the mask, take the packed offset from the counts and fill the index tables as
 // they go.  Longer tracks: hclsm_event_index, then hclsm_event_attention over its tables, which stages the
 // re-read K/V rows in LDS (event_attn_pair_kernel); there every head of a track would otherwise rank the same
@@ -691,7 +694,7 @@ extern "C" int hclsm_track_causal_attention(const void* mask, int mask_dtype, in
   int32_t* indices = offsets + B + 1;
   int32_t* rows = indices + cap;
   int32_t* slot_of = rows + cap;
-  if (B > 0 && T > 0 && T <= ATTN_PAIR_MIN_T && H > 0 && capacity > 0) {
+  if (B > 0 && T > 0 && T <= ATTN_PAIR_MIN_T && B <= ATTN_IDX_MAX_TRACKS && H > 0 && capacity > 0) {
     if (!mask || !q || !k || !v || !out_packed) return HCLSM_ERR_NULL;
     hipStream_t st = (hipStream_t)stream;
     int rc = event_counts(mask, mask_dtype, B, T, rule, counts, st);

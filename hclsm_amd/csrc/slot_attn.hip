@@ -2619,6 +2619,10 @@ static int check_slot_args(const HclsmSlotWeights* W, int64_t B, int64_t N, int6
   const int kpl = dtype == HCLSM_F32 ? 1 : 8;
   if (d % 16 || d % (4 * kpl) || hidden % (4 * kpl)) return HCLSM_ERR_UNSUPPORTED;
   if (N > 16 * CORE_MAX_NT || B > 65535) return HCLSM_ERR_UNSUPPORTED;
+  // 16-bit weights are read with 16-byte loads (the GEMMs, the GRU and the fused core's W_hh tiles)
+  if (dtype != HCLSM_F32 && (!al16(W->w_q) || !al16(W->w_ih) || !al16(W->w_hh) || !al16(W->w1) || !al16(W->w2) ||
+                             (with_kv && !al16(W->w_kv))))
+    return HCLSM_ERR_UNSUPPORTED;
   *L = slot_ws_layout(B, N, M, d, hidden, dtype == HCLSM_F32 ? 4 : 2, with_kv, d_in);
   if (workspace_bytes < (int64_t)L->total) return HCLSM_ERR_SHAPE;
   if (!al16(workspace)) return HCLSM_ERR_UNSUPPORTED;
@@ -2651,10 +2655,10 @@ static int slot_forward_impl(const HclsmSlotWeights* W, const float* inputs, int
   int rc = check_slot_args(W, B, N, M, d, hidden, dtype, workspace, workspace_bytes, true, &L, d_in);
   if (rc) return rc;
   if (B * M > 0x7fffffffLL) return HCLSM_ERR_SHAPE;
-  if (!inputs || !slots0 || !slots_out) return HCLSM_ERR_NULL;
+  if (!inputs || (N > 0 && (!slots0 || !slots_out))) return HCLSM_ERR_NULL;   // no slots: empty slot tensors
   if (d_in < 1 || n_iter < 0) return HCLSM_ERR_SHAPE;
   if (d_in % (4 * (dtype == HCLSM_F32 ? 1 : 8))) return HCLSM_ERR_UNSUPPORTED;
-  if (B == 0 || N == 0) return 0;
+  if (B == 0) return 0;   // (with no slots the keys are still formed: callers read them for slot birth)
   hipStream_t st = (hipStream_t)stream;
   char* ws = reinterpret_cast<char*>(workspace);
   const int esize = dtype == HCLSM_F32 ? 4 : 2;
@@ -2680,6 +2684,7 @@ static int slot_forward_impl(const HclsmSlotWeights* W, const float* inputs, int
   }
   (void)esize;
   const void* k = kv;
+  if (N == 0) return 0;
   if (n_iter == 0) return (int)hipMemcpyAsync(slots_out, slots0, (size_t)B * N * d * 4, hipMemcpyDeviceToDevice, st);
   // k Wq = k (Wq^T)^T once per call, so that no iteration projects the slots to queries
   const void* kq = nullptr;

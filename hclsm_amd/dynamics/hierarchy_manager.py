@@ -60,10 +60,20 @@ class HierarchyManager(nn.Module):
                                         any(p.requires_grad for p in self.parameters())):
             warn_fallback("HierarchyManager", "autograd (the fused top-down output step has no backward)")
             return False
-        if not level0_states.is_cuda or level0_states.dtype != torch.float32 or level1_states.shape[1] == 0:
+        if not level0_states.is_cuda:
+            return False   # the torch path runs HIP kernels only on the GPU; CPU tensors raise there
+        if level0_states.dtype != torch.float32:
+            warn_fallback("HierarchyManager", f"{level0_states.dtype} Level-0 states (the fused top-down output "
+                                              "step takes float32)")
+            return False
+        if level1_states.shape[1] == 0:
+            warn_fallback("HierarchyManager", "no event rows (the fused top-down output step takes at least one)")
             return False
         dl2 = None if level2_context is None else level2_context.shape[-1]
-        return top_down_supported(level0_states.shape[-1], dl2)
+        if not top_down_supported(level0_states.shape[-1], dl2):
+            warn_fallback("HierarchyManager", "a shape outside the fused top-down output step")
+            return False
+        return True
 
     def _fused(self, level0_states, level1_states, idx, level2_context, obj_mask, kpad):
         dtype = torch.float32

@@ -1,10 +1,11 @@
 """Level-1 event dynamics on MI355X: counterpart of hclsm/dynamics/level1_event.py.
 
 Same module tree and parameter names (``attn`` stays an nn.MultiheadAttention so state dicts
-load unchanged).  The attention core of every EventTransformerBlock -- per event, all N slots
-attend to each other with key padding from the alive mask (:37-52) -- runs on the MFMA
-varlen-attention kernel (``hclsm_amd.kernels.slots_attention``); the in/out projections use the
-same weights through torch GEMMs.
+load unchanged).  Without autograd, ``forward`` (padded events, the reference's call) and
+``forward_packed`` run the whole stack -- projections, LayerNorms, MHA over the slots with key padding
+from the alive mask (:37-52), SwiGLU -- in one hclsm_level1_forward call.  Under autograd the
+blocks run as torch ops around the MFMA attention core (``hclsm_amd.kernels.slots_attention``) and
+say so with a HipFallbackWarning.
 """
 
 from __future__ import annotations
@@ -15,7 +16,7 @@ import torch.nn.functional as F
 
 from hclsm_amd.kernels._common import warn_fallback
 from hclsm_amd.kernels.event_attention import slots_attention
-from hclsm_amd.kernels.level1_packed import Level1Weights, level1_forward_packed
+from hclsm_amd.kernels.level1_packed import Level1Weights, level1_forward_dense, level1_forward_packed
 from hclsm_amd.kernels.sparse_event_attn import EventIndex
 
 
@@ -73,6 +74,22 @@ class Level1EventDynamics(nn.Module):
     def forward(self, event_states: torch.Tensor, event_pad_mask: torch.Tensor | None = None,
                 obj_mask: torch.Tensor | None = None) -> torch.Tensor:
         B, K, N, D = event_states.shape
+        if not self._needs_grad(event_states):
+            # every (b, k) of the padded batch is an event of one hclsm_level1_forward call; the padding
+            # mask then zeroes the padded ones (:130-131; a padded event whose keys are all dead stays NaN)
+            dtype = self._compute_dtype()
+            try:
+                W = Level1Weights.from_module(self, dtype)
+            except ValueError as e:
+                warn_fallback("Level1EventDynamics.forward", f"a module the fused stack does not take ({e})")
+            else:
+                x = level1_forward_dense(event_states, obj_mask, W, out_dtype=self._out_dtype(event_states, dtype))
+                if event_pad_mask is not None:
+                    x = x * event_pad_mask[:, :, None, None]
+                return x
+        else:
+            warn_fallback("Level1EventDynamics.forward", "autograd (projections, LayerNorms and SwiGLU as torch "
+                                                         "ops around the HIP attention core)")
         x = self.proj_in(event_states.reshape(B * K, N, D))                     # :102-107
         kpm = None
         if obj_mask is not None:                                                 # :110-114
@@ -86,6 +103,17 @@ class Level1EventDynamics(nn.Module):
         if event_pad_mask is not None:                                           # :130-131
             x = x * event_pad_mask[:, :, None, None]
         return x
+
+    @staticmethod
+    def _compute_dtype() -> torch.dtype:
+        """bf16 GEMM operands under a bf16 autocast, fp32 otherwise."""
+        if torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16:
+            return torch.bfloat16
+        return torch.float32
+
+    @staticmethod
+    def _out_dtype(x: torch.Tensor, dtype: torch.dtype) -> torch.dtype:
+        return x.dtype if x.dtype in (torch.float32, dtype) else torch.float32
 
     def _needs_grad(self, x: torch.Tensor) -> bool:
         if not torch.is_grad_enabled():
@@ -103,12 +131,10 @@ class Level1EventDynamics(nn.Module):
         the live count must be finite (gather_events_packed zero-fills them in grad mode)."""
         cap, N, D = event_states.shape
         if not self._needs_grad(event_states):
-            dtype = torch.bfloat16 if (torch.is_autocast_enabled("cuda") and
-                                       torch.get_autocast_dtype("cuda") == torch.bfloat16) else torch.float32
+            dtype = self._compute_dtype()
             W = Level1Weights.from_module(self, dtype)
             return level1_forward_packed(event_states, index, obj_mask, W,
-                                         out_dtype=event_states.dtype if event_states.dtype in
-                                         (torch.float32, dtype) else torch.float32)
+                                         out_dtype=self._out_dtype(event_states, dtype))
         warn_fallback("Level1EventDynamics.forward_packed", "autograd (projections, LayerNorms and SwiGLU as torch "
                                                             "ops around the HIP attention core)")
         x = self.proj_in(event_states)

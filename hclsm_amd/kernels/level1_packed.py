@@ -98,3 +98,53 @@ def level1_forward_packed(ev: torch.Tensor, idx: EventIndex, obj_mask: torch.Ten
                                 _lib.stream_of(x))
     _lib.check(rc, "hclsm_level1_forward")
     return out
+
+
+_DENSE_TABLES: dict = {}
+
+
+def _dense_tables(B: int, K: int, device) -> tuple:
+    """Device tables of a dense (B, K) event layout, cached per shape: the event count B*K (int32 [1]) and the
+    batch row of each event, e // K (int32 [B*K])."""
+    key = (B, K, device)
+    hit = _DENSE_TABLES.get(key)
+    if hit is None:
+        n = torch.full((1,), B * K, dtype=torch.int32, device=device)
+        rows = torch.arange(B * K, dtype=torch.int32, device=device).div_(K, rounding_mode="floor")
+        hit = (n, rows)
+        _DENSE_TABLES[key] = hit
+    return hit
+
+
+def level1_forward_dense(ev: torch.Tensor, obj_mask: torch.Tensor | None, W: Level1Weights,
+                         out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """Level1EventDynamics' stack over every event of a padded (B, K, N, d_slot) batch (the layout of
+    HierarchyManager.gather_events), padded events included, in one hclsm_level1_forward call; obj_mask (B, N)
+    or None.  Returns (B, K, N, d_slot) in out_dtype.  The caller applies the event padding mask."""
+    require_gpu("level1_forward_dense", ev, obj_mask)
+    B, K, N, d_slot = ev.shape
+    if d_slot != W.d_slot:
+        raise ValueError(f"ev has d_slot {d_slot}, the weights {W.d_slot}")
+    out = torch.empty((B, K, N, d_slot), dtype=out_dtype, device=ev.device)
+    if B * K == 0:
+        return out
+    x = ev if ev.dtype in (torch.float32, W.dtype) else ev.to(torch.float32)
+    x = x.contiguous()
+    om = None
+    if obj_mask is not None:
+        if obj_mask.shape != (B, N):
+            raise ValueError(f"obj_mask must be (B, N) = {(B, N)}, got {tuple(obj_mask.shape)}")
+        om = obj_mask.detach().to(torch.float32).contiguous()
+    n_dev, rows = _dense_tables(B, K, ev.device)
+    L = _lib.lib()
+    code = _lib.dtype_code(W.dtype)
+    cap = B * K
+    wsb = L.hclsm_level1_forward_workspace(cap, N, W.d_model, W.hidden, code)
+    _lib.check(wsb if wsb < 0 else 0, "hclsm_level1_forward_workspace")
+    ws = _workspace(int(wsb), ev.device)
+    rc = L.hclsm_level1_forward(_lib.ptr(x), _lib.dtype_code(x.dtype), _lib.ptr(out), _lib.dtype_code(out_dtype),
+                                _lib.ptr(n_dev), cap, N, _lib.ptr(rows), _lib.ptr(om), d_slot, W.d_model, W.n_heads,
+                                W.hidden, W.n_layers, W.ptrs, W.ln_eps, code, _lib.ptr(ws), ws.numel(),
+                                _lib.stream_of(x))
+    _lib.check(rc, "hclsm_level1_forward")
+    return out

@@ -344,7 +344,9 @@ int hclsm_slot_attention_iteration(const HclsmSlotWeights* W, const float* slots
  * DynamicSlotAttention forward up to the iterations (objects/dynamic_slots.py:149-164): k | v =
  * LN_in(inputs) [W_k; W_v]^T for inputs [B, M, d_in] float32, then n_iter iterations from slots0
  * [B, N, d] float32 into slots_out.  The slot initialisation draw (:86-96), existence head and slot
- * birth (:166-199) stay with the caller.
+ * birth (:166-199) stay with the caller.  With N == 0 only the keys are formed (slots0 / slots_out may be
+ * NULL); birth reads them at hclsm_slot_attention_k_offset in the workspace.  16-bit weight matrices must be
+ * 16-byte aligned (HCLSM_ERR_UNSUPPORTED before any launch otherwise).
  */
 int hclsm_slot_attention_forward(const HclsmSlotWeights* W, const float* inputs, int64_t d_in,
                                  const float* slots0, float* slots_out, int64_t B, int64_t N, int64_t M,
@@ -356,7 +358,8 @@ int hclsm_slot_attention_forward(const HclsmSlotWeights* W, const float* inputs,
  * Allocation-free variant of hclsm_slot_attention_forward: the same arguments and launches, with the workspace
  * taken from a static device array of HCLSM_SLOT_NOALLOC_SCRATCH_BYTES in the library (one copy per GPU, held
  * until the process ends) instead of a caller buffer.  No allocation, free or synchronisation, so the call may
- * run under HIP graph capture.  A shape whose hclsm_slot_attention_workspace exceeds the array returns
+ * run under HIP graph capture once a first call has run on the device (it looks the array's address up and
+ * sets up its launch tables): tests/test_zz_no_alloc.py captures it and replays it on new inputs.  A shape whose hclsm_slot_attention_workspace exceeds the array returns
  * HCLSM_ERR_SCRATCH before any launch (config 2, B=32 M=196 d=384 bf16, needs about 33 MB).  Calls that overlap
  * on one GPU (two streams, two threads) share the array and race; serialise them.
  * No counterpart in the reference: it is for callers that cannot allocate device memory (graph capture, tight

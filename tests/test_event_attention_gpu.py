@@ -118,7 +118,8 @@ def test_against_torch_sdpa_on_gpu():
 @pytest.mark.parametrize("P,T,H,dh,p,dtype", [(1024, 64, 6, 64, 0.15, torch.bfloat16), (37, 300, 2, 32, 0.3, torch.float32),
                                               (5, 1, 1, 16, 1.0, torch.float16), (64, 128, 4, 64, 0.0, torch.bfloat16),
                                               (8, 1024, 3, 64, 0.05, torch.bfloat16), (700, 16, 2, 128, 0.5, torch.float32),
-                                              (3, 1500, 1, 16, 0.3, torch.bfloat16)])
+                                              (3, 1500, 1, 16, 0.3, torch.bfloat16),
+                                              (5000, 32, 1, 16, 0.3, torch.bfloat16)])   # past the in-launch track bound
 def test_one_call_matches_two_calls(P, T, H, dh, p, dtype):
     """hclsm_track_causal_attention (index + attention in one call, capacity given: for T <= 1024 the row
     counts, then the attention building each track's event list from the mask and filling the tables; past

@@ -83,3 +83,45 @@ def test_level1_packed_and_top_down():
         run()
     msgs = " ".join(str(w.message) for w in rec)
     assert "Level1EventDynamics.forward_packed" in msgs and "HierarchyManager" in msgs
+
+
+def test_level1_padded_forward_is_native():
+    """Level1EventDynamics.forward -- the reference's padded call (model.py:302, level1_event.py:85-133) -- runs
+    without autograd as one hclsm_level1_forward call over every (b, k) of the padded batch: no
+    HipFallbackWarning, the oracle's values (fp32 at 1e-5; bf16 autocast at 2e-2), a padded event exactly zero.
+    Under autograd it warns.  The HierarchyManager says why it leaves its fused step for non-fp32 states."""
+    from hclsm_amd.dynamics import HierarchyManager, Level1EventDynamics
+    from hclsm_amd.kernels import HipFallbackWarning
+    from oracle import modules as om
+    from oracle.ssm_scan import normwise_rel_err
+    _reset()
+    torch.manual_seed(3)
+    cfg = SimpleNamespace(d_model=256, n_layers=2, n_heads=4)
+    l1 = Level1EventDynamics(cfg, 128).cuda()
+    B, K, N, D = 2, 3, 16, 128
+    x = torch.randn(B, K, N, D, device="cuda")
+    pad = torch.ones(B, K, device="cuda")
+    pad[1, 2] = 0.0
+    obj = torch.ones(B, N, device="cuda")
+    obj[0, 11:] = 0.0
+    sd = {k: v.detach().double().cpu().numpy() for k, v in l1.state_dict().items()}
+    ref = om.level1_ref(x.double().cpu().numpy(), pad.double().cpu().numpy(), obj.double().cpu().numpy(), sd,
+                        cfg.n_layers, cfg.n_heads)
+    out = _silent(lambda: l1(x, pad, obj))
+    assert out.shape == (B, K, N, D) and out.dtype == torch.float32
+    assert normwise_rel_err(out.double().cpu().numpy(), ref) <= 1e-5
+    assert out[1, 2].abs().sum() == 0
+
+    def bf():
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            return l1(x, pad, obj)
+    out_bf = _silent(bf)
+    assert normwise_rel_err(out_bf.double().cpu().numpy(), ref) <= 2e-2
+    with pytest.warns(HipFallbackWarning, match="Level1EventDynamics.forward"):
+        l1(x.requires_grad_(), pad, obj)
+    hm = HierarchyManager(D, 384).cuda()
+    mask = torch.zeros(B, 6, device="cuda")
+    mask[:, 1] = 1
+    with torch.no_grad(), pytest.warns(HipFallbackWarning, match="HierarchyManager"):
+        hm(torch.randn(B, 6, N, D, device="cuda").half(), torch.randn(B, 1, N, D, device="cuda").half(), None,
+           mask)

@@ -311,3 +311,47 @@ def test_layer_norm_rows(D, pad, io):
     want = sa.layer_norm(_np(x[:, :D]), _np(w), _np(b))
     tol = 1e-5 if dout == torch.float32 and din == torch.float32 else 8e-3
     assert normwise_rel_err(_np(y), want) <= tol
+
+
+def test_forward_rejects_misaligned_weights_before_any_launch():
+    """16-bit weights are read with 16-byte loads; a weight pointer off that alignment (here W_hh moved by one
+    element through the C ABI) is rejected with HCLSM_ERR_UNSUPPORTED before any launch: the output buffer keeps
+    its contents."""
+    import ctypes
+    from hclsm_amd import _lib
+    from hclsm_amd.kernels import slot_iteration as si
+    from hclsm_amd.workloads import slot_config
+    tokens, slots0, w = slot_config(B=2, M=24, N=8)
+    W = si.SlotWeights.from_dict(w, torch.bfloat16)
+    d = W.d
+    whh = torch.empty(W.t["w_hh"].numel() + 8, dtype=torch.bfloat16, device="cuda")
+    whh[1:1 + W.t["w_hh"].numel()].copy_(W.t["w_hh"].reshape(-1))
+    st = si._struct(W)
+    st.w_hh = whh.data_ptr() + 2                                  # 2 bytes past a 16-byte boundary
+    L = _lib.lib()
+    x, s0 = tokens.cuda().contiguous(), slots0.cuda().contiguous()
+    out = torch.full_like(s0, 7.0)
+    B, M, d_in = x.shape
+    nbytes = L.hclsm_slot_attention_workspace(B, s0.shape[1], M, d_in, d, W.hidden, _lib.BF16)
+    ws = torch.empty(int(nbytes), dtype=torch.uint8, device="cuda")
+    rc = L.hclsm_slot_attention_forward(ctypes.byref(st), x.data_ptr(), d_in, s0.data_ptr(), out.data_ptr(), B,
+                                        s0.shape[1], M, d, W.hidden, 3, d ** -0.5, 0.0, 1e-8, 0.0, _lib.BF16,
+                                        ws.data_ptr(), ws.numel(), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rc == -4, _lib.strerror(rc)
+    assert bool((out == 7.0).all())
+
+
+def test_forward_keys_with_no_slots():
+    """slot_attention_forward(..., return_k=True) with no slots (N = 0) still forms the keys: they equal those of
+    a call with slots, bit for bit (k = LN_in(inputs) W_k^T does not depend on the slots)."""
+    from hclsm_amd.kernels import slot_iteration as si
+    from hclsm_amd.workloads import slot_config
+    tokens, slots0, w = slot_config(B=3, M=40, N=8)
+    W = si.SlotWeights.from_dict(w, torch.bfloat16)
+    x = tokens.cuda()
+    _, k_ref = si.slot_attention_forward(x, slots0.cuda(), W, 3, return_k=True)
+    out0, k0 = si.slot_attention_forward(x, slots0[:, :0].cuda(), W, 3, return_k=True)
+    torch.cuda.synchronize()
+    assert out0.shape == (3, 0, W.d) and k0.shape == k_ref.shape
+    assert torch.equal(k0, k_ref)

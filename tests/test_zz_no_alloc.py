@@ -86,3 +86,43 @@ def test_noalloc_rejects_oversized_workspace():
                                                 torch.cuda.current_stream().cuda_stream)
     assert rc == HCLSM_ERR_SCRATCH
     assert "scratch" in _lib.strerror(rc)
+
+
+def test_noalloc_forward_replays_under_graph_capture():
+    """The allocation-free forward captured once in a graph (after a warm call, which sets up the scratch address
+    and the per-device launch tables) and replayed on new inputs copied into the captured buffers: every replay,
+    with eager work and synchronisations between them, equals the eager allocation-free call on the same inputs
+    bit for bit.  The forward records no memset or allocation, only kernel launches and stream-ordered copies."""
+    from hclsm_amd import _lib
+    from hclsm_amd.kernels import slot_iteration as si
+    L = _lib.lib()
+    d, hidden, B, M, N = 384, 768, 8, 196, 32
+    W = _weights(d, hidden, 1002, torch.bfloat16)
+    x, s0 = _inputs(B, M, N, d, 21)
+    out = torch.zeros_like(s0)
+    st = si._struct(W)
+
+    def launch(stream):
+        return L.hclsm_slot_attention_forward_noalloc(ctypes.byref(st), x.data_ptr(), d, s0.data_ptr(), out.data_ptr(),
+                                                      B, N, M, d, W.hidden, 3, d ** -0.5, 0.0, 1e-8, 0.0, _lib.BF16,
+                                                      stream)
+    assert launch(torch.cuda.current_stream().cuda_stream) == 0   # warm call
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    codes = []
+    with torch.cuda.graph(graph):
+        codes.append(launch(torch.cuda.current_stream().cuda_stream))
+    assert codes == [0]
+    torch.cuda.synchronize()
+    for seed in (22, 23, 24):
+        print(f"graph replay seed={seed}", flush=True)
+        xn, sn = _inputs(B, M, N, d, seed)
+        x.copy_(xn)
+        s0.copy_(sn)
+        graph.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        ref = _call(True, W, x, s0, 3, 1e-8)
+        assert torch.isfinite(ref).all()
+        assert torch.equal(got, ref)
+    del graph
