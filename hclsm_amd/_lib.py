@@ -93,7 +93,7 @@ class HclsmSlotWeights(ctypes.Structure):
     """Mirror of the C struct HclsmSlotWeights (include/hclsm_amd.h)."""
     _fields_ = [(n, ctypes.c_void_p) for n in (
         "w_q", "w_kv", "w_ih", "w_hh", "w1", "w2", "b_ih", "b_hh", "b1", "b2",
-        "ln_in_w", "ln_in_b", "ln_pre_w", "ln_pre_b", "ln_mlp_w", "ln_mlp_b")]
+        "ln_in_w", "ln_in_b", "ln_pre_w", "ln_pre_b", "ln_mlp_w", "ln_mlp_b", "w_qt")]
 
 _lib = None
 

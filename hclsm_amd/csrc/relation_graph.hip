@@ -222,8 +222,7 @@ gnn_edge_kernel(GnnArgs a) {
 #pragma unroll
           for (int rr = 0; rr < 4; ++rr)
             sacc = fmaf(fmaxf(acc[t][rr] + a.bm[o], 0.f), sw[wid * 16 + 4 * g + rr], sacc);
-          sacc += __shfl_xor(sacc, 16, 64);
-          sacc += __shfl_xor(sacc, 32, 64);
+          sacc = rows4_sum(sacc);
           if (g == 0) sagg[wid * D + o] = sacc;
         }
       }
@@ -435,10 +434,8 @@ gnn_edge_res_kernel(GnnArgs a, const float* __restrict__ nstat) {
 #pragma unroll
       for (int pt = 0; pt < 2; ++pt) {
         float gg = gs[pt], hh = hs[pt];
-        gg += __shfl_xor(gg, 16, 64);
-        gg += __shfl_xor(gg, 32, 64);
-        hh += __shfl_xor(hh, 16, 64);
-        hh += __shfl_xor(hh, 32, 64);
+        gg = rows4_sum(gg);
+        hh = rows4_sum(hh);
         const int64_t rowj = f * N + (jj[pt] < N ? jj[pt] : N - 1);
         const float qj = nstat[2 * rowj + 1];
         const float mu = MP ? 0.f : (2.f * si + gg) * inv4d;
@@ -507,8 +504,7 @@ gnn_edge_res_kernel(GnnArgs a, const float* __restrict__ nstat) {
             *reinterpret_cast<float4*>(a.edges + (rowi * a.enj + je) * E + 16 * t + 4 * g) =
                 make_float4(A::tof(ev[0]), A::tof(ev[1]), A::tof(ev[2]), A::tof(ev[3]));
         }
-        s += __shfl_xor(s, 16, 64);
-        s += __shfl_xor(s, 32, 64);
+        s = rows4_sum(s);
         const int j = jj[pt];
         const float alj = j < N ? (a.alive ? a.alive[f * N + j] : 1.f) : 0.f;
         wgt[pt] = ali * alj / (1.f + __expf(-(s + a.be[0])));
@@ -574,8 +570,7 @@ gnn_edge_res_kernel(GnnArgs a, const float* __restrict__ nstat) {
               const int o = 16 * t + 4 * g + rr;
               s = fmaf(fmaxf(acc4[t][rr] + sd1[o], 0.f), scc2[o], s);
             }
-          s += __shfl_xor(s, 16, 64);
-          s += __shfl_xor(s, 32, 64);
+          s = rows4_sum(s);
           const int j = jj[pt];
           if (g == 0 && j < N) {
             const float alj = a.alive ? a.alive[f * N + j] : 1.f;
@@ -588,8 +583,7 @@ gnn_edge_res_kernel(GnnArgs a, const float* __restrict__ nstat) {
 #pragma unroll
       for (int t = 0; t < NT3; ++t) {
         float v = aggp[t];
-        v += __shfl_xor(v, 16, 64);
-        v += __shfl_xor(v, 32, 64);
+        v = rows4_sum(v);
         if (g == 0) a.agg[rowi * a.ldagg + 16 * t + li] = v;
       }
     }
@@ -788,10 +782,8 @@ gnn_edge_str_kernel(GnnArgs a, const float* __restrict__ nstat) {
           }
           if constexpr (ch == NA - 1) {
             // normalise: v = rstd (P_i + Q_j + acc - mu r) + c, ReLU (outputs 16t + 4g + rr of pair li)
-            gs += __shfl_xor(gs, 16, 64);
-            gs += __shfl_xor(gs, 32, 64);
-            hs += __shfl_xor(hs, 16, 64);
-            hs += __shfl_xor(hs, 32, 64);
+            gs = rows4_sum(gs);
+            hs = rows4_sum(hs);
             const float qj = nstat[2 * rowj + 1];
             const float mu = MP ? 0.f : (2.f * si + gs) * inv4d;
             const float m2 = (2.f * qi + 2.f * qj - 2.f * gs + hs) * inv4d;
@@ -855,8 +847,7 @@ gnn_edge_str_kernel(GnnArgs a, const float* __restrict__ nstat) {
                 *reinterpret_cast<float4*>(a.edges + (rowi * a.enj + je) * E + 16 * t + 4 * g) =
                     make_float4(A::tof(ev[0]), A::tof(ev[1]), A::tof(ev[2]), A::tof(ev[3]));
             }
-            sw += __shfl_xor(sw, 16, 64);
-            sw += __shfl_xor(sw, 32, 64);
+            sw = rows4_sum(sw);
             const float alj = j < N ? (a.alive ? a.alive[rowj] : 1.f) : 0.f;
             wgt = ali * alj / (1.f + __expf(-(sw + a.be[0])));
           }
@@ -912,8 +903,7 @@ gnn_edge_str_kernel(GnnArgs a, const float* __restrict__ nstat) {
                 const int o = 16 * t + 4 * g + rr;
                 s = fmaf(fmaxf(acc4[t][rr] + sd1[o], 0.f), scc2[o], s);
               }
-            s += __shfl_xor(s, 16, 64);
-            s += __shfl_xor(s, 32, 64);
+            s = rows4_sum(s);
             if (g == 0 && j < N && live_row) {
               const float alj = a.alive ? a.alive[rowj] : 1.f;
               a.causal[rowi * N + j] = ali * alj / (1.f + __expf(-(s + a.d2[0])));
@@ -930,8 +920,7 @@ gnn_edge_str_kernel(GnnArgs a, const float* __restrict__ nstat) {
 #pragma unroll
       for (int t = 0; t < NT3; ++t) {
         float v = aggp[t];
-        v += __shfl_xor(v, 16, 64);
-        v += __shfl_xor(v, 32, 64);
+        v = rows4_sum(v);
         if (g == 0 && live_row) a.agg[rowi * a.ldagg + 16 * t + li] = v;
       }
     }

@@ -108,10 +108,8 @@ __device__ __forceinline__ void ln_stats(const XT* const pa[2], int64_t K, int w
   }
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    s1[t] += __shfl_xor(s1[t], 16, 64);
-    s1[t] += __shfl_xor(s1[t], 32, 64);
-    s2[t] += __shfl_xor(s2[t], 16, 64);
-    s2[t] += __shfl_xor(s2[t], 32, 64);
+    s1[t] = rows4_sum(s1[t]);
+    s2[t] = rows4_sum(s2[t]);
   }
   // lds layout: [wave][row 0..31][2]
   if (g == 0) {
@@ -941,8 +939,7 @@ linear_kreg_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>:
             sacc += pass == 0 ? dv : dv * dv;
           }
         }
-        sacc += __shfl_xor(sacc, 16, 64);
-        sacc += __shfl_xor(sacc, 32, 64);
+        sacc = rows4_sum(sacc);
         if (g == 0) stat[pass][wid][t][li] = sacc;
       }
       __syncthreads();
@@ -1215,8 +1212,7 @@ core_logits_kernel(const typename MM<DT>::T* __restrict__ q, const typename MM<D
       acc[nt][r] = s;
       mx = fmaxf(mx, s);
     }
-  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  mx = rows4_max(mx);
   float sum = 0.f;
 #pragma unroll
   for (int nt = 0; nt < CORE_MAX_NT; ++nt)
@@ -1226,8 +1222,7 @@ core_logits_kernel(const typename MM<DT>::T* __restrict__ q, const typename MM<D
       acc[nt][r] = e;
       sum += e;
     }
-  sum += __shfl_xor(sum, 16, 64);
-  sum += __shfl_xor(sum, 32, 64);
+  sum = rows4_sum(sum);
   const float inv = 1.f / (sum + a.denom_eps);
 #pragma unroll
   for (int nt = 0; nt < CORE_MAX_NT; ++nt) {
@@ -1320,8 +1315,7 @@ core_update_t_kernel(const typename MM<DT>::T* __restrict__ P, int64_t Mp, const
       }
     }
   }
-  cs += __shfl_xor(cs, 16, 64);
-  cs += __shfl_xor(cs, 32, 64);
+  cs = rows4_sum(cs);
   if (d >= a.D) return;
   const float epsv = renorm ? a.renorm_eps * cs : 0.f;
 #pragma unroll
@@ -1474,8 +1468,7 @@ core_update_narrow_kernel(const float* __restrict__ P, int64_t Mp, const float* 
         if (nt < a.NT) acc[nt] = A::mfma(pv[u][nt], vv[u], acc[nt]);
     }
   }
-  cs += __shfl_xor(cs, 16, 64);
-  cs += __shfl_xor(cs, 32, 64);
+  cs = rows4_sum(cs);
   if (g == 0) csum[wid][li] = cs;
 #pragma unroll
   for (int nt = 0; nt < CORE_MAX_NT; ++nt)
@@ -1673,8 +1666,7 @@ core_fused_t_kernel(const typename MM<DT>::T* __restrict__ q, const typename MM<
         acc[nt][r] = sv;
         mx = fmaxf(mx, sv);
       }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = rows4_max(mx);
     float sum = 0.f;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
@@ -1684,8 +1676,7 @@ core_fused_t_kernel(const typename MM<DT>::T* __restrict__ q, const typename MM<
         acc[nt][r] = e;
         sum += e;
       }
-    sum += __shfl_xor(sum, 16, 64);
-    sum += __shfl_xor(sum, 32, 64);
+    sum = rows4_sum(sum);
     const float inv = m < a.M ? 1.f / (sum + a.denom_eps) : 0.f;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
@@ -1775,8 +1766,7 @@ core_fused_t_kernel(const typename MM<DT>::T* __restrict__ q, const typename MM<
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) acc[nt] = A::mfma(A::load(sp + (nt * 16 + li) * PP + m0 + 8 * g), bv, acc[nt]);
     }
-    cs += __shfl_xor(cs, 16, 64);
-    cs += __shfl_xor(cs, 32, 64);
+    cs = rows4_sum(cs);
     const float epsv = renorm ? a.renorm_eps * cs : 0.f;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
@@ -2689,9 +2679,13 @@ static int slot_forward_impl(const HclsmSlotWeights* W, const float* inputs, int
   // k Wq = k (Wq^T)^T once per call, so that no iteration projects the slots to queries
   const void* kq = nullptr;
   if (L.has_kq && core_fused_fits(B, N, M, d, dtype)) {
-    rc = transpose_16(W->w_q, d, ws + L.wqt, d, d, d, st);
-    if (rc) return rc;
-    rc = linear_impl(kv, d, dtype, ws + L.wqt, d, nullptr, nullptr, 0, ws + L.kq, d, dtype, nullptr, 0, B * M, d, d,
+    const void* wqt = W->w_qt;   // the caller's copy, formed once per weight set, or one formed here
+    if (wqt == nullptr || !al16(wqt)) {
+      rc = transpose_16(W->w_q, d, ws + L.wqt, d, d, d, st);
+      if (rc) return rc;
+      wqt = ws + L.wqt;
+    }
+    rc = linear_impl(kv, d, dtype, wqt, d, nullptr, nullptr, 0, ws + L.kq, d, dtype, nullptr, 0, B * M, d, d,
                      0, 0.f, 0, nullptr, nullptr, 0.f, dtype, st);
     if (rc) return rc;
     kq = ws + L.kq;

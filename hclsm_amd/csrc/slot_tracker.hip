@@ -308,8 +308,7 @@ track_cost_res_kernel(TrackCostArgs a) {
           const int o = 16 * t + 4 * g + rr;
           part = fmaf(fmaxf(acc2[pt][t][rr] + sb2[o], 0.f), sw3[o], part);
         }
-      part += __shfl_xor(part, 16, 64);
-      part += __shfl_xor(part, 32, 64);
+      part = rows4_sum(part);
       const int64_t p = pw + 16 * pt + li;
       if (g == 0 && p < a.pairs) {
         float s = part + a.b3[0];

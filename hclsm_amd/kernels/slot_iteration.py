@@ -61,6 +61,9 @@ class SlotWeights:
             t[k] = val.to(device=device, dtype=dtype if k in _WEIGHT_KEYS else torch.float32).contiguous()
         if "w_k" in t and "w_v" in t:
             t["w_kv"] = torch.cat([t["w_k"], t["w_v"]], 0).contiguous()
+        if dtype in (torch.bfloat16, torch.float16):
+            # the forward multiplies the keys by W_q (queries as LN(s) (k W_q)^T): its transpose, once per weight set
+            t["w_qt"] = t["w_q"].t().contiguous()
         d = t["w_q"].shape[0]
         return cls(dtype, d, t["w1"].shape[0], t)
 

@@ -313,6 +313,8 @@ typedef struct HclsmSlotWeights {
   const float* ln_in_w;  const float* ln_in_b;   /* [d_in] norm_input */
   const float* ln_pre_w; const float* ln_pre_b;  /* [d]    norm_pre_attn */
   const float* ln_mlp_w; const float* ln_mlp_b;  /* [d]    norm_slots */
+  const void* w_qt;    /* [d, d] w_q transposed, nullable: formed once per weight set by the caller; when NULL a
+                          16-bit forward forms it in its workspace on every call (one more launch) */
 } HclsmSlotWeights;
 
 /* Workspace bytes for hclsm_slot_attention_iteration / _forward (16-byte aligned buffer). */
