@@ -700,7 +700,7 @@ def _bench_chain(dev, n, warmup, cpu):
                              "bytes_per_call": sb, "kernel": "ssm_scan_fwd_mfma_kernel<raw,TC=2,DPL=2>"},
            "attn_roofline": {"bound": "hbm", "achieved": round(ab / a_t / 1e9, 2), "peak": HBM_PEAK_GBS,
                              "unit": "GB/s", "frac": round(ab / a_t / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_call": ab,
-                             "kernel": "event_attn_kernel<bf16, causal per track> + index build"},
+                             "kernel": "index build + event_attn_pair_kernel<bf16, 64> (K/V staged in LDS)"},
            "scan_parity_normwise_err": err}
     if cpu:
         from oracle.torch_cpu import event_attention_torch, scan_torch
