@@ -203,6 +203,19 @@ __device__ __forceinline__ int64_t xcd_tile(int64_t bid, int64_t G) {
   return x * per + (x < r ? x : r) + k;
 }
 
+// Workgroup -> tile order for a launch whose live tiles are the leading ones (a device-side row count): row
+// block b of the tiles (tiles_n tiles sharing 128 or 64 rows of X) goes to XCD b % 8, in groups of eight row
+// blocks, so the tiles that read the same rows of X meet in one L2 and the leading row blocks still spread
+// over all XCDs.  Taken for narrow outputs (tiles_n <= 8: measured faster on the Level-1 N = 384 layers); wider
+// ones, and the last, partial group, keep the identity order (the wide SwiGLU layer measured slower with it).
+__device__ __forceinline__ int64_t xcd_rowblock_tile(int64_t bid, int64_t tiles_n, int64_t G) {
+  constexpr int64_t NX = 8;
+  const int64_t grp = NX * tiles_n;
+  if (tiles_n > 8 || bid >= G / grp * grp) return bid;
+  const int64_t x = bid % NX, k = bid / NX;
+  return (k / tiles_n) * grp + x * tiles_n + k % tiles_n;
+}
+
 // Epilogue of four consecutive output columns col .. col+3 of one row (columns past N skipped):
 // val = acc + bias, ReLU, gated-linear factor, + resid, clamp; stored to Y (and Y2).  With vec, every
 // row of Y / Y2 / resid / glu starts 16-byte aligned and the four columns are in range: one vector access each.
@@ -321,7 +334,7 @@ linear_lds_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>::
   __shared__ __align__(16) T Bs[64 * LT_LD];
   const int64_t tiles_n = (N + 63) / 64;
   // (a device-side row count leaves only the leading tiles live: keep them spread over the XCDs)
-  const int64_t tile = ext.m_dev ? (int64_t)blockIdx.x : xcd_tile(blockIdx.x, gridDim.x);
+  const int64_t tile = ext.m_dev ? xcd_rowblock_tile(blockIdx.x, tiles_n, gridDim.x) : xcd_tile(blockIdx.x, gridDim.x);
   const int64_t tm = tile / tiles_n, tn = tile - tm * tiles_n;
   M = ext_rows(ext, M);
   if (tm * 64 >= M) return;   // the whole workgroup, before any barrier
@@ -484,7 +497,7 @@ linear_lds128_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT
   __shared__ __align__(16) T Bs[128 * LB_LD];
   const int64_t tiles_n = (N + 127) / 128;
   // (a device-side row count leaves only the leading tiles live: keep them spread over the XCDs)
-  const int64_t tile = ext.m_dev ? (int64_t)blockIdx.x : xcd_tile(blockIdx.x, gridDim.x);
+  const int64_t tile = ext.m_dev ? xcd_rowblock_tile(blockIdx.x, tiles_n, gridDim.x) : xcd_tile(blockIdx.x, gridDim.x);
   const int64_t tm = tile / tiles_n, tn = tile - tm * tiles_n;
   M = ext_rows(ext, M);
   if (tm * 128 >= M) return;   // the whole workgroup, before any barrier
@@ -579,6 +592,166 @@ linear_lds128_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT
   }
 }
 
+// 128x128 output tiles, 16-bit X and W, K a multiple of 64: the operands go from global memory straight into
+// LDS (global_load_lds_dwordx4: each lane's 16 bytes land at lane * 16 of a wave-uniform LDS base, so no VGPRs
+// stage them and no ds_write issues), two 32 KB stages of 64-wide K chunks, one barrier per chunk: chunk k + 1
+// is requested into the other stage as soon as every wave has finished chunk k - 1, and is in flight while
+// chunk k is multiplied.  64 KB of LDS: two workgroups per CU.  Each wave computes a 64x64 quadrant (4 x 4 MFMA
+// tiles) as linear_lds128_kernel does, with the same instruction order, so the two give identical results.
+// LDS layout per stage and operand: row r's eight 16-byte chunks at r * 8 + (c ^ (r & 7)); a fragment read
+// (16 rows, one chunk) then touches eight distinct chunk slots of the bank rows.
+constexpr int LD_KC = 64;
+constexpr int LD_CPR = LD_KC / 8;                 // 16-byte chunks per row and chunk of K
+constexpr int LD_OPB = 128 * LD_CPR * 16;         // bytes of one operand per stage (16 KB)
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// s_waitcnt with only the vector-memory count bounded (gfx9 encoding: vmcnt bits 3:0 and 15:14; expcnt and
+// lgkmcnt at their maxima)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int DT, int OT>
+__global__ void __launch_bounds__(256)
+linear_dma_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const typename MM<DT>::T* __restrict__ W,
+                  int64_t ldw, const float* __restrict__ bias, const float* __restrict__ resid, int64_t ldr,
+                  typename MM<OT>::T* __restrict__ Y, int64_t ldy, typename MM<DT>::T* __restrict__ Y2,
+                  int64_t ldy2, int64_t M, int64_t N, int64_t K, int relu, float clamp_v, OutSplit os, LinExt ext) {
+  using A = MM<DT>;
+  using T = typename A::T;
+  static_assert(A::KPL == 8, "16-bit operands");
+  __shared__ __align__(16) unsigned char smem[2 * 2 * LD_OPB];
+  const int64_t tiles_n = (N + 127) / 128;
+  const int64_t tile = ext.m_dev ? xcd_rowblock_tile(blockIdx.x, tiles_n, gridDim.x) : xcd_tile(blockIdx.x, gridDim.x);
+  const int64_t tm = tile / tiles_n, tn = tile - tm * tiles_n;
+  M = ext_rows(ext, M);
+  if (tm * 128 >= M) return;   // the whole workgroup, before any barrier
+  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, g = lane >> 4, li = lane & 15;
+  const int wr = wid >> 1, wc = wid & 1;
+  const int wu = __builtin_amdgcn_readfirstlane(wid);
+  const int nk = (int)(K / LD_KC);
+  // load map: unit u = 256 i + tid of an operand is LDS slot u (row u / 8, slot u % 8), which holds the row's
+  // chunk (u % 8) ^ (row & 7); rows past M / N repeat the last row (their outputs are not stored)
+  const T* pa[4];
+  const T* pb[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int u = 256 * i + tid, r = u / LD_CPR, c = (u % LD_CPR) ^ (r & (LD_CPR - 1));
+    int64_t ra = tm * 128 + r, rb = tn * 128 + r;
+    ra = ra < M ? ra : M - 1;
+    rb = rb < N ? rb : N - 1;
+    pa[i] = X + ra * ldx + 8 * c;
+    pb[i] = w_row(W, ext, rb, ldw) + 8 * c;
+  }
+  auto request = [&](int kc) {   // chunk kc into stage kc & 1: eight 16-byte loads per lane
+    unsigned char* st = smem + (kc & 1) * 2 * LD_OPB;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      __builtin_amdgcn_global_load_lds((const void*)(pa[i] + (int64_t)kc * LD_KC),
+                                       (lds_void_t*)(st + (256 * i + 64 * wu) * 16), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(pb[i] + (int64_t)kc * LD_KC),
+                                       (lds_void_t*)(st + LD_OPB + (256 * i + 64 * wu) * 16), 16, 0, 0);
+    }
+  };
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  request(0);
+  for (int kc = 0; kc < nk; ++kc) {
+    wait_vmcnt<0>();                // this lane's part of chunk kc is in LDS
+    __builtin_amdgcn_s_barrier();   // ... every lane's, and chunk kc - 1 is consumed by every wave
+    if (kc + 1 < nk) request(kc + 1);
+    const T* As = reinterpret_cast<const T*>(smem + (kc & 1) * 2 * LD_OPB);
+    const T* Bs = reinterpret_cast<const T*>(smem + (kc & 1) * 2 * LD_OPB + LD_OPB);
+#pragma unroll
+    for (int s = 0; s < LD_KC / 32; ++s) {
+      typename A::Op a[4], b[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int ra = wr * 64 + 16 * t + li, rb = wc * 64 + 16 * t + li, c = 4 * s + g;
+        a[t] = A::load(As + (ra * LD_CPR + (c ^ (ra & (LD_CPR - 1)))) * 8);
+        b[t] = A::load(Bs + (rb * LD_CPR + (c ^ (rb & (LD_CPR - 1)))) * 8);
+      }
+      // weights as the A operand: acc[ti][tj][r] = out[row 16 ti + li][col 16 tj + 4g + r]
+#pragma unroll
+      for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+        for (int tj = 0; tj < 4; ++tj) acc[ti][tj] = A::mfma(b[tj], a[ti], acc[ti][tj]);
+    }
+  }
+  const int64_t r0 = tm * 128 + 64 * wr, c0 = tn * 128 + 64 * wc;
+  using TO = typename MM<OT>::T;
+  if (sizeof(TO) == 2 && os.yt != nullptr && tn * 128 >= os.col) {
+    // a tile of the transposed part (16-bit output, os.col a multiple of 128): transpose through LDS so that
+    // consecutive threads write consecutive rows (tokens) of yt
+    constexpr int TP = 130;   // pitch of the transposed tile (elements)
+    TO* Ts = reinterpret_cast<TO*>(smem);
+    static_assert(sizeof(TO) != 2 || 128 * TP * sizeof(TO) <= sizeof(smem), "transposed tile fits the stages");
+    __syncthreads();   // the last chunk is consumed
+#pragma unroll
+    for (int tj = 0; tj < 4; ++tj)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t col = c0 + 16 * tj + 4 * g + r;
+        const float bv = (bias && col < N) ? bias[col] : 0.f;
+#pragma unroll
+        for (int ti = 0; ti < 4; ++ti) {
+          const int64_t row = r0 + 16 * ti + li;
+          float val = acc[ti][tj][r] + bv;
+          if (relu) val = fmaxf(val, 0.f);
+          if (resid && row < M && col < N) val += resid[row * ldr + col];
+          if (clamp_v > 0.f) val = fminf(fmaxf(val, -clamp_v), clamp_v);
+          Ts[(64 * wc + 16 * tj + 4 * g + r) * TP + 64 * wr + 16 * ti + li] = MM<OT>::fromf(val);
+        }
+      }
+    __syncthreads();
+    TO* yt = reinterpret_cast<TO*>(os.yt);
+    for (int i = tid; i < 128 * 128; i += 256) {
+      const int c = i >> 7, rl = i & 127;
+      const int64_t row = tm * 128 + rl, col = tn * 128 + c;
+      if (row < M && col < N) {
+        const int64_t fr = row / os.frame_rows, rr = row - fr * os.frame_rows;
+        yt[fr * os.bstride + (col - os.col) * os.ldyt + rr] = Ts[c * TP + rl];
+      }
+    }
+    return;
+  }
+  if (ext.w3 != nullptr) {   // (w1, w3) tile pairs (0, 1) and (2, 3) of the wave's 64 columns
+    const int64_t H = N / 2;
+    const bool v4 = lin_vec4_ok<DT, OT>(Y, ldy, Y2, ldy2, resid, ldr, kNoLinExt);
+#pragma unroll
+    for (int tj = 0; tj < 4; tj += 2) {
+      const int64_t col = (c0 + 16 * tj) / 2 + 4 * g;
+#pragma unroll
+      for (int ti = 0; ti < 4; ++ti) {
+        const int64_t row = r0 + 16 * ti + li;
+        if (row < M && col < H)
+          glu_pair_epilogue<DT, OT>(acc[ti][tj], acc[ti][tj + 1], row, col, H, resid, ldr, Y, ldy, Y2, ldy2, v4);
+      }
+    }
+    return;
+  }
+  const bool vec = lin_vec4_ok<DT, OT>(Y, ldy, Y2, ldy2, resid, ldr, ext);
+#pragma unroll
+  for (int tj = 0; tj < 4; ++tj) {
+    const int64_t col = c0 + 16 * tj + 4 * g;
+    float bv[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) bv[r] = (bias && col + r < N) ? bias[col + r] : 0.f;
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti) {
+      const int64_t row = r0 + 16 * ti + li;
+      if (row >= M || col >= N) continue;
+      lin_epilogue4<DT, OT>(acc[ti][tj], bv, row, col, N, relu, clamp_v, resid, ldr, Y, ldy, Y2, ldy2, ext, vec);
+    }
+  }
+}
+
 // fp32 operands: the same 64x64 tile with A and W rows staged in LDS in K chunks of 64 floats (the next
 // chunk in flight), each wave a 32x32 quadrant of v_mfma_f32_16x16x4_f32.  The contraction is permuted
 // so that a lane's operands are float4 reads: in a 16-wide k block, lane group g owns k = 4g .. 4g+3 and
@@ -595,7 +768,8 @@ linear_lds_f32_kernel(const float* __restrict__ X, int64_t ldx, const float* __r
   __shared__ __align__(16) float As[64 * LF_LD];
   __shared__ __align__(16) float Bs[64 * LF_LD];
   const int64_t tiles_n = (N + 63) / 64;
-  // (a device-side row count leaves only the leading tiles live: keep them spread over the XCDs)
+  // (a device-side row count leaves only the leading tiles live: keep them spread over the XCDs; the row-block
+  // order of the 16-bit kernels measured slower here)
   const int64_t tile = ext.m_dev ? (int64_t)blockIdx.x : xcd_tile(blockIdx.x, gridDim.x);
   const int64_t tm = tile / tiles_n, tn = tile - tm * tiles_n;
   M = ext_rows(ext, M);
@@ -1965,7 +2139,19 @@ static void launch_linear_quad(const void* x, int64_t ldx, const void* w, int64_
     const unsigned grid = (unsigned)(((M + 63) / 64) * ((N + 63) / 64));
     const int64_t tiles128 = ((M + 127) / 128) * ((N + 127) / 128);
     if constexpr (MM<DT>::KPL == 8) {
-      if (os.yt == nullptr && N >= 768 && tiles128 >= 512)
+      // 16-bit X with 16-byte rows and K in 64-wide chunks: the direct-to-LDS kernel (a transposed part must
+      // start on a 128-column tile)
+      // narrow layers (N <= 512) behind a device-side row count: the direct-to-LDS kernel (measured faster there
+      // than the 64x64 tiles; wider layers and host-side row counts measured no faster or slower with it)
+      const bool dma = direct && ext.m_dev != nullptr && os.yt == nullptr && K % LD_KC == 0 && al16(x) &&
+                       ldx % 8 == 0 && N >= 256 && N <= 512;
+      if (dma) {
+        if constexpr (direct)
+          hipLaunchKernelGGL((linear_dma_kernel<DT, OT>), dim3((unsigned)tiles128), dim3(256), 0, st,
+                             (const typename MM<DT>::T*)x, ldx, (const typename MM<DT>::T*)w, ldw, bias, resid, ldr,
+                             (typename MM<OT>::T*)y, ldy, (typename MM<DT>::T*)y2, ldy2, M, N, K, relu, clamp, os,
+                             ext);
+      } else if (os.yt == nullptr && N >= 768 && tiles128 >= 512)
         hipLaunchKernelGGL((linear_lds128_kernel<DT, OT, XT>), dim3((unsigned)tiles128), dim3(256), 0, st,
                            (const XT*)x, ldx, (const typename MM<DT>::T*)w, ldw, bias, resid, ldr,
                            (typename MM<OT>::T*)y, ldy, (typename MM<DT>::T*)y2, ldy2, M, N, K, relu, clamp, ext);

@@ -274,6 +274,8 @@ def test_large_linear_lds_tiles(dtype, tol):
     (torch.bfloat16, 2e-2, 8200, 1040, 416),    # 128x128 LDS tiles: N >= 768, >= 512 tiles; ragged M, N; K tail
     (torch.float16, 2e-2, 8200, 1040, 416),
     (torch.float32, 1e-5, 2085, 1040, 420),     # fp32 LDS-staged tiles (float4 operands), K tail of 4
+    (torch.bfloat16, 2e-2, 8200, 1040, 448),    # direct-to-LDS tiles: K a multiple of 64; ragged M, N
+    (torch.float16, 2e-2, 8200, 272, 1536),     # direct-to-LDS tiles, long K (24 chunks), a partial column tile
 ])
 def test_large_linear_wide_tiles(dtype, tol, M, N, K):
     """hclsm_linear at sizes that take the 128x128-tile 16-bit kernel and the fp32 LDS kernel, with bias,
@@ -289,6 +291,26 @@ def test_large_linear_wide_tiles(dtype, tol, M, N, K):
                    stream=st)
     ref = np.clip(np.maximum(_np(x) @ _np(w).T + _np(b), 0) + _np(r), -2.0, 2.0)
     assert normwise_rel_err(_np(y), ref) <= tol
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_large_linear_direct_tiles_16bit_out(dtype):
+    """The direct-to-LDS kernel with 16-bit output and the fp32 shadow copy (Y2): both equal the oracle's
+    product rounded once, and the two copies agree with each other."""
+    from hclsm_amd.kernels import slot_iteration as si
+    g = torch.Generator().manual_seed(33)
+    M, N, K = 4100, 1152, 384
+    x = torch.randn(M, K, generator=g).to(dtype)
+    w = (torch.randn(N, K, generator=g) / 16).to(dtype)
+    b = torch.randn(N, generator=g)
+    st = torch.cuda.current_stream().cuda_stream
+    y, y2 = si._linear(x.cuda(), w.cuda(), bias=b.cuda(), out_dtype=torch.float32, shadow=True, stream=st)
+    ref = _np(x) @ _np(w).T + _np(b)
+    assert normwise_rel_err(_np(y), ref) <= 1e-5 * 10
+    assert normwise_rel_err(_np(y2.float()), ref) <= 2e-2
+    assert torch.equal(y.to(dtype), y2)
+    yb = si._linear(x.cuda(), w.cuda(), bias=b.cuda(), out_dtype=dtype, stream=st)
+    assert torch.equal(yb, y2)
 
 
 @pytest.mark.parametrize("D,pad", [(96, 0), (384, 0), (384, 4), (1000, 0), (1024, 0), (97, 0), (384, 1), (1030, 0),
