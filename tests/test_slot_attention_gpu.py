@@ -274,8 +274,8 @@ def test_large_linear_lds_tiles(dtype, tol):
     (torch.bfloat16, 2e-2, 8200, 1040, 416),    # 128x128 LDS tiles: N >= 768, >= 512 tiles; ragged M, N; K tail
     (torch.float16, 2e-2, 8200, 1040, 416),
     (torch.float32, 1e-5, 2085, 1040, 420),     # fp32 LDS-staged tiles (float4 operands), K tail of 4
-    (torch.bfloat16, 2e-2, 8200, 1040, 448),    # direct-to-LDS tiles: K a multiple of 64; ragged M, N
-    (torch.float16, 2e-2, 8200, 272, 1536),     # direct-to-LDS tiles, long K (24 chunks), a partial column tile
+    (torch.bfloat16, 2e-2, 8200, 1040, 448),    # 128x128 tiles, K a whole number of 64-wide chunks; ragged M, N
+    (torch.float16, 2e-2, 8200, 272, 1536),     # 64x64 tiles, long K (12 chunks), a partial column tile
 ])
 def test_large_linear_wide_tiles(dtype, tol, M, N, K):
     """hclsm_linear at sizes that take the 128x128-tile 16-bit kernel and the fp32 LDS kernel, with bias,
@@ -294,9 +294,9 @@ def test_large_linear_wide_tiles(dtype, tol, M, N, K):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_large_linear_direct_tiles_16bit_out(dtype):
-    """The direct-to-LDS kernel with 16-bit output and the fp32 shadow copy (Y2): both equal the oracle's
-    product rounded once, and the two copies agree with each other."""
+def test_large_linear_wide_tiles_16bit_out(dtype):
+    """The 128x128-tile kernel with fp32 output plus the 16-bit shadow copy (Y2), and with 16-bit output: each
+    equals the oracle's product (rounded once for the 16-bit copies), and the copies agree bit for bit."""
     from hclsm_amd.kernels import slot_iteration as si
     g = torch.Generator().manual_seed(33)
     M, N, K = 4100, 1152, 384
