@@ -421,18 +421,37 @@ def _bench_scan_bwd(dev, n, warmup):
     ws = torch.empty(max(wsb, 256), dtype=torch.uint8, device=dev)
     st = torch.cuda.current_stream(dev).cuda_stream
 
-    def step():
-        rc = L.hclsm_ssm_scan_bwd(d["x"].data_ptr(), d["dt"].data_ptr(), d["A_log"].data_ptr(), d["B"].data_ptr(),
-                                  d["C"].data_ptr(), d["D"].data_ptr(), gy.data_ptr(), gx.data_ptr(), gdt.data_ptr(),
-                                  gA.data_ptr(), gB.data_ptr(), gC.data_ptr(), gD.data_ptr(), N, T, Dn, S,
-                                  _lib.BF16, _lib.SCAN_RAW, ws.data_ptr(), ws.numel(), st)
+    y = torch.empty_like(d["x"])
+    grads = (gy, gx, gdt, gA, gB, gC, gD)
+
+    def bwd(fn):
+        rc = fn(d["x"].data_ptr(), d["dt"].data_ptr(), d["A_log"].data_ptr(), d["B"].data_ptr(), d["C"].data_ptr(),
+                d["D"].data_ptr(), *(g.data_ptr() for g in grads), N, T, Dn, S, _lib.BF16, _lib.SCAN_RAW,
+                ws.data_ptr(), ws.numel(), st)
         if rc:
             raise RuntimeError(_lib.strerror(rc))
-    t = _event_timing(step, n, warmup)
+
+    def fwd(ckpt):
+        args = (d["x"].data_ptr(), d["dt"].data_ptr(), d["A_log"].data_ptr(), d["B"].data_ptr(), d["C"].data_ptr(),
+                d["D"].data_ptr(), y.data_ptr(), None, N, T, Dn, S, _lib.BF16, _lib.SCAN_RAW)
+        rc = L.hclsm_ssm_scan_fwd_ckpt(*args, ws.data_ptr(), ws.numel(), st) if ckpt else L.hclsm_ssm_scan_fwd(*args, st)
+        if rc:
+            raise RuntimeError(_lib.strerror(rc))
+
+    # the self-contained backward (recomputes its checkpoints), then the training pair: the forward that leaves
+    # the checkpoints in the workspace and the backward that starts from them
+    t_plain = _event_timing(lambda: bwd(L.hclsm_ssm_scan_bwd), n, warmup)
+    t_fwd = _event_timing(lambda: fwd(False), n, warmup)
+    t_fwd_ck = _event_timing(lambda: fwd(True), n, warmup)
+    t = _event_timing(lambda: bwd(L.hclsm_ssm_scan_bwd_ckpt), n, warmup)
     nbytes = 2 * (N * T * Dn * 5 + N * T * S * 4) + 4 * (Dn * S + Dn) * 2
     return {"workload": "scan backward, config-1 shape (1024 x 64 x 384, S=16, bf16, raw + D), one C call "
-                        "(checkpoint pass, reverse pass, finalize)",
+                        "(reverse pass and finalize, from the checkpoints the training forward "
+                        "hclsm_ssm_scan_fwd_ckpt leaves in the workspace)",
             "us_per_call": round(t * 1e6, 2), "workspace_bytes": wsb,
+            "standalone_us": round(t_plain * 1e6, 2),
+            "forward_us": round(t_fwd * 1e6, 2), "forward_ckpt_us": round(t_fwd_ck * 1e6, 2),
+            "pair_us": round((t_fwd_ck + t) * 1e6, 2), "plain_pair_us": round((t_fwd + t_plain) * 1e6, 2),
             "roofline": {"bound": "hbm", "achieved": round(nbytes / t / 1e9, 1), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_call": nbytes}}
 

@@ -17,6 +17,7 @@ LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libhclsm_amd.so"
 
 F32, BF16, F16, U8 = 0, 1, 2, 3
 SCAN_RAW, SCAN_MODEL, SCAN_BLOCK = 0, 1, 2
+ERR_UNSUPPORTED = -4   # HCLSM_ERR_UNSUPPORTED: valid arguments the entry point does not implement
 EVENT_GT_HALF, EVENT_NONZERO = 0, 1
 ATTN_TRACK_CAUSAL, ATTN_SLOTS = 0, 1
 
@@ -33,6 +34,9 @@ _SIGNATURES: dict[str, list] = {
     "hclsm_ssm_block_scan_fwd": [_c_void_p] * 9 + [_i64] * 4 + [_int, _c_void_p],
     "hclsm_ssm_scan_bwd_workspace": [_i64, _i64, _i64, _i64],
     "hclsm_ssm_scan_bwd": [_c_void_p] * 13 + [_i64] * 4 + [_int, _int, _c_void_p, _i64, _c_void_p],
+    "hclsm_ssm_scan_fwd_ckpt": [_c_void_p] * 8 + [_i64] * 4 + [_int, _int, _c_void_p, _i64, _c_void_p],
+    "hclsm_ssm_block_scan_fwd_ckpt": [_c_void_p] * 9 + [_i64] * 4 + [_int, _c_void_p, _i64, _c_void_p],
+    "hclsm_ssm_scan_bwd_ckpt": [_c_void_p] * 13 + [_i64] * 4 + [_int, _int, _c_void_p, _i64, _c_void_p],
     "hclsm_event_index": [_c_void_p, _int, _i64, _i64, _int] + [_c_void_p] * 6 + [_c_void_p],
     "hclsm_event_gather": [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64] + [_c_void_p] * 3 + [_c_void_p],
     "hclsm_event_gather_packed": [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64] + [_c_void_p] * 3 + [_c_void_p],

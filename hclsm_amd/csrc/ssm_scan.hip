@@ -26,6 +26,9 @@ constexpr int SCAN_BLOCK = HCLSM_SCAN_BLOCK;
 struct ScanEpi {
   const void* gate;   // [batch][T][d_inner], I/O type; required in SCAN_BLOCK
   void* y_pre;        // optional: the scan output before gating (kept for the backward)
+  float* ck;          // checkpointing launches only: [batch][ceil(T / 8)][d_inner][16] fp32, the state
+                      // before steps 8, 16, ... (the backward's checkpoint slab; entry 0, the zero initial
+                      // state, is not stored)
 };
 
 
@@ -446,9 +449,10 @@ static int launch_scan_sgpr(const void* x, const void* dt, const float* A_log, c
 // two 16x16x32 products per channel) issues fewer VALU instructions but ran
 // slower here, as did one barrier-synchronised workgroup per CU.
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4v __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-template <int MODE, int TC, int DPL>
+template <int MODE, int TC, int DPL, bool CK = false>
 __global__ void __launch_bounds__(64)
 ssm_scan_fwd_mfma_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ dt,
                          const float* __restrict__ A_log, const uint16_t* __restrict__ Bm,
@@ -544,6 +548,16 @@ ssm_scan_fwd_mfma_kernel(const uint16_t* __restrict__ x, const uint16_t* __restr
   };
 
   auto step = [&](int t, uint32_t xw, uint32_t dw_next, uint16_t bb, uint32_t gw) {
+    if constexpr (CK) {   // the state before steps 8, 16, ..., for the backward (before step 0 it is zero)
+      if ((t & 7) == 0 && t > 0 && act) {
+        float* cp = epi.ck + (((size_t)n * ((T + 7) >> 3) + (t >> 3)) * Dn + d0) * SP;
+#pragma unroll
+        for (int k = 0; k < DPL; ++k)
+#pragma unroll
+          for (int s = 0; s < SP; s += 4)
+            *reinterpret_cast<f32x4v*>(cp + k * SP + s) = f32x4v{h[k][s], h[k][s + 1], h[k][s + 2], h[k][s + 3]};
+      }
+    }
     const int tn = t + 1 < T ? t + 1 : T - 1;
     uint32_t cwn[8];
 #pragma unroll
@@ -631,13 +645,13 @@ ssm_scan_fwd_mfma_kernel(const uint16_t* __restrict__ x, const uint16_t* __restr
   }
 }
 
-template <int MODE, int TC, int DPL>
+template <int MODE, int TC, int DPL, bool CK = false>
 static int launch_scan_mfma(const void* x, const void* dt, const float* A_log, const void* B,
                             const void* C, const float* Dskip, void* y, float* h_final,
                             int64_t batch, int64_t T, int64_t Dn, hipStream_t st, ScanEpi epi) {
   const int64_t lanes = Dn / DPL;
   dim3 grid((unsigned)batch, (unsigned)((lanes + 63) / 64));
-  hipLaunchKernelGGL((ssm_scan_fwd_mfma_kernel<MODE, TC, DPL>), grid, dim3(64), 0, st,
+  hipLaunchKernelGGL((ssm_scan_fwd_mfma_kernel<MODE, TC, DPL, CK>), grid, dim3(64), 0, st,
                      (const uint16_t*)x, (const uint16_t*)dt, A_log, (const uint16_t*)B,
                      (const uint16_t*)C, Dskip, (uint16_t*)y, h_final, (int)T, (int)Dn, epi);
   HCLSM_LAUNCH_CHECK();
@@ -765,6 +779,41 @@ static int scan_entry(int mode, const void* x, const void* dt, const float* A_lo
     default:
       return dispatch_sp<HCLSM_F16>(mode, x, dt, A_log, B, C, Dskip, y, h_final, batch, T, d_inner, d_state, st, epi);
   }
+}
+
+// The forward that also writes the backward's checkpoints (epi.ck): the bf16, d_state 16 matrix-core kernel
+// only, with the chunking the plain forward picks.  HCLSM_ERR_UNSUPPORTED where that kernel does not apply.
+int scan_fwd_ckpt(int mode, const void* x, const void* dt, const float* A_log, const void* B, const void* C,
+                  const float* Dskip, void* y, float* h_final, int64_t batch, int64_t T, int64_t Dn, int64_t S,
+                  int dtype, const void* gate, void* y_pre, float* ck, hipStream_t st) {
+  const ScanEpi epi{gate, y_pre, ck};
+  if (batch < 1 || T < 1 || Dn < 1 || batch > 0x7fffffffLL || T > 0x7fffffffLL || (Dn * 4 + 63) / 64 > 65535)
+    return HCLSM_ERR_SHAPE;
+  if (dtype != HCLSM_BF16 || S != 16 || T * Dn * 2 >= 0x7fffffffLL) return HCLSM_ERR_UNSUPPORTED;
+  if (!x || !dt || !A_log || !B || !C || !y || !epi.ck) return HCLSM_ERR_NULL;
+  if (mode == SCAN_BLOCK && !epi.gate) return HCLSM_ERR_NULL;
+  if (!aligned(B, 4) || !aligned(C, 4) || !aligned(epi.ck, 16)) return HCLSM_ERR_UNSUPPORTED;
+  const bool pair = (Dn % 2 == 0) && aligned(x, 4) && aligned(dt, 4) && aligned(y, 4) &&
+                    (!epi.gate || aligned(epi.gate, 4)) && (!epi.y_pre || aligned(epi.y_pre, 4));
+  int cus = 0;
+  const int rc = device_cus(&cus);
+  if (rc) return rc;
+  const bool many = batch * ((Dn / (pair ? 2 : 1) + 63) / 64) > 3 * 4 * (int64_t)cus;
+#define HCLSM_CK(MODE_)                                                                                       \
+  if constexpr (MODE_ == SCAN_BLOCK) {                                                                        \
+    if (pair) return launch_scan_mfma<MODE_, 4, 2, true>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, st, epi); \
+    return launch_scan_mfma<MODE_, 4, 1, true>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, st, epi); \
+  } else {                                                                                                    \
+    if (pair && many) return launch_scan_mfma<MODE_, 2, 2, true>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, st, epi); \
+    if (pair) return launch_scan_mfma<MODE_, 4, 2, true>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, st, epi); \
+    if (many) return launch_scan_mfma<MODE_, 2, 1, true>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, st, epi); \
+    return launch_scan_mfma<MODE_, 4, 1, true>(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, Dn, st, epi); \
+  }
+  if (mode == HCLSM_SCAN_RAW) { HCLSM_CK(HCLSM_SCAN_RAW) }
+  if (mode == HCLSM_SCAN_MODEL) { HCLSM_CK(HCLSM_SCAN_MODEL) }
+  if (mode == SCAN_BLOCK) { HCLSM_CK(SCAN_BLOCK) }
+#undef HCLSM_CK
+  return HCLSM_ERR_MODE;
 }
 
 }  // namespace hclsm

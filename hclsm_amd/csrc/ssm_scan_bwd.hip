@@ -17,7 +17,7 @@
 // over the channel axis (gB, gC) are a recursive-halving reduce-scatter across the wave's channels
 // followed by a cross-wave sum through LDS once per chunk, one part per channel block.  Small kernels
 // then reduce the per-sequence partials of gA_log and gD, and add the blocks' gB / gC parts and cast.
-#include "common.h"
+#include "internal.h"
 
 namespace hclsm {
 
@@ -126,6 +126,7 @@ template <int N_, int MASK_LO> struct RSCount {  // values left per lane after R
 struct BwdArgs {
   int T, Dn, S, nchunk, nck, DW;   // nck = checkpoints per sequence = ceil(nchunk / BWD_CKR)
   int64_t ld_ck;  // floats per (n, checkpoint) slab = Dn * SP
+  int have_ck;    // the checkpoints are already in ckpt (written by the forward): no pass 1
 };
 
 // Steps of B / C rows staged in LDS at a time (a multiple of every chunk length K).
@@ -225,8 +226,8 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
   float* ck = ckpt + (size_t)n * a.nck * a.ld_ck + (size_t)dd * SP + s0;
 
   // ---- pass 1: forward recompute, checkpoint at every chunk start; the next chunk's x / dt are in
-  // flight while a chunk is stepped
-  {
+  // flight while a chunk is stepped (skipped when the forward wrote the checkpoints)
+  if (!a.have_ck) {
     float h[SG];
 #pragma unroll
     for (int j = 0; j < SG; ++j) h[j] = 0.f;
@@ -244,7 +245,7 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
       }
       float xn[K], dn[K];
       ld_chunk(c + 1, xn, dn);
-      if (act && c % BWD_CKR == 0)
+      if (act && c % BWD_CKR == 0 && c > 0)   // (checkpoint 0 is the zero initial state: never stored)
 #pragma unroll
         for (int j = 0; j < SG; ++j) ck[(size_t)(c / BWD_CKR) * a.ld_ck + j] = h[j];
 #pragma unroll
@@ -273,7 +274,7 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
     const int w0 = t0 / BWD_WT * BWD_WT;
     float hc[SG], xs[K], ds[K], gs[K];
 #pragma unroll
-    for (int j = 0; j < SG; ++j) hc[j] = act ? ck[(size_t)(c / BWD_CKR) * a.ld_ck + j] : 0.f;
+    for (int j = 0; j < SG; ++j) hc[j] = (act && c >= BWD_CKR) ? ck[(size_t)(c / BWD_CKR) * a.ld_ck + j] : 0.f;
     ld_chunk(c, xs, ds);
 #pragma unroll
     for (int i = 0; i < K; ++i) {
@@ -476,7 +477,7 @@ template <int DT, int SP, int MODE>
 static int launch_bwd(const void* x, const void* dt, const float* A_log, const void* B, const void* C,
                       const float* Dskip, const void* gy, void* gx, void* gdt, float* gA_log, void* gB, void* gC,
                       float* gD, char* ws, const BwdWs& L, int64_t N, int64_t T, int64_t Dn, int64_t S,
-                      hipStream_t st) {
+                      bool have_ck, hipStream_t st) {
   using TT = typename Elem<DT>::T;
   constexpr int SG = bwd_sg(SP);
   constexpr int G = SP / SG;
@@ -486,6 +487,7 @@ static int launch_bwd(const void* x, const void* dt, const float* A_log, const v
   BwdArgs a;
   a.T = (int)T; a.Dn = (int)Dn; a.S = (int)S; a.nchunk = L.nchunk; a.nck = L.nck; a.DW = DW;
   a.ld_ck = Dn * SP;
+  a.have_ck = have_ck ? 1 : 0;
   float* gbc = reinterpret_cast<float*>(ws + L.gbc);
   hipLaunchKernelGGL((ssm_scan_bwd_kernel<DT, SP, MODE>), dim3((unsigned)N, (unsigned)nblk_d), dim3(threads), 0, st,
                      (const TT*)x, (const TT*)dt, A_log, (const TT*)B, (const TT*)C, Dskip, (const TT*)gy, (TT*)gx,
@@ -520,10 +522,10 @@ extern "C" int64_t hclsm_ssm_scan_bwd_workspace(int64_t batch, int64_t T, int64_
   return (int64_t)bwd_ws(batch, T, d_inner, d_state).total;
 }
 
-extern "C" int hclsm_ssm_scan_bwd(const void* x, const void* dt, const float* A_log, const void* B, const void* C,
-                                  const float* Dskip, const void* gy, void* gx, void* gdt, float* gA_log, void* gB,
-                                  void* gC, float* gD, int64_t batch, int64_t T, int64_t d_inner, int64_t d_state,
-                                  int dtype, int mode, void* workspace, int64_t workspace_bytes, void* stream) {
+static int scan_bwd_entry(const void* x, const void* dt, const float* A_log, const void* B, const void* C,
+                          const float* Dskip, const void* gy, void* gx, void* gdt, float* gA_log, void* gB, void* gC,
+                          float* gD, int64_t batch, int64_t T, int64_t d_inner, int64_t d_state, int dtype, int mode,
+                          void* workspace, int64_t workspace_bytes, bool have_ck, void* stream) {
   if (batch < 0 || T < 0 || d_inner < 0 || d_state < 1) return HCLSM_ERR_SHAPE;
   if (batch > 0x7fffffffLL || T > 0x7fffffffLL || d_inner > 0x7fffffffLL) return HCLSM_ERR_SHAPE;
   if (d_state > 128) return HCLSM_ERR_UNSUPPORTED;
@@ -550,12 +552,12 @@ extern "C" int hclsm_ssm_scan_bwd(const void* x, const void* dt, const float* A_
   if (sp_of(d_state) == SP_) {                                                                               \
     if (mode == HCLSM_SCAN_RAW)                                                                              \
       return launch_bwd<DT_, SP_, HCLSM_SCAN_RAW>(x, dt, A_log, B, C, Dskip, gy, gx, gdt, gA_log, gB, gC, gD, ws, L, \
-                                                  batch, T, d_inner, d_state, st);                           \
+                                                  batch, T, d_inner, d_state, have_ck, st);                  \
     if (mode == HCLSM_SCAN_BLOCK)                                                                            \
       return launch_bwd<DT_, SP_, HCLSM_SCAN_BLOCK>(x, dt, A_log, B, C, Dskip, gy, gx, gdt, gA_log, gB, gC, gD, ws, \
-                                                    L, batch, T, d_inner, d_state, st);                      \
+                                                    L, batch, T, d_inner, d_state, have_ck, st);             \
     return launch_bwd<DT_, SP_, HCLSM_SCAN_MODEL>(x, dt, A_log, B, C, Dskip, gy, gx, gdt, gA_log, gB, gC, gD, ws, L, \
-                                                  batch, T, d_inner, d_state, st);                           \
+                                                  batch, T, d_inner, d_state, have_ck, st);                  \
   }
 #define HCLSM_BWD_DT(DT_) \
   HCLSM_BWD(DT_, 4) HCLSM_BWD(DT_, 8) HCLSM_BWD(DT_, 16) HCLSM_BWD(DT_, 32) HCLSM_BWD(DT_, 64) HCLSM_BWD(DT_, 128)
@@ -565,4 +567,58 @@ extern "C" int hclsm_ssm_scan_bwd(const void* x, const void* dt, const float* A_
 #undef HCLSM_BWD_DT
 #undef HCLSM_BWD
   return HCLSM_ERR_UNSUPPORTED;
+}
+
+extern "C" int hclsm_ssm_scan_bwd(const void* x, const void* dt, const float* A_log, const void* B, const void* C,
+                                  const float* Dskip, const void* gy, void* gx, void* gdt, float* gA_log, void* gB,
+                                  void* gC, float* gD, int64_t batch, int64_t T, int64_t d_inner, int64_t d_state,
+                                  int dtype, int mode, void* workspace, int64_t workspace_bytes, void* stream) {
+  return scan_bwd_entry(x, dt, A_log, B, C, Dskip, gy, gx, gdt, gA_log, gB, gC, gD, batch, T, d_inner, d_state, dtype,
+                        mode, workspace, workspace_bytes, false, stream);
+}
+
+// The checkpointing forward writes the state before steps 8, 16, ... into the backward workspace's checkpoint
+// slab (offset 0): exactly what pass 1 of the backward would write for d_state 16 (4-step chunks, a checkpoint
+// every second chunk).
+static_assert(bwd_k(16) * BWD_CKR == 8, "the checkpointing forward stores the state before every 8th step");
+static bool ckpt_shape_ok(int64_t d_state, int dtype) { return dtype == HCLSM_BF16 && d_state == 16; }
+
+extern "C" int hclsm_ssm_scan_fwd_ckpt(const void* x, const void* dt, const float* A_log, const void* B,
+                                       const void* C, const float* Dskip, void* y, float* h_final, int64_t batch,
+                                       int64_t T, int64_t d_inner, int64_t d_state, int dtype, int mode,
+                                       void* workspace, int64_t workspace_bytes, void* stream) {
+  if (mode != HCLSM_SCAN_RAW && mode != HCLSM_SCAN_MODEL) return HCLSM_ERR_MODE;
+  if (batch < 1 || T < 1 || d_inner < 1 || d_state < 1) return HCLSM_ERR_SHAPE;
+  if (!ckpt_shape_ok(d_state, dtype)) return HCLSM_ERR_UNSUPPORTED;
+  if (!workspace) return HCLSM_ERR_NULL;
+  const BwdWs L = bwd_ws(batch, T, d_inner, d_state);
+  if (workspace_bytes < (int64_t)L.total) return HCLSM_ERR_SHAPE;
+  return scan_fwd_ckpt(mode, x, dt, A_log, B, C, Dskip, y, h_final, batch, T, d_inner, d_state, dtype, nullptr,
+                       nullptr, reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + L.ck),
+                       (hipStream_t)stream);
+}
+
+extern "C" int hclsm_ssm_block_scan_fwd_ckpt(const void* z, const void* dt_in, const float* A_log, const void* B,
+                                             const void* C, const void* gate, void* y, void* y_pre, float* h_final,
+                                             int64_t batch, int64_t T, int64_t d_inner, int64_t d_state, int dtype,
+                                             void* workspace, int64_t workspace_bytes, void* stream) {
+  if (batch < 1 || T < 1 || d_inner < 1 || d_state < 1) return HCLSM_ERR_SHAPE;
+  if (!ckpt_shape_ok(d_state, dtype)) return HCLSM_ERR_UNSUPPORTED;
+  if (!workspace || !gate) return HCLSM_ERR_NULL;
+  const BwdWs L = bwd_ws(batch, T, d_inner, d_state);
+  if (workspace_bytes < (int64_t)L.total) return HCLSM_ERR_SHAPE;
+  return scan_fwd_ckpt(HCLSM_SCAN_BLOCK, z, dt_in, A_log, B, C, nullptr, y, h_final, batch, T, d_inner, d_state,
+                       dtype, gate, y_pre, reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + L.ck),
+                       (hipStream_t)stream);
+}
+
+extern "C" int hclsm_ssm_scan_bwd_ckpt(const void* x, const void* dt, const float* A_log, const void* B,
+                                       const void* C, const float* Dskip, const void* gy, void* gx, void* gdt,
+                                       float* gA_log, void* gB, void* gC, float* gD, int64_t batch, int64_t T,
+                                       int64_t d_inner, int64_t d_state, int dtype, int mode, void* workspace,
+                                       int64_t workspace_bytes, void* stream) {
+  if (batch < 1 || T < 1 || d_inner < 1 || d_state < 1) return HCLSM_ERR_SHAPE;
+  if (!ckpt_shape_ok(d_state, dtype)) return HCLSM_ERR_UNSUPPORTED;
+  return scan_bwd_entry(x, dt, A_log, B, C, Dskip, gy, gx, gdt, gA_log, gB, gC, gD, batch, T, d_inner, d_state, dtype,
+                        mode, workspace, workspace_bytes, true, stream);
 }

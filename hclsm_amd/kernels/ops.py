@@ -80,7 +80,7 @@ def _index_of(B, T, counts, offsets, indices, slot_of=None):
 @torch.library.custom_op("hclsm_hip::ssm_scan_fwd", mutates_args=())
 def ssm_scan_fwd(x: Tensor, dt: Tensor, A_log: Tensor, B: Tensor, C: Tensor, D: Optional[Tensor],
                  mode: int, want_h: bool) -> tuple[Tensor, Tensor]:
-    y, h = _scan_forward(x, dt, A_log, B, C, D, int(mode), bool(want_h))
+    y, h, _ = _scan_forward(x, dt, A_log, B, C, D, int(mode), bool(want_h))
     return y, (h if h is not None else x.new_empty((0,), dtype=torch.float32))
 
 
@@ -93,7 +93,8 @@ def _(x, dt, A_log, B, C, D, mode, want_h):
 @torch.library.custom_op("hclsm_hip::ssm_block_scan_fwd", mutates_args=())
 def ssm_block_scan_fwd(z: Tensor, dt_in: Tensor, A_log: Tensor, B: Tensor, C: Tensor,
                        gate: Tensor) -> tuple[Tensor, Tensor]:
-    return _block_forward(z, dt_in, A_log, B, C, gate, True)
+    y, y_pre, _ = _block_forward(z, dt_in, A_log, B, C, gate, True)
+    return y, y_pre
 
 
 @ssm_block_scan_fwd.register_fake

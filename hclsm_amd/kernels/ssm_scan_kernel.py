@@ -64,8 +64,18 @@ def _check_shapes(x, dt, A_log, B, C, D):
     return batch, T, d_inner, d_state
 
 
-def _scan_forward(x, dt, A_log, B, C, D, mode: int, want_h: bool):
-    """Launch hclsm_ssm_scan_fwd; returns (y in x.dtype, h_final or None, io dtype)."""
+def _ckpt_workspace(batch, T, d_inner, d_state, io, device):
+    """The backward's workspace for the checkpointing forward (bf16 I/O, d_state 16), else None."""
+    if io != torch.bfloat16 or d_state != 16:
+        return None
+    from hclsm_amd.kernels.ssm_scan_bwd import bwd_workspace
+    return bwd_workspace(batch, T, d_inner, d_state, device)
+
+
+def _scan_forward(x, dt, A_log, B, C, D, mode: int, want_h: bool, for_grad: bool = False):
+    """Launch hclsm_ssm_scan_fwd; returns (y in x.dtype, h_final or None, checkpointed backward workspace or
+    None).  With for_grad, bf16 inputs with d_state 16 go through hclsm_ssm_scan_fwd_ckpt, which also leaves
+    the backward's chunk checkpoints in the returned workspace."""
     batch, T, d_inner, d_state = _check_shapes(x, dt, A_log, B, C, D)
     io = common_float_dtype(x, dt, B, C)
     xc = x.to(io).contiguous()
@@ -76,14 +86,25 @@ def _scan_forward(x, dt, A_log, B, C, D, mode: int, want_h: bool):
     Dc = None if D is None else D.to(torch.float32).contiguous()
     y = torch.empty((batch, T, d_inner), dtype=io, device=x.device)
     h = torch.empty((batch, d_inner, d_state), dtype=torch.float32, device=x.device) if want_h else None
-    code = _lib.lib().hclsm_ssm_scan_fwd(
-        _lib.ptr(xc), _lib.ptr(dtc), _lib.ptr(Ac), _lib.ptr(Bc), _lib.ptr(Cc), _lib.ptr(Dc),
-        _lib.ptr(y), _lib.ptr(h), batch, T, d_inner, d_state,
-        _lib.dtype_code(io), mode, _lib.stream_of(x))
-    _lib.check(code, "hclsm_ssm_scan_fwd")
+    ws = _ckpt_workspace(batch, T, d_inner, d_state, io, x.device) if (for_grad and batch * T * d_inner > 0) else None
+    if ws is not None:
+        code = _lib.lib().hclsm_ssm_scan_fwd_ckpt(
+            _lib.ptr(xc), _lib.ptr(dtc), _lib.ptr(Ac), _lib.ptr(Bc), _lib.ptr(Cc), _lib.ptr(Dc),
+            _lib.ptr(y), _lib.ptr(h), batch, T, d_inner, d_state,
+            _lib.dtype_code(io), mode, _lib.ptr(ws), ws.numel(), _lib.stream_of(x))
+        if code == _lib.ERR_UNSUPPORTED:   # layouts the checkpointing kernel does not take: the plain pair
+            ws = None
+        else:
+            _lib.check(code, "hclsm_ssm_scan_fwd_ckpt")
+    if ws is None:
+        code = _lib.lib().hclsm_ssm_scan_fwd(
+            _lib.ptr(xc), _lib.ptr(dtc), _lib.ptr(Ac), _lib.ptr(Bc), _lib.ptr(Cc), _lib.ptr(Dc),
+            _lib.ptr(y), _lib.ptr(h), batch, T, d_inner, d_state,
+            _lib.dtype_code(io), mode, _lib.stream_of(x))
+        _lib.check(code, "hclsm_ssm_scan_fwd")
     if y.dtype != x.dtype:
         y = y.to(x.dtype)
-    return y, h
+    return y, h, ws
 
 
 class _HipSSMScan(torch.autograd.Function):
@@ -91,9 +112,10 @@ class _HipSSMScan(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, dt, A_log, B, C, D, mode, want_h):
-        y, h = _scan_forward(x, dt, A_log, B, C, D, mode, want_h)
+        y, h, ws = _scan_forward(x, dt, A_log, B, C, D, mode, want_h, for_grad=any(ctx.needs_input_grad[:6]))
         ctx.save_for_backward(x, dt, A_log, B, C, D)
         ctx.mode = mode
+        ctx.ws = ws   # the backward workspace holding the forward's checkpoints (or None)
         if h is not None:
             ctx.mark_non_differentiable(h)
             return y, h
@@ -103,7 +125,7 @@ class _HipSSMScan(torch.autograd.Function):
     def backward(ctx, gy, *unused):
         from hclsm_amd.kernels.ssm_scan_bwd import scan_backward
         x, dt, A_log, B, C, D = ctx.saved_tensors
-        grads = scan_backward(x, dt, A_log, B, C, D, gy, ctx.mode)
+        grads = scan_backward(x, dt, A_log, B, C, D, gy, ctx.mode, ws=ctx.ws)
         return (grads["x"], grads["dt"], grads["A_log"], grads["B"], grads["C"],
                 grads.get("D"), None, None)
 
@@ -149,7 +171,9 @@ def ssm_scan_fn(x, dt, A_log, B, C, backend: str = "auto", *, D=None, clamp_mode
                               return_h_final=return_h_final)
 
 
-def _block_forward(z, dt_in, A_log, B, C, gate, want_pre: bool):
+def _block_forward(z, dt_in, A_log, B, C, gate, want_pre: bool, for_grad: bool = False):
+    """Launch hclsm_ssm_block_scan_fwd (with for_grad, the checkpointing form where it applies); returns
+    (y, y_pre or None, checkpointed backward workspace or None)."""
     batch, T, d_inner, d_state = _check_shapes(z, dt_in, A_log, B, C, None)
     if gate.shape != z.shape:
         raise ValueError(f"gate shape {tuple(gate.shape)} != z shape {tuple(z.shape)}")
@@ -158,11 +182,22 @@ def _block_forward(z, dt_in, A_log, B, C, gate, want_pre: bool):
     Ac = A_log.to(torch.float32).contiguous()
     y = torch.empty((batch, T, d_inner), dtype=io, device=z.device)
     y_pre = torch.empty_like(y) if want_pre else None
-    code = _lib.lib().hclsm_ssm_block_scan_fwd(
-        _lib.ptr(zc), _lib.ptr(dc), _lib.ptr(Ac), _lib.ptr(Bc), _lib.ptr(Cc), _lib.ptr(gc), _lib.ptr(y),
-        _lib.ptr(y_pre), None, batch, T, d_inner, d_state, _lib.dtype_code(io), _lib.stream_of(zc))
-    _lib.check(code, "hclsm_ssm_block_scan_fwd")
-    return y, y_pre
+    ws = _ckpt_workspace(batch, T, d_inner, d_state, io, z.device) if (for_grad and batch * T * d_inner > 0) else None
+    if ws is not None:
+        code = _lib.lib().hclsm_ssm_block_scan_fwd_ckpt(
+            _lib.ptr(zc), _lib.ptr(dc), _lib.ptr(Ac), _lib.ptr(Bc), _lib.ptr(Cc), _lib.ptr(gc), _lib.ptr(y),
+            _lib.ptr(y_pre), None, batch, T, d_inner, d_state, _lib.dtype_code(io), _lib.ptr(ws), ws.numel(),
+            _lib.stream_of(zc))
+        if code == _lib.ERR_UNSUPPORTED:
+            ws = None
+        else:
+            _lib.check(code, "hclsm_ssm_block_scan_fwd_ckpt")
+    if ws is None:
+        code = _lib.lib().hclsm_ssm_block_scan_fwd(
+            _lib.ptr(zc), _lib.ptr(dc), _lib.ptr(Ac), _lib.ptr(Bc), _lib.ptr(Cc), _lib.ptr(gc), _lib.ptr(y),
+            _lib.ptr(y_pre), None, batch, T, d_inner, d_state, _lib.dtype_code(io), _lib.stream_of(zc))
+        _lib.check(code, "hclsm_ssm_block_scan_fwd")
+    return y, y_pre, ws
 
 
 class _HipSSMBlockScan(torch.autograd.Function):
@@ -173,9 +208,10 @@ class _HipSSMBlockScan(torch.autograd.Function):
     @staticmethod
     def forward(ctx, z, dt_in, A_log, B, C, gate):
         need = any(ctx.needs_input_grad)
-        y, y_pre = _block_forward(z, dt_in, A_log, B, C, gate, need)
+        y, y_pre, ws = _block_forward(z, dt_in, A_log, B, C, gate, need, for_grad=need)
         if need:
             ctx.save_for_backward(z, dt_in, A_log, B, C, gate, y_pre)
+            ctx.ws = ws
         return y
 
     @staticmethod
@@ -186,7 +222,8 @@ class _HipSSMBlockScan(torch.autograd.Function):
         sg = torch.sigmoid(gatef)
         g_y = gf * gatef * sg
         g_gate = gf * y_pre.float() * sg * (1.0 + gatef * (1.0 - sg))
-        grads = scan_backward(z, dt_in.to(y_pre.dtype), A_log, B, C, None, g_y.to(y_pre.dtype), _lib.SCAN_BLOCK)
+        grads = scan_backward(z, dt_in.to(y_pre.dtype), A_log, B, C, None, g_y.to(y_pre.dtype), _lib.SCAN_BLOCK,
+                              ws=ctx.ws)
         return (grads["x"].to(z.dtype), grads["dt"].to(dt_in.dtype), grads["A_log"], grads["B"].to(B.dtype),
                 grads["C"].to(C.dtype), g_gate.to(gate.dtype))
 

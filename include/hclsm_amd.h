@@ -121,6 +121,32 @@ int hclsm_ssm_scan_bwd(const void* x, const void* dt, const float* A_log, const 
                        int dtype, int mode, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * Training pair: a forward that also leaves the backward's chunk checkpoints in `workspace`, and a backward
+ * that starts from them instead of recomputing them (its first pass).  bf16 I/O with d_state 16 only (the
+ * matrix-core forward); HCLSM_ERR_UNSUPPORTED otherwise, and the caller uses the plain pair.
+ *   hclsm_ssm_scan_fwd_ckpt:       hclsm_ssm_scan_fwd's arguments (RAW or MODEL) plus the backward workspace
+ *                                  (>= hclsm_ssm_scan_bwd_workspace bytes); y and h_final as hclsm_ssm_scan_fwd.
+ *   hclsm_ssm_block_scan_fwd_ckpt: the same for hclsm_ssm_block_scan_fwd (its backward runs in BLOCK mode).
+ *   hclsm_ssm_scan_bwd_ckpt:       hclsm_ssm_scan_bwd's arguments; `workspace` must hold the checkpoints a
+ *                                  *_fwd_ckpt call wrote for the same inputs and mode, unmodified since.
+ * The gradients equal hclsm_ssm_scan_bwd's within fp32 rounding of the recomputed states.
+ * Replaces: the saved-for-backward split of _TritonSSMScan (hclsm/kernels/ssm_scan_kernel.py:294-377); the
+ *   reference's forward saves its inputs, this one also saves the states the backward restarts from.
+ */
+int hclsm_ssm_scan_fwd_ckpt(const void* x, const void* dt, const float* A_log, const void* B, const void* C,
+                            const float* Dskip, void* y, float* h_final, int64_t batch, int64_t T,
+                            int64_t d_inner, int64_t d_state, int dtype, int mode, void* workspace,
+                            int64_t workspace_bytes, void* stream);
+int hclsm_ssm_block_scan_fwd_ckpt(const void* z, const void* dt_in, const float* A_log, const void* B,
+                                  const void* C, const void* gate, void* y, void* y_pre, float* h_final,
+                                  int64_t batch, int64_t T, int64_t d_inner, int64_t d_state, int dtype,
+                                  void* workspace, int64_t workspace_bytes, void* stream);
+int hclsm_ssm_scan_bwd_ckpt(const void* x, const void* dt, const float* A_log, const void* B, const void* C,
+                            const float* Dskip, const void* gy, void* gx, void* gdt, float* gA_log, void* gB,
+                            void* gC, float* gD, int64_t batch, int64_t T, int64_t d_inner, int64_t d_state,
+                            int dtype, int mode, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Event index of a [B, T] mask, built on the device with no host synchronisation.
  *   counts  [B]      int32  events per row
  *   offsets [B+1]    int32  exclusive prefix sum of counts; offsets[B] = total
