@@ -385,3 +385,36 @@ def test_hot_path_from_reference_checkpoint_matches_oracle(tmp_path):
     pg = {k: _np(v) for k, v in module_state(sd, "relation_graph").items()}
     rn, rc = ob.relation_graph_ref(_np(a), _np(al), pg, cfg.objects.gnn_rounds)
     assert normwise_rel_err(_np(nodes), rn) <= 1e-5 and normwise_rel_err(_np(causal), rc) <= 1e-5
+
+
+@pytest.mark.parametrize("autocast", [False, True])
+def test_ssm_block_out_projection_residual_fused(autocast):
+    """SimplifiedSSMBlock's out-projection and residual add run as one hclsm_linear launch (no fallback warning,
+    raised as an error here): in fp32 the block matches its torch form (the same scan, then residual + out_proj)
+    at 1e-5, under a bf16 autocast within the bf16 bar, and the gradients reach x and every weight.  The oracle and
+    float64-autograd checks of the block run through the same path (test_level0_output_shape_and_oracle,
+    test_ssm_block_gradients_match_float64_autograd)."""
+    import warnings
+    from hclsm_amd.dynamics import SimplifiedSSMBlock
+    from hclsm_amd.kernels import HipFallbackWarning
+    torch.manual_seed(5)
+    blk = SimplifiedSSMBlock(192, 16).cuda()
+    x = torch.randn(4, 40, 192, device="cuda")
+    with warnings.catch_warnings():
+        warnings.simplefilter("error", HipFallbackWarning)
+        with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+            out = blk(x)
+            xr = x.clone().requires_grad_()
+            (blk(xr) ** 2).mean().backward()
+    assert out.dtype == torch.float32
+    # the torch form of the same block: the scan output from the same kernel, then residual + out_proj
+    from hclsm_amd.kernels import ssm_block_scan
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+        h = blk.norm(x)
+        z, gate = blk.in_proj(h), blk.gate_proj(h)
+        y = ssm_block_scan(z, blk.dt_proj(z), blk.A_log, blk.B_proj(z), blk.C_proj(z), gate)
+        want = x + blk.out_proj(y.to(h.dtype))
+    assert normwise_rel_err(_np(out), _np(want.float())) <= (2e-2 if autocast else 1e-5)
+    assert xr.grad is not None and torch.isfinite(xr.grad).all()
+    for name, prm in blk.named_parameters():
+        assert prm.grad is not None and torch.isfinite(prm.grad).all(), name
