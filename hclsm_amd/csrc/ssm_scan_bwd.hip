@@ -588,8 +588,10 @@ extern "C" int hclsm_ssm_scan_fwd_ckpt(const void* x, const void* dt, const floa
                                        int64_t T, int64_t d_inner, int64_t d_state, int dtype, int mode,
                                        void* workspace, int64_t workspace_bytes, void* stream) {
   if (mode != HCLSM_SCAN_RAW && mode != HCLSM_SCAN_MODEL) return HCLSM_ERR_MODE;
-  if (batch < 1 || T < 1 || d_inner < 1 || d_state < 1) return HCLSM_ERR_SHAPE;
+  if (batch < 0 || T < 0 || d_inner < 0 || d_state < 1) return HCLSM_ERR_SHAPE;
   if (!ckpt_shape_ok(d_state, dtype)) return HCLSM_ERR_UNSUPPORTED;
+  if (batch == 0 || T == 0 || d_inner == 0)   // no steps, no checkpoints: the plain forward's empty case
+    return hclsm_ssm_scan_fwd(x, dt, A_log, B, C, Dskip, y, h_final, batch, T, d_inner, d_state, dtype, mode, stream);
   if (!workspace) return HCLSM_ERR_NULL;
   const BwdWs L = bwd_ws(batch, T, d_inner, d_state);
   if (workspace_bytes < (int64_t)L.total) return HCLSM_ERR_SHAPE;
@@ -602,8 +604,11 @@ extern "C" int hclsm_ssm_block_scan_fwd_ckpt(const void* z, const void* dt_in, c
                                              const void* C, const void* gate, void* y, void* y_pre, float* h_final,
                                              int64_t batch, int64_t T, int64_t d_inner, int64_t d_state, int dtype,
                                              void* workspace, int64_t workspace_bytes, void* stream) {
-  if (batch < 1 || T < 1 || d_inner < 1 || d_state < 1) return HCLSM_ERR_SHAPE;
+  if (batch < 0 || T < 0 || d_inner < 0 || d_state < 1) return HCLSM_ERR_SHAPE;
   if (!ckpt_shape_ok(d_state, dtype)) return HCLSM_ERR_UNSUPPORTED;
+  if (batch == 0 || T == 0 || d_inner == 0)
+    return hclsm_ssm_block_scan_fwd(z, dt_in, A_log, B, C, gate, y, y_pre, h_final, batch, T, d_inner, d_state, dtype,
+                                    stream);
   if (!workspace || !gate) return HCLSM_ERR_NULL;
   const BwdWs L = bwd_ws(batch, T, d_inner, d_state);
   if (workspace_bytes < (int64_t)L.total) return HCLSM_ERR_SHAPE;
@@ -617,8 +622,10 @@ extern "C" int hclsm_ssm_scan_bwd_ckpt(const void* x, const void* dt, const floa
                                        float* gA_log, void* gB, void* gC, float* gD, int64_t batch, int64_t T,
                                        int64_t d_inner, int64_t d_state, int dtype, int mode, void* workspace,
                                        int64_t workspace_bytes, void* stream) {
-  if (batch < 1 || T < 1 || d_inner < 1 || d_state < 1) return HCLSM_ERR_SHAPE;
+  if (batch < 0 || T < 0 || d_inner < 0 || d_state < 1) return HCLSM_ERR_SHAPE;
   if (!ckpt_shape_ok(d_state, dtype)) return HCLSM_ERR_UNSUPPORTED;
+  // (an empty problem has no checkpoints: the plain backward's zero gradients)
+  const bool empty = batch == 0 || T == 0 || d_inner == 0;
   return scan_bwd_entry(x, dt, A_log, B, C, Dskip, gy, gx, gdt, gA_log, gB, gC, gD, batch, T, d_inner, d_state, dtype,
-                        mode, workspace, workspace_bytes, true, stream);
+                        mode, workspace, workspace_bytes, !empty, stream);
 }

@@ -162,3 +162,25 @@ def test_noalloc_forward_rejects_oversized_shapes_before_launch(lib):
     assert need > (64 << 20)
     assert f(None, None, 384, None, None, 512, 32, 196, 384, 768, 3, 0.05, 0.0, 1e-8, 0.0, 1, None) == -6
     assert f(None, None, 384, None, None, -1, 32, 196, 384, 768, 3, 0.05, 0.0, 1e-8, 0.0, 1, None) == -2
+
+
+def test_scan_checkpoint_pair_argument_errors_before_launch(lib):
+    """The training pair's entry points reject what they do not take on the host: modes, shapes, dtypes other
+    than bf16 with d_state 16, missing or short workspaces; empty problems behave as the plain pair's."""
+    fwd, blk, bwd = lib.hclsm_ssm_scan_fwd_ckpt, lib.hclsm_ssm_block_scan_fwd_ckpt, lib.hclsm_ssm_scan_bwd_ckpt
+    n8, n9, n13 = [None] * 8, [None] * 9, [None] * 13
+    ws_need = lib.hclsm_ssm_scan_bwd_workspace(2, 16, 64, 16)
+    assert ws_need > 0
+    assert fwd(*n8, 2, 16, 64, 16, 1, 2, None, 0, None) == -5        # BLOCK is the block entry's mode
+    assert fwd(*n8, -1, 16, 64, 16, 1, 0, None, 0, None) == -2
+    assert fwd(*n8, 2, 16, 64, 8, 1, 0, None, 0, None) == -4          # d_state 8
+    assert fwd(*n8, 2, 16, 64, 16, 0, 0, None, 0, None) == -4         # fp32 I/O
+    assert fwd(*n8, 2, 16, 64, 16, 1, 0, None, 0, None) == -1         # no workspace
+    assert fwd(*n8, 2, 16, 64, 16, 1, 0, ctypes.c_void_p(256), ws_need - 1, None) == -2   # workspace too small
+    assert fwd(*n8, 0, 16, 64, 16, 1, 0, None, 0, None) == 0          # nothing to scan
+    assert blk(*n9, 2, 16, 64, 16, 1, None, 0, None) == -1
+    assert blk(*n9, 2, 16, 64, 32, 1, None, 0, None) == -4
+    assert blk(*n9, 0, 16, 64, 16, 1, None, 0, None) == 0
+    assert bwd(*n13, 2, 16, 64, 16, 1, 0, None, 0, None) == -1
+    assert bwd(*n13, 2, 16, 64, 16, 2, 0, None, 0, None) == -4        # fp16
+    assert bwd(*n13, 2, 16, 64, 16, 1, 7, None, 0, None) == -5
