@@ -663,8 +663,9 @@ linear_dma_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const t
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   request(0);
   for (int kc = 0; kc < nk; ++kc) {
-    wait_vmcnt<0>();                // this lane's part of chunk kc is in LDS
-    __builtin_amdgcn_s_barrier();   // ... every lane's, and chunk kc - 1 is consumed by every wave
+    wait_vmcnt<0>();   // this lane's part of chunk kc is in LDS
+    __syncthreads();   // ... every lane's, and chunk kc - 1 is consumed by every wave (the fences also keep the
+                       // compiler from moving LDS reads across the barrier)
     if (kc + 1 < nk) request(kc + 1);
     const T* As = reinterpret_cast<const T*>(smem + (kc & 1) * 2 * LD_OPB);
     const T* Bs = reinterpret_cast<const T*>(smem + (kc & 1) * 2 * LD_OPB + LD_OPB);
