@@ -15,8 +15,8 @@
 // registers, then runs the reverse recurrence step by step.  B_t / C_t rows are staged in LDS as fp32,
 // 64 steps at a time.  Sums over the state axis (gx, gdt) are DPP sums inside the G-lane group; sums
 // over the channel axis (gB, gC) are a recursive-halving reduce-scatter across the wave's channels
-// followed by a cross-wave sum through LDS once per chunk, one part per channel block.  Small kernels
-// then reduce the per-sequence partials of gA_log and gD, and add the blocks' gB / gC parts and cast.
+// followed by a cross-wave sum through LDS once per chunk, one part per channel block.  One tail launch
+// then reduces the per-sequence partials of gA_log and gD, and adds the blocks' gB / gC parts and casts.
 #include "internal.h"
 
 namespace hclsm {
@@ -387,42 +387,55 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
   }
 }
 
-// out[c] = sum_n part[n * ncols + c]: 64 columns per workgroup, 16 row groups, reads coalesced along c.
-__global__ void __launch_bounds__(1024)
-ssm_scan_bwd_reduce(const float* __restrict__ part, int64_t N, int64_t ncols, float* __restrict__ out) {
-  __shared__ float red[16][64];
-  const int c = threadIdx.x & 63, rg = threadIdx.x >> 6;
-  const int64_t col = (int64_t)blockIdx.x * 64 + c;
-  float acc = 0.f;
-  if (col < ncols) {
-#pragma unroll 8
-    for (int64_t n = rg; n < N; n += 16) acc += part[n * ncols + col];
-  }
-  red[rg][c] = acc;
-  __syncthreads();
-  if (rg == 0 && col < ncols) {
-    float t = 0.f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) t += red[r][c];
-    out[col] = t;
-  }
-}
-
-// gB, gC (dtype) from the channel blocks' parts in gbc (summed in block order); gA_log[d, s] = (sum_n gA_part) * dA/dA_log; gD[d] = sum_n gD_part (both sums
-// already reduced into ga_sum / gd_sum).
+// The backward's tail in one launch: blocks [0, nga) reduce the per-sequence gA partials over the sequences and
+// write gA_log[d, s] = sum * dA/dA_log; blocks [nga, nga + ngd) reduce the gD partials; the remaining blocks add
+// the channel blocks' gB / gC parts in block order and cast.  The three parts are independent.  Each reducing
+// block sums 64 columns in 16 row groups (fixed order: deterministic).
 template <int DT, int SP, int MODE>
-__global__ void __launch_bounds__(256)
-ssm_scan_bwd_finalize(const float* __restrict__ gbc, const float* __restrict__ ga_sum,
-                      const float* __restrict__ gd_sum, const float* __restrict__ A_log,
-                      typename Elem<DT>::T* __restrict__ gB, typename Elem<DT>::T* __restrict__ gC,
-                      float* __restrict__ gA_log, float* __restrict__ gD, int64_t N, int T, int Dn, int S,
-                      int nblk) {
+__global__ void __launch_bounds__(1024)
+ssm_scan_bwd_tail(const float* __restrict__ ga_part, const float* __restrict__ gd_part, const float* __restrict__ gbc,
+                  const float* __restrict__ A_log, typename Elem<DT>::T* __restrict__ gB,
+                  typename Elem<DT>::T* __restrict__ gC, float* __restrict__ gA_log, float* __restrict__ gD,
+                  int64_t N, int T, int Dn, int S, int nblk, int nga, int ngd) {
   using E = Elem<DT>;
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  const int64_t tid0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  __shared__ float red[16][64];
+  const int bx = blockIdx.x;
+  if (bx < nga + ngd) {
+    const bool is_a = bx < nga;
+    const int64_t ncols = is_a ? (int64_t)Dn * SP : Dn;
+    const float* part = is_a ? ga_part : gd_part;
+    const int c = threadIdx.x & 63, rg = threadIdx.x >> 6;
+    const int64_t col = (int64_t)(is_a ? bx : bx - nga) * 64 + c;
+    float acc = 0.f;
+    if (col < ncols) {
+#pragma unroll 8
+      for (int64_t n = rg; n < N; n += 16) acc += part[n * ncols + col];
+    }
+    red[rg][c] = acc;
+    __syncthreads();
+    if (rg == 0 && col < ncols) {
+      float t = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) t += red[r][c];
+      if (is_a) {
+        const int64_t dd = col / SP, s = col - dd * SP;
+        if (s < S) {   // (padded states carry no gradient)
+          const int64_t i = dd * S + s;
+          const float e = expf(A_log[i]);
+          float dadl = -e;                          // d(-exp(A_log))/dA_log
+          if (MODE != HCLSM_SCAN_RAW && !(e >= 1e-6f && e <= 1.0f)) dadl = 0.f;
+          gA_log[i] = t * dadl;
+        }
+      } else {
+        gD[col] = t;
+      }
+    }
+    return;
+  }
+  const int64_t stride = (int64_t)(gridDim.x - nga - ngd) * blockDim.x;
   const int64_t nbc = N * T * S;
   const int64_t part = N * T * 2 * SP;   // floats per channel block's partial
-  for (int64_t i = tid0; i < nbc; i += stride) {
+  for (int64_t i = (int64_t)(bx - nga - ngd) * blockDim.x + threadIdx.x; i < nbc; i += stride) {
     const int64_t r = i / S, s = i - r * S;
     float b = 0.f, c = 0.f;
     for (int k = 0; k < nblk; ++k) {   // fixed order: deterministic
@@ -432,15 +445,6 @@ ssm_scan_bwd_finalize(const float* __restrict__ gbc, const float* __restrict__ g
     E::st(gB + i, b);
     E::st(gC + i, c);
   }
-  for (int64_t i = tid0; i < (int64_t)Dn * S; i += stride) {
-    const int64_t dd = i / S, s = i - dd * S;
-    const float e = expf(A_log[i]);
-    float dadl = -e;                          // d(-exp(A_log))/dA_log
-    if (MODE != HCLSM_SCAN_RAW && !(e >= 1e-6f && e <= 1.0f)) dadl = 0.f;
-    gA_log[i] = ga_sum[dd * SP + s] * dadl;
-  }
-  if (gD)
-    for (int64_t dd = tid0; dd < Dn; dd += stride) gD[dd] = gd_sum[dd];
 }
 
 static int64_t sp_of(int64_t S) {
@@ -448,7 +452,7 @@ static int64_t sp_of(int64_t S) {
 }
 
 struct BwdWs {
-  size_t ck, gbc, ga, gd, ga_sum, gd_sum, total;
+  size_t ck, gbc, ga, gd, total;
   int nchunk, nck;
   BwdGrid grid;
 };
@@ -467,8 +471,6 @@ static BwdWs bwd_ws(int64_t N, int64_t T, int64_t Dn, int64_t S) {
   w.gbc = o; o += al((size_t)w.grid.nblk * N * T * 2 * SP * 4);
   w.ga = o; o += al((size_t)N * Dn * SP * 4);
   w.gd = o; o += al((size_t)N * Dn * 4);
-  w.ga_sum = o; o += al((size_t)Dn * SP * 4);
-  w.gd_sum = o; o += al((size_t)Dn * 4);
   w.total = o;
   return w;
 }
@@ -494,21 +496,13 @@ static int launch_bwd(const void* x, const void* dt, const float* A_log, const v
                      (TT*)gdt, reinterpret_cast<float*>(ws + L.ck), gbc, reinterpret_cast<float*>(ws + L.ga),
                      reinterpret_cast<float*>(ws + L.gd), a);
   HCLSM_LAUNCH_CHECK();
-  float* ga_sum = reinterpret_cast<float*>(ws + L.ga_sum);
-  float* gd_sum = reinterpret_cast<float*>(ws + L.gd_sum);
-  const int64_t nga = Dn * SP;
-  hipLaunchKernelGGL(ssm_scan_bwd_reduce, dim3((unsigned)((nga + 63) / 64)), dim3(1024), 0, st,
-                     reinterpret_cast<const float*>(ws + L.ga), N, nga, ga_sum);
-  HCLSM_LAUNCH_CHECK();
-  if (gD) {
-    hipLaunchKernelGGL(ssm_scan_bwd_reduce, dim3((unsigned)((Dn + 63) / 64)), dim3(1024), 0, st,
-                       reinterpret_cast<const float*>(ws + L.gd), N, Dn, gd_sum);
-    HCLSM_LAUNCH_CHECK();
-  }
-  int64_t g = (N * T * S + 255) / 256;
-  g = g < 1 ? 1 : (g > 2048 ? 2048 : g);
-  hipLaunchKernelGGL((ssm_scan_bwd_finalize<DT, SP, MODE>), dim3((unsigned)g), dim3(256), 0, st, gbc, ga_sum,
-                     gd_sum, A_log, (TT*)gB, (TT*)gC, gA_log, gD, N, (int)T, (int)Dn, (int)S, nblk_d);
+  // the tail: gA_log and gD reductions and the gB / gC block sums, one launch
+  const int nga = (int)((Dn * SP + 63) / 64), ngd = gD ? (int)((Dn + 63) / 64) : 0;
+  int64_t g = (N * T * S + 1023) / 1024;
+  g = g < 1 ? 1 : (g > 1024 ? 1024 : g);
+  hipLaunchKernelGGL((ssm_scan_bwd_tail<DT, SP, MODE>), dim3((unsigned)(nga + ngd + g)), dim3(1024), 0, st,
+                     reinterpret_cast<const float*>(ws + L.ga), reinterpret_cast<const float*>(ws + L.gd), gbc, A_log,
+                     (TT*)gB, (TT*)gC, gA_log, gD, N, (int)T, (int)Dn, (int)S, nblk_d, nga, ngd);
   HCLSM_LAUNCH_CHECK();
   return 0;
 }

@@ -109,7 +109,7 @@ int64_t hclsm_ssm_scan_bwd_workspace(int64_t batch, int64_t T, int64_t d_inner, 
  * block's dt input (before softplus) as `dt`, recomputes dt = clamp(softplus(dt), 1e-3, 1) in fp32 exactly as
  * the fused block forward does, and returns in gdt the gradient with respect to that input (through the clamp,
  * closed interval, and softplus).  Chunk checkpoints and
- * partial sums live in `workspace` (>= hclsm_ssm_scan_bwd_workspace bytes).  Four launches at most.
+ * partial sums live in `workspace` (>= hclsm_ssm_scan_bwd_workspace bytes).  Two launches.
  * Deterministic (no float atomics).  One sequence's [T, d_inner] slab must be < 2^31 bytes
  * (HCLSM_ERR_UNSUPPORTED otherwise).
  * Replaces: _TritonSSMScan.backward (hclsm/kernels/ssm_scan_kernel.py:321-377) and the autograd of
