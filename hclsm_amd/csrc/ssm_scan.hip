@@ -437,8 +437,9 @@ static int launch_scan_sgpr(const void* x, const void* dt, const float* A_log, c
 // Both products are exact in fp32, so the state keeps fp32 accuracy; the
 // matrix core replaces one multiply and turns the FMA into a multiply.  Each
 // lane needs b_s for a lane-dependent s, so the B row is read with a per-lane
-// 2-byte load; the C row is uniform and goes through scalar loads, unpacked on
-// the scalar unit.
+// 2-byte load (lanes whose row belongs to the other k half load from past the
+// buffer's range, which reads 0); the C row is uniform and goes through scalar
+// loads, unpacked on the scalar unit.
 //
 // The loop is bound by VALU issue: per state update one multiply for the
 // exponent, one v_exp_f32 (two FMA issue slots on gfx950), one multiply for
@@ -504,7 +505,7 @@ ssm_scan_fwd_mfma_kernel(const uint16_t* __restrict__ x, const uint16_t* __restr
       epi.y_pre ? slab : 0, kRawBufferWord3);
   const int vo = d0 * 2;
   const int vo_st = act ? vo : 0x7ffffff0;             // past num_records: the store is dropped
-  const int vo_b = s_row * 2;
+  const int vo_b = a_on ? s_row * 2 : 0x7ffffff0;   // rows of the other k half read 0 (past num_records)
   const int pitch = Dn * 2;
   const uint32_t* cw0 = reinterpret_cast<const uint32_t*>(Cm + row0 * SP);
 
@@ -547,6 +548,12 @@ ssm_scan_fwd_mfma_kernel(const uint16_t* __restrict__ x, const uint16_t* __restr
     }
   };
 
+  // MFMA operands: only the low halves change per step; the zero halves stay in their registers (built once, so
+  // no per-step copies of zeros)
+  s16x4_t aop = {0, 0, 0, 0};
+  s16x4_t bop[DPL];
+#pragma unroll
+  for (int k = 0; k < DPL; ++k) bop[k] = s16x4_t{0, 0, 0, 0};
   auto step = [&](int t, uint32_t xw, uint32_t dw_next, uint16_t bb, uint32_t gw) {
     if constexpr (CK) {   // the state before steps 8, 16, ..., for the backward (before step 0 it is zero)
       if ((t & 7) == 0 && t > 0 && act) {
@@ -562,8 +569,8 @@ ssm_scan_fwd_mfma_kernel(const uint16_t* __restrict__ x, const uint16_t* __restr
     uint32_t cwn[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) cwn[i] = cw0[(size_t)tn * 8 + i];
-    const short ab = a_on ? (short)bb : (short)0;
-    const s16x4_t aop = {ab, ab, 0, 0};
+    aop.x = (short)bb;
+    aop.y = (short)bb;
     float xs[DPL];
 #pragma unroll
     for (int k = 0; k < DPL; ++k) {
@@ -571,10 +578,11 @@ ssm_scan_fwd_mfma_kernel(const uint16_t* __restrict__ x, const uint16_t* __restr
       const float u = dtc[k] * xs[k];
       const uint32_t uhi = __float_as_uint(u) & 0xffff0000u;
       const float ulo = u - __uint_as_float(uhi);
-      const s16x4_t bop = {(short)(uhi >> 16), (short)(__float_as_uint(ulo) >> 16), 0, 0};
+      bop[k].x = (short)(uhi >> 16);
+      bop[k].y = (short)(__float_as_uint(ulo) >> 16);
 #pragma unroll
       for (int s = 0; s < SP; ++s) h[k][s] *= gt[k][s];
-      h[k] = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(aop, bop, h[k], 0, 0, 0);
+      h[k] = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(aop, bop[k], h[k], 0, 0, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
     gates(dw_next);
