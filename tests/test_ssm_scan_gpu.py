@@ -101,21 +101,26 @@ def test_reference_test_distribution_modes_differ():
     assert normwise_rel_err(ref_raw, ref_mod) > 1e-2
 
 
-def test_config1_bf16_subset_and_properties():
-    """Full config-1 launch (1024, 64, 384) bf16; oracle on a subset of sequences,
-    plus size-independent properties on the whole output."""
+def test_config1_bf16_full_and_properties():
+    """Full config-1 launch (1024, 64, 384) bf16 against the oracle on every sequence (in blocks of 256, each
+    block and the whole output at the bf16 bar), plus linearity on the whole output."""
     from hclsm_amd.workloads import scan_config
     d = scan_config(1)
     y = _run(d, "raw", True)
     torch.cuda.synchronize()
     assert y.shape == (1024, 64, 384) and y.dtype == torch.bfloat16
     assert torch.isfinite(y).all()
-    sel = list(range(0, 48)) + list(range(1000, 1024))
-    sub = {k: (v[sel] if k in ("x", "dt", "B", "C") else v) for k, v in d.items()}
-    ref = ssm_scan_ref(_np(sub["x"]), _np(sub["dt"]), _np(sub["A_log"]), _np(sub["B"]), _np(sub["C"]),
-                       D=_np(sub["D"]), clamp_mode="raw")
-    err = normwise_rel_err(_np(y[sel]), ref)
-    assert err <= LOWP_TOL, f"cfg1 normwise err {err:.3e}"
+    yn = _np(y)
+    dmax = rmax = 0.0
+    for s0 in range(0, 1024, 256):
+        sel = slice(s0, s0 + 256)
+        ref = ssm_scan_ref(_np(d["x"][sel]), _np(d["dt"][sel]), _np(d["A_log"]), _np(d["B"][sel]), _np(d["C"][sel]),
+                           D=_np(d["D"]), clamp_mode="raw")
+        err = normwise_rel_err(yn[sel], ref)
+        assert err <= LOWP_TOL, f"cfg1 sequences {s0}..{s0 + 255}: normwise err {err:.3e}"
+        dmax = max(dmax, float(np.abs(yn[sel] - ref).max()))
+        rmax = max(rmax, float(np.abs(ref).max()))
+    assert dmax / rmax <= LOWP_TOL, f"cfg1 all sequences: normwise err {dmax / rmax:.3e}"
     # linearity in x (dt fixed): y(2x) - D*2x == 2 (y(x) - D*x) up to bf16 rounding
     d2 = dict(d)
     d2["x"] = (d["x"].float() * 2).to(torch.bfloat16)   # exact in bf16
