@@ -60,6 +60,7 @@ _SIGNATURES: dict[str, list] = {
                              _int, _c_void_p, _i64, _c_void_p],
     "hclsm_slot_attention_workspace": [_i64, _i64, _i64, _i64, _i64, _i64, _int],
     "hclsm_slot_attention_k_offset": [_i64, _i64, _i64, _i64, _i64, _i64, _int],
+    "hclsm_slot_attention_kq_offset": [_i64, _i64, _i64, _i64, _i64, _i64, _int],
     "hclsm_slot_attention_iteration": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _c_void_p,
                                        _i64, _i64, _i64, _i64, _i64, _f32, _f32, _f32, _f32, _int, _c_void_p,
                                        _i64, _c_void_p],
@@ -86,7 +87,8 @@ _SIGNATURES: dict[str, list] = {
 }
 _RESTYPES = {"hclsm_strerror": ctypes.c_char_p, "hclsm_slot_attn_core_workspace": ctypes.c_int64,
              "hclsm_ssm_scan_bwd_workspace": ctypes.c_int64,
-             "hclsm_slot_attention_workspace": ctypes.c_int64, "hclsm_slot_attention_k_offset": ctypes.c_int64, "hclsm_level1_forward_workspace": ctypes.c_int64,
+             "hclsm_slot_attention_workspace": ctypes.c_int64, "hclsm_slot_attention_k_offset": ctypes.c_int64,
+             "hclsm_slot_attention_kq_offset": ctypes.c_int64, "hclsm_level1_forward_workspace": ctypes.c_int64,
              "hclsm_relation_graph_workspace": ctypes.c_int64, "hclsm_slot_track_cost_workspace": ctypes.c_int64,
              "hclsm_slot_track_reorder_update_workspace": ctypes.c_int64,
              "hclsm_slot_track_sequence_workspace": ctypes.c_int64,
@@ -97,7 +99,7 @@ class HclsmSlotWeights(ctypes.Structure):
     """Mirror of the C struct HclsmSlotWeights (include/hclsm_amd.h)."""
     _fields_ = [(n, ctypes.c_void_p) for n in (
         "w_q", "w_kv", "w_ih", "w_hh", "w1", "w2", "b_ih", "b_hh", "b1", "b2",
-        "ln_in_w", "ln_in_b", "ln_pre_w", "ln_pre_b", "ln_mlp_w", "ln_mlp_b", "w_qt")]
+        "ln_in_w", "ln_in_b", "ln_pre_w", "ln_pre_b", "ln_mlp_w", "ln_mlp_b", "w_qt", "w_qkv")]
 
 _lib = None
 

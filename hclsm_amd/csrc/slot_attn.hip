@@ -2786,6 +2786,11 @@ static int slot_iteration_impl(const HclsmSlotWeights* W, const float* slots_in,
                      d, hidden, 0, slot_clamp, 0, nullptr, nullptr, 0.f, dtype, st);
 }
 
+// The 16-bit forward forms kq = k W_q (and its iterations run the fused core's LNQ form).
+static bool kq_formed(const SlotWs& L, int64_t B, int64_t N, int64_t M, int64_t d, int dtype) {
+  return L.has_kq && core_fused_fits(B, N, M, d, dtype);
+}
+
 static int check_slot_args(const HclsmSlotWeights* W, int64_t B, int64_t N, int64_t M, int64_t d, int64_t hidden,
                            int dtype, void* workspace, int64_t workspace_bytes, bool with_kv, SlotWs* L,
                            int64_t d_in = 0) {
@@ -2798,7 +2803,7 @@ static int check_slot_args(const HclsmSlotWeights* W, int64_t B, int64_t N, int6
   if (N > 16 * CORE_MAX_NT || B > 65535) return HCLSM_ERR_UNSUPPORTED;
   // 16-bit weights are read with 16-byte loads (the GEMMs, the GRU and the fused core's W_hh tiles)
   if (dtype != HCLSM_F32 && (!al16(W->w_q) || !al16(W->w_ih) || !al16(W->w_hh) || !al16(W->w1) || !al16(W->w2) ||
-                             (with_kv && !al16(W->w_kv))))
+                             (with_kv && (!al16(W->w_kv) || !al16(W->w_qkv)))))
     return HCLSM_ERR_UNSUPPORTED;
   *L = slot_ws_layout(B, N, M, d, hidden, dtype == HCLSM_F32 ? 4 : 2, with_kv, d_in);
   if (workspace_bytes < (int64_t)L->total) return HCLSM_ERR_SHAPE;
@@ -2840,7 +2845,10 @@ static int slot_forward_impl(const HclsmSlotWeights* W, const float* inputs, int
   char* ws = reinterpret_cast<char*>(workspace);
   const int esize = dtype == HCLSM_F32 ? 4 : 2;
   void* kv = ws + L.kv;
-  // k | v = LN_in(inputs) [W_k; W_v]^T     (dynamic_slots.py:152-154)
+  // The iterations run the fused core's LNQ form (queries as LN_pre(slots) (k W_q)^T): with the caller's
+  // [W_q^T W_k; W_v] the projection writes kq = k W_q itself, and k is not formed.
+  const bool qkv = W->w_qkv != nullptr && kq_formed(L, B, N, M, d, dtype);
+  // k | v = LN_in(inputs) [W_k; W_v]^T     (dynamic_slots.py:152-154), or kq | v
   void* xin = ws + L.xin;
   rc = ln_impl(inputs, d_in, W->ln_in_w, W->ln_in_b, xin, d_in, B * M, d_in, 1e-5f, HCLSM_F32, dtype, st);
   if (rc) return rc;
@@ -2851,8 +2859,8 @@ static int slot_forward_impl(const HclsmSlotWeights* W, const float* inputs, int
     const OutSplit os{d, M, Mp, d * Mp, vt};
 #define HCLSM_KV(D_, XT_)                                                                                    \
     if (dtype == D_)                                                                                         \
-      launch_linear_quad<D_, D_, XT_>(xin, d_in, W->w_kv, d_in, nullptr, nullptr, 0, kv, d, nullptr, 0, B * M, \
-                                      2 * d, d_in, 0, 0.f, st, os);
+      launch_linear_quad<D_, D_, XT_>(xin, d_in, qkv ? W->w_qkv : W->w_kv, d_in, nullptr, nullptr, 0,         \
+                                      qkv ? ws + L.kq : kv, d, nullptr, 0, B * M, 2 * d, d_in, 0, 0.f, st, os);
     HCLSM_KV(HCLSM_BF16, uint16_t)
     HCLSM_KV(HCLSM_F16, _Float16)
     HCLSM_KV(HCLSM_F32, float)
@@ -2863,9 +2871,10 @@ static int slot_forward_impl(const HclsmSlotWeights* W, const float* inputs, int
   const void* k = kv;
   if (N == 0) return 0;
   if (n_iter == 0) return (int)hipMemcpyAsync(slots_out, slots0, (size_t)B * N * d * 4, hipMemcpyDeviceToDevice, st);
-  // k Wq = k (Wq^T)^T once per call, so that no iteration projects the slots to queries
-  const void* kq = nullptr;
-  if (L.has_kq && core_fused_fits(B, N, M, d, dtype)) {
+  // k Wq = k (Wq^T)^T once per call (unless the projection formed it), so that no iteration projects the
+  // slots to queries
+  const void* kq = qkv ? ws + L.kq : nullptr;
+  if (!qkv && kq_formed(L, B, N, M, d, dtype)) {
     const void* wqt = W->w_qt;   // the caller's copy, formed once per weight set, or one formed here
     if (wqt == nullptr || !al16(wqt)) {
       rc = transpose_16(W->w_q, d, ws + L.wqt, d, d, d, st);
@@ -2891,6 +2900,14 @@ extern "C" int64_t hclsm_slot_attention_k_offset(int64_t B, int64_t N, int64_t M
   if (B < 0 || N < 0 || M < 1 || d < 1 || hidden < 1 || d_in < 1) return HCLSM_ERR_SHAPE;
   if (dtype != HCLSM_BF16 && dtype != HCLSM_F16 && dtype != HCLSM_F32) return HCLSM_ERR_DTYPE;
   return (int64_t)slot_ws_layout(B, N, M, d, hidden, dtype == HCLSM_F32 ? 4 : 2, true, d_in).kv;
+}
+
+extern "C" int64_t hclsm_slot_attention_kq_offset(int64_t B, int64_t N, int64_t M, int64_t d_in, int64_t d,
+                                                  int64_t hidden, int dtype) {
+  if (B < 0 || N < 0 || M < 1 || d < 1 || hidden < 1 || d_in < 1) return HCLSM_ERR_SHAPE;
+  if (dtype != HCLSM_BF16 && dtype != HCLSM_F16 && dtype != HCLSM_F32) return HCLSM_ERR_DTYPE;
+  const SlotWs L = slot_ws_layout(B, N, M, d, hidden, dtype == HCLSM_F32 ? 4 : 2, true, d_in);
+  return kq_formed(L, B, N, M, d, dtype) ? (int64_t)L.kq : (int64_t)HCLSM_ERR_UNSUPPORTED;
 }
 
 extern "C" int hclsm_slot_attention_forward(const HclsmSlotWeights* W, const float* inputs, int64_t d_in,

@@ -64,6 +64,12 @@ class SlotWeights:
         if dtype in (torch.bfloat16, torch.float16):
             # the forward multiplies the keys by W_q (queries as LN(s) (k W_q)^T): its transpose, once per weight set
             t["w_qt"] = t["w_q"].t().contiguous()
+            if "w_k" in t and "w_v" in t:
+                # kq = LN_in(x) (W_q^T W_k)^T: the product of the rounded weights in fp32, rounded once; the
+                # projection then forms kq and v in one launch
+                with torch.autocast("cuda", enabled=False):
+                    wqk = t["w_q"].float().t() @ t["w_k"].float()
+                t["w_qkv"] = torch.cat([wqk.to(dtype), t["w_v"]], 0).contiguous()
         d = t["w_q"].shape[0]
         return cls(dtype, d, t["w1"].shape[0], t)
 
@@ -171,12 +177,23 @@ def slot_attention_iteration(slots: torch.Tensor, k: torch.Tensor, v: torch.Tens
     return out.reshape(B, N, d)
 
 
+def forms_kq(B: int, N: int, M: int, d_in: int, W: SlotWeights) -> bool:
+    """Whether slot_attention_forward forms kq = k W_q for this shape (16-bit, fused-core shapes)."""
+    return int(_lib.lib().hclsm_slot_attention_kq_offset(B, N, M, d_in, W.d, W.hidden, _lib.dtype_code(W.dtype))) >= 0
+
+
 def slot_attention_forward(inputs: torch.Tensor, slots0: torch.Tensor, W: SlotWeights, n_iter: int,
-                           mode: SlotMode = REFERENCE_MODE, scale: float | None = None, return_k: bool = False):
-    """k, v = LN_in(inputs) W_k^T, W_v^T (one MFMA linear over [W_k; W_v]), then n_iter iterations
-    from slots0.  inputs (B, M, d_in), slots0 (B, N, d).  Returns slots (B, N, d) fp32, and with
-    return_k also a copy of the keys k (B, M, d) in W.dtype.  One C call, no host synchronisation."""
+                           mode: SlotMode = REFERENCE_MODE, scale: float | None = None, return_k: bool = False,
+                           return_kq: bool = False):
+    """k, v = LN_in(inputs) W_k^T, W_v^T (one MFMA linear over [W_k; W_v]; for 16-bit fused-core shapes
+    kq = k W_q and v over [W_q^T W_k; W_v] instead), then n_iter iterations from slots0.  inputs (B, M, d_in),
+    slots0 (B, N, d).  Returns slots (B, N, d) fp32; with return_k also a copy of the keys k (B, M, d) in
+    W.dtype (that call projects through [W_k; W_v]), with return_kq a copy of kq (B, M, d), for which the
+    logits are LN_pre(slots) kq^T scale (ValueError where forms_kq is False).  One C call, no host
+    synchronisation."""
     require_gpu("slot_attention_forward", inputs, slots0)
+    if return_k and return_kq:
+        raise ValueError("slot_attention_forward: return_k and return_kq are exclusive")
     B, M, d_in = inputs.shape
     N, d = slots0.shape[1], W.d
     if scale is None:
@@ -189,16 +206,24 @@ def slot_attention_forward(inputs: torch.Tensor, slots0: torch.Tensor, W: SlotWe
     wsb = L.hclsm_slot_attention_workspace(B, N, M, d_in, d, W.hidden, code)
     ws = _workspace(int(wsb), x.device)
     lc, re, sc = _mode_args(mode)
+    if return_kq:
+        off = int(L.hclsm_slot_attention_kq_offset(B, N, M, d_in, d, W.hidden, code))
+        if off < 0:
+            raise ValueError(f"slot_attention_forward: no kq for this shape and dtype (B={B} N={N} M={M} d={d} "
+                             f"{W.dtype}); use return_k")
     st = _struct(W)
+    if return_k:
+        st.w_qkv = None      # the keys themselves: project through [W_k; W_v]
     rc = L.hclsm_slot_attention_forward(ctypes.byref(st), _lib.ptr(x), d_in, _lib.ptr(s0), _lib.ptr(out), B, N, M, d,
                                         W.hidden, int(n_iter), float(scale), lc, re, sc, code, _lib.ptr(ws),
                                         ws.numel(), _lib.stream_of(x))
     _lib.check(rc, "hclsm_slot_attention_forward")
-    if not return_k:
+    if not (return_k or return_kq):
         return out
-    off = int(L.hclsm_slot_attention_k_offset(B, N, M, d_in, d, W.hidden, code))
-    if off < 0:
-        _lib.check(off, "hclsm_slot_attention_k_offset")
+    if return_k:
+        off = int(L.hclsm_slot_attention_k_offset(B, N, M, d_in, d, W.hidden, code))
+        if off < 0:
+            _lib.check(off, "hclsm_slot_attention_k_offset")
     nb = B * M * d * torch.tensor([], dtype=W.dtype).element_size()
     k = ws[off:off + nb].view(W.dtype).view(B, M, d).clone()
     return out, k

@@ -21,7 +21,7 @@ import torch.nn.functional as F
 
 from hclsm_amd.kernels._common import warn_fallback
 from hclsm_amd.kernels.slot_attention_kernel import slot_attention_core
-from hclsm_amd.kernels.slot_iteration import SlotMode, SlotWeights, slot_attention_forward
+from hclsm_amd.kernels.slot_iteration import SlotMode, SlotWeights, forms_kq, slot_attention_forward
 
 _LOGIT_CLAMP = 30.0   # dynamic_slots.py:118
 _SLOT_CLAMP = 50.0    # dynamic_slots.py:130
@@ -78,6 +78,7 @@ class DynamicSlotAttention(nn.Module):
     def forward(self, inputs: torch.Tensor, return_attention: bool = False):
         B, M, _ = inputs.shape
         slots = self._init_slots(B, inputs.device)
+        use_kq = False
         if self._needs_grad(inputs):
             warn_fallback("DynamicSlotAttention", "autograd (LayerNorm / Linear / GRUCell as torch ops around the "
                                                   "HIP attention core; the fused forward has no backward)")
@@ -93,13 +94,17 @@ class DynamicSlotAttention(nn.Module):
                 else torch.float32
             W = SlotWeights.from_module(self, dtype)
             mode = SlotMode(logit_clamp=_LOGIT_CLAMP, renorm_eps=None, slot_clamp=_SLOT_CLAMP)
+            # 16-bit fused-core shapes form kq = k W_q instead of k: birth's logits are then LN_pre(slots) kq^T
+            use_kq = forms_kq(B, slots.shape[1], inputs.shape[1], inputs.shape[2], W)
             slots, k = slot_attention_forward(inputs.float(), slots.float(), W, self.n_iterations, mode,
-                                              scale=self.scale, return_k=True)
+                                              scale=self.scale, return_k=not use_kq, return_kq=use_kq)
             slots = slots.to(inputs.dtype)
         alive = torch.sigmoid(self.existence_head(slots).squeeze(-1))              # :167-168
         final_attn = None
         with torch.no_grad():
-            q = self.project_q(self.norm_pre_attn(slots))
+            q = self.norm_pre_attn(slots)
+            if not use_kq:
+                q = self.project_q(q)
             k = k.to(q.dtype)
             _, attn = slot_attention_core(q.detach(), k.detach(), k.detach(), scale=self.scale)   # :172-177
             if return_attention:

@@ -341,6 +341,10 @@ typedef struct HclsmSlotWeights {
   const float* ln_mlp_w; const float* ln_mlp_b;  /* [d]    norm_slots */
   const void* w_qt;    /* [d, d] w_q transposed, nullable: formed once per weight set by the caller; when NULL a
                           16-bit forward forms it in its workspace on every call (one more launch) */
+  const void* w_qkv;   /* [2d, d_in] [w_q^T w_k; w_v], nullable: formed once per weight set by the caller (the
+                          product in fp32, then rounded).  A 16-bit forward whose iterations run the fused core
+                          (hclsm_slot_attention_kq_offset >= 0) then projects the inputs straight to kq = k w_q
+                          and v, with no kq GEMM per call, and forms no k */
 } HclsmSlotWeights;
 
 /* Workspace bytes for hclsm_slot_attention_iteration / _forward (16-byte aligned buffer). */
@@ -355,6 +359,17 @@ int64_t hclsm_slot_attention_workspace(int64_t B, int64_t N, int64_t M, int64_t 
  */
 int64_t hclsm_slot_attention_k_offset(int64_t B, int64_t N, int64_t M, int64_t d_in, int64_t d, int64_t hidden,
                                       int dtype);
+
+/*
+ * Byte offset, inside the workspace of hclsm_slot_attention_forward, of kq = k w_q ([B*M, d] row-major in
+ * `dtype`), which a 16-bit forward forms for shapes whose iterations run the fused attention core; a negative
+ * code (HCLSM_ERR_UNSUPPORTED) for shapes and dtypes that form none.  The logits are then
+ * LN_pre(slots) kq^T scale, so slot birth (dynamic_slots.py:180-186) can take its attention from kq without
+ * project_q.  When W->w_qkv is given and this offset is valid, the forward forms kq and no k: the keys at
+ * hclsm_slot_attention_k_offset are then not written.
+ */
+int64_t hclsm_slot_attention_kq_offset(int64_t B, int64_t N, int64_t M, int64_t d_in, int64_t d, int64_t hidden,
+                                       int dtype);
 
 /*
  * One slot-attention iteration (objects/dynamic_slots.py:98-131) for B frames of N slots:
@@ -372,9 +387,9 @@ int hclsm_slot_attention_iteration(const HclsmSlotWeights* W, const float* slots
  * DynamicSlotAttention forward up to the iterations (objects/dynamic_slots.py:149-164): k | v =
  * LN_in(inputs) [W_k; W_v]^T for inputs [B, M, d_in] float32, then n_iter iterations from slots0
  * [B, N, d] float32 into slots_out.  The slot initialisation draw (:86-96), existence head and slot
- * birth (:166-199) stay with the caller.  With N == 0 only the keys are formed (slots0 / slots_out may be
- * NULL); birth reads them at hclsm_slot_attention_k_offset in the workspace.  16-bit weight matrices must be
- * 16-byte aligned (HCLSM_ERR_UNSUPPORTED before any launch otherwise).
+ * birth (:166-199) stay with the caller.  With N == 0 only the keys k are formed (slots0 / slots_out may be
+ * NULL, W->w_qkv is not used); birth reads them at hclsm_slot_attention_k_offset in the workspace.  16-bit
+ * weight matrices must be 16-byte aligned (HCLSM_ERR_UNSUPPORTED before any launch otherwise).
  */
 int hclsm_slot_attention_forward(const HclsmSlotWeights* W, const float* inputs, int64_t d_in,
                                  const float* slots0, float* slots_out, int64_t B, int64_t N, int64_t M,

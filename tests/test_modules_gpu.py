@@ -332,6 +332,30 @@ def test_dynamic_slots_birth_matches_oracle(grad):
     assert torch.isfinite(s2).all() and torch.equal(s2, s3)
 
 
+def test_dynamic_slots_bf16_birth_attention_from_kq():
+    """Under a bf16 autocast the fused forward forms kq = k W_q instead of k (TINY's 128-wide slots take the
+    fused core), and the birth step takes its attention as softmax over slots of LN_pre(slots) kq^T scale,
+    without project_q.  The final attention map, the residual-driven birth and the slots agree with the fp32
+    forward (keys k, then project_q) within the bf16 bar."""
+    from hclsm_amd.kernels import slot_iteration as si
+    from hclsm_amd.objects import DynamicSlotAttention
+    torch.manual_seed(41)
+    m = DynamicSlotAttention(TINY.objects, TINY.d_world).cuda()
+    x = torch.randn(3, 100, TINY.d_world, device="cuda")
+    assert si.forms_kq(3, TINY.objects.n_max_slots, 100, TINY.d_world, si.SlotWeights.from_module(m, torch.bfloat16))
+    out = {}
+    for bf16 in (False, True):
+        torch.manual_seed(42)
+        with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16, enabled=bf16):
+            out[bf16] = m(x, return_attention=True)
+    (s32, a32, attn32), (s16, a16, attn16) = out[False], out[True]
+    assert attn16.shape == attn32.shape == (3, TINY.objects.n_max_slots, 100)
+    assert torch.allclose(attn16.float().sum(1), attn32.float().sum(1), atol=2e-2)
+    assert normwise_rel_err(_np(attn16), _np(attn32)) <= 2e-2
+    assert normwise_rel_err(_np(a16), _np(a32)) <= 2e-2
+    assert normwise_rel_err(_np(s16), _np(s32)) <= 2e-2
+
+
 def test_hot_path_from_reference_checkpoint_matches_oracle(tmp_path):
     """step_N.pt with the reference's layout (distributed.py:295-304) -> build_hot_path -> Level-0 and
     packed Level-1 forwards against oracle/modules.py with the checkpoint's weights."""

@@ -377,3 +377,58 @@ def test_forward_keys_with_no_slots():
     torch.cuda.synchronize()
     assert out0.shape == (3, 0, W.d) and k0.shape == k_ref.shape
     assert torch.equal(k0, k_ref)
+
+
+@pytest.mark.parametrize("B,M,N,d,d_in", [(6, 196, 32, 384, 384), (3, 70, 16, 128, 96)])
+def test_forward_kq_projection(B, M, N, d, d_in):
+    """With the weight set's [W_q^T W_k; W_v] (w_qkv) the 16-bit forward projects the inputs straight to
+    kq = k W_q and v, with no kq GEMM per call and no k.  The slots are checked against the oracle and against
+    the forward without w_qkv (k projected, then k W_q); kq from both against LN_in(x) W_k^T W_q in float64."""
+    from hclsm_amd.kernels import slot_iteration as si
+    from hclsm_amd.workloads import slot_config, xavier_uniform
+    tokens, slots0, w = slot_config(B=B, M=M, N=N, d=d, hidden=2 * d, seed=B + M)
+    g = torch.Generator().manual_seed(M)
+    w["w_k"] = xavier_uniform((d, d_in), g).to(torch.bfloat16).float()
+    w["w_v"] = xavier_uniform((d, d_in), g).to(torch.bfloat16).float()
+    w["ln_in_w"] = torch.rand(d_in, generator=g) + 0.5
+    w["ln_in_b"] = torch.randn(d_in, generator=g) * 0.1
+    tokens = torch.randn(B, M, d_in, generator=g) + 0.3
+    W = si.SlotWeights.from_dict(w, torch.bfloat16)
+    assert "w_qkv" in W.t and si.forms_kq(B, N, M, d_in, W)
+    W_plain = si.SlotWeights(W.dtype, W.d, W.hidden, {n: t for n, t in W.t.items() if n != "w_qkv"})
+    x, s0 = tokens.cuda(), slots0.cuda()
+    out, kq = si.slot_attention_forward(x, s0, W, 3, si.CONFIG2_MODE, return_kq=True)
+    out_p, kq_p = si.slot_attention_forward(x, s0, W_plain, 3, si.CONFIG2_MODE, return_kq=True)
+    torch.cuda.synchronize()
+    ref = sa.slot_attention_forward(tokens.numpy(), slots0.numpy(), {n: _np(t) for n, t in w.items()}, 3,
+                                    logit_clamp=None, renorm_eps=1e-8, slot_clamp=None)
+    assert normwise_rel_err(_np(out), ref) <= 2e-2
+    assert normwise_rel_err(_np(out_p), ref) <= 2e-2
+    assert normwise_rel_err(_np(out), _np(out_p)) <= 1e-2
+    xn = sa.layer_norm(_np(tokens), _np(w["ln_in_w"]), _np(w["ln_in_b"]))
+    kq64 = (xn @ _np(w["w_k"]).T) @ _np(w["w_q"])
+    assert kq.shape == (B, M, d) and kq.dtype == torch.bfloat16
+    assert normwise_rel_err(_np(kq), kq64) <= 1e-2
+    assert normwise_rel_err(_np(kq_p), kq64) <= 1e-2
+
+
+def test_kq_offset_only_for_fused_core_shapes():
+    """hclsm_slot_attention_kq_offset is valid for 16-bit fused-core shapes only: fp32, no slots, and a slot
+    width the fused core does not take give HCLSM_ERR_UNSUPPORTED, and return_kq raises there; return_k still
+    gives the keys (projected through [W_k; W_v]) where w_qkv is present."""
+    from hclsm_amd import _lib
+    from hclsm_amd.kernels import slot_iteration as si
+    from hclsm_amd.workloads import slot_config
+    L = _lib.lib()
+    assert L.hclsm_slot_attention_kq_offset(2, 8, 40, 384, 384, 768, _lib.BF16) >= 0
+    assert L.hclsm_slot_attention_kq_offset(2, 8, 40, 384, 384, 768, _lib.F32) == -4
+    assert L.hclsm_slot_attention_kq_offset(2, 0, 40, 384, 384, 768, _lib.BF16) == -4
+    assert L.hclsm_slot_attention_kq_offset(2, 8, 40, 64, 64, 256, _lib.BF16) == -4
+    tokens, slots0, w = slot_config(B=2, M=40, N=8)
+    W32 = si.SlotWeights.from_dict(w, torch.float32)
+    with pytest.raises(ValueError):
+        si.slot_attention_forward(tokens.cuda(), slots0.cuda(), W32, 3, return_kq=True)
+    W = si.SlotWeights.from_dict(w, torch.bfloat16)
+    _, k = si.slot_attention_forward(tokens.cuda(), slots0.cuda(), W, 3, return_k=True)
+    xn = sa.layer_norm(_np(tokens))
+    assert normwise_rel_err(_np(k), xn @ _np(w["w_k"]).T) <= 1e-2
