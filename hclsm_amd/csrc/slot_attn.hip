@@ -2431,48 +2431,51 @@ __device__ __forceinline__ void ln_store4(typename MM<DT>::T* p, float4 v) {
   }
 }
 
-// LayerNorm for rows of D = 4u elements (u <= 64 * VPL 4-element units) starting 16-byte (fp32) / 8-byte aligned:
-// one wave per row, lane l holding units l, l + 64, ... in registers, every load issued before the reductions.
-// Same two-pass statistics as layer_norm_kernel.  With xc the input rows are also written, in the output type,
-// to xc (row stride ldy).
-template <int DTI, int DTO, int VPL>
+// LayerNorm for rows of D = 4u elements (u <= LPR * VPL 4-element units) starting 16-byte (fp32) / 8-byte aligned:
+// LPR lanes per row (64: a wave per row; 32: two rows per wave, one per half), lane l of a row holding units
+// l, l + LPR, ... in registers, every load issued before the reductions.  Same two-pass statistics as
+// layer_norm_kernel.  With xc the input rows are also written, in the output type, to xc (row stride ldy).
+template <int DTI, int DTO, int VPL, int LPR = 64>
 __global__ void __launch_bounds__(256)
 layer_norm_vec_kernel(const typename MM<DTI>::T* __restrict__ x, int64_t ldx, const float* __restrict__ w,
                       const float* __restrict__ b, typename MM<DTO>::T* __restrict__ y, int64_t ldy, int64_t M,
                       int D, float eps, LinExt ext, typename MM<DTO>::T* __restrict__ xc) {
-  const int lane = threadIdx.x & 63;
+  static_assert(LPR == 64 || LPR == 32, "a row per wave or per half-wave");
+  constexpr int RPW = 64 / LPR;   // rows per wave
+  const int lane = threadIdx.x & 63, ll = lane % LPR;
   M = ext_rows(ext, M);
   const int U = D >> 2;
-  // rows walked with the grid's stride (the grid may be smaller than M / 4 with a device-side row count)
-  for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < M; row += (int64_t)gridDim.x * 4) {
+  // rows walked with the grid's stride (the grid may be smaller than M / (4 RPW) with a device-side row count)
+  for (int64_t row = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW + lane / LPR; row < M;
+       row += (int64_t)gridDim.x * 4 * RPW) {
     const typename MM<DTI>::T* xr = x + row * ldx;
     float4 v[VPL];
     float s = 0.f;
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
-      const int u = lane + 64 * j;
+      const int u = ll + LPR * j;
       v[j] = u < U ? ln_load4<DTI>(xr + 4 * u) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
 #pragma unroll
     for (int j = 0; j < VPL; ++j) s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+    for (int o = LPR / 2; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
     const float mean = s / (float)D;
     float q = 0.f;
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
-      if (lane + 64 * j < U) {
+      if (ll + LPR * j < U) {
         const float a = v[j].x - mean, c = v[j].y - mean, d = v[j].z - mean, e = v[j].w - mean;
         q += (a * a + c * c) + (d * d + e * e);
       }
     }
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o, 64);
+    for (int o = LPR / 2; o > 0; o >>= 1) q += __shfl_xor(q, o, 64);
     const float rstd = 1.f / sqrtf(q / (float)D + eps);
     typename MM<DTO>::T* yr = y + row * ldy;
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
-      const int u = lane + 64 * j;
+      const int u = ll + LPR * j;
       if (u < U) {
         float4 t = make_float4((v[j].x - mean) * rstd, (v[j].y - mean) * rstd, (v[j].z - mean) * rstd,
                                (v[j].w - mean) * rstd);
@@ -2527,33 +2530,51 @@ static int ln_impl(const void* x, int64_t ldx, const float* w, const float* b, v
   const bool vec = D % 4 == 0 && D <= 1024 && ((uintptr_t)x % (4 * ies)) == 0 && ((uintptr_t)y % (4 * oes)) == 0 &&
                    (ldx * ies) % (4 * ies) == 0 && (ldy * oes) % (4 * oes) == 0 && ((uintptr_t)w % 16) == 0 &&
                    ((uintptr_t)b % 16) == 0;
-  const int vpl = D <= 256 ? 1 : D <= 512 ? 2 : 4;
+  // Rows of up to 128 units walked over more rows than one round of the grid covers (a device-side row count,
+  // or many rows): a half-wave per row (1 .. 4 units per lane), half the waves per row; otherwise a wave per row
+  // (up to 4 units per lane), which is faster when every row gets a wave of its own (measured: Level-1 step
+  // -1.5% with half-wave rows, the 1024- and 6272-row slot-attention LayerNorms +0.3 us each).
+  const int U = (int)(D / 4);
+  const bool half = U <= 128 && (ext.m_dev != nullptr || M > 8192);
+  const int vpl = half ? (U + 31) / 32 : (U + 63) / 64;
+  const unsigned hgrid = half ? (unsigned)((M + 7) / 8) : grid;
   // device row count: at most what the device holds at once (the vector kernel walks the rows); every
   // instantiation has the same occupancy, so one of each width stands for all element types
-  unsigned vgrid = grid;
+  unsigned vgrid = hgrid;
   if (vec && ext.m_dev) {
-    static std::atomic<int> cache[3][HCLSM_MAX_DEVICES];
-    const void* fn = vpl == 1 ? (const void*)layer_norm_vec_kernel<HCLSM_F32, HCLSM_BF16, 1>
-                   : vpl == 2 ? (const void*)layer_norm_vec_kernel<HCLSM_F32, HCLSM_BF16, 2>
-                              : (const void*)layer_norm_vec_kernel<HCLSM_F32, HCLSM_BF16, 4>;
+    static std::atomic<int> cache[8][HCLSM_MAX_DEVICES];
+    const void* fns[8] = {(const void*)layer_norm_vec_kernel<HCLSM_F32, HCLSM_BF16, 1, 64>,
+                          (const void*)layer_norm_vec_kernel<HCLSM_F32, HCLSM_BF16, 2, 64>,
+                          (const void*)layer_norm_vec_kernel<HCLSM_F32, HCLSM_BF16, 3, 64>,
+                          (const void*)layer_norm_vec_kernel<HCLSM_F32, HCLSM_BF16, 4, 64>,
+                          (const void*)layer_norm_vec_kernel<HCLSM_F32, HCLSM_BF16, 1, 32>,
+                          (const void*)layer_norm_vec_kernel<HCLSM_F32, HCLSM_BF16, 2, 32>,
+                          (const void*)layer_norm_vec_kernel<HCLSM_F32, HCLSM_BF16, 3, 32>,
+                          (const void*)layer_norm_vec_kernel<HCLSM_F32, HCLSM_BF16, 4, 32>};
+    const int fi = (half ? 4 : 0) + vpl - 1;
     int slots = 0;
-    if (device_launch_setup(fn, 256, 0, 0, cache[vpl >> 1], &slots) == 0 && slots > 0 && (unsigned)slots < grid)
+    if (device_launch_setup(fns[fi], 256, 0, 0, cache[fi], &slots) == 0 && slots > 0 && (unsigned)slots < hgrid)
       vgrid = (unsigned)slots;
   }
+#define HCLSM_LN_V(I, O, V, P)                                                                             \
+  hipLaunchKernelGGL((layer_norm_vec_kernel<I, O, V, P>), dim3(vgrid), dim3(256), 0, st, (const MM<I>::T*)x,   \
+                     ldx, w, b, (MM<O>::T*)y, ldy, M, (int)D, eps, ext, (MM<O>::T*)xc)
 #define HCLSM_LN(I, O)                                                                                     \
   if (in_dtype == I && out_dtype == O) {                                                                   \
-    if (vec && vpl == 1)                                                                                   \
-      hipLaunchKernelGGL((layer_norm_vec_kernel<I, O, 1>), dim3(vgrid), dim3(256), 0, st, (const MM<I>::T*)x, \
-                         ldx, w, b, (MM<O>::T*)y, ldy, M, (int)D, eps, ext, (MM<O>::T*)xc);               \
-    else if (vec && vpl == 2)                                                                              \
-      hipLaunchKernelGGL((layer_norm_vec_kernel<I, O, 2>), dim3(vgrid), dim3(256), 0, st, (const MM<I>::T*)x, \
-                         ldx, w, b, (MM<O>::T*)y, ldy, M, (int)D, eps, ext, (MM<O>::T*)xc);               \
-    else if (vec)                                                                                          \
-      hipLaunchKernelGGL((layer_norm_vec_kernel<I, O, 4>), dim3(vgrid), dim3(256), 0, st, (const MM<I>::T*)x, \
-                         ldx, w, b, (MM<O>::T*)y, ldy, M, (int)D, eps, ext, (MM<O>::T*)xc);               \
-    else                                                                                                   \
+    if (vec && half) {                                                                                     \
+      if (vpl == 1) HCLSM_LN_V(I, O, 1, 32);                                                               \
+      else if (vpl == 2) HCLSM_LN_V(I, O, 2, 32);                                                          \
+      else if (vpl == 3) HCLSM_LN_V(I, O, 3, 32);                                                          \
+      else HCLSM_LN_V(I, O, 4, 32);                                                                        \
+    } else if (vec) {                                                                                      \
+      if (vpl == 1) HCLSM_LN_V(I, O, 1, 64);                                                               \
+      else if (vpl == 2) HCLSM_LN_V(I, O, 2, 64);                                                          \
+      else if (vpl == 3) HCLSM_LN_V(I, O, 3, 64);                                                          \
+      else HCLSM_LN_V(I, O, 4, 64);                                                                        \
+    } else {                                                                                               \
       hipLaunchKernelGGL((layer_norm_kernel<I, O>), dim3(grid), dim3(256), 0, st, (const MM<I>::T*)x, ldx, w, \
                          b, (MM<O>::T*)y, ldy, M, (int)D, eps, ext);                                       \
+    }                                                                                                      \
     HCLSM_LAUNCH_CHECK();                                                                                  \
     if (xc && !vec) return convert_f32((const float*)x, xc, M * D, out_dtype, st);                         \
     return 0;                                                                                              \
@@ -2565,6 +2586,7 @@ static int ln_impl(const void* x, int64_t ldx, const float* w, const float* b, v
   HCLSM_LN(HCLSM_F32, HCLSM_F16)
   HCLSM_LN(HCLSM_F16, HCLSM_F16)
 #undef HCLSM_LN
+#undef HCLSM_LN_V
   return HCLSM_ERR_DTYPE;
 }
 

@@ -75,13 +75,20 @@ class SlotWeights:
 
     @classmethod
     def from_module(cls, m, dtype=torch.bfloat16) -> "SlotWeights":
-        """From a DynamicSlotAttention-shaped module (attribute names of dynamic_slots.py:47-82)."""
+        """From a DynamicSlotAttention-shaped module (attribute names of dynamic_slots.py:47-82); cached on the
+        module until a parameter changes (in place or replaced)."""
+        key = (dtype,) + tuple((p.data_ptr(), p._version) for p in m.parameters())
+        hit = getattr(m, "_hclsm_slot_weights", None)
+        if hit is not None and hit[0] == key:
+            return hit[1]
         w = dict(ln_pre_w=m.norm_pre_attn.weight, ln_pre_b=m.norm_pre_attn.bias, w_q=m.project_q.weight,
                  w_ih=m.gru.weight_ih, w_hh=m.gru.weight_hh, b_ih=m.gru.bias_ih, b_hh=m.gru.bias_hh,
                  ln_mlp_w=m.norm_slots.weight, ln_mlp_b=m.norm_slots.bias, w1=m.mlp[0].weight, b1=m.mlp[0].bias,
                  w2=m.mlp[2].weight, b2=m.mlp[2].bias, ln_in_w=m.norm_input.weight, ln_in_b=m.norm_input.bias,
                  w_k=m.project_k.weight, w_v=m.project_v.weight)
-        return cls.from_dict({k: v.detach() for k, v in w.items()}, dtype, m.project_q.weight.device)
+        W = cls.from_dict({k: v.detach() for k, v in w.items()}, dtype, m.project_q.weight.device)
+        m._hclsm_slot_weights = (key, W)
+        return W
 
 
 def _ln(x, ldx, M, D, w, b, out_dtype, stream, eps=1e-5):

@@ -314,20 +314,23 @@ def test_large_linear_wide_tiles_16bit_out(dtype):
 
 
 @pytest.mark.parametrize("D,pad", [(96, 0), (384, 0), (384, 4), (1000, 0), (1024, 0), (97, 0), (384, 1), (1030, 0),
-                                   (4, 0)])
+                                   (4, 0), (256, 0), (512, 0)])
 @pytest.mark.parametrize("io", [(torch.float32, torch.float32), (torch.float32, torch.bfloat16),
                                 (torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16)])
-def test_layer_norm_rows(D, pad, io):
-    """hclsm_layer_norm over row widths taking the vector kernel (D % 4 == 0, D <= 1024, aligned rows: one, two
-    or four 4-element units per lane) and the scalar one (odd widths, unaligned row strides, D > 1024), rows
-    with a large common offset, against the float64 LayerNorm."""
+@pytest.mark.parametrize("M", [37, 8203])
+def test_layer_norm_rows(D, pad, io, M):
+    """hclsm_layer_norm over row widths taking the vector kernel (D % 4 == 0, D <= 1024, aligned rows: one to four
+    4-element units per lane, a wave per row, or with more than 8192 rows and D <= 512 a half-wave per row, the
+    last wave half empty at an odd row count) and the scalar one (odd widths, unaligned row strides, D > 1024),
+    rows with a large common offset (20; 2 at 8203 rows, whose lowest-variance 4-wide rows lose more than 1e-5 to
+    the fp32 rounding of a mean near 20 in any fp32 LayerNorm), against the float64 LayerNorm."""
     from hclsm_amd.kernels import slot_iteration as si
     din, dout = io
-    g = torch.Generator().manual_seed(D + pad)
-    M, ldx = 37, D + pad
-    x = (torch.randn(M, ldx, generator=g) * 0.5 + 20.0).to(din)
+    g = torch.Generator().manual_seed(D + pad + M)
+    ldx = D + pad
+    x = (torch.randn(M, ldx, generator=g) * 0.5 + (20.0 if M < 1000 else 2.0)).to(din)
     w, b = torch.rand(D, generator=g) + 0.5, torch.randn(D, generator=g)
-    print(f"layer_norm D={D} pad={pad} io={io}", flush=True)
+    print(f"layer_norm M={M} D={D} pad={pad} io={io}", flush=True)
     y = si._ln(x.cuda(), ldx, M, D, w.cuda(), b.cuda(), dout, torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     want = sa.layer_norm(_np(x[:, :D]), _np(w), _np(b))
