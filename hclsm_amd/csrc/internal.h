@@ -95,7 +95,7 @@ int attn_slots_packed(const void* q, const void* k, const void* v, int64_t ldi, 
                       const int32_t* nseg_dev, int64_t cap, int64_t N, int H, int dh, const float* obj_mask,
                       const int32_t* seg_rows, float scale, int dtype, hipStream_t st);
 
-// Forward scan that also writes the backward's checkpoint slab ck ([batch][ceil(T / 8)][d_inner][16] fp32, the
+// Forward scan that also writes the backward's checkpoint slab ck ([batch][ceil(T / 8)][16][d_inner] fp32, the
 // state before steps 8, 16, ...; entry 0, the zero initial state, is not stored): the bf16, d_state 16
 // matrix-core kernel; HCLSM_ERR_UNSUPPORTED elsewhere.
 // mode: HCLSM_SCAN_RAW / _MODEL, or HCLSM_SCAN_BLOCK with gate (and optional y_pre).  Defined in ssm_scan.hip.

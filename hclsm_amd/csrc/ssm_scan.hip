@@ -26,7 +26,7 @@ constexpr int SCAN_BLOCK = HCLSM_SCAN_BLOCK;
 struct ScanEpi {
   const void* gate;   // [batch][T][d_inner], I/O type; required in SCAN_BLOCK
   void* y_pre;        // optional: the scan output before gating (kept for the backward)
-  float* ck;          // checkpointing launches only: [batch][ceil(T / 8)][d_inner][16] fp32, the state
+  float* ck;          // checkpointing launches only: [batch][ceil(T / 8)][16][d_inner] fp32, the state
                       // before steps 8, 16, ... (the backward's checkpoint slab; entry 0, the zero initial
                       // state, is not stored)
 };
@@ -450,7 +450,7 @@ static int launch_scan_sgpr(const void* x, const void* dt, const float* A_log, c
 // two 16x16x32 products per channel) issues fewer VALU instructions but ran
 // slower here, as did one barrier-synchronised workgroup per CU.
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
-typedef float f32x4v __attribute__((ext_vector_type(4)));
+typedef float f32x2v __attribute__((ext_vector_type(2)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 template <int MODE, int TC, int DPL, bool CK = false>
@@ -556,13 +556,17 @@ ssm_scan_fwd_mfma_kernel(const uint16_t* __restrict__ x, const uint16_t* __restr
   for (int k = 0; k < DPL; ++k) bop[k] = s16x4_t{0, 0, 0, 0};
   auto step = [&](int t, uint32_t xw, uint32_t dw_next, uint16_t bb, uint32_t gw) {
     if constexpr (CK) {   // the state before steps 8, 16, ..., for the backward (before step 0 it is zero)
+      // state-major slabs (state s of channel d at s * Dn + d): one store per state writes the wave's channels,
+      // whole lines
       if ((t & 7) == 0 && t > 0 && act) {
-        float* cp = epi.ck + (((size_t)n * ((T + 7) >> 3) + (t >> 3)) * Dn + d0) * SP;
+        float* cp = epi.ck + ((size_t)n * ((T + 7) >> 3) + (t >> 3)) * Dn * SP + d0;
 #pragma unroll
-        for (int k = 0; k < DPL; ++k)
-#pragma unroll
-          for (int s = 0; s < SP; s += 4)
-            *reinterpret_cast<f32x4v*>(cp + k * SP + s) = f32x4v{h[k][s], h[k][s + 1], h[k][s + 2], h[k][s + 3]};
+        for (int s = 0; s < SP; ++s) {
+          if constexpr (DPL == 2)
+            *reinterpret_cast<f32x2v*>(cp + (size_t)s * Dn) = f32x2v{h[0][s], h[1][s]};
+          else
+            cp[(size_t)s * Dn] = h[0][s];
+        }
       }
     }
     const int tn = t + 1 < T ? t + 1 : T - 1;

@@ -125,7 +125,7 @@ template <int N_, int MASK_LO> struct RSCount {  // values left per lane after R
 
 struct BwdArgs {
   int T, Dn, S, nchunk, nck, DW;   // nck = checkpoints per sequence = ceil(nchunk / BWD_CKR)
-  int64_t ld_ck;  // floats per (n, checkpoint) slab = Dn * SP
+  int64_t ld_ck;  // floats per (n, checkpoint) slab = Dn * SP, state-major: state s of channel d at s * Dn + d
   int have_ck;    // the checkpoints are already in ckpt (written by the forward): no pass 1
 };
 
@@ -223,7 +223,9 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
       dto[i] = buf_ld<DT>(rdt, vo, so);
     }
   };
-  float* ck = ckpt + (size_t)n * a.nck * a.ld_ck + (size_t)dd * SP + s0;
+  // this lane's states in the checkpoint slabs: state s0 + j of channel dd at (s0 + j) * Dn + dd, so that a wave's
+  // channels read and write whole lines
+  float* ck = ckpt + (size_t)n * a.nck * a.ld_ck + (size_t)s0 * Dn + dd;
 
   // ---- pass 1: forward recompute, checkpoint at every chunk start; the next chunk's x / dt are in
   // flight while a chunk is stepped (skipped when the forward wrote the checkpoints)
@@ -247,7 +249,7 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
       ld_chunk(c + 1, xn, dn);
       if (act && c % BWD_CKR == 0 && c > 0)   // (checkpoint 0 is the zero initial state: never stored)
 #pragma unroll
-        for (int j = 0; j < SG; ++j) ck[(size_t)(c / BWD_CKR) * a.ld_ck + j] = h[j];
+        for (int j = 0; j < SG; ++j) ck[(size_t)(c / BWD_CKR) * a.ld_ck + (size_t)j * Dn] = h[j];
 #pragma unroll
       for (int i = 0; i < K; ++i) {
         const float dtv = dt_of(dc[i], i < len);
@@ -274,7 +276,7 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
     const int w0 = t0 / BWD_WT * BWD_WT;
     float hc[SG], xs[K], ds[K], gs[K];
 #pragma unroll
-    for (int j = 0; j < SG; ++j) hc[j] = (act && c >= BWD_CKR) ? ck[(size_t)(c / BWD_CKR) * a.ld_ck + j] : 0.f;
+    for (int j = 0; j < SG; ++j) hc[j] = (act && c >= BWD_CKR) ? ck[(size_t)(c / BWD_CKR) * a.ld_ck + (size_t)j * Dn] : 0.f;
     ld_chunk(c, xs, ds);
 #pragma unroll
     for (int i = 0; i < K; ++i) {
