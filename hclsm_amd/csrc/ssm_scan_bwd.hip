@@ -384,7 +384,7 @@ ssm_scan_bwd_kernel(const typename Elem<DT>::T* __restrict__ x, const typename E
   }
   if (act) {
 #pragma unroll
-    for (int j = 0; j < SG; ++j) gA_part[((size_t)n * Dn + d) * SP + s0 + j] = gA[j];
+    for (int j = 0; j < SG; ++j) gA_part[((size_t)n * SP + s0 + j) * Dn + d] = gA[j];   // state-major: whole lines
     if (gi == 0) gD_part[(size_t)n * Dn + d] = gD;
   }
 }
@@ -419,8 +419,8 @@ ssm_scan_bwd_tail(const float* __restrict__ ga_part, const float* __restrict__ g
       float t = 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) t += red[r][c];
-      if (is_a) {
-        const int64_t dd = col / SP, s = col - dd * SP;
+      if (is_a) {   // the gA partials are state-major: column s * Dn + d
+        const int64_t s = col / Dn, dd = col - s * Dn;
         if (s < S) {   // (padded states carry no gradient)
           const int64_t i = dd * S + s;
           const float e = expf(A_log[i]);
