@@ -16,6 +16,7 @@ import torch  # noqa: F401  (must precede the CDLL load, see module docstring)
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libhclsm_amd.so"
 
 F32, BF16, F16, U8 = 0, 1, 2, 3
+ABI_VERSION = 2   # HCLSM_ABI_VERSION of include/hclsm_amd.h that these bindings (struct layouts) follow
 SCAN_RAW, SCAN_MODEL, SCAN_BLOCK = 0, 1, 2
 ERR_UNSUPPORTED = -4   # HCLSM_ERR_UNSUPPORTED: valid arguments the entry point does not implement
 EVENT_GT_HALF, EVENT_NONZERO = 0, 1
@@ -121,6 +122,10 @@ def lib() -> ctypes.CDLL:
             fn = getattr(handle, name)
             fn.argtypes = argtypes
             fn.restype = _RESTYPES.get(name, _int)
+        got = handle.hclsm_abi_version()
+        if got != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH} has ABI version {got}, these bindings expect {ABI_VERSION}: rebuild it "
+                               "(python -m hclsm_amd.build)")
         _lib = handle
     return _lib
 

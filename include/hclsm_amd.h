@@ -25,7 +25,8 @@
 extern "C" {
 #endif
 
-#define HCLSM_ABI_VERSION 1
+/* 2: HclsmSlotWeights gained w_qkv (a caller built against version 1 passes a shorter struct and must be rebuilt) */
+#define HCLSM_ABI_VERSION 2
 
 /* element types of floating-point tensors */
 #define HCLSM_F32  0

@@ -50,7 +50,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 def test_version_and_strerror(lib):
     from hclsm_amd import _lib
-    assert lib.hclsm_abi_version() == 1
+    assert lib.hclsm_abi_version() == _lib.ABI_VERSION == 2
     for code in (0, -1, -2, -3, -4, -5, -6):
         assert _lib.strerror(code)
     assert "unknown" in _lib.strerror(-999)
@@ -162,6 +162,27 @@ def test_noalloc_forward_rejects_oversized_shapes_before_launch(lib):
     assert need > (64 << 20)
     assert f(None, None, 384, None, None, 512, 32, 196, 384, 768, 3, 0.05, 0.0, 1e-8, 0.0, 1, None) == -6
     assert f(None, None, 384, None, None, -1, 32, 196, 384, 768, 3, 0.05, 0.0, 1e-8, 0.0, 1, None) == -2
+
+
+def test_slot_keys_offsets(lib):
+    """hclsm_slot_attention_k_offset / _kq_offset (host arithmetic, no launch): kq is formed only by 16-bit
+    forwards whose iterations take the fused core (slot widths 128, 192, 256, 384, up to 32 slots), elsewhere
+    HCLSM_ERR_UNSUPPORTED; both offsets sit inside the workspace and apart from each other; bad shapes and dtypes
+    are rejected."""
+    from hclsm_amd import _lib
+    args = (32, 32, 196, 384, 384, 768)
+    ws = lib.hclsm_slot_attention_workspace(*args, _lib.BF16)
+    k_off = lib.hclsm_slot_attention_k_offset(*args, _lib.BF16)
+    kq_off = lib.hclsm_slot_attention_kq_offset(*args, _lib.BF16)
+    nb = 32 * 196 * 384 * 2
+    assert 0 <= k_off and 0 <= kq_off and max(k_off, kq_off) + nb <= ws and abs(kq_off - k_off) >= nb
+    assert lib.hclsm_slot_attention_kq_offset(*args, _lib.F16) >= 0
+    assert lib.hclsm_slot_attention_kq_offset(*args, _lib.F32) == -4           # fp32 keeps the q projection
+    assert lib.hclsm_slot_attention_kq_offset(32, 0, 196, 384, 384, 768, _lib.BF16) == -4   # no slots
+    assert lib.hclsm_slot_attention_kq_offset(32, 33, 196, 384, 384, 768, _lib.BF16) == -4  # > 32 slots
+    assert lib.hclsm_slot_attention_kq_offset(2, 8, 40, 64, 64, 256, _lib.BF16) == -4       # width 64
+    assert lib.hclsm_slot_attention_kq_offset(-1, 8, 40, 384, 384, 768, _lib.BF16) == -2
+    assert lib.hclsm_slot_attention_kq_offset(2, 8, 40, 384, 384, 768, 9) == -3
 
 
 def test_scan_checkpoint_pair_argument_errors_before_launch(lib):

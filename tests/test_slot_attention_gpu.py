@@ -338,10 +338,11 @@ def test_layer_norm_rows(D, pad, io, M):
     assert normwise_rel_err(_np(y), want) <= tol
 
 
-def test_forward_rejects_misaligned_weights_before_any_launch():
-    """16-bit weights are read with 16-byte loads; a weight pointer off that alignment (here W_hh moved by one
-    element through the C ABI) is rejected with HCLSM_ERR_UNSUPPORTED before any launch: the output buffer keeps
-    its contents."""
+@pytest.mark.parametrize("name", ["w_hh", "w_qkv"])
+def test_forward_rejects_misaligned_weights_before_any_launch(name):
+    """16-bit weights are read with 16-byte loads; a weight pointer off that alignment (W_hh, or the optional
+    [W_q^T W_k; W_v], moved by one element through the C ABI) is rejected with HCLSM_ERR_UNSUPPORTED before any
+    launch: the output buffer keeps its contents."""
     import ctypes
     from hclsm_amd import _lib
     from hclsm_amd.kernels import slot_iteration as si
@@ -349,10 +350,11 @@ def test_forward_rejects_misaligned_weights_before_any_launch():
     tokens, slots0, w = slot_config(B=2, M=24, N=8)
     W = si.SlotWeights.from_dict(w, torch.bfloat16)
     d = W.d
-    whh = torch.empty(W.t["w_hh"].numel() + 8, dtype=torch.bfloat16, device="cuda")
-    whh[1:1 + W.t["w_hh"].numel()].copy_(W.t["w_hh"].reshape(-1))
+    wt = W.t[name]
+    shifted = torch.empty(wt.numel() + 8, dtype=torch.bfloat16, device="cuda")
+    shifted[1:1 + wt.numel()].copy_(wt.reshape(-1))
     st = si._struct(W)
-    st.w_hh = whh.data_ptr() + 2                                  # 2 bytes past a 16-byte boundary
+    setattr(st, name, shifted.data_ptr() + 2)                     # 2 bytes past a 16-byte boundary
     L = _lib.lib()
     x, s0 = tokens.cuda().contiguous(), slots0.cuda().contiguous()
     out = torch.full_like(s0, 7.0)
