@@ -85,15 +85,23 @@ int layer_norm_rows(const void* x, int64_t ldx, const float* w, const float* b, 
                     int64_t D, float eps, int in_dtype, int out_dtype, const int32_t* m_dev, int64_t m_mul,
                     hipStream_t st);
 
-// Attention among the N rows of each of cap uniform segments (the first *nseg_dev live): rows p*N + i
-// of q / k / v (row stride ldi) and out (row stride ldo), H heads of dh columns; key j of segment p is
-// excluded when obj_mask[seg_rows[p] * N + j] <= 0.5 (obj_mask nullable).  Defined in event_attn.hip.
 // event_count_kernel over a [B, T] mask: counts[b] = events of row b (events.hip).
 int event_counts(const void* mask, int mdt, int64_t B, int64_t T, int rule, int32_t* counts, hipStream_t st);
 
+// Attention among the N rows of each of cap uniform segments (the first *nseg_dev live): rows p*N + i
+// of q / k / v (row stride ldi) and out (row stride ldo), H heads of dh columns; key j of segment p is
+// excluded when obj_mask[seg_rows[p] * N + j] <= 0.5 (obj_mask nullable).  Defined in event_attn.hip.
 int attn_slots_packed(const void* q, const void* k, const void* v, int64_t ldi, void* out, int64_t ldo,
                       const int32_t* nseg_dev, int64_t cap, int64_t N, int H, int dh, const float* obj_mask,
                       const int32_t* seg_rows, float scale, int dtype, hipStream_t st);
+
+// Level-1 QKV projection and slot attention in one launch: o[e*32 + i, h*64 ..] = attention of event e's 32 rows
+// (head h, keys excluded as attn_slots_packed) over q | k | v = x . w^T (w = in_proj [3d, d], x / o row stride d),
+// for the first *n_events of capacity events.  HCLSM_ERR_UNSUPPORTED unless 16-bit, N = 32, dh = 64, d = 64 H,
+// 16-byte aligned x / w / o; the caller then runs the GEMM and attn_slots_packed.  Defined in slot_attn.hip.
+int qkv_attn_rows(const void* x, const void* w, void* o, const int32_t* n_events, int64_t capacity, int64_t N,
+                  int64_t d, int H, int dh, const float* obj_mask, const int32_t* ev_rows, float scale, int dtype,
+                  hipStream_t st);
 
 // Forward scan that also writes the backward's checkpoint slab ck ([batch][ceil(T / 8)][16][d_inner] fp32, the
 // state before steps 8, 16, ...; entry 0, the zero initial state, is not stored): the bf16, d_state 16

@@ -9,6 +9,7 @@
 //     xn  = LN1(x)                                        (operand dtype)
 //     qkv = xn . in_proj^T
 //     o   = softmax(q k^T / sqrt(dh), keys of dead slots excluded) v, per event and head   :49-51
+//           (16-bit, 32 slots, 64-wide heads: both in one launch, q / k / v kept on chip: qkv_attn_rows)
 //     x  += o . out_proj^T                                (residual in the GEMM epilogue)
 //     xn  = LN2(x)
 //     g   = silu(xn . w1^T) * (xn . w3^T)                 (one GEMM over interleaved w1 / w3 rows whose
@@ -108,9 +109,16 @@ extern "C" int hclsm_level1_forward(const void* ev, int ev_dtype, void* out, int
   for (int64_t l = 0; l < n_layers; ++l) {
     const int64_t b = 4 + 9 * l;   // ln1_w, ln1_b, in_proj, out_proj, ln2_w, ln2_b, w1, w3, w2
     HCLSM_TRY(norm(Pf(b), Pf(b + 1)));
-    HCLSM_TRY(gemm(xn, dtype, P(b + 2), 3 * dm, dm, nullptr, qkv, dtype, nullptr));
-    HCLSM_TRY(attn_slots_packed(qkv, qkv + dm * es, qkv + 2 * dm * es, 3 * dm, o, dm, n_events, capacity, N,
-                                (int)n_heads, (int)dh, obj_mask, ev_rows, scale, dtype, st));
+    // o = attention over q | k | v = xn . in_proj^T: one fused launch (q / k / v stay on chip) where it applies
+    rc = qkv_attn_rows(xn, P(b + 2), o, n_events, capacity, N, dm, (int)n_heads, (int)dh, obj_mask, ev_rows, scale,
+                       dtype, st);
+    if (rc == HCLSM_ERR_UNSUPPORTED) {
+      HCLSM_TRY(gemm(xn, dtype, P(b + 2), 3 * dm, dm, nullptr, qkv, dtype, nullptr));
+      HCLSM_TRY(attn_slots_packed(qkv, qkv + dm * es, qkv + 2 * dm * es, 3 * dm, o, dm, n_events, capacity, N,
+                                  (int)n_heads, (int)dh, obj_mask, ev_rows, scale, dtype, st));
+    } else if (rc) {
+      return rc;
+    }
     HCLSM_TRY(gemm(o, dtype, P(b + 3), dm, dm, x, x, HCLSM_F32, nullptr));
     HCLSM_TRY(norm(Pf(b + 4), Pf(b + 5)));
     // g = silu(xn . w1^T) * (xn . w3^T): one paired GEMM, or two GEMMs through h1 where it does not apply

@@ -753,6 +753,217 @@ linear_dma_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const t
   }
 }
 
+// Level-1 QKV projection and slot attention of one head in one launch (level1_event.py:37-52 for N = 32 slots and
+// 64-wide heads, 16-bit operands).  Workgroup = (block of 128 rows = 4 events, head h); wave w owns event 4 b + w:
+//   GEMM  its 32 rows x the head's 192 projection columns (q_h, k_h, v_h: rows h*64.., d + h*64.., 2d + h*64.. of
+//         in_proj) over K = d_model, X and W chunks loaded straight into LDS as in linear_dma_kernel (two 40 KB
+//         stages, one barrier per chunk);
+//   attention  S^T = K Q^T and O^T = V^T P^T on v_mfma_f32_16x16x16 with the online softmax of event_attn_kernel
+//         (mode 2: keys of dead slots excluded through obj_mask[ev_rows[e]], a query with every key excluded gives
+//         NaN).  The GEMM accumulators hold row li, columns 4g .. 4g+3 of each 16-column block: for q and k that is
+//         exactly the 16x16x16 operand layout (lane group g supplies head dims 16c + 4g .. +3 of MFMA c), so they
+//         become operands by a rounding to the 16-bit type (the rounding the unfused QKV output takes); V is
+//         transposed through LDS.
+// q / k / v never reach HBM.  Output rows e*32 + i, columns h*64 .. h*64+63 of O (row stride ldo).
+constexpr int QA_KC = 64;
+constexpr int QA_VP = 72;   // LDS pitch of a wave's V rows (elements)
+
+template <int DT>
+__device__ __forceinline__ float qa_out(float acc, float inv) {
+  float y = acc * inv;
+  asm volatile("" : "+v"(y));   // as event_attn_kernel: the product rounded on its own, then converted
+  return y;
+}
+
+template <int DT>
+__global__ void __launch_bounds__(256, 2)
+qkv_attn_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const typename MM<DT>::T* __restrict__ W,
+                typename MM<DT>::T* __restrict__ O, int64_t ldo, const int32_t* __restrict__ n_events, int64_t cap_rows,
+                int64_t d, int H, const float* __restrict__ obj_mask, const int32_t* __restrict__ ev_rows,
+                float scale_log2) {
+  using A = MM<DT>;
+  using T = typename A::T;
+  typedef short s16x4v __attribute__((ext_vector_type(4)));
+  typedef _Float16 f16x4v __attribute__((ext_vector_type(4)));
+  constexpr int CPR = QA_KC / 8;          // 16-byte chunks per row and chunk of K
+  constexpr int XB = 128 * CPR * 16;      // X bytes per stage (16 KB)
+  constexpr int WB = 192 * CPR * 16;      // W bytes per stage (24 KB)
+  __shared__ __align__(16) unsigned char smem[2 * (XB + WB)];
+  static_assert(4 * 32 * QA_VP * 2 <= sizeof(smem), "V rows fit the stages");
+  const int64_t tile = xcd_rowblock_tile(blockIdx.x, H, gridDim.x);
+  const int64_t rb = tile / H;
+  const int h = (int)(tile - rb * H);
+  int64_t M = (int64_t)(*n_events) * 32;
+  M = M < cap_rows ? M : cap_rows;
+  if (rb * 128 >= M) return;   // the whole workgroup, before any barrier
+  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, g = lane >> 4, li = lane & 15;
+  const int wu = __builtin_amdgcn_readfirstlane(wid);
+  const int nk = (int)(d / QA_KC);
+  // load maps (as linear_dma_kernel): unit u = 256 i + tid is LDS slot u (row u / 8, slot u % 8), which holds the
+  // row's chunk (u % 8) ^ (row & 7); X rows past M repeat the last row (their outputs are not stored)
+  const T* pa[4];
+  const T* pb[6];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int u = 256 * i + tid, r = u / CPR, c = (u % CPR) ^ (r & (CPR - 1));
+    int64_t ra = rb * 128 + r;
+    ra = ra < M ? ra : M - 1;
+    pa[i] = X + ra * ldx + 8 * c;
+  }
+#pragma unroll
+  for (int i = 0; i < 6; ++i) {
+    const int u = 256 * i + tid, r = u / CPR, c = (u % CPR) ^ (r & (CPR - 1));
+    const int64_t wr = (int64_t)(r >> 6) * d + (int64_t)h * 64 + (r & 63);   // q, k or v row of head h
+    pb[i] = W + wr * d + 8 * c;
+  }
+  auto request = [&](int kc) {
+    unsigned char* st = smem + (kc & 1) * (XB + WB);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_global_load_lds((const void*)(pa[i] + (int64_t)kc * QA_KC),
+                                       (lds_void_t*)(st + (256 * i + 64 * wu) * 16), 16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 6; ++i)
+      __builtin_amdgcn_global_load_lds((const void*)(pb[i] + (int64_t)kc * QA_KC),
+                                       (lds_void_t*)(st + XB + (256 * i + 64 * wu) * 16), 16, 0, 0);
+  };
+  f32x4 acc[2][12];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int j = 0; j < 12; ++j) acc[t][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  request(0);
+  for (int kc = 0; kc < nk; ++kc) {
+    wait_vmcnt<0>();   // this lane's part of chunk kc is in LDS
+    __syncthreads();   // every lane's, and chunk kc - 1 is consumed by every wave
+    if (kc + 1 < nk) request(kc + 1);
+    const T* Xs = reinterpret_cast<const T*>(smem + (kc & 1) * (XB + WB));
+    const T* Ws = reinterpret_cast<const T*>(smem + (kc & 1) * (XB + WB) + XB);
+#pragma unroll
+    for (int s = 0; s < QA_KC / 32; ++s) {
+      const int c = 4 * s + g;
+      typename A::Op a[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int ra = 32 * wid + 16 * t + li;
+        a[t] = A::load(Xs + (ra * CPR + (c ^ (ra & (CPR - 1)))) * 8);
+      }
+#pragma unroll
+      for (int j = 0; j < 12; ++j) {
+        const int rw = 16 * j + li;
+        const typename A::Op b = A::load(Ws + (rw * CPR + (c ^ (rw & (CPR - 1)))) * 8);
+        // weights as the A operand: acc[t][j][r] = out[row 16 t + li][col 16 j + 4 g + r]
+#pragma unroll
+        for (int t = 0; t < 2; ++t) acc[t][j] = A::mfma(b, a[t], acc[t][j]);
+      }
+    }
+  }
+  __syncthreads();   // every wave is done with the stages: they take the V rows now
+  // this wave's event; q / k as 16x16x16 operands (dims 16 c + 4 g .. +3 of row 16 t + li), V to LDS
+  const int64_t e = rb * 4 + wid;
+  const bool live = e * 32 < M;
+  s16x4v qo[2][4], ko[2][4];
+  T* sv = reinterpret_cast<T*>(smem) + wid * 32 * QA_VP;
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        qo[t][c][r] = __builtin_bit_cast(short, A::fromf(acc[t][c][r]));   // the element's bits
+        ko[t][c][r] = __builtin_bit_cast(short, A::fromf(acc[t][4 + c][r]));
+      }
+      T vv[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) vv[r] = A::fromf(acc[t][8 + c][r]);
+      *reinterpret_cast<uint2*>(sv + (16 * t + li) * QA_VP + 16 * c + 4 * g) = *reinterpret_cast<const uint2*>(vv);
+    }
+  __syncthreads();   // (a wave reads only its own V rows; the barrier orders the LDS stores before the reads)
+  if (!live) return;
+  const float* om = obj_mask ? obj_mask + (int64_t)ev_rows[e] * 32 : nullptr;
+  bool kok[2][4];
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) kok[kt][r] = om == nullptr || om[16 * kt + 4 * g + r] > 0.5f;
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    float m = -INFINITY, l = 0.f;
+    float oacc[4][4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) oacc[r][nt] = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      // V operand: keys 16 kt + 4 g + r, head columns 4 li .. 4 li + 3
+      T ve[4][4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        *reinterpret_cast<uint2*>(ve[r]) = *reinterpret_cast<const uint2*>(sv + (16 * kt + 4 * g + r) * QA_VP + 4 * li);
+      f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if constexpr (DT == HCLSM_BF16)
+          s4 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ko[kt][c], qo[qt][c], s4, 0, 0, 0);
+        else
+          s4 = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4v, ko[kt][c]),
+                                                     __builtin_bit_cast(f16x4v, qo[qt][c]), s4, 0, 0, 0);
+      }
+      // s4[r] = S[query 16 qt + li][key 16 kt + 4 g + r]
+      float sc[4];
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        sc[r] = kok[kt][r] ? s4[r] * scale_log2 : -INFINITY;
+        tmax = fmaxf(tmax, sc[r]);
+      }
+      tmax = rows4_max(tmax);
+      const float m_new = fmaxf(m, tmax);
+      float pr[4], psum = 0.f;
+      float alpha = 1.f;
+      if (m_new != -INFINITY) {
+        alpha = fast_exp2(m - m_new);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) { pr[r] = fast_exp2(sc[r] - m_new); psum += pr[r]; }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pr[r] = 0.f;
+      }
+      psum = rows4_sum(psum);
+      l = l * alpha + psum;
+      m = m_new;
+      s16x4v pb4;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) pb4[r] = __builtin_bit_cast(short, A::fromf(pr[r]));
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        f32x4 o4 = {oacc[0][nt] * alpha, oacc[1][nt] * alpha, oacc[2][nt] * alpha, oacc[3][nt] * alpha};
+        s16x4v av;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) av[r] = __builtin_bit_cast(short, ve[r][nt]);
+        if constexpr (DT == HCLSM_BF16)
+          o4 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, pb4, o4, 0, 0, 0);
+        else
+          o4 = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4v, av), __builtin_bit_cast(f16x4v, pb4),
+                                                     o4, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) oacc[r][nt] = o4[r];
+      }
+    }
+    // O[query 16 qt + li][dims 16 g + 4 r + nt]; l == 0 (every key excluded) -> NaN, as softmax over all -inf
+    const float inv = 1.f / l;
+    T ov[16];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) ov[4 * r + nt] = A::fromf(qa_out<DT>(oacc[r][nt], inv));
+    T* dst = O + (e * 32 + 16 * qt + li) * ldo + (int64_t)h * 64 + 16 * g;
+    *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(ov);
+    *reinterpret_cast<uint4*>(dst + 8) = *reinterpret_cast<const uint4*>(ov + 8);
+  }
+}
+
 // fp32 operands: the same 64x64 tile with A and W rows staged in LDS in K chunks of 64 floats (the next
 // chunk in flight), each wave a 32x32 quadrant of v_mfma_f32_16x16x4_f32.  The contraction is permuted
 // so that a lane's operands are float4 reads: in a 16-wide k block, lane group g owns k = 4g .. 4g+3 and
@@ -2283,6 +2494,28 @@ int linear_rows(const void* x, int64_t ldx, int x_dtype, const void* w, int64_t 
 // SwiGLU input layer Y[M, H] = silu(X . w1^T) * (X . w3^T) as one GEMM over 2H interleaved columns (w_row) on
 // the LDS kernels (HCLSM_ERR_UNSUPPORTED for shapes or alignments they do not take: the caller runs two GEMMs).
 // Declared in internal.h.
+int qkv_attn_rows(const void* x, const void* w, void* o, const int32_t* n_events, int64_t capacity, int64_t N,
+                  int64_t d, int H, int dh, const float* obj_mask, const int32_t* ev_rows, float scale, int dtype,
+                  hipStream_t st) {
+  if ((dtype != HCLSM_BF16 && dtype != HCLSM_F16) || N != 32 || dh != 64 || H <= 0 || d != (int64_t)H * 64 ||
+      d % QA_KC || !al16(x) || !al16(w) || !al16(o))
+    return HCLSM_ERR_UNSUPPORTED;
+  if (capacity <= 0) return 0;
+  if (!n_events || (obj_mask && !ev_rows)) return HCLSM_ERR_NULL;
+  const int64_t rows = capacity * 32;
+  const int64_t grid = (rows + 127) / 128 * H;
+  if (grid > 0x7fffffffLL) return HCLSM_ERR_SHAPE;
+  const float sl2 = scale * HCLSM_LOG2E;
+  if (dtype == HCLSM_BF16)
+    hipLaunchKernelGGL(qkv_attn_kernel<HCLSM_BF16>, dim3((unsigned)grid), dim3(256), 0, st, (const uint16_t*)x, d,
+                       (const uint16_t*)w, (uint16_t*)o, d, n_events, rows, d, H, obj_mask, ev_rows, sl2);
+  else
+    hipLaunchKernelGGL(qkv_attn_kernel<HCLSM_F16>, dim3((unsigned)grid), dim3(256), 0, st, (const _Float16*)x, d,
+                       (const _Float16*)w, (_Float16*)o, d, n_events, rows, d, H, obj_mask, ev_rows, sl2);
+  HCLSM_LAUNCH_CHECK();
+  return 0;
+}
+
 int linear_glu_rows(const void* x, int64_t ldx, int x_dtype, const void* w1, const void* w3, int64_t ldw, void* y,
                     int64_t ldy, int y_dtype, int64_t M, int64_t H, int64_t K, const int32_t* m_dev, int64_t m_mul,
                     int dtype, hipStream_t st) {

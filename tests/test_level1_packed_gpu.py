@@ -109,6 +109,31 @@ def test_level1_packed_bf16_autocast_wide_tiles():
     assert normwise_rel_err(_np(got), np.stack([ref[b, k] for b, k in bk])) <= 2e-2
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_level1_fused_qkv_attention_32_slots(dtype):
+    """32 slots per event and 64-wide heads with 16-bit operands: the QKV projection and the slot attention run as
+    one launch (q / k / v never leave the chip).  Against the oracle at the 16-bit bar, with a clip whose slots
+    are all dead (its events' rows NaN, as softmax over all -inf), dead slots elsewhere, and a capacity whose
+    128-row blocks are partly live."""
+    from hclsm_amd.kernels.level1_packed import Level1Weights, level1_forward_packed
+    hm, l1 = _modules(21)
+    states, mask, obj = _case(5, 9, 32, 21, p=0.45)
+    obj[2] = 0.0
+    mask[2, 0] = 1.0
+    with torch.no_grad():
+        ev, idx = hm.gather_events_packed(states, mask)
+        out = level1_forward_packed(ev, idx, obj, Level1Weights.from_module(l1, dtype))
+        ev_pad, pad, K = hm.gather_events(states, mask)
+    ref = om.level1_ref(_np(ev_pad), _np(pad), _np(obj), _sd(l1), L1.n_layers, L1.n_heads)
+    got, bk = _live_rows(out, idx)
+    assert len(bk) % 4 != 0 and ev.shape[0] * 32 % 128 != 0
+    dead = torch.tensor([b == 2 for b, _ in bk], device="cuda")
+    assert bool(dead.any()) and torch.isnan(got[dead]).all() and torch.isfinite(got[~dead]).all()
+    keep = [i for i, (b, _) in enumerate(bk) if b != 2]
+    want = np.stack([ref[b, k] for b, k in bk if b != 2])
+    assert normwise_rel_err(_np(got[keep]), want) <= 2e-2
+
+
 def test_level1_packed_all_slots_dead_gives_nan_like_softmax():
     """An event whose slots are all dead: every key excluded, softmax over all -inf -> NaN rows, as
     nn.MultiheadAttention gives; other rows unaffected."""
