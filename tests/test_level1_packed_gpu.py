@@ -134,6 +134,22 @@ def test_level1_fused_qkv_attention_32_slots(dtype):
     assert normwise_rel_err(_np(got[keep]), want) <= 2e-2
 
 
+def test_level1_padded_forward_bf16_fused_attention():
+    """The reference-shaped padded call (Level1EventDynamics.forward over (B, K_max, N, d_slot), level1_event.py:85-133)
+    under a bf16 autocast with 32 slots: the dense event index feeds the fused QKV projection + slot attention
+    (key padding through obj_mask of each event's clip).  Against the oracle at the bf16 bar, padded events zero."""
+    hm, l1 = _modules(23)
+    states, mask, obj = _case(3, 11, 32, 23, p=0.4)
+    with torch.no_grad():
+        ev_pad, pad, K = hm.gather_events(states, mask)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            out = l1(ev_pad, pad, obj)
+    ref = om.level1_ref(_np(ev_pad), _np(pad), _np(obj), _sd(l1), L1.n_layers, L1.n_heads)
+    real = _np(pad) > 0.5
+    assert normwise_rel_err(_np(out.float())[real], ref[real]) <= 2e-2
+    assert bool((out.float()[~torch.as_tensor(real, device="cuda")] == 0).all())
+
+
 def test_level1_packed_all_slots_dead_gives_nan_like_softmax():
     """An event whose slots are all dead: every key excluded, softmax over all -inf -> NaN rows, as
     nn.MultiheadAttention gives; other rows unaffected."""
