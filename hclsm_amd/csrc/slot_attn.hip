@@ -2501,7 +2501,7 @@ int qkv_attn_rows(const void* x, const void* w, void* o, const int32_t* n_events
       d % QA_KC || !al16(x) || !al16(w) || !al16(o))
     return HCLSM_ERR_UNSUPPORTED;
   if (capacity <= 0) return 0;
-  if (!n_events || (obj_mask && !ev_rows)) return HCLSM_ERR_NULL;
+  if (!x || !w || !o || !n_events || (obj_mask && !ev_rows)) return HCLSM_ERR_NULL;
   const int64_t rows = capacity * 32;
   const int64_t grid = (rows + 127) / 128 * H;
   if (grid > 0x7fffffffLL) return HCLSM_ERR_SHAPE;
