@@ -16,7 +16,7 @@ import torch  # noqa: F401  (must precede the CDLL load, see module docstring)
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libhclsm_amd.so"
 
 F32, BF16, F16, U8 = 0, 1, 2, 3
-ABI_VERSION = 2   # HCLSM_ABI_VERSION of include/hclsm_amd.h that these bindings (struct layouts) follow
+ABI_VERSION = 3   # HCLSM_ABI_VERSION of include/hclsm_amd.h that these bindings (struct layouts) follow
 SCAN_RAW, SCAN_MODEL, SCAN_BLOCK = 0, 1, 2
 ERR_UNSUPPORTED = -4   # HCLSM_ERR_UNSUPPORTED: valid arguments the entry point does not implement
 EVENT_GT_HALF, EVENT_NONZERO = 0, 1
@@ -100,7 +100,8 @@ class HclsmSlotWeights(ctypes.Structure):
     """Mirror of the C struct HclsmSlotWeights (include/hclsm_amd.h)."""
     _fields_ = [(n, ctypes.c_void_p) for n in (
         "w_q", "w_kv", "w_ih", "w_hh", "w1", "w2", "b_ih", "b_hh", "b1", "b2",
-        "ln_in_w", "ln_in_b", "ln_pre_w", "ln_pre_b", "ln_mlp_w", "ln_mlp_b", "w_qt", "w_qkv")]
+        "ln_in_w", "ln_in_b", "ln_pre_w", "ln_pre_b", "ln_mlp_w", "ln_mlp_b", "w_qt", "w_qkv",
+        "w1_n", "w1_n_sum", "w1_n_bias")]
 
 _lib = None
 

@@ -1236,20 +1236,28 @@ linear_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>::T* _
 // registers (mean, then the centred sum of squares: two passes, two barriers) and the operands are
 // normalised in place: LN(X) W^T with no separate LayerNorm launch.  xout (nullable): the workgroups
 // of column tile 0 also store X rounded to DT.
-template <int DT, int OT, typename XT, bool LN, int KB>
+// FOLD: LayerNorm folded into the weights instead.  With W = W0 diag(gamma) (rounded to DT), fsum[n] = the sum of
+// row n of W (its rounded entries, in fp32) and bias = W0 beta (+ the layer's bias),
+//   LN(x) W0^T + b = rstd (x W^T - mean fsum) + bias,
+// so the operands go to the MFMAs as loaded and the row statistics (two passes over the same registers, while the
+// products run) enter only the epilogue.  x (16-bit) is exact as given, and x W^T - mean fsum is the sum of
+// (x - mean) W over the rounded entries, so nothing cancels beyond the fp32 accumulation.
+template <int DT, int OT, typename XT, bool LN, int KB, bool FOLD = false>
 __global__ void __launch_bounds__(256)
 linear_kreg_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>::T* __restrict__ W, int64_t ldw,
                    const float* __restrict__ bias, const float* __restrict__ resid, int64_t ldr,
                    typename MM<OT>::T* __restrict__ Y, int64_t ldy, typename MM<DT>::T* __restrict__ Y2,
                    int64_t ldy2, int64_t M, int64_t N, int64_t K, int relu, float clamp_v,
                    const float* __restrict__ lnw, const float* __restrict__ lnb, float ln_eps,
-                   typename MM<DT>::T* __restrict__ xout, int64_t ldxo) {
+                   typename MM<DT>::T* __restrict__ xout, int64_t ldxo, const float* __restrict__ fsum) {
   using A = MM<DT>;
   constexpr int KPL = A::KPL;
   constexpr int BLK = 4 * KPL;
   static_assert(KPL == 8, "16-bit operands");
+  static_assert(!(LN && FOLD), "one LayerNorm form");
   __shared__ float red[4][2][2][4][64];   // 16 KB
   __shared__ float stat[2][4][2][16];     // [pass][wave][row tile][li]
+  __shared__ float2 fstat[FOLD ? 4 : 1][2][16];   // FOLD: (mean, centred sum of squares) [wave][row tile][li]
   const int64_t tiles_n = (N + 31) / 32;
   const int64_t tm = blockIdx.x / tiles_n, tn = blockIdx.x - tm * tiles_n;
   const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, g = lane >> 4, li = lane & 15;
@@ -1269,9 +1277,10 @@ linear_kreg_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>:
   // latency overlaps the operand loads instead of following the reduction
   const int ti = wid >> 1, tj = wid & 1;
   const int64_t col = tn * 32 + 16 * tj + li;
-  float bv = 0.f, rv[4] = {0.f, 0.f, 0.f, 0.f};
+  float bv = 0.f, rv[4] = {0.f, 0.f, 0.f, 0.f}, fs = 0.f;
   if (col < N) {
     if (bias) bv = bias[col];
+    if constexpr (FOLD) fs = fsum[col];
     if (resid) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -1379,6 +1388,43 @@ linear_kreg_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>:
     acc[1][0] = A::mfma(a[1], bo[i][0], acc[1][0]);
     acc[1][1] = A::mfma(a[1], bo[i][1], acc[1][1]);
   }
+  // FOLD: the row statistics of this lane's rows 16 t + li over the wave's part of K, with no barrier: the mean
+  // and centred sum of squares of the lane's own values, combined over the 4 lane groups (equal counts) by
+  // M2 = sum M2_g + n_g sum (m_g - m)^2; the waves' parts are combined the same way in the epilogue
+  if constexpr (FOLD) {
+    const int kbw = nblk > wid ? (nblk - 1 - wid) / 4 + 1 : 0;   // blocks of this wave
+    const float ng = (float)(KPL * kbw), inv = kbw > 0 ? __builtin_amdgcn_rcpf(ng) : 0.f;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      float xs[KB][KPL];
+      float s1 = 0.f;
+#pragma unroll
+      for (int i = 0; i < KB; ++i) {
+        typename A::T e8[8];
+        *reinterpret_cast<uint4*>(e8) = __builtin_bit_cast(uint4, ao[i][t]);
+#pragma unroll
+        for (int e = 0; e < KPL; ++e) {
+          xs[i][e] = A::tof(e8[e]);
+          if (wid + 4 * i < nblk) s1 += xs[i][e];
+        }
+      }
+      const float mg = s1 * inv;
+      float m2 = 0.f;
+#pragma unroll
+      for (int i = 0; i < KB; ++i) {
+        if (wid + 4 * i >= nblk) continue;
+#pragma unroll
+        for (int e = 0; e < KPL; ++e) {
+          const float dv = xs[i][e] - mg;
+          m2 += dv * dv;
+        }
+      }
+      const float mw = rows4_sum(mg) * 0.25f;
+      const float dg = mg - mw;
+      m2 = rows4_sum(m2 + ng * dg * dg);
+      if (g == 0) fstat[wid][t][li] = make_float2(mw, m2);
+    }
+  }
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -1388,12 +1434,44 @@ linear_kreg_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>:
   __syncthreads();
   // 1024 outputs, 4 per thread: thread -> (ti, tj) = wave index, lane, all four r
   if (col >= N) return;
+  float fmu[4], frs[4];   // FOLD: mean and rstd of this thread's rows 16 ti + 4 g + r
+  if constexpr (FOLD) {
+    // the waves' parts: wave w holds 32 x (its block count) of the row's K values
+    float2 p[4][4];
+    const float invk = __builtin_amdgcn_rcpf((float)K);
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) p[w][r] = fstat[w][ti][4 * g + r];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float nw[4], mu = 0.f, m2 = 0.f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        nw[w] = (float)(BLK * (nblk > w ? (nblk - 1 - w) / 4 + 1 : 0));
+        mu += nw[w] * p[w][r].x;
+      }
+      mu *= invk;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float dw = p[w][r].x - mu;
+        m2 += p[w][r].y + nw[w] * dw * dw;
+      }
+      fmu[r] = mu;
+      frs[r] = rsqrtf(m2 * invk + ln_eps);
+    }
+  }
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int64_t row = tm * 32 + 16 * ti + 4 * g + r;
     if (row >= M) continue;
     float val = red[0][ti][tj][r][lane] + red[1][ti][tj][r][lane] + red[2][ti][tj][r][lane] +
-                red[3][ti][tj][r][lane] + bv;
+                red[3][ti][tj][r][lane];
+    if constexpr (FOLD) {
+      val = frs[r] * (val - fmu[r] * fs) + bv;
+    } else {
+      val += bv;
+    }
     if (relu) val = fmaxf(val, 0.f);
     if (resid) val += rv[r];
     if (clamp_v > 0.f) val = fminf(fmaxf(val, -clamp_v), clamp_v);
@@ -2386,20 +2464,21 @@ static void launch_linear_quad(const void* x, int64_t ldx, const void* w, int64_
 
 // linear_kreg_kernel with KB = the smallest instantiated count of blocks per wave covering K; false
 // (nothing launched) past the largest.
-template <int DT, int OT, typename XT, bool LN>
+template <int DT, int OT, typename XT, bool LN, bool FOLD = false>
 static bool launch_linear_kreg(const void* x, int64_t ldx, const void* w, int64_t ldw, const float* bias,
                                const float* resid, int64_t ldr, void* y, int64_t ldy, void* y2, int64_t ldy2,
                                int64_t M, int64_t N, int64_t K, int relu, float clamp, const float* lnw,
-                               const float* lnb, float eps, void* xout, int64_t ldxo, hipStream_t st) {
+                               const float* lnb, float eps, void* xout, int64_t ldxo, hipStream_t st,
+                               const float* fsum = nullptr) {
   const int64_t nblk = K / 32;
   const int need = (int)((nblk + 3) / 4);
   const unsigned grid = (unsigned)(((M + 31) / 32) * ((N + 31) / 32));
   using TT = typename MM<DT>::T;
 #define HCLSM_KREG(KBV)                                                                                      \
   if (need <= KBV) {                                                                                         \
-    hipLaunchKernelGGL((linear_kreg_kernel<DT, OT, XT, LN, KBV>), dim3(grid), dim3(256), 0, st, (const XT*)x, ldx, \
-                       (const TT*)w, ldw, bias, resid, ldr, (typename MM<OT>::T*)y, ldy, (TT*)y2, ldy2, M, N, K,   \
-                       relu, clamp, lnw, lnb, eps, (TT*)xout, ldxo);                                         \
+    hipLaunchKernelGGL((linear_kreg_kernel<DT, OT, XT, LN, KBV, FOLD>), dim3(grid), dim3(256), 0, st,        \
+                       (const XT*)x, ldx, (const TT*)w, ldw, bias, resid, ldr, (typename MM<OT>::T*)y, ldy,   \
+                       (TT*)y2, ldy2, M, N, K, relu, clamp, lnw, lnb, eps, (TT*)xout, ldxo, fsum);           \
     return true;                                                                                             \
   }
   HCLSM_KREG(1) HCLSM_KREG(2) HCLSM_KREG(3)
@@ -2974,6 +3053,32 @@ static int linear_ln_fold(const float* x, int64_t ldx, const void* w, int64_t ld
   return 0;
 }
 
+// norm_slots folded into W1 by the caller's weights (16-bit, K = d within the linear_kreg_kernel instantiations).
+static bool norm_fold_fits(const HclsmSlotWeights* W, int64_t d, int64_t hidden, int dtype) {
+  return (dtype == HCLSM_BF16 || dtype == HCLSM_F16) && W->w1_n != nullptr && W->w1_n_sum != nullptr &&
+         W->w1_n_bias != nullptr && d % 32 == 0 && d <= 1024 && hidden > 0;
+}
+
+// y = act(rstd (x w_n^T - mean w_sum) + bias) for 16-bit x: LN(x) w^T + b with the LayerNorm folded into
+// w_n = w diag(gamma), w_sum (row sums of w_n) and bias = w beta + b (linear_kreg_kernel, FOLD).
+static int linear_norm_folded(const void* x, int64_t ldx, const void* w_n, const float* w_sum, const float* bias,
+                              void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, int relu, float eps, int dtype,
+                              hipStream_t st) {
+  if (!al16(x) || ldx % 8 || !al16(w_n) || K % 32 || ldy % 8) return HCLSM_ERR_UNSUPPORTED;
+  bool ok = false;
+  if (dtype == HCLSM_BF16)
+    ok = launch_linear_kreg<HCLSM_BF16, HCLSM_BF16, uint16_t, false, true>(x, ldx, w_n, K, bias, nullptr, 0, y, ldy,
+                                                                         nullptr, 0, M, N, K, relu, 0.f, nullptr,
+                                                                         nullptr, eps, nullptr, 0, st, w_sum);
+  else if (dtype == HCLSM_F16)
+    ok = launch_linear_kreg<HCLSM_F16, HCLSM_F16, _Float16, false, true>(x, ldx, w_n, K, bias, nullptr, 0, y, ldy,
+                                                                        nullptr, 0, M, N, K, relu, 0.f, nullptr,
+                                                                        nullptr, eps, nullptr, 0, st, w_sum);
+  if (!ok) return HCLSM_ERR_UNSUPPORTED;
+  HCLSM_LAUNCH_CHECK();
+  return 0;
+}
+
 // kq (nullable; v transposed, shapes the fused core takes): k Wq with the same strides as k, and the iteration
 // runs no q projection (the fused core's LNQ form).
 static int slot_iteration_impl(const HclsmSlotWeights* W, const float* slots_in, void* sb, bool make_sb,
@@ -3021,13 +3126,23 @@ static int slot_iteration_impl(const HclsmSlotWeights* W, const float* slots_in,
     rc = launch_core(q, d, N * d, k, ldk, k_bstride, v, ldv, v_bstride, upd, d, N * d, nullptr, dtype, B, N, M, d,
                      scale, 0.f, logit_clamp, renorm_eps, dtype, ws + L.core, st, v_transposed);
   if (rc) return rc;
+  // norm_slots folded into W1 (the caller's w1 diag(gamma), its row sums and w1 beta + b1): the GRU also writes h in
+  // dtype, and W1 forms the row statistics itself
+  const bool nfold = norm_fold_fits(W, d, hidden, dtype);
   // h = GRUCell(updates, slots)
-  rc = gru_impl(upd, d, sb, d, slots_in, d, W->w_ih, W->w_hh, W->b_ih, W->b_hh, h, d, nullptr, 0, rows, d, d, dtype,
-                st, gh, 3 * d);
+  rc = gru_impl(upd, d, sb, d, slots_in, d, W->w_ih, W->w_hh, W->b_ih, W->b_hh, h, d, nfold ? xn : nullptr, d, rows, d,
+                d, dtype, st, gh, 3 * d);
   if (rc) return rc;
   // m1 = ReLU(LN_mlp(h) W1^T + b1)
-  rc = linear_ln_fold(h, d, W->w1, d, W->b1, m1, hidden, rows, hidden, d, 1, W->ln_mlp_w, W->ln_mlp_b, 1e-5f, nullptr,
-                      0, dtype, st, &folded);
+  if (nfold) {
+    rc = linear_norm_folded(xn, d, W->w1_n, W->w1_n_sum, W->w1_n_bias, m1, hidden, rows, hidden, d, 1, 1e-5f, dtype,
+                            st);
+    if (rc) return rc;
+    folded = true;
+  } else {
+    rc = linear_ln_fold(h, d, W->w1, d, W->b1, m1, hidden, rows, hidden, d, 1, W->ln_mlp_w, W->ln_mlp_b, 1e-5f,
+                        nullptr, 0, dtype, st, &folded);
+  }
   if (rc) return rc;
   if (!folded) {
     rc = ln_impl(h, d, W->ln_mlp_w, W->ln_mlp_b, xn, d, rows, d, 1e-5f, HCLSM_F32, dtype, st);
@@ -3058,7 +3173,7 @@ static int check_slot_args(const HclsmSlotWeights* W, int64_t B, int64_t N, int6
   if (N > 16 * CORE_MAX_NT || B > 65535) return HCLSM_ERR_UNSUPPORTED;
   // 16-bit weights are read with 16-byte loads (the GEMMs, the GRU and the fused core's W_hh tiles)
   if (dtype != HCLSM_F32 && (!al16(W->w_q) || !al16(W->w_ih) || !al16(W->w_hh) || !al16(W->w1) || !al16(W->w2) ||
-                             (with_kv && (!al16(W->w_kv) || !al16(W->w_qkv)))))
+                             !al16(W->w1_n) || (with_kv && (!al16(W->w_kv) || !al16(W->w_qkv)))))
     return HCLSM_ERR_UNSUPPORTED;
   *L = slot_ws_layout(B, N, M, d, hidden, dtype == HCLSM_F32 ? 4 : 2, with_kv, d_in);
   if (workspace_bytes < (int64_t)L->total) return HCLSM_ERR_SHAPE;

@@ -70,6 +70,16 @@ class SlotWeights:
                 with torch.autocast("cuda", enabled=False):
                     wqk = t["w_q"].float().t() @ t["w_k"].float()
                 t["w_qkv"] = torch.cat([wqk.to(dtype), t["w_v"]], 0).contiguous()
+            # norm_slots folded into W1: LN(h) W1^T + b1 = rstd (h W1n^T - mean rowsum(W1n)) + W1 beta + b1 with
+            # W1n = W1 diag(gamma) (from the given weights in fp32, rounded once)
+            with torch.autocast("cuda", enabled=False):
+                w1 = torch.as_tensor(w["w1"]).to(device=device, dtype=torch.float32)
+                gam, bet, b1 = (t.get(k) for k in ("ln_mlp_w", "ln_mlp_b", "b1"))
+                w1n = (w1 * gam[None, :] if gam is not None else w1).to(dtype)
+                t["w1_n"] = w1n.contiguous()
+                t["w1_n_sum"] = w1n.float().sum(1).contiguous()
+                nb = w1 @ bet if bet is not None else torch.zeros(w1.shape[0], device=device)
+                t["w1_n_bias"] = (nb + b1 if b1 is not None else nb).contiguous()
         d = t["w_q"].shape[0]
         return cls(dtype, d, t["w1"].shape[0], t)
 
@@ -161,7 +171,7 @@ def _mode_args(mode: SlotMode):
 def slot_attention_iteration(slots: torch.Tensor, k: torch.Tensor, v: torch.Tensor, W: SlotWeights,
                              mode: SlotMode = REFERENCE_MODE, scale: float | None = None) -> torch.Tensor:
     """One iteration.  slots (B, N, d) (any float dtype; carried as fp32), k, v (B, M, d).
-    Returns the new slots (B, N, d) fp32.  One C call: eight launches on the current stream."""
+    Returns the new slots (B, N, d) fp32.  One C call, its launches on the current stream."""
     require_gpu("slot_attention_iteration", slots, k, v)
     B, N, d = slots.shape
     M = k.shape[1]

@@ -25,8 +25,9 @@
 extern "C" {
 #endif
 
-/* 2: HclsmSlotWeights gained w_qkv (a caller built against version 1 passes a shorter struct and must be rebuilt) */
-#define HCLSM_ABI_VERSION 2
+/* 2: HclsmSlotWeights gained w_qkv (a caller built against version 1 passes a shorter struct and must be rebuilt)
+ * 3: HclsmSlotWeights gained w1_n, w1_n_sum, w1_n_bias (the same holds for a caller built against version 2) */
+#define HCLSM_ABI_VERSION 3
 
 /* element types of floating-point tensors */
 #define HCLSM_F32  0
@@ -346,6 +347,12 @@ typedef struct HclsmSlotWeights {
                           product in fp32, then rounded).  A 16-bit forward whose iterations run the fused core
                           (hclsm_slot_attention_kq_offset >= 0) then projects the inputs straight to kq = k w_q
                           and v, with no kq GEMM per call, and forms no k */
+  const void* w1_n;        /* [hidden, d] w1 diag(ln_mlp_w) in dtype, nullable (then w1_n_sum and w1_n_bias are not
+                              read): formed once per weight set by the caller.  A 16-bit iteration then folds
+                              norm_slots into the W1 launch, ReLU(rstd (h w1_n^T - mean w1_n_sum) + w1_n_bias) with
+                              mean and rstd of h's rows in dtype formed there, and runs no LayerNorm launch for it */
+  const float* w1_n_sum;   /* [hidden] row sums of w1_n (its entries in dtype, summed in fp32) */
+  const float* w1_n_bias;  /* [hidden] w1 ln_mlp_b + b1 */
 } HclsmSlotWeights;
 
 /* Workspace bytes for hclsm_slot_attention_iteration / _forward (16-byte aligned buffer). */

@@ -50,7 +50,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 def test_version_and_strerror(lib):
     from hclsm_amd import _lib
-    assert lib.hclsm_abi_version() == _lib.ABI_VERSION == 2
+    assert lib.hclsm_abi_version() == _lib.ABI_VERSION == 3
     for code in (0, -1, -2, -3, -4, -5, -6):
         assert _lib.strerror(code)
     assert "unknown" in _lib.strerror(-999)

@@ -338,10 +338,10 @@ def test_layer_norm_rows(D, pad, io, M):
     assert normwise_rel_err(_np(y), want) <= tol
 
 
-@pytest.mark.parametrize("name", ["w_hh", "w_qkv"])
+@pytest.mark.parametrize("name", ["w_hh", "w_qkv", "w1_n"])
 def test_forward_rejects_misaligned_weights_before_any_launch(name):
     """16-bit weights are read with 16-byte loads; a weight pointer off that alignment (W_hh, or the optional
-    [W_q^T W_k; W_v], moved by one element through the C ABI) is rejected with HCLSM_ERR_UNSUPPORTED before any
+    [W_q^T W_k; W_v] or W1 diag(gamma), moved by one element through the C ABI) is rejected with HCLSM_ERR_UNSUPPORTED before any
     launch: the output buffer keeps its contents."""
     import ctypes
     from hclsm_amd import _lib
@@ -415,6 +415,46 @@ def test_forward_kq_projection(B, M, N, d, d_in):
     assert kq.shape == (B, M, d) and kq.dtype == torch.bfloat16
     assert normwise_rel_err(_np(kq), kq64) <= 1e-2
     assert normwise_rel_err(_np(kq_p), kq64) <= 1e-2
+
+
+@pytest.mark.parametrize("B,M,N,d,hidden,dtype", [(6, 196, 32, 384, 768, torch.bfloat16),
+                                                   (3, 70, 16, 128, 256, torch.float16),
+                                                   (2, 40, 8, 64, 128, torch.bfloat16)])
+def test_forward_norm_slots_folded_into_w1(B, M, N, d, hidden, dtype):
+    """With the weight set's W1 diag(gamma), its row sums and W1 beta + b1 (w1_n, w1_n_sum, w1_n_bias), a 16-bit
+    iteration takes norm_slots into the W1 launch (statistics of the slot rows formed there, no LayerNorm launch).
+    gamma, beta and b1 are non-trivial and the slot rows carry a mean offset.  The slots match the oracle and the
+    forward without the folded weights, and one iteration through hclsm_slot_attention_iteration matches the
+    oracle's iteration."""
+    from hclsm_amd.kernels import slot_iteration as si
+    from hclsm_amd.workloads import slot_config
+    tokens, slots0, w = slot_config(B=B, M=M, N=N, d=d, hidden=hidden, seed=B * M + d)
+    g = torch.Generator().manual_seed(d + hidden)
+    w["ln_mlp_w"] = torch.rand(d, generator=g) + 0.5
+    w["ln_mlp_b"] = torch.randn(d, generator=g) * 0.2
+    w["b1"] = torch.randn(hidden, generator=g) * 0.1
+    slots0 = slots0 + 1.5
+    W = si.SlotWeights.from_dict(w, dtype)
+    assert "w1_n" in W.t
+    W_plain = si.SlotWeights(W.dtype, W.d, W.hidden, {n: t for n, t in W.t.items() if not n.startswith("w1_n")})
+    x, s0 = tokens.cuda(), slots0.cuda()
+    print(f"norm fold B={B} M={M} N={N} d={d} hidden={hidden} {dtype}", flush=True)
+    out = si.slot_attention_forward(x, s0, W, 3, si.CONFIG2_MODE)
+    out_p = si.slot_attention_forward(x, s0, W_plain, 3, si.CONFIG2_MODE)
+    torch.cuda.synchronize()
+    wn = {n: _np(t) for n, t in w.items()}
+    ref = sa.slot_attention_forward(tokens.numpy(), slots0.numpy(), wn, 3, logit_clamp=None, renorm_eps=1e-8,
+                                    slot_clamp=None)
+    assert normwise_rel_err(_np(out), ref) <= 2e-2
+    assert normwise_rel_err(_np(out), _np(out_p)) <= 1e-2
+    # one iteration on given keys and values
+    k = torch.randn(B, M, d, generator=g).to(dtype)
+    v = torch.randn(B, M, d, generator=g).to(dtype)
+    it = si.slot_attention_iteration(s0, k.cuda(), v.cuda(), W, si.CONFIG2_MODE)
+    torch.cuda.synchronize()
+    ref_it = sa.slot_iteration(slots0.numpy(), _np(k), _np(v), wn, logit_clamp=None, renorm_eps=1e-8,
+                               slot_clamp=None)
+    assert normwise_rel_err(_np(it), ref_it) <= 2e-2
 
 
 def test_kq_offset_only_for_fused_core_shapes():
