@@ -74,7 +74,8 @@ _SIGNATURES: dict[str, list] = {
     "hclsm_relation_graph_forward": [_c_void_p] * 4 + [_i64] * 5 + [_int, _c_void_p, _f32, _int, _c_void_p, _i64,
                                                                     _c_void_p],
     "hclsm_level1_forward": [_c_void_p, _int, _c_void_p, _int, _c_void_p, _i64, _i64, _c_void_p, _c_void_p,
-                             _i64, _i64, _i64, _i64, _i64, _c_void_p, _f32, _int, _c_void_p, _i64, _c_void_p],
+                             _i64, _i64, _i64, _i64, _i64, _c_void_p, _c_void_p, _f32, _int, _c_void_p, _i64,
+                             _c_void_p],
     "hclsm_gnn_message_pass_workspace": [_i64, _i64, _i64, _i64, _int],
     "hclsm_gnn_message_pass": [_c_void_p] * 4 + [_i64] * 7 + [_c_void_p, _int, _c_void_p, _i64, _c_void_p],
     "hclsm_slot_track_cost_workspace": [_i64, _i64, _i64, _int],

@@ -79,6 +79,23 @@ int linear_glu_rows(const void* x, int64_t ldx, int x_dtype, const void* w1, con
                     int64_t ldy, int y_dtype, int64_t M, int64_t H, int64_t K, const int32_t* m_dev, int64_t m_mul,
                     int dtype, hipStream_t st);
 
+// Y[M, N] (fp32) = X . W^T + resid for 16-bit X, also writing Y rounded to dtype into y2 and, per row and 64-column
+// block b, the LayerNorm partial pst[row * N / 64 + b] = (mean, centred sum of squares) as float2 (device row count
+// as linear_rows, required).  HCLSM_ERR_UNSUPPORTED unless K % 64 == 0, N % 64 == 0 and 16-byte alignment.
+// Defined in slot_attn.hip.
+int linear_stats_rows(const void* x, int64_t ldx, const void* w, int64_t ldw, const float* resid, int64_t ldr,
+                      float* y, int64_t ldy, void* y2, int64_t ldy2, void* pst, int64_t M, int64_t N, int64_t K,
+                      const int32_t* m_dev, int64_t m_mul, int dtype, hipStream_t st);
+
+// Y = LN(X) . W0^T for the rows of a linear_stats_rows output: x its 16-bit copy, fst its partials (fparts per row),
+// w = W0 diag(gamma) in dtype, fsum[j] = sum of row j of w (fp32), fbias[j] = (W0 beta)[j]; the output is
+// rstd (x w^T - mean fsum) + fbias.  With w3 (rows of W0 diag(gamma) for the gate's second factor, N = 2 H):
+// Y[M, H] = silu(h1) * h3 with fsum / fbias holding the w columns, then the w3 columns.  HCLSM_ERR_UNSUPPORTED
+// unless 16-bit, K % 32 == 0, N % 4 == 0 (% 32 with w3) and 16-byte alignment.  Defined in slot_attn.hip.
+int linear_fold_rows(const void* x, int64_t ldx, const void* w, const void* w3, int64_t ldw, const float* fsum,
+                     const float* fbias, const void* fst, int64_t fparts, float eps, void* y, int64_t ldy, int y_dtype,
+                     int64_t M, int64_t N, int64_t K, const int32_t* m_dev, int64_t m_mul, int dtype, hipStream_t st);
+
 // LayerNorm of M rows (row count min(M, *m_dev * m_mul) when m_dev is set), as hclsm_layer_norm.
 // Defined in slot_attn.hip.
 int layer_norm_rows(const void* x, int64_t ldx, const float* w, const float* b, void* y, int64_t ldy, int64_t M,

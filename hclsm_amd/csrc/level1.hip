@@ -17,6 +17,11 @@
 //     x  += g . w2^T
 //   out = LN(x) . proj_out^T                                                                 :124-128
 //
+// 16-bit with the caller's folded weights (fold): the out-projection also writes x in dtype and x's LayerNorm
+// partials per 64 columns (linear_stats_rows), and the SwiGLU input takes LN2 from them through
+// w1 diag(gamma2), w3 diag(gamma2), their row sums and w1 beta2 | w3 beta2 (linear_fold_rows): no LN2 launch.  The
+// last W2 does the same for the final LayerNorm, folded into proj_out.
+//
 // GEMMs are the MFMA linear kernels of slot_attn.hip (64x64 LDS-staged tiles for 16-bit operands at
 // these sizes), LayerNorm its one-wave-per-row kernel, the attention the uniform-segment mode of the
 // varlen event-attention kernel (event_attn.hip).  The reference's event_pad_mask multiply (:130-131)
@@ -26,10 +31,11 @@
 namespace hclsm {
 
 struct L1Ws {
-  size_t x, xn, qkv, o, h1, g, total;
+  size_t x, xn, qkv, o, h1, g, st, total;
 };
 
 static size_t al256(size_t v) { return (v + 255) / 256 * 256; }
+static bool al16(const void* p) { return (((uintptr_t)p) & 15) == 0; }
 
 static L1Ws l1_ws(int64_t cap, int64_t N, int64_t dm, int64_t hid, int es) {
   const size_t R = (size_t)cap * N;
@@ -41,6 +47,7 @@ static L1Ws l1_ws(int64_t cap, int64_t N, int64_t dm, int64_t hid, int es) {
   w.o = o; o += al256(R * dm * es);
   w.h1 = o; o += al256(R * hid * es);
   w.g = o; o += al256(R * hid * es);
+  w.st = o; o += al256(R * ((dm + 63) / 64) * 8);   // LayerNorm partials of x's rows (folded LayerNorms)
   w.total = o;
   return w;
 }
@@ -59,8 +66,9 @@ extern "C" int64_t hclsm_level1_forward_workspace(int64_t capacity, int64_t N, i
 extern "C" int hclsm_level1_forward(const void* ev, int ev_dtype, void* out, int out_dtype, const int32_t* n_events,
                                     int64_t capacity, int64_t N, const int32_t* ev_rows, const float* obj_mask,
                                     int64_t d_slot, int64_t d_model, int64_t n_heads, int64_t hidden,
-                                    int64_t n_layers, const void* const* params, float ln_eps, int dtype,
-                                    void* workspace, int64_t workspace_bytes, void* stream) {
+                                    int64_t n_layers, const void* const* params, const void* const* fold,
+                                    float ln_eps, int dtype, void* workspace, int64_t workspace_bytes,
+                                    void* stream) {
   if (capacity < 0 || N < 0 || d_slot <= 0 || d_model <= 0 || n_heads <= 0 || hidden <= 0 || n_layers < 0)
     return HCLSM_ERR_SHAPE;
   if (capacity * N > 0x7fffffffLL || d_model % n_heads) return HCLSM_ERR_SHAPE;
@@ -78,6 +86,17 @@ extern "C" int hclsm_level1_forward(const void* ev, int ev_dtype, void* out, int
   if (workspace_bytes < (int64_t)L.total) return HCLSM_ERR_SHAPE;
   for (int64_t i = 0; i < 4 + 9 * n_layers; ++i)
     if (params[i] == nullptr) return HCLSM_ERR_NULL;
+  // the LayerNorms before the SwiGLU inputs and proj_out folded into those layers' weights: 16-bit, the
+  // out-projection and the last W2 writing x's LayerNorm partials (d_model a multiple of 64)
+  // (shapes or alignments the fold's kernels do not take: the LayerNorm launches instead)
+  bool folded = fold != nullptr && dtype != HCLSM_F32 && d_model % 64 == 0 && hidden % 64 == 0 && d_slot % 4 == 0 &&
+                n_layers > 0;
+  if (fold != nullptr)
+    for (int64_t i = 0; i < 3 + 4 * n_layers; ++i) {
+      if (fold[i] == nullptr) return HCLSM_ERR_NULL;
+      folded = folded && al16(fold[i]);
+    }
+  for (int64_t l = 0; folded && l < n_layers; ++l) folded = al16(params[4 + 9 * l + 3]) && al16(params[4 + 9 * l + 8]);
   hipStream_t st = (hipStream_t)stream;
   char* ws = reinterpret_cast<char*>(workspace);
   float* x = reinterpret_cast<float*>(ws + L.x);
@@ -86,6 +105,7 @@ extern "C" int hclsm_level1_forward(const void* ev, int ev_dtype, void* out, int
   void* o = ws + L.o;
   void* h1 = ws + L.h1;
   void* g = ws + L.g;
+  void* st_part = ws + L.st;
   const int64_t R = capacity * N, dm = d_model;
   auto P = [&](int64_t i) { return params[i]; };
   auto Pf = [&](int64_t i) { return reinterpret_cast<const float*>(params[i]); };
@@ -119,6 +139,23 @@ extern "C" int hclsm_level1_forward(const void* ev, int ev_dtype, void* out, int
     } else if (rc) {
       return rc;
     }
+    if (folded) {
+      // x += o . out_proj^T, x also in dtype (into xn) with its LayerNorm partials; g = SwiGLU(LN2 x) with LN2
+      // folded into w1 / w3: fold[3 + 4 l ..] = w1 diag(g2), w3 diag(g2), their row sums, w1 b2 | w3 b2
+      const int64_t f = 3 + 4 * l;
+      HCLSM_TRY(linear_stats_rows(o, dm, P(b + 3), dm, x, dm, x, dm, xn, dm, st_part, R, dm, dm, n_events, N, dtype,
+                                  st));
+      HCLSM_TRY(linear_fold_rows(xn, dm, fold[f], fold[f + 1], dm, reinterpret_cast<const float*>(fold[f + 2]),
+                                 reinterpret_cast<const float*>(fold[f + 3]), st_part, dm / 64, ln_eps, g, hidden,
+                                 dtype, R, 2 * hidden, dm, n_events, N, dtype, st));
+      if (l + 1 < n_layers) {
+        HCLSM_TRY(gemm(g, dtype, P(b + 8), dm, hidden, x, x, HCLSM_F32, nullptr));
+      } else {   // the last W2 also writes the partials of the final LayerNorm, folded into proj_out
+        HCLSM_TRY(linear_stats_rows(g, hidden, P(b + 8), hidden, x, dm, x, dm, xn, dm, st_part, R, dm, hidden,
+                                    n_events, N, dtype, st));
+      }
+      continue;
+    }
     HCLSM_TRY(gemm(o, dtype, P(b + 3), dm, dm, x, x, HCLSM_F32, nullptr));
     HCLSM_TRY(norm(Pf(b + 4), Pf(b + 5)));
     // g = silu(xn . w1^T) * (xn . w3^T): one paired GEMM, or two GEMMs through h1 where it does not apply
@@ -131,6 +168,12 @@ extern "C" int hclsm_level1_forward(const void* ev, int ev_dtype, void* out, int
       return rc;
     }
     HCLSM_TRY(gemm(g, dtype, P(b + 8), dm, hidden, x, x, HCLSM_F32, nullptr));
+  }
+  if (folded) {   // out = LN(x) . proj_out^T with the LayerNorm folded: fold[0 ..] = proj_out diag(g), sums, proj_out b
+    HCLSM_TRY(linear_fold_rows(xn, dm, fold[0], nullptr, dm, reinterpret_cast<const float*>(fold[1]),
+                               reinterpret_cast<const float*>(fold[2]), st_part, dm / 64, ln_eps, out, d_slot,
+                               out_dtype, R, d_slot, dm, n_events, N, dtype, st));
+    return 0;
   }
   HCLSM_TRY(norm(Pf(1), Pf(2)));
   HCLSM_TRY(gemm(xn, dtype, P(3), d_slot, dm, nullptr, out, out_dtype, nullptr));   // out = LN(x) . proj_out^T

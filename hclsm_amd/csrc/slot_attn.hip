@@ -150,14 +150,78 @@ struct OutSplit {
 //   for a capacity does only the rows a preceding kernel produced (workgroups past them exit);
 // - a gated-linear epilogue: val = silu(glu[row, col]) * val (glu in the operand type), applied after
 //   bias / ReLU and before the residual.
+// - LayerNorm statistics of the output rows (linear_dma_kernel, fp32 output): pst[row * N / 64 + b] = (mean, centred
+//   sum of squares) of the row's 64 columns 64 b .. 64 b + 63;
+// - a LayerNorm folded into the weights (linear_lds_kernel, linear_lds128_kernel): with W = W0 diag(gamma),
+//   fsum[j] = sum of row j of W and fbias[j] = (W0 beta)[j] + b[j], the output is rstd (acc - mean fsum[j]) + fbias[j]
+//   with the row's mean and rstd combined from fparts such 64-column partials fst[row * fparts ..] (eps feps); for
+//   a (w1, w3) pair fsum and fbias hold the w1 columns, then the w3 columns.
 struct LinExt {
   const int32_t* m_dev;
   int64_t m_mul;
   const void* glu;
   int64_t ldg;
   const void* w3;   // paired gated-linear GEMM (LDS kernels): see w_row
+  float2* pst = nullptr;
+  const float2* fst = nullptr;
+  int64_t fparts = 0;
+  const float* fsum = nullptr;
+  const float* fbias = nullptr;
+  float feps = 0.f;
 };
 constexpr LinExt kNoLinExt{nullptr, 1, nullptr, 0, nullptr};
+
+// (mean, rstd) of a row from its 64-column partials (mean_p, M2_p), parts <= FOLD_MAX_PARTS: every partial requested
+// at once, then M2 = sum M2_p + 64 sum (mean_p - mean)^2.
+constexpr int FOLD_MAX_PARTS = 16;   // rows of up to 1024 columns
+__device__ __forceinline__ float2 fold_row_stats(const float2* __restrict__ p, int64_t parts, float eps) {
+  // two rounds of at most 8 requests (8 partials in registers at a time); the partial means enter shifted by the
+  // first, sum (m_p - m_0) and sum (m_p - m_0)^2, so that an offset of the row's values cancels exactly
+  float m0 = 0.f, s1 = 0.f, s2 = 0.f, m2 = 0.f;
+#pragma unroll
+  for (int h = 0; h < FOLD_MAX_PARTS; h += 8) {
+    if (h >= parts) break;
+    float2 v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = h + i < parts ? p[h + i] : make_float2(0.f, 0.f);
+    if (h == 0) m0 = v[0].x;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float dv = h + i < parts ? v[i].x - m0 : 0.f;
+      s1 += dv;
+      s2 += dv * dv;
+      m2 += v[i].y;
+    }
+  }
+  const float inv = __builtin_amdgcn_rcpf((float)parts);
+  const float d = s1 * inv;   // mean - m_0
+  m2 += 64.f * fmaxf(s2 - s1 * d, 0.f);
+  return make_float2(m0 + d, rsqrtf(m2 * (inv * (1.f / 64.f)) + eps));
+}
+
+// Prologue of a folded-LayerNorm consumer (ROWS x 128 or 64 x 64 tile): threads 0 .. ROWS-1 form the (mean, rstd) of
+// the tile's rows, threads ROWS .. ROWS+COLS-1 stage fsum / fbias of its COLS weight columns (jc of column c).
+template <int ROWS, int COLS>
+__device__ __forceinline__ void fold_prologue(const LinExt& e, int tid, int64_t row0, int64_t M, int64_t col0,
+                                              int64_t N, float2 (&rst)[ROWS], float2 (&cst)[COLS]) {
+  if (tid < ROWS) {
+    const int64_t row = row0 + tid < M ? row0 + tid : M - 1;
+    rst[tid] = fold_row_stats(e.fst + row * e.fparts, e.fparts, e.feps);
+  } else if (tid < ROWS + COLS) {
+    const int c = tid - ROWS;
+    const int64_t col = col0 + c;
+    if (col < N) {
+      const int64_t jc = e.w3 == nullptr ? col : (col >> 5) * 16 + (col & 15) + ((col & 16) ? N / 2 : 0);
+      cst[c] = make_float2(e.fsum[jc], e.fbias[jc]);
+    }
+  }
+}
+
+// The folded LayerNorm on one accumulator of columns c .. c + 3 of the tile (cst) and row statistics st.
+__device__ __forceinline__ void fold_acc4(f32x4& acc, float2 st, const float2* cst) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) acc[r] = st.y * (acc[r] - st.x * cst[r].x) + cst[r].y;
+}
 
 // Weight row of GEMM column j.  With e.w3 set (LDS kernels) the GEMM is 2H columns wide and its 16-column tiles alternate
 // between W (= w1) and e.w3: column j is row 16 (j / 32) + j % 16 of w1 for j % 32 < 16, of w3 otherwise.  A
@@ -229,8 +293,9 @@ __device__ __forceinline__ bool lin_vec4_ok(const void* Y, int64_t ldy, const vo
          al(resid, ldr, 4) && al(e.glu, e.ldg, (int)sizeof(typename MM<DT>::T));
 }
 
+// acc is left holding the values stored (before their rounding to the output type).
 template <int DT, int OT>
-__device__ __forceinline__ void lin_epilogue4(const f32x4& acc, const float (&bv)[4], int64_t row, int64_t col,
+__device__ __forceinline__ void lin_epilogue4(f32x4& acc, const float (&bv)[4], int64_t row, int64_t col,
                                               int64_t N, int relu, float clamp_v, const float* __restrict__ resid,
                                               int64_t ldr, typename MM<OT>::T* __restrict__ Y, int64_t ldy,
                                               typename MM<DT>::T* __restrict__ Y2, int64_t ldy2, const LinExt& e,
@@ -268,6 +333,7 @@ __device__ __forceinline__ void lin_epilogue4(const f32x4& acc, const float (&bv
       if constexpr (sizeof(TD) == 4) *reinterpret_cast<float4*>(Y2 + row * ldy2 + col) = *reinterpret_cast<float4*>(o2);
       else *reinterpret_cast<uint2*>(Y2 + row * ldy2 + col) = *reinterpret_cast<uint2*>(o2);
     }
+    acc = f32x4{v[0], v[1], v[2], v[3]};
     return;
   }
 #pragma unroll
@@ -278,6 +344,7 @@ __device__ __forceinline__ void lin_epilogue4(const f32x4& acc, const float (&bv
     if (clamp_v > 0.f) val = fminf(fmaxf(val, -clamp_v), clamp_v);
     Y[row * ldy + col + r] = MM<OT>::fromf(val);
     if (Y2) Y2[row * ldy2 + col + r] = MM<DT>::fromf(val);
+    acc[r] = val;
   }
 }
 
@@ -321,7 +388,7 @@ struct AUnit<DT, float> {
 constexpr int LT_KC = 128;
 constexpr int LT_LD = LT_KC + 8;   // LDS row pitch (elements): spreads the 16 rows of an operand over banks
 
-template <int DT, int OT, typename XT = typename MM<DT>::T>
+template <int DT, int OT, typename XT = typename MM<DT>::T, bool FOLD = false>
 __global__ void __launch_bounds__(256)
 linear_lds_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>::T* __restrict__ W,
                   int64_t ldw, const float* __restrict__ bias, const float* __restrict__ resid, int64_t ldr,
@@ -372,6 +439,9 @@ linear_lds_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>::
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   fetch(0, (int)(K < LT_KC ? K : LT_KC));
+  // FOLD: (mean, rstd) of the tile's rows and (fsum, fbias) of its columns, read after the loop's barriers
+  __shared__ float2 rst[FOLD ? 64 : 1], cst[FOLD ? 64 : 1];
+  if constexpr (FOLD) fold_prologue<64, 64>(ext, tid, tm * 64, M, tn * 64, N, rst, cst);
   for (int64_t k0 = 0; k0 < K; k0 += LT_KC) {
     const int kc = (int)(K - k0 < LT_KC ? K - k0 : LT_KC);
     __syncthreads();   // the previous chunk is consumed
@@ -395,6 +465,13 @@ linear_lds_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>::
     }
   }
   const int64_t r0 = tm * 64 + 32 * wr, c0 = tn * 64 + 32 * wc;
+  if constexpr (FOLD) {   // folded LayerNorm (host: no output split, N a multiple of 4)
+#pragma unroll
+    for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+      for (int tj = 0; tj < 2; ++tj)
+        fold_acc4(acc[ti][tj], rst[32 * wr + 16 * ti + li], cst + 32 * wc + 16 * tj + 4 * g);
+  }
   if (os.yt != nullptr && Y2 == nullptr && os.col % 64 == 0 && tn * 64 >= os.col) {
     // a tile of the transposed half: transpose through LDS so that consecutive threads write
     // consecutive rows (tokens) of yt
@@ -484,8 +561,9 @@ linear_lds_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>::
 constexpr int LB_KC = 64;
 constexpr int LB_LD = LB_KC + 8;   // pitch 144 B: the 16 rows of a fragment read hit distinct banks
 
-template <int DT, int OT, typename XT = typename MM<DT>::T>
-__global__ void __launch_bounds__(256)
+template <int DT, int OT, typename XT = typename MM<DT>::T, bool FOLD = false>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(FOLD ? 3 : 1)))
+// (FOLD: three waves per SIMD, as the plain form has; the folded epilogue would otherwise take two)
 linear_lds128_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>::T* __restrict__ W,
                      int64_t ldw, const float* __restrict__ bias, const float* __restrict__ resid, int64_t ldr,
                      typename MM<OT>::T* __restrict__ Y, int64_t ldy, typename MM<DT>::T* __restrict__ Y2,
@@ -535,6 +613,9 @@ linear_lds128_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   fetch(0, (int)(K < LB_KC ? K : LB_KC));
+  // FOLD: (mean, rstd) of the tile's rows and (fsum, fbias) of its columns, read after the loop's barriers
+  __shared__ float2 rst[FOLD ? 128 : 1], cst[FOLD ? 128 : 1];
+  if constexpr (FOLD) fold_prologue<128, 128>(ext, tid, tm * 128, M, tn * 128, N, rst, cst);
   for (int64_t k0 = 0; k0 < K; k0 += LB_KC) {
     const int kc = (int)(K - k0 < LB_KC ? K - k0 : LB_KC);
     __syncthreads();   // the previous chunk is consumed
@@ -561,6 +642,14 @@ linear_lds128_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT
     }
   }
   const int64_t r0 = tm * 128 + 64 * wr, c0 = tn * 128 + 64 * wc;
+  // FOLD (host: N a multiple of 4): the folded LayerNorm on each accumulator right before its epilogue, so that
+  // few folded values are live at a time
+  auto fold = [&](int ti, int tj) {
+    if constexpr (FOLD) {
+      asm volatile("" ::: "memory");   // keeps the LDS reads here instead of all hoisted to the epilogue's start
+      fold_acc4(acc[ti][tj], rst[64 * wr + 16 * ti + li], cst + 64 * wc + 16 * tj + 4 * g);
+    }
+  };
   if (ext.w3 != nullptr) {   // (w1, w3) tile pairs (0, 1) and (2, 3) of the wave's 64 columns
     const int64_t H = N / 2;
     const bool v4 = lin_vec4_ok<DT, OT>(Y, ldy, Y2, ldy2, resid, ldr, kNoLinExt);
@@ -570,6 +659,8 @@ linear_lds128_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT
 #pragma unroll
       for (int ti = 0; ti < 4; ++ti) {
         const int64_t row = r0 + 16 * ti + li;
+        fold(ti, tj);
+        fold(ti, tj + 1);
         if (row < M && col < H)
           glu_pair_epilogue<DT, OT>(acc[ti][tj], acc[ti][tj + 1], row, col, H, resid, ldr, Y, ldy, Y2, ldy2, v4);
       }
@@ -586,6 +677,7 @@ linear_lds128_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti) {
       const int64_t row = r0 + 16 * ti + li;
+      fold(ti, tj);
       if (row >= M || col >= N) continue;
       lin_epilogue4<DT, OT>(acc[ti][tj], bv, row, col, N, relu, clamp_v, resid, ldr, Y, ldy, Y2, ldy2, ext, vec);
     }
@@ -614,7 +706,7 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-template <int DT, int OT>
+template <int DT, int OT, bool STATS = false>
 __global__ void __launch_bounds__(256)
 linear_dma_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const typename MM<DT>::T* __restrict__ W,
                   int64_t ldw, const float* __restrict__ bias, const float* __restrict__ resid, int64_t ldr,
@@ -748,7 +840,58 @@ linear_dma_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const t
     for (int ti = 0; ti < 4; ++ti) {
       const int64_t row = r0 + 16 * ti + li;
       if (row >= M || col >= N) continue;
-      lin_epilogue4<DT, OT>(acc[ti][tj], bv, row, col, N, relu, clamp_v, resid, ldr, Y, ldy, Y2, ldy2, ext, vec);
+      lin_epilogue4<DT, OT>(acc[ti][tj], bv, row, col, N, relu, clamp_v, resid, ldr, Y, ldy, STATS ? nullptr : Y2,
+                            ldy2, ext, vec);
+    }
+  }
+  if (STATS && c0 < N) {
+    // the 16-bit copy through LDS, in the stage the last chunk did not use (8 KB per wave; no other wave reads it
+    // after the last chunk's barrier), so that each store writes 8 whole 128-byte rows of the quadrant: row r's
+    // 16-byte chunk c at r * 64 + 8 (c ^ (r & 7)) elements
+    if (Y2 != nullptr) {
+      T* tb = reinterpret_cast<T*>(smem + (nk & 1) * 2 * LD_OPB) + wid * 64 * 64;
+#pragma unroll
+      for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+        for (int tj = 0; tj < 4; ++tj) {
+          const int rl = 16 * ti + li, ch = (2 * tj + (g >> 1)) ^ (rl & 7);
+          T e4[4] = {A::fromf(acc[ti][tj][0]), A::fromf(acc[ti][tj][1]), A::fromf(acc[ti][tj][2]),
+                     A::fromf(acc[ti][tj][3])};
+          *reinterpret_cast<uint2*>(tb + rl * 64 + 8 * ch + 4 * (g & 1)) = *reinterpret_cast<const uint2*>(e4);
+        }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the wave's stores are in LDS before any lane reads
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int rl = 8 * k + (lane >> 3), ch = lane & 7;
+        const uint4 v = *reinterpret_cast<const uint4*>(tb + rl * 64 + 8 * (ch ^ (rl & 7)));
+        const int64_t row = r0 + rl, col = c0 + 8 * ch;
+        if (row < M && col < N) *reinterpret_cast<uint4*>(Y2 + row * ldy2 + col) = v;
+      }
+    }
+    // LayerNorm partials of the stored rows over the wave's 64 columns (host: N a multiple of 64): each lane's mean
+    // and centred sum of squares of its 16 values, combined over the 4 lane groups of the row
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti) {
+      float s1 = 0.f;
+#pragma unroll
+      for (int tj = 0; tj < 4; ++tj)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s1 += acc[ti][tj][r];
+      const float ml = s1 * (1.f / 16.f);
+      float m2 = 0.f;
+#pragma unroll
+      for (int tj = 0; tj < 4; ++tj)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float dv = acc[ti][tj][r] - ml;
+          m2 += dv * dv;
+        }
+      const float m = rows4_sum(ml) * 0.25f;
+      const float dg = ml - m;
+      m2 = rows4_sum(m2 + 16.f * dg * dg);
+      const int64_t row = r0 + 16 * ti + li;
+      if (g == 0 && row < M) ext.pst[row * (N / 64) + c0 / 64] = make_float2(m, m2);
     }
   }
 }
@@ -2570,8 +2713,6 @@ int linear_rows(const void* x, int64_t ldx, int x_dtype, const void* w, int64_t 
                      ln_w, ln_b, ln_eps, dtype, st, LinExt{m_dev, m_mul, glu, ldg});
 }
 
-// SwiGLU input layer Y[M, H] = silu(X . w1^T) * (X . w3^T) as one GEMM over 2H interleaved columns (w_row) on
-// the LDS kernels (HCLSM_ERR_UNSUPPORTED for shapes or alignments they do not take: the caller runs two GEMMs).
 // Declared in internal.h.
 int qkv_attn_rows(const void* x, const void* w, void* o, const int32_t* n_events, int64_t capacity, int64_t N,
                   int64_t d, int H, int dh, const float* obj_mask, const int32_t* ev_rows, float scale, int dtype,
@@ -2595,6 +2736,80 @@ int qkv_attn_rows(const void* x, const void* w, void* o, const int32_t* n_events
   return 0;
 }
 
+// Y[M, N] = X W^T + resid (fp32) on linear_dma_kernel, with Y rounded to dtype in y2 and the LayerNorm partials of
+// Y's rows in pst (LinExt pst).  Declared in internal.h.
+int linear_stats_rows(const void* x, int64_t ldx, const void* w, int64_t ldw, const float* resid, int64_t ldr,
+                      float* y, int64_t ldy, void* y2, int64_t ldy2, void* pst, int64_t M, int64_t N, int64_t K,
+                      const int32_t* m_dev, int64_t m_mul, int dtype, hipStream_t st) {
+  if (M < 0 || N < 0 || K < 0) return HCLSM_ERR_SHAPE;
+  if ((dtype != HCLSM_BF16 && dtype != HCLSM_F16) || K == 0 || K % LD_KC || N % 64 || !al16(x) || ldx % 8 ||
+      !al16(w) || ldw % 8 || !al16(y) || ldy % 4 || !al16(y2) || ldy2 % 8 || !al16(resid) || ldr % 4 || !m_dev)
+    return HCLSM_ERR_UNSUPPORTED;
+  if (M == 0 || N == 0) return 0;
+  if (!x || !w || !y || !y2 || !pst) return HCLSM_ERR_NULL;
+  LinExt ext{m_dev, m_mul, nullptr, 0, nullptr};
+  ext.pst = reinterpret_cast<float2*>(pst);
+  const int64_t tiles128 = ((M + 127) / 128) * ((N + 127) / 128);
+  if (tiles128 > 0x7fffffffLL) return HCLSM_ERR_SHAPE;
+#define HCLSM_ST(D)                                                                                          \
+  if (dtype == D)                                                                                            \
+    hipLaunchKernelGGL((linear_dma_kernel<D, HCLSM_F32, true>), dim3((unsigned)tiles128), dim3(256), 0, st,  \
+                       (const MM<D>::T*)x, ldx, (const MM<D>::T*)w, ldw, nullptr, resid, ldr, y, ldy,         \
+                       (MM<D>::T*)y2, ldy2, M, N, K, 0, 0.f, OutSplit{0, 1, 0, 0, nullptr}, ext);
+  HCLSM_ST(HCLSM_BF16)
+  HCLSM_ST(HCLSM_F16)
+#undef HCLSM_ST
+  HCLSM_LAUNCH_CHECK();
+  return 0;
+}
+
+// Y = LN(X) W0^T with the LayerNorm folded into the weights (LinExt fst / fsum / fbias): w = W0 diag(gamma), x the
+// 16-bit rows whose partials fst [M][fparts] linear_stats_rows wrote.  With w3 the SwiGLU input layer over N = 2 H
+// interleaved columns (Y [M, H], linear_lds128_kernel), else Y [M, N] (linear_lds_kernel).  Declared in
+// internal.h.
+int linear_fold_rows(const void* x, int64_t ldx, const void* w, const void* w3, int64_t ldw, const float* fsum,
+                     const float* fbias, const void* fst, int64_t fparts, float eps, void* y, int64_t ldy, int y_dtype,
+                     int64_t M, int64_t N, int64_t K, const int32_t* m_dev, int64_t m_mul, int dtype, hipStream_t st) {
+  if (M < 0 || N < 0 || K < 0 || fparts <= 0) return HCLSM_ERR_SHAPE;
+  if (fparts > FOLD_MAX_PARTS) return HCLSM_ERR_UNSUPPORTED;
+  if ((dtype != HCLSM_BF16 && dtype != HCLSM_F16) || (y_dtype != dtype && y_dtype != HCLSM_F32)) return HCLSM_ERR_DTYPE;
+  if (K == 0 || K % 32 || N % (w3 ? 32 : 4) || !al16(x) || ldx % 8 || !al16(w) || !al16(w3) || ldw % 8 ||
+      !al16(fsum) || !al16(fbias) || (((uintptr_t)fst) & 7))
+    return HCLSM_ERR_UNSUPPORTED;
+  if (M == 0 || N == 0) return 0;
+  if (!x || !w || !fsum || !fbias || !fst || !y) return HCLSM_ERR_NULL;
+  LinExt ext{m_dev, m_mul, nullptr, 0, w3};
+  ext.fst = reinterpret_cast<const float2*>(fst);
+  ext.fparts = fparts;
+  ext.fsum = fsum;
+  ext.fbias = fbias;
+  ext.feps = eps;
+  const int64_t tiles128 = ((M + 127) / 128) * ((N + 127) / 128), tiles64 = ((M + 63) / 64) * ((N + 63) / 64);
+  if (tiles64 > 0x7fffffffLL) return HCLSM_ERR_SHAPE;
+#define HCLSM_FO(D, O)                                                                                       \
+  if (dtype == D && y_dtype == O) {                                                                          \
+    if (w3)                                                                                                  \
+      hipLaunchKernelGGL((linear_lds128_kernel<D, O, MM<D>::T, true>), dim3((unsigned)tiles128), dim3(256), 0,  \
+                         st,                                                                                 \
+                         (const MM<D>::T*)x, ldx, (const MM<D>::T*)w, ldw, nullptr, nullptr, 0, (MM<O>::T*)y,  \
+                         ldy, nullptr, 0, M, N, K, 0, 0.f, ext);                                              \
+    else                                                                                                     \
+      hipLaunchKernelGGL((linear_lds_kernel<D, O, MM<D>::T, true>), dim3((unsigned)tiles64), dim3(256), 0, st, \
+                         (const MM<D>::T*)x, ldx, (const MM<D>::T*)w, ldw, nullptr, nullptr, 0, (MM<O>::T*)y,  \
+                         ldy, nullptr, 0, M, N, K, 0, 0.f, OutSplit{0, 1, 0, 0, nullptr}, ext);             \
+  }
+  HCLSM_FO(HCLSM_BF16, HCLSM_BF16)
+  HCLSM_FO(HCLSM_BF16, HCLSM_F32)
+  HCLSM_FO(HCLSM_F16, HCLSM_F16)
+  HCLSM_FO(HCLSM_F16, HCLSM_F32)
+#undef HCLSM_FO
+  HCLSM_LAUNCH_CHECK();
+  return 0;
+}
+
+// SwiGLU input layer Y[M, H] = silu(X . w1^T) * (X . w3^T) as one GEMM over 2H interleaved columns (w_row) on
+// the LDS kernels (HCLSM_ERR_UNSUPPORTED for shapes or alignments they do not take: the caller runs two GEMMs).
+// Declared in internal.h.
 int linear_glu_rows(const void* x, int64_t ldx, int x_dtype, const void* w1, const void* w3, int64_t ldw, void* y,
                     int64_t ldy, int y_dtype, int64_t M, int64_t H, int64_t K, const int32_t* m_dev, int64_t m_mul,
                     int dtype, hipStream_t st) {

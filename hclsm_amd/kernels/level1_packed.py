@@ -26,9 +26,13 @@ class Level1Weights:
     LayerNorm vectors fp32."""
 
     def __init__(self, tensors: list, dtype: torch.dtype, d_slot: int, d_model: int, hidden: int, n_layers: int,
-                 n_heads: int, ln_eps: float) -> None:
+                 n_heads: int, ln_eps: float, fold: list | None = None) -> None:
         self.tensors = tensors
         self.ptrs = (ctypes.c_void_p * len(tensors))(*[t.data_ptr() for t in tensors])
+        # the folded LayerNorms (16-bit): proj_out diag(g), its row sums, proj_out b; per block w1 diag(g2),
+        # w3 diag(g2), their row sums and w1 b2 | w3 b2 (the C call's fold array)
+        self.fold = fold
+        self.fold_ptrs = None if fold is None else (ctypes.c_void_p * len(fold))(*[t.data_ptr() for t in fold])
         self.dtype, self.d_slot, self.d_model, self.hidden = dtype, d_slot, d_model, hidden
         self.n_layers, self.n_heads, self.ln_eps = n_layers, n_heads, ln_eps
 
@@ -63,7 +67,21 @@ class Level1Weights:
                   mat(b.ffn.w2.weight)]
         n_heads = m.blocks[0].attn.num_heads if len(m.blocks) else 1
         hidden = m.blocks[0].ffn.w1.weight.shape[0] if len(m.blocks) else 32
-        W = cls(t, dtype, m.d_slot, m.d_model, hidden, len(m.blocks), n_heads, float(eps.pop()))
+        fold = None
+        if dtype in (torch.bfloat16, torch.float16) and len(m.blocks):
+            # LN(x) W^T = rstd (x (W diag g)^T - mean rowsum(W diag g)) + W b, from the fp32 weights, rounded once
+            def folded(w, ln):
+                with torch.autocast(w.device.type, enabled=False):
+                    w32 = w.detach().float()
+                    wn = (w32 * ln.weight.detach().float()[None, :]).to(dtype).contiguous()
+                    return wn, wn.float().sum(1), w32 @ ln.bias.detach().float()
+            po, po_s, po_b = folded(m.proj_out.weight, m.norm)
+            fold = [po, po_s.contiguous(), po_b.contiguous()]
+            for b in m.blocks:
+                w1, w1_s, w1_b = folded(b.ffn.w1.weight, b.norm2)
+                w3, w3_s, w3_b = folded(b.ffn.w3.weight, b.norm2)
+                fold += [w1, w3, torch.cat([w1_s, w3_s]).contiguous(), torch.cat([w1_b, w3_b]).contiguous()]
+        W = cls(t, dtype, m.d_slot, m.d_model, hidden, len(m.blocks), n_heads, float(eps.pop()), fold)
         m._hclsm_level1_weights = (key, W)
         return W
 
@@ -94,8 +112,8 @@ def level1_forward_packed(ev: torch.Tensor, idx: EventIndex, obj_mask: torch.Ten
     ws = _workspace(int(wsb), ev.device)
     rc = L.hclsm_level1_forward(_lib.ptr(x), _lib.dtype_code(x.dtype), _lib.ptr(out), _lib.dtype_code(out_dtype),
                                 idx.ptr("stats"), cap, N, idx.ptr("rows"), _lib.ptr(om), d_slot, W.d_model,
-                                W.n_heads, W.hidden, W.n_layers, W.ptrs, W.ln_eps, code, _lib.ptr(ws), ws.numel(),
-                                _lib.stream_of(x))
+                                W.n_heads, W.hidden, W.n_layers, W.ptrs, W.fold_ptrs, W.ln_eps, code, _lib.ptr(ws),
+                                ws.numel(), _lib.stream_of(x))
     _lib.check(rc, "hclsm_level1_forward")
     return out
 
@@ -144,7 +162,7 @@ def level1_forward_dense(ev: torch.Tensor, obj_mask: torch.Tensor | None, W: Lev
     ws = _workspace(int(wsb), ev.device)
     rc = L.hclsm_level1_forward(_lib.ptr(x), _lib.dtype_code(x.dtype), _lib.ptr(out), _lib.dtype_code(out_dtype),
                                 _lib.ptr(n_dev), cap, N, _lib.ptr(rows), _lib.ptr(om), d_slot, W.d_model, W.n_heads,
-                                W.hidden, W.n_layers, W.ptrs, W.ln_eps, code, _lib.ptr(ws), ws.numel(),
+                                W.hidden, W.n_layers, W.ptrs, W.fold_ptrs, W.ln_eps, code, _lib.ptr(ws), ws.numel(),
                                 _lib.stream_of(x))
     _lib.check(rc, "hclsm_level1_forward")
     return out

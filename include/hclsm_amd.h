@@ -26,7 +26,8 @@ extern "C" {
 #endif
 
 /* 2: HclsmSlotWeights gained w_qkv (a caller built against version 1 passes a shorter struct and must be rebuilt)
- * 3: HclsmSlotWeights gained w1_n, w1_n_sum, w1_n_bias (the same holds for a caller built against version 2) */
+ * 3: HclsmSlotWeights gained w1_n, w1_n_sum, w1_n_bias (the same holds for a caller built against version 2), and
+ *    hclsm_level1_forward the fold argument */
 #define HCLSM_ABI_VERSION 3
 
 /* element types of floating-point tensors */
@@ -440,14 +441,21 @@ int64_t hclsm_level1_forward_workspace(int64_t capacity, int64_t N, int64_t d_mo
  *   ln2_b [d_model], w1 [hidden, d_model], w3 [hidden, d_model], w2 [d_model, hidden]
  * (LayerNorm weights float32, the rest in `dtype`; no biases, as in the reference).  A query whose keys
  * are all excluded gives NaN, as torch's softmax over all -inf does.
+ * fold (nullable; read for 16-bit dtypes): host array of 3 + 4 * n_layers device pointers, formed once per
+ * weight set, with which each block's LayerNorm before the SwiGLU input and the final LayerNorm are folded
+ * into the next layer (LN(x) W^T = rstd (x (W diag g)^T - mean s) + W b, s the row sums of W diag g): no
+ * LayerNorm launch for them.  proj_out diag(norm_w) [d_slot, d_model] (dtype), its row sums [d_slot],
+ * proj_out norm_b [d_slot], then per layer w1 diag(ln2_w), w3 diag(ln2_w) [hidden, d_model] (dtype), their row
+ * sums [2 hidden] (w1 rows, then w3 rows), w1 ln2_b | w3 ln2_b [2 hidden] (float32); 16-byte aligned, else (or
+ * for d_model or hidden not multiples of 64) the LayerNorms run as launches.
  * Replaces: Level1EventDynamics.forward with EventTransformerBlock and SwiGLUFFN
  *   (hclsm/dynamics/level1_event.py:17-133) on the events gathered by HierarchyManager.gather_events.
  */
 int hclsm_level1_forward(const void* ev, int ev_dtype, void* out, int out_dtype, const int32_t* n_events,
                          int64_t capacity, int64_t N, const int32_t* ev_rows, const float* obj_mask,
                          int64_t d_slot, int64_t d_model, int64_t n_heads, int64_t hidden, int64_t n_layers,
-                         const void* const* params, float ln_eps, int dtype, void* workspace,
-                         int64_t workspace_bytes, void* stream);
+                         const void* const* params, const void* const* fold, float ln_eps, int dtype,
+                         void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Workspace bytes for hclsm_relation_graph_forward, or HCLSM_ERR_UNSUPPORTED for a shape outside it. */
 int64_t hclsm_relation_graph_workspace(int64_t frames, int64_t N, int64_t D, int64_t E, int dtype);

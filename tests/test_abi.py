@@ -86,12 +86,12 @@ def test_level1_forward_argument_errors_before_launch(lib):
     assert ws(4, 4, 64, 256, 9) == -3
     assert ws(0, 4, 64, 256, 1) >= 0
     args = dict(ev=None, evd=0, out=None, outd=0, n=None, cap=4, N=8, rows=None, om=None, ds=64, dm=64, H=4,
-                hid=256, L=1, params=None, eps=1e-5, dt=1, ws=None, wsb=0, st=None)
+                hid=256, L=1, params=None, fold=None, eps=1e-5, dt=1, ws=None, wsb=0, st=None)
 
     def call(**kw):
         a = {**args, **kw}
         return f(a["ev"], a["evd"], a["out"], a["outd"], a["n"], a["cap"], a["N"], a["rows"], a["om"], a["ds"], a["dm"],
-                 a["H"], a["hid"], a["L"], a["params"], a["eps"], a["dt"], a["ws"], a["wsb"], a["st"])
+                 a["H"], a["hid"], a["L"], a["params"], a["fold"], a["eps"], a["dt"], a["ws"], a["wsb"], a["st"])
     assert call(dm=60, H=4) == -4            # head dim 15: unsupported
     assert call(dm=64, H=3) == -2            # d_model not a multiple of n_heads
     assert call(dt=7) == -3                  # compute dtype

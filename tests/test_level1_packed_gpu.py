@@ -134,6 +134,40 @@ def test_level1_fused_qkv_attention_32_slots(dtype):
     assert normwise_rel_err(_np(got[keep]), want) <= 2e-2
 
 
+@pytest.mark.parametrize("dtype,N,B,T", [(torch.bfloat16, 32, 5, 9), (torch.float16, 16, 4, 12),
+                                         (torch.bfloat16, 32, 16, 128)])
+def test_level1_folded_layernorms(dtype, N, B, T):
+    """16-bit calls fold the LayerNorms before the SwiGLU inputs and before proj_out into those layers' weights
+    (Level1Weights' fold array: W diag(gamma), its row sums, W beta); the out-projection and the last W2 write the
+    rows' LayerNorm partials.  With non-trivial gamma / beta in every LayerNorm and a mean offset on the events,
+    the output matches the oracle at the 16-bit bar and the call without the fold array within 1e-2; the last case
+    has a 65,536-row capacity."""
+    from hclsm_amd.kernels.level1_packed import Level1Weights, level1_forward_packed
+    hm, l1 = _modules(31 + N)
+    g = torch.Generator().manual_seed(N + T)
+    with torch.no_grad():
+        for ln in [l1.norm] + [m for b in l1.blocks for m in (b.norm1, b.norm2)]:
+            ln.weight.copy_(torch.rand(ln.weight.shape, generator=g) + 0.5)
+            ln.bias.copy_(torch.randn(ln.bias.shape, generator=g) * 0.2)
+    states, mask, obj = _case(B, T, N, 31 + N, p=0.3)
+    states = states + 0.7
+    W = Level1Weights.from_module(l1, dtype)
+    assert W.fold is not None and len(W.fold) == 3 + 4 * L1.n_layers
+    W0 = Level1Weights(W.tensors, W.dtype, W.d_slot, W.d_model, W.hidden, W.n_layers, W.n_heads, W.ln_eps)
+    print(f"level1 fold {dtype} N={N} B={B} T={T}", flush=True)
+    with torch.no_grad():
+        ev, idx = hm.gather_events_packed(states, mask)
+        out = level1_forward_packed(ev, idx, obj, W)
+        out0 = level1_forward_packed(ev, idx, obj, W0)
+        ev_pad, pad, K = hm.gather_events(states, mask)
+    ref = om.level1_ref(_np(ev_pad), _np(pad), _np(obj), _sd(l1), L1.n_layers, L1.n_heads)
+    got, bk = _live_rows(out, idx)
+    got0, _ = _live_rows(out0, idx)
+    want = np.stack([ref[b, k] for b, k in bk])
+    assert normwise_rel_err(_np(got), want) <= 2e-2
+    assert normwise_rel_err(_np(got), _np(got0)) <= 1e-2
+
+
 def test_level1_padded_forward_bf16_fused_attention():
     """The reference-shaped padded call (Level1EventDynamics.forward over (B, K_max, N, d_slot), level1_event.py:85-133)
     under a bf16 autocast with 32 slots: the dense event index feeds the fused QKV projection + slot attention
