@@ -91,7 +91,7 @@ extern "C" int hclsm_level1_forward(const void* ev, int ev_dtype, void* out, int
   // (shapes or alignments the fold's kernels do not take: the LayerNorm launches instead)
   bool folded = fold != nullptr && dtype != HCLSM_F32 && d_model % 64 == 0 && hidden % 64 == 0 && d_slot % 4 == 0 &&
                 n_layers > 0;
-  if (fold != nullptr)
+  if (fold != nullptr && dtype != HCLSM_F32)
     for (int64_t i = 0; i < 3 + 4 * n_layers; ++i) {
       if (fold[i] == nullptr) return HCLSM_ERR_NULL;
       folded = folded && al16(fold[i]);
