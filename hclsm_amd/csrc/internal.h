@@ -116,9 +116,12 @@ int attn_slots_packed(const void* q, const void* k, const void* v, int64_t ldi, 
 // (head h, keys excluded as attn_slots_packed) over q | k | v = x . w^T (w = in_proj [3d, d], x / o row stride d),
 // for the first *n_events of capacity events.  HCLSM_ERR_UNSUPPORTED unless 16-bit, N = 32, dh = 64, d = 64 H,
 // 16-byte aligned x / w / o; the caller then runs the GEMM and attn_slots_packed.  Defined in slot_attn.hip.
+// fst (nullable): x is the 16-bit copy of a linear_stats_rows output and LN1 is folded into w as in
+// linear_fold_rows (fsum / fbias per in_proj row, fparts partials per row of x).
 int qkv_attn_rows(const void* x, const void* w, void* o, const int32_t* n_events, int64_t capacity, int64_t N,
                   int64_t d, int H, int dh, const float* obj_mask, const int32_t* ev_rows, float scale, int dtype,
-                  hipStream_t st);
+                  hipStream_t st, const float* fsum = nullptr, const float* fbias = nullptr,
+                  const void* fst = nullptr, int64_t fparts = 0, float eps = 0.f);
 
 // Forward scan that also writes the backward's checkpoint slab ck ([batch][ceil(T / 8)][16][d_inner] fp32, the
 // state before steps 8, 16, ...; entry 0, the zero initial state, is not stored): the bf16, d_state 16

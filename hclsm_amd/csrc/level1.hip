@@ -19,8 +19,9 @@
 //
 // 16-bit with the caller's folded weights (fold): the out-projection also writes x in dtype and x's LayerNorm
 // partials per 64 columns (linear_stats_rows), and the SwiGLU input takes LN2 from them through
-// w1 diag(gamma2), w3 diag(gamma2), their row sums and w1 beta2 | w3 beta2 (linear_fold_rows): no LN2 launch.  The
-// last W2 does the same for the final LayerNorm, folded into proj_out.
+// w1 diag(gamma2), w3 diag(gamma2), their row sums and w1 beta2 | w3 beta2 (linear_fold_rows): no LN2 launch.  W2
+// does the same for the next layer's LN1 (folded into the fused QKV attention, where it applies) and, in the last
+// layer, for the final LayerNorm, folded into proj_out.
 //
 // GEMMs are the MFMA linear kernels of slot_attn.hip (64x64 LDS-staged tiles for 16-bit operands at
 // these sizes), LayerNorm its one-wave-per-row kernel, the attention the uniform-segment mode of the
@@ -92,7 +93,7 @@ extern "C" int hclsm_level1_forward(const void* ev, int ev_dtype, void* out, int
   bool folded = fold != nullptr && dtype != HCLSM_F32 && d_model % 64 == 0 && hidden % 64 == 0 && d_slot % 4 == 0 &&
                 n_layers > 0;
   if (fold != nullptr && dtype != HCLSM_F32)
-    for (int64_t i = 0; i < 3 + 4 * n_layers; ++i) {
+    for (int64_t i = 0; i < 3 + 7 * n_layers; ++i) {
       if (fold[i] == nullptr) return HCLSM_ERR_NULL;
       folded = folded && al16(fold[i]);
     }
@@ -126,12 +127,24 @@ extern "C" int hclsm_level1_forward(const void* ev, int ev_dtype, void* out, int
   };
   HCLSM_TRY(gemm(ev, ev_dtype, P(0), dm, d_slot, nullptr, x, HCLSM_F32, nullptr));   // x = ev . proj_in^T
   const float scale = 1.f / sqrtf((float)dh);
+  // with the fold, LN1 of layers after the first is folded into the fused QKV attention (from the previous W2's
+  // partials) where that launch applies (the shapes qkv_attn_rows takes: 32 slots, 64-wide heads, d_model = 64 H)
+  const bool qkv_fold = folded && N == 32 && dh == 64 && dm == 64 * n_heads && al16(xn);
   for (int64_t l = 0; l < n_layers; ++l) {
     const int64_t b = 4 + 9 * l;   // ln1_w, ln1_b, in_proj, out_proj, ln2_w, ln2_b, w1, w3, w2
-    HCLSM_TRY(norm(Pf(b), Pf(b + 1)));
-    // o = attention over q | k | v = xn . in_proj^T: one fused launch (q / k / v stay on chip) where it applies
-    rc = qkv_attn_rows(xn, P(b + 2), o, n_events, capacity, N, dm, (int)n_heads, (int)dh, obj_mask, ev_rows, scale,
-                       dtype, st);
+    const int64_t f = 3 + 7 * l;   // fold: in_proj diag(g1), its row sums, in_proj b1, w1 / w3 diag(g2), sums, biases
+    if (qkv_fold && l > 0) {
+      // xn holds x in dtype and st_part its partials (the previous layer's W2)
+      HCLSM_TRY(qkv_attn_rows(xn, fold[f], o, n_events, capacity, N, dm, (int)n_heads, (int)dh, obj_mask, ev_rows,
+                              scale, dtype, st, reinterpret_cast<const float*>(fold[f + 1]),
+                              reinterpret_cast<const float*>(fold[f + 2]), st_part, dm / 64, ln_eps));
+      rc = 0;
+    } else {
+      HCLSM_TRY(norm(Pf(b), Pf(b + 1)));
+      // o = attention over q | k | v = xn . in_proj^T: one fused launch (q / k / v stay on chip) where it applies
+      rc = qkv_attn_rows(xn, P(b + 2), o, n_events, capacity, N, dm, (int)n_heads, (int)dh, obj_mask, ev_rows, scale,
+                         dtype, st);
+    }
     if (rc == HCLSM_ERR_UNSUPPORTED) {
       HCLSM_TRY(gemm(xn, dtype, P(b + 2), 3 * dm, dm, nullptr, qkv, dtype, nullptr));
       HCLSM_TRY(attn_slots_packed(qkv, qkv + dm * es, qkv + 2 * dm * es, 3 * dm, o, dm, n_events, capacity, N,
@@ -141,16 +154,15 @@ extern "C" int hclsm_level1_forward(const void* ev, int ev_dtype, void* out, int
     }
     if (folded) {
       // x += o . out_proj^T, x also in dtype (into xn) with its LayerNorm partials; g = SwiGLU(LN2 x) with LN2
-      // folded into w1 / w3: fold[3 + 4 l ..] = w1 diag(g2), w3 diag(g2), their row sums, w1 b2 | w3 b2
-      const int64_t f = 3 + 4 * l;
+      // folded into w1 / w3: fold[f + 3 ..] = w1 diag(g2), w3 diag(g2), their row sums, w1 b2 | w3 b2
       HCLSM_TRY(linear_stats_rows(o, dm, P(b + 3), dm, x, dm, x, dm, xn, dm, st_part, R, dm, dm, n_events, N, dtype,
                                   st));
-      HCLSM_TRY(linear_fold_rows(xn, dm, fold[f], fold[f + 1], dm, reinterpret_cast<const float*>(fold[f + 2]),
-                                 reinterpret_cast<const float*>(fold[f + 3]), st_part, dm / 64, ln_eps, g, hidden,
+      HCLSM_TRY(linear_fold_rows(xn, dm, fold[f + 3], fold[f + 4], dm, reinterpret_cast<const float*>(fold[f + 5]),
+                                 reinterpret_cast<const float*>(fold[f + 6]), st_part, dm / 64, ln_eps, g, hidden,
                                  dtype, R, 2 * hidden, dm, n_events, N, dtype, st));
-      if (l + 1 < n_layers) {
+      if (l + 1 < n_layers && !qkv_fold) {
         HCLSM_TRY(gemm(g, dtype, P(b + 8), dm, hidden, x, x, HCLSM_F32, nullptr));
-      } else {   // the last W2 also writes the partials of the final LayerNorm, folded into proj_out
+      } else {   // W2 also writes the partials of the next LayerNorm: the next layer's LN1 or the final one
         HCLSM_TRY(linear_stats_rows(g, hidden, P(b + 8), hidden, x, dm, x, dm, xn, dm, st_part, R, dm, hidden,
                                     n_events, N, dtype, st));
       }

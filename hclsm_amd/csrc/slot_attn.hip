@@ -918,12 +918,15 @@ __device__ __forceinline__ float qa_out(float acc, float inv) {
   return y;
 }
 
-template <int DT>
+// FOLD: LN1 folded into the weights (LinExt fst / fsum / fbias of linear_fold_rows, in_proj rows as the columns): each
+// lane requests its two rows' partials and its 48 columns' (fsum, fbias) before the K loop (the LDS is full; the
+// registers are not: two workgroups per CU leave 256 per lane) and folds the accumulators after it.
+template <int DT, bool FOLD = false>
 __global__ void __launch_bounds__(256, 2)
 qkv_attn_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const typename MM<DT>::T* __restrict__ W,
                 typename MM<DT>::T* __restrict__ O, int64_t ldo, const int32_t* __restrict__ n_events, int64_t cap_rows,
                 int64_t d, int H, const float* __restrict__ obj_mask, const int32_t* __restrict__ ev_rows,
-                float scale_log2) {
+                float scale_log2, LinExt fx) {
   using A = MM<DT>;
   using T = typename A::T;
   typedef short s16x4v __attribute__((ext_vector_type(4)));
@@ -976,6 +979,22 @@ qkv_attn_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const typ
 #pragma unroll
     for (int j = 0; j < 12; ++j) acc[t][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   request(0);
+  float2 rs[2];          // FOLD: (mean, rstd) of rows 16 t + li of this wave's event
+  float4 fc[12], fb[12];  // FOLD: fsum / fbias of columns 16 j + 4 g .. +3 of the head's 192
+  if constexpr (FOLD) {
+#pragma unroll
+    for (int j = 0; j < 12; ++j) {
+      const int64_t wr = (int64_t)(j >> 2) * d + (int64_t)h * 64 + 16 * (j & 3) + 4 * g;
+      fc[j] = *reinterpret_cast<const float4*>(fx.fsum + wr);
+      fb[j] = *reinterpret_cast<const float4*>(fx.fbias + wr);
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      int64_t row = rb * 128 + 32 * wid + 16 * t + li;
+      row = row < M ? row : M - 1;
+      rs[t] = fold_row_stats(fx.fst + row * fx.fparts, fx.fparts, fx.feps);
+    }
+  }
   for (int kc = 0; kc < nk; ++kc) {
     wait_vmcnt<0>();   // this lane's part of chunk kc is in LDS
     __syncthreads();   // every lane's, and chunk kc - 1 is consumed by every wave
@@ -1002,6 +1021,16 @@ qkv_attn_kernel(const typename MM<DT>::T* __restrict__ X, int64_t ldx, const typ
     }
   }
   __syncthreads();   // every wave is done with the stages: they take the V rows now
+  if constexpr (FOLD) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int j = 0; j < 12; ++j) {
+        const float c[4] = {fc[j].x, fc[j].y, fc[j].z, fc[j].w}, b[4] = {fb[j].x, fb[j].y, fb[j].z, fb[j].w};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[t][j][r] = rs[t].y * (acc[t][j][r] - rs[t].x * c[r]) + b[r];
+      }
+  }
   // this wave's event; q / k as 16x16x16 operands (dims 16 c + 4 g .. +3 of row 16 t + li), V to LDS
   const int64_t e = rb * 4 + wid;
   const bool live = e * 32 < M;
@@ -2716,9 +2745,13 @@ int linear_rows(const void* x, int64_t ldx, int x_dtype, const void* w, int64_t 
 // Declared in internal.h.
 int qkv_attn_rows(const void* x, const void* w, void* o, const int32_t* n_events, int64_t capacity, int64_t N,
                   int64_t d, int H, int dh, const float* obj_mask, const int32_t* ev_rows, float scale, int dtype,
-                  hipStream_t st) {
+                  hipStream_t st, const float* fsum, const float* fbias, const void* fst, int64_t fparts, float eps) {
   if ((dtype != HCLSM_BF16 && dtype != HCLSM_F16) || N != 32 || dh != 64 || H <= 0 || d != (int64_t)H * 64 ||
       d % QA_KC || !al16(x) || !al16(w) || !al16(o))
+    return HCLSM_ERR_UNSUPPORTED;
+  const bool fold = fst != nullptr;
+  if (fold && (!fsum || !fbias || !al16(fsum) || !al16(fbias) || (((uintptr_t)fst) & 7) || fparts <= 0 ||
+               fparts > FOLD_MAX_PARTS))
     return HCLSM_ERR_UNSUPPORTED;
   if (capacity <= 0) return 0;
   if (!x || !w || !o || !n_events || (obj_mask && !ev_rows)) return HCLSM_ERR_NULL;
@@ -2726,12 +2759,23 @@ int qkv_attn_rows(const void* x, const void* w, void* o, const int32_t* n_events
   const int64_t grid = (rows + 127) / 128 * H;
   if (grid > 0x7fffffffLL) return HCLSM_ERR_SHAPE;
   const float sl2 = scale * HCLSM_LOG2E;
-  if (dtype == HCLSM_BF16)
-    hipLaunchKernelGGL(qkv_attn_kernel<HCLSM_BF16>, dim3((unsigned)grid), dim3(256), 0, st, (const uint16_t*)x, d,
-                       (const uint16_t*)w, (uint16_t*)o, d, n_events, rows, d, H, obj_mask, ev_rows, sl2);
-  else
-    hipLaunchKernelGGL(qkv_attn_kernel<HCLSM_F16>, dim3((unsigned)grid), dim3(256), 0, st, (const _Float16*)x, d,
-                       (const _Float16*)w, (_Float16*)o, d, n_events, rows, d, H, obj_mask, ev_rows, sl2);
+  LinExt fx = kNoLinExt;
+  fx.fst = reinterpret_cast<const float2*>(fst);
+  fx.fparts = fparts;
+  fx.fsum = fsum;
+  fx.fbias = fbias;
+  fx.feps = eps;
+#define HCLSM_QA(D, TT, F)                                                                                   \
+  hipLaunchKernelGGL((qkv_attn_kernel<D, F>), dim3((unsigned)grid), dim3(256), 0, st, (const TT*)x, d,        \
+                     (const TT*)w, (TT*)o, d, n_events, rows, d, H, obj_mask, ev_rows, sl2, fx)
+  if (dtype == HCLSM_BF16) {
+    if (fold) HCLSM_QA(HCLSM_BF16, uint16_t, true);
+    else HCLSM_QA(HCLSM_BF16, uint16_t, false);
+  } else {
+    if (fold) HCLSM_QA(HCLSM_F16, _Float16, true);
+    else HCLSM_QA(HCLSM_F16, _Float16, false);
+  }
+#undef HCLSM_QA
   HCLSM_LAUNCH_CHECK();
   return 0;
 }

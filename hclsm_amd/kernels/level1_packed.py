@@ -29,8 +29,9 @@ class Level1Weights:
                  n_heads: int, ln_eps: float, fold: list | None = None) -> None:
         self.tensors = tensors
         self.ptrs = (ctypes.c_void_p * len(tensors))(*[t.data_ptr() for t in tensors])
-        # the folded LayerNorms (16-bit): proj_out diag(g), its row sums, proj_out b; per block w1 diag(g2),
-        # w3 diag(g2), their row sums and w1 b2 | w3 b2 (the C call's fold array)
+        # the folded LayerNorms (16-bit): proj_out diag(g), its row sums, proj_out b; per block in_proj diag(g1),
+        # its row sums, in_proj b1, w1 diag(g2), w3 diag(g2), their row sums and w1 b2 | w3 b2 (the C call's fold
+        # array)
         self.fold = fold
         self.fold_ptrs = None if fold is None else (ctypes.c_void_p * len(fold))(*[t.data_ptr() for t in fold])
         self.dtype, self.d_slot, self.d_model, self.hidden = dtype, d_slot, d_model, hidden
@@ -78,9 +79,11 @@ class Level1Weights:
             po, po_s, po_b = folded(m.proj_out.weight, m.norm)
             fold = [po, po_s.contiguous(), po_b.contiguous()]
             for b in m.blocks:
+                qkv, qkv_s, qkv_b = folded(b.attn.in_proj_weight, b.norm1)
                 w1, w1_s, w1_b = folded(b.ffn.w1.weight, b.norm2)
                 w3, w3_s, w3_b = folded(b.ffn.w3.weight, b.norm2)
-                fold += [w1, w3, torch.cat([w1_s, w3_s]).contiguous(), torch.cat([w1_b, w3_b]).contiguous()]
+                fold += [qkv, qkv_s.contiguous(), qkv_b.contiguous(),
+                         w1, w3, torch.cat([w1_s, w3_s]).contiguous(), torch.cat([w1_b, w3_b]).contiguous()]
         W = cls(t, dtype, m.d_slot, m.d_model, hidden, len(m.blocks), n_heads, float(eps.pop()), fold)
         m._hclsm_level1_weights = (key, W)
         return W

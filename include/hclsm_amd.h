@@ -441,13 +441,15 @@ int64_t hclsm_level1_forward_workspace(int64_t capacity, int64_t N, int64_t d_mo
  *   ln2_b [d_model], w1 [hidden, d_model], w3 [hidden, d_model], w2 [d_model, hidden]
  * (LayerNorm weights float32, the rest in `dtype`; no biases, as in the reference).  A query whose keys
  * are all excluded gives NaN, as torch's softmax over all -inf does.
- * fold (nullable; read for 16-bit dtypes): host array of 3 + 4 * n_layers device pointers, formed once per
- * weight set, with which each block's LayerNorm before the SwiGLU input and the final LayerNorm are folded
- * into the next layer (LN(x) W^T = rstd (x (W diag g)^T - mean s) + W b, s the row sums of W diag g): no
- * LayerNorm launch for them.  proj_out diag(norm_w) [d_slot, d_model] (dtype), its row sums [d_slot],
- * proj_out norm_b [d_slot], then per layer w1 diag(ln2_w), w3 diag(ln2_w) [hidden, d_model] (dtype), their row
- * sums [2 hidden] (w1 rows, then w3 rows), w1 ln2_b | w3 ln2_b [2 hidden] (float32); 16-byte aligned, else (or
- * for d_model or hidden not multiples of 64) the LayerNorms run as launches.
+ * fold (nullable; read for 16-bit dtypes): host array of 3 + 7 * n_layers device pointers, formed once per
+ * weight set, with which the LayerNorms inside the stack are folded into the next layer (LN(x) W^T =
+ * rstd (x (W diag g)^T - mean s) + W b, s the row sums of W diag g): no launch for the final LayerNorm and each
+ * block's LN2, nor for LN1 of the blocks after the first where the QKV projection and the attention are one
+ * launch (N = 32, 64-wide heads).  proj_out diag(norm_w) [d_slot, d_model] (dtype), its row sums [d_slot],
+ * proj_out norm_b [d_slot]; then per layer in_proj diag(ln1_w) [3 d_model, d_model] (dtype), its row sums,
+ * in_proj ln1_b [3 d_model], w1 diag(ln2_w), w3 diag(ln2_w) [hidden, d_model] (dtype), their row sums
+ * [2 hidden] (w1 rows, then w3 rows), w1 ln2_b | w3 ln2_b [2 hidden] (float32 where not dtype); 16-byte aligned,
+ * else (or for d_model or hidden not multiples of 64) the LayerNorms run as launches.
  * Replaces: Level1EventDynamics.forward with EventTransformerBlock and SwiGLUFFN
  *   (hclsm/dynamics/level1_event.py:17-133) on the events gathered by HierarchyManager.gather_events.
  */

@@ -65,7 +65,7 @@ def test_level1_weights_fold_array():
             ln.weight.copy_(torch.rand(ln.weight.shape, generator=g) + 0.5)
             ln.bias.copy_(torch.randn(ln.bias.shape, generator=g) * 0.3)
     W = Level1Weights.from_module(l1, torch.bfloat16)
-    assert W.fold is not None and len(W.fold) == 3 + 4 * cfg.n_layers and W.fold_ptrs is not None
+    assert W.fold is not None and len(W.fold) == 3 + 7 * cfg.n_layers and W.fold_ptrs is not None
     assert Level1Weights.from_module(l1, torch.float32).fold is None
     x = _f64(torch.randn(50, cfg.d_model, generator=g)) * 0.8 - 1.2
 
@@ -77,6 +77,7 @@ def test_level1_weights_fold_array():
     check(l1.proj_out.weight, l1.norm, *W.fold[0:3])
     H = l1.blocks[0].ffn.w1.weight.shape[0]
     for i, blk in enumerate(l1.blocks):
-        w1n, w3n, sums, bias = W.fold[3 + 4 * i: 7 + 4 * i]
+        qkv, qkv_s, qkv_b, w1n, w3n, sums, bias = W.fold[3 + 7 * i: 10 + 7 * i]
+        check(blk.attn.in_proj_weight, blk.norm1, qkv, qkv_s, qkv_b)
         check(blk.ffn.w1.weight, blk.norm2, w1n, sums[:H], bias[:H])   # w1 rows first
         check(blk.ffn.w3.weight, blk.norm2, w3n, sums[H:], bias[H:])   # then w3

@@ -137,9 +137,9 @@ def test_level1_fused_qkv_attention_32_slots(dtype):
 @pytest.mark.parametrize("dtype,N,B,T", [(torch.bfloat16, 32, 5, 9), (torch.float16, 16, 4, 12),
                                          (torch.bfloat16, 32, 16, 128)])
 def test_level1_folded_layernorms(dtype, N, B, T):
-    """16-bit calls fold the LayerNorms before the SwiGLU inputs and before proj_out into those layers' weights
-    (Level1Weights' fold array: W diag(gamma), its row sums, W beta); the out-projection and the last W2 write the
-    rows' LayerNorm partials.  With non-trivial gamma / beta in every LayerNorm and a mean offset on the events,
+    """16-bit calls fold the LayerNorms before the SwiGLU inputs, before proj_out and (32 slots: the fused QKV
+    attention) LN1 of every block after the first into those layers' weights (Level1Weights' fold array: W diag(gamma),
+    its row sums, W beta); the out-projection and W2 write the rows' LayerNorm partials.  With non-trivial gamma / beta in every LayerNorm and a mean offset on the events,
     the output matches the oracle at the 16-bit bar and the call without the fold array within 1e-2; the last case
     has a 65,536-row capacity."""
     from hclsm_amd.kernels.level1_packed import Level1Weights, level1_forward_packed
@@ -152,7 +152,7 @@ def test_level1_folded_layernorms(dtype, N, B, T):
     states, mask, obj = _case(B, T, N, 31 + N, p=0.3)
     states = states + 0.7
     W = Level1Weights.from_module(l1, dtype)
-    assert W.fold is not None and len(W.fold) == 3 + 4 * L1.n_layers
+    assert W.fold is not None and len(W.fold) == 3 + 7 * L1.n_layers
     W0 = Level1Weights(W.tensors, W.dtype, W.d_slot, W.d_model, W.hidden, W.n_layers, W.n_heads, W.ln_eps)
     print(f"level1 fold {dtype} N={N} B={B} T={T}", flush=True)
     with torch.no_grad():
