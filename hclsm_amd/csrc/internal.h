@@ -87,6 +87,10 @@ int linear_stats_rows(const void* x, int64_t ldx, const void* w, int64_t ldw, co
                       float* y, int64_t ldy, void* y2, int64_t ldy2, void* pst, int64_t M, int64_t N, int64_t K,
                       const int32_t* m_dev, int64_t m_mul, int dtype, hipStream_t st);
 
+// Most 64-column LayerNorm partials a folded row may have (rows of up to 1024 columns): linear_fold_rows and
+// qkv_attn_rows refuse more (HCLSM_ERR_UNSUPPORTED).
+constexpr int FOLD_MAX_PARTS = 16;
+
 // Y = LN(X) . W0^T for the rows of a linear_stats_rows output: x its 16-bit copy, fst its partials (fparts per row),
 // w = W0 diag(gamma) in dtype, fsum[j] = sum of row j of w (fp32), fbias[j] = (W0 beta)[j]; the output is
 // rstd (x w^T - mean fsum) + fbias.  With w3 (rows of W0 diag(gamma) for the gate's second factor, N = 2 H):

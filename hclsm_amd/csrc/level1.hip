@@ -90,8 +90,8 @@ extern "C" int hclsm_level1_forward(const void* ev, int ev_dtype, void* out, int
   // the LayerNorms before the SwiGLU inputs and proj_out folded into those layers' weights: 16-bit, the
   // out-projection and the last W2 writing x's LayerNorm partials (d_model a multiple of 64)
   // (shapes or alignments the fold's kernels do not take: the LayerNorm launches instead)
-  bool folded = fold != nullptr && dtype != HCLSM_F32 && d_model % 64 == 0 && hidden % 64 == 0 && d_slot % 4 == 0 &&
-                n_layers > 0;
+  bool folded = fold != nullptr && dtype != HCLSM_F32 && d_model % 64 == 0 && d_model <= 64 * FOLD_MAX_PARTS &&
+                hidden % 64 == 0 && d_slot % 4 == 0 && n_layers > 0;
   if (fold != nullptr && dtype != HCLSM_F32)
     for (int64_t i = 0; i < 3 + 7 * n_layers; ++i) {
       if (fold[i] == nullptr) return HCLSM_ERR_NULL;

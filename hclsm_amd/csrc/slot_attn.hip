@@ -173,7 +173,6 @@ constexpr LinExt kNoLinExt{nullptr, 1, nullptr, 0, nullptr};
 
 // (mean, rstd) of a row from its 64-column partials (mean_p, M2_p), parts <= FOLD_MAX_PARTS: every partial requested
 // at once, then M2 = sum M2_p + 64 sum (mean_p - mean)^2.
-constexpr int FOLD_MAX_PARTS = 16;   // rows of up to 1024 columns
 __device__ __forceinline__ float2 fold_row_stats(const float2* __restrict__ p, int64_t parts, float eps) {
   // two rounds of at most 8 requests (8 partials in registers at a time); the partial means enter shifted by the
   // first, sum (m_p - m_0) and sum (m_p - m_0)^2, so that an offset of the row's values cancels exactly

@@ -168,6 +168,35 @@ def test_level1_folded_layernorms(dtype, N, B, T):
     assert normwise_rel_err(_np(got), _np(got0)) <= 1e-2
 
 
+def test_level1_fold_array_past_the_partials_limit():
+    """d_model = 1088 (17 heads of 64) has 17 64-column LayerNorm partials per row, one more than the folded kernels
+    combine: with the fold array given, the 16-bit call takes the LayerNorm launches instead and still matches the
+    oracle at the 16-bit bar (and the call without the fold array within 1e-2)."""
+    from hclsm_amd.dynamics import Level1EventDynamics
+    from hclsm_amd.kernels.level1_packed import Level1Weights, level1_forward_packed
+    cfg = SimpleNamespace(d_model=1088, n_layers=2, n_heads=17)
+    hm, _ = _modules(41)
+    torch.manual_seed(41)
+    l1 = Level1EventDynamics(cfg, D_SLOT).cuda()
+    states, mask, obj = _case(3, 6, 32, 41, p=0.5)
+    mask[0, :2] = 1.0   # live events in clip 0 whatever the draw (clip 1 has none)
+    W = Level1Weights.from_module(l1, torch.bfloat16)
+    assert W.fold is not None
+    W0 = Level1Weights(W.tensors, W.dtype, W.d_slot, W.d_model, W.hidden, W.n_layers, W.n_heads, W.ln_eps)
+    print("level1 fold past the partials limit: d_model 1088", flush=True)
+    with torch.no_grad():
+        ev, idx = hm.gather_events_packed(states, mask)
+        out = level1_forward_packed(ev, idx, obj, W)
+        out0 = level1_forward_packed(ev, idx, obj, W0)
+        ev_pad, pad, K = hm.gather_events(states, mask)
+    ref = om.level1_ref(_np(ev_pad), _np(pad), _np(obj), _sd(l1), cfg.n_layers, cfg.n_heads)
+    got, bk = _live_rows(out, idx)
+    got0, _ = _live_rows(out0, idx)
+    want = np.stack([ref[b, k] for b, k in bk])
+    assert normwise_rel_err(_np(got), want) <= 2e-2
+    assert normwise_rel_err(_np(got), _np(got0)) <= 1e-2
+
+
 def test_level1_padded_forward_bf16_fused_attention():
     """The reference-shaped padded call (Level1EventDynamics.forward over (B, K_max, N, d_slot), level1_event.py:85-133)
     under a bf16 autocast with 32 slots: the dense event index feeds the fused QKV projection + slot attention
