@@ -385,9 +385,9 @@ struct AUnit<DT, float> {
 };
 
 constexpr int LT_KC = 128;
-constexpr int LT_LD = LT_KC + 8;   // LDS row pitch (elements): spreads the 16 rows of an operand over banks
 
-template <int DT, int OT, typename XT = typename MM<DT>::T, bool FOLD = false>
+// KC: the K chunk staged per round (128, or 64 for half the LDS: twice the workgroups resident per CU)
+template <int DT, int OT, typename XT = typename MM<DT>::T, bool FOLD = false, int KC = LT_KC>
 __global__ void __launch_bounds__(256)
 linear_lds_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>::T* __restrict__ W,
                   int64_t ldw, const float* __restrict__ bias, const float* __restrict__ resid, int64_t ldr,
@@ -396,6 +396,10 @@ linear_lds_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>::
   using A = MM<DT>;
   using T = typename A::T;
   static_assert(A::KPL == 8, "16-bit operands");
+  static_assert(KC == 64 || KC == 128, "K chunk");
+  constexpr int LT_LD = KC + 8;      // LDS row pitch (elements): spreads the 16 rows of an operand over banks
+  constexpr int UPR = KC / 8;        // 16-byte units per row of a chunk
+  constexpr int NU = 64 * UPR / 256; // units per thread and operand
   __shared__ __align__(16) T As[64 * LT_LD];
   __shared__ __align__(16) T Bs[64 * LT_LD];
   const int64_t tiles_n = (N + 63) / 64;
@@ -406,14 +410,14 @@ linear_lds_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>::
   if (tm * 64 >= M) return;   // the whole workgroup, before any barrier
   const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, g = lane >> 4, li = lane & 15;
   const int wr = wid >> 1, wc = wid & 1;
-  // staging map: 64 rows x (KC / 8) 16-byte units = 1024 units per operand, 4 per thread
-  const XT* pa[4];
-  const T* pb[4];
-  int soff[4], ucol[4];
+  // staging map: 64 rows x (KC / 8) 16-byte units per operand, NU per thread
+  const XT* pa[NU];
+  const T* pb[NU];
+  int soff[NU], ucol[NU];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int u = tid + 256 * i, r = u >> 4;
-    ucol[i] = (u & 15) * 8;
+  for (int i = 0; i < NU; ++i) {
+    const int u = tid + 256 * i, r = u / UPR;
+    ucol[i] = (u % UPR) * 8;
     int64_t ra = tm * 64 + r, rb = tn * 64 + r;
     ra = ra < M ? ra : M - 1;
     rb = rb < N ? rb : N - 1;
@@ -421,11 +425,11 @@ linear_lds_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>::
     pb[i] = w_row(W, ext, rb, ldw) + ucol[i];
     soff[i] = r * LT_LD + ucol[i];
   }
-  AUnit<DT, XT> ra_[4];
-  uint4 rb_[4];
+  AUnit<DT, XT> ra_[NU];
+  uint4 rb_[NU];
   auto fetch = [&](int64_t k0, int kc) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < NU; ++i) {
       const bool in = ucol[i] < kc;
       if (in) ra_[i].load(pa[i] + k0);
       else ra_[i].zero();
@@ -437,20 +441,20 @@ linear_lds_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>::
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  fetch(0, (int)(K < LT_KC ? K : LT_KC));
+  fetch(0, (int)(K < KC ? K : KC));
   // FOLD: (mean, rstd) of the tile's rows and (fsum, fbias) of its columns, read after the loop's barriers
   __shared__ float2 rst[FOLD ? 64 : 1], cst[FOLD ? 64 : 1];
   if constexpr (FOLD) fold_prologue<64, 64>(ext, tid, tm * 64, M, tn * 64, N, rst, cst);
-  for (int64_t k0 = 0; k0 < K; k0 += LT_KC) {
-    const int kc = (int)(K - k0 < LT_KC ? K - k0 : LT_KC);
+  for (int64_t k0 = 0; k0 < K; k0 += KC) {
+    const int kc = (int)(K - k0 < KC ? K - k0 : KC);
     __syncthreads();   // the previous chunk is consumed
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < NU; ++i) {
       *reinterpret_cast<uint4*>(As + soff[i]) = ra_[i].get();
       *reinterpret_cast<uint4*>(Bs + soff[i]) = rb_[i];
     }
     __syncthreads();
-    if (k0 + LT_KC < K) fetch(k0 + LT_KC, (int)(K - k0 - LT_KC < LT_KC ? K - k0 - LT_KC : LT_KC));
+    if (k0 + KC < K) fetch(k0 + KC, (int)(K - k0 - KC < KC ? K - k0 - KC : KC));
     for (int s = 0; s < kc / 32; ++s) {
       const typename A::Op a0 = A::load(As + (wr * 32 + li) * LT_LD + s * 32 + 8 * g);
       const typename A::Op a1 = A::load(As + (wr * 32 + 16 + li) * LT_LD + s * 32 + 8 * g);
@@ -475,6 +479,7 @@ linear_lds_kernel(const XT* __restrict__ X, int64_t ldx, const typename MM<DT>::
     // a tile of the transposed half: transpose through LDS so that consecutive threads write
     // consecutive rows (tokens) of yt
     constexpr int TP = 66;   // pitch of the transposed tile (elements)
+    static_assert(64 * TP <= 64 * LT_LD, "the transposed tile fits As");
     T* Ts = As;
     __syncthreads();   // the last chunk is consumed
 #pragma unroll
@@ -2617,8 +2622,8 @@ static void launch_linear_quad(const void* x, int64_t ldx, const void* w, int64_
                            (const XT*)x, ldx, (const typename MM<DT>::T*)w, ldw, bias, resid, ldr,
                            (typename MM<OT>::T*)y, ldy, (typename MM<DT>::T*)y2, ldy2, M, N, K, relu, clamp, ext);
       else
-        hipLaunchKernelGGL((linear_lds_kernel<DT, OT, XT>), dim3(grid), dim3(256), 0, st, (const XT*)x, ldx,
-                           (const typename MM<DT>::T*)w, ldw, bias, resid, ldr, (typename MM<OT>::T*)y, ldy,
+        hipLaunchKernelGGL((linear_lds_kernel<DT, OT, XT, false, 64>), dim3(grid), dim3(256), 0, st, (const XT*)x,
+                           ldx, (const typename MM<DT>::T*)w, ldw, bias, resid, ldr, (typename MM<OT>::T*)y, ldy,
                            (typename MM<DT>::T*)y2, ldy2, M, N, K, relu, clamp, os, ext);
     } else if constexpr (direct) {
       if (os.yt == nullptr && al16(x) && al16(w) && ldx % 4 == 0 && ldw % 4 == 0)
